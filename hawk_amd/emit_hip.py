@@ -1,0 +1,594 @@
+"""The HIP writer of hawk's gfx950 target: IR -> one self-contained HIP
+translation unit per kernel stage.
+
+The emitted entry has the reference's device signature — one by-value mirror
+per ``arg_spec`` slot, then ``long long base, count, nSamples`` (reference
+``hawk/emit/cuda.py:46-54``) — and its ONE geometry prologue binds
+``i = base + flat`` (reference ``:73-81``).  Each thread takes ``per_thread``
+samples a workgroup-width apart, so every load and store of a wave is one
+contiguous 64-lane run of a ``[component, sample]`` plane (coalesced), and the
+samples of one thread are independent work for the scheduler to overlap.
+
+The body is scalarised: a vector or matrix node is one C++ variable per
+component, every operation one statement in the reference's operation order
+(a ``dot``/``mv``/``mm`` adds its products left to right; the Cholesky factor
+and solve follow reference ``hawk/embedded/linalg.py:233-271`` and
+``:443-536``).  With ``-ffp-contract=off`` the device computes the same IEEE
+operations as the host oracle built in the reference's ``native`` profile.
+
+A rolled loop stays rolled: its loop-invariant inputs are hoisted, its carried
+slots are locals, and a loop whose carries a reversed loop reads keeps a tape
+(one local array per carried component) that the compiler holds in registers
+when the loop is unrolled.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+from . import ir
+from .ir import AccumWrite, Assign, Deps, HawkError, Node, Program, SampleSum, free_inputs, level_order
+
+ABI_TAG = "aether-abi/2"
+LAYOUT_SIZES = (40, 32, 32, 8, 24)
+
+#: The by-value ABI shape of each role (reference hawk/emit/spelling.py:63-69);
+#: a rank-0 ``mutable`` is a 32-byte handle, a ranked one a 40-byte mirror.
+MIRROR_OF = {"out": "gref", "vec_in": "gref", "mat_in": "gref", "per_sample": "handle",
+             "wide_out": "handle", "accum_out": "handle", "lookup": "handle", "uniform": "value"}
+
+_UNARY_C = {"exp": "exp", "sin": "sin", "cos": "cos", "tanh": "tanh", "sqrt": "sqrt",
+            "log": "log", "abs": "fabs"}
+_BINARY_C = {"add": "+", "sub": "-", "mul": "*", "div": "/"}
+_COMPARE_C = {"lt": "<", "le": "<=", "gt": ">", "ge": ">=", "eq": "==", "ne": "!="}
+
+
+def kind_for(role: str, ttype, mode: str) -> str:
+    """The ``hk_argblock`` kind name of a slot (reference hawk/runtime.py:96-110)."""
+    if role == "uniform":
+        return "f32" if mode == "float32" else "f64"
+    shape = "gref" if role in ("out", "vec_in", "mat_in") or (role == "mutable" and ttype.shape) else "handle"
+    if shape == "handle" and ttype.dtype == "i32":
+        return "int_handle"
+    return shape
+
+
+def _literal(x: float) -> str:
+    if math.isnan(x):
+        return "Real(__builtin_nan(\"\"))"
+    if math.isinf(x):
+        return "Real(__builtin_inf())" if x > 0 else "Real(-__builtin_inf())"
+    text = repr(float(x))
+    return f"Real({text})"
+
+
+def _entries(shape: tuple) -> list:
+    if len(shape) == 0:
+        return [()]
+    if len(shape) == 1:
+        return [(i,) for i in range(shape[0])]
+    return [(i, j) for i in range(shape[0]) for j in range(shape[1])]
+
+
+def _flat(shape: tuple, idx) -> int:
+    if isinstance(idx, int):
+        idx = (idx,)
+    if len(shape) == 1:
+        return idx[0]
+    return idx[0] * shape[1] + idx[1]
+
+
+@dataclass
+class Stage:
+    """One per-sample stage of a kernel: the planes it binds and what it writes."""
+
+    name: str
+    arg_spec: list                  # [(role, name)]
+    planes: dict                    # name -> {"role", "shape", "dtype"}
+    writes: list                    # [(plane, node)]
+    scratch: dict = field(default_factory=dict)   # name -> {"dtype", "per_sample": 1}
+
+
+class _Scope:
+    def __init__(self):
+        self.memo = [{}]
+
+    def get(self, n: Node):
+        for frame in reversed(self.memo):
+            hit = frame.get(n.uid)
+            if hit is not None:
+                return hit
+        return None
+
+    def put(self, n: Node, value) -> None:
+        self.memo[-1][n.uid] = value
+
+
+class _Writer:
+    """Scalarises nodes into C++ statements."""
+
+    def __init__(self, stage: Stage, mode: str):
+        self.stage = stage
+        self.mode = mode
+        self.lines: list = []
+        self.indent = 2
+        self.count = 0
+        self.scope = _Scope()
+        self.deps = Deps()
+        self.taped = {}              # loop uid -> True when a tape_read reads it
+
+    # -- text --------------------------------------------------------------
+    def emit(self, text: str) -> None:
+        self.lines.append("    " * self.indent + text)
+
+    def fresh(self, stem: str = "v") -> str:
+        self.count += 1
+        return f"hk_{stem}{self.count}"
+
+    def ctype(self, dtype: str) -> str:
+        return {"f64": "Real", "f32": "Real", "i64": "long long", "i32": "int", "bool": "bool"}[dtype]
+
+    def let(self, dtype: str, expr: str, stem: str = "v") -> str:
+        name = self.fresh(stem)
+        self.emit(f"const {self.ctype(dtype)} {name} = {expr};")
+        return name
+
+    # -- values ------------------------------------------------------------
+    def value(self, n: Node) -> list:
+        hit = self.scope.get(n)
+        if hit is None:
+            raise HawkError(f"internal: {n!r} used before it was emitted")
+        return hit
+
+    def scalar(self, n: Node) -> str:
+        v = self.value(n)
+        if len(v) != 1:
+            raise HawkError(f"internal: {n!r} is not a scalar")
+        return v[0]
+
+    def run(self, roots) -> None:
+        for n in level_order(roots, self.deps):
+            if self.scope.get(n) is None:
+                self.node(n)
+
+    # -- nodes -------------------------------------------------------------
+    def node(self, n: Node) -> None:
+        k = n.kind
+        handler = getattr(self, "_" + k, None)
+        if handler is None:
+            raise HawkError(f"the hip writer has no spelling for the IR kind {k!r}")
+        out = handler(n)
+        if out is not None:
+            self.scope.put(n, out)
+
+    def _leaf(self, n: Node) -> list:
+        role, name = n.literal
+        p = self.stage.planes[name]["var"]
+        if role == "uniform":
+            return [p]
+        if role == "mutable":         # a prior read of an output plane
+            role = "per_sample" if not n.ttype.shape else ("vec_in" if len(n.ttype.shape) == 1 else "mat_in")
+        dt = n.ttype.dtype
+        if not n.ttype.shape:
+            return [self.let(dt, f"{p}[hk_i]", "in")]
+        out = []
+        for e in _entries(n.ttype.shape):
+            c = _flat(n.ttype.shape, e)
+            out.append(self.let(dt, f"{p}[{c} * {p}_cs + hk_i]", "in"))
+        return out
+
+    def _const(self, n: Node) -> list:
+        return [_literal(n.literal)]
+
+    def _iconst(self, n: Node) -> list:
+        return [f"{int(n.literal)}LL"]
+
+    def _real(self, n: Node) -> list:
+        return [f"Real({x})" for x in self.value(n.operands[0])]
+
+    def _neg(self, n: Node) -> list:
+        return [self.let(n.ttype.dtype, f"-{x}") for x in self.value(n.operands[0])]
+
+    def _unary(self, n: Node) -> list:
+        fn = _UNARY_C[n.kind]
+        return [self.let(n.ttype.dtype, f"{fn}({x})") for x in self.value(n.operands[0])]
+
+    _exp = _sin = _cos = _tanh = _sqrt = _log = _abs = _unary
+
+    def _bcast(self, n: Node, k: int) -> list:
+        v = self.value(n.operands[k])
+        size = n.ttype.size if n.ttype.shape else 1
+        return v * size if len(v) == 1 and size > 1 else v
+
+    def _binary(self, n: Node) -> list:
+        op = _BINARY_C[n.kind]
+        a, b = self._bcast(n, 0), self._bcast(n, 1)
+        return [self.let(n.ttype.dtype, f"{x} {op} {y}") for x, y in zip(a, b)]
+
+    _add = _sub = _mul = _div = _binary
+
+    def _compare(self, n: Node) -> list:
+        a, b = self.scalar(n.operands[0]), self.scalar(n.operands[1])
+        return [self.let("bool", f"{a} {_COMPARE_C[n.kind]} {b}", "c")]
+
+    _lt = _le = _gt = _ge = _eq = _ne = _compare
+
+    def _select(self, n: Node) -> list:
+        c = self.scalar(n.operands[0])
+        a, b = self.value(n.operands[1]), self.value(n.operands[2])
+        return [self.let(n.ttype.dtype, f"{c} ? {x} : {y}") for x, y in zip(a, b)]
+
+    def _fold(self, terms: list, dtype: str) -> str:
+        acc = terms[0]
+        for t in terms[1:]:
+            acc = self.let(dtype, f"{acc} + {t}")
+        return acc
+
+    def _dot(self, n: Node) -> list:
+        a, b = self.value(n.operands[0]), self.value(n.operands[1])
+        prods = [self.let(n.ttype.dtype, f"{x} * {y}") for x, y in zip(a, b)]
+        return [self._fold(prods, n.ttype.dtype)]
+
+    def _norm(self, n: Node) -> list:
+        a = self.value(n.operands[0])
+        prods = [self.let(n.ttype.dtype, f"{x} * {x}") for x in a]
+        return [self.let(n.ttype.dtype, f"sqrt({self._fold(prods, n.ttype.dtype)})")]
+
+    def _sum(self, n: Node) -> list:
+        return [self._fold(self.value(n.operands[0]), n.ttype.dtype)]
+
+    def _splat(self, n: Node) -> list:
+        return self.value(n.operands[0]) * n.ttype.size
+
+    def _component(self, n: Node) -> list:
+        src = n.operands[0]
+        return [self.value(src)[_flat(src.ttype.shape, n.literal)]]
+
+    def _vec(self, n: Node) -> list:
+        return [self.scalar(c) for c in n.operands]
+
+    def _transpose(self, n: Node) -> list:
+        r, c = n.operands[0].ttype.shape
+        v = self.value(n.operands[0])
+        return [v[i * c + j] for j in range(c) for i in range(r)]
+
+    def _mv(self, n: Node) -> list:
+        m, v = self.value(n.operands[0]), self.value(n.operands[1])
+        r, c = n.operands[0].ttype.shape
+        dt = n.ttype.dtype
+        out = []
+        for i in range(r):
+            prods = [self.let(dt, f"{m[i * c + j]} * {v[j]}") for j in range(c)]
+            out.append(self._fold(prods, dt))
+        return out
+
+    def _mm(self, n: Node) -> list:
+        a, b = self.value(n.operands[0]), self.value(n.operands[1])
+        r, k = n.operands[0].ttype.shape
+        c = n.operands[1].ttype.shape[1]
+        dt = n.ttype.dtype
+        out = []
+        for i in range(r):
+            for j in range(c):
+                prods = [self.let(dt, f"{a[i * k + q]} * {b[q * c + j]}") for q in range(k)]
+                out.append(self._fold(prods, dt))
+        return out
+
+    def _outer(self, n: Node) -> list:
+        a, b = self.value(n.operands[0]), self.value(n.operands[1])
+        return [self.let(n.ttype.dtype, f"{x} * {y}") for x in a for y in b]
+
+    # -- Cholesky (reference hawk/embedded/linalg.py:233-271) -------------------
+    def _chol(self, n: Node) -> list:
+        a = self.value(n.operands[0])
+        size = n.ttype.shape[0]
+        stem = self.fresh("L")
+        names = [f"{stem}_{i}_{j}" for i in range(size) for j in range(size)]
+        info = f"{stem}_info"
+        self.emit("Real " + ", ".join(f"{x} = Real(0.0)" for x in names) + ";")
+        self.emit(f"int {info} = 0;")
+
+        def el(i, j):
+            return names[i * size + j]
+
+        def sym(i, j):
+            return f"(Real(0.5) * {a[i * size + j]}) + (Real(0.5) * {a[j * size + i]})"
+        for j in range(size):
+            self.emit(f"if ({info} == 0) {{")
+            self.indent += 1
+            self.emit(f"Real hk_d = {sym(j, j)};")
+            for k in range(j):
+                self.emit(f"hk_d = hk_d - ({el(j, k)} * {el(j, k)});")
+            self.emit("if (hk_d > Real(0.0)) {")
+            self.indent += 1
+            self.emit("const Real hk_ljj = sqrt(hk_d);")
+            self.emit(f"{el(j, j)} = hk_ljj;")
+            for i in range(j + 1, size):
+                self.emit(f"{{ Real hk_acc = {sym(i, j)};")
+                for k in range(j):
+                    self.emit(f"  hk_acc = hk_acc - ({el(i, k)} * {el(j, k)});")
+                self.emit(f"  {el(i, j)} = hk_acc / hk_ljj; }}")
+            self.indent -= 1
+            self.emit(f"}} else {{ {info} = {j + 1}; }}")
+            self.indent -= 1
+            self.emit("}")
+        self._chol_info_of = getattr(self, "_chol_info_of", {})
+        self._chol_info_of[n.uid] = info
+        return names
+
+    def _chol_info(self, n: Node) -> list:
+        f = n.operands[0]
+        return [self._chol_info_of[f.uid]]
+
+    def _chol_factor(self, n: Node) -> list:
+        f = n.operands[0]
+        size = f.ttype.shape[0]
+        src = self.value(f)
+        info = self._chol_info_of[f.uid]
+        return [self.let(n.ttype.dtype, f"({info} == 0 && {j} <= {i}) ? {src[i * size + j]} : Real(0.0)")
+                for i in range(size) for j in range(size)]
+
+    def _cho_solve(self, n: Node) -> list:
+        f, b = n.operands
+        size = f.ttype.shape[0]
+        L = self.value(f)
+        info = self._chol_info_of[f.uid]
+        rhs = self.value(b)
+        stem = self.fresh("x")
+        x = [f"{stem}_{i}" for i in range(size)]
+        self.emit("Real " + ", ".join(f"{v} = Real(0.0)" for v in x) + ";")
+        self.emit(f"if ({info} == 0) {{")
+        self.indent += 1
+        for i in range(size):                       # forward: L y = b, rows ascending
+            self.emit(f"{{ Real hk_acc = {rhs[i]};")
+            for j in range(i):
+                self.emit(f"  hk_acc = hk_acc - ({L[i * size + j]} * {x[j]});")
+            self.emit(f"  {x[i]} = hk_acc / {L[i * size + i]}; }}")
+        for r in range(size):                       # backward: L^T x = y, rows descending
+            i = size - 1 - r
+            self.emit(f"{{ Real hk_acc = {x[i]};")
+            for j in range(i + 1, size):
+                self.emit(f"  hk_acc = hk_acc - ({L[j * size + i]} * {x[j]});")
+            self.emit(f"  {x[i]} = hk_acc / {L[i * size + i]}; }}")
+        self.indent -= 1
+        self.emit("}")
+        return x
+
+    # -- loops ---------------------------------------------------------------
+    def _loop(self, n: Node) -> list:
+        info = n.literal
+        inits = [self.value(x) for x in n.operands]
+        for f in free_inputs(n, self.deps):            # hoisted: already emitted at this level
+            if self.scope.get(f) is None:
+                self.run([f])
+        carry_vars = []
+        for j, c in enumerate(info.carries):
+            stem = self.fresh("c")
+            names = [f"{stem}_{e}" for e in range(max(1, c.ttype.size if c.ttype.shape else 1))]
+            ct = self.ctype(c.ttype.dtype)
+            for name, init in zip(names, inits[j] * (len(names) if len(inits[j]) == 1 else 1)):
+                self.emit(f"{ct} {name} = {init};")
+            carry_vars.append(names)
+        tapes = None
+        if n.uid in self.taped:
+            tapes = []
+            for j, names in enumerate(carry_vars):
+                row = [f"hk_tape{n.uid}_{j}_{e}" for e in range(len(names))]
+                ct = self.ctype(info.carries[j].ttype.dtype)
+                self.emit(f"{ct} " + ", ".join(f"{t}[{info.trip}]" for t in row) + ";")
+                tapes.append(row)
+            self.tape_of = getattr(self, "tape_of", {})
+            self.tape_of[n.uid] = (tapes, info.start, info.step)
+        k = f"hk_k{n.uid}"
+        if info.unroll:
+            self.emit("#pragma unroll")
+        self.emit(f"for (long long {k} = {info.start}LL; {k} != {info.stop()}LL; {k} += {info.step}LL) {{")
+        self.indent += 1
+        self.scope.memo.append({})
+        self.scope.put(info.index, [k])
+        for c, names in zip(info.carries, carry_vars):
+            self.scope.put(c, names)
+        if tapes is not None:
+            slot = f"(({k} - {info.start}LL) / {info.step}LL)"
+            for row, names in zip(tapes, carry_vars):
+                for t, v in zip(row, names):
+                    self.emit(f"{t}[{slot}] = {v};")
+        self.run(info.nexts)
+        nexts = [self.value(x) for x in info.nexts]
+        temps = []
+        for names, nv in zip(carry_vars, nexts):
+            nv = nv * len(names) if len(nv) == 1 and len(names) > 1 else nv
+            row = []
+            for name, val in zip(names, nv):
+                t = self.fresh("n")
+                self.emit(f"const auto {t} = {val};")
+                row.append(t)
+            temps.append(row)
+        for names, row in zip(carry_vars, temps):
+            for name, t in zip(names, row):
+                self.emit(f"{name} = {t};")
+        self.scope.memo.pop()
+        self.indent -= 1
+        self.emit("}")
+        return carry_vars
+
+    def _loop_value(self, n: Node) -> list:
+        return self.value(n.operands[0])[n.literal]
+
+    def _loop_index(self, n: Node) -> list:
+        raise HawkError("internal: a loop index read outside its loop")
+
+    _carry = _loop_index
+
+    def _tape_read(self, n: Node) -> list:
+        loop, index = n.operands
+        tapes, start, step = self.tape_of[loop.uid]
+        k = self.scalar(index)
+        slot = f"(({k} - {start}LL) / {step}LL)"
+        return [f"{t}[{slot}]" for t in tapes[n.literal]]
+
+
+def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: list) -> Stage:
+    """The plane table and arg_spec of the per-sample stage of ``program``."""
+    writes = [(s.name, s.value) for s in program.sinks if isinstance(s, Assign)] + extra_writes
+    roots = [node for _, node in writes]
+    used_leaves = ir.leaves_of(roots)
+    used = {n.literal[1] for n in used_leaves} | {name for name, _ in writes}
+    decls = dict(program.decls)
+    planes = {}
+    for name, node in extra_writes:
+        if name not in decls:
+            decls[name] = ir.Decl(name, "wide_out", node.ttype)
+    prog2 = Program(decls, program.sinks)
+    spec = ir.arg_spec(prog2, used)
+    for role, name in spec:
+        d = decls[name]
+        planes[name] = {"role": role, "shape": list(d.ttype.shape), "dtype": d.ttype.dtype,
+                        "kind": kind_for(role, d.ttype, mode), "var": f"hk_p_{name}"}
+    return Stage(stage_name, spec, planes, writes)
+
+
+def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_taped: bool = True) -> str:
+    """The HIP source of one per-sample stage."""
+    w = _Writer(stage, mode)
+    roots = [node for _, node in stage.writes]
+    # which loops keep a tape
+    for n in ir.topo(roots):
+        if n.kind == "tape_read":
+            w.taped[n.operands[0].uid] = True
+            if unroll_taped:
+                n.operands[0].literal.unroll = True
+                for m in ir.topo([n]):
+                    if m.kind == "loop":
+                        m.literal.unroll = True
+    for n in ir.topo(roots):
+        if n.kind == "loop" and any(t.kind == "tape_read" for t in ir.topo(n.literal.nexts)) and unroll_taped:
+            n.literal.unroll = True
+    w.run(roots)
+    body = list(w.lines)
+    w.lines = []
+    for plane, node in stage.writes:
+        info = stage.planes[plane]
+        var = info["var"]
+        vals = w.value(node)
+        if not node.ttype.shape:
+            w.emit(f"{var}[hk_i] = {vals[0]};")
+        else:
+            for e in _entries(node.ttype.shape):
+                c = _flat(node.ttype.shape, e)
+                w.emit(f"{var}[{c} * {var}_cs + hk_i] = {vals[c]};")
+    stores = list(w.lines)
+
+    real = "float" if mode == "float32" else "double"
+    params, unpack = [], []
+    for role, name in stage.arg_spec:
+        info = stage.planes[name]
+        var = info["var"]
+        kind = info["kind"]
+        if kind in ("f64", "f32"):
+            params.append(f"Real {var}")
+            continue
+        is_input = role not in ("mutable", "out", "wide_out", "accum_out")
+        cq = "const " if is_input else ""
+        elem = "int" if info["dtype"] == "i32" else "Real"
+        if kind == "gref":
+            params.append(f"GRefMirror {var}_m")
+            unpack.append(f"{cq}{elem}* __restrict__ {var} = reinterpret_cast<{cq}{elem}*>({var}_m.data_);")
+            unpack.append(f"const long long {var}_cs = static_cast<long long>({var}_m.compStride_);")
+        else:
+            params.append(f"ScalarHandle {var}_m")
+            unpack.append(f"{cq}{elem}* __restrict__ {var} = reinterpret_cast<{cq}{elem}*>({var}_m.data);")
+    params += ["long long base", "long long count", "long long nSamples"]
+    out = [
+        f"// hawk gfx950 stage '{stage.name}' (generated; mode {mode}).",
+        f"typedef {real} Real;",
+        "struct GRefMirror { Real* data_; unsigned long long samples_, compStride_, sampleStride_; "
+        "int deviceType_, deviceId_; };",
+        "struct ScalarHandle { void* data; unsigned long long samples, stride; int deviceType, deviceId; };",
+        f'extern "C" __attribute__((used)) __device__ char eagle_abi_tag[] = "{ABI_TAG}";',
+        "extern \"C\" __attribute__((used)) __device__ unsigned long long eagle_layout_sizes[5] = {"
+        + ", ".join(str(s) for s in LAYOUT_SIZES) + "};",
+        "",
+        f'extern "C" __global__ void __launch_bounds__({block}) {stage.name}(',
+        "        " + ",\n        ".join(params) + ") {",
+        "    (void)nSamples;",
+    ]
+    out += ["    " + u for u in unpack]
+    out += [
+        "#pragma unroll",
+        f"    for (int hk_v = 0; hk_v < {per_thread}; ++hk_v) {{",
+        f"        const long long hk_flat = (static_cast<long long>(blockIdx.x) * {per_thread} + hk_v) * {block}"
+        " + static_cast<long long>(threadIdx.x);",
+        "        if (hk_flat >= count) break;",
+        "        const long long hk_i = base + hk_flat;",
+    ]
+    out += body + stores
+    out += ["    }", "}", ""]
+    return "\n".join(out)
+
+
+@dataclass
+class Plan:
+    """How one kernel runs on the hip target: its per-sample stage (if any)
+    and the team stages after it."""
+
+    stage: Stage | None
+    source: str | None
+    team: list                      # [{"op": ..., planes...}]
+    planes: dict                    # every plane a caller binds: name -> {"role", "shape", "dtype"}
+
+
+def plan_kernel(program: Program, name: str, mode: str = "float64", block: int = 256,
+                per_thread: int = 1) -> Plan:
+    """Split ``program`` into its per-sample stage and team stages, and render
+    the per-sample stage."""
+    if mode not in ("float64", "float32"):
+        raise HawkError(f"mode={mode!r}: the hip target builds 'float64' or 'float32'")
+    assigned = {id(s.value): s.name for s in program.sinks if isinstance(s, Assign)}
+    extra, team = [], []
+    for s in program.sinks:
+        if isinstance(s, SampleSum):
+            if mode != "float64":
+                raise HawkError("hawk.sum(policy='ordered') on the hip target is built in float64")
+            src = assigned.get(id(s.value))
+            if src is None and s.value.kind == "leaf" and s.value.literal[0] == "per_sample":
+                src = s.value.literal[1]
+            if src is None:
+                src = f"hk_sum_{s.name}"
+                extra.append((src, s.value))
+            team.append({"op": "ordered_sum", "u": src, "out": s.name})
+        elif isinstance(s, AccumWrite):
+            if mode != "float64":
+                raise HawkError("hawk.scatter(policy='ordered') on the hip target is built in float64")
+            src = assigned.get(id(s.value))
+            if src is None and s.value.kind == "leaf" and s.value.literal[0] == "per_sample":
+                src = s.value.literal[1]
+            if src is None:
+                src = f"hk_scatter_{s.name}"
+                extra.append((src, s.value))
+            team.append({"op": "ordered_scatter", "key": s.key.literal[1], "v": src, "target": s.name})
+    has_stage = any(isinstance(s, Assign) for s in program.sinks) or extra
+    stage = source = None
+    if has_stage:
+        stage = _stage_planes(program, name, mode, extra)
+        source = render_stage(stage, mode, block, per_thread)
+    planes = {}
+    if stage is not None:
+        for pname, info in stage.planes.items():
+            planes[pname] = {k: info[k] for k in ("role", "shape", "dtype")}
+    for t in team:
+        for key in ("u", "key", "v"):
+            pname = t.get(key)
+            if pname and pname not in planes:
+                d = program.decls[pname]
+                planes[pname] = {"role": d.role, "shape": list(d.ttype.shape), "dtype": d.ttype.dtype}
+        for key in ("out", "target"):
+            pname = t.get(key)
+            if pname:
+                planes[pname] = {"role": "cell" if t["op"] == "ordered_sum" else "accum_out",
+                                 "shape": [], "dtype": "f64"}
+    for pname, info in planes.items():
+        if pname.startswith("hk_"):
+            info["scratch"] = True
+    return Plan(stage, source, team, planes)

@@ -1,0 +1,103 @@
+"""The five benchmark kernels, written as a hawk user writes them.
+
+These are the workloads the benchmark and the parity tests run (one per
+benchmark configuration): a pure streaming kernel, a vector kernel with its
+reverse and forward derivatives, a rolled 32-substep leapfrog with its
+reverse-mode derivative, per-sample linear algebra (a 6x6 SPD solve; a
+16x16 fp32 product), and a fused elementwise chain feeding a fixed-tree
+ordered sum and a keyed ordered scatter.
+"""
+
+from __future__ import annotations
+
+from . import diff
+from . import trace as _trace
+from .math import abs as _abs
+from .math import cho_solve, cholesky, dot, exp, sin, sqrt, tanh
+from .trace import Kernel, kernel
+from .types import Index, Matrix, Mutable, Param, Scalar, Vector
+
+#: Leapfrog step and substep count of the two-body kernel.
+DT = 1e-3
+SUBSTEPS = 32
+
+
+@kernel
+def scale(x: Scalar, a: Param, b: Param) -> Scalar:
+    return a * x + b
+
+
+@kernel
+def energy(v: Vector[3], out: Mutable[Scalar]):
+    out = 0.5 * dot(v, v)
+
+
+energy_vjp = Kernel("energy_vjp", diff.vjp(energy, wrt=("v",)))
+energy_jvp = Kernel("energy_jvp", diff.jvp(energy, wrt=("v",)))
+
+
+@kernel
+def twobody(r0: Vector[3], v0: Vector[3], mu: Param, r: Mutable[Vector[3]], v: Mutable[Vector[3]]):
+    rr = r0
+    vv = v0
+    for k in range(SUBSTEPS):
+        r2 = dot(rr, rr)
+        acc = (-mu / (r2 * sqrt(r2))) * rr
+        vh = vv + (0.5 * DT) * acc
+        rr = rr + DT * vh
+        r2n = dot(rr, rr)
+        accn = (-mu / (r2n * sqrt(r2n))) * rr
+        vv = vh + (0.5 * DT) * accn
+    r = rr
+    v = vv
+
+
+twobody_vjp = Kernel("twobody_vjp", diff.vjp(twobody, wrt=("r0", "v0")))
+
+
+@kernel
+def spd_solve(A: Matrix[6, 6], b: Vector[6], x: Mutable[Vector[6]]):
+    L, info = cholesky(A)
+    x = cho_solve(L, b)
+
+
+spd_solve_vjp = Kernel("spd_solve_vjp", diff.vjp(spd_solve, wrt=("A", "b")))
+
+
+@kernel
+def mm16(A: Matrix[16, 16], B: Matrix[16, 16], C: Mutable[Matrix[16, 16]]):
+    C = A @ B
+
+
+mm16_vjp = Kernel("mm16_vjp", diff.vjp(mm16, wrt=("A", "B")))
+
+
+@kernel
+def chain(x: Scalar, key: Index, y: Mutable[Scalar], total: Mutable[Scalar], bins: Mutable[Scalar]):
+    t1 = exp(x)
+    t2 = sin(t1)
+    t3 = 1.5 * t2 + 0.25
+    t4 = tanh(t3)
+    t5 = sqrt(_abs(t4) + 1.0)
+    t6 = t5 * t5 - x
+    t7 = exp(-_abs(t6))
+    y = t7 * x + t4
+    total = _trace.sum(y, policy="ordered")
+    _trace.scatter(bins, policy="ordered")[key] += y
+
+
+@kernel
+def ordered_total(x: Scalar, total: Mutable[Scalar]):
+    total = _trace.sum(x, policy="ordered")
+
+
+@kernel
+def ordered_add(key: Index, x: Scalar, acc: Mutable[Scalar]):
+    _trace.scatter(acc, policy="ordered")[key] += x
+
+
+#: Every kernel above, by name.
+ALL = {k.name: k for k in (scale, energy, energy_vjp, energy_jvp, twobody, twobody_vjp, spd_solve,
+                            spd_solve_vjp, chain, ordered_total, ordered_add)}
+#: The float32 unit (built with mode="float32").
+FLOAT32 = {k.name: k for k in (mm16, mm16_vjp)}

@@ -1,0 +1,514 @@
+"""The tensor-typed IR of hawk's gfx950 target.
+
+One node family (:class:`Node`): a ``kind``, its ``operands``, a static
+:class:`~hawk_amd.types.TensorType` and an optional ``literal``.  Scalars,
+vectors and matrices are all nodes; the emitter scalarises them.  A rolled
+``for`` is one ``loop`` node whose body is the ``nexts`` of its carried slots
+(reference ``hawk/ir/loops.py``), read back through ``loop_value``; a reversed
+loop reads the forward loop's per-iteration carries through ``tape_read``
+(reference ``hawk/diff/loops.py:484-540``).
+
+Sinks are what a kernel commits: a per-sample :class:`Assign`, an
+over-every-sample :class:`SampleSum` (``hawk.sum``) and a keyed
+:class:`AccumWrite` (``hawk.scatter``), as reference ``hawk/ir/nodes.py``.
+"""
+
+from __future__ import annotations
+
+import itertools
+from dataclasses import dataclass, field
+
+from .types import TensorType
+
+
+class HawkError(Exception):
+    """Every refusal of the authoring surface, the compiler and the runtime."""
+
+
+#: Canonical role order of ``arg_spec`` == the entry-signature order
+#: (reference ``hawk/ir/nodes.py:51-52``).
+ROLE_ORDER = ("mutable", "out", "wide_out", "accum_out", "vec_in", "mat_in",
+              "wide_in", "per_sample", "lookup", "terminated", "uniform", "nsamples")
+
+UNARY = ("neg", "exp", "sin", "cos", "tanh", "sqrt", "abs", "log", "real")
+BINARY = ("add", "sub", "mul", "div")
+COMPARE = ("lt", "le", "gt", "ge", "eq", "ne")
+ELEMENTWISE = UNARY + BINARY + COMPARE + ("select",)
+
+_uid = itertools.count(1)
+
+
+class Node:
+    """One IR node.  Identity is the object: two structurally equal nodes are
+    two values (the emitter and the compiler fold duplicates)."""
+
+    __slots__ = ("kind", "operands", "ttype", "literal", "uid")
+
+    def __init__(self, kind: str, operands: tuple, ttype: TensorType, literal=None):
+        self.kind = kind
+        self.operands = tuple(operands)
+        self.ttype = ttype
+        self.literal = literal
+        self.uid = next(_uid)
+
+    def __repr__(self) -> str:
+        lit = "" if self.literal is None else f" {self.literal!r}"
+        return f"<{self.kind}#{self.uid}{lit} {self.ttype.shape}{self.ttype.dtype}>"
+
+
+@dataclass
+class LoopInfo:
+    """The static half of a ``loop`` node: trip, index and carried slots."""
+
+    trip: int
+    start: int
+    step: int
+    index: Node                      # kind "loop_index"
+    carries: tuple                   # kind "carry" placeholders, one per slot
+    nexts: tuple                     # the body's value of each slot
+    names: tuple = ()                # the authored names of the slots (diagnostics)
+    unroll: bool = False             # emit with #pragma unroll
+
+    def stop(self) -> int:
+        return self.start + self.trip * self.step
+
+
+# --------------------------------------------------------------------------
+# constructors
+
+
+def const(value: float, dtype: str = "f64") -> Node:
+    return Node("const", (), TensorType((), dtype), float(value))
+
+
+def index_const(value: int) -> Node:
+    return Node("iconst", (), TensorType((), "i64"), int(value))
+
+
+def leaf(role: str, name: str, ttype: TensorType) -> Node:
+    return Node("leaf", (), ttype, (role, name))
+
+
+def _broadcast(a: TensorType, b: TensorType, kind: str) -> tuple:
+    if a.shape == b.shape:
+        return a.shape
+    if a.shape == ():
+        return b.shape
+    if b.shape == ():
+        return a.shape
+    raise HawkError(f"{kind}: operands of shapes {a.shape} and {b.shape} do not broadcast "
+                    "(a scalar broadcasts; two tensors must have one shape)")
+
+
+def _real_dtype(*nodes: Node) -> str:
+    for n in nodes:
+        if n.ttype.dtype in ("f64", "f32"):
+            return n.ttype.dtype
+    return "f64"
+
+
+def as_real(n: Node) -> Node:
+    """An integer value (a loop index, an int constant) as a real."""
+    if n.ttype.dtype in ("f64", "f32"):
+        return n
+    if n.ttype.dtype == "bool":
+        raise HawkError("a bool mask is not a number; use hawk.math.where(mask, a, b)")
+    if n.kind == "iconst":
+        return const(float(n.literal))
+    return Node("real", (n,), TensorType(n.ttype.shape, "f64"))
+
+
+def make(kind: str, operands: tuple, literal=None) -> Node:
+    """Build a node of ``kind``, typing it from its operands."""
+    ops = tuple(operands)
+    if kind in BINARY:
+        a, b = (as_real(o) for o in ops)
+        return Node(kind, (a, b), TensorType(_broadcast(a.ttype, b.ttype, kind), _real_dtype(a, b)))
+    if kind in UNARY:
+        (a,) = ops
+        if kind == "real":
+            return as_real(a)
+        a = as_real(a)
+        return Node(kind, (a,), TensorType(a.ttype.shape, a.ttype.dtype))
+    if kind in COMPARE:
+        a, b = (as_real(o) for o in ops)
+        shape = _broadcast(a.ttype, b.ttype, kind)
+        if shape:
+            raise HawkError(f"{kind}: comparisons are per scalar in this build")
+        return Node(kind, (a, b), TensorType((), "bool"))
+    if kind == "select":
+        cond, a, b = ops
+        a, b = as_real(a), as_real(b)
+        shape = _broadcast(a.ttype, b.ttype, "select")
+        if a.ttype.shape != shape:
+            a = make("splat", (a,), shape)
+        if b.ttype.shape != shape:
+            b = make("splat", (b,), shape)
+        return Node(kind, (cond, a, b), TensorType(shape, _real_dtype(a, b)))
+    if kind == "splat":
+        (a,) = ops
+        a = as_real(a)
+        if a.ttype.shape:
+            raise HawkError("splat widens a scalar")
+        return Node(kind, (a,), TensorType(tuple(literal), a.ttype.dtype), tuple(literal))
+    if kind == "dot":
+        a, b = ops
+        if len(a.ttype.shape) != 1 or a.ttype.shape != b.ttype.shape:
+            raise HawkError(f"dot takes two vectors of one width, got {a.ttype.shape} and {b.ttype.shape}")
+        return Node(kind, (a, b), TensorType((), _real_dtype(a, b)))
+    if kind == "norm":
+        (a,) = ops
+        if len(a.ttype.shape) != 1:
+            raise HawkError("norm takes a vector")
+        return Node(kind, (a,), TensorType((), a.ttype.dtype))
+    if kind == "sum":
+        (a,) = ops
+        return Node(kind, (a,), TensorType((), a.ttype.dtype))
+    if kind == "component":
+        (a,) = ops
+        shape = a.ttype.shape
+        idx = literal if isinstance(literal, tuple) else (literal,)
+        if len(idx) != len(shape) or any(not (0 <= i < e) for i, e in zip(idx, shape)):
+            raise HawkError(f"index {literal!r} is outside a value of shape {shape}")
+        return Node(kind, (a,), TensorType((), a.ttype.dtype), idx if len(idx) > 1 else idx[0])
+    if kind == "vec":
+        parts = tuple(as_real(o) for o in ops)
+        if any(p.ttype.shape for p in parts):
+            raise HawkError("vec/mat take scalar entries")
+        shape = tuple(literal) if literal is not None else (len(parts),)
+        count = 1
+        for e in shape:
+            count *= e
+        if count != len(parts):
+            raise HawkError(f"{len(parts)} entries do not fill shape {shape}")
+        return Node(kind, parts, TensorType(shape, _real_dtype(*parts) if parts else "f64"), shape)
+    if kind == "transpose":
+        (a,) = ops
+        if len(a.ttype.shape) != 2:
+            raise HawkError("transpose takes a matrix")
+        r, c = a.ttype.shape
+        return Node(kind, (a,), TensorType((c, r), a.ttype.dtype))
+    if kind == "mv":
+        m, v = ops
+        if len(m.ttype.shape) != 2 or len(v.ttype.shape) != 1 or m.ttype.shape[1] != v.ttype.shape[0]:
+            raise HawkError(f"matrix @ vector: shapes {m.ttype.shape} and {v.ttype.shape} disagree")
+        return Node(kind, (m, v), TensorType((m.ttype.shape[0],), _real_dtype(m, v)))
+    if kind == "mm":
+        a, b = ops
+        if len(a.ttype.shape) != 2 or len(b.ttype.shape) != 2 or a.ttype.shape[1] != b.ttype.shape[0]:
+            raise HawkError(f"matrix @ matrix: shapes {a.ttype.shape} and {b.ttype.shape} disagree")
+        return Node(kind, (a, b), TensorType((a.ttype.shape[0], b.ttype.shape[1]), _real_dtype(a, b)))
+    if kind == "outer":
+        a, b = ops
+        if len(a.ttype.shape) != 1 or len(b.ttype.shape) != 1:
+            raise HawkError("outer takes two vectors")
+        return Node(kind, (a, b), TensorType((a.ttype.shape[0], b.ttype.shape[0]), _real_dtype(a, b)))
+    if kind == "chol":
+        (a,) = ops
+        if len(a.ttype.shape) != 2 or a.ttype.shape[0] != a.ttype.shape[1]:
+            raise HawkError("cholesky takes a square matrix")
+        return Node(kind, (a,), TensorType(a.ttype.shape, a.ttype.dtype, "chol_factor"))
+    if kind == "chol_factor":
+        (f,) = ops
+        return Node(kind, (f,), TensorType(f.ttype.shape, f.ttype.dtype))
+    if kind == "chol_info":
+        (f,) = ops
+        return Node(kind, (f,), TensorType((), "i32"))
+    if kind == "cho_solve":
+        f, b = ops
+        if f.ttype.tag != "chol_factor":
+            raise HawkError("cho_solve reads the factor that cholesky() returned, not a matrix "
+                            f"built or changed since (got {f.ttype!r})")
+        if len(b.ttype.shape) != 1 or b.ttype.shape[0] != f.ttype.shape[0]:
+            raise HawkError(f"cho_solve: a right-hand side of shape {b.ttype.shape} for a "
+                            f"{f.ttype.shape[0]}x{f.ttype.shape[0]} factor (a vector is supported)")
+        return Node(kind, (f, b), TensorType(b.ttype.shape, _real_dtype(b)))
+    raise HawkError(f"no IR kind {kind!r}")
+
+
+def zero_like(t: TensorType) -> Node:
+    z = const(0.0)
+    return z if t.shape == () else make("splat", (z,), t.shape)
+
+
+def is_zero(n: Node) -> bool:
+    if n.kind == "const":
+        return n.literal == 0.0
+    if n.kind == "splat":
+        return is_zero(n.operands[0])
+    return False
+
+
+def new_loop(trip: int, start: int, step: int, inits: tuple, body, names: tuple = ()) -> Node:
+    """A rolled loop: ``body(index, *carries) -> nexts`` traced once over
+    placeholders typed like ``inits``."""
+    uid = next(_uid)
+    index = Node("loop_index", (), TensorType((), "i64"), uid)
+    carries = tuple(Node("carry", (), as_real(x).ttype if x.ttype.dtype != "i64" else x.ttype, (uid, j))
+                    for j, x in enumerate(inits))
+    nexts = tuple(body(index, *carries))
+    return loop_node(uid, trip, start, step, index, carries, tuple(inits), nexts, names)
+
+
+def loop_node(uid: int, trip: int, start: int, step: int, index: Node, carries: tuple,
+              inits: tuple, nexts: tuple, names: tuple = ()) -> Node:
+    if len(nexts) != len(carries):
+        raise HawkError("a loop body must give one value per carried slot")
+    fixed = []
+    for j, (c, x) in enumerate(zip(carries, nexts)):
+        if x.ttype.shape != c.ttype.shape:
+            if x.ttype.shape and not c.ttype.shape:
+                raise HawkError(f"loop slot {names[j] if j < len(names) else j!r} changes shape in the body: "
+                                f"{c.ttype.shape} before, {x.ttype.shape} after")
+            x = make("splat", (as_real(x),), c.ttype.shape)
+        fixed.append(as_real(x) if c.ttype.dtype in ("f64", "f32") else x)
+    info = LoopInfo(trip, start, step, index, tuple(carries), tuple(fixed), tuple(names))
+    node = Node("loop", tuple(as_real(x) if c.ttype.dtype in ("f64", "f32") else x
+                              for c, x in zip(carries, inits)), TensorType((), "tuple"), info)
+    node.uid = uid
+    return node
+
+
+def loop_value(loop: Node, j: int) -> Node:
+    return Node("loop_value", (loop,), loop.literal.carries[j].ttype, j)
+
+
+def tape_read(loop: Node, j: int, index: Node) -> Node:
+    """Carry ``j`` of the forward ``loop`` as it stood at the START of the
+    iteration whose index value ``index`` holds."""
+    return Node("tape_read", (loop, index), loop.literal.carries[j].ttype, j)
+
+
+# --------------------------------------------------------------------------
+# loop structure (shared by the emitter and autodiff)
+
+
+class Deps:
+    """Which loops (by the uid of their index node) each node depends on."""
+
+    def __init__(self):
+        self.memo: dict = {}
+        self.owner: dict = {}          # carry/index uid -> loop index uid
+
+    def register(self, loop: Node) -> None:
+        info = loop.literal
+        key = info.index.uid
+        self.owner[info.index.uid] = key
+        for c in info.carries:
+            self.owner[c.uid] = key
+
+    def of(self, n: Node) -> frozenset:
+        hit = self.memo.get(n.uid)
+        if hit is not None:
+            return hit
+        order = topo([n])
+        for m in order:             # every loop first: a carry is reached before its loop
+            if m.kind == "loop":
+                self.register(m)
+        for m in order:
+            if m.uid in self.memo:
+                continue
+            if m.kind in ("carry", "loop_index"):
+                own = self.owner.get(m.uid)
+                self.memo[m.uid] = frozenset() if own is None else frozenset((own,))
+                continue
+            deps = set()
+            for o in m.operands:
+                deps |= self.memo[o.uid]
+            if m.kind == "loop":
+                inner = set()
+                for x in m.literal.nexts:
+                    inner |= self.memo[x.uid]
+                inner.discard(m.literal.index.uid)
+                deps |= inner
+            self.memo[m.uid] = frozenset(deps)
+        return self.memo[n.uid]
+
+
+def free_inputs(loop: Node, deps: Deps) -> list:
+    """The nodes outside ``loop`` its body reads: every operand of a body node
+    that does not itself depend on the loop, in first-reach order."""
+    deps.register(loop)
+    body = topo(loop.literal.nexts)
+    for n in body:               # a body can reach other loops (a tape read's loop): register them first
+        if n.kind == "loop":
+            deps.register(n)
+    key = loop.literal.index.uid
+    out, seen = [], set()
+    for n in body:
+        if key not in deps.of(n):
+            continue
+        kids = list(n.operands)
+        if n.kind == "loop":
+            kids += free_inputs(n, deps)
+        for k in kids:
+            if key not in deps.of(k) and k.uid not in seen and k.kind not in ("const", "iconst"):
+                seen.add(k.uid)
+                out.append(k)
+    for x in loop.literal.nexts:
+        if key not in deps.of(x) and x.uid not in seen and x.kind not in ("const", "iconst"):
+            seen.add(x.uid)
+            out.append(x)
+    return out
+
+
+def level_order(roots, deps: Deps, stops=frozenset()) -> list:
+    """Nodes reachable from ``roots`` at this level: a loop is opaque, its
+    operands being its inits and its body's free inputs.  Nodes in ``stops``
+    are reached but not expanded."""
+    order, seen = [], set()
+    stack = [(r, False) for r in reversed(list(roots))]
+    while stack:
+        node, expanded = stack.pop()
+        if expanded:
+            order.append(node)
+            continue
+        if node.uid in seen:
+            continue
+        seen.add(node.uid)
+        stack.append((node, True))
+        if node.uid in stops:
+            continue
+        kids = list(node.operands)
+        if node.kind == "loop":
+            kids += free_inputs(node, deps)
+        for k in reversed(kids):
+            if k.uid not in seen:
+                stack.append((k, False))
+    return order
+
+
+def fresh_placeholders(loop: Node) -> tuple:
+    """New index and carry placeholders for a copy of ``loop``'s body, and the
+    substitution map from the old ones."""
+    info = loop.literal
+    uid = next(_uid)
+    index = Node("loop_index", (), info.index.ttype, uid)
+    carries = tuple(Node("carry", (), c.ttype, (uid, j)) for j, c in enumerate(info.carries))
+    mapping = {info.index.uid: index, **{c.uid: nc for c, nc in zip(info.carries, carries)}}
+    return uid, index, carries, mapping
+
+
+# --------------------------------------------------------------------------
+# sinks
+
+
+@dataclass
+class Assign:
+    """The per-sample commit of ``value`` into the plane ``name``."""
+
+    name: str
+    value: Node
+    role: str = "mutable"
+
+
+@dataclass
+class SampleSum:
+    """``name = hawk.sum(value, policy=...)``: one cell over every sample."""
+
+    name: str
+    value: Node
+    policy: str = "ordered"
+
+
+@dataclass
+class AccumWrite:
+    """``hawk.scatter(name, policy=...)[key] += value``."""
+
+    name: str
+    value: Node
+    key: Node
+    policy: str = "ordered"
+
+
+@dataclass
+class Decl:
+    """One declared plane or uniform of a kernel."""
+
+    name: str
+    role: str            # per_sample / vec_in / mat_in / uniform / mutable / out
+    ttype: TensorType
+
+
+@dataclass
+class Program:
+    """What a kernel is: its declarations and its sinks (a traced kernel, or a
+    derivative of one)."""
+
+    decls: dict = field(default_factory=dict)     # name -> Decl, declaration order
+    sinks: list = field(default_factory=list)
+
+
+# --------------------------------------------------------------------------
+# walks
+
+
+def sink_roots(sinks) -> list:
+    roots = []
+    for s in sinks:
+        roots.append(s.value)
+        if isinstance(s, AccumWrite):
+            roots.append(s.key)
+    return roots
+
+
+def topo(roots) -> list:
+    """Every node reachable from ``roots`` (through operands and loop bodies),
+    operands first.  Iterative, so deep chains do not hit Python's recursion limit."""
+    order, seen = [], set()
+    stack = [(r, False) for r in reversed(list(roots))]
+    while stack:
+        node, expanded = stack.pop()
+        if expanded:
+            order.append(node)
+            continue
+        if node.uid in seen:
+            continue
+        seen.add(node.uid)
+        stack.append((node, True))
+        kids = list(node.operands)
+        if node.kind == "loop":
+            kids += list(node.literal.nexts)
+        for k in reversed(kids):
+            if k.uid not in seen:
+                stack.append((k, False))
+    return order
+
+
+def leaves_of(roots) -> list:
+    """The ``leaf`` nodes reachable from ``roots``, first reach first."""
+    return [n for n in topo(roots) if n.kind == "leaf"]
+
+
+def substitute(roots, mapping: dict) -> list:
+    """Copies of ``roots`` with every node whose uid is in ``mapping`` replaced;
+    nodes that reach no replaced node are shared, not copied."""
+    memo = dict(mapping)
+    order = topo(roots)
+    for n in order:
+        if n.uid in memo:
+            continue
+        kids = n.operands
+        new_kids = tuple(memo.get(k.uid, k) for k in kids)
+        if n.kind == "loop":
+            info = n.literal
+            new_nexts = tuple(memo.get(x.uid, x) for x in info.nexts)
+            if any(a is not b for a, b in zip(new_kids, kids)) or \
+                    any(a is not b for a, b in zip(new_nexts, info.nexts)):
+                copy = loop_node(next(_uid), info.trip, info.start, info.step, info.index,
+                                 info.carries, new_kids, new_nexts, info.names)
+                copy.literal.unroll = info.unroll
+                memo[n.uid] = copy
+            continue
+        if any(a is not b for a, b in zip(new_kids, kids)):
+            copy = Node(n.kind, new_kids, n.ttype, n.literal)
+            memo[n.uid] = copy
+    return [memo.get(r.uid, r) for r in roots]
+
+
+def arg_spec(program: Program, used: set) -> list:
+    """``[(role, name)]`` of the planes a kernel binds, in :data:`ROLE_ORDER`,
+    declaration order within a role; ``used`` holds the names the body reads
+    or writes (an unused declaration gets no slot)."""
+    decls = [d for d in program.decls.values() if d.name in used]
+    return [(d.role, d.name) for role in ROLE_ORDER for d in decls if d.role == role]

@@ -1,0 +1,317 @@
+"""``hawk.load`` / ``hawk.run`` for the gfx950 target.
+
+The thin Python face over ``libhawk_core.so`` (reference ``hawk/runtime.py``):
+``load`` opens a built unit's kernel (code object loaded and ABI-checked by
+``hk_load``), ``run`` validates and binds the caller's planes — PyTorch-ROCm
+tensors, bound by their device pointers, never copied — launches the
+per-sample stage over ``[base, base+count)``, then the team stages (the
+fixed-tree ordered sum, the ordered scatter) on the same HIP stream.
+
+Ownership as in the reference (``hawk/runtime.py:20-22``, ``:655-696``): the
+planes are the caller's and are written in place; the runtime owns only its
+scratch (term planes of a split kernel, the sum's lane partials, the
+scatter's chunk partials and status plane), made once per sample count.
+
+Threading: one :class:`DeviceKernel` shared by threads is safe: ``run`` holds
+the kernel's lock over bind and launch (reference ``hawk/runtime.py:46-53``).
+"""
+
+from __future__ import annotations
+
+import json
+import threading
+from pathlib import Path
+
+from . import _contracts, _core
+from .ir import HawkError
+
+_PER_SAMPLE = ("per_sample", "vec_in", "mat_in", "mutable", "out", "wide_out")
+
+
+def _torch():
+    import torch
+    return torch
+
+
+class DeviceKernel:
+    """One kernel of a built unit, loaded for the gfx950 target."""
+
+    def __init__(self, directory: Path, sidecar: dict):
+        if sidecar.get("target") != "hip":
+            raise HawkError(f"{sidecar.get('kernel')!r} was not built for the hip target")
+        self.directory = Path(directory)
+        self.sidecar = sidecar
+        self.name = sidecar["kernel"]
+        self.planes = sidecar["planes"]
+        self.team = sidecar.get("team") or []
+        self.arg_spec = [tuple(p) for p in sidecar.get("arg_spec") or []]
+        self.mode = sidecar.get("mode", "float64")
+        self.launch_shape = sidecar.get("launch", {"block": 256, "per_thread": 1})
+        self.entry = None
+        self.block = None
+        if sidecar.get("entry"):
+            code = (self.directory / sidecar["code_object"]).read_bytes()
+            self.library = _core.DeviceLibrary(code)
+            self.entry = self.library.entry(sidecar["entry"])
+            self.block = _core.ArgBlock(sidecar["descriptor"])
+        self._scratch: dict = {}
+        self._lock = threading.Lock()
+        self.scatter_chunks = None
+
+    # -- validation ----------------------------------------------------------
+    def _real_dtype(self):
+        torch = _torch()
+        return torch.float32 if self.mode == "float32" else torch.float64
+
+    def caller_planes(self) -> list:
+        return [n for n, p in self.planes.items() if not p.get("scratch")]
+
+    def check_planes(self, arrays: dict, n_samples=None) -> int:
+        """Validate every bound plane against the sidecar; return the sample count."""
+        torch = _torch()
+        declared = set(self.caller_planes())
+        unknown = sorted(set(arrays) - declared)
+        if unknown:
+            raise HawkError(f"kernel {self.name!r}: {unknown} are not planes it declares "
+                            f"(declared: {sorted(declared)})")
+        missing = sorted(declared - set(arrays))
+        if missing:
+            raise HawkError(f"kernel {self.name!r}: bind {missing}")
+        n = n_samples
+        problems = []
+        for name in sorted(declared):
+            info = self.planes[name]
+            x = arrays[name]
+            role = info["role"]
+            if role == "uniform":
+                if isinstance(x, bool) or not isinstance(x, (int, float)):
+                    problems.append(f"{name!r} is a Param: pass a Python number, got {type(x).__name__}")
+                continue
+            if not isinstance(x, torch.Tensor):
+                problems.append(f"{name!r} must be a torch tensor on the GPU (the hip target binds device "
+                                f"pointers), got {type(x).__name__}")
+                continue
+            if not x.is_cuda:
+                problems.append(f"{name!r} is on {x.device}; the hip target binds device planes")
+                continue
+            if not x.is_contiguous():
+                problems.append(f"{name!r} is not contiguous; pass x.contiguous()")
+                continue
+            want = torch.int32 if info["dtype"] == "i32" else (
+                torch.float64 if role in ("cell", "accum_out") else self._real_dtype())
+            if x.dtype != want:
+                problems.append(f"{name!r} has dtype {x.dtype}, the kernel reads {want}")
+                continue
+            if role in _PER_SAMPLE:
+                lead = tuple(info["shape"])
+                if x.dim() != len(lead) + 1 or tuple(x.shape[:-1]) != lead:
+                    problems.append(f"{name!r} has shape {tuple(x.shape)}; a {lead or 'scalar'} plane is "
+                                    f"({', '.join(str(e) for e in lead + ('N',))})")
+                    continue
+                if n is None:
+                    n = int(x.shape[-1])
+                elif int(x.shape[-1]) != n:
+                    problems.append(f"{name!r} holds {int(x.shape[-1])} samples, other planes {n}")
+            elif role == "cell":
+                if x.numel() != 1:
+                    problems.append(f"{name!r} is a one-cell result of hawk.sum: bind 1 element, got {x.numel()}")
+            elif role == "accum_out":
+                if x.dim() != 1:
+                    problems.append(f"{name!r} is the 1-D plane of cells hawk.scatter adds into")
+        if problems:
+            raise HawkError(f"kernel {self.name!r}: " + "; ".join(problems))
+        if n is None:
+            raise HawkError(f"kernel {self.name!r}: no per-sample plane is bound, so the sample count is "
+                            "unknown; pass n_samples=")
+        return n
+
+    # -- scratch -------------------------------------------------------------
+    def _buffer(self, key, nbytes: int, device, zero: bool = True):
+        torch = _torch()
+        held = self._scratch.get(key)
+        if held is None or held.numel() < max(1, nbytes) or held.device != device:
+            held = (torch.zeros if zero else torch.empty)(max(1, nbytes), dtype=torch.uint8, device=device)
+            self._scratch[key] = held
+        return held
+
+    def _term_plane(self, name: str, n: int, device):
+        torch = _torch()
+        info = self.planes[name]
+        lead = tuple(info["shape"])
+        key = ("plane", name, n)
+        held = self._scratch.get(key)
+        if held is None or held.device != device:
+            held = torch.empty(lead + (n,), dtype=self._real_dtype(), device=device)
+            self._scratch[key] = held
+        return held
+
+    # -- launch --------------------------------------------------------------
+    def bind_all(self, arrays: dict, n: int) -> None:
+        """Bind every slot of the per-sample stage (validated planes)."""
+        for slot, (role, name) in enumerate(self.arg_spec):
+            kind = self.block.descriptor[slot]
+            x = arrays[name]
+            if kind in ("f64", "f32"):
+                self.block.bind_value(slot, float(x))
+                continue
+            self.block.bind(slot, x.data_ptr(), n, 1, _contracts.DEVICE_ROCM, x.device.index or 0)
+
+    def _run(self, arrays: dict, base: int, count: int, n: int, stream: int, check: bool) -> None:
+        torch = _torch()
+        device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
+        bound = dict(arrays)
+        for name, info in self.planes.items():
+            if info.get("scratch"):
+                bound[name] = self._term_plane(name, n, device)
+        if self.entry is not None:
+            self.bind_all(bound, n)
+            self.entry.run(self.block, base, count, n, threads=self.launch_shape["block"],
+                           per_thread=self.launch_shape["per_thread"], stream=stream)
+        statuses = []
+        for t in self.team:
+            if t["op"] == "ordered_sum":
+                u = bound[t["u"]]
+                scratch = self._buffer(("sum", t["out"]), _core.ordered_sum_scratch_bytes(), device)
+                _core.ordered_sum(u.data_ptr(), n, bound[t["out"]].data_ptr(), scratch.data_ptr(), stream)
+            elif t["op"] == "ordered_scatter":
+                target = bound[t["target"]]
+                cells = int(target.numel())
+                if cells == 0:
+                    continue              # an ordered scatter into no cells adds nothing
+                scratch = self._buffer(("scatter", t["target"], n, cells),
+                                       _core.ordered_scatter_scratch_bytes(n, cells), device, zero=False)
+                status = self._buffer(("status", t["target"]), 4 * 257, device)
+                _core.ordered_scatter(bound[t["key"]].data_ptr(), bound[t["v"]].data_ptr(), n,
+                                      target.data_ptr(), cells, scratch.data_ptr(), status.data_ptr(), stream)
+                self.scatter_chunks = _core.scatter_chunks(n, cells)
+                statuses.append((t, status, cells))
+            else:
+                raise HawkError(f"kernel {self.name!r}: unknown team stage {t['op']!r}")
+        if check:
+            for t, status, cells in statuses:
+                flags = status.view(torch.int32)[:257].cpu()
+                if bool((flags[1:] != 0).any()):
+                    raise HawkError(
+                        f"{self.name}: hawk.scatter({t['target']}, policy='ordered') got a key outside "
+                        f"[0, {cells}) that is not the skip key -1; those adds were dropped, the rest are "
+                        f"in {t['target']}")
+
+    def prepare(self, *, stream=None, **arrays) -> Prepared:
+        """Validate and bind ``arrays`` once and return a :class:`Prepared`
+        launcher that re-runs the whole kernel (per-sample stage and team
+        stages) over every sample with no per-call validation: the stable-binding
+        path of reference ``tests/cards/CARD_LAUNCH_CROSSINGS.md`` (one crossing
+        per launch).  The planes must stay alive and unmoved while it is used."""
+        return Prepared(self, arrays, stream)
+
+    def launch(self, base: int, count: int, n_samples: int, stream: int = 0) -> None:
+        """The per-sample stage alone over ``[base, base+count)`` (planes already bound)."""
+        with self._lock:
+            if self.entry is None:
+                raise HawkError(f"kernel {self.name!r} has no per-sample stage")
+            self.entry.run(self.block, base, count, n_samples, threads=self.launch_shape["block"],
+                           per_thread=self.launch_shape["per_thread"], stream=stream)
+
+
+def load(directory, kernel: str, sidecar: dict | None = None) -> DeviceKernel:
+    """Open ``<directory>/<kernel>`` of a unit built for the hip target."""
+    directory = Path(directory)
+    if sidecar is None:
+        path = directory / f"{kernel}.json"
+        if not path.exists():
+            raise HawkError(f"{directory} holds no kernel {kernel!r} (no {path.name})")
+        sidecar = json.loads(path.read_text())
+    return DeviceKernel(directory, sidecar)
+
+
+def run(kernel: DeviceKernel, *, base: int = 0, count: int | None = None, n_samples: int | None = None,
+        stream=None, check: bool = True, **arrays) -> None:
+    """Bind ``arrays`` and run the kernel once, in place, on the current HIP
+    stream (or ``stream``).  ``count`` defaults to every sample from ``base``.
+    A kernel with team stages (``hawk.sum`` / ``hawk.scatter`` with
+    policy='ordered') runs over every sample (no ``base``/``count``)."""
+    torch = _torch()
+    if not isinstance(kernel, DeviceKernel):
+        raise HawkError("hawk.run takes a kernel loaded with hawk.load")
+    n = kernel.check_planes(arrays, n_samples)
+    if kernel.team and (base != 0 or count not in (None, n)):
+        raise HawkError(f"{kernel.name}: this kernel reduces over every sample, so it runs over every "
+                        "sample (no base= or count=)")
+    if count is None:
+        count = n - base
+    if base < 0 or count < 0 or base + count > n:
+        raise HawkError(f"{kernel.name}: [base, base+count) = [{base}, {base + count}) is outside [0, {n})")
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    elif hasattr(stream, "cuda_stream"):
+        stream = stream.cuda_stream
+    with kernel._lock:
+        kernel._run(arrays, int(base), int(count), int(n), int(stream), check)
+
+
+class Prepared:
+    """A kernel bound once to fixed planes (see :meth:`DeviceKernel.prepare`)."""
+
+    def __init__(self, kernel: DeviceKernel, arrays: dict, stream=None):
+        torch = _torch()
+        self.kernel = kernel
+        self.n = kernel.check_planes(arrays)
+        self.arrays = dict(arrays)
+        if stream is None:
+            stream = torch.cuda.current_stream().cuda_stream
+        elif hasattr(stream, "cuda_stream"):
+            stream = stream.cuda_stream
+        self.stream = int(stream)
+        device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
+        bound = dict(arrays)
+        for name, info in kernel.planes.items():
+            if info.get("scratch"):
+                bound[name] = kernel._term_plane(name, self.n, device)
+        self.bound = bound
+        self.block = None
+        if kernel.entry is not None:
+            self.block = _core.ArgBlock(kernel.sidecar["descriptor"])
+            for slot, (role, name) in enumerate(kernel.arg_spec):
+                kind = self.block.descriptor[slot]
+                x = bound[name]
+                if kind in ("f64", "f32"):
+                    self.block.bind_value(slot, float(x))
+                else:
+                    self.block.bind(slot, x.data_ptr(), self.n, 1, _contracts.DEVICE_ROCM, x.device.index or 0)
+        self.steps = []
+        self.statuses = []
+        for t in kernel.team:
+            if t["op"] == "ordered_sum":
+                scratch = kernel._buffer(("sum", t["out"]), _core.ordered_sum_scratch_bytes(), device)
+                args = (bound[t["u"]].data_ptr(), self.n, bound[t["out"]].data_ptr(), scratch.data_ptr())
+                self.steps.append((_core.ordered_sum, args))
+            elif t["op"] == "ordered_scatter":
+                target = bound[t["target"]]
+                cells = int(target.numel())
+                if cells == 0:
+                    continue
+                scratch = kernel._buffer(("scatter", t["target"], self.n, cells),
+                                         _core.ordered_scatter_scratch_bytes(self.n, cells), device, zero=False)
+                status = kernel._buffer(("status", t["target"]), 4 * 257, device)
+                args = (bound[t["key"]].data_ptr(), bound[t["v"]].data_ptr(), self.n, target.data_ptr(), cells,
+                        scratch.data_ptr(), status.data_ptr())
+                self.steps.append((_core.ordered_scatter, args))
+                self.statuses.append((t, status, cells))
+
+    def __call__(self) -> None:
+        k = self.kernel
+        if k.entry is not None:
+            k.entry.run(self.block, 0, self.n, self.n, threads=k.launch_shape["block"],
+                        per_thread=k.launch_shape["per_thread"], stream=self.stream)
+        for fn, args in self.steps:
+            fn(*args, self.stream)
+
+    def check(self) -> None:
+        """Refuse, by name, a run whose ordered scatter met a bad key (synchronises)."""
+        torch = _torch()
+        for t, status, cells in self.statuses:
+            flags = status.view(torch.int32)[:257].cpu()
+            if bool((flags[1:] != 0).any()):
+                raise HawkError(
+                    f"{self.kernel.name}: hawk.scatter({t['target']}, policy='ordered') got a key outside "
+                    f"[0, {cells}) that is not the skip key -1; those adds were dropped")

@@ -1,0 +1,549 @@
+"""The authoring surface: ``@hawk.kernel``, traced values, ``hawk.sum`` and
+``hawk.scatter``.
+
+A kernel is a plain Python function for ONE sample.  Tracing runs it once over
+:class:`Value` objects (operator overloading builds IR nodes), after a small
+``ast`` rewrite (reference ``hawk/trace/astpass.py``):
+
+* ``for k in range(...)`` becomes ONE rolled ``loop`` node: the names the body
+  assigns that were bound before the loop are its carried slots;
+* every ``return`` (and the end of the body) reports the final value of each
+  ``Mutable`` parameter, so ``y = expr`` commits ``expr`` into the plane ``y``
+  (reference ``hawk/trace/kernel.py:480-525``), and a returned value commits
+  into a synthesised slot named ``out``.
+
+A ``Mutable`` read before it is assigned reads the value the plane held when
+the launch began (a prior read, refused by ``vjp``/``jvp`` as in reference
+``hawk/diff/transform.py:169-192``).
+"""
+
+from __future__ import annotations
+
+import ast
+import inspect
+import textwrap
+from typing import Any
+
+from . import ir
+from .ir import AccumWrite, Assign, Decl, HawkError, Node, Program, SampleSum, make
+from .types import MutableDecl, TensorType, _ParamDecl, role_of
+
+SUM_POLICIES = ("auto", "compensated", "ordered")
+SCATTER_POLICIES = ("ordered",)
+
+
+# --------------------------------------------------------------------------
+# values
+
+
+def node_of(x: Any) -> Node:
+    """The IR node of a traced value or a Python number."""
+    if isinstance(x, Value):
+        return x.node
+    if isinstance(x, bool):
+        raise HawkError("a Python bool is not a number in a kernel body")
+    if isinstance(x, int):
+        return ir.const(float(x))
+    if isinstance(x, float):
+        return ir.const(x)
+    try:
+        import numpy as np
+        if isinstance(x, np.floating | np.integer):
+            return ir.const(float(x))
+    except ImportError:       # pragma: no cover - numpy is a test dependency only
+        pass
+    if isinstance(x, Reduced):
+        raise HawkError("a value reduced over every sample (hawk.sum) is read back in the body: "
+                        "that needs a stage boundary this build does not cut; assign it to a "
+                        "Mutable (or return it) instead")
+    raise HawkError(f"{x!r} ({type(x).__name__}) is not a traced value or a number")
+
+
+def _projected(n: Node) -> Node:
+    """A Cholesky factor used as a matrix reads its lower triangle."""
+    return make("chol_factor", (n,)) if n.ttype.tag == "chol_factor" else n
+
+
+def _bin(kind: str, a: Any, b: Any) -> Value:
+    return Value(make(kind, (_projected(node_of(a)), _projected(node_of(b)))))
+
+
+class Value:
+    """One traced value (scalar, vector or matrix) of the current sample."""
+
+    __slots__ = ("node",)
+    __array_priority__ = 1000      # numpy scalars defer to these operators
+
+    def __init__(self, node: Node):
+        self.node = node
+
+    @property
+    def ttype(self) -> TensorType:
+        return self.node.ttype
+
+    @property
+    def shape(self) -> tuple:
+        return self.node.ttype.shape
+
+    def __add__(self, o): return _bin("add", self, o)
+    def __radd__(self, o): return _bin("add", o, self)
+    def __sub__(self, o): return _bin("sub", self, o)
+    def __rsub__(self, o): return _bin("sub", o, self)
+    def __mul__(self, o): return _bin("mul", self, o)
+    def __rmul__(self, o): return _bin("mul", o, self)
+    def __truediv__(self, o): return _bin("div", self, o)
+    def __rtruediv__(self, o): return _bin("div", o, self)
+    def __neg__(self): return Value(make("neg", (_projected(self.node),)))
+    def __pos__(self): return self
+    def __abs__(self): return Value(make("abs", (_projected(self.node),)))
+
+    def __pow__(self, p):
+        if isinstance(p, int) and not isinstance(p, bool) and 1 <= p <= 8:
+            out = self
+            for _ in range(p - 1):
+                out = out * self
+            return out
+        raise HawkError("x ** p is written for a literal integer 1 <= p <= 8 in this build "
+                        "(repeated products); use hawk.math.exp/log for other powers")
+
+    def __lt__(self, o): return _bin("lt", self, o)
+    def __le__(self, o): return _bin("le", self, o)
+    def __gt__(self, o): return _bin("gt", self, o)
+    def __ge__(self, o): return _bin("ge", self, o)
+
+    def __matmul__(self, o):
+        a, b = _projected(self.node), _projected(node_of(o))
+        kind = "mm" if len(b.ttype.shape) == 2 else "mv"
+        return Value(make(kind, (a, b)))
+
+    def __rmatmul__(self, o):
+        return Value(node_of(o)) @ self
+
+    @property
+    def T(self) -> Value:
+        return Value(make("transpose", (_projected(self.node),)))
+
+    def __getitem__(self, k) -> Value:
+        n = _projected(self.node)
+        if isinstance(k, Value):
+            raise HawkError("a component read at a runtime index is not in this build; "
+                            "index with a literal int")
+        if isinstance(k, tuple) and all(isinstance(i, int) for i in k):
+            return Value(make("component", (n,), tuple(k)))
+        if isinstance(k, int):
+            if len(n.ttype.shape) == 2:
+                r, c = n.ttype.shape
+                return Value(make("vec", tuple(make("component", (n,), (k, j)) for j in range(c))))
+            return Value(make("component", (n,), k))
+        raise HawkError(f"index {k!r}: a value is indexed by literal ints")
+
+    def __len__(self) -> int:
+        if not self.shape:
+            raise HawkError("a scalar has no length")
+        return self.shape[0]
+
+    def __bool__(self):
+        raise HawkError("a traced value has no Python truth value: a branch on a per-sample value "
+                        "is written hawk.math.where(cond, a, b)")
+
+    def __iter__(self):
+        if not self.shape:
+            raise HawkError("a scalar is not iterable")
+        return (self[i] for i in range(self.shape[0]))
+
+    def __repr__(self) -> str:
+        return f"Value({self.node!r})"
+
+
+class MutableRef(Value):
+    """A ``Mutable`` parameter before it is assigned: reading it reads the
+    value the plane held when the launch began."""
+
+    __slots__ = ("name",)
+
+    def __init__(self, name: str, ttype: TensorType):
+        super().__init__(ir.leaf("mutable", name, ttype))
+        self.name = name
+
+
+class Reduced:
+    """The result of ``hawk.sum``: one value for the whole run.  It can be
+    committed (assigned to a ``Mutable`` or returned), not read back."""
+
+    def __init__(self, node: Node, policy: str):
+        self.node = node
+        self.policy = policy
+
+    def _refuse(self, *_):
+        raise HawkError("a value reduced over every sample (hawk.sum) is read back in the body: "
+                        "that needs a stage boundary this build does not cut; assign it to a "
+                        "Mutable (or return it) instead")
+
+    __add__ = __radd__ = __sub__ = __rsub__ = __mul__ = __rmul__ = _refuse
+    __truediv__ = __rtruediv__ = __neg__ = __getitem__ = _refuse
+
+
+# --------------------------------------------------------------------------
+# cross-sample vocabulary
+
+
+class _Trace:
+    """The sinks a kernel body records while it is traced."""
+
+    stack: list = []
+
+    def __init__(self):
+        self.sinks: list = []
+
+    def __enter__(self):
+        _Trace.stack.append(self)
+        return self
+
+    def __exit__(self, *exc):
+        _Trace.stack.pop()
+
+    @classmethod
+    def current(cls, where: str) -> _Trace:
+        if not cls.stack:
+            raise HawkError(f"{where} is written inside a @hawk.kernel body")
+        return cls.stack[-1]
+
+
+def sum(x: Any, policy: str = "auto") -> Reduced:  # noqa: A001 - hawk's spelling
+    """The sum of ``x`` over every sample of the run (reference
+    ``hawk/trace/reduce.py:277-287``).  ``policy="ordered"`` adds in a fixed
+    tree that depends on the sample count only: 65536 virtual lanes, each
+    adding its rows in order, folded in groups of 1024 by a halving tree and
+    the 64 group results by the same tree — the same bits on every launch."""
+    if policy not in SUM_POLICIES:
+        raise HawkError(f"hawk.sum(x, policy={policy!r}): policy={policy!r} is not one of {SUM_POLICIES}")
+    if policy != "ordered":
+        raise HawkError(f"hawk.sum(x, policy={policy!r}): the hip target builds policy='ordered' "
+                        "(the fixed tree); the compensated row sums are not in this build")
+    n = _projected(node_of(x))
+    if n.ttype.shape:
+        raise HawkError("hawk.sum over samples of a vector or matrix is not in this build; "
+                        "sum each component")
+    return Reduced(n, policy)
+
+
+class _Stored:
+    """What ``hawk.scatter(y)[key] += v`` leaves in the statement's target."""
+
+
+class _ScatterSlot:
+    def __init__(self, target: _ScatterTarget, key: Any):
+        self.target, self.key = target, key
+
+    def __iadd__(self, value: Any) -> _Stored:
+        t = self.target
+        key = node_of(self.key) if isinstance(self.key, Value) else None
+        if key is None or key.ttype.dtype != "i32" or key.kind != "leaf":
+            raise HawkError(f"hawk.scatter({t.name})[key] += v: the key is an Index plane in this build")
+        v = _projected(node_of(value))
+        if v.ttype.shape:
+            raise HawkError(f"hawk.scatter({t.name}, policy='ordered') adds a scalar payload in this build")
+        _Trace.current("hawk.scatter").sinks.append(AccumWrite(t.name, v, key, t.policy))
+        return _Stored()
+
+
+class _ScatterTarget:
+    def __init__(self, ref: MutableRef, policy: str):
+        self.name, self.policy = ref.name, policy
+
+    def __getitem__(self, key) -> _ScatterSlot:
+        return _ScatterSlot(self, key)
+
+    def __setitem__(self, key, value) -> None:
+        if not isinstance(value, _Stored):
+            raise HawkError(f"hawk.scatter({self.name})[key] = v (a keyed store) is not in this build; "
+                            "hawk.scatter(y, policy='ordered')[key] += v is")
+
+
+def scatter(sink: Any, policy: str = "auto") -> _ScatterTarget:
+    """``hawk.scatter(sink, policy="ordered")[key] += v`` adds ``v`` into the
+    plane ``sink`` at ``key`` with no atomics: lanes are cut into chunks
+    (``clamp(N // cells, 1, 256)``), each chunk adds its lanes in order into
+    its own partial of every key, and each cell adds its partials in chunk
+    order (reference ``hawk/trace/reduce.py:383-402``).  Key -1 adds nothing;
+    another key outside the plane is reported by name after the run."""
+    if not isinstance(sink, MutableRef):
+        raise HawkError("hawk.scatter(y): y is a Mutable parameter of the kernel")
+    if policy not in SCATTER_POLICIES:
+        raise HawkError(f"hawk.scatter({sink.name}, policy={policy!r}): the hip target builds "
+                        "policy='ordered' (no atomics, the serial walk's bits)")
+    return _ScatterTarget(sink, policy)
+
+
+# --------------------------------------------------------------------------
+# loops
+
+
+def _for(bounds: tuple, body, inits: tuple, names: tuple):
+    """The rolled loop the ast pass made of ``for k in range(*bounds)``."""
+    if not all(isinstance(b, int) and not isinstance(b, bool) for b in bounds):
+        raise HawkError(f"for ... in range{bounds!r}: a loop's trip count is a literal int "
+                        "(the body is emitted once, rolled)")
+    rng = range(*bounds)
+    if len(rng) == 0:
+        return tuple(inits)
+    init_nodes = []
+    for name, x in zip(names, inits):
+        if isinstance(x, Reduced):
+            raise HawkError(f"{name!r}: a hawk.sum result cannot be carried through a loop")
+        if isinstance(x, MutableRef):
+            init_nodes.append(x.node)
+        else:
+            init_nodes.append(_projected(node_of(x)))
+    marker = len(_Trace.current("a for loop").sinks)
+
+    def traced(index: Node, *carries: Node):
+        out = body(Value(index), *[Value(c) for c in carries])
+        return tuple(_projected(node_of(v)) for v in out)
+
+    loop = ir.new_loop(len(rng), rng.start, rng.step, tuple(init_nodes), traced, tuple(names))
+    if len(_Trace.current("a for loop").sinks) != marker:
+        raise HawkError("hawk.scatter inside a for loop is not in this build")
+    return tuple(Value(ir.loop_value(loop, j)) for j in range(len(names)))
+
+
+def _exit(ret, finals: dict):
+    return ret, finals
+
+
+# --------------------------------------------------------------------------
+# the ast pass
+
+
+def _stored_names(nodes) -> list:
+    """Names bound by the statements ``nodes`` (nested defs excluded), in order."""
+    out = []
+
+    class V(ast.NodeVisitor):
+        def visit_Name(self, n):
+            if isinstance(n.ctx, ast.Store) and n.id not in out:
+                out.append(n.id)
+
+        def visit_FunctionDef(self, n):
+            pass
+
+        visit_AsyncFunctionDef = visit_FunctionDef
+        visit_Lambda = visit_FunctionDef
+
+    for st in nodes:
+        V().visit(st)
+    return out
+
+
+class _Rewriter:
+    def __init__(self, mutables: tuple):
+        self.mutables = mutables
+        self.count = 0
+
+    def exit_call(self, value) -> ast.expr:
+        finals = ast.Dict(keys=[ast.Constant(m) for m in self.mutables],
+                          values=[ast.Name(m, ast.Load()) for m in self.mutables])
+        return ast.Call(ast.Name("__hawk_exit__", ast.Load()), [value or ast.Constant(None), finals], [])
+
+    def block(self, stmts: list, defined: set, in_loop: bool) -> list:
+        out = []
+        for st in stmts:
+            if isinstance(st, ast.For):
+                out.extend(self.loop(st, defined))
+                defined |= set(_stored_names([st]))
+                continue
+            if isinstance(st, ast.Return):
+                if in_loop:
+                    raise HawkError("return inside a for loop of a kernel body")
+                out.append(ast.Return(self.exit_call(st.value)))
+                continue
+            if isinstance(st, (ast.While, ast.Break, ast.Continue)):
+                raise HawkError(f"{type(st).__name__.lower()} is not in this build's kernel language; "
+                                "loops are for ... in range(<int>)")
+            if isinstance(st, ast.If):
+                st.body = self.block(st.body, set(defined), in_loop)
+                st.orelse = self.block(st.orelse, set(defined), in_loop)
+            out.append(st)
+            defined |= set(_stored_names([st]))
+        return out
+
+    def loop(self, st: ast.For, defined: set) -> list:
+        it = st.iter
+        if not (isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range"):
+            st.body = self.block(st.body, set(defined), True)
+            return [st]           # a Python-level loop over a static sequence: unrolled at trace
+        if st.orelse:
+            raise HawkError("for ... else is not in the kernel language")
+        if not isinstance(st.target, ast.Name):
+            raise HawkError("a rolled loop binds one index name: for k in range(...)")
+        index = st.target.id
+        carried = [n for n in _stored_names(st.body) if n in defined and n != index]
+        body = self.block(st.body, set(defined) | {index}, True)
+        self.count += 1
+        fname = f"__hawk_body_{self.count}"
+        fdef = ast.FunctionDef(
+            name=fname,
+            args=ast.arguments(posonlyargs=[], args=[ast.arg(index)] + [ast.arg(c) for c in carried],
+                               vararg=None, kwonlyargs=[], kw_defaults=[], kwarg=None, defaults=[]),
+            body=body + [ast.Return(ast.Tuple([ast.Name(c, ast.Load()) for c in carried], ast.Load()))],
+            decorator_list=[], returns=None, type_comment=None)
+        call = ast.Call(ast.Name("__hawk_for__", ast.Load()),
+                        [ast.Tuple(list(it.args), ast.Load()), ast.Name(fname, ast.Load()),
+                         ast.Tuple([ast.Name(c, ast.Load()) for c in carried], ast.Load()),
+                         ast.Tuple([ast.Constant(c) for c in carried], ast.Load())], [])
+        if carried:
+            assign = ast.Assign(targets=[ast.Tuple([ast.Name(c, ast.Store()) for c in carried], ast.Store())],
+                                value=call)
+        else:
+            assign = ast.Expr(call)
+        return [ast.copy_location(fdef, st), ast.copy_location(assign, st)]
+
+
+def _rewritten(fn, mutables: tuple):
+    try:
+        source = textwrap.dedent(inspect.getsource(fn))
+    except (OSError, TypeError) as exc:
+        raise HawkError(f"@hawk.kernel needs the source of {fn.__name__!r} to trace it: {exc}") from None
+    tree = ast.parse(source)
+    fdef = tree.body[0]
+    if not isinstance(fdef, ast.FunctionDef):
+        raise HawkError("@hawk.kernel decorates a def")
+    fdef.decorator_list = []
+    fdef.returns = None
+    for a in fdef.args.args:
+        a.annotation = None
+    rw = _Rewriter(mutables)
+    params = {a.arg for a in fdef.args.args}
+    fdef.body = rw.block(fdef.body, set(params), False) + [ast.Return(rw.exit_call(None))]
+    ast.fix_missing_locations(tree)
+    first = fn.__code__.co_firstlineno
+    ast.increment_lineno(tree, first - 1)
+    code = compile(tree, inspect.getsourcefile(fn) or "<kernel>", "exec")
+    ns = dict(fn.__globals__)
+    if fn.__closure__:
+        for name, cell in zip(fn.__code__.co_freevars, fn.__closure__):
+            ns[name] = cell.cell_contents
+    ns["__hawk_for__"] = _for
+    ns["__hawk_exit__"] = _exit
+    exec(code, ns)
+    return ns[fdef.name]
+
+
+def _annotation(fn, raw, ns):
+    if isinstance(raw, str):
+        try:
+            return eval(raw, ns)  # noqa: S307 - the kernel author's own annotation text
+        except Exception as exc:
+            raise HawkError(f"{fn.__name__}: cannot read the annotation {raw!r}: {exc}") from None
+    return raw
+
+
+def trace(fn) -> Program:
+    """Trace ``fn`` into a :class:`~hawk_amd.ir.Program`."""
+    ns = dict(fn.__globals__)
+    if fn.__closure__:
+        for name, cell in zip(fn.__code__.co_freevars, fn.__closure__):
+            ns[name] = cell.cell_contents
+    sig = inspect.signature(fn)
+    program = Program()
+    args, mutables = [], []
+    for p in sig.parameters.values():
+        if p.kind not in (p.POSITIONAL_ONLY, p.POSITIONAL_OR_KEYWORD):
+            raise HawkError(f"{fn.__name__}: parameter {p.name!r} must be a plain positional parameter")
+        ann = _annotation(fn, p.annotation, ns)
+        if ann is inspect.Parameter.empty:
+            raise HawkError(f"{fn.__name__}: parameter {p.name!r} has no declaration "
+                            "(Scalar, Vector[n], Matrix[r, c], Index, Param, Mutable[...])")
+        if isinstance(ann, MutableDecl):
+            program.decls[p.name] = Decl(p.name, "mutable", ann.ttype)
+            args.append(MutableRef(p.name, ann.ttype))
+            mutables.append(p.name)
+        elif isinstance(ann, _ParamDecl):
+            program.decls[p.name] = Decl(p.name, "uniform", TensorType((), "f64"))
+            args.append(Value(ir.leaf("uniform", p.name, TensorType((), "f64"))))
+        elif isinstance(ann, TensorType):
+            role = role_of(ann)
+            program.decls[p.name] = Decl(p.name, role, ann)
+            args.append(Value(ir.leaf(role, p.name, ann)))
+        else:
+            raise HawkError(f"{fn.__name__}: parameter {p.name!r} is declared {ann!r}, which is not "
+                            "Scalar, Vector[n], Matrix[r, c], Index, Param or Mutable[...]")
+    body = _rewritten(fn, tuple(mutables))
+    with _Trace() as tr:
+        ret, finals = body(*args)
+    sinks = list(tr.sinks)
+    for name in mutables:
+        final = finals[name]
+        decl = program.decls[name]
+        if isinstance(final, MutableRef) and final.name == name:
+            continue                      # never assigned per lane (a scatter target, or unused)
+        if isinstance(final, Reduced):
+            if decl.ttype.shape:
+                raise HawkError(f"{name!r}: hawk.sum commits a scalar cell; declare Mutable[Scalar]")
+            sinks.append(SampleSum(name, final.node, final.policy))
+            continue
+        node = _projected(node_of(final))
+        if node.ttype.shape != decl.ttype.shape:
+            if node.ttype.shape == ():
+                node = make("splat", (node,), decl.ttype.shape)
+            else:
+                raise HawkError(f"{name!r} is declared {decl.ttype.shape or 'scalar'} but assigned a value "
+                                f"of shape {node.ttype.shape}")
+        sinks.append(Assign(name, ir.as_real(node), "mutable"))
+    if ret is not None:
+        ret_ann = _annotation(fn, sig.return_annotation, ns)
+        if isinstance(ret, Reduced):
+            program.decls["out"] = Decl("out", "mutable", TensorType((), "f64"))
+            sinks.append(SampleSum("out", ret.node, ret.policy))
+        else:
+            node = ir.as_real(_projected(node_of(ret)))
+            if isinstance(ret_ann, TensorType) and ret_ann.shape != node.ttype.shape:
+                if node.ttype.shape == ():
+                    node = make("splat", (node,), ret_ann.shape)
+                else:
+                    raise HawkError(f"{fn.__name__} returns shape {node.ttype.shape}, annotated {ret_ann.shape}")
+            program.decls["out"] = Decl("out", "out", node.ttype)
+            sinks.append(Assign("out", node, "out"))
+    if not sinks:
+        raise HawkError(f"{fn.__name__}: the kernel commits nothing (assign a Mutable, return a value, "
+                        "or hawk.scatter into one)")
+    names = [s.name for s in sinks if not isinstance(s, AccumWrite)]
+    dup = sorted({n for n in names if names.count(n) > 1})
+    if dup:
+        raise HawkError(f"{fn.__name__}: {dup} are committed twice")
+    program.sinks = sinks
+    return program
+
+
+class Kernel:
+    """A traced kernel (or a derivative of one): a name and its
+    :class:`~hawk_amd.ir.Program`.  ``Kernel("energy_vjp", vjp(energy, wrt=("v",)))``
+    names a derivative, as the reference spells it (``README.md:75``)."""
+
+    def __init__(self, name: str, program):
+        if callable(program) and not isinstance(program, Program):
+            program = trace(program)
+        if not isinstance(program, Program):
+            raise HawkError(f"Kernel({name!r}, ...) takes a traced program (vjp/jvp's result) or a function")
+        if not name.isidentifier():
+            raise HawkError(f"kernel name {name!r} is not an identifier")
+        self.name = name
+        self.program = program
+
+    @property
+    def decls(self) -> dict:
+        return self.program.decls
+
+    @property
+    def sinks(self) -> list:
+        return self.program.sinks
+
+    def __repr__(self) -> str:
+        return f"<hawk kernel {self.name}: {[type(s).__name__ + ':' + s.name for s in self.sinks]}>"
+
+
+def kernel(fn=None, *, name: str | None = None):
+    """``@hawk.kernel``: trace a per-sample function into a :class:`Kernel`."""
+    def wrap(f):
+        return Kernel(name or f.__name__, trace(f))
+    return wrap(fn) if fn is not None else wrap

@@ -1,0 +1,186 @@
+/* hawk_core.h — the C-ABI of hawk's MI355X (gfx950) device target.
+ *
+ * This library replaces the reference's nanobind module `hawk._core`
+ * (reference `src/hawk_core.cpp:518-679`) with a plain C ABI that any FFI
+ * (Python ctypes here) can bind: every argument is a pointer, a size or a
+ * scalar, and no PyTorch or Python type crosses it.  Device planes are passed
+ * as raw HIP device pointers (`torch.Tensor.data_ptr()` on the Python side).
+ *
+ * Every call returns HK_OK (0) or a non-zero HK_E* code; on failure the
+ * thread-local text returned by hk_last_error() names the field, slot or
+ * argument at fault, with the same wording the reference raises as
+ * ValueError / IndexError (reference `src/hawk_core.cpp:152-156`, `:274-302`,
+ * `:360-389`).  Every exported call counts one boundary crossing
+ * (hk_crossings), like the reference's `crossings()` instrument
+ * (reference `src/hawk_core.cpp:97-118`).
+ *
+ * Threading: distinct objects may be used from distinct threads.  One
+ * ArgBlock shared by threads must be serialised by the caller (the Python
+ * runtime holds a per-kernel lock, as reference `hawk/runtime.py:46-53`).
+ */
+#ifndef HAWK_CORE_H
+#define HAWK_CORE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+#define HK_OK 0
+#define HK_EVALUE 1   /* a ValueError in the reference's binding           */
+#define HK_EINDEX 2   /* an IndexError (slot out of range)                  */
+#define HK_EHIP 3     /* a HIP runtime / hipRTC call failed                 */
+#define HK_ESTATUS 4  /* a team stage reported a bad key (status plane)     */
+
+/* The ABI generation every artifact must export as `eagle_abi_tag`
+ * (reference `hawk/_contracts.py:40-92`, `src/hawk_core.cpp:366-374`). */
+#define HK_ABI_TAG "aether-abi/2"
+
+/* Field order of the exported `eagle_layout_sizes[5]` table:
+ * GRefMirror (40), ScalarHandle (32), IntHandle (32), index_t (8),
+ * PartitionTriple (24) (reference `hawk/artifact/layout.py:35-61`). */
+#define HK_LAYOUT_FIELDS 5
+
+/* DLPack device codes a mirror carries: CPU = 1, ROCm = 10. */
+#define HK_DEVICE_CPU 1
+#define HK_DEVICE_ROCM 10
+
+typedef struct hk_library hk_library;   /* a loaded gfx950 code object */
+typedef struct hk_entry hk_entry;       /* one __global__ entry of it  */
+typedef struct hk_argblock hk_argblock; /* the by-value mirror block   */
+
+/* ---- diagnostics / self-check ------------------------------------------- */
+
+/* Thread-local text of the last failure on this thread ("" if none). */
+const char* hk_last_error(void);
+
+/* Replaces `_core.layout_sizes()` (reference `src/hawk_core.cpp:536-541`):
+ * this library's own sizes, in the field order above. */
+int hk_layout_sizes(uint64_t out[HK_LAYOUT_FIELDS]);
+
+/* Replaces `_core.layout_field_name(i)` (reference `src/hawk_core.cpp:543`). */
+const char* hk_layout_field_name(int i);
+
+/* Replaces `_core.build_digest()` (reference `src/hawk_core.cpp:522-529`):
+ * the sha256 of this library's sources, stamped at build. */
+const char* hk_build_digest(void);
+
+/* Replaces `_core.build_info()` (reference `src/hawk_core.cpp:544-559`):
+ * "key=value" lines (compiler, flags, offload arch, abi tag, index width). */
+const char* hk_build_info(void);
+
+/* Replaces `_core.crossings()` (reference `src/hawk_core.cpp:561-567`). */
+uint64_t hk_crossings(void);
+
+/* ---- build: hipRTC pinned to gfx950 -------------------------------------- */
+
+/* Compile `source` (HIP C++) with hipRTC for --offload-arch=gfx950 plus the
+ * given extra options.  On success *code / *code_size hold a malloc'ed code
+ * object (free with hk_free).  *log (may be NULL) receives the compiler log,
+ * malloc'ed, on success and failure.  Replaces the NVRTC route of reference
+ * `hawk/compile/nvrtc.py:479-582`. */
+int hk_rtc_compile(const char* source, const char* name,
+                   const char* const* options, int n_options,
+                   void** code, size_t* code_size, char** log);
+
+/* The hipRTC version as major*100+minor (part of the compile-cache key). */
+int hk_rtc_version(void);
+
+void hk_free(void* p);
+
+/* ---- load: module + ABI self-check -------------------------------------- */
+
+/* Load a gfx950 code object and check its exported `eagle_abi_tag` and
+ * `eagle_layout_sizes` against this library, refusing a mismatch by naming
+ * the field.  Replaces `_core.HostLibrary(path)` (reference
+ * `src/hawk_core.cpp:354-390`). */
+int hk_load(const void* code, size_t code_size, hk_library** out);
+void hk_unload(hk_library* lib);
+
+/* Resolve one __global__ entry.  Replaces `HostLibrary.entry(name)`
+ * (reference `src/hawk_core.cpp:395-401`). */
+int hk_entry_get(hk_library* lib, const char* name, hk_entry** out);
+
+/* ---- bind: the by-value mirror block ------------------------------------ */
+
+/* One kind name per slot, in arg_spec order: "gref" (40 B GRefMirror),
+ * "handle" / "int_handle" (32 B), "f64" / "f32" / "int" / "nsamples"
+ * (by value).  Replaces `_core.ArgBlock(descriptor)` (reference
+ * `src/hawk_core.cpp:185-215`). */
+int hk_argblock_new(const char* const* kinds, int n_slots, hk_argblock** out);
+void hk_argblock_free(hk_argblock* ab);
+int hk_argblock_size(const hk_argblock* ab);
+
+/* Write ONE slot's mirror.  For a by-value slot `ptr` is the ADDRESS of the
+ * value, which is copied.  A GRef plane's component pitch is
+ * samples*stride.  Replaces `ArgBlock.bind` (reference
+ * `src/hawk_core.cpp:228-267`). */
+int hk_bind(hk_argblock* ab, int slot, uint64_t ptr, uint64_t samples,
+            uint64_t stride, int32_t device_type, int32_t device_id);
+
+/* The bulk pointer swap: `n` (slot, ptr) pairs in one crossing.  A by-value
+ * slot is refused.  Replaces `ArgBlock.rebind` (reference
+ * `src/hawk_core.cpp:270-305`). */
+int hk_rebind(hk_argblock* ab, const int64_t* slots, const int64_t* ptrs,
+              size_t n);
+
+/* ---- launch ------------------------------------------------------------ */
+
+/* Launch `entry` over samples [base, base+count) of n_samples on `stream`
+ * (a hipStream_t, NULL = default stream): ceil(count/(block*per_thread))
+ * workgroups of `block` threads, each thread taking `per_thread` samples.
+ * Replaces `HostEntry.run(argblock, base, count, n_samples)` (reference
+ * `src/hawk_core.cpp:438-442`); the device entry signature is
+ * `(mirrors..., long long base, long long count, long long nSamples)` as
+ * reference `hawk/emit/cuda.py:46-54`. */
+int hk_launch(const hk_entry* entry, const hk_argblock* ab, int64_t base,
+              int64_t count, int64_t n_samples, uint32_t block,
+              uint32_t per_thread, void* stream);
+
+/* Launch `entry` on exactly `grid` workgroups of `block` threads with the
+ * triple (base, count, n_samples) — the virtual-lane form of a fused
+ * ordered-sum stage, whose grid is fixed by the sum, not by count. */
+int hk_launch_grid(const hk_entry* entry, const hk_argblock* ab, int64_t base,
+                   int64_t count, int64_t n_samples, uint32_t grid,
+                   uint32_t block, void* stream);
+
+/* ---- team stages: hand-written gfx950 kernels --------------------------- */
+
+/* The fixed-tree ordered sum of reference `hawk/emit/team.py:208-278`
+ * (`_block_part`) and `:173-192` (`_block`, gp form): 65536 virtual lanes,
+ * lane l adds u[l], u[l+65536], ... in order from 0; each group of 1024 lanes
+ * is folded by the halving tree s[i] += s[i+w], w = 512..1; the 64 group
+ * values by the same tree, w = 32..1; the result is STORED to *out.
+ * Scratch: hk_ordered_sum_scratch_bytes() bytes, zero before the first call
+ * (each call leaves its counters at zero again). */
+size_t hk_ordered_sum_scratch_bytes(void);
+int hk_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch,
+                       void* stream);
+
+/* The same fold over 65536 lane partials already computed in `lanes`
+ * (the second half of a fused ordered-sum stage). */
+int hk_ordered_fold_f64(const double* lanes, double* out, void* scratch,
+                        void* stream);
+
+/* The keyed ordered scatter of reference `hawk/emit/team.py:322-460`
+ * (`_scatter_zero`, `_scatter_chunks`, `_scatter_cells`) with the chunk rule
+ * of `hawk/_lane_bind.py:111-114`: chunks = clamp(n / cells, 1, 256),
+ * span = ceil(n / chunks); part[key][b] = the in-order sum from 0 of chunk
+ * b's values with that key; target[c] += (sum from 0 over b, in order, of
+ * part[c][b]).  Key -1 adds nothing; any other key outside [0, cells) adds
+ * nothing and sets status[1+b] (status[0] = cells).  Returns HK_OK even when
+ * a bad key was met: read the status plane (hk_scatter_check).
+ * Scratch: hk_ordered_scatter_scratch_bytes(n, cells) bytes. */
+int hk_scatter_chunks(int64_t n, int64_t cells);
+size_t hk_ordered_scatter_scratch_bytes(int64_t n, int64_t cells);
+int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n,
+                           double* target, int64_t cells, void* scratch,
+                           int32_t* status, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HAWK_CORE_H */

@@ -1,0 +1,531 @@
+/* hawk_oracle.c — TEST INFRASTRUCTURE, not product code.
+ *
+ * A plain-C restatement of what hawk's HOST target computes for the five
+ * benchmark kernels, used only as the parity checker (tests/, the smoke
+ * check of __graft_entry__.py) and as the CPU baseline of bench.py.  Nothing
+ * in hawk_amd/ links, loads or calls it.
+ *
+ * It is built the way hawk builds a host .so in its exact `native` profile
+ * (reference hawk/compile/toolchain.py:956-987): gcc -O3 -march=native
+ * -mprefer-vector-width=512 -ffp-contract=off -fno-math-errno, so every
+ * operation below is one IEEE operation and the transcendentals are glibc's
+ * (reference tests/test_math_parity.py:279: host `native` == glibc bit for bit).
+ * The per-sample loops have the host wrapper's shape: a serial loop over
+ * [base, base+count) (reference hawk/emit/host.py:213-217, :1450-1460).
+ *
+ * Planes are component-major [component][sample] (reference
+ * hawk/emit/wrapper.py:1029-1055): component c of sample s at c*n + s.
+ *
+ * How each function is pinned (golden vectors, closed forms, brute force,
+ * finite differences, invariants) is tested in tests/test_oracle.py; every
+ * function here has at least one such check.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define HKO_EXPORT __attribute__((visibility("default")))
+
+/* ---- config 1: scale(x, a, b) = a*x + b ------------------------------------
+ * The kernel `return a * x + b` (reference README.md:44-56): mul then add. */
+HKO_EXPORT void hko_scale(const double* x, double a, double b, double* out,
+                          int64_t base, int64_t count) {
+#pragma GCC ivdep
+    for (int64_t i = base; i < base + count; ++i) out[i] = (a * x[i]) + b;
+}
+
+/* ---- config 2: energy = 0.5 * dot(v, v), its VJP and its JVP ---------------
+ * dot adds its products left to right.  VJP by reference hawk/diff/rules.py:
+ * mul(0.5, d) sends g*0.5 to d, and dot sends (g*0.5)*v to each of its two
+ * operands, accumulated held + new.  JVP: 0.5 * (dot(dv, v) + dot(v, dv)). */
+HKO_EXPORT void hko_energy(const double* v, int64_t n, double* out, int64_t base, int64_t count) {
+#pragma GCC ivdep
+    for (int64_t i = base; i < base + count; ++i) {
+        const double a = v[i], b = v[n + i], c = v[2 * n + i];
+        out[i] = 0.5 * (((a * a) + (b * b)) + (c * c));
+    }
+}
+
+HKO_EXPORT void hko_energy_vjp(const double* v, const double* bar_out, int64_t n, double* bar_v,
+                               int64_t base, int64_t count) {
+#pragma GCC ivdep
+    for (int64_t i = base; i < base + count; ++i) {
+        const double g = bar_out[i] * 0.5;
+        for (int c = 0; c < 3; ++c) {
+            const double t = g * v[c * n + i];
+            bar_v[c * n + i] = t + t;
+        }
+    }
+}
+
+HKO_EXPORT void hko_energy_jvp(const double* v, const double* dv, int64_t n, double* dot_out,
+                               int64_t base, int64_t count) {
+#pragma GCC ivdep
+    for (int64_t i = base; i < base + count; ++i) {
+        const double a = v[i], b = v[n + i], c = v[2 * n + i];
+        const double da = dv[i], db = dv[n + i], dc = dv[2 * n + i];
+        const double d1 = ((da * a) + (db * b)) + (dc * c);
+        const double d2 = ((a * da) + (b * db)) + (c * dc);
+        dot_out[i] = 0.5 * (d1 + d2);
+    }
+}
+
+/* ---- config 5a: the 8-stage chain --------------------------------------- */
+static inline double chain1(double x) {
+    const double t1 = exp(x);
+    const double t2 = sin(t1);
+    const double t3 = (1.5 * t2) + 0.25;
+    const double t4 = tanh(t3);
+    const double t5 = sqrt(fabs(t4) + 1.0);
+    const double t6 = (t5 * t5) - x;
+    const double t7 = exp(-fabs(t6));
+    return (t7 * x) + t4;
+}
+
+HKO_EXPORT void hko_chain(const double* x, double* y, int64_t base, int64_t count) {
+    for (int64_t i = base; i < base + count; ++i) y[i] = chain1(x[i]);
+}
+
+/* The transcendentals one at a time (for ULP tests of the device's). */
+HKO_EXPORT void hko_libm(int which, const double* x, double* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        switch (which) {
+            case 0: y[i] = exp(x[i]); break;
+            case 1: y[i] = sin(x[i]); break;
+            case 2: y[i] = tanh(x[i]); break;
+            case 3: y[i] = sqrt(x[i]); break;
+            case 4: y[i] = cos(x[i]); break;
+            default: y[i] = log(x[i]); break;
+        }
+    }
+}
+
+/* ---- config 5b: the fixed-tree ordered sum --------------------------------
+ * Reference hawk/emit/team.py:208-278 (`_block_part`, host form) and
+ * :173-192 (`_block`, gp form): group g's 1024 lanes accumulate rows
+ * b + t (b = g*1024, g*1024 + 65536, ...) into sh[t] from 0; the halving tree
+ * sh[i] += sh[i+w], w = 512..1, gives gp[g]; the same tree, w = 32..1, over
+ * the 64 gp values gives the sum. */
+#define HKO_V 65536
+#define HKO_W 1024
+#define HKO_G 64
+
+static double group_part(const double* u, int64_t rows, int g) {
+    double sh[HKO_W];
+    for (int t = 0; t < HKO_W; ++t) sh[t] = 0.0;
+    for (int64_t b = (int64_t)g * HKO_W; b < rows; b += HKO_V) {
+        const int64_t m = rows - b < HKO_W ? rows - b : HKO_W;
+        for (int64_t t = 0; t < m; ++t) sh[t] += u[b + t];
+    }
+    for (int w = HKO_W / 2; w > 0; w >>= 1)
+        for (int i = 0; i < w; ++i) sh[i] += sh[i + w];
+    return sh[0];
+}
+
+static double fold_groups(double* gp) {
+    for (int w = HKO_G / 2; w > 0; w >>= 1)
+        for (int i = 0; i < w; ++i) gp[i] += gp[i + w];
+    return gp[0];
+}
+
+HKO_EXPORT double hko_ordered_sum(const double* u, int64_t n) {
+    double gp[HKO_G];
+    for (int g = 0; g < HKO_G; ++g) gp[g] = group_part(u, n, g);
+    return fold_groups(gp);
+}
+
+/* ---- config 5c: the keyed ordered scatter ---------------------------------
+ * Reference hawk/emit/team.py:322-460 and hawk/_lane_bind.py:111-114:
+ * chunks = clamp(n / cells, 1, 256), span = ceil(n / chunks); chunk b walks
+ * its lanes in order, parts[key*chunks + b] += v (from 0); key -1 skipped,
+ * another key outside [0, cells) sets status[1+b]; then each cell adds its
+ * parts in chunk order from 0 and adds that onto target[cell]. */
+HKO_EXPORT int hko_scatter_chunks(int64_t n, int64_t cells) {
+    if (cells <= 0) return 1;
+    const int64_t fit = n / cells;
+    return (int)(fit < 1 ? 1 : (fit > 256 ? 256 : fit));
+}
+
+static void scatter_chunk(const int32_t* key, const double* v, int64_t n, int64_t cells, int chunks,
+                          int b, double* parts, int32_t* status) {
+    const int64_t span = (n + chunks - 1) / chunks;
+    const int64_t lo = (int64_t)b * span;
+    const int64_t hi = lo + span < n ? lo + span : n;
+    for (int64_t r = lo; r < hi; ++r) {
+        const int32_t k = key[r];
+        if (k == -1) continue;
+        if (k >= 0 && k < cells) parts[(int64_t)k * chunks + b] += v[r];
+        else status[1 + b] = 1;
+    }
+}
+
+static void scatter_cells(const double* parts, int64_t c_lo, int64_t c_hi, int chunks, double* target) {
+    for (int64_t c = c_lo; c < c_hi; ++c) {
+        double s = 0.0;
+        for (int b = 0; b < chunks; ++b) s += parts[c * chunks + b];
+        target[c] += s;
+    }
+}
+
+/* parts: chunks*cells doubles of scratch; status: 257 int32. */
+HKO_EXPORT void hko_ordered_scatter(const int32_t* key, const double* v, int64_t n, double* target,
+                                    int64_t cells, double* parts, int32_t* status) {
+    if (cells <= 0) return;
+    const int chunks = hko_scatter_chunks(n, cells);
+    memset(parts, 0, sizeof(double) * (size_t)chunks * (size_t)cells);
+    status[0] = (int32_t)cells;
+    for (int b = 0; b < 256; ++b) status[1 + b] = 0;
+    for (int b = 0; b < chunks; ++b) scatter_chunk(key, v, n, cells, chunks, b, parts, status);
+    scatter_cells(parts, 0, cells, chunks, target);
+}
+
+/* ---- config 3: two-body leapfrog, 32 kick-drift-kick substeps ------------
+ * The kernel (tests/kernels.py `twobody`):
+ *   r2 = dot(r, r); a = (-mu / (r2 * sqrt(r2))) * r
+ *   vh = v + (0.5*dt) * a; r = r + dt * vh
+ *   r2 = dot(r, r); a = (-mu / (r2 * sqrt(r2))) * r; v = vh + (0.5*dt) * a */
+#define HKO_STEPS 32
+#define HKO_DT 1e-3
+
+static inline void accel(const double r[3], double mu, double a[3]) {
+    const double r2 = ((r[0] * r[0]) + (r[1] * r[1])) + (r[2] * r[2]);
+    const double s = -mu / (r2 * sqrt(r2));
+    for (int c = 0; c < 3; ++c) a[c] = s * r[c];
+}
+
+static inline void substep(double r[3], double v[3], double mu) {
+    double a[3], vh[3];
+    accel(r, mu, a);
+    for (int c = 0; c < 3; ++c) vh[c] = v[c] + ((0.5 * HKO_DT) * a[c]);
+    for (int c = 0; c < 3; ++c) r[c] = r[c] + (HKO_DT * vh[c]);
+    accel(r, mu, a);
+    for (int c = 0; c < 3; ++c) v[c] = vh[c] + ((0.5 * HKO_DT) * a[c]);
+}
+
+HKO_EXPORT void hko_twobody(const double* r0, const double* v0, double mu, int64_t n, double* r_out,
+                            double* v_out, int64_t base, int64_t count) {
+    for (int64_t i = base; i < base + count; ++i) {
+        double r[3], v[3];
+        for (int c = 0; c < 3; ++c) { r[c] = r0[c * n + i]; v[c] = v0[c * n + i]; }
+        for (int k = 0; k < HKO_STEPS; ++k) substep(r, v, mu);
+        for (int c = 0; c < 3; ++c) { r_out[c * n + i] = r[c]; v_out[c * n + i] = v[c]; }
+    }
+}
+
+/* The adjoint of a = s * r with s = -mu / (r2 * sqrt(r2)), r2 = dot(r, r):
+ * given g = bar_a, accumulate into bar_r (held + new, in the reverse order of
+ * the forward operations: the product's term, then the dot's two).
+ * Rules of reference hawk/diff/rules.py:
+ * mul(s, r): s gets sum(g*r), r gets g*s; div(-mu, q): q gets -(gs*s)/q;
+ * mul(r2, sq): r2 gets gq*sq, sq gets gq*r2; sqrt: r2 gets gsq*(0.5/sq);
+ * dot(r, r): r gets gr2*r twice. */
+static inline void accel_vjp(const double r[3], double mu, const double g[3], double bar_r[3]) {
+    const double r2 = ((r[0] * r[0]) + (r[1] * r[1])) + (r[2] * r[2]);
+    const double sq = sqrt(r2);
+    const double q = r2 * sq;
+    const double s = -mu / q;
+    const double gs = ((g[0] * r[0]) + (g[1] * r[1])) + (g[2] * r[2]);
+    const double gq = -((gs * s) / q);
+    const double gr2 = (gq * sq) + ((gq * r2) * (0.5 / sq));
+    for (int c = 0; c < 3; ++c) bar_r[c] = ((bar_r[c] + (g[c] * s)) + (gr2 * r[c])) + (gr2 * r[c]);
+}
+
+/* Reverse of one substep from its start state (r, v) (replayed from the
+ * tape): incoming (br, bv) are the adjoints of the substep's outputs and are
+ * replaced by the adjoints of its inputs. */
+static inline void substep_vjp(const double r_in[3], const double v_in[3], double mu, double br[3],
+                               double bv[3]) {
+    double a[3], vh[3], r1[3];
+    accel(r_in, mu, a);
+    for (int c = 0; c < 3; ++c) vh[c] = v_in[c] + ((0.5 * HKO_DT) * a[c]);
+    for (int c = 0; c < 3; ++c) r1[c] = r_in[c] + (HKO_DT * vh[c]);
+    /* v_out = vh + (0.5 dt) a(r1) */
+    double bvh[3], ba1[3], br1[3];
+    for (int c = 0; c < 3; ++c) { bvh[c] = bv[c]; ba1[c] = bv[c] * (0.5 * HKO_DT); br1[c] = br[c]; }
+    accel_vjp(r1, mu, ba1, br1);
+    /* r1 = r + dt * vh */
+    double brn[3];
+    for (int c = 0; c < 3; ++c) { brn[c] = br1[c]; bvh[c] += br1[c] * HKO_DT; }
+    /* vh = v + (0.5 dt) a(r) */
+    double ba0[3];
+    for (int c = 0; c < 3; ++c) { bv[c] = bvh[c]; ba0[c] = bvh[c] * (0.5 * HKO_DT); }
+    accel_vjp(r_in, mu, ba0, brn);
+    for (int c = 0; c < 3; ++c) br[c] = brn[c];
+}
+
+HKO_EXPORT void hko_twobody_vjp(const double* r0, const double* v0, double mu, const double* bar_r,
+                                const double* bar_v, int64_t n, double* bar_r0, double* bar_v0,
+                                int64_t base, int64_t count) {
+    for (int64_t i = base; i < base + count; ++i) {
+        double tr[HKO_STEPS][3], tv[HKO_STEPS][3], r[3], v[3], br[3], bv[3];
+        for (int c = 0; c < 3; ++c) { r[c] = r0[c * n + i]; v[c] = v0[c * n + i]; }
+        for (int k = 0; k < HKO_STEPS; ++k) {
+            for (int c = 0; c < 3; ++c) { tr[k][c] = r[c]; tv[k][c] = v[c]; }
+            substep(r, v, mu);
+        }
+        for (int c = 0; c < 3; ++c) { br[c] = bar_r[c * n + i]; bv[c] = bar_v[c * n + i]; }
+        for (int k = HKO_STEPS - 1; k >= 0; --k) substep_vjp(tr[k], tv[k], mu, br, bv);
+        for (int c = 0; c < 3; ++c) { bar_r0[c * n + i] = br[c]; bar_v0[c * n + i] = bv[c]; }
+    }
+}
+
+/* ---- config 4a: 6x6 SPD Cholesky solve and its VJP -------------------------
+ * Factor and solve in the operation order of reference
+ * hawk/embedded/linalg.py:233-271 (`_chol`: the symmetrised entry
+ * (0.5*a_ij) + (0.5*a_ji), row-ordered dot updates) and :443-536 (`_dot_rows`:
+ * forward rows ascending, backward rows descending, each acc = src - sum in
+ * column order, then / diagonal).  info != 0 gives zeros.
+ * VJP (reference hawk/diff/linalg_rules.py:230-233): lam = cho_solve(L, bar_x);
+ * bar_b = lam; bar_A = -((outer(lam, x) + outer(lam, x)^T) * 0.5). */
+#define HKO_N 6
+
+static int chol6(const double a[HKO_N][HKO_N], double l[HKO_N][HKO_N]) {
+    int info = 0;
+    for (int i = 0; i < HKO_N; ++i)
+        for (int c = 0; c < HKO_N; ++c) l[i][c] = 0.0;
+    for (int j = 0; j < HKO_N; ++j) {
+        if (info != 0) continue;
+        double d = (0.5 * a[j][j]) + (0.5 * a[j][j]);
+        for (int k = 0; k < j; ++k) d = d - (l[j][k] * l[j][k]);
+        if (d > 0.0) {
+            const double ljj = sqrt(d);
+            l[j][j] = ljj;
+            for (int i = j + 1; i < HKO_N; ++i) {
+                double acc = (0.5 * a[i][j]) + (0.5 * a[j][i]);
+                for (int k = 0; k < j; ++k) acc = acc - (l[i][k] * l[j][k]);
+                l[i][j] = acc / ljj;
+            }
+        } else {
+            info = j + 1;
+        }
+    }
+    return info;
+}
+
+static void cho_solve6(const double l[HKO_N][HKO_N], int info, const double b[HKO_N], double x[HKO_N]) {
+    if (info != 0) {
+        for (int i = 0; i < HKO_N; ++i) x[i] = 0.0;
+        return;
+    }
+    for (int i = 0; i < HKO_N; ++i) {
+        double acc = b[i];
+        for (int j = 0; j < i; ++j) acc = acc - (l[i][j] * x[j]);
+        x[i] = acc / l[i][i];
+    }
+    for (int r = 0; r < HKO_N; ++r) {
+        const int i = HKO_N - 1 - r;
+        double acc = x[i];
+        for (int j = i + 1; j < HKO_N; ++j) acc = acc - (l[j][i] * x[j]);
+        x[i] = acc / l[i][i];
+    }
+}
+
+static void load6(const double* A, const double* b, int64_t n, int64_t i, double a[HKO_N][HKO_N],
+                  double bb[HKO_N]) {
+    for (int r = 0; r < HKO_N; ++r) {
+        for (int c = 0; c < HKO_N; ++c) a[r][c] = A[(r * HKO_N + c) * n + i];
+        bb[r] = b[r * n + i];
+    }
+}
+
+HKO_EXPORT void hko_spd_solve(const double* A, const double* b, int64_t n, double* x_out, int64_t base,
+                              int64_t count) {
+    for (int64_t i = base; i < base + count; ++i) {
+        double a[HKO_N][HKO_N], l[HKO_N][HKO_N], bb[HKO_N], x[HKO_N];
+        load6(A, b, n, i, a, bb);
+        const int info = chol6(a, l);
+        cho_solve6(l, info, bb, x);
+        for (int r = 0; r < HKO_N; ++r) x_out[r * n + i] = x[r];
+    }
+}
+
+HKO_EXPORT void hko_spd_solve_vjp(const double* A, const double* b, const double* bar_x, int64_t n,
+                                  double* bar_A, double* bar_b, int64_t base, int64_t count) {
+    for (int64_t i = base; i < base + count; ++i) {
+        double a[HKO_N][HKO_N], l[HKO_N][HKO_N], bb[HKO_N], x[HKO_N], g[HKO_N], lam[HKO_N];
+        load6(A, b, n, i, a, bb);
+        const int info = chol6(a, l);
+        cho_solve6(l, info, bb, x);
+        for (int r = 0; r < HKO_N; ++r) g[r] = bar_x[r * n + i];
+        cho_solve6(l, info, g, lam);
+        for (int r = 0; r < HKO_N; ++r) {
+            bar_b[r * n + i] = lam[r];
+            for (int c = 0; c < HKO_N; ++c)
+                bar_A[(r * HKO_N + c) * n + i] = -(((lam[r] * x[c]) + (lam[c] * x[r])) * 0.5);
+        }
+    }
+}
+
+/* ---- config 4b: fp32 16x16 product and its VJP --------------------------------
+ * C_ij = sum_k A_ik B_kj added in k order (the rolled product); the VJP is
+ * bar_A = bar_C B^T, bar_B = A^T bar_C (reference hawk/diff/rules.py `mm`),
+ * each entry's products added in index order. */
+#define HKO_M 16
+
+HKO_EXPORT void hko_mm16(const float* A, const float* B, int64_t n, float* C, int64_t base, int64_t count) {
+    for (int64_t i = base; i < base + count; ++i) {
+        float a[HKO_M][HKO_M], b[HKO_M][HKO_M];
+        for (int r = 0; r < HKO_M; ++r)
+            for (int c = 0; c < HKO_M; ++c) {
+                a[r][c] = A[(r * HKO_M + c) * n + i];
+                b[r][c] = B[(r * HKO_M + c) * n + i];
+            }
+        for (int r = 0; r < HKO_M; ++r)
+            for (int c = 0; c < HKO_M; ++c) {
+                float acc = a[r][0] * b[0][c];
+                for (int k = 1; k < HKO_M; ++k) acc = acc + (a[r][k] * b[k][c]);
+                C[(r * HKO_M + c) * n + i] = acc;
+            }
+    }
+}
+
+HKO_EXPORT void hko_mm16_vjp(const float* A, const float* B, const float* bar_C, int64_t n, float* bar_A,
+                             float* bar_B, int64_t base, int64_t count) {
+    for (int64_t i = base; i < base + count; ++i) {
+        float a[HKO_M][HKO_M], b[HKO_M][HKO_M], g[HKO_M][HKO_M];
+        for (int r = 0; r < HKO_M; ++r)
+            for (int c = 0; c < HKO_M; ++c) {
+                a[r][c] = A[(r * HKO_M + c) * n + i];
+                b[r][c] = B[(r * HKO_M + c) * n + i];
+                g[r][c] = bar_C[(r * HKO_M + c) * n + i];
+            }
+        for (int r = 0; r < HKO_M; ++r)
+            for (int c = 0; c < HKO_M; ++c) {
+                float acc = g[r][0] * b[c][0];                 /* (g B^T)_rc = sum_k g_rk B_ck */
+                for (int k = 1; k < HKO_M; ++k) acc = acc + (g[r][k] * b[c][k]);
+                bar_A[(r * HKO_M + c) * n + i] = acc;
+                float acc2 = a[0][r] * g[0][c];                /* (A^T g)_rc = sum_k A_kr g_kc */
+                for (int k = 1; k < HKO_M; ++k) acc2 = acc2 + (a[k][r] * g[k][c]);
+                bar_B[(r * HKO_M + c) * n + i] = acc2;
+            }
+    }
+}
+
+/* ---- the CPU baseline's tiling (eagle HostTeam shape) ------------------------
+ * [0, n) is cut into T contiguous tiles, one thread per tile calling the
+ * serial entry with its own (base, count) (reference hawk/emit/host.py:4-12);
+ * the ordered sum runs one group per thread-slot and the ordered scatter one
+ * chunk per thread-slot, each reproducing the serial bits. */
+typedef struct {
+    int which;
+    const void* in0; const void* in1; const void* in2; const void* in3;
+    void* out0; void* out1;
+    double s0, s1;
+    int64_t n, base, count;
+    double* gp;
+    int g_lo, g_hi;
+    int64_t cells;
+    int chunks;
+    double* parts;
+    int32_t* status;
+} hko_job;
+
+static void* job_main(void* arg) {
+    hko_job* j = (hko_job*)arg;
+    switch (j->which) {
+        case 1: hko_scale((const double*)j->in0, j->s0, j->s1, (double*)j->out0, j->base, j->count); break;
+        case 2: hko_energy((const double*)j->in0, j->n, (double*)j->out0, j->base, j->count); break;
+        case 3: hko_energy_vjp((const double*)j->in0, (const double*)j->in1, j->n, (double*)j->out0,
+                               j->base, j->count); break;
+        case 4: hko_energy_jvp((const double*)j->in0, (const double*)j->in1, j->n, (double*)j->out0,
+                               j->base, j->count); break;
+        case 5: hko_chain((const double*)j->in0, (double*)j->out0, j->base, j->count); break;
+        case 6:
+            for (int g = j->g_lo; g < j->g_hi; ++g) j->gp[g] = group_part((const double*)j->in0, j->n, g);
+            break;
+        case 7:
+            for (int b = j->g_lo; b < j->g_hi; ++b)
+                scatter_chunk((const int32_t*)j->in0, (const double*)j->in1, j->n, j->cells, j->chunks, b,
+                              j->parts, j->status);
+            break;
+        case 8: scatter_cells(j->parts, j->base, j->base + j->count, j->chunks, (double*)j->out0); break;
+        case 9: hko_twobody((const double*)j->in0, (const double*)j->in1, j->s0, j->n, (double*)j->out0,
+                            (double*)j->out1, j->base, j->count); break;
+        case 10: hko_twobody_vjp((const double*)j->in0, (const double*)j->in1, j->s0, (const double*)j->in2,
+                                 (const double*)j->in3, j->n, (double*)j->out0, (double*)j->out1, j->base,
+                                 j->count); break;
+        case 11: hko_spd_solve((const double*)j->in0, (const double*)j->in1, j->n, (double*)j->out0, j->base,
+                               j->count); break;
+        case 12: hko_spd_solve_vjp((const double*)j->in0, (const double*)j->in1, (const double*)j->in2, j->n,
+                                   (double*)j->out0, (double*)j->out1, j->base, j->count); break;
+        case 13: hko_mm16((const float*)j->in0, (const float*)j->in1, j->n, (float*)j->out0, j->base,
+                          j->count); break;
+        case 14: hko_mm16_vjp((const float*)j->in0, (const float*)j->in1, (const float*)j->in2, j->n,
+                              (float*)j->out0, (float*)j->out1, j->base, j->count); break;
+        default: break;
+    }
+    return NULL;
+}
+
+static void run_jobs(hko_job* jobs, int t) {
+    pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)t);
+    for (int k = 0; k < t; ++k) pthread_create(&th[k], NULL, job_main, &jobs[k]);
+    for (int k = 0; k < t; ++k) pthread_join(th[k], NULL);
+    free(th);
+}
+
+/* One tiled run of a per-sample entry over [0, n) on `threads` threads. */
+HKO_EXPORT void hko_tiled(int which, const void* in0, const void* in1, const void* in2, const void* in3,
+                          void* out0, void* out1, double s0, double s1, int64_t n, int threads) {
+    if (threads < 1) threads = 1;
+    hko_job* jobs = (hko_job*)calloc((size_t)threads, sizeof(hko_job));
+    const int64_t tile = (n + threads - 1) / threads;
+    for (int k = 0; k < threads; ++k) {
+        jobs[k].which = which;
+        jobs[k].in0 = in0; jobs[k].in1 = in1; jobs[k].in2 = in2; jobs[k].in3 = in3;
+        jobs[k].out0 = out0; jobs[k].out1 = out1; jobs[k].s0 = s0; jobs[k].s1 = s1; jobs[k].n = n;
+        jobs[k].base = (int64_t)k * tile < n ? (int64_t)k * tile : n;
+        const int64_t hi = jobs[k].base + tile < n ? jobs[k].base + tile : n;
+        jobs[k].count = hi - jobs[k].base;
+    }
+    run_jobs(jobs, threads);
+    free(jobs);
+}
+
+/* The ordered sum with its 64 groups spread over `threads` threads (same bits). */
+HKO_EXPORT double hko_ordered_sum_threads(const double* u, int64_t n, int threads) {
+    double gp[HKO_G];
+    if (threads < 1) threads = 1;
+    if (threads > HKO_G) threads = HKO_G;
+    hko_job jobs[HKO_G];
+    memset(jobs, 0, sizeof(jobs));
+    const int per = (HKO_G + threads - 1) / threads;
+    for (int k = 0; k < threads; ++k) {
+        jobs[k].which = 6; jobs[k].in0 = u; jobs[k].n = n; jobs[k].gp = gp;
+        jobs[k].g_lo = k * per < HKO_G ? k * per : HKO_G;
+        jobs[k].g_hi = (k + 1) * per < HKO_G ? (k + 1) * per : HKO_G;
+    }
+    run_jobs(jobs, threads);
+    return fold_groups(gp);
+}
+
+/* The ordered scatter with its chunks spread over `threads` threads (same bits). */
+HKO_EXPORT void hko_ordered_scatter_threads(const int32_t* key, const double* v, int64_t n, double* target,
+                                            int64_t cells, double* parts, int32_t* status, int threads) {
+    if (cells <= 0) return;
+    if (threads < 1) threads = 1;
+    const int chunks = hko_scatter_chunks(n, cells);
+    memset(parts, 0, sizeof(double) * (size_t)chunks * (size_t)cells);
+    status[0] = (int32_t)cells;
+    for (int b = 0; b < 256; ++b) status[1 + b] = 0;
+    hko_job* jobs = (hko_job*)calloc((size_t)threads, sizeof(hko_job));
+    const int per = (chunks + threads - 1) / threads;
+    for (int k = 0; k < threads; ++k) {
+        jobs[k].which = 7; jobs[k].in0 = key; jobs[k].in1 = v; jobs[k].n = n; jobs[k].cells = cells;
+        jobs[k].chunks = chunks; jobs[k].parts = parts; jobs[k].status = status;
+        jobs[k].g_lo = k * per < chunks ? k * per : chunks;
+        jobs[k].g_hi = (k + 1) * per < chunks ? (k + 1) * per : chunks;
+    }
+    run_jobs(jobs, threads);
+    const int64_t tile = (cells + threads - 1) / threads;
+    for (int k = 0; k < threads; ++k) {
+        jobs[k].which = 8; jobs[k].out0 = target;
+        jobs[k].base = (int64_t)k * tile < cells ? (int64_t)k * tile : cells;
+        const int64_t hi = jobs[k].base + tile < cells ? jobs[k].base + tile : cells;
+        jobs[k].count = hi - jobs[k].base;
+    }
+    run_jobs(jobs, threads);
+    free(jobs);
+}

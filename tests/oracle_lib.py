@@ -1,0 +1,196 @@
+"""ctypes face of the CPU oracle (oracle/hawk_oracle.c) — TEST INFRASTRUCTURE.
+
+Only tests/, the smoke check of __graft_entry__.py and bench.py's CPU
+baseline use this module, and only as the checker or the baseline: the
+product (hawk_amd/) never imports it.  The library is built by
+``make -C oracle`` (portable profile) when it is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE = ROOT / "oracle"
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_D = ctypes.c_double
+_libs: dict = {}
+
+
+def build(profile: str = "portable") -> Path:
+    out = ORACLE / ("libhawk_oracle.so" if profile == "portable" else "_native/libhawk_oracle.so")
+    src = ORACLE / "hawk_oracle.c"
+    if not out.exists() or out.stat().st_mtime < src.stat().st_mtime:
+        subprocess.run(["make", "-s", "-C", str(ORACLE), f"PROFILE={profile}"], check=True)
+    return out
+
+
+def lib(profile: str = "portable"):
+    if profile in _libs:
+        return _libs[profile]
+    L = ctypes.CDLL(str(build(profile)))
+    sigs = {
+        "hko_scale": (None, [_P, _D, _D, _P, _I64, _I64]),
+        "hko_energy": (None, [_P, _I64, _P, _I64, _I64]),
+        "hko_energy_vjp": (None, [_P, _P, _I64, _P, _I64, _I64]),
+        "hko_energy_jvp": (None, [_P, _P, _I64, _P, _I64, _I64]),
+        "hko_chain": (None, [_P, _P, _I64, _I64]),
+        "hko_libm": (None, [ctypes.c_int, _P, _P, _I64]),
+        "hko_ordered_sum": (_D, [_P, _I64]),
+        "hko_scatter_chunks": (ctypes.c_int, [_I64, _I64]),
+        "hko_ordered_scatter": (None, [_P, _P, _I64, _P, _I64, _P, _P]),
+        "hko_twobody": (None, [_P, _P, _D, _I64, _P, _P, _I64, _I64]),
+        "hko_twobody_vjp": (None, [_P, _P, _D, _P, _P, _I64, _P, _P, _I64, _I64]),
+        "hko_spd_solve": (None, [_P, _P, _I64, _P, _I64, _I64]),
+        "hko_spd_solve_vjp": (None, [_P, _P, _P, _I64, _P, _P, _I64, _I64]),
+        "hko_mm16": (None, [_P, _P, _I64, _P, _I64, _I64]),
+        "hko_mm16_vjp": (None, [_P, _P, _P, _I64, _P, _P, _I64, _I64]),
+        "hko_tiled": (None, [ctypes.c_int, _P, _P, _P, _P, _P, _P, _D, _D, _I64, ctypes.c_int]),
+        "hko_ordered_sum_threads": (_D, [_P, _I64, ctypes.c_int]),
+        "hko_ordered_scatter_threads": (None, [_P, _P, _I64, _P, _I64, _P, _P, ctypes.c_int]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype, fn.argtypes = res, args
+    _libs[profile] = L
+    return L
+
+
+def _p(a: np.ndarray):
+    assert a.flags.c_contiguous
+    return a.ctypes.data_as(_P)
+
+
+# -- convenience wrappers (whole range) -----------------------------------------
+
+def scale(x, a, b):
+    out = np.empty_like(x)
+    lib().hko_scale(_p(x), a, b, _p(out), 0, x.size)
+    return out
+
+
+def energy(v):
+    n = v.shape[1]
+    out = np.empty(n)
+    lib().hko_energy(_p(v), n, _p(out), 0, n)
+    return out
+
+
+def energy_vjp(v, bar_out):
+    n = v.shape[1]
+    out = np.empty_like(v)
+    lib().hko_energy_vjp(_p(v), _p(bar_out), n, _p(out), 0, n)
+    return out
+
+
+def energy_jvp(v, dv):
+    n = v.shape[1]
+    out = np.empty(n)
+    lib().hko_energy_jvp(_p(v), _p(dv), n, _p(out), 0, n)
+    return out
+
+
+def chain(x, threads: int = 1):
+    y = np.empty_like(x)
+    if threads > 1:
+        lib().hko_tiled(5, _p(x), None, None, None, _p(y), None, 0.0, 0.0, x.size, threads)
+    else:
+        lib().hko_chain(_p(x), _p(y), 0, x.size)
+    return y
+
+
+def libm(which: str, x):
+    y = np.empty_like(x)
+    code = {"exp": 0, "sin": 1, "tanh": 2, "sqrt": 3, "cos": 4, "log": 5}[which]
+    lib().hko_libm(code, _p(x), _p(y), x.size)
+    return y
+
+
+def ordered_sum(u, threads: int = 1) -> float:
+    if threads > 1:
+        return lib().hko_ordered_sum_threads(_p(u), u.size, threads)
+    return lib().hko_ordered_sum(_p(u), u.size)
+
+
+def scatter_chunks(n, cells) -> int:
+    return lib().hko_scatter_chunks(n, cells)
+
+
+def ordered_scatter(key, v, target, threads: int = 1):
+    """``target`` after the ordered scatter (a copy), and the status plane."""
+    out = target.copy()
+    cells = out.size
+    chunks = scatter_chunks(key.size, cells)
+    parts = np.empty(chunks * max(cells, 1))
+    status = np.zeros(257, dtype=np.int32)
+    if threads > 1:
+        lib().hko_ordered_scatter_threads(_p(key), _p(v), key.size, _p(out), cells, _p(parts), _p(status), threads)
+    else:
+        lib().hko_ordered_scatter(_p(key), _p(v), key.size, _p(out), cells, _p(parts), _p(status))
+    return out, status
+
+
+def twobody(r0, v0, mu, threads: int = 1):
+    n = r0.shape[1]
+    r, v = np.empty_like(r0), np.empty_like(v0)
+    if threads > 1:
+        lib().hko_tiled(9, _p(r0), _p(v0), None, None, _p(r), _p(v), mu, 0.0, n, threads)
+    else:
+        lib().hko_twobody(_p(r0), _p(v0), mu, n, _p(r), _p(v), 0, n)
+    return r, v
+
+
+def twobody_vjp(r0, v0, mu, bar_r, bar_v, threads: int = 1):
+    n = r0.shape[1]
+    br0, bv0 = np.empty_like(r0), np.empty_like(v0)
+    if threads > 1:
+        lib().hko_tiled(10, _p(r0), _p(v0), _p(bar_r), _p(bar_v), _p(br0), _p(bv0), mu, 0.0, n, threads)
+    else:
+        lib().hko_twobody_vjp(_p(r0), _p(v0), mu, _p(bar_r), _p(bar_v), n, _p(br0), _p(bv0), 0, n)
+    return br0, bv0
+
+
+def spd_solve(A, b, threads: int = 1):
+    n = b.shape[1]
+    x = np.empty_like(b)
+    if threads > 1:
+        lib().hko_tiled(11, _p(A), _p(b), None, None, _p(x), None, 0.0, 0.0, n, threads)
+    else:
+        lib().hko_spd_solve(_p(A), _p(b), n, _p(x), 0, n)
+    return x
+
+
+def spd_solve_vjp(A, b, bar_x, threads: int = 1):
+    n = b.shape[1]
+    bA, bb = np.empty_like(A), np.empty_like(b)
+    if threads > 1:
+        lib().hko_tiled(12, _p(A), _p(b), _p(bar_x), None, _p(bA), _p(bb), 0.0, 0.0, n, threads)
+    else:
+        lib().hko_spd_solve_vjp(_p(A), _p(b), _p(bar_x), n, _p(bA), _p(bb), 0, n)
+    return bA, bb
+
+
+def mm16(A, B, threads: int = 1):
+    n = A.shape[-1]
+    C = np.empty_like(A)
+    if threads > 1:
+        lib().hko_tiled(13, _p(A), _p(B), None, None, _p(C), None, 0.0, 0.0, n, threads)
+    else:
+        lib().hko_mm16(_p(A), _p(B), n, _p(C), 0, n)
+    return C
+
+
+def mm16_vjp(A, B, bar_C, threads: int = 1):
+    n = A.shape[-1]
+    bA, bB = np.empty_like(A), np.empty_like(B)
+    if threads > 1:
+        lib().hko_tiled(14, _p(A), _p(B), _p(bar_C), None, _p(bA), _p(bB), 0.0, 0.0, n, threads)
+    else:
+        lib().hko_mm16_vjp(_p(A), _p(B), _p(bar_C), n, _p(bA), _p(bB), 0, n)
+    return bA, bB

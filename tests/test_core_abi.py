@@ -1,0 +1,113 @@
+"""The C-ABI library on the CPU: it loads (digest and layout self-check),
+exports every symbol include/hawk_core.h declares, and its argument-block and
+launch-argument checks refuse by name without touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from hawk_amd import _contracts, _core
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "hawk_core.h"
+
+
+def declared_symbols() -> list:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    lib = ctypes.CDLL(str(_core.library_path()))
+    names = declared_symbols()
+    assert len(names) >= 25
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_layout_and_digest_self_check():
+    assert _core.layout_sizes() == [size for _, size in _contracts.LAYOUT]
+    assert [_core.layout_field_name(i) for i in range(5)] == [f for f, _ in _contracts.LAYOUT]
+    from hawk_amd._build import source_digest
+    assert _core.build_digest() == source_digest()
+    info = _core.build_info()
+    assert info["abi_tag"] == "aether-abi/2" and info["index_type_bytes"] == "8"
+    assert "gfx950" in info["offload_arch"]
+
+
+def test_crossings_count_every_call():
+    a = _core.crossings()
+    _core.layout_sizes()
+    b = _core.crossings()
+    assert b - a == 2          # layout_sizes and the second crossings()
+
+
+def test_argblock_refuses_an_unknown_kind():
+    with pytest.raises(ValueError, match="unknown slot kind 'mirror'"):
+        _core.ArgBlock(["gref", "mirror"])
+
+
+def test_argblock_bind_and_rebind_refusals():
+    ab = _core.ArgBlock(["gref", "handle", "f64"])
+    assert ab.size == 3
+    ab.bind(0, 0x1000, 128)
+    ab.bind(1, 0x2000, 128)
+    ab.bind_value(2, 2.5)
+    with pytest.raises(IndexError, match="slot 3 is outside this block's 3 slots"):
+        ab.bind(3, 0x1000, 1)
+    with pytest.raises(ValueError, match="by-value 'f64' slot"):
+        ab.rebind([2], [0x3000])
+    with pytest.raises(ValueError, match="sample stride 2"):
+        ab.bind(0, 0x1000, 128, stride=2)
+    with pytest.raises(ValueError, match="null pointer"):
+        ab.bind(2, 0, 1)
+    ab.rebind([0, 1], [0x5000, 0x6000])
+
+
+def test_rtc_refuses_another_architecture():
+    from hawk_amd import HawkError
+    with pytest.raises(HawkError, match="pinned to gfx950"):
+        _core.rtc_compile('extern "C" __global__ void k() {}', "k.hip", ["--offload-arch=gfx942"])
+
+
+def test_rtc_compiles_for_gfx950_without_a_gpu():
+    code, _log = _core.rtc_compile('extern "C" __global__ void k(double* p) { p[threadIdx.x] = 1.0; }',
+                                   "k.hip", ["-O3"])
+    assert code[:4] in (b"\x7fELF", b"__CL")     # an ELF code object or a clang offload bundle
+
+
+def test_rtc_reports_a_compile_error():
+    from hawk_amd import HawkError
+    with pytest.raises(HawkError, match="could not compile"):
+        _core.rtc_compile('extern "C" __global__ void k() { undeclared(); }', "bad.hip", [])
+
+
+def test_team_stage_arguments_are_checked_before_any_launch():
+    L = _core.lib()
+    rc = L.hk_ordered_sum_f64(None, -1, None, None, None)
+    assert rc != 0 and b"n must be >= 0" in L.hk_last_error()
+    rc = L.hk_ordered_scatter_f64(None, None, 10, None, 5, None, None, None)
+    assert rc != 0 and b"required" in L.hk_last_error()
+    assert L.hk_ordered_scatter_f64(None, None, 10, None, 0, None, None, None) == 0   # no cells: nothing
+
+
+def test_scatter_chunk_rule():
+    """clamp(n // cells, 1, 256) (reference tests/test_scatter_ordered.py:119-121)."""
+    cases = ((20000, 7), (50, 200), (1000, 1000), (10**6, 10**4), (10**6, 1), (10, 0))
+    got = [_core.scatter_chunks(n, t) for n, t in cases]
+    assert got[:5] == [256, 1, 1, 100, 256]
+
+
+def test_launch_arguments_are_checked_before_hip():
+    ab = _core.ArgBlock(["handle"])
+    L = _core.lib()
+    fake = ctypes.c_void_p(1)       # never dereferenced: the checks refuse first
+    rc = L.hk_launch(fake, ab.handle, 0, 10, 5, 256, 1, None)
+    assert rc != 0 and b"not inside" in L.hk_last_error()
+    rc = L.hk_launch(fake, ab.handle, 0, 10, 10, 100, 1, None)
+    assert rc != 0 and b"multiple of 64" in L.hk_last_error()
+    assert L.hk_launch(fake, ab.handle, 0, 0, 10, 256, 1, None) == 0     # empty range: nothing launched

@@ -1,0 +1,212 @@
+"""The authoring surface, the IR and the derivative transforms, on the CPU:
+tracing and arg_spec order, refusals by name, the rolled loop, and the
+vjp/jvp of every benchmark kernel against central differences (through the
+numpy IR interpreter) and against the oracle's operation order."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import hawk_amd as hawk
+import oracle_lib as O
+from hawk_amd import HawkError, Index, Matrix, Mutable, Param, Scalar, Vector, ir
+from hawk_amd import examples as E
+from hawk_amd.diff import jvp, vjp
+from hawk_amd.math import dot, exp, sqrt
+from ir_eval import evaluate
+
+
+def test_declarations_give_roles_and_the_canonical_arg_spec():
+    from hawk_amd.emit_hip import plan_kernel
+    p = plan_kernel(E.energy_vjp.program, "energy_vjp")
+    # ROLE_ORDER: mutable, out, ..., vec_in, ..., per_sample, ..., uniform
+    assert p.stage.arg_spec == [("mutable", "bar_v"), ("vec_in", "v"), ("per_sample", "bar_out")]
+    p = plan_kernel(E.scale.program, "scale")
+    assert p.stage.arg_spec == [("out", "out"), ("per_sample", "x"), ("uniform", "a"), ("uniform", "b")]
+    assert [p.stage.planes[n]["kind"] for _, n in p.stage.arg_spec] == ["gref", "handle", "f64", "f64"]
+
+
+def test_a_returned_value_commits_into_out():
+    assert [(type(s).__name__, s.name) for s in E.scale.sinks] == [("Assign", "out")]
+    assert E.scale.decls["out"].role == "out"
+
+
+def test_sum_and_scatter_become_team_stages():
+    from hawk_amd.emit_hip import plan_kernel
+    p = plan_kernel(E.chain.program, "chain")
+    ops = sorted(t["op"] for t in p.team)
+    assert ops == ["ordered_scatter", "ordered_sum"]
+    assert {t.get("u") or t.get("v") for t in p.team} == {"y"}     # both read the stored y, no extra plane
+    assert p.planes["total"]["role"] == "cell" and p.planes["bins"]["role"] == "accum_out"
+
+
+def test_refuses_a_branch_on_a_traced_value():
+    with pytest.raises(HawkError, match="where"):
+        @hawk.kernel
+        def k(x: Scalar, y: Mutable[Scalar]):
+            if x > 0.0:
+                y = x
+            else:
+                y = -x
+
+
+def test_refuses_an_undeclared_parameter():
+    with pytest.raises(HawkError, match="no declaration"):
+        @hawk.kernel
+        def k(x, y: Mutable[Scalar]):
+            y = x
+
+
+def test_refuses_a_non_literal_trip_count():
+    with pytest.raises(HawkError, match="literal int"):
+        @hawk.kernel
+        def k(x: Scalar, n: Param, y: Mutable[Scalar]):
+            acc = x
+            for i in range(n):
+                acc = acc * x
+            y = acc
+
+
+def test_vjp_refuses_a_prior_read():
+    @hawk.kernel
+    def running(x: Scalar, m: Mutable[Scalar]):
+        m = m + x
+    with pytest.raises(HawkError, match="before it writes it"):
+        vjp(running)
+
+
+def test_sum_read_back_is_refused():
+    with pytest.raises(HawkError, match="stage boundary"):
+        @hawk.kernel
+        def k(x: Scalar, y: Mutable[Scalar]):
+            y = x / hawk.sum(x, policy="ordered")
+
+
+def test_the_loop_is_rolled_with_its_carries():
+    loops = [n for n in ir.topo([s.value for s in E.twobody.sinks]) if n.kind == "loop"]
+    assert len(loops) == 1
+    info = loops[0].literal
+    assert info.trip == E.SUBSTEPS and info.names == ("rr", "vv")
+
+
+def test_energy_vjp_is_the_reference_rule():
+    """bar_v = (bar_out * 0.5) * v + (bar_out * 0.5) * v: the oracle's expression, bit for bit."""
+    g = np.random.default_rng(7)
+    n = 1000
+    v = g.normal(size=(3, n))
+    bar_out = g.normal(size=n)
+    got = evaluate(E.energy_vjp.program, {"v": v, "bar_out": bar_out}, n)["bar_v"]
+    assert got.tobytes() == O.energy_vjp(v, bar_out).tobytes()
+    dv = g.normal(size=(3, n))
+    got = evaluate(E.energy_jvp.program, {"v": v, "dot_v": dv}, n)["dot_out"]
+    assert got.tobytes() == O.energy_jvp(v, dv).tobytes()
+
+
+def _central(fn, x, h):
+    return (fn(x + h) - fn(x - h)) / (2 * h)
+
+
+def test_twobody_vjp_ir_matches_the_oracle_and_finite_differences():
+    n = 64
+    g = np.random.default_rng(3)
+    d = g.normal(size=(3, n))
+    d /= np.linalg.norm(d, axis=0)
+    r0 = d * g.uniform(0.5, 2.0, n)
+    v0 = g.normal(0.0, 0.3, size=(3, n))
+    bar_r, bar_v = g.normal(size=(3, n)), g.normal(size=(3, n))
+    env = {"r0": r0, "v0": v0, "mu": 1.0, "bar_r": bar_r, "bar_v": bar_v}
+    got = evaluate(E.twobody_vjp.program, env, n)
+    want_r0, want_v0 = O.twobody_vjp(r0, v0, 1.0, bar_r, bar_v)
+    np.testing.assert_allclose(got["bar_r0"], want_r0, rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(got["bar_v0"], want_v0, rtol=1e-13, atol=1e-15)
+    fwd = evaluate(E.twobody.program, {"r0": r0, "v0": v0, "mu": 1.0}, n)
+    wr, wv = O.twobody(r0, v0, 1.0)
+    assert fwd["r"].tobytes() == wr.tobytes() and fwd["v"].tobytes() == wv.tobytes()
+    # <bar, J e_c> by central differences for each input component
+    h = 1e-6
+    for name, grad in (("r0", got["bar_r0"]), ("v0", got["bar_v0"])):
+        for c in range(3):
+            e = np.zeros((3, n))
+            e[c] = h
+
+            def loss(delta):
+                args = {"r0": r0, "v0": v0}
+                args[name] = args[name] + delta
+                r, v = O.twobody(np.ascontiguousarray(args["r0"]), np.ascontiguousarray(args["v0"]), 1.0)
+                return (bar_r * r).sum(axis=0) + (bar_v * v).sum(axis=0)
+            fd = (loss(e) - loss(-e)) / (2 * h)
+            np.testing.assert_allclose(grad[c], fd, rtol=1e-6, atol=1e-8)
+
+
+def test_spd_vjp_ir_matches_the_oracle_and_finite_differences():
+    n = 32
+    g = np.random.default_rng(4)
+    B = g.normal(size=(n, 6, 6))
+    A = np.ascontiguousarray((np.matmul(B, B.transpose(0, 2, 1)) + 6.0 * np.eye(6)).transpose(1, 2, 0))
+    b = np.ascontiguousarray(g.normal(size=(n, 6)).T)
+    bar_x = g.normal(size=(6, n))
+    x = evaluate(E.spd_solve.program, {"A": A, "b": b}, n)["x"]
+    assert x.tobytes() == O.spd_solve(A, b).tobytes()
+    got = evaluate(E.spd_solve_vjp.program, {"A": A, "b": b, "bar_x": bar_x}, n)
+    wA, wb = O.spd_solve_vjp(A, b, bar_x)
+    assert got["bar_A"].tobytes() == wA.tobytes() and got["bar_b"].tobytes() == wb.tobytes()
+    h = 1e-6
+    for (i, j) in ((0, 0), (2, 5), (5, 1)):
+        e = np.zeros_like(A)
+        e[i, j] = h
+        fd = ((bar_x * O.spd_solve(A + e, b)).sum(0) - (bar_x * O.spd_solve(A - e, b)).sum(0)) / (2 * h)
+        # a symmetric-part derivative: the unsymmetric perturbation reads 0.5(e + e^T)
+        np.testing.assert_allclose(got["bar_A"][i, j], fd, rtol=1e-6, atol=1e-9)
+
+
+def test_jvp_and_vjp_are_adjoint_on_a_loop():
+    """<bar, J t> == <J^T bar, t> for the rolled two-body loop (forward mode through
+    the augmented loop, reverse mode through the taped reverse loop)."""
+    n = 16
+    g = np.random.default_rng(9)
+    d = g.normal(size=(3, n))
+    d /= np.linalg.norm(d, axis=0)
+    r0 = d * g.uniform(0.5, 2.0, n)
+    v0 = g.normal(0.0, 0.3, size=(3, n))
+    tr, tv = g.normal(size=(3, n)), g.normal(size=(3, n))
+    br, bv = g.normal(size=(3, n)), g.normal(size=(3, n))
+    tangent = evaluate(jvp(E.twobody, wrt=("r0", "v0")),
+                       {"r0": r0, "v0": v0, "mu": 1.0, "dot_r0": tr, "dot_v0": tv}, n)
+    adjoint = evaluate(E.twobody_vjp.program, {"r0": r0, "v0": v0, "mu": 1.0, "bar_r": br, "bar_v": bv}, n)
+    lhs = (br * tangent["dot_r"]).sum(0) + (bv * tangent["dot_v"]).sum(0)
+    rhs = (adjoint["bar_r0"] * tr).sum(0) + (adjoint["bar_v0"] * tv).sum(0)
+    np.testing.assert_allclose(lhs, rhs, rtol=1e-11)
+
+
+def test_chain_forward_is_the_oracle_expression():
+    """The chain's IR computes the oracle's operations (transcendentals aside):
+    evaluated with numpy's libm the two agree to a few ulp."""
+    x = np.random.default_rng(5).normal(size=4096)
+    prog = E.chain.program
+    y = evaluate(prog, {"x": x, "key": np.zeros(4096, np.int32)}, 4096)["y"]
+    np.testing.assert_allclose(y, O.chain(x), rtol=1e-12, atol=1e-14)
+
+
+def test_emitted_source_has_one_geometry_prologue():
+    from hawk_amd.emit_hip import plan_kernel
+    src = plan_kernel(E.energy.program, "energy").source
+    assert src.count("blockIdx.x") == 1 and src.count("hk_i = base + hk_flat") == 1
+    assert 'eagle_abi_tag[] = "aether-abi/2"' in src
+    assert "eagle_layout_sizes[5] = {40, 32, 32, 8, 24}" in src
+
+
+def test_build_writes_the_unit(tmp_path):
+    b = hawk.build([E.scale, E.chain], tmp_path)
+    names = sorted(p.name for p in tmp_path.iterdir())
+    assert names == ["chain.hip", "chain.hsaco", "chain.json", "manifest.json", "scale.hip", "scale.hsaco",
+                     "scale.json"]
+    side = b.sidecar("chain")
+    assert side["target"] == "hip" and side["offload_arch"] == "gfx950"
+    assert side["descriptor"] == ["handle", "handle"]    # y (mutable, rank 0) and x (per_sample)
+    assert hawk.compile.cache_stats()["hits"] + hawk.compile.cache_stats()["misses"] >= 2
+
+
+def test_build_refuses_another_target(tmp_path):
+    with pytest.raises(HawkError, match="'hip'"):
+        hawk.build([E.scale], tmp_path, targets=("cuda",))

@@ -1,0 +1,292 @@
+"""Parity of the hip target with the CPU oracle, at sizes the oracle runs in
+seconds.  Every case builds inputs from a seeded generator, runs the kernel on
+the MI355X through hawk.build/load/run (the C-ABI), and compares with the
+oracle's host-target restatement on the same inputs:
+
+* bit-exact for the ordered sum, the ordered scatter, and the kernels built
+  from IEEE operations only (configs 1, 2, 4a and the two-body forward);
+* within 4 ulp or 1e-13 relative (the north star's fp64 bar) otherwise.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from conftest import rng, ulp_diff, within_contract
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, gpu):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def _load(unit, name):
+    import hawk_amd as hawk
+    return hawk.load(unit, name)
+
+
+def tree_sum(x: np.ndarray) -> float:
+    """The fixed grouping in NumPy: 65536 virtual lanes adding rows in order,
+    the halving tree over each group of 1024, then over the 64 groups."""
+    V, W, G = 65536, 1024, 64
+    part = np.zeros(V, x.dtype)
+    for r in range(0, len(x), V):
+        row = x[r:r + V]
+        part[:len(row)] += row
+
+    def tree(s):
+        s = s.copy()
+        w = len(s) // 2
+        while w:
+            s[:w] += s[w:2 * w]
+            w //= 2
+        return s[0]
+    return tree(np.array([tree(part[g * W:(g + 1) * W]) for g in range(G)], x.dtype))
+
+
+# -- config 1 -------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 255, 1000, 65537, (1 << 20) + 3])
+def test_scale_is_the_oracle_bitwise(unit, gpu, n):
+    import hawk_amd as hawk
+    x = rng(1).uniform(-1.0, 1.0, n)
+    out = dev(np.zeros(n), gpu)
+    hawk.run(_load(unit, "scale"), x=dev(x, gpu), a=2.0, b=1.0, out=out)
+    want = O.scale(x, 2.0, 1.0)
+    assert host(out).tobytes() == want.tobytes()
+
+
+def test_a_partition_writes_its_range_only(unit, gpu):
+    """A run over [base, base+count) with the true n_samples writes exactly that
+    range (reference tests/test_serial_oracle.py:7-35): a prime N, an uneven cut,
+    and a sentinel elsewhere."""
+    import hawk_amd as hawk
+    n, base, count = 100_003, 31_337, 40_009
+    x = rng(11).uniform(-1.0, 1.0, n)
+    out = dev(np.full(n, -12345.0), gpu)
+    hawk.run(_load(unit, "scale"), x=dev(x, gpu), a=2.0, b=1.0, out=out, base=base, count=count)
+    got = host(out)
+    want = O.scale(x, 2.0, 1.0)
+    assert np.all(got[:base] == -12345.0) and np.all(got[base + count:] == -12345.0)
+    assert got[base:base + count].tobytes() == want[base:base + count].tobytes()
+
+
+def test_empty_run_touches_nothing(unit, gpu):
+    import hawk_amd as hawk
+    x = dev(np.zeros(16), gpu)
+    out = dev(np.full(16, 7.0), gpu)
+    hawk.run(_load(unit, "scale"), x=x, a=2.0, b=1.0, out=out, base=3, count=0)
+    assert np.all(host(out) == 7.0)
+
+
+# -- config 2 -------------------------------------------------------------------
+
+def test_energy_readme_vectors(unit, gpu):
+    """The reference's own golden vectors (README.md:82-103)."""
+    import hawk_amd as hawk
+    v = np.array([[1.0, 2.0, 3.0, 4.0], [0.0, 1.0, 0.0, 1.0], [0.0, 0.0, 1.0, 1.0]])
+    e = dev(np.zeros(4), gpu)
+    hawk.run(_load(unit, "energy"), v=dev(v, gpu), out=e)
+    assert host(e).tolist() == [0.5, 2.5, 5.0, 9.0]
+    bar_v = dev(np.zeros((3, 4)), gpu)
+    hawk.run(_load(unit, "energy_vjp"), v=dev(v, gpu), bar_out=dev(np.ones(4), gpu), bar_v=bar_v)
+    assert host(bar_v).tolist() == v.tolist()
+
+
+@pytest.mark.parametrize("n", [7, 4097, 300_001])
+def test_energy_fwd_vjp_jvp_are_the_oracle_bitwise(unit, gpu, n):
+    import hawk_amd as hawk
+    g = rng(2)
+    v = g.normal(size=(3, n))
+    bar_out = g.normal(size=n)
+    dv = g.normal(size=(3, n))
+    out = dev(np.zeros(n), gpu)
+    hawk.run(_load(unit, "energy"), v=dev(v, gpu), out=out)
+    assert host(out).tobytes() == O.energy(v).tobytes()
+    bar_v = dev(np.zeros((3, n)), gpu)
+    hawk.run(_load(unit, "energy_vjp"), v=dev(v, gpu), bar_out=dev(bar_out, gpu), bar_v=bar_v)
+    assert host(bar_v).tobytes() == O.energy_vjp(v, bar_out).tobytes()
+    dot_out = dev(np.zeros(n), gpu)
+    hawk.run(_load(unit, "energy_jvp"), v=dev(v, gpu), dot_v=dev(dv, gpu), dot_out=dot_out)
+    assert host(dot_out).tobytes() == O.energy_jvp(v, dv).tobytes()
+
+
+# -- config 3 -------------------------------------------------------------------
+
+def _twobody_inputs(n, seed=3):
+    g = rng(seed)
+    d = g.normal(size=(3, n))
+    d /= np.linalg.norm(d, axis=0)
+    r0 = d * g.uniform(0.5, 2.0, n)
+    v0 = g.normal(0.0, 0.3, size=(3, n))
+    return r0, v0
+
+
+@pytest.mark.parametrize("n", [5, 20_011])
+def test_twobody_forward_and_vjp(unit, gpu, n):
+    import hawk_amd as hawk
+    r0, v0 = _twobody_inputs(n)
+    r = dev(np.zeros((3, n)), gpu)
+    v = dev(np.zeros((3, n)), gpu)
+    hawk.run(_load(unit, "twobody"), r0=dev(r0, gpu), v0=dev(v0, gpu), mu=1.0, r=r, v=v)
+    wr, wv = O.twobody(r0, v0, 1.0)
+    assert within_contract(host(r), wr).all() and within_contract(host(v), wv).all()
+    assert host(r).tobytes() == wr.tobytes() and host(v).tobytes() == wv.tobytes()
+    g = rng(103)
+    bar_r, bar_v = g.normal(size=(3, n)), g.normal(size=(3, n))
+    br0 = dev(np.zeros((3, n)), gpu)
+    bv0 = dev(np.zeros((3, n)), gpu)
+    hawk.run(_load(unit, "twobody_vjp"), r0=dev(r0, gpu), v0=dev(v0, gpu), mu=1.0, bar_r=dev(bar_r, gpu),
+             bar_v=dev(bar_v, gpu), bar_r0=br0, bar_v0=bv0)
+    wbr0, wbv0 = O.twobody_vjp(r0, v0, 1.0, bar_r, bar_v)
+    assert within_contract(host(br0), wbr0).all()
+    assert within_contract(host(bv0), wbv0).all()
+
+
+# -- config 4a ------------------------------------------------------------------
+
+def _spd_inputs(n, seed=4):
+    g = rng(seed)
+    B = g.normal(size=(n, 6, 6))
+    A = np.einsum("nij,nkj->nik", B, B) + 6.0 * np.eye(6)
+    b = g.normal(size=(n, 6))
+    return np.ascontiguousarray(A.transpose(1, 2, 0)), np.ascontiguousarray(b.T)
+
+
+@pytest.mark.parametrize("n", [3, 10_007])
+def test_spd_solve_and_vjp_are_the_oracle(unit, gpu, n):
+    import hawk_amd as hawk
+    A, b = _spd_inputs(n)
+    x = dev(np.zeros((6, n)), gpu)
+    hawk.run(_load(unit, "spd_solve"), A=dev(A, gpu), b=dev(b, gpu), x=x)
+    want = O.spd_solve(A, b)
+    assert host(x).tobytes() == want.tobytes()
+    bar_x = rng(104).normal(size=(6, n))
+    bA = dev(np.zeros((6, 6, n)), gpu)
+    bb = dev(np.zeros((6, n)), gpu)
+    hawk.run(_load(unit, "spd_solve_vjp"), A=dev(A, gpu), b=dev(b, gpu), bar_x=dev(bar_x, gpu), bar_A=bA,
+             bar_b=bb)
+    wA, wb = O.spd_solve_vjp(A, b, bar_x)
+    assert within_contract(host(bA), wA).all() and within_contract(host(bb), wb).all()
+
+
+# -- config 5 -------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 1000, 65536, 3 * 65536 + 777, 200_003])
+def test_ordered_sum_is_the_numpy_tree_bitwise_and_replays(unit, gpu, n):
+    import hawk_amd as hawk
+    g = rng(n)
+    x = g.normal(size=n) * np.exp(g.normal(size=n))
+    k = _load(unit, "ordered_total")
+    runs = []
+    for _ in range(3):
+        total = dev(np.zeros(1), gpu)
+        hawk.run(k, x=dev(x, gpu), total=total)
+        runs.append(host(total))
+    assert runs[0].tobytes() == runs[1].tobytes() == runs[2].tobytes()
+    assert runs[0][0] == tree_sum(x)
+    assert runs[0][0] == O.ordered_sum(x)
+
+
+@pytest.mark.parametrize("cells, n, heavy", [(7, 30_000, False), (1000, 30_000, False), (1500, 30_000, False),
+                                             (7, 20_000, True), (1, 3000, False), (200, 50, False),
+                                             (1000, 1000, False), (65536, 400_000, False),
+                                             (70_000, 300_000, False)])
+def test_ordered_scatter_is_the_serial_walk_bitwise(unit, gpu, cells, n, heavy):
+    import hawk_amd as hawk
+    g = rng(cells + n)
+    key = g.integers(0, cells, n).astype(np.int32)
+    if heavy:
+        key[g.random(n) < 0.9] = cells // 2
+    key[::7] = -1
+    x = g.normal(size=n) * np.exp(g.normal(size=n))
+    acc0 = np.linspace(1.0, 2.0, cells)
+    k = _load(unit, "ordered_add")
+    outs = []
+    for _ in range(2):
+        acc = dev(acc0, gpu)
+        hawk.run(k, key=dev(key, gpu), x=dev(x, gpu), acc=acc)
+        outs.append(host(acc))
+    want, status = O.ordered_scatter(key, x, acc0)
+    assert not status[1:].any()
+    assert outs[0].tobytes() == outs[1].tobytes()
+    assert outs[0].tobytes() == want.tobytes()
+    assert k.scatter_chunks == O.scatter_chunks(n, cells)
+
+
+def test_ordered_scatter_reports_a_bad_key(unit, gpu):
+    import hawk_amd as hawk
+    from hawk_amd import HawkError
+    key = np.arange(100, dtype=np.int32) % 10
+    key[57] = 12
+    key[58] = -3
+    x = np.ones(100)
+    acc = dev(np.zeros(10), gpu)
+    with pytest.raises(HawkError, match="outside \\[0, 10\\)"):
+        hawk.run(_load(unit, "ordered_add"), key=dev(key, gpu), x=dev(x, gpu), acc=acc)
+    want, status = O.ordered_scatter(key, x, np.zeros(10))
+    assert status[1:].any()
+    assert host(acc).tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("which", ["exp", "sin", "tanh", "sqrt"])
+def test_transcendentals_are_within_4_ulp_of_glibc(unit, gpu, which):
+    """The device's fp64 exp/sin/tanh/sqrt on the chain's argument ranges, in ULP of
+    glibc (reference tests/test_math_parity.py: device within ULP of host)."""
+    import hawk_amd as hawk
+    from hawk_amd import Scalar, kernel
+    from hawk_amd import math as m
+
+    fn = {"exp": m.exp, "sin": m.sin, "tanh": m.tanh, "sqrt": m.sqrt}[which]
+
+    @kernel
+    def one(x: Scalar) -> Scalar:
+        return fn(x)
+
+    import tempfile
+    d = tempfile.mkdtemp()
+    hawk.build([one], d)
+    g = rng(6)
+    if which == "exp":
+        x = np.concatenate([g.normal(size=100_000) * 5, -np.abs(g.normal(size=20_000)) * 20])
+    elif which == "sin":
+        x = np.concatenate([np.exp(g.normal(size=100_000)), g.uniform(-200, 200, 20_000)])
+    elif which == "tanh":
+        x = np.concatenate([g.uniform(-2, 2, 100_000), g.normal(size=20_000) * 1e-3])
+    else:
+        x = np.abs(g.normal(size=120_000)) + 1.0
+    out = dev(np.zeros_like(x), gpu)
+    hawk.run(hawk.load(d, "one"), x=dev(x, gpu), out=out)
+    u = ulp_diff(host(out), O.libm(which, x))
+    assert u.max() <= 4.0, f"{which}: max {u.max()} ulp"
+
+
+@pytest.mark.parametrize("n", [1000, 262_147])
+def test_chain_kernel_total_and_bins(unit, gpu, n):
+    """The fused chain y within the fp64 bar; the ordered total and the bins
+    bit-exact against the oracle's walk of the same y."""
+    import hawk_amd as hawk
+    g = rng(5)
+    x = g.normal(size=n)
+    cells = 1 << 16
+    key = ((g.zipf(1.1, n) - 1) % cells).astype(np.int32)
+    y = dev(np.zeros(n), gpu)
+    total = dev(np.zeros(1), gpu)
+    bins = dev(np.zeros(cells), gpu)
+    hawk.run(_load(unit, "chain"), x=dev(x, gpu), key=dev(key, gpu), y=y, total=total, bins=bins)
+    gy = host(y)
+    wy = O.chain(x)
+    ok = within_contract(gy, wy)
+    assert ok.mean() >= 0.999, f"{(~ok).sum()} of {n} outside 4 ulp / 1e-13"
+    assert host(total)[0] == O.ordered_sum(gy)
+    want_bins, status = O.ordered_scatter(key, gy, np.zeros(cells))
+    assert not status[1:].any()
+    assert host(bins).tobytes() == want_bins.tobytes()

@@ -1,0 +1,260 @@
+"""Pins the CPU oracle (oracle/hawk_oracle.c) before it is trusted as the
+parity checker: the reference's golden vectors, closed forms, brute force,
+numpy/LAPACK, finite differences and invariants — each chosen so a plausible
+mistake (a dropped term, a wrong sign, a transposed operand, a wrong index,
+a changed order) fails one of them."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+
+def tree_sum(x: np.ndarray) -> float:
+    """The fixed tree in NumPy (reference tests/test_ordered_fixed_tree.py:25-40)."""
+    V, W, G = 65536, 1024, 64
+    part = np.zeros(V, x.dtype)
+    for r in range(0, len(x), V):
+        row = x[r:r + V]
+        part[:len(row)] += row
+
+    def tree(s):
+        s = s.copy()
+        w = len(s) // 2
+        while w:
+            s[:w] += s[w:2 * w]
+            w //= 2
+        return s[0]
+    return tree(np.array([tree(part[g * W:(g + 1) * W]) for g in range(G)], x.dtype))
+
+
+def test_energy_readme_golden_vectors():
+    v = np.array([[1.0, 2.0, 3.0, 4.0], [0.0, 1.0, 0.0, 1.0], [0.0, 0.0, 1.0, 1.0]])
+    assert O.energy(v).tolist() == [0.5, 2.5, 5.0, 9.0]
+    assert O.energy_vjp(v, np.ones(4)).tolist() == v.tolist()
+
+
+def test_energy_closed_forms():
+    g = np.random.default_rng(0)
+    v, dv, bo = g.normal(size=(3, 999)), g.normal(size=(3, 999)), g.normal(size=999)
+    assert O.energy(v).tobytes() == (0.5 * (((v[0] * v[0]) + (v[1] * v[1])) + (v[2] * v[2]))).tobytes()
+    assert O.energy_vjp(v, bo).tobytes() == (bo * v).tobytes()          # 2*((0.5 b) v) == b v exactly
+    d = ((dv[0] * v[0]) + (dv[1] * v[1])) + (dv[2] * v[2])
+    assert O.energy_jvp(v, dv).tobytes() == d.tobytes()                   # 0.5*(d + d) == d exactly
+
+
+def test_scale_is_one_mul_and_one_add():
+    x = np.random.default_rng(1).uniform(-1, 1, 1000)
+    assert O.scale(x, 2.0, 1.0).tobytes() == ((2.0 * x) + 1.0).tobytes()
+
+
+@pytest.mark.parametrize("n", [1, 1000, 65536, 3 * 65536 + 777, 200003, 1 << 20])
+def test_ordered_sum_is_the_numpy_tree(n):
+    g = np.random.default_rng(n)
+    x = g.normal(size=n) * np.exp(g.normal(size=n))
+    assert O.ordered_sum(x) == tree_sum(x)
+    assert O.ordered_sum(x, threads=6) == tree_sum(x)
+
+
+def test_ordered_sum_small_cases():
+    assert O.ordered_sum(np.zeros(0)) == 0.0
+    assert O.ordered_sum(np.array([3.5])) == 3.5
+    x = np.arange(1.0, 70001.0)
+    assert O.ordered_sum(x) == 70000 * 70001 / 2
+
+
+def test_scatter_chunk_rule():
+    cases = ((20000, 7), (50, 200), (1000, 1000), (10**6, 10**4), (10**6, 1), (10, 0))
+    assert [O.scatter_chunks(n, t) for n, t in cases] == [256, 1, 1, 100, 256, 1]
+
+
+@pytest.mark.parametrize("n, cells, heavy", [(20000, 7, True), (3000, 1, False), (5000, 40, False),
+                                             (50, 200, False), (1000, 1000, False)])
+def test_ordered_scatter_equals_add_at_and_replays(n, cells, heavy):
+    g = np.random.default_rng(n)
+    key = g.integers(0, cells, n).astype(np.int32)
+    if heavy:
+        key[g.random(n) < 0.9] = cells // 2
+    x = g.normal(size=n) * np.exp(g.normal(size=n))
+    want = np.zeros(cells)
+    np.add.at(want, key, x)
+    a, sa = O.ordered_scatter(key, x, np.zeros(cells))
+    b, _ = O.ordered_scatter(key, x, np.zeros(cells), threads=4)
+    assert a.tobytes() == b.tobytes()
+    assert not sa[1:].any() and sa[0] == cells
+    np.testing.assert_allclose(a, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+
+
+def test_ordered_scatter_is_the_serial_chunk_walk():
+    """Brute force in Python over a small case: per-(key, chunk) sums in lane order
+    from 0, then per cell in chunk order from 0, added onto the target."""
+    g = np.random.default_rng(3)
+    n, cells = 2000, 9
+    key = g.integers(-1, cells + 2, n).astype(np.int32)
+    x = g.normal(size=n)
+    base = g.normal(size=cells)
+    chunks = O.scatter_chunks(n, cells)
+    span = -(-n // chunks)
+    parts = [[0.0] * chunks for _ in range(cells)]
+    bad = [0] * chunks
+    for r in range(n):
+        b, k = r // span, int(key[r])
+        if k == -1:
+            continue
+        if 0 <= k < cells:
+            parts[k][b] = parts[k][b] + float(x[r])
+        else:
+            bad[b] = 1
+    want = base.copy()
+    for c in range(cells):
+        s = 0.0
+        for b in range(chunks):
+            s = s + parts[c][b]
+        want[c] = want[c] + s
+    got, status = O.ordered_scatter(key, x, base)
+    assert got.tobytes() == want.tobytes()
+    assert list(status[1:1 + chunks]) == bad
+
+
+@pytest.mark.parametrize("which, lo, hi", [("exp", -30, 30), ("sin", 0.01, 200), ("tanh", -3, 3), ("sqrt", 0, 9)])
+def test_libm_is_close_to_numpy(which, lo, hi):
+    x = np.random.default_rng(2).uniform(lo, hi, 10000)
+    want = {"exp": np.exp, "sin": np.sin, "tanh": np.tanh, "sqrt": np.sqrt}[which](x)
+    ulps = np.abs(O.libm(which, x) - want) / np.spacing(np.abs(want))
+    assert ulps.max() <= 2.0      # two libms, each within an ulp of the true value
+
+
+def _twobody_inputs(n, seed):
+    g = np.random.default_rng(seed)
+    d = g.normal(size=(3, n))
+    d /= np.linalg.norm(d, axis=0)
+    return d * g.uniform(0.5, 2.0, n), g.normal(0.0, 0.3, size=(3, n))
+
+
+def test_twobody_conserves_energy_and_angular_momentum():
+    r0, v0 = _twobody_inputs(200, 3)
+    r, v = O.twobody(r0, v0, 1.0)
+
+    def energy(r, v):
+        return 0.5 * (v * v).sum(0) - 1.0 / np.linalg.norm(r, axis=0)
+    drift = np.abs(energy(r, v) - energy(r0, v0)) / np.abs(energy(r0, v0))
+    assert drift.max() < 1e-5
+    L0, L1 = np.cross(r0.T, v0.T), np.cross(r.T, v.T)
+    np.testing.assert_allclose(L1, L0, rtol=1e-12, atol=1e-13)
+
+
+def test_twobody_matches_a_numpy_leapfrog():
+    """The same KDK step in numpy (vectorised): a transposed or dropped term fails."""
+    r0, v0 = _twobody_inputs(100, 4)
+    r, v = r0.copy(), v0.copy()
+    dt = 1e-3
+    for _ in range(32):
+        r2 = ((r[0] * r[0]) + (r[1] * r[1])) + (r[2] * r[2])
+        a = (-1.0 / (r2 * np.sqrt(r2))) * r
+        vh = v + (0.5 * dt) * a
+        r = r + dt * vh
+        r2 = ((r[0] * r[0]) + (r[1] * r[1])) + (r[2] * r[2])
+        a = (-1.0 / (r2 * np.sqrt(r2))) * r
+        v = vh + (0.5 * dt) * a
+    wr, wv = O.twobody(r0, v0, 1.0)
+    assert wr.tobytes() == r.tobytes() and wv.tobytes() == v.tobytes()
+
+
+def test_twobody_vjp_is_the_transposed_jacobian():
+    n = 20
+    r0, v0 = _twobody_inputs(n, 5)
+    g = np.random.default_rng(6)
+    br, bv = g.normal(size=(3, n)), g.normal(size=(3, n))
+    gr0, gv0 = O.twobody_vjp(r0, v0, 1.0, br, bv)
+    h = 1e-6
+    for name in ("r0", "v0"):
+        for c in range(3):
+            e = np.zeros((3, n))
+            e[c] = h
+
+            def loss(sign):
+                a = r0 + sign * e if name == "r0" else r0
+                b = v0 + sign * e if name == "v0" else v0
+                r, v = O.twobody(np.ascontiguousarray(a), np.ascontiguousarray(b), 1.0)
+                return (br * r).sum(0) + (bv * v).sum(0)
+            fd = (loss(1) - loss(-1)) / (2 * h)
+            got = (gr0 if name == "r0" else gv0)[c]
+            np.testing.assert_allclose(got, fd, rtol=1e-6, atol=1e-8)
+
+
+def _spd(n, seed):
+    g = np.random.default_rng(seed)
+    B = g.normal(size=(n, 6, 6))
+    A = np.matmul(B, B.transpose(0, 2, 1)) + 6.0 * np.eye(6)
+    b = g.normal(size=(n, 6))
+    return A, b, np.ascontiguousarray(A.transpose(1, 2, 0)), np.ascontiguousarray(b.T)
+
+
+def test_spd_solve_matches_lapack():
+    A, b, Ap, bp = _spd(500, 1)
+    x = O.spd_solve(Ap, bp)
+    want = np.linalg.solve(A, b[..., None])[..., 0].T
+    np.testing.assert_allclose(x, want, rtol=1e-12, atol=1e-13)
+    resid = np.matmul(A, x.T[..., None])[..., 0] - b
+    assert np.abs(resid).max() < 1e-12
+
+
+def test_spd_solve_refuses_an_indefinite_matrix_with_zeros():
+    A = np.eye(6)[..., None].repeat(2, axis=2).copy()
+    A[3, 3, 1] = -1.0
+    b = np.ones((6, 2))
+    x = O.spd_solve(np.ascontiguousarray(A), b)
+    assert np.all(x[:, 0] == 1.0) and np.all(x[:, 1] == 0.0)
+
+
+def test_spd_vjp_closed_form_and_finite_differences():
+    A, b, Ap, bp = _spd(40, 2)
+    bar_x = np.random.default_rng(3).normal(size=(6, 40))
+    bA, bb = O.spd_solve_vjp(Ap, bp, bar_x)
+    lam = np.linalg.solve(A.transpose(0, 2, 1), bar_x.T[..., None])[..., 0]     # A^T lam = g (A symmetric)
+    np.testing.assert_allclose(bb, lam.T, rtol=1e-11, atol=1e-13)
+    x = np.linalg.solve(A, b[..., None])[..., 0]
+    outer = lam[:, :, None] * x[:, None, :]
+    want = -0.5 * (outer + outer.transpose(0, 2, 1))
+    np.testing.assert_allclose(bA, want.transpose(1, 2, 0), rtol=1e-10, atol=1e-13)
+    h = 1e-6
+    for i, j in ((0, 0), (1, 4), (5, 2)):
+        e = np.zeros_like(Ap)
+        e[i, j] = h
+        e[j, i] = h if i != j else h
+        fd = ((bar_x * O.spd_solve(Ap + e, bp)).sum(0) - (bar_x * O.spd_solve(Ap - e, bp)).sum(0)) / (2 * h)
+        got = bA[i, j] + (bA[j, i] if i != j else 0.0)
+        np.testing.assert_allclose(got, fd, rtol=1e-6, atol=1e-9)
+
+
+def test_mm16_brute_force_and_vjp():
+    g = np.random.default_rng(8)
+    n = 50
+    A = g.normal(0, 0.25, size=(16, 16, n)).astype(np.float32)
+    B = g.normal(0, 0.25, size=(16, 16, n)).astype(np.float32)
+    G = g.normal(0, 0.25, size=(16, 16, n)).astype(np.float32)
+    C = O.mm16(A, B)
+    want = np.einsum("ikn,kjn->ijn", A.astype(np.float64), B.astype(np.float64))
+    scale = np.einsum("ikn,kjn->ijn", np.abs(A).astype(np.float64), np.abs(B).astype(np.float64))
+    assert np.all(np.abs(C - want) <= 1e-6 * scale + 1e-30)
+    # the rolled order: k ascending, from the first product
+    acc = A[0, 0] * B[0, 0]
+    for k in range(1, 16):
+        acc = acc + A[0, k] * B[k, 0]
+    assert C[0, 0].tobytes() == acc.tobytes()
+    bA, bB = O.mm16_vjp(A, B, G)
+    wA = np.einsum("ikn,jkn->ijn", G.astype(np.float64), B.astype(np.float64))
+    wB = np.einsum("kin,kjn->ijn", A.astype(np.float64), G.astype(np.float64))
+    np.testing.assert_allclose(bA, wA, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(bB, wB, rtol=1e-4, atol=1e-5)
+
+
+def test_threaded_tiles_are_the_serial_bits():
+    x = np.random.default_rng(9).normal(size=100_003)
+    assert O.chain(x, threads=7).tobytes() == O.chain(x).tobytes()
+    r0, v0 = _twobody_inputs(1001, 7)
+    a = O.twobody(r0, v0, 1.0)
+    b = O.twobody(r0, v0, 1.0, threads=5)
+    assert a[0].tobytes() == b[0].tobytes() and a[1].tobytes() == b[1].tobytes()
