@@ -438,9 +438,13 @@ def _annotation(fn, raw, ns):
     return raw
 
 
-def trace(fn) -> Program:
-    """Trace ``fn`` into a :class:`~hawk_amd.ir.Program`."""
+def trace(fn, scope: dict | None = None) -> Program:
+    """Trace ``fn`` into a :class:`~hawk_amd.ir.Program`.  ``scope`` holds the
+    names visible where the kernel was defined (a function's locals), so a
+    string annotation resolves as it would at the definition."""
     ns = dict(fn.__globals__)
+    if scope:
+        ns.update(scope)
     if fn.__closure__:
         for name, cell in zip(fn.__code__.co_freevars, fn.__closure__):
             ns[name] = cell.cell_contents
@@ -544,6 +548,10 @@ class Kernel:
 
 def kernel(fn=None, *, name: str | None = None):
     """``@hawk.kernel``: trace a per-sample function into a :class:`Kernel`."""
-    def wrap(f):
-        return Kernel(name or f.__name__, trace(f))
-    return wrap(fn) if fn is not None else wrap
+    def wrap(f, scope):
+        return Kernel(name or f.__name__, trace(f, scope))
+    caller = inspect.currentframe().f_back
+    scope = dict(caller.f_locals) if caller is not None else None
+    if fn is not None:
+        return wrap(fn, scope)
+    return lambda f: wrap(f, scope)

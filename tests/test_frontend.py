@@ -210,3 +210,12 @@ def test_build_writes_the_unit(tmp_path):
 def test_build_refuses_another_target(tmp_path):
     with pytest.raises(HawkError, match="'hip'"):
         hawk.build([E.scale], tmp_path, targets=("cuda",))
+
+
+def test_a_kernel_defined_in_a_function_reads_its_local_names():
+    from hawk_amd import Scalar as LocalScalar
+
+    @hawk.kernel
+    def k(x: LocalScalar) -> LocalScalar:
+        return x + 1.0
+    assert k.decls["x"].role == "per_sample"
