@@ -51,7 +51,7 @@ def _write(path: Path, data: bytes) -> None:
 
 
 def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64", cache_dir=None,
-                 block: int = 256, per_thread: int = 1) -> Bundle:
+                 block: int = 256, per_thread: int = 1, nontemporal: bool = True) -> Bundle:
     """Build ``kernels`` (a Kernel or a list of them) into ``directory``."""
     if isinstance(kernels, Kernel):
         kernels = [kernels]
@@ -69,11 +69,12 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
     if len(set(names)) != len(names):
         raise HawkError(f"two kernels share a name in {names}")
     for k in kernels:
-        plan = plan_kernel(k.program, k.name, mode=mode, block=block, per_thread=per_thread)
+        plan = plan_kernel(k.program, k.name, mode=mode, block=block, per_thread=per_thread,
+                           nontemporal=nontemporal)
         sidecar = {
             "kernel": k.name, "target": "hip", "offload_arch": "gfx950", "mode": mode,
             "scalar_type": mode, "planes": plan.planes, "team": plan.team,
-            "launch": {"block": block, "per_thread": per_thread},
+            "launch": {"block": block, "per_thread": per_thread, "nontemporal": nontemporal},
             "entry": None, "arg_spec": [], "descriptor": [],
         }
         if plan.stage is not None:

@@ -25,7 +25,7 @@ constexpr int kVirtualLanes = 65536;   // reference hawk/emit/team.py:21-23
 constexpr int kFoldLanes = 1024;
 constexpr int kGroups = 64;            // reference hawk/ir/team.py:649 GROUPS
 constexpr int kLaneBlock = 256;
-constexpr int kSumUnroll = 16;
+constexpr int kSumUnroll = 32;
 
 // Scratch layout (bytes): lanes[65536] f64 | gp[64] f64 | ticket u32 (+pad).
 constexpr size_t kLanesBytes = sizeof(double) * kVirtualLanes;
@@ -94,17 +94,18 @@ __global__ __launch_bounds__(256) void hawk_sum_fold(const double* __restrict__ 
 // Keyed ordered scatter.
 // ---------------------------------------------------------------------------
 constexpr int kScatterChunks = 256;    // reference hawk/_lane_bind.py:108
-constexpr int kWalkThreads = 256;
-constexpr int kWalkItems = 8;
-constexpr int kTile = kWalkThreads * kWalkItems;   // raw lanes per tile, and staged entries per batch
-constexpr int kIdxBits = 11;                       // 2^11 == kTile
+constexpr int kWalkThreads = 512;
+constexpr int kWalkWaves = kWalkThreads / 64;
+constexpr int kWalkItems = 8;                      // keys per thread per tile (striped)
+constexpr int kTile = kWalkThreads * kWalkItems;   // 4096 raw lanes per tile
+constexpr int kStage = 2048;                       // staged entries per batch
+constexpr int kSortItems = kStage / kWalkThreads;  // 4 per thread in the sort
+constexpr int kIdxBits = 11;                       // 2^11 == kStage
 constexpr int kBinCap = 8192;                      // f64 bins a workgroup holds in LDS (64 KiB)
 constexpr int kDigitBits = 4;
 constexpr int kDigits = 1 << kDigitBits;
-constexpr int kSegBatch = 16;
 
-__device__ __forceinline__ unsigned wave_exclusive_scan(unsigned v, unsigned* total_of_wave) {
-    // Inclusive scan over the 64 lanes of this wave by shuffles, then shift.
+__device__ __forceinline__ unsigned wave_inclusive_scan(unsigned v) {
     const int lane = threadIdx.x & 63;
     unsigned x = v;
 #pragma unroll
@@ -112,80 +113,83 @@ __device__ __forceinline__ unsigned wave_exclusive_scan(unsigned v, unsigned* to
         unsigned y = __shfl_up(x, d, 64);
         if (lane >= d) x += y;
     }
-    *total_of_wave = __shfl(x, 63, 64);
-    return x - v;
+    return x;
 }
 
-// Exclusive scan of one value per thread over the 256-thread block.
-__device__ __forceinline__ unsigned block_exclusive_scan(unsigned v, unsigned* scratch4, unsigned* total) {
-    unsigned wave_total;
-    unsigned ex = wave_exclusive_scan(v, &wave_total);
+// Exclusive scan of one value per thread over the block (all threads call it).
+__device__ __forceinline__ unsigned block_exclusive_scan(unsigned v, unsigned* scratch, unsigned* total) {
+    const unsigned incl = wave_inclusive_scan(v);
     const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) scratch4[wave] = wave_total;
+    if ((threadIdx.x & 63) == 63) scratch[wave] = incl;
     __syncthreads();
     unsigned before = 0, all = 0;
 #pragma unroll
-    for (int w = 0; w < kWalkThreads / 64; ++w) {
-        const unsigned s = scratch4[w];
+    for (int w = 0; w < kWalkWaves; ++w) {
+        const unsigned s = scratch[w];
         if (w < wave) before += s;
         all += s;
     }
     __syncthreads();
     *total = all;
-    return ex + before;
+    return incl - v + before;
 }
 
 struct WalkShared {
     double bins[kBinCap];                          // 64 KiB: this partition's partial sums
-    unsigned comp[2][kTile];                       // 16 KiB: (local key << 11) | staged index
-    double vals[kTile];                            // 16 KiB: staged values, arrival order
-    double sorted_vals[kTile];                     // 16 KiB: values in sorted order
-    unsigned short cnt[kDigits * kWalkThreads];    //  8 KiB: radix counters, digit-major
-    unsigned scan[kWalkThreads / 64];
+    unsigned comp[2][kStage];                      // 16 KiB: (local key << 11) | staged index
+    double vals[kStage];                           // 16 KiB: staged values, arrival order
+    double sorted_vals[kStage];                    // 16 KiB: values in sorted order
+    unsigned counts[kDigits * kWalkWaves * kSortItems];   // 2 KiB: per (digit, wave, slot)
+    unsigned scan[kWalkWaves];
+    unsigned slab[kWalkItems][kWalkWaves];         // per (slab, wave) counts of a tile
+    int longs[kStage / 64 + 1];                    // heads of runs of 64 or more
+    int nlong;
 };
 
-// Stable LSD radix sort of kTile composite keys over bits [lo, hi), 4 bits a
-// pass, ping-ponging comp[0] <-> comp[1]; returns the buffer holding the result.
-// Thread t owns items t*8 .. t*8+7 (blocked), processed in order, and the
-// digit-major prefix over (digit, thread) makes every pass stable.
+static_assert(kDigits * kWalkWaves * kSortItems == kWalkThreads, "one radix counter per thread");
+
+// Stable LSD radix sort of the kStage composite keys over bits [lo, hi), 4 bits
+// a pass, ping-ponging comp[0] <-> comp[1]; returns the buffer holding the
+// result.  Element e = wave*256 + slot*64 + lane (the input order); within a
+// (wave, slot) group the lanes with one digit are ranked by ballots, and the
+// exclusive scan over (digit, wave, slot) in that order places every group's
+// members after all earlier ones: each pass is stable.
 __device__ int radix_sort(WalkShared& sh, int lo, int hi) {
     const int t = threadIdx.x;
+    const int wave = t >> 6;
+    const int lane = t & 63;
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     int src = 0;
     for (int shift = lo; shift < hi; shift += kDigitBits) {
         const unsigned* in = sh.comp[src];
         unsigned* out = sh.comp[src ^ 1];
-        unsigned item[kWalkItems];
+        unsigned item[kSortItems], digit[kSortItems], rank[kSortItems];
 #pragma unroll
-        for (int j = 0; j < kWalkItems; ++j) item[j] = in[t * kWalkItems + j];
+        for (int j = 0; j < kSortItems; ++j) {
+            item[j] = in[wave * (kSortItems * 64) + j * 64 + lane];
+            digit[j] = (item[j] >> shift) & (kDigits - 1);
+            unsigned long long bits[kDigitBits];
 #pragma unroll
-        for (int d = 0; d < kDigits; ++d) sh.cnt[d * kWalkThreads + t] = 0;
+            for (int b = 0; b < kDigitBits; ++b) bits[b] = __ballot((digit[j] >> b) & 1u);
+            unsigned long long peers = ~0ull;          // lanes whose digit equals mine
 #pragma unroll
-        for (int j = 0; j < kWalkItems; ++j) {
-            const unsigned d = (item[j] >> shift) & (kDigits - 1);
-            sh.cnt[d * kWalkThreads + t] = static_cast<unsigned short>(sh.cnt[d * kWalkThreads + t] + 1);
+            for (int b = 0; b < kDigitBits; ++b) peers &= ((digit[j] >> b) & 1u) ? bits[b] : ~bits[b];
+            rank[j] = static_cast<unsigned>(__popcll(peers & below));
+            // lane d < 16 counts the group's members with digit d
+            unsigned long long with_d = ~0ull;
+#pragma unroll
+            for (int b = 0; b < kDigitBits; ++b) with_d &= ((lane >> b) & 1) ? bits[b] : ~bits[b];
+            if (lane < kDigits)
+                sh.counts[(lane * kWalkWaves + wave) * kSortItems + j] = static_cast<unsigned>(__popcll(with_d));
         }
         __syncthreads();
-        // Thread t scans the 16 consecutive counters [16t, 16t+16) of the
-        // digit-major order, then the block offsets those runs.
-        unsigned run = 0;
-#pragma unroll
-        for (int k = 0; k < kDigits; ++k) run += sh.cnt[t * kDigits + k];
         unsigned total;
-        unsigned base = block_exclusive_scan(run, sh.scan, &total);
-#pragma unroll
-        for (int k = 0; k < kDigits; ++k) {
-            const unsigned c = sh.cnt[t * kDigits + k];
-            sh.cnt[t * kDigits + k] = static_cast<unsigned short>(base);
-            base += c;
-        }
+        const unsigned off = block_exclusive_scan(sh.counts[t], sh.scan, &total);
+        sh.counts[t] = off;                          // every thread read its count before the scan's barrier
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < kWalkItems; ++j) {
-            const unsigned d = (item[j] >> shift) & (kDigits - 1);
-            const unsigned pos = sh.cnt[d * kWalkThreads + t];
-            sh.cnt[d * kWalkThreads + t] = static_cast<unsigned short>(pos + 1);
-            out[pos] = item[j];
-        }
+        for (int j = 0; j < kSortItems; ++j)
+            out[sh.counts[(digit[j] * kWalkWaves + wave) * kSortItems + j] + rank[j]] = item[j];
         __syncthreads();
         src ^= 1;
     }
@@ -193,56 +197,81 @@ __device__ int radix_sort(WalkShared& sh, int lo, int hi) {
 }
 
 // Sort the `m` staged entries by local key (stable, so arrival order holds
-// within a key) and add each key's run, in order, onto its bin.
+// within a key) and add each key's run, in order, onto its bin: a run shorter
+// than 64 by one lane, a longer one by a whole wave (64 values per LDS load,
+// folded in order through uniform readlanes).
 __device__ void flush_batch(WalkShared& sh, int m, int key_bits) {
     const int t = threadIdx.x;
-    for (int j = m + t; j < kTile; j += kWalkThreads) sh.comp[0][j] = 0xffffffffu;
+    const int wave = t >> 6;
+    const int lane = t & 63;
+    for (int j = m + t; j < kStage; j += kWalkThreads) sh.comp[0][j] = 0xffffffffu;
+    if (t == 0) sh.nlong = 0;
     __syncthreads();
     const int buf = radix_sort(sh, kIdxBits, kIdxBits + key_bits);
     unsigned* comp = sh.comp[buf];
-    for (int j = t; j < m; j += kWalkThreads) sh.sorted_vals[j] = sh.vals[comp[j] & (kTile - 1)];
+    for (int j = t; j < m; j += kWalkThreads) sh.sorted_vals[j] = sh.vals[comp[j] & (kStage - 1)];
     __syncthreads();
     for (int j = t; j < m; j += kWalkThreads) {
         const unsigned key = comp[j] >> kIdxBits;
         if (j > 0 && (comp[j - 1] >> kIdxBits) == key) continue;   // not the head of its run
-        double acc = sh.bins[key];
-        int jj = j;
-        bool open = true;
-        while (open) {
-            unsigned ck[kSegBatch];
-            double cv[kSegBatch];
-#pragma unroll
-            for (int k = 0; k < kSegBatch; ++k) {
-                const int at = jj + k < m ? jj + k : m - 1;
-                ck[k] = comp[at] >> kIdxBits;
-                cv[k] = sh.sorted_vals[at];
-            }
-#pragma unroll
-            for (int k = 0; k < kSegBatch; ++k) {
-                if (open && jj + k < m && ck[k] == key) acc = acc + cv[k];
-                else open = false;
-            }
-            jj += kSegBatch;
-            open = open && jj < m;
+        if (j + 63 < m && (comp[j + 63] >> kIdxBits) == key) {     // sorted: a run of 64 or more
+            sh.longs[atomicAdd(&sh.nlong, 1)] = j;
+            continue;
         }
+        double acc = sh.bins[key];
+        for (int jj = j; jj < m && (comp[jj] >> kIdxBits) == key; ++jj) acc = acc + sh.sorted_vals[jj];
         sh.bins[key] = acc;
+    }
+    __syncthreads();
+    for (int r = wave; r < sh.nlong; r += kWalkWaves) {
+        const int j = sh.longs[r];
+        const unsigned key = comp[j] >> kIdxBits;
+        double acc = sh.bins[key];
+        for (int base = j; base < m; base += 64) {
+            const int e = base + lane;
+            const bool in = e < m && (comp[e] >> kIdxBits) == key;
+            const double x = in ? sh.sorted_vals[e] : 0.0;
+            const int cnt = __popcll(__ballot(in));     // a prefix of the lanes: the run is contiguous
+            const int xlo = __double2loint(x);
+            const int xhi = __double2hiint(x);
+            for (int k = 0; k < cnt; ++k)
+                acc = acc + __hiloint2double(__builtin_amdgcn_readlane(xhi, k), __builtin_amdgcn_readlane(xlo, k));
+            if (cnt < 64) break;
+        }
+        if (lane == 0) sh.bins[key] = acc;
     }
     __syncthreads();
 }
 
+// Load the striped tile at `tile`: element j*512 + t of the tile goes to
+// thread t's slot j, so every load instruction of a wave is one contiguous run.
+__device__ __forceinline__ void load_tile(const int* __restrict__ key, const double* __restrict__ v, long long tile,
+                                          long long hi, int (&kk)[kWalkItems], double (&vv)[kWalkItems]) {
+#pragma unroll
+    for (int j = 0; j < kWalkItems; ++j) {
+        const long long i = tile + static_cast<long long>(j) * kWalkThreads + threadIdx.x;
+        const bool in = i < hi;
+        kk[j] = in ? __builtin_nontemporal_load(key + i) : -1;
+        vv[j] = in ? __builtin_nontemporal_load(v + i) : 0.0;
+    }
+}
+
 // One workgroup per (chunk b, key partition q): keys k with k % Q == q, local
 // key k / Q, live in LDS bins.  The workgroup walks its chunk's lanes in
-// order, stages its partition's (key, value) pairs, and adds every batch into
-// the bins; the bins of every key of the partition (zeros included) go to
-// partsT[b*cells + k] at the end, so no zeroing stage is needed.
-// The Q workgroups of one chunk take consecutive dispatch slots of one XCD,
-// so the chunk's key lines are fetched from HBM once and re-read from L2.
+// order (the next tile's keys and values in flight while the current one is
+// staged), stages its partition's (key, value) pairs in lane order, and adds
+// every batch into the bins; the bins of every key of the partition (zeros
+// included) go to partsT[b*cells + k] at the end, so no zeroing stage is
+// needed.  The Q workgroups of one chunk take consecutive dispatch slots of
+// one XCD, so the chunk's keys are fetched from HBM once and re-read from L2.
 __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
         const int* __restrict__ key, const double* __restrict__ v, long long n, long long cells,
         int chunks, long long span, int parts, int key_bits, double* __restrict__ partsT,
         int* __restrict__ status) {
     __shared__ WalkShared sh;
     const int t = threadIdx.x;
+    const int wave = t >> 6;
+    const int lane = t & 63;
     const long long total = static_cast<long long>(chunks) * parts;
     long long w = blockIdx.x;
     if (total % 8 == 0) w = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
@@ -255,33 +284,54 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
     for (long long k = t; k < nb; k += kWalkThreads) sh.bins[k] = 0.0;
     int staged = 0;
     bool bad = false;
+    int nk[kWalkItems];
+    double nv[kWalkItems];
+    if (lo < hi) load_tile(key, v, lo, hi, nk, nv);
     __syncthreads();
     for (long long tile = lo; tile < hi; tile += kTile) {
         int kk[kWalkItems];
-        bool mine[kWalkItems];
-        unsigned count = 0;
+        double vv[kWalkItems];
+#pragma unroll
+        for (int j = 0; j < kWalkItems; ++j) { kk[j] = nk[j]; vv[j] = nv[j]; }
+        if (tile + kTile < hi) load_tile(key, v, tile + kTile, hi, nk, nv);
+        // Per slab j (512 consecutive lanes), this wave's members in lane order.
+        unsigned long long mask[kWalkItems];
 #pragma unroll
         for (int j = 0; j < kWalkItems; ++j) {
-            const long long i = tile + static_cast<long long>(t) * kWalkItems + j;
-            kk[j] = i < hi ? key[i] : -1;
             const bool valid = kk[j] >= 0 && kk[j] < cells;
             bad = bad || (kk[j] != -1 && !valid);
-            mine[j] = valid && (kk[j] % parts == q);
-            count += mine[j] ? 1u : 0u;
+            const bool mine = valid && (kk[j] % parts == q);
+            mask[j] = __ballot(mine);
+            if (lane == 0) sh.slab[j][wave] = static_cast<unsigned>(__popcll(mask[j]));
         }
-        unsigned m;
-        unsigned off = block_exclusive_scan(count, sh.scan, &m);
-        if (staged + static_cast<int>(m) > kTile) {
-            flush_batch(sh, staged, key_bits);
-            staged = 0;
-        }
+        __syncthreads();
+        // Offsets: all of slab j' < j first, then the waves before this one in slab j.
+        unsigned before[kWalkItems];
+        unsigned m = 0;
 #pragma unroll
         for (int j = 0; j < kWalkItems; ++j) {
-            if (!mine[j]) continue;
-            const unsigned idx = static_cast<unsigned>(staged) + off++;
-            const long long i = tile + static_cast<long long>(t) * kWalkItems + j;
+            unsigned inslab = 0, mine_before = 0;
+#pragma unroll
+            for (int x = 0; x < kWalkWaves; ++x) {
+                const unsigned c = sh.slab[j][x];
+                if (x < wave) mine_before += c;
+                inslab += c;
+            }
+            before[j] = m + mine_before;
+            m += inslab;
+        }
+        if (staged + static_cast<int>(m) > kStage) {
+            flush_batch(sh, staged, key_bits);      // ends with a barrier
+            staged = 0;
+        }
+        const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+        for (int j = 0; j < kWalkItems; ++j) {
+            if (!((mask[j] >> lane) & 1ull)) continue;
+            const unsigned idx = static_cast<unsigned>(staged) + before[j] +
+                                 static_cast<unsigned>(__popcll(mask[j] & below));
             sh.comp[0][idx] = (static_cast<unsigned>(kk[j] / parts) << kIdxBits) | idx;
-            sh.vals[idx] = v[i];
+            sh.vals[idx] = vv[j];
         }
         staged += static_cast<int>(m);
         __syncthreads();

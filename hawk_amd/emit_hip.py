@@ -108,9 +108,10 @@ class _Scope:
 class _Writer:
     """Scalarises nodes into C++ statements."""
 
-    def __init__(self, stage: Stage, mode: str):
+    def __init__(self, stage: Stage, mode: str, nontemporal: bool = False):
         self.stage = stage
         self.mode = mode
+        self.nontemporal = nontemporal
         self.lines: list = []
         self.indent = 2
         self.count = 0
@@ -171,12 +172,18 @@ class _Writer:
             role = "per_sample" if not n.ttype.shape else ("vec_in" if len(n.ttype.shape) == 1 else "mat_in")
         dt = n.ttype.dtype
         if not n.ttype.shape:
-            return [self.let(dt, f"{p}[hk_i]", "in")]
+            return [self.let(dt, self.load(f"{p}[hk_i]"), "in")]
         out = []
         for e in _entries(n.ttype.shape):
             c = _flat(n.ttype.shape, e)
-            out.append(self.let(dt, f"{p}[{c} * {p}_cs + hk_i]", "in"))
+            out.append(self.let(dt, self.load(f"{p}[{c} * {p}_cs + hk_i]"), "in"))
         return out
+
+    def load(self, ref: str) -> str:
+        return f"__builtin_nontemporal_load(&{ref})" if self.nontemporal else ref
+
+    def store(self, ref: str, value: str) -> str:
+        return f"__builtin_nontemporal_store({value}, &{ref});" if self.nontemporal else f"{ref} = {value};"
 
     def _const(self, n: Node) -> list:
         return [_literal(n.literal)]
@@ -449,9 +456,11 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
     return Stage(stage_name, spec, planes, writes)
 
 
-def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_taped: bool = True) -> str:
-    """The HIP source of one per-sample stage."""
-    w = _Writer(stage, mode)
+def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_taped: bool = True,
+                 nontemporal: bool = False) -> str:
+    """The HIP source of one per-sample stage.  ``nontemporal`` marks the
+    plane loads and stores as streaming (read or written once, not kept in cache)."""
+    w = _Writer(stage, mode, nontemporal)
     roots = [node for _, node in stage.writes]
     # which loops keep a tape
     for n in ir.topo(roots):
@@ -473,11 +482,11 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         var = info["var"]
         vals = w.value(node)
         if not node.ttype.shape:
-            w.emit(f"{var}[hk_i] = {vals[0]};")
+            w.emit(w.store(f"{var}[hk_i]", vals[0]))
         else:
             for e in _entries(node.ttype.shape):
                 c = _flat(node.ttype.shape, e)
-                w.emit(f"{var}[{c} * {var}_cs + hk_i] = {vals[c]};")
+                w.emit(w.store(f"{var}[{c} * {var}_cs + hk_i]", vals[c]))
     stores = list(w.lines)
 
     real = "float" if mode == "float32" else "double"
@@ -540,7 +549,7 @@ class Plan:
 
 
 def plan_kernel(program: Program, name: str, mode: str = "float64", block: int = 256,
-                per_thread: int = 1) -> Plan:
+                per_thread: int = 1, nontemporal: bool = False) -> Plan:
     """Split ``program`` into its per-sample stage and team stages, and render
     the per-sample stage."""
     if mode not in ("float64", "float32"):
@@ -572,7 +581,7 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
     stage = source = None
     if has_stage:
         stage = _stage_planes(program, name, mode, extra)
-        source = render_stage(stage, mode, block, per_thread)
+        source = render_stage(stage, mode, block, per_thread, nontemporal=nontemporal)
     planes = {}
     if stage is not None:
         for pname, info in stage.planes.items():
