@@ -94,8 +94,12 @@ def lib():
             # PyTorch-ROCm ships its own HIP runtime (libamdhip64, libhsa-runtime64,
             # libhiprtc) under torch/lib.  Loading it first makes this library's
             # NEEDED sonames bind to that one copy; loading /opt/rocm's beside it
-            # would put two HIP runtimes in one process, which faults.
-            import torch  # noqa: F401
+            # would put two HIP runtimes in one process, which faults.  Only the
+            # compile worker (hawk_amd._rtc_worker), which never touches a GPU,
+            # loads the system copies instead.
+            import os
+            if os.environ.get("HAWK_NO_TORCH_PRELOAD") != "1":
+                import torch  # noqa: F401
             if not _LIB_PATH.exists():
                 raise HawkError(f"hawk_amd: {_LIB_PATH} is not built; build it first "
                                 "(python hawk_amd/_build.py). The hip target has no fallback path.")

@@ -18,6 +18,7 @@ from dataclasses import dataclass
 from pathlib import Path
 
 from . import compile as _compile
+from .resources import kernel_resources
 from .emit_hip import plan_kernel
 from .ir import HawkError
 from .trace import Kernel
@@ -68,9 +69,12 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
     names = [k.name for k in kernels]
     if len(set(names)) != len(names):
         raise HawkError(f"two kernels share a name in {names}")
-    for k in kernels:
-        plan = plan_kernel(k.program, k.name, mode=mode, block=block, per_thread=per_thread,
-                           nontemporal=nontemporal)
+    plans = [(k, plan_kernel(k.program, k.name, mode=mode, block=block, per_thread=per_thread,
+                             nontemporal=nontemporal)) for k in kernels]
+    staged = [(k, p) for k, p in plans if p.stage is not None]
+    compiled = dict(zip([k.name for k, _ in staged],
+                        _compile.compile_units([(k.name, p.source) for k, p in staged], cache_dir=cache_dir)))
+    for k, plan in plans:
         sidecar = {
             "kernel": k.name, "target": "hip", "offload_arch": "gfx950", "mode": mode,
             "scalar_type": mode, "planes": plan.planes, "team": plan.team,
@@ -78,7 +82,7 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
             "entry": None, "arg_spec": [], "descriptor": [],
         }
         if plan.stage is not None:
-            code, key, _hit = _compile.compile_source(plan.source, k.name, cache_dir=cache_dir)
+            code, key, _hit = compiled[k.name]
             _write(directory / f"{k.name}.hip", plan.source.encode())
             _write(directory / f"{k.name}.hsaco", code)
             sidecar.update({
@@ -89,6 +93,8 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
                 "source_sha256": hashlib.sha256(plan.source.encode()).hexdigest(),
                 "code_sha256": hashlib.sha256(code).hexdigest(),
                 "cache_key": key, "compile_options": list(_compile.RTC_OPTIONS),
+                "toolchain": _compile.toolchain(),
+                "resources": kernel_resources(code).get(k.name, {}),
             })
         _write(directory / f"{k.name}.json", json.dumps(sidecar, indent=1, sort_keys=True).encode())
         artifacts.append(Artifact(k.name, sidecar))

@@ -1,23 +1,32 @@
 """The hipRTC build-and-cache path of the gfx950 target.
 
-``compile_source`` compiles one HIP translation unit with hipRTC for
+``compile_units`` compiles HIP translation units with hipRTC for
 ``--offload-arch=gfx950`` (through ``hk_rtc_compile`` of the C-ABI) and keeps
-the code object in a content-addressed cache, the shape of reference
+the code objects in a content-addressed cache, the shape of reference
 ``hawk/compile/cache.py:347-459``: the key is the sha256 of the source, the
-options, the hipRTC version and the target, so a changed compiler or flag is a
-miss and an unchanged kernel is one file read.  Entries are published
-atomically (write to a temporary name, then rename).
+options, the compiler's identity and the target, so a changed compiler or
+flag is a miss and an unchanged kernel is one file read.  Entries are
+published atomically (write to a temporary name, then rename).
+
+The compile itself runs in a worker process that never imports torch
+(:mod:`hawk_amd._rtc_worker`), so it uses the system ROCm toolchain rather
+than the copy PyTorch-ROCm bundles; ``HAWK_RTC_IN_PROCESS=1`` compiles in this
+process with whichever hipRTC is loaded here.
 """
 
 from __future__ import annotations
 
+import base64
 import hashlib
 import json
 import os
+import subprocess
+import sys
 import threading
 from pathlib import Path
 
 from . import _core
+from .ir import HawkError
 
 #: Options every device unit is compiled with: no floating-point contraction
 #: (the device computes the host oracle's ``native``-profile operations),
@@ -34,9 +43,45 @@ def default_cache_dir() -> Path:
     return Path(env) if env else Path(__file__).resolve().parent / "_cache"
 
 
+_toolchain_lock = threading.Lock()
+_toolchain: dict = {}
+
+
+def _in_process() -> bool:
+    return os.environ.get("HAWK_RTC_IN_PROCESS") == "1"
+
+
+def _run_worker(units: list, options) -> dict:
+    job = json.dumps({"options": list(options), "units": [list(u) for u in units]})
+    env = dict(os.environ, HAWK_NO_TORCH_PRELOAD="1")
+    root = str(Path(__file__).resolve().parent.parent)
+    env["PYTHONPATH"] = root + (os.pathsep + env["PYTHONPATH"] if env.get("PYTHONPATH") else "")
+    proc = subprocess.run([sys.executable, "-m", "hawk_amd._rtc_worker"], input=job, capture_output=True,
+                          text=True, env=env)
+    if proc.returncode != 0:
+        raise HawkError(f"the hipRTC worker failed (exit {proc.returncode}): {proc.stderr[-2000:]}")
+    reply = json.loads(proc.stdout)
+    if not reply.get("ok"):
+        raise HawkError(reply.get("error", "the hipRTC worker failed"))
+    return reply
+
+
+def toolchain() -> str:
+    """The identity of the compiler the build uses (part of every cache key)."""
+    key = "in-process" if _in_process() else "worker"
+    with _toolchain_lock:
+        if key not in _toolchain:
+            if _in_process():
+                from ._rtc_worker import toolchain_identity
+                _toolchain[key] = toolchain_identity(_core.lib())
+            else:
+                _toolchain[key] = _run_worker([], RTC_OPTIONS)["toolchain"]
+        return _toolchain[key]
+
+
 def cache_key(source: str, options) -> str:
     blob = json.dumps({"source": source, "options": list(options), "target": "gfx950",
-                       "hiprtc": _core.rtc_version()}, sort_keys=True)
+                       "toolchain": toolchain()}, sort_keys=True)
     return hashlib.sha256(blob.encode()).hexdigest()
 
 
@@ -45,20 +90,38 @@ def cache_stats() -> dict:
         return dict(_stats)
 
 
-def compile_source(source: str, name: str, options=RTC_OPTIONS, cache_dir=None) -> tuple:
-    """``(code object bytes, cache key, hit)`` for ``source``."""
+def compile_units(units: list, options=RTC_OPTIONS, cache_dir=None) -> list:
+    """``[(code object bytes, cache key, hit)]`` for ``units`` = ``[(name, source)]``,
+    compiling every miss in one hipRTC worker call."""
     cache = Path(cache_dir) if cache_dir is not None else default_cache_dir()
-    key = cache_key(source, options)
-    path = cache / f"{key}.hsaco"
-    if path.exists():
-        with _stats_lock:
-            _stats["hits"] += 1
-        return path.read_bytes(), key, True
-    code, _log = _core.rtc_compile(source, f"{name}.hip", list(options))
-    cache.mkdir(parents=True, exist_ok=True)
-    tmp = path.with_suffix(f".tmp{os.getpid()}_{threading.get_ident()}")
-    tmp.write_bytes(code)
-    os.replace(tmp, path)
+    keys = [cache_key(src, options) for _, src in units]
+    out: list = [None] * len(units)
+    misses = []
+    for i, ((name, src), key) in enumerate(zip(units, keys)):
+        path = cache / f"{key}.hsaco"
+        if path.exists():
+            out[i] = (path.read_bytes(), key, True)
+        else:
+            misses.append(i)
+    if misses:
+        todo = [(f"{units[i][0]}.hip", units[i][1]) for i in misses]
+        if _in_process():
+            codes = [_core.rtc_compile(src, name, list(options))[0] for name, src in todo]
+        else:
+            codes = [base64.b64decode(c) for _n, c, _log in _run_worker(todo, options)["units"]]
+        cache.mkdir(parents=True, exist_ok=True)
+        for i, code in zip(misses, codes):
+            path = cache / f"{keys[i]}.hsaco"
+            tmp = path.with_suffix(f".tmp{os.getpid()}_{threading.get_ident()}")
+            tmp.write_bytes(code)
+            os.replace(tmp, path)
+            out[i] = (code, keys[i], False)
     with _stats_lock:
-        _stats["misses"] += 1
-    return code, key, False
+        _stats["hits"] += len(units) - len(misses)
+        _stats["misses"] += len(misses)
+    return out
+
+
+def compile_source(source: str, name: str, options=RTC_OPTIONS, cache_dir=None) -> tuple:
+    """``(code object bytes, cache key, hit)`` for one unit."""
+    return compile_units([(name, source)], options, cache_dir)[0]

@@ -221,6 +221,9 @@ class _Reverse:
         return store
 
     def _reverse_loop(self, loop: Node, seeds: dict) -> list:
+        segmented = _strip_mined(loop, self.deps)
+        if segmented is not None:
+            loop = segmented
         info = loop.literal
         m = len(info.carries)
         free = [f for f in free_inputs(loop, self.deps) if self.active(f)]
@@ -247,6 +250,46 @@ class _Reverse:
         out = [(info_init, ir.loop_value(reverse, j)) for j, info_init in enumerate(loop.operands)]
         out += [(f, ir.loop_value(reverse, m + i)) for i, f in enumerate(free)]
         return out
+
+
+#: The longest recurrence reversed with a single tape: a longer one is cut into
+#: segments of this many iterations first (see :func:`_strip_mined`).
+CHECKPOINT_SEGMENT = 4
+
+
+def _strip_mined(loop: Node, deps: Deps):
+    """``loop`` (trip T) as an outer loop of T/S iterations whose body is an inner
+    loop of S iterations, S = :data:`CHECKPOINT_SEGMENT`, or None when it does
+    not apply (T <= S, T not a multiple of S, or a body reading its index).
+
+    The two compute the same operations in the same order, so the primal bits
+    do not change.  Reversing the nested form tapes only the T/S segment starts
+    and, per segment, replays the segment forward with an S-entry tape before
+    reversing it: checkpointing by construction, which keeps the live tape at
+    T/S + S carried values instead of T (the reference tapes every iteration,
+    hawk/diff/loops.py:484-540, in local memory; a gfx950 lane keeps its tape
+    in registers, so the tape's size sets the occupancy)."""
+    info = loop.literal
+    seg = CHECKPOINT_SEGMENT
+    if info.trip <= seg or info.trip % seg:
+        return None
+    if any(n is info.index for n in ir.topo(info.nexts)):
+        return None
+    _, outer_index, outer_carries, _ = fresh_placeholders(loop)
+    inner_uid, inner_index, inner_carries, mapping = fresh_placeholders(loop)
+    outer_uid = next(ir._uid)
+    outer_index.literal = outer_uid
+    outer_carries = tuple(Node("carry", (), c.ttype, (outer_uid, j)) for j, c in enumerate(outer_carries))
+    inner_nexts = ir.substitute(info.nexts, mapping)
+    inner = ir.loop_node(inner_uid, seg, 0, 1, inner_index, inner_carries, outer_carries, tuple(inner_nexts),
+                         info.names)
+    outer_nexts = tuple(ir.loop_value(inner, j) for j in range(len(info.carries)))
+    outer = ir.loop_node(outer_uid, info.trip // seg, 0, 1, outer_index, outer_carries, loop.operands,
+                         outer_nexts, info.names)
+    inner.literal.unroll = outer.literal.unroll = info.unroll
+    deps.register(inner)
+    deps.register(outer)
+    return outer
 
 
 def _refuse_prior_reads(program: Program, what: str) -> None:

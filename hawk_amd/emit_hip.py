@@ -388,8 +388,10 @@ class _Writer:
             self.tape_of = getattr(self, "tape_of", {})
             self.tape_of[n.uid] = (tapes, info.start, info.step)
         k = f"hk_k{n.uid}"
-        if info.unroll:
+        if info.unroll is True:
             self.emit("#pragma unroll")
+        elif info.unroll is False:
+            self.emit("#pragma unroll 1")
         self.emit(f"for (long long {k} = {info.start}LL; {k} != {info.stop()}LL; {k} += {info.step}LL) {{")
         self.indent += 1
         self.scope.memo.append({})
@@ -462,18 +464,22 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     plane loads and stores as streaming (read or written once, not kept in cache)."""
     w = _Writer(stage, mode, nontemporal)
     roots = [node for _, node in stage.writes]
-    # which loops keep a tape
+    # Which loops keep a tape: a loop that keeps or reads a tape, and every loop
+    # nested in one, is unrolled, so every tape index is a constant and the tapes
+    # live in registers (a checkpointed reverse keeps few enough of them live).
     for n in ir.topo(roots):
         if n.kind == "tape_read":
             w.taped[n.operands[0].uid] = True
-            if unroll_taped:
-                n.operands[0].literal.unroll = True
-                for m in ir.topo([n]):
-                    if m.kind == "loop":
-                        m.literal.unroll = True
-    for n in ir.topo(roots):
-        if n.kind == "loop" and any(t.kind == "tape_read" for t in ir.topo(n.literal.nexts)) and unroll_taped:
-            n.literal.unroll = True
+    if unroll_taped:
+        for n in ir.topo(roots):
+            if n.kind != "loop":
+                continue
+            inner = ir.topo(n.literal.nexts)
+            taped = n.uid in w.taped or any(m.kind == "tape_read" or (m.kind == "loop" and m.uid in w.taped)
+                                            for m in inner)
+            if taped:
+                for m in [n] + [m for m in inner if m.kind == "loop"]:
+                    m.literal.unroll = True
     w.run(roots)
     body = list(w.lines)
     w.lines = []

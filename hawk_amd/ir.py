@@ -67,7 +67,7 @@ class LoopInfo:
     carries: tuple                   # kind "carry" placeholders, one per slot
     nexts: tuple                     # the body's value of each slot
     names: tuple = ()                # the authored names of the slots (diagnostics)
-    unroll: bool = False             # emit with #pragma unroll
+    unroll: bool | None = None       # True: #pragma unroll; False: kept rolled; None: the compiler's choice
 
     def stop(self) -> int:
         return self.start + self.trip * self.step
@@ -326,29 +326,31 @@ class Deps:
 
 
 def free_inputs(loop: Node, deps: Deps) -> list:
-    """The nodes outside ``loop`` its body reads: every operand of a body node
-    that does not itself depend on the loop, in first-reach order."""
+    """The nodes outside ``loop`` its body reads, in first-reach order: a walk
+    from the body's values that stops at every node not depending on the loop
+    and sees a nested loop as one node whose operands are its inits and its own
+    free inputs (never the nodes inside the nested body)."""
     deps.register(loop)
-    body = topo(loop.literal.nexts)
-    for n in body:               # a body can reach other loops (a tape read's loop): register them first
+    for n in topo(loop.literal.nexts):    # a body can reach other loops (a tape read's loop): register them
         if n.kind == "loop":
             deps.register(n)
     key = loop.literal.index.uid
-    out, seen = [], set()
-    for n in body:
+    out, seen, expanded = [], set(), set()
+    stack = list(reversed(loop.literal.nexts))
+    while stack:
+        n = stack.pop()
         if key not in deps.of(n):
+            if n.uid not in seen and n.kind not in ("const", "iconst"):
+                seen.add(n.uid)
+                out.append(n)
             continue
+        if n.uid in expanded:
+            continue
+        expanded.add(n.uid)
         kids = list(n.operands)
-        if n.kind == "loop":
+        if n.kind == "loop" and n is not loop:
             kids += free_inputs(n, deps)
-        for k in kids:
-            if key not in deps.of(k) and k.uid not in seen and k.kind not in ("const", "iconst"):
-                seen.add(k.uid)
-                out.append(k)
-    for x in loop.literal.nexts:
-        if key not in deps.of(x) and x.uid not in seen and x.kind not in ("const", "iconst"):
-            seen.add(x.uid)
-            out.append(x)
+        stack.extend(reversed(kids))
     return out
 
 

@@ -149,6 +149,8 @@ def test_twobody_forward_and_vjp(unit, gpu, n):
     wbr0, wbv0 = O.twobody_vjp(r0, v0, 1.0, bar_r, bar_v)
     assert within_contract(host(br0), wbr0).all()
     assert within_contract(host(bv0), wbv0).all()
+    # the checkpointed rolled reverse replays the oracle's operations: the same bits
+    assert host(br0).tobytes() == wbr0.tobytes() and host(bv0).tobytes() == wbv0.tobytes()
 
 
 # -- config 4a ------------------------------------------------------------------
@@ -176,6 +178,7 @@ def test_spd_solve_and_vjp_are_the_oracle(unit, gpu, n):
              bar_b=bb)
     wA, wb = O.spd_solve_vjp(A, b, bar_x)
     assert within_contract(host(bA), wA).all() and within_contract(host(bb), wb).all()
+    assert host(bA).tobytes() == wA.tobytes() and host(bb).tobytes() == wb.tobytes()
 
 
 # -- config 5 -------------------------------------------------------------------
