@@ -6,10 +6,14 @@ resident in HBM.  The default workload is BASELINE.json's ``configs[1]``: the
 ``energy`` kernel's forward, VJP and JVP over N = 2^25 samples (fp64).  Other
 configurations (``--config 1|3|4a|5``) time the remaining workloads the same way.
 
-Each kernel launch of the timed steps is bracketed by HIP events on the stream
-it is launched on (torch's current stream), so the per-kernel durations, the
-achieved algorithmic GB/s (bytes per sample x samples / duration) and the
-roofline fraction come from the timed run itself.  The CPU baseline is the C
+Each stage launch of the timed steps (a per-sample kernel, or a team stage:
+the ordered sum or the ordered scatter) is bracketed by HIP events on the
+stream it is launched on (torch's current stream), so the per-stage durations,
+the achieved algorithmic GB/s (bytes per sample x samples / duration) and the
+roofline fraction come from the timed run itself.  ``roofline.traffic`` is the
+dominant stage's HBM bytes per launch from two child ``rocprofv3 --pmc`` passes
+(FETCH_SIZE, then WRITE_SIZE), each scaled by what that counter reads for a
+plain 1 GiB copy (``--no-traffic`` skips them).  The CPU baseline is the C
 oracle (the host-target restatement, hawk's ``native`` profile) on the same
 workload, on this host's cores.
 """
@@ -62,13 +66,14 @@ def workload(config: str, device):
         hawk.build([E.scale], unit)
         k = hawk.load(unit, "scale")
         X, OUT = _dev(x, device), torch.zeros(n, dtype=torch.float64, device=device)
-        kernels = [("scale", k.prepare(x=X, a=2.0, b=1.0, out=OUT), 16, 2)]
+        kernels = [k.prepare(x=X, a=2.0, b=1.0, out=OUT)]
+        work = {"scale": (16, 2)}
 
         def cpu(threads):
             import oracle_lib as O
             out = np.empty(n)
             O.lib("native").hko_tiled(1, O._p(x), None, None, None, O._p(out), None, 2.0, 1.0, n, threads)
-        return dict(name="scale fwd (config 1)", n=n, kernels=kernels, cpu=cpu, dtype="f64")
+        return dict(name="scale fwd (config 1)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64")
     if config == "2":
         n = 1 << 25
         g = np.random.default_rng(2)
@@ -82,9 +87,9 @@ def workload(config: str, device):
         OUT = torch.zeros(n, dtype=torch.float64, device=device)
         BV = torch.zeros((3, n), dtype=torch.float64, device=device)
         DO = torch.zeros(n, dtype=torch.float64, device=device)
-        kernels = [("energy", kf.prepare(v=V, out=OUT), 32, 6),
-                   ("energy_vjp", kv.prepare(v=V, bar_out=BO, bar_v=BV), 56, 4),
-                   ("energy_jvp", kj.prepare(v=V, dot_v=DV, dot_out=DO), 56, 12)]
+        kernels = [kf.prepare(v=V, out=OUT), kv.prepare(v=V, bar_out=BO, bar_v=BV),
+                   kj.prepare(v=V, dot_v=DV, dot_out=DO)]
+        work = {"energy": (32, 6), "energy_vjp": (56, 4), "energy_jvp": (56, 12)}
 
         def cpu(threads):
             import oracle_lib as O
@@ -93,7 +98,7 @@ def workload(config: str, device):
             L.hko_tiled(2, O._p(v), None, None, None, O._p(out), None, 0.0, 0.0, n, threads)
             L.hko_tiled(3, O._p(v), O._p(bar_out), None, None, O._p(bv), None, 0.0, 0.0, n, threads)
             L.hko_tiled(4, O._p(v), O._p(dv), None, None, O._p(do), None, 0.0, 0.0, n, threads)
-        return dict(name="energy fwd + VJP + JVP (config 2)", n=n, kernels=kernels, cpu=cpu, dtype="f64")
+        return dict(name="energy fwd + VJP + JVP (config 2)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64")
     if config == "3":
         n = 1 << 22
         g = np.random.default_rng(3)
@@ -107,15 +112,15 @@ def workload(config: str, device):
         kf, kv = hawk.load(unit, "twobody"), hawk.load(unit, "twobody_vjp")
         R0, V0, BR, BV = (_dev(a, device) for a in (r0, v0, bar_r, bar_v))
         R, VV, BR0, BV0 = (torch.zeros((3, n), dtype=torch.float64, device=device) for _ in range(4))
-        kernels = [("twobody", kf.prepare(r0=R0, v0=V0, mu=1.0, r=R, v=VV), 96, 42 * 32),
-                   ("twobody_vjp", kv.prepare(r0=R0, v0=V0, mu=1.0, bar_r=BR, bar_v=BV, bar_r0=BR0, bar_v0=BV0),
-                    144, 3 * 42 * 32)]
+        kernels = [kf.prepare(r0=R0, v0=V0, mu=1.0, r=R, v=VV),
+                   kv.prepare(r0=R0, v0=V0, mu=1.0, bar_r=BR, bar_v=BV, bar_r0=BR0, bar_v0=BV0)]
+        work = {"twobody": (96, 42 * 32), "twobody_vjp": (144, 3 * 42 * 32)}
 
         def cpu(threads):
             import oracle_lib as O
             O.twobody(r0, v0, 1.0, threads=threads)
             O.twobody_vjp(r0, v0, 1.0, bar_r, bar_v, threads=threads)
-        return dict(name="two-body leapfrog fwd + VJP (config 3)", n=n, kernels=kernels, cpu=cpu,
+        return dict(name="two-body leapfrog fwd + VJP (config 3)", n=n, kernels=kernels, work=work, cpu=cpu,
                     dtype="f64", bound="fp64")
     if config == "4a":
         n = 1 << 20
@@ -130,14 +135,14 @@ def workload(config: str, device):
         X = torch.zeros((6, n), dtype=torch.float64, device=device)
         BA = torch.zeros((6, 6, n), dtype=torch.float64, device=device)
         BB = torch.zeros((6, n), dtype=torch.float64, device=device)
-        kernels = [("spd_solve", kf.prepare(A=Ad, b=bd, x=X), 384, 230),
-                   ("spd_solve_vjp", kv.prepare(A=Ad, b=bd, bar_x=BX, bar_A=BA, bar_b=BB), 720, 410)]
+        kernels = [kf.prepare(A=Ad, b=bd, x=X), kv.prepare(A=Ad, b=bd, bar_x=BX, bar_A=BA, bar_b=BB)]
+        work = {"spd_solve": (384, 230), "spd_solve_vjp": (720, 410)}
 
         def cpu(threads):
             import oracle_lib as O
             O.spd_solve(A, b, threads=threads)
             O.spd_solve_vjp(A, b, bar_x, threads=threads)
-        return dict(name="6x6 SPD solve fwd + VJP (config 4a)", n=n, kernels=kernels, cpu=cpu, dtype="f64")
+        return dict(name="6x6 SPD solve fwd + VJP (config 4a)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64")
     if config == "5":
         n = 1 << 26
         g = np.random.default_rng(5)
@@ -150,16 +155,86 @@ def workload(config: str, device):
         Y = torch.zeros(n, dtype=torch.float64, device=device)
         TOT = torch.zeros(1, dtype=torch.float64, device=device)
         BINS = torch.zeros(cells, dtype=torch.float64, device=device)
-        kernels = [("chain", k.prepare(x=X, key=KEY, y=Y, total=TOT, bins=BINS), 20, 14)]
+        kernels = [k.prepare(x=X, key=KEY, y=Y, total=TOT, bins=BINS)]
+        # per stage: the chain reads x, writes y; the sum reads y; the scatter reads key and y and
+        # reads + writes every bin once
+        work = {"chain": (16, 14), "ordered_sum": (8, 1), "ordered_scatter": (12 + 16 * cells / n, 1)}
 
         def cpu(threads):
             import oracle_lib as O
             y = O.chain(x, threads=threads)
             O.ordered_sum(y, threads=threads)
             O.ordered_scatter(key, y, np.zeros(cells), threads=threads)
-        return dict(name="chain + ordered sum + ordered scatter (config 5)", n=n, kernels=kernels, cpu=cpu,
+        return dict(name="chain + ordered sum + ordered scatter (config 5)", n=n, kernels=kernels, work=work, cpu=cpu,
                     dtype="f64")
     raise SystemExit(f"unknown --config {config!r}")
+
+
+#: The kernels a team stage launches, as rocprofv3 names them (the per-sample
+#: stage is one kernel named after the hawk kernel).
+STAGE_KERNELS = {"ordered_sum": ("hawk_sum_lanes", "hawk_sum_fold"),
+                 "ordered_scatter": ("hawk_scatter_status", "hawk_scatter_walk", "hawk_scatter_cells")}
+COPY_PROBE_BYTES = 1 << 30
+
+
+def _kernel_base(name: str) -> str:
+    name = name.replace("(anonymous namespace)::", "")
+    return name.split("(")[0].strip()
+
+
+def _pmc_pass(counter: str, config: str) -> dict:
+    """One ``rocprofv3 --pmc <counter>`` pass over a short run of this bench
+    (plus the 1 GiB copy probe) in a child process: ``{kernel: [KiB per dispatch]}``."""
+    import csv
+    import shutil
+    import signal
+    import subprocess
+
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        raise RuntimeError("rocprofv3 is not on PATH")
+    out = Path(tempfile.mkdtemp(prefix="hawk_pmc_"))
+    cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(out), "-o", "run", "--",
+           sys.executable, str(ROOT / "bench.py"), "--config", config, "--steps", "2", "--warmup", "1",
+           "--no-cpu", "--no-traffic", "--copy-probe"]
+    proc = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, text=True,
+                            start_new_session=True)
+    try:
+        _, err = proc.communicate(timeout=180)
+    except subprocess.TimeoutExpired:
+        os.killpg(proc.pid, signal.SIGKILL)
+        proc.communicate()
+        raise RuntimeError(f"rocprofv3 --pmc {counter} did not finish in 180 s")
+    table = out / "run_counter_collection.csv"
+    if not table.exists():       # the profiler can end badly after a complete run; only a missing table counts
+        raise RuntimeError(f"rocprofv3 --pmc {counter} wrote no counters (exit {proc.returncode}): {err[-300:]}")
+    seen: dict = {}
+    with table.open() as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] == counter:
+                seen.setdefault(_kernel_base(row["Kernel_Name"]), []).append(float(row["Counter_Value"]))
+    return seen
+
+
+def measure_traffic(config: str, kernels: list) -> dict:
+    """HBM bytes per launch of the stage whose kernels are ``kernels``: FETCH_SIZE
+    and WRITE_SIZE (KiB per dispatch, one pass each), each scaled by what the same
+    counter reads for a plain copy of 1 GiB."""
+    total = 0.0
+    factors = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        log(f"traffic: rocprofv3 --pmc {counter} pass over --config {config}")
+        seen = _pmc_pass(counter, config)
+        copies = [v for k, vs in seen.items() if "copyBuffer" in k for v in vs]
+        if not copies or max(copies) <= 0:
+            raise RuntimeError(f"{counter}: the copy probe was not seen")
+        factor = COPY_PROBE_BYTES / (max(copies) * 1024.0)
+        factors[counter] = round(factor, 4)
+        for k in kernels:
+            if k not in seen:
+                raise RuntimeError(f"{counter}: kernel {k} was not seen")
+            total += statistics.median(seen[k]) * 1024.0 * factor
+    return {"bytes": total, "factors": factors}
 
 
 def main() -> int:
@@ -169,6 +244,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="2")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc passes that measure the dominant stage's HBM traffic")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="after the timed steps, run one plain 1 GiB device copy (untimed): the "
+                         "known-size kernel that scales HBM counters read by rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build's hot path runs on a single MI355X "
@@ -179,52 +259,69 @@ def main() -> int:
     log(f"config {args.config}: building and uploading inputs")
     w = workload(args.config, device)
     n = w["n"]
+    stages = [st for prep in w["kernels"] for st in prep.stages()]
     for _ in range(args.warmup):
-        for _name, fn, _b, _f in w["kernels"]:
-            fn()
+        for _label, launch in stages:
+            launch()
     torch.cuda.synchronize()
     log(f"warmup done ({args.warmup} steps); timing {args.steps} steps")
+    # every launch is on the stream the launchers were prepared on (torch's current stream)
     stream = torch.cuda.current_stream()
-    events = {name: [] for name, *_ in w["kernels"]}
+    events = {label: [] for label, _ in stages}
     t0 = time.perf_counter()
     torch.cuda.synchronize()
     start_all = torch.cuda.Event(enable_timing=True)
     end_all = torch.cuda.Event(enable_timing=True)
     start_all.record(stream)
     for _ in range(args.steps):
-        for name, fn, _b, _f in w["kernels"]:
+        for label, launch in stages:
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record(stream)
-            fn()
+            launch()
             b.record(stream)
-            events[name].append((a, b))
+            events[label].append((a, b))
     end_all.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    if args.copy_probe:
+        src = torch.ones(COPY_PROBE_BYTES // 8, dtype=torch.float64, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy probe: 1 GiB read + 1 GiB written by one copy kernel")
+        del src, dst
     ms_step = start_all.elapsed_time(end_all) / args.steps
-    per_kernel = {}
-    for name, b_per, f_per in ((k[0], k[2], k[3]) for k in w["kernels"]):
-        ms = [a.elapsed_time(b) for a, b in events[name]]
-        med = statistics.median(ms)
-        per_kernel[name] = {"ms": round(med, 5), "samples_per_s": n / (med * 1e-3),
+    per_stage = {}
+    for label in events:
+        b_per, f_per = w["work"][label]
+        med = statistics.median(a.elapsed_time(b) for a, b in events[label])
+        per_stage[label] = {"ms": round(med, 5), "samples_per_s": n / (med * 1e-3),
                             "bytes_per_sample": b_per, "flops_per_sample": f_per,
                             "achieved_GBs": b_per * n / (med * 1e-3) / 1e9,
                             "hbm_frac": b_per * n / (med * 1e-3) / 1e9 / HBM_PEAK_GBS}
-    dominant = max(per_kernel, key=lambda k: per_kernel[k]["ms"])
-    d = per_kernel[dominant]
+    dominant = max(per_stage, key=lambda k: per_stage[k]["ms"])
+    d = per_stage[dominant]
+    traffic = None
+    if not args.no_traffic:
+        try:
+            t = measure_traffic(args.config, STAGE_KERNELS.get(dominant, (dominant,)))
+            traffic = round(t["bytes"])
+            log(f"traffic of {dominant}: {traffic / 1e6:.1f} MB per launch "
+                f"(algorithmic {d['bytes_per_sample'] * n / 1e6:.1f} MB; counter factors {t['factors']})")
+        except Exception as exc:        # counters are evidence, not the measurement: report null
+            log(f"traffic not measured: {exc}")
     if w.get("bound") == "fp64":
         achieved = d["flops_per_sample"] * n / (d["ms"] * 1e-3) / 1e12
         roofline = {"bound": "fp64-valu", "kernel": dominant, "achieved": round(achieved, 3),
                     "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP64_PEAK_TFLOPS, 4),
-                    "traffic": None}
+                    "traffic": traffic}
     else:
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(d["achieved_GBs"], 1),
-                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(d["hbm_frac"], 4), "traffic": None}
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(d["hbm_frac"], 4), "traffic": traffic}
     cpu_baseline = None
     if not args.no_cpu:
-        threads = os.cpu_count() or 1
-        threads = min(threads, 16)
+        threads = min(os.cpu_count() or 1, 16)
         log(f"CPU baseline: oracle (native profile) on {threads} threads")
         import oracle_lib as O
         O.build("native")
@@ -243,8 +340,8 @@ def main() -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": w["dtype"],
         "data": "synthetic (seeded numpy, resident in HBM before timing)",
         "config": {"workload": w["name"], "N": n,
-                   "kernels": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                               for k, v in per_kernel.items()}},
+                   "stages": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                              for k, v in per_stage.items()}},
         "roofline": roofline, "cpu_baseline": cpu_baseline, "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)

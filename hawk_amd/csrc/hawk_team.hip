@@ -401,8 +401,8 @@ int hk_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch, v
 }
 
 int hk_scatter_chunks(int64_t n, int64_t cells) {
-    if (n <= 0 || cells <= 0) return 1;
-    const int64_t fit = n / cells;
+    if (n <= 0) return 1;
+    const int64_t fit = n / (cells < 1 ? 1 : cells);
     return static_cast<int>(fit < 1 ? 1 : (fit > kScatterChunks ? kScatterChunks : fit));
 }
 

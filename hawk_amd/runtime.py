@@ -299,12 +299,24 @@ class Prepared:
                 self.statuses.append((t, status, cells))
 
     def __call__(self) -> None:
+        for _label, launch in self.stages():
+            launch()
+
+    def stages(self) -> list:
+        """``[(label, launch)]`` in run order: the per-sample stage (labelled
+        with the kernel's name) and each team stage (``"ordered_sum"``,
+        ``"ordered_scatter"``); calling every ``launch`` in order is one run."""
         k = self.kernel
+        out = []
         if k.entry is not None:
-            k.entry.run(self.block, 0, self.n, self.n, threads=k.launch_shape["block"],
-                        per_thread=k.launch_shape["per_thread"], stream=self.stream)
+            def stage():
+                k.entry.run(self.block, 0, self.n, self.n, threads=k.launch_shape["block"],
+                            per_thread=k.launch_shape["per_thread"], stream=self.stream)
+            out.append((k.name, stage))
         for fn, args in self.steps:
-            fn(*args, self.stream)
+            label = "ordered_sum" if fn is _core.ordered_sum else "ordered_scatter"
+            out.append((label, lambda fn=fn, args=args: fn(*args, self.stream)))
+        return out
 
     def check(self) -> None:
         """Refuse, by name, a run whose ordered scatter met a bad key (synchronises)."""

@@ -143,8 +143,7 @@ HKO_EXPORT double hko_ordered_sum(const double* u, int64_t n) {
  * another key outside [0, cells) sets status[1+b]; then each cell adds its
  * parts in chunk order from 0 and adds that onto target[cell]. */
 HKO_EXPORT int hko_scatter_chunks(int64_t n, int64_t cells) {
-    if (cells <= 0) return 1;
-    const int64_t fit = n / cells;
+    const int64_t fit = n / (cells < 1 ? 1 : cells);
     return (int)(fit < 1 ? 1 : (fit > 256 ? 256 : fit));
 }
 

@@ -3,7 +3,9 @@ and the seeded synthetic inputs of the five configurations."""
 
 from __future__ import annotations
 
+import json
 import sys
+from functools import lru_cache
 from pathlib import Path
 
 import numpy as np
@@ -53,6 +55,18 @@ def unit32(tmp_path_factory):
     directory = tmp_path_factory.mktemp("unit32")
     hawk.build(list(E.FLOAT32.values()), directory, mode="float32")
     return directory
+
+
+@lru_cache(maxsize=None)
+def _golden() -> dict:
+    return json.loads((Path(__file__).resolve().parent / "golden" / "known_answers.json").read_text())
+
+
+def golden(name: str) -> dict:
+    """One entry of tests/golden/known_answers.json: known answers and case
+    lists transcribed from the reference's README and tests (each entry cites
+    its source file:line)."""
+    return _golden()[name]
 
 
 def rng(seed: int):

@@ -10,6 +10,7 @@ from pathlib import Path
 
 import pytest
 
+from conftest import golden
 from hawk_amd import _contracts, _core
 
 HEADER = Path(__file__).resolve().parent.parent / "include" / "hawk_core.h"
@@ -96,10 +97,9 @@ def test_team_stage_arguments_are_checked_before_any_launch():
 
 
 def test_scatter_chunk_rule():
-    """clamp(n // cells, 1, 256) (reference tests/test_scatter_ordered.py:119-121)."""
-    cases = ((20000, 7), (50, 200), (1000, 1000), (10**6, 10**4), (10**6, 1), (10, 0))
-    got = [_core.scatter_chunks(n, t) for n, t in cases]
-    assert got[:5] == [256, 1, 1, 100, 256]
+    """clamp(n // max(cells, 1), 1, 256), the reference's own vectors."""
+    ga = golden("scatter_chunks")
+    assert [_core.scatter_chunks(n, t) for n, t in ga["cases"]] == ga["chunks"]
 
 
 def test_launch_arguments_are_checked_before_hip():

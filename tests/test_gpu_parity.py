@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from conftest import rng, ulp_diff, within_contract
+from conftest import golden, rng, ulp_diff, within_contract
 
 pytestmark = pytest.mark.gpu
 
@@ -90,15 +90,16 @@ def test_empty_run_touches_nothing(unit, gpu):
 # -- config 2 -------------------------------------------------------------------
 
 def test_energy_readme_vectors(unit, gpu):
-    """The reference's own golden vectors (README.md:82-103)."""
+    """The reference's own golden vectors."""
     import hawk_amd as hawk
-    v = np.array([[1.0, 2.0, 3.0, 4.0], [0.0, 1.0, 0.0, 1.0], [0.0, 0.0, 1.0, 1.0]])
+    ga = golden("energy_readme")
+    v = np.array(ga["v"])
     e = dev(np.zeros(4), gpu)
     hawk.run(_load(unit, "energy"), v=dev(v, gpu), out=e)
-    assert host(e).tolist() == [0.5, 2.5, 5.0, 9.0]
+    assert host(e).tolist() == ga["energy"]
     bar_v = dev(np.zeros((3, 4)), gpu)
-    hawk.run(_load(unit, "energy_vjp"), v=dev(v, gpu), bar_out=dev(np.ones(4), gpu), bar_v=bar_v)
-    assert host(bar_v).tolist() == v.tolist()
+    hawk.run(_load(unit, "energy_vjp"), v=dev(v, gpu), bar_out=dev(np.array(ga["bar_out"]), gpu), bar_v=bar_v)
+    assert host(bar_v).tolist() == ga["bar_v"]
 
 
 @pytest.mark.parametrize("n", [7, 4097, 300_001])
@@ -183,7 +184,7 @@ def test_spd_solve_and_vjp_are_the_oracle(unit, gpu, n):
 
 # -- config 5 -------------------------------------------------------------------
 
-@pytest.mark.parametrize("n", [1, 1000, 65536, 3 * 65536 + 777, 200_003])
+@pytest.mark.parametrize("n", golden("ordered_sum_sizes")["sizes"])
 def test_ordered_sum_is_the_numpy_tree_bitwise_and_replays(unit, gpu, n):
     import hawk_amd as hawk
     g = rng(n)
@@ -223,6 +224,36 @@ def test_ordered_scatter_is_the_serial_walk_bitwise(unit, gpu, cells, n, heavy):
     assert outs[0].tobytes() == outs[1].tobytes()
     assert outs[0].tobytes() == want.tobytes()
     assert k.scatter_chunks == O.scatter_chunks(n, cells)
+
+
+@pytest.mark.parametrize("n, cells, heavy", golden("ordered_scatter_cases")["cases"])
+def test_ordered_scatter_reference_cases(unit, gpu, n, cells, heavy):
+    """The reference's scatter cases: add.at within 1e-12, an empty cell stays
+    zero, replays are bitwise, a second run adds onto what the plane held —
+    and every result is the oracle's bits."""
+    import hawk_amd as hawk
+    ga = golden("ordered_scatter_cases")
+    g = rng(n)
+    key = g.integers(0, cells, n).astype(np.int32)
+    if heavy:
+        key[g.random(n) < 0.9] = cells // 2
+    empty = ga["empty_cell"]
+    if cells == empty["cells"]:
+        key[key == empty["moved_from"]] = empty["moved_to"]
+    x = g.normal(size=n) * np.exp(g.normal(size=n))
+    k = _load(unit, "ordered_add")
+    seen = []
+    for base in (np.zeros(cells), np.zeros(cells), np.linspace(1.0, 2.0, cells)):
+        acc = dev(base, gpu)
+        hawk.run(k, key=dev(key, gpu), x=dev(x, gpu), acc=acc)
+        seen.append(host(acc))
+        assert seen[-1].tobytes() == O.ordered_scatter(key, x, base)[0].tobytes()
+    assert seen[0].tobytes() == seen[1].tobytes()
+    want = np.zeros(cells)
+    np.add.at(want, key, x)
+    np.testing.assert_allclose(seen[0], want, rtol=ga["rtol"], atol=ga["rtol"] * np.abs(want).max())
+    if cells == empty["cells"]:
+        assert seen[0][empty["moved_from"]] == 0.0
 
 
 def test_ordered_scatter_reports_a_bad_key(unit, gpu):

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
+from conftest import golden
 
 
 def tree_sum(x: np.ndarray) -> float:
@@ -31,9 +32,10 @@ def tree_sum(x: np.ndarray) -> float:
 
 
 def test_energy_readme_golden_vectors():
-    v = np.array([[1.0, 2.0, 3.0, 4.0], [0.0, 1.0, 0.0, 1.0], [0.0, 0.0, 1.0, 1.0]])
-    assert O.energy(v).tolist() == [0.5, 2.5, 5.0, 9.0]
-    assert O.energy_vjp(v, np.ones(4)).tolist() == v.tolist()
+    ga = golden("energy_readme")
+    v = np.array(ga["v"])
+    assert O.energy(v).tolist() == ga["energy"]
+    assert O.energy_vjp(v, np.array(ga["bar_out"])).tolist() == ga["bar_v"]
 
 
 def test_energy_closed_forms():
@@ -50,7 +52,7 @@ def test_scale_is_one_mul_and_one_add():
     assert O.scale(x, 2.0, 1.0).tobytes() == ((2.0 * x) + 1.0).tobytes()
 
 
-@pytest.mark.parametrize("n", [1, 1000, 65536, 3 * 65536 + 777, 200003, 1 << 20])
+@pytest.mark.parametrize("n", golden("ordered_sum_sizes")["sizes"])
 def test_ordered_sum_is_the_numpy_tree(n):
     g = np.random.default_rng(n)
     x = g.normal(size=n) * np.exp(g.normal(size=n))
@@ -66,17 +68,20 @@ def test_ordered_sum_small_cases():
 
 
 def test_scatter_chunk_rule():
-    cases = ((20000, 7), (50, 200), (1000, 1000), (10**6, 10**4), (10**6, 1), (10, 0))
-    assert [O.scatter_chunks(n, t) for n, t in cases] == [256, 1, 1, 100, 256, 1]
+    ga = golden("scatter_chunks")
+    assert [O.scatter_chunks(n, t) for n, t in ga["cases"]] == ga["chunks"]
 
 
-@pytest.mark.parametrize("n, cells, heavy", [(20000, 7, True), (3000, 1, False), (5000, 40, False),
-                                             (50, 200, False), (1000, 1000, False)])
+@pytest.mark.parametrize("n, cells, heavy", golden("ordered_scatter_cases")["cases"])
 def test_ordered_scatter_equals_add_at_and_replays(n, cells, heavy):
+    ga = golden("ordered_scatter_cases")
     g = np.random.default_rng(n)
     key = g.integers(0, cells, n).astype(np.int32)
     if heavy:
         key[g.random(n) < 0.9] = cells // 2
+    empty = ga["empty_cell"]
+    if cells == empty["cells"]:
+        key[key == empty["moved_from"]] = empty["moved_to"]
     x = g.normal(size=n) * np.exp(g.normal(size=n))
     want = np.zeros(cells)
     np.add.at(want, key, x)
@@ -84,7 +89,12 @@ def test_ordered_scatter_equals_add_at_and_replays(n, cells, heavy):
     b, _ = O.ordered_scatter(key, x, np.zeros(cells), threads=4)
     assert a.tobytes() == b.tobytes()
     assert not sa[1:].any() and sa[0] == cells
-    np.testing.assert_allclose(a, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+    np.testing.assert_allclose(a, want, rtol=ga["rtol"], atol=ga["rtol"] * np.abs(want).max())
+    if cells == empty["cells"]:
+        assert a[empty["moved_from"]] == 0.0
+    base = np.linspace(1.0, 2.0, cells)             # the sum adds onto what the plane held
+    more, _ = O.ordered_scatter(key, x, base)
+    np.testing.assert_allclose(more - base, a, rtol=1e-9, atol=1e-9 * np.abs(a).max())
 
 
 def test_ordered_scatter_is_the_serial_chunk_walk():
