@@ -92,264 +92,347 @@ __global__ __launch_bounds__(256) void hawk_sum_fold(const double* __restrict__ 
 
 // ---------------------------------------------------------------------------
 // Keyed ordered scatter.
+//
+// parts[b][k] is the in-lane-order sum (from +0.0) of chunk b's values with
+// key k; cell k then adds parts[0][k], parts[1][k], ... in chunk order from
+// +0.0 and adds that onto target[k].  One 1024-thread workgroup walks one
+// chunk in tiles of 4096 lanes: each tile is sorted stably by key in LDS (LSD
+// radix, 8-bit digits), so every key's lanes form one run in lane order, and
+// the run's owner thread adds them one by one onto the key's accumulator —
+// the additions the serial walk makes, in its order.  Accumulators of keys
+// below kAccKeys live in LDS, the others in parts[b] (L2-resident: only this
+// workgroup touches that row).  A per-chunk bitmap of touched keys replaces a
+// zero fill of parts: an untouched (chunk, key) is skipped by the cell pass,
+// which is exact because a sum that starts at +0.0 is never -0.0, so adding
+// the +0.0 the serial walk would add changes nothing.
 // ---------------------------------------------------------------------------
 constexpr int kScatterChunks = 256;    // reference hawk/_lane_bind.py:108
-constexpr int kWalkThreads = 512;
+constexpr int kWalkThreads = 1024;
 constexpr int kWalkWaves = kWalkThreads / 64;
-constexpr int kWalkItems = 8;                      // keys per thread per tile (striped)
-constexpr int kTile = kWalkThreads * kWalkItems;   // 4096 raw lanes per tile
-constexpr int kStage = 2048;                       // staged entries per batch
-constexpr int kSortItems = kStage / kWalkThreads;  // 4 per thread in the sort
-constexpr int kIdxBits = 11;                       // 2^11 == kStage
-constexpr int kBinCap = 8192;                      // f64 bins a workgroup holds in LDS (64 KiB)
-constexpr int kDigitBits = 4;
+constexpr int kWalkItems = 4;                      // lanes per thread per tile
+constexpr int kTile = kWalkThreads * kWalkItems;   // 4096 lanes per tile
+constexpr int kPosBits = 12;                       // 2^12 == kTile
+constexpr unsigned kPosMask = (1u << kPosBits) - 1u;
+constexpr unsigned kInvalid = 0x80000000u;         // a skipped (-1), bad or padding lane
+constexpr int kMaxKeyBits = 31 - kPosBits;         // key field: bits 12..30
+constexpr int kDigitBits = 8;
 constexpr int kDigits = 1 << kDigitBits;
+constexpr int kAccKeys = 4096;                     // keys whose accumulators live in LDS
+constexpr long long kSeenCells = 65536;            // a touched bitmap up to this many cells
+constexpr int kSeenWords = static_cast<int>(kSeenCells / 32);
+constexpr int kFoldUnroll = 8;
+
+static_assert(kTile == 1 << kPosBits, "tile positions fill the position field");
 
 __device__ __forceinline__ unsigned wave_inclusive_scan(unsigned v) {
     const int lane = threadIdx.x & 63;
     unsigned x = v;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-        unsigned y = __shfl_up(x, d, 64);
+        const unsigned y = __shfl_up(x, d, 64);
         if (lane >= d) x += y;
     }
     return x;
 }
 
-// Exclusive scan of one value per thread over the block (all threads call it).
-__device__ __forceinline__ unsigned block_exclusive_scan(unsigned v, unsigned* scratch, unsigned* total) {
-    const unsigned incl = wave_inclusive_scan(v);
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 63) scratch[wave] = incl;
-    __syncthreads();
-    unsigned before = 0, all = 0;
-#pragma unroll
-    for (int w = 0; w < kWalkWaves; ++w) {
-        const unsigned s = scratch[w];
-        if (w < wave) before += s;
-        all += s;
-    }
-    __syncthreads();
-    *total = all;
-    return incl - v + before;
-}
-
 struct WalkShared {
-    double bins[kBinCap];                          // 64 KiB: this partition's partial sums
-    unsigned comp[2][kStage];                      // 16 KiB: (local key << 11) | staged index
-    double vals[kStage];                           // 16 KiB: staged values, arrival order
-    double sorted_vals[kStage];                    // 16 KiB: values in sorted order
-    unsigned counts[kDigits * kWalkWaves * kSortItems];   // 2 KiB: per (digit, wave, slot)
-    unsigned scan[kWalkWaves];
-    unsigned slab[kWalkItems][kWalkWaves];         // per (slab, wave) counts of a tile
-    int longs[kStage / 64 + 1];                    // heads of runs of 64 or more
-    int nlong;
+    double vals[kTile];                               // 32 KiB: the tile's values, lane order
+    unsigned ent[2][kTile];                           // 32 KiB: (key << 12) | position | invalid
+    unsigned hist[kWalkWaves][kDigits];               // 16 KiB: per-wave digit counts, then offsets
+    union {
+        unsigned long long peer[kWalkWaves][kDigits]; // 32 KiB: per-wave lane masks of one digit (sort)
+        double sv[kTile];                             //         the tile's values in sorted order (fold)
+    };
+    double acc[kAccKeys];                             // 32 KiB: accumulators of keys < kAccKeys
+    unsigned seen[kSeenWords];                        //  8 KiB: keys this chunk has touched
+    unsigned long long starts[kTile / 64];            // run heads of the sorted tile
+    unsigned wsum[kWalkWaves];
 };
 
-static_assert(kDigits * kWalkWaves * kSortItems == kWalkThreads, "one radix counter per thread");
-
-// Stable LSD radix sort of the kStage composite keys over bits [lo, hi), 4 bits
-// a pass, ping-ponging comp[0] <-> comp[1]; returns the buffer holding the
-// result.  Element e = wave*256 + slot*64 + lane (the input order); within a
-// (wave, slot) group the lanes with one digit are ranked by ballots, and the
-// exclusive scan over (digit, wave, slot) in that order places every group's
-// members after all earlier ones: each pass is stable.
-__device__ int radix_sort(WalkShared& sh, int lo, int hi) {
+// Stable LSD radix sort of the tile's entries by the key field (bits
+// 12..12+key_bits), 8 bits a pass, ping-ponging ent[0] <-> ent[1]; returns the
+// buffer holding the result.  Wave w ranks its 256 entries w*256 + j*64 + lane
+// window by window (j = 0..3, in order): the lanes of a window holding digit d
+// find each other through one LDS OR into peer[w][d]; the lowest of them adds
+// the group's size onto hist[w][d] after all of them read it.  The exclusive
+// scan of hist in (digit, wave) order then places every wave's group after
+// the earlier waves' groups of the same digit, so each pass keeps input order
+// within a digit.
+__device__ int walk_sort(WalkShared& sh, int key_bits) {
     const int t = threadIdx.x;
     const int wave = t >> 6;
     const int lane = t & 63;
-    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const unsigned long long me = 1ull << lane;
     int src = 0;
-    for (int shift = lo; shift < hi; shift += kDigitBits) {
-        const unsigned* in = sh.comp[src];
-        unsigned* out = sh.comp[src ^ 1];
-        unsigned item[kSortItems], digit[kSortItems], rank[kSortItems];
+    for (int lo = 0; lo < key_bits; lo += kDigitBits) {
+        const int width = key_bits - lo < kDigitBits ? key_bits - lo : kDigitBits;
+        const unsigned dmask = (1u << width) - 1u;
+        const int shift = kPosBits + lo;
+        const unsigned* in = sh.ent[src];
+        unsigned* out = sh.ent[src ^ 1];
+        for (int d = lane; d < kDigits; d += 64) sh.hist[wave][d] = 0u;
+        __builtin_amdgcn_wave_barrier();
+        unsigned item[kWalkItems], digit[kWalkItems], rank[kWalkItems];
 #pragma unroll
-        for (int j = 0; j < kSortItems; ++j) {
-            item[j] = in[wave * (kSortItems * 64) + j * 64 + lane];
-            digit[j] = (item[j] >> shift) & (kDigits - 1);
-            unsigned long long bits[kDigitBits];
-#pragma unroll
-            for (int b = 0; b < kDigitBits; ++b) bits[b] = __ballot((digit[j] >> b) & 1u);
-            unsigned long long peers = ~0ull;          // lanes whose digit equals mine
-#pragma unroll
-            for (int b = 0; b < kDigitBits; ++b) peers &= ((digit[j] >> b) & 1u) ? bits[b] : ~bits[b];
-            rank[j] = static_cast<unsigned>(__popcll(peers & below));
-            // lane d < 16 counts the group's members with digit d
-            unsigned long long with_d = ~0ull;
-#pragma unroll
-            for (int b = 0; b < kDigitBits; ++b) with_d &= ((lane >> b) & 1) ? bits[b] : ~bits[b];
-            if (lane < kDigits)
-                sh.counts[(lane * kWalkWaves + wave) * kSortItems + j] = static_cast<unsigned>(__popcll(with_d));
+        for (int j = 0; j < kWalkItems; ++j) {
+            item[j] = in[wave * (kWalkItems * 64) + j * 64 + lane];
+            digit[j] = (item[j] >> shift) & dmask;
+            atomicOr(&sh.peer[wave][digit[j]], me);
+            __builtin_amdgcn_wave_barrier();
+            const unsigned long long peers = sh.peer[wave][digit[j]];
+            const unsigned below = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(peers >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(peers), 0u));
+            const unsigned old = sh.hist[wave][digit[j]];
+            rank[j] = old + below;
+            __builtin_amdgcn_wave_barrier();
+            if (below == 0u) {
+                sh.hist[wave][digit[j]] = old + static_cast<unsigned>(__popcll(peers));
+                sh.peer[wave][digit[j]] = 0ull;
+            }
+            __builtin_amdgcn_wave_barrier();
         }
         __syncthreads();
-        unsigned total;
-        const unsigned off = block_exclusive_scan(sh.counts[t], sh.scan, &total);
-        sh.counts[t] = off;                          // every thread read its count before the scan's barrier
+        // Exclusive scan over f = digit*16 + wave: thread t owns f = 4t .. 4t+3.
+        const int d = t >> 2;
+        const int w0 = (t & 3) * 4;
+        const unsigned c0 = sh.hist[w0][d], c1 = sh.hist[w0 + 1][d];
+        const unsigned c2 = sh.hist[w0 + 2][d], c3 = sh.hist[w0 + 3][d];
+        const unsigned mine = c0 + c1 + c2 + c3;
+        const unsigned incl = wave_inclusive_scan(mine);
+        if (lane == 63) sh.wsum[wave] = incl;
+        __syncthreads();
+        unsigned before = 0u;
+        for (int w = 0; w < wave; ++w) before += sh.wsum[w];
+        const unsigned base = incl - mine + before;
+        sh.hist[w0][d] = base;
+        sh.hist[w0 + 1][d] = base + c0;
+        sh.hist[w0 + 2][d] = base + c0 + c1;
+        sh.hist[w0 + 3][d] = base + c0 + c1 + c2;
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < kSortItems; ++j)
-            out[sh.counts[(digit[j] * kWalkWaves + wave) * kSortItems + j] + rank[j]] = item[j];
+        for (int j = 0; j < kWalkItems; ++j) out[sh.hist[wave][digit[j]] + rank[j]] = item[j];
         __syncthreads();
         src ^= 1;
     }
     return src;
 }
 
-// Sort the `m` staged entries by local key (stable, so arrival order holds
-// within a key) and add each key's run, in order, onto its bin: a run shorter
-// than 64 by one lane, a longer one by a whole wave (64 values per LDS load,
-// folded in order through uniform readlanes).
-__device__ void flush_batch(WalkShared& sh, int m, int key_bits) {
-    const int t = threadIdx.x;
-    const int wave = t >> 6;
-    const int lane = t & 63;
-    for (int j = m + t; j < kStage; j += kWalkThreads) sh.comp[0][j] = 0xffffffffu;
-    if (t == 0) sh.nlong = 0;
-    __syncthreads();
-    const int buf = radix_sort(sh, kIdxBits, kIdxBits + key_bits);
-    unsigned* comp = sh.comp[buf];
-    for (int j = t; j < m; j += kWalkThreads) sh.sorted_vals[j] = sh.vals[comp[j] & (kStage - 1)];
-    __syncthreads();
-    for (int j = t; j < m; j += kWalkThreads) {
-        const unsigned key = comp[j] >> kIdxBits;
-        if (j > 0 && (comp[j - 1] >> kIdxBits) == key) continue;   // not the head of its run
-        if (j + 63 < m && (comp[j + 63] >> kIdxBits) == key) {     // sorted: a run of 64 or more
-            sh.longs[atomicAdd(&sh.nlong, 1)] = j;
-            continue;
-        }
-        double acc = sh.bins[key];
-        for (int jj = j; jj < m && (comp[jj] >> kIdxBits) == key; ++jj) acc = acc + sh.sorted_vals[jj];
-        sh.bins[key] = acc;
-    }
-    __syncthreads();
-    for (int r = wave; r < sh.nlong; r += kWalkWaves) {
-        const int j = sh.longs[r];
-        const unsigned key = comp[j] >> kIdxBits;
-        double acc = sh.bins[key];
-        for (int base = j; base < m; base += 64) {
-            const int e = base + lane;
-            const bool in = e < m && (comp[e] >> kIdxBits) == key;
-            const double x = in ? sh.sorted_vals[e] : 0.0;
-            const int cnt = __popcll(__ballot(in));     // a prefix of the lanes: the run is contiguous
-            const int xlo = __double2loint(x);
-            const int xhi = __double2hiint(x);
-            for (int k = 0; k < cnt; ++k)
-                acc = acc + __hiloint2double(__builtin_amdgcn_readlane(xhi, k), __builtin_amdgcn_readlane(xlo, k));
-            if (cnt < 64) break;
-        }
-        if (lane == 0) sh.bins[key] = acc;
-    }
-    __syncthreads();
-}
-
-// Load the striped tile at `tile`: element j*512 + t of the tile goes to
-// thread t's slot j, so every load instruction of a wave is one contiguous run.
-__device__ __forceinline__ void load_tile(const int* __restrict__ key, const double* __restrict__ v, long long tile,
+// Lane base + wave*256 + j*64 + lane goes to thread slot j: every load
+// instruction of a wave reads 64 consecutive lanes.  Lanes past `hi` read as
+// the skip key -1.
+__device__ __forceinline__ void walk_load(const int* __restrict__ key, const double* __restrict__ v, long long base,
                                           long long hi, int (&kk)[kWalkItems], double (&vv)[kWalkItems]) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int j = 0; j < kWalkItems; ++j) {
-        const long long i = tile + static_cast<long long>(j) * kWalkThreads + threadIdx.x;
+        const long long i = base + wave * (kWalkItems * 64) + j * 64 + lane;
         const bool in = i < hi;
         kk[j] = in ? __builtin_nontemporal_load(key + i) : -1;
         vv[j] = in ? __builtin_nontemporal_load(v + i) : 0.0;
     }
 }
 
-// One workgroup per (chunk b, key partition q): keys k with k % Q == q, local
-// key k / Q, live in LDS bins.  The workgroup walks its chunk's lanes in
-// order (the next tile's keys and values in flight while the current one is
-// staged), stages its partition's (key, value) pairs in lane order, and adds
-// every batch into the bins; the bins of every key of the partition (zeros
-// included) go to partsT[b*cells + k] at the end, so no zeroing stage is
-// needed.  The Q workgroups of one chunk take consecutive dispatch slots of
-// one XCD, so the chunk's keys are fetched from HBM once and re-read from L2.
+// The first run head after position i of the sorted tile (kTile if none).
+__device__ __forceinline__ int next_head(const WalkShared& sh, int i) {
+    int wi = i >> 6;
+    const int bit = i & 63;
+    unsigned long long m = bit == 63 ? 0ull : (sh.starts[wi] & (~0ull << (bit + 1)));
+    while (m == 0ull && ++wi < kTile / 64) m = sh.starts[wi];
+    return m ? (wi << 6) + __builtin_ctzll(m) : kTile;
+}
+
+// a + x[s] + x[s+1] + ... + x[e-1], one addition at a time in that order; the
+// next eight values are in flight while the current eight are added.
+__device__ __forceinline__ double fold_run(const double* x, int s, int e, double a) {
+    int m = s;
+    if (e - m >= 2 * kFoldUnroll) {
+        double cur[kFoldUnroll];
+#pragma unroll
+        for (int q = 0; q < kFoldUnroll; ++q) cur[q] = x[m + q];
+        m += kFoldUnroll;
+        for (; m + kFoldUnroll <= e; m += kFoldUnroll) {
+            double nxt[kFoldUnroll];
+#pragma unroll
+            for (int q = 0; q < kFoldUnroll; ++q) nxt[q] = x[m + q];
+#pragma unroll
+            for (int q = 0; q < kFoldUnroll; ++q) a = a + cur[q];
+#pragma unroll
+            for (int q = 0; q < kFoldUnroll; ++q) cur[q] = nxt[q];
+        }
+#pragma unroll
+        for (int q = 0; q < kFoldUnroll; ++q) a = a + cur[q];
+    }
+    for (; m < e; ++m) a = a + x[m];
+    return a;
+}
+
+// Accumulators outside LDS are read and written at agent scope, so a value
+// one thread stores in a tile is what another thread of the workgroup loads
+// after the tile's closing barrier.
+__device__ __forceinline__ double acc_load(const double* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void acc_store(double* p, double x) {
+    __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One workgroup per chunk b: lanes [b*span, min((b+1)*span, n)).  With
+// use_seen, keys are below kSeenCells, parts[b] is never zero-filled and the
+// touched bitmap goes to touched[b]; without it parts arrives zero-filled and
+// every accumulator is read.
 __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
-        const int* __restrict__ key, const double* __restrict__ v, long long n, long long cells,
-        int chunks, long long span, int parts, int key_bits, double* __restrict__ partsT,
+        const int* __restrict__ key, const double* __restrict__ v, long long n, long long cells, long long span,
+        int key_bits, int use_seen, double* __restrict__ parts, unsigned* __restrict__ touched,
         int* __restrict__ status) {
     __shared__ WalkShared sh;
     const int t = threadIdx.x;
     const int wave = t >> 6;
     const int lane = t & 63;
-    const long long total = static_cast<long long>(chunks) * parts;
-    long long w = blockIdx.x;
-    if (total % 8 == 0) w = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
-    const int b = static_cast<int>(w / parts);
-    const int q = static_cast<int>(w % parts);
+    const int b = blockIdx.x;
     const long long lo = static_cast<long long>(b) * span;
     const long long hi = lo + span < n ? lo + span : n;
-    const long long nb = (cells - q + parts - 1) / parts;   // keys q, q+Q, ... below cells
+    const int acc_n = cells < kAccKeys ? static_cast<int>(cells) : kAccKeys;
+    const int words = use_seen ? static_cast<int>((cells + 31) / 32) : 0;
+    const unsigned kmask = (1u << key_bits) - 1u;
+    const unsigned sentinel = kmask;          // the key field of an invalid lane
+    double* row = parts + static_cast<long long>(b) * cells;
 
-    for (long long k = t; k < nb; k += kWalkThreads) sh.bins[k] = 0.0;
-    int staged = 0;
+    for (int k = t; k < acc_n; k += kWalkThreads) sh.acc[k] = 0.0;
+    for (int i = t; i < words; i += kWalkThreads) sh.seen[i] = 0u;
     bool bad = false;
     int nk[kWalkItems];
     double nv[kWalkItems];
-    if (lo < hi) load_tile(key, v, lo, hi, nk, nv);
+    if (lo < hi) walk_load(key, v, lo, hi, nk, nv);
     __syncthreads();
-    for (long long tile = lo; tile < hi; tile += kTile) {
+    for (long long base = lo; base < hi; base += kTile) {
         int kk[kWalkItems];
         double vv[kWalkItems];
 #pragma unroll
         for (int j = 0; j < kWalkItems; ++j) { kk[j] = nk[j]; vv[j] = nv[j]; }
-        if (tile + kTile < hi) load_tile(key, v, tile + kTile, hi, nk, nv);
-        // Per slab j (512 consecutive lanes), this wave's members in lane order.
-        unsigned long long mask[kWalkItems];
+        if (base + kTile < hi) walk_load(key, v, base + kTile, hi, nk, nv);
 #pragma unroll
         for (int j = 0; j < kWalkItems; ++j) {
+            const unsigned p = static_cast<unsigned>(wave * (kWalkItems * 64) + j * 64 + lane);
             const bool valid = kk[j] >= 0 && kk[j] < cells;
             bad = bad || (kk[j] != -1 && !valid);
-            const bool mine = valid && (kk[j] % parts == q);
-            mask[j] = __ballot(mine);
-            if (lane == 0) sh.slab[j][wave] = static_cast<unsigned>(__popcll(mask[j]));
+            const unsigned field = valid ? static_cast<unsigned>(kk[j]) : sentinel;
+            sh.ent[0][p] = (field << kPosBits) | p | (valid ? 0u : kInvalid);
+            sh.vals[p] = vv[j];
+            // the previous tile's sorted values share LDS with the sort's peer
+            // masks, which must start at zero
+            (&sh.peer[0][0])[p] = 0ull;
         }
         __syncthreads();
-        // Offsets: all of slab j' < j first, then the waves before this one in slab j.
-        unsigned before[kWalkItems];
-        unsigned m = 0;
+        const unsigned* sorted = sh.ent[walk_sort(sh, key_bits)];
+        // The values in sorted order (an invalid lane's as +0.0) and the run
+        // heads, one ballot per 64 entries.
+        bool head[kWalkItems];
 #pragma unroll
         for (int j = 0; j < kWalkItems; ++j) {
-            unsigned inslab = 0, mine_before = 0;
+            const int i = j * kWalkThreads + t;
+            const unsigned e = sorted[i];
+            sh.sv[i] = (e & kInvalid) ? 0.0 : sh.vals[e & kPosMask];
+            const unsigned k = (e >> kPosBits) & kmask;
+            head[j] = i == 0 || k != ((sorted[i - (i > 0)] >> kPosBits) & kmask);
+            const unsigned long long m = __ballot(head[j]);
+            if (lane == 0) sh.starts[(j * kWalkThreads + wave * 64) >> 6] = m;
+        }
+        __syncthreads();
+        // Every run's owner: its accumulator first (the loads of all its runs
+        // in flight together), then its lanes in order, then the store.
+        int rs[kWalkItems], re[kWalkItems];
+        unsigned rk[kWalkItems];
+        bool load[kWalkItems];
 #pragma unroll
-            for (int x = 0; x < kWalkWaves; ++x) {
-                const unsigned c = sh.slab[j][x];
-                if (x < wave) mine_before += c;
-                inslab += c;
+        for (int j = 0; j < kWalkItems; ++j) {
+            rs[j] = j * kWalkThreads + t;
+            rk[j] = (sorted[rs[j]] >> kPosBits) & kmask;
+            re[j] = 0;
+            load[j] = false;
+            if (!head[j] || rk[j] >= cells) continue;
+            re[j] = next_head(sh, rs[j]);
+            const unsigned k = rk[j];
+            load[j] = k >= static_cast<unsigned>(acc_n) && (!use_seen || ((sh.seen[k >> 5] >> (k & 31)) & 1u));
+        }
+        double ra[kWalkItems];
+#pragma unroll
+        for (int j = 0; j < kWalkItems; ++j) {
+            const unsigned k = rk[j] < static_cast<unsigned>(acc_n) ? rk[j] : 0u;
+            ra[j] = load[j] ? acc_load(row + rk[j])
+                            : (re[j] != 0 && rk[j] < static_cast<unsigned>(acc_n) ? sh.acc[k] : 0.0);
+        }
+#pragma unroll 1
+        for (int j = 0; j < kWalkItems; ++j) {
+            if (re[j] == 0) continue;
+            const unsigned k = rk[j];
+            double a = ra[j];
+            bool any = true;
+            if (k == sentinel) {
+                // The one run that can hold invalid lanes: skip them.
+                any = false;
+                for (int m = rs[j]; m < re[j]; ++m) {
+                    if (sorted[m] & kInvalid) continue;
+                    a = a + sh.sv[m];
+                    any = true;
+                }
+            } else {
+                a = fold_run(sh.sv, rs[j], re[j], a);
             }
-            before[j] = m + mine_before;
-            m += inslab;
+            if (!any) continue;
+            if (k < static_cast<unsigned>(acc_n)) sh.acc[k] = a;
+            else acc_store(row + k, a);
+            if (use_seen) atomicOr(&sh.seen[k >> 5], 1u << (k & 31));
         }
-        if (staged + static_cast<int>(m) > kStage) {
-            flush_batch(sh, staged, key_bits);      // ends with a barrier
-            staged = 0;
-        }
-        const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-#pragma unroll
-        for (int j = 0; j < kWalkItems; ++j) {
-            if (!((mask[j] >> lane) & 1ull)) continue;
-            const unsigned idx = static_cast<unsigned>(staged) + before[j] +
-                                 static_cast<unsigned>(__popcll(mask[j] & below));
-            sh.comp[0][idx] = (static_cast<unsigned>(kk[j] / parts) << kIdxBits) | idx;
-            sh.vals[idx] = vv[j];
-        }
-        staged += static_cast<int>(m);
         __syncthreads();
     }
-    if (staged > 0) flush_batch(sh, staged, key_bits);
-    double* row = partsT + static_cast<long long>(b) * cells;
-    for (long long k = t; k < nb; k += kWalkThreads) row[k * parts + q] = sh.bins[k];
+    for (int k = t; k < acc_n; k += kWalkThreads)
+        if (!use_seen || ((sh.seen[k >> 5] >> (k & 31)) & 1u)) row[k] = sh.acc[k];
+    for (int i = t; i < words; i += kWalkThreads) touched[static_cast<long long>(b) * words + i] = sh.seen[i];
     if (bad) status[1 + b] = 1;
 }
 
+// More keys than the sort's key field holds: one thread per chunk walks its
+// lanes in order onto the zero-filled parts[b] (the reference's serial walk).
+__global__ __launch_bounds__(64) void hawk_scatter_serial(const int* __restrict__ key, const double* __restrict__ v,
+                                                          long long n, long long cells, long long span,
+                                                          double* __restrict__ parts, int* __restrict__ status) {
+    if (threadIdx.x != 0) return;
+    const int b = blockIdx.x;
+    const long long lo = static_cast<long long>(b) * span;
+    const long long hi = lo + span < n ? lo + span : n;
+    double* row = parts + static_cast<long long>(b) * cells;
+    bool bad = false;
+    for (long long i = lo; i < hi; ++i) {
+        const int k = key[i];
+        if (k == -1) continue;
+        if (k < 0 || k >= cells) { bad = true; continue; }
+        row[k] = row[k] + v[i];
+    }
+    if (bad) status[1 + b] = 1;
+}
+
+__global__ __launch_bounds__(256) void hawk_fill_zero(double* __restrict__ p, long long count) {
+    for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < count;
+         i += static_cast<long long>(gridDim.x) * 256)
+        p[i] = 0.0;
+}
+
 // Cell c adds its chunk partials in chunk order from +0.0, then onto the
-// target: target[c] += sum (reference hawk/emit/team.py:437-460).
-__global__ __launch_bounds__(256) void hawk_scatter_cells(const double* __restrict__ partsT, long long cells,
-                                                          int chunks, double* __restrict__ target) {
+// target: target[c] += sum (reference hawk/emit/team.py:437-460).  With a
+// touched bitmap, a (chunk, cell) the walk never touched holds no partial and
+// is skipped (its +0.0 would change nothing).
+__global__ __launch_bounds__(256) void hawk_scatter_cells(const double* __restrict__ parts,
+                                                          const unsigned* __restrict__ touched, long long cells,
+                                                          int chunks, int use_seen, double* __restrict__ target) {
     const long long c = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     if (c >= cells) return;
+    const long long words = (cells + 31) / 32;
     double s = 0.0;
-    for (int b = 0; b < chunks; ++b) s = s + partsT[static_cast<long long>(b) * cells + c];
+    for (int b = 0; b < chunks; ++b) {
+        if (use_seen && !((touched[b * words + (c >> 5)] >> (c & 31)) & 1u)) continue;
+        s = s + parts[static_cast<long long>(b) * cells + c];
+    }
     target[c] = target[c] + s;
 }
 
@@ -408,7 +491,11 @@ int hk_scatter_chunks(int64_t n, int64_t cells) {
 
 size_t hk_ordered_scatter_scratch_bytes(int64_t n, int64_t cells) {
     if (cells <= 0) return 0;
-    return sizeof(double) * static_cast<size_t>(hk_scatter_chunks(n, cells)) * static_cast<size_t>(cells);
+    const size_t chunks = static_cast<size_t>(hk_scatter_chunks(n, cells));
+    const size_t parts = sizeof(double) * chunks * static_cast<size_t>(cells);
+    const size_t words = static_cast<size_t>((cells + 31) / 32);
+    const size_t seen = cells <= kSeenCells ? sizeof(unsigned) * chunks * words : 0;
+    return ((parts + 255) & ~static_cast<size_t>(255)) + seen;
 }
 
 int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n, double* target, int64_t cells,
@@ -424,26 +511,38 @@ int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n, doubl
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int chunks = hk_scatter_chunks(n, cells);
     const long long span = (n + chunks - 1) / chunks;
-    const long long parts = (cells + kBinCap - 1) / kBinCap;
-    const long long nb = (cells + parts - 1) / parts;
-    const int key_bits = bits_for(nb - 1);
-    if (key_bits + kIdxBits > 31)
-        return hawk_internal::set_error(HK_EVALUE, "hk_ordered_scatter_f64: too many cells for one partition");
+    const int key_bits = bits_for(cells - 1);
+    const bool sorted_walk = key_bits <= kMaxKeyBits;
+    const int use_seen = sorted_walk && cells <= kSeenCells ? 1 : 0;
+    auto* parts = static_cast<double*>(scratch);
+    const size_t parts_bytes = sizeof(double) * static_cast<size_t>(chunks) * static_cast<size_t>(cells);
+    auto* touched = reinterpret_cast<unsigned*>(static_cast<unsigned char*>(scratch) +
+                                                ((parts_bytes + 255) & ~static_cast<size_t>(255)));
     hipLaunchKernelGGL(hawk_scatter_status, dim3(1), dim3(kScatterChunks + 64), 0, s, status,
                        static_cast<long long>(cells));
     int rc = launch_error("hawk_scatter_status launch");
     if (rc != HK_OK) return rc;
-    const long long blocks = static_cast<long long>(chunks) * parts;
-    if (blocks > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_ordered_scatter_f64: grid too large");
-    auto* partsT = static_cast<double*>(scratch);
-    hipLaunchKernelGGL(hawk_scatter_walk, dim3(static_cast<unsigned>(blocks)), dim3(kWalkThreads), 0, s, key, v,
-                       static_cast<long long>(n), static_cast<long long>(cells), chunks, span,
-                       static_cast<int>(parts), key_bits, partsT, status);
-    rc = launch_error("hawk_scatter_walk launch");
+    if (!use_seen) {
+        const long long count = static_cast<long long>(chunks) * cells;
+        const long long blocks = (count + 255) / 256 < 4096 ? (count + 255) / 256 : 4096;
+        hipLaunchKernelGGL(hawk_fill_zero, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, parts, count);
+        rc = launch_error("hawk_fill_zero launch");
+        if (rc != HK_OK) return rc;
+    }
+    if (sorted_walk) {
+        hipLaunchKernelGGL(hawk_scatter_walk, dim3(static_cast<unsigned>(chunks)), dim3(kWalkThreads), 0, s, key, v,
+                           static_cast<long long>(n), static_cast<long long>(cells), span, key_bits, use_seen,
+                           parts, touched, status);
+        rc = launch_error("hawk_scatter_walk launch");
+    } else {
+        hipLaunchKernelGGL(hawk_scatter_serial, dim3(static_cast<unsigned>(chunks)), dim3(64), 0, s, key, v,
+                           static_cast<long long>(n), static_cast<long long>(cells), span, parts, status);
+        rc = launch_error("hawk_scatter_serial launch");
+    }
     if (rc != HK_OK) return rc;
     const long long grid = (cells + 255) / 256;
-    hipLaunchKernelGGL(hawk_scatter_cells, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, partsT,
-                       static_cast<long long>(cells), chunks, target);
+    hipLaunchKernelGGL(hawk_scatter_cells, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, parts, touched,
+                       static_cast<long long>(cells), chunks, use_seen, target);
     return launch_error("hawk_scatter_cells launch");
 }
 

@@ -203,7 +203,7 @@ def test_ordered_sum_is_the_numpy_tree_bitwise_and_replays(unit, gpu, n):
 @pytest.mark.parametrize("cells, n, heavy", [(7, 30_000, False), (1000, 30_000, False), (1500, 30_000, False),
                                              (7, 20_000, True), (1, 3000, False), (200, 50, False),
                                              (1000, 1000, False), (65536, 400_000, False),
-                                             (70_000, 300_000, False)])
+                                             (70_000, 300_000, False), (600_000, 1_300_000, False)])
 def test_ordered_scatter_is_the_serial_walk_bitwise(unit, gpu, cells, n, heavy):
     import hawk_amd as hawk
     g = rng(cells + n)
