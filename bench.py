@@ -53,6 +53,12 @@ def _dev(a, device):
 # algorithmic bytes per sample of each kernel, and the CPU baseline's step.
 
 
+def ops(kernel) -> int:
+    """Floating-point operations per sample of a loaded kernel's per-sample
+    stage, as its build counted them in the emitted code."""
+    return int(kernel.sidecar.get("fp_ops_per_sample", 0))
+
+
 def workload(config: str, device):
     import torch
 
@@ -67,7 +73,7 @@ def workload(config: str, device):
         k = hawk.load(unit, "scale")
         X, OUT = _dev(x, device), torch.zeros(n, dtype=torch.float64, device=device)
         kernels = [k.prepare(x=X, a=2.0, b=1.0, out=OUT)]
-        work = {"scale": (16, 2)}
+        work = {"scale": (16, ops(k))}
 
         def cpu(threads):
             import oracle_lib as O
@@ -89,7 +95,7 @@ def workload(config: str, device):
         DO = torch.zeros(n, dtype=torch.float64, device=device)
         kernels = [kf.prepare(v=V, out=OUT), kv.prepare(v=V, bar_out=BO, bar_v=BV),
                    kj.prepare(v=V, dot_v=DV, dot_out=DO)]
-        work = {"energy": (32, 6), "energy_vjp": (56, 4), "energy_jvp": (56, 12)}
+        work = {"energy": (32, ops(kf)), "energy_vjp": (56, ops(kv)), "energy_jvp": (56, ops(kj))}
 
         def cpu(threads):
             import oracle_lib as O
@@ -114,7 +120,7 @@ def workload(config: str, device):
         R, VV, BR0, BV0 = (torch.zeros((3, n), dtype=torch.float64, device=device) for _ in range(4))
         kernels = [kf.prepare(r0=R0, v0=V0, mu=1.0, r=R, v=VV),
                    kv.prepare(r0=R0, v0=V0, mu=1.0, bar_r=BR, bar_v=BV, bar_r0=BR0, bar_v0=BV0)]
-        work = {"twobody": (96, 42 * 32), "twobody_vjp": (144, 3 * 42 * 32)}
+        work = {"twobody": (96, ops(kf)), "twobody_vjp": (144, ops(kv))}
 
         def cpu(threads):
             import oracle_lib as O
@@ -136,7 +142,7 @@ def workload(config: str, device):
         BA = torch.zeros((6, 6, n), dtype=torch.float64, device=device)
         BB = torch.zeros((6, n), dtype=torch.float64, device=device)
         kernels = [kf.prepare(A=Ad, b=bd, x=X), kv.prepare(A=Ad, b=bd, bar_x=BX, bar_A=BA, bar_b=BB)]
-        work = {"spd_solve": (384, 230), "spd_solve_vjp": (720, 410)}
+        work = {"spd_solve": (384, ops(kf)), "spd_solve_vjp": (720, ops(kv))}
 
         def cpu(threads):
             import oracle_lib as O
@@ -158,7 +164,7 @@ def workload(config: str, device):
         kernels = [k.prepare(x=X, key=KEY, y=Y, total=TOT, bins=BINS)]
         # per stage: the chain reads x, writes y; the sum reads y; the scatter reads key and y and
         # reads + writes every bin once
-        work = {"chain": (16, 14), "ordered_sum": (8, 1), "ordered_scatter": (12 + 16 * cells / n, 1)}
+        work = {"chain": (16, ops(k)), "ordered_sum": (8, 1), "ordered_scatter": (12 + 16 * cells / n, 1)}
 
         def cpu(threads):
             import oracle_lib as O

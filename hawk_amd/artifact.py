@@ -18,6 +18,7 @@ from dataclasses import dataclass
 from pathlib import Path
 
 from . import compile as _compile
+from .emit_hip import fp_ops_per_sample
 from .resources import kernel_resources
 from .emit_hip import plan_kernel
 from .ir import HawkError
@@ -95,6 +96,7 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
                 "cache_key": key, "compile_options": list(_compile.RTC_OPTIONS),
                 "toolchain": _compile.toolchain(),
                 "resources": kernel_resources(code).get(k.name, {}),
+                "fp_ops_per_sample": fp_ops_per_sample(plan.source),
             })
         _write(directory / f"{k.name}.json", json.dumps(sidecar, indent=1, sort_keys=True).encode())
         artifacts.append(Artifact(k.name, sidecar))

@@ -24,6 +24,8 @@ when the loop is unrolled.
 
 from __future__ import annotations
 
+import re
+
 import math
 from dataclasses import dataclass, field
 
@@ -541,6 +543,38 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     out += body + stores
     out += ["    }", "}", ""]
     return "\n".join(out)
+
+
+_FP_CALL = re.compile(r"\b(?:exp|sin|cos|tanh|sqrt|log|fabs)\(")
+_FP_BINARY = re.compile(r"(?<=[\w\)\]]) [-+*/] (?=[\w\(])")
+_PLANE_ACCESS = re.compile(r"hk_p_\w+(?:\[|_m\.|_cs\b)")
+_SAMPLE_LOOP = re.compile(r"^\s*for \(long long \w+ = (-?\d+)LL; \w+ != (-?\d+)LL; \w+ \+= (-?\d+)LL\) \{")
+
+
+def fp_ops_per_sample(source: str) -> int:
+    """The floating-point operations one sample executes in a rendered
+    per-sample stage: every binary + - * / and every exp/sin/cos/tanh/sqrt/
+    log/fabs call in the value statements (plane loads, stores and index
+    arithmetic excluded), each loop body counted trip times.  A division, a
+    square root and a transcendental each count as one operation."""
+    total = 0
+    mult = [1]
+    opens = []               # brace depth at which each sample loop was opened
+    depth = 0
+    body = source[source.index("const long long hk_i = base + hk_flat;"):]
+    for line in body.splitlines():
+        m = _SAMPLE_LOOP.match(line)
+        if m:
+            start, stop, step = (int(x) for x in m.groups())
+            mult.append(mult[-1] * max(0, (stop - start) // step))
+            opens.append(depth)
+        elif not _PLANE_ACCESS.search(line) and "hk_flat" not in line:
+            total += mult[-1] * (len(_FP_BINARY.findall(line)) + len(_FP_CALL.findall(line)))
+        depth += line.count("{") - line.count("}")
+        while opens and depth <= opens[-1]:
+            opens.pop()
+            mult.pop()
+    return total
 
 
 @dataclass

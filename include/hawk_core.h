@@ -167,13 +167,16 @@ int hk_ordered_fold_f64(const double* lanes, double* out, void* scratch,
 
 /* The keyed ordered scatter of reference `hawk/emit/team.py:322-460`
  * (`_scatter_zero`, `_scatter_chunks`, `_scatter_cells`) with the chunk rule
- * of `hawk/_lane_bind.py:111-114`: chunks = clamp(n / cells, 1, 256),
+ * of `hawk/_lane_bind.py:111-114`: chunks = clamp(n / max(cells, 1), 1, 256),
  * span = ceil(n / chunks); part[key][b] = the in-order sum from 0 of chunk
  * b's values with that key; target[c] += (sum from 0 over b, in order, of
  * part[c][b]).  Key -1 adds nothing; any other key outside [0, cells) adds
  * nothing and sets status[1+b] (status[0] = cells).  Returns HK_OK even when
- * a bad key was met: read the status plane (hk_scatter_check).
- * Scratch: hk_ordered_scatter_scratch_bytes(n, cells) bytes. */
+ * a bad key was met: the caller reads status[1..256] (the reference's
+ * `check_scatter_status`, `hawk/_lane_bind.py:148-154`).
+ * Scratch: hk_ordered_scatter_scratch_bytes(n, cells) bytes, no initial
+ * contents needed: the per-(chunk, cell) partials, then (up to 65536 cells)
+ * a per-chunk bitmap of the cells each chunk touched. */
 int hk_scatter_chunks(int64_t n, int64_t cells);
 size_t hk_ordered_scatter_scratch_bytes(int64_t n, int64_t cells);
 int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n,

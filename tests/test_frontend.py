@@ -247,3 +247,18 @@ def test_checkpointed_reverse_keeps_the_bits():
     assert got["bar_r0"].tobytes() == w0.tobytes() and got["bar_v0"].tobytes() == w1.tobytes()
     loops = [m for m in ir.topo([s.value for s in E.twobody_vjp.sinks]) if m.kind == "loop"]
     assert sorted(m.literal.trip for m in loops) == [4, 4, 4, 8, 8]
+
+
+def test_fp_op_count_of_the_emitted_stages():
+    """The sidecar's per-sample operation count is read off the emitted code:
+    scale is a*x+b (2), energy 0.5*((v0*v0+v1*v1)+v2*v2) (6), the chain's eight
+    stages 14 (exp, sin, 2, tanh, 3, 2, exp+fabs, 2), and a 32-substep loop body
+    counts 32 times."""
+    from hawk_amd import emit_hip
+
+    def count(k):
+        return emit_hip.fp_ops_per_sample(emit_hip.plan_kernel(k.program, k.name, "float64", 256, 1, True).source)
+    assert count(E.scale) == 2
+    assert count(E.energy) == 6
+    assert count(E.chain) == 14
+    assert count(E.twobody) % 32 == 0 and count(E.twobody) // 32 >= 30
