@@ -149,6 +149,26 @@ def workload(config: str, device):
             O.spd_solve(A, b, threads=threads)
             O.spd_solve_vjp(A, b, bar_x, threads=threads)
         return dict(name="6x6 SPD solve fwd + VJP (config 4a)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64")
+    if config == "4b":
+        n = 1 << 20
+        g = np.random.default_rng(4)
+        A = g.normal(0.0, 0.25, size=(16, 16, n)).astype(np.float32)
+        B = g.normal(0.0, 0.25, size=(16, 16, n)).astype(np.float32)
+        bar_C = np.random.default_rng(104).normal(0.0, 0.25, size=(16, 16, n)).astype(np.float32)
+        hawk.build([E.mm16, E.mm16_vjp], unit, mode="float32")
+        kf, kv = hawk.load(unit, "mm16"), hawk.load(unit, "mm16_vjp")
+        Ad, Bd, BC = _dev(A, device), _dev(B, device), _dev(bar_C, device)
+        C, BA, BB = (torch.zeros((16, 16, n), dtype=torch.float32, device=device) for _ in range(3))
+        kernels = [kf.prepare(A=Ad, B=Bd, C=C), kv.prepare(A=Ad, B=Bd, bar_C=BC, bar_A=BA, bar_B=BB)]
+        # labels are the team stage's: the forward's mm16 launch, then the VJP's
+        work = {"mm16": (3072, 8192), "mm16#2": (5120, 16384)}
+
+        def cpu(threads):
+            import oracle_lib as O
+            O.mm16(A, B, threads=threads)
+            O.mm16_vjp(A, B, bar_C, threads=threads)
+        return dict(name="fp32 16x16 product fwd + VJP (config 4b)", n=n, kernels=kernels, work=work, cpu=cpu,
+                    dtype="f32")
     if config == "5":
         n = 1 << 26
         g = np.random.default_rng(5)
@@ -179,7 +199,8 @@ def workload(config: str, device):
 #: The kernels a team stage launches, as rocprofv3 names them (the per-sample
 #: stage is one kernel named after the hawk kernel).
 STAGE_KERNELS = {"ordered_sum": ("hawk_sum_lanes", "hawk_sum_fold"),
-                 "ordered_scatter": ("hawk_scatter_status", "hawk_scatter_walk", "hawk_scatter_cells")}
+                 "ordered_scatter": ("hawk_scatter_status", "hawk_scatter_walk", "hawk_scatter_cells"),
+                 "mm16": ("hawk_mm16_f32",)}
 COPY_PROBE_BYTES = 1 << 30
 
 
@@ -222,10 +243,12 @@ def _pmc_pass(counter: str, config: str) -> dict:
     return seen
 
 
-def measure_traffic(config: str, kernels: list) -> dict:
+def measure_traffic(config: str, kernels: list, occurrence: int = 0, per_step: int = 1) -> dict:
     """HBM bytes per launch of the stage whose kernels are ``kernels``: FETCH_SIZE
     and WRITE_SIZE (KiB per dispatch, one pass each), each scaled by what the same
-    counter reads for a plain copy of 1 GiB."""
+    counter reads for a plain copy of 1 GiB.  When a step launches the same
+    kernel ``per_step`` times, the stage's dispatches are every ``per_step``-th
+    from ``occurrence``."""
     total = 0.0
     factors = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
@@ -239,7 +262,7 @@ def measure_traffic(config: str, kernels: list) -> dict:
         for k in kernels:
             if k not in seen:
                 raise RuntimeError(f"{counter}: kernel {k} was not seen")
-            total += statistics.median(seen[k]) * 1024.0 * factor
+            total += statistics.median(seen[k][occurrence::per_step]) * 1024.0 * factor
     return {"bytes": total, "factors": factors}
 
 
@@ -265,7 +288,12 @@ def main() -> int:
     log(f"config {args.config}: building and uploading inputs")
     w = workload(args.config, device)
     n = w["n"]
-    stages = [st for prep in w["kernels"] for st in prep.stages()]
+    stages = []
+    for prep in w["kernels"]:
+        for label, launch in prep.stages():
+            while label in (x for x, _ in stages):     # a stage label taken by an earlier kernel
+                label = label.split("#")[0] + "#" + str(int(label.split("#")[1]) + 1 if "#" in label else 2)
+            stages.append((label, launch))
     for _ in range(args.warmup):
         for _label, launch in stages:
             launch()
@@ -311,7 +339,10 @@ def main() -> int:
     traffic = None
     if not args.no_traffic:
         try:
-            t = measure_traffic(args.config, STAGE_KERNELS.get(dominant, (dominant,)))
+            base_label = dominant.split("#")[0]
+            occurrence = int(dominant.split("#")[1]) - 1 if "#" in dominant else 0
+            per_step = sum(1 for x in per_stage if x.split("#")[0] == base_label)
+            t = measure_traffic(args.config, STAGE_KERNELS.get(base_label, (base_label,)), occurrence, per_step)
             traffic = round(t["bytes"])
             log(f"traffic of {dominant}: {traffic / 1e6:.1f} MB per launch "
                 f"(algorithmic {d['bytes_per_sample'] * n / 1e6:.1f} MB; counter factors {t['factors']})")

@@ -1,7 +1,7 @@
 """Build step of hawk's gfx950 target: compile ``libhawk_core.so`` in-tree.
 
 The library is the C-ABI launcher (``csrc/hawk_core.cpp``) plus the
-hand-written team-stage kernels (``csrc/hawk_team.hip``), built by ``hipcc``
+hand-written team-stage kernels (``csrc/hawk_team.hip``, ``csrc/hawk_linalg.hip``), built by ``hipcc``
 for gfx950 only.  Its build digest is the sha256 of its own sources (each
 file's name and sha256, in sorted order), stamped into the library and
 recomputed by :mod:`hawk_amd._core` at load, the same self-check the
@@ -53,7 +53,7 @@ def build_library(verbose: bool = False) -> Path:
     cmd = [HIPCC, *HIP_FLAGS, "-fPIC", "-shared", "-std=c++17",
            f"-I{INCLUDE}", f"-I{CSRC}",
            f'-DHAWK_BUILD_DIGEST="{digest}"', f'-DHAWK_BUILD_INFO="{info}"',
-           str(CSRC / "hawk_core.cpp"), str(CSRC / "hawk_team.hip"),
+           str(CSRC / "hawk_core.cpp"), str(CSRC / "hawk_team.hip"), str(CSRC / "hawk_linalg.hip"),
            "-o", str(tmp), "-lhiprtc", "-lamdhip64"]
     if verbose:
         print(" ".join(cmd), flush=True)

@@ -58,6 +58,7 @@ def _declare(lib) -> None:
         "hk_scatter_chunks": (I, [I64, I64]),
         "hk_ordered_scatter_scratch_bytes": (SZ, [I64, I64]),
         "hk_ordered_scatter_f64": (I, [V, V, I64, V, I64, V, V, V]),
+        "hk_mm16_f32": (I, [ctypes.POINTER(V), I, ctypes.POINTER(V), I, ctypes.POINTER(ctypes.c_int32), I64, V]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -290,3 +291,15 @@ def ordered_scatter(key: int, v: int, n: int, target: int, cells: int, scratch: 
     check(lib().hk_ordered_scatter_f64(ctypes.c_void_p(key or None), ctypes.c_void_p(v or None), int(n),
                                        ctypes.c_void_p(target), int(cells), ctypes.c_void_p(scratch),
                                        ctypes.c_void_p(status), ctypes.c_void_p(stream or None)))
+
+
+def mm16(ins: list, outs: list, products: list, n: int, stream: int = 0) -> None:
+    """Per-sample 16x16 fp32 products on MFMA: ``outs[o] = op(ins[lhs]) @ op(ins[rhs])``
+    for ``products[o] = (lhs, rhs, transpose_lhs, transpose_rhs)``; planes by pointer."""
+    flat = []
+    for lhs, rhs, tl, tr in products:
+        flat += [int(lhs), int(rhs), (1 if tl else 0) | (2 if tr else 0)]
+    c_in = (ctypes.c_void_p * len(ins))(*[ctypes.c_void_p(p) for p in ins])
+    c_out = (ctypes.c_void_p * len(outs))(*[ctypes.c_void_p(p) for p in outs])
+    c_prod = (ctypes.c_int32 * len(flat))(*flat)
+    check(lib().hk_mm16_f32(c_in, len(ins), c_out, len(outs), c_prod, int(n), ctypes.c_void_p(stream or None)))

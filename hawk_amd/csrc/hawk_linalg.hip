@@ -1,0 +1,224 @@
+// hawk_linalg.hip — per-sample 16x16 fp32 matrix products on gfx950 MFMA.
+//
+// A hawk kernel whose every sink is a product of two 16x16 fp32 planes (each
+// possibly transposed) — the per-sample `mm` of reference
+// hawk/emit/policy.py:283-299 and hawk/emit/writer_aether.py:663-671, and its
+// VJP bar_A = bar_C B^T, bar_B = A^T bar_C — runs here as one team stage
+// instead of a thread-per-sample loop.  Planes keep hawk's layout: element
+// (r, c) of sample s at (r*16 + c)*N + s.
+//
+// A workgroup takes a tile of 32 consecutive samples (each element row of the
+// tile is one contiguous 128-byte run in HBM).  The product's K = 16 runs as
+// four MFMA K-slices (v_mfma_f32_16x16x4f32): for each slice the workgroup
+// stages in LDS only the 64 operand elements of each side of each product, so
+// a workgroup needs 34 KB of LDS and four share a CU; the accumulators stay in
+// registers across slices, and the results go back through LDS and out as
+// contiguous element rows.
+
+#include "hawk_core.h"
+#include "hawk_internal.h"
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <string>
+
+namespace {
+
+constexpr int kDim = 16;
+constexpr int kElems = kDim * kDim;          // 256 elements per sample
+constexpr int kTile = 32;                    // samples per workgroup: 128-byte runs of each element row
+constexpr int kStride = kTile + 1;           // LDS row stride (floats): odd, so rows fall in different banks
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kRowStep = kThreads / kTile;   // thread t stages rows t/32 + 8r
+constexpr int kMaxIn = 3;
+constexpr int kMaxOut = 2;
+constexpr int kSlices = 4;                   // K = 16 as four MFMA K-slices of 4
+constexpr int kSlotRows = 64;                // operand elements of one side of one product per slice
+
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+struct Product {
+    int lhs, lhs_t, rhs, rhs_t, out;
+};
+
+struct MmArgs {
+    const float* in[kMaxIn];
+    float* out[kMaxOut];
+    Product prod[kMaxOut];
+    int n_in, n_out;
+};
+
+// The MFMA's operand fragments for K slice q: lane l holds A[i][k] with
+// i = l % 16, k = 4q + l / 16 and B[k][j] with j = l % 16, k = 4q + l / 16;
+// the 4 accumulator registers of lane l hold D[4*(l/16) + v][l % 16], v = 0..3.
+__device__ __forceinline__ int lhs_elem(int lane, int q, int t) {
+    const int i = lane & 15, k = 4 * q + (lane >> 4);
+    return t ? k * kDim + i : i * kDim + k;
+}
+__device__ __forceinline__ int rhs_elem(int lane, int q, int t) {
+    const int j = lane & 15, k = 4 * q + (lane >> 4);
+    return t ? j * kDim + k : k * kDim + j;
+}
+
+// LDS (NOUT products): during the products, slot (o*2 + side)*64 + l holds,
+// for the tile's samples, the element that lane l of the MFMA reads for
+// product o's side (0 = lhs, 1 = rhs) in the current K slice; afterwards the
+// same memory holds half of one output (128 element rows) at a time.
+constexpr int kHalfRows = kElems / 2;
+template <int NOUT>
+constexpr int lds_floats() {
+    return (NOUT * 2 * kSlotRows > kHalfRows ? NOUT * 2 * kSlotRows : kHalfRows) * kStride;
+}
+
+// Load slice q of the tile into registers: thread t takes sample s0 + t % 32
+// of slots t/32 + 8r, so a wave's 64 lanes read two element rows of 32
+// consecutive samples (128 bytes each).
+template <int NOUT>
+__device__ __forceinline__ void slice_load(const MmArgs& args, long long n, long long s0, int count, int q,
+                                           float (&staged)[NOUT * 2 * kSlotRows / kRowStep]) {
+    const int s_own = threadIdx.x % kTile;
+    const int e_own = threadIdx.x / kTile;
+    const bool live = s_own < count;
+    constexpr int rows = NOUT * 2 * kSlotRows / kRowStep;
+    // Slots 8r .. 8r+7 lie in one 64-slot group, so product and side depend on
+    // r alone: the plane pointer and transposition are uniform per load.
+    constexpr int kRowsPerGroup = kSlotRows / kRowStep;
+#pragma unroll
+    for (int r = 0; r < rows; ++r) {
+        const int group = r / kRowsPerGroup;
+        const int o = group >> 1, side = group & 1;
+        const int l = e_own + (r % kRowsPerGroup) * kRowStep;
+        const Product& pr = args.prod[o];
+        const float* plane = args.in[side ? pr.rhs : pr.lhs];
+        const int e = side ? rhs_elem(l, q, pr.rhs_t) : lhs_elem(l, q, pr.lhs_t);
+        staged[r] = live ? __builtin_nontemporal_load(plane + static_cast<long long>(e) * n + s0 + s_own) : 0.0f;
+    }
+}
+
+// One workgroup per tile of 32 samples: four K slices (the next slice's loads
+// in flight during the current slice's MFMAs), then each output through LDS,
+// half at a time, and out as contiguous element rows.
+template <int NOUT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NOUT == 1 ? 4 : 3)))
+void hawk_mm16_f32(MmArgs args, long long n, long long tiles) {
+    __shared__ float lds[lds_floats<NOUT>()];
+    constexpr int rows = NOUT * 2 * kSlotRows / kRowStep;
+    const int t = threadIdx.x;
+    const int wave = t >> 6;
+    const int lane = t & 63;
+    const int s_own = t % kTile;
+    const int e_own = t / kTile;
+    const long long tile = blockIdx.x;
+    if (tile >= tiles) return;
+    const long long s0 = tile * kTile;
+    const int count = n - s0 < kTile ? static_cast<int>(n - s0) : kTile;
+
+    float4_t acc[NOUT][kTile / kWaves];
+#pragma unroll
+    for (int o = 0; o < NOUT; ++o)
+#pragma unroll
+        for (int m = 0; m < kTile / kWaves; ++m) acc[o][m] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    float staged[rows];
+    slice_load<NOUT>(args, n, s0, count, 0, staged);
+#pragma unroll
+    for (int q = 0; q < kSlices; ++q) {
+        if (q > 0) __syncthreads();                     // the previous slice's operands are read
+#pragma unroll
+        for (int r = 0; r < rows; ++r) lds[(e_own + r * kRowStep) * kStride + s_own] = staged[r];
+        __syncthreads();
+        if (q + 1 < kSlices) slice_load<NOUT>(args, n, s0, count, q + 1, staged);
+#pragma unroll
+        for (int o = 0; o < NOUT; ++o) {
+            const float* L = lds + (o * 2) * kSlotRows * kStride;
+            const float* R = L + kSlotRows * kStride;
+#pragma unroll
+            for (int m = 0; m < kTile / kWaves; ++m) {
+                const int s = wave + m * kWaves;
+                acc[o][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(L[lane * kStride + s], R[lane * kStride + s],
+                                                                 acc[o][m], 0, 0, 0);
+            }
+        }
+    }
+
+    // Lane l holds rows 4*(l/16) .. +3 of column l % 16: rows 0..7 (the first
+    // 128 elements) live in lanes 0..31, rows 8..15 in lanes 32..63.
+#pragma unroll
+    for (int o = 0; o < NOUT; ++o) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            __syncthreads();                            // the LDS is free for this half
+            if ((lane >> 5) == h) {
+#pragma unroll
+                for (int m = 0; m < kTile / kWaves; ++m) {
+                    const int s = wave + m * kWaves;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int e = (4 * (lane >> 4) + v) * kDim + (lane & 15) - h * kHalfRows;
+                        lds[e * kStride + s] = acc[o][m][v];
+                    }
+                }
+            }
+            __syncthreads();
+            if (s_own < count) {
+                float* dst = args.out[o] + s0 + s_own;
+#pragma unroll
+                for (int r = 0; r < kHalfRows / kRowStep; ++r) {
+                    const int e = e_own + r * kRowStep;
+                    __builtin_nontemporal_store(lds[e * kStride + s_own],
+                                                dst + static_cast<long long>(e + h * kHalfRows) * n);
+                }
+            }
+        }
+    }
+}
+
+int launch_error(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hawk_internal::set_hip_error(what, e);
+    return HK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hk_mm16_f32(const float* const* in, int n_in, float* const* out, int n_out, const int32_t* products,
+                int64_t n, void* stream) {
+    if (n_in < 1 || n_in > kMaxIn || n_out < 1 || n_out > kMaxOut || n_out > n_in)
+        return hawk_internal::set_error(HK_EVALUE,
+                                        "hk_mm16_f32: 1..3 input planes and 1..2 products, no more products than inputs");
+    if (n < 0) return hawk_internal::set_error(HK_EVALUE, "hk_mm16_f32: n must be >= 0");
+    if (!in || !out || !products)
+        return hawk_internal::set_error(HK_EVALUE, "hk_mm16_f32: in, out and products are required");
+    MmArgs args{};
+    args.n_in = n_in;
+    args.n_out = n_out;
+    for (int p = 0; p < n_in; ++p) {
+        if (!in[p]) return hawk_internal::set_error(HK_EVALUE, "hk_mm16_f32: input plane " + std::to_string(p) + " is null");
+        args.in[p] = in[p];
+    }
+    for (int o = 0; o < n_out; ++o) {
+        const int32_t* d = products + 3 * o;
+        const Product pr{d[0], d[2] & 1, d[1], (d[2] >> 1) & 1, o};
+        if (pr.lhs < 0 || pr.lhs >= n_in || pr.rhs < 0 || pr.rhs >= n_in)
+            return hawk_internal::set_error(HK_EINDEX, "hk_mm16_f32: product " + std::to_string(o) +
+                                                           " names an input plane outside [0, n_in)");
+        if (!out[o]) return hawk_internal::set_error(HK_EVALUE, "hk_mm16_f32: output plane " + std::to_string(o) + " is null");
+        args.prod[o] = pr;
+        args.out[o] = out[o];
+    }
+    if (n == 0) return HK_OK;
+    const long long tiles = (n + kTile - 1) / kTile;
+    if (tiles > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_mm16_f32: too many samples");
+    if (n_out == 1)
+        hipLaunchKernelGGL(hawk_mm16_f32<1>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
+                           static_cast<hipStream_t>(stream), args, static_cast<long long>(n), tiles);
+    else
+        hipLaunchKernelGGL(hawk_mm16_f32<2>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
+                           static_cast<hipStream_t>(stream), args, static_cast<long long>(n), tiles);
+    return launch_error("hawk_mm16_f32 launch");
+}
+
+}  // extern "C"

@@ -588,12 +588,52 @@ class Plan:
     planes: dict                    # every plane a caller binds: name -> {"role", "shape", "dtype"}
 
 
+def _mm16_products(program: Program):
+    """``(inputs, products)`` when every sink of ``program`` assigns a 16x16
+    product of two input planes, each possibly transposed (a forward ``C = A @ B``
+    or its VJP): the kernel then runs as one MFMA team stage.  ``None`` otherwise."""
+    sinks = program.sinks
+    if not sinks or len(sinks) > 2 or not all(isinstance(s, Assign) for s in sinks):
+        return None
+    ins, prods = [], []
+
+    def operand(n):
+        transposed = n.kind == "transpose"
+        if transposed:
+            n = n.operands[0]
+        if n.kind != "leaf" or n.ttype.shape != (16, 16) or n.literal[0] != "mat_in":
+            return None
+        pname = n.literal[1]
+        if pname not in ins:
+            ins.append(pname)
+        return ins.index(pname), transposed
+
+    for s in sinks:
+        v = s.value
+        if v.kind != "mm" or v.ttype.shape != (16, 16) or program.decls[s.name].ttype.shape != (16, 16):
+            return None
+        lhs, rhs = operand(v.operands[0]), operand(v.operands[1])
+        if lhs is None or rhs is None:
+            return None
+        prods.append([lhs[0], rhs[0], lhs[1], rhs[1]])
+    if len(ins) > 3 or len(prods) > len(ins):
+        return None
+    return ins, prods
+
+
 def plan_kernel(program: Program, name: str, mode: str = "float64", block: int = 256,
                 per_thread: int = 1, nontemporal: bool = False) -> Plan:
     """Split ``program`` into its per-sample stage and team stages, and render
     the per-sample stage."""
     if mode not in ("float64", "float32"):
         raise HawkError(f"mode={mode!r}: the hip target builds 'float64' or 'float32'")
+    products = _mm16_products(program) if mode == "float32" else None
+    if products is not None:
+        ins, prods = products
+        outs = [s.name for s in program.sinks]
+        planes = {pname: {"role": program.decls[pname].role, "shape": [16, 16], "dtype": "f32"}
+                  for pname in ins + outs}
+        return Plan(None, None, [{"op": "mm16", "in": ins, "out": outs, "products": prods}], planes)
     assigned = {id(s.value): s.name for s in program.sinks if isinstance(s, Assign)}
     extra, team = [], []
     for s in program.sinks:

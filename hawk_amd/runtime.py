@@ -185,6 +185,9 @@ class DeviceKernel:
                                       target.data_ptr(), cells, scratch.data_ptr(), status.data_ptr(), stream)
                 self.scatter_chunks = _core.scatter_chunks(n, cells)
                 statuses.append((t, status, cells))
+            elif t["op"] == "mm16":
+                _core.mm16([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
+                           t["products"], n, stream)
             else:
                 raise HawkError(f"kernel {self.name!r}: unknown team stage {t['op']!r}")
         if check:
@@ -297,6 +300,12 @@ class Prepared:
                         scratch.data_ptr(), status.data_ptr())
                 self.steps.append((_core.ordered_scatter, args))
                 self.statuses.append((t, status, cells))
+            elif t["op"] == "mm16":
+                args = ([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
+                        t["products"], self.n)
+                self.steps.append((_core.mm16, args))
+            else:
+                raise HawkError(f"kernel {kernel.name!r}: unknown team stage {t['op']!r}")
 
     def __call__(self) -> None:
         for _label, launch in self.stages():
@@ -313,9 +322,9 @@ class Prepared:
                 k.entry.run(self.block, 0, self.n, self.n, threads=k.launch_shape["block"],
                             per_thread=k.launch_shape["per_thread"], stream=self.stream)
             out.append((k.name, stage))
+        labels = {_core.ordered_sum: "ordered_sum", _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16"}
         for fn, args in self.steps:
-            label = "ordered_sum" if fn is _core.ordered_sum else "ordered_scatter"
-            out.append((label, lambda fn=fn, args=args: fn(*args, self.stream)))
+            out.append((labels[fn], lambda fn=fn, args=args: fn(*args, self.stream)))
         return out
 
     def check(self) -> None:

@@ -183,6 +183,18 @@ int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n,
                            double* target, int64_t cells, void* scratch,
                            int32_t* status, void* stream);
 
+/* Per-sample 16x16 fp32 matrix products on MFMA: for every sample s < n and
+ * product o < n_out, out[o] = op(in[lhs]) @ op(in[rhs]) with
+ * products[3*o .. 3*o+2] = {lhs, rhs, flags}, flags bit 0 = transpose lhs,
+ * bit 1 = transpose rhs.  Planes are [16, 16, n] fp32 (element (r, c) of
+ * sample s at (r*16 + c)*n + s); outputs are overwritten.  1..3 inputs,
+ * 1..2 products, no more products than inputs.  This is the per-sample `mm`
+ * of reference `hawk/emit/policy.py:283-299` / `hawk/emit/writer_aether.py:663-671`
+ * (forward C = A @ B) and its VJP (bar_A = bar_C @ B^T, bar_B = A^T @ bar_C,
+ * reference `hawk/diff/rules.py`), as one team stage. */
+int hk_mm16_f32(const float* const* in, int n_in, float* const* out, int n_out,
+                const int32_t* products, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -324,3 +324,43 @@ def test_chain_kernel_total_and_bins(unit, gpu, n):
     want_bins, status = O.ordered_scatter(key, gy, np.zeros(cells))
     assert not status[1:].any()
     assert host(bins).tobytes() == want_bins.tobytes()
+
+
+# -- config 4b --------------------------------------------------------------------
+
+def _mm_bound(X, Y):
+    """Per element of X @ Y (planes [16, 16, n]): 1e-6 * sum_k |x_ik| |y_kj|,
+    the north star's fp32 bar written as a bound on the products' magnitudes."""
+    return 1e-6 * np.einsum("ikn,kjn->ijn", np.abs(X).astype(np.float64), np.abs(Y).astype(np.float64))
+
+
+def _mm_exact(X, Y):
+    return np.einsum("ikn,kjn->ijn", X.astype(np.float64), Y.astype(np.float64))
+
+
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 1000, 65_537])
+def test_mm16_forward_and_vjp_on_mfma(unit32, gpu, n):
+    """C = A @ B and its VJP (bar_A = bar_C B^T, bar_B = A^T bar_C) per sample,
+    fp32 on MFMA: every element within 1e-6 * sum |a||b| of the exact product,
+    and of the oracle's fp32 loop."""
+    import hawk_amd as hawk
+    g = rng(4)
+    A = g.normal(0.0, 0.25, size=(16, 16, n)).astype(np.float32)
+    B = g.normal(0.0, 0.25, size=(16, 16, n)).astype(np.float32)
+    bar_C = rng(104).normal(0.0, 0.25, size=(16, 16, n)).astype(np.float32)
+    C = dev(np.zeros((16, 16, n), np.float32), gpu)
+    hawk.run(_load(unit32, "mm16"), A=dev(A, gpu), B=dev(B, gpu), C=C)
+    got = host(C)
+    bound = _mm_bound(A, B)
+    assert (np.abs(got - _mm_exact(A, B)) <= bound).all()
+    assert (np.abs(got - O.mm16(A, B)) <= 2 * bound).all()
+    bA = dev(np.zeros((16, 16, n), np.float32), gpu)
+    bB = dev(np.zeros((16, 16, n), np.float32), gpu)
+    hawk.run(_load(unit32, "mm16_vjp"), A=dev(A, gpu), B=dev(B, gpu), bar_C=dev(bar_C, gpu), bar_A=bA, bar_B=bB)
+    Bt, At = B.transpose(1, 0, 2), A.transpose(1, 0, 2)
+    wA, wB = O.mm16_vjp(A, B, bar_C)
+    assert (np.abs(host(bA) - _mm_exact(bar_C, Bt)) <= _mm_bound(bar_C, Bt)).all()
+    assert (np.abs(host(bB) - _mm_exact(At, bar_C)) <= _mm_bound(At, bar_C)).all()
+    assert (np.abs(host(bA) - wA) <= 2 * _mm_bound(bar_C, Bt)).all()
+    assert (np.abs(host(bB) - wB) <= 2 * _mm_bound(At, bar_C)).all()
+
