@@ -58,6 +58,8 @@ def _declare(lib) -> None:
         "hk_scatter_chunks": (I, [I64, I64]),
         "hk_ordered_scatter_scratch_bytes": (SZ, [I64, I64]),
         "hk_ordered_scatter_f64": (I, [V, V, I64, V, I64, V, V, V]),
+        "hk_rows_finish_scratch_bytes": (SZ, [I64]),
+        "hk_rows_finish_f64": (I, [V, V, I64, V, V, V]),
         "hk_mm16_f32": (I, [ctypes.POINTER(V), I, ctypes.POINTER(V), I, ctypes.POINTER(ctypes.c_int32), I64, V]),
     }
     for name, (res, args) in sig.items():
@@ -303,3 +305,13 @@ def mm16(ins: list, outs: list, products: list, n: int, stream: int = 0) -> None
     c_out = (ctypes.c_void_p * len(outs))(*[ctypes.c_void_p(p) for p in outs])
     c_prod = (ctypes.c_int32 * len(flat))(*flat)
     check(lib().hk_mm16_f32(c_in, len(ins), c_out, len(outs), c_prod, int(n), ctypes.c_void_p(stream or None)))
+
+
+def rows_finish_scratch_bytes(rows: int) -> int:
+    return int(lib().hk_rows_finish_scratch_bytes(int(rows)))
+
+
+def rows_finish(hi: int, comp: int, rows: int, out: int, scratch: int, stream: int = 0) -> None:
+    """Fold ``rows`` compensated row pairs into the cell ``out`` (canonical ordered tree)."""
+    check(lib().hk_rows_finish_f64(ctypes.c_void_p(hi), ctypes.c_void_p(comp), int(rows), ctypes.c_void_p(out),
+                                   ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))

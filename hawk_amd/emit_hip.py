@@ -38,7 +38,8 @@ LAYOUT_SIZES = (40, 32, 32, 8, 24)
 #: The by-value ABI shape of each role (reference hawk/emit/spelling.py:63-69);
 #: a rank-0 ``mutable`` is a 32-byte handle, a ranked one a 40-byte mirror.
 MIRROR_OF = {"out": "gref", "vec_in": "gref", "mat_in": "gref", "per_sample": "handle",
-             "wide_out": "handle", "accum_out": "handle", "lookup": "handle", "uniform": "value"}
+             "wide_out": "handle", "accum_out": "handle", "rows_out": "handle", "lookup": "handle",
+             "uniform": "value"}
 
 _UNARY_C = {"exp": "exp", "sin": "sin", "cos": "cos", "tanh": "tanh", "sqrt": "sqrt",
             "log": "log", "abs": "fabs"}
@@ -90,6 +91,7 @@ class Stage:
     planes: dict                    # name -> {"role", "shape", "dtype"}
     writes: list                    # [(plane, node)]
     scratch: dict = field(default_factory=dict)   # name -> {"dtype", "per_sample": 1}
+    row_sums: list = field(default_factory=list)  # [(cell, node, hi plane, comp plane)]
 
 
 class _Scope:
@@ -440,24 +442,32 @@ class _Writer:
         return [f"{t}[{slot}]" for t in tapes[n.literal]]
 
 
-def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: list) -> Stage:
-    """The plane table and arg_spec of the per-sample stage of ``program``."""
+def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: list,
+                  row_sums: list = ()) -> Stage:
+    """The plane table and arg_spec of the per-sample stage of ``program``;
+    ``row_sums`` = ``[(cell, node)]`` are default-policy sample sums whose
+    compensated 32-sample rows the stage writes."""
     writes = [(s.name, s.value) for s in program.sinks if isinstance(s, Assign)] + extra_writes
-    roots = [node for _, node in writes]
+    roots = [node for _, node in writes] + [node for _, node in row_sums]
     used_leaves = ir.leaves_of(roots)
-    used = {n.literal[1] for n in used_leaves} | {name for name, _ in writes}
+    rows = [(cell, node, f"hk_rows_{cell}", f"hk_rows_{cell}_comp") for cell, node in row_sums]
+    used = ({n.literal[1] for n in used_leaves} | {name for name, _ in writes}
+            | {p for r in rows for p in r[2:]})
     decls = dict(program.decls)
     planes = {}
     for name, node in extra_writes:
         if name not in decls:
             decls[name] = ir.Decl(name, "wide_out", node.ttype)
+    for _, _, hi, comp in rows:
+        for pname in (hi, comp):
+            decls[pname] = ir.Decl(pname, "rows_out", ir.TensorType((), "f64"))
     prog2 = Program(decls, program.sinks)
     spec = ir.arg_spec(prog2, used)
     for role, name in spec:
         d = decls[name]
         planes[name] = {"role": role, "shape": list(d.ttype.shape), "dtype": d.ttype.dtype,
                         "kind": kind_for(role, d.ttype, mode), "var": f"hk_p_{name}"}
-    return Stage(stage_name, spec, planes, writes)
+    return Stage(stage_name, spec, planes, writes, row_sums=rows)
 
 
 def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_taped: bool = True,
@@ -465,7 +475,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     """The HIP source of one per-sample stage.  ``nontemporal`` marks the
     plane loads and stores as streaming (read or written once, not kept in cache)."""
     w = _Writer(stage, mode, nontemporal)
-    roots = [node for _, node in stage.writes]
+    roots = [node for _, node in stage.writes] + [node for _, node, _, _ in stage.row_sums]
     # Which loops keep a tape: a loop that keeps or reads a tape, and every loop
     # nested in one, is unrolled, so every tape index is a constant and the tapes
     # live in registers (a checkpointed reverse keeps few enough of them live).
@@ -496,6 +506,10 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
                 c = _flat(node.ttype.shape, e)
                 w.emit(w.store(f"{var}[{c} * {var}_cs + hk_i]", vals[c]))
     stores = list(w.lines)
+    w.lines = []
+    row_terms = [(w.value(node)[0], stage.planes[hi]["var"], stage.planes[comp]["var"])
+                 for _, node, hi, comp in stage.row_sums]
+    body += w.lines                                   # (memoized: nothing new unless a term is a bare leaf)
 
     real = "float" if mode == "float32" else "double"
     params, unpack = [], []
@@ -506,7 +520,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         if kind in ("f64", "f32"):
             params.append(f"Real {var}")
             continue
-        is_input = role not in ("mutable", "out", "wide_out", "accum_out")
+        is_input = role not in ("mutable", "out", "wide_out", "accum_out", "rows_out")
         cq = "const " if is_input else ""
         elem = "int" if info["dtype"] == "i32" else "Real"
         if kind == "gref":
@@ -527,6 +541,10 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         "extern \"C\" __attribute__((used)) __device__ unsigned long long eagle_layout_sizes[5] = {"
         + ", ".join(str(s) for s in LAYOUT_SIZES) + "};",
         "",
+    ]
+    if row_terms:
+        out += _ROW_SUM_HELPERS.splitlines()
+    out += [
         f'extern "C" __global__ void __launch_bounds__({block}) {stage.name}(',
         "        " + ",\n        ".join(params) + ") {",
         "    (void)nSamples;",
@@ -537,12 +555,55 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         f"    for (int hk_v = 0; hk_v < {per_thread}; ++hk_v) {{",
         f"        const long long hk_flat = (static_cast<long long>(blockIdx.x) * {per_thread} + hk_v) * {block}"
         " + static_cast<long long>(threadIdx.x);",
-        "        if (hk_flat >= count) break;",
-        "        const long long hk_i = base + hk_flat;",
     ]
-    out += body + stores
+    if not row_terms:
+        out += ["        if (hk_flat >= count) break;",
+                "        const long long hk_i = base + hk_flat;"]
+        out += body + stores
+    else:
+        # Every lane of a half-wave takes part in its row's butterfly: a lane
+        # past `count` computes sample `base` (always bound) and adds +0.
+        out += ["        const bool hk_live = hk_flat < count;",
+                "        const long long hk_i = base + (hk_live ? hk_flat : 0LL);"]
+        out += body
+        out += ["        if (hk_live) {"] + ["    " + line for line in stores] + ["        }"]
+        for k, (term, hi, comp) in enumerate(row_terms):
+            out += [f"        {{ double hk_rh = hk_live ? static_cast<double>({term}) : 0.0, hk_rc = 0.0;",
+                    "          hk_row_sum(hk_rh, hk_rc);",
+                    "          if ((threadIdx.x & 31) == 0 && hk_live) {",
+                    "              const long long hk_r = (base + hk_flat) >> 5;",
+                    f"              {hi}[hk_r] = hk_rh;",
+                    f"              {comp}[hk_r] = hk_rc;",
+                    "          } }"]
     out += ["    }", "}", ""]
     return "\n".join(out)
+
+
+#: The row sum of a default-policy ``hawk.sum`` (reference
+#: ``hawk/emit/wrapper.py:542-665``): the 32 samples of a row (one half of a
+#: wave64) combine as compensated (hi, comp) pairs over the pairs (l, l ^ 16),
+#: (l, l ^ 8), ..., (l, l ^ 1) — the pairs of the reference's warp butterfly
+#: and of its host row walk.  The combine is symmetric, so both lanes of a
+#: pair hold its bits and every lane of the half ends with the row's partial.
+_ROW_SUM_HELPERS = """
+__device__ __forceinline__ bool hk_finite(double x) { return (x - x) == 0.0; }
+__device__ __forceinline__ double hk_two_sum_err(double a, double b, double s) {
+    const bool big_a = fabs(a) >= fabs(b);
+    const double big = big_a ? a : b;
+    const double small = big_a ? b : a;
+    return hk_finite(s) ? (small - (s - big)) + 0.0 : __builtin_nan("");
+}
+__device__ __forceinline__ void hk_row_sum(double& h, double& c) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) {
+        const double h2 = __shfl_xor(h, off, 64);
+        const double c2 = __shfl_xor(c, off, 64);
+        const double t = h + h2;
+        c = hk_finite(t) ? (c + c2) + hk_two_sum_err(h, h2, t) : 0.0;
+        h = t;
+    }
+}
+"""
 
 
 _FP_CALL = re.compile(r"\b(?:exp|sin|cos|tanh|sqrt|log|fabs)\(")
@@ -561,7 +622,7 @@ def fp_ops_per_sample(source: str) -> int:
     mult = [1]
     opens = []               # brace depth at which each sample loop was opened
     depth = 0
-    body = source[source.index("const long long hk_i = base + hk_flat;"):]
+    body = source[source.index("const long long hk_i = base"):]
     for line in body.splitlines():
         m = _SAMPLE_LOOP.match(line)
         if m:
@@ -635,9 +696,15 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                   for pname in ins + outs}
         return Plan(None, None, [{"op": "mm16", "in": ins, "out": outs, "products": prods}], planes)
     assigned = {id(s.value): s.name for s in program.sinks if isinstance(s, Assign)}
-    extra, team = [], []
+    extra, team, row_sums = [], [], []
     for s in program.sinks:
-        if isinstance(s, SampleSum):
+        if isinstance(s, SampleSum) and s.policy != "ordered":
+            if mode != "float64":
+                raise HawkError(f"hawk.sum(policy={s.policy!r}) on the hip target is built in float64")
+            row_sums.append((s.name, s.value))
+            team.append({"op": "row_sum", "hi": f"hk_rows_{s.name}", "comp": f"hk_rows_{s.name}_comp",
+                         "out": s.name})
+        elif isinstance(s, SampleSum):
             if mode != "float64":
                 raise HawkError("hawk.sum(policy='ordered') on the hip target is built in float64")
             src = assigned.get(id(s.value))
@@ -657,15 +724,17 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                 src = f"hk_scatter_{s.name}"
                 extra.append((src, s.value))
             team.append({"op": "ordered_scatter", "key": s.key.literal[1], "v": src, "target": s.name})
-    has_stage = any(isinstance(s, Assign) for s in program.sinks) or extra
+    has_stage = any(isinstance(s, Assign) for s in program.sinks) or extra or row_sums
     stage = source = None
     if has_stage:
-        stage = _stage_planes(program, name, mode, extra)
+        stage = _stage_planes(program, name, mode, extra, row_sums)
         source = render_stage(stage, mode, block, per_thread, nontemporal=nontemporal)
     planes = {}
     if stage is not None:
         for pname, info in stage.planes.items():
             planes[pname] = {k: info[k] for k in ("role", "shape", "dtype")}
+            if info["role"] == "rows_out":
+                planes[pname]["rows"] = 32                 # one value per 32 samples
     for t in team:
         for key in ("u", "key", "v"):
             pname = t.get(key)
@@ -674,8 +743,8 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                 planes[pname] = {"role": d.role, "shape": list(d.ttype.shape), "dtype": d.ttype.dtype}
         for key in ("out", "target"):
             pname = t.get(key)
-            if pname:
-                planes[pname] = {"role": "cell" if t["op"] == "ordered_sum" else "accum_out",
+            if pname and isinstance(pname, str):
+                planes[pname] = {"role": "cell" if t["op"] in ("ordered_sum", "row_sum") else "accum_out",
                                  "shape": [], "dtype": "f64"}
     for pname, info in planes.items():
         if pname.startswith("hk_"):

@@ -96,8 +96,19 @@ def ordered_add(key: Index, x: Scalar, acc: Mutable[Scalar]):
     _trace.scatter(acc, policy="ordered")[key] += x
 
 
+@kernel
+def sample_total(x: Scalar, y: Mutable[Scalar], total: Mutable[Scalar]):
+    y = 2.0 * x
+    total = _trace.sum(x * x)
+
+
+@kernel
+def plain_total(x: Scalar, total: Mutable[Scalar]):
+    total = _trace.sum(x)
+
+
 #: Every kernel above, by name.
 ALL = {k.name: k for k in (scale, energy, energy_vjp, energy_jvp, twobody, twobody_vjp, spd_solve,
-                            spd_solve_vjp, chain, ordered_total, ordered_add)}
+                            spd_solve_vjp, chain, ordered_total, ordered_add, sample_total, plain_total)}
 #: The float32 unit (built with mode="float32").
 FLOAT32 = {k.name: k for k in (mm16, mm16_vjp)}

@@ -27,7 +27,10 @@ class HawkError(Exception):
 
 #: Canonical role order of ``arg_spec`` == the entry-signature order
 #: (reference ``hawk/ir/nodes.py:51-52``).
-ROLE_ORDER = ("mutable", "out", "wide_out", "accum_out", "vec_in", "mat_in",
+#: ``rows_out`` is this target's own: the per-32-sample compensated row
+#: partials of a default-policy ``hawk.sum``, which the reference keeps as
+#: runtime-owned scratch rather than kernel arguments.
+ROLE_ORDER = ("mutable", "out", "wide_out", "accum_out", "rows_out", "vec_in", "mat_in",
               "wide_in", "per_sample", "lookup", "terminated", "uniform", "nsamples")
 
 UNARY = ("neg", "exp", "sin", "cos", "tanh", "sqrt", "abs", "log", "real")

@@ -134,6 +134,17 @@ class DeviceKernel:
             self._scratch[key] = held
         return held
 
+    def _row_sum(self, t: dict, bound: dict, n: int, device, stream: int) -> None:
+        """Fold the stage's row partials into the cell (a run of no samples sums to 0)."""
+        out = bound[t["out"]]
+        rows = -(-n // 32)
+        if rows == 0:
+            out.zero_()
+            return
+        scratch = self._buffer(("rows", t["out"], rows), _core.rows_finish_scratch_bytes(rows), device, zero=False)
+        _core.rows_finish(bound[t["hi"]].data_ptr(), bound[t["comp"]].data_ptr(), rows, out.data_ptr(),
+                          scratch.data_ptr(), stream)
+
     def _term_plane(self, name: str, n: int, device):
         torch = _torch()
         info = self.planes[name]
@@ -141,7 +152,10 @@ class DeviceKernel:
         key = ("plane", name, n)
         held = self._scratch.get(key)
         if held is None or held.device != device:
-            held = torch.empty(lead + (n,), dtype=self._real_dtype(), device=device)
+            if info.get("rows"):                       # one row partial per `rows` samples
+                held = torch.empty(max(1, -(-n // info["rows"])), dtype=torch.float64, device=device)
+            else:
+                held = torch.empty(lead + (n,), dtype=self._real_dtype(), device=device)
             self._scratch[key] = held
         return held
 
@@ -188,6 +202,8 @@ class DeviceKernel:
             elif t["op"] == "mm16":
                 _core.mm16([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
                            t["products"], n, stream)
+            elif t["op"] == "row_sum":
+                self._row_sum(t, bound, n, device, stream)
             else:
                 raise HawkError(f"kernel {self.name!r}: unknown team stage {t['op']!r}")
         if check:
@@ -304,6 +320,8 @@ class Prepared:
                 args = ([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
                         t["products"], self.n)
                 self.steps.append((_core.mm16, args))
+            elif t["op"] == "row_sum":
+                self.steps.append((kernel._row_sum, (t, bound, self.n, device)))
             else:
                 raise HawkError(f"kernel {kernel.name!r}: unknown team stage {t['op']!r}")
 
@@ -324,7 +342,8 @@ class Prepared:
             out.append((k.name, stage))
         labels = {_core.ordered_sum: "ordered_sum", _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16"}
         for fn, args in self.steps:
-            out.append((labels[fn], lambda fn=fn, args=args: fn(*args, self.stream)))
+            label = labels.get(fn, "row_sum")
+            out.append((label, lambda fn=fn, args=args: fn(*args, self.stream)))
         return out
 
     def check(self) -> None:

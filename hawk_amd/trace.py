@@ -214,12 +214,13 @@ def sum(x: Any, policy: str = "auto") -> Reduced:  # noqa: A001 - hawk's spellin
     ``hawk/trace/reduce.py:277-287``).  ``policy="ordered"`` adds in a fixed
     tree that depends on the sample count only: 65536 virtual lanes, each
     adding its rows in order, folded in groups of 1024 by a halving tree and
-    the 64 group results by the same tree — the same bits on every launch."""
+    the 64 group results by the same tree — the same bits on every launch.
+    The default policies (``"auto"``, ``"compensated"``) sum each row of 32
+    samples as a compensated (hi, comp) pair and fold the rows in the
+    canonical ordered tree of reference ``hawk/_cells.py`` — also the same
+    bits on every launch."""
     if policy not in SUM_POLICIES:
         raise HawkError(f"hawk.sum(x, policy={policy!r}): policy={policy!r} is not one of {SUM_POLICIES}")
-    if policy != "ordered":
-        raise HawkError(f"hawk.sum(x, policy={policy!r}): the hip target builds policy='ordered' "
-                        "(the fixed tree); the compensated row sums are not in this build")
     n = _projected(node_of(x))
     if n.ttype.shape:
         raise HawkError("hawk.sum over samples of a vector or matrix is not in this build; "

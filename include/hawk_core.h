@@ -165,6 +165,18 @@ int hk_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch,
 int hk_ordered_fold_f64(const double* lanes, double* out, void* scratch,
                         void* stream);
 
+/* The finish of a default-policy sample sum (`hawk.sum(x)`): `rows`
+ * compensated (hi, comp) row pairs (one per 32 samples, written by the
+ * per-sample stage as reference `hawk/emit/wrapper.py:542-665` does) folded
+ * in the canonical ordered tree of reference `hawk/_cells.py:71-119` (leaves
+ * of 256 slots x 16 rows with Neumaier adds, the in-leaf halving tree,
+ * pairwise levels over the leaves) and STORED to *out as hi + comp.  The
+ * reference finishes on the host; here it stays on the device.
+ * Scratch: hk_rows_finish_scratch_bytes(rows) bytes. */
+size_t hk_rows_finish_scratch_bytes(int64_t rows);
+int hk_rows_finish_f64(const double* hi, const double* comp, int64_t rows,
+                       double* out, void* scratch, void* stream);
+
 /* The keyed ordered scatter of reference `hawk/emit/team.py:322-460`
  * (`_scatter_zero`, `_scatter_chunks`, `_scatter_cells`) with the chunk rule
  * of `hawk/_lane_bind.py:111-114`: chunks = clamp(n / max(cells, 1), 1, 256),

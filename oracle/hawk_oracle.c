@@ -130,6 +130,111 @@ static double fold_groups(double* gp) {
     return gp[0];
 }
 
+/* ---- default-policy sample sum: compensated rows, canonical finish -------
+ * Reference hawk/emit/wrapper.py:542-665 (sampleSumRow_: a row of 32 slots,
+ * slot l combined with slot l + off for off = 16, 8, 4, 2, 1 by pairCombine_)
+ * and hawk/_cells.py:44-119 (twoSumErr, Neumaier add, pair combine, leaves of
+ * 256 slots x 16 rows, the in-leaf halving tree, pairwise levels, hi + comp). */
+static int fin(double x) { return (x - x) == 0.0; }
+
+static double two_sum_err(double a, double b, double s) {
+    const int big_a = fabs(a) >= fabs(b);
+    const double big = big_a ? a : b, small = big_a ? b : a;
+    return fin(s) ? (small - (s - big)) + 0.0 : NAN;
+}
+
+static void pair_add(double* h, double* c, double h2, double c2) {
+    const double s = *h + h2;
+    *c = fin(s) ? (*c + c2) + two_sum_err(*h, h2, s) : 0.0;
+    *h = s;
+}
+
+static void neumaier_add(double* h, double* c, double x, double xc) {
+    const double s = *h + x;
+    *c = fin(s) ? *c + two_sum_err(*h, x, s) : 0.0;
+    *c = fin(s) ? *c + xc : 0.0;
+    *h = s;
+}
+
+/* Rows of 32 terms (a ragged last row padded with +0). */
+HKO_EXPORT void hko_row_sums(const double* t, int64_t n, double* hi, double* comp) {
+    const int64_t rows = (n + 31) / 32;
+    for (int64_t r = 0; r < rows; ++r) {
+        double h[32], c[32];
+        for (int l = 0; l < 32; ++l) {
+            h[l] = r * 32 + l < n ? t[r * 32 + l] : 0.0;
+            c[l] = 0.0;
+        }
+        for (int off = 16; off >= 1; off >>= 1)
+            for (int l = 0; l < off; ++l) pair_add(&h[l], &c[l], h[l + off], c[l + off]);
+        hi[r] = h[0];
+        comp[r] = c[0];
+    }
+}
+
+/* The leaf of rows [0, cnt) of (hi, comp), cnt <= 4096. */
+static void rows_leaf(const double* hi, const double* comp, int cnt, double* lh, double* lc) {
+    double sh[256], sc[256];
+    const int live = cnt < 256 ? cnt : 256;
+    for (int s = 0; s < live; ++s) {
+        sh[s] = hi[s];
+        sc[s] = fin(hi[s]) ? comp[s] : 0.0;
+    }
+    for (int k = 1; k < 16; ++k) {
+        const int m = live < cnt - k * 256 ? live : cnt - k * 256;
+        if (m <= 0) break;
+        for (int s = 0; s < m; ++s) neumaier_add(&sh[s], &sc[s], hi[k * 256 + s], comp[k * 256 + s]);
+    }
+    for (int off = 128; off > 0; off >>= 1) {
+        const int lim = live > off ? (off < live - off ? off : live - off) : 0;
+        for (int s = 0; s < lim; ++s) pair_add(&sh[s], &sc[s], sh[s + off], sc[s + off]);
+    }
+    *lh = sh[0];
+    *lc = sc[0];
+}
+
+HKO_EXPORT double hko_rows_finish(const double* hi, const double* comp, int64_t rows) {
+    if (rows <= 0) return 0.0;
+    const int64_t leaves = (rows + 4095) / 4096;
+    double* vh = (double*)malloc(sizeof(double) * (size_t)leaves);
+    double* vc = (double*)malloc(sizeof(double) * (size_t)leaves);
+    for (int64_t j = 0; j < leaves; ++j) {
+        const int64_t rest = rows - j * 4096;
+        rows_leaf(hi + j * 4096, comp + j * 4096, (int)(rest < 4096 ? rest : 4096), &vh[j], &vc[j]);
+    }
+    int64_t m = leaves;
+    while (m > 1) {
+        const int64_t pairs = m / 2;
+        for (int64_t p = 0; p < pairs; ++p) {
+            double h = vh[2 * p], c = vc[2 * p];
+            pair_add(&h, &c, vh[2 * p + 1], vc[2 * p + 1]);
+            vh[p] = h;
+            vc[p] = c;
+        }
+        if (m & 1) {
+            vh[pairs] = vh[m - 1];
+            vc[pairs] = vc[m - 1];
+        }
+        m = pairs + (m & 1);
+    }
+    const double out = fin(vh[0]) ? vh[0] + vc[0] : vh[0];
+    free(vh);
+    free(vc);
+    return out;
+}
+
+HKO_EXPORT double hko_sample_sum(const double* t, int64_t n) {
+    const int64_t rows = (n + 31) / 32;
+    if (rows == 0) return 0.0;
+    double* hi = (double*)malloc(sizeof(double) * (size_t)rows);
+    double* comp = (double*)malloc(sizeof(double) * (size_t)rows);
+    hko_row_sums(t, n, hi, comp);
+    const double out = hko_rows_finish(hi, comp, rows);
+    free(hi);
+    free(comp);
+    return out;
+}
+
 HKO_EXPORT double hko_ordered_sum(const double* u, int64_t n) {
     double gp[HKO_G];
     for (int g = 0; g < HKO_G; ++g) gp[g] = group_part(u, n, g);

@@ -43,6 +43,9 @@ def lib(profile: str = "portable"):
         "hko_chain": (None, [_P, _P, _I64, _I64]),
         "hko_libm": (None, [ctypes.c_int, _P, _P, _I64]),
         "hko_ordered_sum": (_D, [_P, _I64]),
+        "hko_row_sums": (None, [_P, _I64, _P, _P]),
+        "hko_rows_finish": (_D, [_P, _P, _I64]),
+        "hko_sample_sum": (_D, [_P, _I64]),
         "hko_scatter_chunks": (ctypes.c_int, [_I64, _I64]),
         "hko_ordered_scatter": (None, [_P, _P, _I64, _P, _I64, _P, _P]),
         "hko_twobody": (None, [_P, _P, _D, _I64, _P, _P, _I64, _I64]),
@@ -116,6 +119,27 @@ def ordered_sum(u, threads: int = 1) -> float:
     if threads > 1:
         return lib().hko_ordered_sum_threads(_p(u), u.size, threads)
     return lib().hko_ordered_sum(_p(u), u.size)
+
+
+def row_sums(t):
+    """The compensated (hi, comp) pair of every row of 32 terms."""
+    t = np.ascontiguousarray(t, dtype=np.float64)
+    rows = -(-t.size // 32)
+    hi, comp = np.empty(rows), np.empty(rows)
+    lib().hko_row_sums(_p(t), t.size, _p(hi), _p(comp))
+    return hi, comp
+
+
+def rows_finish(hi, comp) -> float:
+    hi = np.ascontiguousarray(hi, dtype=np.float64)
+    comp = np.ascontiguousarray(comp, dtype=np.float64)
+    return lib().hko_rows_finish(_p(hi), _p(comp), hi.size)
+
+
+def sample_sum(t) -> float:
+    """The default-policy hawk.sum of the terms t (rows, then the canonical finish)."""
+    t = np.ascontiguousarray(t, dtype=np.float64)
+    return lib().hko_sample_sum(_p(t), t.size)
 
 
 def scatter_chunks(n, cells) -> int:

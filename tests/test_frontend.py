@@ -276,3 +276,15 @@ def test_mm16_and_its_vjp_are_one_mfma_team_stage(tmp_path):
     assert t["out"] == ["bar_A", "bar_B"]
     named = [(t["in"][l], t["in"][r], tl, tr) for l, r, tl, tr in t["products"]]
     assert named == [("bar_C", "B", False, True), ("A", "bar_C", True, False)]
+
+
+def test_default_sum_is_a_row_sum_team_stage(tmp_path):
+    """hawk.sum(x) with the default policy: the stage writes compensated
+    32-sample rows into runtime-owned planes, a row_sum team stage finishes the
+    cell; the rows are not planes the caller binds."""
+    b = hawk.build([E.sample_total], tmp_path)
+    sc = b.sidecar("sample_total")
+    assert sc["team"] == [{"op": "row_sum", "hi": "hk_rows_total", "comp": "hk_rows_total_comp", "out": "total"}]
+    assert sc["planes"]["hk_rows_total"]["rows"] == 32 and sc["planes"]["hk_rows_total"]["scratch"]
+    assert sc["planes"]["total"]["role"] == "cell"
+    assert [n for r, n in sc["arg_spec"] if r == "rows_out"] == ["hk_rows_total", "hk_rows_total_comp"]

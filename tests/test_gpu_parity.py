@@ -364,3 +364,41 @@ def test_mm16_forward_and_vjp_on_mfma(unit32, gpu, n):
     assert (np.abs(host(bA) - wA) <= 2 * _mm_bound(bar_C, Bt)).all()
     assert (np.abs(host(bB) - wB) <= 2 * _mm_bound(At, bar_C)).all()
 
+
+
+# -- the default-policy sample sum (a7') ----------------------------------------
+
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 1000, 65_536, 4096 * 32 + 5, 300_001])
+def test_default_sum_is_the_oracle_bitwise(unit, gpu, n):
+    """hawk.sum(x * x) with the default policy: 32-sample compensated rows on
+    the device (half-wave butterflies) and the canonical finish, the oracle's
+    bits on every replay; the stage's per-sample output is untouched by it."""
+    import hawk_amd as hawk
+    g = rng(n)
+    x = g.normal(size=n) * np.exp(g.normal(size=n))
+    k = _load(unit, "sample_total")
+    want = O.sample_sum(x * x)
+    for _ in range(3):
+        y = dev(np.zeros(n), gpu)
+        total = dev(np.zeros(1), gpu)
+        hawk.run(k, x=dev(x, gpu), y=y, total=total)
+        assert host(total)[0] == want
+        assert host(y).tobytes() == (2.0 * x).tobytes()
+
+
+def test_default_sum_special_values(unit, gpu):
+    import hawk_amd as hawk
+    k = _load(unit, "plain_total")
+
+    def total_of(x):
+        t = dev(np.full(1, 7.0), gpu)
+        hawk.run(k, x=dev(x, gpu), total=t)
+        return host(t)[0]
+    z = total_of(np.zeros(1000))
+    assert z == 0.0 and not np.signbit(z)
+    x = np.ones(5000)
+    x[1234] = np.inf
+    assert total_of(x) == np.inf
+    x[999] = -np.inf
+    assert np.isnan(total_of(x))
+    assert total_of(np.arange(1.0, 100_001.0)) == 100_000 * 100_001 / 2

@@ -268,3 +268,76 @@ def test_threaded_tiles_are_the_serial_bits():
     a = O.twobody(r0, v0, 1.0)
     b = O.twobody(r0, v0, 1.0, threads=5)
     assert a[0].tobytes() == b[0].tobytes() and a[1].tobytes() == b[1].tobytes()
+
+
+# -- the default-policy sample sum (compensated rows, canonical finish) ------
+
+def _ulp(x):
+    return np.spacing(np.abs(np.float64(x)))
+
+
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 1000, 65536])
+def test_row_sums_equal_the_float64_reference(n):
+    """Each row's hi + comp equals the float64 sum of its 32 terms within
+    1e-14 of the run's sum of |term| (the reference's own row check,
+    tests/test_sample_sum.py:36-38, :98-112), and is the correctly rounded
+    sum to one ulp (math.fsum)."""
+    import math
+    t = np.random.default_rng(n).normal(size=n) * np.exp(np.random.default_rng(n + 1).normal(size=n))
+    hi, comp = O.row_sums(t)
+    pad = np.zeros(hi.size * 32)
+    pad[:n] = t
+    rows = pad.reshape(-1, 32)
+    got = hi + comp
+    assert np.all(np.abs(got - rows.sum(1)) <= 1e-14 * np.abs(rows).sum(1) + 1e-300)
+    exact = np.array([math.fsum(r) for r in rows])
+    assert np.all(np.abs(got - exact) <= _ulp(exact))
+
+
+def test_row_sums_compensate_cancellation():
+    """Rows whose terms cancel to 1e-8 of their magnitude: the compensated
+    pair gives the correctly rounded sum, which the plain pairwise tree of the
+    same rows misses by many ulps — a dropped or sign-flipped compensation
+    term fails here."""
+    import math
+    g = np.random.default_rng(7)
+    base = g.normal(size=(64, 16)) * 1e8
+    t = np.concatenate([base, -base + g.normal(size=(64, 16))], axis=1)
+    t = np.take_along_axis(t, np.argsort(g.random(t.shape), axis=1), axis=1).reshape(-1)
+    hi, comp = O.row_sums(t)
+    exact = np.array([math.fsum(r) for r in t.reshape(-1, 32)])
+    assert np.all(np.abs(hi + comp - exact) <= _ulp(exact))
+    plain = t.reshape(-1, 32).copy()
+    w = 16
+    while w:
+        plain[:, :w] += plain[:, w:2 * w]
+        w //= 2
+    assert np.max(np.abs(plain[:, 0] - exact) / _ulp(exact)) > 100
+
+
+@pytest.mark.parametrize("rows", [1, 255, 256, 257, 4095, 4096, 4097, 3 * 4096 + 17, 70000])
+def test_rows_finish_is_the_correctly_rounded_sum(rows):
+    """The finish across leaf boundaries (4096 rows a leaf) equals fsum of
+    every hi and comp to one ulp.  The bits of the leaf structure beyond that
+    are pinned only by the fsum property (the reference pins them against
+    eagle's ordered finish by import, tests/test_run_cells.py:83-99)."""
+    import math
+    g = np.random.default_rng(rows)
+    hi = g.normal(size=rows) * np.exp(g.normal(size=rows))
+    comp = hi * g.normal(size=rows) * 1e-17
+    exact = math.fsum(np.concatenate([hi, comp]))
+    assert abs(O.rows_finish(hi, comp) - exact) <= _ulp(exact)
+
+
+def test_sample_sum_special_values():
+    assert O.sample_sum(np.zeros(100)) == 0.0 and not np.signbit(O.sample_sum(np.zeros(100)))
+    assert O.sample_sum(np.zeros(0)) == 0.0
+    x = np.ones(5000)
+    x[1234] = np.inf
+    assert O.sample_sum(x) == np.inf
+    x[999] = -np.inf
+    assert np.isnan(O.sample_sum(x))
+    x = np.ones(5000)
+    x[17] = np.nan
+    assert np.isnan(O.sample_sum(x))
+    assert O.sample_sum(np.arange(1.0, 100001.0)) == 100000 * 100001 / 2
