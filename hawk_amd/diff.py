@@ -22,7 +22,7 @@ plane ``bar_x``; a tangent input is ``dot_x`` and a tangent output ``dot_y``.
 from __future__ import annotations
 
 from . import ir
-from .ir import (Assign, Decl, Deps, HawkError, Node, Program, fresh_placeholders, free_inputs,
+from .ir import (Assign, Decl, SampleSum, Deps, HawkError, Node, Program, fresh_placeholders, free_inputs,
                  level_order, make, zero_like)
 from .trace import Kernel
 from .types import role_of
@@ -319,28 +319,44 @@ def _namer(program: Program, prefix: str):
     return name
 
 
-def _differentiable_inputs(program: Program, wrt) -> list:
+def _differentiable_inputs(program: Program, wrt, params: bool = False) -> list:
+    """The inputs ``wrt`` names (default: every real input plane).  With
+    ``params``, a ``Param`` may be named too (a reverse-mode gradient of a
+    parameter is a cell summed over samples)."""
     inputs = [d for d in program.decls.values()
               if d.role in ("per_sample", "vec_in", "mat_in") and d.ttype.dtype in ("f64", "f32")]
     if wrt is None:
         return inputs
     wrt = (wrt,) if isinstance(wrt, str) else tuple(wrt)
     by_name = {d.name: d for d in inputs}
+    if params:
+        by_name.update({d.name: d for d in program.decls.values() if d.role == "uniform"})
     missing = [w for w in wrt if w not in by_name]
     if missing:
-        raise HawkError(f"wrt={missing}: not differentiable input planes of this kernel "
+        raise HawkError(f"wrt={missing}: not differentiable inputs of this kernel "
                         f"(those are {sorted(by_name)})")
     return [by_name[w] for w in wrt]
+
+
+def param_planes(kernel):
+    """The reference's spelling for differentiating a kernel's parameters
+    (reference ``hawk/diff/transform.py:443-456``): ``vjp(param_planes(k),
+    wrt=(..., "mu"))``.  On this target ``vjp`` takes a ``Param`` in ``wrt``
+    directly, so this returns the kernel unchanged."""
+    return kernel
 
 
 def vjp(kernel, wrt=None) -> Program:
     """The reverse-mode derivative: a program reading the primal inputs and an
     adjoint seed plane ``bar_<sink>`` per per-sample sink, and writing
-    ``bar_<x>`` for each input ``x`` of ``wrt`` (default: every real input)."""
+    ``bar_<x>`` for each input ``x`` of ``wrt`` (default: every real input
+    plane).  A ``Param`` named in ``wrt`` gets a cell ``bar_<param>``: the
+    sum over samples of each sample's contribution, by ``hawk.sum``'s default
+    policy."""
     program = _program_of(kernel)
     _refuse_prior_reads(program, "vjp")
     name = _namer(program, "bar")
-    targets = _differentiable_inputs(program, wrt)
+    targets = _differentiable_inputs(program, wrt, params=True)
     for s in program.sinks:
         if not isinstance(s, Assign):
             raise HawkError(f"vjp of a kernel with {type(s).__name__} sink {s.name!r} is not in this build")
@@ -369,7 +385,12 @@ def vjp(kernel, wrt=None) -> Program:
         if g.ttype.shape != d.ttype.shape:
             g = make("splat", (g,), d.ttype.shape)
         out.decls[grad_name] = Decl(grad_name, "mutable", d.ttype)
-        out.sinks.append(Assign(grad_name, g, "mutable"))
+        if d.role == "uniform":
+            # a parameter's gradient: every sample's contribution, summed
+            # (reference hawk/diff/transform.py:443-456, the default policy)
+            out.sinks.append(SampleSum(grad_name, g, "auto"))
+        else:
+            out.sinks.append(Assign(grad_name, g, "mutable"))
     _drop_unused_inputs(out)
     return out
 

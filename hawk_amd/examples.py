@@ -53,6 +53,9 @@ def twobody(r0: Vector[3], v0: Vector[3], mu: Param, r: Mutable[Vector[3]], v: M
 
 
 twobody_vjp = Kernel("twobody_vjp", diff.vjp(twobody, wrt=("r0", "v0")))
+#: The two-body VJP with the gravitational parameter's gradient too: a cell
+#: summed over every sample.
+twobody_vjp_mu = Kernel("twobody_vjp_mu", diff.vjp(diff.param_planes(twobody), wrt=("r0", "v0", "mu")))
 
 
 @kernel
@@ -109,6 +112,7 @@ def plain_total(x: Scalar, total: Mutable[Scalar]):
 
 #: Every kernel above, by name.
 ALL = {k.name: k for k in (scale, energy, energy_vjp, energy_jvp, twobody, twobody_vjp, spd_solve,
-                            spd_solve_vjp, chain, ordered_total, ordered_add, sample_total, plain_total)}
+                            spd_solve_vjp, chain, ordered_total, ordered_add, sample_total, plain_total,
+                            twobody_vjp_mu)}
 #: The float32 unit (built with mode="float32").
 FLOAT32 = {k.name: k for k in (mm16, mm16_vjp)}

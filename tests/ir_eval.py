@@ -182,10 +182,11 @@ class Evaluator:
 
 
 def evaluate(program, env: dict, n: int) -> dict:
-    """``{sink name: value}`` of the per-sample sinks of ``program``."""
+    """``{sink name: value}`` of the per-sample sinks of ``program``; a
+    ``hawk.sum`` sink gives its per-sample terms (the caller sums them)."""
     ev = Evaluator(env, n)
     out = {}
     for s in program.sinks:
-        if isinstance(s, ir.Assign):
+        if isinstance(s, (ir.Assign, ir.SampleSum)):
             out[s.name] = ev.value(s.value)
     return out

@@ -288,3 +288,33 @@ def test_default_sum_is_a_row_sum_team_stage(tmp_path):
     assert sc["planes"]["hk_rows_total"]["rows"] == 32 and sc["planes"]["hk_rows_total"]["scratch"]
     assert sc["planes"]["total"]["role"] == "cell"
     assert [n for r, n in sc["arg_spec"] if r == "rows_out"] == ["hk_rows_total", "hk_rows_total_comp"]
+
+
+def test_param_gradient_is_a_summed_cell_matching_finite_differences():
+    """vjp(param_planes(twobody), wrt=(r0, v0, mu)): bar_r0 / bar_v0 are the
+    plain VJP's planes, bar_mu is a default-policy hawk.sum of each sample's
+    contribution, and that sum is d/dmu of sum_s <bar, (r, v)(mu)> by central
+    differences of the oracle's forward."""
+    import math
+    n = 200
+    g = np.random.default_rng(11)
+    d = g.normal(size=(3, n))
+    d /= np.linalg.norm(d, axis=0)
+    r0 = d * g.uniform(0.5, 2.0, n)
+    v0 = g.normal(0.0, 0.3, size=(3, n))
+    bar_r, bar_v = g.normal(size=(3, n)), g.normal(size=(3, n))
+    env = {"r0": r0, "v0": v0, "mu": 1.3, "bar_r": bar_r, "bar_v": bar_v}
+    prog = E.twobody_vjp_mu.program
+    assert [type(s).__name__ for s in prog.sinks] == ["Assign", "Assign", "SampleSum"]
+    got = evaluate(prog, env, n)
+    plain = evaluate(E.twobody_vjp.program, env, n)
+    assert got["bar_r0"].tobytes() == plain["bar_r0"].tobytes()
+    assert got["bar_v0"].tobytes() == plain["bar_v0"].tobytes()
+
+    def loss(mu):
+        r, v = O.twobody(r0, v0, mu)
+        return math.fsum(((bar_r * r).sum(axis=0) + (bar_v * v).sum(axis=0)).tolist())
+    h = 1e-6
+    fd = (loss(1.3 + h) - loss(1.3 - h)) / (2 * h)
+    total = O.sample_sum(got["bar_mu"])
+    assert abs(total - fd) <= 1e-6 * abs(fd) + 1e-8

@@ -402,3 +402,28 @@ def test_default_sum_special_values(unit, gpu):
     x[999] = -np.inf
     assert np.isnan(total_of(x))
     assert total_of(np.arange(1.0, 100_001.0)) == 100_000 * 100_001 / 2
+
+
+@pytest.mark.parametrize("n", [1, 1000, 65_537])
+def test_param_gradient_cell_on_the_device(unit, gpu, n):
+    """The two-body VJP with mu's gradient: bar_r0 / bar_v0 are the oracle's
+    bits, bar_mu is the default-policy sum of the per-sample contributions the
+    IR gives (tests/ir_eval.py), bit for bit."""
+    import hawk_amd as hawk
+    from hawk_amd import examples as E
+    from ir_eval import evaluate
+    g = rng(3 + n)
+    d = g.normal(size=(3, n))
+    d /= np.linalg.norm(d, axis=0)
+    r0 = d * g.uniform(0.5, 2.0, n)
+    v0 = g.normal(0.0, 0.3, size=(3, n))
+    bar_r, bar_v = g.normal(size=(3, n)), g.normal(size=(3, n))
+    bR0, bV0 = dev(np.zeros((3, n)), gpu), dev(np.zeros((3, n)), gpu)
+    bmu = dev(np.zeros(1), gpu)
+    hawk.run(_load(unit, "twobody_vjp_mu"), r0=dev(r0, gpu), v0=dev(v0, gpu), mu=1.3, bar_r=dev(bar_r, gpu),
+             bar_v=dev(bar_v, gpu), bar_r0=bR0, bar_v0=bV0, bar_mu=bmu)
+    want_r0, want_v0 = O.twobody_vjp(r0, v0, 1.3, bar_r, bar_v)
+    assert host(bR0).tobytes() == want_r0.tobytes() and host(bV0).tobytes() == want_v0.tobytes()
+    terms = evaluate(E.twobody_vjp_mu.program, {"r0": r0, "v0": v0, "mu": 1.3, "bar_r": bar_r, "bar_v": bar_v},
+                     n)["bar_mu"]
+    assert host(bmu)[0] == O.sample_sum(terms)
