@@ -234,14 +234,17 @@ constexpr int kFoldUnroll = 8;
 
 static_assert(kTile == 1 << kPosBits, "tile positions fill the position field");
 
-__device__ __forceinline__ unsigned wave_inclusive_scan(unsigned v) {
-    const int lane = threadIdx.x & 63;
-    unsigned x = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const unsigned y = __shfl_up(x, d, 64);
-        if (lane >= d) x += y;
-    }
+// Inclusive scan over the 64 lanes of a wave in DPP moves, no LDS: within
+// each row of 16 lanes by row shifts 1, 2, 4, 8 (a lane past the row's start
+// adds 0), then row 15's total into rows 1 and 3 and lane 31's into rows 2
+// and 3 (row broadcasts).
+__device__ __forceinline__ unsigned wave_inclusive_scan(unsigned x) {
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x111, 0xf, 0xf, false);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x112, 0xf, 0xf, false);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xf, 0xf, false);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xf, 0xf, false);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x142, 0xa, 0xf, false);   // row_bcast:15 into rows 1, 3
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x143, 0xc, 0xf, false);   // row_bcast:31 into rows 2, 3
     return x;
 }
 
@@ -284,8 +287,9 @@ __device__ int walk_sort(WalkShared& sh, int key_bits) {
         __builtin_amdgcn_wave_barrier();
         unsigned item[kWalkItems], digit[kWalkItems], rank[kWalkItems];
 #pragma unroll
+        for (int j = 0; j < kWalkItems; ++j) item[j] = in[wave * (kWalkItems * 64) + j * 64 + lane];
+#pragma unroll
         for (int j = 0; j < kWalkItems; ++j) {
-            item[j] = in[wave * (kWalkItems * 64) + j * 64 + lane];
             digit[j] = (item[j] >> shift) & dmask;
             atomicOr(&sh.peer[wave][digit[j]], me);
             __builtin_amdgcn_wave_barrier();
@@ -538,8 +542,24 @@ __global__ __launch_bounds__(256) void hawk_scatter_cells(const double* __restri
     const long long c = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     if (c >= cells) return;
     const long long words = (cells + 31) / 32;
+    constexpr int kAhead = 8;                 // chunks whose loads are in flight before their adds
     double s = 0.0;
-    for (int b = 0; b < chunks; ++b) {
+    int b = 0;
+    for (; b + kAhead <= chunks; b += kAhead) {
+        double x[kAhead];
+        bool on[kAhead];
+#pragma unroll
+        for (int q = 0; q < kAhead; ++q) {
+            on[q] = !use_seen || ((touched[(b + q) * words + (c >> 5)] >> (c & 31)) & 1u);
+            x[q] = on[q] ? parts[static_cast<long long>(b + q) * cells + c] : 0.0;
+        }
+        // an untouched partial is skipped, not added as +0.0 (the sum is never
+        // -0.0, so the two agree; skipping also keeps a NaN's payload)
+#pragma unroll
+        for (int q = 0; q < kAhead; ++q)
+            if (on[q]) s = s + x[q];
+    }
+    for (; b < chunks; ++b) {
         if (use_seen && !((touched[b * words + (c >> 5)] >> (c & 31)) & 1u)) continue;
         s = s + parts[static_cast<long long>(b) * cells + c];
     }
