@@ -28,9 +28,9 @@ constexpr int kDim = 16;
 constexpr int kElems = kDim * kDim;          // 256 elements per sample
 constexpr int kTile = 32;                    // samples per workgroup: 128-byte runs of each element row
 constexpr int kStride = kTile + 1;           // LDS row stride (floats): odd, so rows fall in different banks
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kRowStep = kThreads / kTile;   // thread t stages rows t/32 + 8r
+constexpr int kRowStep = kThreads / kTile;   // thread t stages rows t/32 + 16r
 constexpr int kMaxIn = 3;
 constexpr int kMaxOut = 2;
 constexpr int kSlices = 4;                   // K = 16 as four MFMA K-slices of 4
@@ -100,7 +100,7 @@ __device__ __forceinline__ void slice_load(const MmArgs& args, long long n, long
 // in flight during the current slice's MFMAs), then each output through LDS,
 // half at a time, and out as contiguous element rows.
 template <int NOUT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NOUT == 1 ? 4 : 3)))
+__global__ __launch_bounds__(kThreads)
 void hawk_mm16_f32(MmArgs args, long long n, long long tiles) {
     __shared__ float lds[lds_floats<NOUT>()];
     constexpr int rows = NOUT * 2 * kSlotRows / kRowStep;
