@@ -36,6 +36,9 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "samples/s + achieved HBM GB/s (% of 8 TB/s) for fwd and VJP kernels, 1 GPU"
 HBM_PEAK_GBS = 8000.0
+#: The CPU baseline repeats the step until this much wall time has passed
+#: (at least 3, at most 50 repetitions).
+CPU_SECONDS = 10.0
 FP64_PEAK_TFLOPS = 78.6
 
 
@@ -205,8 +208,9 @@ COPY_PROBE_BYTES = 1 << 30
 
 
 def _kernel_base(name: str) -> str:
+    """A kernel's name without namespace, template arguments and signature."""
     name = name.replace("(anonymous namespace)::", "")
-    return name.split("(")[0].strip()
+    return name.split("(")[0].split("<")[0].strip()
 
 
 def _pmc_pass(counter: str, config: str) -> dict:
@@ -364,13 +368,16 @@ def main() -> int:
         O.build("native")
         w["cpu"](threads)
         times = []
-        for _ in range(3):
+        begin = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - begin < CPU_SECONDS and len(times) < 50):
             t = time.perf_counter()
             w["cpu"](threads)
             times.append(time.perf_counter() - t)
         tc = statistics.median(times)
         cpu_baseline = {"value": n / tc, "unit": "samples/s", "cores": threads, "kind": "port",
-                        "sample": f"the full step ({w['name']}, N={n}) on the C oracle, median of 3 after 1 warm-up"}
+                        "sample": f"the full step ({w['name']}, N={n}) on the C oracle (native profile, "
+                                  f"{threads} threads), median of {len(times)} repetitions "
+                                  f"({sum(times):.1f} s of CPU work) after 1 warm-up"}
     line = {
         "metric": METRIC, "value": n / (ms_step * 1e-3), "unit": "samples/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
