@@ -54,8 +54,10 @@ def _write(path: Path, data: bytes) -> None:
 
 #: Per-sample plane bytes and operations at or below which a stage is a pure
 #: stream: four samples a thread keep more loads in flight (measured on
-#: MI355X: a*x+b 5.7 -> 6.4 TB/s); other stages run one sample a thread in
-#: workgroups of 128 (energy 6.4 -> 6.8 TB/s, the 6x6 SPD solve 5.1 -> 5.5).
+#: MI355X: a*x+b 5.7 -> 6.4 TB/s).  Other stages run one sample a thread:
+#: in workgroups of 128 up to 32 bytes a sample (energy 6.5 -> 6.8 TB/s) and
+#: beyond 64 (the 6x6 SPD solve 5.1 -> 5.5), of 256 in between (the energy
+#: VJP and JVP, 56 bytes: 6.2 -> 6.45).
 STREAM_BYTES, STREAM_OPS = 16, 4
 
 
@@ -75,9 +77,10 @@ def _stage_bytes(plan, mode: str) -> int:
 def launch_shape(plan, mode: str) -> tuple:
     """``(block, per_thread)`` a stage runs with when the build does not fix them."""
     from .emit_hip import fp_ops_per_sample
-    if _stage_bytes(plan, mode) <= STREAM_BYTES and fp_ops_per_sample(plan.source) <= STREAM_OPS:
+    nbytes = _stage_bytes(plan, mode)
+    if nbytes <= STREAM_BYTES and fp_ops_per_sample(plan.source) <= STREAM_OPS:
         return 256, 4
-    return 128, 1
+    return (256, 1) if 32 < nbytes <= 64 else (128, 1)
 
 
 def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64", cache_dir=None,
