@@ -427,3 +427,87 @@ def test_param_gradient_cell_on_the_device(unit, gpu, n):
     terms = evaluate(E.twobody_vjp_mu.program, {"r0": r0, "v0": v0, "mu": 1.3, "bar_r": bar_r, "bar_v": bar_v},
                      n)["bar_mu"]
     assert host(bmu)[0] == O.sample_sum(terms)
+
+
+# -- partitions and special values ------------------------------------------------
+
+@pytest.mark.parametrize("name", ["energy", "energy_vjp", "energy_jvp", "twobody", "twobody_vjp", "spd_solve",
+                                  "spd_solve_vjp"])
+def test_every_per_sample_kernel_runs_a_partition(unit, gpu, name):
+    """A run over [base, base+count) with the true n_samples writes exactly
+    that range, with the oracle's bits (one GPU's share of a sharded run,
+    reference tests/test_serial_oracle.py:203); a sentinel stays elsewhere."""
+    import hawk_amd as hawk
+    n, base, count = 20_011, 7_001, 9_973
+    g = rng(21)
+    d = g.normal(size=(3, n))
+    d /= np.linalg.norm(d, axis=0)
+    r0 = d * g.uniform(0.5, 2.0, n)
+    v3, t3, w3 = g.normal(size=(3, n)), g.normal(size=(3, n)), g.normal(size=(3, n))
+    Bm = g.normal(size=(n, 6, 6))
+    A = np.ascontiguousarray((np.matmul(Bm, Bm.transpose(0, 2, 1)) + 6.0 * np.eye(6)).transpose(1, 2, 0))
+    b6, bx = g.normal(size=(6, n)), g.normal(size=(6, n))
+    s1 = g.normal(size=n)
+    cases = {
+        "energy": ({"v": v3}, {"out": (n,)}, lambda: {"out": O.energy(v3)}),
+        "energy_vjp": ({"v": v3, "bar_out": s1}, {"bar_v": (3, n)}, lambda: {"bar_v": O.energy_vjp(v3, s1)}),
+        "energy_jvp": ({"v": v3, "dot_v": t3}, {"dot_out": (n,)}, lambda: {"dot_out": O.energy_jvp(v3, t3)}),
+        "twobody": ({"r0": r0, "v0": 0.3 * v3, "mu": 1.0}, {"r": (3, n), "v": (3, n)},
+                    lambda: dict(zip(("r", "v"), O.twobody(r0, 0.3 * v3, 1.0)))),
+        "twobody_vjp": ({"r0": r0, "v0": 0.3 * v3, "mu": 1.0, "bar_r": t3, "bar_v": w3},
+                        {"bar_r0": (3, n), "bar_v0": (3, n)},
+                        lambda: dict(zip(("bar_r0", "bar_v0"), O.twobody_vjp(r0, 0.3 * v3, 1.0, t3, w3)))),
+        "spd_solve": ({"A": A, "b": b6}, {"x": (6, n)}, lambda: {"x": O.spd_solve(A, b6)}),
+        "spd_solve_vjp": ({"A": A, "b": b6, "bar_x": bx}, {"bar_A": (6, 6, n), "bar_b": (6, n)},
+                          lambda: dict(zip(("bar_A", "bar_b"), O.spd_solve_vjp(A, b6, bx)))),
+    }
+    ins, outs, want = cases[name]
+    planes = {k: (dev(v, gpu) if isinstance(v, np.ndarray) else v) for k, v in ins.items()}
+    for k, shape in outs.items():
+        planes[k] = dev(np.full(shape, -12345.0), gpu)
+    hawk.run(_load(unit, name), base=base, count=count, **planes)
+    for k, w in want().items():
+        got = host(planes[k])
+        assert np.all(got[..., :base] == -12345.0) and np.all(got[..., base + count:] == -12345.0), k
+        assert got[..., base:base + count].tobytes() == np.ascontiguousarray(w[..., base:base + count]).tobytes(), k
+
+
+SPECIALS = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 5e-324, -5e-324, 2.2250738585072014e-308, 1e-310,
+                     -1e-310, 1.0, -1.0, 709.782712893384, 709.79, -745.13321910194122, -745.2, 710.0, -1000.0,
+                     1e300, -1e300, 3.141592653589793, 1.5707963267948966, 1e-8, 19.0615, 20.0, -20.0, 1e15,
+                     6.283185307179586e10, 0.5, 2.0, 4.0, 1e-300])
+
+
+@pytest.mark.parametrize("which", ["exp", "sin", "tanh", "sqrt"])
+def test_transcendentals_on_special_values(unit, gpu, which):
+    """The special-value corpus of reference tests/test_math_parity.py (signed
+    zeros, infinities, NaN, subnormals, overflow and underflow edges, large
+    arguments): NaN where glibc gives NaN, a zero of glibc's sign, an infinity
+    exactly, and every finite value within 4 ulp of glibc."""
+    import tempfile
+
+    import hawk_amd as hawk
+    from hawk_amd import Scalar, kernel
+    from hawk_amd import math as m
+
+    fn = {"exp": m.exp, "sin": m.sin, "tanh": m.tanh, "sqrt": m.sqrt}[which]
+
+    @kernel
+    def special(x: Scalar) -> Scalar:
+        return fn(x)
+
+    d = tempfile.mkdtemp()
+    hawk.build([special], d)
+    x = np.ascontiguousarray(SPECIALS)
+    out = dev(np.zeros_like(x), gpu)
+    hawk.run(hawk.load(d, "special"), x=dev(x, gpu), out=out)
+    got, want = host(out), O.libm(which, x)
+    for xi, g_, w_ in zip(x, got, want):
+        if np.isnan(w_):
+            assert np.isnan(g_), (which, xi, g_)
+        elif w_ == 0.0:
+            assert g_ == 0.0 and np.signbit(g_) == np.signbit(w_), (which, xi, g_, w_)
+        elif np.isinf(w_):
+            assert g_ == w_, (which, xi, g_)
+        else:
+            assert ulp_diff(np.array([g_]), np.array([w_]))[0] <= 4.0, (which, xi, g_, w_)
