@@ -227,6 +227,7 @@ constexpr unsigned kInvalid = 0x80000000u;         // a skipped (-1), bad or pad
 constexpr int kMaxKeyBits = 31 - kPosBits;         // key field: bits 12..30
 constexpr int kDigitBits = 8;
 constexpr int kDigits = 1 << kDigitBits;
+constexpr int kHistRow = kWalkWaves + 1;          // one digit's per-wave counts, padded: rows in different banks
 constexpr int kAccKeys = 4096;                     // keys whose accumulators live in LDS
 constexpr long long kSeenCells = 65536;            // a touched bitmap up to this many cells
 constexpr int kSeenWords = static_cast<int>(kSeenCells / 32);
@@ -251,7 +252,7 @@ __device__ __forceinline__ unsigned wave_inclusive_scan(unsigned x) {
 struct WalkShared {
     double vals[kTile];                               // 32 KiB: the tile's values, lane order
     unsigned ent[2][kTile];                           // 32 KiB: (key << 12) | position | invalid
-    unsigned hist[kWalkWaves][kDigits];               // 16 KiB: per-wave digit counts, then offsets
+    unsigned hist[kDigits][kHistRow];                 // 17 KiB: [digit][wave] counts, then offsets
     union {
         unsigned long long peer[kWalkWaves][kDigits]; // 32 KiB: per-wave lane masks of one digit (sort)
         double sv[kTile];                             //         the tile's values in sorted order (fold)
@@ -267,7 +268,7 @@ struct WalkShared {
 // buffer holding the result.  Wave w ranks its 256 entries w*256 + j*64 + lane
 // window by window (j = 0..3, in order): the lanes of a window holding digit d
 // find each other through one LDS OR into peer[w][d]; the lowest of them adds
-// the group's size onto hist[w][d] after all of them read it.  The exclusive
+// the group's size onto hist[d][w] after all of them read it.  The exclusive
 // scan of hist in (digit, wave) order then places every wave's group after
 // the earlier waves' groups of the same digit, so each pass keeps input order
 // within a digit.
@@ -283,7 +284,7 @@ __device__ int walk_sort(WalkShared& sh, int key_bits) {
         const int shift = kPosBits + lo;
         const unsigned* in = sh.ent[src];
         unsigned* out = sh.ent[src ^ 1];
-        for (int d = lane; d < kDigits; d += 64) sh.hist[wave][d] = 0u;
+        for (int d = lane; d < kDigits; d += 64) sh.hist[d][wave] = 0u;
         __builtin_amdgcn_wave_barrier();
         unsigned item[kWalkItems], digit[kWalkItems], rank[kWalkItems];
 #pragma unroll
@@ -296,11 +297,11 @@ __device__ int walk_sort(WalkShared& sh, int key_bits) {
             const unsigned long long peers = sh.peer[wave][digit[j]];
             const unsigned below = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(peers >> 32),
                                                              __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(peers), 0u));
-            const unsigned old = sh.hist[wave][digit[j]];
+            const unsigned old = sh.hist[digit[j]][wave];
             rank[j] = old + below;
             __builtin_amdgcn_wave_barrier();
             if (below == 0u) {
-                sh.hist[wave][digit[j]] = old + static_cast<unsigned>(__popcll(peers));
+                sh.hist[digit[j]][wave] = old + static_cast<unsigned>(__popcll(peers));
                 sh.peer[wave][digit[j]] = 0ull;
             }
             __builtin_amdgcn_wave_barrier();
@@ -309,8 +310,8 @@ __device__ int walk_sort(WalkShared& sh, int key_bits) {
         // Exclusive scan over f = digit*16 + wave: thread t owns f = 4t .. 4t+3.
         const int d = t >> 2;
         const int w0 = (t & 3) * 4;
-        const unsigned c0 = sh.hist[w0][d], c1 = sh.hist[w0 + 1][d];
-        const unsigned c2 = sh.hist[w0 + 2][d], c3 = sh.hist[w0 + 3][d];
+        const unsigned c0 = sh.hist[d][w0], c1 = sh.hist[d][w0 + 1];
+        const unsigned c2 = sh.hist[d][w0 + 2], c3 = sh.hist[d][w0 + 3];
         const unsigned mine = c0 + c1 + c2 + c3;
         const unsigned incl = wave_inclusive_scan(mine);
         if (lane == 63) sh.wsum[wave] = incl;
@@ -318,13 +319,13 @@ __device__ int walk_sort(WalkShared& sh, int key_bits) {
         unsigned before = 0u;
         for (int w = 0; w < wave; ++w) before += sh.wsum[w];
         const unsigned base = incl - mine + before;
-        sh.hist[w0][d] = base;
-        sh.hist[w0 + 1][d] = base + c0;
-        sh.hist[w0 + 2][d] = base + c0 + c1;
-        sh.hist[w0 + 3][d] = base + c0 + c1 + c2;
+        sh.hist[d][w0] = base;
+        sh.hist[d][w0 + 1] = base + c0;
+        sh.hist[d][w0 + 2] = base + c0 + c1;
+        sh.hist[d][w0 + 3] = base + c0 + c1 + c2;
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < kWalkItems; ++j) out[sh.hist[wave][digit[j]] + rank[j]] = item[j];
+        for (int j = 0; j < kWalkItems; ++j) out[sh.hist[digit[j]][wave] + rank[j]] = item[j];
         __syncthreads();
         src ^= 1;
     }
