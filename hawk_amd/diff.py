@@ -22,10 +22,10 @@ plane ``bar_x``; a tangent input is ``dot_x`` and a tangent output ``dot_y``.
 from __future__ import annotations
 
 from . import ir
-from .ir import (Assign, Decl, SampleSum, Deps, HawkError, Node, Program, fresh_placeholders, free_inputs,
-                 level_order, make, zero_like)
+from .ir import (AccumWrite, Assign, Decl, Deps, HawkError, Node, Program, SampleSum, fresh_placeholders,
+                 free_inputs, level_order, make, zero_like)
 from .trace import Kernel
-from .types import role_of
+from .types import TensorType, role_of
 
 __all__ = ["jvp", "vjp"]
 
@@ -346,6 +346,21 @@ def param_planes(kernel):
     return kernel
 
 
+def _seed(sink, seed_name: str) -> tuple:
+    """``(node, role)``: the incoming adjoint of one primal sink, as reference
+    ``hawk/diff/transform.py:989-1000`` derives it.  An assigned plane's adjoint
+    is a plane of the same shape; the reverse of a sum over samples is a
+    broadcast of the cell's adjoint (a uniform); the transpose of a keyed add
+    ``acc[key] += v`` is a gather of the cells' adjoint, ``bar_acc[key]``."""
+    t = sink.value.ttype
+    if isinstance(sink, SampleSum):
+        return ir.leaf("uniform", seed_name, t), "uniform"
+    if isinstance(sink, AccumWrite):
+        table = ir.leaf("lookup", seed_name, TensorType((), "f64"))
+        return make("gather", (table, sink.key)), "lookup"
+    return ir.leaf(role_of(t), seed_name, t), role_of(t)
+
+
 def vjp(kernel, wrt=None) -> Program:
     """The reverse-mode derivative: a program reading the primal inputs and an
     adjoint seed plane ``bar_<sink>`` per per-sample sink, and writing
@@ -357,9 +372,6 @@ def vjp(kernel, wrt=None) -> Program:
     _refuse_prior_reads(program, "vjp")
     name = _namer(program, "bar")
     targets = _differentiable_inputs(program, wrt, params=True)
-    for s in program.sinks:
-        if not isinstance(s, Assign):
-            raise HawkError(f"vjp of a kernel with {type(s).__name__} sink {s.name!r} is not in this build")
     roots = [s.value for s in program.sinks]
     leaf_nodes = {n.literal[1]: n for n in ir.leaves_of(roots)}
     target_leaves = [leaf_nodes[d.name] for d in targets if d.name in leaf_nodes]
@@ -368,9 +380,8 @@ def vjp(kernel, wrt=None) -> Program:
     seeds = []
     for s in program.sinks:
         seed_name = name(s.name)
-        t = s.value.ttype
-        seed = ir.leaf(role_of(t), seed_name, t)
-        out.decls[seed_name] = Decl(seed_name, role_of(t), t)
+        seed, role = _seed(s, seed_name)
+        out.decls[seed_name] = Decl(seed_name, role, seed.ttype)
         seeds.append((s.value, seed))
     store = rev.pullback(roots, seeds)
     for d in program.decls.values():
@@ -523,9 +534,6 @@ def jvp(kernel, wrt=None) -> Program:
     _refuse_prior_reads(program, "jvp")
     name = _namer(program, "dot")
     targets = _differentiable_inputs(program, wrt)
-    for s in program.sinks:
-        if not isinstance(s, Assign):
-            raise HawkError(f"jvp of a kernel with {type(s).__name__} sink {s.name!r} is not in this build")
     roots = [s.value for s in program.sinks]
     leaf_nodes = {n.literal[1]: n for n in ir.leaves_of(roots)}
     out = Program()
@@ -546,7 +554,15 @@ def jvp(kernel, wrt=None) -> Program:
         if tv is None:
             tv = zero_like(s.value.ttype)
         out.decls[tname] = Decl(tname, "mutable", s.value.ttype)
-        out.sinks.append(Assign(tname, tv, "mutable"))
+        # the tangent sink is the primal's kind at the same lane (reference
+        # hawk/diff/transform.py:1003-1022): a sum of tangents, or a keyed add of
+        # tangents at the primal's key under the primal's policy
+        if isinstance(s, SampleSum):
+            out.sinks.append(SampleSum(tname, tv, s.policy))
+        elif isinstance(s, AccumWrite):
+            out.sinks.append(AccumWrite(tname, tv, s.key, s.policy))
+        else:
+            out.sinks.append(Assign(tname, tv, "mutable"))
     _drop_unused_inputs(out)
     return out
 

@@ -170,8 +170,8 @@ class _Writer:
     def _leaf(self, n: Node) -> list:
         role, name = n.literal
         p = self.stage.planes[name]["var"]
-        if role == "uniform":
-            return [p]
+        if role in ("uniform", "lookup"):
+            return [p]                # a value, or a table that `gather` indexes
         if role == "mutable":         # a prior read of an output plane
             role = "per_sample" if not n.ttype.shape else ("vec_in" if len(n.ttype.shape) == 1 else "mat_in")
         dt = n.ttype.dtype
@@ -182,6 +182,15 @@ class _Writer:
             c = _flat(n.ttype.shape, e)
             out.append(self.let(dt, self.load(f"{p}[{c} * {p}_cs + hk_i]"), "in"))
         return out
+
+    def _gather(self, n: Node) -> list:
+        # one guarded read of the table (kept in cache: many samples share a
+        # cell); a key outside [0, cells), the skip key -1 included, reads 0
+        table, key = n.operands
+        p = self.value(table)[0]
+        k = self.scalar(key)
+        return [self.let(n.ttype.dtype, f"static_cast<unsigned long long>(static_cast<long long>({k})) < {p}_n"
+                                        f" ? {p}[{k}] : Real(0)", "g")]
 
     def load(self, ref: str) -> str:
         return f"__builtin_nontemporal_load(&{ref})" if self.nontemporal else ref
@@ -530,6 +539,8 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         else:
             params.append(f"ScalarHandle {var}_m")
             unpack.append(f"{cq}{elem}* __restrict__ {var} = reinterpret_cast<{cq}{elem}*>({var}_m.data);")
+            if role == "lookup":
+                unpack.append(f"const unsigned long long {var}_n = {var}_m.samples;   // cells")
     params += ["long long base", "long long count", "long long nSamples"]
     out = [
         f"// hawk gfx950 stage '{stage.name}' (generated; mode {mode}).",

@@ -110,9 +110,26 @@ def plain_total(x: Scalar, total: Mutable[Scalar]):
     total = _trace.sum(x)
 
 
+@kernel
+def add_sq(key: Index, x: Scalar, acc: Mutable[Scalar]):
+    _trace.scatter(acc, policy="ordered")[key] += x * x
+
+
+#: The VJP of a keyed add is a gather: bar_x = 2 x bar_acc[key] (reference
+#: tests/test_scatter_ordered.py:42-51).
+add_sq_grad = Kernel("add_sq_grad", diff.vjp(add_sq, wrt=("x",)))
+
+#: The chain's derivatives through all three of its sinks: the reverse reads
+#: bar_y (a plane), bar_total (a broadcast cell) and bar_bins[key] (a gather);
+#: the forward writes dot_y and adds its tangents into dot_total and dot_bins
+#: with the primal's ordered policies.
+chain_vjp = Kernel("chain_vjp", diff.vjp(chain, wrt=("x",)))
+chain_jvp = Kernel("chain_jvp", diff.jvp(chain, wrt=("x",)))
+
+
 #: Every kernel above, by name.
 ALL = {k.name: k for k in (scale, energy, energy_vjp, energy_jvp, twobody, twobody_vjp, spd_solve,
                             spd_solve_vjp, chain, ordered_total, ordered_add, sample_total, plain_total,
-                            twobody_vjp_mu)}
+                            twobody_vjp_mu, add_sq, add_sq_grad, chain_vjp, chain_jvp)}
 #: The float32 unit (built with mode="float32").
 FLOAT32 = {k.name: k for k in (mm16, mm16_vjp)}

@@ -226,6 +226,15 @@ def make(kind: str, operands: tuple, literal=None) -> Node:
             raise HawkError(f"cho_solve: a right-hand side of shape {b.ttype.shape} for a "
                             f"{f.ttype.shape[0]}x{f.ttype.shape[0]} factor (a vector is supported)")
         return Node(kind, (f, b), TensorType(b.ttype.shape, _real_dtype(b)))
+    if kind == "gather":
+        # table[key] of a 1-D plane of cells (role "lookup"); a key outside
+        # [0, cells) — the skip key -1 of hawk.scatter among them — reads 0
+        table, key = ops
+        if table.kind != "leaf" or table.literal[0] != "lookup" or table.ttype.shape:
+            raise HawkError("gather reads a scalar lookup plane (a 1-D plane of cells)")
+        if key.ttype != TensorType((), "i32"):
+            raise HawkError(f"gather: the key is an Index, got {key.ttype!r}")
+        return Node(kind, (table, key), TensorType((), table.ttype.dtype))
     raise HawkError(f"no IR kind {kind!r}")
 
 

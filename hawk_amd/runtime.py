@@ -25,6 +25,12 @@ from pathlib import Path
 from . import _contracts, _core
 from .ir import HawkError
 
+def _bound_length(role: str, x, n: int) -> int:
+    """The length a slot is bound with: its cells for a lookup plane (the
+    gather's bound), the sample count otherwise."""
+    return int(x.numel()) if role == "lookup" else n
+
+
 _PER_SAMPLE = ("per_sample", "vec_in", "mat_in", "mutable", "out", "wide_out")
 
 
@@ -118,6 +124,10 @@ class DeviceKernel:
             elif role == "accum_out":
                 if x.dim() != 1:
                     problems.append(f"{name!r} is the 1-D plane of cells hawk.scatter adds into")
+            elif role == "lookup":
+                if x.dim() != 1:
+                    problems.append(f"{name!r} is a 1-D plane of cells read at a key (the adjoint of a "
+                                    "hawk.scatter target): bind one value per cell")
         if problems:
             raise HawkError(f"kernel {self.name!r}: " + "; ".join(problems))
         if n is None:
@@ -168,7 +178,8 @@ class DeviceKernel:
             if kind in ("f64", "f32"):
                 self.block.bind_value(slot, float(x))
                 continue
-            self.block.bind(slot, x.data_ptr(), n, 1, _contracts.DEVICE_ROCM, x.device.index or 0)
+            self.block.bind(slot, x.data_ptr(), _bound_length(role, x, n), 1, _contracts.DEVICE_ROCM,
+                            x.device.index or 0)
 
     def _run(self, arrays: dict, base: int, count: int, n: int, stream: int, check: bool) -> None:
         torch = _torch()
@@ -296,7 +307,8 @@ class Prepared:
                 if kind in ("f64", "f32"):
                     self.block.bind_value(slot, float(x))
                 else:
-                    self.block.bind(slot, x.data_ptr(), self.n, 1, _contracts.DEVICE_ROCM, x.device.index or 0)
+                    self.block.bind(slot, x.data_ptr(), _bound_length(role, x, self.n), 1, _contracts.DEVICE_ROCM,
+                                    x.device.index or 0)
         self.steps = []
         self.statuses = []
         for t in kernel.team:

@@ -88,6 +88,39 @@ HKO_EXPORT void hko_chain(const double* x, double* y, int64_t base, int64_t coun
     for (int64_t i = base; i < base + count; ++i) y[i] = chain1(x[i]);
 }
 
+/* dy/dx of the chain, by the chain rule written out stage by stage (not by
+ * the derivative transform under test; pinned by central differences of
+ * chain1).  d|u|/du is +1 at u >= 0 and -1 below, as reference
+ * hawk/diff/rules.py's abs rule takes it. */
+static inline double chain1_dx(double x) {
+    const double t1 = exp(x), d1 = t1;
+    const double t2 = sin(t1), d2 = cos(t1) * d1;
+    const double t3 = (1.5 * t2) + 0.25, d3 = 1.5 * d2;
+    const double t4 = tanh(t3), d4 = (1.0 - t4 * t4) * d3;
+    const double t5 = sqrt(fabs(t4) + 1.0), d5 = (0.5 / t5) * (t4 >= 0.0 ? d4 : -d4);
+    const double t6 = (t5 * t5) - x, d6 = 2.0 * t5 * d5 - 1.0;
+    const double t7 = exp(-fabs(t6)), d7 = -t7 * (t6 >= 0.0 ? d6 : -d6);
+    return (d7 * x + t7) + d4;
+}
+
+/* The chain's derivatives through its three sinks (y per sample, the total,
+ * the bins at key): the VJP bar_x = dy/dx * (bar_y + bar_total + bar_bins[key])
+ * (a key outside [0, cells) reads 0: the scatter's skip key), and the JVP's
+ * per-sample tangent dot_y = dy/dx * dot_x (its total and bins are the ordered
+ * sum and scatter of dot_y). */
+HKO_EXPORT void hko_chain_vjp(const double* x, const int32_t* key, const double* bar_y, double bar_total,
+                              const double* bar_bins, int64_t cells, int64_t n, double* bar_x) {
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t k = key[i];
+        const double g = (bar_y[i] + bar_total) + ((k >= 0 && k < cells) ? bar_bins[k] : 0.0);
+        bar_x[i] = chain1_dx(x[i]) * g;
+    }
+}
+
+HKO_EXPORT void hko_chain_jvp(const double* x, const double* dot_x, int64_t n, double* dot_y) {
+    for (int64_t i = 0; i < n; ++i) dot_y[i] = chain1_dx(x[i]) * dot_x[i];
+}
+
 /* The transcendentals one at a time (for ULP tests of the device's). */
 HKO_EXPORT void hko_libm(int which, const double* x, double* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) {

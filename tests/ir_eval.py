@@ -108,6 +108,12 @@ class Evaluator:
         if k == "cho_solve":
             (L, info), b = self.memo[m.operands[0].uid], self._op(m, 1)
             return self._cho_solve(L, info, b)
+        if k == "gather":
+            table, key = self._op(m, 0), self._op(m, 1)
+            ok = (key >= 0) & (key < table.shape[0])
+            if table.shape[0] == 0:
+                return np.zeros(n)
+            return np.where(ok, table[np.where(ok, key, 0)], 0.0)
         if k == "loop":
             return self._loop(m)
         if k == "loop_value":
@@ -183,10 +189,11 @@ class Evaluator:
 
 def evaluate(program, env: dict, n: int) -> dict:
     """``{sink name: value}`` of the per-sample sinks of ``program``; a
-    ``hawk.sum`` sink gives its per-sample terms (the caller sums them)."""
+    ``hawk.sum`` sink gives its per-sample terms (the caller sums them), a
+    ``hawk.scatter`` sink its per-sample payloads (the caller adds them at
+    the keys)."""
     ev = Evaluator(env, n)
     out = {}
     for s in program.sinks:
-        if isinstance(s, (ir.Assign, ir.SampleSum)):
-            out[s.name] = ev.value(s.value)
+        out[s.name] = ev.value(s.value)
     return out

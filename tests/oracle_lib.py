@@ -41,6 +41,8 @@ def lib(profile: str = "portable"):
         "hko_energy_vjp": (None, [_P, _P, _I64, _P, _I64, _I64]),
         "hko_energy_jvp": (None, [_P, _P, _I64, _P, _I64, _I64]),
         "hko_chain": (None, [_P, _P, _I64, _I64]),
+        "hko_chain_vjp": (None, [_P, _P, _P, _D, _P, _I64, _I64, _P]),
+        "hko_chain_jvp": (None, [_P, _P, _I64, _P]),
         "hko_libm": (None, [ctypes.c_int, _P, _P, _I64]),
         "hko_ordered_sum": (_D, [_P, _I64]),
         "hko_row_sums": (None, [_P, _I64, _P, _P]),
@@ -106,6 +108,37 @@ def chain(x, threads: int = 1):
     else:
         lib().hko_chain(_p(x), _p(y), 0, x.size)
     return y
+
+
+def chain_vjp(x, key, bar_y, bar_total, bar_bins):
+    """bar_x of the chain through its three sinks (hand-derived dy/dx)."""
+    x, bar_y, bar_bins = (np.ascontiguousarray(a, dtype=np.float64) for a in (x, bar_y, bar_bins))
+    key = np.ascontiguousarray(key, dtype=np.int32)
+    out = np.empty_like(x)
+    lib().hko_chain_vjp(_p(x), _p(key), _p(bar_y), float(bar_total), _p(bar_bins), bar_bins.size, x.size, _p(out))
+    return out
+
+
+def chain_jvp(x, dot_x):
+    x, dot_x = (np.ascontiguousarray(a, dtype=np.float64) for a in (x, dot_x))
+    out = np.empty_like(x)
+    lib().hko_chain_jvp(_p(x), _p(dot_x), x.size, _p(out))
+    return out
+
+
+def chain_dx_scale(x):
+    """|d7 x| + |t7| + |d4|: the magnitudes of the three terms dy/dx of the
+    chain adds (numpy), the scale a rounding error of dy/dx is measured on
+    where the terms cancel."""
+    t1 = np.exp(x)
+    t2 = np.sin(t1)
+    d3 = 1.5 * np.cos(t1) * t1
+    t4 = np.tanh(1.5 * t2 + 0.25)
+    d4 = (1.0 - t4 * t4) * d3
+    t5 = np.sqrt(np.abs(t4) + 1.0)
+    d6 = 2.0 * t5 * (0.5 / t5) * np.abs(d4) + 1.0
+    t7 = np.exp(-np.abs(t5 * t5 - x))
+    return np.abs(t7 * d6 * x) + t7 + np.abs(d4)
 
 
 def libm(which: str, x):

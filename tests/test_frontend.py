@@ -318,3 +318,126 @@ def test_param_gradient_is_a_summed_cell_matching_finite_differences():
     fd = (loss(1.3 + h) - loss(1.3 - h)) / (2 * h)
     total = O.sample_sum(got["bar_mu"])
     assert abs(total - fd) <= 1e-6 * abs(fd) + 1e-8
+
+
+def _ref_case(n, cells, seed):
+    """The reference's scatter case (tests/test_scatter_ordered.py:81-87)."""
+    g = np.random.default_rng(seed)
+    key = g.integers(0, cells, n).astype(np.int32)
+    x = g.normal(size=n) * np.exp(g.normal(size=n))
+    return key, x
+
+
+def test_scatter_vjp_is_a_gather_matching_finite_differences():
+    """vjp(add_sq, wrt=x) of scatter(acc)[key] += x*x reads bar_acc at the key:
+    bar_x == 2 x bar_acc[key] (to the reference's rtol 1e-12; here bit for bit),
+    and central differences of g . acc(x) agree at 6 samples (eps 1e-6, rtol
+    1e-5, atol 1e-7), as reference tests/test_scatter_ordered.py:124-157."""
+    n, cells = 3000, 11
+    key, x = _ref_case(n, cells, seed=5)
+    g = np.random.default_rng(9).normal(size=cells)
+    prog = E.add_sq_grad.program
+    assert prog.decls["bar_acc"].role == "lookup"
+    bar = evaluate(prog, {"key": key, "x": x, "bar_acc": g}, n)["bar_x"]
+    assert bar.tobytes() == (2 * x * g[key]).tobytes()
+
+    def loss(v):
+        acc, status = O.ordered_scatter(key, v * v, np.zeros(cells))
+        assert not status[1:].any()
+        return float(g @ acc)
+    eps = 1e-6
+    for i in np.random.default_rng(2).choice(n, 6, replace=False):
+        hi, lo = x.copy(), x.copy()
+        hi[i] += eps
+        lo[i] -= eps
+        np.testing.assert_allclose((loss(hi) - loss(lo)) / (2 * eps), bar[i], rtol=1e-5, atol=1e-7)
+
+
+def test_gather_of_a_skip_or_outside_key_reads_zero():
+    n, cells = 500, 7
+    g = np.random.default_rng(3)
+    key = g.integers(-3, cells + 3, n).astype(np.int32)
+    x = g.normal(size=n)
+    table = g.normal(size=cells)
+    bar = evaluate(E.add_sq_grad.program, {"key": key, "x": x, "bar_acc": table}, n)["bar_x"]
+    inside = (key >= 0) & (key < cells)
+    assert np.all(bar[~inside] == 0.0) and (~inside).sum() > 50
+    assert bar[inside].tobytes() == (2 * x[inside] * table[key[inside]]).tobytes()
+    with pytest.raises(HawkError, match="lookup"):
+        ir.make("gather", (ir.leaf("per_sample", "t", ir.TensorType((), "f64")), ir.leaf("per_sample", "k", ir.TensorType((), "i32"))))
+
+
+def _chain_case(n, cells, seed):
+    g = np.random.default_rng(seed)
+    x = g.normal(size=n)
+    key = g.integers(-1, cells, n).astype(np.int32)          # -1: the scatter's skip key
+    return g, x, key
+
+
+def test_chain_vjp_through_all_three_sinks():
+    """vjp(chain, wrt=x): the seeds are a plane (bar_y), a broadcast cell
+    (bar_total, the reverse of a sum over samples) and a gather (bar_bins[key],
+    the transpose of a keyed add).  Within 4 ulp / 1e-13 of the oracle's
+    hand-derived bar_x, and central differences of the whole loss
+    bar_y.y + bar_total*sum(y) + bar_bins.bins(y) agree."""
+    import math
+    n, cells = 2000, 13
+    g, x, key = _chain_case(n, cells, 31)
+    bar_y, bar_bins, bar_total = g.normal(size=n), g.normal(size=cells), 0.625
+    prog = E.chain_vjp.program
+    roles = {name: d.role for name, d in prog.decls.items()}
+    assert roles["bar_y"] == "per_sample" and roles["bar_total"] == "uniform" and roles["bar_bins"] == "lookup"
+    env = {"x": x, "key": key, "bar_y": bar_y, "bar_total": bar_total, "bar_bins": bar_bins}
+    got = evaluate(prog, env, n)["bar_x"]
+    want = O.chain_vjp(x, key, bar_y, bar_total, bar_bins)
+    scale = O.chain_dx_scale(x) * (np.abs(bar_y) + abs(bar_total) + np.abs(bar_bins).max())
+    assert np.all(np.abs(got - want) <= 1e-13 * scale + 1e-300)
+
+    def loss(v):
+        y = O.chain(v)
+        bins, _ = O.ordered_scatter(key, y, np.zeros(cells))
+        return math.fsum((bar_y * y).tolist()) + bar_total * math.fsum(y.tolist()) + math.fsum((bar_bins * bins).tolist())
+    eps = 1e-6
+    for i in np.random.default_rng(4).choice(n, 8, replace=False):
+        hi, lo = x.copy(), x.copy()
+        hi[i] += eps
+        lo[i] -= eps
+        np.testing.assert_allclose((loss(hi) - loss(lo)) / (2 * eps), got[i], rtol=1e-5, atol=1e-7)
+
+
+def test_chain_jvp_keeps_the_sinks_kinds_and_policies():
+    """jvp(chain, wrt=x): dot_y per sample, dot_total an ordered sum of dot_y and
+    dot_bins an ordered keyed add of dot_y at the primal's key (reference
+    hawk/diff/transform.py:1003-1022), planned as the same two team stages
+    reading the stored dot_y."""
+    from hawk_amd.emit_hip import plan_kernel
+    prog = E.chain_jvp.program
+    kinds = {s.name: (type(s).__name__, getattr(s, "policy", None)) for s in prog.sinks}
+    assert kinds == {"dot_y": ("Assign", None), "dot_total": ("SampleSum", "ordered"),
+                     "dot_bins": ("AccumWrite", "ordered")}
+    p = plan_kernel(prog, "chain_jvp")
+    assert sorted((t["op"], t.get("u") or t.get("v")) for t in p.team) == [("ordered_scatter", "dot_y"),
+                                                                         ("ordered_sum", "dot_y")]
+    n = 3000
+    g, x, key = _chain_case(n, 5, 32)
+    dx = g.normal(size=n)
+    got = evaluate(prog, {"x": x, "key": key, "dot_x": dx}, n)
+    want = O.chain_jvp(x, dx)
+    scale = O.chain_dx_scale(x) * np.abs(dx)
+    assert np.all(np.abs(got["dot_y"] - want) <= 1e-13 * scale + 1e-300)
+    assert got["dot_total"].tobytes() == got["dot_y"].tobytes()     # the same per-sample terms
+    h = 1e-6
+    fd = (O.chain(x + h * dx) - O.chain(x - h * dx)) / (2 * h)
+    ok = np.abs(got["dot_y"] - fd) <= 1e-5 * np.abs(fd) + 1e-7
+    assert ok.mean() > 0.995                                          # central differences straddle a kink
+
+
+def test_vjp_of_a_default_sum_seeds_a_broadcast():
+    """vjp(sample_total): y = 2x and total = sum(x*x) give bar_x = 2 bar_y + 2x bar_total."""
+    prog = vjp(E.sample_total, wrt=("x",))
+    assert prog.decls["bar_total"].role == "uniform"
+    n = 400
+    g = np.random.default_rng(8)
+    x, bar_y = g.normal(size=n), g.normal(size=n)
+    got = evaluate(prog, {"x": x, "bar_y": bar_y, "bar_total": -1.25}, n)["bar_x"]
+    np.testing.assert_allclose(got, 2 * bar_y + 2 * x * -1.25, rtol=1e-15, atol=1e-15)

@@ -511,3 +511,99 @@ def test_transcendentals_on_special_values(unit, gpu, which):
             assert g_ == w_, (which, xi, g_)
         else:
             assert ulp_diff(np.array([g_]), np.array([w_]))[0] <= 4.0, (which, xi, g_, w_)
+
+
+# -- derivatives through the team sinks --------------------------------------------
+
+@pytest.mark.parametrize("n, cells, outside", [(3000, 11, False), ((1 << 22) + 5, 4096, True)])
+def test_scatter_vjp_is_a_gather_on_the_device(unit, gpu, n, cells, outside):
+    """add_sq_grad, the VJP of scatter(acc)[key] += x*x: bar_x == 2 x bar_acc[key]
+    bit for bit (the reference's bar is rtol 1e-12), a key outside [0, cells) or
+    the skip key -1 gathering 0; the prepared launcher gives the same bits; and
+    on the reference's case central differences of g . acc(x), with acc from the
+    device's ordered scatter, agree at 6 samples (reference
+    tests/test_scatter_ordered.py:124-157: eps 1e-6, rtol 1e-5, atol 1e-7)."""
+    import hawk_amd as hawk
+    g = rng(5)
+    key = g.integers(-2 if outside else 0, cells + (2 if outside else 0), n).astype(np.int32)
+    x = g.normal(size=n) * np.exp(g.normal(size=n))
+    table = rng(9).normal(size=cells)
+    print(f"add_sq_grad n={n} cells={cells}", flush=True)
+    kern = _load(unit, "add_sq_grad")
+    bar = dev(np.full(n, np.nan), gpu)
+    dkey, dx, dtab = dev(key, gpu), dev(x, gpu), dev(table, gpu)
+    hawk.run(kern, key=dkey, x=dx, bar_acc=dtab, bar_x=bar)
+    inside = (key >= 0) & (key < cells)
+    gathered = np.where(inside, table[np.where(inside, key, 0)], 0.0)
+    want = 2 * x * gathered                 # a gathered 0 keeps x's sign: (+-0) + (+-0)
+    got = host(bar)
+    assert got.tobytes() == want.tobytes()
+    if outside:
+        assert (~inside).sum() > 1000
+    bar2 = dev(np.full(n, np.nan), gpu)
+    kern.prepare(key=dkey, x=dx, bar_acc=dtab, bar_x=bar2)()
+    assert host(bar2).tobytes() == want.tobytes()
+    if outside:
+        return
+    fwd = _load(unit, "add_sq")
+
+    def loss(v):
+        acc = dev(np.zeros(cells), gpu)
+        hawk.run(fwd, key=dkey, x=dev(v, gpu), acc=acc)
+        return float(table @ host(acc))
+    eps = 1e-6
+    for i in np.random.default_rng(2).choice(n, 6, replace=False):
+        hi, lo = x.copy(), x.copy()
+        hi[i] += eps
+        lo[i] -= eps
+        np.testing.assert_allclose((loss(hi) - loss(lo)) / (2 * eps), got[i], rtol=1e-5, atol=1e-7)
+
+
+def _chain_bound(got, want, scale):
+    """The fp64 bar where dy/dx cancels: within 4 ulp / 1e-13 relative of the
+    oracle, or 1e-13 of the magnitudes of the terms that cancel."""
+    return within_contract(got, want) | (np.abs(got - want) <= 1e-13 * scale)
+
+
+@pytest.mark.parametrize("n", [1000, 262_147])
+def test_chain_vjp_on_the_device(unit, gpu, n):
+    """vjp(chain, wrt=x) on the device: bar_x within the bar of the oracle's
+    hand-derived dy/dx * (bar_y + bar_total + bar_bins[key]); keys include the
+    skip key -1 (its gather reads 0)."""
+    import hawk_amd as hawk
+    g = rng(40)
+    cells = 1 << 12
+    x = g.normal(size=n)
+    key = g.integers(-1, cells, n).astype(np.int32)
+    bar_y, bar_bins, bar_total = g.normal(size=n), g.normal(size=cells), 0.625
+    out = dev(np.full(n, np.nan), gpu)
+    print(f"chain_vjp n={n}", flush=True)
+    hawk.run(_load(unit, "chain_vjp"), x=dev(x, gpu), key=dev(key, gpu), bar_y=dev(bar_y, gpu),
+             bar_total=bar_total, bar_bins=dev(bar_bins, gpu), bar_x=out)
+    want = O.chain_vjp(x, key, bar_y, bar_total, bar_bins)
+    scale = O.chain_dx_scale(x) * (np.abs(bar_y) + abs(bar_total) + np.abs(bar_bins).max())
+    ok = _chain_bound(host(out), want, scale)
+    assert ok.all(), f"{(~ok).sum()} of {n} outside the bar"
+
+
+@pytest.mark.parametrize("n", [1000, 262_147])
+def test_chain_jvp_on_the_device(unit, gpu, n):
+    """jvp(chain, wrt=x): dot_y within the bar of the oracle's dy/dx * dot_x;
+    dot_total and dot_bins (keys with the skip key -1) bit for bit the oracle's
+    ordered sum and ordered scatter of the device's dot_y."""
+    import hawk_amd as hawk
+    g = rng(41)
+    cells = 1 << 12
+    x, dx = g.normal(size=n), g.normal(size=n)
+    key = g.integers(-1, cells, n).astype(np.int32)
+    dot_y, dot_total, dot_bins = dev(np.zeros(n), gpu), dev(np.zeros(1), gpu), dev(np.zeros(cells), gpu)
+    print(f"chain_jvp n={n}", flush=True)
+    hawk.run(_load(unit, "chain_jvp"), x=dev(x, gpu), dot_x=dev(dx, gpu), key=dev(key, gpu), dot_y=dot_y,
+             dot_total=dot_total, dot_bins=dot_bins)
+    gy = host(dot_y)
+    ok = _chain_bound(gy, O.chain_jvp(x, dx), O.chain_dx_scale(x) * np.abs(dx))
+    assert ok.all(), f"{(~ok).sum()} of {n} outside the bar"
+    assert host(dot_total)[0] == O.ordered_sum(gy)
+    want_bins, status = O.ordered_scatter(key, gy, np.zeros(cells))
+    assert not status[1:].any()
+    assert host(dot_bins).tobytes() == want_bins.tobytes()

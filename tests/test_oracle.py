@@ -341,3 +341,42 @@ def test_sample_sum_special_values():
     x[17] = np.nan
     assert np.isnan(O.sample_sum(x))
     assert O.sample_sum(np.arange(1.0, 100001.0)) == 100000 * 100001 / 2
+
+
+def _chain_kinks(x):
+    """|t4| and |t6| of the chain: where either is near 0 the chain has a kink."""
+    t4 = np.tanh(1.5 * np.sin(np.exp(x)) + 0.25)
+    t6 = (np.sqrt(np.abs(t4) + 1.0) ** 2) - x
+    return np.minimum(np.abs(t4), np.abs(t6))
+
+
+def test_chain_derivative_matches_central_differences():
+    """The oracle's hand-derived dy/dx (chain_jvp with dot_x = 1) against central
+    differences of the oracle's forward, on both sides of both kinks."""
+    g = np.random.default_rng(21)
+    x = np.concatenate([g.normal(size=4000), g.uniform(-4.0, 3.0, 4000)])
+    x = x[_chain_kinks(x) > 1e-3]
+    h = 1e-6
+    fd = (O.chain(x + h) - O.chain(x - h)) / (2 * h)
+    d = O.chain_jvp(x, np.ones_like(x))
+    assert np.all(np.abs(d - fd) <= 1e-5 * np.abs(fd) + 1e-7)
+    # both signs of t6 (the exp(-|t6|) kink) are present in the sample
+    t4 = np.tanh(1.5 * np.sin(np.exp(x)) + 0.25)
+    t6 = (np.sqrt(np.abs(t4) + 1.0) ** 2) - x
+    assert (t6 > 0).any() and (t6 < 0).any() and (t4 > 0).any() and (t4 < 0).any()
+
+
+def test_chain_vjp_gathers_the_bins_adjoint_at_the_key():
+    """bar_x = dy/dx * (bar_y + bar_total + bar_bins[key]); a key outside
+    [0, cells), the skip key -1 among them, gathers 0."""
+    g = np.random.default_rng(22)
+    n, cells = 3000, 11
+    x = g.normal(size=n)
+    key = g.integers(-1, cells + 2, n).astype(np.int32)
+    bar_y, bar_bins = g.normal(size=n), g.normal(size=cells)
+    got = O.chain_vjp(x, key, bar_y, 0.75, bar_bins)
+    d = O.chain_jvp(x, np.ones(n))
+    inside = (key >= 0) & (key < cells)
+    gathered = np.where(inside, bar_bins[np.where(inside, key, 0)], 0.0)
+    assert np.array_equal(got, d * ((bar_y + 0.75) + gathered))
+    assert (~inside).sum() > 100
