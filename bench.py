@@ -208,9 +208,11 @@ COPY_PROBE_BYTES = 1 << 30
 
 
 def _kernel_base(name: str) -> str:
-    """A kernel's name without namespace, template arguments and signature."""
+    """A kernel's name without namespace, template arguments, signature and the
+    return type a demangled template function carries ("void f<2>(...)")."""
     name = name.replace("(anonymous namespace)::", "")
-    return name.split("(")[0].split("<")[0].strip()
+    name = name.split("(")[0].split("<")[0].strip()
+    return name[len("void "):] if name.startswith("void ") else name
 
 
 def _pmc_pass(counter: str, config: str) -> dict:

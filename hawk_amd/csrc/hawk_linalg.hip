@@ -7,13 +7,17 @@
 // instead of a thread-per-sample loop.  Planes keep hawk's layout: element
 // (r, c) of sample s at (r*16 + c)*N + s.
 //
-// A workgroup takes a tile of 32 consecutive samples (each element row of the
-// tile is one contiguous 128-byte run in HBM).  The product's K = 16 runs as
-// four MFMA K-slices (v_mfma_f32_16x16x4f32): for each slice the workgroup
-// stages in LDS only the 64 operand elements of each side of each product, so
-// a workgroup needs 34 KB of LDS and four share a CU; the accumulators stay in
-// registers across slices, and the results go back through LDS and out as
-// contiguous element rows.
+// A workgroup takes a tile of consecutive samples: 64 on 1024 threads for one
+// product (each element row of the tile is a 256-byte run in HBM), 32 on 512
+// threads for two (128-byte runs; the VJP's second set of accumulators would
+// otherwise cost occupancy).  Workgroup i runs on XCD i % 8, so tiles are
+// handed out XCD by XCD in contiguous eighths: the tiles one XCD's L2 serves
+// are neighbours, which share the lines a run straddles when N*4 is not a
+// multiple of 128.  The product's K = 16 runs as four MFMA K-slices
+// (v_mfma_f32_16x16x4f32): for each slice the workgroup stages in LDS only
+// the 64 operand elements of each side of each product (33-34 KB of LDS); the
+// accumulators stay in registers across slices, and the results go back
+// through LDS and out as contiguous element rows.
 
 #include "hawk_core.h"
 #include "hawk_internal.h"
@@ -26,11 +30,6 @@ namespace {
 
 constexpr int kDim = 16;
 constexpr int kElems = kDim * kDim;          // 256 elements per sample
-constexpr int kTile = 32;                    // samples per workgroup: 128-byte runs of each element row
-constexpr int kStride = kTile + 1;           // LDS row stride (floats): odd, so rows fall in different banks
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / 64;
-constexpr int kRowStep = kThreads / kTile;   // thread t stages rows t/32 + 16r
 constexpr int kMaxIn = 3;
 constexpr int kMaxOut = 2;
 constexpr int kSlices = 4;                   // K = 16 as four MFMA K-slices of 4
@@ -61,22 +60,31 @@ __device__ __forceinline__ int rhs_elem(int lane, int q, int t) {
     return t ? j * kDim + k : k * kDim + j;
 }
 
+// The launch shape per number of products: TILE samples on THREADS threads.
+template <int NOUT> struct Shape;
+template <> struct Shape<1> { static constexpr int kTile = 64, kThreads = 1024; };
+template <> struct Shape<2> { static constexpr int kTile = 32, kThreads = 512; };
+
 // LDS (NOUT products): during the products, slot (o*2 + side)*64 + l holds,
 // for the tile's samples, the element that lane l of the MFMA reads for
 // product o's side (0 = lhs, 1 = rhs) in the current K slice; afterwards the
-// same memory holds half of one output (128 element rows) at a time.
+// same memory holds half of one output (128 element rows) at a time.  A row
+// is TILE + 1 floats: odd, so rows fall in different banks.
 constexpr int kHalfRows = kElems / 2;
 template <int NOUT>
 constexpr int lds_floats() {
-    return (NOUT * 2 * kSlotRows > kHalfRows ? NOUT * 2 * kSlotRows : kHalfRows) * kStride;
+    return (NOUT * 2 * kSlotRows > kHalfRows ? NOUT * 2 * kSlotRows : kHalfRows) * (Shape<NOUT>::kTile + 1);
 }
 
-// Load slice q of the tile into registers: thread t takes sample s0 + t % 32
-// of slots t/32 + 8r, so a wave's 64 lanes read two element rows of 32
-// consecutive samples (128 bytes each).
+// Load slice q of the tile into registers: thread t takes sample s0 + t % TILE
+// of slots t/TILE + (THREADS/TILE)*r, so every load instruction of a wave
+// reads whole runs of TILE consecutive samples of an element row.
 template <int NOUT>
 __device__ __forceinline__ void slice_load(const MmArgs& args, long long n, long long s0, int count, int q,
-                                           float (&staged)[NOUT * 2 * kSlotRows / kRowStep]) {
+                                           float (&staged)[NOUT * 2 * kSlotRows * Shape<NOUT>::kTile /
+                                                           Shape<NOUT>::kThreads]) {
+    constexpr int kTile = Shape<NOUT>::kTile;
+    constexpr int kRowStep = Shape<NOUT>::kThreads / kTile;
     const int s_own = threadIdx.x % kTile;
     const int e_own = threadIdx.x / kTile;
     const bool live = s_own < count;
@@ -96,12 +104,18 @@ __device__ __forceinline__ void slice_load(const MmArgs& args, long long n, long
     }
 }
 
-// One workgroup per tile of 32 samples: four K slices (the next slice's loads
-// in flight during the current slice's MFMAs), then each output through LDS,
-// half at a time, and out as contiguous element rows.
+// One workgroup per tile: four K slices (the next slice's loads in flight
+// during the current slice's MFMAs), then each output through LDS, half at a
+// time, and out as contiguous element rows.  The grid is 8 * ceil(tiles / 8)
+// workgroups; workgroup i takes tile (i % 8) * ceil(tiles / 8) + i / 8, and
+// one past the last tile returns.
 template <int NOUT>
-__global__ __launch_bounds__(kThreads)
+__global__ __launch_bounds__(Shape<NOUT>::kThreads)
 void hawk_mm16_f32(MmArgs args, long long n, long long tiles) {
+    constexpr int kTile = Shape<NOUT>::kTile;
+    constexpr int kStride = kTile + 1;
+    constexpr int kWaves = Shape<NOUT>::kThreads / 64;
+    constexpr int kRowStep = Shape<NOUT>::kThreads / kTile;
     __shared__ float lds[lds_floats<NOUT>()];
     constexpr int rows = NOUT * 2 * kSlotRows / kRowStep;
     const int t = threadIdx.x;
@@ -109,7 +123,8 @@ void hawk_mm16_f32(MmArgs args, long long n, long long tiles) {
     const int lane = t & 63;
     const int s_own = t % kTile;
     const int e_own = t / kTile;
-    const long long tile = blockIdx.x;
+    const long long per_xcd = (tiles + 7) / 8;
+    const long long tile = static_cast<long long>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (tile >= tiles) return;
     const long long s0 = tile * kTile;
     const int count = n - s0 < kTile ? static_cast<int>(n - s0) : kTile;
@@ -210,13 +225,15 @@ int hk_mm16_f32(const float* const* in, int n_in, float* const* out, int n_out, 
         args.out[o] = out[o];
     }
     if (n == 0) return HK_OK;
-    const long long tiles = (n + kTile - 1) / kTile;
-    if (tiles > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_mm16_f32: too many samples");
+    const int tile = n_out == 1 ? Shape<1>::kTile : Shape<2>::kTile;
+    const long long tiles = (n + tile - 1) / tile;
+    const long long grid = 8 * ((tiles + 7) / 8);     // every tile gets a workgroup on its XCD
+    if (grid > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_mm16_f32: too many samples");
     if (n_out == 1)
-        hipLaunchKernelGGL(hawk_mm16_f32<1>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
+        hipLaunchKernelGGL(hawk_mm16_f32<1>, dim3(static_cast<unsigned>(grid)), dim3(Shape<1>::kThreads), 0,
                            static_cast<hipStream_t>(stream), args, static_cast<long long>(n), tiles);
     else
-        hipLaunchKernelGGL(hawk_mm16_f32<2>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
+        hipLaunchKernelGGL(hawk_mm16_f32<2>, dim3(static_cast<unsigned>(grid)), dim3(Shape<2>::kThreads), 0,
                            static_cast<hipStream_t>(stream), args, static_cast<long long>(n), tiles);
     return launch_error("hawk_mm16_f32 launch");
 }
