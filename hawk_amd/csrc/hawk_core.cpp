@@ -488,7 +488,9 @@ int hk_launch(const hk_entry* entry, const hk_argblock* ab, int64_t base,
     if (per_thread == 0 || per_thread > 64)
         return fail(HK_EVALUE, "hk_launch: per_thread must be in [1, 64], got " + std::to_string(per_thread));
     const int64_t per_block = static_cast<int64_t>(block) * per_thread;
-    const int64_t grid = (count + per_block - 1) / per_block;
+    // a multiple of 8 workgroups, so the emitted stage can hand each XCD a
+    // contiguous eighth of the blocks (a workgroup past `count` finds no samples)
+    const int64_t grid = ((count + per_block - 1) / per_block + 7) / 8 * 8;
     if (grid > 0x7fffffffLL) return fail(HK_EVALUE, "hk_launch: " + std::to_string(grid) + " workgroups exceed the grid limit");
     return launch_impl(entry, ab, base, count, n_samples, static_cast<uint32_t>(grid), block, stream);
 }

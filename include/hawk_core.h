@@ -131,7 +131,9 @@ int hk_rebind(hk_argblock* ab, const int64_t* slots, const int64_t* ptrs,
 
 /* Launch `entry` over samples [base, base+count) of n_samples on `stream`
  * (a hipStream_t, NULL = default stream): ceil(count/(block*per_thread))
- * workgroups of `block` threads, each thread taking `per_thread` samples.
+ * workgroups of `block` threads, each thread taking `per_thread` samples,
+ * rounded up to a multiple of 8 workgroups (one per XCD in turn; a workgroup
+ * past `count` finds no samples).
  * Replaces `HostEntry.run(argblock, base, count, n_samples)` (reference
  * `src/hawk_core.cpp:438-442`); the device entry signature is
  * `(mirrors..., long long base, long long count, long long nSamples)` as
