@@ -200,10 +200,13 @@ def workload(config: str, device):
 
 
 #: The kernels a team stage launches, as rocprofv3 names them (the per-sample
-#: stage is one kernel named after the hawk kernel).
+#: stage is one kernel named after the hawk kernel).  A full stage label
+#: ("mm16#2": the VJP's two products, which share bar_C) names kernels its
+#: step launches once; a base label's kernels may serve several stages.
 STAGE_KERNELS = {"ordered_sum": ("hawk_sum_lanes", "hawk_sum_fold"),
                  "ordered_scatter": ("hawk_scatter_status", "hawk_scatter_walk", "hawk_scatter_cells"),
-                 "mm16": ("hawk_mm16_f32",)}
+                 "mm16": ("hawk_mm16_f32",),
+                 "mm16#2": ("hawk_mm16_f32_shared",)}
 COPY_PROBE_BYTES = 1 << 30
 
 
@@ -345,10 +348,14 @@ def main() -> int:
     traffic = None
     if not args.no_traffic:
         try:
-            base_label = dominant.split("#")[0]
-            occurrence = int(dominant.split("#")[1]) - 1 if "#" in dominant else 0
-            per_step = sum(1 for x in per_stage if x.split("#")[0] == base_label)
-            t = measure_traffic(args.config, STAGE_KERNELS.get(base_label, (base_label,)), occurrence, per_step)
+            if dominant in STAGE_KERNELS:
+                kernels, occurrence, per_step = STAGE_KERNELS[dominant], 0, 1
+            else:
+                base_label = dominant.split("#")[0]
+                kernels = STAGE_KERNELS.get(base_label, (base_label,))
+                occurrence = int(dominant.split("#")[1]) - 1 if "#" in dominant else 0
+                per_step = sum(1 for x in per_stage if x.split("#")[0] == base_label)
+            t = measure_traffic(args.config, kernels, occurrence, per_step)
             traffic = round(t["bytes"])
             log(f"traffic of {dominant}: {traffic / 1e6:.1f} MB per launch "
                 f"(algorithmic {d['bytes_per_sample'] * n / 1e6:.1f} MB; counter factors {t['factors']})")

@@ -46,6 +46,8 @@ struct MmArgs {
     float* out[kMaxOut];
     Product prod[kMaxOut];
     int n_in, n_out;
+    int shared;              // two products reading one plane: its index (else -1)
+    int shared_side[kMaxOut];  // the side (0 = lhs, 1 = rhs) product o reads it on
 };
 
 // The MFMA's operand fragments for K slice q: lane l holds A[i][k] with
@@ -189,6 +191,125 @@ void hawk_mm16_f32(MmArgs args, long long n, long long tiles) {
     }
 }
 
+// Two products that read one plane between them (the VJP: bar_A = bar_C B^T
+// and bar_B = A^T bar_C both read bar_C) on 32-sample tiles of 512 threads:
+// the shared plane's whole tile (256 element rows) is staged in LDS once, and
+// each K slice stages only the other operand of each product, so every input
+// element is read from HBM once.  LDS: the shared tile (33 KB, later the
+// output halves) and one slice of the two other operands (17 KB).
+constexpr int kShTile = 32, kShThreads = 512, kShStride = kShTile + 1, kShRowStep = kShThreads / kShTile;
+constexpr int kShWaves = kShThreads / 64;
+constexpr int kShFullRows = kElems / kShRowStep;          // 16 shared-tile rows per thread
+constexpr int kShSliceRows = 2 * kSlotRows / kShRowStep;  // 8 slice rows per thread
+
+// Slice q of the non-shared operands: slot row o*64 + l holds the element lane
+// l of the MFMA reads from product o's other side.
+__device__ __forceinline__ void shared_slice_load(const MmArgs& args, long long n, long long s0, int count, int q,
+                                                  float (&staged)[kShSliceRows]) {
+    const int s_own = threadIdx.x % kShTile;
+    const int e_own = threadIdx.x / kShTile;
+    const bool live = s_own < count;
+    constexpr int kRowsPerGroup = kSlotRows / kShRowStep;
+#pragma unroll
+    for (int r = 0; r < kShSliceRows; ++r) {
+        const int o = r / kRowsPerGroup;
+        const int l = e_own + (r % kRowsPerGroup) * kShRowStep;
+        const Product& pr = args.prod[o];
+        const bool other_rhs = args.shared_side[o] == 0;
+        const float* plane = args.in[other_rhs ? pr.rhs : pr.lhs];
+        const int e = other_rhs ? rhs_elem(l, q, pr.rhs_t) : lhs_elem(l, q, pr.lhs_t);
+        staged[r] = live ? __builtin_nontemporal_load(plane + static_cast<long long>(e) * n + s0 + s_own) : 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(kShThreads)
+void hawk_mm16_f32_shared(MmArgs args, long long n, long long tiles) {
+    __shared__ float full[kElems * kShStride];
+    __shared__ float slot[2 * kSlotRows * kShStride];
+    const int t = threadIdx.x;
+    const int wave = t >> 6;
+    const int lane = t & 63;
+    const int s_own = t % kShTile;
+    const int e_own = t / kShTile;
+    const long long per_xcd = (tiles + 7) / 8;
+    const long long tile = static_cast<long long>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (tile >= tiles) return;
+    const long long s0 = tile * kShTile;
+    const int count = n - s0 < kShTile ? static_cast<int>(n - s0) : kShTile;
+    const bool live = s_own < count;
+
+    const float* S = args.in[args.shared];
+    float whole[kShFullRows];
+#pragma unroll
+    for (int r = 0; r < kShFullRows; ++r)
+        whole[r] = live ? __builtin_nontemporal_load(S + static_cast<long long>(e_own + r * kShRowStep) * n + s0 + s_own)
+                        : 0.0f;
+    float staged[kShSliceRows];
+    shared_slice_load(args, n, s0, count, 0, staged);
+#pragma unroll
+    for (int r = 0; r < kShFullRows; ++r) full[(e_own + r * kShRowStep) * kShStride + s_own] = whole[r];
+
+    float4_t acc[2][kShTile / kShWaves];
+#pragma unroll
+    for (int o = 0; o < 2; ++o)
+#pragma unroll
+        for (int m = 0; m < kShTile / kShWaves; ++m) acc[o][m] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < kSlices; ++q) {
+        if (q > 0) __syncthreads();                     // the previous slice's operands are read
+#pragma unroll
+        for (int r = 0; r < kShSliceRows; ++r) slot[(e_own + r * kShRowStep) * kShStride + s_own] = staged[r];
+        __syncthreads();
+        if (q + 1 < kSlices) shared_slice_load(args, n, s0, count, q + 1, staged);
+#pragma unroll
+        for (int o = 0; o < 2; ++o) {
+            const Product& pr = args.prod[o];
+            const bool lhs_shared = args.shared_side[o] == 0;
+            const int e = lhs_shared ? lhs_elem(lane, q, pr.lhs_t) : rhs_elem(lane, q, pr.rhs_t);
+            const float* F = full + e * kShStride;
+            const float* O = slot + (o * kSlotRows + lane) * kShStride;
+#pragma unroll
+            for (int m = 0; m < kShTile / kShWaves; ++m) {
+                const int sm = wave + m * kShWaves;
+                const float fv = F[sm], ov = O[sm];
+                acc[o][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(lhs_shared ? fv : ov, lhs_shared ? ov : fv,
+                                                                 acc[o][m], 0, 0, 0);
+            }
+        }
+    }
+
+    // As hawk_mm16_f32: each output through LDS (the shared tile's memory),
+    // half at a time, and out as contiguous element rows.
+#pragma unroll
+    for (int o = 0; o < 2; ++o) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            __syncthreads();
+            if ((lane >> 5) == h) {
+#pragma unroll
+                for (int m = 0; m < kShTile / kShWaves; ++m) {
+                    const int sm = wave + m * kShWaves;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int e = (4 * (lane >> 4) + v) * kDim + (lane & 15) - h * kHalfRows;
+                        full[e * kShStride + sm] = acc[o][m][v];
+                    }
+                }
+            }
+            __syncthreads();
+            if (live) {
+                float* dst = args.out[o] + s0 + s_own;
+#pragma unroll
+                for (int r = 0; r < kHalfRows / kShRowStep; ++r) {
+                    const int e = e_own + r * kShRowStep;
+                    __builtin_nontemporal_store(full[e * kShStride + s_own],
+                                                dst + static_cast<long long>(e + h * kHalfRows) * n);
+                }
+            }
+        }
+    }
+}
+
 int launch_error(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hawk_internal::set_hip_error(what, e);
@@ -224,7 +345,28 @@ int hk_mm16_f32(const float* const* in, int n_in, float* const* out, int n_out, 
         args.prod[o] = pr;
         args.out[o] = out[o];
     }
+    // Two products that share exactly one plane, each reading it on one side,
+    // take the kernel that stages it once.
+    args.shared = -1;
+    if (n_out == 2 && args.prod[0].lhs != args.prod[0].rhs && args.prod[1].lhs != args.prod[1].rhs) {
+        for (int side = 0; side < 2 && args.shared < 0; ++side) {
+            const int cand = side == 0 ? args.prod[0].lhs : args.prod[0].rhs;
+            if (cand == args.prod[1].lhs || cand == args.prod[1].rhs) {
+                args.shared = cand;
+                args.shared_side[0] = side;
+                args.shared_side[1] = cand == args.prod[1].lhs ? 0 : 1;
+            }
+        }
+    }
     if (n == 0) return HK_OK;
+    if (args.shared >= 0) {
+        const long long tiles = (n + kShTile - 1) / kShTile;
+        const long long grid = 8 * ((tiles + 7) / 8);
+        if (grid > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_mm16_f32: too many samples");
+        hipLaunchKernelGGL(hawk_mm16_f32_shared, dim3(static_cast<unsigned>(grid)), dim3(kShThreads), 0,
+                           static_cast<hipStream_t>(stream), args, static_cast<long long>(n), tiles);
+        return launch_error("hawk_mm16_f32_shared launch");
+    }
     const int tile = n_out == 1 ? Shape<1>::kTile : Shape<2>::kTile;
     const long long tiles = (n + tile - 1) / tile;
     const long long grid = 8 * ((tiles + 7) / 8);     // every tile gets a workgroup on its XCD
