@@ -141,7 +141,10 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
                 "cache_key": key, "compile_options": list(_compile.RTC_OPTIONS),
                 "toolchain": _compile.toolchain(),
                 "resources": kernel_resources(code).get(k.name, {}),
-                "fp_ops_per_sample": fp_ops_per_sample(plan.source),
+                # the program's ops as traced (the algorithmic count), and what
+                # the emitted stage executes after carried reuse
+                "fp_ops_per_sample": plan.algorithmic_ops,
+                "fp_ops_emitted": fp_ops_per_sample(plan.source),
             })
         _write(directory / f"{k.name}.json", json.dumps(sidecar, indent=1, sort_keys=True).encode())
         artifacts.append(Artifact(k.name, sidecar))

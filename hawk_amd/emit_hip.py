@@ -27,6 +27,7 @@ from __future__ import annotations
 import re
 
 import math
+import dataclasses
 from dataclasses import dataclass, field
 
 from . import ir
@@ -693,6 +694,7 @@ class Plan:
     source: str | None
     team: list                      # [{"op": ..., planes...}]
     planes: dict                    # every plane a caller binds: name -> {"role", "shape", "dtype"}
+    algorithmic_ops: int = 0        # FP ops per sample of the program as traced (before carried reuse)
 
 
 def _mm16_products(program: Program):
@@ -728,12 +730,39 @@ def _mm16_products(program: Program):
     return ins, prods
 
 
+def _carry_repeats(program: Program) -> Program:
+    """``program`` with :func:`ir.carry_repeats` applied to its sinks' values
+    (one pass over all of them, so values the sinks share stay shared)."""
+    roots = [s.value for s in program.sinks]
+    keys = [s.key for s in program.sinks if isinstance(s, AccumWrite)]
+    new = ir.carry_repeats(roots + keys)
+    if all(a is b for a, b in zip(new, roots + keys)):
+        return program
+    values, new_keys = iter(new[:len(roots)]), iter(new[len(roots):])
+    sinks = []
+    for s in program.sinks:
+        if isinstance(s, AccumWrite):
+            sinks.append(dataclasses.replace(s, value=next(values), key=next(new_keys)))
+        else:
+            sinks.append(dataclasses.replace(s, value=next(values)))
+    return Program(program.decls, sinks)
+
+
 def plan_kernel(program: Program, name: str, mode: str = "float64", block: int = 256,
-                per_thread: int = 1, nontemporal: bool = False) -> Plan:
+                per_thread: int = 1, nontemporal: bool = False, reuse_carries: bool = True) -> Plan:
     """Split ``program`` into its per-sample stage and team stages, and render
-    the per-sample stage."""
+    the per-sample stage.  With ``reuse_carries``, a loop's value that its next
+    iteration would compute again is carried instead (:func:`ir.carry_repeats`);
+    ``Plan.algorithmic_ops`` still counts the program as traced."""
     if mode not in ("float64", "float32"):
         raise HawkError(f"mode={mode!r}: the hip target builds 'float64' or 'float32'")
+    if reuse_carries:
+        reused = _carry_repeats(program)
+        if reused is not program:
+            traced = plan_kernel(program, name, mode, block, per_thread, nontemporal, reuse_carries=False)
+            plan = plan_kernel(reused, name, mode, block, per_thread, nontemporal, reuse_carries=False)
+            plan.algorithmic_ops = traced.algorithmic_ops
+            return plan
     products = _mm16_products(program) if mode == "float32" else None
     if products is not None:
         ins, prods = products
@@ -795,4 +824,4 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
     for pname, info in planes.items():
         if pname.startswith("hk_"):
             info["scratch"] = True
-    return Plan(stage, source, team, planes)
+    return Plan(stage, source, team, planes, fp_ops_per_sample(source) if source else 0)

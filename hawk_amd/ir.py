@@ -520,6 +520,140 @@ def substitute(roots, mapping: dict) -> list:
     return [memo.get(r.uid, r) for r in roots]
 
 
+#: Kinds whose presence makes a repeated subexpression worth a carried slot.
+_COSTLY = frozenset(("sqrt", "div", "exp", "sin", "cos", "tanh", "log", "norm", "chol", "cho_solve"))
+
+
+def _literal_key(lit):
+    try:
+        hash(lit)
+        return lit
+    except TypeError:
+        return repr(lit)
+
+
+def _carry_repeats_of(loop: Node, deps: Deps):
+    """The loop with each costly body value that the next iteration would
+    compute again carried instead, or ``None`` if there is none.
+
+    A body node X that reads the carries (and not the loop index) is computed
+    again by iteration k+1 exactly when the body also computes Y = X with every
+    carry replaced by its next value: the same operations on the values that
+    become iteration k+1's carries.  X then becomes a carried slot, initialised
+    by X over the inits and advanced by Y, so iteration k+1 reads the value
+    iteration k computed.  The bits do not change: every value is produced by
+    the same operations, in the same order, from the same operands (the kernel
+    is compiled without contraction)."""
+    info = loop.literal
+    key_of = info.index.uid
+    deps.register(loop)
+    carry_slot = {c.uid: j for j, c in enumerate(info.carries)}
+    body = [m for m in topo(info.nexts) if key_of in deps.of(m)]
+    if any(m.kind in ("loop", "loop_value", "tape_read") for m in body):
+        return None                           # innermost loops without tapes only
+    outside: dict = {}
+
+    def ext(n: Node):
+        # a value the body reads from outside the loop, keyed by structure so
+        # that two equal computations (two `-mu` nodes) are one key
+        hit = outside.get(n.uid)
+        if hit is None:
+            for m in topo([n]):
+                if m.uid not in outside:
+                    if m.kind in ("loop", "carry", "loop_index", "loop_value", "tape_read"):
+                        outside[m.uid] = ("x", m.uid)
+                    else:
+                        outside[m.uid] = ("x", m.kind, _literal_key(m.literal), m.ttype,
+                                          tuple(outside[o.uid] for o in m.operands))
+            hit = outside[n.uid]
+        return hit
+
+    keys: dict = {}
+    shifted: dict = {}
+    costly: dict = {}
+    for m in body:
+        if m.uid in carry_slot:
+            keys[m.uid] = ("c", carry_slot[m.uid])
+            shifted[m.uid] = None             # filled below, once every next has a key
+            costly[m.uid] = False
+            continue
+        if m is info.index:
+            keys[m.uid] = ("i",)
+            costly[m.uid] = False
+            continue
+        ops = []
+        for o in m.operands:
+            ops.append(keys[o.uid] if o.uid in keys else ext(o))
+        keys[m.uid] = (m.kind, _literal_key(m.literal), m.ttype, tuple(ops))
+        costly[m.uid] = m.kind in _COSTLY or any(costly.get(o.uid, False) for o in m.operands)
+    for c in info.carries:
+        x = info.nexts[carry_slot[c.uid]]
+        shifted[c.uid] = keys[x.uid] if x.uid in keys else ext(x)
+    by_key = {}
+    for m in body:
+        by_key.setdefault(keys[m.uid], m)
+    for m in body:
+        if m.uid in shifted or m is info.index:
+            continue
+        ops = []
+        for o in m.operands:
+            if o is info.index or (o.uid in keys and shifted.get(o.uid, 0) is None):
+                ops = None
+                break
+            ops.append(shifted[o.uid] if o.uid in shifted else ext(o))
+        shifted[m.uid] = None if ops is None else (m.kind, _literal_key(m.literal), m.ttype, tuple(ops))
+    found = {}
+    for m in body:
+        if m.uid in carry_slot or m is info.index or not costly[m.uid]:
+            continue
+        s = shifted.get(m.uid)
+        y = by_key.get(s) if s is not None else None
+        if y is not None and y is not m:
+            found[m.uid] = (m, y)
+    if not found:
+        return None
+    users: dict = {}
+    for m in body:
+        for o in m.operands:
+            users.setdefault(o.uid, set()).add(m.uid)
+    roots = {x.uid for x in info.nexts}
+    chosen = [(x, y) for u, (x, y) in found.items()
+              if u in roots or any(v not in found for v in users.get(u, ()))]
+    if not chosen:
+        return None
+    slot0 = len(info.carries)
+    places = tuple(Node("carry", (), x.ttype, (loop.uid, slot0 + i)) for i, (x, _) in enumerate(chosen))
+    to_init = {c.uid: init for c, init in zip(info.carries, loop.operands)}
+    inits = tuple(substitute([x for x, _ in chosen], to_init))
+    body_map = {x.uid: p for (x, _), p in zip(chosen, places)}
+    new_nexts = substitute(list(info.nexts) + [y for _, y in chosen], body_map)
+    copy = loop_node(loop.uid, info.trip, info.start, info.step, info.index, info.carries + places,
+                     tuple(loop.operands) + inits, tuple(new_nexts),
+                     tuple(info.names) + tuple(f"hk_reuse{i}" for i in range(len(places))))
+    copy.literal.unroll = info.unroll
+    return copy
+
+
+def carry_repeats(roots) -> list:
+    """``roots`` with :func:`_carry_repeats_of` applied to every innermost loop
+    that no tape reads (the two-body leapfrog's closing half-kick acceleration
+    is the next substep's opening one)."""
+    nodes = topo(roots)
+    loops = [n for n in nodes if n.kind == "loop"]
+    if not loops:
+        return list(roots)
+    taped = {n.operands[0].uid for n in nodes if n.kind == "tape_read"}
+    deps = Deps()
+    mapping = {}
+    for lp in loops:
+        if lp.uid in taped:
+            continue
+        copy = _carry_repeats_of(lp, deps)
+        if copy is not None:
+            mapping[lp.uid] = copy
+    return substitute(roots, mapping) if mapping else list(roots)
+
+
 def arg_spec(program: Program, used: set) -> list:
     """``[(role, name)]`` of the planes a kernel binds, in :data:`ROLE_ORDER`,
     declaration order within a role; ``used`` holds the names the body reads

@@ -250,18 +250,19 @@ def test_checkpointed_reverse_keeps_the_bits():
 
 
 def test_fp_op_count_of_the_emitted_stages():
-    """The sidecar's per-sample operation count is read off the emitted code:
-    scale is a*x+b (2), energy 0.5*((v0*v0+v1*v1)+v2*v2) (6), the chain's eight
-    stages 14 (exp, sin, 2, tanh, 3, 2, exp+fabs, 2), and a 32-substep loop body
-    counts 32 times."""
+    """The sidecar's per-sample operation count is read off the code emitted
+    for the program as traced: scale is a*x+b (2), energy
+    0.5*((v0*v0+v1*v1)+v2*v2) (6), the chain's eight stages 14 (exp, sin, 2,
+    tanh, 3, 2, exp+fabs, 2), and the two-body loop body (two force
+    evaluations, 40 ops) counts 32 times."""
     from hawk_amd import emit_hip
 
     def count(k):
-        return emit_hip.fp_ops_per_sample(emit_hip.plan_kernel(k.program, k.name, "float64", 256, 1, True).source)
+        return emit_hip.plan_kernel(k.program, k.name, "float64", 256, 1, True).algorithmic_ops
     assert count(E.scale) == 2
     assert count(E.energy) == 6
     assert count(E.chain) == 14
-    assert count(E.twobody) % 32 == 0 and count(E.twobody) // 32 >= 30
+    assert count(E.twobody) == 40 * 32
 
 
 def test_mm16_and_its_vjp_are_one_mfma_team_stage(tmp_path):
@@ -441,3 +442,44 @@ def test_vjp_of_a_default_sum_seeds_a_broadcast():
     x, bar_y = g.normal(size=n), g.normal(size=n)
     got = evaluate(prog, {"x": x, "bar_y": bar_y, "bar_total": -1.25}, n)["bar_x"]
     np.testing.assert_allclose(got, 2 * bar_y + 2 * x * -1.25, rtol=1e-15, atol=1e-15)
+
+
+def test_carried_reuse_keeps_the_bits_and_halves_the_leapfrog_force_evaluations():
+    """The leapfrog's closing half-kick evaluates a(r') and the next substep's
+    opening half-kick a(r') again; the emitter carries the first instead
+    (ir.carry_repeats).  The program computes the same bits (the numpy
+    interpreter, bit for bit), the loop body holds one sqrt and one division
+    instead of two, and the sidecar's algorithmic count is still the traced
+    program's."""
+    from hawk_amd.emit_hip import _carry_repeats, fp_ops_per_sample, plan_kernel
+    n = 300
+    g = np.random.default_rng(12)
+    d = g.normal(size=(3, n))
+    d /= np.linalg.norm(d, axis=0)
+    env = {"r0": d * g.uniform(0.5, 2.0, n), "v0": g.normal(0.0, 0.3, size=(3, n)), "mu": 1.1,
+           "bar_r": g.normal(size=(3, n)), "bar_v": g.normal(size=(3, n))}
+    for k in (E.twobody, E.twobody_vjp):
+        reused = _carry_repeats(k.program)
+        assert reused is not k.program
+        a, b = evaluate(k.program, env, n), evaluate(reused, env, n)
+        assert all(a[x].tobytes() == b[x].tobytes() for x in a), k.name
+    p = plan_kernel(E.twobody.program, "twobody")
+    body = p.source[p.source.index("for (long long hk_k"):]
+    assert body.count("sqrt(") == 1 and body.count(" / ") == 1
+    assert p.algorithmic_ops == 1280 and fp_ops_per_sample(p.source) < 900
+    plain = plan_kernel(E.twobody.program, "twobody", reuse_carries=False)
+    assert plain.algorithmic_ops == 1280 and plain.source.count("sqrt(") == 2
+
+
+def test_carried_reuse_leaves_a_value_that_reads_the_index_alone():
+    """x_{k+1} = x_k + sqrt(x_k + k): sqrt(x + k) of the next iteration reads a
+    different index, so nothing is carried."""
+    from hawk_amd.emit_hip import _carry_repeats
+
+    @hawk.kernel
+    def walk(x: Scalar, y: Mutable[Scalar]):
+        acc = x
+        for k in range(8):
+            acc = acc + sqrt(acc + k)
+        y = acc
+    assert _carry_repeats(walk.program) is walk.program
