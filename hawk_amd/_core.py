@@ -60,6 +60,8 @@ def _declare(lib) -> None:
         "hk_ordered_scatter_f64": (I, [V, V, I64, V, I64, V, V, V]),
         "hk_rows_finish_scratch_bytes": (SZ, [I64]),
         "hk_rows_finish_f64": (I, [V, V, I64, V, V, V]),
+        "hk_keyed_ordered_sum_scratch_bytes": (SZ, [I64, I64]),
+        "hk_keyed_ordered_sum_f64": (I, [V, I64, I64, V, V, V]),
         "hk_mm16_f32": (I, [ctypes.POINTER(V), I, ctypes.POINTER(V), I, ctypes.POINTER(ctypes.c_int32), I64, V]),
     }
     for name, (res, args) in sig.items():
@@ -305,6 +307,16 @@ def mm16(ins: list, outs: list, products: list, n: int, stream: int = 0) -> None
     c_out = (ctypes.c_void_p * len(outs))(*[ctypes.c_void_p(p) for p in outs])
     c_prod = (ctypes.c_int32 * len(flat))(*flat)
     check(lib().hk_mm16_f32(c_in, len(ins), c_out, len(outs), c_prod, int(n), ctypes.c_void_p(stream or None)))
+
+
+def keyed_ordered_sum_scratch_bytes(n: int, group: int) -> int:
+    return int(lib().hk_keyed_ordered_sum_scratch_bytes(int(n), int(group)))
+
+
+def keyed_ordered_sum(u: int, n: int, group: int, out: int, scratch: int, stream: int = 0) -> None:
+    """``out[k]`` = key k's ``group`` rows by the ordered sum's tree, k < n / group."""
+    check(lib().hk_keyed_ordered_sum_f64(ctypes.c_void_p(u or None), int(n), int(group), ctypes.c_void_p(out),
+                                         ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
 
 
 def rows_finish_scratch_bytes(rows: int) -> int:

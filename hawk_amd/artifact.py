@@ -125,6 +125,7 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
             "kernel": k.name, "target": "hip", "offload_arch": "gfx950", "mode": mode,
             "scalar_type": mode, "planes": plan.planes, "team": plan.team,
             "launch": {"block": shape[0], "per_thread": shape[1], "nontemporal": nontemporal},
+            "grid": [list(a) for a in k.program.grid.axes] if k.program.grid is not None else None,
             "entry": None, "arg_spec": [], "descriptor": [],
         }
         if plan.stage is not None:

@@ -201,6 +201,72 @@ __global__ __launch_bounds__(256) void hawk_rows_levels(double* __restrict__ buf
 }
 
 // ---------------------------------------------------------------------------
+// Keyed fixed-tree sum: hawk.sum(x, over=<trailing lane axes>, policy=
+// "ordered").  Key k's rows are the `group` consecutive values
+// u[k*group .. (k+1)*group), and each key takes the ordered sum's tree
+// (reference hawk/emit/team.py:115-205 with its gp stage): virtual lane l of
+// 65536 adds rows l, l + 65536, ... from +0.0, groups of 1024 lanes fold by
+// the halving tree, then the 64 group values by the same tree.
+//
+// Only the first lv = min(group, 65536) lanes of a key can hold rows; the
+// others are +0.0, and so are the groups past ceil(lv / 1024).  No lane value
+// or tree sum is ever -0.0 (each starts at +0.0; a round-to-nearest sum is
+// -0.0 only from two -0.0 operands), so adding +0.0 is the identity and the
+// trees need only their first P = min(1024, 2^ceil(log2 lv)) lanes and first
+// Q = 2^ceil(log2 groups) group values: the bits of the full trees.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void hawk_keyed_lanes(const double* __restrict__ u, long long group, long long lv,
+                                                        long long total, double* __restrict__ lanes) {
+    for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < total;
+         i += static_cast<long long>(gridDim.x) * 256) {
+        const long long k = i / lv, l = i - k * lv;
+        const double* row = u + k * group;
+        double part = 0.0;
+        for (long long r = l; r < group; r += kVirtualLanes) part = part + __builtin_nontemporal_load(row + r);
+        lanes[i] = part;
+    }
+}
+
+__device__ __forceinline__ int pow2_at_least(long long x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+// One workgroup per key: the used groups' halving trees, then the group values' tree.
+__global__ __launch_bounds__(256) void hawk_keyed_fold(const double* __restrict__ lanes, long long lv,
+                                                       double* __restrict__ out) {
+    __shared__ double sh[kFoldLanes];
+    __shared__ double gp[kGroups];
+    const long long k = blockIdx.x;
+    const int t = threadIdx.x;
+    const int used = static_cast<int>((lv + kFoldLanes - 1) / kFoldLanes);     // <= 64
+    const int width = lv >= kFoldLanes ? kFoldLanes : pow2_at_least(lv);
+    const double* mine = lanes + k * lv;
+    for (int g = 0; g < used; ++g) {
+        for (int i = t; i < width; i += 256) {
+            const long long at = static_cast<long long>(g) * kFoldLanes + i;
+            sh[i] = at < lv ? mine[at] : 0.0;
+        }
+        __syncthreads();
+        for (int w = width / 2; w > 0; w >>= 1) {
+            for (int i = t; i < w; i += 256) sh[i] = sh[i] + sh[i + w];
+            __syncthreads();
+        }
+        if (t == 0) gp[g] = sh[0];
+        __syncthreads();
+    }
+    const int q = pow2_at_least(used);
+    for (int i = used + t; i < q; i += 256) gp[i] = 0.0;
+    __syncthreads();
+    for (int w = q / 2; w > 0; w >>= 1) {
+        if (t < w) gp[t] = gp[t] + gp[t + w];
+        __syncthreads();
+    }
+    if (t == 0) out[k] = gp[0];
+}
+
+// ---------------------------------------------------------------------------
 // Keyed ordered scatter.
 //
 // parts[b][k] is the in-lane-order sum (from +0.0) of chunk b's values with
@@ -612,6 +678,39 @@ int hk_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch, v
     int rc = launch_error("hawk_sum_lanes launch");
     if (rc != HK_OK) return rc;
     return hk_ordered_fold_f64(lanes, out, scratch, stream);
+}
+
+size_t hk_keyed_ordered_sum_scratch_bytes(int64_t n, int64_t group) {
+    if (n <= 0 || group <= 0 || n % group != 0) return 0;
+    if (n == group) return kSumScratch;
+    const long long lv = group < kVirtualLanes ? group : kVirtualLanes;
+    return sizeof(double) * static_cast<size_t>(n / group) * static_cast<size_t>(lv) + 256;
+}
+
+int hk_keyed_ordered_sum_f64(const double* u, int64_t n, int64_t group, double* out, void* scratch, void* stream) {
+    if (n < 0 || group <= 0)
+        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_ordered_sum_f64: n must be >= 0 and group >= 1");
+    if (n % group != 0)
+        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_ordered_sum_f64: n (" + std::to_string(n) +
+                                                       ") is not a whole number of groups of " + std::to_string(group));
+    if (n == 0) return HK_OK;
+    if (!u || !out || !scratch)
+        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_ordered_sum_f64: u, out and scratch are required");
+    if (n == group) return hk_ordered_sum_f64(u, n, out, scratch, stream);    // one key: the ordered sum
+    const long long keys = n / group;
+    if (keys > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_ordered_sum_f64: too many keys");
+    const long long lv = group < kVirtualLanes ? group : kVirtualLanes;
+    const long long total = keys * lv;
+    auto* lanes = static_cast<double*>(scratch);
+    long long blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(hawk_keyed_lanes, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), u, static_cast<long long>(group), lv, total, lanes);
+    int rc = launch_error("hawk_keyed_lanes launch");
+    if (rc != HK_OK) return rc;
+    hipLaunchKernelGGL(hawk_keyed_fold, dim3(static_cast<unsigned>(keys)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), lanes, lv, out);
+    return launch_error("hawk_keyed_fold launch");
 }
 
 size_t hk_rows_finish_scratch_bytes(int64_t rows) {

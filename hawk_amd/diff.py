@@ -87,7 +87,7 @@ _UNARY_D = {
     "tanh": lambda n, x: _o("sub", _c(1.0), _o("mul", n, n)),
 }
 
-_TERMINAL = ("leaf", "const", "iconst", "loop_index", "carry", "tape_read")
+_TERMINAL = ("leaf", "const", "iconst", "loop_index", "carry", "tape_read", "lane_axis", "gather")
 _NO_DERIVATIVE = ("lt", "le", "gt", "ge", "eq", "ne", "chol_info", "real")
 
 
@@ -353,6 +353,11 @@ def _seed(sink, seed_name: str) -> tuple:
     broadcast of the cell's adjoint (a uniform); the transpose of a keyed add
     ``acc[key] += v`` is a gather of the cells' adjoint, ``bar_acc[key]``."""
     t = sink.value.ttype
+    if isinstance(sink, SampleSum) and sink.group is not None:
+        # a sum over the trailing lane axes: each lane reads its key's adjoint
+        # (key = flat lane // group), a gather from a plane of keys
+        table = ir.leaf("lookup", seed_name, TensorType((), "f64"))
+        return make("gather", (table, make("lane_axis", (), (sink.group, None)))), "lookup"
     if isinstance(sink, SampleSum):
         return ir.leaf("uniform", seed_name, t), "uniform"
     if isinstance(sink, AccumWrite):
@@ -376,7 +381,7 @@ def vjp(kernel, wrt=None) -> Program:
     leaf_nodes = {n.literal[1]: n for n in ir.leaves_of(roots)}
     target_leaves = [leaf_nodes[d.name] for d in targets if d.name in leaf_nodes]
     rev = _Reverse({n.uid for n in target_leaves})
-    out = Program()
+    out = Program(grid=program.grid)
     seeds = []
     for s in program.sinks:
         seed_name = name(s.name)
@@ -536,7 +541,7 @@ def jvp(kernel, wrt=None) -> Program:
     targets = _differentiable_inputs(program, wrt)
     roots = [s.value for s in program.sinks]
     leaf_nodes = {n.literal[1]: n for n in ir.leaves_of(roots)}
-    out = Program()
+    out = Program(grid=program.grid)
     for d in program.decls.values():
         if d.role in ("per_sample", "vec_in", "mat_in", "uniform"):
             out.decls.setdefault(d.name, d)
@@ -558,7 +563,7 @@ def jvp(kernel, wrt=None) -> Program:
         # hawk/diff/transform.py:1003-1022): a sum of tangents, or a keyed add of
         # tangents at the primal's key under the primal's policy
         if isinstance(s, SampleSum):
-            out.sinks.append(SampleSum(tname, tv, s.policy))
+            out.sinks.append(SampleSum(tname, tv, s.policy, s.group))
         elif isinstance(s, AccumWrite):
             out.sinks.append(AccumWrite(tname, tv, s.key, s.policy))
         else:

@@ -184,6 +184,13 @@ class _Writer:
             out.append(self.let(dt, self.load(f"{p}[{c} * {p}_cs + hk_i]"), "in"))
         return out
 
+    def _lane_axis(self, n: Node) -> list:
+        div, mod = n.literal
+        if mod == 0:
+            return ["hk_i"]                                  # the flat lane index
+        q = "hk_i" if div == 1 else f"(hk_i / {div}LL)"
+        return [self.let("i32", f"static_cast<int>({q})" if mod is None else f"static_cast<int>({q} % {mod}LL)", "ax")]
+
     def _gather(self, n: Node) -> list:
         # one guarded read of the table (kept in cache: many samples share a
         # cell); a key outside [0, cells), the skip key -1 included, reads 0
@@ -471,7 +478,7 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
     for _, _, hi, comp in rows:
         for pname in (hi, comp):
             decls[pname] = ir.Decl(pname, "rows_out", ir.TensorType((), "f64"))
-    prog2 = Program(decls, program.sinks)
+    prog2 = Program(decls, program.sinks, program.grid)
     spec = ir.arg_spec(prog2, used)
     for role, name in spec:
         d = decls[name]
@@ -745,7 +752,7 @@ def _carry_repeats(program: Program) -> Program:
             sinks.append(dataclasses.replace(s, value=next(values), key=next(new_keys)))
         else:
             sinks.append(dataclasses.replace(s, value=next(values)))
-    return Program(program.decls, sinks)
+    return Program(program.decls, sinks, program.grid)
 
 
 def plan_kernel(program: Program, name: str, mode: str = "float64", block: int = 256,
@@ -788,7 +795,10 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
             if src is None:
                 src = f"hk_sum_{s.name}"
                 extra.append((src, s.value))
-            team.append({"op": "ordered_sum", "u": src, "out": s.name})
+            if s.group is None:
+                team.append({"op": "ordered_sum", "u": src, "out": s.name})
+            else:
+                team.append({"op": "keyed_sum", "u": src, "out": s.name, "group": s.group})
         elif isinstance(s, AccumWrite):
             if mode != "float64":
                 raise HawkError("hawk.scatter(policy='ordered') on the hip target is built in float64")
@@ -819,8 +829,10 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
         for key in ("out", "target"):
             pname = t.get(key)
             if pname and isinstance(pname, str):
-                planes[pname] = {"role": "cell" if t["op"] in ("ordered_sum", "row_sum") else "accum_out",
+                planes[pname] = {"role": "cell" if t["op"] in ("ordered_sum", "row_sum", "keyed_sum") else "accum_out",
                                  "shape": [], "dtype": "f64"}
+                if t["op"] == "keyed_sum":
+                    planes[pname]["group"] = t["group"]       # one cell per `group` samples
     for pname, info in planes.items():
         if pname.startswith("hk_"):
             info["scratch"] = True

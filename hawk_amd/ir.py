@@ -18,11 +18,7 @@ from __future__ import annotations
 import itertools
 from dataclasses import dataclass, field
 
-from .types import TensorType
-
-
-class HawkError(Exception):
-    """Every refusal of the authoring surface, the compiler and the runtime."""
+from .types import HawkError, TensorType   # noqa: F401 - HawkError is re-exported
 
 
 #: Canonical role order of ``arg_spec`` == the entry-signature order
@@ -226,6 +222,13 @@ def make(kind: str, operands: tuple, literal=None) -> Node:
             raise HawkError(f"cho_solve: a right-hand side of shape {b.ttype.shape} for a "
                             f"{f.ttype.shape[0]}x{f.ttype.shape[0]} factor (a vector is supported)")
         return Node(kind, (f, b), TensorType(b.ttype.shape, _real_dtype(b)))
+    if kind == "lane_axis":
+        # a coordinate of the lane on its Grid: (sample // div) % mod (no mod
+        # for the first axis), an Index; mod == 0 and div == 1 is the flat index
+        div, mod = literal
+        if mod == 0:
+            return Node(kind, (), TensorType((), "i64"), (1, 0))
+        return Node(kind, (), TensorType((), "i32"), (int(div), None if mod is None else int(mod)))
     if kind == "gather":
         # table[key] of a 1-D plane of cells (role "lookup"); a key outside
         # [0, cells) — the skip key -1 of hawk.scatter among them — reads 0
@@ -418,11 +421,15 @@ class Assign:
 
 @dataclass
 class SampleSum:
-    """``name = hawk.sum(value, policy=...)``: one cell over every sample."""
+    """``name = hawk.sum(value, policy=...)``: one cell over every sample; with
+    ``group`` (``hawk.sum(value, over=<trailing lane axes>)``), one cell per
+    run of ``group`` consecutive samples (one per coordinate of the kept
+    leading axes)."""
 
     name: str
     value: Node
     policy: str = "ordered"
+    group: int | None = None
 
 
 @dataclass
@@ -451,6 +458,7 @@ class Program:
 
     decls: dict = field(default_factory=dict)     # name -> Decl, declaration order
     sinks: list = field(default_factory=list)
+    grid: object = None                           # the GridDecl of the launch's lane axes, if declared
 
 
 # --------------------------------------------------------------------------

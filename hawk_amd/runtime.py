@@ -75,6 +75,25 @@ class DeviceKernel:
     def check_planes(self, arrays: dict, n_samples=None) -> int:
         """Validate every bound plane against the sidecar; return the sample count."""
         torch = _torch()
+        grid = self.sidecar.get("grid")
+        n_grid = None
+        if grid:
+            # a Grid's extents may be given by label (reference hawk/trace/decl.py:135-145:
+            # "the caller gives it as node=N"): the first axis's sets the lane count
+            static = 1
+            for _, e in grid:
+                static *= e if e is not None else 1
+            for pos, (label, extent) in enumerate(grid):
+                if label not in arrays:
+                    continue
+                value = arrays.pop(label)
+                if isinstance(value, bool) or not isinstance(value, int) or value < 0:
+                    raise HawkError(f"kernel {self.name!r}: the Grid extent {label}= is an int >= 0, got {value!r}")
+                if extent is not None and value != extent:
+                    raise HawkError(f"kernel {self.name!r}: the Grid declares {label}:{extent}, the call gives "
+                                    f"{label}={value}")
+                if pos == 0:
+                    n_grid = value * (static // (extent or 1)) if extent else value * static
         declared = set(self.caller_planes())
         unknown = sorted(set(arrays) - declared)
         if unknown:
@@ -85,6 +104,7 @@ class DeviceKernel:
             raise HawkError(f"kernel {self.name!r}: bind {missing}")
         n = n_samples
         problems = []
+        keyed = []
         for name in sorted(declared):
             info = self.planes[name]
             x = arrays[name]
@@ -118,6 +138,8 @@ class DeviceKernel:
                     n = int(x.shape[-1])
                 elif int(x.shape[-1]) != n:
                     problems.append(f"{name!r} holds {int(x.shape[-1])} samples, other planes {n}")
+            elif role == "cell" and info.get("group"):
+                keyed.append((name, x, info["group"]))
             elif role == "cell":
                 if x.numel() != 1:
                     problems.append(f"{name!r} is a one-cell result of hawk.sum: bind 1 element, got {x.numel()}")
@@ -128,11 +150,26 @@ class DeviceKernel:
                 if x.dim() != 1:
                     problems.append(f"{name!r} is a 1-D plane of cells read at a key (the adjoint of a "
                                     "hawk.scatter target): bind one value per cell")
+        if n_grid is not None:
+            if n is not None and n != n_grid:
+                problems.append(f"the Grid's extents give {n_grid} lanes, the planes {n}")
+            n = n_grid
+        if n is not None and grid:
+            static = 1
+            for _, e in grid:
+                static *= e if e is not None else 1
+            if n % static:
+                problems.append(f"{n} lanes are not a whole number of Grid{[tuple(a) for a in grid]} rows "
+                                f"of {static}")
+        for name, x, group in keyed:
+            if n is not None and x.numel() != n // group:
+                problems.append(f"{name!r} holds hawk.sum over the trailing lane axes, one cell per {group} "
+                                f"lanes: bind {n // group} elements, got {x.numel()}")
         if problems:
             raise HawkError(f"kernel {self.name!r}: " + "; ".join(problems))
         if n is None:
             raise HawkError(f"kernel {self.name!r}: no per-sample plane is bound, so the sample count is "
-                            "unknown; pass n_samples=")
+                            "unknown; pass n_samples=" + (f" or the Grid's {grid[0][0]}=" if grid else ""))
         return n
 
     # -- scratch -------------------------------------------------------------
@@ -215,6 +252,11 @@ class DeviceKernel:
                            t["products"], n, stream)
             elif t["op"] == "row_sum":
                 self._row_sum(t, bound, n, device, stream)
+            elif t["op"] == "keyed_sum":
+                scratch = self._buffer(("keyed", t["out"], n), _core.keyed_ordered_sum_scratch_bytes(n, t["group"]),
+                                       device)
+                _core.keyed_ordered_sum(bound[t["u"]].data_ptr(), n, t["group"], bound[t["out"]].data_ptr(),
+                                        scratch.data_ptr(), stream)
             else:
                 raise HawkError(f"kernel {self.name!r}: unknown team stage {t['op']!r}")
         if check:
@@ -334,6 +376,11 @@ class Prepared:
                 self.steps.append((_core.mm16, args))
             elif t["op"] == "row_sum":
                 self.steps.append((kernel._row_sum, (t, bound, self.n, device)))
+            elif t["op"] == "keyed_sum":
+                scratch = kernel._buffer(("keyed", t["out"], self.n),
+                                         _core.keyed_ordered_sum_scratch_bytes(self.n, t["group"]), device)
+                args = (bound[t["u"]].data_ptr(), self.n, t["group"], bound[t["out"]].data_ptr(), scratch.data_ptr())
+                self.steps.append((_core.keyed_ordered_sum, args))
             else:
                 raise HawkError(f"kernel {kernel.name!r}: unknown team stage {t['op']!r}")
 
@@ -352,7 +399,8 @@ class Prepared:
                 k.entry.run(self.block, 0, self.n, self.n, threads=k.launch_shape["block"],
                             per_thread=k.launch_shape["per_thread"], stream=self.stream)
             out.append((k.name, stage))
-        labels = {_core.ordered_sum: "ordered_sum", _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16"}
+        labels = {_core.ordered_sum: "ordered_sum", _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16",
+                  _core.keyed_ordered_sum: "keyed_sum"}
         for fn, args in self.steps:
             label = labels.get(fn, "row_sum")
             out.append((label, lambda fn=fn, args=args: fn(*args, self.stream)))

@@ -26,7 +26,7 @@ from typing import Any
 
 from . import ir
 from .ir import AccumWrite, Assign, Decl, HawkError, Node, Program, SampleSum, make
-from .types import MutableDecl, TensorType, _ParamDecl, role_of
+from .types import GridDecl, MutableDecl, TensorType, _ParamDecl, role_of
 
 SUM_POLICIES = ("auto", "compensated", "ordered")
 SCATTER_POLICIES = ("ordered",)
@@ -167,12 +167,16 @@ class MutableRef(Value):
 
 
 class Reduced:
-    """The result of ``hawk.sum``: one value for the whole run.  It can be
-    committed (assigned to a ``Mutable`` or returned), not read back."""
+    """The result of ``hawk.sum``: one value for the whole run, or with
+    ``over=`` one per coordinate of the kept lane axes (``group`` consecutive
+    samples each).  It can be committed (assigned to a ``Mutable`` or
+    returned), not read back."""
 
-    def __init__(self, node: Node, policy: str):
+    def __init__(self, node: Node, policy: str, group: int | None = None, kept: tuple = ()):
         self.node = node
         self.policy = policy
+        self.group = group
+        self.kept = kept
 
     def _refuse(self, *_):
         raise HawkError("a value reduced over every sample (hawk.sum) is read back in the body: "
@@ -187,13 +191,47 @@ class Reduced:
 # cross-sample vocabulary
 
 
+class LaneRef:
+    """The ``Grid`` parameter: the lane's coordinates, as Index values.
+    ``lane.<axis>`` or ``lane[i]`` (0 the slowest axis, -1 the fastest) is
+    ``(sample // stride) % extent`` with the stride the product of the later
+    axes' extents; ``lane.flat`` is the flat lane index (reference
+    ``hawk/trace/decl.py:135-145``)."""
+
+    def __init__(self, grid: GridDecl):
+        object.__setattr__(self, "_grid", grid)
+
+    def _axis(self, pos: int) -> Value:
+        axes = self._grid.axes
+        stride = 1
+        for _, e in axes[pos + 1:]:
+            stride *= e
+        return Value(make("lane_axis", (), (stride, axes[pos][1])))
+
+    def __getattr__(self, label: str) -> Value:
+        if label == "flat":
+            return Value(make("lane_axis", (), (1, 0)))
+        for pos, (name, _) in enumerate(self._grid.axes):
+            if name == label:
+                return self._axis(pos)
+        raise HawkError(f"the Grid has no axis {label!r} (its axes: {[a for a, _ in self._grid.axes]})")
+
+    def __getitem__(self, pos: int) -> Value:
+        axes = self._grid.axes
+        if not isinstance(pos, int) or not -len(axes) <= pos < len(axes):
+            raise HawkError(f"lane[{pos!r}]: the Grid has {len(axes)} axes")
+        return self._axis(pos % len(axes))
+
+
 class _Trace:
-    """The sinks a kernel body records while it is traced."""
+    """The sinks a kernel body records while it is traced, and the Grid of
+    its lanes (if declared)."""
 
     stack: list = []
 
-    def __init__(self):
+    def __init__(self, grid: GridDecl | None = None):
         self.sinks: list = []
+        self.grid = grid
 
     def __enter__(self):
         _Trace.stack.append(self)
@@ -209,23 +247,57 @@ class _Trace:
         return cls.stack[-1]
 
 
-def sum(x: Any, policy: str = "auto") -> Reduced:  # noqa: A001 - hawk's spelling
-    """The sum of ``x`` over every sample of the run (reference
-    ``hawk/trace/reduce.py:277-287``).  ``policy="ordered"`` adds in a fixed
-    tree that depends on the sample count only: 65536 virtual lanes, each
-    adding its rows in order, folded in groups of 1024 by a halving tree and
-    the 64 group results by the same tree — the same bits on every launch.
-    The default policies (``"auto"``, ``"compensated"``) sum each row of 32
-    samples as a compensated (hi, comp) pair and fold the rows in the
-    canonical ordered tree of reference ``hawk/_cells.py`` — also the same
-    bits on every launch."""
+def sum(x: Any, over: Any = None, policy: str = "auto") -> Reduced:  # noqa: A001 - hawk's spelling
+    """The sum of ``x`` over every sample of the run, or over the lane axes
+    ``over`` names (a label, a position, or a tuple of them) of the kernel's
+    ``Grid`` (reference ``hawk/trace/reduce.py:277-301``).
+
+    ``policy="ordered"`` adds in a fixed tree that depends on the sample count
+    only: 65536 virtual lanes, each adding its rows in order, folded in groups
+    of 1024 by a halving tree and the 64 group results by the same tree — the
+    same bits on every launch.  Over some axes it sums over the TRAILING ones
+    only: each coordinate of the kept leading axes is a run of consecutive
+    samples, and each run takes that tree.  The default policies (``"auto"``,
+    ``"compensated"``) sum each row of 32 samples as a compensated
+    (hi, comp) pair and fold the rows in the canonical ordered tree of
+    reference ``hawk/_cells.py``; over some axes they are not in this build."""
     if policy not in SUM_POLICIES:
         raise HawkError(f"hawk.sum(x, policy={policy!r}): policy={policy!r} is not one of {SUM_POLICIES}")
     n = _projected(node_of(x))
     if n.ttype.shape:
         raise HawkError("hawk.sum over samples of a vector or matrix is not in this build; "
                         "sum each component")
-    return Reduced(n, policy)
+    if over is None:
+        return Reduced(n, policy)
+    grid = _Trace.current("hawk.sum").grid
+    if grid is None:
+        raise HawkError("hawk.sum(x, over=...) names lane axes: declare the kernel's lanes with a "
+                        'Grid parameter, e.g. lane: Grid["key", "sample":1024]')
+    labels = [a for a, _ in grid.axes]
+    items = over if isinstance(over, tuple) else (over,)
+    reduced = set()
+    for item in items:
+        if isinstance(item, str) and item in labels:
+            reduced.add(labels.index(item))
+        elif isinstance(item, int) and not isinstance(item, bool) and -len(labels) <= item < len(labels):
+            reduced.add(item % len(labels))
+        else:
+            raise HawkError(f"hawk.sum(x, over={over!r}): {item!r} is not an axis of the Grid {labels}")
+    if len(reduced) == len(labels):
+        return Reduced(n, policy)
+    spelled = f"over={over!r}"
+    if policy != "ordered":
+        raise HawkError(f"hawk.sum(x, {spelled}, policy={policy!r}): a sum over some lane axes is built with "
+                        "policy='ordered' on this target (the default policies commit per key atomically in "
+                        "the reference)")
+    if reduced != set(range(len(labels) - len(reduced), len(labels))):
+        raise HawkError(f"hawk.sum(x, {spelled}, policy='ordered'): policy='ordered' sums over the trailing "
+                        f"lane axes only (the Grid's axes are {labels})")
+    group = 1
+    for pos in reduced:
+        group *= grid.axes[pos][1]
+    kept = tuple(labels[:len(labels) - len(reduced)])
+    return Reduced(n, policy, group, kept)
 
 
 class _Stored:
@@ -452,6 +524,7 @@ def trace(fn, scope: dict | None = None) -> Program:
     sig = inspect.signature(fn)
     program = Program()
     args, mutables = [], []
+    axes_of = {}                     # a Mutable declared with lane axes -> its axes
     for p in sig.parameters.values():
         if p.kind not in (p.POSITIONAL_ONLY, p.POSITIONAL_OR_KEYWORD):
             raise HawkError(f"{fn.__name__}: parameter {p.name!r} must be a plain positional parameter")
@@ -459,8 +532,15 @@ def trace(fn, scope: dict | None = None) -> Program:
         if ann is inspect.Parameter.empty:
             raise HawkError(f"{fn.__name__}: parameter {p.name!r} has no declaration "
                             "(Scalar, Vector[n], Matrix[r, c], Index, Param, Mutable[...])")
-        if isinstance(ann, MutableDecl):
+        if isinstance(ann, GridDecl):
+            if program.grid is not None:
+                raise HawkError(f"{fn.__name__}: one Grid parameter declares the lanes; {p.name!r} is a second")
+            program.grid = ann
+            args.append(LaneRef(ann))
+        elif isinstance(ann, MutableDecl):
             program.decls[p.name] = Decl(p.name, "mutable", ann.ttype)
+            if ann.axes:
+                axes_of[p.name] = ann.axes
             args.append(MutableRef(p.name, ann.ttype))
             mutables.append(p.name)
         elif isinstance(ann, _ParamDecl):
@@ -474,8 +554,25 @@ def trace(fn, scope: dict | None = None) -> Program:
             raise HawkError(f"{fn.__name__}: parameter {p.name!r} is declared {ann!r}, which is not "
                             "Scalar, Vector[n], Matrix[r, c], Index, Param or Mutable[...]")
     body = _rewritten(fn, tuple(mutables))
-    with _Trace() as tr:
+    with _Trace(program.grid) as tr:
         ret, finals = body(*args)
+
+    def keyed(name: str, red: Reduced):
+        """The SampleSum committing ``red`` into ``name`` (a Mutable declared
+        with the kept axes, or the returned ``out``)."""
+        axes = axes_of.get(name)
+        if red.group is None:
+            if axes:
+                raise HawkError(f"{name!r} is declared with lane axes {[a for a, _ in axes]} but assigned a sum "
+                                "over every sample (one cell); declare Mutable[Scalar]")
+            return SampleSum(name, red.node, red.policy)
+        grid_axes = dict(program.grid.axes)
+        if axes is not None:
+            if tuple(a for a, _ in axes) != red.kept or any(
+                    e is not None and grid_axes[a] is not None and e != grid_axes[a] for a, e in axes):
+                raise HawkError(f"{name!r} is declared with lane axes {list(axes)} but holds the sum over the "
+                                f"other axes, one value per {list(red.kept)} coordinate")
+        return SampleSum(name, red.node, red.policy, red.group)
     sinks = list(tr.sinks)
     for name in mutables:
         final = finals[name]
@@ -485,8 +582,14 @@ def trace(fn, scope: dict | None = None) -> Program:
         if isinstance(final, Reduced):
             if decl.ttype.shape:
                 raise HawkError(f"{name!r}: hawk.sum commits a scalar cell; declare Mutable[Scalar]")
-            sinks.append(SampleSum(name, final.node, final.policy))
+            if final.group is not None and name not in axes_of:
+                raise HawkError(f"{name!r} holds hawk.sum over some lane axes, one value per "
+                                f"{list(final.kept)} coordinate: declare it Mutable[{', '.join(repr(k) for k in final.kept)}]")
+            sinks.append(keyed(name, final))
             continue
+        if name in axes_of:
+            raise HawkError(f"{name!r} is declared with lane axes: it holds hawk.sum(x, over=...), "
+                            "not a per-sample value")
         node = _projected(node_of(final))
         if node.ttype.shape != decl.ttype.shape:
             if node.ttype.shape == ():
@@ -499,7 +602,7 @@ def trace(fn, scope: dict | None = None) -> Program:
         ret_ann = _annotation(fn, sig.return_annotation, ns)
         if isinstance(ret, Reduced):
             program.decls["out"] = Decl("out", "mutable", TensorType((), "f64"))
-            sinks.append(SampleSum("out", ret.node, ret.policy))
+            sinks.append(keyed("out", ret))
         else:
             node = ir.as_real(_projected(node_of(ret)))
             if isinstance(ret_ann, TensorType) and ret_ann.shape != node.ttype.shape:

@@ -167,6 +167,20 @@ int hk_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch,
 int hk_ordered_fold_f64(const double* lanes, double* out, void* scratch,
                         void* stream);
 
+/* Keyed fixed-tree sum: out[k] for k < n / group is key k's rows
+ * u[k*group .. (k+1)*group) added by the ordered sum's tree, the same bits
+ * hk_ordered_sum_f64 gives for those rows alone — hawk.sum(x, over=<trailing
+ * lane axes>, policy="ordered") of a Grid's leading-axis coordinates.
+ * Replaces the block-sum team stage of reference hawk/emit/team.py:115-205
+ * (`_block` with its `gp` stage) and hawk/emit/team.py:208-278
+ * (`_block_part`).  n must be a multiple of group (HK_EVALUE otherwise);
+ * group == n is the one-key case and runs hk_ordered_sum_f64.
+ * Scratch: hk_keyed_ordered_sum_scratch_bytes(n, group) bytes, no contents
+ * needed (for group == n, the ordered sum's scratch, zero before its first call). */
+size_t hk_keyed_ordered_sum_scratch_bytes(int64_t n, int64_t group);
+int hk_keyed_ordered_sum_f64(const double* u, int64_t n, int64_t group, double* out,
+                             void* scratch, void* stream);
+
 /* The finish of a default-policy sample sum (`hawk.sum(x)`): `rows`
  * compensated (hi, comp) row pairs (one per 32 samples, written by the
  * per-sample stage as reference `hawk/emit/wrapper.py:542-665` does) folded

@@ -274,6 +274,14 @@ HKO_EXPORT double hko_ordered_sum(const double* u, int64_t n) {
     return fold_groups(gp);
 }
 
+/* hawk.sum(x, over=<trailing lane axes>, policy="ordered"): key k's rows are
+ * u[k*group .. (k+1)*group), each key takes the ordered sum's tree on its own
+ * rows (reference hawk/emit/team.py:115-205 and :208-278: block b is group
+ * b % 64 of key b / 64; the gp stage folds a key's 64 group values). */
+HKO_EXPORT void hko_keyed_ordered_sum(const double* u, int64_t n, int64_t group, double* out) {
+    for (int64_t k = 0; k * group < n; ++k) out[k] = hko_ordered_sum(u + k * group, group);
+}
+
 /* ---- config 5c: the keyed ordered scatter ---------------------------------
  * Reference hawk/emit/team.py:322-460 and hawk/_lane_bind.py:111-114:
  * chunks = clamp(n / cells, 1, 256), span = ceil(n / chunks); chunk b walks

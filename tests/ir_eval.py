@@ -108,6 +108,13 @@ class Evaluator:
         if k == "cho_solve":
             (L, info), b = self.memo[m.operands[0].uid], self._op(m, 1)
             return self._cho_solve(L, info, b)
+        if k == "lane_axis":
+            div, mod = m.literal
+            idx = np.arange(n, dtype=np.int64)
+            if mod == 0:
+                return idx
+            q = idx // div
+            return (q if mod is None else q % mod).astype(np.int32)
         if k == "gather":
             table, key = self._op(m, 0), self._op(m, 1)
             ok = (key >= 0) & (key < table.shape[0])

@@ -483,3 +483,76 @@ def test_carried_reuse_leaves_a_value_that_reads_the_index_alone():
             acc = acc + sqrt(acc + k)
         y = acc
     assert _carry_repeats(walk.program) is walk.program
+
+
+# -- lane axes: Grid[...] and hawk.sum(x, over=...) ------------------------------------------
+
+@hawk.kernel
+def keyed_rows(lane: hawk.Grid["a", "b":8], x: Scalar, y: Mutable["a"]):
+    y = hawk.sum(x, over="b", policy="ordered")
+
+
+@hawk.kernel
+def lane_coords(lane: hawk.Grid["a", "b":4, "c":8], y: Mutable[Scalar]):
+    y = lane.a * 100.0 + lane.b * 10.0 + lane[-1] + 0.0 * lane.flat
+
+
+def test_grid_axes_and_refusals_follow_the_reference():
+    """Grid labels in numpy order, only the first bare; an ordered sum over
+    some axes sums the TRAILING ones only (reference
+    tests/test_ordered_trailing_axes.py:20-38, same messages)."""
+    assert hawk.Grid["key", "sample":8].axes == (("key", None), ("sample", 8))
+    with pytest.raises(HawkError, match="only the FIRST axis may"):
+        hawk.Grid["a", "b"]
+    with pytest.raises(HawkError, match="duplicate"):
+        hawk.Grid["a", "a":3]
+    with pytest.raises(HawkError, match=r"policy='ordered' sums over the trailing lane axes only"):
+        @hawk.kernel
+        def leading(lane: hawk.Grid["a":4, "b":8], x: Scalar, y: Mutable["b":8]):
+            y = hawk.sum(x, over="a", policy="ordered")
+    with pytest.raises(HawkError, match=r"over=\('b'\)|over='b'"):
+        @hawk.kernel
+        def middle(lane: hawk.Grid["a", "b":4, "c":8], x: Scalar, y: Mutable["a"]):
+            y = hawk.sum(x, over="b", policy="ordered")
+
+    @hawk.kernel
+    def last_two(lane: hawk.Grid["a", "b":4, "c":8], x: Scalar, y: Mutable["a"]):
+        y = hawk.sum(x, over=("b", "c"), policy="ordered")
+    assert [(s.name, s.group) for s in last_two.sinks] == [("y", 32)]
+    with pytest.raises(HawkError, match="policy='ordered'"):
+        @hawk.kernel
+        def compensated(lane: hawk.Grid["a", "b":8], x: Scalar, y: Mutable["a"]):
+            y = hawk.sum(x, over="b")
+    with pytest.raises(HawkError, match="Grid parameter"):
+        @hawk.kernel
+        def no_grid(x: Scalar, y: Mutable["a"]):
+            y = hawk.sum(x, over="b", policy="ordered")
+    with pytest.raises(HawkError, match=r"Mutable\['a'\]"):
+        @hawk.kernel
+        def plain_cell(lane: hawk.Grid["a", "b":8], x: Scalar, y: Mutable[Scalar]):
+            y = hawk.sum(x, over="b", policy="ordered")
+
+
+def test_lane_coordinates_are_the_numpy_order_of_the_grid():
+    n = 3 * 32
+    got = evaluate(lane_coords.program, {}, n)["y"]
+    i = np.arange(n)
+    assert np.array_equal(got, (i // 32) * 100.0 + ((i // 8) % 4) * 10.0 + i % 8)
+
+
+def test_keyed_sum_plans_a_keyed_team_stage_and_its_derivatives(tmp_path):
+    """The keyed sum is one team stage reading x in place; its VJP gathers the
+    key's adjoint (bar_y is a lookup plane of keys, key = lane // 8); its JVP
+    is the keyed sum of the tangents."""
+    b = hawk.build([keyed_rows], tmp_path)
+    sc = b.sidecar("keyed_rows")
+    assert sc["team"] == [{"op": "keyed_sum", "u": "x", "out": "y", "group": 8}]
+    assert sc["planes"]["y"]["group"] == 8 and sc["grid"] == [["a", None], ["b", 8]]
+    back = vjp(keyed_rows, wrt=("x",))
+    assert back.decls["bar_y"].role == "lookup"
+    n = 5 * 8
+    bar = np.random.default_rng(1).normal(size=5)
+    got = evaluate(back, {"x": np.zeros(n), "bar_y": bar}, n)["bar_x"]
+    assert got.tobytes() == np.repeat(bar, 8).tobytes()
+    fwd = jvp(keyed_rows, wrt=("x",))
+    assert [(type(s).__name__, s.name, s.group) for s in fwd.sinks] == [("SampleSum", "dot_y", 8)]

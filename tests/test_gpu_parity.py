@@ -607,3 +607,111 @@ def test_chain_jvp_on_the_device(unit, gpu, n):
     want_bins, status = O.ordered_scatter(key, gy, np.zeros(cells))
     assert not status[1:].any()
     assert host(dot_bins).tobytes() == want_bins.tobytes()
+
+
+# -- keyed ordered sums over trailing lane axes ------------------------------------------------
+
+def _keyed_kernels(group):
+    import hawk_amd as hawk
+    from hawk_amd import Grid, Mutable, Scalar
+
+    @hawk.kernel
+    def ksum(lane: Grid["key", "sample":group], x: Scalar) -> Scalar:
+        return hawk.sum(x, over="sample", policy="ordered")
+    return ksum
+
+
+@pytest.mark.parametrize("n", [1, 1000, 65536, 3 * 65536 + 777, 200003])
+def test_keyed_ordered_sum_reference_cases(gpu, tmp_path, n):
+    """Reference tests/test_ordered_fixed_tree.py:43-79: the one-key kernel
+    total(lane: Grid["key", "sample":n], x) = hawk.sum(x, over="sample",
+    policy="ordered") gives the fixed tree's bits (the oracle, pinned to the
+    reference's NumPy emulation) on three replays."""
+    import hawk_amd as hawk
+    k = _keyed_kernels(n)
+    hawk.build([k], tmp_path)
+    kern = hawk.load(tmp_path, "ksum")
+    x = rng(n).normal(size=n) * np.exp(rng(n + 1).normal(size=n))
+    X = dev(x, gpu)
+    runs = []
+    for _ in range(3):
+        out = dev(np.zeros(1), gpu)
+        hawk.run(kern, x=X, out=out)
+        runs.append(host(out).tobytes())
+    assert runs[0] == runs[1] == runs[2]
+    assert np.frombuffer(runs[0])[0] == O.ordered_sum(x)
+
+
+@pytest.mark.parametrize("keys, group", [(4, 8), (1000, 5000), (3, 200003), (70000, 7), (2, 65536), (17, 1025),
+                                         (5, 1)])
+def test_keyed_ordered_sum_many_keys(gpu, tmp_path, keys, group):
+    """One cell per key, each key's run by the fixed tree, bit for bit the
+    oracle's (and, for the reference's A=4, B=8 case, numpy's row sums within
+    rtol 1e-13, tests/test_ordered_trailing_axes.py:66-76); two launches give
+    the same bits."""
+    import hawk_amd as hawk
+    kern_def = _keyed_kernels(group)
+    hawk.build([kern_def], tmp_path)
+    kern = hawk.load(tmp_path, "ksum")
+    n = keys * group
+    x = rng(7 + group).uniform(-2.0, 2.0, n) * np.exp(rng(8).normal(size=n))
+    X = dev(x, gpu)
+    print(f"keyed sum keys={keys} group={group}", flush=True)
+    out = dev(np.full(keys, np.nan), gpu)
+    hawk.run(kern, x=X, out=out)
+    got = host(out)
+    assert got.tobytes() == O.keyed_ordered_sum(x, group).tobytes()
+    out2 = dev(np.full(keys, np.nan), gpu)
+    kern.prepare(x=X, out=out2)()
+    assert host(out2).tobytes() == got.tobytes()
+    if (keys, group) == (4, 8):
+        np.testing.assert_allclose(got, x.reshape(keys, group).sum(axis=1), rtol=1e-13, atol=1e-13)
+
+
+def test_keyed_sum_derivatives_and_lane_coordinates_on_the_device(gpu, tmp_path):
+    """The VJP of y = hawk.sum(f(x), over="b", policy="ordered") reads each
+    lane's key adjoint (bar_x = f'(x) * bar_y[lane // 8]); the JVP's tangent
+    cells are the keyed sums of the tangents (the oracle's bits); lane
+    coordinates are the numpy order of the Grid; the Grid's runtime extent can
+    be given by label."""
+    import hawk_amd as hawk
+    from hawk_amd import Grid, Mutable, Scalar
+    from hawk_amd.diff import jvp, vjp
+    from hawk_amd.trace import Kernel
+
+    @hawk.kernel
+    def rows(lane: Grid["a", "b":8], x: Scalar, y: Mutable["a"]):
+        y = hawk.sum(x * x, over="b", policy="ordered")
+
+    @hawk.kernel
+    def coords(lane: Grid["a", "b":4, "c":8], y: Mutable[Scalar]):
+        y = lane.a * 100.0 + lane.b * 10.0 + lane[-1]
+
+    @hawk.kernel
+    def iota(lane: Grid["key", "sample":16], y: Mutable["key"]):
+        y = hawk.sum(lane.sample * 1.0, over="sample", policy="ordered")
+
+    back = Kernel("rows_vjp", vjp(rows, wrt=("x",)))
+    fwd = Kernel("rows_jvp", jvp(rows, wrt=("x",)))
+    hawk.build([rows, back, fwd, coords, iota], tmp_path)
+    keys = 50_000
+    n = keys * 8
+    g = rng(21)
+    x, bar, dx = g.normal(size=n), g.normal(size=keys), g.normal(size=n)
+    X = dev(x, gpu)
+    bx = dev(np.full(n, np.nan), gpu)
+    hawk.run(hawk.load(tmp_path, "rows_vjp"), x=X, bar_y=dev(bar, gpu), bar_x=bx)
+    assert host(bx).tobytes() == (2.0 * x * np.repeat(bar, 8)).tobytes() or \
+        host(bx).tobytes() == ((x * np.repeat(bar, 8)) + (x * np.repeat(bar, 8))).tobytes()
+    dy = dev(np.full(keys, np.nan), gpu)
+    hawk.run(hawk.load(tmp_path, "rows_jvp"), x=X, dot_x=dev(dx, gpu), dot_y=dy)
+    from ir_eval import evaluate
+    terms = evaluate(fwd.program, {"x": x, "dot_x": dx}, n)["dot_y"]
+    assert host(dy).tobytes() == O.keyed_ordered_sum(terms, 8).tobytes()
+    yc = dev(np.zeros(3 * 32), gpu)
+    hawk.run(hawk.load(tmp_path, "coords"), y=yc)
+    i = np.arange(3 * 32)
+    assert host(yc).tobytes() == ((i // 32) * 100.0 + ((i // 8) % 4) * 10.0 + i % 8).tobytes()
+    yi = dev(np.zeros(1000), gpu)
+    hawk.run(hawk.load(tmp_path, "iota"), key=1000, y=yi)
+    assert np.all(host(yi) == 120.0)

@@ -380,3 +380,34 @@ def test_chain_vjp_gathers_the_bins_adjoint_at_the_key():
     gathered = np.where(inside, bar_bins[np.where(inside, key, 0)], 0.0)
     assert np.array_equal(got, d * ((bar_y + 0.75) + gathered))
     assert (~inside).sum() > 100
+
+
+def _np_tree(s):
+    s = s.copy()
+    w = len(s) // 2
+    while w:
+        s[:w] += s[w:2 * w]
+        w //= 2
+    return s[0]
+
+
+def _np_ordered_sum(x):
+    """The fixed grouping in NumPy (reference tests/test_ordered_fixed_tree.py:25-40)."""
+    V, G, W = 65536, 64, 1024
+    part = np.zeros(V, x.dtype)
+    for r in range(0, len(x), V):
+        row = x[r:r + V]
+        part[:len(row)] += row
+    return _np_tree(np.array([_np_tree(part[g * W:(g + 1) * W]) for g in range(G)], x.dtype))
+
+
+@pytest.mark.parametrize("keys, group", [(1, 1), (4, 8), (7, 1), (3, 1000), (2, 65536), (2, 70001), (300, 17)])
+def test_keyed_ordered_sum_is_the_numpy_tree_per_key(keys, group):
+    """hawk.sum(x, over=<trailing axes>, policy="ordered"): each key's run of
+    `group` values takes the reference's fixed tree, bit for bit against its
+    NumPy emulation run on that key's values alone."""
+    g = np.random.default_rng(keys * 1000 + group)
+    x = g.normal(size=keys * group) * np.exp(g.normal(size=keys * group))
+    got = O.keyed_ordered_sum(x, group)
+    want = np.array([_np_ordered_sum(x[k * group:(k + 1) * group]) for k in range(keys)])
+    assert got.tobytes() == want.tobytes()
