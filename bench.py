@@ -4,7 +4,9 @@
 A step is one pass of the hot path over one batch of synthetic inputs already
 resident in HBM.  The default workload is BASELINE.json's ``configs[1]``: the
 ``energy`` kernel's forward, VJP and JVP over N = 2^25 samples (fp64).  Other
-configurations (``--config 1|3|4a|5``) time the remaining workloads the same way.
+configurations (``--config 1|3|4a|4b|5``) time the remaining workloads the same
+way; ``--config 5k`` times config 5's ordered sum in the reference's keyed
+spelling (``hawk.sum(x, over=...)``) over 16384 keys.
 
 Each stage launch of the timed steps (a per-sample kernel, or a team stage:
 the ordered sum or the ordered scatter) is bracketed by HIP events on the
@@ -196,6 +198,27 @@ def workload(config: str, device):
             O.ordered_scatter(key, y, np.zeros(cells), threads=threads)
         return dict(name="chain + ordered sum + ordered scatter (config 5)", n=n, kernels=kernels, work=work, cpu=cpu,
                     dtype="f64")
+    if config == "5k":
+        # config 5b in the reference's keyed spelling (tests/test_ordered_fixed_tree.py:43-47), over
+        # 16384 keys of 4096 samples: hawk.sum(x, over="sample", policy="ordered") per key
+        n, group = 1 << 26, 4096
+        x = np.random.default_rng(5).normal(size=n)
+
+        @hawk.kernel
+        def keyed_total(lane: hawk.Grid["key", "sample":4096], x: hawk.Scalar) -> hawk.Scalar:
+            return hawk.sum(x, over="sample", policy="ordered")
+        hawk.build([keyed_total], unit)
+        k = hawk.load(unit, "keyed_total")
+        X = _dev(x, device)
+        OUT = torch.zeros(n // group, dtype=torch.float64, device=device)
+        kernels = [k.prepare(x=X, out=OUT)]
+        work = {"keyed_sum": (8 + 8 / group, 1)}    # every x once, every cell once
+
+        def cpu(threads):
+            import oracle_lib as O
+            O.keyed_ordered_sum(x, group, threads=threads, profile="native")
+        return dict(name="keyed ordered sum, 16384 keys x 4096 samples (config 5b, keyed)", n=n, kernels=kernels,
+                    work=work, cpu=cpu, dtype="f64")
     raise SystemExit(f"unknown --config {config!r}")
 
 
@@ -206,6 +229,7 @@ def workload(config: str, device):
 STAGE_KERNELS = {"ordered_sum": ("hawk_sum_lanes", "hawk_sum_fold"),
                  "ordered_scatter": ("hawk_scatter_status", "hawk_scatter_walk", "hawk_scatter_cells"),
                  "mm16": ("hawk_mm16_f32",),
+                 "keyed_sum": ("hawk_keyed_rows",),      # keys of at most 65536 samples (config 5k: 4096)
                  "mm16#2": ("hawk_mm16_f32_shared",)}
 COPY_PROBE_BYTES = 1 << 30
 

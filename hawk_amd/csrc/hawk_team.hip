@@ -233,10 +233,53 @@ __device__ __forceinline__ int pow2_at_least(long long x) {
     return p;
 }
 
-// One workgroup per key: the used groups' halving trees, then the group values' tree.
+// The halving tree s[i] += s[i + w], w = P/2 .. 1, of P <= 1024 values (a
+// power of 2; zeros past the data) held by a 256-thread workgroup as
+// s[t + 256j] = v[j]: the levels w = 512 and 256 pair values of one thread,
+// w = 128 and 64 go through LDS, w = 32 .. 1 through the first wave's
+// shuffles (lane i reads lane i + w; only lanes below w carry on).  The
+// same pairs, in the same order, as the tree over LDS.  Thread 0 returns s[0].
+__device__ __forceinline__ double block_tree(double (&v)[4], int P, double* sh) {
+    const int t = threadIdx.x;
+    if (P > 512) { v[0] = v[0] + v[2]; v[1] = v[1] + v[3]; }
+    if (P > 256) v[0] = v[0] + v[1];
+    double x = v[0];
+    if (P > 64) {
+        sh[t] = x;
+        __syncthreads();
+        if (P > 128 && t < 128) sh[t] = sh[t] + sh[t + 128];
+        __syncthreads();
+        if (t < 64) x = sh[t] + sh[t + 64];
+    }
+    if (t < 64) {
+#pragma unroll
+        for (int w = 32; w >= 1; w >>= 1) {
+            const double y = __shfl_down(x, w, 64);
+            if (P > w) x = x + y;
+        }
+    }
+    __syncthreads();                      // sh is free for the next tree
+    return x;
+}
+
+// The 64 group values' tree over Q = 2^ceil(log2 used) of them, in the first wave.
+__device__ __forceinline__ double group_tree(const double* gp, int used) {
+    const int t = threadIdx.x;
+    const int q = pow2_at_least(used);
+    double x = t < used ? gp[t] : 0.0;
+#pragma unroll
+    for (int w = 32; w >= 1; w >>= 1) {
+        const double y = __shfl_down(x, w, 64);
+        if (q > w) x = x + y;
+    }
+    return x;
+}
+
+// One workgroup per key whose lanes are already folded into `lanes` (groups
+// of more than 65536 rows): the used groups' trees, then the group values'.
 __global__ __launch_bounds__(256) void hawk_keyed_fold(const double* __restrict__ lanes, long long lv,
                                                        double* __restrict__ out) {
-    __shared__ double sh[kFoldLanes];
+    __shared__ double sh[256];
     __shared__ double gp[kGroups];
     const long long k = blockIdx.x;
     const int t = threadIdx.x;
@@ -244,26 +287,57 @@ __global__ __launch_bounds__(256) void hawk_keyed_fold(const double* __restrict_
     const int width = lv >= kFoldLanes ? kFoldLanes : pow2_at_least(lv);
     const double* mine = lanes + k * lv;
     for (int g = 0; g < used; ++g) {
-        for (int i = t; i < width; i += 256) {
-            const long long at = static_cast<long long>(g) * kFoldLanes + i;
-            sh[i] = at < lv ? mine[at] : 0.0;
+        double v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const long long at = static_cast<long long>(g) * kFoldLanes + t + 256 * j;
+            v[j] = at < lv ? mine[at] : 0.0;
         }
-        __syncthreads();
-        for (int w = width / 2; w > 0; w >>= 1) {
-            for (int i = t; i < w; i += 256) sh[i] = sh[i] + sh[i + w];
-            __syncthreads();
-        }
-        if (t == 0) gp[g] = sh[0];
-        __syncthreads();
+        const double s = block_tree(v, width, sh);
+        if (t == 0) gp[g] = s;
     }
-    const int q = pow2_at_least(used);
-    for (int i = used + t; i < q; i += 256) gp[i] = 0.0;
     __syncthreads();
-    for (int w = q / 2; w > 0; w >>= 1) {
-        if (t < w) gp[t] = gp[t] + gp[t + w];
-        __syncthreads();
+    const double total = t < 64 ? group_tree(gp, used) : 0.0;
+    if (t == 0) out[k] = total;
+}
+
+// One workgroup per key of at most 65536 rows: virtual lane l holds row l
+// alone (0.0 + u[l], the add from +0.0), so the trees read u directly.
+__global__ __launch_bounds__(256) void hawk_keyed_rows(const double* __restrict__ u, long long group,
+                                                       double* __restrict__ out) {
+    __shared__ double sh[256];
+    __shared__ double gp[kGroups];
+    const long long k = blockIdx.x;
+    const int t = threadIdx.x;
+    const int used = static_cast<int>((group + kFoldLanes - 1) / kFoldLanes);
+    const int width = group >= kFoldLanes ? kFoldLanes : pow2_at_least(group);
+    const double* mine = u + k * group;
+    double nxt[4];                        // the next group's rows, loaded during this group's tree
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const long long at = t + 256 * j;
+        nxt[j] = at < group ? __builtin_nontemporal_load(mine + at) : 0.0;
     }
-    if (t == 0) out[k] = gp[0];
+    for (int g = 0; g < used; ++g) {
+        double v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const long long at = static_cast<long long>(g) * kFoldLanes + t + 256 * j;
+            v[j] = at < group ? 0.0 + nxt[j] : 0.0;
+        }
+        if (g + 1 < used) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const long long at = static_cast<long long>(g + 1) * kFoldLanes + t + 256 * j;
+                nxt[j] = at < group ? __builtin_nontemporal_load(mine + at) : 0.0;
+            }
+        }
+        const double s = block_tree(v, width, sh);
+        if (t == 0) gp[g] = s;
+    }
+    __syncthreads();
+    const double total = t < 64 ? group_tree(gp, used) : 0.0;
+    if (t == 0) out[k] = total;
 }
 
 // ---------------------------------------------------------------------------
@@ -683,6 +757,7 @@ int hk_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch, v
 size_t hk_keyed_ordered_sum_scratch_bytes(int64_t n, int64_t group) {
     if (n <= 0 || group <= 0 || n % group != 0) return 0;
     if (n == group) return kSumScratch;
+    if (group <= kVirtualLanes) return 256;                  // the keys read their rows directly
     const long long lv = group < kVirtualLanes ? group : kVirtualLanes;
     return sizeof(double) * static_cast<size_t>(n / group) * static_cast<size_t>(lv) + 256;
 }
@@ -699,6 +774,11 @@ int hk_keyed_ordered_sum_f64(const double* u, int64_t n, int64_t group, double* 
     if (n == group) return hk_ordered_sum_f64(u, n, out, scratch, stream);    // one key: the ordered sum
     const long long keys = n / group;
     if (keys > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_ordered_sum_f64: too many keys");
+    if (group <= kVirtualLanes) {
+        hipLaunchKernelGGL(hawk_keyed_rows, dim3(static_cast<unsigned>(keys)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), u, static_cast<long long>(group), out);
+        return launch_error("hawk_keyed_rows launch");
+    }
     const long long lv = group < kVirtualLanes ? group : kVirtualLanes;
     const long long total = keys * lv;
     auto* lanes = static_cast<double*>(scratch);

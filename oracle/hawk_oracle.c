@@ -599,6 +599,10 @@ static void* job_main(void* arg) {
                           j->count); break;
         case 14: hko_mm16_vjp((const float*)j->in0, (const float*)j->in1, (const float*)j->in2, j->n,
                               (float*)j->out0, (float*)j->out1, j->base, j->count); break;
+        case 15:   /* keys [base, base+count) of a keyed ordered sum, group = cells */
+            for (int64_t k = j->base; k < j->base + j->count; ++k)
+                ((double*)j->out0)[k] = hko_ordered_sum((const double*)j->in0 + k * j->cells, j->cells);
+            break;
         default: break;
     }
     return NULL;
@@ -644,6 +648,22 @@ HKO_EXPORT double hko_ordered_sum_threads(const double* u, int64_t n, int thread
     }
     run_jobs(jobs, threads);
     return fold_groups(gp);
+}
+
+/* The keyed ordered sum with its keys spread over `threads` threads (same bits). */
+HKO_EXPORT void hko_keyed_ordered_sum_threads(const double* u, int64_t n, int64_t group, double* out, int threads) {
+    const int64_t keys = group > 0 ? n / group : 0;
+    if (threads < 1) threads = 1;
+    if (threads > keys) threads = keys > 0 ? (int)keys : 1;
+    hko_job* jobs = (hko_job*)calloc((size_t)threads, sizeof(hko_job));
+    const int64_t per = (keys + threads - 1) / threads;
+    for (int k = 0; k < threads; ++k) {
+        jobs[k].which = 15; jobs[k].in0 = u; jobs[k].out0 = out; jobs[k].cells = group;
+        jobs[k].base = k * per < keys ? k * per : keys;
+        jobs[k].count = ((k + 1) * per < keys ? (k + 1) * per : keys) - jobs[k].base;
+    }
+    run_jobs(jobs, threads);
+    free(jobs);
 }
 
 /* The ordered scatter with its chunks spread over `threads` threads (same bits). */

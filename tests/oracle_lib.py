@@ -46,6 +46,7 @@ def lib(profile: str = "portable"):
         "hko_libm": (None, [ctypes.c_int, _P, _P, _I64]),
         "hko_ordered_sum": (_D, [_P, _I64]),
         "hko_keyed_ordered_sum": (None, [_P, _I64, _I64, _P]),
+        "hko_keyed_ordered_sum_threads": (None, [_P, _I64, _I64, _P, ctypes.c_int]),
         "hko_row_sums": (None, [_P, _I64, _P, _P]),
         "hko_rows_finish": (_D, [_P, _P, _I64]),
         "hko_sample_sum": (_D, [_P, _I64]),
@@ -155,12 +156,15 @@ def ordered_sum(u, threads: int = 1) -> float:
     return lib().hko_ordered_sum(_p(u), u.size)
 
 
-def keyed_ordered_sum(u, group: int):
+def keyed_ordered_sum(u, group: int, threads: int = 1, profile: str = "portable"):
     """One ordered-sum cell per run of ``group`` consecutive values."""
     u = np.ascontiguousarray(u, dtype=np.float64)
     assert u.size % group == 0
     out = np.empty(u.size // group)
-    lib().hko_keyed_ordered_sum(_p(u), u.size, group, _p(out))
+    if threads > 1:
+        lib(profile).hko_keyed_ordered_sum_threads(_p(u), u.size, group, _p(out), threads)
+    else:
+        lib(profile).hko_keyed_ordered_sum(_p(u), u.size, group, _p(out))
     return out
 
 

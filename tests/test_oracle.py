@@ -411,3 +411,4 @@ def test_keyed_ordered_sum_is_the_numpy_tree_per_key(keys, group):
     got = O.keyed_ordered_sum(x, group)
     want = np.array([_np_ordered_sum(x[k * group:(k + 1) * group]) for k in range(keys)])
     assert got.tobytes() == want.tobytes()
+    assert O.keyed_ordered_sum(x, group, threads=3).tobytes() == got.tobytes()
