@@ -94,6 +94,18 @@ def test_team_stage_arguments_are_checked_before_any_launch():
     rc = L.hk_ordered_scatter_f64(None, None, 10, None, 5, None, None, None)
     assert rc != 0 and b"required" in L.hk_last_error()
     assert L.hk_ordered_scatter_f64(None, None, 10, None, 0, None, None, None) == 0   # no cells: nothing
+    # the keyed sum: whole groups only; no keys is nothing; scratch sizes by shape
+    rc = L.hk_keyed_ordered_sum_f64(None, 10, 3, None, None, None)
+    assert rc != 0 and b"whole number of groups" in L.hk_last_error()
+    rc = L.hk_keyed_ordered_sum_f64(None, 10, 0, None, None, None)
+    assert rc != 0 and b"group >= 1" in L.hk_last_error()
+    assert L.hk_keyed_ordered_sum_f64(None, 0, 4, None, None, None) == 0
+    assert L.hk_keyed_ordered_sum_scratch_bytes(12, 4) == 256                 # keys read their rows directly
+    assert L.hk_keyed_ordered_sum_scratch_bytes(8, 8) == L.hk_ordered_sum_scratch_bytes()   # one key
+    assert L.hk_keyed_ordered_sum_scratch_bytes(2 * 70001, 70001) == 8 * 2 * 65536 + 256
+    # the per-sample products: plane counts and indices are checked first
+    rc = L.hk_mm16_f32(None, 0, None, 1, None, 1, None)
+    assert rc != 0 and b"1..3 input planes" in L.hk_last_error()
 
 
 def test_scatter_chunk_rule():
