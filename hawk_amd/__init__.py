@@ -23,7 +23,7 @@ tensors.  Typical use::
 from __future__ import annotations
 
 from .ir import HawkError
-from .types import Grid, Index, Matrix, Mutable, Param, Scalar, TensorType, Vector
+from .types import Grid, Index, Matrix, Mutable, Param, Scalar, Table, TensorType, Vector
 
 __version__ = "0.1.0"
 
@@ -39,7 +39,7 @@ _LAZY = {
 }
 _SUBMODULES = ("math", "diff", "runtime", "artifact", "compile", "ir", "emit_hip", "trace")
 
-__all__ = ["Grid", "HawkError", "Index", "Matrix", "Mutable", "Param", "Scalar", "TensorType", "Vector",
+__all__ = ["Grid", "HawkError", "Index", "Matrix", "Mutable", "Param", "Scalar", "Table", "TensorType", "Vector",
            "__version__", *_LAZY, *_SUBMODULES]
 
 

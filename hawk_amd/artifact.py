@@ -126,6 +126,7 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
             "scalar_type": mode, "planes": plan.planes, "team": plan.team,
             "launch": {"block": shape[0], "per_thread": shape[1], "nontemporal": nontemporal},
             "grid": [list(a) for a in k.program.grid.axes] if k.program.grid is not None else None,
+            "tables": {t: [list(a) for a in axes] for t, axes in k.program.tables.items()},
             "entry": None, "arg_spec": [], "descriptor": [],
         }
         if plan.stage is not None:

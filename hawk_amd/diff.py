@@ -161,6 +161,8 @@ class _Reverse:
         self.deps = Deps()
         self.targets = active_targets      # uids of the leaves being differentiated
         self.active_memo: dict = {}
+        self.scatters: list = []           # (table name, contribution, flat cell) of table reads
+        self.depth = 0                     # loop bodies being reversed
 
     def active(self, n: Node) -> bool:
         hit = self.active_memo.get(n.uid)
@@ -213,7 +215,17 @@ class _Reverse:
                             self._accumulate(store, child, g)
                 continue
             g = store.get(n.uid)
-            if g is None or n.kind in _TERMINAL:
+            if g is None:
+                continue
+            if n.kind == "gather" and n.literal is not None and n.operands[0].uid in self.targets:
+                # the reverse of a table read is a scatter-add into the table's
+                # adjoint at the cell it read (reference hawk/diff/transform.py:695-705)
+                if self.depth:
+                    raise HawkError(f"the gradient of a read of the table {n.operands[0].literal[1]!r} inside a for "
+                                    "loop is not in this build (a scatter per iteration)")
+                self.scatters.append((n.operands[0].literal[1], g, make("table_index", n.operands, n.literal)))
+                continue
+            if n.kind in _TERMINAL:
                 continue
             for child, contribution in _vjp_rule(n, g):
                 if self.active(child):
@@ -235,7 +247,11 @@ class _Reverse:
         accs = tuple(Node("carry", (), f.ttype, (uid, m + i)) for i, f in enumerate(free))
         stops = frozenset(t.uid for t in tapes) | frozenset(f.uid for f in free)
         live = [(b, bar) for b, bar in zip(body, bars)]
-        inner = self.pullback(body, live, stops)
+        self.depth += 1
+        try:
+            inner = self.pullback(body, live, stops)
+        finally:
+            self.depth -= 1
         nexts = tuple(inner.get(t.uid) if inner.get(t.uid) is not None else zero_like(c.ttype)
                       for t, c in zip(tapes, info.carries))
         nexts += tuple(_o("add", acc, inner[f.uid]) if inner.get(f.uid) is not None else acc
@@ -324,7 +340,8 @@ def _differentiable_inputs(program: Program, wrt, params: bool = False) -> list:
     ``params``, a ``Param`` may be named too (a reverse-mode gradient of a
     parameter is a cell summed over samples)."""
     inputs = [d for d in program.decls.values()
-              if d.role in ("per_sample", "vec_in", "mat_in") and d.ttype.dtype in ("f64", "f32")]
+              if (d.role in ("per_sample", "vec_in", "mat_in") or d.name in program.tables)
+              and d.ttype.dtype in ("f64", "f32")]
     if wrt is None:
         return inputs
     wrt = (wrt,) if isinstance(wrt, str) else tuple(wrt)
@@ -381,7 +398,7 @@ def vjp(kernel, wrt=None) -> Program:
     leaf_nodes = {n.literal[1]: n for n in ir.leaves_of(roots)}
     target_leaves = [leaf_nodes[d.name] for d in targets if d.name in leaf_nodes]
     rev = _Reverse({n.uid for n in target_leaves})
-    out = Program(grid=program.grid)
+    out = Program(grid=program.grid, tables=dict(program.tables))
     seeds = []
     for s in program.sinks:
         seed_name = name(s.name)
@@ -390,10 +407,19 @@ def vjp(kernel, wrt=None) -> Program:
         seeds.append((s.value, seed))
     store = rev.pullback(roots, seeds)
     for d in program.decls.values():
-        if d.role in ("per_sample", "vec_in", "mat_in", "uniform"):
+        if d.role in ("per_sample", "vec_in", "mat_in", "uniform", "lookup"):
             out.decls.setdefault(d.name, d)
     for d in targets:
         grad_name = name(d.name)
+        if d.name in program.tables:
+            # a table's gradient: every read's contribution added at the cell
+            # it read, in the ordered scatter's order (one stage per read site)
+            out.decls[grad_name] = Decl(grad_name, "mutable", TensorType((), "f64"))
+            out.tables[grad_name] = program.tables[d.name]
+            for table, contribution, cell in rev.scatters:
+                if table == d.name:
+                    out.sinks.append(AccumWrite(grad_name, contribution, cell, "ordered"))
+            continue
         lf = leaf_nodes.get(d.name)
         g = store.get(lf.uid) if lf is not None else None
         if g is None:
@@ -432,6 +458,12 @@ class _Forward:
     def _rule(self, n: Node):
         k, ops = n.kind, n.operands
         t = self.t
+        if n.ttype.dtype in ("i32", "i64", "bool"):
+            return None                   # an index or a mask carries no tangent
+        if k == "gather" and n.literal is not None and t(ops[0]) is not None:
+            # the tangent of a table read is the same clamped read of the
+            # table's tangent plane (reference tests/test_diff_cross_sample.py:66-80)
+            return make("gather", (t(ops[0]), *ops[1:]), n.literal)
         if k in _TERMINAL:
             return None
         if k == "add":
@@ -541,14 +573,16 @@ def jvp(kernel, wrt=None) -> Program:
     targets = _differentiable_inputs(program, wrt)
     roots = [s.value for s in program.sinks]
     leaf_nodes = {n.literal[1]: n for n in ir.leaves_of(roots)}
-    out = Program(grid=program.grid)
+    out = Program(grid=program.grid, tables=dict(program.tables))
     for d in program.decls.values():
-        if d.role in ("per_sample", "vec_in", "mat_in", "uniform"):
+        if d.role in ("per_sample", "vec_in", "mat_in", "uniform", "lookup"):
             out.decls.setdefault(d.name, d)
     tangent_leaves = {}
     for d in targets:
         tname = name(d.name)
         out.decls[tname] = Decl(tname, d.role, d.ttype)
+        if d.name in program.tables:
+            out.tables[tname] = program.tables[d.name]
         if d.name in leaf_nodes:
             tangent_leaves[leaf_nodes[d.name].uid] = ir.leaf(d.role, tname, d.ttype)
     fwd = _Forward(tangent_leaves)

@@ -191,12 +191,55 @@ class _Writer:
         q = "hk_i" if div == 1 else f"(hk_i / {div}LL)"
         return [self.let("i32", f"static_cast<int>({q})" if mod is None else f"static_cast<int>({q} % {mod}LL)", "ax")]
 
-    def _gather(self, n: Node) -> list:
-        # one guarded read of the table (kept in cache: many samples share a
-        # cell); a key outside [0, cells), the skip key -1 included, reads 0
-        table, key = n.operands
+    def _floordiv(self, n: Node) -> list:
+        a, b = self.scalar(n.operands[0]), self.scalar(n.operands[1])
+        ct = self.ctype(n.ttype.dtype)
+        q = self.let(n.ttype.dtype, f"static_cast<{ct}>({a}) / static_cast<{ct}>({b})", "q")
+        # toward minus infinity, as Python's //
+        return [self.let(n.ttype.dtype, f"({q} * static_cast<{ct}>({b}) != static_cast<{ct}>({a}) && "
+                                        f"((static_cast<{ct}>({a}) < 0) != (static_cast<{ct}>({b}) < 0))) ? {q} - 1 : {q}", "q")]
+
+    def _mod(self, n: Node) -> list:
+        a, b = self.scalar(n.operands[0]), self.scalar(n.operands[1])
+        ct = self.ctype(n.ttype.dtype)
+        r = self.let(n.ttype.dtype, f"static_cast<{ct}>({a}) % static_cast<{ct}>({b})", "r")
+        # the sign of the divisor, as Python's %
+        return [self.let(n.ttype.dtype, f"({r} != 0 && (({r} < 0) != (static_cast<{ct}>({b}) < 0))) ? {r} + "
+                                        f"static_cast<{ct}>({b}) : {r}", "r")]
+
+    def _clamped_flat(self, n: Node) -> str:
+        """The row-major flat cell of a clamped table read: each index clamped
+        into [0, extent) of its axis (the first axis's extent from the bound
+        cells when it is a runtime one)."""
+        table, *keys = n.operands
         p = self.value(table)[0]
-        k = self.scalar(key)
+        extents = n.literal[1]
+        rest = 1
+        for e in extents[1:]:
+            rest *= e
+        flat = None
+        for j, (k, e) in enumerate(zip(keys, extents)):
+            extent = f"(static_cast<long long>({p}_n) / {rest}LL)" if e is None else f"{e}LL"
+            idx = self.let("i64", f"static_cast<long long>({self.scalar(k)})", "k")
+            c = self.let("i64", f"{idx} < 0 ? 0LL : ({idx} >= {extent} ? {extent} - 1 : {idx})", "k")
+            stride = 1
+            for e2 in extents[j + 1:]:
+                stride *= e2
+            term = c if stride == 1 else f"{c} * {stride}LL"
+            flat = term if flat is None else f"{flat} + {term}"
+        return self.let("i64", flat, "cell")
+
+    def _table_index(self, n: Node) -> list:
+        return [self.let("i32", f"static_cast<int>({self._clamped_flat(n)})", "cell")]
+
+    def _gather(self, n: Node) -> list:
+        # one read of the table (kept in cache: many samples share a cell)
+        table = n.operands[0]
+        p = self.value(table)[0]
+        if n.literal is not None:                      # a Table read: clamped, never out of the plane
+            return [self.let(n.ttype.dtype, f"{p}[{self._clamped_flat(n)}]", "g")]
+        # a scatter target's adjoint: a key outside [0, cells), the skip key -1 included, reads 0
+        k = self.scalar(n.operands[1])
         return [self.let(n.ttype.dtype, f"static_cast<unsigned long long>(static_cast<long long>({k})) < {p}_n"
                                         f" ? {p}[{k}] : Real(0)", "g")]
 
@@ -478,7 +521,7 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
     for _, _, hi, comp in rows:
         for pname in (hi, comp):
             decls[pname] = ir.Decl(pname, "rows_out", ir.TensorType((), "f64"))
-    prog2 = Program(decls, program.sinks, program.grid)
+    prog2 = Program(decls, program.sinks, program.grid, program.tables)
     spec = ir.arg_spec(prog2, used)
     for role, name in spec:
         d = decls[name]
@@ -752,7 +795,7 @@ def _carry_repeats(program: Program) -> Program:
             sinks.append(dataclasses.replace(s, value=next(values), key=next(new_keys)))
         else:
             sinks.append(dataclasses.replace(s, value=next(values)))
-    return Program(program.decls, sinks, program.grid)
+    return Program(program.decls, sinks, program.grid, program.tables)
 
 
 def plan_kernel(program: Program, name: str, mode: str = "float64", block: int = 256,
@@ -806,9 +849,14 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
             if src is None and s.value.kind == "leaf" and s.value.literal[0] == "per_sample":
                 src = s.value.literal[1]
             if src is None:
-                src = f"hk_scatter_{s.name}"
+                src = f"hk_scatter_{s.name}_{len(team)}"
                 extra.append((src, s.value))
-            team.append({"op": "ordered_scatter", "key": s.key.literal[1], "v": src, "target": s.name})
+            if s.key.kind == "leaf" and s.key.literal[0] == "per_sample":
+                key = s.key.literal[1]
+            else:                                   # a computed key (a table read's cell): stored by the stage
+                key = f"hk_key_{s.name}_{len(team)}"
+                extra.append((key, s.key))
+            team.append({"op": "ordered_scatter", "key": key, "v": src, "target": s.name})
     has_stage = any(isinstance(s, Assign) for s in program.sinks) or extra or row_sums
     stage = source = None
     if has_stage:

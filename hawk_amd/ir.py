@@ -117,9 +117,20 @@ def as_real(n: Node) -> Node:
     return Node("real", (n,), TensorType(n.ttype.shape, "f64"))
 
 
+_INTS = ("i32", "i64")
+
+
 def make(kind: str, operands: tuple, literal=None) -> Node:
     """Build a node of ``kind``, typing it from its operands."""
     ops = tuple(operands)
+    if kind in ("add", "sub", "mul", "floordiv", "mod") and all(
+            o.ttype.dtype in _INTS and not o.ttype.shape for o in ops):
+        # index arithmetic stays integer (64-bit when either side is); floordiv
+        # and mod round toward minus infinity, as Python's // and %
+        dt = "i64" if any(o.ttype.dtype == "i64" for o in ops) else "i32"
+        return Node(kind, ops, TensorType((), dt))
+    if kind in ("floordiv", "mod"):
+        raise HawkError(f"{'//' if kind == 'floordiv' else '%'} takes two Index values (integers)")
     if kind in BINARY:
         a, b = (as_real(o) for o in ops)
         return Node(kind, (a, b), TensorType(_broadcast(a.ttype, b.ttype, kind), _real_dtype(a, b)))
@@ -230,14 +241,27 @@ def make(kind: str, operands: tuple, literal=None) -> Node:
             return Node(kind, (), TensorType((), "i64"), (1, 0))
         return Node(kind, (), TensorType((), "i32"), (int(div), None if mod is None else int(mod)))
     if kind == "gather":
-        # table[key] of a 1-D plane of cells (role "lookup"); a key outside
-        # [0, cells) — the skip key -1 of hawk.scatter among them — reads 0
-        table, key = ops
+        # table[key] of a 1-D plane of cells (role "lookup").  literal None: a
+        # key outside [0, cells) — the skip key -1 of hawk.scatter among them —
+        # reads 0.  literal ("clamp", extents): the key is one index per axis
+        # of a table of those extents (None: the first axis's, from the bound
+        # cells), each clamped into [0, extent), read at their row-major flat
+        # position (a Table read, reference tests/test_table_clamp.py:1-8).
+        table, *keys = ops
         if table.kind != "leaf" or table.literal[0] != "lookup" or table.ttype.shape:
             raise HawkError("gather reads a scalar lookup plane (a 1-D plane of cells)")
-        if key.ttype != TensorType((), "i32"):
-            raise HawkError(f"gather: the key is an Index, got {key.ttype!r}")
-        return Node(kind, (table, key), TensorType((), table.ttype.dtype))
+        if any(k.ttype.dtype not in _INTS or k.ttype.shape for k in keys):
+            raise HawkError(f"gather: a key is an Index (an integer), got {[k.ttype for k in keys]}")
+        if literal is None and len(keys) != 1:
+            raise HawkError("gather: one key")
+        if literal is not None and (literal[0] != "clamp" or len(literal[1]) != len(keys)):
+            raise HawkError("gather: one key per table axis")
+        return Node(kind, (table, *keys), TensorType((), table.ttype.dtype), literal)
+    if kind == "table_index":
+        # the flat cell a clamped table read reads (the key of its gradient's
+        # scatter, an Index): the same clamp and row-major flattening as the gather
+        table, *keys = ops
+        return Node(kind, (table, *keys), TensorType((), "i32"), literal)
     raise HawkError(f"no IR kind {kind!r}")
 
 
@@ -459,6 +483,7 @@ class Program:
     decls: dict = field(default_factory=dict)     # name -> Decl, declaration order
     sinks: list = field(default_factory=list)
     grid: object = None                           # the GridDecl of the launch's lane axes, if declared
+    tables: dict = field(default_factory=dict)    # a Table plane's name -> its axes ((label, extent|None), ...)
 
 
 # --------------------------------------------------------------------------

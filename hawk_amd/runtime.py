@@ -147,9 +147,19 @@ class DeviceKernel:
                 if x.dim() != 1:
                     problems.append(f"{name!r} is the 1-D plane of cells hawk.scatter adds into")
             elif role == "lookup":
-                if x.dim() != 1:
+                axes = (self.sidecar.get("tables") or {}).get(name)
+                if x.dim() != 1 and axes is None:
                     problems.append(f"{name!r} is a 1-D plane of cells read at a key (the adjoint of a "
                                     "hawk.scatter target): bind one value per cell")
+                elif axes is not None:
+                    rest, first = 1, axes[0][1]
+                    for _, e in axes[1:]:
+                        rest *= e
+                    cells = int(x.numel())
+                    if cells == 0 or cells % rest or (first is not None and cells != first * rest):
+                        problems.append(f"{name!r} is a Table{[tuple(a) for a in axes]}: bind "
+                                        + (f"{first * rest}" if first is not None else f"a nonzero multiple of {rest}")
+                                        + f" cells, got {cells} (a read clamps into the table, so it needs a cell)")
         if n_grid is not None:
             if n is not None and n != n_grid:
                 problems.append(f"the Grid's extents give {n_grid} lanes, the planes {n}")
@@ -202,7 +212,8 @@ class DeviceKernel:
             if info.get("rows"):                       # one row partial per `rows` samples
                 held = torch.empty(max(1, -(-n // info["rows"])), dtype=torch.float64, device=device)
             else:
-                held = torch.empty(lead + (n,), dtype=self._real_dtype(), device=device)
+                held = torch.empty(lead + (n,), dtype=torch.int32 if info["dtype"] == "i32" else self._real_dtype(),
+                                   device=device)
             self._scratch[key] = held
         return held
 

@@ -26,7 +26,7 @@ from typing import Any
 
 from . import ir
 from .ir import AccumWrite, Assign, Decl, HawkError, Node, Program, SampleSum, make
-from .types import GridDecl, MutableDecl, TensorType, _ParamDecl, role_of
+from .types import GridDecl, MutableDecl, TableDecl, TensorType, _ParamDecl, role_of
 
 SUM_POLICIES = ("auto", "compensated", "ordered")
 SCATTER_POLICIES = ("ordered",)
@@ -64,8 +64,20 @@ def _projected(n: Node) -> Node:
     return make("chol_factor", (n,)) if n.ttype.tag == "chol_factor" else n
 
 
+def _is_index(x: Any) -> bool:
+    return isinstance(x, Value) and x.node.ttype.dtype in ("i32", "i64") and not x.node.ttype.shape
+
+
+def _operand(x: Any, other: Any) -> Node:
+    """``x`` as an operand beside ``other``: a Python int beside an Index is
+    an integer constant (index arithmetic), otherwise a number."""
+    if isinstance(x, int) and not isinstance(x, bool) and _is_index(other):
+        return ir.index_const(x)
+    return _projected(node_of(x))
+
+
 def _bin(kind: str, a: Any, b: Any) -> Value:
-    return Value(make(kind, (_projected(node_of(a)), _projected(node_of(b)))))
+    return Value(make(kind, (_operand(a, b), _operand(b, a))))
 
 
 class Value:
@@ -91,6 +103,10 @@ class Value:
     def __rsub__(self, o): return _bin("sub", o, self)
     def __mul__(self, o): return _bin("mul", self, o)
     def __rmul__(self, o): return _bin("mul", o, self)
+    def __floordiv__(self, o): return _bin("floordiv", self, o)
+    def __rfloordiv__(self, o): return _bin("floordiv", o, self)
+    def __mod__(self, o): return _bin("mod", self, o)
+    def __rmod__(self, o): return _bin("mod", o, self)
     def __truediv__(self, o): return _bin("div", self, o)
     def __rtruediv__(self, o): return _bin("div", o, self)
     def __neg__(self): return Value(make("neg", (_projected(self.node),)))
@@ -189,6 +205,56 @@ class Reduced:
 
 # --------------------------------------------------------------------------
 # cross-sample vocabulary
+
+
+class TableRef:
+    """A ``Table`` parameter: ``t.at(i)`` / ``t[i]`` reads the flat cell i;
+    ``t.at(row=r, col=c)`` / ``t[r, c]`` reads one index per declared axis in
+    declared order.  Each index is clamped into its axis, so a read outside the
+    table reads its edge (reference tests/test_table_clamp.py:1-8,
+    tests/test_table_positional.py:1-9)."""
+
+    def __init__(self, name: str, decl: TableDecl):
+        self._name, self._decl = name, decl
+        self._leaf = ir.leaf("lookup", name, TensorType((), "f64"))
+
+    def _key(self, x: Any) -> Node:
+        if isinstance(x, int) and not isinstance(x, bool):
+            return ir.index_const(x)
+        if _is_index(x):
+            return x.node
+        raise HawkError(f"{self._name!r}: a table index is an Index (an integer), got {x!r}")
+
+    def _read(self, keys: list, extents: tuple) -> Value:
+        return Value(make("gather", (self._leaf, *[self._key(k) for k in keys]), ("clamp", tuple(extents))))
+
+    def at(self, *positional: Any, **named: Any) -> Value:
+        axes = self._decl.axes
+        labels = [a for a, _ in axes]
+        if named:
+            if positional or set(named) != set(labels):
+                raise HawkError(f"{self._name!r}.at(...) names every axis {labels} once, got "
+                                f"{list(named)} with {len(positional)} positional")
+            return self._read([named[a] for a in labels], tuple(e for _, e in axes))
+        if len(positional) == 1:
+            return self._read([positional[0]], (None,))          # the flat read over every cell
+        if len(positional) == len(axes):
+            return self._read(list(positional), tuple(e for _, e in axes))
+        raise HawkError(f"{self._name!r}: {self._name}.at(...) takes one flat index or one index per declared "
+                        f"axis {labels}, got {len(positional)}")
+
+    def __getitem__(self, idx: Any) -> Value:
+        items = idx if isinstance(idx, tuple) else (idx,)
+        labels = [a for a, _ in self._decl.axes]
+        if len(items) not in (1, len(labels)):
+            raise HawkError(f"{self._name!r}: {self._name}[...] takes one index per declared axis {labels}, "
+                            f"got {len(items)}")
+        return self.at(*items)
+
+    def _refuse(self, *_):
+        raise HawkError(f"{self._name!r} is a Table: read it with {self._name}.at(...) or {self._name}[...]")
+
+    __add__ = __radd__ = __sub__ = __rsub__ = __mul__ = __rmul__ = __truediv__ = __neg__ = _refuse
 
 
 class LaneRef:
@@ -532,7 +598,11 @@ def trace(fn, scope: dict | None = None) -> Program:
         if ann is inspect.Parameter.empty:
             raise HawkError(f"{fn.__name__}: parameter {p.name!r} has no declaration "
                             "(Scalar, Vector[n], Matrix[r, c], Index, Param, Mutable[...])")
-        if isinstance(ann, GridDecl):
+        if isinstance(ann, TableDecl):
+            program.decls[p.name] = Decl(p.name, "lookup", TensorType((), "f64"))
+            program.tables[p.name] = ann.axes
+            args.append(TableRef(p.name, ann))
+        elif isinstance(ann, GridDecl):
             if program.grid is not None:
                 raise HawkError(f"{fn.__name__}: one Grid parameter declares the lanes; {p.name!r} is a second")
             program.grid = ann

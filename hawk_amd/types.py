@@ -142,6 +142,34 @@ Mutable = _MutableFactory()
 
 
 @dataclass(frozen=True)
+class TableDecl:
+    """``Table[Scalar]`` (a 1-D plane of cells read at a flat index) or
+    ``Table["row":R, "col":C]`` (read ``t.at(row=..., col=...)`` or
+    ``t[r, c]``; a bare first label is a runtime extent): a lookup plane any
+    lane reads at any cell (reference ``hawk/trace/decl.py:117-132``).  Every
+    index is clamped into its axis: a read outside the table reads its edge."""
+
+    axes: tuple                  # (("label", extent or None), ...); (("cell", None),) for Table[Scalar]
+    positional: bool = False
+
+
+class _TableFactory:
+    def __getitem__(self, key) -> TableDecl:
+        if isinstance(key, TensorType):
+            if key.shape or key.dtype != "f64":
+                raise HawkError(f"Table[...] holds Scalar cells in this build, got {key!r}")
+            return TableDecl((("cell", None),), positional=True)
+        items = key if isinstance(key, tuple) else (key,)
+        return TableDecl(_axes("Table[...]", items))
+
+    def __repr__(self) -> str:
+        return "Table"
+
+
+Table = _TableFactory()
+
+
+@dataclass(frozen=True)
 class GridDecl:
     """``Grid["key", "sample":8192]``: the launch's lanes as a grid of axes, the
     last the fastest (consecutive lanes); only the first may have a runtime

@@ -115,6 +115,21 @@ class Evaluator:
                 return idx
             q = idx // div
             return (q if mod is None else q % mod).astype(np.int32)
+        if k in ("floordiv", "mod"):
+            a, b = self._op(m, 0), self._op(m, 1)
+            return (np.floor_divide if k == "floordiv" else np.mod)(a, b)
+        if k in ("gather", "table_index") and m.literal is not None:
+            table = np.asarray(self._op(m, 0)).reshape(-1)
+            keys = [np.broadcast_to(np.asarray(self._op(m, j), dtype=np.int64), (n,)) for j in range(1, len(m.operands))]
+            extents = list(m.literal[1])
+            rest = int(np.prod([e for e in extents[1:]] or [1]))
+            if extents[0] is None:
+                extents[0] = table.shape[0] // rest
+            flat = np.zeros(n, dtype=np.int64)
+            for j, (key, e) in enumerate(zip(keys, extents)):
+                stride = int(np.prod(extents[j + 1:] or [1]))
+                flat = flat + np.clip(key, 0, e - 1) * stride
+            return flat if k == "table_index" else table[flat]
         if k == "gather":
             table, key = self._op(m, 0), self._op(m, 1)
             ok = (key >= 0) & (key < table.shape[0])

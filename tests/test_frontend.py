@@ -556,3 +556,99 @@ def test_keyed_sum_plans_a_keyed_team_stage_and_its_derivatives(tmp_path):
     assert got.tobytes() == np.repeat(bar, 8).tobytes()
     fwd = jvp(keyed_rows, wrt=("x",))
     assert [(type(s).__name__, s.name, s.group) for s in fwd.sinks] == [("SampleSum", "dot_y", 8)]
+
+
+# -- Table reads and their derivatives ------------------------------------------------------
+
+@hawk.kernel
+def table_pick(table: hawk.Table[Scalar], where: hawk.Index, x: Scalar, y: Mutable[Scalar]):
+    y = table.at(where) * x + table.at(where - 1000) + table[where + 3] * table[where // 2]
+
+
+@hawk.kernel
+def table_grid(lane: hawk.Grid["e", "a":4], t: hawk.Table["e":8, "a":4], x: Scalar) -> Scalar:
+    return t.at(e=lane.e, a=lane.a) * x + t[lane.a, lane.e] + t[lane.flat % 5]
+
+
+def _scatter_eval(program, env, n, target):
+    """The table gradient ``target`` of a derived program: every read site's
+    per-sample contribution added at its cell (numpy's add.at)."""
+    from ir_eval import Evaluator
+    ev = Evaluator(env, n)
+    out = np.zeros(np.asarray(env[target[4:]]).size)
+    for s in program.sinks:
+        if s.name == target:
+            np.add.at(out, ev.value(s.key), ev.value(s.value))
+    return out
+
+
+def test_table_reads_clamp_every_index_into_the_table():
+    """A read outside the table reads its edge (reference
+    tests/test_table_clamp.py:1-8); t[i] is the flat read, t[r, c] / t.at(r=, c=)
+    one index per axis in declared order; // and % on indices are Python's."""
+    n = 400
+    g = np.random.default_rng(5)
+    table = g.normal(size=37)
+    where = g.integers(-50, 90, n).astype(np.int32)
+    x = g.normal(size=n)
+    got = evaluate(table_pick.program, {"table": table, "where": where, "x": x}, n)["y"]
+    c = lambda i: table[np.clip(i, 0, 36)]
+    want = c(where) * x + c(where - 1000) + c(where + 3) * c(where // 2)
+    assert got.tobytes() == want.tobytes()
+    t = g.normal(size=(8, 4))
+    m = 8 * 4 * 3                       # lanes past the table's first extent read its last row
+    xg = g.normal(size=m)
+    got = evaluate(table_grid.program, {"t": t, "x": xg}, m)["out"]
+    i = np.arange(m)
+    e, a = i // 4, i % 4
+    want = t[np.clip(e, 0, 7), a] * xg + t[np.clip(a, 0, 7), np.clip(e, 0, 3)] + t.reshape(-1)[i % 5]
+    assert got.tobytes() == want.tobytes()
+    with pytest.raises(HawkError, match=r"takes one index per declared axis \['e', 'a'\], got 3"):
+        @hawk.kernel
+        def wrong(lane: hawk.Grid["e", "a":4], t: hawk.Table["e":8, "a":4]) -> Scalar:
+            return t[lane.e, lane.a, 0]
+
+
+def test_table_read_vjp_scatters_to_the_cells_read_and_matches_finite_differences():
+    """vjp wrt a table: each read site adds its contribution at the cell it
+    read, as an ordered scatter into bar_<table> (reference
+    tests/test_diff_cross_sample.py:40-63); central differences on table
+    entries agree, and wrt=x stays a per-sample gradient."""
+    from hawk_amd.emit_hip import plan_kernel
+    n = 300
+    g = np.random.default_rng(6)
+    table = g.normal(size=37)
+    where = g.integers(-5, 45, n).astype(np.int32)
+    x, bar_y = g.normal(size=n), g.normal(size=n)
+    back = vjp(table_pick, wrt=("table", "x"))
+    kinds = sorted((type(s).__name__, s.name) for s in back.sinks)
+    assert kinds.count(("AccumWrite", "bar_table")) == 4 and ("Assign", "bar_x") in kinds
+    env = {"table": table, "where": where, "x": x, "bar_y": bar_y}
+    bar_table = _scatter_eval(back, env, n, "bar_table")
+
+    def loss(tab):
+        return float(bar_y @ evaluate(table_pick.program, {"table": tab, "where": where, "x": x}, n)["y"])
+    h = 1e-6
+    for cell in (0, 3, 17, 36):
+        up, dn = table.copy(), table.copy()
+        up[cell] += h
+        dn[cell] -= h
+        np.testing.assert_allclose((loss(up) - loss(dn)) / (2 * h), bar_table[cell], rtol=1e-6, atol=1e-8)
+    p = plan_kernel(back, "pick_vjp")
+    scatters = [t for t in p.team if t["op"] == "ordered_scatter"]
+    assert len(scatters) == 4 and all(t["key"].startswith("hk_key_bar_table") for t in scatters)
+    assert p.planes[scatters[0]["key"]]["dtype"] == "i32"
+
+
+def test_table_read_jvp_reads_the_tangent_table():
+    fwd = jvp(table_pick, wrt=("table",))
+    assert fwd.decls["dot_table"].role == "lookup" and fwd.tables["dot_table"] == (("cell", None),)
+    n = 200
+    g = np.random.default_rng(7)
+    table, dt = g.normal(size=37), g.normal(size=37)
+    where = g.integers(-5, 45, n).astype(np.int32)
+    x = g.normal(size=n)
+    got = evaluate(fwd, {"table": table, "dot_table": dt, "where": where, "x": x}, n)["dot_y"]
+    h = 1e-6
+    f = lambda tab: evaluate(table_pick.program, {"table": tab, "where": where, "x": x}, n)["y"]
+    np.testing.assert_allclose(got, (f(table + h * dt) - f(table - h * dt)) / (2 * h), rtol=1e-6, atol=1e-8)

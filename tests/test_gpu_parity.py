@@ -715,3 +715,77 @@ def test_keyed_sum_derivatives_and_lane_coordinates_on_the_device(gpu, tmp_path)
     yi = dev(np.zeros(1000), gpu)
     hawk.run(hawk.load(tmp_path, "iota"), key=1000, y=yi)
     assert np.all(host(yi) == 120.0)
+
+
+# -- Table reads and their derivatives -------------------------------------------------------
+
+def _table_kernels():
+    import hawk_amd as hawk
+    from hawk_amd import Grid, Index, Mutable, Scalar, Table
+
+    @hawk.kernel
+    def tpick(table: Table[Scalar], where: Index, x: Scalar, y: Mutable[Scalar]):
+        y = table.at(where) * x + table.at(where - 1000) + table[where + 3] * table[where // 2]
+
+    @hawk.kernel
+    def tgrid(lane: Grid["e", "a":4], t: Table["e":8, "a":4], x: Scalar) -> Scalar:
+        return t.at(e=lane.e, a=lane.a) * x + t[lane.a, lane.e] + t[lane.flat % 5]
+    return tpick, tgrid
+
+
+def test_table_reads_and_derivatives_on_the_device(gpu, tmp_path):
+    """Clamped Table reads (reference tests/test_table_clamp.py) bit for bit
+    against numpy; the VJP wrt the table is the ordered scatter of each read
+    site's contribution at the cell it read (the oracle's walk of the IR's
+    contributions, bit for bit), bar_x and the JVP the IR's bits; an empty
+    table is refused."""
+    import hawk_amd as hawk
+    from hawk_amd import HawkError
+    from hawk_amd.diff import jvp, vjp
+    from hawk_amd.trace import Kernel
+    from ir_eval import Evaluator, evaluate
+    tpick, tgrid = _table_kernels()
+    back = Kernel("tpick_vjp", vjp(tpick, wrt=("table", "x")))
+    fwd = Kernel("tpick_jvp", jvp(tpick, wrt=("table",)))
+    hawk.build([tpick, tgrid, back, fwd], tmp_path)
+    n, cells = 200_003, 4099
+    g = rng(31)
+    table, dt = g.normal(size=cells), g.normal(size=cells)
+    where = g.integers(-100, cells + 100, n).astype(np.int32)
+    x, bar_y = g.normal(size=n), g.normal(size=n)
+    env = {"table": table, "where": where, "x": x}
+    T, W, X = dev(table, gpu), dev(where, gpu), dev(x, gpu)
+    y = dev(np.full(n, np.nan), gpu)
+    hawk.run(hawk.load(tmp_path, "tpick"), table=T, where=W, x=X, y=y)
+    c = lambda i: table[np.clip(i, 0, cells - 1)]
+    assert host(y).tobytes() == (c(where) * x + c(where - 1000) + c(where + 3) * c(where // 2)).tobytes()
+
+    bt = dev(np.zeros(cells), gpu)
+    bx = dev(np.full(n, np.nan), gpu)
+    print("table vjp", flush=True)
+    hawk.run(hawk.load(tmp_path, "tpick_vjp"), table=T, where=W, x=X, bar_y=dev(bar_y, gpu), bar_table=bt,
+             bar_x=bx)
+    genv = {**env, "bar_y": bar_y}
+    ev = Evaluator(genv, n)
+    want = np.zeros(cells)
+    for s in back.program.sinks:
+        if s.name == "bar_table":
+            want, status = O.ordered_scatter(ev.value(s.key).astype(np.int32), ev.value(s.value), want)
+            assert not status[1:].any()
+    assert host(bt).tobytes() == want.tobytes()
+    assert host(bx).tobytes() == evaluate(back.program, genv, n)["bar_x"].tobytes()
+
+    dy = dev(np.full(n, np.nan), gpu)
+    hawk.run(hawk.load(tmp_path, "tpick_jvp"), table=T, dot_table=dev(dt, gpu), where=W, x=X, dot_y=dy)
+    assert host(dy).tobytes() == evaluate(fwd.program, {**env, "dot_table": dt}, n)["dot_y"].tobytes()
+
+    m = 8 * 4 * 3
+    t2, xg = g.normal(size=(8, 4)), g.normal(size=m)
+    out = dev(np.zeros(m), gpu)
+    hawk.run(hawk.load(tmp_path, "tgrid"), t=dev(t2, gpu), x=dev(xg, gpu), out=out)
+    i = np.arange(m)
+    e, a = i // 4, i % 4
+    want2 = t2[np.clip(e, 0, 7), a] * xg + t2[np.clip(a, 0, 7), np.clip(e, 0, 3)] + t2.reshape(-1)[i % 5]
+    assert host(out).tobytes() == want2.tobytes()
+    with pytest.raises(HawkError, match="needs a cell"):
+        hawk.run(hawk.load(tmp_path, "tpick"), table=dev(np.zeros(0), gpu), where=W, x=X, y=y)
