@@ -6,7 +6,8 @@ resident in HBM.  The default workload is BASELINE.json's ``configs[1]``: the
 ``energy`` kernel's forward, VJP and JVP over N = 2^25 samples (fp64).  Other
 configurations (``--config 1|3|4a|4b|5``) time the remaining workloads the same
 way; ``--config 5k`` times config 5's ordered sum in the reference's keyed
-spelling (``hawk.sum(x, over=...)``) over 16384 keys.
+spelling (``hawk.sum(x, over=...)``) over 16384 keys, and ``--config 5t`` a
+``Table`` read at config 5's keys and its VJP (an ordered scatter).
 
 Each stage launch of the timed steps (a per-sample kernel, or a team stage:
 the ordered sum or the ordered scatter) is bracketed by HIP events on the
@@ -219,6 +220,43 @@ def workload(config: str, device):
             O.keyed_ordered_sum(x, group, threads=threads, profile="native")
         return dict(name="keyed ordered sum, 16384 keys x 4096 samples (config 5b, keyed)", n=n, kernels=kernels,
                     work=work, cpu=cpu, dtype="f64")
+    if config == "5t":
+        # a Table read at config 5's Zipf keys, y = table.at(key) * x, and its VJP wrt the table: the
+        # ordered scatter of bar_y * x at the cells read (reference tests/test_diff_cross_sample.py:40-63)
+        from hawk_amd.diff import vjp
+        from hawk_amd.trace import Kernel
+        n, cells = 1 << 26, 1 << 16
+        g = np.random.default_rng(5)
+        x = g.normal(size=n)
+        key = ((g.zipf(1.1, n) - 1) % cells).astype(np.int32)
+        table = np.random.default_rng(105).normal(size=cells)
+        bar_y = np.random.default_rng(205).normal(size=n)
+
+        @hawk.kernel
+        def lookup_scale(table: hawk.Table[hawk.Scalar], key: hawk.Index, x: hawk.Scalar,
+                         y: hawk.Mutable[hawk.Scalar]):
+            y = table.at(key) * x
+        back = Kernel("lookup_scale_vjp", vjp(lookup_scale, wrt=("table",)))
+        hawk.build([lookup_scale, back], unit)
+        kf, kv = hawk.load(unit, "lookup_scale"), hawk.load(unit, "lookup_scale_vjp")
+        T, K, X, BY = _dev(table, device), _dev(key, device), _dev(x, device), _dev(bar_y, device)
+        Y = torch.zeros(n, dtype=torch.float64, device=device)
+        BT = torch.zeros(cells, dtype=torch.float64, device=device)
+        kernels = [kf.prepare(table=T, key=K, x=X, y=Y), kv.prepare(table=T, key=K, x=X, bar_y=BY, bar_table=BT)]
+        # forward: key and x in, y out (the table stays in cache); the VJP's stage reads key, x and
+        # bar_y and writes the cell and the contribution the scatter reads (as config 5's scatter
+        # reads its key and y), and the scatter reads + writes every cell once
+        work = {"lookup_scale": (20, ops(kf)), "lookup_scale_vjp": (20 + 12, ops(kv)),
+                "ordered_scatter": (12 + 16 * cells / n, 1)}
+
+        def cpu(threads):
+            import oracle_lib as O
+            y = table[np.clip(key, 0, cells - 1)] * x
+            O.ordered_scatter(np.clip(key, 0, cells - 1).astype(np.int32), bar_y * x, np.zeros(cells),
+                              threads=threads)
+            return y
+        return dict(name="Table read at Zipf keys + its VJP wrt the table (config 5, tables)", n=n,
+                    kernels=kernels, work=work, cpu=cpu, dtype="f64")
     raise SystemExit(f"unknown --config {config!r}")
 
 
