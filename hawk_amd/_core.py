@@ -63,6 +63,8 @@ def _declare(lib) -> None:
         "hk_keyed_ordered_sum_scratch_bytes": (SZ, [I64, I64]),
         "hk_keyed_ordered_sum_f64": (I, [V, I64, I64, V, V, V]),
         "hk_mm16_f32": (I, [ctypes.POINTER(V), I, ctypes.POINTER(V), I, ctypes.POINTER(ctypes.c_int32), I64, V]),
+        "hk_keyed_log_fold_scratch_bytes": (SZ, [I64]),
+        "hk_keyed_log_fold_f64": (I, [V, I64, V, I64, I64, ctypes.c_int32, V, I64, V, V, V]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -317,6 +319,21 @@ def keyed_ordered_sum(u: int, n: int, group: int, out: int, scratch: int, stream
     """``out[k]`` = key k's ``group`` rows by the ordered sum's tree, k < n / group."""
     check(lib().hk_keyed_ordered_sum_f64(ctypes.c_void_p(u or None), int(n), int(group), ctypes.c_void_p(out),
                                          ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
+
+
+def keyed_log_fold_scratch_bytes(cells: int) -> int:
+    return int(lib().hk_keyed_log_fold_scratch_bytes(int(cells)))
+
+
+def keyed_log_fold(values: int, stride: int, cells_log: int, keys: int, rows: int, width: int, out: int,
+                   cells: int, scratch: int, status: int, stream: int = 0) -> None:
+    """``out[cells_log[e*keys + k]]`` = key k's ``rows`` contributions of slot e
+    (``values[e*stride + k*rows + r]``) added in lane order from +0; status[0]
+    bit 0 = a cell outside ``[0, cells)``, bit 1 = a cell named twice."""
+    check(lib().hk_keyed_log_fold_f64(ctypes.c_void_p(values or None), int(stride), ctypes.c_void_p(cells_log or None),
+                                      int(keys), int(rows), int(width), ctypes.c_void_p(out or None), int(cells),
+                                      ctypes.c_void_p(scratch or None), ctypes.c_void_p(status or None),
+                                      ctypes.c_void_p(stream or None)))
 
 
 def rows_finish_scratch_bytes(rows: int) -> int:

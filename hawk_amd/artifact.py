@@ -65,7 +65,7 @@ def _stage_bytes(plan, mode: str) -> int:
     size = 4 if mode == "float32" else 8
     total = 0
     for info in plan.stage.planes.values():
-        if info["role"] in ("uniform", "rows_out", "nsamples", "lookup"):   # lookup: per cell, cached
+        if info["role"] in ("uniform", "rows_out", "nsamples", "lookup", "key_out"):   # per cell / per key
             continue
         count = 1
         for e in info["shape"]:

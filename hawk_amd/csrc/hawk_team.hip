@@ -713,6 +713,99 @@ __global__ void hawk_scatter_status(int* status, long long cells) {
     if (t < kScatterChunks) status[1 + t] = 0;
 }
 
+// ---- the ordered gradient's log fold ----------------------------------------
+// reference hawk/emit/team.py:281-312 (`_fold`) and hawk/ir/team.py:684-693
+// (`fold_spec`): pair (key k, slot e) adds the key's `rows` contributions
+// v[e * stride + k * rows + r], r = 0, 1, ..., in lane order from +0.0, and
+// STORES the sum into out[cell_of[e * keys + k]].  Pairs run slot-major
+// (pair = e * keys + k), so neighbouring pairs read neighbouring runs of one
+// component plane.  A cell outside [0, cells) is not stored and sets status
+// bit 0; a cell that a second pair names sets bit 1 and lowers status[1] to
+// it (claims counts the pairs naming each cell): such stores race, as they do
+// in the reference, and the caller is told.
+
+__device__ __forceinline__ void log_fold_store(double s, int c, long long cells, double* __restrict__ out,
+                                               int* __restrict__ claims, int* __restrict__ status) {
+    if (c < 0 || c >= cells) {
+        atomicOr(status, 1);
+        return;
+    }
+    if (atomicAdd(claims + c, 1) != 0) {
+        atomicOr(status, 2);
+        atomicMin(status + 1, c);
+    }
+    out[c] = s;
+}
+
+// One thread per pair, for runs of at most 64 rows: the thread's loads are all
+// in flight before its adds.
+__global__ __launch_bounds__(256) void hawk_log_fold_lanes(const double* __restrict__ v, long long stride,
+                                                           const int* __restrict__ cell_of, long long keys,
+                                                           long long rows, long long pairs,
+                                                           double* __restrict__ out, long long cells,
+                                                           int* __restrict__ claims, int* __restrict__ status) {
+    const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= pairs) return;
+    const long long e = t / keys, k = t - e * keys;
+    const double* __restrict__ p = v + e * stride + k * rows;
+    constexpr int kAhead = 8;
+    double s = 0.0;
+    long long r = 0;
+    for (; r + kAhead <= rows; r += kAhead) {
+        double x[kAhead];
+#pragma unroll
+        for (int q = 0; q < kAhead; ++q) x[q] = p[r + q];
+#pragma unroll
+        for (int q = 0; q < kAhead; ++q) s = s + x[q];
+    }
+    for (; r < rows; ++r) s = s + p[r];
+    log_fold_store(s, cell_of[t], cells, out, claims, status);
+}
+
+__device__ __forceinline__ double lane_value(double x, int lane) {
+    const long long bits = __double_as_longlong(x);
+    const int lo = __builtin_amdgcn_readlane(static_cast<int>(bits), lane);
+    const int hi = __builtin_amdgcn_readlane(static_cast<int>(bits >> 32), lane);
+    return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned>(lo));
+}
+
+// One wave per pair, for longer runs: the wave loads 64 consecutive rows (one
+// 512-byte read) while it adds the previous 64 in lane order, every lane
+// holding the same running sum; lane 0 stores it.
+__global__ __launch_bounds__(256) void hawk_log_fold_waves(const double* __restrict__ v, long long stride,
+                                                           const int* __restrict__ cell_of, long long keys,
+                                                           long long rows, long long pairs,
+                                                           double* __restrict__ out, long long cells,
+                                                           int* __restrict__ claims, int* __restrict__ status) {
+    const long long pair = static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (pair >= pairs) return;                 // the whole wave
+    const int lane = threadIdx.x & 63;
+    const long long e = pair / keys, k = pair - e * keys;
+    const double* __restrict__ p = v + e * stride + k * rows;
+    double s = 0.0;
+    double x = lane < rows ? p[lane] : 0.0;
+    long long r0 = 0;
+    for (; r0 + 64 <= rows; r0 += 64) {
+        const double cur = x;
+        x = r0 + 64 + lane < rows ? p[r0 + 64 + lane] : 0.0;
+#pragma unroll
+        for (int j = 0; j < 64; ++j) s = s + lane_value(cur, j);
+    }
+    const int tail = static_cast<int>(rows - r0);
+    for (int j = 0; j < tail; ++j) s = s + lane_value(x, j);
+    if (lane == 0) log_fold_store(s, cell_of[pair], cells, out, claims, status);
+}
+
+__global__ __launch_bounds__(256) void hawk_log_fold_clear(int* __restrict__ claims, long long cells,
+                                                           int* __restrict__ status) {
+    const long long i0 = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i0 == 0) {
+        status[0] = 0;
+        status[1] = 0x7fffffff;
+    }
+    for (long long i = i0; i < cells; i += static_cast<long long>(gridDim.x) * 256) claims[i] = 0;
+}
+
 int launch_error(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hawk_internal::set_hip_error(what, e);
@@ -877,6 +970,50 @@ int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n, doubl
     hipLaunchKernelGGL(hawk_scatter_cells, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, parts, touched,
                        static_cast<long long>(cells), chunks, use_seen, target);
     return launch_error("hawk_scatter_cells launch");
+}
+
+size_t hk_keyed_log_fold_scratch_bytes(int64_t cells) {
+    return cells <= 0 ? 0 : sizeof(int) * static_cast<size_t>(cells);
+}
+
+int hk_keyed_log_fold_f64(const double* values, int64_t stride, const int32_t* cells_log, int64_t keys,
+                          int64_t rows, int32_t width, double* out, int64_t cells, void* scratch,
+                          int32_t* status, void* stream) {
+    if (keys < 0 || rows < 1 || width < 1 || cells < 0)
+        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: keys and cells must be >= 0, rows and "
+                                                   "width >= 1");
+    if (stride < keys * rows)
+        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: stride (" + std::to_string(stride) +
+                                                       ") is shorter than keys * rows (" +
+                                                       std::to_string(keys * rows) + ")");
+    if (!status) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: status is required");
+    const long long pairs = keys * static_cast<long long>(width);
+    if (pairs > 0 && (!values || !cells_log || !out || (cells > 0 && !scratch)))
+        return hawk_internal::set_error(HK_EVALUE,
+                                        "hk_keyed_log_fold_f64: values, cells_log, out and scratch are required");
+    if (cells > 0x7fffffffLL)
+        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: more than 2^31-1 cells");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto* claims = static_cast<int*>(scratch);
+    const long long clear = (cells + 255) / 256 < 1 ? 1 : ((cells + 255) / 256 < 4096 ? (cells + 255) / 256 : 4096);
+    hipLaunchKernelGGL(hawk_log_fold_clear, dim3(static_cast<unsigned>(clear)), dim3(256), 0, s, claims,
+                       static_cast<long long>(cells), status);
+    int rc = launch_error("hawk_log_fold_clear launch");
+    if (rc != HK_OK || pairs == 0) return rc;
+    if (rows <= 64) {
+        const long long blocks = (pairs + 255) / 256;
+        if (blocks > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: too many pairs");
+        hipLaunchKernelGGL(hawk_log_fold_lanes, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, values,
+                           static_cast<long long>(stride), cells_log, static_cast<long long>(keys),
+                           static_cast<long long>(rows), pairs, out, static_cast<long long>(cells), claims, status);
+        return launch_error("hawk_log_fold_lanes launch");
+    }
+    const long long blocks = (pairs + 3) / 4;
+    if (blocks > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: too many pairs");
+    hipLaunchKernelGGL(hawk_log_fold_waves, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, values,
+                       static_cast<long long>(stride), cells_log, static_cast<long long>(keys),
+                       static_cast<long long>(rows), pairs, out, static_cast<long long>(cells), claims, status);
+    return launch_error("hawk_log_fold_waves launch");
 }
 
 }  // extern "C"

@@ -22,8 +22,8 @@ plane ``bar_x``; a tangent input is ``dot_x`` and a tangent output ``dot_y``.
 from __future__ import annotations
 
 from . import ir
-from .ir import (AccumWrite, Assign, Decl, Deps, HawkError, Node, Program, SampleSum, fresh_placeholders,
-                 free_inputs, level_order, make, zero_like)
+from .ir import (AccumWrite, Assign, Decl, Deps, HawkError, Node, OrderedFold, Program, SampleSum,
+                 fresh_placeholders, free_inputs, level_order, make, zero_like)
 from .trace import Kernel
 from .types import TensorType, role_of
 
@@ -220,9 +220,9 @@ class _Reverse:
             if n.kind == "gather" and n.literal is not None and n.operands[0].uid in self.targets:
                 # the reverse of a table read is a scatter-add into the table's
                 # adjoint at the cell it read (reference hawk/diff/transform.py:695-705)
-                if self.depth:
-                    raise HawkError(f"the gradient of a read of the table {n.operands[0].literal[1]!r} inside a for "
-                                    "loop is not in this build (a scatter per iteration)")
+                if self.depth:          # vjp writes such loops out first (ir.unroll_reading)
+                    raise HawkError(f"the gradient of a read of the table {n.operands[0].literal[1]!r} inside a "
+                                    "rolled loop")
                 self.scatters.append((n.operands[0].literal[1], g, make("table_index", n.operands, n.literal)))
                 continue
             if n.kind in _TERMINAL:
@@ -395,30 +395,45 @@ def vjp(kernel, wrt=None) -> Program:
     name = _namer(program, "bar")
     targets = _differentiable_inputs(program, wrt, params=True)
     roots = [s.value for s in program.sinks]
+    read_tables = {d.name for d in targets if d.name in program.tables}
+    if read_tables:
+        # a table read inside a loop adds at a cell per iteration: the loop is
+        # written out, so each iteration's read is a site of its own
+        roots = ir.unroll_reading(roots, lambda m: m.kind == "gather" and m.literal is not None
+                                  and m.operands[0].literal[1] in read_tables)
     leaf_nodes = {n.literal[1]: n for n in ir.leaves_of(roots)}
     target_leaves = [leaf_nodes[d.name] for d in targets if d.name in leaf_nodes]
     rev = _Reverse({n.uid for n in target_leaves})
     out = Program(grid=program.grid, tables=dict(program.tables))
     seeds = []
-    for s in program.sinks:
+    for s, root in zip(program.sinks, roots):
         seed_name = name(s.name)
         seed, role = _seed(s, seed_name)
         out.decls[seed_name] = Decl(seed_name, role, seed.ttype)
-        seeds.append((s.value, seed))
+        seeds.append((root, seed))
     store = rev.pullback(roots, seeds)
+    keyed = next((s.group for s in program.sinks
+                  if isinstance(s, SampleSum) and s.group is not None and s.policy == "ordered"), None)
     for d in program.decls.values():
         if d.role in ("per_sample", "vec_in", "mat_in", "uniform", "lookup"):
             out.decls.setdefault(d.name, d)
     for d in targets:
         grad_name = name(d.name)
         if d.name in program.tables:
-            # a table's gradient: every read's contribution added at the cell
-            # it read, in the ordered scatter's order (one stage per read site)
             out.decls[grad_name] = Decl(grad_name, "mutable", TensorType((), "f64"))
             out.tables[grad_name] = program.tables[d.name]
-            for table, contribution, cell in rev.scatters:
-                if table == d.name:
-                    out.sinks.append(AccumWrite(grad_name, contribution, cell, "ordered"))
+            sites = [(g, cell) for table, g, cell in rev.scatters if table == d.name]
+            if keyed is not None and sites and all(ir.key_only(cell, keyed) for _, cell in sites):
+                # under an ordered keyed sum, each read names one cell per key:
+                # the ordered fold (reference hawk/diff/ordered.py), one log
+                # slot per read site, each key's lanes added in lane order
+                out.sinks.append(OrderedFold(grad_name, tuple(ir.as_real(g) for g, _ in sites),
+                                             tuple(cell for _, cell in sites), keyed))
+                continue
+            # otherwise every read's contribution is added at the cell it
+            # read, in the ordered scatter's order (one stage per read site)
+            for contribution, cell in sites:
+                out.sinks.append(AccumWrite(grad_name, contribution, cell, "ordered"))
             continue
         lf = leaf_nodes.get(d.name)
         g = store.get(lf.uid) if lf is not None else None

@@ -31,7 +31,8 @@ import dataclasses
 from dataclasses import dataclass, field
 
 from . import ir
-from .ir import AccumWrite, Assign, Deps, HawkError, Node, Program, SampleSum, free_inputs, level_order
+from .ir import (AccumWrite, Assign, Deps, HawkError, Node, OrderedFold, Program, SampleSum, free_inputs,
+                 level_order)
 
 ABI_TAG = "aether-abi/2"
 LAYOUT_SIZES = (40, 32, 32, 8, 24)
@@ -52,7 +53,8 @@ def kind_for(role: str, ttype, mode: str) -> str:
     """The ``hk_argblock`` kind name of a slot (reference hawk/runtime.py:96-110)."""
     if role == "uniform":
         return "f32" if mode == "float32" else "f64"
-    shape = "gref" if role in ("out", "vec_in", "mat_in") or (role == "mutable" and ttype.shape) else "handle"
+    shape = "gref" if role in ("out", "vec_in", "mat_in") or (role in ("mutable", "wide_out", "key_out")
+                                                              and ttype.shape) else "handle"
     if shape == "handle" and ttype.dtype == "i32":
         return "int_handle"
     return shape
@@ -93,6 +95,7 @@ class Stage:
     writes: list                    # [(plane, node)]
     scratch: dict = field(default_factory=dict)   # name -> {"dtype", "per_sample": 1}
     row_sums: list = field(default_factory=list)  # [(cell, node, hi plane, comp plane)]
+    key_writes: list = field(default_factory=list)  # [(plane, (node per component), group)]: one entry per key
 
 
 class _Scope:
@@ -503,21 +506,26 @@ class _Writer:
 
 
 def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: list,
-                  row_sums: list = ()) -> Stage:
+                  row_sums: list = (), key_writes: list = ()) -> Stage:
     """The plane table and arg_spec of the per-sample stage of ``program``;
     ``row_sums`` = ``[(cell, node)]`` are default-policy sample sums whose
-    compensated 32-sample rows the stage writes."""
+    compensated 32-sample rows the stage writes; ``key_writes`` =
+    ``[(plane, nodes, group)]`` are integer planes of one entry per key (every
+    lane of the key's run of ``group`` samples stores the same value)."""
     writes = [(s.name, s.value) for s in program.sinks if isinstance(s, Assign)] + extra_writes
-    roots = [node for _, node in writes] + [node for _, node in row_sums]
+    roots = ([node for _, node in writes] + [node for _, node in row_sums]
+             + [node for _, nodes, _ in key_writes for node in nodes])
     used_leaves = ir.leaves_of(roots)
     rows = [(cell, node, f"hk_rows_{cell}", f"hk_rows_{cell}_comp") for cell, node in row_sums]
     used = ({n.literal[1] for n in used_leaves} | {name for name, _ in writes}
-            | {p for r in rows for p in r[2:]})
+            | {p for r in rows for p in r[2:]} | {name for name, _, _ in key_writes})
     decls = dict(program.decls)
     planes = {}
     for name, node in extra_writes:
         if name not in decls:
             decls[name] = ir.Decl(name, "wide_out", node.ttype)
+    for name, nodes, _ in key_writes:
+        decls[name] = ir.Decl(name, "key_out", ir.TensorType((len(nodes),) if len(nodes) > 1 else (), "i32"))
     for _, _, hi, comp in rows:
         for pname in (hi, comp):
             decls[pname] = ir.Decl(pname, "rows_out", ir.TensorType((), "f64"))
@@ -527,7 +535,9 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
         d = decls[name]
         planes[name] = {"role": role, "shape": list(d.ttype.shape), "dtype": d.ttype.dtype,
                         "kind": kind_for(role, d.ttype, mode), "var": f"hk_p_{name}"}
-    return Stage(stage_name, spec, planes, writes, row_sums=rows)
+    for name, _, group in key_writes:
+        planes[name]["group"] = group
+    return Stage(stage_name, spec, planes, writes, row_sums=rows, key_writes=list(key_writes))
 
 
 #: A stage that touches at least this many component planes hands each XCD a
@@ -544,7 +554,7 @@ def component_planes(stage: Stage) -> int:
     """How many component planes (rows of [component, sample]) the stage reads or writes."""
     total = 0
     for info in stage.planes.values():
-        if info["role"] in ("uniform", "nsamples", "lookup", "rows_out"):
+        if info["role"] in ("uniform", "nsamples", "lookup", "rows_out", "key_out"):
             continue
         count = 1
         for e in info["shape"]:
@@ -562,7 +572,8 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     if xcd_order is None:
         xcd_order = component_planes(stage) >= XCD_ORDER_PLANES
     w = _Writer(stage, mode, nontemporal)
-    roots = [node for _, node in stage.writes] + [node for _, node, _, _ in stage.row_sums]
+    roots = ([node for _, node in stage.writes] + [node for _, node, _, _ in stage.row_sums]
+             + [node for _, nodes, _ in stage.key_writes for node in nodes])
     # Which loops keep a tape: a loop that keeps or reads a tape, and every loop
     # nested in one, is unrolled, so every tape index is a constant and the tapes
     # live in registers (a checkpointed reverse keeps few enough of them live).
@@ -592,6 +603,14 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
             for e in _entries(node.ttype.shape):
                 c = _flat(node.ttype.shape, e)
                 w.emit(w.store(f"{var}[{c} * {var}_cs + hk_i]", vals[c]))
+    for plane, nodes, group in stage.key_writes:
+        # every lane of a key stores the key's one value (a wave's equal
+        # addresses merge into one write)
+        var = stage.planes[plane]["var"]
+        at = "hk_i" if group == 1 else f"hk_i / {group}LL"
+        for c, node in enumerate(nodes):
+            where = f"{var}[{at}]" if len(nodes) == 1 else f"{var}[{c} * {var}_cs + {at}]"
+            w.emit(f"{where} = {w.value(node)[0]};")
     stores = list(w.lines)
     w.lines = []
     row_terms = [(w.value(node)[0], stage.planes[hi]["var"], stage.planes[comp]["var"])
@@ -607,7 +626,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         if kind in ("f64", "f32"):
             params.append(f"Real {var}")
             continue
-        is_input = role not in ("mutable", "out", "wide_out", "accum_out", "rows_out")
+        is_input = role not in ("mutable", "out", "wide_out", "key_out", "accum_out", "rows_out")
         cq = "const " if is_input else ""
         elem = "int" if info["dtype"] == "i32" else "Real"
         if kind == "gref":
@@ -783,18 +802,21 @@ def _mm16_products(program: Program):
 def _carry_repeats(program: Program) -> Program:
     """``program`` with :func:`ir.carry_repeats` applied to its sinks' values
     (one pass over all of them, so values the sinks share stay shared)."""
-    roots = [s.value for s in program.sinks]
-    keys = [s.key for s in program.sinks if isinstance(s, AccumWrite)]
-    new = ir.carry_repeats(roots + keys)
-    if all(a is b for a, b in zip(new, roots + keys)):
+    roots = ir.sink_roots(program.sinks)
+    new = ir.carry_repeats(roots)
+    if all(a is b for a, b in zip(new, roots)):
         return program
-    values, new_keys = iter(new[:len(roots)]), iter(new[len(roots):])
+    it = iter(new)
     sinks = []
     for s in program.sinks:
-        if isinstance(s, AccumWrite):
-            sinks.append(dataclasses.replace(s, value=next(values), key=next(new_keys)))
+        if isinstance(s, OrderedFold):
+            values = tuple(next(it) for _ in s.values)
+            sinks.append(dataclasses.replace(s, values=values, cells=tuple(next(it) for _ in s.cells)))
+        elif isinstance(s, AccumWrite):
+            value = next(it)
+            sinks.append(dataclasses.replace(s, value=value, key=next(it)))
         else:
-            sinks.append(dataclasses.replace(s, value=next(values)))
+            sinks.append(dataclasses.replace(s, value=next(it)))
     return Program(program.decls, sinks, program.grid, program.tables)
 
 
@@ -821,8 +843,20 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                   for pname in ins + outs}
         return Plan(None, None, [{"op": "mm16", "in": ins, "out": outs, "products": prods}], planes)
     assigned = {id(s.value): s.name for s in program.sinks if isinstance(s, Assign)}
-    extra, team, row_sums = [], [], []
+    extra, team, row_sums, key_writes = [], [], [], []
     for s in program.sinks:
+        if isinstance(s, OrderedFold):
+            if mode != "float64":
+                raise HawkError("a table's gradient under an ordered keyed sum is built in float64")
+            # the stage logs each lane's contributions (one component plane per
+            # read site) and each key's cells; the fold adds them per key
+            values, cells = f"hk_logv_{s.name}", f"hk_logc_{s.name}"
+            width = len(s.values)
+            extra.append((values, ir.make("vec", s.values) if width > 1 else s.values[0]))
+            key_writes.append((cells, s.cells, s.group))
+            team.append({"op": "ordered_fold", "v": values, "c": cells, "out": s.name, "group": s.group,
+                         "width": width})
+            continue
         if isinstance(s, SampleSum) and s.policy != "ordered":
             if mode != "float64":
                 raise HawkError(f"hawk.sum(policy={s.policy!r}) on the hip target is built in float64")
@@ -860,7 +894,7 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
     has_stage = any(isinstance(s, Assign) for s in program.sinks) or extra or row_sums
     stage = source = None
     if has_stage:
-        stage = _stage_planes(program, name, mode, extra, row_sums)
+        stage = _stage_planes(program, name, mode, extra, row_sums, key_writes)
         source = render_stage(stage, mode, block, per_thread, nontemporal=nontemporal)
     planes = {}
     if stage is not None:
@@ -868,6 +902,8 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
             planes[pname] = {k: info[k] for k in ("role", "shape", "dtype")}
             if info["role"] == "rows_out":
                 planes[pname]["rows"] = 32                 # one value per 32 samples
+            if info["role"] == "key_out":
+                planes[pname]["group"] = info["group"]     # one value per `group` samples
     for t in team:
         for key in ("u", "key", "v"):
             pname = t.get(key)

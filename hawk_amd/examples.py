@@ -15,7 +15,7 @@ from . import trace as _trace
 from .math import abs as _abs
 from .math import cho_solve, cholesky, dot, exp, sin, sqrt, tanh
 from .trace import Kernel, kernel
-from .types import Index, Matrix, Mutable, Param, Scalar, Vector
+from .types import Grid, Index, Matrix, Mutable, Param, Scalar, Table, Vector
 
 #: Leapfrog step and substep count of the two-body kernel.
 DT = 1e-3
@@ -125,6 +125,30 @@ add_sq_grad = Kernel("add_sq_grad", diff.vjp(add_sq, wrt=("x",)))
 #: with the primal's ordered policies.
 chain_vjp = Kernel("chain_vjp", diff.vjp(chain, wrt=("x",)))
 chain_jvp = Kernel("chain_jvp", diff.jvp(chain, wrt=("x",)))
+
+
+#: Hidden units and weights per net of :func:`net_loss_for`.
+NET_UNITS, NET_WEIGHTS = 8, 24
+
+
+def net_loss_for(samples: int) -> Kernel:
+    """Many small models in one launch (the reference's net axis,
+    tests/test_net_axis.py): lanes are (net, sample); net k's weights are row
+    k of the table ``W`` (unit h uses w[3h], w[3h+1], w[3h+2]), a mask row
+    switches its unused units off, and its loss is the ordered sum of the
+    squared residuals over its own samples.  The VJP wrt ``W`` is the ordered
+    log fold: each net's gradient is the sum of its samples' contributions in
+    lane order."""
+    @kernel
+    def net_loss(lane: Grid["net", "sample":samples], W: Table["net", "w":NET_WEIGHTS],
+                 mask: Table["net", "h":NET_UNITS], x: Scalar, y: Scalar) -> Scalar:
+        pred = 0.0 * x
+        for h in range(NET_UNITS):
+            act = tanh(W.at(net=lane.net, w=3 * h) * x + W.at(net=lane.net, w=3 * h + 1))
+            pred = pred + mask.at(net=lane.net, h=h) * W.at(net=lane.net, w=3 * h + 2) * act
+        r = pred - y
+        return _trace.sum(r * r, over="sample", policy="ordered")
+    return Kernel(f"net_loss_{samples}", net_loss.program)
 
 
 #: Every kernel above, by name.

@@ -10,7 +10,8 @@ loop reads the forward loop's per-iteration carries through ``tape_read``
 
 Sinks are what a kernel commits: a per-sample :class:`Assign`, an
 over-every-sample :class:`SampleSum` (``hawk.sum``) and a keyed
-:class:`AccumWrite` (``hawk.scatter``), as reference ``hawk/ir/nodes.py``.
+:class:`AccumWrite` (``hawk.scatter``), as reference ``hawk/ir/nodes.py``;
+a VJP adds :class:`OrderedFold`, a table's gradient under an ordered keyed sum.
 """
 
 from __future__ import annotations
@@ -26,7 +27,7 @@ from .types import HawkError, TensorType   # noqa: F401 - HawkError is re-export
 #: ``rows_out`` is this target's own: the per-32-sample compensated row
 #: partials of a default-policy ``hawk.sum``, which the reference keeps as
 #: runtime-owned scratch rather than kernel arguments.
-ROLE_ORDER = ("mutable", "out", "wide_out", "accum_out", "rows_out", "vec_in", "mat_in",
+ROLE_ORDER = ("mutable", "out", "wide_out", "key_out", "accum_out", "rows_out", "vec_in", "mat_in",
               "wide_in", "per_sample", "lookup", "terminated", "uniform", "nsamples")
 
 UNARY = ("neg", "exp", "sin", "cos", "tanh", "sqrt", "abs", "log", "real")
@@ -467,6 +468,21 @@ class AccumWrite:
 
 
 @dataclass
+class OrderedFold:
+    """The gradient of a table read by key under an ordered keyed sum
+    (reference ``hawk/diff/ordered.py``): ``values[e]`` is a lane's e-th
+    contribution and ``cells[e]`` the table cell it adds to, one cell per key
+    (a run of ``group`` consecutive samples).  For each key and slot the key's
+    contributions are added in lane order, starting from +0, and the sum is
+    stored into that cell."""
+
+    name: str
+    values: tuple
+    cells: tuple
+    group: int
+
+
+@dataclass
 class Decl:
     """One declared plane or uniform of a kernel."""
 
@@ -493,6 +509,9 @@ class Program:
 def sink_roots(sinks) -> list:
     roots = []
     for s in sinks:
+        if isinstance(s, OrderedFold):
+            roots += list(s.values) + list(s.cells)
+            continue
         roots.append(s.value)
         if isinstance(s, AccumWrite):
             roots.append(s.key)
@@ -551,6 +570,59 @@ def substitute(roots, mapping: dict) -> list:
             copy = Node(n.kind, new_kids, n.ttype, n.literal)
             memo[n.uid] = copy
     return [memo.get(r.uid, r) for r in roots]
+
+
+#: The most iterations :func:`unroll_reading` writes out for one loop.
+UNROLL_MAX = 256
+
+
+def unroll_reading(roots, reads) -> list:
+    """``roots`` with every loop whose body reaches a node ``n`` with
+    ``reads(n)`` written out iteration by iteration: iteration t's body over
+    index ``start + t * step`` and the previous iteration's carries.  The
+    operations and their order do not change, so neither do the bits; each
+    iteration's nodes are then values of their own (a table read's gradient
+    needs one log slot per iteration)."""
+    roots = list(roots)
+    while True:
+        loop = next((n for n in topo(roots) if n.kind == "loop"
+                     and any(reads(m) for m in topo(n.literal.nexts))), None)
+        if loop is None:
+            return roots
+        info = loop.literal
+        if info.trip > UNROLL_MAX:
+            raise HawkError(f"a for loop of {info.trip} iterations reads a differentiated table; its gradient "
+                            f"keeps one slot per read and iteration, written out for at most {UNROLL_MAX} "
+                            "iterations")
+        vals = list(loop.operands)
+        for t in range(info.trip):
+            mapping = {info.index.uid: index_const(info.start + t * info.step)}
+            mapping.update({c.uid: v for c, v in zip(info.carries, vals)})
+            vals = substitute(info.nexts, mapping)
+        finals = {m.uid: vals[m.literal] for m in topo(roots)
+                  if m.kind == "loop_value" and m.operands[0] is loop}
+        roots = substitute(roots, finals)
+
+
+def key_only(n: Node, group: int) -> bool:
+    """Whether ``n`` takes one value per key (a run of ``group`` consecutive
+    samples): it reads constants, uniforms, table planes and lane coordinates
+    of the kept (leading) axes, and nothing per sample."""
+    for m in topo([n]):
+        if m.kind in ("const", "iconst"):
+            continue
+        if m.kind == "leaf":
+            if m.literal[0] in ("uniform", "lookup"):
+                continue
+            return False
+        if m.kind == "lane_axis":
+            div, mod = m.literal
+            if (mod == 0 and group != 1) or (mod != 0 and div % group):
+                return False
+            continue
+        if m.kind in ("loop", "loop_value", "carry", "loop_index", "tape_read"):
+            return False
+    return True
 
 
 #: Kinds whose presence makes a repeated subexpression worth a carried slot.

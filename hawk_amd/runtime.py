@@ -27,8 +27,10 @@ from .ir import HawkError
 
 def _bound_length(role: str, x, n: int) -> int:
     """The length a slot is bound with: its cells for a lookup plane (the
-    gather's bound), the sample count otherwise."""
-    return int(x.numel()) if role == "lookup" else n
+    gather's bound), its keys for a per-key plane, the sample count otherwise."""
+    if role == "lookup":
+        return int(x.numel())
+    return int(x.shape[-1]) if role == "key_out" else n
 
 
 _PER_SAMPLE = ("per_sample", "vec_in", "mat_in", "mutable", "out", "wide_out")
@@ -211,11 +213,25 @@ class DeviceKernel:
         if held is None or held.device != device:
             if info.get("rows"):                       # one row partial per `rows` samples
                 held = torch.empty(max(1, -(-n // info["rows"])), dtype=torch.float64, device=device)
+            elif info.get("group"):                    # one entry per key (`group` samples)
+                held = torch.empty(lead + (n // info["group"],), dtype=torch.int32, device=device)
             else:
                 held = torch.empty(lead + (n,), dtype=torch.int32 if info["dtype"] == "i32" else self._real_dtype(),
                                    device=device)
             self._scratch[key] = held
         return held
+
+    def _fold_args(self, t: dict, bound: dict, n: int, device) -> tuple:
+        """``(args, status, cells)`` of the ordered fold ``t`` (the stage's log
+        planes, the gradient plane, its claim counts and its status words)."""
+        out = bound[t["out"]]
+        cells = int(out.numel())
+        scratch = self._buffer(("fold", t["out"], cells), _core.keyed_log_fold_scratch_bytes(cells), device,
+                               zero=False)
+        status = self._buffer(("fold_status", t["out"]), 8, device, zero=False)
+        args = (bound[t["v"]].data_ptr(), n, bound[t["c"]].data_ptr(), n // t["group"], t["group"], t["width"],
+                out.data_ptr(), cells, scratch.data_ptr(), status.data_ptr())
+        return args, status, cells
 
     # -- launch --------------------------------------------------------------
     def bind_all(self, arrays: dict, n: int) -> None:
@@ -268,16 +284,17 @@ class DeviceKernel:
                                        device)
                 _core.keyed_ordered_sum(bound[t["u"]].data_ptr(), n, t["group"], bound[t["out"]].data_ptr(),
                                         scratch.data_ptr(), stream)
+            elif t["op"] == "ordered_fold":
+                args, status, cells = self._fold_args(t, bound, n, device)
+                _core.keyed_log_fold(*args, stream)
+                statuses.append((t, status, cells))
             else:
                 raise HawkError(f"kernel {self.name!r}: unknown team stage {t['op']!r}")
         if check:
             for t, status, cells in statuses:
-                flags = status.view(torch.int32)[:257].cpu()
-                if bool((flags[1:] != 0).any()):
-                    raise HawkError(
-                        f"{self.name}: hawk.scatter({t['target']}, policy='ordered') got a key outside "
-                        f"[0, {cells}) that is not the skip key -1; those adds were dropped, the rest are "
-                        f"in {t['target']}")
+                problem = _status_problem(self.name, t, status, cells)
+                if problem:
+                    raise HawkError(problem)
 
     def prepare(self, *, stream=None, **arrays) -> Prepared:
         """Validate and bind ``arrays`` once and return a :class:`Prepared`
@@ -294,6 +311,27 @@ class DeviceKernel:
                 raise HawkError(f"kernel {self.name!r} has no per-sample stage")
             self.entry.run(self.block, base, count, n_samples, threads=self.launch_shape["block"],
                            per_thread=self.launch_shape["per_thread"], stream=stream)
+
+
+def _status_problem(name: str, t: dict, status, cells: int) -> str | None:
+    """What a team stage's status words report after a run, or ``None``."""
+    torch = _torch()
+    if t["op"] == "ordered_fold":
+        flags = status.view(torch.int32)[:2].cpu().tolist()
+        if flags[0] & 1:
+            return (f"{name}: the gradient {t['out']} has {cells} cells, fewer than the table it is the "
+                    "gradient of; the reads past its end were not stored")
+        if flags[0] & 2:
+            return (f"{name}: cell {flags[1]} of {t['out']} is read by more than one key (or twice by one key): "
+                    "under an ordered keyed sum each cell's gradient is stored from one key's sum, so those "
+                    "stores raced; read a table by the kept lane axes, one cell per key and read")
+        return None
+    flags = status.view(torch.int32)[:257].cpu()
+    if bool((flags[1:] != 0).any()):
+        return (f"{name}: hawk.scatter({t['target']}, policy='ordered') got a key outside "
+                f"[0, {cells}) that is not the skip key -1; those adds were dropped, the rest are "
+                f"in {t['target']}")
+    return None
 
 
 def load(directory, kernel: str, sidecar: dict | None = None) -> DeviceKernel:
@@ -392,6 +430,10 @@ class Prepared:
                                          _core.keyed_ordered_sum_scratch_bytes(self.n, t["group"]), device)
                 args = (bound[t["u"]].data_ptr(), self.n, t["group"], bound[t["out"]].data_ptr(), scratch.data_ptr())
                 self.steps.append((_core.keyed_ordered_sum, args))
+            elif t["op"] == "ordered_fold":
+                args, status, cells = kernel._fold_args(t, bound, self.n, device)
+                self.steps.append((_core.keyed_log_fold, args))
+                self.statuses.append((t, status, cells))
             else:
                 raise HawkError(f"kernel {kernel.name!r}: unknown team stage {t['op']!r}")
 
@@ -411,18 +453,16 @@ class Prepared:
                             per_thread=k.launch_shape["per_thread"], stream=self.stream)
             out.append((k.name, stage))
         labels = {_core.ordered_sum: "ordered_sum", _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16",
-                  _core.keyed_ordered_sum: "keyed_sum"}
+                  _core.keyed_ordered_sum: "keyed_sum", _core.keyed_log_fold: "ordered_fold"}
         for fn, args in self.steps:
             label = labels.get(fn, "row_sum")
             out.append((label, lambda fn=fn, args=args: fn(*args, self.stream)))
         return out
 
     def check(self) -> None:
-        """Refuse, by name, a run whose ordered scatter met a bad key (synchronises)."""
-        torch = _torch()
+        """Refuse, by name, a run whose ordered scatter met a bad key or whose
+        ordered fold met a cell named twice (synchronises)."""
         for t, status, cells in self.statuses:
-            flags = status.view(torch.int32)[:257].cpu()
-            if bool((flags[1:] != 0).any()):
-                raise HawkError(
-                    f"{self.kernel.name}: hawk.scatter({t['target']}, policy='ordered') got a key outside "
-                    f"[0, {cells}) that is not the skip key -1; those adds were dropped")
+            problem = _status_problem(self.kernel.name, t, status, cells)
+            if problem:
+                raise HawkError(problem)

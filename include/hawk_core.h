@@ -211,6 +211,24 @@ int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n,
                            double* target, int64_t cells, void* scratch,
                            int32_t* status, void* stream);
 
+/* The ordered gradient's log fold: reference `hawk/diff/ordered.py` (the VJP
+ * of a kernel holding an ordered keyed sum logs each table read's
+ * contribution per lane and slot, and the cell it adds to per key and slot),
+ * `hawk/ir/team.py:684-693` (`fold_spec`) and `hawk/emit/team.py:281-312`
+ * (`_fold`).  For key k < keys and slot e < width: out[cells_log[e*keys + k]]
+ * = the sum from +0.0, in lane order r = 0 .. rows-1, of
+ * values[e*stride + k*rows + r] (STORED, not added to out).  A cell outside
+ * [0, cells) is skipped and sets status[0] bit 0; a cell named by more than
+ * one (key, slot) sets bit 1 and status[1] = the least such cell (those
+ * stores race, as in the reference).  Returns HK_OK even then: the caller
+ * reads status[0..1] after the stream completes.  Scratch:
+ * hk_keyed_log_fold_scratch_bytes(cells) bytes (the claim counts, cleared by
+ * the call). */
+size_t hk_keyed_log_fold_scratch_bytes(int64_t cells);
+int hk_keyed_log_fold_f64(const double* values, int64_t stride, const int32_t* cells_log,
+                          int64_t keys, int64_t rows, int32_t width, double* out,
+                          int64_t cells, void* scratch, int32_t* status, void* stream);
+
 /* Per-sample 16x16 fp32 matrix products on MFMA: for every sample s < n and
  * product o < n_out, out[o] = op(in[lhs]) @ op(in[rhs]) with
  * products[3*o .. 3*o+2] = {lhs, rhs, flags}, flags bit 0 = transpose lhs,

@@ -282,6 +282,29 @@ HKO_EXPORT void hko_keyed_ordered_sum(const double* u, int64_t n, int64_t group,
     for (int64_t k = 0; k * group < n; ++k) out[k] = hko_ordered_sum(u + k * group, group);
 }
 
+/* The ordered gradient's log fold (reference hawk/diff/ordered.py,
+ * hawk/ir/team.py:684-693, hawk/emit/team.py:281-312 `_fold`): for key k and
+ * slot e, the key's rows contributions values[e*stride + k*rows + r] are
+ * added in lane order from +0 and STORED into out[cells_log[e*keys + k]].
+ * Pairs run in (slot, key) order, so of two pairs naming one cell the later
+ * one's sum is what remains (the device reports such a cell instead).
+ * Returns 1 when a cell is outside [0, cells) (not stored), else 0. */
+HKO_EXPORT int hko_keyed_log_fold(const double* values, int64_t stride, const int32_t* cells_log, int64_t keys,
+                                  int64_t rows, int32_t width, double* out, int64_t cells) {
+    int bad = 0;
+    for (int32_t e = 0; e < width; ++e) {
+        for (int64_t k = 0; k < keys; ++k) {
+            const double* p = values + (int64_t)e * stride + k * rows;
+            double s = 0.0;
+            for (int64_t r = 0; r < rows; ++r) s += p[r];
+            const int32_t c = cells_log[(int64_t)e * keys + k];
+            if (c < 0 || c >= cells) bad = 1;
+            else out[c] = s;
+        }
+    }
+    return bad;
+}
+
 /* ---- config 5c: the keyed ordered scatter ---------------------------------
  * Reference hawk/emit/team.py:322-460 and hawk/_lane_bind.py:111-114:
  * chunks = clamp(n / cells, 1, 256), span = ceil(n / chunks); chunk b walks

@@ -217,5 +217,8 @@ def evaluate(program, env: dict, n: int) -> dict:
     ev = Evaluator(env, n)
     out = {}
     for s in program.sinks:
+        if hasattr(s, "cells"):        # an ordered fold: (contributions, cells) per slot
+            out[s.name] = ([ev.value(v) for v in s.values], [ev.value(c) for c in s.cells])
+            continue
         out[s.name] = ev.value(s.value)
     return out

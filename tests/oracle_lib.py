@@ -47,6 +47,7 @@ def lib(profile: str = "portable"):
         "hko_ordered_sum": (_D, [_P, _I64]),
         "hko_keyed_ordered_sum": (None, [_P, _I64, _I64, _P]),
         "hko_keyed_ordered_sum_threads": (None, [_P, _I64, _I64, _P, ctypes.c_int]),
+        "hko_keyed_log_fold": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, ctypes.c_int32, _P, _I64]),
         "hko_row_sums": (None, [_P, _I64, _P, _P]),
         "hko_rows_finish": (_D, [_P, _P, _I64]),
         "hko_sample_sum": (_D, [_P, _I64]),
@@ -166,6 +167,17 @@ def keyed_ordered_sum(u, group: int, threads: int = 1, profile: str = "portable"
     else:
         lib(profile).hko_keyed_ordered_sum(_p(u), u.size, group, _p(out))
     return out
+
+
+def keyed_log_fold(values, cells_log, rows: int, out):
+    """The ordered gradient's fold into ``out`` (in place): ``values`` is
+    ``[width, keys * rows]``, ``cells_log`` ``[width, keys]``; returns 1 when a
+    cell was outside ``out``."""
+    values = np.ascontiguousarray(values, dtype=np.float64)
+    cells_log = np.ascontiguousarray(cells_log, dtype=np.int32)
+    width, keys = cells_log.shape
+    assert values.shape == (width, keys * rows) and out.dtype == np.float64 and out.flags.c_contiguous
+    return lib().hko_keyed_log_fold(_p(values), keys * rows, _p(cells_log), keys, rows, width, _p(out), out.size)
 
 
 def row_sums(t):

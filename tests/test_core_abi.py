@@ -103,6 +103,19 @@ def test_team_stage_arguments_are_checked_before_any_launch():
     assert L.hk_keyed_ordered_sum_scratch_bytes(12, 4) == 256                 # keys read their rows directly
     assert L.hk_keyed_ordered_sum_scratch_bytes(8, 8) == L.hk_ordered_sum_scratch_bytes()   # one key
     assert L.hk_keyed_ordered_sum_scratch_bytes(2 * 70001, 70001) == 8 * 2 * 65536 + 256
+    # the ordered gradient's fold: shapes and pointers are checked before HIP
+    rc = L.hk_keyed_log_fold_f64(None, 10, None, 2, 0, 1, None, 4, None, None, None)
+    assert rc != 0 and b"rows and width >= 1" in L.hk_last_error()
+    rc = L.hk_keyed_log_fold_f64(None, 10, None, 2, 5, 0, None, 4, None, None, None)
+    assert rc != 0 and b"rows and width >= 1" in L.hk_last_error()
+    rc = L.hk_keyed_log_fold_f64(None, 9, None, 2, 5, 1, None, 4, None, None, None)
+    assert rc != 0 and b"shorter than keys * rows" in L.hk_last_error()
+    rc = L.hk_keyed_log_fold_f64(None, 10, None, 2, 5, 1, None, 4, None, None, None)
+    assert rc != 0 and b"status is required" in L.hk_last_error()
+    status = (ctypes.c_int32 * 2)()
+    rc = L.hk_keyed_log_fold_f64(None, 10, None, 2, 5, 1, None, 4, None, status, None)
+    assert rc != 0 and b"required" in L.hk_last_error()
+    assert L.hk_keyed_log_fold_scratch_bytes(1000) == 4000 and L.hk_keyed_log_fold_scratch_bytes(0) == 0
     # the per-sample products: plane counts and indices are checked first
     rc = L.hk_mm16_f32(None, 0, None, 1, None, 1, None)
     assert rc != 0 and b"1..3 input planes" in L.hk_last_error()

@@ -15,6 +15,7 @@ from hawk_amd import examples as E
 from hawk_amd.diff import jvp, vjp
 from hawk_amd.math import dot, exp, sqrt
 from ir_eval import evaluate
+from net_axis import net_problem
 
 
 def test_declarations_give_roles_and_the_canonical_arg_spec():
@@ -652,3 +653,109 @@ def test_table_read_jvp_reads_the_tangent_table():
     h = 1e-6
     f = lambda tab: evaluate(table_pick.program, {"table": tab, "where": where, "x": x}, n)["y"]
     np.testing.assert_allclose(got, (f(table + h * dt) - f(table - h * dt)) / (2 * h), rtol=1e-6, atol=1e-8)
+
+
+def _fold_of(program, env, n, name):
+    """A fold sink's gradient plane: its IR contributions and cells, folded by the oracle."""
+    values, cells = evaluate(program, env, n)[name]
+    group = next(s.group for s in program.sinks if s.name == name)
+    for c in cells:                                 # one cell per key and slot
+        assert (c.reshape(-1, group) == c.reshape(-1, group)[:, :1]).all()
+    out = np.zeros(env["W"].size)
+    assert O.keyed_log_fold(np.stack(values), np.stack([c[::group] for c in cells]), group, out) == 0
+    return out
+
+
+def test_an_ordered_keyed_sums_table_gradient_is_the_log_fold():
+    """vjp of a kernel holding hawk.sum(over=..., policy="ordered") wrt a
+    Table read by the kept axis (the reference's net axis,
+    tests/test_net_axis.py): each read site, each iteration of the loop
+    around it included, is a slot of the ordered fold (reference
+    hawk/diff/ordered.py); the gradient equals the numpy loop over the nets
+    (the reference's tolerance, 1e-10) and central differences of the loss."""
+    from hawk_amd.emit_hip import plan_kernel
+    s, k = 40, 5
+    net = E.net_loss_for(s)
+    back = vjp(net, wrt=("W",))
+    assert [type(x).__name__ for x in back.sinks] == ["OrderedFold"]
+    p = plan_kernel(back, "net_grad")
+    assert p.team == [{"op": "ordered_fold", "v": "hk_logv_bar_W", "c": "hk_logc_bar_W", "out": "bar_W",
+                       "group": s, "width": E.NET_WEIGHTS}]
+    assert p.planes["hk_logc_bar_W"] == {"role": "key_out", "shape": [24], "dtype": "i32", "group": s,
+                                         "scratch": True}
+    assert p.planes["bar_W"]["role"] == "accum_out"
+    w, x, y, mask, loss, grad = net_problem(k, s, 3)
+    env = {"W": w.ravel(), "mask": mask.ravel(), "x": x.ravel(), "y": y.ravel()}
+    got = _fold_of(back, {**env, "bar_out": np.ones(k)}, k * s, "bar_W").reshape(k, -1)
+    np.testing.assert_allclose(got, grad, rtol=1e-10, atol=1e-10)
+    assert (got[np.repeat(mask == 0.0, 3, axis=1)] == 0.0).all()
+
+    def total(wv):
+        terms = evaluate(net.program, {**env, "W": wv.ravel()}, k * s)["out"]
+        return O.keyed_ordered_sum(terms, s)
+    np.testing.assert_allclose(total(w), loss, rtol=1e-12)
+    h = 1e-6
+    for net_i, col in ((0, 0), (2, 4), (4, 17), (1, 23)):
+        up, dn = w.copy(), w.copy()
+        up[net_i, col] += h
+        dn[net_i, col] -= h
+        slope = (total(up)[net_i] - total(dn)[net_i]) / (2 * h)
+        assert abs(got[net_i, col] - slope) <= 1e-6 * max(1.0, abs(slope))
+    # the JVP: the keyed ordered sum of the tangents
+    fwd = jvp(net, wrt=("W",))
+    dw = np.random.default_rng(4).normal(size=w.shape)
+    dterms = evaluate(fwd, {**env, "dot_W": dw.ravel()}, k * s)["dot_out"]
+    np.testing.assert_allclose(O.keyed_ordered_sum(dterms, s), (total(w + h * dw) - total(w - h * dw)) / (2 * h),
+                               rtol=1e-6, atol=1e-8)
+
+
+@hawk.kernel
+def _by_sample(lane: hawk.Grid["key", "sample":4], t: hawk.Table[Scalar], x: Scalar) -> Scalar:
+    return hawk.sum(t.at(lane.sample) * x, over="sample", policy="ordered")
+
+
+@hawk.kernel
+def _in_a_loop(t: hawk.Table[Scalar], where: Index, x: Scalar, y: Mutable[Scalar]):
+    acc = 0.0 * x
+    for j in range(3):
+        acc = acc + t.at(where + j) * x
+    y = acc
+
+
+def test_a_table_gradient_the_fold_cannot_take_is_the_ordered_scatter():
+    """A read whose cell changes within a key (here by the summed axis) is not
+    one cell per key, so its gradient stays the ordered scatter (the reference
+    folds it into one cell per key, hawk/diff/ordered.py:61-67, which adds
+    other cells' contributions into it); so are reads in a loop of a kernel
+    with no keyed sum, one scatter per read and iteration."""
+    from hawk_amd.emit_hip import plan_kernel
+    back = vjp(_by_sample, wrt=("t",))
+    assert [type(s).__name__ for s in back.sinks] == ["AccumWrite"]
+    assert [t["op"] for t in plan_kernel(back, "by_sample_vjp").team] == ["ordered_scatter"]
+    back = vjp(_in_a_loop, wrt=("t",))
+    assert [type(s).__name__ for s in back.sinks] == ["AccumWrite"] * 3
+    n = 50
+    g = np.random.default_rng(9)
+    table, where, x, bar_y = g.normal(size=11), g.integers(-2, 12, n).astype(np.int32), g.normal(size=n), \
+        g.normal(size=n)
+    want = np.zeros(11)
+    for j in range(3):
+        np.add.at(want, np.clip(where + j, 0, 10), bar_y * x)
+    from ir_eval import Evaluator
+    ev = Evaluator({"t": table, "where": where, "x": x, "bar_y": bar_y}, n)
+    got = np.zeros(11)
+    for s in back.sinks:
+        np.add.at(got, ev.value(s.key), ev.value(s.value))
+    np.testing.assert_allclose(got, want, rtol=1e-12)
+
+
+def test_a_long_loop_reading_a_differentiated_table_is_refused():
+    @hawk.kernel
+    def long_loop(t: hawk.Table[Scalar], x: Scalar, y: Mutable[Scalar]):
+        acc = 0.0 * x
+        for j in range(ir.UNROLL_MAX + 1):
+            acc = acc + t.at(j) * x
+        y = acc
+    with pytest.raises(HawkError, match="written out for at most"):
+        vjp(long_loop, wrt=("t",))
+    vjp(long_loop, wrt=("x",))                  # a per-sample gradient keeps the loop rolled

@@ -789,3 +789,138 @@ def test_table_reads_and_derivatives_on_the_device(gpu, tmp_path):
     assert host(out).tobytes() == want2.tobytes()
     with pytest.raises(HawkError, match="needs a cell"):
         hawk.run(hawk.load(tmp_path, "tpick"), table=dev(np.zeros(0), gpu), where=W, x=X, y=y)
+
+
+# -- the ordered gradient's log fold ----------------------------------------------
+
+def _log_fold(gpu, v, c, rows, init):
+    """Run hk_keyed_log_fold_f64 on copies of ``v``, ``c`` and ``init``; return
+    (out, status) on the host."""
+    import torch
+    from hawk_amd import _core
+    width, keys = c.shape
+    cells = init.size
+    V, C, out = dev(v, gpu), dev(c, gpu), dev(init, gpu)
+    scratch = torch.empty(max(1, _core.keyed_log_fold_scratch_bytes(cells)), dtype=torch.uint8, device=gpu)
+    status = torch.empty(2, dtype=torch.int32, device=gpu)
+    _core.keyed_log_fold(V.data_ptr(), keys * rows, C.data_ptr(), keys, rows, width, out.data_ptr(), cells,
+                         scratch.data_ptr(), status.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return host(out), host(status).tolist()
+
+
+@pytest.mark.parametrize("keys,rows,width", [(1, 1, 1), (1000, 1, 3), (5000, 40, 24), (777, 64, 2),
+                                             (300, 65, 5), (40, 300, 3), (3, 5000, 2)])
+def test_keyed_log_fold_is_the_oracle_bitwise(gpu, keys, rows, width):
+    """The ordered gradient's fold through the C-ABI (a thread per (key, slot)
+    up to 64 rows, a wave per pair beyond): bit for bit the oracle's serial
+    loop; cells no pair names keep their values."""
+    g = rng(keys + 7 * rows + 31 * width)
+    v = g.normal(size=(width, keys * rows)) * np.exp(3 * g.normal(size=(width, keys * rows)))
+    cells = keys * width + 13
+    c = g.permutation(cells)[:keys * width].reshape(width, keys).astype(np.int32)
+    init = g.normal(size=cells)
+    want = init.copy()
+    assert O.keyed_log_fold(v, c, rows, want) == 0
+    print(f"log fold keys={keys} rows={rows} width={width}", flush=True)
+    out, status = _log_fold(gpu, v, c, rows, init)
+    assert out.tobytes() == want.tobytes()
+    assert status == [0, 2 ** 31 - 1]
+
+
+@pytest.mark.parametrize("rows", [10, 100])
+def test_keyed_log_fold_reports_a_cell_named_twice_and_one_outside(gpu, rows):
+    keys, width = 100, 2
+    g = rng(rows)
+    v = g.normal(size=(width, keys * rows))
+    cells = keys * width
+    c = g.permutation(cells).reshape(width, keys).astype(np.int32)
+    twice = c.copy()
+    twice[1, 7] = c[0, 3]
+    print(f"log fold collision rows={rows}", flush=True)
+    out, status = _log_fold(gpu, v, twice, rows, np.zeros(cells))
+    assert status == [2, int(c[0, 3])]
+    sums = [sum(float(x) for x in v[e, k * rows:(k + 1) * rows]) for e, k in ((0, 3), (1, 7))]
+    assert out[c[0, 3]] in sums
+    outside = c.copy()
+    outside[0, 5] = cells + 4
+    out, status = _log_fold(gpu, v, outside, rows, np.full(cells, 9.0))
+    assert status[0] == 1 and out[c[0, 5]] == 9.0
+
+
+@pytest.mark.parametrize("s", [40, 48, 96])
+def test_net_gradients_through_the_ordered_fold(gpu, tmp_path, s):
+    """16384 nets in one launch (reference tests/test_net_axis.py:163-177):
+    the ordered loss equals the numpy loop; the gradient wrt the per-net
+    weights is the same bits on three launches, equals the loop at 256 nets
+    within the reference's 1e-10, is exactly 0 on masked units, and is the
+    oracle's fold of the stage's own log, bit for bit (the stage's logged
+    contributions and cells are the IR's, within 1e-10 and exactly)."""
+    import hawk_amd as hawk
+    from hawk_amd import examples as E
+    from hawk_amd.diff import vjp
+    from hawk_amd.trace import Kernel
+    from ir_eval import evaluate
+    from net_axis import net_problem
+    net = E.net_loss_for(s)
+    back = Kernel(f"net_grad_{s}", vjp(net, wrt=("W",)))
+    hawk.build([net, back], tmp_path)
+    k = 16384
+    n = k * s
+    pick = rng(1).choice(k, 256, replace=False)
+    w, x, y, mask, loss, grad = net_problem(k, s, 3, pick)
+    W, M, X, Y = dev(w.ravel(), gpu), dev(mask.ravel(), gpu), dev(x.ravel(), gpu), dev(y.ravel(), gpu)
+    out = dev(np.zeros(k), gpu)
+    print(f"net loss s={s}", flush=True)
+    hawk.run(hawk.load(tmp_path, net.name), W=W, mask=M, x=X, y=Y, out=out)
+    np.testing.assert_allclose(host(out)[pick], loss, rtol=1e-12)
+    kb = hawk.load(tmp_path, back.name)
+    seen = []
+    for _ in range(3):
+        bw = dev(np.zeros(k * E.NET_WEIGHTS), gpu)
+        print(f"net grad s={s}", flush=True)
+        hawk.run(kb, W=W, mask=M, x=X, y=Y, bar_out=dev(np.ones(k), gpu), bar_W=bw)
+        seen.append(host(bw).reshape(k, -1))
+    assert seen[0].tobytes() == seen[1].tobytes() == seen[2].tobytes()
+    np.testing.assert_allclose(seen[0][pick], grad, rtol=1e-10, atol=1e-10)
+    dead = np.repeat(mask == 0.0, 3, axis=1)
+    assert (seen[0][dead] == 0.0).all() and (seen[0][~dead] != 0.0).all()
+    logv = host(kb._scratch[("plane", "hk_logv_bar_W", n)])
+    logc = host(kb._scratch[("plane", "hk_logc_bar_W", n)])
+    refold = np.zeros(k * E.NET_WEIGHTS)
+    assert O.keyed_log_fold(logv, logc, s, refold) == 0
+    assert refold.tobytes() == seen[0].tobytes()
+    env = {"W": w.ravel(), "mask": mask.ravel(), "x": x.ravel(), "y": y.ravel(), "bar_out": np.ones(k)}
+    values, cells = evaluate(back.program, env, n)["bar_W"]
+    np.testing.assert_allclose(logv, np.stack(values), rtol=1e-10, atol=1e-12)
+    assert (logc == np.stack([c[::s] for c in cells])).all()
+
+
+
+def _shared_cell_kernel():
+    import hawk_amd as hawk
+    from hawk_amd import Grid, Scalar, Table
+
+    @hawk.kernel
+    def shared_cell(lane: Grid["key", "sample":4], t: Table[Scalar], x: Scalar) -> Scalar:
+        return hawk.sum(t.at(0) * x + t.at(lane.key) * x, over="sample", policy="ordered")
+    return shared_cell
+
+
+def test_a_table_cell_every_key_reads_is_reported(gpu, tmp_path):
+    """Under an ordered keyed sum each cell's gradient is stored from one
+    key's sum (reference hawk/emit/team.py:281-312): a cell every key reads
+    (t.at(0)) would race, so the run names it instead of returning its bits."""
+    import hawk_amd as hawk
+    from hawk_amd import HawkError
+    from hawk_amd.diff import vjp
+    from hawk_amd.trace import Kernel
+    back = Kernel("shared_cell_vjp", vjp(_shared_cell_kernel(), wrt=("t",)))
+    hawk.build([back], tmp_path)
+    keys = 50
+    x = rng(5).normal(size=keys * 4)
+    bt = dev(np.zeros(keys), gpu)
+    print("shared cell vjp", flush=True)
+    with pytest.raises(HawkError, match="cell 0 of bar_t is read by more than one key"):
+        hawk.run(hawk.load(tmp_path, back.name), t=dev(np.ones(keys), gpu), x=dev(x, gpu),
+                 bar_out=dev(np.ones(keys), gpu), bar_t=bt)

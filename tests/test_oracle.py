@@ -412,3 +412,33 @@ def test_keyed_ordered_sum_is_the_numpy_tree_per_key(keys, group):
     want = np.array([_np_ordered_sum(x[k * group:(k + 1) * group]) for k in range(keys)])
     assert got.tobytes() == want.tobytes()
     assert O.keyed_ordered_sum(x, group, threads=3).tobytes() == got.tobytes()
+
+
+@pytest.mark.parametrize("keys,rows,width", [(1, 1, 1), (3, 40, 24), (5, 7, 3), (2, 64, 2), (4, 65, 5),
+                                             (2, 300, 1)])
+def test_keyed_log_fold_is_the_serial_loop(keys, rows, width):
+    """The ordered gradient's fold (reference hawk/emit/team.py:281-312): per
+    key and slot, the key's rows added one after another from +0 in plain
+    Python floats (IEEE doubles, the same single roundings), stored at the
+    slot's cell; cells no pair names keep their values; a cell outside the
+    plane is reported and not stored."""
+    g = np.random.default_rng(keys * 100 + rows + width)
+    v = g.normal(size=(width, keys * rows)) * np.exp(3 * g.normal(size=(width, keys * rows)))
+    cells = keys * width + 7
+    c = g.permutation(cells)[:keys * width].reshape(width, keys).astype(np.int32)
+    out = np.full(cells, -3.5)
+    assert O.keyed_log_fold(v, c, rows, out) == 0
+    want = np.full(cells, -3.5)
+    for e in range(width):
+        for k in range(keys):
+            s = 0.0
+            for r in range(rows):
+                s = s + float(v[e, k * rows + r])
+            want[c[e, k]] = s
+    assert out.tobytes() == want.tobytes()
+    if keys * width > 1:
+        c2 = c.copy()
+        c2[0, 0] = cells
+        out2 = np.full(cells, -3.5)
+        assert O.keyed_log_fold(v, c2, rows, out2) == 1
+        assert out2[c[0, 0]] == -3.5
