@@ -227,7 +227,7 @@ __global__ __launch_bounds__(256) void hawk_keyed_lanes(const double* __restrict
     }
 }
 
-__device__ __forceinline__ int pow2_at_least(long long x) {
+__host__ __device__ __forceinline__ int pow2_at_least(long long x) {
     int p = 1;
     while (p < x) p <<= 1;
     return p;
@@ -338,6 +338,28 @@ __global__ __launch_bounds__(256) void hawk_keyed_rows(const double* __restrict_
     __syncthreads();
     const double total = t < 64 ? group_tree(gp, used) : 0.0;
     if (t == 0) out[k] = total;
+}
+
+// Keys of at most 64 rows: a wave holds 64 / P keys, P = 2^ceil(log2 group),
+// in segments of P lanes (lane j of a segment holds row j, 0.0 + u, or +0.0
+// past the key's rows), and each segment runs the halving tree by shuffles
+// (lane j adds lane j + w for w = P/2 .. 1; only lanes below w carry on): the
+// pairs of the tree over P values.  The group tree has one value, which it
+// returns unchanged.
+__global__ __launch_bounds__(256) void hawk_keyed_small(const double* __restrict__ u, long long group, int P,
+                                                        long long keys, double* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const long long per_wave = 64 / P;
+    const long long k = (static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * per_wave + lane / P;
+    const int j = lane & (P - 1);
+    double x = 0.0;
+    if (k < keys && j < group) x = 0.0 + __builtin_nontemporal_load(u + k * group + j);
+#pragma unroll
+    for (int w = 32; w >= 1; w >>= 1) {
+        const double y = __shfl_down(x, w, 64);
+        if (P > w) x = x + y;
+    }
+    if (j == 0 && k < keys) out[k] = x;
 }
 
 // ---------------------------------------------------------------------------
@@ -867,6 +889,13 @@ int hk_keyed_ordered_sum_f64(const double* u, int64_t n, int64_t group, double* 
     if (n == group) return hk_ordered_sum_f64(u, n, out, scratch, stream);    // one key: the ordered sum
     const long long keys = n / group;
     if (keys > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_ordered_sum_f64: too many keys");
+    if (group <= 64) {
+        const int P = pow2_at_least(group);
+        const long long waves = (keys + 64 / P - 1) / (64 / P);
+        hipLaunchKernelGGL(hawk_keyed_small, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), u, static_cast<long long>(group), P, keys, out);
+        return launch_error("hawk_keyed_small launch");
+    }
     if (group <= kVirtualLanes) {
         hipLaunchKernelGGL(hawk_keyed_rows, dim3(static_cast<unsigned>(keys)), dim3(256), 0,
                            static_cast<hipStream_t>(stream), u, static_cast<long long>(group), out);

@@ -305,6 +305,61 @@ HKO_EXPORT int hko_keyed_log_fold(const double* values, int64_t stride, const in
     return bad;
 }
 
+/* ---- the net axis: many small models in one launch ------------------------
+ * Reference tests/test_net_axis.py (its kernel file _net_axis_kernels.py):
+ * lanes are (net, sample), s samples per net; net k's weights
+ * w[k*24 + 3h .. 3h+2] = (a_h, b_h, c_h) of unit h < 8, and mask[k*8 + h]
+ * switches unit h off.  A sample's term is r*r, r = pred - y, pred =
+ * sum over h, in order from 0*x, of (mask_h * c_h) * tanh(a_h*x + b_h).  Net
+ * k's loss is the ordered sum of its s terms (the keyed ordered sum: each
+ * key's run takes the fixed tree); its gradient wrt w adds each weight's
+ * per-sample contributions bar_out[k] * d(term)/dw in lane order from +0
+ * (the ordered fold's order). */
+static double net_residual(const double* w, const double* m, double x, double y, double* t) {
+    double pred = 0.0 * x;
+    for (int h = 0; h < 8; ++h) {
+        t[h] = tanh(w[3 * h] * x + w[3 * h + 1]);
+        pred = pred + m[h] * w[3 * h + 2] * t[h];
+    }
+    return pred - y;
+}
+
+HKO_EXPORT void hko_net_loss(const double* w, const double* mask, const double* x, const double* y, int64_t s,
+                             double* out, int64_t k0, int64_t k1) {
+    double* terms = (double*)malloc(sizeof(double) * (size_t)(s > 0 ? s : 1));
+    double t[8];
+    for (int64_t k = k0; k < k1; ++k) {
+        for (int64_t r = 0; r < s; ++r) {
+            const double e = net_residual(w + k * 24, mask + k * 8, x[k * s + r], y[k * s + r], t);
+            terms[r] = e * e;
+        }
+        out[k] = hko_ordered_sum(terms, s);
+    }
+    free(terms);
+}
+
+HKO_EXPORT void hko_net_grad(const double* w, const double* mask, const double* x, const double* y,
+                             const double* bar_out, int64_t s, double* grad, int64_t k0, int64_t k1) {
+    double t[8];
+    for (int64_t k = k0; k < k1; ++k) {
+        const double* wk = w + k * 24;
+        const double* mk = mask + k * 8;
+        double acc[24];
+        for (int j = 0; j < 24; ++j) acc[j] = 0.0;
+        for (int64_t r = 0; r < s; ++r) {
+            const double xi = x[k * s + r];
+            const double lead = 2.0 * net_residual(wk, mk, xi, y[k * s + r], t) * bar_out[k];
+            for (int h = 0; h < 8; ++h) {
+                const double g = lead * mk[h] * wk[3 * h + 2] * (1.0 - t[h] * t[h]);
+                acc[3 * h] += g * xi;
+                acc[3 * h + 1] += g;
+                acc[3 * h + 2] += lead * mk[h] * t[h];
+            }
+        }
+        for (int j = 0; j < 24; ++j) grad[k * 24 + j] = acc[j];
+    }
+}
+
 /* ---- config 5c: the keyed ordered scatter ---------------------------------
  * Reference hawk/emit/team.py:322-460 and hawk/_lane_bind.py:111-114:
  * chunks = clamp(n / cells, 1, 256), span = ceil(n / chunks); chunk b walks
@@ -578,7 +633,7 @@ HKO_EXPORT void hko_mm16_vjp(const float* A, const float* B, const float* bar_C,
  * chunk per thread-slot, each reproducing the serial bits. */
 typedef struct {
     int which;
-    const void* in0; const void* in1; const void* in2; const void* in3;
+    const void* in0; const void* in1; const void* in2; const void* in3; const void* in4;
     void* out0; void* out1;
     double s0, s1;
     int64_t n, base, count;
@@ -625,6 +680,15 @@ static void* job_main(void* arg) {
         case 15:   /* keys [base, base+count) of a keyed ordered sum, group = cells */
             for (int64_t k = j->base; k < j->base + j->count; ++k)
                 ((double*)j->out0)[k] = hko_ordered_sum((const double*)j->in0 + k * j->cells, j->cells);
+            break;
+        case 16:   /* nets [base, base+count): their losses, s = cells samples each */
+            hko_net_loss((const double*)j->in0, (const double*)j->in1, (const double*)j->in2,
+                         (const double*)j->in3, j->cells, (double*)j->out0, j->base, j->base + j->count);
+            break;
+        case 17:   /* nets [base, base+count): their gradients wrt w */
+            hko_net_grad((const double*)j->in0, (const double*)j->in1, (const double*)j->in2,
+                         (const double*)j->in3, (const double*)j->in4, j->cells, (double*)j->out0, j->base,
+                         j->base + j->count);
             break;
         default: break;
     }
@@ -684,6 +748,24 @@ HKO_EXPORT void hko_keyed_ordered_sum_threads(const double* u, int64_t n, int64_
         jobs[k].which = 15; jobs[k].in0 = u; jobs[k].out0 = out; jobs[k].cells = group;
         jobs[k].base = k * per < keys ? k * per : keys;
         jobs[k].count = ((k + 1) * per < keys ? (k + 1) * per : keys) - jobs[k].base;
+    }
+    run_jobs(jobs, threads);
+    free(jobs);
+}
+
+/* The net axis's loss (which = 16) or gradient (17) with the nets spread over
+ * `threads` threads (same bits). */
+HKO_EXPORT void hko_net_threads(int which, const double* w, const double* mask, const double* x, const double* y,
+                                const double* bar_out, int64_t k, int64_t s, double* out, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > k) threads = k > 0 ? (int)k : 1;
+    hko_job* jobs = (hko_job*)calloc((size_t)threads, sizeof(hko_job));
+    const int64_t per = (k + threads - 1) / threads;
+    for (int t = 0; t < threads; ++t) {
+        jobs[t].which = which; jobs[t].in0 = w; jobs[t].in1 = mask; jobs[t].in2 = x; jobs[t].in3 = y;
+        jobs[t].in4 = bar_out; jobs[t].out0 = out; jobs[t].cells = s;
+        jobs[t].base = t * per < k ? t * per : k;
+        jobs[t].count = ((t + 1) * per < k ? (t + 1) * per : k) - jobs[t].base;
     }
     run_jobs(jobs, threads);
     free(jobs);

@@ -48,6 +48,7 @@ def lib(profile: str = "portable"):
         "hko_keyed_ordered_sum": (None, [_P, _I64, _I64, _P]),
         "hko_keyed_ordered_sum_threads": (None, [_P, _I64, _I64, _P, ctypes.c_int]),
         "hko_keyed_log_fold": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, ctypes.c_int32, _P, _I64]),
+        "hko_net_threads": (None, [ctypes.c_int, _P, _P, _P, _P, _P, _I64, _I64, _P, ctypes.c_int]),
         "hko_row_sums": (None, [_P, _I64, _P, _P]),
         "hko_rows_finish": (_D, [_P, _P, _I64]),
         "hko_sample_sum": (_D, [_P, _I64]),
@@ -178,6 +179,26 @@ def keyed_log_fold(values, cells_log, rows: int, out):
     width, keys = cells_log.shape
     assert values.shape == (width, keys * rows) and out.dtype == np.float64 and out.flags.c_contiguous
     return lib().hko_keyed_log_fold(_p(values), keys * rows, _p(cells_log), keys, rows, width, _p(out), out.size)
+
+
+def net_loss(w, mask, x, y, threads: int = 1, profile: str = "portable"):
+    """Each net's loss: the ordered sum of its samples' squared residuals
+    (``w[k, 24]``, ``mask[k, 8]``, ``x`` and ``y`` ``[k, s]``)."""
+    w, mask, x, y = (np.ascontiguousarray(a, dtype=np.float64) for a in (w, mask, x, y))
+    k, s = x.shape
+    out = np.empty(k)
+    lib(profile).hko_net_threads(16, _p(w), _p(mask), _p(x), _p(y), None, k, s, _p(out), threads)
+    return out
+
+
+def net_grad(w, mask, x, y, bar_out, threads: int = 1, profile: str = "portable"):
+    """Each net's gradient wrt its weights, ``[k, 24]``: the samples'
+    contributions added in lane order from +0."""
+    w, mask, x, y, bar_out = (np.ascontiguousarray(a, dtype=np.float64) for a in (w, mask, x, y, bar_out))
+    k, s = x.shape
+    out = np.empty((k, 24))
+    lib(profile).hko_net_threads(17, _p(w), _p(mask), _p(x), _p(y), _p(bar_out), k, s, _p(out), threads)
+    return out
 
 
 def row_sums(t):

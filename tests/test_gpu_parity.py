@@ -643,7 +643,8 @@ def test_keyed_ordered_sum_reference_cases(gpu, tmp_path, n):
 
 
 @pytest.mark.parametrize("keys, group", [(4, 8), (1000, 5000), (3, 200003), (70000, 7), (2, 65536), (17, 1025),
-                                         (5, 1)])
+                                         (5, 1), (65536, 64), (16384, 40), (1001, 33), (3000, 2), (12345, 63),
+                                         (999, 65)])
 def test_keyed_ordered_sum_many_keys(gpu, tmp_path, keys, group):
     """One cell per key, each key's run by the fixed tree, bit for bit the
     oracle's (and, for the reference's A=4, B=8 case, numpy's row sums within
@@ -851,9 +852,10 @@ def test_keyed_log_fold_reports_a_cell_named_twice_and_one_outside(gpu, rows):
 @pytest.mark.parametrize("s", [40, 48, 96])
 def test_net_gradients_through_the_ordered_fold(gpu, tmp_path, s):
     """16384 nets in one launch (reference tests/test_net_axis.py:163-177):
-    the ordered loss equals the numpy loop; the gradient wrt the per-net
-    weights is the same bits on three launches, equals the loop at 256 nets
-    within the reference's 1e-10, is exactly 0 on masked units, and is the
+    the ordered loss equals the numpy loop and the C oracle; the gradient wrt
+    the per-net weights is the same bits on three launches, equals the loop
+    at 256 nets and the oracle at all of them within the reference's 1e-10,
+    is exactly 0 on masked units, and is the
     oracle's fold of the stage's own log, bit for bit (the stage's logged
     contributions and cells are the IR's, within 1e-10 and exactly)."""
     import hawk_amd as hawk
@@ -874,6 +876,7 @@ def test_net_gradients_through_the_ordered_fold(gpu, tmp_path, s):
     print(f"net loss s={s}", flush=True)
     hawk.run(hawk.load(tmp_path, net.name), W=W, mask=M, x=X, y=Y, out=out)
     np.testing.assert_allclose(host(out)[pick], loss, rtol=1e-12)
+    np.testing.assert_allclose(host(out), O.net_loss(w, mask, x, y, threads=8), rtol=1e-12)
     kb = hawk.load(tmp_path, back.name)
     seen = []
     for _ in range(3):
@@ -883,6 +886,7 @@ def test_net_gradients_through_the_ordered_fold(gpu, tmp_path, s):
         seen.append(host(bw).reshape(k, -1))
     assert seen[0].tobytes() == seen[1].tobytes() == seen[2].tobytes()
     np.testing.assert_allclose(seen[0][pick], grad, rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(seen[0], O.net_grad(w, mask, x, y, np.ones(k), threads=8), rtol=1e-10, atol=1e-10)
     dead = np.repeat(mask == 0.0, 3, axis=1)
     assert (seen[0][dead] == 0.0).all() and (seen[0][~dead] != 0.0).all()
     logv = host(kb._scratch[("plane", "hk_logv_bar_W", n)])

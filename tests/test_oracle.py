@@ -442,3 +442,32 @@ def test_keyed_log_fold_is_the_serial_loop(keys, rows, width):
         out2 = np.full(cells, -3.5)
         assert O.keyed_log_fold(v, c2, rows, out2) == 1
         assert out2[c[0, 0]] == -3.5
+
+
+def test_net_axis_oracle_is_the_loop_over_nets_and_its_slope():
+    """The net-axis restatement (reference tests/test_net_axis.py): each net's
+    loss and gradient equal the numpy loop over the nets (the reference's
+    tolerances, 1e-12 and 1e-10), the gradient is the loss's central
+    difference slope, masked units have exactly zero gradient, and the
+    threaded run gives the same bits."""
+    from net_axis import net_problem
+    k, s = 7, 40
+    w, x, y, mask, loss, grad = net_problem(k, s, 5)
+    got_loss = O.net_loss(w, mask, x, y)
+    got = O.net_grad(w, mask, x, y, np.ones(k))
+    np.testing.assert_allclose(got_loss, loss, rtol=1e-12)
+    np.testing.assert_allclose(got, grad, rtol=1e-10, atol=1e-10)
+    dead = np.repeat(mask == 0.0, 3, axis=1)
+    assert (got[dead] == 0.0).all() and (got[~dead] != 0.0).all()
+    h = 1e-6
+    for net, col in ((0, 0), (3, 10), (6, 23), (5, 5)):
+        up, dn = w.copy(), w.copy()
+        up[net, col] += h
+        dn[net, col] -= h
+        slope = (O.net_loss(up, mask, x, y)[net] - O.net_loss(dn, mask, x, y)[net]) / (2 * h)
+        assert abs(got[net, col] - slope) <= 1e-6 * max(1.0, abs(slope))
+    bar = np.random.default_rng(1).normal(size=k)
+    scaled = O.net_grad(w, mask, x, y, bar)
+    np.testing.assert_allclose(scaled, got * bar[:, None], rtol=1e-12, atol=1e-300)
+    assert O.net_loss(w, mask, x, y, threads=3).tobytes() == got_loss.tobytes()
+    assert O.net_grad(w, mask, x, y, bar, threads=3).tobytes() == scaled.tobytes()
