@@ -759,8 +759,11 @@ __device__ __forceinline__ void log_fold_store(double s, int c, long long cells,
     out[c] = s;
 }
 
-// One thread per pair, for runs of at most 64 rows: the thread's loads are all
-// in flight before its adds.
+// One thread per pair: the thread reads its run 16 rows at a time (then 8,
+// then one), each batch's loads in flight before its adds.  Measured on
+// MI355X over 805 MB of log: 4.6 TB/s at 64 rows a run, against 4.0 with
+// batches of 8; staging the runs through LDS, or a wave reading whole lines,
+// did no better.
 __global__ __launch_bounds__(256) void hawk_log_fold_lanes(const double* __restrict__ v, long long stride,
                                                            const int* __restrict__ cell_of, long long keys,
                                                            long long rows, long long pairs,
@@ -770,15 +773,22 @@ __global__ __launch_bounds__(256) void hawk_log_fold_lanes(const double* __restr
     if (t >= pairs) return;
     const long long e = t / keys, k = t - e * keys;
     const double* __restrict__ p = v + e * stride + k * rows;
-    constexpr int kAhead = 8;
     double s = 0.0;
     long long r = 0;
-    for (; r + kAhead <= rows; r += kAhead) {
-        double x[kAhead];
+    for (; r + 16 <= rows; r += 16) {
+        double x[16];
 #pragma unroll
-        for (int q = 0; q < kAhead; ++q) x[q] = p[r + q];
+        for (int q = 0; q < 16; ++q) x[q] = p[r + q];
 #pragma unroll
-        for (int q = 0; q < kAhead; ++q) s = s + x[q];
+        for (int q = 0; q < 16; ++q) s = s + x[q];
+    }
+    if (r + 8 <= rows) {
+        double x[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) x[q] = p[r + q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) s = s + x[q];
+        r += 8;
     }
     for (; r < rows; ++r) s = s + p[r];
     log_fold_store(s, cell_of[t], cells, out, claims, status);
@@ -791,7 +801,7 @@ __device__ __forceinline__ double lane_value(double x, int lane) {
     return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned>(lo));
 }
 
-// One wave per pair, for longer runs: the wave loads 64 consecutive rows (one
+// One wave per pair, for long runs of few pairs: the wave loads 64 consecutive rows (one
 // 512-byte read) while it adds the previous 64 in lane order, every lane
 // holding the same running sum; lane 0 stores it.
 __global__ __launch_bounds__(256) void hawk_log_fold_waves(const double* __restrict__ v, long long stride,
@@ -1029,7 +1039,7 @@ int hk_keyed_log_fold_f64(const double* values, int64_t stride, const int32_t* c
                        static_cast<long long>(cells), status);
     int rc = launch_error("hawk_log_fold_clear launch");
     if (rc != HK_OK || pairs == 0) return rc;
-    if (rows <= 64) {
+    if (rows <= 64 || pairs >= 65536) {          // enough pairs for a thread each to fill the chip
         const long long blocks = (pairs + 255) / 256;
         if (blocks > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: too many pairs");
         hipLaunchKernelGGL(hawk_log_fold_lanes, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, values,

@@ -266,6 +266,8 @@ class _Writer:
 
     def _unary(self, n: Node) -> list:
         fn = _UNARY_C[n.kind]
+        if fn == "tanh" and n.ttype.dtype == "f64":
+            fn = "hk_tanh"
         return [self.let(n.ttype.dtype, f"{fn}({x})") for x in self.value(n.operands[0])]
 
     _exp = _sin = _cos = _tanh = _sqrt = _log = _abs = _unary
@@ -650,6 +652,8 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         + ", ".join(str(s) for s in LAYOUT_SIZES) + "};",
         "",
     ]
+    if "hk_tanh(" in "\n".join(body + stores):
+        out += _TANH_HELPER.splitlines()
     if row_terms:
         out += _ROW_SUM_HELPERS.splitlines()
     out += [
@@ -695,6 +699,21 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     return "\n".join(out)
 
 
+#: fp64 tanh: tanh x = sign(x) e / (e + 2) with e = expm1(2|x|) >= 0.  The
+#: quotient has no cancellation, and e's relative error reaches it scaled by
+#: 2 / (e + 2) <= 1, so the result is within about 2 ulp (expm1 within 1 ulp,
+#: the add and the correctly rounded divide half an ulp each); from |x| = 22 on
+#: it is +-1 (tanh 22 rounds to 1).  It costs about 70 VALU instructions where
+#: the device library's double-double tanh costs 165.  NaN stays NaN, -0 stays -0.
+_TANH_HELPER = """
+__device__ __forceinline__ double hk_tanh(double x) {
+    const double a = fabs(x);
+    const double e = expm1(a + a);
+    return copysign(a >= 22.0 ? 1.0 : e / (e + 2.0), x);
+}
+"""
+
+
 #: The row sum of a default-policy ``hawk.sum`` (reference
 #: ``hawk/emit/wrapper.py:542-665``): the 32 samples of a row (one half of a
 #: wave64) combine as compensated (hi, comp) pairs over the pairs (l, l ^ 16),
@@ -722,7 +741,7 @@ __device__ __forceinline__ void hk_row_sum(double& h, double& c) {
 """
 
 
-_FP_CALL = re.compile(r"\b(?:exp|sin|cos|tanh|sqrt|log|fabs)\(")
+_FP_CALL = re.compile(r"\b(?:hk_)?(?:exp|sin|cos|tanh|sqrt|log|fabs)\(")
 _FP_BINARY = re.compile(r"(?<=[\w\)\]]) [-+*/] (?=[\w\(])")
 _PLANE_ACCESS = re.compile(r"hk_p_\w+(?:\[|_m\.|_cs\b)")
 _SAMPLE_LOOP = re.compile(r"^\s*for \(long long \w+ = (-?\d+)LL; \w+ != (-?\d+)LL; \w+ \+= (-?\d+)LL\) \{")

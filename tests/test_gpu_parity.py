@@ -294,13 +294,23 @@ def test_transcendentals_are_within_4_ulp_of_glibc(unit, gpu, which):
     elif which == "sin":
         x = np.concatenate([np.exp(g.normal(size=100_000)), g.uniform(-200, 200, 20_000)])
     elif which == "tanh":
-        x = np.concatenate([g.uniform(-2, 2, 100_000), g.normal(size=20_000) * 1e-3])
+        x = np.concatenate([g.uniform(-2, 2, 100_000), g.normal(size=20_000) * 1e-3, g.uniform(-30, 30, 20_000),
+                            np.exp(g.uniform(-700, 3, 20_000)) * np.sign(g.normal(size=20_000)),
+                            [0.0, 5e-324, -5e-324, 1e-300, 19.06, 21.99, 22.0, 22.01, 710.0, -710.0]])
     else:
         x = np.abs(g.normal(size=120_000)) + 1.0
     out = dev(np.zeros_like(x), gpu)
     hawk.run(hawk.load(d, "one"), x=dev(x, gpu), out=out)
     u = ulp_diff(host(out), O.libm(which, x))
     assert u.max() <= 4.0, f"{which}: max {u.max()} ulp"
+    if which == "tanh":
+        # tanh is sign(x) e / (e + 2), e = expm1(2|x|): odd, so -0 stays -0, +-1 far out, NaN through
+        special = np.array([-0.0, np.inf, -np.inf, np.nan, -30.0])
+        out = dev(np.zeros_like(special), gpu)
+        hawk.run(hawk.load(d, "one"), x=dev(special, gpu), out=out)
+        got = host(out)
+        assert np.signbit(got[0]) and got[0] == 0.0 and got[1] == 1.0 and got[2] == -1.0
+        assert np.isnan(got[3]) and got[4] == -1.0
 
 
 @pytest.mark.parametrize("n", [1000, 262_147])
@@ -811,11 +821,13 @@ def _log_fold(gpu, v, c, rows, init):
 
 
 @pytest.mark.parametrize("keys,rows,width", [(1, 1, 1), (1000, 1, 3), (5000, 40, 24), (777, 64, 2),
-                                             (300, 65, 5), (40, 300, 3), (3, 5000, 2)])
+                                             (300, 65, 5), (40, 300, 3), (3, 5000, 2), (40000, 100, 2),
+                                             (70000, 72, 1), (2000, 23, 7)])
 def test_keyed_log_fold_is_the_oracle_bitwise(gpu, keys, rows, width):
     """The ordered gradient's fold through the C-ABI (a thread per (key, slot)
-    up to 64 rows, a wave per pair beyond): bit for bit the oracle's serial
-    loop; cells no pair names keep their values."""
+    for runs of up to 64 rows or 65536 pairs and more, a wave per pair
+    otherwise): bit for bit the oracle's serial loop; cells no pair names keep
+    their values."""
     g = rng(keys + 7 * rows + 31 * width)
     v = g.normal(size=(width, keys * rows)) * np.exp(3 * g.normal(size=(width, keys * rows)))
     cells = keys * width + 13
