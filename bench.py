@@ -274,7 +274,7 @@ def workload(config: str, device):
         mask = (np.arange(H)[None, :] < np.resize([8, 3, 5, 1, 6], k)[:, None]).astype(np.float64)
         net = E.net_loss_for(s)
         back = Kernel(f"net_grad_{s}", vjp(net, wrt=("W",)))
-        hawk.build([net, back], unit)
+        hawk.build([net, back], unit, fuse_folds=os.environ.get("HAWK_BENCH_LOGGED_FOLD") != "1")
         kf, kv = hawk.load(unit, net.name), hawk.load(unit, back.name)
         W, M, X, Y = (_dev(a.ravel(), device) for a in (w, mask, x, y))
         OUT, BO = torch.zeros(k, dtype=torch.float64, device=device), torch.ones(k, dtype=torch.float64, device=device)
@@ -282,18 +282,23 @@ def workload(config: str, device):
         kernels = [kf.prepare(W=W, mask=M, x=X, y=Y, out=OUT),
                    kv.prepare(W=W, mask=M, x=X, y=Y, bar_out=BO, bar_W=BW)]
         tables = 8 * (P + H) / s                  # a net's weights and mask, read once per net
-        # loss: x, y in, the term out; keyed sum: every term once, every cell once; gradient stage: x, y
-        # and the net's cells in, each weight's contribution out (its log); fold: the log in, bar_W out
-        work = {net.name: (24 + tables, ops(kf)), "keyed_sum": (8 + 8 / s, 1),
-                back.name: (16 + 8 * P + tables + (8 + 4 * P) / s, ops(kv)),
-                "ordered_fold": (8 * P + (4 * P + 8 * P) / s, 1)}
+        # loss: x, y in, the term out; keyed sum: every term once, every cell once.  The gradient folds
+        # in the stage's LDS (fold_clear: the claim counts zeroed; the stage: x, y and the net's cells
+        # in, bar_W out); built with fuse_folds=False it logs each contribution for a fold stage instead
+        work = {net.name: (24 + tables, ops(kf)), "keyed_sum": (8 + 8 / s, 1)}
+        if kv.team[0]["op"] == "fused_fold":
+            work.update({"fold_clear": (4 * P / s, 0), back.name: (16 + tables + (8 + 8 * P) / s, ops(kv))})
+        else:
+            work.update({back.name: (16 + 8 * P + tables + (8 + 4 * P) / s, ops(kv)),
+                         "ordered_fold": (8 * P + (4 * P + 8 * P) / s, 1)})
 
         def cpu(threads):
             import oracle_lib as O
             O.net_loss(w, mask, x, y, threads=threads, profile="native")
             O.net_grad(w, mask, x, y, np.ones(k), threads=threads, profile="native")
         return dict(name="net axis: 65536 nets x 64 samples, ordered loss and its gradient (ordered log fold)",
-                    n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64")
+                    n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
+                    bound="fp64" if kv.team[0]["op"] == "fused_fold" else None)
     raise SystemExit(f"unknown --config {config!r}")
 
 

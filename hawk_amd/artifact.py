@@ -65,7 +65,8 @@ def _stage_bytes(plan, mode: str) -> int:
     size = 4 if mode == "float32" else 8
     total = 0
     for info in plan.stage.planes.values():
-        if info["role"] in ("uniform", "rows_out", "nsamples", "lookup", "key_out"):   # per cell / per key
+        if info["role"] in ("uniform", "rows_out", "nsamples", "lookup", "key_out", "fold_scratch",
+                            "accum_out"):                  # per cell / per key
             continue
         count = 1
         for e in info["shape"]:
@@ -84,10 +85,13 @@ def launch_shape(plan, mode: str) -> tuple:
 
 
 def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64", cache_dir=None,
-                 block: int | None = None, per_thread: int | None = None, nontemporal: bool = True) -> Bundle:
+                 block: int | None = None, per_thread: int | None = None, nontemporal: bool = True,
+                 fuse_folds: bool = True) -> Bundle:
     """Build ``kernels`` (a Kernel or a list of them) into ``directory``.
     ``block`` / ``per_thread`` fix every stage's launch shape; left ``None``
-    each stage gets :func:`launch_shape`'s."""
+    each stage gets :func:`launch_shape`'s.  A stage that folds an ordered
+    gradient in LDS keeps the block its keys need, one sample a thread
+    (``fuse_folds=False`` logs and folds in a team stage instead)."""
     if isinstance(kernels, Kernel):
         kernels = [kernels]
     targets = tuple(targets)
@@ -108,14 +112,16 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
     plans = []
     for k in kernels:
         plan = plan_kernel(k.program, k.name, mode=mode, block=block or 256, per_thread=per_thread or 1,
-                           nontemporal=nontemporal)
+                           nontemporal=nontemporal, fuse_folds=fuse_folds)
         shape = (block or 256, per_thread or 1)
-        if plan.stage is not None and (block is None or per_thread is None):
+        if plan.block is not None:
+            shape = (plan.block, 1)
+        elif plan.stage is not None and (block is None or per_thread is None):
             auto = launch_shape(plan, mode)
             shape = (block or auto[0], per_thread or auto[1])
             if shape != (256, 1):
                 plan = plan_kernel(k.program, k.name, mode=mode, block=shape[0], per_thread=shape[1],
-                                   nontemporal=nontemporal)
+                                   nontemporal=nontemporal, fuse_folds=fuse_folds)
         plans.append((k, plan, shape))
     staged = [(k, p) for k, p, _ in plans if p.stage is not None]
     compiled = dict(zip([k.name for k, _ in staged],

@@ -96,6 +96,8 @@ class Stage:
     scratch: dict = field(default_factory=dict)   # name -> {"dtype", "per_sample": 1}
     row_sums: list = field(default_factory=list)  # [(cell, node, hi plane, comp plane)]
     key_writes: list = field(default_factory=list)  # [(plane, (node per component), group)]: one entry per key
+    fused_folds: list = field(default_factory=list)  # [(out plane, scratch plane, values, cells, group)]
+    block: int | None = None        # the launch block a fused fold needs (its keys never cross a block)
 
 
 class _Scope:
@@ -508,7 +510,7 @@ class _Writer:
 
 
 def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: list,
-                  row_sums: list = (), key_writes: list = ()) -> Stage:
+                  row_sums: list = (), key_writes: list = (), fused_folds: list = ()) -> Stage:
     """The plane table and arg_spec of the per-sample stage of ``program``;
     ``row_sums`` = ``[(cell, node)]`` are default-policy sample sums whose
     compensated 32-sample rows the stage writes; ``key_writes`` =
@@ -516,11 +518,13 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
     lane of the key's run of ``group`` samples stores the same value)."""
     writes = [(s.name, s.value) for s in program.sinks if isinstance(s, Assign)] + extra_writes
     roots = ([node for _, node in writes] + [node for _, node in row_sums]
-             + [node for _, nodes, _ in key_writes for node in nodes])
+             + [node for _, nodes, _ in key_writes for node in nodes]
+             + [node for f in fused_folds for node in tuple(f[2]) + tuple(f[3])])
     used_leaves = ir.leaves_of(roots)
     rows = [(cell, node, f"hk_rows_{cell}", f"hk_rows_{cell}_comp") for cell, node in row_sums]
     used = ({n.literal[1] for n in used_leaves} | {name for name, _ in writes}
-            | {p for r in rows for p in r[2:]} | {name for name, _, _ in key_writes})
+            | {p for r in rows for p in r[2:]} | {name for name, _, _ in key_writes}
+            | {f[0] for f in fused_folds} | {f[1] for f in fused_folds})
     decls = dict(program.decls)
     planes = {}
     for name, node in extra_writes:
@@ -528,6 +532,9 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
             decls[name] = ir.Decl(name, "wide_out", node.ttype)
     for name, nodes, _ in key_writes:
         decls[name] = ir.Decl(name, "key_out", ir.TensorType((len(nodes),) if len(nodes) > 1 else (), "i32"))
+    for out, scratch, *_ in fused_folds:
+        decls[out] = ir.Decl(out, "accum_out", ir.TensorType((), "f64"))
+        decls[scratch] = ir.Decl(scratch, "fold_scratch", ir.TensorType((), "i32"))
     for _, _, hi, comp in rows:
         for pname in (hi, comp):
             decls[pname] = ir.Decl(pname, "rows_out", ir.TensorType((), "f64"))
@@ -539,7 +546,14 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
                         "kind": kind_for(role, d.ttype, mode), "var": f"hk_p_{name}"}
     for name, _, group in key_writes:
         planes[name]["group"] = group
-    return Stage(stage_name, spec, planes, writes, row_sums=rows, key_writes=list(key_writes))
+    block = None
+    for f in fused_folds:
+        b = fold_block(f[4])
+        block = b if block is None else block * b // math.gcd(block, b)
+    if block is not None and block > 1024:
+        raise HawkError("the fused ordered folds of this kernel need blocks of more than 1024 threads")
+    return Stage(stage_name, spec, planes, writes, row_sums=rows, key_writes=list(key_writes),
+                 fused_folds=list(fused_folds), block=block)
 
 
 #: A stage that touches at least this many component planes hands each XCD a
@@ -575,7 +589,10 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         xcd_order = component_planes(stage) >= XCD_ORDER_PLANES
     w = _Writer(stage, mode, nontemporal)
     roots = ([node for _, node in stage.writes] + [node for _, node, _, _ in stage.row_sums]
-             + [node for _, nodes, _ in stage.key_writes for node in nodes])
+             + [node for _, nodes, _ in stage.key_writes for node in nodes]
+             + [node for f in stage.fused_folds for node in tuple(f[2]) + tuple(f[3])])
+    if stage.fused_folds:
+        block, per_thread = stage.block, 1
     # Which loops keep a tape: a loop that keeps or reads a tape, and every loop
     # nested in one, is unrolled, so every tape index is a constant and the tapes
     # live in registers (a checkpointed reverse keeps few enough of them live).
@@ -617,7 +634,12 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     w.lines = []
     row_terms = [(w.value(node)[0], stage.planes[hi]["var"], stage.planes[comp]["var"])
                  for _, node, hi, comp in stage.row_sums]
+    folds = [(stage.planes[out]["var"], stage.planes[scratch]["var"], [w.value(v)[0] for v in values],
+              [w.value(c)[0] for c in cells], group) for out, scratch, values, cells, group in stage.fused_folds]
     body += w.lines                                   # (memoized: nothing new unless a term is a bare leaf)
+    whole = _folds_whole(folds, block)
+    if whole:
+        body = _place_fold_stores(body, folds, block)
 
     real = "float" if mode == "float32" else "double"
     params, unpack = [], []
@@ -628,7 +650,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         if kind in ("f64", "f32"):
             params.append(f"Real {var}")
             continue
-        is_input = role not in ("mutable", "out", "wide_out", "key_out", "accum_out", "rows_out")
+        is_input = role not in ("mutable", "out", "wide_out", "key_out", "accum_out", "rows_out", "fold_scratch")
         cq = "const " if is_input else ""
         elem = "int" if info["dtype"] == "i32" else "Real"
         if kind == "gref":
@@ -638,7 +660,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         else:
             params.append(f"ScalarHandle {var}_m")
             unpack.append(f"{cq}{elem}* __restrict__ {var} = reinterpret_cast<{cq}{elem}*>({var}_m.data);")
-            if role == "lookup":
+            if role in ("lookup", "accum_out", "fold_scratch"):
                 unpack.append(f"const unsigned long long {var}_n = {var}_m.samples;   // cells")
     params += ["long long base", "long long count", "long long nSamples"]
     out = [
@@ -656,6 +678,8 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += _TANH_HELPER.splitlines()
     if row_terms:
         out += _ROW_SUM_HELPERS.splitlines()
+    if folds:
+        out += _FOLD_HELPERS.splitlines()
     out += [
         f'extern "C" __global__ void __launch_bounds__({block}) {stage.name}(',
         "        " + ",\n        ".join(params) + ") {",
@@ -676,7 +700,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         f"        const long long hk_flat = (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * {block}"
         " + static_cast<long long>(threadIdx.x);",
     ]
-    if not row_terms:
+    if not row_terms and not folds:
         out += ["        if (hk_flat >= count) break;",
                 "        const long long hk_i = base + hk_flat;"]
         out += body + stores
@@ -695,8 +719,122 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
                     f"              {hi}[hk_r] = hk_rh;",
                     f"              {comp}[hk_r] = hk_rc;",
                     "          } }"]
+        out += _fused_fold_lines(folds, block, whole)
     out += ["    }", "}", ""]
     return "\n".join(out)
+
+
+#: LDS a fused fold stages a chunk of its slots in, per block, when the
+#: block's contributions to every slot do not fit :data:`FOLD_LDS_WHOLE`.
+FOLD_LDS_BYTES = 16384
+#: LDS, per block, that may hold every fused fold's contributions to every
+#: slot at once; each lane then stores each contribution as soon as it is
+#: computed, so none stays in a register until the fold.
+FOLD_LDS_WHOLE = 60 * 1024
+
+
+def _folds_whole(folds: list, block: int) -> bool:
+    """Whether every fused fold's contributions fit :data:`FOLD_LDS_WHOLE` at once."""
+    total = sum(len(v) * (block // g) * ((g + 1) * 8 + 4) for _, _, v, _, g in folds)
+    return bool(folds) and total <= FOLD_LDS_WHOLE
+
+
+def _place_fold_stores(body: list, folds: list, block: int) -> list:
+    """``body`` with each fused fold's LDS buffer declared first and each
+    contribution's LDS store placed right after the line that computes it."""
+    decl = []
+    after: dict = {}
+    for i, (_, _, values, _, g) in enumerate(folds):
+        keys = block // g
+        stride = keys * (g + 1)
+        decl += [f"        __shared__ double hk_fv{i}[{len(values) * stride}];",
+                 f"        __shared__ int hk_fc{i}[{len(values) * keys}];",
+                 f"        const int hk_fk{i} = static_cast<int>(threadIdx.x) / {g};",
+                 f"        const int hk_fr{i} = static_cast<int>(threadIdx.x) - hk_fk{i} * {g};"]
+        for e, var in enumerate(values):
+            after.setdefault(var, []).append(f"hk_fv{i}[{e * stride} + hk_fk{i} * {g + 1} + hk_fr{i}] = {var};")
+    out = list(decl)
+    defined = re.compile(r"^(\s*)const [\w:<> ]+ (\w+) = ")
+    for line in body:
+        out.append(line)
+        m = defined.match(line)
+        if m and m.group(2) in after:
+            out += [m.group(1) + text for text in after.pop(m.group(2))]
+    for texts in after.values():                  # a contribution the body does not compute (a literal)
+        out += ["        " + text for text in texts]
+    return out
+
+
+def fold_block(group: int) -> int | None:
+    """The launch block of a stage that folds keys of ``group`` lanes in LDS:
+    a multiple of 64 (a whole wave) and of ``group`` (no key crosses a block),
+    at least 256 threads where that fits; ``None`` past 1024 threads."""
+    b = group * 64 // math.gcd(group, 64)
+    if b > 1024:
+        return None
+    return b * max(1, 256 // b)
+
+
+def _fold_chunk(group: int, block: int, width: int) -> int:
+    """Slots a fused fold stages at once: within :data:`FOLD_LDS_BYTES`, and no
+    more pairs than the block has threads."""
+    keys = block // group
+    per_slot = keys * (group + 1) * 8 + keys * 4
+    return max(1, min(width, group, FOLD_LDS_BYTES // per_slot))
+
+
+def _fused_fold_lines(folds: list, block: int, whole: bool = False) -> list:
+    """The ordered fold of each fused fold after the stage's values (the
+    reference's log and fold, hawk/emit/team.py:281-312, without the log): the
+    block's lanes put each slot's contribution into LDS, key k's run at
+    k * (group + 1) (the pad keeps a pair's reads on other banks than its
+    neighbours'), and key k's first lane its cell; then one thread per (key,
+    slot) adds the key's run in lane order from +0 and stores the sum at the
+    cell, counting the cell's claims (a second claim is reported, as the
+    unfused fold does).  Every thread reaches every barrier: a lane past
+    `count` computed sample `base` and its key is skipped.  With ``whole``,
+    the body already stored every contribution in each fold's own buffer
+    (:func:`_place_fold_stores`) and each fold is one chunk."""
+    if not folds:
+        return []
+    if whole:
+        return _whole_fold_lines(folds, block)
+    lds_v = max(_fold_chunk(g, block, len(v)) * (block // g) * (g + 1) for _, _, v, _, g in folds)
+    lds_c = max(_fold_chunk(g, block, len(v)) * (block // g) for _, _, v, _, g in folds)
+    lines = [f"        __shared__ double hk_fv[{lds_v}];",
+             f"        __shared__ int hk_fc[{lds_c}];"]
+    for out, scratch, values, cells, g in folds:
+        keys = block // g
+        chunk = _fold_chunk(g, block, len(values))
+        stride = keys * (g + 1)
+        lines += [f"        {{  // ordered fold into {out[5:]}: {len(values)} slots, {g} lanes a key, "
+                  f"{keys} keys a block, {chunk} slots at a time",
+                  f"            const int hk_fk = static_cast<int>(threadIdx.x) / {g};",
+                  f"            const int hk_fr = static_cast<int>(threadIdx.x) - hk_fk * {g};"]
+        for c0 in range(0, len(values), chunk):
+            part = list(range(c0, min(len(values), c0 + chunk)))
+            for j, e in enumerate(part):
+                lines.append(f"            hk_fv[{j * stride} + hk_fk * {g + 1} + hk_fr] = {values[e]};")
+            lines.append("            if (hk_fr == 0) {")
+            for j, e in enumerate(part):
+                lines.append(f"                hk_fc[{j * keys} + hk_fk] = {cells[e]};")
+            lines += ["            }",
+                      "            __syncthreads();",
+                      f"            if (threadIdx.x < {keys * len(part)}) {{",
+                      f"                const int hk_fs = static_cast<int>(threadIdx.x) / {keys};",
+                      f"                const int hk_fq = static_cast<int>(threadIdx.x) - hk_fs * {keys};",
+                      f"                if (static_cast<long long>(hk_blk) * {block} + hk_fq * {g} < count) {{",
+                      f"                    const double* hk_fp = hk_fv + hk_fs * {stride} + hk_fq * {g + 1};",
+                      "                    double hk_fsum = 0.0;",
+                      "                    #pragma unroll 8",
+                      f"                    for (int hk_fj = 0; hk_fj < {g}; ++hk_fj) hk_fsum = hk_fsum + hk_fp[hk_fj];",
+                      f"                    hk_fold_store(hk_fsum, hk_fc[hk_fs * {keys} + hk_fq], {out}_n, {out}, "
+                      f"{scratch} + 64, {scratch});",
+                      "                }",
+                      "            }",
+                      "            __syncthreads();"]
+        lines.append("        }")
+    return lines
 
 
 #: fp64 tanh: tanh x = sign(x) e / (e + 2) with e = expm1(2|x|) >= 0.  The
@@ -710,6 +848,47 @@ __device__ __forceinline__ double hk_tanh(double x) {
     const double a = fabs(x);
     const double e = expm1(a + a);
     return copysign(a >= 22.0 ? 1.0 : e / (e + 2.0), x);
+}
+"""
+
+
+def _whole_fold_lines(folds: list, block: int) -> list:
+    """The fold phase of fused folds whose contributions are all in LDS."""
+    lines = []
+    for i, (out, scratch, values, cells, g) in enumerate(folds):
+        keys = block // g
+        lines.append(f"        if (hk_fr{i} == 0) {{")
+        lines += [f"            hk_fc{i}[{e * keys} + hk_fk{i}] = {c};" for e, c in enumerate(cells)]
+        lines.append("        }")
+    lines.append("        __syncthreads();")
+    for i, (out, scratch, values, cells, g) in enumerate(folds):
+        keys = block // g
+        stride = keys * (g + 1)
+        pairs = keys * len(values)
+        lines += [f"        // ordered fold into {out[5:]}: {len(values)} slots, {g} lanes a key, {keys} keys a block",
+                  f"        for (int hk_ft = static_cast<int>(threadIdx.x); hk_ft < {pairs}; hk_ft += {block}) {{",
+                  f"            const int hk_fs = hk_ft / {keys};",
+                  f"            const int hk_fq = hk_ft - hk_fs * {keys};",
+                  f"            if (static_cast<long long>(hk_blk) * {block} + hk_fq * {g} < count) {{",
+                  f"                const double* hk_fp = hk_fv{i} + hk_fs * {stride} + hk_fq * {g + 1};",
+                  "                double hk_fsum = 0.0;",
+                  "                #pragma unroll 8",
+                  f"                for (int hk_fj = 0; hk_fj < {g}; ++hk_fj) hk_fsum = hk_fsum + hk_fp[hk_fj];",
+                  f"                hk_fold_store(hk_fsum, hk_fc{i}[hk_fs * {keys} + hk_fq], {out}_n, {out}, "
+                  f"{scratch} + 64, {scratch});",
+                  "            }",
+                  "        }"]
+    return lines
+
+
+#: The store of a fused fold's sum: a cell outside the gradient plane sets
+#: status bit 0; a cell claimed twice sets bit 1 and lowers status[1] to it.
+_FOLD_HELPERS = """
+__device__ __forceinline__ void hk_fold_store(double s, int c, unsigned long long cells, double* out, int* claims,
+                                              int* status) {
+    if (c < 0 || static_cast<unsigned long long>(c) >= cells) { atomicOr(status, 1); return; }
+    if (atomicAdd(claims + c, 1) != 0) { atomicOr(status, 2); atomicMin(status + 1, c); }
+    out[c] = s;
 }
 """
 
@@ -783,6 +962,7 @@ class Plan:
     team: list                      # [{"op": ..., planes...}]
     planes: dict                    # every plane a caller binds: name -> {"role", "shape", "dtype"}
     algorithmic_ops: int = 0        # FP ops per sample of the program as traced (before carried reuse)
+    block: int | None = None        # a launch block the stage needs (a fused fold's), else the build's choice
 
 
 def _mm16_products(program: Program):
@@ -840,18 +1020,23 @@ def _carry_repeats(program: Program) -> Program:
 
 
 def plan_kernel(program: Program, name: str, mode: str = "float64", block: int = 256,
-                per_thread: int = 1, nontemporal: bool = False, reuse_carries: bool = True) -> Plan:
+                per_thread: int = 1, nontemporal: bool = False, reuse_carries: bool = True,
+                fuse_folds: bool = True) -> Plan:
     """Split ``program`` into its per-sample stage and team stages, and render
     the per-sample stage.  With ``reuse_carries``, a loop's value that its next
     iteration would compute again is carried instead (:func:`ir.carry_repeats`);
-    ``Plan.algorithmic_ops`` still counts the program as traced."""
+    ``Plan.algorithmic_ops`` still counts the program as traced.  With
+    ``fuse_folds``, an ordered fold whose keys fit a block (:func:`fold_block`)
+    is done by the stage in LDS; otherwise the stage logs and a team stage folds."""
     if mode not in ("float64", "float32"):
         raise HawkError(f"mode={mode!r}: the hip target builds 'float64' or 'float32'")
     if reuse_carries:
         reused = _carry_repeats(program)
         if reused is not program:
-            traced = plan_kernel(program, name, mode, block, per_thread, nontemporal, reuse_carries=False)
-            plan = plan_kernel(reused, name, mode, block, per_thread, nontemporal, reuse_carries=False)
+            traced = plan_kernel(program, name, mode, block, per_thread, nontemporal, reuse_carries=False,
+                                 fuse_folds=fuse_folds)
+            plan = plan_kernel(reused, name, mode, block, per_thread, nontemporal, reuse_carries=False,
+                               fuse_folds=fuse_folds)
             plan.algorithmic_ops = traced.algorithmic_ops
             return plan
     products = _mm16_products(program) if mode == "float32" else None
@@ -862,11 +1047,18 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                   for pname in ins + outs}
         return Plan(None, None, [{"op": "mm16", "in": ins, "out": outs, "products": prods}], planes)
     assigned = {id(s.value): s.name for s in program.sinks if isinstance(s, Assign)}
-    extra, team, row_sums, key_writes = [], [], [], []
+    extra, team, row_sums, key_writes, fused = [], [], [], [], []
     for s in program.sinks:
         if isinstance(s, OrderedFold):
             if mode != "float64":
                 raise HawkError("a table's gradient under an ordered keyed sum is built in float64")
+            if fuse_folds and fold_block(s.group) is not None:
+                # the stage folds in LDS: its claims and status are cleared before it runs
+                scratch = f"hk_fold_{s.name}"
+                fused.append((s.name, scratch, s.values, s.cells, s.group))
+                team.append({"op": "fused_fold", "out": s.name, "scratch": scratch, "group": s.group,
+                             "width": len(s.values), "before": True})
+                continue
             # the stage logs each lane's contributions (one component plane per
             # read site) and each key's cells; the fold adds them per key
             values, cells = f"hk_logv_{s.name}", f"hk_logc_{s.name}"
@@ -910,10 +1102,10 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                 key = f"hk_key_{s.name}_{len(team)}"
                 extra.append((key, s.key))
             team.append({"op": "ordered_scatter", "key": key, "v": src, "target": s.name})
-    has_stage = any(isinstance(s, Assign) for s in program.sinks) or extra or row_sums
+    has_stage = any(isinstance(s, Assign) for s in program.sinks) or extra or row_sums or fused
     stage = source = None
     if has_stage:
-        stage = _stage_planes(program, name, mode, extra, row_sums, key_writes)
+        stage = _stage_planes(program, name, mode, extra, row_sums, key_writes, fused)
         source = render_stage(stage, mode, block, per_thread, nontemporal=nontemporal)
     planes = {}
     if stage is not None:
@@ -923,6 +1115,8 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                 planes[pname]["rows"] = 32                 # one value per 32 samples
             if info["role"] == "key_out":
                 planes[pname]["group"] = info["group"]     # one value per `group` samples
+            if info["role"] == "fold_scratch":
+                planes[pname]["cells_of"] = pname[len("hk_fold_"):]   # 64 status words + a claim per cell
     for t in team:
         for key in ("u", "key", "v"):
             pname = t.get(key)
@@ -939,4 +1133,5 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
     for pname, info in planes.items():
         if pname.startswith("hk_"):
             info["scratch"] = True
-    return Plan(stage, source, team, planes, fp_ops_per_sample(source) if source else 0)
+    return Plan(stage, source, team, planes, fp_ops_per_sample(source) if source else 0,
+                block=stage.block if stage is not None else None)

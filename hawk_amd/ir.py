@@ -27,8 +27,8 @@ from .types import HawkError, TensorType   # noqa: F401 - HawkError is re-export
 #: ``rows_out`` is this target's own: the per-32-sample compensated row
 #: partials of a default-policy ``hawk.sum``, which the reference keeps as
 #: runtime-owned scratch rather than kernel arguments.
-ROLE_ORDER = ("mutable", "out", "wide_out", "key_out", "accum_out", "rows_out", "vec_in", "mat_in",
-              "wide_in", "per_sample", "lookup", "terminated", "uniform", "nsamples")
+ROLE_ORDER = ("mutable", "out", "wide_out", "key_out", "accum_out", "fold_scratch", "rows_out", "vec_in",
+              "mat_in", "wide_in", "per_sample", "lookup", "terminated", "uniform", "nsamples")
 
 UNARY = ("neg", "exp", "sin", "cos", "tanh", "sqrt", "abs", "log", "real")
 BINARY = ("add", "sub", "mul", "div")

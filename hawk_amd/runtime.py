@@ -28,7 +28,7 @@ from .ir import HawkError
 def _bound_length(role: str, x, n: int) -> int:
     """The length a slot is bound with: its cells for a lookup plane (the
     gather's bound), its keys for a per-key plane, the sample count otherwise."""
-    if role == "lookup":
+    if role in ("lookup", "accum_out", "fold_scratch"):
         return int(x.numel())
     return int(x.shape[-1]) if role == "key_out" else n
 
@@ -221,6 +221,21 @@ class DeviceKernel:
             self._scratch[key] = held
         return held
 
+    def _fold_scratch(self, name: str, bound: dict, device):
+        """The claims and status of a fused fold: 64 status words, then one
+        claim count per cell of its gradient plane."""
+        torch = _torch()
+        cells = int(bound[self.planes[name]["cells_of"]].numel())
+        return self._buffer(("fold_scratch", name, cells), 4 * (64 + cells), device, zero=False).view(torch.int32)
+
+    def _fold_clear_args(self, t: dict, bound: dict) -> tuple:
+        """``(args, status, cells)`` of the set-up of a fused fold: its claims and
+        status cleared (the fold entry with no keys), before the stage runs."""
+        scratch = bound[t["scratch"]]
+        cells = int(bound[t["out"]].numel())
+        args = (0, 0, 0, 0, 1, 1, bound[t["out"]].data_ptr(), cells, scratch.data_ptr() + 256, scratch.data_ptr())
+        return args, scratch, cells
+
     def _fold_args(self, t: dict, bound: dict, n: int, device) -> tuple:
         """``(args, status, cells)`` of the ordered fold ``t`` (the stage's log
         planes, the gradient plane, its claim counts and its status words)."""
@@ -250,14 +265,23 @@ class DeviceKernel:
         device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
         bound = dict(arrays)
         for name, info in self.planes.items():
-            if info.get("scratch"):
+            if info.get("cells_of"):
+                bound[name] = self._fold_scratch(name, bound, device)
+            elif info.get("scratch"):
                 bound[name] = self._term_plane(name, n, device)
+        statuses = []
+        for t in self.team:
+            if t.get("before"):                  # a fused fold's claims and status, cleared first
+                args, status, cells = self._fold_clear_args(t, bound)
+                _core.keyed_log_fold(*args, stream)
+                statuses.append((t, status, cells))
         if self.entry is not None:
             self.bind_all(bound, n)
             self.entry.run(self.block, base, count, n, threads=self.launch_shape["block"],
                            per_thread=self.launch_shape["per_thread"], stream=stream)
-        statuses = []
         for t in self.team:
+            if t.get("before"):
+                continue
             if t["op"] == "ordered_sum":
                 u = bound[t["u"]]
                 scratch = self._buffer(("sum", t["out"]), _core.ordered_sum_scratch_bytes(), device)
@@ -316,7 +340,7 @@ class DeviceKernel:
 def _status_problem(name: str, t: dict, status, cells: int) -> str | None:
     """What a team stage's status words report after a run, or ``None``."""
     torch = _torch()
-    if t["op"] == "ordered_fold":
+    if t["op"] in ("ordered_fold", "fused_fold"):
         flags = status.view(torch.int32)[:2].cpu().tolist()
         if flags[0] & 1:
             return (f"{name}: the gradient {t['out']} has {cells} cells, fewer than the table it is the "
@@ -386,7 +410,9 @@ class Prepared:
         device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
         bound = dict(arrays)
         for name, info in kernel.planes.items():
-            if info.get("scratch"):
+            if info.get("cells_of"):
+                bound[name] = kernel._fold_scratch(name, bound, device)
+            elif info.get("scratch"):
                 bound[name] = kernel._term_plane(name, self.n, device)
         self.bound = bound
         self.block = None
@@ -401,8 +427,14 @@ class Prepared:
                     self.block.bind(slot, x.data_ptr(), _bound_length(role, x, self.n), 1, _contracts.DEVICE_ROCM,
                                     x.device.index or 0)
         self.steps = []
+        self.before = []
         self.statuses = []
         for t in kernel.team:
+            if t.get("before"):
+                args, status, cells = kernel._fold_clear_args(t, bound)
+                self.before.append((_core.keyed_log_fold, args))
+                self.statuses.append((t, status, cells))
+                continue
             if t["op"] == "ordered_sum":
                 scratch = kernel._buffer(("sum", t["out"]), _core.ordered_sum_scratch_bytes(), device)
                 args = (bound[t["u"]].data_ptr(), self.n, bound[t["out"]].data_ptr(), scratch.data_ptr())
@@ -442,11 +474,12 @@ class Prepared:
             launch()
 
     def stages(self) -> list:
-        """``[(label, launch)]`` in run order: the per-sample stage (labelled
-        with the kernel's name) and each team stage (``"ordered_sum"``,
-        ``"ordered_scatter"``); calling every ``launch`` in order is one run."""
+        """``[(label, launch)]`` in run order: a fused fold's set-up
+        (``"fold_clear"``), the per-sample stage (labelled with the kernel's
+        name) and each team stage (``"ordered_sum"``, ``"ordered_scatter"``,
+        ...); calling every ``launch`` in order is one run."""
         k = self.kernel
-        out = []
+        out = [("fold_clear", lambda fn=fn, args=args: fn(*args, self.stream)) for fn, args in self.before]
         if k.entry is not None:
             def stage():
                 k.entry.run(self.block, 0, self.n, self.n, threads=k.launch_shape["block"],

@@ -678,12 +678,18 @@ def test_an_ordered_keyed_sums_table_gradient_is_the_log_fold():
     net = E.net_loss_for(s)
     back = vjp(net, wrt=("W",))
     assert [type(x).__name__ for x in back.sinks] == ["OrderedFold"]
-    p = plan_kernel(back, "net_grad")
+    p = plan_kernel(back, "net_grad", fuse_folds=False)
     assert p.team == [{"op": "ordered_fold", "v": "hk_logv_bar_W", "c": "hk_logc_bar_W", "out": "bar_W",
                        "group": s, "width": E.NET_WEIGHTS}]
     assert p.planes["hk_logc_bar_W"] == {"role": "key_out", "shape": [24], "dtype": "i32", "group": s,
                                          "scratch": True}
-    assert p.planes["bar_W"]["role"] == "accum_out"
+    assert p.planes["bar_W"]["role"] == "accum_out" and p.block is None
+    # 40 lanes a key fit blocks of 320 threads (8 keys): the stage folds in LDS, no log
+    p = plan_kernel(back, "net_grad")
+    assert p.team == [{"op": "fused_fold", "out": "bar_W", "scratch": "hk_fold_bar_W", "group": s,
+                       "width": E.NET_WEIGHTS, "before": True}]
+    assert p.block == 320 and not any(n.startswith("hk_log") for n in p.planes)
+    assert ("accum_out", "bar_W") in p.stage.arg_spec and "__syncthreads" in p.source
     w, x, y, mask, loss, grad = net_problem(k, s, 3)
     env = {"W": w.ravel(), "mask": mask.ravel(), "x": x.ravel(), "y": y.ravel()}
     got = _fold_of(back, {**env, "bar_out": np.ones(k)}, k * s, "bar_W").reshape(k, -1)

@@ -867,9 +867,10 @@ def test_net_gradients_through_the_ordered_fold(gpu, tmp_path, s):
     the ordered loss equals the numpy loop and the C oracle; the gradient wrt
     the per-net weights is the same bits on three launches, equals the loop
     at 256 nets and the oracle at all of them within the reference's 1e-10,
-    is exactly 0 on masked units, and is the
-    oracle's fold of the stage's own log, bit for bit (the stage's logged
-    contributions and cells are the IR's, within 1e-10 and exactly)."""
+    and is exactly 0 on masked units.  The stage that folds in LDS and the
+    stage that logs for a fold stage give the same bits, and those are the
+    oracle's fold of the log, bit for bit (the logged contributions and cells
+    are the IR's, within 1e-10 and exactly)."""
     import hawk_amd as hawk
     from hawk_amd import examples as E
     from hawk_amd.diff import vjp
@@ -878,7 +879,8 @@ def test_net_gradients_through_the_ordered_fold(gpu, tmp_path, s):
     from net_axis import net_problem
     net = E.net_loss_for(s)
     back = Kernel(f"net_grad_{s}", vjp(net, wrt=("W",)))
-    hawk.build([net, back], tmp_path)
+    hawk.build([net, back], tmp_path / "fused")
+    hawk.build([back], tmp_path / "logged", fuse_folds=False)
     k = 16384
     n = k * s
     pick = rng(1).choice(k, 256, replace=False)
@@ -886,23 +888,24 @@ def test_net_gradients_through_the_ordered_fold(gpu, tmp_path, s):
     W, M, X, Y = dev(w.ravel(), gpu), dev(mask.ravel(), gpu), dev(x.ravel(), gpu), dev(y.ravel(), gpu)
     out = dev(np.zeros(k), gpu)
     print(f"net loss s={s}", flush=True)
-    hawk.run(hawk.load(tmp_path, net.name), W=W, mask=M, x=X, y=Y, out=out)
+    hawk.run(hawk.load(tmp_path / "fused", net.name), W=W, mask=M, x=X, y=Y, out=out)
     np.testing.assert_allclose(host(out)[pick], loss, rtol=1e-12)
     np.testing.assert_allclose(host(out), O.net_loss(w, mask, x, y, threads=8), rtol=1e-12)
-    kb = hawk.load(tmp_path, back.name)
+    kf, kl = hawk.load(tmp_path / "fused", back.name), hawk.load(tmp_path / "logged", back.name)
+    assert [t["op"] for t in kf.team] == ["fused_fold"] and [t["op"] for t in kl.team] == ["ordered_fold"]
     seen = []
-    for _ in range(3):
+    for kern in (kf, kf, kf, kl):
         bw = dev(np.zeros(k * E.NET_WEIGHTS), gpu)
-        print(f"net grad s={s}", flush=True)
-        hawk.run(kb, W=W, mask=M, x=X, y=Y, bar_out=dev(np.ones(k), gpu), bar_W=bw)
+        print(f"net grad s={s} {kern.team[0]['op']}", flush=True)
+        hawk.run(kern, W=W, mask=M, x=X, y=Y, bar_out=dev(np.ones(k), gpu), bar_W=bw)
         seen.append(host(bw).reshape(k, -1))
-    assert seen[0].tobytes() == seen[1].tobytes() == seen[2].tobytes()
+    assert seen[0].tobytes() == seen[1].tobytes() == seen[2].tobytes() == seen[3].tobytes()
     np.testing.assert_allclose(seen[0][pick], grad, rtol=1e-10, atol=1e-10)
     np.testing.assert_allclose(seen[0], O.net_grad(w, mask, x, y, np.ones(k), threads=8), rtol=1e-10, atol=1e-10)
     dead = np.repeat(mask == 0.0, 3, axis=1)
     assert (seen[0][dead] == 0.0).all() and (seen[0][~dead] != 0.0).all()
-    logv = host(kb._scratch[("plane", "hk_logv_bar_W", n)])
-    logc = host(kb._scratch[("plane", "hk_logc_bar_W", n)])
+    logv = host(kl._scratch[("plane", "hk_logv_bar_W", n)])
+    logc = host(kl._scratch[("plane", "hk_logc_bar_W", n)])
     refold = np.zeros(k * E.NET_WEIGHTS)
     assert O.keyed_log_fold(logv, logc, s, refold) == 0
     assert refold.tobytes() == seen[0].tobytes()
@@ -911,6 +914,45 @@ def test_net_gradients_through_the_ordered_fold(gpu, tmp_path, s):
     np.testing.assert_allclose(logv, np.stack(values), rtol=1e-10, atol=1e-12)
     assert (logc == np.stack([c[::s] for c in cells])).all()
 
+
+def _keyed_table_kernel(group):
+    import hawk_amd as hawk
+    from hawk_amd import Grid, Scalar, Table
+
+    @hawk.kernel
+    def kt(lane: Grid["key", "sample":group], t: Table["key", "w":3], x: Scalar) -> Scalar:
+        a, b, c = t.at(key=lane.key, w=0), t.at(key=lane.key, w=1), t.at(key=lane.key, w=2)
+        return hawk.sum(a * x * x + b * x + c, over="sample", policy="ordered")
+    return kt
+
+
+@pytest.mark.parametrize("keys,group", [(1000, 40), (777, 64), (500, 48), (3001, 5), (5000, 1), (300, 100),
+                                        (9, 2000), (4099, 64)])
+def test_ordered_fold_in_lds_and_through_a_log_are_the_oracles_bits(gpu, tmp_path, keys, group):
+    """A keyed kernel whose contributions are products (numpy has their bits):
+    the gradient wrt a per-key table, folded in the stage's LDS where the
+    keys fit a block (groups 40, 64, 48, 5, 1) and through the log and the
+    fold stage otherwise (100, 2000), is the oracle's fold of the IR's
+    contributions, bit for bit, on a full and a partial last block."""
+    import hawk_amd as hawk
+    from hawk_amd.diff import vjp
+    from hawk_amd.emit_hip import fold_block
+    from hawk_amd.trace import Kernel
+    from ir_eval import evaluate
+    back = Kernel("kt_vjp", vjp(_keyed_table_kernel(group), wrt=("t",)))
+    hawk.build([back], tmp_path)
+    kern = hawk.load(tmp_path, "kt_vjp")
+    assert kern.team[0]["op"] == ("fused_fold" if fold_block(group) else "ordered_fold")
+    n = keys * group
+    g = rng(keys + group)
+    t, x, bar = g.normal(size=keys * 3), g.normal(size=n), g.normal(size=keys)
+    bt = dev(np.full(keys * 3, np.nan), gpu)
+    print(f"fold keys={keys} group={group} {kern.team[0]['op']}", flush=True)
+    hawk.run(kern, t=dev(t, gpu), x=dev(x, gpu), bar_out=dev(bar, gpu), bar_t=bt)
+    values, cells = evaluate(back.program, {"t": t, "x": x, "bar_out": bar}, n)["bar_t"]
+    want = np.full(keys * 3, np.nan)
+    assert O.keyed_log_fold(np.stack(values), np.stack([c[::group] for c in cells]), group, want) == 0
+    assert host(bt).tobytes() == want.tobytes()
 
 
 def _shared_cell_kernel():
