@@ -259,6 +259,44 @@ def workload(config: str, device):
             return y
         return dict(name="Table read at Zipf keys + its VJP wrt the table (config 5, tables)", n=n,
                     kernels=kernels, work=work, cpu=cpu, dtype="f64")
+    if config == "chain":
+        # hawk.chain (reference hawk/trace/chain.py): four kernels passing a vector and a scalar by
+        # name, run as ONE launch; the intermediates a (3 reals) and b never reach HBM
+        members = E.CHAIN_MEMBERS
+        n = 1 << 25
+        g = np.random.default_rng(9)
+        x, acc0 = g.uniform(0.1, 2.0, n), g.uniform(0.0, 1.0, n)
+        chained = hawk.chain(*members, name="fixture")
+        hawk.build([chained, *members], unit)
+        kc = hawk.load(unit, "fixture")
+        X, ACC = _dev(x, device), _dev(acc0, device)
+        Y = torch.zeros((3, n), dtype=torch.float64, device=device)
+        kernels = [kc.prepare(x=X, acc=ACC, y=Y)]
+        work = {"fixture": (48, ops(kc))}          # x and acc in, acc and y out
+
+        def members_ms():
+            # the same work as four launches through planes, for comparison (not the measured step)
+            A = torch.zeros((3, n), dtype=torch.float64, device=device)
+            B = torch.zeros(n, dtype=torch.float64, device=device)
+            preps = [hawk.load(unit, "unit_circle").prepare(x=X, a=A), hawk.load(unit, "decay").prepare(a=A, x=X, b=B),
+                     hawk.load(unit, "accumulate").prepare(b=B, acc=ACC), hawk.load(unit, "scale_vec").prepare(a=A, b=B, y=Y)]
+            for p in preps:
+                p()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(10):
+                for p in preps:
+                    p()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / 10
+
+        def cpu(threads):
+            import oracle_lib as O
+            O.chain_members(x, acc0.copy(), threads=threads, profile="native")
+        return dict(name="hawk.chain of four kernels (vector and scalar passed by name), one launch", n=n,
+                    kernels=kernels, work=work, cpu=cpu, dtype="f64", compare=members_ms)
     if config == "5n":
         # the net axis (reference tests/test_net_axis.py): 65536 small models of 64 samples in one
         # launch, each net's loss an ordered keyed sum and its gradient wrt its 24 weights the
@@ -493,12 +531,16 @@ def main() -> int:
                         "sample": f"the full step ({w['name']}, N={n}) on the C oracle (native profile, "
                                   f"{threads} threads), median of {len(times)} repetitions "
                                   f"({sum(times):.1f} s of CPU work) after 1 warm-up"}
+    compare = {}
+    if "compare" in w:
+        compare["members_launched_one_by_one_ms"] = round(w["compare"](), 5)
+        log(f"the same members as separate launches: {compare['members_launched_one_by_one_ms']} ms a step")
     line = {
         "metric": METRIC, "value": n / (ms_step * 1e-3), "unit": "samples/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": w["dtype"],
         "data": "synthetic (seeded numpy, resident in HBM before timing)",
-        "config": {"workload": w["name"], "N": n,
+        "config": {"workload": w["name"], "N": n, **compare,
                    "stages": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                               for k, v in per_stage.items()}},
         "roofline": roofline, "cpu_baseline": cpu_baseline, "wall_s": round(wall, 3),

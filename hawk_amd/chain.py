@@ -1,0 +1,160 @@
+"""``hawk.chain``: several kernels run in sequence as one kernel.
+
+Reference ``hawk/trace/chain.py`` (the entry) and ``hawk/ir/chain.py`` (the
+binding).  Member ``j``'s read of a name binds to the value an earlier member
+committed under that name; any other read is an input of the chain.  A name
+no later member reads is an output; a name several members update in turn
+(each reading it first) keeps its last value.  The binding is a substitution
+in the IR: the composed body holds each intermediate as one value, read by
+any number of members, and stores none of them, so one per-sample stage runs
+the whole chain and the intermediates never reach HBM.
+
+On gfx950 every boundary is fused (the reference fuses every boundary on a
+GPU too, ``hawk/ir/fusion.py:10``): a lane's registers hold the chain, and
+the build reports the compiled kernel's VGPRs and scratch in its sidecar.
+The derivative of a chain is the derivative of its composed program.
+"""
+
+from __future__ import annotations
+
+from . import ir
+from .ir import AccumWrite, Assign, HawkError, OrderedFold, Program
+from .trace import Kernel
+
+#: The roles a member may read an intermediate as: its own lane's element.
+BOUND_LEAF_ROLES = ("per_sample", "vec_in", "mat_in", "mutable")
+#: The roles an intermediate may be committed as.
+BOUND_SINK_ROLES = ("mutable", "out")
+
+
+class Chain(Kernel):
+    """A kernel composed of ``members`` in order (:func:`chain`)."""
+
+    def __init__(self, name: str, program: Program, members: tuple, outputs: tuple):
+        super().__init__(name, program)
+        self.members = members
+        self.outputs = outputs
+
+
+def chain(*kernels, name: str) -> Chain:
+    """Run ``kernels`` in sequence as ONE kernel named ``name``.
+
+    A member's input binds to the value an earlier member committed under
+    the same name; any other input is the chain's.  A name no later member
+    reads is an output, and a name several members update in turn keeps its
+    last value.  The values passed between members stay in the kernel: they
+    are neither inputs nor outputs of the chain.  A chain of chains is the
+    chain of their members.  The members must agree on their Grid (a chain
+    runs as one launch)."""
+    members = tuple(m for k in kernels for m in (k.members if isinstance(k, Chain) else (k,)))
+    if not members:
+        raise HawkError("chain: give at least one kernel")
+    for k in members:
+        if not isinstance(k, Kernel):
+            raise HawkError(f"chain: {k!r} is not a traced kernel")
+    program, outputs = bind(members)
+    return Chain(name, program, members, outputs)
+
+
+def _grid_of(k: Kernel):
+    g = k.program.grid
+    return None if g is None else tuple(tuple(a) for a in g.axes)
+
+
+def _sink_nodes(s) -> list:
+    if isinstance(s, OrderedFold):
+        return list(s.values) + list(s.cells)
+    return [s.value, s.key] if isinstance(s, AccumWrite) else [s.value]
+
+
+def _rebuilt(s, nodes: list):
+    import dataclasses
+    if isinstance(s, AccumWrite):
+        return dataclasses.replace(s, value=nodes[0], key=nodes[1])
+    if isinstance(s, OrderedFold):
+        k = len(s.values)
+        return dataclasses.replace(s, values=tuple(nodes[:k]), cells=tuple(nodes[k:]))
+    return dataclasses.replace(s, value=nodes[0])
+
+
+def bind(members, keep=()) -> tuple:
+    """``(program, outputs)``: ``members`` composed in order (see the module
+    text); ``keep`` names intermediates to commit as outputs too.  Refuses,
+    naming both members and the name (reference ``hawk/ir/chain.py:67-127``):
+    a name read with two types or two input roles; a second writer of a name
+    that does not read it first; members whose Grids disagree; an
+    intermediate read at another sample, or committed off its own lane (a
+    sum or a scatter)."""
+    first = members[0]
+    for k in members[1:]:
+        if _grid_of(k) != _grid_of(first):
+            raise HawkError(f"chain: members {first.name!r} and {k.name!r} disagree on grid "
+                            f"({_grid_of(first)!r} vs {_grid_of(k)!r}); a chain runs as one launch")
+    latest: dict = {}           # name -> (member, rebuilt sink)
+    inputs: dict = {}           # name -> (member, role, ttype) of an unbound read
+    canon: dict = {}            # name -> the one leaf node every member's read of an input becomes
+    reads: list = []            # per member: the names it reads
+    for k in members:
+        roots = [n for s in k.sinks for n in _sink_nodes(s)]
+        order = ir.topo(roots)
+        leaves = [n for n in order if n.kind == "leaf"]
+        gathered = {n.operands[0].uid for n in order if n.kind == "gather"}
+        reads.append({lf.literal[1] for lf in leaves})
+        mapping = {}
+        for lf in leaves:
+            role, name = lf.literal
+            if name not in latest:
+                held = inputs.setdefault(name, (k.name, role, lf.ttype))
+                if held[1:] != (role, lf.ttype):
+                    raise HawkError(f"chain: {held[0]!r} reads {name!r} as (role={held[1]!r}, {held[2]!r}) but "
+                                    f"{k.name!r} reads it as (role={role!r}, {lf.ttype!r}); rename one")
+                one = canon.setdefault(name, lf)      # one input, one value (and one derivative)
+                if one is not lf:
+                    mapping[lf.uid] = one
+                continue
+            writer, sink = latest[name]
+            if lf.ttype != sink.value.ttype:
+                raise HawkError(f"chain: {writer!r} commits {name!r} as {sink.value.ttype!r} but {k.name!r} reads "
+                                f"it as {lf.ttype!r}; one name is one value")
+            if role not in BOUND_LEAF_ROLES or lf.uid in gathered or not isinstance(sink, Assign) \
+                    or sink.role not in BOUND_SINK_ROLES:
+                raise HawkError(f"chain: {k.name!r} reads {name!r}, which {writer!r} commits, at another sample "
+                                f"(or {writer!r} commits it off its own lane); an intermediate is the lane's own "
+                                "value: end the chain at that name and read the plane in a second chain")
+            mapping[lf.uid] = sink.value
+        for s in k.sinks:
+            if s.name in latest and s.name not in reads[-1]:
+                raise HawkError(f"chain: {latest[s.name][0]!r} and {k.name!r} both commit {s.name!r} and "
+                                f"{k.name!r} does not read it first; the order would decide the value")
+            if s.name in inputs and inputs[s.name][1] != "mutable":
+                held = inputs[s.name]
+                raise HawkError(f"chain: {held[0]!r} reads {s.name!r} as an input (role={held[1]!r}) but "
+                                f"{k.name!r} commits it; rename one")
+        new = ir.substitute(roots, mapping) if mapping else roots
+        at = 0
+        for s in k.sinks:
+            width = len(_sink_nodes(s))
+            latest[s.name] = (k.name, _rebuilt(s, new[at:at + width]))
+            at += width
+    writer_at = {}
+    for j, k in enumerate(members):
+        for s in k.sinks:
+            writer_at[s.name] = j
+    outputs = tuple(n for n, j in writer_at.items() if n in keep or not any(n in r for r in reads[j + 1:]))
+    consumed = set(writer_at) - set(outputs) - set(inputs)
+    decls: dict = {}
+    tables: dict = {}
+    for j, k in enumerate(members):            # an output's declaration is its last writer's
+        for n, decl in k.decls.items():
+            if n not in consumed and (n not in decls or writer_at.get(n) == j):
+                decls[n] = decl
+        for n, axes in k.program.tables.items():
+            if n not in consumed:
+                tables.setdefault(n, axes)
+    sinks = [latest[n][1] for n in outputs]
+    if not sinks:
+        raise HawkError("chain: the members commit nothing a later member does not read")
+    program = Program(decls, sinks, first.program.grid, tables)
+    used = {n.literal[1] for n in ir.leaves_of(ir.sink_roots(sinks))} | {s.name for s in sinks}
+    program.decls = {n: d for n, d in decls.items() if n in used}
+    return program, outputs

@@ -13,7 +13,7 @@ from __future__ import annotations
 from . import diff
 from . import trace as _trace
 from .math import abs as _abs
-from .math import cho_solve, cholesky, dot, exp, sin, sqrt, tanh
+from .math import cho_solve, cholesky, cos, dot, exp, sin, sqrt, tanh, vec
 from .trace import Kernel, kernel
 from .types import Grid, Index, Matrix, Mutable, Param, Scalar, Table, Vector
 
@@ -149,6 +149,33 @@ def net_loss_for(samples: int) -> Kernel:
         r = pred - y
         return _trace.sum(r * r, over="sample", policy="ordered")
     return Kernel(f"net_loss_{samples}", net_loss.program)
+
+
+@kernel
+def unit_circle(x: Scalar, a: Mutable[Vector[3]]):
+    a = vec(sin(x), cos(x), x * 0.5)
+
+
+@kernel
+def decay(a: Vector[3], x: Scalar, b: Mutable[Scalar]):
+    b = exp(-dot(a, a)) + x
+
+
+@kernel
+def accumulate(b: Scalar, acc: Mutable[Scalar]):
+    acc = acc + b * b
+
+
+@kernel
+def scale_vec(a: Vector[3], b: Scalar, y: Mutable[Vector[3]]):
+    y = a * b
+
+
+#: Four kernels that pass values by name (the shape of the reference's
+#: tests/test_chain.py fixture: a vector, a scalar read from it, an
+#: accumulator updated in place, an output read from two earlier values):
+#: ``hawk.chain(*CHAIN_MEMBERS, name=...)`` runs them as one kernel.
+CHAIN_MEMBERS = (unit_circle, decay, accumulate, scale_vec)
 
 
 #: Every kernel above, by name.

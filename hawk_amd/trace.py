@@ -716,6 +716,12 @@ class Kernel:
     def sinks(self) -> list:
         return self.program.sinks
 
+    @property
+    def arg_spec(self) -> list:
+        """``[(role, name)]`` of the planes the kernel binds, in the ABI's role order."""
+        used = {n.literal[1] for n in ir.leaves_of(ir.sink_roots(self.sinks))} | {s.name for s in self.sinks}
+        return ir.arg_spec(self.program, used)
+
     def __repr__(self) -> str:
         return f"<hawk kernel {self.name}: {[type(s).__name__ + ':' + s.name for s in self.sinks]}>"
 

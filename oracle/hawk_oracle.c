@@ -305,6 +305,24 @@ HKO_EXPORT int hko_keyed_log_fold(const double* values, int64_t stride, const in
     return bad;
 }
 
+/* ---- hawk.chain: four members passing values by name ----------------------
+ * Reference hawk/trace/chain.py (and its tests/test_chain.py fixture): a =
+ * (sin x, cos x, x*0.5); b = exp(-((a0*a0 + a1*a1) + a2*a2)) + x;
+ * acc = acc + b*b; y = a * b.  The chain runs them as one kernel; so does
+ * this loop (a and b stay local). */
+HKO_EXPORT void hko_chain_members(const double* x, double* acc, double* y, int64_t n, int64_t base,
+                                  int64_t count) {
+    for (int64_t i = base; i < base + count; ++i) {
+        const double xi = x[i];
+        const double a0 = sin(xi), a1 = cos(xi), a2 = xi * 0.5;
+        const double b = exp(-((a0 * a0 + a1 * a1) + a2 * a2)) + xi;
+        acc[i] = acc[i] + b * b;
+        y[i] = a0 * b;
+        y[n + i] = a1 * b;
+        y[2 * n + i] = a2 * b;
+    }
+}
+
 /* ---- the net axis: many small models in one launch ------------------------
  * Reference tests/test_net_axis.py (its kernel file _net_axis_kernels.py):
  * lanes are (net, sample), s samples per net; net k's weights
@@ -685,6 +703,8 @@ static void* job_main(void* arg) {
             hko_net_loss((const double*)j->in0, (const double*)j->in1, (const double*)j->in2,
                          (const double*)j->in3, j->cells, (double*)j->out0, j->base, j->base + j->count);
             break;
+        case 18: hko_chain_members((const double*)j->in0, (double*)j->out0, (double*)j->out1, j->n, j->base,
+                                   j->count); break;
         case 17:   /* nets [base, base+count): their gradients wrt w */
             hko_net_grad((const double*)j->in0, (const double*)j->in1, (const double*)j->in2,
                          (const double*)j->in3, (const double*)j->in4, j->cells, (double*)j->out0, j->base,
@@ -748,6 +768,20 @@ HKO_EXPORT void hko_keyed_ordered_sum_threads(const double* u, int64_t n, int64_
         jobs[k].which = 15; jobs[k].in0 = u; jobs[k].out0 = out; jobs[k].cells = group;
         jobs[k].base = k * per < keys ? k * per : keys;
         jobs[k].count = ((k + 1) * per < keys ? (k + 1) * per : keys) - jobs[k].base;
+    }
+    run_jobs(jobs, threads);
+    free(jobs);
+}
+
+/* The chain members over [0, n) in `threads` contiguous tiles (same bits). */
+HKO_EXPORT void hko_chain_members_threads(const double* x, double* acc, double* y, int64_t n, int threads) {
+    if (threads < 1) threads = 1;
+    hko_job* jobs = (hko_job*)calloc((size_t)threads, sizeof(hko_job));
+    const int64_t tile = (n + threads - 1) / threads;
+    for (int t = 0; t < threads; ++t) {
+        jobs[t].which = 18; jobs[t].in0 = x; jobs[t].out0 = acc; jobs[t].out1 = y; jobs[t].n = n;
+        jobs[t].base = t * tile < n ? t * tile : n;
+        jobs[t].count = ((t + 1) * tile < n ? (t + 1) * tile : n) - jobs[t].base;
     }
     run_jobs(jobs, threads);
     free(jobs);

@@ -49,6 +49,7 @@ def lib(profile: str = "portable"):
         "hko_keyed_ordered_sum_threads": (None, [_P, _I64, _I64, _P, ctypes.c_int]),
         "hko_keyed_log_fold": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, ctypes.c_int32, _P, _I64]),
         "hko_net_threads": (None, [ctypes.c_int, _P, _P, _P, _P, _P, _I64, _I64, _P, ctypes.c_int]),
+        "hko_chain_members_threads": (None, [_P, _P, _P, _I64, ctypes.c_int]),
         "hko_row_sums": (None, [_P, _I64, _P, _P]),
         "hko_rows_finish": (_D, [_P, _P, _I64]),
         "hko_sample_sum": (_D, [_P, _I64]),
@@ -179,6 +180,16 @@ def keyed_log_fold(values, cells_log, rows: int, out):
     width, keys = cells_log.shape
     assert values.shape == (width, keys * rows) and out.dtype == np.float64 and out.flags.c_contiguous
     return lib().hko_keyed_log_fold(_p(values), keys * rows, _p(cells_log), keys, rows, width, _p(out), out.size)
+
+
+def chain_members(x, acc, threads: int = 1, profile: str = "portable"):
+    """The chain of the four example members over ``x``: ``acc`` updated in
+    place, ``y`` [3, n] returned."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    assert acc.dtype == np.float64 and acc.flags.c_contiguous and acc.size == x.size
+    y = np.empty((3, x.size))
+    lib(profile).hko_chain_members_threads(_p(x), _p(acc), _p(y), x.size, threads)
+    return y
 
 
 def net_loss(w, mask, x, y, threads: int = 1, profile: str = "portable"):

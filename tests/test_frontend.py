@@ -765,3 +765,90 @@ def test_a_long_loop_reading_a_differentiated_table_is_refused():
     with pytest.raises(HawkError, match="written out for at most"):
         vjp(long_loop, wrt=("t",))
     vjp(long_loop, wrt=("x",))                  # a per-sample gradient keeps the loop rolled
+
+
+def _long_double_chain(x):
+    """acc and y of the chain members in long double (the oracle of the chain tests)."""
+    ld = np.longdouble
+    x = x.astype(ld)
+    a = np.stack([np.sin(x), np.cos(x), x * ld("0.5")])
+    b = np.exp(-(a * a).sum(axis=0)) + x
+    return a, b
+
+
+def test_chain_binds_members_by_name_and_stores_no_intermediate():
+    """hawk.chain (reference tests/test_chain.py:180-194): the composed kernel
+    binds x and acc and commits acc and y; a and b stay in the kernel; a chain
+    of chains is the chain of its members; the composed values are the
+    members' run one after another, bit for bit (same operations)."""
+    import chain_members as C
+    from hawk_amd.emit_hip import plan_kernel
+    chained = hawk.chain(*C.MEMBERS, name="fixture")
+    assert {n for _, n in chained.arg_spec} == {"x", "acc", "y"}
+    assert chained.outputs == ("acc", "y") and chained.members == C.MEMBERS
+    nested = hawk.chain(hawk.chain(C.unit_circle, C.decay, name="front"), C.accumulate, C.scale_vec, name="fixture")
+    assert nested.members == C.MEMBERS
+    assert plan_kernel(nested.program, "k").source == plan_kernel(chained.program, "k").source
+    assert [t for t in plan_kernel(chained.program, "k").planes] and \
+        set(plan_kernel(chained.program, "k").planes) == {"x", "acc", "y"}
+    n = 257
+    g = np.random.default_rng(5)
+    x, acc = g.uniform(0.1, 2.0, n), g.uniform(0.0, 1.0, n)
+    got = evaluate(chained.program, {"x": x, "acc": acc}, n)
+    a = evaluate(C.unit_circle.program, {"x": x}, n)["a"]
+    b = evaluate(C.decay.program, {"a": a, "x": x}, n)["b"]
+    want_acc = evaluate(C.accumulate.program, {"b": b, "acc": acc}, n)["acc"]
+    want_y = evaluate(C.scale_vec.program, {"a": a, "b": b}, n)["y"]
+    assert got["acc"].tobytes() == want_acc.tobytes() and got["y"].tobytes() == want_y.tobytes()
+    la, lb = _long_double_chain(x)
+    np.testing.assert_allclose(got["y"], (la * lb).astype(np.float64), rtol=1e-14)
+
+
+def test_chain_refusals_name_both_members_and_the_name():
+    """The reference's refusals, by text (tests/test_chain.py:196-242)."""
+    import chain_members as C
+    with pytest.raises(HawkError, match=r"'unit_circle' commits 'a' .* but 'flat_a' reads it"):
+        hawk.chain(C.unit_circle, C.flat_a, name="c")
+    with pytest.raises(HawkError, match=r"'decay' and 'blind_b' both commit 'b'"):
+        hawk.chain(C.unit_circle, C.decay, C.blind_b, name="c")
+    with pytest.raises(HawkError, match=r"members 'unit_circle' and 'on_grid' disagree on grid"):
+        hawk.chain(C.unit_circle, C.on_grid, name="c")
+    with pytest.raises(HawkError, match=r"'pick' reads 'table', which 'fill' commits, at another sample"):
+        hawk.chain(C.fill, C.pick, name="c")
+    with pytest.raises(HawkError, match=r"'reads_total' reads 't', which 'total_of' commits, at another sample"):
+        hawk.chain(C.total_of, C.reads_total, name="c")
+    with pytest.raises(HawkError, match="give at least one kernel"):
+        hawk.chain(name="c")
+
+
+@pytest.mark.parametrize("direction", ["jvp", "vjp"])
+def test_chain_derivatives_are_the_composed_programs(direction):
+    """The derivative of a chain (reference tests/test_chain.py:497-511) is
+    the derivative of its composed program: against the long-double chain
+    rule and central differences of the chain's value."""
+    import chain_members as C
+    members = (C.unit_circle, C.decay, C.scale_vec)
+    chained = hawk.chain(*members, name="dchain")
+    n = 300
+    g = np.random.default_rng(11)
+    x = g.uniform(0.2, 1.5, n)
+    seed = g.uniform(0.5, 1.5, (3, n))
+    ld = np.longdouble
+    la, lb = _long_double_chain(x)
+    da = np.stack([np.cos(x.astype(ld)), -np.sin(x.astype(ld)), np.full(n, ld("0.5"))])
+    db = np.exp(-(la * la).sum(axis=0)) * (-2 * (la * da).sum(axis=0)) + 1
+    tangent = da * lb + la * db                  # dy/dx, (3, n)
+    if direction == "jvp":
+        got = evaluate(jvp(chained, wrt=("x",)), {"x": x, "dot_x": np.ones(n)}, n)["dot_y"]
+        ref = tangent
+    else:
+        got = evaluate(vjp(chained, wrt=("x",)), {"x": x, "bar_y": seed}, n)["bar_x"]
+        ref = (seed.astype(ld) * tangent).sum(axis=0)
+    np.testing.assert_allclose(got, ref.astype(np.float64), rtol=1e-13, atol=1e-15)
+    h = 1e-6
+    yv = lambda xv: evaluate(chained.program, {"x": xv}, n)["y"]
+    fd = (yv(x + h) - yv(x - h)) / (2 * h)
+    fd = fd if direction == "jvp" else (seed * fd).sum(axis=0)
+    assert np.max(np.abs(got - fd)) / np.max(np.abs(fd)) < 1e-8
+    # every member's read of x is one input, so the derivative reaches all of them
+    assert len({id(n) for n in ir.leaves_of(ir.sink_roots(chained.sinks)) if n.literal[1] == "x"}) == 1

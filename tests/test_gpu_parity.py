@@ -982,3 +982,59 @@ def test_a_table_cell_every_key_reads_is_reported(gpu, tmp_path):
     with pytest.raises(HawkError, match="cell 0 of bar_t is read by more than one key"):
         hawk.run(hawk.load(tmp_path, back.name), t=dev(np.ones(keys), gpu), x=dev(x, gpu),
                  bar_out=dev(np.ones(keys), gpu), bar_t=bt)
+
+
+# -- hawk.chain -------------------------------------------------------------------
+
+def test_chain_is_its_members_launched_in_turn(gpu, tmp_path):
+    """One fused launch of the chain (reference tests/test_chain.py:150-177)
+    gives the bits of the four members launched one after another through
+    planes, twice; its JVP and VJP are within the reference's bound of the
+    long-double chain rule."""
+    import chain_members as C
+    import hawk_amd as hawk
+    from hawk_amd.diff import jvp, vjp
+    from hawk_amd.trace import Kernel
+    from ir_eval import evaluate
+    chained = hawk.chain(*C.MEMBERS, name="fixture")
+    tangent = Kernel("fixture_jvp", jvp(hawk.chain(C.unit_circle, C.decay, C.scale_vec, name="d"), wrt=("x",)))
+    adjoint = Kernel("fixture_vjp", vjp(hawk.chain(C.unit_circle, C.decay, C.scale_vec, name="d"), wrt=("x",)))
+    hawk.build([chained, *C.MEMBERS, tangent, adjoint], tmp_path)
+    n = 100_003
+    g = rng(5)
+    x, acc0 = g.uniform(0.1, 2.0, n), g.uniform(0.0, 1.0, n)
+    X = dev(x, gpu)
+    runs = []
+    for _ in range(2):
+        acc, y = dev(acc0, gpu), dev(np.zeros((3, n)), gpu)
+        print("chain fused", flush=True)
+        hawk.run(hawk.load(tmp_path, "fixture"), x=X, acc=acc, y=y)
+        runs.append((host(acc), host(y)))
+    assert runs[0][0].tobytes() == runs[1][0].tobytes() and runs[0][1].tobytes() == runs[1][1].tobytes()
+    a, b = dev(np.zeros((3, n)), gpu), dev(np.zeros(n), gpu)
+    acc, y = dev(acc0, gpu), dev(np.zeros((3, n)), gpu)
+    print("chain members", flush=True)
+    hawk.run(hawk.load(tmp_path, "unit_circle"), x=X, a=a)
+    hawk.run(hawk.load(tmp_path, "decay"), a=a, x=X, b=b)
+    hawk.run(hawk.load(tmp_path, "accumulate"), b=b, acc=acc)
+    hawk.run(hawk.load(tmp_path, "scale_vec"), a=a, b=b, y=y)
+    assert runs[0][0].tobytes() == host(acc).tobytes() and runs[0][1].tobytes() == host(y).tobytes()
+    ref = evaluate(chained.program, {"x": x, "acc": acc0}, n)
+    assert within_contract(runs[0][1], ref["y"]).all() and within_contract(runs[0][0], ref["acc"]).all()
+    # the derivatives against the long-double chain rule, within the reference's bound: 16 eps of the
+    # output's largest magnitude (tests/test_chain.py:47-54; the terms of dy/dx cancel)
+    ld = np.longdouble
+    xl = x.astype(ld)
+    a = np.stack([np.sin(xl), np.cos(xl), xl * ld("0.5")])
+    da = np.stack([np.cos(xl), -np.sin(xl), np.full(n, ld("0.5"))])
+    e = np.exp(-(a * a).sum(axis=0))
+    dydx = da * (e + xl) + a * (e * (-2 * (a * da).sum(axis=0)) + 1)
+    bound = lambda ref: 16 * np.finfo(np.float64).eps * float(np.max(np.abs(ref)))
+    dy = dev(np.zeros((3, n)), gpu)
+    hawk.run(hawk.load(tmp_path, "fixture_jvp"), x=X, dot_x=dev(np.ones(n), gpu), dot_y=dy)
+    assert float(np.max(np.abs(host(dy).astype(ld) - dydx))) <= bound(dydx)
+    seed = g.uniform(0.5, 1.5, (3, n))
+    bx = dev(np.zeros(n), gpu)
+    hawk.run(hawk.load(tmp_path, "fixture_vjp"), x=X, bar_y=dev(seed, gpu), bar_x=bx)
+    want = (seed.astype(ld) * dydx).sum(axis=0)
+    assert float(np.max(np.abs(host(bx).astype(ld) - want))) <= bound(want)

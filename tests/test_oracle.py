@@ -471,3 +471,22 @@ def test_net_axis_oracle_is_the_loop_over_nets_and_its_slope():
     np.testing.assert_allclose(scaled, got * bar[:, None], rtol=1e-12, atol=1e-300)
     assert O.net_loss(w, mask, x, y, threads=3).tobytes() == got_loss.tobytes()
     assert O.net_grad(w, mask, x, y, bar, threads=3).tobytes() == scaled.tobytes()
+
+
+def test_chain_members_oracle_is_the_long_double_chain():
+    """The chain of the four example members in C (glibc sin/cos/exp) within
+    a few ulp of the same formulas in long double, acc updated in place;
+    threaded == serial."""
+    g = np.random.default_rng(5)
+    n = 10_001
+    x, acc = g.uniform(0.1, 2.0, n), g.uniform(0.0, 1.0, n)
+    got_acc = acc.copy()
+    y = O.chain_members(x, got_acc)
+    ld = np.longdouble
+    xl = x.astype(ld)
+    a = np.stack([np.sin(xl), np.cos(xl), xl * ld("0.5")])
+    b = np.exp(-(a * a).sum(axis=0)) + xl
+    np.testing.assert_allclose(y, (a * b).astype(np.float64), rtol=4e-16 * 8)
+    np.testing.assert_allclose(got_acc, (acc.astype(ld) + b * b).astype(np.float64), rtol=4e-16 * 8)
+    acc2 = acc.copy()
+    assert O.chain_members(x, acc2, threads=3).tobytes() == y.tobytes() and acc2.tobytes() == got_acc.tobytes()
