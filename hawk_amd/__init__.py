@@ -33,12 +33,12 @@ _LAZY = {
     "Value": ("trace", "Value"),
     "sum": ("trace", "sum"),
     "scatter": ("trace", "scatter"),
-    "chain": ("chain", "chain"),
+    "chain": ("chaining", "chain"),
     "build": ("artifact", "build_bundle"),
     "load": ("runtime", "load"),
     "run": ("runtime", "run"),
 }
-_SUBMODULES = ("math", "diff", "runtime", "artifact", "compile", "ir", "emit_hip", "trace", "chain")
+_SUBMODULES = ("math", "diff", "runtime", "artifact", "compile", "ir", "emit_hip", "trace", "chaining")
 
 __all__ = ["Grid", "HawkError", "Index", "Matrix", "Mutable", "Param", "Scalar", "Table", "TensorType", "Vector",
            "__version__", *_LAZY, *_SUBMODULES]

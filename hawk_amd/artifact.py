@@ -84,6 +84,23 @@ def launch_shape(plan, mode: str) -> tuple:
     return (256, 1) if 32 < nbytes <= 64 else (128, 1)
 
 
+def _chain_record(k, sidecar: dict, mode: str) -> None:
+    """A chain's members, outputs, register estimate and fence in its sidecar
+    (reference ``hawk/ir/fusion.py``); one past its fence is reported."""
+    import warnings
+
+    from .chaining import estimate, fence
+    est = estimate(k.program, mode)
+    res = sidecar.get("resources") or {}
+    vgprs, scratch = res.get("vgpr_count"), res.get("private_segment_fixed_size") or 0
+    inside = None if vgprs is None else fence(vgprs, scratch, est)
+    sidecar["chain"] = {"members": [m.name for m in k.members], "outputs": list(k.outputs),
+                        "estimate_vgprs": est, "within_fence": inside}
+    if inside is False:
+        warnings.warn(f"chain {k.name!r} compiled to {vgprs} VGPRs and {scratch} B of scratch a lane, past "
+                      f"its fence (1.6 x the estimate {est} + 16): split it into shorter chains", stacklevel=3)
+
+
 def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64", cache_dir=None,
                  block: int | None = None, per_thread: int | None = None, nontemporal: bool = True,
                  fuse_folds: bool = True) -> Bundle:
@@ -154,6 +171,8 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
                 "fp_ops_per_sample": plan.algorithmic_ops,
                 "fp_ops_emitted": fp_ops_per_sample(plan.source),
             })
+        if getattr(k, "members", None) is not None:
+            _chain_record(k, sidecar, mode)
         _write(directory / f"{k.name}.json", json.dumps(sidecar, indent=1, sort_keys=True).encode())
         artifacts.append(Artifact(k.name, sidecar))
     digest = hashlib.sha256(json.dumps([a.sidecar for a in artifacts], sort_keys=True).encode()).hexdigest()

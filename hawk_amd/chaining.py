@@ -9,10 +9,14 @@ in the IR: the composed body holds each intermediate as one value, read by
 any number of members, and stores none of them, so one per-sample stage runs
 the whole chain and the intermediates never reach HBM.
 
-On gfx950 every boundary is fused (the reference fuses every boundary on a
-GPU too, ``hawk/ir/fusion.py:10``): a lane's registers hold the chain, and
-the build reports the compiled kernel's VGPRs and scratch in its sidecar.
-The derivative of a chain is the derivative of its composed program.
+On gfx950 every boundary is fused, as the reference fuses every boundary
+on a GPU (``hawk/ir/fusion.py:10``): a lane's registers hold the chain.  The
+build estimates the fused stage's registers from the composed body
+(:func:`estimate`, the reference's ``R0 + r x maxlive``,
+``hawk/ir/fusion.py:33-72``), and fences the compiled kernel with it
+(:func:`fence`, ``hawk/ir/fusion.py:124-126``): the sidecar records both,
+and a chain that compiles past the fence is reported.  The derivative of a
+chain is the derivative of its composed program.
 """
 
 from __future__ import annotations
@@ -158,3 +162,58 @@ def bind(members, keep=()) -> tuple:
     used = {n.literal[1] for n in ir.leaves_of(ir.sink_roots(sinks))} | {s.name for s in sinks}
     program.decls = {n: d for n, d in decls.items() if n in used}
     return program, outputs
+
+
+#: Registers a per-sample stage holds besides its values (the lane index,
+#: plane pointers and strides, loop counters), measured on gfx950 builds of
+#: the example kernels.
+R0 = 24
+#: The fence: registers plus scratch words may pass the estimate by this
+#: factor plus :data:`FENCE_SLACK` registers (the reference's constants).
+FENCE_RATIO = 1.6
+FENCE_SLACK = 16
+
+
+def maxlive(program: Program) -> int:
+    """The most elements per sample live at one point of ``program``'s body in
+    its topological order: a value is live from its node (a plane read from
+    the start, as the compiler hoists loads) to its last reader; a sink's
+    value to the end; a literal holds no register."""
+    roots = ir.sink_roots(program.sinks)
+    order = ir.topo(roots)
+    last = {}
+    for i, node in enumerate(order):
+        for o in node.operands:
+            last[o.uid] = i
+        if node.kind == "loop":
+            for x in node.literal.nexts:
+                last[x.uid] = i
+    end = len(order)
+    for r in roots:
+        last[r.uid] = end
+    delta = [0] * (end + 2)
+    for i, node in enumerate(order):
+        if node.kind in ("const", "iconst") or node.uid not in last or node.ttype.dtype == "tuple":
+            continue
+        width = 1
+        for d in node.ttype.shape:
+            width *= d
+        delta[0 if node.kind == "leaf" else i] += width
+        delta[last[node.uid] + 1] -= width
+    best = live = 0
+    for d in delta:
+        live += d
+        best = max(best, live)
+    return best
+
+
+def estimate(program: Program, mode: str = "float64") -> int:
+    """Predicted VGPRs of the fused stage: ``R0 + r x maxlive``, r = 2 for an
+    fp64 element, 1 for fp32."""
+    return R0 + (2 if mode == "float64" else 1) * maxlive(program)
+
+
+def fence(vgprs: int, scratch_bytes: int, est: int) -> bool:
+    """Whether a compiled chain stays inside its estimate: ``vgprs + scratch / 4
+    <= 1.6 x est + 16``."""
+    return vgprs + scratch_bytes / 4 <= FENCE_RATIO * est + FENCE_SLACK

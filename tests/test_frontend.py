@@ -804,6 +804,26 @@ def test_chain_binds_members_by_name_and_stores_no_intermediate():
     np.testing.assert_allclose(got["y"], (la * lb).astype(np.float64), rtol=1e-14)
 
 
+def test_a_chain_build_records_its_members_estimate_and_fence(tmp_path):
+    """The build fuses every boundary (the reference does on a GPU,
+    hawk/ir/fusion.py:10) and records the register estimate R0 + 2 maxlive
+    and the fence 1.6 est + 16 against the compiled kernel's VGPRs."""
+    import json
+
+    import chain_members as C
+    from hawk_amd.chaining import R0, estimate, fence, maxlive
+    chained = hawk.chain(*C.MEMBERS, name="fixture")
+    assert maxlive(chained.program) == 8            # x, acc, the three of a and y's three at the end
+    assert estimate(chained.program) == R0 + 16
+    hawk.build([chained], tmp_path)
+    side = json.loads((tmp_path / "fixture.json").read_text())
+    assert side["chain"]["members"] == ["unit_circle", "decay", "accumulate", "scale_vec"]
+    assert side["chain"]["outputs"] == ["acc", "y"] and side["chain"]["estimate_vgprs"] == R0 + 16
+    vgprs = side["resources"]["vgpr_count"]
+    assert side["chain"]["within_fence"] is fence(vgprs, 0, R0 + 16) is True
+    assert not fence(200, 0, 40) and fence(80, 0, 40)
+
+
 def test_chain_refusals_name_both_members_and_the_name():
     """The reference's refusals, by text (tests/test_chain.py:196-242)."""
     import chain_members as C
