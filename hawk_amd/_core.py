@@ -64,6 +64,7 @@ def _declare(lib) -> None:
         "hk_keyed_ordered_sum_f64": (I, [V, I64, I64, V, V, V]),
         "hk_mm16_f32": (I, [ctypes.POINTER(V), I, ctypes.POINTER(V), I, ctypes.POINTER(ctypes.c_int32), I64, V]),
         "hk_keyed_log_fold_scratch_bytes": (SZ, [I64]),
+        "hk_keyed_sample_sum_f64": (I, [V, I64, I64, V, V]),
         "hk_keyed_log_fold_f64": (I, [V, I64, V, I64, I64, ctypes.c_int32, V, I64, V, V, V]),
     }
     for name, (res, args) in sig.items():
@@ -319,6 +320,12 @@ def keyed_ordered_sum(u: int, n: int, group: int, out: int, scratch: int, stream
     """``out[k]`` = key k's ``group`` rows by the ordered sum's tree, k < n / group."""
     check(lib().hk_keyed_ordered_sum_f64(ctypes.c_void_p(u or None), int(n), int(group), ctypes.c_void_p(out),
                                          ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
+
+
+def keyed_sample_sum(u: int, n: int, group: int, out: int, stream: int = 0) -> None:
+    """``out[k]`` = key k's ``group`` rows as a default-policy sample sum of their own."""
+    check(lib().hk_keyed_sample_sum_f64(ctypes.c_void_p(u or None), int(n), int(group), ctypes.c_void_p(out or None),
+                                        ctypes.c_void_p(stream or None)))
 
 
 def keyed_log_fold_scratch_bytes(cells: int) -> int:

@@ -200,6 +200,94 @@ __global__ __launch_bounds__(256) void hawk_rows_levels(double* __restrict__ buf
     if (threadIdx.x == 0) *out = finite_bits(vh[0]) ? vh[0] + vc[0] : vh[0];
 }
 
+// hawk.sum(x, over=<trailing lane axes>) under the default policy: key k's
+// `group` consecutive values are summed as a sample sum of their own.  Rows
+// of 32 run from the key's first value (a ragged last row padded with +0),
+// each a compensated (hi, comp) pair by the pairs (l, l ^ 16), ..., (l, l ^ 1)
+// of a half-wave; the rows fold in the canonical tree above (leaves of 4096
+// rows over 256 slots with Neumaier's add, the halving tree, the leaves
+// pairwise level by level) and the key's cell is hi + comp.  One workgroup a
+// key: each half-wave sums one row, eight rows a step, and row r lands in
+// slot r % 256 in increasing r, so every slot adds its rows in order.
+constexpr long long kKeyedCompLeaves = kRowSlots;        // leaves a key may span
+
+__device__ __forceinline__ void row_pair_sum(double& h, double& c) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) {
+        const double h2 = __shfl_xor(h, off, 64);
+        const double c2 = __shfl_xor(c, off, 64);
+        const double s = h + h2;
+        c = finite_bits(s) ? (c + c2) + two_sum_err(h, h2, s) : 0.0;
+        h = s;
+    }
+}
+
+__global__ __launch_bounds__(kRowSlots) void hawk_keyed_comp(const double* __restrict__ u, long long group,
+                                                             double* __restrict__ out) {
+    __shared__ double sh[kRowSlots], sc[kRowSlots], lh[kKeyedCompLeaves], lc[kKeyedCompLeaves];
+    const int t = threadIdx.x, half = t >> 5, l = t & 31;
+    const double* __restrict__ mine = u + static_cast<long long>(blockIdx.x) * group;
+    const long long rows = (group + 31) / 32;
+    const long long leaves = (rows + kRowLeaf - 1) / kRowLeaf;
+    for (long long j = 0; j < leaves; ++j) {
+        const long long lo = j * kRowLeaf;
+        const int cnt = static_cast<int>(rows - lo < kRowLeaf ? rows - lo : kRowLeaf);
+        const int live = cnt < kRowSlots ? cnt : kRowSlots;
+        for (int rb = 0; rb < cnt; rb += 8) {
+            const int r = rb + half;
+            const long long at = (lo + r) * 32 + l;
+            double h = (r < cnt && at < group) ? __builtin_nontemporal_load(mine + at) : 0.0, c = 0.0;
+            row_pair_sum(h, c);
+            if (l == 0 && r < cnt) {
+                const int slot = r & (kRowSlots - 1);
+                if (r < kRowSlots) {
+                    sh[slot] = h;
+                    sc[slot] = finite_bits(h) ? c : 0.0;
+                } else {
+                    double a = sh[slot], b = sc[slot];
+                    neumaier_add(a, b, h, c);
+                    sh[slot] = a;
+                    sc[slot] = b;
+                }
+            }
+            __syncthreads();
+        }
+        for (int off = kRowSlots / 2; off > 0; off >>= 1) {
+            const int lim = live > off ? (off < live - off ? off : live - off) : 0;
+            if (t < lim) {
+                double h = sh[t], c = sc[t];
+                pair_add(h, c, sh[t + off], sc[t + off]);
+                sh[t] = h;
+                sc[t] = c;
+            }
+            __syncthreads();
+        }
+        if (t == 0) {
+            lh[j] = sh[0];
+            lc[j] = sc[0];
+        }
+        __syncthreads();
+    }
+    if (t == 0) {
+        long long m = leaves;
+        while (m > 1) {               // in place: pair p reads slots 2p, 2p + 1 >= p
+            const long long pairs = m / 2;
+            for (long long p = 0; p < pairs; ++p) {
+                double h = lh[2 * p], c = lc[2 * p];
+                pair_add(h, c, lh[2 * p + 1], lc[2 * p + 1]);
+                lh[p] = h;
+                lc[p] = c;
+            }
+            if (m & 1) {
+                lh[pairs] = lh[m - 1];
+                lc[pairs] = lc[m - 1];
+            }
+            m = pairs + (m & 1);
+        }
+        out[blockIdx.x] = finite_bits(lh[0]) ? lh[0] + lc[0] : lh[0];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Keyed fixed-tree sum: hawk.sum(x, over=<trailing lane axes>, policy=
 // "ordered").  Key k's rows are the `group` consecutive values
@@ -923,6 +1011,25 @@ int hk_keyed_ordered_sum_f64(const double* u, int64_t n, int64_t group, double* 
     hipLaunchKernelGGL(hawk_keyed_fold, dim3(static_cast<unsigned>(keys)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), lanes, lv, out);
     return launch_error("hawk_keyed_fold launch");
+}
+
+int hk_keyed_sample_sum_f64(const double* u, int64_t n, int64_t group, double* out, void* stream) {
+    if (n < 0 || group <= 0)
+        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: n must be >= 0 and group >= 1");
+    if (n % group != 0)
+        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: n (" + std::to_string(n) +
+                                                       ") is not a whole number of groups of " + std::to_string(group));
+    if ((group + 31) / 32 > kRowLeaf * kKeyedCompLeaves)
+        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: a key of " + std::to_string(group) +
+                                                       " samples spans more than 256 leaves of 4096 rows; sum it "
+                                                       "with policy='ordered'");
+    if (n == 0) return HK_OK;
+    if (!u || !out) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: u and out are required");
+    const long long keys = n / group;
+    if (keys > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: too many keys");
+    hipLaunchKernelGGL(hawk_keyed_comp, dim3(static_cast<unsigned>(keys)), dim3(kRowSlots), 0,
+                       static_cast<hipStream_t>(stream), u, static_cast<long long>(group), out);
+    return launch_error("hawk_keyed_comp launch");
 }
 
 size_t hk_rows_finish_scratch_bytes(int64_t rows) {

@@ -1068,7 +1068,7 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
             team.append({"op": "ordered_fold", "v": values, "c": cells, "out": s.name, "group": s.group,
                          "width": width})
             continue
-        if isinstance(s, SampleSum) and s.policy != "ordered":
+        if isinstance(s, SampleSum) and s.policy != "ordered" and s.group is None:
             if mode != "float64":
                 raise HawkError(f"hawk.sum(policy={s.policy!r}) on the hip target is built in float64")
             row_sums.append((s.name, s.value))
@@ -1076,7 +1076,7 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                          "out": s.name})
         elif isinstance(s, SampleSum):
             if mode != "float64":
-                raise HawkError("hawk.sum(policy='ordered') on the hip target is built in float64")
+                raise HawkError(f"hawk.sum(policy={s.policy!r}) on the hip target is built in float64")
             src = assigned.get(id(s.value))
             if src is None and s.value.kind == "leaf" and s.value.literal[0] == "per_sample":
                 src = s.value.literal[1]
@@ -1085,8 +1085,10 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                 extra.append((src, s.value))
             if s.group is None:
                 team.append({"op": "ordered_sum", "u": src, "out": s.name})
-            else:
+            elif s.policy == "ordered":
                 team.append({"op": "keyed_sum", "u": src, "out": s.name, "group": s.group})
+            else:                                   # the default policy over some axes
+                team.append({"op": "keyed_comp", "u": src, "out": s.name, "group": s.group})
         elif isinstance(s, AccumWrite):
             if mode != "float64":
                 raise HawkError("hawk.scatter(policy='ordered') on the hip target is built in float64")
@@ -1126,9 +1128,10 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
         for key in ("out", "target"):
             pname = t.get(key)
             if pname and isinstance(pname, str):
-                planes[pname] = {"role": "cell" if t["op"] in ("ordered_sum", "row_sum", "keyed_sum") else "accum_out",
+                planes[pname] = {"role": "cell" if t["op"] in ("ordered_sum", "row_sum", "keyed_sum", "keyed_comp")
+                                 else "accum_out",
                                  "shape": [], "dtype": "f64"}
-                if t["op"] == "keyed_sum":
+                if t["op"] in ("keyed_sum", "keyed_comp"):
                     planes[pname]["group"] = t["group"]       # one cell per `group` samples
     for pname, info in planes.items():
         if pname.startswith("hk_"):

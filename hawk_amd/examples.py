@@ -131,14 +131,15 @@ chain_jvp = Kernel("chain_jvp", diff.jvp(chain, wrt=("x",)))
 NET_UNITS, NET_WEIGHTS = 8, 24
 
 
-def net_loss_for(samples: int) -> Kernel:
+def net_loss_for(samples: int, policy: str = "ordered") -> Kernel:
     """Many small models in one launch (the reference's net axis,
     tests/test_net_axis.py): lanes are (net, sample); net k's weights are row
     k of the table ``W`` (unit h uses w[3h], w[3h+1], w[3h+2]), a mask row
     switches its unused units off, and its loss is the ordered sum of the
-    squared residuals over its own samples.  The VJP wrt ``W`` is the ordered
-    log fold: each net's gradient is the sum of its samples' contributions in
-    lane order."""
+    squared residuals over its own samples (``policy="auto"``: the default
+    sum of each net's samples).  Under the ordered policy the VJP wrt ``W`` is
+    the ordered log fold: each net's gradient is the sum of its samples'
+    contributions in lane order."""
     @kernel
     def net_loss(lane: Grid["net", "sample":samples], W: Table["net", "w":NET_WEIGHTS],
                  mask: Table["net", "h":NET_UNITS], x: Scalar, y: Scalar) -> Scalar:
@@ -147,8 +148,8 @@ def net_loss_for(samples: int) -> Kernel:
             act = tanh(W.at(net=lane.net, w=3 * h) * x + W.at(net=lane.net, w=3 * h + 1))
             pred = pred + mask.at(net=lane.net, h=h) * W.at(net=lane.net, w=3 * h + 2) * act
         r = pred - y
-        return _trace.sum(r * r, over="sample", policy="ordered")
-    return Kernel(f"net_loss_{samples}", net_loss.program)
+        return _trace.sum(r * r, over="sample", policy=policy)
+    return Kernel(f"net_loss_{samples}" + ("" if policy == "ordered" else f"_{policy}"), net_loss.program)
 
 
 @kernel

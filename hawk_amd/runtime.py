@@ -312,6 +312,8 @@ class DeviceKernel:
                 args, status, cells = self._fold_args(t, bound, n, device)
                 _core.keyed_log_fold(*args, stream)
                 statuses.append((t, status, cells))
+            elif t["op"] == "keyed_comp":
+                _core.keyed_sample_sum(bound[t["u"]].data_ptr(), n, t["group"], bound[t["out"]].data_ptr(), stream)
             else:
                 raise HawkError(f"kernel {self.name!r}: unknown team stage {t['op']!r}")
         if check:
@@ -466,6 +468,9 @@ class Prepared:
                 args, status, cells = kernel._fold_args(t, bound, self.n, device)
                 self.steps.append((_core.keyed_log_fold, args))
                 self.statuses.append((t, status, cells))
+            elif t["op"] == "keyed_comp":
+                args = (bound[t["u"]].data_ptr(), self.n, t["group"], bound[t["out"]].data_ptr())
+                self.steps.append((_core.keyed_sample_sum, args))
             else:
                 raise HawkError(f"kernel {kernel.name!r}: unknown team stage {t['op']!r}")
 
@@ -486,7 +491,8 @@ class Prepared:
                             per_thread=k.launch_shape["per_thread"], stream=self.stream)
             out.append((k.name, stage))
         labels = {_core.ordered_sum: "ordered_sum", _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16",
-                  _core.keyed_ordered_sum: "keyed_sum", _core.keyed_log_fold: "ordered_fold"}
+                  _core.keyed_ordered_sum: "keyed_sum", _core.keyed_log_fold: "ordered_fold",
+                  _core.keyed_sample_sum: "keyed_comp"}
         for fn, args in self.steps:
             label = labels.get(fn, "row_sum")
             out.append((label, lambda fn=fn, args=args: fn(*args, self.stream)))

@@ -326,7 +326,9 @@ def sum(x: Any, over: Any = None, policy: str = "auto") -> Reduced:  # noqa: A00
     samples, and each run takes that tree.  The default policies (``"auto"``,
     ``"compensated"``) sum each row of 32 samples as a compensated
     (hi, comp) pair and fold the rows in the canonical ordered tree of
-    reference ``hawk/_cells.py``; over some axes they are not in this build."""
+    reference ``hawk/_cells.py``; over some axes each key's run is such a sum
+    of its own (the reference commits keys atomically, in launch-dependent
+    order once a key spans three warps)."""
     if policy not in SUM_POLICIES:
         raise HawkError(f"hawk.sum(x, policy={policy!r}): policy={policy!r} is not one of {SUM_POLICIES}")
     n = _projected(node_of(x))
@@ -352,13 +354,9 @@ def sum(x: Any, over: Any = None, policy: str = "auto") -> Reduced:  # noqa: A00
     if len(reduced) == len(labels):
         return Reduced(n, policy)
     spelled = f"over={over!r}"
-    if policy != "ordered":
-        raise HawkError(f"hawk.sum(x, {spelled}, policy={policy!r}): a sum over some lane axes is built with "
-                        "policy='ordered' on this target (the default policies commit per key atomically in "
-                        "the reference)")
     if reduced != set(range(len(labels) - len(reduced), len(labels))):
-        raise HawkError(f"hawk.sum(x, {spelled}, policy='ordered'): policy='ordered' sums over the trailing "
-                        f"lane axes only (the Grid's axes are {labels})")
+        raise HawkError(f"hawk.sum(x, {spelled}, policy={policy!r}): policy={policy!r} sums over the trailing "
+                        f"lane axes only (the Grid's axes are {labels}): each key's samples are one run")
     group = 1
     for pos in reduced:
         group *= grid.axes[pos][1]

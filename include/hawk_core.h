@@ -181,6 +181,16 @@ size_t hk_keyed_ordered_sum_scratch_bytes(int64_t n, int64_t group);
 int hk_keyed_ordered_sum_f64(const double* u, int64_t n, int64_t group, double* out,
                              void* scratch, void* stream);
 
+/* `hawk.sum(x, over=<trailing lane axes>)` under the default policy: for
+ * k < n / group, out[k] = the default-policy sample sum of u[k*group ..
+ * (k+1)*group) on its own (compensated rows of 32 from the key's first value,
+ * the canonical ordered finish below, hi + comp).  The reference commits
+ * each key with atomic adds of per-warp partials (`hawk/emit/wrapper.py:
+ * 380-415`, the compensated accumulate), whose order varies between launches
+ * once a key spans three warps; here every key takes one fixed order.  A key
+ * of more than 2^25 samples is refused (HK_EVALUE).  No scratch. */
+int hk_keyed_sample_sum_f64(const double* u, int64_t n, int64_t group, double* out, void* stream);
+
 /* The finish of a default-policy sample sum (`hawk.sum(x)`): `rows`
  * compensated (hi, comp) row pairs (one per 32 samples, written by the
  * per-sample stage as reference `hawk/emit/wrapper.py:542-665` does) folded

@@ -268,6 +268,14 @@ HKO_EXPORT double hko_sample_sum(const double* t, int64_t n) {
     return out;
 }
 
+/* The default-policy keyed sum: each key's run of `group` values as a sample
+ * sum of its own (the device's fixed order; the reference's atomic commits,
+ * hawk/emit/wrapper.py:380-415, give these bits when a key spans at most two
+ * warps' partials and one of its possible results otherwise). */
+HKO_EXPORT void hko_keyed_sample_sum(const double* u, int64_t n, int64_t group, double* out) {
+    for (int64_t k = 0; k * group < n; ++k) out[k] = hko_sample_sum(u + k * group, group);
+}
+
 HKO_EXPORT double hko_ordered_sum(const double* u, int64_t n) {
     double gp[HKO_G];
     for (int g = 0; g < HKO_G; ++g) gp[g] = group_part(u, n, g);

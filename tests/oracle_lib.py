@@ -48,6 +48,7 @@ def lib(profile: str = "portable"):
         "hko_keyed_ordered_sum": (None, [_P, _I64, _I64, _P]),
         "hko_keyed_ordered_sum_threads": (None, [_P, _I64, _I64, _P, ctypes.c_int]),
         "hko_keyed_log_fold": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, ctypes.c_int32, _P, _I64]),
+        "hko_keyed_sample_sum": (None, [_P, _I64, _I64, _P]),
         "hko_net_threads": (None, [ctypes.c_int, _P, _P, _P, _P, _P, _I64, _I64, _P, ctypes.c_int]),
         "hko_chain_members_threads": (None, [_P, _P, _P, _I64, ctypes.c_int]),
         "hko_row_sums": (None, [_P, _I64, _P, _P]),
@@ -168,6 +169,15 @@ def keyed_ordered_sum(u, group: int, threads: int = 1, profile: str = "portable"
         lib(profile).hko_keyed_ordered_sum_threads(_p(u), u.size, group, _p(out), threads)
     else:
         lib(profile).hko_keyed_ordered_sum(_p(u), u.size, group, _p(out))
+    return out
+
+
+def keyed_sample_sum(u, group: int):
+    """One default-policy sample sum per run of ``group`` consecutive values."""
+    u = np.ascontiguousarray(u, dtype=np.float64)
+    assert u.size % group == 0
+    out = np.empty(u.size // group)
+    lib().hko_keyed_sample_sum(_p(u), u.size, group, _p(out))
     return out
 
 

@@ -116,6 +116,12 @@ def test_team_stage_arguments_are_checked_before_any_launch():
     rc = L.hk_keyed_log_fold_f64(None, 10, None, 2, 5, 1, None, 4, None, status, None)
     assert rc != 0 and b"required" in L.hk_last_error()
     assert L.hk_keyed_log_fold_scratch_bytes(1000) == 4000 and L.hk_keyed_log_fold_scratch_bytes(0) == 0
+    # the default-policy keyed sum: whole groups, keys of at most 2^25 samples
+    rc = L.hk_keyed_sample_sum_f64(None, 10, 3, None, None)
+    assert rc != 0 and b"whole number of groups" in L.hk_last_error()
+    rc = L.hk_keyed_sample_sum_f64(None, (1 << 25) + 32, (1 << 25) + 32, None, None)
+    assert rc != 0 and b"policy='ordered'" in L.hk_last_error()
+    assert L.hk_keyed_sample_sum_f64(None, 0, 4, None, None) == 0
     # the per-sample products: plane counts and indices are checked first
     rc = L.hk_mm16_f32(None, 0, None, 1, None, 1, None)
     assert rc != 0 and b"1..3 input planes" in L.hk_last_error()

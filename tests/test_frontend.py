@@ -499,9 +499,9 @@ def lane_coords(lane: hawk.Grid["a", "b":4, "c":8], y: Mutable[Scalar]):
 
 
 def test_grid_axes_and_refusals_follow_the_reference():
-    """Grid labels in numpy order, only the first bare; an ordered sum over
-    some axes sums the TRAILING ones only (reference
-    tests/test_ordered_trailing_axes.py:20-38, same messages)."""
+    """Grid labels in numpy order, only the first bare; a sum over some axes
+    sums the TRAILING ones only (reference tests/test_ordered_trailing_axes.py:20-38,
+    same messages), under either policy."""
     assert hawk.Grid["key", "sample":8].axes == (("key", None), ("sample", 8))
     with pytest.raises(HawkError, match="only the FIRST axis may"):
         hawk.Grid["a", "b"]
@@ -520,10 +520,17 @@ def test_grid_axes_and_refusals_follow_the_reference():
     def last_two(lane: hawk.Grid["a", "b":4, "c":8], x: Scalar, y: Mutable["a"]):
         y = hawk.sum(x, over=("b", "c"), policy="ordered")
     assert [(s.name, s.group) for s in last_two.sinks] == [("y", 32)]
-    with pytest.raises(HawkError, match="policy='ordered'"):
+    # the default policy over some axes: each key's run is a default sample sum of its own
+    @hawk.kernel
+    def compensated(lane: hawk.Grid["a", "b":8], x: Scalar, y: Mutable["a"]):
+        y = hawk.sum(x, over="b")
+    assert [(s.name, s.policy, s.group) for s in compensated.sinks] == [("y", "auto", 8)]
+    from hawk_amd.emit_hip import plan_kernel
+    assert plan_kernel(compensated.program, "c").team == [{"op": "keyed_comp", "u": "x", "out": "y", "group": 8}]
+    with pytest.raises(HawkError, match=r"policy='auto' sums over the trailing lane axes only"):
         @hawk.kernel
-        def compensated(lane: hawk.Grid["a", "b":8], x: Scalar, y: Mutable["a"]):
-            y = hawk.sum(x, over="b")
+        def leading_default(lane: hawk.Grid["a":4, "b":8], x: Scalar, y: Mutable["b":8]):
+            y = hawk.sum(x, over="a")
     with pytest.raises(HawkError, match="Grid parameter"):
         @hawk.kernel
         def no_grid(x: Scalar, y: Mutable["a"]):

@@ -1038,3 +1038,80 @@ def test_chain_is_its_members_launched_in_turn(gpu, tmp_path):
     hawk.run(hawk.load(tmp_path, "fixture_vjp"), x=X, bar_y=dev(seed, gpu), bar_x=bx)
     want = (seed.astype(ld) * dydx).sum(axis=0)
     assert float(np.max(np.abs(host(bx).astype(ld) - want))) <= bound(want)
+
+
+# -- the default policy over some axes --------------------------------------------
+
+def _keyed_default_kernel(group):
+    import hawk_amd as hawk
+    from hawk_amd import Grid, Scalar
+
+    @hawk.kernel
+    def kdefault(lane: Grid["key", "sample":group], x: Scalar) -> Scalar:
+        return hawk.sum(x, over="sample")
+    return kdefault
+
+
+@pytest.mark.parametrize("keys,group", [(4, 8), (1000, 40), (65536, 64), (3, 4096 * 32 + 5), (5000, 1),
+                                        (10, 100_000), (1, 1000), (777, 33)])
+def test_keyed_default_sum_is_the_oracle_bitwise(gpu, tmp_path, keys, group):
+    """hawk.sum(x, over=<trailing axes>) under the default policy: each key's
+    run is a default-policy sample sum of its own (compensated rows of 32 from
+    the key's first sample, the canonical finish), bit for bit the oracle's,
+    the same bits on a second launch; one key is the whole run's default sum."""
+    import hawk_amd as hawk
+    hawk.build([_keyed_default_kernel(group)], tmp_path)
+    kern = hawk.load(tmp_path, "kdefault")
+    assert [t["op"] for t in kern.team] == ["keyed_comp"]
+    n = keys * group
+    x = rng(keys + group).normal(size=n) * np.exp(rng(3).normal(size=n))
+    X = dev(x, gpu)
+    print(f"keyed default sum keys={keys} group={group}", flush=True)
+    outs = []
+    for _ in range(2):
+        out = dev(np.full(keys, np.nan), gpu)
+        hawk.run(kern, x=X, out=out)
+        outs.append(host(out))
+    want = O.keyed_sample_sum(x, group)
+    assert outs[0].tobytes() == want.tobytes() == outs[1].tobytes()
+    if keys == 1:
+        assert outs[0][0] == O.sample_sum(x)
+
+
+def test_net_loss_and_gradient_under_the_default_policy(gpu, tmp_path):
+    """The reference's default net axis (tests/test_net_axis.py:103-110,
+    :208-223): 16384 nets of 40 samples, the loss equal to the loop (rtol
+    1e-12) and to the ordered loss within 8 S eps, the same bits on a second
+    launch; its gradient wrt W (an ordered scatter of each read's
+    contribution: no ordered keyed sum to fold under) equal to the loop at
+    256 nets within 1e-10 and the same bits on a second launch."""
+    import hawk_amd as hawk
+    from hawk_amd import examples as E
+    from hawk_amd.diff import vjp
+    from hawk_amd.trace import Kernel
+    from net_axis import net_problem
+    s, k = 40, 16384
+    net, ordered = E.net_loss_for(s, "auto"), E.net_loss_for(s)
+    back = Kernel("net_grad_default", vjp(net, wrt=("W",)))
+    hawk.build([net, ordered, back], tmp_path)
+    assert [t["op"] for t in hawk.load(tmp_path, back.name).team] == ["ordered_scatter"] * E.NET_WEIGHTS
+    pick = rng(1).choice(k, 256, replace=False)
+    w, x, y, mask, loss, grad = net_problem(k, s, 3, pick)
+    W, M, X, Y = dev(w.ravel(), gpu), dev(mask.ravel(), gpu), dev(x.ravel(), gpu), dev(y.ravel(), gpu)
+    runs = []
+    for name in (net.name, net.name, ordered.name):
+        out = dev(np.zeros(k), gpu)
+        print(f"net loss {name}", flush=True)
+        hawk.run(hawk.load(tmp_path, name), W=W, mask=M, x=X, y=Y, out=out)
+        runs.append(host(out))
+    assert runs[0].tobytes() == runs[1].tobytes()
+    np.testing.assert_allclose(runs[0][pick], loss, rtol=1e-12)
+    np.testing.assert_allclose(runs[0], runs[2], rtol=8 * s * np.finfo(np.float64).eps)
+    seen = []
+    for _ in range(2):
+        bw = dev(np.zeros(k * E.NET_WEIGHTS), gpu)
+        print("net grad default", flush=True)
+        hawk.run(hawk.load(tmp_path, back.name), W=W, mask=M, x=X, y=Y, bar_out=dev(np.ones(k), gpu), bar_W=bw)
+        seen.append(host(bw).reshape(k, -1))
+    assert seen[0].tobytes() == seen[1].tobytes()
+    np.testing.assert_allclose(seen[0][pick], grad, rtol=1e-10, atol=1e-10)

@@ -490,3 +490,20 @@ def test_chain_members_oracle_is_the_long_double_chain():
     np.testing.assert_allclose(got_acc, (acc.astype(ld) + b * b).astype(np.float64), rtol=4e-16 * 8)
     acc2 = acc.copy()
     assert O.chain_members(x, acc2, threads=3).tobytes() == y.tobytes() and acc2.tobytes() == got_acc.tobytes()
+
+
+@pytest.mark.parametrize("keys,group", [(1, 1000), (7, 32), (5, 40), (3, 33), (4, 1), (2, 4096 * 32 + 5)])
+def test_keyed_sample_sum_is_each_keys_default_sum(keys, group):
+    """The default policy over some axes: each key's run is a default-policy
+    sample sum of its own, so one key is the whole run's sum bit for bit, and
+    each key is within a few ulp of math.fsum of its values (compensated rows,
+    the reference's row bound of tests/test_sample_sum.py:36-38)."""
+    import math
+    g = np.random.default_rng(keys * 7 + group)
+    x = g.normal(size=keys * group) * np.exp(g.normal(size=keys * group))
+    got = O.keyed_sample_sum(x, group)
+    for k in range(keys):
+        run = x[k * group:(k + 1) * group]
+        assert got[k] == O.sample_sum(run)
+        exact = math.fsum(run)
+        assert abs(got[k] - exact) <= 4 * np.spacing(abs(exact)) + 1e-14 * np.abs(run).sum()
