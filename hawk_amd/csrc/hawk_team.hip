@@ -207,8 +207,7 @@ __global__ __launch_bounds__(256) void hawk_rows_levels(double* __restrict__ buf
 // of a half-wave; the rows fold in the canonical tree above (leaves of 4096
 // rows over 256 slots with Neumaier's add, the halving tree, the leaves
 // pairwise level by level) and the key's cell is hi + comp.  One workgroup a
-// key: each half-wave sums one row, eight rows a step, and row r lands in
-// slot r % 256 in increasing r, so every slot adds its rows in order.
+// key; row r lands in slot r % 256 and every slot adds its rows in order.
 constexpr long long kKeyedCompLeaves = kRowSlots;        // leaves a key may span
 
 __device__ __forceinline__ void row_pair_sum(double& h, double& c) {
@@ -233,25 +232,39 @@ __global__ __launch_bounds__(kRowSlots) void hawk_keyed_comp(const double* __res
         const long long lo = j * kRowLeaf;
         const int cnt = static_cast<int>(rows - lo < kRowLeaf ? rows - lo : kRowLeaf);
         const int live = cnt < kRowSlots ? cnt : kRowSlots;
-        for (int rb = 0; rb < cnt; rb += 8) {
-            const int r = rb + half;
-            const long long at = (lo + r) * 32 + l;
-            double h = (r < cnt && at < group) ? __builtin_nontemporal_load(mine + at) : 0.0, c = 0.0;
-            row_pair_sum(h, c);
-            if (l == 0 && r < cnt) {
-                const int slot = r & (kRowSlots - 1);
-                if (r < kRowSlots) {
-                    sh[slot] = h;
-                    sc[slot] = finite_bits(h) ? c : 0.0;
-                } else {
-                    double a = sh[slot], b = sc[slot];
-                    neumaier_add(a, b, h, c);
-                    sh[slot] = a;
-                    sc[slot] = b;
+        // Half-wave `half` takes rows half, half + 8, ... in increasing order.
+        // Slot s gets rows s, s + 256, ..., all from the one half-wave (256 is
+        // a multiple of 8), so each slot's adds keep row order with no
+        // barrier; four rows' loads are in flight at a time.
+        for (int rb0 = 0; rb0 < cnt; rb0 += 32) {       // the same trips for every lane
+            const int rb = rb0 + half;
+            double x[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = rb + 8 * q;
+                const long long at = (lo + r) * 32 + l;
+                x[q] = (r < cnt && at < group) ? __builtin_nontemporal_load(mine + at) : 0.0;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = rb + 8 * q;
+                double h = x[q], c = 0.0;
+                row_pair_sum(h, c);
+                if (l == 0 && r < cnt) {
+                    const int slot = r & (kRowSlots - 1);
+                    if (r < kRowSlots) {
+                        sh[slot] = h;
+                        sc[slot] = finite_bits(h) ? c : 0.0;
+                    } else {
+                        double a = sh[slot], b = sc[slot];
+                        neumaier_add(a, b, h, c);
+                        sh[slot] = a;
+                        sc[slot] = b;
+                    }
                 }
             }
-            __syncthreads();
         }
+        __syncthreads();
         for (int off = kRowSlots / 2; off > 0; off >>= 1) {
             const int lim = live > off ? (off < live - off ? off : live - off) : 0;
             if (t < lim) {
@@ -286,6 +299,48 @@ __global__ __launch_bounds__(kRowSlots) void hawk_keyed_comp(const double* __res
         }
         out[blockIdx.x] = finite_bits(lh[0]) ? lh[0] + lc[0] : lh[0];
     }
+}
+
+// Keys of at most 64 rows (2048 samples): one wave a key, four keys a block.
+// The wave's halves sum two rows a step into the wave's slots (row r in slot
+// r: fewer than 256 rows, so no slot takes a second row), then the halving
+// tree over the R live slots, as the leaf above: the same bits.  A wave past
+// the last key computes nothing but meets every barrier.
+__global__ __launch_bounds__(256) void hawk_keyed_comp_wave(const double* __restrict__ u, long long group,
+                                                            long long keys, double* __restrict__ out) {
+    __shared__ double sh[4][64], sc[4][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, l = lane & 31;
+    const long long k = static_cast<long long>(blockIdx.x) * 4 + w;
+    const bool live = k < keys;
+    const double* __restrict__ mine = u + (live ? k : 0) * group;
+    const int rows = static_cast<int>((group + 31) / 32);
+    for (int rb = 0; rb < rows; rb += 2) {
+        const int r = rb + half;
+        const long long at = static_cast<long long>(r) * 32 + l;
+        double h = (live && r < rows && at < group) ? __builtin_nontemporal_load(mine + at) : 0.0, c = 0.0;
+        row_pair_sum(h, c);
+        if (l == 0 && r < rows) {
+            sh[w][r] = h;
+            sc[w][r] = finite_bits(h) ? c : 0.0;
+        }
+    }
+    __syncthreads();
+    for (int off = 32; off > 0; off >>= 1) {
+        const int lim = rows > off ? (off < rows - off ? off : rows - off) : 0;
+        double h = 0.0, c = 0.0;
+        if (lane < lim) {
+            h = sh[w][lane];
+            c = sc[w][lane];
+            pair_add(h, c, sh[w][lane + off], sc[w][lane + off]);
+        }
+        __syncthreads();
+        if (lane < lim) {
+            sh[w][lane] = h;
+            sc[w][lane] = c;
+        }
+        __syncthreads();
+    }
+    if (live && lane == 0) out[k] = finite_bits(sh[w][0]) ? sh[w][0] + sc[w][0] : sh[w][0];
 }
 
 // ---------------------------------------------------------------------------
@@ -1027,6 +1082,11 @@ int hk_keyed_sample_sum_f64(const double* u, int64_t n, int64_t group, double* o
     if (!u || !out) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: u and out are required");
     const long long keys = n / group;
     if (keys > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: too many keys");
+    if (group <= 64 * 32) {
+        hipLaunchKernelGGL(hawk_keyed_comp_wave, dim3(static_cast<unsigned>((keys + 3) / 4)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), u, static_cast<long long>(group), keys, out);
+        return launch_error("hawk_keyed_comp_wave launch");
+    }
     hipLaunchKernelGGL(hawk_keyed_comp, dim3(static_cast<unsigned>(keys)), dim3(kRowSlots), 0,
                        static_cast<hipStream_t>(stream), u, static_cast<long long>(group), out);
     return launch_error("hawk_keyed_comp launch");

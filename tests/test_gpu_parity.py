@@ -1053,12 +1053,13 @@ def _keyed_default_kernel(group):
 
 
 @pytest.mark.parametrize("keys,group", [(4, 8), (1000, 40), (65536, 64), (3, 4096 * 32 + 5), (5000, 1),
-                                        (10, 100_000), (1, 1000), (777, 33)])
+                                        (10, 100_000), (1, 1000), (777, 33), (50, 2048), (50, 2049), (7, 8191)])
 def test_keyed_default_sum_is_the_oracle_bitwise(gpu, tmp_path, keys, group):
     """hawk.sum(x, over=<trailing axes>) under the default policy: each key's
     run is a default-policy sample sum of its own (compensated rows of 32 from
     the key's first sample, the canonical finish), bit for bit the oracle's,
-    the same bits on a second launch; one key is the whole run's default sum."""
+    the same bits on a second launch; one key is the whole run's default sum.
+    Keys of up to 2048 samples take a wave each, longer ones a workgroup."""
     import hawk_amd as hawk
     hawk.build([_keyed_default_kernel(group)], tmp_path)
     kern = hawk.load(tmp_path, "kdefault")
