@@ -101,16 +101,47 @@ def _chain_record(k, sidecar: dict, mode: str) -> None:
                       f"its fence (1.6 x the estimate {est} + 16): split it into shorter chains", stacklevel=3)
 
 
+def _cut_chains(kernels, mode: str, register_line: int | None) -> tuple:
+    """``(kernels, chains)``: each chain the cut rule cuts replaced by its
+    segments (``<name>__s<i>``), and ``{chain name: its sidecar}``."""
+    from .chaining import REGISTER_LINE, cuts, segments
+    from .trace import Kernel as _Kernel
+    out, chains = [], {}
+    for k in kernels:
+        members = getattr(k, "members", None)
+        at = cuts(members, mode, register_line or REGISTER_LINE) if members else []
+        if not at:
+            out.append(k)
+            continue
+        names, crossing, planes = [], {}, {}
+        for i, (program, writes, _reads) in enumerate(segments(members, at)):
+            seg = _Kernel(f"{k.name}__s{i}", program)
+            out.append(seg)
+            names.append(seg.name)
+            for w in writes:
+                d = program.decls[w]
+                crossing[w] = {"shape": list(d.ttype.shape), "dtype": d.ttype.dtype}
+        chains[k.name] = {"kernel": k.name, "target": "hip", "offload_arch": "gfx950", "mode": mode,
+                          "segments": names, "crossing": crossing, "cuts": at,
+                          "chain": {"members": [m.name for m in members], "outputs": list(k.outputs)},
+                          "planes": planes, "entry": None, "team": []}
+    return out, chains
+
+
 def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64", cache_dir=None,
                  block: int | None = None, per_thread: int | None = None, nontemporal: bool = True,
-                 fuse_folds: bool = True) -> Bundle:
+                 fuse_folds: bool = True, register_line: int | None = None) -> Bundle:
     """Build ``kernels`` (a Kernel or a list of them) into ``directory``.
     ``block`` / ``per_thread`` fix every stage's launch shape; left ``None``
     each stage gets :func:`launch_shape`'s.  A stage that folds an ordered
     gradient in LDS keeps the block its keys need, one sample a thread
-    (``fuse_folds=False`` logs and folds in a team stage instead)."""
+    (``fuse_folds=False`` logs and folds in a team stage instead).  A
+    ``hawk.chain`` is cut where its fused estimate passes ``register_line``
+    VGPRs (default: the spill line, 512): its segments build as kernels of
+    their own and its sidecar lists them in order."""
     if isinstance(kernels, Kernel):
         kernels = [kernels]
+    kernels, chains = _cut_chains(list(kernels), mode, register_line)
     targets = tuple(targets)
     bad = [t for t in targets if t not in TARGETS]
     if bad:
@@ -175,6 +206,14 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
             _chain_record(k, sidecar, mode)
         _write(directory / f"{k.name}.json", json.dumps(sidecar, indent=1, sort_keys=True).encode())
         artifacts.append(Artifact(k.name, sidecar))
+    for name, sidecar in chains.items():
+        by_name = {a.name: a.sidecar for a in artifacts}
+        for seg in sidecar["segments"]:
+            for pname, info in by_name[seg]["planes"].items():
+                if not info.get("scratch") and pname not in sidecar["crossing"]:
+                    sidecar["planes"].setdefault(pname, info)
+        _write(directory / f"{name}.json", json.dumps(sidecar, indent=1, sort_keys=True).encode())
+        artifacts.append(Artifact(name, sidecar))
     digest = hashlib.sha256(json.dumps([a.sidecar for a in artifacts], sort_keys=True).encode()).hexdigest()
     manifest = {"target": "hip", "offload_arch": "gfx950", "mode": mode, "digest": digest,
                 "kernels": [a.name for a in artifacts]}

@@ -22,8 +22,9 @@ chain is the derivative of its composed program.
 from __future__ import annotations
 
 from . import ir
-from .ir import AccumWrite, Assign, HawkError, OrderedFold, Program
+from .ir import AccumWrite, Assign, Decl, HawkError, OrderedFold, Program
 from .trace import Kernel
+from .types import role_of
 
 #: The roles a member may read an intermediate as: its own lane's element.
 BOUND_LEAF_ROLES = ("per_sample", "vec_in", "mat_in", "mutable")
@@ -217,3 +218,91 @@ def fence(vgprs: int, scratch_bytes: int, est: int) -> bool:
     """Whether a compiled chain stays inside its estimate: ``vgprs + scratch / 4
     <= 1.6 x est + 16``."""
     return vgprs + scratch_bytes / 4 <= FENCE_RATIO * est + FENCE_SLACK
+
+
+# --------------------------------------------------------------------------
+# cuts: a chain past the register line runs as segments
+
+
+#: The prefix of the plane a cut chain passes a value through from one
+#: segment to the next (reference ``hawk/ir/chain.py:130``).
+CROSS_PREFIX = "hwc_"
+#: VGPRs a lane has before a kernel spills to scratch on gfx950: a chain is
+#: cut where fusing the next member would take its estimate past this line.
+REGISTER_LINE = 512
+
+
+def _reads(k: Kernel) -> set:
+    return {n.literal[1] for n in ir.leaves_of(ir.sink_roots(k.sinks))}
+
+
+def cuts(members, mode: str = "float64", line: int = REGISTER_LINE) -> list:
+    """The member boundaries to cut, greedy left to right (the shape of
+    reference ``hawk/ir/fusion.py:95-121``): boundary ``b`` (before member
+    ``b``) is cut when the segment from the last cut through member ``b``,
+    fused, is estimated past ``line`` registers.  A matrix never crosses a cut."""
+    out, a = [], 0
+    for b in range(1, len(members)):
+        later = set().union(*(_reads(k) for k in members[b:])) if b < len(members) else set()
+        crossing = [s for k in members[a:b] for s in k.sinks if s.name in later]
+        if any(len(s.value.ttype.shape) > 1 for s in crossing):
+            continue
+        after = set().union(*(_reads(k) for k in members[b + 1:])) if b + 1 < len(members) else set()
+        program, _ = bind(members[a:b + 1], keep=tuple(after))
+        if estimate(program, mode) > line:
+            out.append(b)
+            a = b
+    return out
+
+
+def segments(members, cut_at) -> list:
+    """``[(program, writes, reads)]``, one per segment of ``members`` cut before
+    each member index in ``cut_at`` (reference ``hawk/ir/chain.py:133-179``).
+    A value one segment computes and a later one reads crosses in a plane of
+    its own (``hwc_<name>``): the writer commits it there and the readers
+    read their own lane's element, as any per-sample input.  ``writes`` and
+    ``reads`` name those planes."""
+    bounds = [0, *cut_at, len(members)]
+    crossed: dict = {}                      # name -> ttype of a value an earlier segment stored
+    out = []
+    for a, b in zip(bounds, bounds[1:]):
+        later = set().union(*(_reads(k) for k in members[b:])) if b < len(members) else set()
+        program, outputs = bind(members[a:b], keep=tuple(later))
+        roots = ir.sink_roots(program.sinks)
+        mapping, reads = {}, []
+        for lf in ir.leaves_of(roots):
+            name = lf.literal[1]
+            if name in crossed and lf.uid not in mapping:
+                mapping[lf.uid] = ir.leaf(role_of(lf.ttype), CROSS_PREFIX + name, lf.ttype)
+                reads.append(CROSS_PREFIX + name)
+        sinks = list(program.sinks)
+        if mapping:
+            new = ir.substitute(roots, mapping)
+            rebuilt, at = [], 0
+            for s in sinks:
+                width = len(_sink_nodes(s))
+                rebuilt.append(_rebuilt(s, new[at:at + width]))
+                at += width
+            sinks = rebuilt
+        decls = {n: d for n, d in program.decls.items() if n not in crossed}
+        for name in reads:
+            base = name[len(CROSS_PREFIX):]
+            decls[name] = Decl(name, role_of(crossed[base]), crossed[base])
+        kept, writes = [], []
+        for s in sinks:
+            if s.name not in later:
+                kept.append(s)
+                continue
+            if not isinstance(s, Assign):
+                raise HawkError(f"chain: {s.name!r} would cross a cut as a sum or a scatter; end the chain there")
+            cross = CROSS_PREFIX + s.name
+            kept.append(Assign(cross, s.value, "mutable"))
+            decls[cross] = Decl(cross, "mutable", s.value.ttype)
+            decls.pop(s.name, None)
+            writes.append(cross)
+            crossed[s.name] = s.value.ttype
+        segment = Program(decls, kept, program.grid, dict(program.tables))
+        used = {n.literal[1] for n in ir.leaves_of(ir.sink_roots(kept))} | {s.name for s in kept}
+        segment.decls = {n: d for n, d in decls.items() if n in used}
+        out.append((segment, writes, reads))
+    return out

@@ -360,7 +360,82 @@ def _status_problem(name: str, t: dict, status, cells: int) -> str | None:
     return None
 
 
-def load(directory, kernel: str, sidecar: dict | None = None) -> DeviceKernel:
+class ChainedKernel:
+    """A ``hawk.chain`` the build cut into segments: each segment is a kernel
+    of its own, run in order; a value one segment passes to a later one
+    crosses in a plane the runtime holds (``hwc_<name>``), made once per
+    sample count (reference ``hawk/ir/chain.py:133-179``)."""
+
+    def __init__(self, directory: Path, sidecar: dict):
+        self.directory = Path(directory)
+        self.sidecar = sidecar
+        self.name = sidecar["kernel"]
+        self.planes = sidecar["planes"]
+        self.team = []
+        self.segments = [load(directory, s) for s in sidecar["segments"]]
+        self.crossing = sidecar["crossing"]
+        self._held: dict = {}
+        self._lock = threading.Lock()
+
+    def caller_planes(self) -> list:
+        return list(self.planes)
+
+    def _bindings(self, arrays: dict, n_samples=None) -> list:
+        """Each segment's planes: the caller's and the crossing planes it reads or writes."""
+        torch = _torch()
+        declared = set(self.planes)
+        unknown = sorted(set(arrays) - declared)
+        if unknown:
+            raise HawkError(f"kernel {self.name!r}: {unknown} are not planes it declares "
+                            f"(declared: {sorted(declared)})")
+        missing = sorted(declared - set(arrays))
+        if missing:
+            raise HawkError(f"kernel {self.name!r}: bind {missing}")
+        ns = {int(x.shape[-1]) for name, x in arrays.items()
+              if isinstance(x, torch.Tensor) and self.planes[name]["role"] in _PER_SAMPLE}
+        n = n_samples if n_samples is not None else (ns.pop() if len(ns) == 1 else None)
+        if n is None:
+            raise HawkError(f"kernel {self.name!r}: its planes disagree on the sample count, or none is bound")
+        device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
+        cross = {}
+        for name, info in self.crossing.items():
+            key = (name, n, device)
+            held = self._held.get(key)
+            if held is None:
+                dt = torch.int32 if info["dtype"] == "i32" else torch.float64
+                held = torch.empty(tuple(info["shape"]) + (n,), dtype=dt, device=device)
+                self._held[key] = held
+            cross[name] = held
+        out = []
+        for seg in self.segments:
+            names = seg.caller_planes()
+            out.append((seg, {p: (cross[p] if p in cross else arrays[p]) for p in names}))
+        return out
+
+    def prepare(self, *, stream=None, **arrays):
+        return _PreparedChain(self, arrays, stream)
+
+
+class _PreparedChain:
+    """The segments of a cut chain, each bound once (see :meth:`DeviceKernel.prepare`)."""
+
+    def __init__(self, chain: ChainedKernel, arrays: dict, stream=None):
+        self.kernel = chain
+        self.parts = [seg.prepare(stream=stream, **planes) for seg, planes in chain._bindings(dict(arrays))]
+
+    def __call__(self) -> None:
+        for part in self.parts:
+            part()
+
+    def stages(self) -> list:
+        return [step for part in self.parts for step in part.stages()]
+
+    def check(self) -> None:
+        for part in self.parts:
+            part.check()
+
+
+def load(directory, kernel: str, sidecar: dict | None = None):
     """Open ``<directory>/<kernel>`` of a unit built for the hip target."""
     directory = Path(directory)
     if sidecar is None:
@@ -368,6 +443,8 @@ def load(directory, kernel: str, sidecar: dict | None = None) -> DeviceKernel:
         if not path.exists():
             raise HawkError(f"{directory} holds no kernel {kernel!r} (no {path.name})")
         sidecar = json.loads(path.read_text())
+    if sidecar.get("segments"):
+        return ChainedKernel(directory, sidecar)
     return DeviceKernel(directory, sidecar)
 
 
@@ -378,6 +455,12 @@ def run(kernel: DeviceKernel, *, base: int = 0, count: int | None = None, n_samp
     A kernel with team stages (``hawk.sum`` / ``hawk.scatter`` with
     policy='ordered') runs over every sample (no ``base``/``count``)."""
     torch = _torch()
+    if isinstance(kernel, ChainedKernel):
+        if base != 0 or count is not None:
+            raise HawkError(f"{kernel.name}: a cut chain runs over every sample (no base= or count=)")
+        for seg, planes in kernel._bindings(dict(arrays), n_samples):
+            run(seg, n_samples=n_samples, stream=stream, check=check, **planes)
+        return
     if not isinstance(kernel, DeviceKernel):
         raise HawkError("hawk.run takes a kernel loaded with hawk.load")
     n = kernel.check_planes(arrays, n_samples)

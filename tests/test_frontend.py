@@ -879,3 +879,33 @@ def test_chain_derivatives_are_the_composed_programs(direction):
     assert np.max(np.abs(got - fd)) / np.max(np.abs(fd)) < 1e-8
     # every member's read of x is one input, so the derivative reaches all of them
     assert len({id(n) for n in ir.leaves_of(ir.sink_roots(chained.sinks)) if n.literal[1] == "x"}) == 1
+
+
+def test_a_chain_past_the_register_line_is_cut_into_segments(tmp_path):
+    """The cut rule (reference hawk/ir/fusion.py:95-121): at the spill line
+    the example chain fuses whole; with a line of 32 registers every boundary
+    is cut, each segment a kernel of its own, the values passing through
+    hwc_ planes; the segments composed give the fused chain's values, bit for
+    bit (the same operations)."""
+    import json
+
+    import chain_members as C
+    from hawk_amd import chaining as CH
+    chained = hawk.chain(*C.MEMBERS, name="fixture")
+    assert CH.cuts(C.MEMBERS) == [] and CH.cuts(C.MEMBERS, line=32) == [1, 2, 3]
+    segs = CH.segments(C.MEMBERS, [1, 2, 3])
+    assert [(w, r) for _, w, r in segs] == [(["hwc_a"], []), (["hwc_b"], ["hwc_a"]), ([], ["hwc_b"]),
+                                            ([], ["hwc_a", "hwc_b"])]
+    n = 101
+    g = np.random.default_rng(2)
+    x, acc0 = g.uniform(0.1, 2.0, n), g.uniform(0.0, 1.0, n)
+    env = {"x": x, "acc": acc0}
+    for prog, _, _ in segs:                     # each segment reads the planes the earlier ones wrote
+        env = {**env, **evaluate(prog, env, n)}
+    fused = evaluate(chained.program, {"x": x, "acc": acc0}, n)
+    assert env["y"].tobytes() == fused["y"].tobytes() and env["acc"].tobytes() == fused["acc"].tobytes()
+    hawk.build([chained], tmp_path, register_line=32)
+    side = json.loads((tmp_path / "fixture.json").read_text())
+    assert side["segments"] == ["fixture__s0", "fixture__s1", "fixture__s2", "fixture__s3"]
+    assert side["crossing"] == {"hwc_a": {"shape": [3], "dtype": "f64"}, "hwc_b": {"shape": [], "dtype": "f64"}}
+    assert set(side["planes"]) == {"x", "acc", "y"} and side["cuts"] == [1, 2, 3]

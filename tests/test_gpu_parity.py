@@ -1116,3 +1116,30 @@ def test_net_loss_and_gradient_under_the_default_policy(gpu, tmp_path):
         seen.append(host(bw).reshape(k, -1))
     assert seen[0].tobytes() == seen[1].tobytes()
     np.testing.assert_allclose(seen[0][pick], grad, rtol=1e-10, atol=1e-10)
+
+
+def test_a_cut_chain_is_the_fused_chain(gpu, tmp_path):
+    """A chain cut at every boundary (a register line of 32, reference
+    tests/test_chain.py:298-334) runs as four segment kernels through hwc_
+    planes and gives the fused chain's bits, by hawk.run and by prepare."""
+    import chain_members as C
+    import hawk_amd as hawk
+    chained = hawk.chain(*C.MEMBERS, name="fixture")
+    hawk.build([chained], tmp_path / "fused")
+    hawk.build([chained], tmp_path / "cut", register_line=32)
+    cut = hawk.load(tmp_path / "cut", "fixture")
+    assert [s.name for s in cut.segments] == [f"fixture__s{i}" for i in range(4)]
+    n = 100_003
+    g = rng(8)
+    x, acc0 = g.uniform(0.1, 2.0, n), g.uniform(0.0, 1.0, n)
+    X = dev(x, gpu)
+    got = []
+    for kern, how in ((hawk.load(tmp_path / "fused", "fixture"), "run"), (cut, "run"), (cut, "prepare")):
+        acc, y = dev(acc0, gpu), dev(np.zeros((3, n)), gpu)
+        print(f"chain {how} {type(kern).__name__}", flush=True)
+        if how == "run":
+            hawk.run(kern, x=X, acc=acc, y=y)
+        else:
+            kern.prepare(x=X, acc=acc, y=y)()
+        got.append((host(acc).tobytes(), host(y).tobytes()))
+    assert got[0] == got[1] == got[2]
