@@ -1143,3 +1143,44 @@ def test_a_cut_chain_is_the_fused_chain(gpu, tmp_path):
             kern.prepare(x=X, acc=acc, y=y)()
         got.append((host(acc).tobytes(), host(y).tobytes()))
     assert got[0] == got[1] == got[2]
+
+
+def test_folds_and_keyed_sums_keep_ieee_specials_and_empty_runs(gpu, tmp_path):
+    """Inf, NaN and -0 through the ordered fold (in LDS and logged) and the
+    keyed sums, against the oracle bit for bit (NaN as NaN); a run of no
+    samples leaves the outputs as they were."""
+    import hawk_amd as hawk
+    from hawk_amd.diff import vjp
+    from hawk_amd.trace import Kernel
+    from ir_eval import evaluate
+    group, keys = 40, 300
+    back = Kernel("kt_vjp", vjp(_keyed_table_kernel(group), wrt=("t",)))
+    hawk.build([back], tmp_path / "fused")
+    hawk.build([back], tmp_path / "logged", fuse_folds=False)
+    hawk.build([_keyed_default_kernel(group), _keyed_kernels(group)], tmp_path / "sums")
+    n = keys * group
+    g = rng(17)
+    t, x, bar = g.normal(size=keys * 3), g.normal(size=n), g.normal(size=keys)
+    x[5], x[n // 2], x[n - 1], x[77] = np.inf, -np.inf, np.nan, -0.0
+    t[4] = np.inf
+    values, cells = evaluate(back.program, {"t": t, "x": x, "bar_out": bar}, n)["bar_t"]
+    want = np.zeros(keys * 3)
+    assert O.keyed_log_fold(np.stack(values), np.stack([c[::group] for c in cells]), group, want) == 0
+    for sub in ("fused", "logged"):
+        bt = dev(np.zeros(keys * 3), gpu)
+        print(f"fold specials {sub}", flush=True)
+        hawk.run(hawk.load(tmp_path / sub, "kt_vjp"), t=dev(t, gpu), x=dev(x, gpu), bar_out=dev(bar, gpu), bar_t=bt)
+        got = host(bt)
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        assert got[~np.isnan(got)].tobytes() == want[~np.isnan(want)].tobytes()
+    for name, oracle in (("kdefault", O.keyed_sample_sum), ("ksum", O.keyed_ordered_sum)):
+        out = dev(np.full(keys, 3.0), gpu)
+        print(f"keyed specials {name}", flush=True)
+        hawk.run(hawk.load(tmp_path / "sums", name), x=dev(x, gpu), out=out)
+        got, w = host(out), oracle(x, group)
+        assert np.array_equal(np.isnan(got), np.isnan(w)) and got[~np.isnan(got)].tobytes() == w[~np.isnan(w)].tobytes()
+    # no samples: nothing written
+    bt = dev(np.full(keys * 3, 7.0), gpu)
+    hawk.run(hawk.load(tmp_path / "fused", "kt_vjp"), t=dev(t, gpu), x=dev(np.zeros(0), gpu),
+             bar_out=dev(np.zeros(0), gpu), bar_t=bt)
+    assert (host(bt) == 7.0).all()
