@@ -909,3 +909,31 @@ def test_a_chain_past_the_register_line_is_cut_into_segments(tmp_path):
     assert side["segments"] == ["fixture__s0", "fixture__s1", "fixture__s2", "fixture__s3"]
     assert side["crossing"] == {"hwc_a": {"shape": [3], "dtype": "f64"}, "hwc_b": {"shape": [], "dtype": "f64"}}
     assert set(side["planes"]) == {"x", "acc", "y"} and side["cuts"] == [1, 2, 3]
+
+
+def test_a_chain_passes_params_tables_and_grids_through(tmp_path):
+    """Members on one Grid, reading a Param and a Table, chain like any
+    others: the Param and the Table stay inputs of the chain, the keyed sum
+    of the last member reads the first member's per-lane value, and the
+    composed values are the members' run in turn."""
+    from hawk_amd import Grid, Param, Table
+
+    @hawk.kernel
+    def weigh(lane: Grid["key", "s":4], w: Table["key", "j":2], x: Scalar, scale: Param, u: Mutable[Scalar]):
+        u = w.at(key=lane.key, j=0) * x * scale + w.at(key=lane.key, j=1)
+
+    @hawk.kernel
+    def total(lane: Grid["key", "s":4], u: Scalar) -> Scalar:
+        return hawk.sum(u * u, over="s", policy="ordered")
+
+    chained = hawk.chain(weigh, total, name="wt")
+    assert {n for _, n in chained.arg_spec} == {"w", "x", "scale", "out"}
+    assert chained.program.tables == {"w": (("key", None), ("j", 2))}
+    n = 40
+    g = np.random.default_rng(4)
+    w, x = g.normal(size=20), g.normal(size=n)
+    got = evaluate(chained.program, {"w": w, "x": x, "scale": 1.5}, n)["out"]
+    u = evaluate(weigh.program, {"w": w, "x": x, "scale": 1.5}, n)["u"]
+    assert got.tobytes() == (u * u).tobytes()
+    back = vjp(chained, wrt=("w",))                 # the keyed sum is ordered: the table's gradient folds
+    assert [type(s).__name__ for s in back.sinks] == ["OrderedFold"]
