@@ -9,7 +9,10 @@ way; ``--config 5k`` times config 5's ordered sum in the reference's keyed
 spelling (``hawk.sum(x, over=...)``) over 16384 keys, ``--config 5t`` a
 ``Table`` read at config 5's keys and its VJP (an ordered scatter), and
 ``--config 5n`` 65536 small models in one launch (the net axis): each net's
-ordered loss and its gradient wrt its weights (the ordered log fold).
+ordered loss and its gradient wrt its weights (the ordered log fold);
+``--config chain`` four kernels chained into one launch (``hawk.chain``), and
+``--config steps`` an oscillator that finishes its own sample, 8 steps a
+launch (``hawk.steps``), over 2^24 samples.
 
 Each stage launch of the timed steps (a per-sample kernel, or a team stage:
 the ordered sum or the ordered scatter) is bracketed by HIP events on the
@@ -297,6 +300,28 @@ def workload(config: str, device):
             O.chain_members(x, acc0.copy(), threads=threads, profile="native")
         return dict(name="hawk.chain of four kernels (vector and scalar passed by name), one launch", n=n,
                     kernels=kernels, work=work, cpu=cpu, dtype="f64", compare=members_ms)
+    if config == "steps":
+        # a kernel finishing its own sample, stepped 8 times a launch (reference hawk/trace/steps.py):
+        # the explicit-Euler oscillator, every sample live (t_final past every timed step), so
+        # each launch takes 8 steps of every sample with its state in registers between them
+        k8 = E.osc_finish_x8
+        n = 1 << 24
+        g = np.random.default_rng(17)
+        x, v = g.uniform(-1.0, 1.0, n), g.uniform(-1.0, 1.0, n)
+        t_final = np.full(n, 1e30)
+        hawk.build([k8], unit)
+        kk = hawk.load(unit, k8.name)
+        planes = {"x": _dev(x, device), "v": _dev(v, device), "t": torch.zeros(n, dtype=torch.float64, device=device),
+                  "t_final": _dev(t_final, device), "terminated": torch.zeros(n, dtype=torch.bool, device=device)}
+        kernels = [kk.prepare(dt=E.OSC_DT, **planes)]
+        work = {k8.name: (33 + 24, ops(kk))}      # x, v, t, t_final and the mask in; x, v, t out
+
+        def cpu(threads):
+            import oracle_lib as O
+            O.osc_launch(8, E.OSC_DT, t_final, x.copy(), v.copy(), np.zeros(n), np.zeros(n, dtype=bool),
+                         profile="native")
+        return dict(name="oscillator finishing its own sample, 8 steps a launch (hawk.steps)", n=n,
+                    kernels=kernels, work=work, cpu=cpu, dtype="f64", cpu_threads=1)
     if config == "5n":
         # the net axis (reference tests/test_net_axis.py): 65536 small models of 64 samples in one
         # launch, each net's loss an ordered keyed sum and its gradient wrt its 24 weights the
@@ -515,7 +540,7 @@ def main() -> int:
                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(d["hbm_frac"], 4), "traffic": traffic}
     cpu_baseline = None
     if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
+        threads = w.get("cpu_threads") or min(os.cpu_count() or 1, 16)
         log(f"CPU baseline: oracle (native profile) on {threads} threads")
         import oracle_lib as O
         O.build("native")

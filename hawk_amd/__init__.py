@@ -23,7 +23,7 @@ tensors.  Typical use::
 from __future__ import annotations
 
 from .ir import HawkError
-from .types import Grid, Index, Matrix, Mutable, Param, Scalar, Table, TensorType, Vector
+from .types import Grid, Index, Matrix, Mutable, Param, Scalar, Table, TensorType, Terminated, Vector
 
 __version__ = "0.1.0"
 
@@ -34,13 +34,15 @@ _LAZY = {
     "sum": ("trace", "sum"),
     "scatter": ("trace", "scatter"),
     "chain": ("chaining", "chain"),
+    "steps": ("trace", "steps"),
     "build": ("artifact", "build_bundle"),
     "load": ("runtime", "load"),
     "run": ("runtime", "run"),
 }
 _SUBMODULES = ("math", "diff", "runtime", "artifact", "compile", "ir", "emit_hip", "trace", "chaining")
 
-__all__ = ["Grid", "HawkError", "Index", "Matrix", "Mutable", "Param", "Scalar", "Table", "TensorType", "Vector",
+__all__ = ["Grid", "HawkError", "Index", "Matrix", "Mutable", "Param", "Scalar", "Table", "TensorType", "Terminated",
+           "Vector",
            "__version__", *_LAZY, *_SUBMODULES]
 
 

@@ -21,7 +21,7 @@ from . import compile as _compile
 from .emit_hip import fp_ops_per_sample
 from .resources import kernel_resources
 from .emit_hip import plan_kernel
-from .ir import HawkError
+from .ir import FINISHED_PLANE, Finish, HawkError
 from .trace import Kernel
 
 TARGETS = ("hip",)
@@ -202,6 +202,12 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
                 "fp_ops_per_sample": plan.algorithmic_ops,
                 "fp_ops_emitted": fp_ops_per_sample(plan.source),
             })
+        finish = next((s for s in k.program.sinks if isinstance(s, Finish)), None)
+        if plan.stage is not None and plan.stage.guard is not None:
+            # reference tests/test_finish_own_sample.py:98-106
+            sidecar["terminated_readonly"] = finish is None
+            if finish is not None:
+                sidecar["finish"] = {"mask": finish.name, "counter": FINISHED_PLANE, "steps": finish.steps}
         if getattr(k, "members", None) is not None:
             _chain_record(k, sidecar, mode)
         _write(directory / f"{k.name}.json", json.dumps(sidecar, indent=1, sort_keys=True).encode())

@@ -22,8 +22,8 @@ plane ``bar_x``; a tangent input is ``dot_x`` and a tangent output ``dot_y``.
 from __future__ import annotations
 
 from . import ir
-from .ir import (AccumWrite, Assign, Decl, Deps, HawkError, Node, OrderedFold, Program, SampleSum,
-                 fresh_placeholders, free_inputs, level_order, make, zero_like)
+from .ir import (GUARD_MASK, AccumWrite, Assign, Decl, Deps, Finish, HawkError, Node, OrderedFold, Program,
+                 SampleSum, fresh_placeholders, free_inputs, level_order, make, zero_like)
 from .trace import Kernel
 from .types import TensorType, role_of
 
@@ -317,11 +317,30 @@ def _refuse_prior_reads(program: Program, what: str) -> None:
 
 
 def _program_of(kernel) -> Program:
+    """The program a derivative is taken of: a finishing kernel's without its
+    finish (a derived kernel reads the mask through its guard and never
+    finishes, reference ``tests/test_finish_own_sample.py:111-120``)."""
     if isinstance(kernel, Kernel):
-        return kernel.program
-    if isinstance(kernel, Program):
-        return kernel
-    raise HawkError("vjp/jvp take a @hawk.kernel (or a Kernel)")
+        program = kernel.program
+    elif isinstance(kernel, Program):
+        program = kernel
+    else:
+        raise HawkError("vjp/jvp take a @hawk.kernel (or a Kernel)")
+    finishes = [s for s in program.sinks if isinstance(s, Finish)]
+    if not finishes:
+        return program
+    if any(f.steps != 1 for f in finishes):
+        raise HawkError(f"vjp/jvp of a kernel taking {finishes[0].steps} steps a launch (hawk.steps): "
+                        "differentiate the single step (its .step)")
+    return Program(dict(program.decls), [s for s in program.sinks if not isinstance(s, Finish)], program.grid,
+                   dict(program.tables))
+
+
+def _keep_guard(program: Program, out: Program) -> None:
+    """A derived kernel of a guarded kernel is guarded by the same mask, read only."""
+    d = program.decls.get(GUARD_MASK)
+    if d is not None and d.role == "terminated":
+        out.decls[GUARD_MASK] = d
 
 
 def _namer(program: Program, prefix: str):
@@ -405,6 +424,7 @@ def vjp(kernel, wrt=None) -> Program:
     target_leaves = [leaf_nodes[d.name] for d in targets if d.name in leaf_nodes]
     rev = _Reverse({n.uid for n in target_leaves})
     out = Program(grid=program.grid, tables=dict(program.tables))
+    _keep_guard(program, out)
     seeds = []
     for s, root in zip(program.sinks, roots):
         seed_name = name(s.name)
@@ -600,6 +620,7 @@ def jvp(kernel, wrt=None) -> Program:
             out.tables[tname] = program.tables[d.name]
         if d.name in leaf_nodes:
             tangent_leaves[leaf_nodes[d.name].uid] = ir.leaf(d.role, tname, d.ttype)
+    _keep_guard(program, out)
     fwd = _Forward(tangent_leaves)
     fwd.tangents(roots)
     for s in program.sinks:
@@ -625,5 +646,6 @@ def _drop_unused_inputs(program: Program) -> None:
     """Keep the declarations the derived body reads or writes."""
     used = {n.literal[1] for n in ir.leaves_of(ir.sink_roots(program.sinks))}
     used |= {s.name for s in program.sinks}
-    program.decls = {k: d for k, d in program.decls.items() if k in used}
+    program.decls = {k: d for k, d in program.decls.items()
+                     if k in used or (k == GUARD_MASK and d.role == "terminated")}
 

@@ -31,7 +31,8 @@ import dataclasses
 from dataclasses import dataclass, field
 
 from . import ir
-from .ir import (AccumWrite, Assign, Deps, HawkError, Node, OrderedFold, Program, SampleSum, free_inputs,
+from .ir import (FINISHED_PLANE, GUARD_MASK, AccumWrite, Assign, Deps, Finish, HawkError, Node, OrderedFold,
+                 Program, SampleSum, free_inputs,
                  level_order)
 
 ABI_TAG = "aether-abi/2"
@@ -55,7 +56,7 @@ def kind_for(role: str, ttype, mode: str) -> str:
         return "f32" if mode == "float32" else "f64"
     shape = "gref" if role in ("out", "vec_in", "mat_in") or (role in ("mutable", "wide_out", "key_out")
                                                               and ttype.shape) else "handle"
-    if shape == "handle" and ttype.dtype == "i32":
+    if shape == "handle" and ttype.dtype in ("i32", "u32"):
         return "int_handle"
     return shape
 
@@ -98,6 +99,8 @@ class Stage:
     key_writes: list = field(default_factory=list)  # [(plane, (node per component), group)]: one entry per key
     fused_folds: list = field(default_factory=list)  # [(out plane, scratch plane, values, cells, group)]
     block: int | None = None        # the launch block a fused fold needs (its keys never cross a block)
+    guard: str | None = None        # the mask plane whose set samples the stage skips
+    finish: tuple | None = None     # (mask plane, counter plane, condition node) of `terminated = cond`
 
 
 class _Scope:
@@ -128,6 +131,7 @@ class _Writer:
         self.scope = _Scope()
         self.deps = Deps()
         self.taped = {}              # loop uid -> True when a tape_read reads it
+        self.exits = {}              # loop uid -> the flag its exit set
 
     # -- text --------------------------------------------------------------
     def emit(self, text: str) -> None:
@@ -178,6 +182,8 @@ class _Writer:
         p = self.stage.planes[name]["var"]
         if role in ("uniform", "lookup"):
             return [p]                # a value, or a table that `gather` indexes
+        if role == "terminated":      # a mask: one byte a sample
+            return [self.let("bool", f"{p}[hk_i] != 0", "in")]
         if role == "mutable":         # a prior read of an output plane
             role = "per_sample" if not n.ttype.shape else ("vec_in" if len(n.ttype.shape) == 1 else "mat_in")
         dt = n.ttype.dtype
@@ -459,6 +465,10 @@ class _Writer:
             self.tape_of = getattr(self, "tape_of", {})
             self.tape_of[n.uid] = (tapes, info.start, info.step)
         k = f"hk_k{n.uid}"
+        exited = None
+        if info.exit is not None:
+            exited = f"hk_exited{n.uid}"
+            self.emit(f"bool {exited} = false;")
         if info.unroll is True:
             self.emit("#pragma unroll")
         elif info.unroll is False:
@@ -474,8 +484,12 @@ class _Writer:
             for row, names in zip(tapes, carry_vars):
                 for t, v in zip(row, names):
                     self.emit(f"{t}[{slot}] = {v};")
-        self.run(info.nexts)
+        self.run(ir.body_roots(info))
         nexts = [self.value(x) for x in info.nexts]
+        leave = None
+        if info.exit is not None:
+            leave = self.fresh("x")
+            self.emit(f"const bool {leave} = {self.scalar(info.exit)};")
         temps = []
         for names, nv in zip(carry_vars, nexts):
             nv = nv * len(names) if len(nv) == 1 and len(names) > 1 else nv
@@ -488,10 +502,18 @@ class _Writer:
         for names, row in zip(carry_vars, temps):
             for name, t in zip(names, row):
                 self.emit(f"{name} = {t};")
+        if leave is not None:         # a tail break: this trip's values stand
+            self.emit(f"if ({leave}) {{ {exited} = true; break; }}")
         self.scope.memo.pop()
         self.indent -= 1
         self.emit("}")
+        if exited is not None:
+            self.exits[n.uid] = exited
         return carry_vars
+
+    def _loop_exit(self, n: Node) -> list:
+        self.value(n.operands[0])
+        return [self.exits[n.operands[0].uid]]
 
     def _loop_value(self, n: Node) -> list:
         return self.value(n.operands[0])[n.literal]
@@ -517,14 +539,21 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
     ``[(plane, nodes, group)]`` are integer planes of one entry per key (every
     lane of the key's run of ``group`` samples stores the same value)."""
     writes = [(s.name, s.value) for s in program.sinks if isinstance(s, Assign)] + extra_writes
+    finish = next((s for s in program.sinks if isinstance(s, Finish)), None)
     roots = ([node for _, node in writes] + [node for _, node in row_sums]
              + [node for _, nodes, _ in key_writes for node in nodes]
-             + [node for f in fused_folds for node in tuple(f[2]) + tuple(f[3])])
+             + [node for f in fused_folds for node in tuple(f[2]) + tuple(f[3])]
+             + ([finish.value] if finish is not None else []))
     used_leaves = ir.leaves_of(roots)
     rows = [(cell, node, f"hk_rows_{cell}", f"hk_rows_{cell}_comp") for cell, node in row_sums]
     used = ({n.literal[1] for n in used_leaves} | {name for name, _ in writes}
             | {p for r in rows for p in r[2:]} | {name for name, _, _ in key_writes}
             | {f[0] for f in fused_folds} | {f[1] for f in fused_folds})
+    guard = GUARD_MASK if GUARD_MASK in program.decls and program.decls[GUARD_MASK].role == "terminated" else None
+    if guard is not None:
+        used.add(guard)
+    if finish is not None:
+        used.add(FINISHED_PLANE)
     decls = dict(program.decls)
     planes = {}
     for name, node in extra_writes:
@@ -553,7 +582,8 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
     if block is not None and block > 1024:
         raise HawkError("the fused ordered folds of this kernel need blocks of more than 1024 threads")
     return Stage(stage_name, spec, planes, writes, row_sums=rows, key_writes=list(key_writes),
-                 fused_folds=list(fused_folds), block=block)
+                 fused_folds=list(fused_folds), block=block, guard=guard,
+                 finish=(finish.name, FINISHED_PLANE, finish.value) if finish is not None else None)
 
 
 #: A stage that touches at least this many component planes hands each XCD a
@@ -590,7 +620,11 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     w = _Writer(stage, mode, nontemporal)
     roots = ([node for _, node in stage.writes] + [node for _, node, _, _ in stage.row_sums]
              + [node for _, nodes, _ in stage.key_writes for node in nodes]
-             + [node for f in stage.fused_folds for node in tuple(f[2]) + tuple(f[3])])
+             + [node for f in stage.fused_folds for node in tuple(f[2]) + tuple(f[3])]
+             + ([stage.finish[2]] if stage.finish is not None else []))
+    if stage.guard is not None and (stage.row_sums or stage.fused_folds):
+        raise HawkError(f"{stage.name}: a guarded kernel (one declaring `terminated: Terminated`) commits "
+                        "per-sample planes; a sum or a fold over the samples its guard skips is not in this build")
     if stage.fused_folds:
         block, per_thread = stage.block, 1
     # Which loops keep a tape: a loop that keeps or reads a tape, and every loop
@@ -651,8 +685,10 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
             params.append(f"Real {var}")
             continue
         is_input = role not in ("mutable", "out", "wide_out", "key_out", "accum_out", "rows_out", "fold_scratch")
+        if stage.finish is not None and name in stage.finish[:2]:
+            is_input = False          # the mask a finish sets and its counter
         cq = "const " if is_input else ""
-        elem = "int" if info["dtype"] == "i32" else "Real"
+        elem = {"i32": "int", "u32": "unsigned int", "bool": "unsigned char"}.get(info["dtype"], "Real")
         if kind == "gref":
             params.append(f"GRefMirror {var}_m")
             unpack.append(f"{cq}{elem}* __restrict__ {var} = reinterpret_cast<{cq}{elem}*>({var}_m.data_);")
@@ -680,6 +716,8 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += _ROW_SUM_HELPERS.splitlines()
     if folds:
         out += _FOLD_HELPERS.splitlines()
+    if stage.finish is not None:
+        out += _FINISH_HELPER.splitlines()
     out += [
         f'extern "C" __global__ void __launch_bounds__({block}) {stage.name}(',
         "        " + ",\n        ".join(params) + ") {",
@@ -700,7 +738,24 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         f"        const long long hk_flat = (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * {block}"
         " + static_cast<long long>(threadIdx.x);",
     ]
-    if not row_terms and not folds:
+    if stage.guard is not None:
+        # The stage skips the samples its mask has finished.  Every lane of a
+        # wave reaches the finish count together (no lane leaves early), and a
+        # lane past `count` takes no sample.
+        mask = stage.planes[stage.guard]["var"]
+        out += ["        const bool hk_in = hk_flat < count;",
+                "        const long long hk_i = base + (hk_in ? hk_flat : 0LL);"]
+        if stage.finish is not None:
+            out += ["        bool hk_new = false;"]
+        out += [f"        if (hk_in && {mask}[hk_i] == 0) {{"]
+        out += ["    " + line for line in body + stores]
+        if stage.finish is not None:
+            cond = w.value(stage.finish[2])[0]
+            out += [f"            if ({cond}) {{ {mask}[hk_i] = 1; hk_new = true; }}"]
+        out += ["        }"]
+        if stage.finish is not None:
+            out += [f"        hk_finish_count({stage.planes[stage.finish[1]]['var']}, hk_new);"]
+    elif not row_terms and not folds:
         out += ["        if (hk_flat >= count) break;",
                 "        const long long hk_i = base + hk_flat;"]
         out += body + stores
@@ -722,6 +777,16 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += _fused_fold_lines(folds, block, whole)
     out += ["    }", "}", ""]
     return "\n".join(out)
+
+
+#: The finish count (reference ``hawk/emit/wrapper.py:522-537``): one atomic
+#: add a wave, of how many of its lanes finished their sample this launch.
+_FINISH_HELPER = r"""
+__device__ __forceinline__ void hk_finish_count(unsigned int* counter, bool newly) {
+    const unsigned long long m = __ballot(newly);
+    if ((threadIdx.x & 63u) == 0u && m != 0ull) atomicAdd(counter, static_cast<unsigned int>(__popcll(m)));
+}
+"""
 
 
 #: LDS a fused fold stages a chunk of its slots in, per block, when the
@@ -1104,7 +1169,10 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                 key = f"hk_key_{s.name}_{len(team)}"
                 extra.append((key, s.key))
             team.append({"op": "ordered_scatter", "key": key, "v": src, "target": s.name})
-    has_stage = any(isinstance(s, Assign) for s in program.sinks) or extra or row_sums or fused
+    has_stage = any(isinstance(s, (Assign, Finish)) for s in program.sinks) or extra or row_sums or fused
+    if has_stage and team and GUARD_MASK in program.decls and program.decls[GUARD_MASK].role == "terminated":
+        raise HawkError(f"{name}: a guarded kernel (one declaring `terminated: Terminated`) commits per-sample "
+                        "planes; a sum or a scatter over the samples its guard skips is not in this build")
     stage = source = None
     if has_stage:
         stage = _stage_planes(program, name, mode, extra, row_sums, key_writes, fused)

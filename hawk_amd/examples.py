@@ -15,7 +15,7 @@ from . import trace as _trace
 from .math import abs as _abs
 from .math import cho_solve, cholesky, cos, dot, exp, sin, sqrt, tanh, vec
 from .trace import Kernel, kernel
-from .types import Grid, Index, Matrix, Mutable, Param, Scalar, Table, Vector
+from .types import Grid, Index, Matrix, Mutable, Param, Scalar, Table, Terminated, Vector
 
 #: Leapfrog step and substep count of the two-body kernel.
 DT = 1e-3
@@ -177,6 +177,41 @@ def scale_vec(a: Vector[3], b: Scalar, y: Mutable[Vector[3]]):
 #: accumulator updated in place, an output read from two earlier values):
 #: ``hawk.chain(*CHAIN_MEMBERS, name=...)`` runs them as one kernel.
 CHAIN_MEMBERS = (unit_circle, decay, accumulate, scale_vec)
+
+
+# -- kernels that finish their own sample (reference tests/test_finish_own_sample.py:52-86)
+
+#: The oscillator's explicit-Euler step (exact in binary: t stays a multiple of it).
+OSC_DT = 0.125
+
+
+@kernel
+def osc_finish(dt: Param, t_final: Scalar, terminated: Terminated,
+               x: Mutable[Scalar], v: Mutable[Scalar], t: Mutable[Scalar]):
+    v_start = v
+    a = -x
+    v = v_start + dt * a
+    x = x + dt * v_start
+    tn = t + dt
+    t = tn
+    terminated = tn >= t_final
+
+
+@kernel
+def stop_only(t: Scalar, t_final: Param, terminated: Terminated):
+    terminated = t >= t_final
+
+
+@kernel
+def smooth_finish(x: Scalar, terminated: Terminated, y: Mutable[Scalar]):
+    y = x * x + 1.0
+    terminated = x > 2.0
+
+
+#: The oscillator taking up to 8 steps a launch.
+osc_finish_x8 = _trace.steps(osc_finish, 8)
+smooth_finish_vjp = Kernel("smooth_finish_vjp", diff.vjp(smooth_finish, wrt=("x",)))
+FINISHING = {k.name: k for k in (osc_finish, osc_finish_x8, stop_only, smooth_finish, smooth_finish_vjp)}
 
 
 #: Every kernel above, by name.

@@ -68,6 +68,7 @@ class LoopInfo:
     nexts: tuple                     # the body's value of each slot
     names: tuple = ()                # the authored names of the slots (diagnostics)
     unroll: bool | None = None       # True: #pragma unroll; False: kept rolled; None: the compiler's choice
+    exit: Node | None = None         # a bool over the trip's inputs: when true, the trip's nexts stand and the loop ends
 
     def stop(self) -> int:
         return self.start + self.trip * self.step
@@ -279,19 +280,27 @@ def is_zero(n: Node) -> bool:
     return False
 
 
-def new_loop(trip: int, start: int, step: int, inits: tuple, body, names: tuple = ()) -> Node:
+def new_loop(trip: int, start: int, step: int, inits: tuple, body, names: tuple = (),
+             exits: bool = False) -> Node:
     """A rolled loop: ``body(index, *carries) -> nexts`` traced once over
-    placeholders typed like ``inits``."""
+    placeholders typed like ``inits``.  With ``exits`` the body gives one more
+    value, a bool: a lane for which it is true keeps that trip's nexts and
+    leaves the loop (a tail break)."""
     uid = next(_uid)
     index = Node("loop_index", (), TensorType((), "i64"), uid)
     carries = tuple(Node("carry", (), as_real(x).ttype if x.ttype.dtype != "i64" else x.ttype, (uid, j))
                     for j, x in enumerate(inits))
     nexts = tuple(body(index, *carries))
-    return loop_node(uid, trip, start, step, index, carries, tuple(inits), nexts, names)
+    exit = None
+    if exits:
+        nexts, exit = nexts[:-1], nexts[-1]
+        if exit.ttype != TensorType((), "bool"):
+            raise HawkError(f"a loop's exit is a rank-0 bool, got {exit.ttype}")
+    return loop_node(uid, trip, start, step, index, carries, tuple(inits), nexts, names, exit=exit)
 
 
 def loop_node(uid: int, trip: int, start: int, step: int, index: Node, carries: tuple,
-              inits: tuple, nexts: tuple, names: tuple = ()) -> Node:
+              inits: tuple, nexts: tuple, names: tuple = (), exit: Node | None = None) -> Node:
     if len(nexts) != len(carries):
         raise HawkError("a loop body must give one value per carried slot")
     fixed = []
@@ -302,7 +311,7 @@ def loop_node(uid: int, trip: int, start: int, step: int, index: Node, carries: 
                                 f"{c.ttype.shape} before, {x.ttype.shape} after")
             x = make("splat", (as_real(x),), c.ttype.shape)
         fixed.append(as_real(x) if c.ttype.dtype in ("f64", "f32") else x)
-    info = LoopInfo(trip, start, step, index, tuple(carries), tuple(fixed), tuple(names))
+    info = LoopInfo(trip, start, step, index, tuple(carries), tuple(fixed), tuple(names), exit=exit)
     node = Node("loop", tuple(as_real(x) if c.ttype.dtype in ("f64", "f32") else x
                               for c, x in zip(carries, inits)), TensorType((), "tuple"), info)
     node.uid = uid
@@ -311,6 +320,16 @@ def loop_node(uid: int, trip: int, start: int, step: int, index: Node, carries: 
 
 def loop_value(loop: Node, j: int) -> Node:
     return Node("loop_value", (loop,), loop.literal.carries[j].ttype, j)
+
+
+def loop_exit(loop: Node) -> Node:
+    """Whether ``loop`` ended on its exit condition (rather than its trip count)."""
+    return Node("loop_exit", (loop,), TensorType((), "bool"))
+
+
+def body_roots(info: LoopInfo) -> tuple:
+    """The nodes a loop's body computes each trip: its nexts and its exit."""
+    return tuple(info.nexts) + ((info.exit,) if info.exit is not None else ())
 
 
 def tape_read(loop: Node, j: int, index: Node) -> Node:
@@ -357,7 +376,7 @@ class Deps:
                 deps |= self.memo[o.uid]
             if m.kind == "loop":
                 inner = set()
-                for x in m.literal.nexts:
+                for x in body_roots(m.literal):
                     inner |= self.memo[x.uid]
                 inner.discard(m.literal.index.uid)
                 deps |= inner
@@ -371,12 +390,12 @@ def free_inputs(loop: Node, deps: Deps) -> list:
     and sees a nested loop as one node whose operands are its inits and its own
     free inputs (never the nodes inside the nested body)."""
     deps.register(loop)
-    for n in topo(loop.literal.nexts):    # a body can reach other loops (a tape read's loop): register them
+    for n in topo(body_roots(loop.literal)):    # a body can reach other loops (a tape read's loop)
         if n.kind == "loop":
             deps.register(n)
     key = loop.literal.index.uid
     out, seen, expanded = [], set(), set()
-    stack = list(reversed(loop.literal.nexts))
+    stack = list(reversed(body_roots(loop.literal)))
     while stack:
         n = stack.pop()
         if key not in deps.of(n):
@@ -468,6 +487,24 @@ class AccumWrite:
 
 
 @dataclass
+class Finish:
+    """``terminated = cond``: the kernel finishes its own sample (reference
+    ``hawk/ir/nodes.py:848-870``): the mask ``name`` becomes ``mask | cond``
+    and each newly finished sample adds one to the ``finished_count`` cell."""
+
+    name: str
+    value: Node
+    steps: int = 1                   # the steps one launch takes (hawk.steps); 1 as authored
+
+
+#: The one-cell counter a finishing kernel adds its newly finished samples to
+#: (reference ``hawk/ir/nodes.py:839``).
+FINISHED_PLANE = "finished_count"
+#: The only mask a kernel's guard gates on: the ``Terminated`` parameter of this name.
+GUARD_MASK = "terminated"
+
+
+@dataclass
 class OrderedFold:
     """The gradient of a table read by key under an ordered keyed sum
     (reference ``hawk/diff/ordered.py``): ``values[e]`` is a lane's e-th
@@ -534,7 +571,7 @@ def topo(roots) -> list:
         stack.append((node, True))
         kids = list(node.operands)
         if node.kind == "loop":
-            kids += list(node.literal.nexts)
+            kids += list(body_roots(node.literal))
         for k in reversed(kids):
             if k.uid not in seen:
                 stack.append((k, False))
@@ -559,10 +596,11 @@ def substitute(roots, mapping: dict) -> list:
         if n.kind == "loop":
             info = n.literal
             new_nexts = tuple(memo.get(x.uid, x) for x in info.nexts)
-            if any(a is not b for a, b in zip(new_kids, kids)) or \
+            new_exit = memo.get(info.exit.uid, info.exit) if info.exit is not None else None
+            if any(a is not b for a, b in zip(new_kids, kids)) or new_exit is not info.exit or \
                     any(a is not b for a, b in zip(new_nexts, info.nexts)):
                 copy = loop_node(next(_uid), info.trip, info.start, info.step, info.index,
-                                 info.carries, new_kids, new_nexts, info.names)
+                                 info.carries, new_kids, new_nexts, info.names, exit=new_exit)
                 copy.literal.unroll = info.unroll
                 memo[n.uid] = copy
             continue
@@ -650,6 +688,8 @@ def _carry_repeats_of(loop: Node, deps: Deps):
     the same operations, in the same order, from the same operands (the kernel
     is compiled without contraction)."""
     info = loop.literal
+    if info.exit is not None:
+        return None                           # a stepped loop's trips end on its exit
     key_of = info.index.uid
     deps.register(loop)
     carry_slot = {c.uid: j for j, c in enumerate(info.carries)}
@@ -757,6 +797,17 @@ def carry_repeats(roots) -> list:
         if copy is not None:
             mapping[lp.uid] = copy
     return substitute(roots, mapping) if mapping else list(roots)
+
+
+def used_names(program: Program) -> set:
+    """The planes a kernel binds: the ones its sinks read or write, the guard's
+    mask when it declares one, and the finish counter when it finishes."""
+    used = {n.literal[1] for n in leaves_of(sink_roots(program.sinks))} | {s.name for s in program.sinks}
+    if GUARD_MASK in program.decls and program.decls[GUARD_MASK].role == "terminated":
+        used.add(GUARD_MASK)
+    if any(isinstance(s, Finish) for s in program.sinks):
+        used.add(FINISHED_PLANE)
+    return used
 
 
 def arg_spec(program: Program, used: set) -> list:

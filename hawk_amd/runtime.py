@@ -33,7 +33,14 @@ def _bound_length(role: str, x, n: int) -> int:
     return int(x.shape[-1]) if role == "key_out" else n
 
 
-_PER_SAMPLE = ("per_sample", "vec_in", "mat_in", "mutable", "out", "wide_out")
+_PER_SAMPLE = ("per_sample", "vec_in", "mat_in", "mutable", "out", "wide_out", "terminated")
+
+#: The finish counter (reference ``hawk/ir/nodes.py:839``): one cell a
+#: finishing kernel adds its newly finished samples to.  The caller may bind
+#: it (an int32 tensor of one element, added to); left unbound the runtime
+#: binds its own, zeroed before each ``hawk.run`` and readable afterwards as
+#: the kernel's ``finished``.
+FINISHED_PLANE = "finished_count"
 
 
 def _torch():
@@ -65,6 +72,7 @@ class DeviceKernel:
         self._scratch: dict = {}
         self._lock = threading.Lock()
         self.scatter_chunks = None
+        self.finished = None      # the runtime's finish counter when the caller binds none
 
     # -- validation ----------------------------------------------------------
     def _real_dtype(self):
@@ -73,6 +81,20 @@ class DeviceKernel:
 
     def caller_planes(self) -> list:
         return [n for n, p in self.planes.items() if not p.get("scratch")]
+
+    def _counter(self, arrays: dict, device):
+        """``arrays`` with the finish counter bound: the caller's, else the
+        runtime's own (zeroed by the caller of this method when it wants a count
+        per run)."""
+        if FINISHED_PLANE not in self.planes or FINISHED_PLANE in arrays:
+            return arrays, None
+        torch = _torch()
+        held = self._scratch.get(("finished", device))
+        if held is None:
+            held = torch.zeros(1, dtype=torch.int32, device=device)
+            self._scratch[("finished", device)] = held
+        self.finished = held
+        return {**arrays, FINISHED_PLANE: held}, held
 
     def check_planes(self, arrays: dict, n_samples=None) -> int:
         """Validate every bound plane against the sidecar; return the sample count."""
@@ -101,13 +123,13 @@ class DeviceKernel:
         if unknown:
             raise HawkError(f"kernel {self.name!r}: {unknown} are not planes it declares "
                             f"(declared: {sorted(declared)})")
-        missing = sorted(declared - set(arrays))
+        missing = sorted(declared - set(arrays) - {FINISHED_PLANE})
         if missing:
             raise HawkError(f"kernel {self.name!r}: bind {missing}")
         n = n_samples
         problems = []
         keyed = []
-        for name in sorted(declared):
+        for name in sorted(declared & set(arrays)):
             info = self.planes[name]
             x = arrays[name]
             role = info["role"]
@@ -125,7 +147,7 @@ class DeviceKernel:
             if not x.is_contiguous():
                 problems.append(f"{name!r} is not contiguous; pass x.contiguous()")
                 continue
-            want = torch.int32 if info["dtype"] == "i32" else (
+            want = torch.int32 if info["dtype"] in ("i32", "u32") else torch.bool if info["dtype"] == "bool" else (
                 torch.float64 if role in ("cell", "accum_out") else self._real_dtype())
             if x.dtype != want:
                 problems.append(f"{name!r} has dtype {x.dtype}, the kernel reads {want}")
@@ -148,6 +170,9 @@ class DeviceKernel:
             elif role == "accum_out":
                 if x.dim() != 1:
                     problems.append(f"{name!r} is the 1-D plane of cells hawk.scatter adds into")
+            elif name == FINISHED_PLANE:
+                if x.numel() != 1:
+                    problems.append(f"{name!r} is the one-cell finish counter: bind 1 element, got {x.numel()}")
             elif role == "lookup":
                 axes = (self.sidecar.get("tables") or {}).get(name)
                 if x.dim() != 1 and axes is None:
@@ -263,7 +288,9 @@ class DeviceKernel:
     def _run(self, arrays: dict, base: int, count: int, n: int, stream: int, check: bool) -> None:
         torch = _torch()
         device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
-        bound = dict(arrays)
+        bound, held = self._counter(dict(arrays), device)
+        if held is not None:
+            held.zero_()                          # a count per run
         for name, info in self.planes.items():
             if info.get("cells_of"):
                 bound[name] = self._fold_scratch(name, bound, device)
@@ -493,7 +520,10 @@ class Prepared:
             stream = stream.cuda_stream
         self.stream = int(stream)
         device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
-        bound = dict(arrays)
+        bound, held = kernel._counter(dict(arrays), device)
+        if held is not None:
+            held.zero_()                          # counts every call from here on
+        self.finished = bound.get(FINISHED_PLANE)
         for name, info in kernel.planes.items():
             if info.get("cells_of"):
                 bound[name] = kernel._fold_scratch(name, bound, device)

@@ -15,6 +15,11 @@ A kernel is a plain Python function for ONE sample.  Tracing runs it once over
 A ``Mutable`` read before it is assigned reads the value the plane held when
 the launch began (a prior read, refused by ``vjp``/``jvp`` as in reference
 ``hawk/diff/transform.py:169-192``).
+
+A kernel that declares ``terminated: Terminated`` runs only the samples its
+mask has not finished; ``terminated = cond`` (one statement, a traced bool)
+finishes a sample, and :func:`steps` makes a finishing kernel take up to K
+steps a launch (reference ``hawk/trace/steps.py``).
 """
 
 from __future__ import annotations
@@ -25,8 +30,9 @@ import textwrap
 from typing import Any
 
 from . import ir
-from .ir import AccumWrite, Assign, Decl, HawkError, Node, Program, SampleSum, make
-from .types import GridDecl, MutableDecl, TableDecl, TensorType, _ParamDecl, role_of
+from .ir import (FINISHED_PLANE, GUARD_MASK, AccumWrite, Assign, Decl, Finish, HawkError, Node, Program, SampleSum,
+                 make)
+from .types import FinishRefusal, GridDecl, MutableDecl, TableDecl, TensorType, _ParamDecl, _TerminatedDecl, role_of
 
 SUM_POLICIES = ("auto", "compensated", "ordered")
 SCATTER_POLICIES = ("ordered",)
@@ -536,7 +542,48 @@ class _Rewriter:
         return [ast.copy_location(fdef, st), ast.copy_location(assign, st)]
 
 
-def _rewritten(fn, mutables: tuple):
+def _finish_checks(fdef: ast.FunctionDef, finishes: tuple) -> None:
+    """The static rules of ``terminated = cond`` (reference
+    ``tests/test_finish_own_sample.py:125-178``): one statement a mask, not
+    inside a ``for``, not a Python literal."""
+    seen: dict = {}
+
+    def walk(stmts, in_for: bool):
+        for st in stmts:
+            if isinstance(st, (ast.FunctionDef, ast.AsyncFunctionDef, ast.ClassDef)):
+                continue
+            targets = []
+            if isinstance(st, ast.Assign):
+                targets = st.targets
+            elif isinstance(st, (ast.AugAssign, ast.AnnAssign)):
+                targets = [st.target]
+            for t in targets:
+                for node in ast.walk(t):
+                    if isinstance(node, ast.Name) and isinstance(node.ctx, ast.Store) and node.id in finishes:
+                        if in_for:
+                            raise FinishRefusal(f"finishes {node.id!r} inside a `for`: a sample finishes once, "
+                                                 "after its step (finish after the loop)")
+                        seen[node.id] = seen.get(node.id, 0) + 1
+                        if seen[node.id] > 1:
+                            raise FinishRefusal(f"{node.id!r} is finished twice: a kernel finishes its sample "
+                                                 "in ONE statement (combine the conditions with where or |)")
+                        value = getattr(st, "value", None)
+                        if isinstance(value, ast.Constant) and isinstance(value.value, bool):
+                            raise FinishRefusal(f"{node.id!r} = {value.value}: a Python literal is no per-sample "
+                                                 "condition; finish on a traced comparison")
+            if isinstance(st, (ast.For, ast.AsyncFor, ast.While)):
+                walk(st.body, True)
+                walk(st.orelse, True)
+            elif isinstance(st, ast.If):
+                walk(st.body, in_for)
+                walk(st.orelse, in_for)
+            elif isinstance(st, ast.With):
+                walk(st.body, in_for)
+
+    walk(fdef.body, False)
+
+
+def _rewritten(fn, mutables: tuple, finishes: tuple = ()):
     try:
         source = textwrap.dedent(inspect.getsource(fn))
     except (OSError, TypeError) as exc:
@@ -549,7 +596,8 @@ def _rewritten(fn, mutables: tuple):
     fdef.returns = None
     for a in fdef.args.args:
         a.annotation = None
-    rw = _Rewriter(mutables)
+    _finish_checks(fdef, finishes)
+    rw = _Rewriter(mutables + finishes)
     params = {a.arg for a in fdef.args.args}
     fdef.body = rw.block(fdef.body, set(params), False) + [ast.Return(rw.exit_call(None))]
     ast.fix_missing_locations(tree)
@@ -587,7 +635,7 @@ def trace(fn, scope: dict | None = None) -> Program:
             ns[name] = cell.cell_contents
     sig = inspect.signature(fn)
     program = Program()
-    args, mutables = [], []
+    args, mutables, finishes = [], [], []
     axes_of = {}                     # a Mutable declared with lane axes -> its axes
     for p in sig.parameters.values():
         if p.kind not in (p.POSITIONAL_ONLY, p.POSITIONAL_OR_KEYWORD):
@@ -611,6 +659,11 @@ def trace(fn, scope: dict | None = None) -> Program:
                 axes_of[p.name] = ann.axes
             args.append(MutableRef(p.name, ann.ttype))
             mutables.append(p.name)
+        elif isinstance(ann, _TerminatedDecl):
+            ttype = TensorType((), "bool")
+            program.decls[p.name] = Decl(p.name, "terminated", ttype)
+            args.append(Value(ir.leaf("terminated", p.name, ttype)))
+            finishes.append(p.name)
         elif isinstance(ann, _ParamDecl):
             program.decls[p.name] = Decl(p.name, "uniform", TensorType((), "f64"))
             args.append(Value(ir.leaf("uniform", p.name, TensorType((), "f64"))))
@@ -621,9 +674,12 @@ def trace(fn, scope: dict | None = None) -> Program:
         else:
             raise HawkError(f"{fn.__name__}: parameter {p.name!r} is declared {ann!r}, which is not "
                             "Scalar, Vector[n], Matrix[r, c], Index, Param or Mutable[...]")
-    body = _rewritten(fn, tuple(mutables))
-    with _Trace(program.grid) as tr:
-        ret, finals = body(*args)
+    try:
+        body = _rewritten(fn, tuple(mutables), tuple(finishes))
+        with _Trace(program.grid) as tr:
+            ret, finals = body(*args)
+    except FinishRefusal as exc:
+        raise HawkError(f"kernel {fn.__name__!r}: {exc}") from None
 
     def keyed(name: str, red: Reduced):
         """The SampleSum committing ``red`` into ``name`` (a Mutable declared
@@ -680,6 +736,22 @@ def trace(fn, scope: dict | None = None) -> Program:
                     raise HawkError(f"{fn.__name__} returns shape {node.ttype.shape}, annotated {ret_ann.shape}")
             program.decls["out"] = Decl("out", "out", node.ttype)
             sinks.append(Assign("out", node, "out"))
+    for name, arg in zip(sig.parameters, args):
+        if name not in finishes or finals[name] is arg:
+            continue                      # a mask read, never finished
+        final = finals[name]
+        if isinstance(final, bool):
+            raise HawkError(f"kernel {fn.__name__!r}: {name!r} = {final}: a Python literal is no per-sample "
+                            "condition; finish on a traced comparison")
+        node = node_of(final)
+        if node.ttype != TensorType((), "bool"):
+            raise HawkError(f"kernel {fn.__name__!r}: {name!r} is finished with a {node.ttype}; a sample "
+                            "finishes on a traced rank-0 bool")
+        if name != GUARD_MASK:
+            raise HawkError(f"kernel {fn.__name__!r}: finishes the mask {name!r}, which the guard does not gate "
+                            f"on ([{GUARD_MASK!r}]); a kernel finishes only the mask its guard skips")
+        program.decls[FINISHED_PLANE] = Decl(FINISHED_PLANE, "lookup", TensorType((), "u32"))
+        sinks.append(Finish(name, node))
     if not sinks:
         raise HawkError(f"{fn.__name__}: the kernel commits nothing (assign a Mutable, return a value, "
                         "or hawk.scatter into one)")
@@ -717,11 +789,75 @@ class Kernel:
     @property
     def arg_spec(self) -> list:
         """``[(role, name)]`` of the planes the kernel binds, in the ABI's role order."""
-        used = {n.literal[1] for n in ir.leaves_of(ir.sink_roots(self.sinks))} | {s.name for s in self.sinks}
-        return ir.arg_spec(self.program, used)
+        return ir.arg_spec(self.program, ir.used_names(self.program))
 
     def __repr__(self) -> str:
         return f"<hawk kernel {self.name}: {[type(s).__name__ + ':' + s.name for s in self.sinks]}>"
+
+
+def steps(kernel: Kernel, K: int) -> Kernel:
+    """``kernel`` stepping up to ``K`` times a launch, named ``<name>_x<K>``
+    (reference ``hawk/trace/steps.py:81-99``).
+
+    ``kernel`` finishes its own sample (``terminated = cond``) and commits
+    only ``Mutable`` planes.  The step becomes one rolled loop of ``K`` trips
+    whose carries are those planes (each launch-start read becomes the carry,
+    each commit its next value) and whose exit is the finish condition,
+    evaluated after the step (a tail break: a sample finishing at trip ``j``
+    keeps step ``j``'s values).  After the loop the carries commit and the
+    finish fires with the loop's exit.  Each trip evaluates the same DAG as
+    one launch of ``kernel``, so K launches of ``kernel`` and one of the
+    result give the same bits (the build does not contract multiply-adds).
+    A sample may run up to ``K - 1`` steps past a caller's own step cap.
+    ``steps="auto"`` (a trip count read at launch) is not in this build."""
+    if not isinstance(kernel, Kernel):
+        raise HawkError("hawk.steps(kernel, K) takes a traced kernel")
+    name = kernel.name
+    if isinstance(K, bool) or not isinstance(K, int) or K < 1:
+        raise HawkError(f"hawk.steps({name!r}, {K!r}): K is an int >= 1 (steps='auto', a trip count read "
+                        "at launch, is not in this build)")
+    program = kernel.program
+    finishes = [s for s in program.sinks if isinstance(s, Finish)]
+    if not finishes:
+        raise HawkError(f"hawk.steps({name!r}): the kernel never finishes its sample -- K steps with no exit "
+                        "is a plain `for` the author can write; finish with `terminated = cond`")
+    finish = finishes[0]
+    if finish.steps != 1:
+        raise HawkError(f"hawk.steps({name!r}): the kernel already takes {finish.steps} steps a launch; "
+                        "derive from the single step")
+    commits = [s for s in program.sinks if s is not finish]
+    for s in commits:
+        if not (isinstance(s, Assign) and s.role == "mutable"):
+            raise HawkError(f"hawk.steps({name!r}): a {type(s).__name__} into {s.name!r} is not a step "
+                            "kernel's commit; a step kernel commits Mutable planes and finishes -- an "
+                            "out, a sum or a scatter has no per-sample state to carry from one step to the next")
+    if not commits:
+        raise HawkError(f"hawk.steps({name!r}): the kernel commits no Mutable plane, so there is no state "
+                        "to step")
+    carried = {s.name for s in commits}
+    roots = [s.value for s in commits] + [finish.value]
+    reads = [n for n in ir.leaves_of(roots) if n.literal[0] == "mutable" and n.literal[1] in carried]
+    read_ids = {n.uid for n in reads}
+    for loop in (n for n in ir.topo(roots) if n.kind == "loop"):
+        if any(m.uid in read_ids for m in ir.topo([loop])):
+            raise HawkError(f"hawk.steps({name!r}): a loop of the step reads the carried state; carry it "
+                            "through a step without inner loops over it")
+    slot = {s.name: j for j, s in enumerate(commits)}
+    inits = []
+    for s in commits:
+        decl = program.decls[s.name]
+        inits.append(ir.leaf("mutable", s.name, decl.ttype))
+
+    def body(index, *carries):
+        mapping = {n.uid: carries[slot[n.literal[1]]] for n in reads}
+        return tuple(ir.substitute(roots, mapping))
+
+    loop = ir.new_loop(K, 0, 1, tuple(inits), body, tuple(s.name for s in commits), exits=True)
+    sinks = [Assign(s.name, ir.loop_value(loop, j), "mutable") for j, s in enumerate(commits)]
+    sinks.append(Finish(finish.name, ir.loop_exit(loop), steps=K))
+    stepped = Kernel(f"{name}_x{K}", Program(dict(program.decls), sinks, program.grid, dict(program.tables)))
+    stepped.step = kernel
+    return stepped
 
 
 def kernel(fn=None, *, name: str | None = None):

@@ -18,6 +18,10 @@ class HawkError(Exception):
     """Every refusal of the authoring surface, the compiler and the runtime."""
 
 
+class FinishRefusal(HawkError):
+    """A refused ``terminated = cond``; the trace names the kernel in front of it."""
+
+
 #: IR dtypes: reals, the 64-bit index integer of loop counters, the int32
 #: plane of an ``Index`` declaration, and the bool of a comparison.
 DTYPES = ("f64", "f32", "i64", "i32", "bool", "tuple")
@@ -81,6 +85,24 @@ class _ParamDecl:
 
 
 Param = _ParamDecl()
+
+
+class _TerminatedDecl:
+    """``Terminated``: the per-sample mask of finished samples (a bool plane,
+    reference ``hawk/ir/nodes.py:848-870``).  A kernel that declares it runs
+    only the samples not finished yet; ``terminated = cond`` finishes a
+    sample (the mask becomes ``mask | cond``) and counts each newly finished
+    one in the ``finished_count`` cell."""
+
+    def __repr__(self) -> str:
+        return "Terminated"
+
+    def __setitem__(self, key, value):
+        raise FinishRefusal("assigns the Terminated declaration itself, but the kernel did not declare a "
+                            "Terminated parameter: declare `terminated: Terminated` and assign `terminated = cond`")
+
+
+Terminated = _TerminatedDecl()
 
 
 @dataclass(frozen=True)

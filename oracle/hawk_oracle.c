@@ -657,6 +657,35 @@ HKO_EXPORT void hko_mm16_vjp(const float* A, const float* B, const float* bar_C,
  * serial entry with its own (base, count) (reference hawk/emit/host.py:4-12);
  * the ordered sum runs one group per thread-slot and the ordered scatter one
  * chunk per thread-slot, each reproducing the serial bits. */
+/* One launch of the oscillator that finishes its own sample (reference
+ * tests/test_finish_own_sample.py:52-64 `osc_finish`, stepped by
+ * hawk/trace/steps.py:1-20 when K > 1), over samples [base, base+count): a
+ * sample whose mask is set is skipped; any other takes up to K steps of
+ *     v' = v + dt*(-x);  x' = x + dt*v;  t' = t + dt
+ * leaving after the step at which t' >= t_final (its values are that step's),
+ * and then its mask is set.  Returns how many samples this launch finished
+ * (the finished_count the reference adds to; :228-241 is its NumPy twin
+ * with K = 1). */
+HKO_EXPORT int64_t hko_osc_launch(int64_t base, int64_t count, int K, double dt, const double* t_final, double* x,
+                                  double* v, double* t, unsigned char* mask) {
+    int64_t finished = 0;
+    for (int64_t i = base; i < base + count; ++i) {
+        if (mask[i]) continue;
+        double xi = x[i], vi = v[i], ti = t[i];
+        int done = 0;
+        for (int k = 0; k < K && !done; ++k) {
+            const double xn = xi + dt * vi;
+            const double vn = vi + dt * (-xi);
+            const double tn = ti + dt;
+            xi = xn; vi = vn; ti = tn;
+            done = tn >= t_final[i];
+        }
+        x[i] = xi; v[i] = vi; t[i] = ti;
+        if (done) { mask[i] = 1; ++finished; }
+    }
+    return finished;
+}
+
 typedef struct {
     int which;
     const void* in0; const void* in1; const void* in2; const void* in3; const void* in4;

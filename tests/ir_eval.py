@@ -24,6 +24,7 @@ class Evaluator:
         self.n = n
         self.memo: dict = {}
         self.tapes: dict = {}
+        self.exits: dict = {}
         self.deps = deps if deps is not None else ir.Deps()
 
     def value(self, node):
@@ -49,6 +50,8 @@ class Evaluator:
             x = self.env[name]
             if role == "uniform":
                 return np.full(n, float(x))
+            if role == "terminated":
+                return np.asarray(x, dtype=bool)
             return np.asarray(x, dtype=np.float64 if m.ttype.dtype != "i32" else np.int32)
         if k == "const":
             return np.full(n, m.literal)
@@ -140,6 +143,8 @@ class Evaluator:
             return self._loop(m)
         if k == "loop_value":
             return self.memo[m.operands[0].uid][m.literal]
+        if k == "loop_exit":
+            return self.exits[m.operands[0].uid]
         if k == "tape_read":
             loop, index = m.operands
             kval = int(self.memo[index.uid][0])
@@ -195,17 +200,28 @@ class Evaluator:
         info = m.literal
         carries = [np.array(self.memo[o.uid], copy=True) for o in m.operands]
         tape = [[] for _ in carries]
+        done = np.zeros(self.n, dtype=bool)       # lanes that took the loop's exit
         for kval in range(info.start, info.stop(), info.step):
             for j, c in enumerate(carries):
                 tape[j].append(c)
             inner = Evaluator(self.env, self.n, self.deps)
             inner.memo = dict(self.memo)
             inner.tapes = self.tapes
+            inner.exits = self.exits
             inner.memo[info.index.uid] = np.full(self.n, kval)
             for c, val in zip(info.carries, carries):
                 inner.memo[c.uid] = val
-            carries = [np.array(inner.value(x), copy=True) for x in info.nexts]
+            nexts = [np.array(inner.value(x), copy=True) for x in info.nexts]
+            if info.exit is None:
+                carries = nexts
+                continue
+            # a tail break: a lane still in the loop keeps this trip's values,
+            # then leaves if its exit holds
+            leave = np.asarray(inner.value(info.exit), dtype=bool)
+            carries = [np.where(done, c, nx) for c, nx in zip(carries, nexts)]
+            done = done | leave
         self.tapes[m.uid] = tape
+        self.exits[m.uid] = done
         return carries
 
 
