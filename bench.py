@@ -12,7 +12,9 @@ spelling (``hawk.sum(x, over=...)``) over 16384 keys, ``--config 5t`` a
 ordered loss and its gradient wrt its weights (the ordered log fold);
 ``--config chain`` four kernels chained into one launch (``hawk.chain``), and
 ``--config steps`` an oscillator that finishes its own sample, 8 steps a
-launch (``hawk.steps``), over 2^24 samples.
+launch (``hawk.steps``), over 2^24 samples, and ``--config persist`` 2^22 such
+oscillators of 1-256 steps each run to their finish in one launch of the
+persistent entry (the plain and range entries timed beside it).
 
 Each stage launch of the timed steps (a per-sample kernel, or a team stage:
 the ordered sum or the ordered scatter) is bracketed by HIP events on the
@@ -322,6 +324,61 @@ def workload(config: str, device):
                          profile="native")
         return dict(name="oscillator finishing its own sample, 8 steps a launch (hawk.steps)", n=n,
                     kernels=kernels, work=work, cpu=cpu, dtype="f64", cpu_threads=1)
+    if config == "persist":
+        # hawk.steps(k, "auto") through its persistent entry (reference hawk/emit/cuda.py:465-689): 2^22
+        # oscillators of 1 to 256 steps each, every one run to its finish in one launch.  Each step
+        # first restores the inputs (the "reset" stage: four plane copies), then runs the launch.
+        ka = E.osc_finish_xauto
+        n = 1 << 22
+        g = np.random.default_rng(41)
+        t_final = E.OSC_DT * g.integers(1, 257, n).astype(float)
+        x, v = g.uniform(-1.0, 1.0, n), g.uniform(-1.0, 1.0, n)
+        hawk.build([ka], unit)
+        kk = hawk.load(unit, ka.name)
+        X0, V0, TF = _dev(x, device), _dev(v, device), _dev(t_final, device)
+        planes = {"x": X0.clone(), "v": V0.clone(), "t": torch.zeros(n, dtype=torch.float64, device=device),
+                  "t_final": TF, "terminated": torch.zeros(n, dtype=torch.bool, device=device)}
+
+        class Reset:
+            def stages(self):
+                def reset():
+                    planes["x"].copy_(X0)
+                    planes["v"].copy_(V0)
+                    planes["t"].zero_()
+                    planes["terminated"].zero_()
+                return [("reset", reset)]
+        kernels = [Reset(), kk.prepare(dt=E.OSC_DT, steps=256, entry="persist", **planes)]
+        mean_steps = float(np.rint(t_final / E.OSC_DT).mean())
+        step_ops = 6                               # a trip: 2 mul, 3 add, 1 compare
+        work = {"reset": (2 * (8 + 8 + 8 + 1), 0),
+                f"{ka.name}_persist": (33 + 25, step_ops * mean_steps)}
+
+        def other_entries():
+            # the same launch through the plain and the range entries (one lane a sample, each wave
+            # held by its longest sample), for comparison
+            out = {}
+            for entry in ("plain", "range"):
+                prep = kk.prepare(dt=E.OSC_DT, steps=256, entry=entry, **planes)
+                reset = Reset().stages()[0][1]
+                times = []
+                for _ in range(6):
+                    reset()
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record()
+                    prep()
+                    b.record()
+                    torch.cuda.synchronize()
+                    times.append(a.elapsed_time(b))
+                out[f"{entry}_entry_ms"] = round(statistics.median(times[1:]), 5)
+            return out
+
+        def cpu(threads):
+            import oracle_lib as O
+            O.osc_launch(256, E.OSC_DT, t_final, x.copy(), v.copy(), np.zeros(n), np.zeros(n, dtype=bool),
+                         profile="native")
+        return dict(name="oscillators of 1-256 steps run to their finish in one launch of the persistent "
+                         "entry (hawk.steps 'auto')", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
+                    cpu_threads=1, bound="fp64", compare_entries=other_entries)
     if config == "5n":
         # the net axis (reference tests/test_net_axis.py): 65536 small models of 64 samples in one
         # launch, each net's loss an ordered keyed sum and its gradient wrt its 24 weights the
@@ -560,6 +617,9 @@ def main() -> int:
     if "compare" in w:
         compare["members_launched_one_by_one_ms"] = round(w["compare"](), 5)
         log(f"the same members as separate launches: {compare['members_launched_one_by_one_ms']} ms a step")
+    if "compare_entries" in w:
+        compare.update(w["compare_entries"]())
+        log(f"the same launch through the other entries: {compare}")
     line = {
         "metric": METRIC, "value": n / (ms_step * 1e-3), "unit": "samples/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),

@@ -21,7 +21,7 @@ from . import compile as _compile
 from .emit_hip import fp_ops_per_sample
 from .resources import kernel_resources
 from .emit_hip import plan_kernel
-from .ir import FINISHED_PLANE, Finish, HawkError
+from .ir import AUTO_K_MAX, FINISHED_PLANE, Finish, HawkError
 from .trace import Kernel
 
 TARGETS = ("hip",)
@@ -208,6 +208,10 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
             sidecar["terminated_readonly"] = finish is None
             if finish is not None:
                 sidecar["finish"] = {"mask": finish.name, "counter": FINISHED_PLANE, "steps": finish.steps}
+            if finish is not None and finish.steps == "auto":
+                # reference hawk/trace/steps.py:31-37 and hawk/emit/cuda.py:465-784
+                sidecar["finish"]["steps_max"] = AUTO_K_MAX
+                sidecar["fast_entries"] = {"range": f"{k.name}_range", "persist": f"{k.name}_persist"}
         if getattr(k, "members", None) is not None:
             _chain_record(k, sidecar, mode)
         _write(directory / f"{k.name}.json", json.dumps(sidecar, indent=1, sort_keys=True).encode())

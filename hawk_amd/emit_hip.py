@@ -132,6 +132,7 @@ class _Writer:
         self.deps = Deps()
         self.taped = {}              # loop uid -> True when a tape_read reads it
         self.exits = {}              # loop uid -> the flag its exit set
+        self.trips = {}              # loop uid -> the trips an automatic loop ran
 
     # -- text --------------------------------------------------------------
     def emit(self, text: str) -> None:
@@ -469,11 +470,20 @@ class _Writer:
         if info.exit is not None:
             exited = f"hk_exited{n.uid}"
             self.emit(f"bool {exited} = false;")
-        if info.unroll is True:
-            self.emit("#pragma unroll")
-        elif info.unroll is False:
-            self.emit("#pragma unroll 1")
-        self.emit(f"for (long long {k} = {info.start}LL; {k} != {info.stop()}LL; {k} += {info.step}LL) {{")
+        if info.count is not None:
+            # the trips run are the launch's word (reference hawk/emit/wrapper.py:973-977
+            # clamps it below INT_MAX; a word below 0 runs none)
+            word = self.stage.planes[info.count]["var"]
+            self.emit(f"const long long hk_cnt{n.uid} = static_cast<long long>({word}[0]);")
+            self.emit(f"long long hk_trips{n.uid} = 0;")
+            self.trips[n.uid] = f"hk_trips{n.uid}"
+            self.emit(f"for (long long {k} = 0LL; {k} < hk_cnt{n.uid}; ++{k}) {{")
+        else:
+            if info.unroll is True:
+                self.emit("#pragma unroll")
+            elif info.unroll is False:
+                self.emit("#pragma unroll 1")
+            self.emit(f"for (long long {k} = {info.start}LL; {k} != {info.stop()}LL; {k} += {info.step}LL) {{")
         self.indent += 1
         self.scope.memo.append({})
         self.scope.put(info.index, [k])
@@ -502,6 +512,8 @@ class _Writer:
         for names, row in zip(carry_vars, temps):
             for name, t in zip(names, row):
                 self.emit(f"{name} = {t};")
+        if info.count is not None:
+            self.emit(f"++hk_trips{n.uid};")
         if leave is not None:         # a tail break: this trip's values stand
             self.emit(f"if ({leave}) {{ {exited} = true; break; }}")
         self.scope.memo.pop()
@@ -549,6 +561,7 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
     used = ({n.literal[1] for n in used_leaves} | {name for name, _ in writes}
             | {p for r in rows for p in r[2:]} | {name for name, _, _ in key_writes}
             | {f[0] for f in fused_folds} | {f[1] for f in fused_folds})
+    used |= {n.literal.count for n in ir.topo(roots) if n.kind == "loop" and n.literal.count}
     guard = GUARD_MASK if GUARD_MASK in program.decls and program.decls[GUARD_MASK].role == "terminated" else None
     if guard is not None:
         used.add(guard)
@@ -738,23 +751,9 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         f"        const long long hk_flat = (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * {block}"
         " + static_cast<long long>(threadIdx.x);",
     ]
+    auto = _auto_loop(stage)
     if stage.guard is not None:
-        # The stage skips the samples its mask has finished.  Every lane of a
-        # wave reaches the finish count together (no lane leaves early), and a
-        # lane past `count` takes no sample.
-        mask = stage.planes[stage.guard]["var"]
-        out += ["        const bool hk_in = hk_flat < count;",
-                "        const long long hk_i = base + (hk_in ? hk_flat : 0LL);"]
-        if stage.finish is not None:
-            out += ["        bool hk_new = false;"]
-        out += [f"        if (hk_in && {mask}[hk_i] == 0) {{"]
-        out += ["    " + line for line in body + stores]
-        if stage.finish is not None:
-            cond = w.value(stage.finish[2])[0]
-            out += [f"            if ({cond}) {{ {mask}[hk_i] = 1; hk_new = true; }}"]
-        out += ["        }"]
-        if stage.finish is not None:
-            out += [f"        hk_finish_count({stage.planes[stage.finish[1]]['var']}, hk_new);"]
+        out += _guarded_lines(stage, w, body, stores)
     elif not row_terms and not folds:
         out += ["        if (hk_flat >= count) break;",
                 "        const long long hk_i = base + hk_flat;"]
@@ -776,7 +775,268 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
                     "          } }"]
         out += _fused_fold_lines(folds, block, whole)
     out += ["    }", "}", ""]
+    if auto is not None:
+        head = out.index(f'extern "C" __global__ void __launch_bounds__({block}) {stage.name}(')
+        top = out[:head]
+        if _STEPS_HELPERS.splitlines()[1] not in top:
+            top += _STEPS_HELPERS.splitlines()
+        out = top + out[head:]
+        out += _range_entry(stage, w, body, stores, params, unpack, block, per_thread, xcd_order, auto)
+        out += _persist_entry(stage, mode, params, unpack, block, nontemporal, auto)
     return "\n".join(out)
+
+
+def _auto_loop(stage: Stage):
+    """The stepping loop of a ``hawk.steps(k, "auto")`` stage (its trips read
+    at launch), or ``None``."""
+    if stage.finish is None or stage.finish[2].kind != "loop_exit":
+        return None
+    loop = stage.finish[2].operands[0]
+    return loop if loop.literal.count is not None else None
+
+
+def _guarded_lines(stage: Stage, w: _Writer, body: list, stores: list, fast: bool = False) -> list:
+    """The per-sample scope of a guarded stage.  The stage skips the samples
+    its mask has finished.  Every lane of a wave reaches the finish count
+    together (no lane leaves early), and a lane past `count` takes no sample.
+    ``fast``: the ``_range`` entry's scope, which also counts a sample finished
+    on entry and keeps each lane's trips in ``hk_ran``."""
+    mask = stage.planes[stage.guard]["var"]
+    out = ["        const bool hk_in = hk_flat < count;",
+           "        const long long hk_i = base + (hk_in ? hk_flat : 0LL);"]
+    if stage.finish is not None:
+        out += ["        bool hk_new = false;"]
+    out += [f"        if (hk_in && {mask}[hk_i] == 0) {{"]
+    out += ["    " + line for line in body + stores]
+    if stage.finish is not None:
+        cond = w.value(stage.finish[2])[0]
+        out += [f"            if ({cond}) {{ {mask}[hk_i] = 1; hk_new = true; }}"]
+    if fast:
+        loop = _auto_loop(stage)
+        out += [f"            hk_ran = hk_ran > static_cast<unsigned>({w.trips[loop.uid]}) ? hk_ran"
+                f" : static_cast<unsigned>({w.trips[loop.uid]});",
+                f"            hk_ransum += static_cast<unsigned long long>({w.trips[loop.uid]});",
+                "        } else if (hk_in) {",
+                "            hk_new = true;               // finished on entry: counted by the fast entries"]
+    out += ["        }"]
+    if stage.finish is not None:
+        out += [f"        hk_finish_count({stage.planes[stage.finish[1]]['var']}, hk_new);"]
+    return out
+
+
+#: The step reports of the fast entries (reference ``hawk/emit/cuda.py:277-370``):
+#: a wave's largest and total trip counts, each added by one atomic a wave.
+_STEPS_HELPERS = r"""
+__device__ __forceinline__ void hk_steps_report(unsigned int* steps_max, unsigned long long* steps_sum,
+                                                unsigned int most, unsigned long long total) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const unsigned int m = __shfl_xor(most, o);
+        most = m > most ? m : most;
+        total += __shfl_xor(total, o);
+    }
+    if ((threadIdx.x & 63u) == 0u) {
+        if (steps_max != nullptr && most != 0u) atomicMax(steps_max, most);
+        if (steps_sum != nullptr && total != 0ull) atomicAdd(steps_sum, total);
+    }
+}
+__device__ __forceinline__ void hk_count_report(unsigned int* counter, unsigned int n) {
+    for (int o = 32; o > 0; o >>= 1) n += __shfl_xor(n, o);
+    if ((threadIdx.x & 63u) == 0u && n != 0u) atomicAdd(counter, n);
+}
+"""
+
+#: Samples a wave of the persistent entry claims with one atomic add (four a
+#: lane): one counter serves the whole grid, and a claim per needy lane set
+#: made it the bottleneck (measured on MI355X: 13.3 ms against 0.97 ms for
+#: the plain entry over 2^22 samples of 1-256 steps).
+PERSIST_BATCH = 256
+
+#: The extra slots of the fast entries, after the kernel's own (each a
+#: handle or a value in the argument block, before the partition triple).
+RANGE_SLOTS = ("int_handle", "handle")                      # steps max (u32), steps sum (u64)
+PERSIST_SLOTS = ("int_handle", "int_handle", "handle", "int")   # claim counter, steps max, steps sum, chunk
+
+
+def _range_entry(stage, w, body, stores, params, unpack, block, per_thread, xcd_order, loop) -> list:
+    """``<name>_range``: the stage over ``[base, base+count)``, one lane a
+    sample, that also reports the steps taken (the largest and the total, into
+    ``hk_steps`` / ``hk_stepsum`` when not null) and counts a sample finished
+    on entry (reference ``hawk/emit/cuda.py:692-784``)."""
+    out = [f'extern "C" __global__ void __launch_bounds__({block}) {stage.name}_range(',
+           "        " + ",\n        ".join(params[:-3] + ["ScalarHandle hk_steps_m", "ScalarHandle hk_stepsum_m"]
+                                         + params[-3:]) + ") {",
+           "    (void)nSamples;"]
+    out += ["    " + u for u in unpack]
+    out += ["    unsigned int* hk_steps = reinterpret_cast<unsigned int*>(hk_steps_m.data);",
+            "    unsigned long long* hk_stepsum = reinterpret_cast<unsigned long long*>(hk_stepsum_m.data);",
+            "    unsigned int hk_ran = 0u;",
+            "    unsigned long long hk_ransum = 0ull;"]
+    out += ["    const unsigned hk_blk = (gridDim.x & 7u) ? blockIdx.x"
+            " : (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3);"] if xcd_order else \
+        ["    const unsigned hk_blk = blockIdx.x;"]
+    out += ["#pragma unroll",
+            f"    for (int hk_v = 0; hk_v < {per_thread}; ++hk_v) {{",
+            f"        const long long hk_flat = (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * {block}"
+            " + static_cast<long long>(threadIdx.x);"]
+    out += _guarded_lines(stage, w, body, stores, fast=True)
+    out += ["    }", "    hk_steps_report(hk_steps, hk_stepsum, hk_ran, hk_ransum);", "}", ""]
+    return out
+
+
+def _persist_entry(stage, mode, params, unpack, block, nontemporal, loop) -> list:
+    """``<name>_persist``: a persistent grid whose waves claim samples
+    (reference ``hawk/emit/cuda.py:465-689``).  A lane without a sample takes
+    the next one at a claim: one ballot, one atomic add of the wave's needy
+    lanes to ``hk_next`` by the wave's first needy lane, each lane taking the
+    base plus its rank.  A claimed sample not finished on entry loads its
+    carried values and the step's inputs into registers; the wave then runs up
+    to ``hk_chunk`` trips of the step, each lane on its own sample; a lane
+    whose sample leaves (its exit, or the launch's trips) writes it back and
+    finishes it, and claims again at the next claim.  A wave leaves once
+    every lane's claim fell past ``count`` and none holds a sample.  Each
+    sample runs exactly the trips one launch of the stage runs, so the bits
+    are the stage's; which lane runs it, and when, moves.  The finish count
+    (samples finished in the launch or on entry) and the steps taken are
+    added once a wave, at the end."""
+    info = loop.literal
+    mask = stage.planes[stage.guard]["var"]
+    counter = stage.planes[stage.finish[1]]["var"]
+    word = stage.planes[info.count]["var"]
+    deps = Deps()
+    free = free_inputs(loop, deps)
+    # the claim: every free input of the step and the carried values' launch-start values
+    wc = _Writer(stage, mode, nontemporal)
+    wc.indent = 5
+    wc.deps = deps
+    wc.run(list(loop.operands) + free)
+    live, live_set, claim = [], [], list(wc.lines)
+    for m, f in enumerate(free):
+        vals = wc.value(f)
+        names = [f"hk_pl{m}_{e}" for e in range(len(vals))]
+        live.append((f, names))
+        ct = wc.ctype(f.ttype.dtype)
+        live_set += [f"{ct} {nm}{{}};" for nm in names]
+        claim += ["    " * 5 + f"{nm} = {v};" for nm, v in zip(names, vals)]
+    carries = []
+    for j, (c, x) in enumerate(zip(info.carries, loop.operands)):
+        vals = wc.value(x)
+        size = max(1, c.ttype.size if c.ttype.shape else 1)
+        vals = vals * size if len(vals) == 1 and size > 1 else vals
+        names = [f"hk_pc{j}_{e}" for e in range(size)]
+        carries.append((c, names))
+        live_set += [f"{wc.ctype(c.ttype.dtype)} {nm}{{}};" for nm in names]
+        claim += ["    " * 5 + f"{nm} = {v};" for nm, v in zip(names, vals)]
+    # one trip of the step, over the registers
+    ws = _Writer(stage, mode, nontemporal)
+    ws.indent = 4
+    ws.deps = deps
+    for f, names in live:
+        ws.scope.put(f, names)
+    for c, names in carries:
+        ws.scope.put(c, names)
+    ws.scope.put(info.index, ["hk_trip"])
+    ws.run(ir.body_roots(info))
+    nexts = [ws.value(x) for x in info.nexts]
+    leave = ws.scalar(info.exit)
+    step = list(ws.lines)
+    temps, assign = [], []
+    for (c, names), nv in zip(carries, nexts):
+        nv = nv * len(names) if len(nv) == 1 and len(names) > 1 else nv
+        for nm, val in zip(names, nv):
+            t = f"hk_t_{nm[3:]}"
+            temps.append("    " * 4 + f"const auto {t} = {val};")
+            assign.append("    " * 4 + f"{nm} = {t};")
+    # the write-back: each commit is a carried value (its loop_value)
+    commit = []
+    for plane, node in stage.writes:
+        j = node.literal
+        names = carries[j][1]
+        var = stage.planes[plane]["var"]
+        st = ws.store if nontemporal else (lambda ref, val: f"{ref} = {val};")
+        if not node.ttype.shape:
+            commit.append("    " * 4 + st(f"{var}[hk_i]", names[0]))
+        else:
+            for e in _entries(node.ttype.shape):
+                cidx = _flat(node.ttype.shape, e)
+                commit.append("    " * 4 + st(f"{var}[{cidx} * {var}_cs + hk_i]", names[cidx]))
+    out = [f'extern "C" __global__ void __launch_bounds__({block}) {stage.name}_persist(',
+           "        " + ",\n        ".join(params[:-3] + ["ScalarHandle hk_next_m", "ScalarHandle hk_steps_m",
+                                                      "ScalarHandle hk_stepsum_m", "long long hk_chunk"]
+                                         + params[-3:]) + ") {",
+           "    (void)nSamples;"]
+    out += ["    " + u for u in unpack]
+    out += ["    unsigned int* hk_next = reinterpret_cast<unsigned int*>(hk_next_m.data);",
+            "    unsigned int* hk_steps = reinterpret_cast<unsigned int*>(hk_steps_m.data);",
+            "    unsigned long long* hk_stepsum = reinterpret_cast<unsigned long long*>(hk_stepsum_m.data);",
+            f"    const long long hk_budget = static_cast<long long>({word}[0]);",
+            "    const long long hk_span = hk_chunk < 1 ? 1 : hk_chunk;     // every chunk runs a trip",
+            "    const unsigned hk_lane = threadIdx.x & 63u;",
+            "    const unsigned long long hk_below = (1ull << hk_lane) - 1ull;"]
+    out += ["    " + d for d in live_set]
+    out += ["    bool hk_has = false, hk_out = false;",
+            "    long long hk_i = base, hk_trip = 0;",
+            "    unsigned int hk_most = 0u, hk_fin = 0u;",
+            "    unsigned long long hk_total = 0ull;",
+            "    long long hk_qn = 0, hk_qe = 0;        // the wave's batch of sample offsets (the same in every lane)",
+            "    while (true) {",
+            "        // the claim: the wave's lanes without a sample take the next ones of the",
+            "        // wave's batch, in lane order; a spent batch is refilled by one atomic add",
+            "        const bool hk_needy = !hk_has && !hk_out;",
+            "        const unsigned long long hk_need = __ballot(hk_needy);",
+            "        if (hk_need != 0ull) {",
+            "            if (hk_qn >= hk_qe) {",
+            "                const int hk_lead = __ffsll(static_cast<long long>(hk_need)) - 1;",
+            "                unsigned int hk_b = 0u;",
+            "                if (hk_lane == static_cast<unsigned>(hk_lead))",
+            f"                    hk_b = atomicAdd(hk_next, {PERSIST_BATCH}u);",
+            "                hk_b = __shfl(hk_b, hk_lead);",
+            "                hk_qn = static_cast<long long>(hk_b);",
+            f"                hk_qe = hk_qn + {PERSIST_BATCH}LL < count ? hk_qn + {PERSIST_BATCH}LL : count;",
+            "            }",
+            "            if (hk_qn >= count) {",
+            "                hk_out = true;                       // every sample is taken",
+            "            } else {",
+            "                const long long hk_avail = hk_qe - hk_qn;",
+            "                const long long hk_r = static_cast<long long>(__popcll(hk_need & hk_below));",
+            "                if (hk_needy && hk_r < hk_avail) {",
+            "                    hk_i = base + hk_qn + hk_r;",
+            f"                    if ({mask}[hk_i] == 0) {{"]
+    out += claim
+    out += ["                        hk_has = true;",
+            "                        hk_trip = 0;",
+            "                    } else {",
+            "                        ++hk_fin;                // finished on entry",
+            "                    }",
+            "                }",
+            "                const long long hk_took = static_cast<long long>(__popcll(hk_need));",
+            "                hk_qn += hk_took < hk_avail ? hk_took : hk_avail;",
+            "            }",
+            "        }",
+            "        if (__ballot(hk_has) == 0ull) {",
+            "            if (__ballot(!hk_out) == 0ull) break;",
+            "            continue;",
+            "        }",
+            "        if (hk_has) {",
+            "            bool hk_exit = false;",
+            "            for (long long hk_c = 0; hk_c < hk_span && hk_trip < hk_budget; ++hk_c) {"]
+    out += step + temps + assign
+    out += ["                ++hk_trip;",
+            f"                if ({leave}) {{ hk_exit = true; break; }}",
+            "            }",
+            "            if (hk_exit || hk_trip >= hk_budget) {"]
+    out += commit
+    out += [f"                if (hk_exit) {{ {mask}[hk_i] = 1; ++hk_fin; }}",
+            "                const unsigned int hk_ran = hk_trip > 0 ? static_cast<unsigned int>(hk_trip) : 0u;",
+            "                hk_most = hk_ran > hk_most ? hk_ran : hk_most;",
+            "                hk_total += hk_ran;",
+            "                hk_has = false;",
+            "            }",
+            "        }",
+            "    }",
+            f"    hk_count_report({counter}, hk_fin);",
+            "    hk_steps_report(hk_steps, hk_stepsum, hk_most, hk_total);",
+            "}", ""]
+    return out
 
 
 #: The finish count (reference ``hawk/emit/wrapper.py:522-537``): one atomic

@@ -210,8 +210,11 @@ def smooth_finish(x: Scalar, terminated: Terminated, y: Mutable[Scalar]):
 
 #: The oscillator taking up to 8 steps a launch.
 osc_finish_x8 = _trace.steps(osc_finish, 8)
+#: The oscillator taking the launch's word of steps, with its fast entries.
+osc_finish_xauto = _trace.steps(osc_finish, "auto")
 smooth_finish_vjp = Kernel("smooth_finish_vjp", diff.vjp(smooth_finish, wrt=("x",)))
-FINISHING = {k.name: k for k in (osc_finish, osc_finish_x8, stop_only, smooth_finish, smooth_finish_vjp)}
+FINISHING = {k.name: k for k in (osc_finish, osc_finish_x8, osc_finish_xauto, stop_only, smooth_finish,
+                                 smooth_finish_vjp)}
 
 
 #: Every kernel above, by name.

@@ -69,6 +69,7 @@ class LoopInfo:
     names: tuple = ()                # the authored names of the slots (diagnostics)
     unroll: bool | None = None       # True: #pragma unroll; False: kept rolled; None: the compiler's choice
     exit: Node | None = None         # a bool over the trip's inputs: when true, the trip's nexts stand and the loop ends
+    count: str | None = None         # a one-cell int32 plane read at launch: the trips run (start 0, step 1)
 
     def stop(self) -> int:
         return self.start + self.trip * self.step
@@ -494,7 +495,7 @@ class Finish:
 
     name: str
     value: Node
-    steps: int = 1                   # the steps one launch takes (hawk.steps); 1 as authored
+    steps: int | str = 1             # the steps one launch takes (hawk.steps): 1 as authored, K, or "auto"
 
 
 #: The one-cell counter a finishing kernel adds its newly finished samples to
@@ -502,6 +503,12 @@ class Finish:
 FINISHED_PLANE = "finished_count"
 #: The only mask a kernel's guard gates on: the ``Terminated`` parameter of this name.
 GUARD_MASK = "terminated"
+#: The one-cell int32 word a ``steps="auto"`` kernel reads its trip count
+#: from (reference ``hawk/ir/nodes.py:841-845``): set by the runtime, never
+#: bound by the caller.
+FUSED_STEPS_PLANE = "fused_steps"
+#: The static bound an automatic kernel records (reference ``hawk/trace/steps.py:70``).
+AUTO_K_MAX = 64
 
 
 @dataclass
@@ -602,6 +609,7 @@ def substitute(roots, mapping: dict) -> list:
                 copy = loop_node(next(_uid), info.trip, info.start, info.step, info.index,
                                  info.carries, new_kids, new_nexts, info.names, exit=new_exit)
                 copy.literal.unroll = info.unroll
+                copy.literal.count = info.count
                 memo[n.uid] = copy
             continue
         if any(a is not b for a, b in zip(new_kids, kids)):
@@ -807,6 +815,7 @@ def used_names(program: Program) -> set:
         used.add(GUARD_MASK)
     if any(isinstance(s, Finish) for s in program.sinks):
         used.add(FINISHED_PLANE)
+    used |= {n.literal.count for n in topo(sink_roots(program.sinks)) if n.kind == "loop" and n.literal.count}
     return used
 
 

@@ -41,6 +41,26 @@ _PER_SAMPLE = ("per_sample", "vec_in", "mat_in", "mutable", "out", "wide_out", "
 #: binds its own, zeroed before each ``hawk.run`` and readable afterwards as
 #: the kernel's ``finished``.
 FINISHED_PLANE = "finished_count"
+#: The trip-count word of a ``hawk.steps(k, "auto")`` kernel: the runtime's
+#: own one-cell int32, set from ``steps=`` (reference ``hawk/ir/nodes.py:841-845``).
+FUSED_STEPS_PLANE = "fused_steps"
+#: The fast entries of an automatic kernel and the slots each adds to the
+#: kernel's own (reference ``hawk/emit/cuda.py:262-281``): the range entry's
+#: steps max (u32) and steps sum (u64); the persistent entry's claim counter,
+#: steps max, steps sum and chunk length.
+FAST_SLOTS = {"range": ("int_handle", "handle"), "persist": ("int_handle", "int_handle", "handle", "int")}
+#: The persistent entry's most workgroups: 256 CUs x 8 workgroups of 256
+#: threads (32 waves a CU, gfx950's most); a smaller run takes one a block of samples.
+PERSIST_BLOCKS = 2048
+#: Trips between two claims of the persistent entry.  Measured on MI355X
+#: (2^22 samples of 1-256 steps of the oscillator, one launch): chunks of 1,
+#: 4, 8, 16, 32, 64 and 256 trips take 1.35, 0.82, 0.65, 0.56, 0.49, 0.50 and
+#: 0.64 ms (the plain entry 0.93 ms): a short chunk spends its time claiming,
+#: a long one holds finished lanes idle until the chunk ends.
+PERSIST_CHUNK = 32
+#: The fast entries' most samples a launch: the persistent grid claims from a
+#: 32-bit counter in batches past the end, so it stays well below 2^32.
+FAST_MAX = 1 << 30
 
 
 def _torch():
@@ -73,6 +93,8 @@ class DeviceKernel:
         self._lock = threading.Lock()
         self.scatter_chunks = None
         self.finished = None      # the runtime's finish counter when the caller binds none
+        self.steps_max = None     # a fast entry's largest trips a sample (one int32 cell)
+        self.steps_sum = None     # a fast entry's trips over every sample (one int64 cell)
 
     # -- validation ----------------------------------------------------------
     def _real_dtype(self):
@@ -80,7 +102,88 @@ class DeviceKernel:
         return torch.float32 if self.mode == "float32" else torch.float64
 
     def caller_planes(self) -> list:
-        return [n for n, p in self.planes.items() if not p.get("scratch")]
+        return [n for n, p in self.planes.items() if not p.get("scratch") and n != FUSED_STEPS_PLANE]
+
+    @property
+    def automatic(self) -> bool:
+        """Whether the kernel reads its trip count at launch (``hawk.steps(k, "auto")``)."""
+        return (self.sidecar.get("finish") or {}).get("steps") == "auto"
+
+    def _word(self, steps, device, stream: int):
+        """The trip-count word, set to ``steps`` on ``stream`` (held; rewritten
+        only when the value changes)."""
+        torch = _torch()
+        if isinstance(steps, bool) or not isinstance(steps, int):
+            raise HawkError(f"kernel {self.name!r}: steps= is an int (the trips this launch runs), got {steps!r}")
+        held = self._scratch.get(("word", device))
+        if held is None:
+            held = torch.zeros(1, dtype=torch.int32, device=device)
+            self._scratch[("word", device)] = held
+            self._word_value = None
+        value = max(-(1 << 31), min(steps, (1 << 31) - 1))
+        if getattr(self, "_word_value", None) != value:
+            with torch.cuda.stream(torch.cuda.ExternalStream(stream)) if stream else _nullcontext():
+                held.fill_(value)
+            self._word_value = value
+        return held
+
+    def _held(self, key, dtype, device):
+        torch = _torch()
+        t = self._scratch.get((key, device))
+        if t is None:
+            t = torch.zeros(1, dtype=dtype, device=device)
+            self._scratch[(key, device)] = t
+        return t
+
+    def _fast(self, entry: str, bound: dict, n: int, chunk: int, device):
+        """``(DeviceEntry, ArgBlock)`` of the fast entry ``entry`` bound to
+        ``bound``, its report cells zeroed (the steps max and sum are then the
+        kernel's ``steps_max`` / ``steps_sum``)."""
+        torch = _torch()
+        if entry not in FAST_SLOTS:
+            raise HawkError(f"kernel {self.name!r}: entry= is 'plain', 'range' or 'persist', got {entry!r}")
+        if not self.automatic:
+            raise HawkError(f"kernel {self.name!r}: the fast entries are built for hawk.steps(k, 'auto') kernels")
+        names = self.sidecar["fast_entries"]
+        fn = self.library.entry(names[entry])
+        block = _core.ArgBlock(list(self.sidecar["descriptor"]) + list(FAST_SLOTS[entry]))
+        self._bind(block, bound, n)
+        self.steps_max = self._held("steps_max", torch.int32, device)
+        self.steps_sum = self._held("steps_sum", torch.int64, device)
+        self.steps_max.zero_()
+        self.steps_sum.zero_()
+        extra = [self.steps_max, self.steps_sum]
+        if entry == "persist":
+            if isinstance(chunk, bool) or not isinstance(chunk, int) or not 1 <= chunk <= 1 << 20:
+                raise HawkError(f"kernel {self.name!r}: chunk= is an int in [1, 2^20], got {chunk!r}")
+            nxt = self._held("claims", torch.int32, device)
+            nxt.zero_()
+            extra = [nxt] + extra
+        slot = len(self.arg_spec)
+        for x in extra:
+            block.bind(slot, x.data_ptr(), 1, 1, _contracts.DEVICE_ROCM, x.device.index or 0)
+            slot += 1
+        if entry == "persist":
+            block.bind_value(slot, int(chunk))
+        return fn, block
+
+    def _bind(self, block, bound: dict, n: int) -> None:
+        for slot, (role, name) in enumerate(self.arg_spec):
+            kind = block.descriptor[slot]
+            x = bound[name]
+            if kind in ("f64", "f32"):
+                block.bind_value(slot, float(x))
+                continue
+            block.bind(slot, x.data_ptr(), _bound_length(role, x, n), 1, _contracts.DEVICE_ROCM,
+                       x.device.index or 0)
+
+    def _launch_fast(self, entry: str, fn, block, base: int, count: int, n: int, stream: int) -> None:
+        threads = self.launch_shape["block"]
+        if entry == "range":
+            fn.run(block, base, count, n, threads=threads, per_thread=self.launch_shape["per_thread"], stream=stream)
+            return
+        grid = max(1, min(-(-count // threads), PERSIST_BLOCKS))
+        fn.run_grid(block, base, count, n, grid, threads, stream=stream)
 
     def _counter(self, arrays: dict, device):
         """``arrays`` with the finish counter bound: the caller's, else the
@@ -285,12 +388,24 @@ class DeviceKernel:
             self.block.bind(slot, x.data_ptr(), _bound_length(role, x, n), 1, _contracts.DEVICE_ROCM,
                             x.device.index or 0)
 
-    def _run(self, arrays: dict, base: int, count: int, n: int, stream: int, check: bool) -> None:
+    def _run(self, arrays: dict, base: int, count: int, n: int, stream: int, check: bool, steps=None,
+             entry: str = "plain", chunk: int = PERSIST_CHUNK) -> None:
         torch = _torch()
         device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
         bound, held = self._counter(dict(arrays), device)
         if held is not None:
             held.zero_()                          # a count per run
+        if self.automatic:
+            bound[FUSED_STEPS_PLANE] = self._word(1 if steps is None else steps, device, stream)
+        elif steps is not None:
+            raise HawkError(f"kernel {self.name!r}: steps= sets the trip count of a hawk.steps(k, 'auto') kernel; "
+                            "this one takes a fixed number of steps")
+        if entry != "plain":
+            if count >= FAST_MAX:
+                raise HawkError(f"kernel {self.name!r}: the fast entries take fewer than 2^30 samples a launch")
+            fn, block = self._fast(entry, bound, n, chunk, device)
+            self._launch_fast(entry, fn, block, base, count, n, stream)
+            return
         for name, info in self.planes.items():
             if info.get("cells_of"):
                 bound[name] = self._fold_scratch(name, bound, device)
@@ -349,13 +464,17 @@ class DeviceKernel:
                 if problem:
                     raise HawkError(problem)
 
-    def prepare(self, *, stream=None, **arrays) -> Prepared:
+    def prepare(self, *, stream=None, steps=None, entry: str = "plain", chunk: int = PERSIST_CHUNK,
+                **arrays) -> Prepared:
         """Validate and bind ``arrays`` once and return a :class:`Prepared`
         launcher that re-runs the whole kernel (per-sample stage and team
         stages) over every sample with no per-call validation: the stable-binding
         path of reference ``tests/cards/CARD_LAUNCH_CROSSINGS.md`` (one crossing
-        per launch).  The planes must stay alive and unmoved while it is used."""
-        return Prepared(self, arrays, stream)
+        per launch).  The planes must stay alive and unmoved while it is used.
+        ``steps`` / ``entry`` / ``chunk`` are :func:`run`'s; a prepared
+        automatic kernel holds its own trip-count word, and its reports and
+        finish count add up over calls."""
+        return Prepared(self, arrays, stream, steps=steps, entry=entry, chunk=chunk)
 
     def launch(self, base: int, count: int, n_samples: int, stream: int = 0) -> None:
         """The per-sample stage alone over ``[base, base+count)`` (planes already bound)."""
@@ -475,12 +594,29 @@ def load(directory, kernel: str, sidecar: dict | None = None):
     return DeviceKernel(directory, sidecar)
 
 
+class _nullcontext:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
+
+
 def run(kernel: DeviceKernel, *, base: int = 0, count: int | None = None, n_samples: int | None = None,
-        stream=None, check: bool = True, **arrays) -> None:
+        stream=None, check: bool = True, steps=None, entry: str = "plain", chunk: int = PERSIST_CHUNK,
+        **arrays) -> None:
     """Bind ``arrays`` and run the kernel once, in place, on the current HIP
     stream (or ``stream``).  ``count`` defaults to every sample from ``base``.
     A kernel with team stages (``hawk.sum`` / ``hawk.scatter`` with
-    policy='ordered') runs over every sample (no ``base``/``count``)."""
+    policy='ordered') runs over every sample (no ``base``/``count``).
+
+    A ``hawk.steps(k, "auto")`` kernel runs ``steps`` trips (default 1) and
+    may run through a fast entry: ``entry="range"`` (one lane a sample) or
+    ``"persist"`` (a persistent grid whose waves claim samples, ``chunk``
+    trips between claims, default :data:`PERSIST_CHUNK`).  Both give the
+    plain entry's bits, count samples finished on entry too (the counter then
+    holds the batch's finished count), and leave the largest and the total
+    trips run in the kernel's ``steps_max`` and ``steps_sum``."""
     torch = _torch()
     if isinstance(kernel, ChainedKernel):
         if base != 0 or count is not None:
@@ -503,13 +639,15 @@ def run(kernel: DeviceKernel, *, base: int = 0, count: int | None = None, n_samp
     elif hasattr(stream, "cuda_stream"):
         stream = stream.cuda_stream
     with kernel._lock:
-        kernel._run(arrays, int(base), int(count), int(n), int(stream), check)
+        kernel._run(arrays, int(base), int(count), int(n), int(stream), check, steps=steps, entry=entry,
+                    chunk=chunk)
 
 
 class Prepared:
     """A kernel bound once to fixed planes (see :meth:`DeviceKernel.prepare`)."""
 
-    def __init__(self, kernel: DeviceKernel, arrays: dict, stream=None):
+    def __init__(self, kernel: DeviceKernel, arrays: dict, stream=None, steps=None, entry: str = "plain",
+                 chunk: int = PERSIST_CHUNK):
         torch = _torch()
         self.kernel = kernel
         self.n = kernel.check_planes(arrays)
@@ -524,6 +662,22 @@ class Prepared:
         if held is not None:
             held.zero_()                          # counts every call from here on
         self.finished = bound.get(FINISHED_PLANE)
+        if kernel.automatic:
+            w = 1 if steps is None else steps
+            if isinstance(w, bool) or not isinstance(w, int):
+                raise HawkError(f"kernel {kernel.name!r}: steps= is an int, got {w!r}")
+            bound[FUSED_STEPS_PLANE] = torch.full((1,), max(-(1 << 31), min(w, (1 << 31) - 1)),
+                                                  dtype=torch.int32, device=device)
+        elif steps is not None:
+            raise HawkError(f"kernel {kernel.name!r}: steps= sets the trip count of a hawk.steps(k, 'auto') kernel")
+        self.fast = None
+        if entry != "plain":
+            if self.n >= FAST_MAX:
+                raise HawkError(f"kernel {kernel.name!r}: the fast entries take fewer than 2^30 samples a launch")
+            fn, block = kernel._fast(entry, bound, self.n, chunk, device)
+            claims = kernel._scratch.get(("claims", device)) if entry == "persist" else None
+            self.fast = (entry, fn, block, claims)
+            self.steps_max, self.steps_sum = kernel.steps_max, kernel.steps_sum
         for name, info in kernel.planes.items():
             if info.get("cells_of"):
                 bound[name] = kernel._fold_scratch(name, bound, device)
@@ -598,6 +752,15 @@ class Prepared:
         ...); calling every ``launch`` in order is one run."""
         k = self.kernel
         out = [("fold_clear", lambda fn=fn, args=args: fn(*args, self.stream)) for fn, args in self.before]
+        if self.fast is not None:
+            entry, fn, block, claims = self.fast
+
+            def fast_stage():
+                if claims is not None:
+                    claims.zero_()              # the persistent grid claims from sample 0 again
+                k._launch_fast(entry, fn, block, 0, self.n, self.n, self.stream)
+            out.append((f"{k.name}_{entry}", fast_stage))
+            return out
         if k.entry is not None:
             def stage():
                 k.entry.run(self.block, 0, self.n, self.n, threads=k.launch_shape["block"],

@@ -795,7 +795,7 @@ class Kernel:
         return f"<hawk kernel {self.name}: {[type(s).__name__ + ':' + s.name for s in self.sinks]}>"
 
 
-def steps(kernel: Kernel, K: int) -> Kernel:
+def steps(kernel: Kernel, K) -> Kernel:
     """``kernel`` stepping up to ``K`` times a launch, named ``<name>_x<K>``
     (reference ``hawk/trace/steps.py:81-99``).
 
@@ -809,13 +809,21 @@ def steps(kernel: Kernel, K: int) -> Kernel:
     one launch of ``kernel``, so K launches of ``kernel`` and one of the
     result give the same bits (the build does not contract multiply-adds).
     A sample may run up to ``K - 1`` steps past a caller's own step cap.
-    ``steps="auto"`` (a trip count read at launch) is not in this build."""
+
+    ``K="auto"`` names the result ``<name>_xauto``: its trip count is read at
+    launch from the one-cell ``fused_steps`` word, which the runtime sets
+    (``hawk.run(..., steps=W)``, default 1; a word below 0 runs none), and it
+    also builds the ``_range`` and ``_persist`` entries that report the
+    steps taken (reference ``hawk/trace/steps.py:27-44``)."""
     if not isinstance(kernel, Kernel):
         raise HawkError("hawk.steps(kernel, K) takes a traced kernel")
     name = kernel.name
-    if isinstance(K, bool) or not isinstance(K, int) or K < 1:
-        raise HawkError(f"hawk.steps({name!r}, {K!r}): K is an int >= 1 (steps='auto', a trip count read "
-                        "at launch, is not in this build)")
+    auto = K == "auto"
+    if not auto and (isinstance(K, bool) or not isinstance(K, int) or K < 1):
+        raise HawkError(f"hawk.steps({name!r}, {K!r}): K is an int >= 1 or 'auto'")
+    if auto and ir.FUSED_STEPS_PLANE in kernel.decls:
+        raise HawkError(f"hawk.steps({name!r}, 'auto'): {ir.FUSED_STEPS_PLANE!r} is reserved for the trip "
+                        "count of an automatic kernel; rename that parameter")
     program = kernel.program
     finishes = [s for s in program.sinks if isinstance(s, Finish)]
     if not finishes:
@@ -852,10 +860,15 @@ def steps(kernel: Kernel, K: int) -> Kernel:
         mapping = {n.uid: carries[slot[n.literal[1]]] for n in reads}
         return tuple(ir.substitute(roots, mapping))
 
-    loop = ir.new_loop(K, 0, 1, tuple(inits), body, tuple(s.name for s in commits), exits=True)
+    loop = ir.new_loop(ir.AUTO_K_MAX if auto else K, 0, 1, tuple(inits), body, tuple(s.name for s in commits),
+                       exits=True)
+    decls = dict(program.decls)
+    if auto:
+        loop.literal.count = ir.FUSED_STEPS_PLANE
+        decls[ir.FUSED_STEPS_PLANE] = Decl(ir.FUSED_STEPS_PLANE, "lookup", TensorType((), "i32"))
     sinks = [Assign(s.name, ir.loop_value(loop, j), "mutable") for j, s in enumerate(commits)]
     sinks.append(Finish(finish.name, ir.loop_exit(loop), steps=K))
-    stepped = Kernel(f"{name}_x{K}", Program(dict(program.decls), sinks, program.grid, dict(program.tables)))
+    stepped = Kernel(f"{name}_x{K}", Program(decls, sinks, program.grid, dict(program.tables)))
     stepped.step = kernel
     return stepped
 

@@ -665,15 +665,16 @@ HKO_EXPORT void hko_mm16_vjp(const float* A, const float* B, const float* bar_C,
  * leaving after the step at which t' >= t_final (its values are that step's),
  * and then its mask is set.  Returns how many samples this launch finished
  * (the finished_count the reference adds to; :228-241 is its NumPy twin
- * with K = 1). */
+ * with K = 1); `trips` (nullable) gets each sample's steps this launch (the
+ * fast entries' reports, hawk/emit/cuda.py:692-702).  K <= 0 takes none. */
 HKO_EXPORT int64_t hko_osc_launch(int64_t base, int64_t count, int K, double dt, const double* t_final, double* x,
-                                  double* v, double* t, unsigned char* mask) {
+                                  double* v, double* t, unsigned char* mask, int32_t* trips) {
     int64_t finished = 0;
     for (int64_t i = base; i < base + count; ++i) {
-        if (mask[i]) continue;
+        if (mask[i]) { if (trips) trips[i] = 0; continue; }
         double xi = x[i], vi = v[i], ti = t[i];
-        int done = 0;
-        for (int k = 0; k < K && !done; ++k) {
+        int done = 0, k = 0;
+        for (; k < K && !done; ++k) {
             const double xn = xi + dt * vi;
             const double vn = vi + dt * (-xi);
             const double tn = ti + dt;
@@ -681,6 +682,7 @@ HKO_EXPORT int64_t hko_osc_launch(int64_t base, int64_t count, int K, double dt,
             done = tn >= t_final[i];
         }
         x[i] = xi; v[i] = vi; t[i] = ti;
+        if (trips) trips[i] = k;          /* the steps this launch took of sample i */
         if (done) { mask[i] = 1; ++finished; }
     }
     return finished;

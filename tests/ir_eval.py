@@ -201,7 +201,12 @@ class Evaluator:
         carries = [np.array(self.memo[o.uid], copy=True) for o in m.operands]
         tape = [[] for _ in carries]
         done = np.zeros(self.n, dtype=bool)       # lanes that took the loop's exit
-        for kval in range(info.start, info.stop(), info.step):
+        trips = range(info.start, info.stop(), info.step)
+        if info.count is not None:                # the launch's word: that many trips
+            trips = range(0, max(0, int(np.asarray(self.env[info.count]).reshape(-1)[0])))
+        for kval in trips:
+            if info.exit is not None and done.all():
+                break
             for j, c in enumerate(carries):
                 tape[j].append(c)
             inner = Evaluator(self.env, self.n, self.deps)

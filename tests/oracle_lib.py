@@ -51,7 +51,7 @@ def lib(profile: str = "portable"):
         "hko_keyed_sample_sum": (None, [_P, _I64, _I64, _P]),
         "hko_net_threads": (None, [ctypes.c_int, _P, _P, _P, _P, _P, _I64, _I64, _P, ctypes.c_int]),
         "hko_chain_members_threads": (None, [_P, _P, _P, _I64, ctypes.c_int]),
-        "hko_osc_launch": (_I64, [_I64, _I64, ctypes.c_int, _D, _P, _P, _P, _P, _P]),
+        "hko_osc_launch": (_I64, [_I64, _I64, ctypes.c_int, _D, _P, _P, _P, _P, _P, _P]),
         "hko_row_sums": (None, [_P, _I64, _P, _P]),
         "hko_rows_finish": (_D, [_P, _P, _I64]),
         "hko_sample_sum": (_D, [_P, _I64]),
@@ -203,16 +203,20 @@ def chain_members(x, acc, threads: int = 1, profile: str = "portable"):
     return y
 
 
-def osc_launch(K, dt, t_final, x, v, t, mask, base: int = 0, count=None, profile: str = "portable") -> int:
+def osc_launch(K, dt, t_final, x, v, t, mask, base: int = 0, count=None, profile: str = "portable",
+               trips=None) -> int:
     """One launch of the oscillator that finishes its own sample, ``K`` steps
     at most: ``x``, ``v``, ``t`` (float64) and ``mask`` (bool) updated in
-    place over ``[base, base+count)``; returns how many samples it finished."""
+    place over ``[base, base+count)``; returns how many samples it finished.
+    ``trips`` (int32, optional) gets each sample's steps this launch."""
     for a in (t_final, x, v, t):
         assert a.dtype == np.float64 and a.flags.c_contiguous
     assert mask.dtype == np.bool_ and mask.flags.c_contiguous
+    if trips is not None:
+        assert trips.dtype == np.int32 and trips.flags.c_contiguous and trips.size == x.size
     count = x.size - base if count is None else count
     return int(lib(profile).hko_osc_launch(base, count, K, dt, _p(t_final), _p(x), _p(v), _p(t),
-                                           mask.ctypes.data_as(_P)))
+                                           mask.ctypes.data_as(_P), None if trips is None else _p(trips)))
 
 
 def net_loss(w, mask, x, y, threads: int = 1, profile: str = "portable"):

@@ -262,7 +262,14 @@ def test_steps_refusals():
     with pytest.raises(HawkError, match="K is an int"):
         hawk.steps(E.osc_finish, 0)
     with pytest.raises(HawkError, match="K is an int"):
-        hawk.steps(E.osc_finish, "auto")
+        hawk.steps(E.osc_finish, "several")
+
+    @hawk.kernel
+    def reserved(fused_steps: Scalar, terminated: Terminated, x: Mutable[Scalar]):
+        x = x + fused_steps
+        terminated = x > 1.0
+    with pytest.raises(HawkError, match="'fused_steps' is reserved"):
+        hawk.steps(reserved, "auto")
     with pytest.raises(HawkError, match="derive from the single step"):
         hawk.steps(E.osc_finish_x8, 2)
     with pytest.raises(HawkError, match="commits no Mutable"):
@@ -313,6 +320,44 @@ def test_the_stepped_program_evaluates_to_the_oracle(K):
         if mask.all():
             break
     assert mask.all()
+
+
+def test_an_automatic_kernel_records_its_word_and_fast_entries(tmp_path):
+    import hawk_amd as hawk
+    from hawk_amd import examples as E
+    ka = E.osc_finish_xauto
+    assert ka.name == "osc_finish_xauto" and ka.sinks[-1].steps == "auto"
+    assert ("lookup", "fused_steps") in ka.arg_spec
+    b = hawk.build([ka], tmp_path)
+    sc = b.sidecar(ka.name)
+    assert sc["finish"] == {"mask": "terminated", "counter": "finished_count", "steps": "auto", "steps_max": 64}
+    assert sc["fast_entries"] == {"range": "osc_finish_xauto_range", "persist": "osc_finish_xauto_persist"}
+    src = (tmp_path / f"{ka.name}.hip").read_text()
+    persist = src[src.index("osc_finish_xauto_persist("):]
+    # one claim a wave: a ballot, one atomic add by the first needy lane; no barrier
+    assert "atomicAdd(hk_next," in persist and "__syncthreads" not in persist
+    assert "hk_span = hk_chunk < 1 ? 1 : hk_chunk" in persist        # every chunk runs a trip
+    from hawk_amd.resources import kernel_resources
+    res = kernel_resources((tmp_path / f"{ka.name}.hsaco").read_bytes())
+    assert set(res) == {ka.name, f"{ka.name}_range", f"{ka.name}_persist"}
+    assert all(r["private_segment_fixed_size"] == 0 for r in res.values())
+
+
+@pytest.mark.parametrize("word", [1, 5, 0, -3, 64, 100])
+def test_the_automatic_program_runs_the_word_of_trips(word):
+    from hawk_amd import examples as E
+    from ir_eval import evaluate
+    t_final, x, v = _inputs(64, seed=19)
+    t, mask = np.zeros(x.size), np.zeros(x.size, dtype=bool)
+    env = {"dt": DT, "t_final": t_final, "x": x, "v": v, "t": t, "terminated": mask,
+           "fused_steps": np.array([word], dtype=np.int32)}
+    got = evaluate(E.osc_finish_xauto.program, env, x.size)
+    ox, ov, ot, om = x.copy(), v.copy(), t.copy(), mask.copy()
+    trips = np.zeros(x.size, dtype=np.int32)
+    O.osc_launch(word, DT, t_final, ox, ov, ot, om, trips=trips)
+    for key, ref in (("x", ox), ("v", ov), ("t", ot), ("terminated", om)):
+        assert np.asarray(got[key]).tobytes() == ref.tobytes(), key
+    assert np.array_equal(trips, np.clip(np.minimum(word, np.rint(t_final / DT)), 0, None))
 
 
 # -- on the GPU -------------------------------------------------------------------
@@ -420,3 +465,70 @@ def test_two_to_the_22_samples_step_to_the_oracle(finishing, gpu):
     assert counted == n and launches == len(counts)
     for key, ref in (("x", rx), ("v", rv), ("t", rt), ("terminated", rmask)):
         assert got[key].tobytes() == ref.tobytes(), key
+
+
+def _run_auto(finishing, gpu, t_final, x, v, mask, word, entry="plain", chunk=8):
+    """One launch of the automatic oscillator; the planes, the runtime's
+    counter and, for a fast entry, its reports."""
+    import hawk_amd as hawk
+    k = hawk.load(finishing, "osc_finish_xauto")
+    planes = {"t_final": _dev(t_final, gpu), "x": _dev(x, gpu), "v": _dev(v, gpu),
+              "t": _dev(np.zeros(x.size), gpu), "terminated": _dev(mask, gpu)}
+    hawk.run(k, dt=DT, steps=word, entry=entry, chunk=chunk, **planes)
+    got = {key: val.cpu().numpy() for key, val in planes.items()}
+    reports = None if entry == "plain" else (int(k.steps_max.item()), int(k.steps_sum.item()))
+    return got, int(k.finished.item()), reports
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("word", [1, 8, 0, -3, 100])
+def test_the_automatic_kernel_runs_its_word(finishing, gpu, word):
+    t_final, x, v = _inputs(5000, seed=23)
+    mask = np.zeros(x.size, dtype=bool)
+    got, counted, _ = _run_auto(finishing, gpu, t_final, x, v, mask, word)
+    ox, ov, ot, om = x.copy(), v.copy(), np.zeros(x.size), mask.copy()
+    want = O.osc_launch(word, DT, t_final, ox, ov, ot, om)
+    assert counted == want
+    for key, ref in (("x", ox), ("v", ov), ("t", ot), ("terminated", om)):
+        assert got[key].tobytes() == ref.tobytes(), key
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("entry,word,chunk", [("range", 7, 8), ("range", 64, 8), ("persist", 1, 8),
+                                              ("persist", 7, 1), ("persist", 64, 3), ("persist", 64, 64),
+                                              ("persist", 0, 8)])
+def test_the_fast_entries_are_the_plain_entrys_bits(finishing, gpu, entry, word, chunk):
+    """The range and persistent entries give the plain entry's bits, report
+    the largest and the total trips, and count the samples finished on entry
+    too (reference hawk/emit/cuda.py:373-380)."""
+    n = 100_003
+    t_final, x, v = _inputs(n, seed=29)
+    g = rng(31)
+    mask = g.uniform(size=n) < 0.1
+    got, counted, (most, total) = _run_auto(finishing, gpu, t_final, x, v, mask, word, entry, chunk)
+    ox, ov, ot, om = x.copy(), v.copy(), np.zeros(n), mask.copy()
+    trips = np.zeros(n, dtype=np.int32)
+    newly = O.osc_launch(word, DT, t_final, ox, ov, ot, om, trips=trips)
+    for key, ref in (("x", ox), ("v", ov), ("t", ot), ("terminated", om)):
+        assert got[key].tobytes() == ref.tobytes(), key
+    assert counted == newly + int(mask.sum())
+    assert (most, total) == (int(trips.max()), int(trips.sum()))
+
+
+@pytest.mark.gpu
+def test_the_persistent_entry_over_two_to_the_22_samples(finishing, gpu):
+    """2^22 samples of 1 to 256 steps each, run whole in one launch of the
+    persistent grid: the oracle's bits, every sample finished and counted."""
+    n = 1 << 22
+    g = np.random.default_rng(37)
+    t_final = DT * g.integers(1, 257, n).astype(float)
+    x, v = g.uniform(-1.0, 1.0, n), g.uniform(-1.0, 1.0, n)
+    got, counted, (most, total) = _run_auto(finishing, gpu, t_final, x, v, np.zeros(n, dtype=bool), 256,
+                                            "persist", 8)
+    ox, ov, ot, om = x.copy(), v.copy(), np.zeros(n), np.zeros(n, dtype=bool)
+    O.osc_launch(256, DT, t_final, ox, ov, ot, om)
+    assert counted == n and got["terminated"].all()
+    for key, ref in (("x", ox), ("v", ov), ("t", ot)):
+        assert got[key].tobytes() == ref.tobytes(), key
+    steps = np.rint(t_final / DT).astype(np.int64)
+    assert (most, total) == (int(steps.max()), int(steps.sum()))
