@@ -321,6 +321,9 @@ def _program_of(kernel) -> Program:
     finish (a derived kernel reads the mask through its guard and never
     finishes, reference ``tests/test_finish_own_sample.py:111-120``)."""
     if isinstance(kernel, Kernel):
+        step = getattr(kernel, "step", None)
+        if step is not None and step.name == kernel.name:
+            kernel = step                  # a default automatic kernel: its single step
         program = kernel.program
     elif isinstance(kernel, Program):
         program = kernel

@@ -185,7 +185,7 @@ CHAIN_MEMBERS = (unit_circle, decay, accumulate, scale_vec)
 OSC_DT = 0.125
 
 
-@kernel
+@kernel(steps=1)
 def osc_finish(dt: Param, t_final: Scalar, terminated: Terminated,
                x: Mutable[Scalar], v: Mutable[Scalar], t: Mutable[Scalar]):
     v_start = v
@@ -202,7 +202,7 @@ def stop_only(t: Scalar, t_final: Param, terminated: Terminated):
     terminated = t >= t_final
 
 
-@kernel
+@kernel(steps=1)
 def smooth_finish(x: Scalar, terminated: Terminated, y: Mutable[Scalar]):
     y = x * x + 1.0
     terminated = x > 2.0
@@ -212,9 +212,16 @@ def smooth_finish(x: Scalar, terminated: Terminated, y: Mutable[Scalar]):
 osc_finish_x8 = _trace.steps(osc_finish, 8)
 #: The oscillator taking the launch's word of steps, with its fast entries.
 osc_finish_xauto = _trace.steps(osc_finish, "auto")
+
+
+@kernel
+def decay_until(rate: Param, floor: Param, terminated: Terminated, y: Mutable[Scalar]):
+    """A finishing kernel built with no ``steps=``: its automatic kernel, under its own name."""
+    y = y * rate
+    terminated = y < floor
 smooth_finish_vjp = Kernel("smooth_finish_vjp", diff.vjp(smooth_finish, wrt=("x",)))
 FINISHING = {k.name: k for k in (osc_finish, osc_finish_x8, osc_finish_xauto, stop_only, smooth_finish,
-                                 smooth_finish_vjp)}
+                                 smooth_finish_vjp, decay_until)}
 
 
 #: Every kernel above, by name.

@@ -817,6 +817,7 @@ def steps(kernel: Kernel, K) -> Kernel:
     steps taken (reference ``hawk/trace/steps.py:27-44``)."""
     if not isinstance(kernel, Kernel):
         raise HawkError("hawk.steps(kernel, K) takes a traced kernel")
+    kernel = default_step(kernel)
     name = kernel.name
     auto = K == "auto"
     if not auto and (isinstance(K, bool) or not isinstance(K, int) or K < 1):
@@ -873,10 +874,52 @@ def steps(kernel: Kernel, K) -> Kernel:
     return stepped
 
 
-def kernel(fn=None, *, name: str | None = None):
-    """``@hawk.kernel``: trace a per-sample function into a :class:`Kernel`."""
+def admits_auto(kernel: Kernel) -> bool:
+    """Whether ``kernel`` is a single step that ``hawk.steps(kernel, "auto")``
+    admits (reference ``hawk/trace/steps.py:119-132``): it finishes its own
+    sample once, commits at least one Mutable plane and nothing else, and
+    declares no ``fused_steps`` plane."""
+    sinks = list(kernel.sinks)
+    finishes = [s for s in sinks if isinstance(s, Finish)]
+    if len(finishes) != 1 or finishes[0].steps != 1:
+        return False
+    commits = [s for s in sinks if s is not finishes[0]]
+    if not commits or not all(isinstance(s, Assign) and s.role == "mutable" for s in commits):
+        return False
+    return ir.FUSED_STEPS_PLANE not in kernel.decls
+
+
+def default_step(kernel: Kernel) -> Kernel:
+    """The single step a default automatic kernel stands for (its ``.step``,
+    under the same name), else ``kernel`` (reference ``hawk/trace/steps.py:101-109``)."""
+    step = getattr(kernel, "step", None)
+    return step if step is not None and step.name == kernel.name else kernel
+
+
+def kernel(fn=None, *, name: str | None = None, steps=None):
+    """``@hawk.kernel``: trace a per-sample function into a :class:`Kernel`.
+
+    A kernel that finishes its own sample and commits only Mutable planes is
+    built, with no ``steps=``, as its automatic kernel under its own name (its
+    trip count read at launch, ``.step`` the single step; reference
+    ``hawk/trace/steps.py:39-44``); ``steps=1`` keeps the single step and
+    ``steps=K`` is ``hawk.steps(kernel, K)``.  A step whose loop
+    :func:`steps` refuses (an inner loop over the carried state) stays a
+    single step."""
     def wrap(f, scope):
-        return Kernel(name or f.__name__, trace(f, scope))
+        k = Kernel(name or f.__name__, trace(f, scope))
+        if steps == 1:
+            return k
+        if steps is not None:
+            return globals()["steps"](k, steps)
+        if not admits_auto(k):
+            return k
+        try:
+            auto = globals()["steps"](k, "auto")
+        except HawkError:
+            return k                  # a step the loop cannot carry stays a single step
+        auto.name = k.name
+        return auto
     caller = inspect.currentframe().f_back
     scope = dict(caller.f_locals) if caller is not None else None
     if fn is not None:

@@ -360,6 +360,23 @@ def test_the_automatic_program_runs_the_word_of_trips(word):
     assert np.array_equal(trips, np.clip(np.minimum(word, np.rint(t_final / DT)), 0, None))
 
 
+def test_a_finishing_kernel_is_its_automatic_kernel_by_default():
+    import hawk_amd as hawk
+    from hawk_amd import examples as E
+    k = E.decay_until
+    assert k.name == "decay_until" and k.sinks[-1].steps == "auto" and k.step.name == "decay_until"
+    assert ("lookup", "fused_steps") in k.arg_spec
+    assert hawk.steps(k, 4).name == "decay_until_x4" and hawk.steps(k, 4).step is k.step
+    assert E.osc_finish.sinks[-1].steps == 1                     # steps=1 keeps the single step
+    assert E.stop_only.sinks[-1].steps == 1                      # commits no plane: not admitted
+
+    @hawk.kernel(steps=3)
+    def three(terminated: Terminated, y: Mutable[Scalar]):
+        y = y * 0.5
+        terminated = y < 0.1
+    assert three.name == "three_x3" and three.sinks[-1].steps == 3
+
+
 # -- on the GPU -------------------------------------------------------------------
 
 @pytest.fixture(scope="module")
@@ -532,3 +549,23 @@ def test_the_persistent_entry_over_two_to_the_22_samples(finishing, gpu):
         assert got[key].tobytes() == ref.tobytes(), key
     steps = np.rint(t_final / DT).astype(np.int64)
     assert (most, total) == (int(steps.max()), int(steps.sum()))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("word", [None, 5])
+def test_a_default_automatic_kernel_runs_one_step_unless_told(finishing, gpu, word):
+    """``decay_until`` (no ``steps=``) runs one step a launch by default and
+    the word's steps when given: y * rate each step, in NumPy's order."""
+    import hawk_amd as hawk
+    k = hawk.load(finishing, "decay_until")
+    n = 3001
+    y0 = rng(43).uniform(0.5, 2.0, n)
+    y, mask = _dev(y0, gpu), _dev(np.zeros(n, dtype=bool), gpu)
+    hawk.run(k, rate=0.75, floor=0.3, terminated=mask, y=y, **({} if word is None else {"steps": word}))
+    want, done = y0.copy(), np.zeros(n, dtype=bool)
+    for _ in range(1 if word is None else word):
+        live = ~done
+        want = np.where(live, want * 0.75, want)
+        done = done | (live & (want < 0.3))
+    assert y.cpu().numpy().tobytes() == want.tobytes()
+    assert np.array_equal(mask.cpu().numpy(), done) and int(k.finished.item()) == int(done.sum())
