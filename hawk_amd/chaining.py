@@ -57,6 +57,10 @@ def chain(*kernels, name: str) -> Chain:
     for k in members:
         if not isinstance(k, Kernel):
             raise HawkError(f"chain: {k!r} is not a traced kernel")
+        if any(d.role == "terminated" for d in k.decls.values()):
+            raise HawkError(f"chain: member {k.name!r} declares a Terminated mask (a guard, or a finish of its "
+                            "own sample); a chain of guarded members is not in this build -- chain the step's "
+                            "members first, then finish in one kernel")
     program, outputs = bind(members)
     return Chain(name, program, members, outputs)
 

@@ -377,6 +377,14 @@ def test_a_finishing_kernel_is_its_automatic_kernel_by_default():
     assert three.name == "three_x3" and three.sinks[-1].steps == 3
 
 
+def test_a_chain_of_a_guarded_member_refuses():
+    import hawk_amd as hawk
+    from hawk_amd import examples as E
+    from hawk_amd.ir import HawkError
+    with pytest.raises(HawkError, match="'osc_finish' declares a Terminated mask"):
+        hawk.chain(E.osc_finish, E.scale, name="c")
+
+
 # -- on the GPU -------------------------------------------------------------------
 
 @pytest.fixture(scope="module")
