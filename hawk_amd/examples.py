@@ -215,13 +215,24 @@ osc_finish_xauto = _trace.steps(osc_finish, "auto")
 
 
 @kernel
+def spin(c: Param, s: Param, limit: Scalar, terminated: Terminated, p: Mutable[Vector[2]], n: Mutable[Scalar]):
+    """A rotation of a 2-vector per step until the step count reaches ``limit``:
+    an automatic kernel carrying a vector and a scalar."""
+    x = p[0]
+    y = p[1]
+    p = vec(c * x - s * y, s * x + c * y)
+    n = n + 1.0
+    terminated = n >= limit
+
+
+@kernel
 def decay_until(rate: Param, floor: Param, terminated: Terminated, y: Mutable[Scalar]):
     """A finishing kernel built with no ``steps=``: its automatic kernel, under its own name."""
     y = y * rate
     terminated = y < floor
 smooth_finish_vjp = Kernel("smooth_finish_vjp", diff.vjp(smooth_finish, wrt=("x",)))
 FINISHING = {k.name: k for k in (osc_finish, osc_finish_x8, osc_finish_xauto, stop_only, smooth_finish,
-                                 smooth_finish_vjp, decay_until)}
+                                 smooth_finish_vjp, decay_until, spin)}
 
 
 #: Every kernel above, by name.

@@ -577,3 +577,33 @@ def test_a_default_automatic_kernel_runs_one_step_unless_told(finishing, gpu, wo
         done = done | (live & (want < 0.3))
     assert y.cpu().numpy().tobytes() == want.tobytes()
     assert np.array_equal(mask.cpu().numpy(), done) and int(k.finished.item()) == int(done.sum())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("entry", ["plain", "range", "persist"])
+def test_a_vector_carry_steps_to_numpy_on_every_entry(finishing, gpu, entry):
+    """``spin`` carries a 2-vector and a scalar: each entry, 100 steps a
+    launch, against NumPy's operation order bit for bit, with the reports."""
+    import hawk_amd as hawk
+    k = hawk.load(finishing, "spin")
+    n = 20_011
+    g = rng(47)
+    p0 = g.uniform(-1.0, 1.0, (2, n))
+    limit = g.integers(1, 151, n).astype(float)
+    c, s = float(np.cos(0.3)), float(np.sin(0.3))
+    P, N, M = _dev(p0, gpu), _dev(np.zeros(n), gpu), _dev(np.zeros(n, dtype=bool), gpu)
+    hawk.run(k, c=c, s=s, limit=_dev(limit, gpu), terminated=M, p=P, n=N, steps=100, entry=entry)
+    x, y, cnt, done = p0[0].copy(), p0[1].copy(), np.zeros(n), np.zeros(n, dtype=bool)
+    trips = np.zeros(n, dtype=np.int64)
+    for _ in range(100):
+        live = ~done
+        x, y = np.where(live, c * x - s * y, x), np.where(live, s * x + c * y, y)
+        cnt = np.where(live, cnt + 1.0, cnt)
+        trips += live
+        done = done | (live & (cnt >= limit))
+    got = P.cpu().numpy()
+    assert got[0].tobytes() == x.tobytes() and got[1].tobytes() == y.tobytes()
+    assert N.cpu().numpy().tobytes() == cnt.tobytes() and np.array_equal(M.cpu().numpy(), done)
+    assert int(k.finished.item()) == int(done.sum())
+    if entry != "plain":
+        assert (int(k.steps_max.item()), int(k.steps_sum.item())) == (int(trips.max()), int(trips.sum()))
