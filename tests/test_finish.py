@@ -607,3 +607,28 @@ def test_a_vector_carry_steps_to_numpy_on_every_entry(finishing, gpu, entry):
     assert int(k.finished.item()) == int(done.sum())
     if entry != "plain":
         assert (int(k.steps_max.item()), int(k.steps_sum.item())) == (int(trips.max()), int(trips.sum()))
+
+
+@pytest.mark.gpu
+def test_the_runtime_refuses_steps_and_entries_it_cannot_run(finishing, gpu):
+    import hawk_amd as hawk
+    from hawk_amd.ir import HawkError
+    n = 1000
+    t_final, x, v = _inputs(n, seed=53)
+
+    def planes():
+        return {"t_final": _dev(t_final, gpu), "x": _dev(x, gpu), "v": _dev(v, gpu),
+                "t": _dev(np.zeros(n), gpu), "terminated": _dev(np.zeros(n, dtype=bool), gpu)}
+    single, auto = hawk.load(finishing, "osc_finish"), hawk.load(finishing, "osc_finish_xauto")
+    with pytest.raises(HawkError, match="steps= sets the trip count"):
+        hawk.run(single, dt=DT, steps=3, **planes())
+    with pytest.raises(HawkError, match="fast entries are built for"):
+        hawk.run(single, dt=DT, entry="persist", **planes())
+    with pytest.raises(HawkError, match="entry= is 'plain', 'range' or 'persist'"):
+        hawk.run(auto, dt=DT, entry="fast", **planes())
+    with pytest.raises(HawkError, match="chunk= is an int"):
+        hawk.run(auto, dt=DT, entry="persist", chunk=0, **planes())
+    with pytest.raises(HawkError, match="steps= is an int"):
+        hawk.run(auto, dt=DT, steps=2.5, **planes())
+    with pytest.raises(HawkError, match="not planes it declares"):
+        hawk.run(auto, dt=DT, fused_steps=_dev(np.ones(1, dtype=np.int32), gpu), **planes())
