@@ -71,7 +71,7 @@ def _stage_bytes(plan, mode: str) -> int:
         count = 1
         for e in info["shape"]:
             count *= e
-        total += count * (4 if info["dtype"] == "i32" else size)
+        total += count * {"i32": 4, "u32": 4, "bool": 1}.get(info["dtype"], size)
     return total
 
 
