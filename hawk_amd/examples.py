@@ -90,6 +90,27 @@ def chain(x: Scalar, key: Index, y: Mutable[Scalar], total: Mutable[Scalar], bin
 
 
 @kernel
+def chain_steps(x: Scalar, e1: Mutable[Scalar], s2: Mutable[Scalar], h4: Mutable[Scalar], e7: Mutable[Scalar],
+                y: Mutable[Scalar]):
+    """The chain's per-sample stage with the outputs of its four
+    transcendentals stored beside ``y`` (the same operations, so ``y`` has
+    the fused chain's bits): each operation can then be checked on its own
+    inputs."""
+    t1 = exp(x)
+    t2 = sin(t1)
+    t3 = 1.5 * t2 + 0.25
+    t4 = tanh(t3)
+    t5 = sqrt(_abs(t4) + 1.0)
+    t6 = t5 * t5 - x
+    t7 = exp(-_abs(t6))
+    e1 = t1
+    s2 = t2
+    h4 = t4
+    e7 = t7
+    y = t7 * x + t4
+
+
+@kernel
 def ordered_total(x: Scalar, total: Mutable[Scalar]):
     total = _trace.sum(x, policy="ordered")
 
@@ -237,7 +258,7 @@ FINISHING = {k.name: k for k in (osc_finish, osc_finish_x8, osc_finish_xauto, st
 
 #: Every kernel above, by name.
 ALL = {k.name: k for k in (scale, energy, energy_vjp, energy_jvp, twobody, twobody_vjp, spd_solve,
-                            spd_solve_vjp, chain, ordered_total, ordered_add, sample_total, plain_total,
+                            spd_solve_vjp, chain, chain_steps, ordered_total, ordered_add, sample_total, plain_total,
                             twobody_vjp_mu, add_sq, add_sq_grad, chain_vjp, chain_jvp)}
 #: The float32 unit (built with mode="float32").
 FLOAT32 = {k.name: k for k in (mm16, mm16_vjp)}

@@ -68,6 +68,14 @@ def _torch():
     return torch
 
 
+def _on(stream: int):
+    """A context in which torch's own work (a counter's ``zero_()``, a cell's
+    ``fill_()``) is issued on ``stream``, the stream the next launch uses, so
+    the reset is ordered before that launch and after the previous one."""
+    torch = _torch()
+    return torch.cuda.stream(torch.cuda.ExternalStream(stream)) if stream else _nullcontext()
+
+
 class DeviceKernel:
     """One kernel of a built unit, loaded for the gfx950 target."""
 
@@ -122,7 +130,7 @@ class DeviceKernel:
             self._word_value = None
         value = max(-(1 << 31), min(steps, (1 << 31) - 1))
         if getattr(self, "_word_value", None) != value:
-            with torch.cuda.stream(torch.cuda.ExternalStream(stream)) if stream else _nullcontext():
+            with _on(stream):
                 held.fill_(value)
             self._word_value = value
         return held
@@ -135,37 +143,38 @@ class DeviceKernel:
             self._scratch[(key, device)] = t
         return t
 
-    def _fast(self, entry: str, bound: dict, n: int, chunk: int, device):
-        """``(DeviceEntry, ArgBlock)`` of the fast entry ``entry`` bound to
-        ``bound``, its report cells zeroed (the steps max and sum are then the
-        kernel's ``steps_max`` / ``steps_sum``)."""
+    def _fast(self, entry: str, bound: dict, n: int, chunk: int, device, stream: int, cells=None):
+        """``(DeviceEntry, ArgBlock, cells)`` of the fast entry ``entry`` bound
+        to ``bound``.  ``cells`` are its claim counter (the persistent entry's
+        only) and report cells (steps max, steps sum), zeroed here on
+        ``stream``; by default the kernel's own (then its ``steps_max`` /
+        ``steps_sum``), or those a :class:`Prepared` holds for itself."""
         torch = _torch()
         if entry not in FAST_SLOTS:
             raise HawkError(f"kernel {self.name!r}: entry= is 'plain', 'range' or 'persist', got {entry!r}")
         if not self.automatic:
             raise HawkError(f"kernel {self.name!r}: the fast entries are built for hawk.steps(k, 'auto') kernels")
+        if entry == "persist" and (isinstance(chunk, bool) or not isinstance(chunk, int) or not 1 <= chunk <= 1 << 20):
+            raise HawkError(f"kernel {self.name!r}: chunk= is an int in [1, 2^20], got {chunk!r}")
         names = self.sidecar["fast_entries"]
         fn = self.library.entry(names[entry])
         block = _core.ArgBlock(list(self.sidecar["descriptor"]) + list(FAST_SLOTS[entry]))
         self._bind(block, bound, n)
-        self.steps_max = self._held("steps_max", torch.int32, device)
-        self.steps_sum = self._held("steps_sum", torch.int64, device)
-        self.steps_max.zero_()
-        self.steps_sum.zero_()
-        extra = [self.steps_max, self.steps_sum]
-        if entry == "persist":
-            if isinstance(chunk, bool) or not isinstance(chunk, int) or not 1 <= chunk <= 1 << 20:
-                raise HawkError(f"kernel {self.name!r}: chunk= is an int in [1, 2^20], got {chunk!r}")
-            nxt = self._held("claims", torch.int32, device)
-            nxt.zero_()
-            extra = [nxt] + extra
+        if cells is None:
+            cells = (self._held("claims", torch.int32, device), self._held("steps_max", torch.int32, device),
+                     self._held("steps_sum", torch.int64, device))
+            self.steps_max, self.steps_sum = cells[1], cells[2]
+        with _on(stream):
+            for c in cells:
+                c.zero_()
+        extra = list(cells) if entry == "persist" else list(cells[1:])
         slot = len(self.arg_spec)
         for x in extra:
             block.bind(slot, x.data_ptr(), 1, 1, _contracts.DEVICE_ROCM, x.device.index or 0)
             slot += 1
         if entry == "persist":
             block.bind_value(slot, int(chunk))
-        return fn, block
+        return fn, block, cells
 
     def _bind(self, block, bound: dict, n: int) -> None:
         for slot, (role, name) in enumerate(self.arg_spec):
@@ -326,9 +335,12 @@ class DeviceKernel:
         out = bound[t["out"]]
         rows = -(-n // 32)
         if rows == 0:
-            out.zero_()
+            with _on(stream):
+                out.zero_()
             return
-        scratch = self._buffer(("rows", t["out"], rows), _core.rows_finish_scratch_bytes(rows), device, zero=False)
+        with _on(stream):
+            scratch = self._buffer(("rows", t["out"], rows), _core.rows_finish_scratch_bytes(rows), device,
+                                   zero=False)
         _core.rows_finish(bound[t["hi"]].data_ptr(), bound[t["comp"]].data_ptr(), rows, out.data_ptr(),
                           scratch.data_ptr(), stream)
 
@@ -390,11 +402,18 @@ class DeviceKernel:
 
     def _run(self, arrays: dict, base: int, count: int, n: int, stream: int, check: bool, steps=None,
              entry: str = "plain", chunk: int = PERSIST_CHUNK) -> None:
+        # every reset, scratch fill and status read is issued on the launch's stream
+        with _on(stream):
+            self._run_on(arrays, base, count, n, stream, check, steps, entry, chunk)
+
+    def _run_on(self, arrays: dict, base: int, count: int, n: int, stream: int, check: bool, steps,
+                entry: str, chunk: int) -> None:
         torch = _torch()
         device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
         bound, held = self._counter(dict(arrays), device)
         if held is not None:
-            held.zero_()                          # a count per run
+            with _on(stream):
+                held.zero_()                      # a count per run
         if self.automatic:
             bound[FUSED_STEPS_PLANE] = self._word(1 if steps is None else steps, device, stream)
         elif steps is not None:
@@ -403,7 +422,7 @@ class DeviceKernel:
         if entry != "plain":
             if count >= FAST_MAX:
                 raise HawkError(f"kernel {self.name!r}: the fast entries take fewer than 2^30 samples a launch")
-            fn, block = self._fast(entry, bound, n, chunk, device)
+            fn, block, _cells = self._fast(entry, bound, n, chunk, device, stream)
             self._launch_fast(entry, fn, block, base, count, n, stream)
             return
         for name, info in self.planes.items():
@@ -644,7 +663,17 @@ def run(kernel: DeviceKernel, *, base: int = 0, count: int | None = None, n_samp
 
 
 class Prepared:
-    """A kernel bound once to fixed planes (see :meth:`DeviceKernel.prepare`)."""
+    """A kernel bound once to fixed planes (see :meth:`DeviceKernel.prepare`).
+
+    Everything it resets runs on its own stream, ordered with its launches.
+    Through a fast entry it holds its own claim counter and report cells
+    (another launcher of the same kernel never shares them), and each call
+    starts them, and the runtime's finish counter, from zero: after a call,
+    ``steps_max`` / ``steps_sum`` are that call's trips and ``finished`` is
+    the batch's finished count (the fast entries count a sample finished on
+    entry too).  Through the plain entry the finish count adds up over calls
+    (each call counts only the samples it finishes), so it too holds the
+    batch's finished count after every call."""
 
     def __init__(self, kernel: DeviceKernel, arrays: dict, stream=None, steps=None, entry: str = "plain",
                  chunk: int = PERSIST_CHUNK):
@@ -657,10 +686,16 @@ class Prepared:
         elif hasattr(stream, "cuda_stream"):
             stream = stream.cuda_stream
         self.stream = int(stream)
+        with _on(self.stream):
+            self._setup(kernel, arrays, steps, entry, chunk)
+
+    def _setup(self, kernel, arrays: dict, steps, entry: str, chunk: int) -> None:
+        torch = _torch()
         device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
         bound, held = kernel._counter(dict(arrays), device)
+        self.held_counter = held
         if held is not None:
-            held.zero_()                          # counts every call from here on
+            held.zero_()
         self.finished = bound.get(FINISHED_PLANE)
         if kernel.automatic:
             w = 1 if steps is None else steps
@@ -674,10 +709,11 @@ class Prepared:
         if entry != "plain":
             if self.n >= FAST_MAX:
                 raise HawkError(f"kernel {kernel.name!r}: the fast entries take fewer than 2^30 samples a launch")
-            fn, block = kernel._fast(entry, bound, self.n, chunk, device)
-            claims = kernel._scratch.get(("claims", device)) if entry == "persist" else None
-            self.fast = (entry, fn, block, claims)
-            self.steps_max, self.steps_sum = kernel.steps_max, kernel.steps_sum
+            own = (torch.zeros(1, dtype=torch.int32, device=device), torch.zeros(1, dtype=torch.int32, device=device),
+                   torch.zeros(1, dtype=torch.int64, device=device))
+            fn, block, cells = kernel._fast(entry, bound, self.n, chunk, device, self.stream, cells=own)
+            self.fast = (entry, fn, block, cells)
+            self.steps_max, self.steps_sum = cells[1], cells[2]
         for name, info in kernel.planes.items():
             if info.get("cells_of"):
                 bound[name] = kernel._fold_scratch(name, bound, device)
@@ -753,11 +789,13 @@ class Prepared:
         k = self.kernel
         out = [("fold_clear", lambda fn=fn, args=args: fn(*args, self.stream)) for fn, args in self.before]
         if self.fast is not None:
-            entry, fn, block, claims = self.fast
+            entry, fn, block, cells = self.fast
+            resets = list(cells) + ([self.held_counter] if self.held_counter is not None else [])
 
             def fast_stage():
-                if claims is not None:
-                    claims.zero_()              # the persistent grid claims from sample 0 again
+                with _on(self.stream):          # claims from sample 0 again; this call's reports and count
+                    for c in resets:
+                        c.zero_()
                 k._launch_fast(entry, fn, block, 0, self.n, self.n, self.stream)
             out.append((f"{k.name}_{entry}", fast_stage))
             return out
@@ -776,8 +814,9 @@ class Prepared:
 
     def check(self) -> None:
         """Refuse, by name, a run whose ordered scatter met a bad key or whose
-        ordered fold met a cell named twice (synchronises)."""
+        ordered fold met a cell named twice (synchronises with its stream)."""
         for t, status, cells in self.statuses:
-            problem = _status_problem(self.kernel.name, t, status, cells)
+            with _on(self.stream):
+                problem = _status_problem(self.kernel.name, t, status, cells)
             if problem:
                 raise HawkError(problem)

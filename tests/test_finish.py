@@ -541,6 +541,70 @@ def test_the_fast_entries_are_the_plain_entrys_bits(finishing, gpu, entry, word,
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("entry", ["persist", "range"])
+def test_fast_entries_twice_on_a_side_stream(finishing, gpu, entry):
+    """Two runs in a row on a stream that is not torch's current one: the
+    claim counter, the report cells and the finish counter are reset on that
+    stream, so each run is the oracle's launch bit for bit (a reset left on
+    the current stream could let the grid claim from the last run's count)."""
+    import torch
+
+    import hawk_amd as hawk
+    k = hawk.load(finishing, "osc_finish_xauto")
+    n = 50_021
+    t_final, x, v = _inputs(n, seed=61)
+    mask = rng(62).uniform(size=n) < 0.05
+    planes = {"t_final": _dev(t_final, gpu), "x": _dev(x, gpu), "v": _dev(v, gpu),
+              "t": _dev(np.zeros(n), gpu), "terminated": _dev(mask, gpu)}
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    ox, ov, ot, om = x.copy(), v.copy(), np.zeros(n), mask.copy()
+    for word in (5, 9):
+        hawk.run(k, dt=DT, steps=word, entry=entry, chunk=4, stream=side, **planes)
+        side.synchronize()
+        trips = np.zeros(n, dtype=np.int32)
+        O.osc_launch(word, DT, t_final, ox, ov, ot, om, trips=trips)
+        got = {key: val.cpu().numpy() for key, val in planes.items()}
+        for key, ref in (("x", ox), ("v", ov), ("t", ot), ("terminated", om)):
+            assert got[key].tobytes() == ref.tobytes(), (word, key)
+        assert int(k.finished.item()) == int(om.sum())
+        assert (int(k.steps_max.item()), int(k.steps_sum.item())) == (int(trips.max()), int(trips.sum()))
+
+
+@pytest.mark.gpu
+def test_a_prepared_persistent_launcher_counts_each_call_afresh(finishing, gpu):
+    """A prepared persistent launcher on a side stream, called twice: each
+    call runs the oracle's launch bit for bit; after each, ``finished`` is the
+    batch's finished count (not the first call's count added again) and the
+    reports are that call's trips.  A second launcher of the same kernel holds
+    cells of its own."""
+    import torch
+
+    import hawk_amd as hawk
+    k = hawk.load(finishing, "osc_finish_xauto")
+    n = 40_009
+    t_final, x, v = _inputs(n, seed=67)
+    planes = {"t_final": _dev(t_final, gpu), "x": _dev(x, gpu), "v": _dev(v, gpu),
+              "t": _dev(np.zeros(n), gpu), "terminated": _dev(np.zeros(n, dtype=bool), gpu)}
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    launch = k.prepare(dt=DT, steps=6, entry="persist", chunk=2, stream=side, **planes)
+    other = k.prepare(dt=DT, steps=6, entry="persist", chunk=2, stream=side, **planes)
+    assert launch.steps_sum.data_ptr() != other.steps_sum.data_ptr()
+    ox, ov, ot, om = x.copy(), v.copy(), np.zeros(n), np.zeros(n, dtype=bool)
+    for call in range(2):
+        launch()
+        side.synchronize()
+        trips = np.zeros(n, dtype=np.int32)
+        O.osc_launch(6, DT, t_final, ox, ov, ot, om, trips=trips)
+        for key, ref in (("x", ox), ("v", ov), ("t", ot), ("terminated", om)):
+            assert planes[key].cpu().numpy().tobytes() == ref.tobytes(), (call, key)
+        assert int(launch.finished.item()) == int(om.sum()), call
+        assert (int(launch.steps_max.item()), int(launch.steps_sum.item())) == (int(trips.max()), int(trips.sum()))
+    assert om.sum() > 0 and not om.all()
+
+
+@pytest.mark.gpu
 def test_the_persistent_entry_over_two_to_the_22_samples(finishing, gpu):
     """2^22 samples of 1 to 256 steps each, run whole in one launch of the
     persistent grid: the oracle's bits, every sample finished and counted."""

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from conftest import golden
+from conftest import golden, within_contract
 
 
 def tree_sum(x: np.ndarray) -> float:
@@ -364,6 +364,54 @@ def test_chain_derivative_matches_central_differences():
     t4 = np.tanh(1.5 * np.sin(np.exp(x)) + 0.25)
     t6 = (np.sqrt(np.abs(t4) + 1.0) ** 2) - x
     assert (t6 > 0).any() and (t6 < 0).any() and (t4 > 0).any() and (t4 < 0).any()
+
+
+def test_chain_oracle_is_the_composition_of_its_operations():
+    """hko_chain is glibc's exp/sin/tanh and the IEEE operations in the order
+    the per-element bound differentiates (tests/chain_bound.py), bit for bit."""
+    import chain_bound as CB
+    g = np.random.default_rng(22)
+    x = np.concatenate([g.normal(size=20000), g.uniform(-6.0, 6.0, 5000), [0.0, -0.0, 1e-300, 700.0, -700.0]])
+    assert CB.parts(x)["y"].tobytes() == O.chain(x).tobytes()
+
+
+def _nudge(ulps):
+    """A planted mistake: move every value by ``ulps`` units in its last place."""
+    return lambda v: v + ulps * np.spacing(np.abs(v))
+
+
+def test_chain_bound_admits_the_allowances_and_catches_larger_mistakes():
+    """The per-element bound of the chain, pinned by mistakes planted in the
+    oracle's own composition (on the CPU): each transcendental moved by its
+    4-ulp allowance, all four at once, is inside the bound at every element;
+    a transcendental off by 64 ulps, a dropped term and a swapped operand are
+    caught.  (64 ulps are 16 allowances, caught only where one operation
+    dominates: the bound adds every operation's allowance, twice.)"""
+    import chain_bound as CB
+    g = np.random.default_rng(23)
+    x = np.concatenate([g.normal(size=200_000), g.uniform(-4.0, 3.0, 50_000)])
+    base = CB.parts(x)
+    bound = CB.element_bound(x, base)
+    assert np.all(bound > 0)
+    for name in ("t1", "t2", "t4", "t7"):
+        for u in (4, -4):
+            moved = CB.parts(x, {name: _nudge(u)})["y"]
+            assert CB.within(moved, base["y"], bound).all(), (name, u)
+    together = CB.parts(x, {n: _nudge(4) for n in ("t1", "t2", "t4", "t7")})["y"]
+    assert CB.within(together, base["y"], bound).all()
+    # mistakes the bound must see: 64 ulps in any one transcendental on at least 2 % of the samples
+    # (those where it dominates y's sensitivity), 1024 ulps on at least 90 %
+    for name in ("t1", "t2", "t4", "t7"):
+        for u, share in ((64, 0.02), (1024, 0.9)):
+            wrong = CB.parts(x, {name: _nudge(u)})["y"]
+            assert (~CB.within(wrong, base["y"], bound)).mean() > share, (name, u)
+    dropped = CB.parts(x, {"y": lambda v: v - base["t4"]})["y"]          # y = t7 x: the t4 term lost
+    assert (~CB.within(dropped, base["y"], bound)).mean() > 0.9
+    swapped = CB.parts(x, {"t7": lambda v: O.libm("exp", -base["t6"])})["y"]     # exp(-t6) for exp(-|t6|)
+    flagged = ~CB.within(swapped, base["y"], bound)
+    assert flagged[base["t6"] < -1e-3].all() and (base["t6"] < -1e-3).sum() > 10_000
+    # a plain 4-ulp bar on y would reject legitimate 4-ulp transcendentals where y cancels
+    assert (~within_contract(together, base["y"], rel=0.0)).any()
 
 
 def test_chain_vjp_gathers_the_bins_adjoint_at_the_key():
