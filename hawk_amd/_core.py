@@ -55,6 +55,8 @@ def _declare(lib) -> None:
         "hk_ordered_sum_scratch_bytes": (SZ, []),
         "hk_ordered_sum_f64": (I, [V, I64, V, V, V]),
         "hk_ordered_fold_f64": (I, [V, V, V, V]),
+        "hk_ordered_sum_noalloc_scratch_bytes": (SZ, []),
+        "hk_ordered_sum_f64_noalloc": (I, [V, I64, V, V]),
         "hk_scatter_chunks": (I, [I64, I64]),
         "hk_ordered_scatter_scratch_bytes": (SZ, [I64, I64]),
         "hk_ordered_scatter_f64": (I, [V, V, I64, V, I64, V, V, V]),
@@ -283,6 +285,13 @@ def ordered_sum_scratch_bytes() -> int:
 def ordered_sum(u: int, n: int, out: int, scratch: int, stream: int = 0) -> None:
     check(lib().hk_ordered_sum_f64(ctypes.c_void_p(u or None), int(n), ctypes.c_void_p(out),
                                    ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
+
+
+def ordered_sum_noalloc(u: int, n: int, out: int, stream: int = 0) -> None:
+    """The ordered sum on the library's static per-GPU scratch: no device
+    memory is allocated (for callers that cannot allocate)."""
+    check(lib().hk_ordered_sum_f64_noalloc(ctypes.c_void_p(u or None), int(n), ctypes.c_void_p(out),
+                                           ctypes.c_void_p(stream or None)))
 
 
 def scatter_chunks(n: int, cells: int) -> int:

@@ -14,6 +14,7 @@
 
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 namespace {
@@ -35,10 +36,14 @@ constexpr size_t kSumScratch = kLanesBytes + kGpBytes + 256;
 // Virtual lane l = blockIdx.x*256 + threadIdx.x adds u[l], u[l+65536], ... in
 // order from +0.0.  The loads of kSumUnroll rows are issued before their adds
 // so each lane keeps kSumUnroll loads in flight; the adds stay in row order.
+// The fold's ticket is cleared here, one launch ahead of the fold that takes
+// it, so a sum never depends on what an earlier call left in its scratch.
 __global__ __launch_bounds__(kLaneBlock) void hawk_sum_lanes(const double* __restrict__ u,
                                                               long long n,
-                                                              double* __restrict__ lanes) {
+                                                              double* __restrict__ lanes,
+                                                              unsigned* __restrict__ ticket) {
     const long long l = static_cast<long long>(blockIdx.x) * kLaneBlock + threadIdx.x;
+    if (l == 0) *ticket = 0u;
     double s = 0.0;
     long long r = l;
     constexpr long long kStep = kVirtualLanes;
@@ -995,6 +1000,52 @@ int bits_for(long long max_value) {
 
 }  // namespace
 
+// The scratch of hk_ordered_sum_f64_noalloc: the ordered sum's 65536 lane
+// partials, 64 group values and ticket, kSumScratch bytes (512 KiB + 768 B)
+// whatever the number of samples.  Each GPU the library runs on holds its own
+// copy until the process ends.  In host code `scratch` names a host-side
+// stand-in, never the device memory: launches take the per-device address
+// that scratch_of() obtains with hipGetSymbolAddress.
+static __device__ __align__(256) unsigned char scratch[kSumScratch];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the GPU that runs `stream` (the current
+// device for the null stream), looked up once per device with that device
+// current.
+int scratch_of(hipStream_t stream, void** out) {
+    int dev = 0;
+    hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return hawk_internal::set_hip_error("hk_ordered_sum_f64_noalloc: the stream's device", e);
+    if (dev < 0 || dev >= kMaxDevices)
+        return hawk_internal::set_error(HK_EVALUE, "hk_ordered_sum_f64_noalloc: device " + std::to_string(dev) +
+                                                       " is past the " + std::to_string(kMaxDevices) +
+                                                       " devices it keeps a scratch address for");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        int current = 0;
+        e = hipGetDevice(&current);
+        if (e != hipSuccess) return hawk_internal::set_hip_error("hk_ordered_sum_f64_noalloc: hipGetDevice", e);
+        if (current != dev && (e = hipSetDevice(dev)) != hipSuccess)
+            return hawk_internal::set_hip_error("hk_ordered_sum_f64_noalloc: hipSetDevice", e);
+        void* ptr = nullptr;
+        const hipError_t got = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (current != dev && (e = hipSetDevice(current)) != hipSuccess)
+            return hawk_internal::set_hip_error("hk_ordered_sum_f64_noalloc: hipSetDevice", e);
+        if (got != hipSuccess)
+            return hawk_internal::set_hip_error("hk_ordered_sum_f64_noalloc: hipGetSymbolAddress(scratch)", got);
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return HK_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 size_t hk_ordered_sum_scratch_bytes(void) { return kSumScratch; }
@@ -1014,12 +1065,26 @@ int hk_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch, v
     if (n < 0) return hawk_internal::set_error(HK_EVALUE, "hk_ordered_sum_f64: n must be >= 0");
     if ((n > 0 && !u) || !out || !scratch)
         return hawk_internal::set_error(HK_EVALUE, "hk_ordered_sum_f64: u, out and scratch are required");
-    auto* lanes = static_cast<double*>(scratch);
+    auto* base = static_cast<unsigned char*>(scratch);
+    auto* lanes = reinterpret_cast<double*>(base);
+    auto* ticket = reinterpret_cast<unsigned*>(base + kLanesBytes + kGpBytes);
     hipLaunchKernelGGL(hawk_sum_lanes, dim3(kVirtualLanes / kLaneBlock), dim3(kLaneBlock), 0,
-                       static_cast<hipStream_t>(stream), u, static_cast<long long>(n), lanes);
+                       static_cast<hipStream_t>(stream), u, static_cast<long long>(n), lanes, ticket);
     int rc = launch_error("hawk_sum_lanes launch");
     if (rc != HK_OK) return rc;
     return hk_ordered_fold_f64(lanes, out, scratch, stream);
+}
+
+size_t hk_ordered_sum_noalloc_scratch_bytes(void) { return kSumScratch; }
+
+int hk_ordered_sum_f64_noalloc(const double* u, int64_t n, double* out, void* stream) {
+    if (n < 0) return hawk_internal::set_error(HK_EVALUE, "hk_ordered_sum_f64_noalloc: n must be >= 0");
+    if ((n > 0 && !u) || !out)
+        return hawk_internal::set_error(HK_EVALUE, "hk_ordered_sum_f64_noalloc: u and out are required");
+    void* ptr = nullptr;
+    const int rc = scratch_of(static_cast<hipStream_t>(stream), &ptr);
+    if (rc != HK_OK) return rc;
+    return hk_ordered_sum_f64(u, n, out, ptr, stream);    // the same kernels, on the static scratch
 }
 
 size_t hk_keyed_ordered_sum_scratch_bytes(int64_t n, int64_t group) {

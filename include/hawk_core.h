@@ -162,6 +162,19 @@ size_t hk_ordered_sum_scratch_bytes(void);
 int hk_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch,
                        void* stream);
 
+/* hk_ordered_sum_f64 for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It has no counterpart in the reference.  It allocates nothing:
+ * its scratch is a static device array of hk_ordered_sum_noalloc_scratch_bytes()
+ * bytes (512 KiB + 768 B, whatever n is), one copy per GPU, held until the
+ * process ends; the caller passes only the input and the output.  Same
+ * kernels, same bits as hk_ordered_sum_f64.  Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU (on different streams,
+ * or from different threads without ordering) race; calls in order on one
+ * stream do not.  n < 0 is refused (HK_EVALUE). */
+size_t hk_ordered_sum_noalloc_scratch_bytes(void);
+int hk_ordered_sum_f64_noalloc(const double* u, int64_t n, double* out, void* stream);
+
 /* The same fold over 65536 lane partials already computed in `lanes`
  * (the second half of a fused ordered-sum stage). */
 int hk_ordered_fold_f64(const double* lanes, double* out, void* scratch,
