@@ -41,17 +41,28 @@ class Chain(Kernel):
         self.outputs = outputs
 
 
-def chain(*kernels, name: str) -> Chain:
-    """Run ``kernels`` in sequence as ONE kernel named ``name``.
+def _flatten(kernels) -> tuple:
+    """The members of a chain call: a chain given as a member contributes its
+    own members, so chaining is associative."""
+    flat = []
+    for k in kernels:
+        flat.extend(k.members if isinstance(k, Chain) else (k,))
+    return tuple(flat)
 
-    A member's input binds to the value an earlier member committed under
-    the same name; any other input is the chain's.  A name no later member
-    reads is an output, and a name several members update in turn keeps its
-    last value.  The values passed between members stay in the kernel: they
-    are neither inputs nor outputs of the chain.  A chain of chains is the
-    chain of their members.  The members must agree on their Grid (a chain
-    runs as one launch)."""
-    members = tuple(m for k in kernels for m in (k.members if isinstance(k, Chain) else (k,)))
+
+def chain(*kernels, name: str) -> Chain:
+    """ONE kernel named ``name`` that runs ``kernels`` one after another on
+    each lane.
+
+    Names connect the members: reading a name an earlier member committed
+    reads that member's value, reading any other name reads an input of the
+    chain.  The chain commits every name that no later member reads; a name
+    several members update in turn (each reading it first) ends with the
+    last update.  Values that pass from member to member never leave the
+    lane.  Members that are chains contribute their own members, and all
+    members must share one Grid (the chain is one launch).  Reference
+    ``hawk/trace/chain.py`` (the user entry)."""
+    members = _flatten(kernels)
     if not members:
         raise HawkError("chain: give at least one kernel")
     for k in members:
@@ -86,85 +97,149 @@ def _rebuilt(s, nodes: list):
     return dataclasses.replace(s, value=nodes[0])
 
 
+class _Timeline:
+    """What the members do with one name, in member order: every read (the
+    member, its leaf, and whether the leaf is indexed by a computed key) and
+    every commit (the member and its sink).  Within one member the reads come
+    before the commits, since a member reads its planes as they were when it
+    started."""
+
+    def __init__(self, name: str):
+        self.name = name
+        self.events: list = []                 # ("read", j, leaf, indexed) | ("commit", j, sink)
+
+    def commits(self) -> list:
+        return [e for e in self.events if e[0] == "commit"]
+
+    def last_commit(self) -> int | None:
+        c = self.commits()
+        return c[-1][1] if c else None
+
+    def read_after(self, j: int) -> bool:
+        return any(e[0] == "read" and e[1] > j for e in self.events)
+
+    def check(self, names: list) -> None:
+        """Refuse what makes the name ambiguous, in the reference's words
+        (``hawk/ir/chain.py:67-127``; these texts are the interface)."""
+        committed = None                       # the (member, sink) a read binds to, once a member commits
+        as_input = None                        # (member, role, ttype) of the first read before any commit
+        for e in self.events:
+            if e[0] == "read":
+                _, j, leaf, indexed = e
+                role, ttype = leaf.literal[0], leaf.ttype
+                if committed is None:
+                    if as_input is None:
+                        as_input = (names[j], role, ttype)
+                    elif as_input[1:] != (role, ttype):
+                        raise HawkError(f"chain: {as_input[0]!r} reads {self.name!r} as (role={as_input[1]!r}, "
+                                        f"{as_input[2]!r}) but {names[j]!r} reads it as (role={role!r}, "
+                                        f"{ttype!r}); rename one")
+                    continue
+                writer, sink = committed
+                if ttype != sink.value.ttype:
+                    raise HawkError(f"chain: {names[writer]!r} commits {self.name!r} as {sink.value.ttype!r} but "
+                                    f"{names[j]!r} reads it as {ttype!r}; one name is one value")
+                lane_local = (role in BOUND_LEAF_ROLES and not indexed and isinstance(sink, Assign)
+                              and sink.role in BOUND_SINK_ROLES)
+                if not lane_local:
+                    raise HawkError(f"chain: {names[j]!r} reads {self.name!r}, which {names[writer]!r} commits, "
+                                    f"at another sample (or {names[writer]!r} commits it off its own lane); an "
+                                    "intermediate is the lane's own value: end the chain at that name and read "
+                                    "the plane in a second chain")
+                continue
+            _, j, sink = e
+            if committed is not None and not any(r[0] == "read" and r[1] == j for r in self.events):
+                raise HawkError(f"chain: {names[committed[0]]!r} and {names[j]!r} both commit {self.name!r} and "
+                                f"{names[j]!r} does not read it first; the order would decide the value")
+            if as_input is not None and as_input[1] != "mutable" and committed is None:
+                raise HawkError(f"chain: {as_input[0]!r} reads {self.name!r} as an input (role={as_input[1]!r}) "
+                                f"but {names[j]!r} commits it; rename one")
+            committed = (j, sink)
+
+
+def _timelines(members) -> dict:
+    """Every name the members touch, with its :class:`_Timeline`."""
+    lines: dict = {}
+    for j, k in enumerate(members):
+        order = ir.topo([n for s in k.sinks for n in _sink_nodes(s)])
+        indexed = {n.operands[0].uid for n in order if n.kind == "gather"}
+        for leaf in (n for n in order if n.kind == "leaf"):
+            name = leaf.literal[1]
+            lines.setdefault(name, _Timeline(name)).events.append(("read", j, leaf, leaf.uid in indexed))
+        for s in k.sinks:
+            lines.setdefault(s.name, _Timeline(s.name)).events.append(("commit", j, s))
+    return lines
+
+
 def bind(members, keep=()) -> tuple:
-    """``(program, outputs)``: ``members`` composed in order (see the module
-    text); ``keep`` names intermediates to commit as outputs too.  Refuses,
-    naming both members and the name (reference ``hawk/ir/chain.py:67-127``):
-    a name read with two types or two input roles; a second writer of a name
-    that does not read it first; members whose Grids disagree; an
-    intermediate read at another sample, or committed off its own lane (a
-    sum or a scatter)."""
+    """``(program, outputs)`` of ``members`` composed in order; ``keep`` names
+    values that later members read but the caller wants committed too.
+
+    Two passes.  The first records, per name, what each member does with it
+    (:class:`_Timeline`) and refuses an ambiguous name: two types or input
+    roles for one name, a second commit by a member that does not read the
+    name first, or a committed value read off its lane (at a computed index,
+    or committed by a sum or a scatter).  The second composes: walking the
+    members in order with an environment from each committed name to its
+    current value, every read of a committed name becomes that value and
+    every read of an input becomes one shared leaf.  Reference
+    ``hawk/ir/chain.py:67-127`` (the binding rules)."""
     first = members[0]
     for k in members[1:]:
         if _grid_of(k) != _grid_of(first):
             raise HawkError(f"chain: members {first.name!r} and {k.name!r} disagree on grid "
                             f"({_grid_of(first)!r} vs {_grid_of(k)!r}); a chain runs as one launch")
-    latest: dict = {}           # name -> (member, rebuilt sink)
-    inputs: dict = {}           # name -> (member, role, ttype) of an unbound read
-    canon: dict = {}            # name -> the one leaf node every member's read of an input becomes
-    reads: list = []            # per member: the names it reads
+    names = [k.name for k in members]
+    lines = _timelines(members)
+    for line in lines.values():
+        line.check(names)
+
+    env: dict = {}              # committed name -> its current sink (operands already composed)
+    shared: dict = {}           # input name -> the one leaf all its reads become (one value, one derivative)
     for k in members:
         roots = [n for s in k.sinks for n in _sink_nodes(s)]
-        order = ir.topo(roots)
-        leaves = [n for n in order if n.kind == "leaf"]
-        gathered = {n.operands[0].uid for n in order if n.kind == "gather"}
-        reads.append({lf.literal[1] for lf in leaves})
-        mapping = {}
-        for lf in leaves:
-            role, name = lf.literal
-            if name not in latest:
-                held = inputs.setdefault(name, (k.name, role, lf.ttype))
-                if held[1:] != (role, lf.ttype):
-                    raise HawkError(f"chain: {held[0]!r} reads {name!r} as (role={held[1]!r}, {held[2]!r}) but "
-                                    f"{k.name!r} reads it as (role={role!r}, {lf.ttype!r}); rename one")
-                one = canon.setdefault(name, lf)      # one input, one value (and one derivative)
-                if one is not lf:
-                    mapping[lf.uid] = one
-                continue
-            writer, sink = latest[name]
-            if lf.ttype != sink.value.ttype:
-                raise HawkError(f"chain: {writer!r} commits {name!r} as {sink.value.ttype!r} but {k.name!r} reads "
-                                f"it as {lf.ttype!r}; one name is one value")
-            if role not in BOUND_LEAF_ROLES or lf.uid in gathered or not isinstance(sink, Assign) \
-                    or sink.role not in BOUND_SINK_ROLES:
-                raise HawkError(f"chain: {k.name!r} reads {name!r}, which {writer!r} commits, at another sample "
-                                f"(or {writer!r} commits it off its own lane); an intermediate is the lane's own "
-                                "value: end the chain at that name and read the plane in a second chain")
-            mapping[lf.uid] = sink.value
-        for s in k.sinks:
-            if s.name in latest and s.name not in reads[-1]:
-                raise HawkError(f"chain: {latest[s.name][0]!r} and {k.name!r} both commit {s.name!r} and "
-                                f"{k.name!r} does not read it first; the order would decide the value")
-            if s.name in inputs and inputs[s.name][1] != "mutable":
-                held = inputs[s.name]
-                raise HawkError(f"chain: {held[0]!r} reads {s.name!r} as an input (role={held[1]!r}) but "
-                                f"{k.name!r} commits it; rename one")
-        new = ir.substitute(roots, mapping) if mapping else roots
-        at = 0
+        swap = {}
+        for leaf in ir.leaves_of(roots):
+            name = leaf.literal[1]
+            if name in env:
+                swap[leaf.uid] = env[name].value
+            elif shared.setdefault(name, leaf) is not leaf:
+                swap[leaf.uid] = shared[name]
+        composed = ir.substitute(roots, swap) if swap else roots
+        pos = 0
         for s in k.sinks:
             width = len(_sink_nodes(s))
-            latest[s.name] = (k.name, _rebuilt(s, new[at:at + width]))
-            at += width
-    writer_at = {}
-    for j, k in enumerate(members):
-        for s in k.sinks:
-            writer_at[s.name] = j
-    outputs = tuple(n for n, j in writer_at.items() if n in keep or not any(n in r for r in reads[j + 1:]))
-    consumed = set(writer_at) - set(outputs) - set(inputs)
-    decls: dict = {}
-    tables: dict = {}
-    for j, k in enumerate(members):            # an output's declaration is its last writer's
-        for n, decl in k.decls.items():
-            if n not in consumed and (n not in decls or writer_at.get(n) == j):
-                decls[n] = decl
-        for n, axes in k.program.tables.items():
-            if n not in consumed:
-                tables.setdefault(n, axes)
-    sinks = [latest[n][1] for n in outputs]
-    if not sinks:
+            env[s.name] = _rebuilt(s, composed[pos:pos + width])
+            pos += width
+
+    committed_in_order = list(dict.fromkeys(s.name for k in members for s in k.sinks))
+    outputs = tuple(name for name in committed_in_order
+                    if name in keep or not lines[name].read_after(lines[name].last_commit()))
+    if not outputs:
         raise HawkError("chain: the members commit nothing a later member does not read")
+    # Planes of the composed kernel: the inputs (declared by their first
+    # reader) and the outputs (declared by their last committer); a value
+    # passed between members has no plane.
+    decls: dict = {}
+    for j, k in enumerate(members):
+        for name, decl in k.decls.items():
+            line = lines.get(name)
+            last = line.last_commit() if line is not None else None
+            if name in outputs:
+                if last == j:
+                    decls[name] = decl
+                else:
+                    decls.setdefault(name, decl)
+            elif name in shared:
+                decls.setdefault(name, decl)
+    tables = {}
+    for k in members:
+        for name, axes in k.program.tables.items():
+            if name in decls:
+                tables.setdefault(name, axes)
+    sinks = [env[name] for name in outputs]
     program = Program(decls, sinks, first.program.grid, tables)
-    used = {n.literal[1] for n in ir.leaves_of(ir.sink_roots(sinks))} | {s.name for s in sinks}
+    used = {n.literal[1] for n in ir.leaves_of(ir.sink_roots(sinks))} | set(outputs)
     program.decls = {n: d for n, d in decls.items() if n in used}
     return program, outputs
 
