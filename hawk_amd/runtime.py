@@ -97,6 +97,9 @@ class DeviceKernel:
             self.library = _core.DeviceLibrary(code)
             self.entry = self.library.entry(sidecar["entry"])
             self.block = _core.ArgBlock(sidecar["descriptor"])
+        # What each slot of self.block holds: ("p", ptr, samples, device) or
+        # ("v", value); None before the first bind.
+        self._held_slots: list = [None] * len(self.arg_spec)
         self._scratch: dict = {}
         self._lock = threading.Lock()
         self.scatter_chunks = None
@@ -390,15 +393,48 @@ class DeviceKernel:
 
     # -- launch --------------------------------------------------------------
     def bind_all(self, arrays: dict, n: int) -> None:
-        """Bind every slot of the per-sample stage (validated planes)."""
+        """Bind the per-sample stage's slots to validated ``arrays``, crossing
+        the C-ABI only for what changed since the last bind: a slot whose
+        length, device or by-value number changed is bound on its own; every
+        slot whose pointer alone moved is swapped in ONE bulk rebind.  So a
+        run over the planes of the last run adds no crossing to its launch,
+        and a run over moved planes adds one (reference ``hawk/runtime.py:330-345``,
+        the stable-binding and rebind arms of its launch-crossing contract)."""
+        moved_slots, moved_ptrs = [], []
         for slot, (role, name) in enumerate(self.arg_spec):
             kind = self.block.descriptor[slot]
             x = arrays[name]
+            held = self._held_slots[slot]
             if kind in ("f64", "f32"):
-                self.block.bind_value(slot, float(x))
+                value = float(x)
+                if held != ("v", value):
+                    self.block.bind_value(slot, value)
+                    self._held_slots[slot] = ("v", value)
                 continue
-            self.block.bind(slot, x.data_ptr(), _bound_length(role, x, n), 1, _contracts.DEVICE_ROCM,
-                            x.device.index or 0)
+            ptr, samples, device = x.data_ptr(), _bound_length(role, x, n), x.device.index or 0
+            if held is not None and held[0] == "p" and held[2:] == (samples, device):
+                if held[1] != ptr:
+                    moved_slots.append(slot)
+                    moved_ptrs.append(ptr)
+                continue
+            self.block.bind(slot, ptr, samples, 1, _contracts.DEVICE_ROCM, device)
+            self._held_slots[slot] = ("p", ptr, samples, device)
+        if moved_slots:
+            self.rebind(moved_slots, moved_ptrs)
+
+    def rebind(self, slots, ptrs) -> None:
+        """The bulk pointer swap: every (slot, pointer) pair in ONE crossing
+        (``hk_rebind``; reference ``hawk/runtime.py:330-345``).  Unchecked by
+        design: it only moves slots a validated bind already shaped, so each
+        slot keeps the length and device it was bound with.  A by-value slot
+        is refused (by the C-ABI, naming the slot)."""
+        slots = [int(s) for s in slots]
+        ptrs = [int(p) for p in ptrs]
+        self.block.rebind(slots, ptrs)
+        for slot, ptr in zip(slots, ptrs):
+            held = self._held_slots[slot]
+            if held is not None and held[0] == "p":
+                self._held_slots[slot] = ("p", ptr, held[2], held[3])
 
     def _run(self, arrays: dict, base: int, count: int, n: int, stream: int, check: bool, steps=None,
              entry: str = "plain", chunk: int = PERSIST_CHUNK) -> None:

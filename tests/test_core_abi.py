@@ -69,6 +69,23 @@ def test_argblock_bind_and_rebind_refusals():
     ab.rebind([0, 1], [0x5000, 0x6000])
 
 
+@pytest.mark.parametrize("slots", [1, 2, 5, 17])
+def test_a_bulk_rebind_is_one_crossing_whatever_the_slot_count(slots):
+    """The rebind arm of the reference's launch-crossing card
+    (tests/cards/CARD_LAUNCH_CROSSINGS.md): swapping every pointer slot costs
+    ONE crossing, not one per slot; binding them one by one costs one each."""
+    ab = _core.ArgBlock(["handle"] * slots)
+    for s in range(slots):
+        ab.bind(s, 0x1000 * (s + 1), 64)
+    before = _core.crossings()
+    ab.rebind(list(range(slots)), [0x9000 + 0x100 * s for s in range(slots)])
+    assert _core.crossings() - before - 1 == 1          # the closing crossings() is its own crossing
+    before = _core.crossings()
+    for s in range(slots):
+        ab.bind(s, 0x7000 + s, 64)
+    assert _core.crossings() - before - 1 == slots
+
+
 def test_rtc_refuses_another_architecture():
     from hawk_amd import HawkError
     with pytest.raises(HawkError, match="pinned to gfx950"):
