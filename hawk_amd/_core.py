@@ -62,6 +62,10 @@ def _declare(lib) -> None:
         "hk_ordered_scatter_f64": (I, [V, V, I64, V, I64, V, V, V]),
         "hk_rows_finish_scratch_bytes": (SZ, [I64]),
         "hk_rows_finish_f64": (I, [V, V, I64, V, V, V]),
+        "hk_band_rows_finish_scratch_bytes": (SZ, [I64]),
+        "hk_band_rows_finish_f64": (I, [V, V, I64, V, V, V]),
+        "hk_band_ordered_sum_scratch_bytes": (SZ, []),
+        "hk_band_ordered_sum_f64": (I, [V, I64, V, V, V]),
         "hk_keyed_ordered_sum_scratch_bytes": (SZ, [I64, I64]),
         "hk_keyed_ordered_sum_f64": (I, [V, I64, I64, V, V, V]),
         "hk_mm16_f32": (I, [ctypes.POINTER(V), I, ctypes.POINTER(V), I, ctypes.POINTER(ctypes.c_int32), I64, V]),
@@ -360,3 +364,21 @@ def rows_finish(hi: int, comp: int, rows: int, out: int, scratch: int, stream: i
     """Fold ``rows`` compensated row pairs into the cell ``out`` (canonical ordered tree)."""
     check(lib().hk_rows_finish_f64(ctypes.c_void_p(hi), ctypes.c_void_p(comp), int(rows), ctypes.c_void_p(out),
                                    ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
+
+
+def band_rows_finish_scratch_bytes(rows: int) -> int:
+    return int(lib().hk_band_rows_finish_scratch_bytes(int(rows)))
+
+
+def band_rows_finish(hi: int, lo: int, rows: int, out: int, scratch: int, stream: int = 0) -> None:
+    check(lib().hk_band_rows_finish_f64(ctypes.c_void_p(hi), ctypes.c_void_p(lo), int(rows), ctypes.c_void_p(out),
+                                        ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
+
+
+def band_ordered_sum_scratch_bytes() -> int:
+    return int(lib().hk_band_ordered_sum_scratch_bytes())
+
+
+def band_ordered_sum(u: int, n: int, out: int, scratch: int, stream: int = 0) -> None:
+    check(lib().hk_band_ordered_sum_f64(ctypes.c_void_p(u or None), int(n), ctypes.c_void_p(out),
+                                        ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))

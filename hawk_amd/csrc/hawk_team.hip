@@ -96,6 +96,110 @@ __global__ __launch_bounds__(256) void hawk_sum_fold(const double* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
+// Banded reductions (the banded scalar mode; reference hawk/emit/wrapper.py:140
+// `BANDED`, hawk/emit/team.py:26-49 and :225-245): every partial is a band, a
+// normalised double-double (h, l) with |l| <= ulp(h)/2, folded in the same
+// fixed order as the float64 stages, and the stored cell is the final band's
+// h.  The adds are those of Hida, Li and Bailey's QD library: a term joins a
+// band by TwoSum of the leading parts plus a quick renormalisation, two bands
+// join by TwoSum of the leading and of the low parts and two
+// renormalisations.  Knuth's TwoSum is exact in either operand order, so both
+// adds are symmetric.  A non-finite leading sum drops the low part, so Inf and
+// NaN follow IEEE through h.
+// ---------------------------------------------------------------------------
+struct Band {
+    double h, l;
+};
+
+__device__ __forceinline__ Band band_two(double a, double b) {
+    const double s = a + b;
+    const double bb = s - a;
+    return Band{s, (a - (s - bb)) + (b - bb)};
+}
+
+__device__ __forceinline__ Band band_quick(double a, double b) {
+    const double s = a + b;
+    return Band{s, b - (s - a)};
+}
+
+__device__ __forceinline__ Band band_add_term(Band a, double x) {
+    const Band s = band_two(a.h, x);
+    if (!((s.h - s.h) == 0.0)) return Band{s.h, 0.0};
+    return band_quick(s.h, s.l + a.l);
+}
+
+__device__ __forceinline__ Band band_add(Band a, Band b) {
+    Band s = band_two(a.h, b.h);
+    if (!((s.h - s.h) == 0.0)) return Band{s.h, 0.0};
+    const Band t = band_two(a.l, b.l);
+    s = band_quick(s.h, s.l + t.h);
+    return band_quick(s.h, s.l + t.l);
+}
+
+constexpr size_t kBandLanesBytes = sizeof(Band) * kVirtualLanes;
+constexpr size_t kBandGpBytes = sizeof(Band) * kGroups;
+constexpr size_t kBandSumScratch = kBandLanesBytes + kBandGpBytes + 256;
+
+// Virtual lane l adds u[l], u[l+65536], ... as terms of its band, in order
+// from (+0, +0); kSumUnroll loads in flight before their adds.  Clears the
+// fold's ticket one launch ahead of the fold.
+__global__ __launch_bounds__(kLaneBlock) void hawk_band_sum_lanes(const double* __restrict__ u, long long n,
+                                                                   Band* __restrict__ lanes,
+                                                                   unsigned* __restrict__ ticket) {
+    const long long l = static_cast<long long>(blockIdx.x) * kLaneBlock + threadIdx.x;
+    if (l == 0) *ticket = 0u;
+    Band s{0.0, 0.0};
+    long long r = l;
+    constexpr long long kStep = kVirtualLanes;
+    for (; r + (kSumUnroll - 1) * kStep < n; r += kSumUnroll * kStep) {
+        double a[kSumUnroll];
+#pragma unroll
+        for (int k = 0; k < kSumUnroll; ++k) a[k] = __builtin_nontemporal_load(u + r + k * kStep);
+#pragma unroll
+        for (int k = 0; k < kSumUnroll; ++k) s = band_add_term(s, a[k]);
+    }
+    for (; r < n; r += kStep) s = band_add_term(s, u[r]);
+    lanes[l] = s;
+}
+
+// Group g's 1024 lane bands by the halving tree into gp[g]; the last group
+// to finish folds the 64 group bands by the same tree and stores h.
+__global__ __launch_bounds__(256) void hawk_band_sum_fold(const Band* __restrict__ lanes, Band* __restrict__ gp,
+                                                          unsigned* __restrict__ ticket, double* __restrict__ out) {
+    __shared__ Band sh[kFoldLanes];
+    __shared__ unsigned last;
+    const int g = blockIdx.x;
+    const int t = threadIdx.x;
+    for (int i = t; i < kFoldLanes; i += 256) sh[i] = lanes[g * kFoldLanes + i];
+    __syncthreads();
+    for (int w = kFoldLanes / 2; w > 0; w >>= 1) {
+        for (int i = t; i < w; i += 256) sh[i] = band_add(sh[i], sh[i + w]);
+        __syncthreads();
+    }
+    if (t == 0) {
+        gp[g] = sh[0];
+        __threadfence();
+        last = atomicAdd(ticket, 1u);
+    }
+    __syncthreads();
+    if (last != kGroups - 1) return;
+    __threadfence();
+    if (t < kGroups) {
+        sh[t].h = __builtin_nontemporal_load(&gp[t].h);
+        sh[t].l = __builtin_nontemporal_load(&gp[t].l);
+    }
+    __syncthreads();
+    for (int w = kGroups / 2; w > 0; w >>= 1) {
+        if (t < w) sh[t] = band_add(sh[t], sh[t + w]);
+        __syncthreads();
+    }
+    if (t == 0) {
+        *out = sh[0].h;
+        *ticket = 0u;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // The default-policy sample sum's finish.  The per-sample stage leaves one
 // compensated (hi, comp) pair per row of 32 samples; the cell is those rows
 // folded in the canonical ordered tree of reference hawk/_cells.py:71-119:
@@ -203,6 +307,67 @@ __global__ __launch_bounds__(256) void hawk_rows_levels(double* __restrict__ buf
         m = pairs + (m & 1);
     }
     if (threadIdx.x == 0) *out = finite_bits(vh[0]) ? vh[0] + vc[0] : vh[0];
+}
+
+// The banded rows' finish: the canonical tree above (leaves of 4096 rows over
+// 256 slots, the in-leaf halving tree, the leaves pairwise level by level)
+// with every add a band add; the cell is the final band's h.  Row r of the
+// stage is the band (hi[r], lo[r]).
+__global__ __launch_bounds__(kRowSlots) void hawk_band_rows_leaves(const double* __restrict__ hi,
+                                                                   const double* __restrict__ lo, long long rows,
+                                                                   double* __restrict__ leaf_h,
+                                                                   double* __restrict__ leaf_l) {
+    __shared__ Band sh[kRowSlots];
+    const int s = threadIdx.x;
+    const long long first = static_cast<long long>(blockIdx.x) * kRowLeaf;
+    const long long rest = rows - first;
+    const int cnt = rest < kRowLeaf ? static_cast<int>(rest) : static_cast<int>(kRowLeaf);
+    const int live = cnt < kRowSlots ? cnt : kRowSlots;
+    if (s < live) {
+        Band b{hi[first + s], lo[first + s]};
+        for (int k = 1; k < kRowTerms; ++k) {
+            const int m = live < cnt - k * kRowSlots ? live : cnt - k * kRowSlots;
+            if (m <= 0 || s >= m) break;
+            b = band_add(b, Band{hi[first + k * kRowSlots + s], lo[first + k * kRowSlots + s]});
+        }
+        sh[s] = b;
+    }
+    __syncthreads();
+    for (int off = kRowSlots / 2; off > 0; off >>= 1) {
+        const int lim = live > off ? (off < live - off ? off : live - off) : 0;
+        if (s < lim) sh[s] = band_add(sh[s], sh[s + off]);
+        __syncthreads();
+    }
+    if (s == 0) {
+        leaf_h[blockIdx.x] = sh[0].h;
+        leaf_l[blockIdx.x] = sh[0].l;
+    }
+}
+
+__global__ __launch_bounds__(256) void hawk_band_rows_levels(double* __restrict__ buf, long long leaves,
+                                                             double* __restrict__ out) {
+    double* vh = buf;
+    double* vl = buf + leaves;
+    double* nh = buf + 2 * leaves;
+    double* nl = buf + 3 * leaves;
+    long long m = leaves;
+    while (m > 1) {
+        const long long pairs = m / 2;
+        for (long long p = threadIdx.x; p < pairs; p += 256) {
+            const Band b = band_add(Band{vh[2 * p], vl[2 * p]}, Band{vh[2 * p + 1], vl[2 * p + 1]});
+            nh[p] = b.h;
+            nl[p] = b.l;
+        }
+        if ((m & 1) && threadIdx.x == 0) {
+            nh[pairs] = vh[m - 1];
+            nl[pairs] = vl[m - 1];
+        }
+        __syncthreads();
+        double* th = vh; vh = nh; nh = th;
+        double* tl = vl; vl = nl; nl = tl;
+        m = pairs + (m & 1);
+    }
+    if (threadIdx.x == 0) *out = vh[0];
 }
 
 // hawk.sum(x, over=<trailing lane axes>) under the default policy: key k's
@@ -1178,6 +1343,44 @@ int hk_rows_finish_f64(const double* hi, const double* comp, int64_t rows, doubl
     if (rc != HK_OK) return rc;
     hipLaunchKernelGGL(hawk_rows_levels, dim3(1), dim3(256), 0, s, buf, leaves, out);
     return launch_error("hawk_rows_levels launch");
+}
+
+size_t hk_band_rows_finish_scratch_bytes(int64_t rows) { return hk_rows_finish_scratch_bytes(rows); }
+
+int hk_band_rows_finish_f64(const double* hi, const double* lo, int64_t rows, double* out, void* scratch,
+                            void* stream) {
+    if (rows < 1) return hawk_internal::set_error(HK_EVALUE, "hk_band_rows_finish_f64: rows must be >= 1");
+    if (!hi || !lo || !out || !scratch)
+        return hawk_internal::set_error(HK_EVALUE, "hk_band_rows_finish_f64: hi, lo, out and scratch are required");
+    const long long leaves = (rows + kRowLeaf - 1) / kRowLeaf;
+    if (leaves > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_band_rows_finish_f64: too many rows");
+    auto* buf = static_cast<double*>(scratch);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(hawk_band_rows_leaves, dim3(static_cast<unsigned>(leaves)), dim3(kRowSlots), 0, s, hi, lo,
+                       static_cast<long long>(rows), buf, buf + leaves);
+    int rc = launch_error("hawk_band_rows_leaves launch");
+    if (rc != HK_OK) return rc;
+    hipLaunchKernelGGL(hawk_band_rows_levels, dim3(1), dim3(256), 0, s, buf, leaves, out);
+    return launch_error("hawk_band_rows_levels launch");
+}
+
+size_t hk_band_ordered_sum_scratch_bytes(void) { return kBandSumScratch; }
+
+int hk_band_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch, void* stream) {
+    if (n < 0) return hawk_internal::set_error(HK_EVALUE, "hk_band_ordered_sum_f64: n must be >= 0");
+    if ((n > 0 && !u) || !out || !scratch)
+        return hawk_internal::set_error(HK_EVALUE, "hk_band_ordered_sum_f64: u, out and scratch are required");
+    auto* base = static_cast<unsigned char*>(scratch);
+    auto* lanes = reinterpret_cast<Band*>(base);
+    auto* gp = reinterpret_cast<Band*>(base + kBandLanesBytes);
+    auto* ticket = reinterpret_cast<unsigned*>(base + kBandLanesBytes + kBandGpBytes);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(hawk_band_sum_lanes, dim3(kVirtualLanes / kLaneBlock), dim3(kLaneBlock), 0, s, u,
+                       static_cast<long long>(n), lanes, ticket);
+    int rc = launch_error("hawk_band_sum_lanes launch");
+    if (rc != HK_OK) return rc;
+    hipLaunchKernelGGL(hawk_band_sum_fold, dim3(kGroups), dim3(256), 0, s, lanes, gp, ticket, out);
+    return launch_error("hawk_band_sum_fold launch");
 }
 
 int hk_scatter_chunks(int64_t n, int64_t cells) {

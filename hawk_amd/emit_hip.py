@@ -101,6 +101,7 @@ class Stage:
     block: int | None = None        # the launch block a fused fold needs (its keys never cross a block)
     guard: str | None = None        # the mask plane whose set samples the stage skips
     finish: tuple | None = None     # (mask plane, counter plane, condition node) of `terminated = cond`
+    banded: bool = False            # the row sums fold double-double bands (the banded scalar mode)
 
 
 class _Scope:
@@ -713,7 +714,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
                 unpack.append(f"const unsigned long long {var}_n = {var}_m.samples;   // cells")
     params += ["long long base", "long long count", "long long nSamples"]
     out = [
-        f"// hawk gfx950 stage '{stage.name}' (generated; mode {mode}).",
+        f"// hawk gfx950 stage '{stage.name}' (generated; mode {'banded' if stage.banded else mode}).",
         f"typedef {real} Real;",
         "struct GRefMirror { Real* data_; unsigned long long samples_, compStride_, sampleStride_; "
         "int deviceType_, deviceId_; };",
@@ -726,7 +727,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     if "hk_tanh(" in "\n".join(body + stores):
         out += _TANH_HELPER.splitlines()
     if row_terms:
-        out += _ROW_SUM_HELPERS.splitlines()
+        out += (_BAND_ROW_SUM_HELPERS if stage.banded else _ROW_SUM_HELPERS).splitlines()
     if folds:
         out += _FOLD_HELPERS.splitlines()
     if stage.finish is not None:
@@ -767,7 +768,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += ["        if (hk_live) {"] + ["    " + line for line in stores] + ["        }"]
         for k, (term, hi, comp) in enumerate(row_terms):
             out += [f"        {{ double hk_rh = hk_live ? static_cast<double>({term}) : 0.0, hk_rc = 0.0;",
-                    "          hk_row_sum(hk_rh, hk_rc);",
+                    f"          {'hk_band_row_sum' if stage.banded else 'hk_row_sum'}(hk_rh, hk_rc);",
                     "          if ((threadIdx.x & 31) == 0 && hk_live) {",
                     "              const long long hk_r = (base + hk_flat) >> 5;",
                     f"              {hi}[hk_r] = hk_rh;",
@@ -1245,6 +1246,43 @@ __device__ __forceinline__ void hk_row_sum(double& h, double& c) {
 """
 
 
+#: The row sum of the banded mode: each lane's term is the double-double
+#: band (term, +0), and the 32 lanes of a row combine by the pairs of the
+#: default sum's row with the band add of Hida, Li and Bailey's QD library
+#: (TwoSum of the leading parts, TwoSum of the low parts, two quick
+#: renormalisations); a non-finite leading sum drops the low part.  Knuth's
+#: TwoSum is exact in either operand order, so the add is symmetric and every
+#: lane of the half ends with the row's band.  The row stores (hi, lo).
+_BAND_ROW_SUM_HELPERS = """
+__device__ __forceinline__ bool hk_finite(double x) { return (x - x) == 0.0; }
+__device__ __forceinline__ void hk_band_add(double& h, double& l, double h2, double l2) {
+    double s = h + h2;
+    const double sb = s - h;
+    double e = (h - (s - sb)) + (h2 - sb);
+    if (!hk_finite(s)) { h = s; l = 0.0; return; }
+    const double t = l + l2;
+    const double tb = t - l;
+    const double f = (l - (t - tb)) + (l2 - tb);
+    e = e + t;
+    double q = s + e;
+    e = e - (q - s);
+    s = q;
+    e = e + f;
+    q = s + e;
+    l = e - (q - s);
+    h = q;
+}
+__device__ __forceinline__ void hk_band_row_sum(double& h, double& l) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) {
+        const double h2 = __shfl_xor(h, off, 64);
+        const double l2 = __shfl_xor(l, off, 64);
+        hk_band_add(h, l, h2, l2);
+    }
+}
+"""
+
+
 _FP_CALL = re.compile(r"\b(?:hk_)?(?:exp|sin|cos|tanh|sqrt|log|fabs)\(")
 _FP_BINARY = re.compile(r"(?<=[\w\)\]]) [-+*/] (?=[\w\(])")
 _PLANE_ACCESS = re.compile(r"hk_p_\w+(?:\[|_m\.|_cs\b)")
@@ -1344,6 +1382,24 @@ def _carry_repeats(program: Program) -> Program:
     return Program(program.decls, sinks, program.grid, program.tables)
 
 
+def _refuse_unbanded(program: Program, name: str) -> None:
+    """The banded mode builds the sample sums (the default policy and
+    ``policy="ordered"``) with band accumulators; a reduction it has no band
+    stage for is refused by name, as the reference refuses the reductions its
+    banded build cannot certify (``hawk/emit/wrapper.py:158-196``)."""
+    for s in program.sinks:
+        what = None
+        if isinstance(s, SampleSum) and s.group is not None:
+            what = f"hawk.sum({s.name}, over=...)"
+        elif isinstance(s, AccumWrite):
+            what = f"hawk.scatter({s.name})"
+        elif isinstance(s, OrderedFold):
+            what = f"the ordered gradient fold into {s.name}"
+        if what is not None:
+            raise HawkError(f"{name}: {what} has no banded stage on the hip target; build this kernel in float64 "
+                            "(the banded mode folds hawk.sum over the samples, default or ordered policy)")
+
+
 def plan_kernel(program: Program, name: str, mode: str = "float64", block: int = 256,
                 per_thread: int = 1, nontemporal: bool = False, reuse_carries: bool = True,
                 fuse_folds: bool = True) -> Plan:
@@ -1353,8 +1409,11 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
     ``Plan.algorithmic_ops`` still counts the program as traced.  With
     ``fuse_folds``, an ordered fold whose keys fit a block (:func:`fold_block`)
     is done by the stage in LDS; otherwise the stage logs and a team stage folds."""
-    if mode not in ("float64", "float32"):
-        raise HawkError(f"mode={mode!r}: the hip target builds 'float64' or 'float32'")
+    if mode not in ("float64", "float32", "banded"):
+        raise HawkError(f"mode={mode!r}: the hip target builds 'float64', 'float32' or 'banded'")
+    banded = mode == "banded"
+    if banded:
+        _refuse_unbanded(program, name)
     if reuse_carries:
         reused = _carry_repeats(program)
         if reused is not program:
@@ -1364,6 +1423,8 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                                fuse_folds=fuse_folds)
             plan.algorithmic_ops = traced.algorithmic_ops
             return plan
+    if banded:
+        mode = "float64"            # the banded mode's values are float64; its reductions fold bands
     products = _mm16_products(program) if mode == "float32" else None
     if products is not None:
         ins, prods = products
@@ -1397,8 +1458,8 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
             if mode != "float64":
                 raise HawkError(f"hawk.sum(policy={s.policy!r}) on the hip target is built in float64")
             row_sums.append((s.name, s.value))
-            team.append({"op": "row_sum", "hi": f"hk_rows_{s.name}", "comp": f"hk_rows_{s.name}_comp",
-                         "out": s.name})
+            team.append({"op": "band_rows" if banded else "row_sum", "hi": f"hk_rows_{s.name}",
+                         "comp": f"hk_rows_{s.name}_comp", "out": s.name})
         elif isinstance(s, SampleSum):
             if mode != "float64":
                 raise HawkError(f"hawk.sum(policy={s.policy!r}) on the hip target is built in float64")
@@ -1409,7 +1470,7 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                 src = f"hk_sum_{s.name}"
                 extra.append((src, s.value))
             if s.group is None:
-                team.append({"op": "ordered_sum", "u": src, "out": s.name})
+                team.append({"op": "band_ordered_sum" if banded else "ordered_sum", "u": src, "out": s.name})
             elif s.policy == "ordered":
                 team.append({"op": "keyed_sum", "u": src, "out": s.name, "group": s.group})
             else:                                   # the default policy over some axes
@@ -1436,6 +1497,7 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
     stage = source = None
     if has_stage:
         stage = _stage_planes(program, name, mode, extra, row_sums, key_writes, fused)
+        stage.banded = banded
         source = render_stage(stage, mode, block, per_thread, nontemporal=nontemporal)
     planes = {}
     if stage is not None:
@@ -1456,7 +1518,8 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
         for key in ("out", "target"):
             pname = t.get(key)
             if pname and isinstance(pname, str):
-                planes[pname] = {"role": "cell" if t["op"] in ("ordered_sum", "row_sum", "keyed_sum", "keyed_comp")
+                planes[pname] = {"role": "cell" if t["op"] in ("ordered_sum", "row_sum", "keyed_sum", "keyed_comp",
+                                                              "band_rows", "band_ordered_sum")
                                  else "accum_out",
                                  "shape": [], "dtype": "f64"}
                 if t["op"] in ("keyed_sum", "keyed_comp"):

@@ -262,3 +262,17 @@ ALL = {k.name: k for k in (scale, energy, energy_vjp, energy_jvp, twobody, twobo
                             twobody_vjp_mu, add_sq, add_sq_grad, chain_vjp, chain_jvp)}
 #: The float32 unit (built with mode="float32").
 FLOAT32 = {k.name: k for k in (mm16, mm16_vjp)}
+
+
+@kernel
+def band_total(x: Scalar, s: Mutable[Scalar], s_sq: Mutable[Scalar], s_ord: Mutable[Scalar]):
+    """The sample sums of the banded mode (the reference's banded row sum
+    kernel, tests/test_banded_sum.py, plus the ordered sum): the default
+    policy over x and over the computed x*x, and the ordered policy over x."""
+    s = _trace.sum(x)
+    s_sq = _trace.sum(x * x)
+    s_ord = _trace.sum(x, policy="ordered")
+
+
+#: The banded unit (built with mode="banded").
+BANDED = {k.name: k for k in (band_total,)}

@@ -334,17 +334,19 @@ class DeviceKernel:
         return held
 
     def _row_sum(self, t: dict, bound: dict, n: int, device, stream: int) -> None:
-        """Fold the stage's row partials into the cell (a run of no samples sums to 0)."""
+        """Fold the stage's row partials into the cell (a run of no samples sums to 0):
+        compensated (hi, comp) rows, or band rows (hi, lo) in the banded mode."""
         out = bound[t["out"]]
         rows = -(-n // 32)
         if rows == 0:
             with _on(stream):
                 out.zero_()
             return
+        band = t["op"] == "band_rows"
         with _on(stream):
-            scratch = self._buffer(("rows", t["out"], rows), _core.rows_finish_scratch_bytes(rows), device,
-                                   zero=False)
-        _core.rows_finish(bound[t["hi"]].data_ptr(), bound[t["comp"]].data_ptr(), rows, out.data_ptr(),
+            nbytes = (_core.band_rows_finish_scratch_bytes if band else _core.rows_finish_scratch_bytes)(rows)
+            scratch = self._buffer(("rows", t["out"], rows), nbytes, device, zero=False)
+        (_core.band_rows_finish if band else _core.rows_finish)(bound[t["hi"]].data_ptr(), bound[t["comp"]].data_ptr(), rows, out.data_ptr(),
                           scratch.data_ptr(), stream)
 
     def _term_plane(self, name: str, n: int, device):
@@ -498,8 +500,13 @@ class DeviceKernel:
             elif t["op"] == "mm16":
                 _core.mm16([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
                            t["products"], n, stream)
-            elif t["op"] == "row_sum":
+            elif t["op"] in ("row_sum", "band_rows"):
                 self._row_sum(t, bound, n, device, stream)
+            elif t["op"] == "band_ordered_sum":
+                u = bound[t["u"]]
+                scratch = self._buffer(("band_sum", t["out"]), _core.band_ordered_sum_scratch_bytes(), device,
+                                       zero=False)
+                _core.band_ordered_sum(u.data_ptr(), n, bound[t["out"]].data_ptr(), scratch.data_ptr(), stream)
             elif t["op"] == "keyed_sum":
                 scratch = self._buffer(("keyed", t["out"], n), _core.keyed_ordered_sum_scratch_bytes(n, t["group"]),
                                        device)
@@ -796,8 +803,13 @@ class Prepared:
                 args = ([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
                         t["products"], self.n)
                 self.steps.append((_core.mm16, args))
-            elif t["op"] == "row_sum":
+            elif t["op"] in ("row_sum", "band_rows"):
                 self.steps.append((kernel._row_sum, (t, bound, self.n, device)))
+            elif t["op"] == "band_ordered_sum":
+                scratch = kernel._buffer(("band_sum", t["out"]), _core.band_ordered_sum_scratch_bytes(), device,
+                                         zero=False)
+                args = (bound[t["u"]].data_ptr(), self.n, bound[t["out"]].data_ptr(), scratch.data_ptr())
+                self.steps.append((_core.band_ordered_sum, args))
             elif t["op"] == "keyed_sum":
                 scratch = kernel._buffer(("keyed", t["out"], self.n),
                                          _core.keyed_ordered_sum_scratch_bytes(self.n, t["group"]), device)
@@ -840,7 +852,8 @@ class Prepared:
                 k.entry.run(self.block, 0, self.n, self.n, threads=k.launch_shape["block"],
                             per_thread=k.launch_shape["per_thread"], stream=self.stream)
             out.append((k.name, stage))
-        labels = {_core.ordered_sum: "ordered_sum", _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16",
+        labels = {_core.ordered_sum: "ordered_sum", _core.band_ordered_sum: "band_ordered_sum",
+                  _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16",
                   _core.keyed_ordered_sum: "keyed_sum", _core.keyed_log_fold: "ordered_fold",
                   _core.keyed_sample_sum: "keyed_comp"}
         for fn, args in self.steps:

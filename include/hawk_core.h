@@ -216,6 +216,29 @@ size_t hk_rows_finish_scratch_bytes(int64_t rows);
 int hk_rows_finish_f64(const double* hi, const double* comp, int64_t rows,
                        double* out, void* scratch, void* stream);
 
+/* Banded reductions: the sample sums of the banded scalar mode (reference
+ * `hawk/emit/wrapper.py:140` BANDED and its row sum `:542-665`,
+ * `hawk/emit/team.py:26-49` and `:225-245`: band partials folded in the
+ * float64 stages' fixed order, one value stored at the end).  A band is a
+ * normalised double-double (h, l), |l| <= ulp(h)/2, added with the QD
+ * library's TwoSum-based adds; the stored cell is the final band's h.
+ *
+ * hk_band_rows_finish_f64: `rows` band rows (hi, lo) (one per 32 samples,
+ * written by a banded per-sample stage) folded in the default sum's
+ * canonical tree (leaves of 256 slots x 16 rows, the halving tree, pairwise
+ * levels), every add a band add.  Scratch: hk_band_rows_finish_scratch_bytes(rows).
+ *
+ * hk_band_ordered_sum_f64: the fixed-tree ordered sum with band
+ * accumulators (65536 virtual lanes add their rows as terms, the group and
+ * final trees add bands).  Scratch: hk_band_ordered_sum_scratch_bytes(), no
+ * initial contents needed. */
+size_t hk_band_rows_finish_scratch_bytes(int64_t rows);
+int hk_band_rows_finish_f64(const double* hi, const double* lo, int64_t rows,
+                            double* out, void* scratch, void* stream);
+size_t hk_band_ordered_sum_scratch_bytes(void);
+int hk_band_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch,
+                            void* stream);
+
 /* The keyed ordered scatter of reference `hawk/emit/team.py:322-460`
  * (`_scatter_zero`, `_scatter_chunks`, `_scatter_cells`) with the chunk rule
  * of `hawk/_lane_bind.py:111-114`: chunks = clamp(n / max(cells, 1), 1, 256),

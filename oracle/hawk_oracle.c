@@ -276,6 +276,138 @@ HKO_EXPORT void hko_keyed_sample_sum(const double* u, int64_t n, int64_t group, 
     for (int64_t k = 0; k * group < n; ++k) out[k] = hko_sample_sum(u + k * group, group);
 }
 
+/* ---- banded reductions: double-double band accumulators ----------------
+ * The banded scalar mode's reductions (reference hawk/emit/wrapper.py:140
+ * `BANDED`, hawk/emit/team.py:26-49 and :225-245: every partial is a
+ * compensated band accumulator, folded in the float64 stages' fixed order,
+ * one value stored at the end).  Here a band is a normalised double-double
+ * (h, l), |l| <= ulp(h)/2, with the additions of Hida, Li and Bailey's QD
+ * library (TwoSum, quick-two-sum; the "accurate" double-double add); a
+ * non-finite leading sum drops the low part.  The stored cell is h. */
+typedef struct { double h, l; } hko_band;
+
+static hko_band band_two(double a, double b) {          /* TwoSum: s + e == a + b exactly */
+    const double s = a + b, bb = s - a;
+    const hko_band r = {s, (a - (s - bb)) + (b - bb)};
+    return r;
+}
+
+static hko_band band_quick(double a, double b) {        /* quick-two-sum, |a| >= |b| (or a == 0) */
+    const double s = a + b;
+    const hko_band r = {s, b - (s - a)};
+    return r;
+}
+
+static hko_band band_add_term(hko_band a, double x) {
+    hko_band s = band_two(a.h, x);
+    if (!fin(s.h)) { s.l = 0.0; return s; }
+    return band_quick(s.h, s.l + a.l);
+}
+
+static hko_band band_add(hko_band a, hko_band b) {
+    hko_band s = band_two(a.h, b.h);
+    if (!fin(s.h)) { s.l = 0.0; return s; }
+    const hko_band t = band_two(a.l, b.l);
+    s = band_quick(s.h, s.l + t.h);
+    return band_quick(s.h, s.l + t.l);
+}
+
+/* Rows of 32 terms, each term the band (t, +0), combined by the pairs (l, l ^ 16), ..., (l, l ^ 1)
+ * of the default sum's row (the band add is symmetric, so every lane of the row ends with these bits). */
+HKO_EXPORT void hko_band_row_sums(const double* t, int64_t n, double* hi, double* lo) {
+    const int64_t rows = (n + 31) / 32;
+    for (int64_t r = 0; r < rows; ++r) {
+        hko_band v[32];
+        for (int l = 0; l < 32; ++l) {
+            v[l].h = r * 32 + l < n ? t[r * 32 + l] : 0.0;
+            v[l].l = 0.0;
+        }
+        for (int off = 16; off >= 1; off >>= 1)
+            for (int l = 0; l < off; ++l) v[l] = band_add(v[l], v[l + off]);
+        hi[r] = v[0].h;
+        lo[r] = v[0].l;
+    }
+}
+
+/* The canonical finish of the default sum (leaves of 256 slots x 16 rows, the in-leaf halving tree,
+ * pairwise levels over the leaves), every add a band add; the cell is the final band's h. */
+static hko_band band_leaf(const double* hi, const double* lo, int cnt) {
+    hko_band sh[256];
+    const int live = cnt < 256 ? cnt : 256;
+    for (int s = 0; s < live; ++s) {
+        sh[s].h = hi[s];
+        sh[s].l = lo[s];
+    }
+    for (int k = 1; k < 16; ++k) {
+        const int m = live < cnt - k * 256 ? live : cnt - k * 256;
+        if (m <= 0) break;
+        for (int s = 0; s < m; ++s) {
+            const hko_band row = {hi[k * 256 + s], lo[k * 256 + s]};
+            sh[s] = band_add(sh[s], row);
+        }
+    }
+    for (int off = 128; off > 0; off >>= 1) {
+        const int lim = live > off ? (off < live - off ? off : live - off) : 0;
+        for (int s = 0; s < lim; ++s) sh[s] = band_add(sh[s], sh[s + off]);
+    }
+    return sh[0];
+}
+
+HKO_EXPORT double hko_band_rows_finish(const double* hi, const double* lo, int64_t rows) {
+    if (rows <= 0) return 0.0;
+    const int64_t leaves = (rows + 4095) / 4096;
+    hko_band* v = (hko_band*)malloc(sizeof(hko_band) * (size_t)leaves);
+    for (int64_t j = 0; j < leaves; ++j) {
+        const int64_t rest = rows - j * 4096;
+        v[j] = band_leaf(hi + j * 4096, lo + j * 4096, (int)(rest < 4096 ? rest : 4096));
+    }
+    int64_t m = leaves;
+    while (m > 1) {
+        const int64_t pairs = m / 2;
+        for (int64_t p = 0; p < pairs; ++p) v[p] = band_add(v[2 * p], v[2 * p + 1]);
+        if (m & 1) v[pairs] = v[m - 1];
+        m = pairs + (m & 1);
+    }
+    const double out = v[0].h;
+    free(v);
+    return out;
+}
+
+HKO_EXPORT double hko_band_sample_sum(const double* t, int64_t n) {
+    const int64_t rows = (n + 31) / 32;
+    if (rows == 0) return 0.0;
+    double* hi = (double*)malloc(sizeof(double) * (size_t)rows);
+    double* lo = (double*)malloc(sizeof(double) * (size_t)rows);
+    hko_band_row_sums(t, n, hi, lo);
+    const double out = hko_band_rows_finish(hi, lo, rows);
+    free(hi);
+    free(lo);
+    return out;
+}
+
+/* The banded ordered sum: the ordered sum's fixed tree (65536 virtual lanes adding their rows in order,
+ * the halving tree over each group of 1024 lanes, then over the 64 groups) with band accumulators: a
+ * lane adds each row as a term, the trees add bands. */
+static hko_band band_group_part(const double* u, int64_t rows, int g) {
+    hko_band sh[HKO_W];
+    for (int t = 0; t < HKO_W; ++t) sh[t].h = sh[t].l = 0.0;
+    for (int64_t b = (int64_t)g * HKO_W; b < rows; b += HKO_V) {
+        const int64_t m = rows - b < HKO_W ? rows - b : HKO_W;
+        for (int64_t t = 0; t < m; ++t) sh[t] = band_add_term(sh[t], u[b + t]);
+    }
+    for (int w = HKO_W / 2; w > 0; w >>= 1)
+        for (int i = 0; i < w; ++i) sh[i] = band_add(sh[i], sh[i + w]);
+    return sh[0];
+}
+
+HKO_EXPORT double hko_band_ordered_sum(const double* u, int64_t n) {
+    hko_band gp[HKO_G];
+    for (int g = 0; g < HKO_G; ++g) gp[g] = band_group_part(u, n, g);
+    for (int w = HKO_G / 2; w > 0; w >>= 1)
+        for (int i = 0; i < w; ++i) gp[i] = band_add(gp[i], gp[i + w]);
+    return gp[0].h;
+}
+
 HKO_EXPORT double hko_ordered_sum(const double* u, int64_t n) {
     double gp[HKO_G];
     for (int g = 0; g < HKO_G; ++g) gp[g] = group_part(u, n, g);

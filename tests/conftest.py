@@ -57,6 +57,17 @@ def unit32(tmp_path_factory):
     return directory
 
 
+@pytest.fixture(scope="session")
+def unit_banded(tmp_path_factory):
+    """The banded example kernels, built in the banded mode."""
+    import hawk_amd as hawk
+    from hawk_amd import examples as E
+
+    directory = tmp_path_factory.mktemp("unit_banded")
+    hawk.build(list(E.BANDED.values()), directory, mode="banded")
+    return directory
+
+
 @lru_cache(maxsize=None)
 def _golden() -> dict:
     return json.loads((Path(__file__).resolve().parent / "golden" / "known_answers.json").read_text())

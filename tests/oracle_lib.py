@@ -55,6 +55,10 @@ def lib(profile: str = "portable"):
         "hko_row_sums": (None, [_P, _I64, _P, _P]),
         "hko_rows_finish": (_D, [_P, _P, _I64]),
         "hko_sample_sum": (_D, [_P, _I64]),
+        "hko_band_row_sums": (None, [_P, _I64, _P, _P]),
+        "hko_band_rows_finish": (_D, [_P, _P, _I64]),
+        "hko_band_sample_sum": (_D, [_P, _I64]),
+        "hko_band_ordered_sum": (_D, [_P, _I64]),
         "hko_scatter_chunks": (ctypes.c_int, [_I64, _I64]),
         "hko_ordered_scatter": (None, [_P, _P, _I64, _P, _I64, _P, _P]),
         "hko_twobody": (None, [_P, _P, _D, _I64, _P, _P, _I64, _I64]),
@@ -258,6 +262,33 @@ def sample_sum(t) -> float:
     """The default-policy hawk.sum of the terms t (rows, then the canonical finish)."""
     t = np.ascontiguousarray(t, dtype=np.float64)
     return lib().hko_sample_sum(_p(t), t.size)
+
+
+def band_row_sums(t):
+    """The banded rows: each row of 32 terms as a normalised double-double band (hi, lo)."""
+    t = np.ascontiguousarray(t, dtype=np.float64)
+    rows = -(-t.size // 32)
+    hi, lo = np.empty(rows), np.empty(rows)
+    lib().hko_band_row_sums(_p(t), t.size, _p(hi), _p(lo))
+    return hi, lo
+
+
+def band_rows_finish(hi, lo) -> float:
+    hi = np.ascontiguousarray(hi, dtype=np.float64)
+    lo = np.ascontiguousarray(lo, dtype=np.float64)
+    return lib().hko_band_rows_finish(_p(hi), _p(lo), hi.size)
+
+
+def band_sample_sum(t) -> float:
+    """hawk.sum of the terms t in the banded mode (band rows, the canonical finish with band adds)."""
+    t = np.ascontiguousarray(t, dtype=np.float64)
+    return lib().hko_band_sample_sum(_p(t), t.size)
+
+
+def band_ordered_sum(u) -> float:
+    """hawk.sum(policy="ordered") in the banded mode: the fixed tree with band accumulators."""
+    u = np.ascontiguousarray(u, dtype=np.float64)
+    return lib().hko_band_ordered_sum(_p(u), u.size)
 
 
 def scatter_chunks(n, cells) -> int:

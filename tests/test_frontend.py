@@ -937,3 +937,30 @@ def test_a_chain_passes_params_tables_and_grids_through(tmp_path):
     assert got.tobytes() == (u * u).tobytes()
     back = vjp(chained, wrt=("w",))                 # the keyed sum is ordered: the table's gradient folds
     assert [type(s).__name__ for s in back.sinks] == ["OrderedFold"]
+
+
+def test_the_banded_mode_plans_band_stages_and_refuses_what_it_cannot_fold():
+    """mode="banded": the default-policy sums' rows fold double-double bands in
+    the stage (hk_band_row_sum) and in the finish (band_rows), the ordered sum
+    is the banded fixed tree (band_ordered_sum); a keyed sum or a scatter is
+    refused by name (the reference refuses the reductions its banded build
+    cannot certify, hawk/emit/wrapper.py:158-196)."""
+    from hawk_amd.emit_hip import plan_kernel
+    p = plan_kernel(E.band_total.program, "band_total", mode="banded")
+    assert [(t["op"], t["out"]) for t in p.team] == [("band_rows", "s"), ("band_rows", "s_sq"),
+                                                     ("band_ordered_sum", "s_ord")]
+    assert "hk_band_row_sum(hk_rh, hk_rc);" in p.source and "hk_row_sum(" not in p.source
+    assert "typedef double Real;" in p.source
+    f64 = plan_kernel(E.band_total.program, "band_total", mode="float64")
+    assert [t["op"] for t in f64.team] == ["row_sum", "row_sum", "ordered_sum"] and "hk_band" not in f64.source
+    with pytest.raises(HawkError, match="hawk.scatter\\(acc\\) has no banded stage"):
+        plan_kernel(E.ordered_add.program, "ordered_add", mode="banded")
+    with pytest.raises(HawkError, match="'float64', 'float32' or 'banded'"):
+        plan_kernel(E.band_total.program, "band_total", mode="float16")
+
+
+def test_a_banded_build_records_its_mode_and_binds_float64_cells(tmp_path):
+    b = hawk.build([E.band_total], tmp_path, mode="banded")
+    side = b.sidecar("band_total")
+    assert side["mode"] == "banded" and {t["op"] for t in side["team"]} == {"band_rows", "band_ordered_sum"}
+    assert all(side["planes"][c] == {"role": "cell", "shape": [], "dtype": "f64"} for c in ("s", "s_sq", "s_ord"))

@@ -1245,3 +1245,68 @@ def test_folds_and_keyed_sums_keep_ieee_specials_and_empty_runs(gpu, tmp_path):
     hawk.run(hawk.load(tmp_path / "fused", "kt_vjp"), t=dev(t, gpu), x=dev(np.zeros(0), gpu),
              bar_out=dev(np.zeros(0), gpu), bar_t=bt)
     assert (host(bt) == 7.0).all()
+
+
+# -- banded reductions ------------------------------------------------------------
+
+def _band_data(kind, n):
+    V = 65536
+    if kind == "cancel_lanes":          # each virtual lane of the ordered tree cancels 2^60 against itself
+        reps = -(-n // (4 * V))
+        block = np.concatenate([np.full(V, 2.0 ** 60), np.ones(V), np.full(V, -(2.0 ** 60)), np.ones(V)])
+        return np.tile(block, reps)[:n]
+    if kind == "reference_series":      # the reference's float32-exact 2^30 cancelling series
+        return np.tile([2.0 ** 30, 1.0, -(2.0 ** 30), 1.0], n // 4 + 1)[:n].astype(np.float32).astype(np.float64)
+    if kind == "exact_integers":        # every partial fits a double-double
+        k = rng(n).integers(-(1 << 40), 1 << 40, n, dtype=np.int64)
+        return k.astype(np.float64) * 2.0 ** -20
+    g = rng(n + 7)
+    return g.normal(size=n) * np.exp(g.normal(size=n) * 8)
+
+
+@pytest.mark.parametrize("kind", ["cancel_lanes", "reference_series", "exact_integers", "wide"])
+@pytest.mark.parametrize("n", [1, 31, 33, 1000, 65537, 3 * 65536 + 777, (1 << 20) + 5])
+def test_banded_sums_are_the_oracles_bits_and_replay(unit_banded, gpu, kind, n):
+    """The banded mode's sample sums on the device (band rows in the stage, the
+    banded canonical finish, the banded ordered tree) are the oracle's bits,
+    on every one of three launches."""
+    import hawk_amd as hawk
+    x = _band_data(kind, n)
+    X = dev(x, gpu)
+    k = _load(unit_banded, "band_total")
+    want = (O.band_sample_sum(x), O.band_sample_sum(x * x), O.band_ordered_sum(x))
+    print(f"band_total {kind} n={n}", flush=True)
+    for _ in range(3):
+        cells = {c: dev(np.full(1, np.nan), gpu) for c in ("s", "s_sq", "s_ord")}
+        hawk.run(k, x=X, **cells)
+        got = tuple(float(host(cells[c])[0]) for c in ("s", "s_sq", "s_ord"))
+        assert np.array(got).tobytes() == np.array(want).tobytes(), (got, want)
+
+
+def test_banded_sums_on_the_device_hold_the_reference_bounds(unit_banded, gpu):
+    """Against exact rational sums: the reference's cancelling series within
+    0.01 ULP53 (tests/test_banded_sum.py), a lane-cancelling series the plain
+    fixed tree gets wrong held exactly, and exact-integer data rounded once."""
+    from fractions import Fraction
+
+    import hawk_amd as hawk
+    k = _load(unit_banded, "band_total")
+
+    def run(x):
+        cells = {c: dev(np.zeros(1), gpu) for c in ("s", "s_sq", "s_ord")}
+        hawk.run(k, x=dev(x, gpu), **cells)
+        return {c: float(host(v)[0]) for c, v in cells.items()}
+    x = _band_data("reference_series", 3 * 65536 + 777)
+    exact = sum(Fraction(float(v)) for v in x)
+    got = run(x)
+    for c in ("s", "s_ord"):
+        assert abs(Fraction(got[c]) - exact) <= Fraction(1, 100) * Fraction(float(np.spacing(float(exact))))
+    x = _band_data("cancel_lanes", 4 * 65536)
+    got = run(x)
+    assert got["s_ord"] == got["s"] == 2.0 * 65536
+    assert O.ordered_sum(x) == 65536.0                       # the plain fixed tree loses a term a lane
+    x = _band_data("exact_integers", (1 << 20) + 5)
+    k_int = (x * 2.0 ** 20).astype(np.int64)
+    want = float(Fraction(int(k_int.sum()), 1 << 20))
+    got = run(x)
+    assert got["s"] == got["s_ord"] == want

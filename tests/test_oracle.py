@@ -555,3 +555,80 @@ def test_keyed_sample_sum_is_each_keys_default_sum(keys, group):
         assert got[k] == O.sample_sum(run)
         exact = math.fsum(run)
         assert abs(got[k] - exact) <= 4 * np.spacing(abs(exact)) + 1e-14 * np.abs(run).sum()
+
+
+# -- banded reductions ------------------------------------------------------------
+
+def _exact_integers(n, seed, bits=40):
+    """Terms k * 2^-20 with |k| < 2^bits: every partial sum of up to 2^20 of
+    them fits a double-double exactly, so a band sum is the exact sum rounded
+    once.  Returns the terms and the exact sum (a Fraction)."""
+    from fractions import Fraction
+    k = np.random.default_rng(seed).integers(-(1 << bits), 1 << bits, n, dtype=np.int64)
+    return k.astype(np.float64) * 2.0 ** -20, Fraction(int(k.sum()), 1 << 20)
+
+
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 1000, 65537, 3 * 65536 + 777, (1 << 20) + 5])
+def test_band_sums_round_the_exact_sum_once_where_double_double_holds_it(n):
+    """Where every partial fits a double-double the banded sums (default and
+    ordered) are the exact sum correctly rounded, bit for bit."""
+    x, exact = _exact_integers(n, n)
+    want = float(exact)
+    assert O.band_sample_sum(x) == want
+    assert O.band_ordered_sum(x) == want
+
+
+def test_band_sums_where_the_plain_ordered_tree_loses_terms():
+    """Lane l of the ordered tree adds rows l, l + 65536, ...: with rows 2^60,
+    1, -2^60, 1 each plain lane loses its first 1; the banded lanes keep it."""
+    V = 65536
+    x = np.concatenate([np.full(V, 2.0 ** 60), np.ones(V), np.full(V, -(2.0 ** 60)), np.ones(V)])
+    assert O.band_ordered_sum(x) == 2.0 * V
+    assert O.ordered_sum(x) == 1.0 * V                      # the plain fixed tree
+    assert O.band_sample_sum(x) == 2.0 * V
+
+
+def _ulp53(got: float, exact) -> float:
+    from fractions import Fraction
+    if exact == 0:
+        return 0.0 if got == 0.0 else float("inf")
+    return float(abs(Fraction(got) - exact) / Fraction(float(np.spacing(abs(float(exact))))))
+
+
+@pytest.mark.parametrize("n", [1000, 3 * 65536 + 777])
+def test_band_sums_within_a_hundredth_of_an_ulp_on_the_reference_cancelling_series(n):
+    """The reference's banded bound (tests/test_banded_sum.py, tests/test_banded_ordered.py):
+    rows of 2^30, 1, -2^30, 1, float32-exact, within 0.01 ULP53 of the exact
+    rational row sums and total; and within half an ulp on uniform float32 data."""
+    from fractions import Fraction
+    x = np.tile([2.0 ** 30, 1.0, -(2.0 ** 30), 1.0], n // 4 + 1)[:n].astype(np.float32).astype(np.float64)
+    hi, lo = O.band_row_sums(x)
+    for r in range(min(hi.size, 64)):
+        exact = sum(Fraction(float(v)) for v in x[r * 32:(r + 1) * 32])
+        assert _ulp53(hi[r], exact) <= 0.01
+        assert Fraction(float(hi[r])) + Fraction(float(lo[r])) == exact      # the band holds the row exactly
+    total = sum(Fraction(float(v)) for v in x)
+    assert _ulp53(O.band_sample_sum(x), total) <= 0.01
+    assert _ulp53(O.band_ordered_sum(x), total) <= 0.01
+    u = np.random.default_rng(n).uniform(-2.0, 2.0, n).astype(np.float32).astype(np.float64)
+    total = sum(Fraction(float(v)) for v in u)
+    assert _ulp53(O.band_sample_sum(u), total) <= 0.5 and _ulp53(O.band_ordered_sum(u), total) <= 0.5
+
+
+def test_band_rows_are_normalised_and_special_values_follow_ieee():
+    g = np.random.default_rng(9)
+    x = g.normal(size=5000) * np.exp(g.normal(size=5000) * 10)
+    hi, lo = O.band_row_sums(x)
+    assert np.all(np.abs(lo) <= np.spacing(np.abs(hi)) / 2)
+    assert O.band_sample_sum(np.zeros(0)) == 0.0 and O.band_ordered_sum(np.zeros(0)) == 0.0
+    z = O.band_sample_sum(np.full(100, -0.0))
+    assert z == 0.0 and not np.signbit(z)
+    for f in (O.band_sample_sum, O.band_ordered_sum):
+        y = np.ones(70000)
+        y[12345] = np.inf
+        assert f(y) == np.inf
+        y[23456] = -np.inf
+        assert np.isnan(f(y))
+        y = np.ones(70000)
+        y[5] = np.nan
+        assert np.isnan(f(y))
