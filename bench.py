@@ -25,7 +25,16 @@ dominant stage's HBM bytes per launch from two child ``rocprofv3 --pmc`` passes
 (FETCH_SIZE, then WRITE_SIZE), each scaled by what that counter reads for a
 plain 1 GiB copy (``--no-traffic`` skips them).  The CPU baseline is the C
 oracle (the host-target restatement, hawk's ``native`` profile) on the same
-workload, on this host's cores.
+workload, on this host's cores: every core of this process's affinity mask,
+then one core, then the same build with ``-ffp-contract=fast``, with the CPU
+model named.
+
+The default run (config 2, without ``--only``) also records configs 1, 3, 4a,
+4b and 5 under ``config.configs``: each one's stages (HIP events, median of 5
+steps after 2 warm-ups), its dominant stage against its roofline and the
+oracle's rate on every host core.  Config 3's FLOPs are algorithmic: the
+traced operations of the forward, and of the VJP's forward and reverse
+without its checkpoint replay.
 """
 
 from __future__ import annotations
@@ -72,6 +81,23 @@ def ops(kernel) -> int:
     return int(kernel.sidecar.get("fp_ops_per_sample", 0))
 
 
+def twobody_vjp_algorithmic_ops() -> int:
+    """The two-body VJP's algorithmic operations per sample: its traced forward
+    and reverse with one tape (no checkpoint replay, whose recomputation the
+    built kernel adds), counted in the rendered stage as the build counts
+    every kernel's operations."""
+    from hawk_amd import diff
+    from hawk_amd import examples as E
+    from hawk_amd.emit_hip import plan_kernel
+    saved = diff.CHECKPOINT_SEGMENT
+    diff.CHECKPOINT_SEGMENT = 1 << 30          # larger than any trip count: the loop keeps one tape
+    try:
+        program = diff.vjp(E.twobody, wrt=("r0", "v0"))
+    finally:
+        diff.CHECKPOINT_SEGMENT = saved
+    return plan_kernel(program, "twobody_vjp_one_tape").algorithmic_ops
+
+
 def workload(config: str, device):
     import torch
 
@@ -91,7 +117,7 @@ def workload(config: str, device):
         def cpu(threads):
             import oracle_lib as O
             out = np.empty(n)
-            O.lib("native").hko_tiled(1, O._p(x), None, None, None, O._p(out), None, 2.0, 1.0, n, threads)
+            O.lib().hko_tiled(1, O._p(x), None, None, None, O._p(out), None, 2.0, 1.0, n, threads)
         return dict(name="scale fwd (config 1)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64")
     if config == "2":
         n = 1 << 25
@@ -112,7 +138,7 @@ def workload(config: str, device):
 
         def cpu(threads):
             import oracle_lib as O
-            L = O.lib("native")
+            L = O.lib()
             out, bv, do = np.empty(n), np.empty((3, n)), np.empty(n)
             L.hko_tiled(2, O._p(v), None, None, None, O._p(out), None, 0.0, 0.0, n, threads)
             L.hko_tiled(3, O._p(v), O._p(bar_out), None, None, O._p(bv), None, 0.0, 0.0, n, threads)
@@ -133,14 +159,20 @@ def workload(config: str, device):
         R, VV, BR0, BV0 = (torch.zeros((3, n), dtype=torch.float64, device=device) for _ in range(4))
         kernels = [kf.prepare(r0=R0, v0=V0, mu=1.0, r=R, v=VV),
                    kv.prepare(r0=R0, v0=V0, mu=1.0, bar_r=BR, bar_v=BV, bar_r0=BR0, bar_v0=BV0)]
-        work = {"twobody": (96, ops(kf)), "twobody_vjp": (144, ops(kv))}
+        work = {"twobody": (96, ops(kf)), "twobody_vjp": (144, twobody_vjp_algorithmic_ops())}
+        outs = [np.empty((3, n)) for _ in range(4)]
 
         def cpu(threads):
+            # the host target's shape for a rolled loop: tiles of samples stepping together (loop interchange)
             import oracle_lib as O
-            O.twobody(r0, v0, 1.0, threads=threads)
-            O.twobody_vjp(r0, v0, 1.0, bar_r, bar_v, threads=threads)
+            L = O.lib()
+            L.hko_tiled(9, O._p(r0), O._p(v0), None, None, O._p(outs[0]), O._p(outs[1]), 1.0, 0.0, n, threads)
+            L.hko_tiled(10, O._p(r0), O._p(v0), O._p(bar_r), O._p(bar_v), O._p(outs[2]), O._p(outs[3]), 1.0, 0.0,
+                        n, threads)
         return dict(name="two-body leapfrog fwd + VJP (config 3)", n=n, kernels=kernels, work=work, cpu=cpu,
-                    dtype="f64", bound="fp64")
+                    dtype="f64", bound="fp64",
+                    flops_basis="traced operations per sample, each + - * / and sqrt one: the forward (1280), "
+                                "the VJP's forward and reverse without its checkpoint replay")
     if config == "4a":
         n = 1 << 20
         g = np.random.default_rng(4)
@@ -224,7 +256,7 @@ def workload(config: str, device):
 
         def cpu(threads):
             import oracle_lib as O
-            O.keyed_ordered_sum(x, group, threads=threads, profile="native")
+            O.keyed_ordered_sum(x, group, threads=threads, profile=None)
         return dict(name="keyed ordered sum, 16384 keys x 4096 samples (config 5b, keyed)", n=n, kernels=kernels,
                     work=work, cpu=cpu, dtype="f64")
     if config == "5t":
@@ -299,7 +331,7 @@ def workload(config: str, device):
 
         def cpu(threads):
             import oracle_lib as O
-            O.chain_members(x, acc0.copy(), threads=threads, profile="native")
+            O.chain_members(x, acc0.copy(), threads=threads, profile=None)
         return dict(name="hawk.chain of four kernels (vector and scalar passed by name), one launch", n=n,
                     kernels=kernels, work=work, cpu=cpu, dtype="f64", compare=members_ms)
     if config == "steps":
@@ -321,7 +353,7 @@ def workload(config: str, device):
         def cpu(threads):
             import oracle_lib as O
             O.osc_launch(8, E.OSC_DT, t_final, x.copy(), v.copy(), np.zeros(n), np.zeros(n, dtype=bool),
-                         profile="native")
+                         profile=None)
         return dict(name="oscillator finishing its own sample, 8 steps a launch (hawk.steps)", n=n,
                     kernels=kernels, work=work, cpu=cpu, dtype="f64", cpu_threads=1)
     if config == "persist":
@@ -375,7 +407,7 @@ def workload(config: str, device):
         def cpu(threads):
             import oracle_lib as O
             O.osc_launch(256, E.OSC_DT, t_final, x.copy(), v.copy(), np.zeros(n), np.zeros(n, dtype=bool),
-                         profile="native")
+                         profile=None)
         return dict(name="oscillators of 1-256 steps run to their finish in one launch of the persistent "
                          "entry (hawk.steps 'auto')", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
                     cpu_threads=1, bound="fp64", compare_entries=other_entries)
@@ -414,8 +446,8 @@ def workload(config: str, device):
 
         def cpu(threads):
             import oracle_lib as O
-            O.net_loss(w, mask, x, y, threads=threads, profile="native")
-            O.net_grad(w, mask, x, y, np.ones(k), threads=threads, profile="native")
+            O.net_loss(w, mask, x, y, threads=threads, profile=None)
+            O.net_grad(w, mask, x, y, np.ones(k), threads=threads, profile=None)
         return dict(name="net axis: 65536 nets x 64 samples, ordered loss and its gradient (ordered log fold)",
                     n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
                     bound="fp64" if kv.team[0]["op"] == "fused_fold" else None)
@@ -501,6 +533,133 @@ def measure_traffic(config: str, kernels: list, occurrence: int = 0, per_step: i
     return {"bytes": total, "factors": factors}
 
 
+def _stages_of(w) -> list:
+    stages = []
+    for prep in w["kernels"]:
+        for label, launch in prep.stages():
+            while label in (x for x, _ in stages):     # a stage label taken by an earlier kernel
+                label = label.split("#")[0] + "#" + str(int(label.split("#")[1]) + 1 if "#" in label else 2)
+            stages.append((label, launch))
+    return stages
+
+
+def time_steps(w, steps: int, warmup: int) -> dict:
+    """Warm up, then time ``steps`` steps of workload ``w``: every stage launch
+    bracketed by HIP events on the stream it runs on (torch's current stream,
+    the stream the launchers were prepared on), the whole run by two more."""
+    import torch
+    stages = _stages_of(w)
+    for _ in range(warmup):
+        for _label, launch in stages:
+            launch()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    events = {label: [] for label, _ in stages}
+    t0 = time.perf_counter()
+    start_all = torch.cuda.Event(enable_timing=True)
+    end_all = torch.cuda.Event(enable_timing=True)
+    start_all.record(stream)
+    for _ in range(steps):
+        for label, launch in stages:
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            launch()
+            b.record(stream)
+            events[label].append((a, b))
+    end_all.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    n = w["n"]
+    per_stage = {}
+    for label in events:
+        b_per, f_per = w["work"][label]
+        med = statistics.median(a.elapsed_time(b) for a, b in events[label])
+        per_stage[label] = {"ms": round(med, 5), "samples_per_s": n / (med * 1e-3),
+                            "bytes_per_sample": b_per, "flops_per_sample": f_per,
+                            "achieved_GBs": b_per * n / (med * 1e-3) / 1e9,
+                            "hbm_frac": b_per * n / (med * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        if w.get("bound") == "fp64" and f_per:
+            tf = f_per * n / (med * 1e-3) / 1e12
+            per_stage[label].update({"achieved_TFLOPs": tf, "fp64_frac": tf / FP64_PEAK_TFLOPS})
+    return {"ms_step": start_all.elapsed_time(end_all) / steps, "per_stage": per_stage, "wall": wall}
+
+
+def roofline_of(w, per_stage: dict, traffic=None) -> dict:
+    dominant = max(per_stage, key=lambda k: per_stage[k]["ms"])
+    d = per_stage[dominant]
+    if w.get("bound") == "fp64":
+        return {"bound": "fp64-valu", "kernel": dominant, "achieved": round(d["achieved_TFLOPs"], 3),
+                "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(d["fp64_frac"], 4), "traffic": traffic,
+                "flops_basis": w.get("flops_basis", "operations counted in the emitted code")}
+    return {"bound": "hbm", "kernel": dominant, "achieved": round(d["achieved_GBs"], 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(d["hbm_frac"], 4), "traffic": traffic}
+
+
+def host_cores() -> int:
+    """The cores this process may run on (its affinity mask)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_rate(w, threads: int, profile: str, seconds: float) -> tuple:
+    """Samples/s of the oracle's step on ``threads`` threads in build
+    ``profile`` (one warm-up, then repetitions for about ``seconds``; at
+    least one): ``(rate, repetitions, seconds of CPU work)``."""
+    import oracle_lib as O
+    O.use_profile(profile)
+    cores = w.get("cpu_threads") or threads
+    w["cpu"](cores)
+    times = []
+    begin = time.perf_counter()
+    while not times or (time.perf_counter() - begin < seconds and len(times) < 2000):
+        t = time.perf_counter()
+        w["cpu"](cores)
+        times.append(time.perf_counter() - t)
+    return w["n"] / statistics.median(times), len(times), sum(times)
+
+
+#: The configurations the default run records beside its headline (config 2).
+OTHER_CONFIGS = ("1", "3", "4a", "4b", "5")
+
+
+def config_record(config: str, device, steps: int = 5, warmup: int = 2) -> dict:
+    """One configuration's record for the default run: its stages timed on
+    the GPU (HIP events, median of ``steps``), the dominant stage against its
+    roofline, and the oracle on every host core (one timed repetition after a
+    warm-up)."""
+    import torch
+    log(f"config {config}: record")
+    w = workload(config, device)
+    t = time_steps(w, steps, warmup)
+    rate, reps, cpu_s = cpu_rate(w, host_cores(), "native", 0.0)
+    rec = {"workload": w["name"], "N": w["n"], "dtype": w["dtype"], "ms_per_step": round(t["ms_step"], 5),
+           "samples_per_s": w["n"] / (t["ms_step"] * 1e-3),
+           "stages": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                      for k, v in t["per_stage"].items()},
+           "roofline": roofline_of(w, t["per_stage"]),
+           "cpu_baseline": {"value": rate, "unit": "samples/s", "cores": w.get("cpu_threads") or host_cores(),
+                            "kind": "port", "sample": f"the full step on the C oracle (native profile), "
+                                                      f"{reps} repetition(s) after 1 warm-up"}}
+    del w
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -510,6 +669,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc passes that measure the dominant stage's HBM traffic")
+    ap.add_argument("--only", action="store_true",
+                    help="time the chosen configuration alone (the default run of config 2 also records "
+                         "configs " + ", ".join(OTHER_CONFIGS) + ")")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed steps, run one plain 1 GiB device copy (untimed): the "
                          "known-size kernel that scales HBM counters read by rocprofv3 --pmc")
@@ -523,36 +685,9 @@ def main() -> int:
     log(f"config {args.config}: building and uploading inputs")
     w = workload(args.config, device)
     n = w["n"]
-    stages = []
-    for prep in w["kernels"]:
-        for label, launch in prep.stages():
-            while label in (x for x, _ in stages):     # a stage label taken by an earlier kernel
-                label = label.split("#")[0] + "#" + str(int(label.split("#")[1]) + 1 if "#" in label else 2)
-            stages.append((label, launch))
-    for _ in range(args.warmup):
-        for _label, launch in stages:
-            launch()
-    torch.cuda.synchronize()
-    log(f"warmup done ({args.warmup} steps); timing {args.steps} steps")
-    # every launch is on the stream the launchers were prepared on (torch's current stream)
-    stream = torch.cuda.current_stream()
-    events = {label: [] for label, _ in stages}
-    t0 = time.perf_counter()
-    torch.cuda.synchronize()
-    start_all = torch.cuda.Event(enable_timing=True)
-    end_all = torch.cuda.Event(enable_timing=True)
-    start_all.record(stream)
-    for _ in range(args.steps):
-        for label, launch in stages:
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            launch()
-            b.record(stream)
-            events[label].append((a, b))
-    end_all.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    log(f"timing {args.steps} steps after {args.warmup} warm-up steps")
+    t = time_steps(w, args.steps, args.warmup)
+    ms_step, per_stage, wall = t["ms_step"], t["per_stage"], t["wall"]
     if args.copy_probe:
         src = torch.ones(COPY_PROBE_BYTES // 8, dtype=torch.float64, device=device)
         dst = torch.empty_like(src)
@@ -560,15 +695,6 @@ def main() -> int:
         torch.cuda.synchronize()
         log("copy probe: 1 GiB read + 1 GiB written by one copy kernel")
         del src, dst
-    ms_step = start_all.elapsed_time(end_all) / args.steps
-    per_stage = {}
-    for label in events:
-        b_per, f_per = w["work"][label]
-        med = statistics.median(a.elapsed_time(b) for a, b in events[label])
-        per_stage[label] = {"ms": round(med, 5), "samples_per_s": n / (med * 1e-3),
-                            "bytes_per_sample": b_per, "flops_per_sample": f_per,
-                            "achieved_GBs": b_per * n / (med * 1e-3) / 1e9,
-                            "hbm_frac": b_per * n / (med * 1e-3) / 1e9 / HBM_PEAK_GBS}
     dominant = max(per_stage, key=lambda k: per_stage[k]["ms"])
     d = per_stage[dominant]
     traffic = None
@@ -581,38 +707,30 @@ def main() -> int:
                 kernels = STAGE_KERNELS.get(base_label, (base_label,))
                 occurrence = int(dominant.split("#")[1]) - 1 if "#" in dominant else 0
                 per_step = sum(1 for x in per_stage if x.split("#")[0] == base_label)
-            t = measure_traffic(args.config, kernels, occurrence, per_step)
-            traffic = round(t["bytes"])
+            tr = measure_traffic(args.config, kernels, occurrence, per_step)
+            traffic = round(tr["bytes"])
             log(f"traffic of {dominant}: {traffic / 1e6:.1f} MB per launch "
-                f"(algorithmic {d['bytes_per_sample'] * n / 1e6:.1f} MB; counter factors {t['factors']})")
+                f"(algorithmic {d['bytes_per_sample'] * n / 1e6:.1f} MB; counter factors {tr['factors']})")
         except Exception as exc:        # counters are evidence, not the measurement: report null
             log(f"traffic not measured: {exc}")
-    if w.get("bound") == "fp64":
-        achieved = d["flops_per_sample"] * n / (d["ms"] * 1e-3) / 1e12
-        roofline = {"bound": "fp64-valu", "kernel": dominant, "achieved": round(achieved, 3),
-                    "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP64_PEAK_TFLOPS, 4),
-                    "traffic": traffic}
-    else:
-        roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(d["achieved_GBs"], 1),
-                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(d["hbm_frac"], 4), "traffic": traffic}
+    roofline = roofline_of(w, per_stage, traffic)
     cpu_baseline = None
     if not args.no_cpu:
-        threads = w.get("cpu_threads") or min(os.cpu_count() or 1, 16)
-        log(f"CPU baseline: oracle (native profile) on {threads} threads")
-        import oracle_lib as O
-        O.build("native")
-        w["cpu"](threads)
-        times = []
-        begin = time.perf_counter()
-        while len(times) < 3 or (time.perf_counter() - begin < CPU_SECONDS and len(times) < 2000):
-            t = time.perf_counter()
-            w["cpu"](threads)
-            times.append(time.perf_counter() - t)
-        tc = statistics.median(times)
-        cpu_baseline = {"value": n / tc, "unit": "samples/s", "cores": threads, "kind": "port",
-                        "sample": f"the full step ({w['name']}, N={n}) on the C oracle (native profile, "
-                                  f"{threads} threads), median of {len(times)} repetitions "
-                                  f"({sum(times):.1f} s of CPU work) after 1 warm-up"}
+        cores = w.get("cpu_threads") or host_cores()
+        log(f"CPU baseline: the oracle on {cores} threads (native profile), then 1 thread, then -ffp-contract=fast")
+        rate, reps, spent = cpu_rate(w, cores, "native", CPU_SECONDS)
+        one, one_reps, one_spent = cpu_rate(w, 1, "native", CPU_SECONDS / 2)
+        fast, fast_reps, _ = cpu_rate(w, cores, "fast", CPU_SECONDS / 4)
+        cpu_baseline = {"value": rate, "unit": "samples/s", "cores": cores, "kind": "port",
+                        "cpu_model": cpu_model(),
+                        "sample": f"the full step ({w['name']}, N={n}) on the C oracle (native profile: gcc -O3 "
+                                  f"-march=native -ffp-contract=off, {cores} threads, one contiguous tile each), "
+                                  f"median of {reps} repetitions ({spent:.1f} s of CPU work) after 1 warm-up",
+                        "one_core": {"value": one, "cores": 1, "sample": f"median of {one_reps} repetitions "
+                                                                          f"({one_spent:.1f} s)"},
+                        "fp_contract_fast": {"value": fast, "cores": cores,
+                                             "sample": f"-ffp-contract=fast build, median of {fast_reps} "
+                                                       "repetitions (its bits are not the exact profile's)"}}
     compare = {}
     if "compare" in w:
         compare["members_launched_one_by_one_ms"] = round(w["compare"](), 5)
@@ -620,14 +738,23 @@ def main() -> int:
     if "compare_entries" in w:
         compare.update(w["compare_entries"]())
         log(f"the same launch through the other entries: {compare}")
+    records = {}
+    name, dtype = w["name"], w["dtype"]
+    if args.config == "2" and not args.only:
+        del w
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        for c in OTHER_CONFIGS:
+            records[c] = config_record(c, device)
     line = {
         "metric": METRIC, "value": n / (ms_step * 1e-3), "unit": "samples/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": w["dtype"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (seeded numpy, resident in HBM before timing)",
-        "config": {"workload": w["name"], "N": n, **compare,
+        "config": {"workload": name, "N": n, **compare,
                    "stages": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                              for k, v in per_stage.items()}},
+                              for k, v in per_stage.items()},
+                   **({"configs": records} if records else {})},
         "roofline": roofline, "cpu_baseline": cpu_baseline, "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)

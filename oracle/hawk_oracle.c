@@ -652,6 +652,120 @@ HKO_EXPORT void hko_twobody_vjp(const double* r0, const double* v0, double mu, c
     }
 }
 
+/* ---- config 3 interchanged: the loop over samples inside the substep loop --
+ * The reference host target's loop interchange for a rolled `for` body
+ * (hawk/emit/host.py:961-1000, :1061 loop_interchange): a tile of samples
+ * steps together, so each operation of a substep runs across the tile's
+ * samples as one SIMD loop.  Per sample the operations and their order are
+ * those of hko_twobody / hko_twobody_vjp, so the bits are theirs (sqrt and
+ * division are correctly rounded in SIMD too); a ragged tail takes the
+ * sample-by-sample loop. */
+#define HKO_TILE 8
+
+static inline void accel_tile(double r[3][HKO_TILE], double mu, double a[3][HKO_TILE]) {
+    for (int t = 0; t < HKO_TILE; ++t) {
+        const double r2 = ((r[0][t] * r[0][t]) + (r[1][t] * r[1][t])) + (r[2][t] * r[2][t]);
+        const double s = -mu / (r2 * sqrt(r2));
+        for (int c = 0; c < 3; ++c) a[c][t] = s * r[c][t];
+    }
+}
+
+static inline void substep_tile(double r[3][HKO_TILE], double v[3][HKO_TILE], double mu) {
+    double a[3][HKO_TILE], vh[3][HKO_TILE];
+    accel_tile(r, mu, a);
+    for (int c = 0; c < 3; ++c)
+        for (int t = 0; t < HKO_TILE; ++t) vh[c][t] = v[c][t] + ((0.5 * HKO_DT) * a[c][t]);
+    for (int c = 0; c < 3; ++c)
+        for (int t = 0; t < HKO_TILE; ++t) r[c][t] = r[c][t] + (HKO_DT * vh[c][t]);
+    accel_tile(r, mu, a);
+    for (int c = 0; c < 3; ++c)
+        for (int t = 0; t < HKO_TILE; ++t) v[c][t] = vh[c][t] + ((0.5 * HKO_DT) * a[c][t]);
+}
+
+HKO_EXPORT void hko_twobody_x(const double* r0, const double* v0, double mu, int64_t n, double* r_out,
+                              double* v_out, int64_t base, int64_t count) {
+    int64_t i = base;
+    for (; i + HKO_TILE <= base + count; i += HKO_TILE) {
+        double r[3][HKO_TILE], v[3][HKO_TILE];
+        for (int c = 0; c < 3; ++c)
+            for (int t = 0; t < HKO_TILE; ++t) { r[c][t] = r0[c * n + i + t]; v[c][t] = v0[c * n + i + t]; }
+        for (int k = 0; k < HKO_STEPS; ++k) substep_tile(r, v, mu);
+        for (int c = 0; c < 3; ++c)
+            for (int t = 0; t < HKO_TILE; ++t) { r_out[c * n + i + t] = r[c][t]; v_out[c * n + i + t] = v[c][t]; }
+    }
+    hko_twobody(r0, v0, mu, n, r_out, v_out, i, base + count - i);
+}
+
+static inline void accel_vjp_tile(double r[3][HKO_TILE], double mu, double g[3][HKO_TILE],
+                                  double bar_r[3][HKO_TILE]) {
+    for (int t = 0; t < HKO_TILE; ++t) {
+        const double r2 = ((r[0][t] * r[0][t]) + (r[1][t] * r[1][t])) + (r[2][t] * r[2][t]);
+        const double sq = sqrt(r2);
+        const double q = r2 * sq;
+        const double s = -mu / q;
+        const double gs = ((g[0][t] * r[0][t]) + (g[1][t] * r[1][t])) + (g[2][t] * r[2][t]);
+        const double gq = -((gs * s) / q);
+        const double gr2 = (gq * sq) + ((gq * r2) * (0.5 / sq));
+        for (int c = 0; c < 3; ++c)
+            bar_r[c][t] = ((bar_r[c][t] + (g[c][t] * s)) + (gr2 * r[c][t])) + (gr2 * r[c][t]);
+    }
+}
+
+static inline void substep_vjp_tile(double r_in[3][HKO_TILE], double v_in[3][HKO_TILE], double mu,
+                                    double br[3][HKO_TILE], double bv[3][HKO_TILE]) {
+    double a[3][HKO_TILE], vh[3][HKO_TILE], r1[3][HKO_TILE];
+    accel_tile(r_in, mu, a);
+    for (int c = 0; c < 3; ++c)
+        for (int t = 0; t < HKO_TILE; ++t) vh[c][t] = v_in[c][t] + ((0.5 * HKO_DT) * a[c][t]);
+    for (int c = 0; c < 3; ++c)
+        for (int t = 0; t < HKO_TILE; ++t) r1[c][t] = r_in[c][t] + (HKO_DT * vh[c][t]);
+    double bvh[3][HKO_TILE], ba1[3][HKO_TILE], br1[3][HKO_TILE];
+    for (int c = 0; c < 3; ++c)
+        for (int t = 0; t < HKO_TILE; ++t) {
+            bvh[c][t] = bv[c][t];
+            ba1[c][t] = bv[c][t] * (0.5 * HKO_DT);
+            br1[c][t] = br[c][t];
+        }
+    accel_vjp_tile(r1, mu, ba1, br1);
+    double brn[3][HKO_TILE], ba0[3][HKO_TILE];
+    for (int c = 0; c < 3; ++c)
+        for (int t = 0; t < HKO_TILE; ++t) {
+            brn[c][t] = br1[c][t];
+            bvh[c][t] += br1[c][t] * HKO_DT;
+        }
+    for (int c = 0; c < 3; ++c)
+        for (int t = 0; t < HKO_TILE; ++t) {
+            bv[c][t] = bvh[c][t];
+            ba0[c][t] = bvh[c][t] * (0.5 * HKO_DT);
+        }
+    accel_vjp_tile(r_in, mu, ba0, brn);
+    for (int c = 0; c < 3; ++c)
+        for (int t = 0; t < HKO_TILE; ++t) br[c][t] = brn[c][t];
+}
+
+HKO_EXPORT void hko_twobody_vjp_x(const double* r0, const double* v0, double mu, const double* bar_r,
+                                  const double* bar_v, int64_t n, double* bar_r0, double* bar_v0,
+                                  int64_t base, int64_t count) {
+    int64_t i = base;
+    for (; i + HKO_TILE <= base + count; i += HKO_TILE) {
+        double tr[HKO_STEPS][3][HKO_TILE], tv[HKO_STEPS][3][HKO_TILE];
+        double r[3][HKO_TILE], v[3][HKO_TILE], br[3][HKO_TILE], bv[3][HKO_TILE];
+        for (int c = 0; c < 3; ++c)
+            for (int t = 0; t < HKO_TILE; ++t) { r[c][t] = r0[c * n + i + t]; v[c][t] = v0[c * n + i + t]; }
+        for (int k = 0; k < HKO_STEPS; ++k) {
+            for (int c = 0; c < 3; ++c)
+                for (int t = 0; t < HKO_TILE; ++t) { tr[k][c][t] = r[c][t]; tv[k][c][t] = v[c][t]; }
+            substep_tile(r, v, mu);
+        }
+        for (int c = 0; c < 3; ++c)
+            for (int t = 0; t < HKO_TILE; ++t) { br[c][t] = bar_r[c * n + i + t]; bv[c][t] = bar_v[c * n + i + t]; }
+        for (int k = HKO_STEPS - 1; k >= 0; --k) substep_vjp_tile(tr[k], tv[k], mu, br, bv);
+        for (int c = 0; c < 3; ++c)
+            for (int t = 0; t < HKO_TILE; ++t) { bar_r0[c * n + i + t] = br[c][t]; bar_v0[c * n + i + t] = bv[c][t]; }
+    }
+    hko_twobody_vjp(r0, v0, mu, bar_r, bar_v, n, bar_r0, bar_v0, i, base + count - i);
+}
+
 /* ---- config 4a: 6x6 SPD Cholesky solve and its VJP -------------------------
  * Factor and solve in the operation order of reference
  * hawk/embedded/linalg.py:233-271 (`_chol`: the symmetrised entry
@@ -853,11 +967,11 @@ static void* job_main(void* arg) {
                               j->parts, j->status);
             break;
         case 8: scatter_cells(j->parts, j->base, j->base + j->count, j->chunks, (double*)j->out0); break;
-        case 9: hko_twobody((const double*)j->in0, (const double*)j->in1, j->s0, j->n, (double*)j->out0,
-                            (double*)j->out1, j->base, j->count); break;
-        case 10: hko_twobody_vjp((const double*)j->in0, (const double*)j->in1, j->s0, (const double*)j->in2,
-                                 (const double*)j->in3, j->n, (double*)j->out0, (double*)j->out1, j->base,
-                                 j->count); break;
+        case 9: hko_twobody_x((const double*)j->in0, (const double*)j->in1, j->s0, j->n, (double*)j->out0,
+                              (double*)j->out1, j->base, j->count); break;
+        case 10: hko_twobody_vjp_x((const double*)j->in0, (const double*)j->in1, j->s0, (const double*)j->in2,
+                                   (const double*)j->in3, j->n, (double*)j->out0, (double*)j->out1, j->base,
+                                   j->count); break;
         case 11: hko_spd_solve((const double*)j->in0, (const double*)j->in1, j->n, (double*)j->out0, j->base,
                                j->count); break;
         case 12: hko_spd_solve_vjp((const double*)j->in0, (const double*)j->in1, (const double*)j->in2, j->n,

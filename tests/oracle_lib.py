@@ -24,14 +24,26 @@ _libs: dict = {}
 
 
 def build(profile: str = "portable") -> Path:
-    out = ORACLE / ("libhawk_oracle.so" if profile == "portable" else "_native/libhawk_oracle.so")
+    out = ORACLE / {"portable": "libhawk_oracle.so", "native": "_native/libhawk_oracle.so",
+                    "fast": "_fast/libhawk_oracle.so"}[profile]
     src = ORACLE / "hawk_oracle.c"
     if not out.exists() or out.stat().st_mtime < src.stat().st_mtime:
         subprocess.run(["make", "-s", "-C", str(ORACLE), f"PROFILE={profile}"], check=True)
     return out
 
 
-def lib(profile: str = "portable"):
+_default_profile = ["portable"]
+
+
+def use_profile(profile: str) -> None:
+    """Make ``profile`` ("portable", "native" or "fast") the build the
+    wrappers below call by default (the CPU baseline times "native")."""
+    build(profile)
+    _default_profile[0] = profile
+
+
+def lib(profile: str | None = None):
+    profile = profile or _default_profile[0]
     if profile in _libs:
         return _libs[profile]
     L = ctypes.CDLL(str(build(profile)))
@@ -63,6 +75,8 @@ def lib(profile: str = "portable"):
         "hko_ordered_scatter": (None, [_P, _P, _I64, _P, _I64, _P, _P]),
         "hko_twobody": (None, [_P, _P, _D, _I64, _P, _P, _I64, _I64]),
         "hko_twobody_vjp": (None, [_P, _P, _D, _P, _P, _I64, _P, _P, _I64, _I64]),
+        "hko_twobody_x": (None, [_P, _P, _D, _I64, _P, _P, _I64, _I64]),
+        "hko_twobody_vjp_x": (None, [_P, _P, _D, _P, _P, _I64, _P, _P, _I64, _I64]),
         "hko_spd_solve": (None, [_P, _P, _I64, _P, _I64, _I64]),
         "hko_spd_solve_vjp": (None, [_P, _P, _P, _I64, _P, _P, _I64, _I64]),
         "hko_mm16": (None, [_P, _P, _I64, _P, _I64, _I64]),

@@ -632,3 +632,28 @@ def test_band_rows_are_normalised_and_special_values_follow_ieee():
         y = np.ones(70000)
         y[5] = np.nan
         assert np.isnan(f(y))
+
+
+@pytest.mark.parametrize("n", [8, 1000, 1003, 4099])
+def test_the_interchanged_twobody_loops_are_the_serial_bits(n):
+    """The CPU baseline's config-3 loops with the host target's interchange
+    (a tile of 8 samples steps together; reference hawk/emit/host.py:1061):
+    bit for bit the sample-by-sample loops, a ragged tail included, in the
+    exact and the native profiles and through the threaded tiles."""
+    r0, v0 = _twobody_inputs(n, 17)
+    g = np.random.default_rng(18)
+    br, bv = g.normal(size=(3, n)), g.normal(size=(3, n))
+    for profile in ("portable", "native"):
+        L = O.lib(profile)
+        r, v, rx, vx = (np.empty((3, n)) for _ in range(4))
+        L.hko_twobody(O._p(r0), O._p(v0), 1.0, n, O._p(r), O._p(v), 0, n)
+        L.hko_twobody_x(O._p(r0), O._p(v0), 1.0, n, O._p(rx), O._p(vx), 0, n)
+        assert r.tobytes() == rx.tobytes() and v.tobytes() == vx.tobytes()
+        a, b, ax, bx = (np.empty((3, n)) for _ in range(4))
+        L.hko_twobody_vjp(O._p(r0), O._p(v0), 1.0, O._p(br), O._p(bv), n, O._p(a), O._p(b), 0, n)
+        L.hko_twobody_vjp_x(O._p(r0), O._p(v0), 1.0, O._p(br), O._p(bv), n, O._p(ax), O._p(bx), 0, n)
+        assert a.tobytes() == ax.tobytes() and b.tobytes() == bx.tobytes()
+    tr, tv = O.twobody(r0, v0, 1.0, threads=3)
+    assert tr.tobytes() == r.tobytes() and tv.tobytes() == v.tobytes()
+    ta, tb = O.twobody_vjp(r0, v0, 1.0, br, bv, threads=3)
+    assert ta.tobytes() == a.tobytes() and tb.tobytes() == b.tobytes()
