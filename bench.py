@@ -238,6 +238,28 @@ def workload(config: str, device):
             O.ordered_scatter(key, y, np.zeros(cells), threads=threads)
         return dict(name="chain + ordered sum + ordered scatter (config 5)", n=n, kernels=kernels, work=work, cpu=cpu,
                     dtype="f64")
+    if config == "band":
+        # the banded mode's sample sums over config 5's input size: the default policy over x and over
+        # x*x (band rows in the stage, the banded canonical finish) and the ordered policy over x (the
+        # banded fixed tree), reference tests/test_banded_sum.py's kernel plus the ordered sum
+        n = 1 << 26
+        x = np.random.default_rng(5).normal(size=n)
+        hawk.build([E.band_total], unit, mode="banded")
+        k = hawk.load(unit, "band_total")
+        X = _dev(x, device)
+        cells = {c: torch.zeros(1, dtype=torch.float64, device=device) for c in ("s", "s_sq", "s_ord")}
+        kernels = [k.prepare(x=X, **cells)]
+        rows = 16 / 32                          # a (hi, lo) band row per 32 samples
+        work = {"band_total": (8 + 2 * rows, 0), "row_sum": (rows, 1), "row_sum#2": (rows, 1),
+                "band_ordered_sum": (8, 1)}
+
+        def cpu(threads):
+            import oracle_lib as O
+            O.band_sample_sum(x)
+            O.band_sample_sum(x * x)
+            O.band_ordered_sum(x)
+        return dict(name="banded sample sums: default policy over x and x*x, ordered over x (mode='banded')",
+                    n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64 (double-double bands)", cpu_threads=1)
     if config == "5k":
         # config 5b in the reference's keyed spelling (tests/test_ordered_fixed_tree.py:43-47), over
         # 16384 keys of 4096 samples: hawk.sum(x, over="sample", policy="ordered") per key
@@ -459,6 +481,7 @@ def workload(config: str, device):
 #: ("mm16#2": the VJP's two products, which share bar_C) names kernels its
 #: step launches once; a base label's kernels may serve several stages.
 STAGE_KERNELS = {"ordered_sum": ("hawk_sum_lanes", "hawk_sum_fold"),
+                 "band_ordered_sum": ("hawk_band_sum_lanes", "hawk_band_sum_fold"),
                  "ordered_scatter": ("hawk_scatter_status", "hawk_scatter_walk", "hawk_scatter_cells"),
                  "mm16": ("hawk_mm16_f32",),
                  "keyed_sum": ("hawk_keyed_rows",),      # keys of at most 65536 samples (config 5k: 4096)
