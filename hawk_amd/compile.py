@@ -90,6 +90,32 @@ def cache_stats() -> dict:
         return dict(_stats)
 
 
+def _publish(path: Path, data: bytes) -> None:
+    """Write ``data`` to ``path`` atomically: a reader sees the old file, or
+    the whole new one."""
+    tmp = path.with_suffix(path.suffix + f".tmp{os.getpid()}_{threading.get_ident()}")
+    tmp.write_bytes(data)
+    os.replace(tmp, path)
+
+
+def _cached(cache: Path, key: str):
+    """The code object stored under ``key``, or ``None`` when the entry is
+    absent or not whole.  An entry is the code object ``<key>.hsaco`` and its
+    validity record ``<key>.json`` (its size and sha256), published after
+    the object: a missing record, or an object that does not match it (a
+    truncated or damaged file), is a miss and gets rebuilt (reference
+    ``hawk/compile/cache.py:385-444``: a record beside the artifact, a miss
+    the safe default)."""
+    try:
+        record = json.loads((cache / f"{key}.json").read_text())
+        code = (cache / f"{key}.hsaco").read_bytes()
+    except (OSError, ValueError):
+        return None
+    if record.get("size") != len(code) or record.get("sha256") != hashlib.sha256(code).hexdigest():
+        return None
+    return code
+
+
 def compile_units(units: list, options=RTC_OPTIONS, cache_dir=None) -> list:
     """``[(code object bytes, cache key, hit)]`` for ``units`` = ``[(name, source)]``,
     compiling every miss in one hipRTC worker call."""
@@ -97,10 +123,10 @@ def compile_units(units: list, options=RTC_OPTIONS, cache_dir=None) -> list:
     keys = [cache_key(src, options) for _, src in units]
     out: list = [None] * len(units)
     misses = []
-    for i, ((name, src), key) in enumerate(zip(units, keys)):
-        path = cache / f"{key}.hsaco"
-        if path.exists():
-            out[i] = (path.read_bytes(), key, True)
+    for i, key in enumerate(keys):
+        code = _cached(cache, key)
+        if code is not None:
+            out[i] = (code, key, True)
         else:
             misses.append(i)
     if misses:
@@ -111,10 +137,10 @@ def compile_units(units: list, options=RTC_OPTIONS, cache_dir=None) -> list:
             codes = [base64.b64decode(c) for _n, c, _log in _run_worker(todo, options)["units"]]
         cache.mkdir(parents=True, exist_ok=True)
         for i, code in zip(misses, codes):
-            path = cache / f"{keys[i]}.hsaco"
-            tmp = path.with_suffix(f".tmp{os.getpid()}_{threading.get_ident()}")
-            tmp.write_bytes(code)
-            os.replace(tmp, path)
+            _publish(cache / f"{keys[i]}.hsaco", code)
+            record = {"size": len(code), "sha256": hashlib.sha256(code).hexdigest(), "unit": units[i][0],
+                      "options": list(options), "toolchain": toolchain()}
+            _publish(cache / f"{keys[i]}.json", json.dumps(record, sort_keys=True).encode())
             out[i] = (code, keys[i], False)
     with _stats_lock:
         _stats["hits"] += len(units) - len(misses)

@@ -964,3 +964,60 @@ def test_a_banded_build_records_its_mode_and_binds_float64_cells(tmp_path):
     side = b.sidecar("band_total")
     assert side["mode"] == "banded" and {t["op"] for t in side["team"]} == {"band_rows", "band_ordered_sum"}
     assert all(side["planes"][c] == {"role": "cell", "shape": [], "dtype": "f64"} for c in ("s", "s_sq", "s_ord"))
+
+
+# -- the build cache (reference hawk/compile/cache.py:347-459, hawk/artifact/bundle.py:1497-1575) ------
+
+def _unit_bytes(directory):
+    return {p.name: p.read_bytes() for p in sorted(directory.iterdir()) if p.suffix in (".hsaco", ".json", ".hip")}
+
+
+def test_a_second_build_is_all_hits_and_publishes_the_same_bytes(tmp_path):
+    from hawk_amd import compile as C
+    cache = tmp_path / "cache"
+    kernels = [E.scale, E.energy, E.energy_vjp, E.chain]
+    before = C.cache_stats()
+    hawk.build(kernels, tmp_path / "a", cache_dir=cache)
+    mid = C.cache_stats()
+    assert mid["misses"] - before["misses"] == 4 and mid["hits"] == before["hits"]
+    hawk.build(kernels, tmp_path / "b", cache_dir=cache)
+    after = C.cache_stats()
+    assert after["hits"] - mid["hits"] == 4 and after["misses"] == mid["misses"]
+    a, b = _unit_bytes(tmp_path / "a"), _unit_bytes(tmp_path / "b")
+    assert sorted(a) == sorted(b) and "manifest.json" in a
+    assert all(a[name] == b[name] for name in a)          # code objects, sidecars and manifest, byte for byte
+
+
+def test_a_changed_option_or_toolchain_misses(tmp_path, monkeypatch):
+    from hawk_amd import compile as C
+    from hawk_amd.emit_hip import plan_kernel
+    cache = tmp_path / "cache"
+    src = plan_kernel(E.scale.program, "scale").source
+    _, key, hit = C.compile_source(src, "scale", cache_dir=cache)
+    assert not hit
+    assert C.compile_source(src, "scale", cache_dir=cache)[2]                       # the same: a hit
+    _, key2, hit2 = C.compile_source(src, "scale", options=C.RTC_OPTIONS + ("-DHAWK_PROBE=1",), cache_dir=cache)
+    assert not hit2 and key2 != key
+    real = C.toolchain()
+    monkeypatch.setattr(C, "toolchain", lambda: real + ";another-comgr")
+    _, key3, hit3 = C.compile_source(src, "scale", cache_dir=cache)
+    assert not hit3 and key3 not in (key, key2)
+
+
+@pytest.mark.parametrize("damage", ["truncate", "flip", "no_record"])
+def test_a_damaged_cache_entry_is_rebuilt_not_loaded(tmp_path, damage):
+    from hawk_amd import compile as C
+    from hawk_amd.emit_hip import plan_kernel
+    cache = tmp_path / "cache"
+    src = plan_kernel(E.energy.program, "energy").source
+    code, key, _ = C.compile_source(src, "energy", cache_dir=cache)
+    obj, record = cache / f"{key}.hsaco", cache / f"{key}.json"
+    if damage == "truncate":
+        obj.write_bytes(code[: len(code) // 2])
+    elif damage == "flip":
+        obj.write_bytes(code[:100] + bytes([code[100] ^ 1]) + code[101:])
+    else:
+        record.unlink()
+    again, key2, hit = C.compile_source(src, "energy", cache_dir=cache)
+    assert not hit and key2 == key and again == code       # rebuilt, the same code object
+    assert obj.read_bytes() == code and C.compile_source(src, "energy", cache_dir=cache)[2]
