@@ -22,9 +22,8 @@ from .emit_hip import fp_ops_per_sample
 from .resources import kernel_resources
 from .emit_hip import plan_kernel
 from .ir import AUTO_K_MAX, FINISHED_PLANE, Finish, HawkError
+from .targets import TARGETS, row
 from .trace import Kernel
-
-TARGETS = ("hip",)
 
 
 @dataclass
@@ -101,7 +100,7 @@ def _chain_record(k, sidecar: dict, mode: str) -> None:
                       f"its fence (1.6 x the estimate {est} + 16): split it into shorter chains", stacklevel=3)
 
 
-def _cut_chains(kernels, mode: str, register_line: int | None) -> tuple:
+def _cut_chains(kernels, mode: str, register_line: int | None, target) -> tuple:
     """``(kernels, chains)``: each chain the cut rule cuts replaced by its
     segments (``<name>__s<i>``), and ``{chain name: its sidecar}``."""
     from .chaining import REGISTER_LINE, cuts, segments
@@ -121,7 +120,7 @@ def _cut_chains(kernels, mode: str, register_line: int | None) -> tuple:
             for w in writes:
                 d = program.decls[w]
                 crossing[w] = {"shape": list(d.ttype.shape), "dtype": d.ttype.dtype}
-        chains[k.name] = {"kernel": k.name, "target": "hip", "offload_arch": "gfx950", "mode": mode,
+        chains[k.name] = {"kernel": k.name, "target": target.id, "offload_arch": target.offload_arch, "mode": mode,
                           "segments": names, "crossing": crossing, "cuts": at,
                           "chain": {"members": [m.name for m in members], "outputs": list(k.outputs)},
                           "planes": planes, "entry": None, "team": []}
@@ -141,12 +140,13 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
     their own and its sidecar lists them in order."""
     if isinstance(kernels, Kernel):
         kernels = [kernels]
-    kernels, chains = _cut_chains(list(kernels), mode, register_line)
     targets = tuple(targets)
     bad = [t for t in targets if t not in TARGETS]
     if bad:
         raise HawkError(f"targets={bad}: this build's target row is 'hip' (gfx950); the reference's host "
                         "and cuda rows are not part of it")
+    (target,) = [row(t) for t in dict.fromkeys(targets)] or [row("hip")]
+    kernels, chains = _cut_chains(list(kernels), mode, register_line, target)
     if block is not None and (block % 64 or not 64 <= block <= 1024):
         raise HawkError(f"block={block}: a multiple of 64 in [64, 1024] (wave64)")
     if per_thread is not None and not 1 <= per_thread <= 64:
@@ -160,7 +160,7 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
     plans = []
     for k in kernels:
         plan = plan_kernel(k.program, k.name, mode=mode, block=block or 256, per_thread=per_thread or 1,
-                           nontemporal=nontemporal, fuse_folds=fuse_folds)
+                           nontemporal=nontemporal, fuse_folds=fuse_folds, target=target)
         shape = (block or 256, per_thread or 1)
         if plan.block is not None:
             shape = (plan.block, 1)
@@ -169,14 +169,14 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
             shape = (block or auto[0], per_thread or auto[1])
             if shape != (256, 1):
                 plan = plan_kernel(k.program, k.name, mode=mode, block=shape[0], per_thread=shape[1],
-                                   nontemporal=nontemporal, fuse_folds=fuse_folds)
+                                   nontemporal=nontemporal, fuse_folds=fuse_folds, target=target)
         plans.append((k, plan, shape))
     staged = [(k, p) for k, p, _ in plans if p.stage is not None]
     compiled = dict(zip([k.name for k, _ in staged],
                         _compile.compile_units([(k.name, p.source) for k, p in staged], cache_dir=cache_dir)))
     for k, plan, shape in plans:
         sidecar = {
-            "kernel": k.name, "target": "hip", "offload_arch": "gfx950", "mode": mode,
+            "kernel": k.name, "target": target.id, "offload_arch": target.offload_arch, "mode": mode,
             "scalar_type": mode, "planes": plan.planes, "team": plan.team,
             "launch": {"block": shape[0], "per_thread": shape[1], "nontemporal": nontemporal},
             "grid": [list(a) for a in k.program.grid.axes] if k.program.grid is not None else None,
@@ -185,13 +185,14 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
         }
         if plan.stage is not None:
             code, key, _hit = compiled[k.name]
-            _write(directory / f"{k.name}.hip", plan.source.encode())
-            _write(directory / f"{k.name}.hsaco", code)
+            _write(directory / f"{k.name}{target.source}", plan.source.encode())
+            _write(directory / f"{k.name}{target.artifact}", code)
             sidecar.update({
                 "entry": k.name,
                 "arg_spec": [list(p) for p in plan.stage.arg_spec],
                 "descriptor": [plan.stage.planes[n]["kind"] for _, n in plan.stage.arg_spec],
-                "source": f"{k.name}.hip", "code_object": f"{k.name}.hsaco",
+                "source": f"{k.name}{target.source}", "code_object": f"{k.name}{target.artifact}",
+                "format": target.format, "entry_kind": target.entry,
                 "source_sha256": hashlib.sha256(plan.source.encode()).hexdigest(),
                 "code_sha256": hashlib.sha256(code).hexdigest(),
                 "cache_key": key, "compile_options": list(_compile.RTC_OPTIONS),
@@ -225,7 +226,7 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
         _write(directory / f"{name}.json", json.dumps(sidecar, indent=1, sort_keys=True).encode())
         artifacts.append(Artifact(name, sidecar))
     digest = hashlib.sha256(json.dumps([a.sidecar for a in artifacts], sort_keys=True).encode()).hexdigest()
-    manifest = {"target": "hip", "offload_arch": "gfx950", "mode": mode, "digest": digest,
+    manifest = {"target": target.id, "offload_arch": target.offload_arch, "mode": mode, "digest": digest,
                 "kernels": [a.name for a in artifacts]}
     _write(directory / "manifest.json", json.dumps(manifest, indent=1, sort_keys=True).encode())
     return Bundle(directory, artifacts, digest)

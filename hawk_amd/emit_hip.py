@@ -35,6 +35,9 @@ from .ir import (FINISHED_PLANE, GUARD_MASK, AccumWrite, Assign, Deps, Finish, H
                  Program, SampleSum, free_inputs,
                  level_order)
 
+from .hip_target import HIP_WRITER, _literal  # noqa: E402  (the hip row's spellings)
+from .targets import TARGETS  # noqa: E402
+
 ABI_TAG = "aether-abi/2"
 LAYOUT_SIZES = (40, 32, 32, 8, 24)
 
@@ -44,10 +47,6 @@ MIRROR_OF = {"out": "gref", "vec_in": "gref", "mat_in": "gref", "per_sample": "h
              "wide_out": "handle", "accum_out": "handle", "rows_out": "handle", "lookup": "handle",
              "uniform": "value"}
 
-_UNARY_C = {"exp": "exp", "sin": "sin", "cos": "cos", "tanh": "tanh", "sqrt": "sqrt",
-            "log": "log", "abs": "fabs"}
-_BINARY_C = {"add": "+", "sub": "-", "mul": "*", "div": "/"}
-_COMPARE_C = {"lt": "<", "le": "<=", "gt": ">", "ge": ">=", "eq": "==", "ne": "!="}
 
 
 def kind_for(role: str, ttype, mode: str) -> str:
@@ -59,15 +58,6 @@ def kind_for(role: str, ttype, mode: str) -> str:
     if shape == "handle" and ttype.dtype in ("i32", "u32"):
         return "int_handle"
     return shape
-
-
-def _literal(x: float) -> str:
-    if math.isnan(x):
-        return "Real(__builtin_nan(\"\"))"
-    if math.isinf(x):
-        return "Real(__builtin_inf())" if x > 0 else "Real(-__builtin_inf())"
-    text = repr(float(x))
-    return f"Real({text})"
 
 
 def _entries(shape: tuple) -> list:
@@ -122,10 +112,11 @@ class _Scope:
 class _Writer:
     """Scalarises nodes into C++ statements."""
 
-    def __init__(self, stage: Stage, mode: str, nontemporal: bool = False):
+    def __init__(self, stage: Stage, mode: str, nontemporal: bool = False, spell=HIP_WRITER):
         self.stage = stage
         self.mode = mode
         self.nontemporal = nontemporal
+        self.spell = spell                   # the target row's writer: every piece of text
         self.lines: list = []
         self.indent = 2
         self.count = 0
@@ -144,11 +135,11 @@ class _Writer:
         return f"hk_{stem}{self.count}"
 
     def ctype(self, dtype: str) -> str:
-        return {"f64": "Real", "f32": "Real", "i64": "long long", "i32": "int", "bool": "bool"}[dtype]
+        return self.spell.ctype(dtype)
 
     def let(self, dtype: str, expr: str, stem: str = "v") -> str:
         name = self.fresh(stem)
-        self.emit(f"const {self.ctype(dtype)} {name} = {expr};")
+        self.emit(self.spell.declare(name, dtype, expr))
         return name
 
     # -- values ------------------------------------------------------------
@@ -181,26 +172,16 @@ class _Writer:
 
     def _leaf(self, n: Node) -> list:
         role, name = n.literal
-        p = self.stage.planes[name]["var"]
+        texts = self.spell.leaf(self, n)
         if role in ("uniform", "lookup"):
-            return [p]                # a value, or a table that `gather` indexes
-        if role == "terminated":      # a mask: one byte a sample
-            return [self.let("bool", f"{p}[hk_i] != 0", "in")]
-        if role == "mutable":         # a prior read of an output plane
-            role = "per_sample" if not n.ttype.shape else ("vec_in" if len(n.ttype.shape) == 1 else "mat_in")
-        dt = n.ttype.dtype
-        if not n.ttype.shape:
-            return [self.let(dt, self.load(f"{p}[hk_i]"), "in")]
-        out = []
-        for e in _entries(n.ttype.shape):
-            c = _flat(n.ttype.shape, e)
-            out.append(self.let(dt, self.load(f"{p}[{c} * {p}_cs + hk_i]"), "in"))
-        return out
+            return texts              # a value, or a table that `gather` indexes
+        dt = "bool" if role == "terminated" else n.ttype.dtype
+        return [self.let(dt, t, "in") for t in texts]
 
     def _lane_axis(self, n: Node) -> list:
         div, mod = n.literal
         if mod == 0:
-            return ["hk_i"]                                  # the flat lane index
+            return [self.spell.sample_index_value()]          # the flat lane index
         q = "hk_i" if div == 1 else f"(hk_i / {div}LL)"
         return [self.let("i32", f"static_cast<int>({q})" if mod is None else f"static_cast<int>({q} % {mod}LL)", "ax")]
 
@@ -232,7 +213,7 @@ class _Writer:
             rest *= e
         flat = None
         for j, (k, e) in enumerate(zip(keys, extents)):
-            extent = f"(static_cast<long long>({p}_n) / {rest}LL)" if e is None else f"{e}LL"
+            extent = f"({self.spell.plane_extent_value(p)} / {rest}LL)" if e is None else f"{e}LL"
             idx = self.let("i64", f"static_cast<long long>({self.scalar(k)})", "k")
             c = self.let("i64", f"{idx} < 0 ? 0LL : ({idx} >= {extent} ? {extent} - 1 : {idx})", "k")
             stride = 1
@@ -250,35 +231,30 @@ class _Writer:
         table = n.operands[0]
         p = self.value(table)[0]
         if n.literal is not None:                      # a Table read: clamped, never out of the plane
-            return [self.let(n.ttype.dtype, f"{p}[{self._clamped_flat(n)}]", "g")]
+            return [self.let(n.ttype.dtype, self.spell.at(self, p, self._clamped_flat(n)), "g")]
         # a scatter target's adjoint: a key outside [0, cells), the skip key -1 included, reads 0
         k = self.scalar(n.operands[1])
-        return [self.let(n.ttype.dtype, f"static_cast<unsigned long long>(static_cast<long long>({k})) < {p}_n"
-                                        f" ? {p}[{k}] : Real(0)", "g")]
+        return [self.let(n.ttype.dtype, self.spell.at(self, p, k, guard_cells=True), "g")]
 
     def load(self, ref: str) -> str:
-        return f"__builtin_nontemporal_load(&{ref})" if self.nontemporal else ref
+        return self.spell.load(self, ref)
 
     def store(self, ref: str, value: str) -> str:
-        return f"__builtin_nontemporal_store({value}, &{ref});" if self.nontemporal else f"{ref} = {value};"
+        return self.spell.store(self, None, ref, value)
 
     def _const(self, n: Node) -> list:
-        return [_literal(n.literal)]
+        return [self.spell.const(n)]
 
-    def _iconst(self, n: Node) -> list:
-        return [f"{int(n.literal)}LL"]
+    _iconst = _const
 
     def _real(self, n: Node) -> list:
-        return [f"Real({x})" for x in self.value(n.operands[0])]
+        return [self.spell.op(self, n, [x]) for x in self.value(n.operands[0])]
 
     def _neg(self, n: Node) -> list:
-        return [self.let(n.ttype.dtype, f"-{x}") for x in self.value(n.operands[0])]
+        return [self.let(n.ttype.dtype, self.spell.op(self, n, [x])) for x in self.value(n.operands[0])]
 
     def _unary(self, n: Node) -> list:
-        fn = _UNARY_C[n.kind]
-        if fn == "tanh" and n.ttype.dtype == "f64":
-            fn = "hk_tanh"
-        return [self.let(n.ttype.dtype, f"{fn}({x})") for x in self.value(n.operands[0])]
+        return [self.let(n.ttype.dtype, self.spell.op(self, n, [x])) for x in self.value(n.operands[0])]
 
     _exp = _sin = _cos = _tanh = _sqrt = _log = _abs = _unary
 
@@ -288,37 +264,39 @@ class _Writer:
         return v * size if len(v) == 1 and size > 1 else v
 
     def _binary(self, n: Node) -> list:
-        op = _BINARY_C[n.kind]
         a, b = self._bcast(n, 0), self._bcast(n, 1)
-        return [self.let(n.ttype.dtype, f"{x} {op} {y}") for x, y in zip(a, b)]
+        return [self.let(n.ttype.dtype, self.spell.op(self, n, [x, y])) for x, y in zip(a, b)]
 
     _add = _sub = _mul = _div = _binary
 
     def _compare(self, n: Node) -> list:
         a, b = self.scalar(n.operands[0]), self.scalar(n.operands[1])
-        return [self.let("bool", f"{a} {_COMPARE_C[n.kind]} {b}", "c")]
+        return [self.let("bool", self.spell.op(self, n, [a, b]), "c")]
 
     _lt = _le = _gt = _ge = _eq = _ne = _compare
 
     def _select(self, n: Node) -> list:
         c = self.scalar(n.operands[0])
         a, b = self.value(n.operands[1]), self.value(n.operands[2])
-        return [self.let(n.ttype.dtype, f"{c} ? {x} : {y}") for x, y in zip(a, b)]
+        return [self.let(n.ttype.dtype, self.spell.select(self, n, c, x, y)) for x, y in zip(a, b)]
 
     def _fold(self, terms: list, dtype: str) -> str:
         acc = terms[0]
         for t in terms[1:]:
-            acc = self.let(dtype, f"{acc} + {t}")
+            acc = self.let(dtype, self.spell.op(self, "add", [acc, t]))
         return acc
+
+    def _mul_text(self, x: str, y: str) -> str:
+        return self.spell.op(self, "mul", [x, y])
 
     def _dot(self, n: Node) -> list:
         a, b = self.value(n.operands[0]), self.value(n.operands[1])
-        prods = [self.let(n.ttype.dtype, f"{x} * {y}") for x, y in zip(a, b)]
+        prods = [self.let(n.ttype.dtype, self._mul_text(x, y)) for x, y in zip(a, b)]
         return [self._fold(prods, n.ttype.dtype)]
 
     def _norm(self, n: Node) -> list:
         a = self.value(n.operands[0])
-        prods = [self.let(n.ttype.dtype, f"{x} * {x}") for x in a]
+        prods = [self.let(n.ttype.dtype, self._mul_text(x, x)) for x in a]
         return [self.let(n.ttype.dtype, f"sqrt({self._fold(prods, n.ttype.dtype)})")]
 
     def _sum(self, n: Node) -> list:
@@ -345,7 +323,7 @@ class _Writer:
         dt = n.ttype.dtype
         out = []
         for i in range(r):
-            prods = [self.let(dt, f"{m[i * c + j]} * {v[j]}") for j in range(c)]
+            prods = [self.let(dt, self._mul_text(m[i * c + j], v[j])) for j in range(c)]
             out.append(self._fold(prods, dt))
         return out
 
@@ -357,13 +335,13 @@ class _Writer:
         out = []
         for i in range(r):
             for j in range(c):
-                prods = [self.let(dt, f"{a[i * k + q]} * {b[q * c + j]}") for q in range(k)]
+                prods = [self.let(dt, self._mul_text(a[i * k + q], b[q * c + j])) for q in range(k)]
                 out.append(self._fold(prods, dt))
         return out
 
     def _outer(self, n: Node) -> list:
         a, b = self.value(n.operands[0]), self.value(n.operands[1])
-        return [self.let(n.ttype.dtype, f"{x} * {y}") for x in a for y in b]
+        return [self.let(n.ttype.dtype, self._mul_text(x, y)) for x in a for y in b]
 
     # -- Cholesky (reference hawk/embedded/linalg.py:233-271) -------------------
     def _chol(self, n: Node) -> list:
@@ -452,7 +430,7 @@ class _Writer:
         for j, c in enumerate(info.carries):
             stem = self.fresh("c")
             names = [f"{stem}_{e}" for e in range(max(1, c.ttype.size if c.ttype.shape else 1))]
-            ct = self.ctype(c.ttype.dtype)
+            ct = self.spell.carry_type(c.ttype)
             for name, init in zip(names, inits[j] * (len(names) if len(inits[j]) == 1 else 1)):
                 self.emit(f"{ct} {name} = {init};")
             carry_vars.append(names)
@@ -461,8 +439,7 @@ class _Writer:
             tapes = []
             for j, names in enumerate(carry_vars):
                 row = [f"hk_tape{n.uid}_{j}_{e}" for e in range(len(names))]
-                ct = self.ctype(info.carries[j].ttype.dtype)
-                self.emit(f"{ct} " + ", ".join(f"{t}[{info.trip}]" for t in row) + ";")
+                self.emit(self.spell.tape_decl(self.spell.carry_type(info.carries[j].ttype), row, info.trip))
                 tapes.append(row)
             self.tape_of = getattr(self, "tape_of", {})
             self.tape_of[n.uid] = (tapes, info.start, info.step)
@@ -476,15 +453,15 @@ class _Writer:
             # clamps it below INT_MAX; a word below 0 runs none)
             word = self.stage.planes[info.count]["var"]
             self.emit(f"const long long hk_cnt{n.uid} = static_cast<long long>({word}[0]);")
-            self.emit(f"long long hk_trips{n.uid} = 0;")
+            self.emit(self.spell.counter_decl(f"hk_trips{n.uid}"))
             self.trips[n.uid] = f"hk_trips{n.uid}"
-            self.emit(f"for (long long {k} = 0LL; {k} < hk_cnt{n.uid}; ++{k}) {{")
+            self.emit(self.spell.for_header(self, k, info, f"hk_cnt{n.uid}"))
         else:
             if info.unroll is True:
                 self.emit("#pragma unroll")
             elif info.unroll is False:
                 self.emit("#pragma unroll 1")
-            self.emit(f"for (long long {k} = {info.start}LL; {k} != {info.stop()}LL; {k} += {info.step}LL) {{")
+            self.emit(self.spell.for_header(self, k, info, None))
         self.indent += 1
         self.scope.memo.append({})
         self.scope.put(info.index, [k])
@@ -494,7 +471,7 @@ class _Writer:
             slot = f"(({k} - {info.start}LL) / {info.step}LL)"
             for row, names in zip(tapes, carry_vars):
                 for t, v in zip(row, names):
-                    self.emit(f"{t}[{slot}] = {v};")
+                    self.emit(self.spell.tape_write(self, t, slot, v))
         self.run(ir.body_roots(info))
         nexts = [self.value(x) for x in info.nexts]
         leave = None
@@ -516,7 +493,7 @@ class _Writer:
         if info.count is not None:
             self.emit(f"++hk_trips{n.uid};")
         if leave is not None:         # a tail break: this trip's values stand
-            self.emit(f"if ({leave}) {{ {exited} = true; break; }}")
+            self.emit(self.spell.tail_break(leave, exited))
         self.scope.memo.pop()
         self.indent -= 1
         self.emit("}")
@@ -624,14 +601,17 @@ def component_planes(stage: Stage) -> int:
 
 
 def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_taped: bool = True,
-                 nontemporal: bool = False, xcd_order: bool | None = None) -> str:
+                 nontemporal: bool = False, xcd_order: bool | None = None, target=None) -> str:
     """The HIP source of one per-sample stage.  ``nontemporal`` marks the
     plane loads and stores as streaming (read or written once, not kept in
     cache); ``xcd_order`` (default: at least ``XCD_ORDER_PLANES`` component
-    planes) hands each XCD a contiguous eighth of the blocks."""
+    planes) hands each XCD a contiguous eighth of the blocks.  ``target`` is
+    the row whose writer spells the body and whose wrapper makes the entry
+    (default: the ``hip`` row)."""
+    target = TARGETS["hip"] if target is None else target
     if xcd_order is None:
         xcd_order = component_planes(stage) >= XCD_ORDER_PLANES
-    w = _Writer(stage, mode, nontemporal)
+    w = _Writer(stage, mode, nontemporal, spell=target.writer)
     roots = ([node for _, node in stage.writes] + [node for _, node, _, _ in stage.row_sums]
              + [node for _, nodes, _ in stage.key_writes for node in nodes]
              + [node for f in stage.fused_folds for node in tuple(f[2]) + tuple(f[3])]
@@ -665,11 +645,11 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         var = info["var"]
         vals = w.value(node)
         if not node.ttype.shape:
-            w.emit(w.store(f"{var}[hk_i]", vals[0]))
+            w.emit(w.spell.component_commit(w, var, None, "=", vals[0]))
         else:
             for e in _entries(node.ttype.shape):
                 c = _flat(node.ttype.shape, e)
-                w.emit(w.store(f"{var}[{c} * {var}_cs + hk_i]", vals[c]))
+                w.emit(w.spell.component_commit(w, var, c, "=", vals[c]))
     for plane, nodes, group in stage.key_writes:
         # every lane of a key stores the key's one value (a wave's equal
         # addresses merge into one write)
@@ -690,29 +670,8 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         body = _place_fold_stores(body, folds, block)
 
     real = "float" if mode == "float32" else "double"
-    params, unpack = [], []
-    for role, name in stage.arg_spec:
-        info = stage.planes[name]
-        var = info["var"]
-        kind = info["kind"]
-        if kind in ("f64", "f32"):
-            params.append(f"Real {var}")
-            continue
-        is_input = role not in ("mutable", "out", "wide_out", "key_out", "accum_out", "rows_out", "fold_scratch")
-        if stage.finish is not None and name in stage.finish[:2]:
-            is_input = False          # the mask a finish sets and its counter
-        cq = "const " if is_input else ""
-        elem = {"i32": "int", "u32": "unsigned int", "bool": "unsigned char"}.get(info["dtype"], "Real")
-        if kind == "gref":
-            params.append(f"GRefMirror {var}_m")
-            unpack.append(f"{cq}{elem}* __restrict__ {var} = reinterpret_cast<{cq}{elem}*>({var}_m.data_);")
-            unpack.append(f"const long long {var}_cs = static_cast<long long>({var}_m.compStride_);")
-        else:
-            params.append(f"ScalarHandle {var}_m")
-            unpack.append(f"{cq}{elem}* __restrict__ {var} = reinterpret_cast<{cq}{elem}*>({var}_m.data);")
-            if role in ("lookup", "accum_out", "fold_scratch"):
-                unpack.append(f"const unsigned long long {var}_n = {var}_m.samples;   // cells")
-    params += ["long long base", "long long count", "long long nSamples"]
+    wrap = target.wrapper
+    params, unpack = wrap.params(stage), wrap.unpack(stage)
     out = [
         f"// hawk gfx950 stage '{stage.name}' (generated; mode {'banded' if stage.banded else mode}).",
         f"typedef {real} Real;",
@@ -732,50 +691,26 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += _FOLD_HELPERS.splitlines()
     if stage.finish is not None:
         out += _FINISH_HELPER.splitlines()
-    out += [
-        f'extern "C" __global__ void __launch_bounds__({block}) {stage.name}(',
-        "        " + ",\n        ".join(params) + ") {",
-        "    (void)nSamples;",
-    ]
+    out += wrap.entry_signature(stage, stage.name, block, params)
     out += ["    " + u for u in unpack]
-    if xcd_order:
-        # Workgroup i runs on XCD i % 8: with a grid of 8k workgroups, XCD x
-        # takes the contiguous blocks [x*k, (x+1)*k) (any other grid keeps the
-        # plain order), so each XCD's L2 streams one contiguous eighth.
-        out += ["    const unsigned hk_blk = (gridDim.x & 7u) ? blockIdx.x"
-                " : (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3);"]
-    else:
-        out += ["    const unsigned hk_blk = blockIdx.x;"]
-    out += [
-        "#pragma unroll",
-        f"    for (int hk_v = 0; hk_v < {per_thread}; ++hk_v) {{",
-        f"        const long long hk_flat = (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * {block}"
-        " + static_cast<long long>(threadIdx.x);",
-    ]
     auto = _auto_loop(stage)
     if stage.guard is not None:
+        out += wrap.index_prologue(block, per_thread, xcd_order, form="guard")
         out += _guarded_lines(stage, w, body, stores)
     elif not row_terms and not folds:
-        out += ["        if (hk_flat >= count) break;",
-                "        const long long hk_i = base + hk_flat;"]
+        out += wrap.index_prologue(block, per_thread, xcd_order, form="plain")
         out += body + stores
     else:
         # Every lane of a half-wave takes part in its row's butterfly: a lane
         # past `count` computes sample `base` (always bound) and adds +0.
-        out += ["        const bool hk_live = hk_flat < count;",
-                "        const long long hk_i = base + (hk_live ? hk_flat : 0LL);"]
+        out += wrap.index_prologue(block, per_thread, xcd_order, form="live")
         out += body
-        out += ["        if (hk_live) {"] + ["    " + line for line in stores] + ["        }"]
+        opened, closed = wrap.sample_sum_frame(len(row_terms), "double", "")
+        out += opened + ["    " + line for line in stores] + closed
         for k, (term, hi, comp) in enumerate(row_terms):
-            out += [f"        {{ double hk_rh = hk_live ? static_cast<double>({term}) : 0.0, hk_rc = 0.0;",
-                    f"          {'hk_band_row_sum' if stage.banded else 'hk_row_sum'}(hk_rh, hk_rc);",
-                    "          if ((threadIdx.x & 31) == 0 && hk_live) {",
-                    "              const long long hk_r = (base + hk_flat) >> 5;",
-                    f"              {hi}[hk_r] = hk_rh;",
-                    f"              {comp}[hk_r] = hk_rc;",
-                    "          } }"]
+            out += w.spell.sample_sum(w, stage.banded, term, hi, comp)
         out += _fused_fold_lines(folds, block, whole)
-    out += ["    }", "}", ""]
+    out += wrap.index_epilogue()
     if auto is not None:
         head = out.index(f'extern "C" __global__ void __launch_bounds__({block}) {stage.name}(')
         top = out[:head]
@@ -807,11 +742,11 @@ def _guarded_lines(stage: Stage, w: _Writer, body: list, stores: list, fast: boo
            "        const long long hk_i = base + (hk_in ? hk_flat : 0LL);"]
     if stage.finish is not None:
         out += ["        bool hk_new = false;"]
-    out += [f"        if (hk_in && {mask}[hk_i] == 0) {{"]
+    out += [f"        if ({w.spell.guard([mask])}) {{"]
     out += ["    " + line for line in body + stores]
     if stage.finish is not None:
         cond = w.value(stage.finish[2])[0]
-        out += [f"            if ({cond}) {{ {mask}[hk_i] = 1; hk_new = true; }}"]
+        out += [w.spell.finish(w, mask, cond)]
     if fast:
         loop = _auto_loop(stage)
         out += [f"            hk_ran = hk_ran > static_cast<unsigned>({w.trips[loop.uid]}) ? hk_ran"
@@ -1402,15 +1337,18 @@ def _refuse_unbanded(program: Program, name: str) -> None:
 
 def plan_kernel(program: Program, name: str, mode: str = "float64", block: int = 256,
                 per_thread: int = 1, nontemporal: bool = False, reuse_carries: bool = True,
-                fuse_folds: bool = True) -> Plan:
+                fuse_folds: bool = True, target=None) -> Plan:
     """Split ``program`` into its per-sample stage and team stages, and render
     the per-sample stage.  With ``reuse_carries``, a loop's value that its next
     iteration would compute again is carried instead (:func:`ir.carry_repeats`);
     ``Plan.algorithmic_ops`` still counts the program as traced.  With
     ``fuse_folds``, an ordered fold whose keys fit a block (:func:`fold_block`)
     is done by the stage in LDS; otherwise the stage logs and a team stage folds."""
-    if mode not in ("float64", "float32", "banded"):
-        raise HawkError(f"mode={mode!r}: the hip target builds 'float64', 'float32' or 'banded'")
+    target = TARGETS["hip"] if target is None else target
+    if mode not in target.modes:
+        said = [repr(m) for m in target.modes]
+        said = said[0] if len(said) == 1 else ", ".join(said[:-1]) + " or " + said[-1]
+        raise HawkError(f"mode={mode!r}: the {target.id} target builds {said}")
     banded = mode == "banded"
     if banded:
         _refuse_unbanded(program, name)
@@ -1418,9 +1356,9 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
         reused = _carry_repeats(program)
         if reused is not program:
             traced = plan_kernel(program, name, mode, block, per_thread, nontemporal, reuse_carries=False,
-                                 fuse_folds=fuse_folds)
+                                 fuse_folds=fuse_folds, target=target)
             plan = plan_kernel(reused, name, mode, block, per_thread, nontemporal, reuse_carries=False,
-                               fuse_folds=fuse_folds)
+                               fuse_folds=fuse_folds, target=target)
             plan.algorithmic_ops = traced.algorithmic_ops
             return plan
     if banded:
@@ -1498,7 +1436,7 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
     if has_stage:
         stage = _stage_planes(program, name, mode, extra, row_sums, key_writes, fused)
         stage.banded = banded
-        source = render_stage(stage, mode, block, per_thread, nontemporal=nontemporal)
+        source = render_stage(stage, mode, block, per_thread, nontemporal=nontemporal, target=target)
     planes = {}
     if stage is not None:
         for pname, info in stage.planes.items():

@@ -1,0 +1,345 @@
+"""The ``hip`` row's writer and wrapper: every piece of gfx950 HIP text the
+per-sample renderer (:class:`hawk_amd.emit_hip._Writer`, the traversal) emits.
+
+The reference splits its emitter the same way (``hawk/emit/writer.py``: a
+writer spells each construct, ``WRITER_MEMBERS``; ``hawk/emit/wrapper.py:225-284``:
+a wrapper wraps a body for one execution model), and a target row pairs one
+of each (``hawk/targets/__init__.py:37-71``).  These two objects are that
+pair for MI355X: :data:`HIP_WRITER` answers every member of the reference's
+writer seam and :data:`HIP_WRAPPER` every member of its wrapper seam, over
+this repository's IR.  A construct this build has no form for (the
+reference's multi-branch dispatch, a scattered store from the per-sample
+stage: scatters here are team stages) is refused by name.
+
+Members take already-rendered operand text and return text; ``r`` is the
+renderer, whose ``let`` / ``emit`` / ``stage`` the writer uses as the
+reference's writers use their renderer's ``_emit`` and walk.
+"""
+
+from __future__ import annotations
+
+import math
+
+from .ir import HawkError, Node
+
+#: The reference's writer seam, member for member (``hawk/emit/writer.py:29-38``).
+WRITER_MEMBERS = (
+    "declare", "carry_type", "tape_decl", "counter_decl", "for_header",
+    "tail_break", "sample_index_value", "plane_extent_value", "hoist",
+    "selector_decl", "mix_count", "predicated_rank0", "predicated_tensor",
+    "switch_default_tail", "typed_zero",
+    "leaf", "const", "at", "select", "op",
+    "guard", "store", "scatter_store", "accum_scattered", "or_scattered", "store_compensated",
+    "sample_sum", "tape_write", "finish", "exit_if",
+    "component_commit", "in_place_accumulate", "zero_row",
+)
+#: The reference's wrapper seam (``hawk/emit/wrapper.py:225-284``).
+WRAPPER_MEMBERS = ("qualifier", "entry_signature", "index_prologue", "index_epilogue", "unpack", "fold_rows",
+                   "sample_sum_frame", "dispatch")
+
+_UNARY = {"exp": "exp", "sin": "sin", "cos": "cos", "tanh": "tanh", "sqrt": "sqrt", "log": "log",
+          "abs": "fabs"}
+_BINARY = {"add": "+", "sub": "-", "mul": "*", "div": "/"}
+_COMPARE = {"lt": "<", "le": "<=", "gt": ">", "ge": ">=", "eq": "==", "ne": "!="}
+_CTYPES = {"f64": "Real", "f32": "Real", "i64": "long long", "i32": "int", "bool": "bool"}
+
+
+def _literal(x: float) -> str:
+    if math.isnan(x):
+        return "Real(__builtin_nan(\"\"))"
+    if math.isinf(x):
+        return "Real(__builtin_inf())" if x > 0 else "Real(-__builtin_inf())"
+    return f"Real({repr(float(x))})"
+
+
+def _dtype(ttype) -> str:
+    return ttype if isinstance(ttype, str) else ttype.dtype
+
+
+def _refuse(what: str):
+    raise HawkError(f"the hip target has no form for {what} in this build")
+
+
+class HipWriter:
+    """gfx950 HIP spellings (``Real`` is ``double`` or ``float`` by the
+    build's mode; fp64 ``tanh`` is the emitted ``hk_tanh``)."""
+
+    id = "hip"
+    #: Every component of a tensor value is a named local of its own.
+    names_every_tensor = True
+    #: A vector is stored one component at a time.
+    commits_per_component = True
+    #: No library twins: every site is scalarised.
+    rolled_forms = False
+
+    # -- declarations and loops ------------------------------------------
+    def ctype(self, ttype) -> str:
+        return _CTYPES[_dtype(ttype)]
+
+    def declare(self, name: str, ttype, text: str, ordered: bool = True, held: bool = False) -> str:
+        return f"const {self.ctype(ttype)} {name} = {text};"
+
+    def reads_raw(self, kind: str) -> bool:
+        return False
+
+    def carry_type(self, ttype) -> str:
+        return self.ctype(ttype)
+
+    def tape_decl(self, elem: str, name, trip: int) -> str:
+        names = [name] if isinstance(name, str) else list(name)
+        return f"{elem} " + ", ".join(f"{t}[{trip}]" for t in names) + ";"
+
+    def counter_decl(self, counter: str) -> str:
+        return f"long long {counter} = 0;"
+
+    def for_header(self, r, index: str, loop, count: str | None) -> str:
+        if count is not None:
+            return f"for (long long {index} = 0LL; {index} < {count}; ++{index}) {{"
+        return (f"for (long long {index} = {loop.start}LL; {index} != {loop.stop()}LL; "
+                f"{index} += {loop.step}LL) {{")
+
+    def tail_break(self, flag: str, exited: str | None = None) -> str:
+        return f"if ({flag}) {{ {exited} = true; break; }}" if exited else f"if ({flag}) break;"
+
+    def exit_if(self, cond: str) -> str:
+        return f"if ({cond}) {{"
+
+    def sample_index_value(self) -> str:
+        return "hk_i"
+
+    def plane_extent_value(self, var: str) -> str:
+        return f"static_cast<long long>({var}_n)"
+
+    def hoist(self, r, text: str, ttype) -> str:
+        return r.let(_dtype(ttype), text)
+
+    # -- dispatch (the reference's multi-branch kernels: not in this build) --
+    def selector_decl(self, r, kname: str, kind_expr: str, k: int, *, in_range: bool = False) -> str:
+        _refuse("a multi-branch dispatch selector")
+
+    def mix_count(self, mix: str, k: int, kname: str) -> str:
+        _refuse("a dispatch branch-mix count")
+
+    def predicated_rank0(self, kname: str, texts) -> str:
+        _refuse("a predicated dispatch")
+
+    def predicated_tensor(self, r, kname: str, texts) -> str:
+        _refuse("a predicated dispatch")
+
+    def switch_default_tail(self) -> str:
+        return ""
+
+    def typed_zero(self, ttype) -> str:
+        return "Real(0)" if _dtype(ttype) in ("f64", "f32") else f"static_cast<{self.ctype(ttype)}>(0)"
+
+    # -- expressions -------------------------------------------------------
+    def leaf(self, r, leaf: Node, materialised: bool = True) -> list:
+        """A plane's element(s) at the lane's sample: one load per component
+        (component c of a plane at ``c * compStride + i``); a mask reads its
+        byte; a uniform or a table is its binding itself."""
+        role, name = leaf.literal
+        p = r.stage.planes[name]["var"]
+        if role in ("uniform", "lookup"):
+            return [p]
+        if role == "terminated":
+            return [f"{p}[hk_i] != 0"]
+        from .emit_hip import _entries, _flat
+        if not leaf.ttype.shape:
+            return [self.load(r, f"{p}[hk_i]")]
+        return [self.load(r, f"{p}[{_flat(leaf.ttype.shape, e)} * {p}_cs + hk_i]")
+                for e in _entries(leaf.ttype.shape)]
+
+    def load(self, r, ref: str) -> str:
+        return f"__builtin_nontemporal_load(&{ref})" if r.nontemporal else ref
+
+    def const(self, node: Node) -> str:
+        if node.kind == "iconst":
+            return f"{int(node.literal)}LL"
+        return _literal(node.literal)
+
+    def at(self, r, table: str, cell: str, guard_cells: bool = False) -> str:
+        """A plane read at a computed index: a Table's clamped cell, or (``guard_cells``)
+        a scatter target's adjoint at the key, 0 outside ``[0, cells)``."""
+        if guard_cells:
+            return (f"static_cast<unsigned long long>(static_cast<long long>({cell})) < {table}_n"
+                    f" ? {table}[{cell}] : Real(0)")
+        return f"{table}[{cell}]"
+
+    def select(self, r, node, c: str, a: str, b: str) -> str:
+        return f"{c} ? {a} : {b}"
+
+    def op(self, r, node, args, ranks=()) -> str:
+        """One scalar operation: ``+ - * /`` infix, comparisons, negation,
+        the math calls (fp64 tanh as ``hk_tanh``), ``Real(x)`` casts."""
+        k = node.kind if isinstance(node, Node) else node
+        if k in _BINARY:
+            return f"{args[0]} {_BINARY[k]} {args[1]}"
+        if k in _COMPARE:
+            return f"{args[0]} {_COMPARE[k]} {args[1]}"
+        if k == "neg":
+            return f"-{args[0]}"
+        if k == "real":
+            return f"Real({args[0]})"
+        if k in _UNARY:
+            fn = _UNARY[k]
+            dtype = node.ttype.dtype if isinstance(node, Node) else "f64"
+            if fn == "tanh" and dtype == "f64":
+                fn = "hk_tanh"
+            return f"{fn}({args[0]})"
+        _refuse(f"the operation {k!r}")
+
+    # -- sinks and the guard -----------------------------------------------
+    def guard(self, bound) -> str | None:
+        """The body-wide mask condition: the lane has a sample and its mask is clear."""
+        if not bound:
+            return None
+        return " && ".join(["hk_in"] + [f"{m}[hk_i] == 0" for m in bound])
+
+    def store(self, r, sink, target: str, value: str) -> str:
+        """An own-lane store (non-temporal when the build streams)."""
+        if r.nontemporal:
+            return f"__builtin_nontemporal_store({value}, &{target});"
+        return f"{target} = {value};"
+
+    def scatter_store(self, r, sink, target: str, index: str, value: str) -> None:
+        _refuse("a scattered store from the per-sample stage (hawk.scatter builds as an ordered team stage)")
+
+    def accum_scattered(self, r, sink, target: str, index: str, value: str) -> None:
+        _refuse("an atomic accumulate (hawk.scatter policy 'plain'); the ordered policy is a team stage")
+
+    def or_scattered(self, r, sink, target: str, index: str, value: str) -> None:
+        _refuse("a scattered OR commit (policy 'or')")
+
+    def store_compensated(self, r, sink, target: str, comp: str, value: str) -> None:
+        _refuse("a compensated scattered commit")
+
+    def sample_sum(self, r, banded: bool, term: str, hi: str, comp: str) -> list:
+        """A default-policy ``hawk.sum``'s row: the lane's term joins its
+        half-wave's row of 32 (compensated pairs, or double-double bands in
+        the banded mode; a lane past ``count`` adds +0) and lane 0 of the half
+        stores the row."""
+        return [f"        {{ double hk_rh = hk_live ? static_cast<double>({term}) : 0.0, hk_rc = 0.0;",
+                f"          {'hk_band_row_sum' if banded else 'hk_row_sum'}(hk_rh, hk_rc);",
+                "          if ((threadIdx.x & 31) == 0 && hk_live) {",
+                "              const long long hk_r = (base + hk_flat) >> 5;",
+                f"              {hi}[hk_r] = hk_rh;",
+                f"              {comp}[hk_r] = hk_rc;",
+                "          } }"]
+
+    def tape_write(self, r, tape: str, slot: str, value: str) -> str:
+        return f"{tape}[{slot}] = {value};"
+
+    def finish(self, r, mask: str, cond: str) -> str:
+        """Mark the sample finished and count it once."""
+        return f"            if ({cond}) {{ {mask}[hk_i] = 1; hk_new = true; }}"
+
+    def component_commit(self, r, target: str, at, op: str, value: str) -> str:
+        ref = f"{target}[hk_i]" if at is None else f"{target}[{at} * {target}_cs + hk_i]"
+        if op == "=":
+            return self.store(r, None, ref, value)
+        return f"{ref} {op} {value};"
+
+    def in_place_accumulate(self, r, target: str, k: str, value: str) -> str:
+        _refuse("an accumulate into a plane row inside a lowered loop")
+
+    def zero_row(self, r, target: str, width: int) -> str:
+        _refuse("a zeroed plane row ahead of a lowered loop")
+
+
+class HipWrapper:
+    """How a per-sample stage is wrapped for the gfx950 launch: the entry's
+    signature (one by-value mirror per slot in ``arg_spec`` order, then the
+    partition triple, reference ``hawk/emit/cuda.py:46-54``), the unpacking of
+    the mirrors, and the one geometry seam (``i = base + flat``)."""
+
+    qualifier = "__device__ __forceinline__"
+
+    def params(self, stage) -> list:
+        out = []
+        for role, name in stage.arg_spec:
+            info = stage.planes[name]
+            var = info["var"]
+            if info["kind"] in ("f64", "f32"):
+                out.append(f"Real {var}")
+            elif info["kind"] == "gref":
+                out.append(f"GRefMirror {var}_m")
+            else:
+                out.append(f"ScalarHandle {var}_m")
+        return out + ["long long base", "long long count", "long long nSamples"]
+
+    def entry_signature(self, stage, name: str, block: int, params: list | None = None) -> list:
+        params = self.params(stage) if params is None else params
+        return [f'extern "C" __global__ void __launch_bounds__({block}) {name}(',
+                "        " + ",\n        ".join(params) + ") {",
+                "    (void)nSamples;"]
+
+    def unpack(self, stage) -> list:
+        """Each mirror's pointer (and component stride, and a table's cells)."""
+        out = []
+        for role, name in stage.arg_spec:
+            info = stage.planes[name]
+            var, kind = info["var"], info["kind"]
+            if kind in ("f64", "f32"):
+                continue
+            is_input = role not in ("mutable", "out", "wide_out", "key_out", "accum_out", "rows_out",
+                                    "fold_scratch")
+            if stage.finish is not None and name in stage.finish[:2]:
+                is_input = False          # the mask a finish sets and its counter
+            cq = "const " if is_input else ""
+            elem = {"i32": "int", "u32": "unsigned int", "bool": "unsigned char"}.get(info["dtype"], "Real")
+            if kind == "gref":
+                out.append(f"{cq}{elem}* __restrict__ {var} = reinterpret_cast<{cq}{elem}*>({var}_m.data_);")
+                out.append(f"const long long {var}_cs = static_cast<long long>({var}_m.compStride_);")
+            else:
+                out.append(f"{cq}{elem}* __restrict__ {var} = reinterpret_cast<{cq}{elem}*>({var}_m.data);")
+                if role in ("lookup", "accum_out", "fold_scratch"):
+                    out.append(f"const unsigned long long {var}_n = {var}_m.samples;   // cells")
+        return out
+
+    def index_prologue(self, block: int, per_thread: int, xcd_order: bool, form: str = "plain") -> list:
+        """The launch geometry: block ``i`` of the grid (XCD x takes a
+        contiguous eighth when ``xcd_order``), ``per_thread`` samples a thread,
+        and the lane's sample ``hk_i = base + hk_flat``.  ``form``: "plain" (a
+        lane past ``count`` leaves), "live" (it computes sample ``base`` and
+        stores nothing: a row sum or a fold needs every lane), "guard" (the
+        guarded stage binds ``hk_i`` itself)."""
+        if xcd_order:
+            # Workgroup i runs on XCD i % 8: with a grid of 8k workgroups, XCD x
+            # takes the contiguous blocks [x*k, (x+1)*k) (any other grid keeps the
+            # plain order), so each XCD's L2 streams one contiguous eighth.
+            out = ["    const unsigned hk_blk = (gridDim.x & 7u) ? blockIdx.x"
+                   " : (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3);"]
+        else:
+            out = ["    const unsigned hk_blk = blockIdx.x;"]
+        out += ["#pragma unroll",
+                f"    for (int hk_v = 0; hk_v < {per_thread}; ++hk_v) {{",
+                f"        const long long hk_flat = (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * {block}"
+                " + static_cast<long long>(threadIdx.x);"]
+        if form == "plain":
+            out += ["        if (hk_flat >= count) break;",
+                    "        const long long hk_i = base + hk_flat;"]
+        elif form == "live":
+            out += ["        const bool hk_live = hk_flat < count;",
+                    "        const long long hk_i = base + (hk_live ? hk_flat : 0LL);"]
+        return out
+
+    def index_epilogue(self) -> list:
+        return ["    }", "}", ""]
+
+    def fold_rows(self, width: int) -> int:
+        """Rows of 32 samples a wave64 reduces at once: a half-wave is a row."""
+        return 2
+
+    def sample_sum_frame(self, width: int, elem: str, store: str, op: str = "sum", live: str | None = None) -> tuple:
+        """(open, close) around the row sums of a stage: every lane takes part
+        (``hk_live``), the stores of a live lane only."""
+        if op != "sum":
+            _refuse(f"a sample reduction by {op!r}")
+        return (["        if (hk_live) {"], ["        }"])
+
+    def dispatch(self, kind_spelling: str, branch_spellings, policy: str, **kw) -> str:
+        _refuse("a multi-branch dispatch")
+
+
+HIP_WRITER = HipWriter()
+HIP_WRAPPER = HipWrapper()

@@ -80,7 +80,9 @@ class DeviceKernel:
     """One kernel of a built unit, loaded for the gfx950 target."""
 
     def __init__(self, directory: Path, sidecar: dict):
-        if sidecar.get("target") != "hip":
+        from .targets import ENTRY_DEVICE, TARGETS
+        built_for = TARGETS.get(sidecar.get("target"))
+        if built_for is None or built_for.entry != ENTRY_DEVICE:
             raise HawkError(f"{sidecar.get('kernel')!r} was not built for the hip target")
         self.directory = Path(directory)
         self.sidecar = sidecar
