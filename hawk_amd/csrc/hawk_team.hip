@@ -680,16 +680,14 @@ __global__ __launch_bounds__(256) void hawk_keyed_small(const double* __restrict
 //
 // parts[b][k] is the in-lane-order sum (from +0.0) of chunk b's values with
 // key k; cell k then adds parts[0][k], parts[1][k], ... in chunk order from
-// +0.0 and adds that onto target[k].  One 1024-thread workgroup walks one
-// chunk in tiles of 4096 lanes: each tile is sorted stably by key in LDS (LSD
-// radix, 8-bit digits), so every key's lanes form one run in lane order, and
-// the run's owner thread adds them one by one onto the key's accumulator —
-// the additions the serial walk makes, in its order.  Accumulators of keys
-// below kAccKeys live in LDS, the others in parts[b] (L2-resident: only this
-// workgroup touches that row).  A per-chunk bitmap of touched keys replaces a
-// zero fill of parts: an untouched (chunk, key) is skipped by the cell pass,
-// which is exact because a sum that starts at +0.0 is never -0.0, so adding
-// the +0.0 the serial walk would add changes nothing.
+// +0.0 and adds that onto target[k].  Up to 65536 cells the split walk below
+// makes those additions.  Past that, one 1024-thread workgroup walks one chunk
+// in tiles of 4096 lanes: each tile is sorted stably by key in LDS (LSD radix,
+// 8-bit digits), so every key's lanes form one run in lane order, and the
+// run's owner thread adds them one by one onto the key's accumulator — the
+// additions the serial walk makes, in its order.  Accumulators of keys below
+// kAccKeys live in LDS, the others in the zero-filled parts[b] (only this
+// workgroup touches that row).
 // ---------------------------------------------------------------------------
 constexpr int kScatterChunks = 256;    // reference hawk/_lane_bind.py:108
 constexpr int kWalkThreads = 1024;
@@ -704,8 +702,6 @@ constexpr int kDigitBits = 8;
 constexpr int kDigits = 1 << kDigitBits;
 constexpr int kHistRow = kWalkWaves + 1;          // one digit's per-wave counts, padded: rows in different banks
 constexpr int kAccKeys = 4096;                     // keys whose accumulators live in LDS
-constexpr long long kSeenCells = 65536;            // a touched bitmap up to this many cells
-constexpr int kSeenWords = static_cast<int>(kSeenCells / 32);
 constexpr int kFoldUnroll = 8;
 
 static_assert(kTile == 1 << kPosBits, "tile positions fill the position field");
@@ -733,7 +729,6 @@ struct WalkShared {
         double sv[kTile];                             //         the tile's values in sorted order (fold)
     };
     double acc[kAccKeys];                             // 32 KiB: accumulators of keys < kAccKeys
-    unsigned seen[kSeenWords];                        //  8 KiB: keys this chunk has touched
     unsigned long long starts[kTile / 64];            // run heads of the sorted tile
     unsigned wsum[kWalkWaves];
 };
@@ -867,14 +862,11 @@ __device__ __forceinline__ void acc_store(double* p, double x) {
     __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One workgroup per chunk b: lanes [b*span, min((b+1)*span, n)).  With
-// use_seen, keys are below kSeenCells, parts[b] is never zero-filled and the
-// touched bitmap goes to touched[b]; without it parts arrives zero-filled and
-// every accumulator is read.
+// One workgroup per chunk b: lanes [b*span, min((b+1)*span, n)); parts
+// arrives zero-filled.
 __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
         const int* __restrict__ key, const double* __restrict__ v, long long n, long long cells, long long span,
-        int key_bits, int use_seen, double* __restrict__ parts, unsigned* __restrict__ touched,
-        int* __restrict__ status) {
+        int key_bits, double* __restrict__ parts, int* __restrict__ status) {
     __shared__ WalkShared sh;
     const int t = threadIdx.x;
     const int wave = t >> 6;
@@ -883,13 +875,11 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
     const long long lo = static_cast<long long>(b) * span;
     const long long hi = lo + span < n ? lo + span : n;
     const int acc_n = cells < kAccKeys ? static_cast<int>(cells) : kAccKeys;
-    const int words = use_seen ? static_cast<int>((cells + 31) / 32) : 0;
     const unsigned kmask = (1u << key_bits) - 1u;
     const unsigned sentinel = kmask;          // the key field of an invalid lane
     double* row = parts + static_cast<long long>(b) * cells;
 
     for (int k = t; k < acc_n; k += kWalkThreads) sh.acc[k] = 0.0;
-    for (int i = t; i < words; i += kWalkThreads) sh.seen[i] = 0u;
     bool bad = false;
     int nk[kWalkItems];
     double nv[kWalkItems];
@@ -943,7 +933,7 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
             if (!head[j] || rk[j] >= cells) continue;
             re[j] = next_head(sh, rs[j]);
             const unsigned k = rk[j];
-            load[j] = k >= static_cast<unsigned>(acc_n) && (!use_seen || ((sh.seen[k >> 5] >> (k & 31)) & 1u));
+            load[j] = k >= static_cast<unsigned>(acc_n);
         }
         double ra[kWalkItems];
 #pragma unroll
@@ -972,13 +962,10 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
             if (!any) continue;
             if (k < static_cast<unsigned>(acc_n)) sh.acc[k] = a;
             else acc_store(row + k, a);
-            if (use_seen) atomicOr(&sh.seen[k >> 5], 1u << (k & 31));
         }
         __syncthreads();
     }
-    for (int k = t; k < acc_n; k += kWalkThreads)
-        if (!use_seen || ((sh.seen[k >> 5] >> (k & 31)) & 1u)) row[k] = sh.acc[k];
-    for (int i = t; i < words; i += kWalkThreads) touched[static_cast<long long>(b) * words + i] = sh.seen[i];
+    for (int k = t; k < acc_n; k += kWalkThreads) row[k] = sh.acc[k];
     if (bad) status[1 + b] = 1;
 }
 
@@ -1009,35 +996,37 @@ __global__ __launch_bounds__(256) void hawk_fill_zero(double* __restrict__ p, lo
 }
 
 // Cell c adds its chunk partials in chunk order from +0.0, then onto the
-// target: target[c] += sum (reference hawk/emit/team.py:437-460).  With a
-// touched bitmap, a (chunk, cell) the walk never touched holds no partial and
-// is skipped (its +0.0 would change nothing).
-__global__ __launch_bounds__(256) void hawk_scatter_cells(const double* __restrict__ parts,
-                                                          const unsigned* __restrict__ touched, long long cells,
-                                                          int chunks, int use_seen, double* __restrict__ target) {
+// target: target[c] += sum (reference hawk/emit/team.py:437-460).  Two blocks
+// of kAhead chunks are in flight while a third is added.
+__global__ __launch_bounds__(256) void hawk_scatter_cells(const double* __restrict__ parts, long long cells,
+                                                          int chunks, double* __restrict__ target) {
     const long long c = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     if (c >= cells) return;
-    const long long words = (cells + 31) / 32;
-    constexpr int kAhead = 8;                 // chunks whose loads are in flight before their adds
-    double s = 0.0;
-    int b = 0;
-    for (; b + kAhead <= chunks; b += kAhead) {
-        double x[kAhead];
-        bool on[kAhead];
+    constexpr int kAhead = 8;
+    auto fetch = [&](int b, double (&x)[kAhead]) {
 #pragma unroll
         for (int q = 0; q < kAhead; ++q) {
-            on[q] = !use_seen || ((touched[(b + q) * words + (c >> 5)] >> (c & 31)) & 1u);
-            x[q] = on[q] ? parts[static_cast<long long>(b + q) * cells + c] : 0.0;
+            // past the last chunk a partial reads as +0.0, which adds nothing
+            // to a sum that is never -0.0
+            const int bq = b + q < chunks ? b + q : chunks - 1;
+            const double p = parts[static_cast<long long>(bq) * cells + c];
+            x[q] = b + q < chunks ? p : 0.0;
         }
-        // an untouched partial is skipped, not added as +0.0 (the sum is never
-        // -0.0, so the two agree; skipping also keeps a NaN's payload)
+    };
+    double x0[kAhead], x1[kAhead];
+    fetch(0, x0);
+    fetch(kAhead, x1);
+    double s = 0.0;
+    for (int b = 0; b < chunks; b += kAhead) {
+        double x2[kAhead];
+        fetch(b + 2 * kAhead, x2);
 #pragma unroll
-        for (int q = 0; q < kAhead; ++q)
-            if (on[q]) s = s + x[q];
-    }
-    for (; b < chunks; ++b) {
-        if (use_seen && !((touched[b * words + (c >> 5)] >> (c & 31)) & 1u)) continue;
-        s = s + parts[static_cast<long long>(b) * cells + c];
+        for (int q = 0; q < kAhead; ++q) s = s + x0[q];
+#pragma unroll
+        for (int q = 0; q < kAhead; ++q) {
+            x0[q] = x1[q];
+            x1[q] = x2[q];
+        }
     }
     target[c] = target[c] + s;
 }
@@ -1046,6 +1035,471 @@ __global__ void hawk_scatter_status(int* status, long long cells) {
     const int t = threadIdx.x;
     if (t == 0) status[0] = static_cast<int>(cells);
     if (t < kScatterChunks) status[1 + t] = 0;
+}
+
+// ---- the split walk: the ordered scatter into at most 65536 cells ----------
+// The same additions as hawk_scatter_walk (each (chunk, key) sum in lane order
+// from +0.0), with every accumulator in LDS, so no partial is read back from
+// memory while a chunk is walked:
+//
+// * hawk_split_hot: one workgroup per chunk, keys [0, kSplitHot) in LDS.  Each
+//   tile of 4096 lanes is split stably into buckets in one pass: window keys
+//   0..15 each a bucket of their own, keys 16..kSplitHot-1 sixteen classes by
+//   key & 15, and keys from kSplitHot up one bucket per tail range of
+//   kSplitHot keys.  Wave c then folds bucket c (a single key: one chain of
+//   adds over a contiguous run) and class c (64 entries at a time: equal keys
+//   find each other, and the lowest lane adds its group in lane order onto the
+//   key's accumulator; a wave's LDS operations complete in issue order, so a
+//   key's groups meet the accumulator window after window).  The tail buckets
+//   are one contiguous run, copied to the tile's slot of the chunk's bin with
+//   the offset of each range.
+// * hawk_split_tail: one workgroup per (chunk, tail range), keys of the range
+//   in LDS; it reads the range's segment of every slot in tile order (lane
+//   order), a batch of whole segments at a time, and folds them as above.
+//
+// Both write every key's accumulator of their window to parts[b] (+0.0 for a
+// key no lane named); hawk_scatter_cells then adds the partials in chunk order.
+constexpr int kSplitHot = 12288;                 // keys a workgroup keeps in LDS (96 KiB of accumulators)
+constexpr long long kSplitCells = 65536;         // the split walk's largest cell count
+constexpr int kSplitMaxRanges = static_cast<int>((kSplitCells - kSplitHot + kSplitHot - 1) / kSplitHot);  // 5
+constexpr int kSplitClassBase = 16;              // buckets 0..15: window keys 0..15
+constexpr int kSplitTailBase = 32;               // buckets 16..31: classes; 32..: tail ranges
+constexpr int kSplitStride = kSplitTailBase + kSplitMaxRanges + 3;   // 40: a wave's row of bucket counts
+constexpr int kSplitNone = 63;                   // a lane that adds nothing (skip key, bad key, padding)
+constexpr int kSplitSegs = 64;                   // segments one tail batch can hold
+
+static_assert(kSplitHot < (1 << 14), "class matching covers key bits 4..13");
+static_assert(kSplitStride >= kSplitTailBase + kSplitMaxRanges + 1, "bucket starts need one past the last bucket");
+static_assert(kSplitNone >= kSplitStride, "the no-bucket code is outside the count rows");
+
+constexpr int kSplitPad = 64;                    // entries read (and ignored) past a run's end
+
+struct SplitShared {
+    double acc[kSplitHot];                          // 96 KiB: the window's accumulators
+    double val[kTile + kSplitPad];                  // 32 KiB: the tile's values, bucket order
+    unsigned short key[kTile + kSplitPad];          //  8 KiB: their window-local keys
+    union {                                         // 20 KiB, one phase at a time:
+        unsigned long long win[kWalkWaves][kWalkItems][kSplitStride];  // split: a match table per window
+        struct {
+            unsigned long long peer[kWalkWaves][64];                   // fold: per-wave match masks
+        } f;
+        unsigned short seg_pos[kSplitSegs];         // a tail batch: each segment's place in the batch
+    };
+    alignas(16) unsigned cnt[kSplitStride][kWalkWaves];  // 2.5 KiB: bucket counts, bucket-major (a 64-byte row each)
+    unsigned bstart[kSplitStride + 1];              // bucket d holds [bstart[d], bstart[d+1])
+    unsigned short grp_lo[kSplitSegs];              // a tail group of 64 tiles: each tile's segment
+    unsigned short grp_hi[kSplitSegs];              //   [lo, hi) in its slot
+    unsigned batch_segs, batch_n;
+};
+
+// The bucket of window-local key kl (0 <= kl < window).
+__device__ __forceinline__ int split_bucket(unsigned kl) {
+    return kl < 16u ? static_cast<int>(kl) : kSplitClassBase + static_cast<int>(kl & 15u);
+}
+
+// Stable split of the tile held in registers (thread slot j of wave w is tile
+// position w*256 + j*64 + lane) into nb buckets: sh.key/sh.val in bucket order,
+// lane order within a bucket; bucket bounds in sh.bstart.  Each wave matches
+// its four windows at once, one table per window, so a lane's rank is the
+// count of its bucket in the wave's earlier windows plus the lanes below it
+// in its own.  Every wave then forms its own positions from all waves'
+// counts.  Starts and ends with every thread of the workgroup.
+__device__ void split_tile(SplitShared& sh, const unsigned (&kl)[kWalkItems], const int (&d)[kWalkItems],
+                           const double (&vv)[kWalkItems], int nb) {
+    const int t = threadIdx.x;
+    const int wave = t >> 6;
+    const int lane = t & 63;
+    const unsigned long long me = 1ull << lane;
+    unsigned long long* tab = &sh.win[wave][0][0];
+    for (int i = lane; i < kWalkItems * kSplitStride; i += 64) tab[i] = 0ull;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < kWalkItems; ++j)
+        if (d[j] != kSplitNone) atomicOr(&sh.win[wave][j][d[j]], me);
+    __builtin_amdgcn_wave_barrier();
+    // lane b: bucket b's four window masks, their counts and the running
+    // count before each window; each item then takes its bucket's running
+    // count from lane d (a permute) and adds the lanes below it in its window
+    unsigned long long own[kWalkItems];
+#pragma unroll
+    for (int j = 0; j < kWalkItems; ++j) own[j] = sh.win[wave][j][d[j] != kSplitNone ? d[j] : 0];
+    unsigned run[kWalkItems];
+    unsigned total = 0u;
+    {
+        const int b = lane < kSplitStride ? lane : 0;
+#pragma unroll
+        for (int j = 0; j < kWalkItems; ++j) {
+            run[j] = total;
+            total += static_cast<unsigned>(__popcll(sh.win[wave][j][b]));
+        }
+    }
+    if (lane < kSplitStride) sh.cnt[lane][wave] = total;
+    unsigned rank[kWalkItems];
+#pragma unroll
+    for (int j = 0; j < kWalkItems; ++j) {
+        const int dj = d[j] != kSplitNone ? d[j] : 0;
+        rank[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(dj << 2, static_cast<int>(run[j]))) +
+                  __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(own[j] >> 32),
+                                            __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(own[j]), 0u));
+    }
+    __syncthreads();
+    // lane b: bucket b's total over the waves, the earlier waves' share of it,
+    // and (a scan over the lanes) where bucket b starts
+    unsigned before = 0u, sum = 0u;
+    if (lane < nb) {
+        const uint4* row = reinterpret_cast<const uint4*>(&sh.cnt[lane][0]);
+#pragma unroll
+        for (int q = 0; q < kWalkWaves / 4; ++q) {
+            const uint4 c = row[q];
+            const unsigned cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                before += q * 4 + i < wave ? cw[i] : 0u;
+                sum += cw[i];
+            }
+        }
+    }
+    const unsigned start = wave_inclusive_scan(sum) - sum;
+    if (wave == 0 && lane <= nb) sh.bstart[lane] = start;
+    const unsigned base = start + before;
+#pragma unroll
+    for (int j = 0; j < kWalkItems; ++j) {
+        const int dj = d[j] != kSplitNone ? d[j] : 0;
+        const unsigned p = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(dj << 2, static_cast<int>(base))) + rank[j];
+        if (d[j] != kSplitNone) {
+            sh.key[p] = static_cast<unsigned short>(kl[j]);
+            sh.val[p] = vv[j];
+        }
+    }
+    __syncthreads();
+}
+
+// a + x[s] + x[s+1] + ... + x[e-1] in that order, with 16 to 24 values in
+// flight: three blocks of kB take turns (no register moves, so each add waits
+// only for its own block).  Loads run up to 3*kB entries past e (x is padded
+// for that) and are never branched around.
+template <int kB>
+__device__ __forceinline__ void stream_load(const double* x, int m, double (&c)[kB]) {
+#pragma unroll
+    for (int q = 0; q < kB; ++q) c[q] = x[m + q];
+}
+
+template <int kB>
+__device__ __forceinline__ double stream_last(const double (&c)[kB], int m, int e, double a) {
+#pragma unroll
+    for (int q = 0; q < kB; ++q)
+        if (m + q < e) a = a + c[q];
+    return a;
+}
+
+__device__ __forceinline__ double fold_stream(const double* x, int s, int e, double a) {
+    constexpr int kB = 8;
+    double c0[kB], c1[kB], c2[kB];
+    stream_load(x, s, c0);
+    stream_load(x, s + kB, c1);
+    int m = s;
+    for (;;) {
+        stream_load(x, m + 2 * kB, c2);
+        if (m + kB > e) return stream_last(c0, m, e, a);
+#pragma unroll
+        for (int q = 0; q < kB; ++q) a = a + c0[q];
+        m += kB;
+        stream_load(x, m + 2 * kB, c0);
+        if (m + kB > e) return stream_last(c1, m, e, a);
+#pragma unroll
+        for (int q = 0; q < kB; ++q) a = a + c1[q];
+        m += kB;
+        stream_load(x, m + 2 * kB, c1);
+        if (m + kB > e) return stream_last(c2, m, e, a);
+#pragma unroll
+        for (int q = 0; q < kB; ++q) a = a + c2[q];
+        m += kB;
+    }
+}
+
+// Wave c folds bucket c (window key c) and class c of the split tile onto the
+// LDS accumulators.
+__device__ void split_fold(SplitShared& sh, int window) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const unsigned long long me = 1ull << lane;
+    // one lane folds the single key's run: LDS returns each read to the
+    // active lanes only, so a one-lane read costs a sixty-fourth of a
+    // full-wave one
+    if (wave < window && lane == 0) {
+        const int s = static_cast<int>(sh.bstart[wave]);
+        const int e = static_cast<int>(sh.bstart[wave + 1]);
+        if (s < e) sh.acc[wave] = fold_stream(sh.val, s, e, sh.acc[wave]);
+    }
+    const int s = static_cast<int>(sh.bstart[kSplitClassBase + wave]);
+    const int e = static_cast<int>(sh.bstart[kSplitClassBase + wave + 1]);
+    if (s >= e) return;
+    sh.f.peer[wave][lane] = 0ull;
+    __builtin_amdgcn_wave_barrier();
+    // 64 entries a window; the next window's entries are read while this one
+    // is folded.  A lane past the end reads (padding or another bucket's
+    // entry) and ignores it; its match bit goes to a slot of its own.
+    unsigned k = sh.key[s + lane];
+    double x = sh.val[s + lane];
+    for (int base = s; base < e; base += 64) {
+        const bool valid = base + lane < e;
+        const unsigned nk = sh.key[base + 64 + lane];
+        const double nx = sh.val[base + 64 + lane];
+        const unsigned kv = valid ? k : 0u;
+        const unsigned h = valid ? (kv >> 4) & 63u : static_cast<unsigned>(lane);
+        atomicOr(&sh.f.peer[wave][h], valid ? me : 0ull);
+        __builtin_amdgcn_wave_barrier();
+        unsigned long long pm = sh.f.peer[wave][h];
+        double a = sh.acc[kv];
+        __builtin_amdgcn_wave_barrier();
+        sh.f.peer[wave][h] = 0ull;
+        // the slot matched key bits 4..9 (bits 0..3 are the class); bits
+        // 10..13 by ballots
+#pragma unroll
+        for (int bit = 10; bit < 14; ++bit) {
+            const bool one = (kv >> bit) & 1u;
+            const unsigned long long ones = __ballot(valid && one);
+            pm &= one ? ones : ~ones;
+        }
+        // the group's lowest lane adds its own value, then the others' in
+        // lane order, read straight from the bucket four at a time
+        if (valid && (pm & (me - 1ull)) == 0ull) {
+            a = a + x;
+            unsigned long long m = pm & ~me;
+            while (m) {
+                int q[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    q[u] = m ? __builtin_ctzll(m) : -1;
+                    m &= m - 1ull;
+                }
+                double y[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) y[u] = sh.val[base + (q[u] < 0 ? 0 : q[u])];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (q[u] >= 0) a = a + y[u];
+            }
+            sh.acc[kv] = a;
+        }
+        __builtin_amdgcn_wave_barrier();
+        k = nk;
+        x = nx;
+    }
+}
+
+// The window's partials of chunk b, every key [klo, klo+window): a key no
+// lane named holds +0.0, the walk's starting value.
+__device__ void split_store(SplitShared& sh, long long b, long long cells, long long klo, int window,
+                            double* __restrict__ parts) {
+    __syncthreads();
+    double* row = parts + b * cells + klo;
+    for (int k = threadIdx.x; k < window; k += kWalkThreads) row[k] = sh.acc[k];
+}
+
+__device__ void split_clear(SplitShared& sh, int window) {
+    for (int k = threadIdx.x; k < window; k += kWalkThreads) sh.acc[k] = 0.0;
+    __syncthreads();
+}
+
+// Chunk b = blockIdx.x: lanes [b*span, min((b+1)*span, n)), keys below
+// kSplitHot folded here, the others copied to the chunk's bin (slot = tile,
+// offsets of the `ranges` tail ranges in bin_off[b][tile][0..ranges]).
+__global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
+        const int* __restrict__ key, const double* __restrict__ v, long long n, long long cells, long long span,
+        int tiles, int ranges, unsigned short* __restrict__ bin_key, double* __restrict__ bin_val,
+        unsigned* __restrict__ bin_off, double* __restrict__ parts, int* __restrict__ status) {
+    __shared__ SplitShared sh;
+    const int t = threadIdx.x;
+    const long long b = blockIdx.x;
+    const long long lo = b * span;
+    const long long hi = lo + span < n ? lo + span : n;
+    const int window = cells < kSplitHot ? static_cast<int>(cells) : kSplitHot;
+    const int nb = kSplitTailBase + ranges;
+    split_clear(sh, window);
+    bool bad = false;
+    int nk[kWalkItems];
+    double nv[kWalkItems];
+    if (lo < hi) walk_load(key, v, lo, hi, nk, nv);
+    int tile = 0;
+    for (long long base = lo; base < hi; base += kTile, ++tile) {
+        unsigned kl[kWalkItems];
+        int d[kWalkItems];
+        double vv[kWalkItems];
+#pragma unroll
+        for (int j = 0; j < kWalkItems; ++j) {
+            const int k = nk[j];
+            vv[j] = nv[j];
+            const bool valid = k >= 0 && k < cells;
+            bad = bad || (k != -1 && !valid);
+            if (!valid) {
+                d[j] = kSplitNone;
+                kl[j] = 0u;
+            } else if (k < window) {
+                d[j] = split_bucket(static_cast<unsigned>(k));
+                kl[j] = static_cast<unsigned>(k);
+            } else {
+                const int r = (k - kSplitHot) / kSplitHot;
+                d[j] = kSplitTailBase + r;
+                kl[j] = static_cast<unsigned>(k - kSplitHot - r * kSplitHot);
+            }
+        }
+        if (base + kTile < hi) walk_load(key, v, base + kTile, hi, nk, nv);
+        split_tile(sh, kl, d, vv, nb);
+        if (ranges > 0) {
+            const unsigned ts = sh.bstart[kSplitTailBase];
+            const unsigned te = sh.bstart[kSplitTailBase + ranges];
+            const long long slot = (b * tiles + tile) * kTile;
+            for (unsigned i = ts + t; i < te; i += kWalkThreads) {
+                bin_key[slot + (i - ts)] = sh.key[i];
+                bin_val[slot + (i - ts)] = sh.val[i];
+            }
+            if (t <= ranges) bin_off[(b * tiles + tile) * (ranges + 1) + t] = sh.bstart[kSplitTailBase + t] - ts;
+        }
+        split_fold(sh, window);
+        __syncthreads();
+    }
+    // a chunk with fewer tiles than `tiles` (the last, short one) leaves its
+    // later slots empty
+    if (ranges > 0)
+        for (int i = t; i < (tiles - tile) * (ranges + 1); i += kWalkThreads)
+            bin_off[(b * tiles + tile) * (ranges + 1) + i] = 0u;
+    split_store(sh, b, cells, 0, window, parts);
+    if (bad) status[1 + b] = 1;
+}
+
+// (chunk b, tail range r) = (blockIdx.x / ranges, blockIdx.x % ranges): keys
+// [kSplitHot*(r+1), +kSplitHot) of chunk b, read from the bin's slots in tile
+// order.
+__global__ __launch_bounds__(kWalkThreads) void hawk_split_tail(
+        long long cells, int tiles, int ranges, const unsigned short* __restrict__ bin_key,
+        const double* __restrict__ bin_val, const unsigned* __restrict__ bin_off, double* __restrict__ parts) {
+    __shared__ SplitShared sh;
+    const int t = threadIdx.x;
+    const int wave = t >> 6;
+    const int lane = t & 63;
+    const long long b = blockIdx.x / ranges;
+    const int r = static_cast<int>(blockIdx.x % ranges);
+    const long long klo = static_cast<long long>(kSplitHot) * (r + 1);
+    const int window = cells - klo < kSplitHot ? static_cast<int>(cells - klo) : kSplitHot;
+    split_clear(sh, window);
+    for (int g0 = 0; g0 < tiles; g0 += kSplitSegs) {
+        // the group's segments: hawk_split_hot wrote 0 <= o[r] <= o[r+1] <=
+        // 4096; the clamps keep every read inside its slot whatever the plane
+        // holds
+        const int gn = tiles - g0 < kSplitSegs ? tiles - g0 : kSplitSegs;
+        if (wave == 0) {
+            unsigned a0 = 0u, a1 = 0u;
+            if (lane < gn) {
+                const unsigned* o = bin_off + (b * tiles + g0 + lane) * (ranges + 1);
+                a0 = o[r] < static_cast<unsigned>(kTile) ? o[r] : static_cast<unsigned>(kTile);
+                a1 = o[r + 1] < a0 ? a0 : (o[r + 1] < static_cast<unsigned>(kTile) ? o[r + 1]
+                                                                                : static_cast<unsigned>(kTile));
+            }
+            sh.grp_lo[lane] = static_cast<unsigned short>(a0);
+            sh.grp_hi[lane] = static_cast<unsigned short>(a1);
+        }
+        __syncthreads();
+        for (int t0 = 0; t0 < gn;) {
+            if (wave == 0) {
+                const int tt = t0 + lane;
+                const unsigned c = tt < gn ? static_cast<unsigned>(sh.grp_hi[tt] - sh.grp_lo[tt]) : 0u;
+                const unsigned incl = wave_inclusive_scan(c);
+                const unsigned long long fits = __ballot(tt < gn && incl <= static_cast<unsigned>(kTile));
+                const int segs = __popcll(fits);
+                if (lane < segs) sh.seg_pos[lane] = static_cast<unsigned short>(incl - c);
+                if (lane == segs - 1) sh.batch_n = incl;
+                if (lane == 0) sh.batch_segs = static_cast<unsigned>(segs);
+            }
+            __syncthreads();
+            const int segs = static_cast<int>(sh.batch_segs);
+            const int total = static_cast<int>(sh.batch_n);
+            for (int g = wave; g < segs; g += kWalkWaves) {
+                const int tt = t0 + g;
+                const long long src = (b * tiles + g0 + tt) * kTile + sh.grp_lo[tt];
+                const unsigned pos = sh.seg_pos[g];
+                const unsigned c = static_cast<unsigned>(sh.grp_hi[tt] - sh.grp_lo[tt]);
+                for (unsigned i0 = 0; i0 < c; i0 += 4 * 64) {
+                    unsigned short kk[4];
+                    double vv[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const unsigned i = i0 + q * 64 + lane;
+                        kk[q] = i < c ? bin_key[src + i] : 0;
+                        vv[q] = i < c ? bin_val[src + i] : 0.0;
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const unsigned i = i0 + q * 64 + lane;
+                        if (i < c) {
+                            sh.key[pos + i] = kk[q];
+                            sh.val[pos + i] = vv[q];
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            unsigned kl[kWalkItems];
+            int d[kWalkItems];
+            double vv[kWalkItems];
+#pragma unroll
+            for (int j = 0; j < kWalkItems; ++j) {
+                const int i = wave * (kWalkItems * 64) + j * 64 + lane;
+                const bool on = i < total;
+                kl[j] = on ? sh.key[i] : 0u;
+                vv[j] = on ? sh.val[i] : 0.0;
+                d[j] = on ? split_bucket(kl[j]) : kSplitNone;
+            }
+            __syncthreads();
+            split_tile(sh, kl, d, vv, kSplitTailBase);
+            split_fold(sh, window);
+            __syncthreads();
+            t0 += segs;
+        }
+    }
+    split_store(sh, b, cells, klo, window, parts);
+}
+
+// The ordered scatter's scratch, in this order (each part 256-byte aligned):
+// parts[chunks][cells] f64; and for the split walk with tail ranges, the bin
+// offsets [chunks][tiles][ranges+1] u32, the bin keys [chunks][tiles][4096]
+// u16 and the bin values [chunks][tiles][4096] f64.
+struct ScatterLayout {
+    int chunks = 1;
+    long long span = 0;
+    bool split = false;
+    int tiles = 0;
+    int ranges = 0;
+    size_t parts = 0, bin_off = 0, bin_key = 0, bin_val = 0, bytes = 0;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+ScatterLayout scatter_layout(int64_t n, int64_t cells, int chunks) {
+    ScatterLayout L;
+    L.chunks = chunks;
+    L.span = (n + chunks - 1) / chunks;
+    L.split = cells <= kSplitCells;
+    const size_t c = static_cast<size_t>(chunks);
+    size_t at = 0;
+    L.parts = at;
+    at += align256(sizeof(double) * c * static_cast<size_t>(cells));
+    if (L.split) {
+        const long long tiles = (L.span + kTile - 1) / kTile;
+        L.tiles = static_cast<int>(tiles < 1 ? 1 : tiles);
+        L.ranges = cells > kSplitHot ? static_cast<int>((cells - kSplitHot + kSplitHot - 1) / kSplitHot) : 0;
+        if (L.ranges > 0) {
+            const size_t slots = c * static_cast<size_t>(L.tiles);
+            L.bin_off = at;
+            at += align256(sizeof(unsigned) * slots * static_cast<size_t>(L.ranges + 1));
+            L.bin_key = at;
+            at += align256(sizeof(unsigned short) * slots * kTile);
+            L.bin_val = at;
+            at += align256(sizeof(double) * slots * kTile);
+        }
+    }
+    L.bytes = at;
+    return L;
 }
 
 // ---- the ordered gradient's log fold ----------------------------------------
@@ -1391,11 +1845,7 @@ int hk_scatter_chunks(int64_t n, int64_t cells) {
 
 size_t hk_ordered_scatter_scratch_bytes(int64_t n, int64_t cells) {
     if (cells <= 0) return 0;
-    const size_t chunks = static_cast<size_t>(hk_scatter_chunks(n, cells));
-    const size_t parts = sizeof(double) * chunks * static_cast<size_t>(cells);
-    const size_t words = static_cast<size_t>((cells + 31) / 32);
-    const size_t seen = cells <= kSeenCells ? sizeof(unsigned) * chunks * words : 0;
-    return ((parts + 255) & ~static_cast<size_t>(255)) + seen;
+    return scatter_layout(n, cells, hk_scatter_chunks(n, cells)).bytes;
 }
 
 int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n, double* target, int64_t cells,
@@ -1410,39 +1860,54 @@ int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n, doubl
         return hawk_internal::set_error(HK_EVALUE, "hk_ordered_scatter_f64: more than 2^31-1 cells");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int chunks = hk_scatter_chunks(n, cells);
-    const long long span = (n + chunks - 1) / chunks;
-    const int key_bits = bits_for(cells - 1);
-    const bool sorted_walk = key_bits <= kMaxKeyBits;
-    const int use_seen = sorted_walk && cells <= kSeenCells ? 1 : 0;
-    auto* parts = static_cast<double*>(scratch);
-    const size_t parts_bytes = sizeof(double) * static_cast<size_t>(chunks) * static_cast<size_t>(cells);
-    auto* touched = reinterpret_cast<unsigned*>(static_cast<unsigned char*>(scratch) +
-                                                ((parts_bytes + 255) & ~static_cast<size_t>(255)));
+    const ScatterLayout L = scatter_layout(n, cells, chunks);
+    unsigned char* base = static_cast<unsigned char*>(scratch);
+    auto* parts = reinterpret_cast<double*>(base + L.parts);
     hipLaunchKernelGGL(hawk_scatter_status, dim3(1), dim3(kScatterChunks + 64), 0, s, status,
                        static_cast<long long>(cells));
     int rc = launch_error("hawk_scatter_status launch");
     if (rc != HK_OK) return rc;
-    if (!use_seen) {
+    if (L.split) {
+        auto* bin_off = reinterpret_cast<unsigned*>(base + L.bin_off);
+        auto* bin_key = reinterpret_cast<unsigned short*>(base + L.bin_key);
+        auto* bin_val = reinterpret_cast<double*>(base + L.bin_val);
+        hipLaunchKernelGGL(hawk_split_hot, dim3(static_cast<unsigned>(chunks)), dim3(kWalkThreads), 0, s, key, v,
+                           static_cast<long long>(n), static_cast<long long>(cells), L.span, L.tiles, L.ranges,
+                           bin_key, bin_val, bin_off, parts, status);
+        rc = launch_error("hawk_split_hot launch");
+        if (rc != HK_OK) return rc;
+        if (L.ranges > 0) {
+            hipLaunchKernelGGL(hawk_split_tail, dim3(static_cast<unsigned>(chunks * L.ranges)), dim3(kWalkThreads),
+                               0, s, static_cast<long long>(cells), L.tiles, L.ranges, bin_key, bin_val, bin_off,
+                               parts);
+            rc = launch_error("hawk_split_tail launch");
+            if (rc != HK_OK) return rc;
+        }
+    } else {
+        // more cells than the split walk's windows cover: parts arrives
+        // zero-filled and the sorted walk (or, past its key field, the serial
+        // walk) adds onto it
         const long long count = static_cast<long long>(chunks) * cells;
         const long long blocks = (count + 255) / 256 < 4096 ? (count + 255) / 256 : 4096;
         hipLaunchKernelGGL(hawk_fill_zero, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, parts, count);
         rc = launch_error("hawk_fill_zero launch");
         if (rc != HK_OK) return rc;
+        const int key_bits = bits_for(cells - 1);
+        if (key_bits <= kMaxKeyBits) {
+            hipLaunchKernelGGL(hawk_scatter_walk, dim3(static_cast<unsigned>(chunks)), dim3(kWalkThreads), 0, s,
+                               key, v, static_cast<long long>(n), static_cast<long long>(cells), L.span, key_bits,
+                               parts, status);
+            rc = launch_error("hawk_scatter_walk launch");
+        } else {
+            hipLaunchKernelGGL(hawk_scatter_serial, dim3(static_cast<unsigned>(chunks)), dim3(64), 0, s, key, v,
+                               static_cast<long long>(n), static_cast<long long>(cells), L.span, parts, status);
+            rc = launch_error("hawk_scatter_serial launch");
+        }
+        if (rc != HK_OK) return rc;
     }
-    if (sorted_walk) {
-        hipLaunchKernelGGL(hawk_scatter_walk, dim3(static_cast<unsigned>(chunks)), dim3(kWalkThreads), 0, s, key, v,
-                           static_cast<long long>(n), static_cast<long long>(cells), span, key_bits, use_seen,
-                           parts, touched, status);
-        rc = launch_error("hawk_scatter_walk launch");
-    } else {
-        hipLaunchKernelGGL(hawk_scatter_serial, dim3(static_cast<unsigned>(chunks)), dim3(64), 0, s, key, v,
-                           static_cast<long long>(n), static_cast<long long>(cells), span, parts, status);
-        rc = launch_error("hawk_scatter_serial launch");
-    }
-    if (rc != HK_OK) return rc;
     const long long grid = (cells + 255) / 256;
-    hipLaunchKernelGGL(hawk_scatter_cells, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, parts, touched,
-                       static_cast<long long>(cells), chunks, use_seen, target);
+    hipLaunchKernelGGL(hawk_scatter_cells, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, parts,
+                       static_cast<long long>(cells), chunks, target);
     return launch_error("hawk_scatter_cells launch");
 }
 

@@ -200,9 +200,15 @@ def test_ordered_sum_is_the_numpy_tree_bitwise_and_replays(unit, gpu, n):
     assert runs[0][0] == O.ordered_sum(x)
 
 
+# The split walk's window is 12288 keys and each tail range 12288 more:
+# 12288 has no tail, 12289 a one-key range, 24577 a second range of one key,
+# 3 cells over 1000 lanes leaves empty chunks; 65536 is config 5's cell count.
 @pytest.mark.parametrize("cells, n, heavy", [(7, 30_000, False), (1000, 30_000, False), (1500, 30_000, False),
                                              (7, 20_000, True), (1, 3000, False), (200, 50, False),
-                                             (1000, 1000, False), (65536, 400_000, False),
+                                             (1000, 1000, False), (3, 1000, False), (65536, 400_000, False),
+                                             (12288, 300_001, False), (12289, 300_001, False),
+                                             (24577, 500_000, False), (40_000, 2_000_003, True),
+                                             (65536, 3_000_017, False),
                                              (70_000, 300_000, False), (600_000, 1_300_000, False)])
 def test_ordered_scatter_is_the_serial_walk_bitwise(unit, gpu, cells, n, heavy):
     import hawk_amd as hawk
@@ -211,6 +217,7 @@ def test_ordered_scatter_is_the_serial_walk_bitwise(unit, gpu, cells, n, heavy):
     if heavy:
         key[g.random(n) < 0.9] = cells // 2
     key[::7] = -1
+    print(f"scatter cells={cells} n={n} heavy={heavy}", flush=True)
     x = g.normal(size=n) * np.exp(g.normal(size=n))
     acc0 = np.linspace(1.0, 2.0, cells)
     k = _load(unit, "ordered_add")
@@ -254,6 +261,62 @@ def test_ordered_scatter_reference_cases(unit, gpu, n, cells, heavy):
     np.testing.assert_allclose(seen[0], want, rtol=ga["rtol"], atol=ga["rtol"] * np.abs(want).max())
     if cells == empty["cells"]:
         assert seen[0][empty["moved_from"]] == 0.0
+
+
+@pytest.mark.parametrize("n", [1 << 20, 1 << 22])
+def test_ordered_scatter_zipf_keys_into_65536_cells(unit, gpu, n):
+    """Config 5's key shape, Zipf(1.1) folded into 65536 cells (a head key
+    with a tenth of the lanes, a uniform floor over every cell), with skip
+    keys: the oracle's bits, the same on a replay."""
+    import hawk_amd as hawk
+    cells = 1 << 16
+    g = rng(n + 11)
+    key = ((g.zipf(1.1, n) - 1) % cells).astype(np.int32)
+    key[g.random(n) < 0.01] = -1
+    x = g.normal(size=n)
+    acc0 = g.normal(size=cells)
+    k = _load(unit, "ordered_add")
+    print(f"scatter zipf n={n}", flush=True)
+    outs = []
+    for _ in range(2):
+        acc = dev(acc0, gpu)
+        hawk.run(k, key=dev(key, gpu), x=dev(x, gpu), acc=acc)
+        outs.append(host(acc))
+    want, status = O.ordered_scatter(key, x, acc0)
+    assert not status[1:].any()
+    assert outs[0].tobytes() == outs[1].tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("cells", [5, 30_000])
+def test_ordered_scatter_special_values(unit, gpu, cells):
+    """-0.0, infinities, NaN and subnormals through every bucket kind (window
+    keys 0..15, classes, a tail range): the oracle's bits, NaN as NaN.  A key
+    whose only values are -0.0 sums to +0.0 (the walk starts at +0.0)."""
+    import hawk_amd as hawk
+    n = 50_000
+    g = rng(cells)
+    key = g.integers(0, cells, n).astype(np.int32)
+    x = g.normal(size=n)
+    special = np.array([-0.0, np.inf, -np.inf, np.nan, 5e-324, -5e-324, 1e-310])
+    hit = g.random(n) < 0.02
+    x[hit] = special[g.integers(0, len(special), hit.sum())]
+    lone = [1, cells - 1]
+    for c in lone:
+        key[key == c] = 0
+    key[[10, 20, 30]] = lone[0]
+    x[[10, 20, 30]] = -0.0
+    key[40] = lone[1]
+    x[40] = -0.0
+    acc0 = np.zeros(cells)
+    acc = dev(acc0, gpu)
+    print(f"scatter specials cells={cells}", flush=True)
+    hawk.run(_load(unit, "ordered_add"), key=dev(key, gpu), x=dev(x, gpu), acc=acc)
+    got = host(acc)
+    want, status = O.ordered_scatter(key, x, acc0)
+    nan = np.isnan(want)
+    assert (np.isnan(got) == nan).all()
+    assert got[~nan].tobytes() == want[~nan].tobytes()
+    assert np.signbit(got[lone]).tolist() == [False, False]
 
 
 def test_ordered_scatter_reports_a_bad_key(unit, gpu):
