@@ -1217,12 +1217,13 @@ __device__ __forceinline__ double fold_stream(const double* x, int s, int e, dou
     }
 }
 
-// Wave c folds bucket c (window key c) and class c of the split tile onto the
-// LDS accumulators.
+__device__ void split_fold_class(SplitShared& sh, int c);
+
+// Wave c folds bucket c (window key c) and, as a rule, class c of the split
+// tile onto the LDS accumulators.
 __device__ void split_fold(SplitShared& sh, int window) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const unsigned long long me = 1ull << lane;
     // one lane folds the single key's run: LDS returns each read to the
     // active lanes only, so a one-lane read costs a sixty-fourth of a
     // full-wave one
@@ -1231,11 +1232,33 @@ __device__ void split_fold(SplitShared& sh, int window) {
         const int e = static_cast<int>(sh.bstart[wave + 1]);
         if (s < e) sh.acc[wave] = fold_stream(sh.val, s, e, sh.acc[wave]);
     }
-    const int s = static_cast<int>(sh.bstart[kSplitClassBase + wave]);
-    const int e = static_cast<int>(sh.bstart[kSplitClassBase + wave + 1]);
-    if (s >= e) return;
+    // When one single-key chain is longer than another by more than a
+    // window, the wave with the longest leaves its class to the wave with
+    // the shortest (every wave finds the same two from the bucket bounds):
+    // any wave may fold a class, as long as one wave folds all of it.
+    const int len = lane < 16 ? static_cast<int>(sh.bstart[lane + 1] - sh.bstart[lane]) : 0;
+    int longest = 0, shortest = 0;
+    int lmax = __builtin_amdgcn_readlane(len, 0), lmin = lmax;
+    for (int c = 1; c < 16; ++c) {
+        const int v = __builtin_amdgcn_readlane(len, c);
+        if (v > lmax) { lmax = v; longest = c; }
+        if (v <= lmin) { lmin = v; shortest = c; }
+    }
     sh.f.peer[wave][lane] = 0ull;
     __builtin_amdgcn_wave_barrier();
+    const bool move = lmax - lmin > 64;
+    if (wave != longest || !move) split_fold_class(sh, wave);
+    if (wave == shortest && move) split_fold_class(sh, longest);
+}
+
+// The caller's wave folds class c of the split tile, 64 entries a window.
+__device__ void split_fold_class(SplitShared& sh, int c) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const unsigned long long me = 1ull << lane;
+    const int s = static_cast<int>(sh.bstart[kSplitClassBase + c]);
+    const int e = static_cast<int>(sh.bstart[kSplitClassBase + c + 1]);
+    if (s >= e) return;
     // 64 entries a window; the next window's entries are read while this one
     // is folded.  A lane past the end reads (padding or another bucket's
     // entry) and ignores it; its match bit goes to a slot of its own.
