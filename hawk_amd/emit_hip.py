@@ -683,8 +683,9 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         + ", ".join(str(s) for s in LAYOUT_SIZES) + "};",
         "",
     ]
-    if "hk_tanh(" in "\n".join(body + stores):
-        out += _TANH_HELPER.splitlines()
+    text = "\n".join(body + stores)
+    if any(c in text for c in MATH_HELPER_CALLS):
+        out += MATH_DEVICE_DEFINES + _MATH_HELPERS.splitlines()
     if row_terms:
         out += (_BAND_ROW_SUM_HELPERS if stage.banded else _ROW_SUM_HELPERS).splitlines()
     if folds:
@@ -1098,19 +1099,139 @@ def _fused_fold_lines(folds: list, block: int, whole: bool = False) -> list:
     return lines
 
 
-#: fp64 tanh: tanh x = sign(x) e / (e + 2) with e = expm1(2|x|) >= 0.  The
-#: quotient has no cancellation, and e's relative error reaches it scaled by
-#: 2 / (e + 2) <= 1, so the result is within about 2 ulp (expm1 within 1 ulp,
-#: the add and the correctly rounded divide half an ulp each); from |x| = 22 on
-#: it is +-1 (tanh 22 rounds to 1).  It costs about 70 VALU instructions where
-#: the device library's double-double tanh costs 165.  NaN stays NaN, -0 stays -0.
-_TANH_HELPER = """
-__device__ __forceinline__ double hk_tanh(double x) {
+#: fp64 exp, sin and cos of this target (``HK_MATH_QUAL`` is the qualifier:
+#: ``__device__ __forceinline__`` on the device; a host compiler builds the
+#: same text to test it).  Method: Cody–Waite reduction with the constant's
+#: head cut to trailing zeros, so the first step is exact, then a polynomial
+#: on the reduced interval whose coefficients are Chebyshev fits computed at
+#: 60 digits (mpmath ``chebyfit``) and rounded to double, evaluated by Horner
+#: with fused multiply-adds.
+#:
+#: * exp: x = k ln2 + r, ln2 as a 42-bit head and a tail, |r| <= ln2/2;
+#:   exp r = 1 + r + r^2 P(r), P of degree 10 fitting (e^r - 1 - r)/r^2
+#:   (fit error 0.002 ulp of the result); 2^k by ldexp, which rounds once into
+#:   the subnormal range.  The input is clamped to [-1200, 1200], where exp
+#:   is 0 or inf anyway; NaN returns NaN.
+#: * sin, cos: x = q pi/2 + r, pi/2 as two 33-bit heads and a tail (q * head
+#:   exact for |x| < 2^17), |r| <= pi/4; sin r = r + r^3 S(r^2) with S of
+#:   degree 6, cos r = 1 - r^2/2 + r^4 C(r^2) with C of degree 5 (1 - r^2/2
+#:   kept with its rounding error); the quadrant q mod 4 picks and signs one
+#:   of them.  |x| >= 2^17, infinities and NaN go to the library's sin/cos
+#:   (its long reduction); sin returns x itself below 2^-26 (sin x rounds to
+#:   x there, and -0 stays -0).
+_MATH_HELPERS = """
+// hk_c(c): the constant c held in a scalar register pair, which the
+// multiply-adds read directly; a literal the compiler can see would be
+// rebuilt by two vector moves per sample.
+HK_MATH_QUAL double hk_c(double c) {
+    HK_MATH_PIN(c);
+    return c;
+}
+
+// P(r) with exp r = 1 + r + r^2 P(r), |r| <= ln2/2.
+HK_MATH_QUAL double hk_exp_poly(double r) {
+    double p = hk_c(0x1.1f72fc848c527p-29);
+    p = fma(p, r, hk_c(0x1.af4ddda32bea9p-26));
+    p = fma(p, r, hk_c(0x1.27e4db67abc75p-22));
+    p = fma(p, r, hk_c(0x1.71de0237479e4p-19));
+    p = fma(p, r, hk_c(0x1.a01a01a6d7833p-16));
+    p = fma(p, r, hk_c(0x1.a01a01abe6327p-13));
+    p = fma(p, r, hk_c(0x1.6c16c16c162d6p-10));
+    p = fma(p, r, hk_c(0x1.11111111100dfp-7));
+    p = fma(p, r, hk_c(0x1.5555555555556p-5));
+    p = fma(p, r, hk_c(0x1.5555555555557p-3));
+    return fma(p, r, 0.5);
+}
+
+// x = k ln2 + r, |r| <= ln2/2; k returned through *k.
+HK_MATH_QUAL double hk_exp_reduce(double x, double* k) {
+    *k = rint(x * hk_c(0x1.71547652b82fep+0));
+    const double r = fma(-*k, hk_c(0x1.62e42fefa3800p-1), x);
+    return fma(-*k, hk_c(0x1.ef35793c76730p-45), r);
+}
+
+HK_MATH_QUAL double hk_exp(double x) {
+    double k;
+    const double r = hk_exp_reduce(fmin(fmax(x, -1200.0), 1200.0), &k);
+    const double e = ldexp(1.0 + fma(r * r, hk_exp_poly(r), r), static_cast<int>(k));
+    return x != x ? x + x : e;
+}
+
+// exp a - 1 for 0 <= a <= 64 (the tanh's argument), t = 2^k:
+// (t - 1 + t r) + t r^2 P(r).  t r is exact and t - 1 >= t |r| for k >= 1
+// (k = 0 makes t - 1 zero), so the head's sum and its rounding error are
+// exact (Fast2Sum); the tail joins the error term before the last rounding,
+// which keeps the cancellation just above a = ln2/2 from costing an ulp.
+HK_MATH_QUAL double hk_expm1_pos(double a) {
+    double k;
+    const double r = hk_exp_reduce(a, &k);
+    const double t = ldexp(1.0, static_cast<int>(k));
+    const double tr = t * r;
+    const double head = (t - 1.0) + tr;
+    const double err = tr - (head - (t - 1.0));
+    return head + fma(tr * r, hk_exp_poly(r), err);
+}
+
+HK_MATH_QUAL double hk_quadrant(double r, int n) {
+    const double w = r * r;
+    double s = hk_c(-0x1.ab17d393166dcp-41);
+    s = fma(s, w, hk_c(0x1.61217f0abf087p-33));
+    s = fma(s, w, hk_c(-0x1.ae645412c46d3p-26));
+    s = fma(s, w, hk_c(0x1.71de3a5460952p-19));
+    s = fma(s, w, hk_c(-0x1.a01a01a019938p-13));
+    s = fma(s, w, hk_c(0x1.1111111111110p-7));
+    s = fma(s, w, hk_c(-0x1.5555555555555p-3));
+    const double sr = fma(r * w, s, r);
+    double c = hk_c(-0x1.907da3000171dp-37);
+    c = fma(c, w, hk_c(0x1.1eeb68e8ab8d4p-29));
+    c = fma(c, w, hk_c(-0x1.27e4fa17d97fdp-22));
+    c = fma(c, w, hk_c(0x1.a01a019f4eafap-16));
+    c = fma(c, w, hk_c(-0x1.6c16c16c16967p-10));
+    c = fma(c, w, hk_c(0x1.5555555555555p-5));
+    const double hz = 0.5 * w;
+    const double t = 1.0 - hz;
+    const double cr = t + (((1.0 - t) - hz) + (w * w) * c);
+    const double v = (n & 1) ? cr : sr;
+    return (n & 2) ? -v : v;
+}
+
+HK_MATH_QUAL double hk_reduce(double x, int* n) {
+    const double q = rint(x * hk_c(0x1.45f306dc9c883p-1));
+    double r = fma(-q, hk_c(0x1.921fb54400000p+0), x);
+    r = fma(-q, hk_c(0x1.0b4611a600000p-34), r);
+    r = fma(-q, hk_c(0x1.3198a2e037073p-69), r);
+    *n = static_cast<int>(q);
+    return r;
+}
+
+HK_MATH_QUAL double hk_sin(double x) {
+    if (!(fabs(x) < 0x1p17)) return sin(x);
+    int n;
+    const double r = hk_reduce(x, &n);
+    const double y = hk_quadrant(r, n);
+    return fabs(x) < 0x1p-26 ? x : y;
+}
+
+HK_MATH_QUAL double hk_cos(double x) {
+    if (!(fabs(x) < 0x1p17)) return cos(x);
+    int n;
+    const double r = hk_reduce(x, &n);
+    return hk_quadrant(r, n + 1);
+}
+
+// tanh x = sign(x) e / (e + 2), e = expm1(2|x|) >= 0; +-1 from |x| = 22 on.
+HK_MATH_QUAL double hk_tanh(double x) {
     const double a = fabs(x);
-    const double e = expm1(a + a);
-    return copysign(a >= 22.0 ? 1.0 : e / (e + 2.0), x);
+    const double e = hk_expm1_pos(fmin(a + a, 64.0));
+    return x != x ? x + x : copysign(a >= 22.0 ? 1.0 : e / (e + 2.0), x);
 }
 """
+
+#: The fp64 math calls this target spells with its own helpers, and the
+#: qualifiers the device build gives them.
+MATH_HELPER_CALLS = ("hk_exp(", "hk_sin(", "hk_cos(", "hk_tanh(")
+MATH_DEVICE_DEFINES = ["#define HK_MATH_QUAL __device__ __forceinline__",
+                       "#define HK_MATH_PIN(c) asm(\"\" : \"+s\"(c))"]
 
 
 def _whole_fold_lines(folds: list, block: int) -> list:

@@ -62,7 +62,8 @@ def _refuse(what: str):
 
 class HipWriter:
     """gfx950 HIP spellings (``Real`` is ``double`` or ``float`` by the
-    build's mode; fp64 ``tanh`` is the emitted ``hk_tanh``)."""
+    build's mode; fp64 ``tanh``, ``exp``, ``sin`` and ``cos`` are the emitted
+    ``hk_`` helpers)."""
 
     id = "hip"
     #: Every component of a tensor value is a named local of its own.
@@ -170,7 +171,8 @@ class HipWriter:
 
     def op(self, r, node, args, ranks=()) -> str:
         """One scalar operation: ``+ - * /`` infix, comparisons, negation,
-        the math calls (fp64 tanh as ``hk_tanh``), ``Real(x)`` casts."""
+        the math calls (fp64 tanh, exp, sin and cos as the ``hk_`` helpers),
+        ``Real(x)`` casts."""
         k = node.kind if isinstance(node, Node) else node
         if k in _BINARY:
             return f"{args[0]} {_BINARY[k]} {args[1]}"
@@ -183,8 +185,8 @@ class HipWriter:
         if k in _UNARY:
             fn = _UNARY[k]
             dtype = node.ttype.dtype if isinstance(node, Node) else "f64"
-            if fn == "tanh" and dtype == "f64":
-                fn = "hk_tanh"
+            if dtype == "f64" and fn in ("tanh", "exp", "sin", "cos"):
+                fn = "hk_" + fn
             return f"{fn}({args[0]})"
         _refuse(f"the operation {k!r}")
 

@@ -334,7 +334,7 @@ def test_ordered_scatter_reports_a_bad_key(unit, gpu):
     assert host(acc).tobytes() == want.tobytes()
 
 
-@pytest.mark.parametrize("which", ["exp", "sin", "tanh", "sqrt"])
+@pytest.mark.parametrize("which", ["exp", "sin", "cos", "tanh", "sqrt"])
 def test_transcendentals_are_within_4_ulp_of_glibc(unit, gpu, which):
     """The device's fp64 exp/sin/tanh/sqrt on the chain's argument ranges, in ULP of
     glibc (reference tests/test_math_parity.py: device within ULP of host)."""
@@ -342,7 +342,7 @@ def test_transcendentals_are_within_4_ulp_of_glibc(unit, gpu, which):
     from hawk_amd import Scalar, kernel
     from hawk_amd import math as m
 
-    fn = {"exp": m.exp, "sin": m.sin, "tanh": m.tanh, "sqrt": m.sqrt}[which]
+    fn = {"exp": m.exp, "sin": m.sin, "cos": m.cos, "tanh": m.tanh, "sqrt": m.sqrt}[which]
 
     @kernel
     def one(x: Scalar) -> Scalar:
@@ -354,8 +354,9 @@ def test_transcendentals_are_within_4_ulp_of_glibc(unit, gpu, which):
     g = rng(6)
     if which == "exp":
         x = np.concatenate([g.normal(size=100_000) * 5, -np.abs(g.normal(size=20_000)) * 20])
-    elif which == "sin":
-        x = np.concatenate([np.exp(g.normal(size=100_000)), g.uniform(-200, 200, 20_000)])
+    elif which in ("sin", "cos"):
+        x = np.concatenate([np.exp(g.normal(size=100_000)), g.uniform(-200, 200, 20_000),
+                            g.uniform(-1.4e5, 1.4e5, 20_000), np.pi / 2 * np.arange(-300, 300)])
     elif which == "tanh":
         x = np.concatenate([g.uniform(-2, 2, 100_000), g.normal(size=20_000) * 1e-3, g.uniform(-30, 30, 20_000),
                             np.exp(g.uniform(-700, 3, 20_000)) * np.sign(g.normal(size=20_000)),
@@ -611,7 +612,7 @@ SPECIALS = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 5e-324, -5e-324, 2.2250
                      6.283185307179586e10, 0.5, 2.0, 4.0, 1e-300])
 
 
-@pytest.mark.parametrize("which", ["exp", "sin", "tanh", "sqrt"])
+@pytest.mark.parametrize("which", ["exp", "sin", "cos", "tanh", "sqrt"])
 def test_transcendentals_on_special_values(unit, gpu, which):
     """The special-value corpus of reference tests/test_math_parity.py (signed
     zeros, infinities, NaN, subnormals, overflow and underflow edges, large
@@ -623,7 +624,7 @@ def test_transcendentals_on_special_values(unit, gpu, which):
     from hawk_amd import Scalar, kernel
     from hawk_amd import math as m
 
-    fn = {"exp": m.exp, "sin": m.sin, "tanh": m.tanh, "sqrt": m.sqrt}[which]
+    fn = {"exp": m.exp, "sin": m.sin, "cos": m.cos, "tanh": m.tanh, "sqrt": m.sqrt}[which]
 
     @kernel
     def special(x: Scalar) -> Scalar:

@@ -38,16 +38,21 @@ def test_conformance_names_a_missing_member():
 
 
 def test_the_renderer_spells_through_the_rows_writer():
+    """A writer that spells fp64 exp its own way changes exactly the call
+    sites (and, with no hk_ call left, the helper block drops out)."""
+    from hawk_amd.emit_hip import _MATH_HELPERS, MATH_DEVICE_DEFINES
+
     class Renamed(HipWriter):
         def op(self, r, node, args, ranks=()):
             text = super().op(r, node, args, ranks)
-            return text.replace("exp(", "my_exp(", 1) if text.startswith("exp(") else text
+            return text.replace("hk_exp(", "my_exp(", 1) if text.startswith("hk_exp(") else text
     base = plan_kernel(E.decay.program, "decay").source
     other = plan_kernel(E.decay.program, "decay",
                         target=dataclasses.replace(TARGETS["hip"], writer=Renamed())).source
-    assert " exp(" in base or "(exp(" in base or "= exp(" in base
-    assert "my_exp(" in other and "my_exp(" not in base
-    assert other.replace("my_exp(", "exp(") == base
+    helpers = "\n".join(MATH_DEVICE_DEFINES + _MATH_HELPERS.splitlines()) + "\n"
+    assert helpers in base and "= hk_exp(" in base
+    assert "my_exp(" in other and "my_exp(" not in base and "HK_MATH_QUAL" not in other
+    assert other.replace("my_exp(", "hk_exp(") == base.replace(helpers, "")
 
 
 def test_the_renderer_wraps_through_the_rows_wrapper():
