@@ -62,6 +62,7 @@ def _declare(lib) -> None:
         "hk_ordered_scatter_f64": (I, [V, V, I64, V, I64, V, V, V]),
         "hk_rows_finish_scratch_bytes": (SZ, [I64]),
         "hk_rows_finish_f64": (I, [V, V, I64, V, V, V]),
+        "hk_rows_finish_f32": (I, [V, V, I64, V, V, V]),
         "hk_band_rows_finish_scratch_bytes": (SZ, [I64]),
         "hk_band_rows_finish_f64": (I, [V, V, I64, V, V, V]),
         "hk_band_ordered_sum_scratch_bytes": (SZ, []),
@@ -363,6 +364,12 @@ def rows_finish_scratch_bytes(rows: int) -> int:
 def rows_finish(hi: int, comp: int, rows: int, out: int, scratch: int, stream: int = 0) -> None:
     """Fold ``rows`` compensated row pairs into the cell ``out`` (canonical ordered tree)."""
     check(lib().hk_rows_finish_f64(ctypes.c_void_p(hi), ctypes.c_void_p(comp), int(rows), ctypes.c_void_p(out),
+                                   ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
+
+
+def rows_finish_f32(hi: int, comp: int, rows: int, out: int, scratch: int, stream: int = 0) -> None:
+    """The same finish of float32 rows, in float32."""
+    check(lib().hk_rows_finish_f32(ctypes.c_void_p(hi), ctypes.c_void_p(comp), int(rows), ctypes.c_void_p(out),
                                    ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
 
 

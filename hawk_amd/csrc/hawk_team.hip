@@ -213,47 +213,52 @@ constexpr int kRowSlots = 256;
 constexpr int kRowTerms = 16;
 constexpr long long kRowLeaf = static_cast<long long>(kRowSlots) * kRowTerms;
 
-__device__ __forceinline__ bool finite_bits(double x) { return (x - x) == 0.0; }
+template <class T>
+__device__ __forceinline__ bool finite_bits(T x) { return (x - x) == T(0); }
 
 // The exact residual of s == a + b, the larger magnitude first, a zero
 // residual +0 (reference hawk/_cells.py:46-52); NaN when s is not finite.
-__device__ __forceinline__ double two_sum_err(double a, double b, double s) {
+template <class T>
+__device__ __forceinline__ T two_sum_err(T a, T b, T s) {
     const bool big_a = fabs(a) >= fabs(b);
-    const double big = big_a ? a : b;
-    const double small = big_a ? b : a;
-    return finite_bits(s) ? (small - (s - big)) + 0.0 : __builtin_nan("");
+    const T big = big_a ? a : b;
+    const T small = big_a ? b : a;
+    return finite_bits(s) ? (small - (s - big)) + T(0) : T(__builtin_nan(""));
 }
 
 // Neumaier's add of (x, xc) onto (h, c) (reference hawk/_cells.py:55-58).
-__device__ __forceinline__ void neumaier_add(double& h, double& c, double x, double xc) {
-    const double s = h + x;
+template <class T>
+__device__ __forceinline__ void neumaier_add(T& h, T& c, T x, T xc) {
+    const T s = h + x;
     const bool fin = finite_bits(s);
-    c = fin ? c + two_sum_err(h, x, s) : 0.0;
-    c = fin ? c + xc : 0.0;
+    c = fin ? c + two_sum_err(h, x, s) : T(0);
+    c = fin ? c + xc : T(0);
     h = s;
 }
 
 // Two partials combined (reference hawk/_cells.py:61-63).
-__device__ __forceinline__ void pair_add(double& h, double& c, double h2, double c2) {
-    const double s = h + h2;
-    c = finite_bits(s) ? (c + c2) + two_sum_err(h, h2, s) : 0.0;
+template <class T>
+__device__ __forceinline__ void pair_add(T& h, T& c, T h2, T c2) {
+    const T s = h + h2;
+    c = finite_bits(s) ? (c + c2) + two_sum_err(h, h2, s) : T(0);
     h = s;
 }
 
-// Leaf j: rows [j*4096, min((j+1)*4096, rows)).
-__global__ __launch_bounds__(kRowSlots) void hawk_rows_leaves(const double* __restrict__ hi,
-                                                              const double* __restrict__ comp, long long rows,
-                                                              double* __restrict__ leaf_h,
-                                                              double* __restrict__ leaf_c) {
-    __shared__ double sh[kRowSlots], sc[kRowSlots];
+// Leaf j: rows [j*4096, min((j+1)*4096, rows)).  T is the rows' type: the
+// finish runs in it, as the reference's finish runs in the rows' dtype.
+template <class T>
+__global__ __launch_bounds__(kRowSlots) void hawk_rows_leaves(const T* __restrict__ hi, const T* __restrict__ comp,
+                                                              long long rows, T* __restrict__ leaf_h,
+                                                              T* __restrict__ leaf_c) {
+    __shared__ T sh[kRowSlots], sc[kRowSlots];
     const int s = threadIdx.x;
     const long long lo = static_cast<long long>(blockIdx.x) * kRowLeaf;
     const long long rest = rows - lo;
     const int cnt = rest < kRowLeaf ? static_cast<int>(rest) : static_cast<int>(kRowLeaf);
     const int live = cnt < kRowSlots ? cnt : kRowSlots;
     if (s < live) {
-        double h = hi[lo + s];
-        double c = finite_bits(h) ? comp[lo + s] : 0.0;
+        T h = hi[lo + s];
+        T c = finite_bits(h) ? comp[lo + s] : T(0);
         for (int k = 1; k < kRowTerms; ++k) {
             const int m = live < cnt - k * kRowSlots ? live : cnt - k * kRowSlots;
             if (m <= 0 || s >= m) break;
@@ -266,7 +271,7 @@ __global__ __launch_bounds__(kRowSlots) void hawk_rows_leaves(const double* __re
     for (int off = kRowSlots / 2; off > 0; off >>= 1) {
         const int lim = live > off ? (off < live - off ? off : live - off) : 0;
         if (s < lim) {
-            double h = sh[s], c = sc[s];
+            T h = sh[s], c = sc[s];
             pair_add(h, c, sh[s + off], sc[s + off]);
             sh[s] = h;
             sc[s] = c;
@@ -282,17 +287,17 @@ __global__ __launch_bounds__(kRowSlots) void hawk_rows_leaves(const double* __re
 // The leaves folded pairwise level by level by one workgroup, ping-ponging
 // between the two halves of the scratch; the cell gets hi + comp (hi alone
 // when it is not finite).
-__global__ __launch_bounds__(256) void hawk_rows_levels(double* __restrict__ buf, long long leaves,
-                                                        double* __restrict__ out) {
-    double* vh = buf;
-    double* vc = buf + leaves;
-    double* nh = buf + 2 * leaves;
-    double* nc = buf + 3 * leaves;
+template <class T>
+__global__ __launch_bounds__(256) void hawk_rows_levels(T* __restrict__ buf, long long leaves, T* __restrict__ out) {
+    T* vh = buf;
+    T* vc = buf + leaves;
+    T* nh = buf + 2 * leaves;
+    T* nc = buf + 3 * leaves;
     long long m = leaves;
     while (m > 1) {
         const long long pairs = m / 2;
         for (long long p = threadIdx.x; p < pairs; p += 256) {
-            double h = vh[2 * p], c = vc[2 * p];
+            T h = vh[2 * p], c = vc[2 * p];
             pair_add(h, c, vh[2 * p + 1], vc[2 * p + 1]);
             nh[p] = h;
             nc[p] = c;
@@ -302,8 +307,8 @@ __global__ __launch_bounds__(256) void hawk_rows_levels(double* __restrict__ buf
             nc[pairs] = vc[m - 1];
         }
         __syncthreads();
-        double* th = vh; vh = nh; nh = th;
-        double* tc = vc; vc = nc; nc = tc;
+        T* th = vh; vh = nh; nh = th;
+        T* tc = vc; vc = nc; nc = tc;
         m = pairs + (m & 1);
     }
     if (threadIdx.x == 0) *out = finite_bits(vh[0]) ? vh[0] + vc[0] : vh[0];
@@ -1686,6 +1691,24 @@ int scratch_of(hipStream_t stream, void** out) {
     return HK_OK;
 }
 
+// The rows' finish in T: the leaves, then the levels into *out.
+template <class T>
+int rows_finish(const T* hi, const T* comp, int64_t rows, T* out, void* scratch, void* stream, const char* name) {
+    if (rows < 1) return hawk_internal::set_error(HK_EVALUE, std::string(name) + ": rows must be >= 1");
+    if (!hi || !comp || !out || !scratch)
+        return hawk_internal::set_error(HK_EVALUE, std::string(name) + ": hi, comp, out and scratch are required");
+    const long long leaves = (rows + kRowLeaf - 1) / kRowLeaf;
+    if (leaves > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, std::string(name) + ": too many rows");
+    auto* buf = static_cast<T*>(scratch);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(hawk_rows_leaves<T>, dim3(static_cast<unsigned>(leaves)), dim3(kRowSlots), 0, s, hi, comp,
+                       static_cast<long long>(rows), buf, buf + leaves);
+    int rc = launch_error("hawk_rows_leaves launch");
+    if (rc != HK_OK) return rc;
+    hipLaunchKernelGGL(hawk_rows_levels<T>, dim3(1), dim3(256), 0, s, buf, leaves, out);
+    return launch_error("hawk_rows_levels launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -1807,19 +1830,12 @@ size_t hk_rows_finish_scratch_bytes(int64_t rows) {
 
 int hk_rows_finish_f64(const double* hi, const double* comp, int64_t rows, double* out, void* scratch,
                        void* stream) {
-    if (rows < 1) return hawk_internal::set_error(HK_EVALUE, "hk_rows_finish_f64: rows must be >= 1");
-    if (!hi || !comp || !out || !scratch)
-        return hawk_internal::set_error(HK_EVALUE, "hk_rows_finish_f64: hi, comp, out and scratch are required");
-    const long long leaves = (rows + kRowLeaf - 1) / kRowLeaf;
-    if (leaves > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_rows_finish_f64: too many rows");
-    auto* buf = static_cast<double*>(scratch);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(hawk_rows_leaves, dim3(static_cast<unsigned>(leaves)), dim3(kRowSlots), 0, s, hi, comp,
-                       static_cast<long long>(rows), buf, buf + leaves);
-    int rc = launch_error("hawk_rows_leaves launch");
-    if (rc != HK_OK) return rc;
-    hipLaunchKernelGGL(hawk_rows_levels, dim3(1), dim3(256), 0, s, buf, leaves, out);
-    return launch_error("hawk_rows_levels launch");
+    return rows_finish(hi, comp, rows, out, scratch, stream, "hk_rows_finish_f64");
+}
+
+int hk_rows_finish_f32(const float* hi, const float* comp, int64_t rows, float* out, void* scratch,
+                       void* stream) {
+    return rows_finish(hi, comp, rows, out, scratch, stream, "hk_rows_finish_f32");
 }
 
 size_t hk_band_rows_finish_scratch_bytes(int64_t rows) { return hk_rows_finish_scratch_bytes(rows); }

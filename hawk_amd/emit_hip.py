@@ -557,7 +557,7 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
         decls[scratch] = ir.Decl(scratch, "fold_scratch", ir.TensorType((), "i32"))
     for _, _, hi, comp in rows:
         for pname in (hi, comp):
-            decls[pname] = ir.Decl(pname, "rows_out", ir.TensorType((), "f64"))
+            decls[pname] = ir.Decl(pname, "rows_out", ir.TensorType((), "f32" if mode == "float32" else "f64"))
     prog2 = Program(decls, program.sinks, program.grid, program.tables)
     spec = ir.arg_spec(prog2, used)
     for role, name in spec:
@@ -706,7 +706,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         # past `count` computes sample `base` (always bound) and adds +0.
         out += wrap.index_prologue(block, per_thread, xcd_order, form="live")
         out += body
-        opened, closed = wrap.sample_sum_frame(len(row_terms), "double", "")
+        opened, closed = wrap.sample_sum_frame(len(row_terms), "Real", "")
         out += opened + ["    " + line for line in stores] + closed
         for k, (term, hi, comp) in enumerate(row_terms):
             out += w.spell.sample_sum(w, stage.banded, term, hi, comp)
@@ -1282,20 +1282,20 @@ __device__ __forceinline__ void hk_fold_store(double s, int c, unsigned long lon
 #: and of its host row walk.  The combine is symmetric, so both lanes of a
 #: pair hold its bits and every lane of the half ends with the row's partial.
 _ROW_SUM_HELPERS = """
-__device__ __forceinline__ bool hk_finite(double x) { return (x - x) == 0.0; }
-__device__ __forceinline__ double hk_two_sum_err(double a, double b, double s) {
+__device__ __forceinline__ bool hk_finite(Real x) { return (x - x) == Real(0); }
+__device__ __forceinline__ Real hk_two_sum_err(Real a, Real b, Real s) {
     const bool big_a = fabs(a) >= fabs(b);
-    const double big = big_a ? a : b;
-    const double small = big_a ? b : a;
-    return hk_finite(s) ? (small - (s - big)) + 0.0 : __builtin_nan("");
+    const Real big = big_a ? a : b;
+    const Real small = big_a ? b : a;
+    return hk_finite(s) ? (small - (s - big)) + Real(0) : Real(__builtin_nan(""));
 }
-__device__ __forceinline__ void hk_row_sum(double& h, double& c) {
+__device__ __forceinline__ void hk_row_sum(Real& h, Real& c) {
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1) {
-        const double h2 = __shfl_xor(h, off, 64);
-        const double c2 = __shfl_xor(c, off, 64);
-        const double t = h + h2;
-        c = hk_finite(t) ? (c + c2) + hk_two_sum_err(h, h2, t) : 0.0;
+        const Real h2 = __shfl_xor(h, off, 64);
+        const Real c2 = __shfl_xor(c, off, 64);
+        const Real t = h + h2;
+        c = hk_finite(t) ? (c + c2) + hk_two_sum_err(h, h2, t) : Real(0);
         h = t;
     }
 }
@@ -1514,8 +1514,6 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                          "width": width})
             continue
         if isinstance(s, SampleSum) and s.policy != "ordered" and s.group is None:
-            if mode != "float64":
-                raise HawkError(f"hawk.sum(policy={s.policy!r}) on the hip target is built in float64")
             row_sums.append((s.name, s.value))
             team.append({"op": "band_rows" if banded else "row_sum", "hi": f"hk_rows_{s.name}",
                          "comp": f"hk_rows_{s.name}_comp", "out": s.name})
@@ -1580,7 +1578,7 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
                 planes[pname] = {"role": "cell" if t["op"] in ("ordered_sum", "row_sum", "keyed_sum", "keyed_comp",
                                                               "band_rows", "band_ordered_sum")
                                  else "accum_out",
-                                 "shape": [], "dtype": "f64"}
+                                 "shape": [], "dtype": "f32" if mode == "float32" else "f64"}
                 if t["op"] in ("keyed_sum", "keyed_comp"):
                     planes[pname]["group"] = t["group"]       # one cell per `group` samples
     for pname, info in planes.items():

@@ -220,7 +220,7 @@ class HipWriter:
         half-wave's row of 32 (compensated pairs, or double-double bands in
         the banded mode; a lane past ``count`` adds +0) and lane 0 of the half
         stores the row."""
-        return [f"        {{ double hk_rh = hk_live ? static_cast<double>({term}) : 0.0, hk_rc = 0.0;",
+        return [f"        {{ Real hk_rh = hk_live ? static_cast<Real>({term}) : Real(0), hk_rc = Real(0);",
                 f"          {'hk_band_row_sum' if banded else 'hk_row_sum'}(hk_rh, hk_rc);",
                 "          if ((threadIdx.x & 31) == 0 && hk_live) {",
                 "              const long long hk_r = (base + hk_flat) >> 5;",

@@ -264,8 +264,12 @@ class DeviceKernel:
             if not x.is_contiguous():
                 problems.append(f"{name!r} is not contiguous; pass x.contiguous()")
                 continue
+            # a cell or scatter target holds its declared type (a float32
+            # build's default sum has a float32 cell); a per-sample plane the
+            # build's Real
             want = torch.int32 if info["dtype"] in ("i32", "u32") else torch.bool if info["dtype"] == "bool" else (
-                torch.float64 if role in ("cell", "accum_out") else self._real_dtype())
+                (torch.float32 if info["dtype"] == "f32" else torch.float64) if role in ("cell", "accum_out")
+                else self._real_dtype())
             if x.dtype != want:
                 problems.append(f"{name!r} has dtype {x.dtype}, the kernel reads {want}")
                 continue
@@ -348,8 +352,11 @@ class DeviceKernel:
         with _on(stream):
             nbytes = (_core.band_rows_finish_scratch_bytes if band else _core.rows_finish_scratch_bytes)(rows)
             scratch = self._buffer(("rows", t["out"], rows), nbytes, device, zero=False)
-        (_core.band_rows_finish if band else _core.rows_finish)(bound[t["hi"]].data_ptr(), bound[t["comp"]].data_ptr(), rows, out.data_ptr(),
-                          scratch.data_ptr(), stream)
+        if band:
+            finish = _core.band_rows_finish
+        else:       # the rows are the stage's Real: the finish runs in it
+            finish = _core.rows_finish_f32 if self.planes[t["hi"]]["dtype"] == "f32" else _core.rows_finish
+        finish(bound[t["hi"]].data_ptr(), bound[t["comp"]].data_ptr(), rows, out.data_ptr(), scratch.data_ptr(), stream)
 
     def _term_plane(self, name: str, n: int, device):
         torch = _torch()
@@ -358,8 +365,9 @@ class DeviceKernel:
         key = ("plane", name, n)
         held = self._scratch.get(key)
         if held is None or held.device != device:
-            if info.get("rows"):                       # one row partial per `rows` samples
-                held = torch.empty(max(1, -(-n // info["rows"])), dtype=torch.float64, device=device)
+            if info.get("rows"):                       # one row partial per `rows` samples, in the stage's Real
+                held = torch.empty(max(1, -(-n // info["rows"])),
+                                   dtype=torch.float32 if info["dtype"] == "f32" else torch.float64, device=device)
             elif info.get("group"):                    # one entry per key (`group` samples)
                 held = torch.empty(lead + (n // info["group"],), dtype=torch.int32, device=device)
             else:

@@ -215,6 +215,13 @@ int hk_keyed_sample_sum_f64(const double* u, int64_t n, int64_t group, double* o
 size_t hk_rows_finish_scratch_bytes(int64_t rows);
 int hk_rows_finish_f64(const double* hi, const double* comp, int64_t rows,
                        double* out, void* scratch, void* stream);
+/* The same finish of float32 rows in float32 arithmetic: the float32 scalar
+ * mode's default-policy sum (reference `hawk/_cells.py:44-119` runs the
+ * finish in the rows' dtype, float32 in that mode; the rows are the
+ * per-sample stage's in `Real`, reference `hawk/emit/wrapper.py:542-665`).
+ * Scratch: hk_rows_finish_scratch_bytes(rows) bytes. */
+int hk_rows_finish_f32(const float* hi, const float* comp, int64_t rows,
+                       float* out, void* scratch, void* stream);
 
 /* Banded reductions: the sample sums of the banded scalar mode (reference
  * `hawk/emit/wrapper.py:140` BANDED and its row sum `:542-665`,

@@ -256,6 +256,107 @@ HKO_EXPORT double hko_rows_finish(const double* hi, const double* comp, int64_t 
     return out;
 }
 
+/* The float32 scalar mode's default-policy sum: the same rows and finish in
+ * float32 arithmetic (the reference's rows are the stage's `Real`, float in
+ * that mode, and hawk/_cells.py:44-119 runs the finish in the rows' dtype). */
+static int fin_f(float x) { return (x - x) == 0.0f; }
+
+static float two_sum_err_f(float a, float b, float s) {
+    const int big_a = fabsf(a) >= fabsf(b);
+    const float big = big_a ? a : b, small = big_a ? b : a;
+    return fin_f(s) ? (small - (s - big)) + 0.0f : NAN;
+}
+
+static void pair_add_f(float* h, float* c, float h2, float c2) {
+    const float s = *h + h2;
+    *c = fin_f(s) ? (*c + c2) + two_sum_err_f(*h, h2, s) : 0.0f;
+    *h = s;
+}
+
+static void neumaier_add_f(float* h, float* c, float x, float xc) {
+    const float s = *h + x;
+    *c = fin_f(s) ? *c + two_sum_err_f(*h, x, s) : 0.0f;
+    *c = fin_f(s) ? *c + xc : 0.0f;
+    *h = s;
+}
+
+HKO_EXPORT void hko_row_sums_f32(const float* t, int64_t n, float* hi, float* comp) {
+    const int64_t rows = (n + 31) / 32;
+    for (int64_t r = 0; r < rows; ++r) {
+        float h[32], c[32];
+        for (int l = 0; l < 32; ++l) {
+            h[l] = r * 32 + l < n ? t[r * 32 + l] : 0.0f;
+            c[l] = 0.0f;
+        }
+        for (int off = 16; off >= 1; off >>= 1)
+            for (int l = 0; l < off; ++l) pair_add_f(&h[l], &c[l], h[l + off], c[l + off]);
+        hi[r] = h[0];
+        comp[r] = c[0];
+    }
+}
+
+static void rows_leaf_f(const float* hi, const float* comp, int cnt, float* lh, float* lc) {
+    float sh[256], sc[256];
+    const int live = cnt < 256 ? cnt : 256;
+    for (int s = 0; s < live; ++s) {
+        sh[s] = hi[s];
+        sc[s] = fin_f(hi[s]) ? comp[s] : 0.0f;
+    }
+    for (int k = 1; k < 16; ++k) {
+        const int m = live < cnt - k * 256 ? live : cnt - k * 256;
+        if (m <= 0) break;
+        for (int s = 0; s < m; ++s) neumaier_add_f(&sh[s], &sc[s], hi[k * 256 + s], comp[k * 256 + s]);
+    }
+    for (int off = 128; off > 0; off >>= 1) {
+        const int lim = live > off ? (off < live - off ? off : live - off) : 0;
+        for (int s = 0; s < lim; ++s) pair_add_f(&sh[s], &sc[s], sh[s + off], sc[s + off]);
+    }
+    *lh = sh[0];
+    *lc = sc[0];
+}
+
+HKO_EXPORT float hko_rows_finish_f32(const float* hi, const float* comp, int64_t rows) {
+    if (rows <= 0) return 0.0f;
+    const int64_t leaves = (rows + 4095) / 4096;
+    float* vh = (float*)malloc(sizeof(float) * (size_t)leaves);
+    float* vc = (float*)malloc(sizeof(float) * (size_t)leaves);
+    for (int64_t j = 0; j < leaves; ++j) {
+        const int64_t rest = rows - j * 4096;
+        rows_leaf_f(hi + j * 4096, comp + j * 4096, (int)(rest < 4096 ? rest : 4096), &vh[j], &vc[j]);
+    }
+    int64_t m = leaves;
+    while (m > 1) {
+        const int64_t pairs = m / 2;
+        for (int64_t p = 0; p < pairs; ++p) {
+            float h = vh[2 * p], c = vc[2 * p];
+            pair_add_f(&h, &c, vh[2 * p + 1], vc[2 * p + 1]);
+            vh[p] = h;
+            vc[p] = c;
+        }
+        if (m & 1) {
+            vh[pairs] = vh[m - 1];
+            vc[pairs] = vc[m - 1];
+        }
+        m = pairs + (m & 1);
+    }
+    const float out = fin_f(vh[0]) ? vh[0] + vc[0] : vh[0];
+    free(vh);
+    free(vc);
+    return out;
+}
+
+HKO_EXPORT float hko_sample_sum_f32(const float* t, int64_t n) {
+    const int64_t rows = (n + 31) / 32;
+    if (rows == 0) return 0.0f;
+    float* hi = (float*)malloc(sizeof(float) * (size_t)rows);
+    float* comp = (float*)malloc(sizeof(float) * (size_t)rows);
+    hko_row_sums_f32(t, n, hi, comp);
+    const float out = hko_rows_finish_f32(hi, comp, rows);
+    free(hi);
+    free(comp);
+    return out;
+}
+
 HKO_EXPORT double hko_sample_sum(const double* t, int64_t n) {
     const int64_t rows = (n + 31) / 32;
     if (rows == 0) return 0.0;

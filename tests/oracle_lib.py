@@ -67,6 +67,9 @@ def lib(profile: str | None = None):
         "hko_row_sums": (None, [_P, _I64, _P, _P]),
         "hko_rows_finish": (_D, [_P, _P, _I64]),
         "hko_sample_sum": (_D, [_P, _I64]),
+        "hko_row_sums_f32": (None, [_P, _I64, _P, _P]),
+        "hko_rows_finish_f32": (ctypes.c_float, [_P, _P, _I64]),
+        "hko_sample_sum_f32": (ctypes.c_float, [_P, _I64]),
         "hko_band_row_sums": (None, [_P, _I64, _P, _P]),
         "hko_band_rows_finish": (_D, [_P, _P, _I64]),
         "hko_band_sample_sum": (_D, [_P, _I64]),
@@ -276,6 +279,27 @@ def sample_sum(t) -> float:
     """The default-policy hawk.sum of the terms t (rows, then the canonical finish)."""
     t = np.ascontiguousarray(t, dtype=np.float64)
     return lib().hko_sample_sum(_p(t), t.size)
+
+
+def row_sums_f32(t):
+    """The float32 mode's rows: the compensated (hi, comp) of every 32 terms, in float32."""
+    t = np.ascontiguousarray(t, dtype=np.float32)
+    rows = -(-t.size // 32)
+    hi, comp = np.empty(rows, dtype=np.float32), np.empty(rows, dtype=np.float32)
+    lib().hko_row_sums_f32(_p(t), t.size, _p(hi), _p(comp))
+    return hi, comp
+
+
+def rows_finish_f32(hi, comp) -> np.float32:
+    hi = np.ascontiguousarray(hi, dtype=np.float32)
+    comp = np.ascontiguousarray(comp, dtype=np.float32)
+    return np.float32(lib().hko_rows_finish_f32(_p(hi), _p(comp), hi.size))
+
+
+def sample_sum_f32(t) -> np.float32:
+    """The float32 mode's default-policy hawk.sum of the terms t (rows, then the canonical finish, in float32)."""
+    t = np.ascontiguousarray(t, dtype=np.float32)
+    return np.float32(lib().hko_sample_sum_f32(_p(t), t.size))
 
 
 def band_row_sums(t):

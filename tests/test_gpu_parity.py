@@ -520,6 +520,45 @@ def test_default_sum_is_the_oracle_bitwise(unit, gpu, n):
         assert host(y).tobytes() == (2.0 * x).tobytes()
 
 
+@pytest.mark.parametrize("n", [1, 33, 1000, 4096 * 32 + 5, 300_001])
+def test_float32_default_sum_is_the_oracle_bitwise(unit32, gpu, n):
+    """The float32 mode's hawk.sum(x * x): float32 rows on the device (the
+    stage's half-wave butterflies in float32) and the float32 finish, the
+    float32 oracle's bits on every replay; y = 2 x in float32."""
+    import hawk_amd as hawk
+    g = rng(n)
+    x = (g.normal(size=n) * np.exp(g.normal(size=n))).astype(np.float32)
+    k = _load(unit32, "sample_total")
+    want = O.sample_sum_f32(x * x)
+    print(f"float32 default sum n={n}", flush=True)
+    for _ in range(3):
+        y = dev(np.zeros(n, dtype=np.float32), gpu)
+        total = dev(np.zeros(1, dtype=np.float32), gpu)
+        hawk.run(k, x=dev(x, gpu), y=y, total=total)
+        assert host(total)[0].tobytes() == want.tobytes()
+        assert host(y).tobytes() == (np.float32(2.0) * x).tobytes()
+
+
+def test_float32_default_sum_special_values(unit32, gpu):
+    import hawk_amd as hawk
+    k = _load(unit32, "plain_total")
+
+    def total_of(x):
+        t = dev(np.full(1, 7.0, dtype=np.float32), gpu)
+        hawk.run(k, x=dev(np.asarray(x, dtype=np.float32), gpu), total=t)
+        return host(t)[0]
+    z = total_of(np.zeros(1000))
+    assert z == 0.0 and not np.signbit(z)
+    x = np.ones(5000, dtype=np.float32)
+    x[1234] = np.inf
+    assert total_of(x) == np.inf
+    x[999] = -np.inf
+    assert np.isnan(total_of(x))
+    assert total_of(np.float32([1e8, 1.0, -1e8])) == 1.0
+    x = (np.arange(1, 200_001) % 97).astype(np.float32)
+    assert total_of(x) == O.sample_sum_f32(x)
+
+
 def test_default_sum_special_values(unit, gpu):
     import hawk_amd as hawk
     k = _load(unit, "plain_total")

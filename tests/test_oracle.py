@@ -315,6 +315,65 @@ def test_row_sums_compensate_cancellation():
     assert np.max(np.abs(plain[:, 0] - exact) / _ulp(exact)) > 100
 
 
+# -- the float32 mode's default-policy sum: the same algorithm in float32 -----
+
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 1000, 65536])
+def test_float32_rows_are_compensated_sums(n):
+    """Each float32 row's hi + comp (read exactly in float64) is the row's
+    exact sum to within 2^-44 of its sum of |term|: the compensation keeps
+    about twice float32's precision, which the plain float32 pairwise tree of
+    the same rows misses by orders of magnitude (a dropped or sign-flipped
+    compensation fails)."""
+    import math
+    g = np.random.default_rng(n)
+    t = (g.normal(size=n) * np.exp(g.normal(size=n))).astype(np.float32)
+    hi, comp = O.row_sums_f32(t)
+    assert hi.dtype == np.float32 and comp.dtype == np.float32
+    pad = np.zeros(hi.size * 32, dtype=np.float32)
+    pad[:n] = t
+    rows = pad.reshape(-1, 32).astype(np.float64)
+    exact = np.array([math.fsum(r) for r in rows])
+    got = hi.astype(np.float64) + comp.astype(np.float64)
+    assert np.all(np.abs(got - exact) <= 2.0 ** -44 * np.abs(rows).sum(1) + 1e-300)
+    plain = pad.reshape(-1, 32).copy()
+    w = 16
+    while w:
+        plain[:, :w] += plain[:, w:2 * w]
+        w //= 2
+    if n >= 1000:
+        assert np.max(np.abs(plain[:, 0].astype(np.float64) - exact) / (np.abs(rows).sum(1) + 1e-300)) > 2.0 ** -30
+
+
+@pytest.mark.parametrize("rows", [1, 257, 4097, 3 * 4096 + 17])
+def test_float32_finish_is_within_an_ulp_of_the_exact_sum(rows):
+    """The float32 finish across leaf boundaries equals the exact sum of every
+    hi and comp to within one float32 ulp (the last rounding of hi + comp is
+    half of it), and an exactly representable total comes out exactly."""
+    import math
+    g = np.random.default_rng(rows)
+    hi = (g.normal(size=rows) * np.exp(g.normal(size=rows))).astype(np.float32)
+    comp = (hi * g.normal(size=rows) * np.float32(2.0 ** -26)).astype(np.float32)
+    exact = math.fsum(np.concatenate([hi, comp]).astype(np.float64))
+    got = O.rows_finish_f32(hi, comp)
+    assert isinstance(got, np.float32)
+    assert abs(float(got) - exact) <= float(np.spacing(np.float32(abs(exact))))
+    ints = g.integers(-1000, 1000, rows).astype(np.float32)
+    assert float(O.rows_finish_f32(ints, np.zeros_like(ints))) == float(ints.astype(np.int64).sum())
+
+
+def test_float32_sum_is_float32_arithmetic():
+    """The float32 sum is not the float64 sum rounded at the end: terms whose
+    float32 partials round differ from the float64 oracle's, and both agree
+    with the exact sum to their own precision."""
+    import math
+    t = (np.arange(1, 5001, dtype=np.float64) / 7.0).astype(np.float32)
+    s32 = O.sample_sum_f32(t)
+    exact = math.fsum(t.astype(np.float64))
+    assert abs(float(s32) - exact) <= float(np.spacing(np.float32(exact)))
+    assert abs(O.sample_sum(t.astype(np.float64)) - exact) <= np.spacing(exact)
+    assert float(O.sample_sum_f32(np.float32([1e8, 1.0, -1e8]))) == 1.0
+
+
 @pytest.mark.parametrize("rows", [1, 255, 256, 257, 4095, 4096, 4097, 3 * 4096 + 17, 70000])
 def test_rows_finish_is_the_correctly_rounded_sum(rows):
     """The finish across leaf boundaries (4096 rows a leaf) equals fsum of
