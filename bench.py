@@ -5,7 +5,7 @@ A step is one pass of the hot path over one batch of synthetic inputs already
 resident in HBM.  The default workload is BASELINE.json's ``configs[1]``: the
 ``energy`` kernel's forward, VJP and JVP over N = 2^25 samples (fp64).  Other
 configurations (``--config 1|3|4a|4b|5``) time the remaining workloads the same
-way; ``--config 5k`` times config 5's ordered sum in the reference's keyed
+way; ``--config 4b64`` is config 4b's product in the float64 mode; ``--config 5k`` times config 5's ordered sum in the reference's keyed
 spelling (``hawk.sum(x, over=...)``) over 16384 keys, ``--config 5t`` a
 ``Table`` read at config 5's keys and its VJP (an ordered scatter), and
 ``--config 5n`` 65536 small models in one launch (the net axis): each net's
@@ -194,26 +194,30 @@ def workload(config: str, device):
             O.spd_solve(A, b, threads=threads)
             O.spd_solve_vjp(A, b, bar_x, threads=threads)
         return dict(name="6x6 SPD solve fwd + VJP (config 4a)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64")
-    if config == "4b":
+    if config in ("4b", "4b64"):
+        # 4b64: the same product in the float64 mode (fp64 planes, v_mfma_f64_16x16x4f64)
+        f64 = config == "4b64"
+        nt, tdt, esize = (np.float64, torch.float64, 8) if f64 else (np.float32, torch.float32, 4)
         n = 1 << 20
         g = np.random.default_rng(4)
-        A = g.normal(0.0, 0.25, size=(16, 16, n)).astype(np.float32)
-        B = g.normal(0.0, 0.25, size=(16, 16, n)).astype(np.float32)
-        bar_C = np.random.default_rng(104).normal(0.0, 0.25, size=(16, 16, n)).astype(np.float32)
-        hawk.build([E.mm16, E.mm16_vjp], unit, mode="float32")
+        A = g.normal(0.0, 0.25, size=(16, 16, n)).astype(nt)
+        B = g.normal(0.0, 0.25, size=(16, 16, n)).astype(nt)
+        bar_C = np.random.default_rng(104).normal(0.0, 0.25, size=(16, 16, n)).astype(nt)
+        hawk.build([E.mm16, E.mm16_vjp], unit, mode="float64" if f64 else "float32")
         kf, kv = hawk.load(unit, "mm16"), hawk.load(unit, "mm16_vjp")
         Ad, Bd, BC = _dev(A, device), _dev(B, device), _dev(bar_C, device)
-        C, BA, BB = (torch.zeros((16, 16, n), dtype=torch.float32, device=device) for _ in range(3))
+        C, BA, BB = (torch.zeros((16, 16, n), dtype=tdt, device=device) for _ in range(3))
         kernels = [kf.prepare(A=Ad, B=Bd, C=C), kv.prepare(A=Ad, B=Bd, bar_C=BC, bar_A=BA, bar_B=BB)]
-        # labels are the team stage's: the forward's mm16 launch, then the VJP's
-        work = {"mm16": (3072, 8192), "mm16#2": (5120, 16384)}
+        # labels are the team stage's: the forward's mm16 launch, then the VJP's;
+        # bytes are 768 (fwd) and 1280 (VJP) elements a sample
+        work = {"mm16": (768 * esize, 8192), "mm16#2": (1280 * esize, 16384)}
 
         def cpu(threads):
             import oracle_lib as O
             O.mm16(A, B, threads=threads)
             O.mm16_vjp(A, B, bar_C, threads=threads)
-        return dict(name="fp32 16x16 product fwd + VJP (config 4b)", n=n, kernels=kernels, work=work, cpu=cpu,
-                    dtype="f32")
+        what = "fp64 16x16 product fwd + VJP (config 4b in float64)" if f64 else "fp32 16x16 product fwd + VJP (config 4b)"
+        return dict(name=what, n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64" if f64 else "f32")
     if config == "5":
         n = 1 << 26
         g = np.random.default_rng(5)
@@ -482,10 +486,11 @@ def workload(config: str, device):
 #: step launches once; a base label's kernels may serve several stages.
 STAGE_KERNELS = {"ordered_sum": ("hawk_sum_lanes", "hawk_sum_fold"),
                  "band_ordered_sum": ("hawk_band_sum_lanes", "hawk_band_sum_fold"),
-                 "ordered_scatter": ("hawk_scatter_status", "hawk_scatter_walk", "hawk_scatter_cells"),
-                 "mm16": ("hawk_mm16_f32",),
+                 "ordered_scatter": ("hawk_scatter_status", "hawk_split_hot", "hawk_split_tail", "hawk_fill_zero",
+                                     "hawk_scatter_walk", "hawk_scatter_serial", "hawk_scatter_cells"),
+                 "mm16": ("hawk_mm16_f32", "hawk_mm16_f64"),
                  "keyed_sum": ("hawk_keyed_rows",),      # keys of at most 65536 samples (config 5k: 4096)
-                 "mm16#2": ("hawk_mm16_f32_shared",),
+                 "mm16#2": ("hawk_mm16_f32_shared", "hawk_mm16_f64_shared"),
                  "ordered_fold": ("hawk_log_fold_lanes", "hawk_log_fold_waves")}
 COPY_PROBE_BYTES = 1 << 30
 

@@ -70,6 +70,7 @@ def _declare(lib) -> None:
         "hk_keyed_ordered_sum_scratch_bytes": (SZ, [I64, I64]),
         "hk_keyed_ordered_sum_f64": (I, [V, I64, I64, V, V, V]),
         "hk_mm16_f32": (I, [ctypes.POINTER(V), I, ctypes.POINTER(V), I, ctypes.POINTER(ctypes.c_int32), I64, V]),
+        "hk_mm16_f64": (I, [ctypes.POINTER(V), I, ctypes.POINTER(V), I, ctypes.POINTER(ctypes.c_int32), I64, V]),
         "hk_keyed_log_fold_scratch_bytes": (SZ, [I64]),
         "hk_keyed_sample_sum_f64": (I, [V, I64, I64, V, V]),
         "hk_keyed_log_fold_f64": (I, [V, I64, V, I64, I64, ctypes.c_int32, V, I64, V, V, V]),
@@ -314,16 +315,25 @@ def ordered_scatter(key: int, v: int, n: int, target: int, cells: int, scratch: 
                                        ctypes.c_void_p(status), ctypes.c_void_p(stream or None)))
 
 
-def mm16(ins: list, outs: list, products: list, n: int, stream: int = 0) -> None:
-    """Per-sample 16x16 fp32 products on MFMA: ``outs[o] = op(ins[lhs]) @ op(ins[rhs])``
-    for ``products[o] = (lhs, rhs, transpose_lhs, transpose_rhs)``; planes by pointer."""
+def mm16(ins: list, outs: list, products: list, n: int, stream: int = 0, dtype: str = "f32") -> None:
+    """Per-sample 16x16 products on MFMA: ``outs[o] = op(ins[lhs]) @ op(ins[rhs])``
+    for ``products[o] = (lhs, rhs, transpose_lhs, transpose_rhs)``; planes by
+    pointer, all of ``dtype`` ("f32" or "f64")."""
+    if dtype not in ("f32", "f64"):
+        raise ValueError(f"mm16: dtype must be 'f32' or 'f64', not {dtype!r}")
     flat = []
     for lhs, rhs, tl, tr in products:
         flat += [int(lhs), int(rhs), (1 if tl else 0) | (2 if tr else 0)]
     c_in = (ctypes.c_void_p * len(ins))(*[ctypes.c_void_p(p) for p in ins])
     c_out = (ctypes.c_void_p * len(outs))(*[ctypes.c_void_p(p) for p in outs])
     c_prod = (ctypes.c_int32 * len(flat))(*flat)
-    check(lib().hk_mm16_f32(c_in, len(ins), c_out, len(outs), c_prod, int(n), ctypes.c_void_p(stream or None)))
+    entry = lib().hk_mm16_f64 if dtype == "f64" else lib().hk_mm16_f32
+    check(entry(c_in, len(ins), c_out, len(outs), c_prod, int(n), ctypes.c_void_p(stream or None)))
+
+
+def mm16_f64(ins: list, outs: list, products: list, n: int, stream: int = 0) -> None:
+    """:func:`mm16` on fp64 planes."""
+    mm16(ins, outs, products, n, stream, "f64")
 
 
 def keyed_ordered_sum_scratch_bytes(n: int, group: int) -> int:

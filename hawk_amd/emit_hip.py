@@ -1484,13 +1484,15 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
             return plan
     if banded:
         mode = "float64"            # the banded mode's values are float64; its reductions fold bands
-    products = _mm16_products(program) if mode == "float32" else None
+    products = _mm16_products(program)
     if products is not None:
         ins, prods = products
         outs = [s.name for s in program.sinks]
-        planes = {pname: {"role": program.decls[pname].role, "shape": [16, 16], "dtype": "f32"}
+        dtype = "f32" if mode == "float32" else "f64"
+        planes = {pname: {"role": program.decls[pname].role, "shape": [16, 16], "dtype": dtype}
                   for pname in ins + outs}
-        return Plan(None, None, [{"op": "mm16", "in": ins, "out": outs, "products": prods}], planes)
+        return Plan(None, None, [{"op": "mm16", "in": ins, "out": outs, "products": prods, "dtype": dtype}],
+                    planes)
     assigned = {id(s.value): s.name for s in program.sinks if isinstance(s, Assign)}
     extra, team, row_sums, key_writes, fused = [], [], [], [], []
     for s in program.sinks:

@@ -259,7 +259,7 @@ FINISHING = {k.name: k for k in (osc_finish, osc_finish_x8, osc_finish_xauto, st
 #: Every kernel above, by name.
 ALL = {k.name: k for k in (scale, energy, energy_vjp, energy_jvp, twobody, twobody_vjp, spd_solve,
                             spd_solve_vjp, chain, chain_steps, ordered_total, ordered_add, sample_total, plain_total,
-                            twobody_vjp_mu, add_sq, add_sq_grad, chain_vjp, chain_jvp)}
+                            twobody_vjp_mu, add_sq, add_sq_grad, chain_vjp, chain_jvp, mm16, mm16_vjp)}
 #: The float32 unit (built with mode="float32").
 FLOAT32 = {k.name: k for k in (mm16, mm16_vjp, sample_total, plain_total)}
 

@@ -509,7 +509,7 @@ class DeviceKernel:
                 statuses.append((t, status, cells))
             elif t["op"] == "mm16":
                 _core.mm16([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
-                           t["products"], n, stream)
+                           t["products"], n, stream, t.get("dtype", "f32"))
             elif t["op"] in ("row_sum", "band_rows"):
                 self._row_sum(t, bound, n, device, stream)
             elif t["op"] == "band_ordered_sum":
@@ -812,7 +812,7 @@ class Prepared:
             elif t["op"] == "mm16":
                 args = ([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
                         t["products"], self.n)
-                self.steps.append((_core.mm16, args))
+                self.steps.append((_core.mm16_f64 if t.get("dtype") == "f64" else _core.mm16, args))
             elif t["op"] in ("row_sum", "band_rows"):
                 self.steps.append((kernel._row_sum, (t, bound, self.n, device)))
             elif t["op"] == "band_ordered_sum":
@@ -863,7 +863,7 @@ class Prepared:
                             per_thread=k.launch_shape["per_thread"], stream=self.stream)
             out.append((k.name, stage))
         labels = {_core.ordered_sum: "ordered_sum", _core.band_ordered_sum: "band_ordered_sum",
-                  _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16",
+                  _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16", _core.mm16_f64: "mm16",
                   _core.keyed_ordered_sum: "keyed_sum", _core.keyed_log_fold: "ordered_fold",
                   _core.keyed_sample_sum: "keyed_comp"}
         for fn, args in self.steps:

@@ -294,6 +294,13 @@ int hk_keyed_log_fold_f64(const double* values, int64_t stride, const int32_t* c
 int hk_mm16_f32(const float* const* in, int n_in, float* const* out, int n_out,
                 const int32_t* products, int64_t n, void* stream);
 
+/* hk_mm16_f32 for fp64 planes ([16, 16, n] doubles), on v_mfma_f64_16x16x4f64:
+ * the per-sample `mm` of reference `hawk/emit/policy.py:283-299` in the
+ * float64 mode (reference `hawk/targets/__init__.py:48-49` builds both scalar
+ * modes), same arguments and refusals. */
+int hk_mm16_f64(const double* const* in, int n_in, double* const* out, int n_out,
+                const int32_t* products, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

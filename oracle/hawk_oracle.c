@@ -999,6 +999,48 @@ HKO_EXPORT void hko_mm16_vjp(const float* A, const float* B, const float* bar_C,
     }
 }
 
+/* The same products in float64 (the reference's float64 mode builds the same
+ * per-sample `mm`, reference hawk/targets/__init__.py:48-49): each element a
+ * sequential sum over k of rounded products, from k = 0. */
+HKO_EXPORT void hko_mm16_f64(const double* A, const double* B, int64_t n, double* C, int64_t base, int64_t count) {
+    for (int64_t i = base; i < base + count; ++i) {
+        double a[HKO_M][HKO_M], b[HKO_M][HKO_M];
+        for (int r = 0; r < HKO_M; ++r)
+            for (int c = 0; c < HKO_M; ++c) {
+                a[r][c] = A[(r * HKO_M + c) * n + i];
+                b[r][c] = B[(r * HKO_M + c) * n + i];
+            }
+        for (int r = 0; r < HKO_M; ++r)
+            for (int c = 0; c < HKO_M; ++c) {
+                double acc = a[r][0] * b[0][c];
+                for (int k = 1; k < HKO_M; ++k) acc = acc + (a[r][k] * b[k][c]);
+                C[(r * HKO_M + c) * n + i] = acc;
+            }
+    }
+}
+
+HKO_EXPORT void hko_mm16_vjp_f64(const double* A, const double* B, const double* bar_C, int64_t n, double* bar_A,
+                                 double* bar_B, int64_t base, int64_t count) {
+    for (int64_t i = base; i < base + count; ++i) {
+        double a[HKO_M][HKO_M], b[HKO_M][HKO_M], g[HKO_M][HKO_M];
+        for (int r = 0; r < HKO_M; ++r)
+            for (int c = 0; c < HKO_M; ++c) {
+                a[r][c] = A[(r * HKO_M + c) * n + i];
+                b[r][c] = B[(r * HKO_M + c) * n + i];
+                g[r][c] = bar_C[(r * HKO_M + c) * n + i];
+            }
+        for (int r = 0; r < HKO_M; ++r)
+            for (int c = 0; c < HKO_M; ++c) {
+                double acc = g[r][0] * b[c][0];
+                for (int k = 1; k < HKO_M; ++k) acc = acc + (g[r][k] * b[c][k]);
+                bar_A[(r * HKO_M + c) * n + i] = acc;
+                double acc2 = a[0][r] * g[0][c];
+                for (int k = 1; k < HKO_M; ++k) acc2 = acc2 + (a[k][r] * g[k][c]);
+                bar_B[(r * HKO_M + c) * n + i] = acc2;
+            }
+    }
+}
+
 /* ---- the CPU baseline's tiling (eagle HostTeam shape) ------------------------
  * [0, n) is cut into T contiguous tiles, one thread per tile calling the
  * serial entry with its own (base, count) (reference hawk/emit/host.py:4-12);
@@ -1089,6 +1131,10 @@ static void* job_main(void* arg) {
             hko_net_loss((const double*)j->in0, (const double*)j->in1, (const double*)j->in2,
                          (const double*)j->in3, j->cells, (double*)j->out0, j->base, j->base + j->count);
             break;
+        case 21: hko_mm16_f64((const double*)j->in0, (const double*)j->in1, j->n, (double*)j->out0, j->base,
+                              j->count); break;
+        case 22: hko_mm16_vjp_f64((const double*)j->in0, (const double*)j->in1, (const double*)j->in2, j->n,
+                                  (double*)j->out0, (double*)j->out1, j->base, j->count); break;
         case 18: hko_chain_members((const double*)j->in0, (double*)j->out0, (double*)j->out1, j->n, j->base,
                                    j->count); break;
         case 17:   /* nets [base, base+count): their gradients wrt w */

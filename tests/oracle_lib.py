@@ -84,6 +84,8 @@ def lib(profile: str | None = None):
         "hko_spd_solve_vjp": (None, [_P, _P, _P, _I64, _P, _P, _I64, _I64]),
         "hko_mm16": (None, [_P, _P, _I64, _P, _I64, _I64]),
         "hko_mm16_vjp": (None, [_P, _P, _P, _I64, _P, _P, _I64, _I64]),
+        "hko_mm16_f64": (None, [_P, _P, _I64, _P, _I64, _I64]),
+        "hko_mm16_vjp_f64": (None, [_P, _P, _P, _I64, _P, _P, _I64, _I64]),
         "hko_tiled": (None, [ctypes.c_int, _P, _P, _P, _P, _P, _P, _D, _D, _I64, ctypes.c_int]),
         "hko_ordered_sum_threads": (_D, [_P, _I64, ctypes.c_int]),
         "hko_ordered_scatter_threads": (None, [_P, _P, _I64, _P, _I64, _P, _P, ctypes.c_int]),
@@ -390,6 +392,13 @@ def spd_solve_vjp(A, b, bar_x, threads: int = 1):
 def mm16(A, B, threads: int = 1):
     n = A.shape[-1]
     C = np.empty_like(A)
+    if A.dtype == np.float64:
+        assert B.dtype == np.float64
+        if threads > 1:
+            lib().hko_tiled(21, _p(A), _p(B), None, None, _p(C), None, 0.0, 0.0, n, threads)
+        else:
+            lib().hko_mm16_f64(_p(A), _p(B), n, _p(C), 0, n)
+        return C
     if threads > 1:
         lib().hko_tiled(13, _p(A), _p(B), None, None, _p(C), None, 0.0, 0.0, n, threads)
     else:
@@ -400,6 +409,13 @@ def mm16(A, B, threads: int = 1):
 def mm16_vjp(A, B, bar_C, threads: int = 1):
     n = A.shape[-1]
     bA, bB = np.empty_like(A), np.empty_like(B)
+    if A.dtype == np.float64:
+        assert B.dtype == bar_C.dtype == np.float64
+        if threads > 1:
+            lib().hko_tiled(22, _p(A), _p(B), _p(bar_C), None, _p(bA), _p(bB), 0.0, 0.0, n, threads)
+        else:
+            lib().hko_mm16_vjp_f64(_p(A), _p(B), _p(bar_C), n, _p(bA), _p(bB), 0, n)
+        return bA, bB
     if threads > 1:
         lib().hko_tiled(14, _p(A), _p(B), _p(bar_C), None, _p(bA), _p(bB), 0.0, 0.0, n, threads)
     else:

@@ -142,6 +142,15 @@ def test_team_stage_arguments_are_checked_before_any_launch():
     # the per-sample products: plane counts and indices are checked first
     rc = L.hk_mm16_f32(None, 0, None, 1, None, 1, None)
     assert rc != 0 and b"1..3 input planes" in L.hk_last_error()
+    rc = L.hk_mm16_f64(None, 2, None, 1, None, 1, None)
+    assert rc != 0 and b"hk_mm16_f64: in, out and products are required" in L.hk_last_error()
+    ins = (ctypes.c_void_p * 2)(1, 2)
+    outs = (ctypes.c_void_p * 1)(3)
+    prods = (ctypes.c_int32 * 3)(0, 2, 0)
+    rc = L.hk_mm16_f64(ins, 2, outs, 1, prods, 1, None)
+    assert rc != 0 and b"outside [0, n_in)" in L.hk_last_error()
+    prods = (ctypes.c_int32 * 3)(0, 1, 0)
+    assert L.hk_mm16_f64(ins, 2, outs, 1, prods, 0, None) == 0     # no samples: nothing launched
 
 
 def test_scatter_chunk_rule():

@@ -266,16 +266,19 @@ def test_fp_op_count_of_the_emitted_stages():
     assert count(E.twobody) == 40 * 32
 
 
-def test_mm16_and_its_vjp_are_one_mfma_team_stage(tmp_path):
-    """In float32 a kernel whose sinks are 16x16 products of input planes runs
-    as one mm16 team stage: the forward one product, the VJP two with the
-    transposes of bar_A = bar_C B^T and bar_B = A^T bar_C."""
-    b = hawk.build([E.mm16, E.mm16_vjp], tmp_path, mode="float32")
+@pytest.mark.parametrize("mode,dtype", [("float32", "f32"), ("float64", "f64")])
+def test_mm16_and_its_vjp_are_one_mfma_team_stage(tmp_path, mode, dtype):
+    """In either scalar mode a kernel whose sinks are 16x16 products of input
+    planes runs as one mm16 team stage of that mode's planes: the forward one
+    product, the VJP two with the transposes of bar_A = bar_C B^T and
+    bar_B = A^T bar_C."""
+    b = hawk.build([E.mm16, E.mm16_vjp], tmp_path, mode=mode)
     fwd, rev = b.sidecar("mm16"), b.sidecar("mm16_vjp")
     assert fwd["entry"] is None and fwd["team"] == [{"op": "mm16", "in": ["A", "B"], "out": ["C"],
-                                                     "products": [[0, 1, False, False]]}]
+                                                     "products": [[0, 1, False, False]], "dtype": dtype}]
+    assert {p["dtype"] for p in fwd["planes"].values()} == {dtype}
     (t,) = rev["team"]
-    assert t["out"] == ["bar_A", "bar_B"]
+    assert t["out"] == ["bar_A", "bar_B"] and t["dtype"] == dtype
     named = [(t["in"][l], t["in"][r], tl, tr) for l, r, tl, tr in t["products"]]
     assert named == [("bar_C", "B", False, True), ("A", "bar_C", True, False)]
 

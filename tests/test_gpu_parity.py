@@ -499,6 +499,46 @@ def test_mm16_forward_and_vjp_on_mfma(unit32, gpu, n):
     assert (np.abs(host(bB) - wB) <= 2 * _mm_bound(At, bar_C)).all()
 
 
+#: gamma_16 = 16u / (1 - 16u), u = 2^-53: a 16-term fp64 dot product summed in
+#: any order, with any mix of rounded and fused steps, lies within
+#: gamma_16 * sum_k |x_ik| |y_kj| of the exact value (about 1.8e-15 of the
+#: magnitudes, inside the north star's 1e-13 relative bar for fp64).
+_GAMMA16 = 16 * 2.0 ** -53 / (1 - 16 * 2.0 ** -53)
+
+
+def _mm_exact_ld(X, Y):
+    L = np.longdouble
+    return np.einsum("ikn,kjn->ijn", X.astype(L), Y.astype(L))
+
+
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 33, 1000, 65_537])
+def test_mm16_f64_forward_and_vjp_on_mfma(unit, gpu, n):
+    """The float64 mode's C = A @ B and its VJP on v_mfma_f64_16x16x4f64: on
+    integer inputs (every partial sum exact) the bits of the oracle's loop;
+    on normal inputs every element within gamma_16 * sum |a||b| of the
+    product in long double, and within twice that of the oracle."""
+    import hawk_amd as hawk
+    g = rng(5)
+    ints = [g.integers(-8, 9, size=(16, 16, n)).astype(np.float64) for _ in range(3)]
+    normals = [g.normal(0.0, 0.25, size=(16, 16, n)) for _ in range(3)]
+    for exact, (A, B, bar_C) in ((True, ints), (False, normals)):
+        C = dev(np.zeros((16, 16, n)), gpu)
+        hawk.run(_load(unit, "mm16"), A=dev(A, gpu), B=dev(B, gpu), C=C)
+        bA, bB = dev(np.zeros((16, 16, n)), gpu), dev(np.zeros((16, 16, n)), gpu)
+        hawk.run(_load(unit, "mm16_vjp"), A=dev(A, gpu), B=dev(B, gpu), bar_C=dev(bar_C, gpu), bar_A=bA, bar_B=bB)
+        got = [host(C), host(bA), host(bB)]
+        Bt, At = B.transpose(1, 0, 2), A.transpose(1, 0, 2)
+        pairs = [(A, B), (bar_C, Bt), (At, bar_C)]
+        want = [O.mm16(A, B), *O.mm16_vjp(A, B, bar_C)]
+        for x, w, (X, Y) in zip(got, want, pairs):
+            if exact:
+                assert x.tobytes() == w.tobytes()
+                continue
+            bound = _GAMMA16 * np.einsum("ikn,kjn->ijn", np.abs(X), np.abs(Y))
+            assert (np.abs(x.astype(np.longdouble) - _mm_exact_ld(X, Y)) <= bound).all()
+            assert (np.abs(x - w) <= 2 * bound).all()
+
+
 
 # -- the default-policy sample sum (a7') ----------------------------------------
 

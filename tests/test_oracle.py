@@ -261,6 +261,33 @@ def test_mm16_brute_force_and_vjp():
     np.testing.assert_allclose(bB, wB, rtol=1e-4, atol=1e-5)
 
 
+def test_mm16_f64_is_exact_on_integers_and_within_the_dot_bound():
+    """The float64 products: on small integers every product and partial sum
+    is exact, so C, bar_A and bar_B must equal the integer products bit for
+    bit (a dropped term, a swapped index or a missing transpose changes them);
+    on normal inputs each element lies within gamma_15 * sum |a||b| of the
+    product in long double (the textbook bound of a 16-term dot product)."""
+    g = np.random.default_rng(18)
+    n = 40
+    Ai, Bi, Gi = (g.integers(-8, 9, size=(16, 16, n)) for _ in range(3))
+    A, B, G = (x.astype(np.float64) for x in (Ai, Bi, Gi))
+    assert (O.mm16(A, B) == np.einsum("ikn,kjn->ijn", Ai, Bi)).all()
+    bA, bB = O.mm16_vjp(A, B, G)
+    assert (bA == np.einsum("ikn,jkn->ijn", Gi, Bi)).all()
+    assert (bB == np.einsum("kin,kjn->ijn", Ai, Gi)).all()
+    A, B, G = (g.normal(0, 0.25, size=(16, 16, n)) for _ in range(3))
+    gamma = 15 * 2.0 ** -53 / (1 - 15 * 2.0 ** -53)
+    L = np.longdouble
+    want = np.einsum("ikn,kjn->ijn", A.astype(L), B.astype(L))
+    scale = np.einsum("ikn,kjn->ijn", np.abs(A), np.abs(B))
+    assert (np.abs(O.mm16(A, B).astype(L) - want) <= gamma * scale).all()
+    bA, bB = O.mm16_vjp(A, B, G)
+    assert (np.abs(bA.astype(L) - np.einsum("ikn,jkn->ijn", G.astype(L), B.astype(L)))
+            <= gamma * np.einsum("ikn,jkn->ijn", np.abs(G), np.abs(B))).all()
+    assert (np.abs(bB.astype(L) - np.einsum("kin,kjn->ijn", A.astype(L), G.astype(L)))
+            <= gamma * np.einsum("kin,kjn->ijn", np.abs(A), np.abs(G))).all()
+
+
 def test_threaded_tiles_are_the_serial_bits():
     x = np.random.default_rng(9).normal(size=100_003)
     assert O.chain(x, threads=7).tobytes() == O.chain(x).tobytes()
