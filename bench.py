@@ -217,7 +217,11 @@ def workload(config: str, device):
             O.mm16(A, B, threads=threads)
             O.mm16_vjp(A, B, bar_C, threads=threads)
         what = "fp64 16x16 product fwd + VJP (config 4b in float64)" if f64 else "fp32 16x16 product fwd + VJP (config 4b)"
-        return dict(name=what, n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64" if f64 else "f32")
+        # each stage's HBM pattern (element rows read, rows written, tile samples, threads), for pattern_ceiling
+        tile = 256 // esize
+        pattern = {"mm16": (512, 256, tile, 16 * tile), "mm16#2": (768, 512, tile // 2, 8 * tile)}
+        return dict(name=what, n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64" if f64 else "f32",
+                    pattern=pattern, esize=esize)
     if config == "5":
         n = 1 << 26
         g = np.random.default_rng(5)
@@ -503,6 +507,97 @@ def _kernel_base(name: str) -> str:
     return name[len("void "):] if name.startswith("void ") else name
 
 
+_PATTERN_SOURCE = """
+typedef {elem} E;
+struct GRefMirror {{ void* data_; unsigned long long samples_, compStride_, sampleStride_; int deviceType_, deviceId_; }};
+extern "C" __attribute__((used)) __device__ char eagle_abi_tag[] = "aether-abi/2";
+extern "C" __attribute__((used)) __device__ unsigned long long eagle_layout_sizes[5] = {{40, 32, 32, 8, 24}};
+// The HBM pattern of a per-sample 16x16 product stage without its arithmetic:
+// a workgroup reads a tile of {tile} consecutive samples from {rows_in} element
+// rows (rows nSamples apart) and writes {rows_out} rows, every load issued
+// before the first is used.  Tiles are handed out XCD by XCD like the product's.
+extern "C" __global__ void __launch_bounds__({threads}) hawk_pattern_copy(
+        GRefMirror in_m, GRefMirror out_m, long long base, long long count, long long nSamples) {{
+    const E* in = static_cast<const E*>(in_m.data_);
+    E* out = static_cast<E*>(out_m.data_);
+    constexpr int kStep = {threads} / {tile}, kIn = {rows_in} / kStep, kOut = {rows_out} / kStep;
+    const long long tiles = count / {tile};
+    const long long per_xcd = (tiles + 7) / 8;
+    const long long tile = static_cast<long long>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (tile >= tiles) return;
+    const long long s0 = base + tile * {tile} + threadIdx.x % {tile};
+    const int e_own = threadIdx.x / {tile};
+    E x[kIn];
+#pragma unroll
+    for (int r = 0; r < kIn; ++r)
+        x[r] = __builtin_nontemporal_load(in + static_cast<long long>(e_own + r * kStep) * nSamples + s0);
+#pragma unroll
+    for (int r = 0; r < kOut; ++r) {{
+        E v = x[r];
+        if (r + kOut < kIn) v += x[r + kOut];
+        __builtin_nontemporal_store(v, out + static_cast<long long>(e_own + r * kStep) * nSamples + s0);
+    }}
+}}
+"""
+
+
+def pattern_ceiling(w, device, reps: int = 10) -> dict:
+    """Per stage of ``w`` that names its HBM pattern: the rate (algorithmic
+    GB/s) of a copy kernel with exactly that pattern and no arithmetic, built
+    by hipRTC and launched through ``hk_launch_grid`` on the stage's stream:
+    the ceiling that layout and tile shape leave the stage."""
+    import torch
+
+    from hawk_amd import _core
+    from hawk_amd.compile import compile_source
+    out = {}
+    n, esize = w["n"], w["esize"]
+    dt = torch.float64 if esize == 8 else torch.float32
+    for label, (rows_in, rows_out, tile, threads) in w["pattern"].items():
+        src = _PATTERN_SOURCE.format(elem="double" if esize == 8 else "float", rows_in=rows_in,
+                                     rows_out=rows_out, tile=tile, threads=threads)
+        code, _key, _hit = compile_source(src, "hawk_pattern_copy")
+        entry = _core.DeviceLibrary(code).entry("hawk_pattern_copy")
+        src_t = torch.zeros((rows_in, n), dtype=dt, device=device)
+        dst_t = torch.empty((rows_out, n), dtype=dt, device=device)
+        ab = _core.ArgBlock(["gref", "gref"])
+        ab.bind(0, src_t.data_ptr(), n)
+        ab.bind(1, dst_t.data_ptr(), n)
+        if n % tile:
+            raise ValueError(f"pattern_ceiling: N={n} is not a multiple of the tile ({tile})")
+        grid = 8 * ((n // tile + 7) // 8)
+        stream = torch.cuda.current_stream()
+        launch = lambda: entry.run_grid(ab, 0, n, n, grid, threads, stream.cuda_stream)  # noqa: E731
+        for _ in range(3):
+            launch()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            launch()
+        b.record(stream)
+        b.synchronize()
+        ms = a.elapsed_time(b) / reps
+        gbs = (rows_in + rows_out) * esize * n / (ms * 1e-3) / 1e9
+        out[label] = {"pattern": f"{rows_in} rows in, {rows_out} out, {tile}-sample tiles of {threads} threads",
+                      "ms": round(ms, 5), "copy_GBs": round(gbs, 1)}
+        del src_t, dst_t
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+def _with_pattern(w, device, per_stage: dict) -> dict:
+    """``pattern_ceiling`` of ``w``'s stages, each with the stage's fraction of it."""
+    if "pattern" not in w:
+        return {}
+    ceil = pattern_ceiling(w, device)
+    for label, c in ceil.items():
+        if label in per_stage:
+            c["stage_of_pattern"] = round(per_stage[label]["achieved_GBs"] / c["copy_GBs"], 4)
+    log(f"pattern ceilings: {ceil}")
+    return ceil
+
+
 def _pmc_pass(counter: str, config: str) -> dict:
     """One ``rocprofv3 --pmc <counter>`` pass over a short run of this bench
     (plus the 1 GiB copy probe) in a child process: ``{kernel: [KiB per dispatch]}``."""
@@ -673,12 +768,14 @@ def config_record(config: str, device, steps: int = 5, warmup: int = 2) -> dict:
     log(f"config {config}: record")
     w = workload(config, device)
     t = time_steps(w, steps, warmup)
+    ceiling = _with_pattern(w, device, t["per_stage"])
     rate, reps, cpu_s = cpu_rate(w, host_cores(), "native", 0.0)
     rec = {"workload": w["name"], "N": w["n"], "dtype": w["dtype"], "ms_per_step": round(t["ms_step"], 5),
            "samples_per_s": w["n"] / (t["ms_step"] * 1e-3),
            "stages": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                       for k, v in t["per_stage"].items()},
            "roofline": roofline_of(w, t["per_stage"]),
+           **({"pattern_ceiling": ceiling} if ceiling else {}),
            "cpu_baseline": {"value": rate, "unit": "samples/s", "cores": w.get("cpu_threads") or host_cores(),
                             "kind": "port", "sample": f"the full step on the C oracle (native profile), "
                                                       f"{reps} repetition(s) after 1 warm-up"}}
@@ -723,6 +820,7 @@ def main() -> int:
         torch.cuda.synchronize()
         log("copy probe: 1 GiB read + 1 GiB written by one copy kernel")
         del src, dst
+    ceiling = _with_pattern(w, device, per_stage)
     dominant = max(per_stage, key=lambda k: per_stage[k]["ms"])
     d = per_stage[dominant]
     traffic = None
@@ -782,6 +880,7 @@ def main() -> int:
         "config": {"workload": name, "N": n, **compare,
                    "stages": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                               for k, v in per_stage.items()},
+                   **({"pattern_ceiling": ceiling} if ceiling else {}),
                    **({"configs": records} if records else {})},
         "roofline": roofline, "cpu_baseline": cpu_baseline, "wall_s": round(wall, 3),
     }

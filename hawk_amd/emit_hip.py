@@ -660,6 +660,22 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
             w.emit(f"{where} = {w.value(node)[0]};")
     stores = list(w.lines)
     w.lines = []
+    # the same commits with their values taken from hk_sv[hk_v][k] (the
+    # two-pass full-block form): only when every written plane holds Real
+    deferred = None
+    if not stage.key_writes and all(stage.planes[p].get("dtype") in (None, "f64", "f32") for p, _ in stage.writes):
+        deferred = ([], [])
+        for plane, node in stage.writes:
+            var = stage.planes[plane]["var"]
+            vals = w.value(node)
+            comps = [None] if not node.ttype.shape else [_flat(node.ttype.shape, e) for e in _entries(node.ttype.shape)]
+            for c in comps:
+                k = len(deferred[0])
+                deferred[0].append(f"hk_sv[hk_v][{k}] = {vals[0 if c is None else c]};")
+                deferred[1].append(w.spell.component_commit(w, var, c, "=", f"hk_sv[hk_v][{k}]"))
+        if w.lines or len(stores) != len(deferred[0]):
+            deferred = None               # the stores computed a value of their own: keep one pass
+        w.lines = []
     row_terms = [(w.value(node)[0], stage.planes[hi]["var"], stage.planes[comp]["var"])
                  for _, node, hi, comp in stage.row_sums]
     folds = [(stage.planes[out]["var"], stage.planes[scratch]["var"], [w.value(v)[0] for v in values],
@@ -699,7 +715,26 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += wrap.index_prologue(block, per_thread, xcd_order, form="guard")
         out += _guarded_lines(stage, w, body, stores)
     elif not row_terms and not folds:
-        out += wrap.index_prologue(block, per_thread, xcd_order, form="plain")
+        if per_thread > 1 and deferred and deferred[0]:
+            # a full block in two passes: every sample's values (and so every
+            # load) first, then every store, so no load waits behind a store
+            keep, commit = deferred
+            head = wrap.index_prologue(block, per_thread, xcd_order, form="full")
+            at = next(i for i, line in enumerate(head) if line.startswith("    if (")) + 1
+            out += head[:at] + [f"    Real hk_sv[{per_thread}][{len(keep)}];"] + head[at:]
+            out += body + ["        " + line for line in keep]
+            out += ["    }", "#pragma unroll",
+                    f"    for (int hk_v = 0; hk_v < {per_thread}; ++hk_v) {{",
+                    f"        const long long hk_i = base + (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * "
+                    f"{block} + static_cast<long long>(threadIdx.x);"]
+            out += ["        " + line for line in commit]
+            out += wrap.index_partial(block, per_thread)
+        elif per_thread > 1:
+            out += wrap.index_prologue(block, per_thread, xcd_order, form="full")
+            out += body + stores
+            out += wrap.index_partial(block, per_thread)
+        else:
+            out += wrap.index_prologue(block, per_thread, xcd_order, form="plain")
         out += body + stores
     else:
         # Every lane of a half-wave takes part in its row's butterfly: a lane

@@ -313,10 +313,18 @@ class HipWrapper:
                    " : (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3);"]
         else:
             out = ["    const unsigned hk_blk = blockIdx.x;"]
+        if form == "full":
+            # a block whose samples all lie below `count` runs the unguarded
+            # copy of the body: no exit between samples, so every sample's
+            # loads can issue before the first store (the partial last block
+            # takes the guarded copy that index_partial opens)
+            out += [f"    if ((static_cast<long long>(hk_blk) + 1) * {per_thread * block} <= count) {{"]
         out += ["#pragma unroll",
                 f"    for (int hk_v = 0; hk_v < {per_thread}; ++hk_v) {{",
                 f"        const long long hk_flat = (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * {block}"
                 " + static_cast<long long>(threadIdx.x);"]
+        if form == "full":
+            out += ["        const long long hk_i = base + hk_flat;"]
         if form == "plain":
             out += ["        if (hk_flat >= count) break;",
                     "        const long long hk_i = base + hk_flat;"]
@@ -324,6 +332,17 @@ class HipWrapper:
             out += ["        const bool hk_live = hk_flat < count;",
                     "        const long long hk_i = base + (hk_live ? hk_flat : 0LL);"]
         return out
+
+    def index_partial(self, block: int, per_thread: int) -> list:
+        """After the full block's body (``form="full"``): close it and open the
+        guarded loop of the partial last block."""
+        return ["    }", "    return;", "    }",
+                "#pragma unroll",
+                f"    for (int hk_v = 0; hk_v < {per_thread}; ++hk_v) {{",
+                f"        const long long hk_flat = (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * {block}"
+                " + static_cast<long long>(threadIdx.x);",
+                "        if (hk_flat >= count) break;",
+                "        const long long hk_i = base + hk_flat;"]
 
     def index_epilogue(self) -> list:
         return ["    }", "}", ""]
