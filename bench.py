@@ -218,8 +218,8 @@ def workload(config: str, device):
             O.mm16_vjp(A, B, bar_C, threads=threads)
         what = "fp64 16x16 product fwd + VJP (config 4b in float64)" if f64 else "fp32 16x16 product fwd + VJP (config 4b)"
         # each stage's HBM pattern (element rows read, rows written, tile samples, threads), for pattern_ceiling
-        tile = 256 // esize
-        pattern = {"mm16": (512, 256, tile, 16 * tile), "mm16#2": (768, 512, tile // 2, 8 * tile)}
+        tile = 256 // esize      # hawk_linalg.hip's shapes: 16 threads a sample (fp32), 32 (fp64 forward)
+        pattern = {"mm16": (512, 256, tile, (32 if f64 else 16) * tile), "mm16#2": (768, 512, tile // 2, 8 * tile)}
         return dict(name=what, n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64" if f64 else "f32",
                     pattern=pattern, esize=esize)
     if config == "5":
@@ -531,6 +531,13 @@ extern "C" __global__ void __launch_bounds__({threads}) hawk_pattern_copy(
 #pragma unroll
     for (int r = 0; r < kIn; ++r)
         x[r] = __builtin_nontemporal_load(in + static_cast<long long>(e_own + r * kStep) * nSamples + s0);
+    if ({read_only}) {{           // the reads alone: one store a thread, never taken for finite data
+        E a = x[0];
+#pragma unroll
+        for (int r = 1; r < kIn; ++r) a += x[r];
+        if (a != a) out[threadIdx.x] = a;
+        return;
+    }}
 #pragma unroll
     for (int r = 0; r < kOut; ++r) {{
         E v = x[r];
@@ -554,32 +561,36 @@ def pattern_ceiling(w, device, reps: int = 10) -> dict:
     n, esize = w["n"], w["esize"]
     dt = torch.float64 if esize == 8 else torch.float32
     for label, (rows_in, rows_out, tile, threads) in w["pattern"].items():
-        src = _PATTERN_SOURCE.format(elem="double" if esize == 8 else "float", rows_in=rows_in,
-                                     rows_out=rows_out, tile=tile, threads=threads)
-        code, _key, _hit = compile_source(src, "hawk_pattern_copy")
-        entry = _core.DeviceLibrary(code).entry("hawk_pattern_copy")
+        if n % tile:
+            raise ValueError(f"pattern_ceiling: N={n} is not a multiple of the tile ({tile})")
         src_t = torch.zeros((rows_in, n), dtype=dt, device=device)
         dst_t = torch.empty((rows_out, n), dtype=dt, device=device)
         ab = _core.ArgBlock(["gref", "gref"])
         ab.bind(0, src_t.data_ptr(), n)
         ab.bind(1, dst_t.data_ptr(), n)
-        if n % tile:
-            raise ValueError(f"pattern_ceiling: N={n} is not a multiple of the tile ({tile})")
         grid = 8 * ((n // tile + 7) // 8)
         stream = torch.cuda.current_stream()
-        launch = lambda: entry.run_grid(ab, 0, n, n, grid, threads, stream.cuda_stream)  # noqa: E731
-        for _ in range(3):
-            launch()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(reps):
-            launch()
-        b.record(stream)
-        b.synchronize()
-        ms = a.elapsed_time(b) / reps
-        gbs = (rows_in + rows_out) * esize * n / (ms * 1e-3) / 1e9
+        rate = {}
+        for read_only in (0, 1):
+            src = _PATTERN_SOURCE.format(elem="double" if esize == 8 else "float", rows_in=rows_in,
+                                         rows_out=rows_out, tile=tile, threads=threads, read_only=read_only)
+            code, _key, _hit = compile_source(src, "hawk_pattern_copy")
+            entry = _core.DeviceLibrary(code).entry("hawk_pattern_copy")
+            launch = lambda: entry.run_grid(ab, 0, n, n, grid, threads, stream.cuda_stream)  # noqa: E731
+            for _ in range(3):
+                launch()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(reps):
+                launch()
+            b.record(stream)
+            b.synchronize()
+            ms = a.elapsed_time(b) / reps
+            moved = rows_in if read_only else rows_in + rows_out
+            rate[read_only] = (ms, moved * esize * n / (ms * 1e-3) / 1e9)
         out[label] = {"pattern": f"{rows_in} rows in, {rows_out} out, {tile}-sample tiles of {threads} threads",
-                      "ms": round(ms, 5), "copy_GBs": round(gbs, 1)}
+                      "ms": round(rate[0][0], 5), "copy_GBs": round(rate[0][1], 1),
+                      "reads_only_GBs": round(rate[1][1], 1)}
         del src_t, dst_t
     torch.cuda.synchronize()
     torch.cuda.empty_cache()

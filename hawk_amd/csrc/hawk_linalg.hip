@@ -9,9 +9,9 @@
 //
 // A workgroup takes a tile of consecutive samples whose element rows are
 // 256-byte runs in HBM for one product (fp32: 64 samples on 1024 threads;
-// fp64: 32 on 512) and 128-byte runs for two (fp32: 32 on 512; fp64: 16 on
-// 256; the VJP's second set of accumulators would otherwise cost occupancy):
-// sixteen threads per sample, four samples per wave, whatever the type.
+// fp64: 32 on 1024) and 128-byte runs for two (fp32: 32 on 512; fp64: 16 on
+// 512, or on 256 when the two share a plane; the VJP's second set of
+// accumulators would otherwise cost occupancy).
 // Workgroup i runs on XCD i % 8, so tiles are handed out XCD by XCD in
 // contiguous eighths: the tiles one XCD's L2 serves are neighbours, which
 // share the lines a run straddles when N*sizeof(T) is not a multiple of 128.
@@ -87,12 +87,14 @@ __device__ __forceinline__ int rhs_elem(int lane, int q, int t) {
     return t ? j * kDim + k : k * kDim + j;
 }
 
-// The launch shape per element type and number of products: TILE samples on
-// THREADS = 16 * TILE threads, TILE * sizeof(T) = 256 bytes for one product
-// and 128 for two.
+// The launch shape per element type and number of products: TILE samples,
+// TILE * sizeof(T) = 256 bytes for one product and 128 for two, on 16 threads
+// a sample for fp32 and 32 for fp64.  With 32, a thread stages half an fp64
+// slice's rows and a CU has twice as many rows in flight (the fp64 forward at
+// 2^20 samples: 1.30 ms on 512 threads, 1.25 ms on 1024).
 template <class T, int NOUT> struct Shape {
     static constexpr int kTile = 256 / static_cast<int>(sizeof(T)) / NOUT;
-    static constexpr int kThreads = 16 * kTile;
+    static constexpr int kThreads = (sizeof(T) == 8 ? 32 : 16) * kTile;
 };
 
 // LDS (NOUT products): during the products, slot (o*2 + side)*64 + l holds,
