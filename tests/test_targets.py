@@ -108,3 +108,13 @@ def test_the_build_records_what_the_row_says(tmp_path):
     assert (tmp_path / side["code_object"]).is_file() and (tmp_path / side["source"]).is_file()
     assert (manifest["target"], manifest["offload_arch"]) == (hip.id, hip.offload_arch)
     assert bundle.digest == manifest["digest"]
+
+
+def test_the_latency_probe_builds_for_gfx950(tmp_path):
+    """hawk_amd.latency's probe kernel compiles through the build's hipRTC path
+    and carries the ABI tag every loaded code object is checked for."""
+    from hawk_amd import latency
+    from hawk_amd.compile import compile_source
+    code, _key, hit = compile_source(latency._SOURCE, "hawk_latency", cache_dir=tmp_path)
+    assert not hit and code[:4] == b"\x7fELF" and b"aether-abi/2" in code
+    assert sorted(latency.PROBES) == list(range(len(latency.PROBES)))
