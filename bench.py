@@ -193,7 +193,11 @@ def workload(config: str, device):
             import oracle_lib as O
             O.spd_solve(A, b, threads=threads)
             O.spd_solve_vjp(A, b, bar_x, threads=threads)
-        return dict(name="6x6 SPD solve fwd + VJP (config 4a)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64")
+        # each stage's HBM pattern: element rows read and written, one sample a thread
+        bf, bv = kf.launch_shape["block"], kv.launch_shape["block"]
+        pattern = {"spd_solve": (42, 6, bf, bf), "spd_solve_vjp": (48, 42, bv, bv)}
+        return dict(name="6x6 SPD solve fwd + VJP (config 4a)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
+                    pattern=pattern, esize=8)
     if config in ("4b", "4b64"):
         # 4b64: the same product in the float64 mode (fp64 planes, v_mfma_f64_16x16x4f64)
         f64 = config == "4b64"
@@ -539,9 +543,10 @@ extern "C" __global__ void __launch_bounds__({threads}) hawk_pattern_copy(
         return;
     }}
 #pragma unroll
-    for (int r = 0; r < kOut; ++r) {{
+    for (int r = 0; r < kOut; ++r) {{              // output row r folds input rows r, r + kOut, ...
         E v = x[r];
-        if (r + kOut < kIn) v += x[r + kOut];
+#pragma unroll
+        for (int j = r + kOut; j < kIn; j += kOut) v += x[j];
         __builtin_nontemporal_store(v, out + static_cast<long long>(e_own + r * kStep) * nSamples + s0);
     }}
 }}
