@@ -54,6 +54,9 @@ def _declare(lib) -> None:
         "hk_launch_grid": (I, [V, V, I64, I64, I64, ctypes.c_uint32, ctypes.c_uint32, V]),
         "hk_ordered_sum_scratch_bytes": (SZ, []),
         "hk_ordered_sum_f64": (I, [V, I64, V, V, V]),
+        "hk_ordered_sum_f32": (I, [V, I64, V, V, V]),
+        "hk_keyed_ordered_sum_f32": (I, [V, I64, I64, V, V, V]),
+        "hk_ordered_scatter_f32": (I, [V, V, I64, V, I64, V, V, V]),
         "hk_ordered_fold_f64": (I, [V, V, V, V]),
         "hk_ordered_sum_noalloc_scratch_bytes": (SZ, []),
         "hk_ordered_sum_f64_noalloc": (I, [V, I64, V, V]),
@@ -293,6 +296,12 @@ def ordered_sum(u: int, n: int, out: int, scratch: int, stream: int = 0) -> None
                                    ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
 
 
+def ordered_sum_f32(u: int, n: int, out: int, scratch: int, stream: int = 0) -> None:
+    """:func:`ordered_sum` of a float32 plane into a float32 cell."""
+    check(lib().hk_ordered_sum_f32(ctypes.c_void_p(u or None), int(n), ctypes.c_void_p(out),
+                                   ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
+
+
 def ordered_sum_noalloc(u: int, n: int, out: int, stream: int = 0) -> None:
     """The ordered sum on the library's static per-GPU scratch: no device
     memory is allocated (for callers that cannot allocate)."""
@@ -311,6 +320,14 @@ def ordered_scatter_scratch_bytes(n: int, cells: int) -> int:
 def ordered_scatter(key: int, v: int, n: int, target: int, cells: int, scratch: int, status: int,
                     stream: int = 0) -> None:
     check(lib().hk_ordered_scatter_f64(ctypes.c_void_p(key or None), ctypes.c_void_p(v or None), int(n),
+                                       ctypes.c_void_p(target), int(cells), ctypes.c_void_p(scratch),
+                                       ctypes.c_void_p(status), ctypes.c_void_p(stream or None)))
+
+
+def ordered_scatter_f32(key: int, v: int, n: int, target: int, cells: int, scratch: int, status: int,
+                        stream: int = 0) -> None:
+    """:func:`ordered_scatter` of float32 values into a float32 target."""
+    check(lib().hk_ordered_scatter_f32(ctypes.c_void_p(key or None), ctypes.c_void_p(v or None), int(n),
                                        ctypes.c_void_p(target), int(cells), ctypes.c_void_p(scratch),
                                        ctypes.c_void_p(status), ctypes.c_void_p(stream or None)))
 
@@ -343,6 +360,12 @@ def keyed_ordered_sum_scratch_bytes(n: int, group: int) -> int:
 def keyed_ordered_sum(u: int, n: int, group: int, out: int, scratch: int, stream: int = 0) -> None:
     """``out[k]`` = key k's ``group`` rows by the ordered sum's tree, k < n / group."""
     check(lib().hk_keyed_ordered_sum_f64(ctypes.c_void_p(u or None), int(n), int(group), ctypes.c_void_p(out),
+                                         ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
+
+
+def keyed_ordered_sum_f32(u: int, n: int, group: int, out: int, scratch: int, stream: int = 0) -> None:
+    """:func:`keyed_ordered_sum` of a float32 plane into float32 cells."""
+    check(lib().hk_keyed_ordered_sum_f32(ctypes.c_void_p(u or None), int(n), int(group), ctypes.c_void_p(out),
                                          ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
 
 

@@ -38,17 +38,18 @@ constexpr size_t kSumScratch = kLanesBytes + kGpBytes + 256;
 // so each lane keeps kSumUnroll loads in flight; the adds stay in row order.
 // The fold's ticket is cleared here, one launch ahead of the fold that takes
 // it, so a sum never depends on what an earlier call left in its scratch.
-__global__ __launch_bounds__(kLaneBlock) void hawk_sum_lanes(const double* __restrict__ u,
+template <class T>
+__global__ __launch_bounds__(kLaneBlock) void hawk_sum_lanes(const T* __restrict__ u,
                                                               long long n,
-                                                              double* __restrict__ lanes,
+                                                              T* __restrict__ lanes,
                                                               unsigned* __restrict__ ticket) {
     const long long l = static_cast<long long>(blockIdx.x) * kLaneBlock + threadIdx.x;
     if (l == 0) *ticket = 0u;
-    double s = 0.0;
+    T s = T(0);
     long long r = l;
     constexpr long long kStep = kVirtualLanes;
     for (; r + (kSumUnroll - 1) * kStep < n; r += kSumUnroll * kStep) {
-        double a[kSumUnroll];
+        T a[kSumUnroll];
 #pragma unroll
         for (int k = 0; k < kSumUnroll; ++k) a[k] = __builtin_nontemporal_load(u + r + k * kStep);
 #pragma unroll
@@ -61,11 +62,12 @@ __global__ __launch_bounds__(kLaneBlock) void hawk_sum_lanes(const double* __res
 // Group g of 1024 lanes folded by s[i] += s[i+w], w = 512..1, into gp[g]; the
 // last group to finish folds the 64 group values by the same tree, w = 32..1,
 // and stores the result.  The ticket is left at zero for the next call.
-__global__ __launch_bounds__(256) void hawk_sum_fold(const double* __restrict__ lanes,
-                                                     double* __restrict__ gp,
+template <class T>
+__global__ __launch_bounds__(256) void hawk_sum_fold(const T* __restrict__ lanes,
+                                                     T* __restrict__ gp,
                                                      unsigned* __restrict__ ticket,
-                                                     double* __restrict__ out) {
-    __shared__ double sh[kFoldLanes];
+                                                     T* __restrict__ out) {
+    __shared__ T sh[kFoldLanes];
     __shared__ unsigned last;
     const int g = blockIdx.x;
     const int t = threadIdx.x;
@@ -533,13 +535,14 @@ __global__ __launch_bounds__(256) void hawk_keyed_comp_wave(const double* __rest
 // trees need only their first P = min(1024, 2^ceil(log2 lv)) lanes and first
 // Q = 2^ceil(log2 groups) group values: the bits of the full trees.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void hawk_keyed_lanes(const double* __restrict__ u, long long group, long long lv,
-                                                        long long total, double* __restrict__ lanes) {
+template <class T>
+__global__ __launch_bounds__(256) void hawk_keyed_lanes(const T* __restrict__ u, long long group, long long lv,
+                                                        long long total, T* __restrict__ lanes) {
     for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < total;
          i += static_cast<long long>(gridDim.x) * 256) {
         const long long k = i / lv, l = i - k * lv;
-        const double* row = u + k * group;
-        double part = 0.0;
+        const T* row = u + k * group;
+        T part = T(0);
         for (long long r = l; r < group; r += kVirtualLanes) part = part + __builtin_nontemporal_load(row + r);
         lanes[i] = part;
     }
@@ -557,11 +560,12 @@ __host__ __device__ __forceinline__ int pow2_at_least(long long x) {
 // w = 128 and 64 go through LDS, w = 32 .. 1 through the first wave's
 // shuffles (lane i reads lane i + w; only lanes below w carry on).  The
 // same pairs, in the same order, as the tree over LDS.  Thread 0 returns s[0].
-__device__ __forceinline__ double block_tree(double (&v)[4], int P, double* sh) {
+template <class T>
+__device__ __forceinline__ T block_tree(T (&v)[4], int P, T* sh) {
     const int t = threadIdx.x;
     if (P > 512) { v[0] = v[0] + v[2]; v[1] = v[1] + v[3]; }
     if (P > 256) v[0] = v[0] + v[1];
-    double x = v[0];
+    T x = v[0];
     if (P > 64) {
         sh[t] = x;
         __syncthreads();
@@ -572,7 +576,7 @@ __device__ __forceinline__ double block_tree(double (&v)[4], int P, double* sh) 
     if (t < 64) {
 #pragma unroll
         for (int w = 32; w >= 1; w >>= 1) {
-            const double y = __shfl_down(x, w, 64);
+            const T y = __shfl_down(x, w, 64);
             if (P > w) x = x + y;
         }
     }
@@ -581,13 +585,14 @@ __device__ __forceinline__ double block_tree(double (&v)[4], int P, double* sh) 
 }
 
 // The 64 group values' tree over Q = 2^ceil(log2 used) of them, in the first wave.
-__device__ __forceinline__ double group_tree(const double* gp, int used) {
+template <class T>
+__device__ __forceinline__ T group_tree(const T* gp, int used) {
     const int t = threadIdx.x;
     const int q = pow2_at_least(used);
-    double x = t < used ? gp[t] : 0.0;
+    T x = t < used ? gp[t] : T(0);
 #pragma unroll
     for (int w = 32; w >= 1; w >>= 1) {
-        const double y = __shfl_down(x, w, 64);
+        const T y = __shfl_down(x, w, 64);
         if (q > w) x = x + y;
     }
     return x;
@@ -595,66 +600,68 @@ __device__ __forceinline__ double group_tree(const double* gp, int used) {
 
 // One workgroup per key whose lanes are already folded into `lanes` (groups
 // of more than 65536 rows): the used groups' trees, then the group values'.
-__global__ __launch_bounds__(256) void hawk_keyed_fold(const double* __restrict__ lanes, long long lv,
-                                                       double* __restrict__ out) {
-    __shared__ double sh[256];
-    __shared__ double gp[kGroups];
+template <class T>
+__global__ __launch_bounds__(256) void hawk_keyed_fold(const T* __restrict__ lanes, long long lv,
+                                                       T* __restrict__ out) {
+    __shared__ T sh[256];
+    __shared__ T gp[kGroups];
     const long long k = blockIdx.x;
     const int t = threadIdx.x;
     const int used = static_cast<int>((lv + kFoldLanes - 1) / kFoldLanes);     // <= 64
     const int width = lv >= kFoldLanes ? kFoldLanes : pow2_at_least(lv);
-    const double* mine = lanes + k * lv;
+    const T* mine = lanes + k * lv;
     for (int g = 0; g < used; ++g) {
-        double v[4];
+        T v[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const long long at = static_cast<long long>(g) * kFoldLanes + t + 256 * j;
-            v[j] = at < lv ? mine[at] : 0.0;
+            v[j] = at < lv ? mine[at] : T(0);
         }
-        const double s = block_tree(v, width, sh);
+        const T s = block_tree<T>(v, width, sh);
         if (t == 0) gp[g] = s;
     }
     __syncthreads();
-    const double total = t < 64 ? group_tree(gp, used) : 0.0;
+    const T total = t < 64 ? group_tree<T>(gp, used) : T(0);
     if (t == 0) out[k] = total;
 }
 
 // One workgroup per key of at most 65536 rows: virtual lane l holds row l
 // alone (0.0 + u[l], the add from +0.0), so the trees read u directly.
-__global__ __launch_bounds__(256) void hawk_keyed_rows(const double* __restrict__ u, long long group,
-                                                       double* __restrict__ out) {
-    __shared__ double sh[256];
-    __shared__ double gp[kGroups];
+template <class T>
+__global__ __launch_bounds__(256) void hawk_keyed_rows(const T* __restrict__ u, long long group,
+                                                       T* __restrict__ out) {
+    __shared__ T sh[256];
+    __shared__ T gp[kGroups];
     const long long k = blockIdx.x;
     const int t = threadIdx.x;
     const int used = static_cast<int>((group + kFoldLanes - 1) / kFoldLanes);
     const int width = group >= kFoldLanes ? kFoldLanes : pow2_at_least(group);
-    const double* mine = u + k * group;
-    double nxt[4];                        // the next group's rows, loaded during this group's tree
+    const T* mine = u + k * group;
+    T nxt[4];                        // the next group's rows, loaded during this group's tree
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const long long at = t + 256 * j;
-        nxt[j] = at < group ? __builtin_nontemporal_load(mine + at) : 0.0;
+        nxt[j] = at < group ? __builtin_nontemporal_load(mine + at) : T(0);
     }
     for (int g = 0; g < used; ++g) {
-        double v[4];
+        T v[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const long long at = static_cast<long long>(g) * kFoldLanes + t + 256 * j;
-            v[j] = at < group ? 0.0 + nxt[j] : 0.0;
+            v[j] = at < group ? T(0) + nxt[j] : T(0);
         }
         if (g + 1 < used) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const long long at = static_cast<long long>(g + 1) * kFoldLanes + t + 256 * j;
-                nxt[j] = at < group ? __builtin_nontemporal_load(mine + at) : 0.0;
+                nxt[j] = at < group ? __builtin_nontemporal_load(mine + at) : T(0);
             }
         }
-        const double s = block_tree(v, width, sh);
+        const T s = block_tree<T>(v, width, sh);
         if (t == 0) gp[g] = s;
     }
     __syncthreads();
-    const double total = t < 64 ? group_tree(gp, used) : 0.0;
+    const T total = t < 64 ? group_tree<T>(gp, used) : T(0);
     if (t == 0) out[k] = total;
 }
 
@@ -664,17 +671,18 @@ __global__ __launch_bounds__(256) void hawk_keyed_rows(const double* __restrict_
 // (lane j adds lane j + w for w = P/2 .. 1; only lanes below w carry on): the
 // pairs of the tree over P values.  The group tree has one value, which it
 // returns unchanged.
-__global__ __launch_bounds__(256) void hawk_keyed_small(const double* __restrict__ u, long long group, int P,
-                                                        long long keys, double* __restrict__ out) {
+template <class T>
+__global__ __launch_bounds__(256) void hawk_keyed_small(const T* __restrict__ u, long long group, int P,
+                                                        long long keys, T* __restrict__ out) {
     const int lane = threadIdx.x & 63;
     const long long per_wave = 64 / P;
     const long long k = (static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * per_wave + lane / P;
     const int j = lane & (P - 1);
-    double x = 0.0;
-    if (k < keys && j < group) x = 0.0 + __builtin_nontemporal_load(u + k * group + j);
+    T x = T(0);
+    if (k < keys && j < group) x = T(0) + __builtin_nontemporal_load(u + k * group + j);
 #pragma unroll
     for (int w = 32; w >= 1; w >>= 1) {
-        const double y = __shfl_down(x, w, 64);
+        const T y = __shfl_down(x, w, 64);
         if (P > w) x = x + y;
     }
     if (j == 0 && k < keys) out[k] = x;
@@ -725,15 +733,16 @@ __device__ __forceinline__ unsigned wave_inclusive_scan(unsigned x) {
     return x;
 }
 
+template <class T>
 struct WalkShared {
-    double vals[kTile];                               // 32 KiB: the tile's values, lane order
+    T vals[kTile];                               // 32 KiB: the tile's values, lane order
     unsigned ent[2][kTile];                           // 32 KiB: (key << 12) | position | invalid
     unsigned hist[kDigits][kHistRow];                 // 17 KiB: [digit][wave] counts, then offsets
     union {
         unsigned long long peer[kWalkWaves][kDigits]; // 32 KiB: per-wave lane masks of one digit (sort)
-        double sv[kTile];                             //         the tile's values in sorted order (fold)
+        T sv[kTile];                             //         the tile's values in sorted order (fold)
     };
-    double acc[kAccKeys];                             // 32 KiB: accumulators of keys < kAccKeys
+    T acc[kAccKeys];                             // 32 KiB: accumulators of keys < kAccKeys
     unsigned long long starts[kTile / 64];            // run heads of the sorted tile
     unsigned wsum[kWalkWaves];
 };
@@ -747,7 +756,8 @@ struct WalkShared {
 // scan of hist in (digit, wave) order then places every wave's group after
 // the earlier waves' groups of the same digit, so each pass keeps input order
 // within a digit.
-__device__ int walk_sort(WalkShared& sh, int key_bits) {
+template <class T>
+__device__ int walk_sort(WalkShared<T>& sh, int key_bits) {
     const int t = threadIdx.x;
     const int wave = t >> 6;
     const int lane = t & 63;
@@ -810,8 +820,9 @@ __device__ int walk_sort(WalkShared& sh, int key_bits) {
 // Lane base + wave*256 + j*64 + lane goes to thread slot j: every load
 // instruction of a wave reads 64 consecutive lanes.  Lanes past `hi` read as
 // the skip key -1.
-__device__ __forceinline__ void walk_load(const int* __restrict__ key, const double* __restrict__ v, long long base,
-                                          long long hi, int (&kk)[kWalkItems], double (&vv)[kWalkItems]) {
+template <class T>
+__device__ __forceinline__ void walk_load(const int* __restrict__ key, const T* __restrict__ v, long long base,
+                                          long long hi, int (&kk)[kWalkItems], T (&vv)[kWalkItems]) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
 #pragma unroll
@@ -819,12 +830,13 @@ __device__ __forceinline__ void walk_load(const int* __restrict__ key, const dou
         const long long i = base + wave * (kWalkItems * 64) + j * 64 + lane;
         const bool in = i < hi;
         kk[j] = in ? __builtin_nontemporal_load(key + i) : -1;
-        vv[j] = in ? __builtin_nontemporal_load(v + i) : 0.0;
+        vv[j] = in ? __builtin_nontemporal_load(v + i) : T(0);
     }
 }
 
 // The first run head after position i of the sorted tile (kTile if none).
-__device__ __forceinline__ int next_head(const WalkShared& sh, int i) {
+template <class T>
+__device__ __forceinline__ int next_head(const WalkShared<T>& sh, int i) {
     int wi = i >> 6;
     const int bit = i & 63;
     unsigned long long m = bit == 63 ? 0ull : (sh.starts[wi] & (~0ull << (bit + 1)));
@@ -834,15 +846,16 @@ __device__ __forceinline__ int next_head(const WalkShared& sh, int i) {
 
 // a + x[s] + x[s+1] + ... + x[e-1], one addition at a time in that order; the
 // next eight values are in flight while the current eight are added.
-__device__ __forceinline__ double fold_run(const double* x, int s, int e, double a) {
+template <class T>
+__device__ __forceinline__ T fold_run(const T* x, int s, int e, T a) {
     int m = s;
     if (e - m >= 2 * kFoldUnroll) {
-        double cur[kFoldUnroll];
+        T cur[kFoldUnroll];
 #pragma unroll
         for (int q = 0; q < kFoldUnroll; ++q) cur[q] = x[m + q];
         m += kFoldUnroll;
         for (; m + kFoldUnroll <= e; m += kFoldUnroll) {
-            double nxt[kFoldUnroll];
+            T nxt[kFoldUnroll];
 #pragma unroll
             for (int q = 0; q < kFoldUnroll; ++q) nxt[q] = x[m + q];
 #pragma unroll
@@ -860,19 +873,22 @@ __device__ __forceinline__ double fold_run(const double* x, int s, int e, double
 // Accumulators outside LDS are read and written at agent scope, so a value
 // one thread stores in a tile is what another thread of the workgroup loads
 // after the tile's closing barrier.
-__device__ __forceinline__ double acc_load(const double* p) {
+template <class T>
+__device__ __forceinline__ T acc_load(const T* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void acc_store(double* p, double x) {
+template <class T>
+__device__ __forceinline__ void acc_store(T* p, T x) {
     __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One workgroup per chunk b: lanes [b*span, min((b+1)*span, n)); parts
 // arrives zero-filled.
+template <class T>
 __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
-        const int* __restrict__ key, const double* __restrict__ v, long long n, long long cells, long long span,
-        int key_bits, double* __restrict__ parts, int* __restrict__ status) {
-    __shared__ WalkShared sh;
+        const int* __restrict__ key, const T* __restrict__ v, long long n, long long cells, long long span,
+        int key_bits, T* __restrict__ parts, int* __restrict__ status) {
+    __shared__ WalkShared<T> sh;
     const int t = threadIdx.x;
     const int wave = t >> 6;
     const int lane = t & 63;
@@ -882,17 +898,17 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
     const int acc_n = cells < kAccKeys ? static_cast<int>(cells) : kAccKeys;
     const unsigned kmask = (1u << key_bits) - 1u;
     const unsigned sentinel = kmask;          // the key field of an invalid lane
-    double* row = parts + static_cast<long long>(b) * cells;
+    T* row = parts + static_cast<long long>(b) * cells;
 
-    for (int k = t; k < acc_n; k += kWalkThreads) sh.acc[k] = 0.0;
+    for (int k = t; k < acc_n; k += kWalkThreads) sh.acc[k] = T(0);
     bool bad = false;
     int nk[kWalkItems];
-    double nv[kWalkItems];
+    T nv[kWalkItems];
     if (lo < hi) walk_load(key, v, lo, hi, nk, nv);
     __syncthreads();
     for (long long base = lo; base < hi; base += kTile) {
         int kk[kWalkItems];
-        double vv[kWalkItems];
+        T vv[kWalkItems];
 #pragma unroll
         for (int j = 0; j < kWalkItems; ++j) { kk[j] = nk[j]; vv[j] = nv[j]; }
         if (base + kTile < hi) walk_load(key, v, base + kTile, hi, nk, nv);
@@ -917,7 +933,7 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
         for (int j = 0; j < kWalkItems; ++j) {
             const int i = j * kWalkThreads + t;
             const unsigned e = sorted[i];
-            sh.sv[i] = (e & kInvalid) ? 0.0 : sh.vals[e & kPosMask];
+            sh.sv[i] = (e & kInvalid) ? T(0) : sh.vals[e & kPosMask];
             const unsigned k = (e >> kPosBits) & kmask;
             head[j] = i == 0 || k != ((sorted[i - (i > 0)] >> kPosBits) & kmask);
             const unsigned long long m = __ballot(head[j]);
@@ -940,18 +956,18 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
             const unsigned k = rk[j];
             load[j] = k >= static_cast<unsigned>(acc_n);
         }
-        double ra[kWalkItems];
+        T ra[kWalkItems];
 #pragma unroll
         for (int j = 0; j < kWalkItems; ++j) {
             const unsigned k = rk[j] < static_cast<unsigned>(acc_n) ? rk[j] : 0u;
             ra[j] = load[j] ? acc_load(row + rk[j])
-                            : (re[j] != 0 && rk[j] < static_cast<unsigned>(acc_n) ? sh.acc[k] : 0.0);
+                            : (re[j] != 0 && rk[j] < static_cast<unsigned>(acc_n) ? sh.acc[k] : T(0));
         }
 #pragma unroll 1
         for (int j = 0; j < kWalkItems; ++j) {
             if (re[j] == 0) continue;
             const unsigned k = rk[j];
-            double a = ra[j];
+            T a = ra[j];
             bool any = true;
             if (k == sentinel) {
                 // The one run that can hold invalid lanes: skip them.
@@ -976,14 +992,15 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_scatter_walk(
 
 // More keys than the sort's key field holds: one thread per chunk walks its
 // lanes in order onto the zero-filled parts[b] (the reference's serial walk).
-__global__ __launch_bounds__(64) void hawk_scatter_serial(const int* __restrict__ key, const double* __restrict__ v,
+template <class T>
+__global__ __launch_bounds__(64) void hawk_scatter_serial(const int* __restrict__ key, const T* __restrict__ v,
                                                           long long n, long long cells, long long span,
-                                                          double* __restrict__ parts, int* __restrict__ status) {
+                                                          T* __restrict__ parts, int* __restrict__ status) {
     if (threadIdx.x != 0) return;
     const int b = blockIdx.x;
     const long long lo = static_cast<long long>(b) * span;
     const long long hi = lo + span < n ? lo + span : n;
-    double* row = parts + static_cast<long long>(b) * cells;
+    T* row = parts + static_cast<long long>(b) * cells;
     bool bad = false;
     for (long long i = lo; i < hi; ++i) {
         const int k = key[i];
@@ -994,36 +1011,38 @@ __global__ __launch_bounds__(64) void hawk_scatter_serial(const int* __restrict_
     if (bad) status[1 + b] = 1;
 }
 
-__global__ __launch_bounds__(256) void hawk_fill_zero(double* __restrict__ p, long long count) {
+template <class T>
+__global__ __launch_bounds__(256) void hawk_fill_zero(T* __restrict__ p, long long count) {
     for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < count;
          i += static_cast<long long>(gridDim.x) * 256)
-        p[i] = 0.0;
+        p[i] = T(0);
 }
 
 // Cell c adds its chunk partials in chunk order from +0.0, then onto the
 // target: target[c] += sum (reference hawk/emit/team.py:437-460).  Two blocks
 // of kAhead chunks are in flight while a third is added.
-__global__ __launch_bounds__(256) void hawk_scatter_cells(const double* __restrict__ parts, long long cells,
-                                                          int chunks, double* __restrict__ target) {
+template <class T>
+__global__ __launch_bounds__(256) void hawk_scatter_cells(const T* __restrict__ parts, long long cells,
+                                                          int chunks, T* __restrict__ target) {
     const long long c = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     if (c >= cells) return;
     constexpr int kAhead = 8;
-    auto fetch = [&](int b, double (&x)[kAhead]) {
+    auto fetch = [&](int b, T (&x)[kAhead]) {
 #pragma unroll
         for (int q = 0; q < kAhead; ++q) {
             // past the last chunk a partial reads as +0.0, which adds nothing
             // to a sum that is never -0.0
             const int bq = b + q < chunks ? b + q : chunks - 1;
-            const double p = parts[static_cast<long long>(bq) * cells + c];
-            x[q] = b + q < chunks ? p : 0.0;
+            const T p = parts[static_cast<long long>(bq) * cells + c];
+            x[q] = b + q < chunks ? p : T(0);
         }
     };
-    double x0[kAhead], x1[kAhead];
+    T x0[kAhead], x1[kAhead];
     fetch(0, x0);
     fetch(kAhead, x1);
-    double s = 0.0;
+    T s = T(0);
     for (int b = 0; b < chunks; b += kAhead) {
-        double x2[kAhead];
+        T x2[kAhead];
         fetch(b + 2 * kAhead, x2);
 #pragma unroll
         for (int q = 0; q < kAhead; ++q) s = s + x0[q];
@@ -1079,9 +1098,10 @@ static_assert(kSplitNone >= kSplitStride, "the no-bucket code is outside the cou
 
 constexpr int kSplitPad = 64;                    // entries read (and ignored) past a run's end
 
+template <class T>
 struct SplitShared {
-    double acc[kSplitHot];                          // 96 KiB: the window's accumulators
-    double val[kTile + kSplitPad];                  // 32 KiB: the tile's values, bucket order
+    T acc[kSplitHot];                          // 96 KiB: the window's accumulators
+    T val[kTile + kSplitPad];                  // 32 KiB: the tile's values, bucket order
     unsigned short key[kTile + kSplitPad];          //  8 KiB: their window-local keys
     union {                                         // 20 KiB, one phase at a time:
         unsigned long long win[kWalkWaves][kWalkItems][kSplitStride];  // split: a match table per window
@@ -1109,8 +1129,9 @@ __device__ __forceinline__ int split_bucket(unsigned kl) {
 // count of its bucket in the wave's earlier windows plus the lanes below it
 // in its own.  Every wave then forms its own positions from all waves'
 // counts.  Starts and ends with every thread of the workgroup.
-__device__ void split_tile(SplitShared& sh, const unsigned (&kl)[kWalkItems], const int (&d)[kWalkItems],
-                           const double (&vv)[kWalkItems], int nb) {
+template <class T>
+__device__ void split_tile(SplitShared<T>& sh, const unsigned (&kl)[kWalkItems], const int (&d)[kWalkItems],
+                           const T (&vv)[kWalkItems], int nb) {
     const int t = threadIdx.x;
     const int wave = t >> 6;
     const int lane = t & 63;
@@ -1179,12 +1200,15 @@ __device__ void split_tile(SplitShared& sh, const unsigned (&kl)[kWalkItems], co
     __syncthreads();
 }
 
-// Lane `lane`'s double, to every lane (two readlanes: the lane select is uniform).
+// Lane `lane`'s T, to every lane (two readlanes: the lane select is uniform).
 __device__ __forceinline__ double lane_value(double x, int lane) {
     const long long bits = __double_as_longlong(x);
     const int lo = __builtin_amdgcn_readlane(static_cast<int>(bits), lane);
     const int hi = __builtin_amdgcn_readlane(static_cast<int>(bits >> 32), lane);
     return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned>(lo));
+}
+__device__ __forceinline__ float lane_value(float x, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
 
 // a + x[s] + x[s+1] + ... + x[e-1] in that order, by the whole wave: each
@@ -1194,13 +1218,14 @@ __device__ __forceinline__ double lane_value(double x, int lane) {
 // to 25 for one fed by one lane's own LDS reads while the workgroup's other
 // waves use the LDS.  s and e are the same in every lane; x is readable up to
 // 63 entries past e.
-__device__ __forceinline__ double fold_lanes(const double* x, int s, int e, double a) {
+template <class T>
+__device__ __forceinline__ T fold_lanes(const T* x, int s, int e, T a) {
     const int lane = threadIdx.x & 63;
     s = __builtin_amdgcn_readfirstlane(s);
     e = __builtin_amdgcn_readfirstlane(e);
-    double cur = x[s + lane];
+    T cur = x[s + lane];
     for (int m = s; m < e; m += 64) {
-        const double nxt = m + 64 < e ? x[m + 64 + lane] : 0.0;
+        const T nxt = m + 64 < e ? x[m + 64 + lane] : T(0);
         if (e - m >= 64) {
 #pragma unroll
             for (int q = 0; q < 64; ++q) a = a + lane_value(cur, q);
@@ -1212,11 +1237,13 @@ __device__ __forceinline__ double fold_lanes(const double* x, int s, int e, doub
     return a;
 }
 
-__device__ void split_fold_class(SplitShared& sh, int c);
+template <class T>
+__device__ void split_fold_class(SplitShared<T>& sh, int c);
 
 // Wave c folds bucket c (window key c) and, as a rule, class c of the split
 // tile onto the LDS accumulators.
-__device__ void split_fold(SplitShared& sh, int window) {
+template <class T>
+__device__ void split_fold(SplitShared<T>& sh, int window) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     // the whole wave folds the single key's run (fold_lanes)
@@ -1224,7 +1251,7 @@ __device__ void split_fold(SplitShared& sh, int window) {
         const int s = static_cast<int>(sh.bstart[wave]);
         const int e = static_cast<int>(sh.bstart[wave + 1]);
         if (s < e) {
-            const double a = fold_lanes(sh.val, s, e, sh.acc[wave]);
+            const T a = fold_lanes(sh.val, s, e, sh.acc[wave]);
             if (lane == 0) sh.acc[wave] = a;
         }
     }
@@ -1248,7 +1275,8 @@ __device__ void split_fold(SplitShared& sh, int window) {
 }
 
 // The caller's wave folds class c of the split tile, 64 entries a window.
-__device__ void split_fold_class(SplitShared& sh, int c) {
+template <class T>
+__device__ void split_fold_class(SplitShared<T>& sh, int c) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const unsigned long long me = 1ull << lane;
@@ -1259,17 +1287,17 @@ __device__ void split_fold_class(SplitShared& sh, int c) {
     // is folded.  A lane past the end reads (padding or another bucket's
     // entry) and ignores it; its match bit goes to a slot of its own.
     unsigned k = sh.key[s + lane];
-    double x = sh.val[s + lane];
+    T x = sh.val[s + lane];
     for (int base = s; base < e; base += 64) {
         const bool valid = base + lane < e;
         const unsigned nk = sh.key[base + 64 + lane];
-        const double nx = sh.val[base + 64 + lane];
+        const T nx = sh.val[base + 64 + lane];
         const unsigned kv = valid ? k : 0u;
         const unsigned h = valid ? (kv >> 4) & 63u : static_cast<unsigned>(lane);
         atomicOr(&sh.f.peer[wave][h], valid ? me : 0ull);
         __builtin_amdgcn_wave_barrier();
         unsigned long long pm = sh.f.peer[wave][h];
-        double a = sh.acc[kv];
+        T a = sh.acc[kv];
         __builtin_amdgcn_wave_barrier();
         sh.f.peer[wave][h] = 0ull;
         // the slot matched key bits 4..9 (bits 0..3 are the class); bits
@@ -1292,7 +1320,7 @@ __device__ void split_fold_class(SplitShared& sh, int c) {
                     q[u] = m ? __builtin_ctzll(m) : -1;
                     m &= m - 1ull;
                 }
-                double y[4];
+                T y[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) y[u] = sh.val[base + (q[u] < 0 ? 0 : q[u])];
 #pragma unroll
@@ -1309,26 +1337,29 @@ __device__ void split_fold_class(SplitShared& sh, int c) {
 
 // The window's partials of chunk b, every key [klo, klo+window): a key no
 // lane named holds +0.0, the walk's starting value.
-__device__ void split_store(SplitShared& sh, long long b, long long cells, long long klo, int window,
-                            double* __restrict__ parts) {
+template <class T>
+__device__ void split_store(SplitShared<T>& sh, long long b, long long cells, long long klo, int window,
+                            T* __restrict__ parts) {
     __syncthreads();
-    double* row = parts + b * cells + klo;
+    T* row = parts + b * cells + klo;
     for (int k = threadIdx.x; k < window; k += kWalkThreads) row[k] = sh.acc[k];
 }
 
-__device__ void split_clear(SplitShared& sh, int window) {
-    for (int k = threadIdx.x; k < window; k += kWalkThreads) sh.acc[k] = 0.0;
+template <class T>
+__device__ void split_clear(SplitShared<T>& sh, int window) {
+    for (int k = threadIdx.x; k < window; k += kWalkThreads) sh.acc[k] = T(0);
     __syncthreads();
 }
 
 // Chunk b = blockIdx.x: lanes [b*span, min((b+1)*span, n)), keys below
 // kSplitHot folded here, the others copied to the chunk's bin (slot = tile,
 // offsets of the `ranges` tail ranges in bin_off[b][tile][0..ranges]).
+template <class T>
 __global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
-        const int* __restrict__ key, const double* __restrict__ v, long long n, long long cells, long long span,
-        int tiles, int ranges, unsigned short* __restrict__ bin_key, double* __restrict__ bin_val,
-        unsigned* __restrict__ bin_off, double* __restrict__ parts, int* __restrict__ status) {
-    __shared__ SplitShared sh;
+        const int* __restrict__ key, const T* __restrict__ v, long long n, long long cells, long long span,
+        int tiles, int ranges, unsigned short* __restrict__ bin_key, T* __restrict__ bin_val,
+        unsigned* __restrict__ bin_off, T* __restrict__ parts, int* __restrict__ status) {
+    __shared__ SplitShared<T> sh;
     const int t = threadIdx.x;
     const long long b = blockIdx.x;
     const long long lo = b * span;
@@ -1338,13 +1369,13 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
     split_clear(sh, window);
     bool bad = false;
     int nk[kWalkItems];
-    double nv[kWalkItems];
+    T nv[kWalkItems];
     if (lo < hi) walk_load(key, v, lo, hi, nk, nv);
     int tile = 0;
     for (long long base = lo; base < hi; base += kTile, ++tile) {
         unsigned kl[kWalkItems];
         int d[kWalkItems];
-        double vv[kWalkItems];
+        T vv[kWalkItems];
 #pragma unroll
         for (int j = 0; j < kWalkItems; ++j) {
             const int k = nk[j];
@@ -1390,10 +1421,11 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
 // (chunk b, tail range r) = (blockIdx.x / ranges, blockIdx.x % ranges): keys
 // [kSplitHot*(r+1), +kSplitHot) of chunk b, read from the bin's slots in tile
 // order.
+template <class T>
 __global__ __launch_bounds__(kWalkThreads) void hawk_split_tail(
         long long cells, int tiles, int ranges, const unsigned short* __restrict__ bin_key,
-        const double* __restrict__ bin_val, const unsigned* __restrict__ bin_off, double* __restrict__ parts) {
-    __shared__ SplitShared sh;
+        const T* __restrict__ bin_val, const unsigned* __restrict__ bin_off, T* __restrict__ parts) {
+    __shared__ SplitShared<T> sh;
     const int t = threadIdx.x;
     const int wave = t >> 6;
     const int lane = t & 63;
@@ -1440,12 +1472,12 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_tail(
                 const unsigned c = static_cast<unsigned>(sh.grp_hi[tt] - sh.grp_lo[tt]);
                 for (unsigned i0 = 0; i0 < c; i0 += 4 * 64) {
                     unsigned short kk[4];
-                    double vv[4];
+                    T vv[4];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const unsigned i = i0 + q * 64 + lane;
                         kk[q] = i < c ? bin_key[src + i] : 0;
-                        vv[q] = i < c ? bin_val[src + i] : 0.0;
+                        vv[q] = i < c ? bin_val[src + i] : T(0);
                     }
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
@@ -1460,13 +1492,13 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_tail(
             __syncthreads();
             unsigned kl[kWalkItems];
             int d[kWalkItems];
-            double vv[kWalkItems];
+            T vv[kWalkItems];
 #pragma unroll
             for (int j = 0; j < kWalkItems; ++j) {
                 const int i = wave * (kWalkItems * 64) + j * 64 + lane;
                 const bool on = i < total;
                 kl[j] = on ? sh.key[i] : 0u;
-                vv[j] = on ? sh.val[i] : 0.0;
+                vv[j] = on ? sh.val[i] : T(0);
                 d[j] = on ? split_bucket(kl[j]) : kSplitNone;
             }
             __syncthreads();
@@ -1675,6 +1707,66 @@ int scratch_of(hipStream_t stream, void** out) {
     return HK_OK;
 }
 
+// The ordered sum in T (hk_ordered_sum_f64 / _f32): the lanes, then the fold.
+// A float sum keeps the double layout's offsets, its data in the front of
+// each region.
+template <class T>
+int ordered_sum(const T* u, int64_t n, T* out, void* scratch, void* stream, const char* name) {
+    if (n < 0) return hawk_internal::set_error(HK_EVALUE, std::string(name) + ": n must be >= 0");
+    if ((n > 0 && !u) || !out || !scratch)
+        return hawk_internal::set_error(HK_EVALUE, std::string(name) + ": u, out and scratch are required");
+    auto* base = static_cast<unsigned char*>(scratch);
+    auto* lanes = reinterpret_cast<T*>(base);
+    auto* gp = reinterpret_cast<T*>(base + kLanesBytes);
+    auto* ticket = reinterpret_cast<unsigned*>(base + kLanesBytes + kGpBytes);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(hawk_sum_lanes<T>, dim3(kVirtualLanes / kLaneBlock), dim3(kLaneBlock), 0, s, u,
+                       static_cast<long long>(n), lanes, ticket);
+    int rc = launch_error("hawk_sum_lanes launch");
+    if (rc != HK_OK) return rc;
+    hipLaunchKernelGGL(hawk_sum_fold<T>, dim3(kGroups), dim3(256), 0, s, lanes, gp, ticket, out);
+    return launch_error("hawk_sum_fold launch");
+}
+
+// The keyed ordered sum in T (hk_keyed_ordered_sum_f64 / _f32).
+template <class T>
+int keyed_ordered_sum(const T* u, int64_t n, int64_t group, T* out, void* scratch, void* stream, const char* name) {
+    const std::string who(name);
+    if (n < 0 || group <= 0) return hawk_internal::set_error(HK_EVALUE, who + ": n must be >= 0 and group >= 1");
+    if (n % group != 0)
+        return hawk_internal::set_error(HK_EVALUE, who + ": n (" + std::to_string(n) +
+                                                       ") is not a whole number of groups of " + std::to_string(group));
+    if (n == 0) return HK_OK;
+    if (!u || !out || !scratch) return hawk_internal::set_error(HK_EVALUE, who + ": u, out and scratch are required");
+    if (n == group) return ordered_sum<T>(u, n, out, scratch, stream, name);    // one key: the ordered sum
+    const long long keys = n / group;
+    if (keys > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, who + ": too many keys");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (group <= 64) {
+        const int P = pow2_at_least(group);
+        const long long waves = (keys + 64 / P - 1) / (64 / P);
+        hipLaunchKernelGGL(hawk_keyed_small<T>, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, s, u,
+                           static_cast<long long>(group), P, keys, out);
+        return launch_error("hawk_keyed_small launch");
+    }
+    if (group <= kVirtualLanes) {
+        hipLaunchKernelGGL(hawk_keyed_rows<T>, dim3(static_cast<unsigned>(keys)), dim3(256), 0, s, u,
+                           static_cast<long long>(group), out);
+        return launch_error("hawk_keyed_rows launch");
+    }
+    const long long lv = group < kVirtualLanes ? group : kVirtualLanes;
+    const long long total = keys * lv;
+    auto* lanes = static_cast<T*>(scratch);
+    long long blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(hawk_keyed_lanes<T>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, u,
+                       static_cast<long long>(group), lv, total, lanes);
+    int rc = launch_error("hawk_keyed_lanes launch");
+    if (rc != HK_OK) return rc;
+    hipLaunchKernelGGL(hawk_keyed_fold<T>, dim3(static_cast<unsigned>(keys)), dim3(256), 0, s, lanes, lv, out);
+    return launch_error("hawk_keyed_fold launch");
+}
+
 // The rows' finish in T: the leaves, then the levels into *out.
 template <class T>
 int rows_finish(const T* hi, const T* comp, int64_t rows, T* out, void* scratch, void* stream, const char* name) {
@@ -1693,6 +1785,72 @@ int rows_finish(const T* hi, const T* comp, int64_t rows, T* out, void* scratch,
     return launch_error("hawk_rows_levels launch");
 }
 
+// The ordered scatter in T (hk_ordered_scatter_f64 / _f32).
+template <class T>
+int ordered_scatter(const int32_t* key, const T* v, int64_t n, T* target, int64_t cells, void* scratch,
+                    int32_t* status, void* stream, const char* name) {
+    const std::string who(name);
+    if (n < 0 || cells < 0)
+        return hawk_internal::set_error(HK_EVALUE, who + ": n and cells must be >= 0");
+    if (cells == 0) return HK_OK;   // a scatter into no cells adds nothing (reference hawk/runtime.py:727)
+    if ((n > 0 && (!key || !v)) || !target || !scratch || !status)
+        return hawk_internal::set_error(HK_EVALUE,
+                                        who + ": key, v, target, scratch and status are required");
+    if (cells > 0x7fffffffLL)
+        return hawk_internal::set_error(HK_EVALUE, who + ": more than 2^31-1 cells");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int chunks = hk_scatter_chunks(n, cells);
+    const ScatterLayout L = scatter_layout(n, cells, chunks);
+    unsigned char* base = static_cast<unsigned char*>(scratch);
+    auto* parts = reinterpret_cast<T*>(base + L.parts);     // a float scatter uses the front of each region
+    hipLaunchKernelGGL(hawk_scatter_status, dim3(1), dim3(kScatterChunks + 64), 0, s, status,
+                       static_cast<long long>(cells));
+    int rc = launch_error("hawk_scatter_status launch");
+    if (rc != HK_OK) return rc;
+    if (L.split) {
+        auto* bin_off = reinterpret_cast<unsigned*>(base + L.bin_off);
+        auto* bin_key = reinterpret_cast<unsigned short*>(base + L.bin_key);
+        auto* bin_val = reinterpret_cast<T*>(base + L.bin_val);
+        hipLaunchKernelGGL(hawk_split_hot<T>, dim3(static_cast<unsigned>(chunks)), dim3(kWalkThreads), 0, s, key, v,
+                           static_cast<long long>(n), static_cast<long long>(cells), L.span, L.tiles, L.ranges,
+                           bin_key, bin_val, bin_off, parts, status);
+        rc = launch_error("hawk_split_hot launch");
+        if (rc != HK_OK) return rc;
+        if (L.ranges > 0) {
+            hipLaunchKernelGGL(hawk_split_tail<T>, dim3(static_cast<unsigned>(chunks * L.ranges)), dim3(kWalkThreads),
+                               0, s, static_cast<long long>(cells), L.tiles, L.ranges, bin_key, bin_val, bin_off,
+                               parts);
+            rc = launch_error("hawk_split_tail launch");
+            if (rc != HK_OK) return rc;
+        }
+    } else {
+        // more cells than the split walk's windows cover: parts arrives
+        // zero-filled and the sorted walk (or, past its key field, the serial
+        // walk) adds onto it
+        const long long count = static_cast<long long>(chunks) * cells;
+        const long long blocks = (count + 255) / 256 < 4096 ? (count + 255) / 256 : 4096;
+        hipLaunchKernelGGL(hawk_fill_zero<T>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, parts, count);
+        rc = launch_error("hawk_fill_zero launch");
+        if (rc != HK_OK) return rc;
+        const int key_bits = bits_for(cells - 1);
+        if (key_bits <= kMaxKeyBits) {
+            hipLaunchKernelGGL(hawk_scatter_walk<T>, dim3(static_cast<unsigned>(chunks)), dim3(kWalkThreads), 0, s,
+                               key, v, static_cast<long long>(n), static_cast<long long>(cells), L.span, key_bits,
+                               parts, status);
+            rc = launch_error("hawk_scatter_walk launch");
+        } else {
+            hipLaunchKernelGGL(hawk_scatter_serial<T>, dim3(static_cast<unsigned>(chunks)), dim3(64), 0, s, key, v,
+                               static_cast<long long>(n), static_cast<long long>(cells), L.span, parts, status);
+            rc = launch_error("hawk_scatter_serial launch");
+        }
+        if (rc != HK_OK) return rc;
+    }
+    const long long grid = (cells + 255) / 256;
+    hipLaunchKernelGGL(hawk_scatter_cells<T>, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, parts,
+                       static_cast<long long>(cells), chunks, target);
+    return launch_error("hawk_scatter_cells launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -1705,23 +1863,17 @@ int hk_ordered_fold_f64(const double* lanes, double* out, void* scratch, void* s
     auto* base = static_cast<unsigned char*>(scratch);
     auto* gp = reinterpret_cast<double*>(base + kLanesBytes);
     auto* ticket = reinterpret_cast<unsigned*>(base + kLanesBytes + kGpBytes);
-    hipLaunchKernelGGL(hawk_sum_fold, dim3(kGroups), dim3(256), 0, static_cast<hipStream_t>(stream),
+    hipLaunchKernelGGL(hawk_sum_fold<double>, dim3(kGroups), dim3(256), 0, static_cast<hipStream_t>(stream),
                        lanes, gp, ticket, out);
     return launch_error("hawk_sum_fold launch");
 }
 
 int hk_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch, void* stream) {
-    if (n < 0) return hawk_internal::set_error(HK_EVALUE, "hk_ordered_sum_f64: n must be >= 0");
-    if ((n > 0 && !u) || !out || !scratch)
-        return hawk_internal::set_error(HK_EVALUE, "hk_ordered_sum_f64: u, out and scratch are required");
-    auto* base = static_cast<unsigned char*>(scratch);
-    auto* lanes = reinterpret_cast<double*>(base);
-    auto* ticket = reinterpret_cast<unsigned*>(base + kLanesBytes + kGpBytes);
-    hipLaunchKernelGGL(hawk_sum_lanes, dim3(kVirtualLanes / kLaneBlock), dim3(kLaneBlock), 0,
-                       static_cast<hipStream_t>(stream), u, static_cast<long long>(n), lanes, ticket);
-    int rc = launch_error("hawk_sum_lanes launch");
-    if (rc != HK_OK) return rc;
-    return hk_ordered_fold_f64(lanes, out, scratch, stream);
+    return ordered_sum<double>(u, n, out, scratch, stream, "hk_ordered_sum_f64");
+}
+
+int hk_ordered_sum_f32(const float* u, int64_t n, float* out, void* scratch, void* stream) {
+    return ordered_sum<float>(u, n, out, scratch, stream, "hk_ordered_sum_f32");
 }
 
 size_t hk_ordered_sum_noalloc_scratch_bytes(void) { return kSumScratch; }
@@ -1745,41 +1897,11 @@ size_t hk_keyed_ordered_sum_scratch_bytes(int64_t n, int64_t group) {
 }
 
 int hk_keyed_ordered_sum_f64(const double* u, int64_t n, int64_t group, double* out, void* scratch, void* stream) {
-    if (n < 0 || group <= 0)
-        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_ordered_sum_f64: n must be >= 0 and group >= 1");
-    if (n % group != 0)
-        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_ordered_sum_f64: n (" + std::to_string(n) +
-                                                       ") is not a whole number of groups of " + std::to_string(group));
-    if (n == 0) return HK_OK;
-    if (!u || !out || !scratch)
-        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_ordered_sum_f64: u, out and scratch are required");
-    if (n == group) return hk_ordered_sum_f64(u, n, out, scratch, stream);    // one key: the ordered sum
-    const long long keys = n / group;
-    if (keys > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_ordered_sum_f64: too many keys");
-    if (group <= 64) {
-        const int P = pow2_at_least(group);
-        const long long waves = (keys + 64 / P - 1) / (64 / P);
-        hipLaunchKernelGGL(hawk_keyed_small, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0,
-                           static_cast<hipStream_t>(stream), u, static_cast<long long>(group), P, keys, out);
-        return launch_error("hawk_keyed_small launch");
-    }
-    if (group <= kVirtualLanes) {
-        hipLaunchKernelGGL(hawk_keyed_rows, dim3(static_cast<unsigned>(keys)), dim3(256), 0,
-                           static_cast<hipStream_t>(stream), u, static_cast<long long>(group), out);
-        return launch_error("hawk_keyed_rows launch");
-    }
-    const long long lv = group < kVirtualLanes ? group : kVirtualLanes;
-    const long long total = keys * lv;
-    auto* lanes = static_cast<double*>(scratch);
-    long long blocks = (total + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(hawk_keyed_lanes, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), u, static_cast<long long>(group), lv, total, lanes);
-    int rc = launch_error("hawk_keyed_lanes launch");
-    if (rc != HK_OK) return rc;
-    hipLaunchKernelGGL(hawk_keyed_fold, dim3(static_cast<unsigned>(keys)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), lanes, lv, out);
-    return launch_error("hawk_keyed_fold launch");
+    return keyed_ordered_sum<double>(u, n, group, out, scratch, stream, "hk_keyed_ordered_sum_f64");
+}
+
+int hk_keyed_ordered_sum_f32(const float* u, int64_t n, int64_t group, float* out, void* scratch, void* stream) {
+    return keyed_ordered_sum<float>(u, n, group, out, scratch, stream, "hk_keyed_ordered_sum_f32");
 }
 
 int hk_keyed_sample_sum_f64(const double* u, int64_t n, int64_t group, double* out, void* stream) {
@@ -1873,65 +1995,12 @@ size_t hk_ordered_scatter_scratch_bytes(int64_t n, int64_t cells) {
 
 int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n, double* target, int64_t cells,
                            void* scratch, int32_t* status, void* stream) {
-    if (n < 0 || cells < 0)
-        return hawk_internal::set_error(HK_EVALUE, "hk_ordered_scatter_f64: n and cells must be >= 0");
-    if (cells == 0) return HK_OK;   // a scatter into no cells adds nothing (reference hawk/runtime.py:727)
-    if ((n > 0 && (!key || !v)) || !target || !scratch || !status)
-        return hawk_internal::set_error(HK_EVALUE,
-                                        "hk_ordered_scatter_f64: key, v, target, scratch and status are required");
-    if (cells > 0x7fffffffLL)
-        return hawk_internal::set_error(HK_EVALUE, "hk_ordered_scatter_f64: more than 2^31-1 cells");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const int chunks = hk_scatter_chunks(n, cells);
-    const ScatterLayout L = scatter_layout(n, cells, chunks);
-    unsigned char* base = static_cast<unsigned char*>(scratch);
-    auto* parts = reinterpret_cast<double*>(base + L.parts);
-    hipLaunchKernelGGL(hawk_scatter_status, dim3(1), dim3(kScatterChunks + 64), 0, s, status,
-                       static_cast<long long>(cells));
-    int rc = launch_error("hawk_scatter_status launch");
-    if (rc != HK_OK) return rc;
-    if (L.split) {
-        auto* bin_off = reinterpret_cast<unsigned*>(base + L.bin_off);
-        auto* bin_key = reinterpret_cast<unsigned short*>(base + L.bin_key);
-        auto* bin_val = reinterpret_cast<double*>(base + L.bin_val);
-        hipLaunchKernelGGL(hawk_split_hot, dim3(static_cast<unsigned>(chunks)), dim3(kWalkThreads), 0, s, key, v,
-                           static_cast<long long>(n), static_cast<long long>(cells), L.span, L.tiles, L.ranges,
-                           bin_key, bin_val, bin_off, parts, status);
-        rc = launch_error("hawk_split_hot launch");
-        if (rc != HK_OK) return rc;
-        if (L.ranges > 0) {
-            hipLaunchKernelGGL(hawk_split_tail, dim3(static_cast<unsigned>(chunks * L.ranges)), dim3(kWalkThreads),
-                               0, s, static_cast<long long>(cells), L.tiles, L.ranges, bin_key, bin_val, bin_off,
-                               parts);
-            rc = launch_error("hawk_split_tail launch");
-            if (rc != HK_OK) return rc;
-        }
-    } else {
-        // more cells than the split walk's windows cover: parts arrives
-        // zero-filled and the sorted walk (or, past its key field, the serial
-        // walk) adds onto it
-        const long long count = static_cast<long long>(chunks) * cells;
-        const long long blocks = (count + 255) / 256 < 4096 ? (count + 255) / 256 : 4096;
-        hipLaunchKernelGGL(hawk_fill_zero, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, parts, count);
-        rc = launch_error("hawk_fill_zero launch");
-        if (rc != HK_OK) return rc;
-        const int key_bits = bits_for(cells - 1);
-        if (key_bits <= kMaxKeyBits) {
-            hipLaunchKernelGGL(hawk_scatter_walk, dim3(static_cast<unsigned>(chunks)), dim3(kWalkThreads), 0, s,
-                               key, v, static_cast<long long>(n), static_cast<long long>(cells), L.span, key_bits,
-                               parts, status);
-            rc = launch_error("hawk_scatter_walk launch");
-        } else {
-            hipLaunchKernelGGL(hawk_scatter_serial, dim3(static_cast<unsigned>(chunks)), dim3(64), 0, s, key, v,
-                               static_cast<long long>(n), static_cast<long long>(cells), L.span, parts, status);
-            rc = launch_error("hawk_scatter_serial launch");
-        }
-        if (rc != HK_OK) return rc;
-    }
-    const long long grid = (cells + 255) / 256;
-    hipLaunchKernelGGL(hawk_scatter_cells, dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, parts,
-                       static_cast<long long>(cells), chunks, target);
-    return launch_error("hawk_scatter_cells launch");
+    return ordered_scatter<double>(key, v, n, target, cells, scratch, status, stream, "hk_ordered_scatter_f64");
+}
+
+int hk_ordered_scatter_f32(const int32_t* key, const float* v, int64_t n, float* target, int64_t cells,
+                           void* scratch, int32_t* status, void* stream) {
+    return ordered_scatter<float>(key, v, n, target, cells, scratch, status, stream, "hk_ordered_scatter_f32");
 }
 
 size_t hk_keyed_log_fold_scratch_bytes(int64_t cells) {

@@ -1555,8 +1555,9 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
             team.append({"op": "band_rows" if banded else "row_sum", "hi": f"hk_rows_{s.name}",
                          "comp": f"hk_rows_{s.name}_comp", "out": s.name})
         elif isinstance(s, SampleSum):
-            if mode != "float64":
-                raise HawkError(f"hawk.sum(policy={s.policy!r}) on the hip target is built in float64")
+            if mode != "float64" and s.policy != "ordered":
+                raise HawkError(f"hawk.sum(x, over=...) with policy={s.policy!r} on the hip target is built in "
+                                "float64 (float32 builds hawk.sum over every sample and policy='ordered')")
             src = assigned.get(id(s.value))
             if src is None and s.value.kind == "leaf" and s.value.literal[0] == "per_sample":
                 src = s.value.literal[1]
@@ -1570,8 +1571,6 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
             else:                                   # the default policy over some axes
                 team.append({"op": "keyed_comp", "u": src, "out": s.name, "group": s.group})
         elif isinstance(s, AccumWrite):
-            if mode != "float64":
-                raise HawkError("hawk.scatter(policy='ordered') on the hip target is built in float64")
             src = assigned.get(id(s.value))
             if src is None and s.value.kind == "leaf" and s.value.literal[0] == "per_sample":
                 src = s.value.literal[1]
@@ -1621,5 +1620,7 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
     for pname, info in planes.items():
         if pname.startswith("hk_"):
             info["scratch"] = True
+        if mode == "float32" and info["dtype"] == "f64":
+            info["dtype"] = "f32"                # a float32 build's real planes hold float32
     return Plan(stage, source, team, planes, fp_ops_per_sample(source) if source else 0,
                 block=stage.block if stage is not None else None)

@@ -261,7 +261,7 @@ ALL = {k.name: k for k in (scale, energy, energy_vjp, energy_jvp, twobody, twobo
                             spd_solve_vjp, chain, chain_steps, ordered_total, ordered_add, sample_total, plain_total,
                             twobody_vjp_mu, add_sq, add_sq_grad, chain_vjp, chain_jvp, mm16, mm16_vjp)}
 #: The float32 unit (built with mode="float32").
-FLOAT32 = {k.name: k for k in (mm16, mm16_vjp, sample_total, plain_total)}
+FLOAT32 = {k.name: k for k in (mm16, mm16_vjp, sample_total, plain_total, ordered_total, ordered_add, add_sq)}
 
 
 @kernel

@@ -331,6 +331,11 @@ class DeviceKernel:
         return n
 
     # -- scratch -------------------------------------------------------------
+    def _is_f32(self, plane: str) -> bool:
+        """Whether a team stage's cell or target plane holds float32 (a float32
+        build's sums and scatters run in float32)."""
+        return self.planes[plane]["dtype"] == "f32"
+
     def _buffer(self, key, nbytes: int, device, zero: bool = True):
         torch = _torch()
         held = self._scratch.get(key)
@@ -494,7 +499,8 @@ class DeviceKernel:
             if t["op"] == "ordered_sum":
                 u = bound[t["u"]]
                 scratch = self._buffer(("sum", t["out"]), _core.ordered_sum_scratch_bytes(), device)
-                _core.ordered_sum(u.data_ptr(), n, bound[t["out"]].data_ptr(), scratch.data_ptr(), stream)
+                fn = _core.ordered_sum_f32 if self._is_f32(t["out"]) else _core.ordered_sum
+                fn(u.data_ptr(), n, bound[t["out"]].data_ptr(), scratch.data_ptr(), stream)
             elif t["op"] == "ordered_scatter":
                 target = bound[t["target"]]
                 cells = int(target.numel())
@@ -503,8 +509,9 @@ class DeviceKernel:
                 scratch = self._buffer(("scatter", t["target"], n, cells),
                                        _core.ordered_scatter_scratch_bytes(n, cells), device, zero=False)
                 status = self._buffer(("status", t["target"]), 4 * 257, device)
-                _core.ordered_scatter(bound[t["key"]].data_ptr(), bound[t["v"]].data_ptr(), n,
-                                      target.data_ptr(), cells, scratch.data_ptr(), status.data_ptr(), stream)
+                fn = _core.ordered_scatter_f32 if self._is_f32(t["target"]) else _core.ordered_scatter
+                fn(bound[t["key"]].data_ptr(), bound[t["v"]].data_ptr(), n, target.data_ptr(), cells,
+                   scratch.data_ptr(), status.data_ptr(), stream)
                 self.scatter_chunks = _core.scatter_chunks(n, cells)
                 statuses.append((t, status, cells))
             elif t["op"] == "mm16":
@@ -520,8 +527,8 @@ class DeviceKernel:
             elif t["op"] == "keyed_sum":
                 scratch = self._buffer(("keyed", t["out"], n), _core.keyed_ordered_sum_scratch_bytes(n, t["group"]),
                                        device)
-                _core.keyed_ordered_sum(bound[t["u"]].data_ptr(), n, t["group"], bound[t["out"]].data_ptr(),
-                                        scratch.data_ptr(), stream)
+                fn = _core.keyed_ordered_sum_f32 if self._is_f32(t["out"]) else _core.keyed_ordered_sum
+                fn(bound[t["u"]].data_ptr(), n, t["group"], bound[t["out"]].data_ptr(), scratch.data_ptr(), stream)
             elif t["op"] == "ordered_fold":
                 args, status, cells = self._fold_args(t, bound, n, device)
                 _core.keyed_log_fold(*args, stream)
@@ -796,7 +803,7 @@ class Prepared:
             if t["op"] == "ordered_sum":
                 scratch = kernel._buffer(("sum", t["out"]), _core.ordered_sum_scratch_bytes(), device)
                 args = (bound[t["u"]].data_ptr(), self.n, bound[t["out"]].data_ptr(), scratch.data_ptr())
-                self.steps.append((_core.ordered_sum, args))
+                self.steps.append((_core.ordered_sum_f32 if kernel._is_f32(t["out"]) else _core.ordered_sum, args))
             elif t["op"] == "ordered_scatter":
                 target = bound[t["target"]]
                 cells = int(target.numel())
@@ -807,7 +814,8 @@ class Prepared:
                 status = kernel._buffer(("status", t["target"]), 4 * 257, device)
                 args = (bound[t["key"]].data_ptr(), bound[t["v"]].data_ptr(), self.n, target.data_ptr(), cells,
                         scratch.data_ptr(), status.data_ptr())
-                self.steps.append((_core.ordered_scatter, args))
+                self.steps.append((_core.ordered_scatter_f32 if kernel._is_f32(t["target"]) else _core.ordered_scatter,
+                                   args))
                 self.statuses.append((t, status, cells))
             elif t["op"] == "mm16":
                 args = ([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
@@ -824,7 +832,8 @@ class Prepared:
                 scratch = kernel._buffer(("keyed", t["out"], self.n),
                                          _core.keyed_ordered_sum_scratch_bytes(self.n, t["group"]), device)
                 args = (bound[t["u"]].data_ptr(), self.n, t["group"], bound[t["out"]].data_ptr(), scratch.data_ptr())
-                self.steps.append((_core.keyed_ordered_sum, args))
+                self.steps.append((_core.keyed_ordered_sum_f32 if kernel._is_f32(t["out"]) else _core.keyed_ordered_sum,
+                                   args))
             elif t["op"] == "ordered_fold":
                 args, status, cells = kernel._fold_args(t, bound, self.n, device)
                 self.steps.append((_core.keyed_log_fold, args))
@@ -862,9 +871,11 @@ class Prepared:
                 k.entry.run(self.block, 0, self.n, self.n, threads=k.launch_shape["block"],
                             per_thread=k.launch_shape["per_thread"], stream=self.stream)
             out.append((k.name, stage))
-        labels = {_core.ordered_sum: "ordered_sum", _core.band_ordered_sum: "band_ordered_sum",
-                  _core.ordered_scatter: "ordered_scatter", _core.mm16: "mm16", _core.mm16_f64: "mm16",
-                  _core.keyed_ordered_sum: "keyed_sum", _core.keyed_log_fold: "ordered_fold",
+        labels = {_core.ordered_sum: "ordered_sum", _core.ordered_sum_f32: "ordered_sum",
+                  _core.band_ordered_sum: "band_ordered_sum",
+                  _core.ordered_scatter: "ordered_scatter", _core.ordered_scatter_f32: "ordered_scatter",
+                  _core.mm16: "mm16", _core.mm16_f64: "mm16",
+                  _core.keyed_ordered_sum: "keyed_sum", _core.keyed_ordered_sum_f32: "keyed_sum", _core.keyed_log_fold: "ordered_fold",
                   _core.keyed_sample_sum: "keyed_comp"}
         for fn, args in self.steps:
             label = labels.get(fn, "row_sum")

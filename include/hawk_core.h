@@ -161,6 +161,11 @@ int hk_launch_grid(const hk_entry* entry, const hk_argblock* ab, int64_t base,
 size_t hk_ordered_sum_scratch_bytes(void);
 int hk_ordered_sum_f64(const double* u, int64_t n, double* out, void* scratch,
                        void* stream);
+/* The same sum in the float32 mode: the lanes, the trees and *out are float
+ * (the reference's team stages add `Real`s, `hawk/emit/team.py:248-261`).
+ * Same scratch (size and zero-before-first-call rule) as the fp64 sum. */
+int hk_ordered_sum_f32(const float* u, int64_t n, float* out, void* scratch,
+                       void* stream);
 
 /* hk_ordered_sum_f64 for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
@@ -192,6 +197,10 @@ int hk_ordered_fold_f64(const double* lanes, double* out, void* scratch,
  * needed (for group == n, the ordered sum's scratch, zero before its first call). */
 size_t hk_keyed_ordered_sum_scratch_bytes(int64_t n, int64_t group);
 int hk_keyed_ordered_sum_f64(const double* u, int64_t n, int64_t group, double* out,
+                             void* scratch, void* stream);
+/* The keyed ordered sum in the float32 mode (float rows, trees and cells),
+ * same scratch and refusals. */
+int hk_keyed_ordered_sum_f32(const float* u, int64_t n, int64_t group, float* out,
                              void* scratch, void* stream);
 
 /* `hawk.sum(x, over=<trailing lane axes>)` under the default policy: for
@@ -256,12 +265,20 @@ int hk_band_ordered_sum_f64(const double* u, int64_t n, double* out, void* scrat
  * a bad key was met: the caller reads status[1..256] (the reference's
  * `check_scatter_status`, `hawk/_lane_bind.py:148-154`).
  * Scratch: hk_ordered_scatter_scratch_bytes(n, cells) bytes, no initial
- * contents needed: the per-(chunk, cell) partials, then (up to 65536 cells)
- * a per-chunk bitmap of the cells each chunk touched. */
+ * contents needed: the per-(chunk, cell) partials, then (for 12288 < cells
+ * <= 65536) the bins that carry each tile's lanes of keys past the first
+ * 12288 from the first walk to the second. */
 int hk_scatter_chunks(int64_t n, int64_t cells);
 size_t hk_ordered_scatter_scratch_bytes(int64_t n, int64_t cells);
 int hk_ordered_scatter_f64(const int32_t* key, const double* v, int64_t n,
                            double* target, int64_t cells, void* scratch,
+                           int32_t* status, void* stream);
+/* The ordered scatter in the float32 mode: v, the partials, the cells' sums
+ * and target are float, every addition a float addition (the reference's
+ * `_scatter_chunks` / `_scatter_cells` over `Real`).  Same scratch (the fp64
+ * size is an upper bound), status and refusals. */
+int hk_ordered_scatter_f32(const int32_t* key, const float* v, int64_t n,
+                           float* target, int64_t cells, void* scratch,
                            int32_t* status, void* stream);
 
 /* The ordered gradient's log fold: reference `hawk/diff/ordered.py` (the VJP

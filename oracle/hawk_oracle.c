@@ -515,6 +515,33 @@ HKO_EXPORT double hko_ordered_sum(const double* u, int64_t n) {
     return fold_groups(gp);
 }
 
+/* The ordered sum in the float32 mode: the reference's team stages are
+ * written over `Real` (hawk/emit/team.py:248-261), so in float32 every lane
+ * sum and every tree level is a float addition. */
+static float group_part_f(const float* u, int64_t rows, int g) {
+    float sh[HKO_W];
+    for (int t = 0; t < HKO_W; ++t) sh[t] = 0.0f;
+    for (int64_t b = (int64_t)g * HKO_W; b < rows; b += HKO_V) {
+        const int64_t m = rows - b < HKO_W ? rows - b : HKO_W;
+        for (int64_t t = 0; t < m; ++t) sh[t] += u[b + t];
+    }
+    for (int w = HKO_W / 2; w > 0; w >>= 1)
+        for (int i = 0; i < w; ++i) sh[i] += sh[i + w];
+    return sh[0];
+}
+
+HKO_EXPORT float hko_ordered_sum_f32(const float* u, int64_t n) {
+    float gp[HKO_G];
+    for (int g = 0; g < HKO_G; ++g) gp[g] = group_part_f(u, n, g);
+    for (int w = HKO_G / 2; w > 0; w >>= 1)
+        for (int i = 0; i < w; ++i) gp[i] += gp[i + w];
+    return gp[0];
+}
+
+HKO_EXPORT void hko_keyed_ordered_sum_f32(const float* u, int64_t n, int64_t group, float* out) {
+    for (int64_t k = 0; k * group < n; ++k) out[k] = hko_ordered_sum_f32(u + k * group, group);
+}
+
 /* hawk.sum(x, over=<trailing lane axes>, policy="ordered"): key k's rows are
  * u[k*group .. (k+1)*group), each key takes the ordered sum's tree on its own
  * rows (reference hawk/emit/team.py:115-205 and :208-278: block b is group
@@ -661,6 +688,34 @@ HKO_EXPORT void hko_ordered_scatter(const int32_t* key, const double* v, int64_t
     for (int b = 0; b < 256; ++b) status[1 + b] = 0;
     for (int b = 0; b < chunks; ++b) scatter_chunk(key, v, n, cells, chunks, b, parts, status);
     scatter_cells(parts, 0, cells, chunks, target);
+}
+
+/* The keyed ordered scatter in the float32 mode (the walk's parts, the cells'
+ * sums and the target are float; reference hawk/emit/team.py:322-460 over
+ * `Real`).  parts: chunks*cells floats of scratch; status: 257 int32. */
+HKO_EXPORT void hko_ordered_scatter_f32(const int32_t* key, const float* v, int64_t n, float* target,
+                                        int64_t cells, float* parts, int32_t* status) {
+    if (cells <= 0) return;
+    const int chunks = hko_scatter_chunks(n, cells);
+    memset(parts, 0, sizeof(float) * (size_t)chunks * (size_t)cells);
+    status[0] = (int32_t)cells;
+    for (int b = 0; b < 256; ++b) status[1 + b] = 0;
+    const int64_t span = (n + chunks - 1) / chunks;
+    for (int b = 0; b < chunks; ++b) {
+        const int64_t lo = (int64_t)b * span;
+        const int64_t hi = lo + span < n ? lo + span : n;
+        for (int64_t r = lo; r < hi; ++r) {
+            const int32_t k = key[r];
+            if (k == -1) continue;
+            if (k >= 0 && k < cells) parts[(int64_t)k * chunks + b] += v[r];
+            else status[1 + b] = 1;
+        }
+    }
+    for (int64_t c = 0; c < cells; ++c) {
+        float acc = 0.0f;
+        for (int b = 0; b < chunks; ++b) acc += parts[c * chunks + b];
+        target[c] += acc;
+    }
 }
 
 /* ---- config 3: two-body leapfrog, 32 kick-drift-kick substeps ------------

@@ -57,6 +57,9 @@ def lib(profile: str | None = None):
         "hko_chain_jvp": (None, [_P, _P, _I64, _P]),
         "hko_libm": (None, [ctypes.c_int, _P, _P, _I64]),
         "hko_ordered_sum": (_D, [_P, _I64]),
+        "hko_ordered_sum_f32": (ctypes.c_float, [_P, _I64]),
+        "hko_keyed_ordered_sum_f32": (None, [_P, _I64, _I64, _P]),
+        "hko_ordered_scatter_f32": (None, [_P, _P, _I64, _P, _I64, _P, _P]),
         "hko_keyed_ordered_sum": (None, [_P, _I64, _I64, _P]),
         "hko_keyed_ordered_sum_threads": (None, [_P, _I64, _I64, _P, ctypes.c_int]),
         "hko_keyed_log_fold": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, ctypes.c_int32, _P, _I64]),
@@ -179,13 +182,22 @@ def libm(which: str, x):
 
 
 def ordered_sum(u, threads: int = 1) -> float:
+    if u.dtype == np.float32:                     # the float32 mode: every addition in float
+        return np.float32(lib().hko_ordered_sum_f32(_p(u), u.size))
     if threads > 1:
         return lib().hko_ordered_sum_threads(_p(u), u.size, threads)
     return lib().hko_ordered_sum(_p(u), u.size)
 
 
 def keyed_ordered_sum(u, group: int, threads: int = 1, profile: str = "portable"):
-    """One ordered-sum cell per run of ``group`` consecutive values."""
+    """One ordered-sum cell per run of ``group`` consecutive values (float32
+    cells, float32 additions, for a float32 ``u``)."""
+    if getattr(u, "dtype", None) == np.float32:
+        u = np.ascontiguousarray(u)
+        assert u.size % group == 0
+        out = np.empty(u.size // group, dtype=np.float32)
+        lib(profile).hko_keyed_ordered_sum_f32(_p(u), u.size, group, _p(out))
+        return out
     u = np.ascontiguousarray(u, dtype=np.float64)
     assert u.size % group == 0
     out = np.empty(u.size // group)
@@ -340,8 +352,13 @@ def ordered_scatter(key, v, target, threads: int = 1):
     out = target.copy()
     cells = out.size
     chunks = scatter_chunks(key.size, cells)
-    parts = np.empty(chunks * max(cells, 1))
     status = np.zeros(257, dtype=np.int32)
+    if out.dtype == np.float32:                   # the float32 mode: parts, cells and target in float
+        assert v.dtype == np.float32
+        parts = np.empty(chunks * max(cells, 1), dtype=np.float32)
+        lib().hko_ordered_scatter_f32(_p(key), _p(v), key.size, _p(out), cells, _p(parts), _p(status))
+        return out, status
+    parts = np.empty(chunks * max(cells, 1))
     if threads > 1:
         lib().hko_ordered_scatter_threads(_p(key), _p(v), key.size, _p(out), cells, _p(parts), _p(status), threads)
     else:

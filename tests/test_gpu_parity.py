@@ -1453,3 +1453,82 @@ def test_banded_sums_on_the_device_hold_the_reference_bounds(unit_banded, gpu):
     want = float(Fraction(int(k_int.sum()), 1 << 20))
     got = run(x)
     assert got["s"] == got["s_ord"] == want
+
+
+# -- the float32 mode's ordered reductions ----------------------------------
+
+@pytest.mark.parametrize("n", golden("ordered_sum_sizes")["sizes"])
+def test_float32_ordered_sum_is_the_float32_tree_bitwise(unit32, gpu, n):
+    """hawk.sum(x, policy="ordered") in a float32 build: every lane sum and
+    tree level a float addition (the reference's team stages add `Real`s):
+    the float32 oracle's bits, NumPy's float32 tree, on three launches."""
+    import hawk_amd as hawk
+    g = rng(n + 32)
+    x = (g.normal(size=n) * np.exp(g.normal(size=n))).astype(np.float32)
+    k = _load(unit32, "ordered_total")
+    runs = []
+    for _ in range(3):
+        total = dev(np.zeros(1, np.float32), gpu)
+        hawk.run(k, x=dev(x, gpu), total=total)
+        runs.append(host(total))
+    assert runs[0].dtype == np.float32
+    assert runs[0].tobytes() == runs[1].tobytes() == runs[2].tobytes()
+    assert runs[0][0].tobytes() == O.ordered_sum(x).tobytes() == np.float32(tree_sum(x)).tobytes()
+
+
+@pytest.mark.parametrize("cells, n, heavy", [(7, 30_000, False), (1000, 30_000, False), (7, 20_000, True),
+                                             (3, 1000, False), (65536, 400_000, False), (12289, 300_001, False),
+                                             (40_000, 2_000_003, True), (70_000, 300_000, False),
+                                             (600_000, 1_300_000, False)])
+def test_float32_ordered_scatter_is_the_float32_walk_bitwise(unit32, gpu, cells, n, heavy):
+    """hawk.scatter(acc, policy="ordered")[key] += x in a float32 build, through
+    every form of the walk (split walk with and without tail ranges, sorted
+    walk, serial walk): the float32 oracle's bits, the same on a replay."""
+    import hawk_amd as hawk
+    g = rng(cells + n + 32)
+    key = g.integers(0, cells, n).astype(np.int32)
+    if heavy:
+        key[g.random(n) < 0.9] = cells // 2
+    key[::7] = -1
+    print(f"float32 scatter cells={cells} n={n} heavy={heavy}", flush=True)
+    x = (g.normal(size=n) * np.exp(g.normal(size=n))).astype(np.float32)
+    acc0 = np.linspace(1.0, 2.0, cells).astype(np.float32)
+    k = _load(unit32, "ordered_add")
+    outs = []
+    for _ in range(2):
+        acc = dev(acc0, gpu)
+        hawk.run(k, key=dev(key, gpu), x=dev(x, gpu), acc=acc)
+        outs.append(host(acc))
+    want, status = O.ordered_scatter(key, x, acc0)
+    assert not status[1:].any() and want.dtype == np.float32
+    assert outs[0].tobytes() == outs[1].tobytes() == want.tobytes()
+
+
+def test_float32_scatter_of_a_computed_value_and_zipf_keys(unit32, gpu):
+    """A float32 stage computes x*x into its own plane and the float32 scatter
+    folds it at config 5's Zipf keys into 65536 cells: the oracle's bits."""
+    import hawk_amd as hawk
+    n, cells = 1 << 20, 1 << 16
+    g = rng(321)
+    key = ((g.zipf(1.1, n) - 1) % cells).astype(np.int32)
+    x = g.normal(size=n).astype(np.float32)
+    acc0 = g.normal(size=cells).astype(np.float32)
+    acc = dev(acc0, gpu)
+    hawk.run(_load(unit32, "add_sq"), key=dev(key, gpu), x=dev(x, gpu), acc=acc)
+    want, _ = O.ordered_scatter(key, (x * x).astype(np.float32), acc0)
+    assert host(acc).tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("keys, group", [(4, 8), (1000, 5000), (3, 200003), (70000, 7), (17, 1025), (3000, 2)])
+def test_float32_keyed_ordered_sum_bitwise(gpu, tmp_path, keys, group):
+    """hawk.sum(x, over=<trailing axes>, policy="ordered") in a float32 build:
+    each key's run by the fixed tree in float, the float32 oracle's bits."""
+    import hawk_amd as hawk
+    hawk.build([_keyed_kernels(group)], tmp_path, mode="float32")
+    kern = hawk.load(tmp_path, "ksum")
+    n = keys * group
+    x = (rng(70 + group).uniform(-2.0, 2.0, n) * np.exp(rng(8).normal(size=n))).astype(np.float32)
+    print(f"float32 keyed sum keys={keys} group={group}", flush=True)
+    out = dev(np.full(keys, np.nan, np.float32), gpu)
+    hawk.run(kern, x=dev(x, gpu), out=out)
+    assert host(out).tobytes() == O.keyed_ordered_sum(x, group).tobytes()

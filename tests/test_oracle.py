@@ -743,3 +743,74 @@ def test_the_interchanged_twobody_loops_are_the_serial_bits(n):
     assert tr.tobytes() == r.tobytes() and tv.tobytes() == v.tobytes()
     ta, tb = O.twobody_vjp(r0, v0, 1.0, br, bv, threads=3)
     assert ta.tobytes() == a.tobytes() and tb.tobytes() == b.tobytes()
+
+
+# -- the float32 mode's ordered reductions ----------------------------------
+
+@pytest.mark.parametrize("n", golden("ordered_sum_sizes")["sizes"])
+def test_float32_ordered_sum_is_the_numpy_float32_tree(n):
+    """The reference's team stages add `Real`s: in float32 every lane sum and
+    tree level is a float addition.  NumPy's tree over float32 arrays is the
+    closed form (reference tests/test_ordered_fixed_tree.py:25-40)."""
+    g = np.random.default_rng(n + 32)
+    x = (g.normal(size=n) * np.exp(g.normal(size=n))).astype(np.float32)
+    got = O.ordered_sum(x)
+    assert isinstance(got, np.float32) and got.tobytes() == np.float32(tree_sum(x)).tobytes()
+
+
+def test_float32_ordered_sum_is_float32_arithmetic():
+    """Small integers are exact in float32: their sums are the integer sums;
+    on normal values the float32 tree rounds where the float64 one does not."""
+    x = np.arange(1, 70001, dtype=np.float32)
+    assert O.ordered_sum(x) == np.float32(70000 * 70001 / 2)
+    y = np.random.default_rng(34).normal(size=1 << 20).astype(np.float32)
+    assert O.ordered_sum(y) != np.float32(O.ordered_sum(y.astype(np.float64)))
+    assert O.ordered_sum(y) == np.float32(tree_sum(y))
+
+
+def test_float32_keyed_ordered_sum_is_each_keys_tree():
+    g = np.random.default_rng(40)
+    for group in (1, 7, 64, 4096, 70001):
+        u = g.normal(size=3 * group).astype(np.float32)
+        got = O.keyed_ordered_sum(u, group)
+        assert got.dtype == np.float32
+        want = [np.float32(tree_sum(u[k * group:(k + 1) * group])) for k in range(3)]
+        assert got.tobytes() == np.array(want, np.float32).tobytes()
+
+
+def test_float32_ordered_scatter_is_the_serial_chunk_walk():
+    """Brute force with numpy float32 scalars over a small case (per (key,
+    chunk) in lane order from 0, per cell in chunk order from 0, onto the
+    target), and integer values against np.add.at exactly."""
+    g = np.random.default_rng(33)
+    n, cells = 3000, 11
+    key = g.integers(-1, cells + 2, n).astype(np.int32)
+    x = g.normal(size=n).astype(np.float32)
+    base = g.normal(size=cells).astype(np.float32)
+    chunks = O.scatter_chunks(n, cells)
+    span = -(-n // chunks)
+    parts = np.zeros((cells, chunks), np.float32)
+    bad = [0] * chunks
+    for r in range(n):
+        b, k = r // span, int(key[r])
+        if k == -1:
+            continue
+        if 0 <= k < cells:
+            parts[k, b] = np.float32(parts[k, b] + x[r])
+        else:
+            bad[b] = 1
+    want = base.copy()
+    for c in range(cells):
+        s = np.float32(0.0)
+        for b in range(chunks):
+            s = np.float32(s + parts[c, b])
+        want[c] = np.float32(want[c] + s)
+    got, status = O.ordered_scatter(key, x, base)
+    assert got.dtype == np.float32 and got.tobytes() == want.tobytes()
+    assert list(status[1:1 + chunks]) == bad
+    ki = g.integers(0, 300, 200_000).astype(np.int32)
+    xi = g.integers(-50, 51, 200_000).astype(np.float32)
+    exact = np.zeros(300, np.float64)
+    np.add.at(exact, ki, xi.astype(np.float64))
+    got, _ = O.ordered_scatter(ki, xi, np.zeros(300, np.float32))
+    assert (got.astype(np.float64) == exact).all()
