@@ -76,6 +76,7 @@ def _declare(lib) -> None:
         "hk_mm16_f64": (I, [ctypes.POINTER(V), I, ctypes.POINTER(V), I, ctypes.POINTER(ctypes.c_int32), I64, V]),
         "hk_keyed_log_fold_scratch_bytes": (SZ, [I64]),
         "hk_keyed_sample_sum_f64": (I, [V, I64, I64, V, V]),
+        "hk_keyed_sample_sum_f32": (I, [V, I64, I64, V, V]),
         "hk_keyed_log_fold_f64": (I, [V, I64, V, I64, I64, ctypes.c_int32, V, I64, V, V, V]),
     }
     for name, (res, args) in sig.items():
@@ -372,6 +373,12 @@ def keyed_ordered_sum_f32(u: int, n: int, group: int, out: int, scratch: int, st
 def keyed_sample_sum(u: int, n: int, group: int, out: int, stream: int = 0) -> None:
     """``out[k]`` = key k's ``group`` rows as a default-policy sample sum of their own."""
     check(lib().hk_keyed_sample_sum_f64(ctypes.c_void_p(u or None), int(n), int(group), ctypes.c_void_p(out or None),
+                                        ctypes.c_void_p(stream or None)))
+
+
+def keyed_sample_sum_f32(u: int, n: int, group: int, out: int, stream: int = 0) -> None:
+    """keyed_sample_sum of a float32 plane into float32 cells."""
+    check(lib().hk_keyed_sample_sum_f32(ctypes.c_void_p(u or None), int(n), int(group), ctypes.c_void_p(out or None),
                                         ctypes.c_void_p(stream or None)))
 
 

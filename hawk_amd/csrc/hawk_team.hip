@@ -387,22 +387,24 @@ __global__ __launch_bounds__(256) void hawk_band_rows_levels(double* __restrict_
 // key; row r lands in slot r % 256 and every slot adds its rows in order.
 constexpr long long kKeyedCompLeaves = kRowSlots;        // leaves a key may span
 
-__device__ __forceinline__ void row_pair_sum(double& h, double& c) {
+template <class T>
+__device__ __forceinline__ void row_pair_sum(T& h, T& c) {
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1) {
-        const double h2 = __shfl_xor(h, off, 64);
-        const double c2 = __shfl_xor(c, off, 64);
-        const double s = h + h2;
-        c = finite_bits(s) ? (c + c2) + two_sum_err(h, h2, s) : 0.0;
+        const T h2 = __shfl_xor(h, off, 64);
+        const T c2 = __shfl_xor(c, off, 64);
+        const T s = h + h2;
+        c = finite_bits(s) ? (c + c2) + two_sum_err(h, h2, s) : T(0);
         h = s;
     }
 }
 
-__global__ __launch_bounds__(kRowSlots) void hawk_keyed_comp(const double* __restrict__ u, long long group,
-                                                             double* __restrict__ out) {
-    __shared__ double sh[kRowSlots], sc[kRowSlots], lh[kKeyedCompLeaves], lc[kKeyedCompLeaves];
+template <class T>
+__global__ __launch_bounds__(kRowSlots) void hawk_keyed_comp(const T* __restrict__ u, long long group,
+                                                             T* __restrict__ out) {
+    __shared__ T sh[kRowSlots], sc[kRowSlots], lh[kKeyedCompLeaves], lc[kKeyedCompLeaves];
     const int t = threadIdx.x, half = t >> 5, l = t & 31;
-    const double* __restrict__ mine = u + static_cast<long long>(blockIdx.x) * group;
+    const T* __restrict__ mine = u + static_cast<long long>(blockIdx.x) * group;
     const long long rows = (group + 31) / 32;
     const long long leaves = (rows + kRowLeaf - 1) / kRowLeaf;
     for (long long j = 0; j < leaves; ++j) {
@@ -415,25 +417,25 @@ __global__ __launch_bounds__(kRowSlots) void hawk_keyed_comp(const double* __res
         // barrier; four rows' loads are in flight at a time.
         for (int rb0 = 0; rb0 < cnt; rb0 += 32) {       // the same trips for every lane
             const int rb = rb0 + half;
-            double x[4];
+            T x[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int r = rb + 8 * q;
                 const long long at = (lo + r) * 32 + l;
-                x[q] = (r < cnt && at < group) ? __builtin_nontemporal_load(mine + at) : 0.0;
+                x[q] = (r < cnt && at < group) ? __builtin_nontemporal_load(mine + at) : T(0);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int r = rb + 8 * q;
-                double h = x[q], c = 0.0;
-                row_pair_sum(h, c);
+                T h = x[q], c = T(0);
+                row_pair_sum<T>(h, c);
                 if (l == 0 && r < cnt) {
                     const int slot = r & (kRowSlots - 1);
                     if (r < kRowSlots) {
                         sh[slot] = h;
-                        sc[slot] = finite_bits(h) ? c : 0.0;
+                        sc[slot] = finite_bits(h) ? c : T(0);
                     } else {
-                        double a = sh[slot], b = sc[slot];
+                        T a = sh[slot], b = sc[slot];
                         neumaier_add(a, b, h, c);
                         sh[slot] = a;
                         sc[slot] = b;
@@ -445,7 +447,7 @@ __global__ __launch_bounds__(kRowSlots) void hawk_keyed_comp(const double* __res
         for (int off = kRowSlots / 2; off > 0; off >>= 1) {
             const int lim = live > off ? (off < live - off ? off : live - off) : 0;
             if (t < lim) {
-                double h = sh[t], c = sc[t];
+                T h = sh[t], c = sc[t];
                 pair_add(h, c, sh[t + off], sc[t + off]);
                 sh[t] = h;
                 sc[t] = c;
@@ -463,7 +465,7 @@ __global__ __launch_bounds__(kRowSlots) void hawk_keyed_comp(const double* __res
         while (m > 1) {               // in place: pair p reads slots 2p, 2p + 1 >= p
             const long long pairs = m / 2;
             for (long long p = 0; p < pairs; ++p) {
-                double h = lh[2 * p], c = lc[2 * p];
+                T h = lh[2 * p], c = lc[2 * p];
                 pair_add(h, c, lh[2 * p + 1], lc[2 * p + 1]);
                 lh[p] = h;
                 lc[p] = c;
@@ -483,28 +485,29 @@ __global__ __launch_bounds__(kRowSlots) void hawk_keyed_comp(const double* __res
 // r: fewer than 256 rows, so no slot takes a second row), then the halving
 // tree over the R live slots, as the leaf above: the same bits.  A wave past
 // the last key computes nothing but meets every barrier.
-__global__ __launch_bounds__(256) void hawk_keyed_comp_wave(const double* __restrict__ u, long long group,
-                                                            long long keys, double* __restrict__ out) {
-    __shared__ double sh[4][64], sc[4][64];
+template <class T>
+__global__ __launch_bounds__(256) void hawk_keyed_comp_wave(const T* __restrict__ u, long long group,
+                                                            long long keys, T* __restrict__ out) {
+    __shared__ T sh[4][64], sc[4][64];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, half = lane >> 5, l = lane & 31;
     const long long k = static_cast<long long>(blockIdx.x) * 4 + w;
     const bool live = k < keys;
-    const double* __restrict__ mine = u + (live ? k : 0) * group;
+    const T* __restrict__ mine = u + (live ? k : 0) * group;
     const int rows = static_cast<int>((group + 31) / 32);
     for (int rb = 0; rb < rows; rb += 2) {
         const int r = rb + half;
         const long long at = static_cast<long long>(r) * 32 + l;
-        double h = (live && r < rows && at < group) ? __builtin_nontemporal_load(mine + at) : 0.0, c = 0.0;
-        row_pair_sum(h, c);
+        T h = (live && r < rows && at < group) ? __builtin_nontemporal_load(mine + at) : T(0), c = T(0);
+        row_pair_sum<T>(h, c);
         if (l == 0 && r < rows) {
             sh[w][r] = h;
-            sc[w][r] = finite_bits(h) ? c : 0.0;
+            sc[w][r] = finite_bits(h) ? c : T(0);
         }
     }
     __syncthreads();
     for (int off = 32; off > 0; off >>= 1) {
         const int lim = rows > off ? (off < rows - off ? off : rows - off) : 0;
-        double h = 0.0, c = 0.0;
+        T h = T(0), c = T(0);
         if (lane < lim) {
             h = sh[w][lane];
             c = sc[w][lane];
@@ -1785,6 +1788,33 @@ int rows_finish(const T* hi, const T* comp, int64_t rows, T* out, void* scratch,
     return launch_error("hawk_rows_levels launch");
 }
 
+// The keyed default-policy sum in T (hk_keyed_sample_sum_f64 / _f32).
+template <class T>
+int keyed_sample_sum(const T* u, int64_t n, int64_t group, T* out, void* stream, const char* name) {
+    const std::string who(name);
+    if (n < 0 || group <= 0)
+        return hawk_internal::set_error(HK_EVALUE, who + ": n must be >= 0 and group >= 1");
+    if (n % group != 0)
+        return hawk_internal::set_error(HK_EVALUE, who + ": n (" + std::to_string(n) +
+                                                       ") is not a whole number of groups of " + std::to_string(group));
+    if ((group + 31) / 32 > kRowLeaf * kKeyedCompLeaves)
+        return hawk_internal::set_error(HK_EVALUE, who + ": a key of " + std::to_string(group) +
+                                                       " samples spans more than 256 leaves of 4096 rows; sum it "
+                                                       "with policy='ordered'");
+    if (n == 0) return HK_OK;
+    if (!u || !out) return hawk_internal::set_error(HK_EVALUE, who + ": u and out are required");
+    const long long keys = n / group;
+    if (keys > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, who + ": too many keys");
+    if (group <= 64 * 32) {
+        hipLaunchKernelGGL(hawk_keyed_comp_wave<T>, dim3(static_cast<unsigned>((keys + 3) / 4)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), u, static_cast<long long>(group), keys, out);
+        return launch_error("hawk_keyed_comp_wave launch");
+    }
+    hipLaunchKernelGGL(hawk_keyed_comp<T>, dim3(static_cast<unsigned>(keys)), dim3(kRowSlots), 0,
+                       static_cast<hipStream_t>(stream), u, static_cast<long long>(group), out);
+    return launch_error("hawk_keyed_comp launch");
+}
+
 // The ordered scatter in T (hk_ordered_scatter_f64 / _f32).
 template <class T>
 int ordered_scatter(const int32_t* key, const T* v, int64_t n, T* target, int64_t cells, void* scratch,
@@ -1905,27 +1935,11 @@ int hk_keyed_ordered_sum_f32(const float* u, int64_t n, int64_t group, float* ou
 }
 
 int hk_keyed_sample_sum_f64(const double* u, int64_t n, int64_t group, double* out, void* stream) {
-    if (n < 0 || group <= 0)
-        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: n must be >= 0 and group >= 1");
-    if (n % group != 0)
-        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: n (" + std::to_string(n) +
-                                                       ") is not a whole number of groups of " + std::to_string(group));
-    if ((group + 31) / 32 > kRowLeaf * kKeyedCompLeaves)
-        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: a key of " + std::to_string(group) +
-                                                       " samples spans more than 256 leaves of 4096 rows; sum it "
-                                                       "with policy='ordered'");
-    if (n == 0) return HK_OK;
-    if (!u || !out) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: u and out are required");
-    const long long keys = n / group;
-    if (keys > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_sample_sum_f64: too many keys");
-    if (group <= 64 * 32) {
-        hipLaunchKernelGGL(hawk_keyed_comp_wave, dim3(static_cast<unsigned>((keys + 3) / 4)), dim3(256), 0,
-                           static_cast<hipStream_t>(stream), u, static_cast<long long>(group), keys, out);
-        return launch_error("hawk_keyed_comp_wave launch");
-    }
-    hipLaunchKernelGGL(hawk_keyed_comp, dim3(static_cast<unsigned>(keys)), dim3(kRowSlots), 0,
-                       static_cast<hipStream_t>(stream), u, static_cast<long long>(group), out);
-    return launch_error("hawk_keyed_comp launch");
+    return keyed_sample_sum<double>(u, n, group, out, stream, "hk_keyed_sample_sum_f64");
+}
+
+int hk_keyed_sample_sum_f32(const float* u, int64_t n, int64_t group, float* out, void* stream) {
+    return keyed_sample_sum<float>(u, n, group, out, stream, "hk_keyed_sample_sum_f32");
 }
 
 size_t hk_rows_finish_scratch_bytes(int64_t rows) {

@@ -1555,9 +1555,6 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
             team.append({"op": "band_rows" if banded else "row_sum", "hi": f"hk_rows_{s.name}",
                          "comp": f"hk_rows_{s.name}_comp", "out": s.name})
         elif isinstance(s, SampleSum):
-            if mode != "float64" and s.policy != "ordered":
-                raise HawkError(f"hawk.sum(x, over=...) with policy={s.policy!r} on the hip target is built in "
-                                "float64 (float32 builds hawk.sum over every sample and policy='ordered')")
             src = assigned.get(id(s.value))
             if src is None and s.value.kind == "leaf" and s.value.literal[0] == "per_sample":
                 src = s.value.literal[1]

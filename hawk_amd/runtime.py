@@ -534,7 +534,8 @@ class DeviceKernel:
                 _core.keyed_log_fold(*args, stream)
                 statuses.append((t, status, cells))
             elif t["op"] == "keyed_comp":
-                _core.keyed_sample_sum(bound[t["u"]].data_ptr(), n, t["group"], bound[t["out"]].data_ptr(), stream)
+                fn = _core.keyed_sample_sum_f32 if self._is_f32(t["out"]) else _core.keyed_sample_sum
+                fn(bound[t["u"]].data_ptr(), n, t["group"], bound[t["out"]].data_ptr(), stream)
             else:
                 raise HawkError(f"kernel {self.name!r}: unknown team stage {t['op']!r}")
         if check:
@@ -840,7 +841,8 @@ class Prepared:
                 self.statuses.append((t, status, cells))
             elif t["op"] == "keyed_comp":
                 args = (bound[t["u"]].data_ptr(), self.n, t["group"], bound[t["out"]].data_ptr())
-                self.steps.append((_core.keyed_sample_sum, args))
+                self.steps.append((_core.keyed_sample_sum_f32 if kernel._is_f32(t["out"]) else _core.keyed_sample_sum,
+                                   args))
             else:
                 raise HawkError(f"kernel {kernel.name!r}: unknown team stage {t['op']!r}")
 
@@ -876,7 +878,7 @@ class Prepared:
                   _core.ordered_scatter: "ordered_scatter", _core.ordered_scatter_f32: "ordered_scatter",
                   _core.mm16: "mm16", _core.mm16_f64: "mm16",
                   _core.keyed_ordered_sum: "keyed_sum", _core.keyed_ordered_sum_f32: "keyed_sum", _core.keyed_log_fold: "ordered_fold",
-                  _core.keyed_sample_sum: "keyed_comp"}
+                  _core.keyed_sample_sum: "keyed_comp", _core.keyed_sample_sum_f32: "keyed_comp"}
         for fn, args in self.steps:
             label = labels.get(fn, "row_sum")
             out.append((label, lambda fn=fn, args=args: fn(*args, self.stream)))

@@ -212,6 +212,9 @@ int hk_keyed_ordered_sum_f32(const float* u, int64_t n, int64_t group, float* ou
  * once a key spans three warps; here every key takes one fixed order.  A key
  * of more than 2^25 samples is refused (HK_EVALUE).  No scratch. */
 int hk_keyed_sample_sum_f64(const double* u, int64_t n, int64_t group, double* out, void* stream);
+/* The same in the float32 mode: float rows, float compensation, a float
+ * cell (the reference finishes a float32 build's rows in their dtype). */
+int hk_keyed_sample_sum_f32(const float* u, int64_t n, int64_t group, float* out, void* stream);
 
 /* The finish of a default-policy sample sum (`hawk.sum(x)`): `rows`
  * compensated (hi, comp) row pairs (one per 32 samples, written by the

@@ -209,7 +209,12 @@ def keyed_ordered_sum(u, group: int, threads: int = 1, profile: str = "portable"
 
 
 def keyed_sample_sum(u, group: int):
-    """One default-policy sample sum per run of ``group`` consecutive values."""
+    """One default-policy sample sum per run of ``group`` consecutive values
+    (each a float32 sample sum, in float32, for a float32 ``u``)."""
+    if getattr(u, "dtype", None) == np.float32:
+        u = np.ascontiguousarray(u)
+        assert u.size % group == 0
+        return np.array([sample_sum_f32(u[k * group:(k + 1) * group]) for k in range(u.size // group)], np.float32)
     u = np.ascontiguousarray(u, dtype=np.float64)
     assert u.size % group == 0
     out = np.empty(u.size // group)

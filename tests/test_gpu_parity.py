@@ -1532,3 +1532,23 @@ def test_float32_keyed_ordered_sum_bitwise(gpu, tmp_path, keys, group):
     out = dev(np.full(keys, np.nan, np.float32), gpu)
     hawk.run(kern, x=dev(x, gpu), out=out)
     assert host(out).tobytes() == O.keyed_ordered_sum(x, group).tobytes()
+
+
+@pytest.mark.parametrize("keys,group", [(4, 8), (1000, 40), (3, 4096 * 32 + 5), (5000, 1), (10, 100_000),
+                                        (777, 33), (50, 2049)])
+def test_float32_keyed_default_sum_is_the_oracle_bitwise(gpu, tmp_path, keys, group):
+    """The default policy over some axes in a float32 build: each key's run a
+    float32 default-policy sample sum of its own (float rows and compensation,
+    the canonical finish in float32), the float32 oracle's bits; one key is
+    the whole run's float32 default sum."""
+    import hawk_amd as hawk
+    hawk.build([_keyed_default_kernel(group)], tmp_path, mode="float32")
+    kern = hawk.load(tmp_path, "kdefault")
+    assert [t["op"] for t in kern.team] == ["keyed_comp"]
+    n = keys * group
+    x = (rng(keys + group + 32).normal(size=n) * np.exp(rng(3).normal(size=n))).astype(np.float32)
+    print(f"float32 keyed default sum keys={keys} group={group}", flush=True)
+    out = dev(np.full(keys, np.nan, np.float32), gpu)
+    hawk.run(kern, x=dev(x, gpu), out=out)
+    got = host(out)
+    assert got.dtype == np.float32 and got.tobytes() == O.keyed_sample_sum(x, group).tobytes()
