@@ -78,6 +78,7 @@ def _declare(lib) -> None:
         "hk_keyed_sample_sum_f64": (I, [V, I64, I64, V, V]),
         "hk_keyed_sample_sum_f32": (I, [V, I64, I64, V, V]),
         "hk_keyed_log_fold_f64": (I, [V, I64, V, I64, I64, ctypes.c_int32, V, I64, V, V, V]),
+        "hk_keyed_log_fold_f32": (I, [V, I64, V, I64, I64, ctypes.c_int32, V, I64, V, V, V]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -392,6 +393,15 @@ def keyed_log_fold(values: int, stride: int, cells_log: int, keys: int, rows: in
     (``values[e*stride + k*rows + r]``) added in lane order from +0; status[0]
     bit 0 = a cell outside ``[0, cells)``, bit 1 = a cell named twice."""
     check(lib().hk_keyed_log_fold_f64(ctypes.c_void_p(values or None), int(stride), ctypes.c_void_p(cells_log or None),
+                                      int(keys), int(rows), int(width), ctypes.c_void_p(out or None), int(cells),
+                                      ctypes.c_void_p(scratch or None), ctypes.c_void_p(status or None),
+                                      ctypes.c_void_p(stream or None)))
+
+
+def keyed_log_fold_f32(values: int, stride: int, cells_log: int, keys: int, rows: int, width: int, out: int,
+                       cells: int, scratch: int, status: int, stream: int = 0) -> None:
+    """:func:`keyed_log_fold` of float32 contributions into a float32 gradient plane."""
+    check(lib().hk_keyed_log_fold_f32(ctypes.c_void_p(values or None), int(stride), ctypes.c_void_p(cells_log or None),
                                       int(keys), int(rows), int(width), ctypes.c_void_p(out or None), int(cells),
                                       ctypes.c_void_p(scratch or None), ctypes.c_void_p(status or None),
                                       ctypes.c_void_p(stream or None)))

@@ -1567,7 +1567,8 @@ ScatterLayout scatter_layout(int64_t n, int64_t cells, int chunks) {
 // it (claims counts the pairs naming each cell): such stores race, as they do
 // in the reference, and the caller is told.
 
-__device__ __forceinline__ void log_fold_store(double s, int c, long long cells, double* __restrict__ out,
+template <class T>
+__device__ __forceinline__ void log_fold_store(T s, int c, long long cells, T* __restrict__ out,
                                                int* __restrict__ claims, int* __restrict__ status) {
     if (c < 0 || c >= cells) {
         atomicOr(status, 1);
@@ -1585,26 +1586,27 @@ __device__ __forceinline__ void log_fold_store(double s, int c, long long cells,
 // MI355X over 805 MB of log: 4.6 TB/s at 64 rows a run, against 4.0 with
 // batches of 8; staging the runs through LDS, or a wave reading whole lines,
 // did no better.
-__global__ __launch_bounds__(256) void hawk_log_fold_lanes(const double* __restrict__ v, long long stride,
+template <class T>
+__global__ __launch_bounds__(256) void hawk_log_fold_lanes(const T* __restrict__ v, long long stride,
                                                            const int* __restrict__ cell_of, long long keys,
                                                            long long rows, long long pairs,
-                                                           double* __restrict__ out, long long cells,
+                                                           T* __restrict__ out, long long cells,
                                                            int* __restrict__ claims, int* __restrict__ status) {
     const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     if (t >= pairs) return;
     const long long e = t / keys, k = t - e * keys;
-    const double* __restrict__ p = v + e * stride + k * rows;
-    double s = 0.0;
+    const T* __restrict__ p = v + e * stride + k * rows;
+    T s = T(0);
     long long r = 0;
     for (; r + 16 <= rows; r += 16) {
-        double x[16];
+        T x[16];
 #pragma unroll
         for (int q = 0; q < 16; ++q) x[q] = p[r + q];
 #pragma unroll
         for (int q = 0; q < 16; ++q) s = s + x[q];
     }
     if (r + 8 <= rows) {
-        double x[8];
+        T x[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) x[q] = p[r + q];
 #pragma unroll
@@ -1618,22 +1620,23 @@ __global__ __launch_bounds__(256) void hawk_log_fold_lanes(const double* __restr
 // One wave per pair, for long runs of few pairs: the wave loads 64 consecutive rows (one
 // 512-byte read) while it adds the previous 64 in lane order, every lane
 // holding the same running sum; lane 0 stores it.
-__global__ __launch_bounds__(256) void hawk_log_fold_waves(const double* __restrict__ v, long long stride,
+template <class T>
+__global__ __launch_bounds__(256) void hawk_log_fold_waves(const T* __restrict__ v, long long stride,
                                                            const int* __restrict__ cell_of, long long keys,
                                                            long long rows, long long pairs,
-                                                           double* __restrict__ out, long long cells,
+                                                           T* __restrict__ out, long long cells,
                                                            int* __restrict__ claims, int* __restrict__ status) {
     const long long pair = static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (pair >= pairs) return;                 // the whole wave
     const int lane = threadIdx.x & 63;
     const long long e = pair / keys, k = pair - e * keys;
-    const double* __restrict__ p = v + e * stride + k * rows;
-    double s = 0.0;
-    double x = lane < rows ? p[lane] : 0.0;
+    const T* __restrict__ p = v + e * stride + k * rows;
+    T s = T(0);
+    T x = lane < rows ? p[lane] : T(0);
     long long r0 = 0;
     for (; r0 + 64 <= rows; r0 += 64) {
-        const double cur = x;
-        x = r0 + 64 + lane < rows ? p[r0 + 64 + lane] : 0.0;
+        const T cur = x;
+        x = r0 + 64 + lane < rows ? p[r0 + 64 + lane] : T(0);
 #pragma unroll
         for (int j = 0; j < 64; ++j) s = s + lane_value(cur, j);
     }
@@ -1813,6 +1816,48 @@ int keyed_sample_sum(const T* u, int64_t n, int64_t group, T* out, void* stream,
     hipLaunchKernelGGL(hawk_keyed_comp<T>, dim3(static_cast<unsigned>(keys)), dim3(kRowSlots), 0,
                        static_cast<hipStream_t>(stream), u, static_cast<long long>(group), out);
     return launch_error("hawk_keyed_comp launch");
+}
+
+// The ordered gradient's log fold in T (hk_keyed_log_fold_f64 / _f32).
+template <class T>
+int keyed_log_fold(const T* values, int64_t stride, const int32_t* cells_log, int64_t keys, int64_t rows,
+                   int32_t width, T* out, int64_t cells, void* scratch, int32_t* status, void* stream,
+                   const char* name) {
+    const std::string who(name);
+    if (keys < 0 || rows < 1 || width < 1 || cells < 0)
+        return hawk_internal::set_error(HK_EVALUE, who + ": keys and cells must be >= 0, rows and width >= 1");
+    if (stride < keys * rows)
+        return hawk_internal::set_error(HK_EVALUE, who + ": stride (" + std::to_string(stride) +
+                                                       ") is shorter than keys * rows (" +
+                                                       std::to_string(keys * rows) + ")");
+    if (!status) return hawk_internal::set_error(HK_EVALUE, who + ": status is required");
+    const long long pairs = keys * static_cast<long long>(width);
+    if (pairs > 0 && (!values || !cells_log || !out || (cells > 0 && !scratch)))
+        return hawk_internal::set_error(HK_EVALUE,
+                                        who + ": values, cells_log, out and scratch are required");
+    if (cells > 0x7fffffffLL)
+        return hawk_internal::set_error(HK_EVALUE, who + ": more than 2^31-1 cells");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto* claims = static_cast<int*>(scratch);
+    const long long clear = (cells + 255) / 256 < 1 ? 1 : ((cells + 255) / 256 < 4096 ? (cells + 255) / 256 : 4096);
+    hipLaunchKernelGGL(hawk_log_fold_clear, dim3(static_cast<unsigned>(clear)), dim3(256), 0, s, claims,
+                       static_cast<long long>(cells), status);
+    int rc = launch_error("hawk_log_fold_clear launch");
+    if (rc != HK_OK || pairs == 0) return rc;
+    if (rows <= 64 || pairs >= 65536) {          // enough pairs for a thread each to fill the chip
+        const long long blocks = (pairs + 255) / 256;
+        if (blocks > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, who + ": too many pairs");
+        hipLaunchKernelGGL(hawk_log_fold_lanes<T>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, values,
+                           static_cast<long long>(stride), cells_log, static_cast<long long>(keys),
+                           static_cast<long long>(rows), pairs, out, static_cast<long long>(cells), claims, status);
+        return launch_error("hawk_log_fold_lanes launch");
+    }
+    const long long blocks = (pairs + 3) / 4;
+    if (blocks > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, who + ": too many pairs");
+    hipLaunchKernelGGL(hawk_log_fold_waves<T>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, values,
+                       static_cast<long long>(stride), cells_log, static_cast<long long>(keys),
+                       static_cast<long long>(rows), pairs, out, static_cast<long long>(cells), claims, status);
+    return launch_error("hawk_log_fold_waves launch");
 }
 
 // The ordered scatter in T (hk_ordered_scatter_f64 / _f32).
@@ -2024,41 +2069,15 @@ size_t hk_keyed_log_fold_scratch_bytes(int64_t cells) {
 int hk_keyed_log_fold_f64(const double* values, int64_t stride, const int32_t* cells_log, int64_t keys,
                           int64_t rows, int32_t width, double* out, int64_t cells, void* scratch,
                           int32_t* status, void* stream) {
-    if (keys < 0 || rows < 1 || width < 1 || cells < 0)
-        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: keys and cells must be >= 0, rows and "
-                                                   "width >= 1");
-    if (stride < keys * rows)
-        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: stride (" + std::to_string(stride) +
-                                                       ") is shorter than keys * rows (" +
-                                                       std::to_string(keys * rows) + ")");
-    if (!status) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: status is required");
-    const long long pairs = keys * static_cast<long long>(width);
-    if (pairs > 0 && (!values || !cells_log || !out || (cells > 0 && !scratch)))
-        return hawk_internal::set_error(HK_EVALUE,
-                                        "hk_keyed_log_fold_f64: values, cells_log, out and scratch are required");
-    if (cells > 0x7fffffffLL)
-        return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: more than 2^31-1 cells");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    auto* claims = static_cast<int*>(scratch);
-    const long long clear = (cells + 255) / 256 < 1 ? 1 : ((cells + 255) / 256 < 4096 ? (cells + 255) / 256 : 4096);
-    hipLaunchKernelGGL(hawk_log_fold_clear, dim3(static_cast<unsigned>(clear)), dim3(256), 0, s, claims,
-                       static_cast<long long>(cells), status);
-    int rc = launch_error("hawk_log_fold_clear launch");
-    if (rc != HK_OK || pairs == 0) return rc;
-    if (rows <= 64 || pairs >= 65536) {          // enough pairs for a thread each to fill the chip
-        const long long blocks = (pairs + 255) / 256;
-        if (blocks > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: too many pairs");
-        hipLaunchKernelGGL(hawk_log_fold_lanes, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, values,
-                           static_cast<long long>(stride), cells_log, static_cast<long long>(keys),
-                           static_cast<long long>(rows), pairs, out, static_cast<long long>(cells), claims, status);
-        return launch_error("hawk_log_fold_lanes launch");
-    }
-    const long long blocks = (pairs + 3) / 4;
-    if (blocks > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, "hk_keyed_log_fold_f64: too many pairs");
-    hipLaunchKernelGGL(hawk_log_fold_waves, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, values,
-                       static_cast<long long>(stride), cells_log, static_cast<long long>(keys),
-                       static_cast<long long>(rows), pairs, out, static_cast<long long>(cells), claims, status);
-    return launch_error("hawk_log_fold_waves launch");
+    return keyed_log_fold<double>(values, stride, cells_log, keys, rows, width, out, cells, scratch, status, stream,
+                                  "hk_keyed_log_fold_f64");
+}
+
+int hk_keyed_log_fold_f32(const float* values, int64_t stride, const int32_t* cells_log, int64_t keys,
+                          int64_t rows, int32_t width, float* out, int64_t cells, void* scratch,
+                          int32_t* status, void* stream) {
+    return keyed_log_fold<float>(values, stride, cells_log, keys, rows, width, out, cells, scratch, status, stream,
+                                 "hk_keyed_log_fold_f32");
 }
 
 }  // extern "C"

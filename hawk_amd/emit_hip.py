@@ -1044,7 +1044,7 @@ def _place_fold_stores(body: list, folds: list, block: int) -> list:
     for i, (_, _, values, _, g) in enumerate(folds):
         keys = block // g
         stride = keys * (g + 1)
-        decl += [f"        __shared__ double hk_fv{i}[{len(values) * stride}];",
+        decl += [f"        __shared__ Real hk_fv{i}[{len(values) * stride}];",
                  f"        __shared__ int hk_fc{i}[{len(values) * keys}];",
                  f"        const int hk_fk{i} = static_cast<int>(threadIdx.x) / {g};",
                  f"        const int hk_fr{i} = static_cast<int>(threadIdx.x) - hk_fk{i} * {g};"]
@@ -1098,7 +1098,7 @@ def _fused_fold_lines(folds: list, block: int, whole: bool = False) -> list:
         return _whole_fold_lines(folds, block)
     lds_v = max(_fold_chunk(g, block, len(v)) * (block // g) * (g + 1) for _, _, v, _, g in folds)
     lds_c = max(_fold_chunk(g, block, len(v)) * (block // g) for _, _, v, _, g in folds)
-    lines = [f"        __shared__ double hk_fv[{lds_v}];",
+    lines = [f"        __shared__ Real hk_fv[{lds_v}];",
              f"        __shared__ int hk_fc[{lds_c}];"]
     for out, scratch, values, cells, g in folds:
         keys = block // g
@@ -1121,8 +1121,8 @@ def _fused_fold_lines(folds: list, block: int, whole: bool = False) -> list:
                       f"                const int hk_fs = static_cast<int>(threadIdx.x) / {keys};",
                       f"                const int hk_fq = static_cast<int>(threadIdx.x) - hk_fs * {keys};",
                       f"                if (static_cast<long long>(hk_blk) * {block} + hk_fq * {g} < count) {{",
-                      f"                    const double* hk_fp = hk_fv + hk_fs * {stride} + hk_fq * {g + 1};",
-                      "                    double hk_fsum = 0.0;",
+                      f"                    const Real* hk_fp = hk_fv + hk_fs * {stride} + hk_fq * {g + 1};",
+                      "                    Real hk_fsum = Real(0);",
                       "                    #pragma unroll 8",
                       f"                    for (int hk_fj = 0; hk_fj < {g}; ++hk_fj) hk_fsum = hk_fsum + hk_fp[hk_fj];",
                       f"                    hk_fold_store(hk_fsum, hk_fc[hk_fs * {keys} + hk_fq], {out}_n, {out}, "
@@ -1287,8 +1287,8 @@ def _whole_fold_lines(folds: list, block: int) -> list:
                   f"            const int hk_fs = hk_ft / {keys};",
                   f"            const int hk_fq = hk_ft - hk_fs * {keys};",
                   f"            if (static_cast<long long>(hk_blk) * {block} + hk_fq * {g} < count) {{",
-                  f"                const double* hk_fp = hk_fv{i} + hk_fs * {stride} + hk_fq * {g + 1};",
-                  "                double hk_fsum = 0.0;",
+                  f"                const Real* hk_fp = hk_fv{i} + hk_fs * {stride} + hk_fq * {g + 1};",
+                  "                Real hk_fsum = Real(0);",
                   "                #pragma unroll 8",
                   f"                for (int hk_fj = 0; hk_fj < {g}; ++hk_fj) hk_fsum = hk_fsum + hk_fp[hk_fj];",
                   f"                hk_fold_store(hk_fsum, hk_fc{i}[hk_fs * {keys} + hk_fq], {out}_n, {out}, "
@@ -1301,7 +1301,7 @@ def _whole_fold_lines(folds: list, block: int) -> list:
 #: The store of a fused fold's sum: a cell outside the gradient plane sets
 #: status bit 0; a cell claimed twice sets bit 1 and lowers status[1] to it.
 _FOLD_HELPERS = """
-__device__ __forceinline__ void hk_fold_store(double s, int c, unsigned long long cells, double* out, int* claims,
+__device__ __forceinline__ void hk_fold_store(Real s, int c, unsigned long long cells, Real* out, int* claims,
                                               int* status) {
     if (c < 0 || static_cast<unsigned long long>(c) >= cells) { atomicOr(status, 1); return; }
     if (atomicAdd(claims + c, 1) != 0) { atomicOr(status, 2); atomicMin(status + 1, c); }
@@ -1532,8 +1532,6 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
     extra, team, row_sums, key_writes, fused = [], [], [], [], []
     for s in program.sinks:
         if isinstance(s, OrderedFold):
-            if mode != "float64":
-                raise HawkError("a table's gradient under an ordered keyed sum is built in float64")
             if fuse_folds and fold_block(s.group) is not None:
                 # the stage folds in LDS: its claims and status are cleared before it runs
                 scratch = f"hk_fold_{s.name}"

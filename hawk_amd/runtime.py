@@ -531,7 +531,7 @@ class DeviceKernel:
                 fn(bound[t["u"]].data_ptr(), n, t["group"], bound[t["out"]].data_ptr(), scratch.data_ptr(), stream)
             elif t["op"] == "ordered_fold":
                 args, status, cells = self._fold_args(t, bound, n, device)
-                _core.keyed_log_fold(*args, stream)
+                (_core.keyed_log_fold_f32 if self._is_f32(t["out"]) else _core.keyed_log_fold)(*args, stream)
                 statuses.append((t, status, cells))
             elif t["op"] == "keyed_comp":
                 fn = _core.keyed_sample_sum_f32 if self._is_f32(t["out"]) else _core.keyed_sample_sum
@@ -837,7 +837,8 @@ class Prepared:
                                    args))
             elif t["op"] == "ordered_fold":
                 args, status, cells = kernel._fold_args(t, bound, self.n, device)
-                self.steps.append((_core.keyed_log_fold, args))
+                self.steps.append((_core.keyed_log_fold_f32 if kernel._is_f32(t["out"]) else _core.keyed_log_fold,
+                                   args))
                 self.statuses.append((t, status, cells))
             elif t["op"] == "keyed_comp":
                 args = (bound[t["u"]].data_ptr(), self.n, t["group"], bound[t["out"]].data_ptr())
@@ -877,7 +878,7 @@ class Prepared:
                   _core.band_ordered_sum: "band_ordered_sum",
                   _core.ordered_scatter: "ordered_scatter", _core.ordered_scatter_f32: "ordered_scatter",
                   _core.mm16: "mm16", _core.mm16_f64: "mm16",
-                  _core.keyed_ordered_sum: "keyed_sum", _core.keyed_ordered_sum_f32: "keyed_sum", _core.keyed_log_fold: "ordered_fold",
+                  _core.keyed_ordered_sum: "keyed_sum", _core.keyed_ordered_sum_f32: "keyed_sum", _core.keyed_log_fold: "ordered_fold", _core.keyed_log_fold_f32: "ordered_fold",
                   _core.keyed_sample_sum: "keyed_comp", _core.keyed_sample_sum_f32: "keyed_comp"}
         for fn, args in self.steps:
             label = labels.get(fn, "row_sum")

@@ -301,6 +301,11 @@ size_t hk_keyed_log_fold_scratch_bytes(int64_t cells);
 int hk_keyed_log_fold_f64(const double* values, int64_t stride, const int32_t* cells_log,
                           int64_t keys, int64_t rows, int32_t width, double* out,
                           int64_t cells, void* scratch, int32_t* status, void* stream);
+/* The same fold in the float32 mode (float contributions, sums and gradient
+ * plane), with the same scratch, status words and refusals. */
+int hk_keyed_log_fold_f32(const float* values, int64_t stride, const int32_t* cells_log, int64_t keys,
+                          int64_t rows, int32_t width, float* out, int64_t cells, void* scratch,
+                          int32_t* status, void* stream);
 
 /* Per-sample 16x16 fp32 matrix products on MFMA: for every sample s < n and
  * product o < n_out, out[o] = op(in[lhs]) @ op(in[rhs]) with

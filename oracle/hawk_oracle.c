@@ -573,6 +573,23 @@ HKO_EXPORT int hko_keyed_log_fold(const double* values, int64_t stride, const in
     return bad;
 }
 
+/* The same fold in the float32 mode: each key's run added in float from +0. */
+HKO_EXPORT int hko_keyed_log_fold_f32(const float* values, int64_t stride, const int32_t* cells_log, int64_t keys,
+                                      int64_t rows, int32_t width, float* out, int64_t cells) {
+    int bad = 0;
+    for (int32_t e = 0; e < width; ++e) {
+        for (int64_t k = 0; k < keys; ++k) {
+            const float* p = values + (int64_t)e * stride + k * rows;
+            float s = 0.0f;
+            for (int64_t r = 0; r < rows; ++r) s += p[r];
+            const int32_t c = cells_log[(int64_t)e * keys + k];
+            if (c < 0 || c >= cells) bad = 1;
+            else out[c] = s;
+        }
+    }
+    return bad;
+}
+
 /* ---- hawk.chain: four members passing values by name ----------------------
  * Reference hawk/trace/chain.py (and its tests/test_chain.py fixture): a =
  * (sin x, cos x, x*0.5); b = exp(-((a0*a0 + a1*a1) + a2*a2)) + x;

@@ -63,6 +63,7 @@ def lib(profile: str | None = None):
         "hko_keyed_ordered_sum": (None, [_P, _I64, _I64, _P]),
         "hko_keyed_ordered_sum_threads": (None, [_P, _I64, _I64, _P, ctypes.c_int]),
         "hko_keyed_log_fold": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, ctypes.c_int32, _P, _I64]),
+        "hko_keyed_log_fold_f32": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, ctypes.c_int32, _P, _I64]),
         "hko_keyed_sample_sum": (None, [_P, _I64, _I64, _P]),
         "hko_net_threads": (None, [ctypes.c_int, _P, _P, _P, _P, _P, _I64, _I64, _P, ctypes.c_int]),
         "hko_chain_members_threads": (None, [_P, _P, _P, _I64, ctypes.c_int]),
@@ -225,7 +226,14 @@ def keyed_sample_sum(u, group: int):
 def keyed_log_fold(values, cells_log, rows: int, out):
     """The ordered gradient's fold into ``out`` (in place): ``values`` is
     ``[width, keys * rows]``, ``cells_log`` ``[width, keys]``; returns 1 when a
-    cell was outside ``out``."""
+    cell was outside ``out``.  Float32 ``values`` and ``out`` fold in float32."""
+    if getattr(values, "dtype", None) == np.float32:
+        values = np.ascontiguousarray(values)
+        cells_log = np.ascontiguousarray(cells_log, dtype=np.int32)
+        width, keys = cells_log.shape
+        assert values.shape == (width, keys * rows) and out.dtype == np.float32 and out.flags.c_contiguous
+        return lib().hko_keyed_log_fold_f32(_p(values), keys * rows, _p(cells_log), keys, rows, width, _p(out),
+                                            out.size)
     values = np.ascontiguousarray(values, dtype=np.float64)
     cells_log = np.ascontiguousarray(cells_log, dtype=np.int32)
     width, keys = cells_log.shape

@@ -1008,8 +1008,8 @@ def test_table_reads_and_derivatives_on_the_device(gpu, tmp_path):
 # -- the ordered gradient's log fold ----------------------------------------------
 
 def _log_fold(gpu, v, c, rows, init):
-    """Run hk_keyed_log_fold_f64 on copies of ``v``, ``c`` and ``init``; return
-    (out, status) on the host."""
+    """Run hk_keyed_log_fold_f64 (hk_keyed_log_fold_f32 for float32 ``v``) on
+    copies of ``v``, ``c`` and ``init``; return (out, status) on the host."""
     import torch
     from hawk_amd import _core
     width, keys = c.shape
@@ -1017,8 +1017,9 @@ def _log_fold(gpu, v, c, rows, init):
     V, C, out = dev(v, gpu), dev(c, gpu), dev(init, gpu)
     scratch = torch.empty(max(1, _core.keyed_log_fold_scratch_bytes(cells)), dtype=torch.uint8, device=gpu)
     status = torch.empty(2, dtype=torch.int32, device=gpu)
-    _core.keyed_log_fold(V.data_ptr(), keys * rows, C.data_ptr(), keys, rows, width, out.data_ptr(), cells,
-                         scratch.data_ptr(), status.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    fold = _core.keyed_log_fold_f32 if v.dtype == np.float32 else _core.keyed_log_fold
+    fold(V.data_ptr(), keys * rows, C.data_ptr(), keys, rows, width, out.data_ptr(), cells,
+         scratch.data_ptr(), status.data_ptr(), torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     return host(out), host(status).tolist()
 
@@ -1552,3 +1553,54 @@ def test_float32_keyed_default_sum_is_the_oracle_bitwise(gpu, tmp_path, keys, gr
     hawk.run(kern, x=dev(x, gpu), out=out)
     got = host(out)
     assert got.dtype == np.float32 and got.tobytes() == O.keyed_sample_sum(x, group).tobytes()
+
+
+@pytest.mark.parametrize("keys,rows,width", [(1000, 1, 3), (5000, 40, 24), (300, 65, 5), (3, 5000, 2),
+                                             (70000, 72, 1)])
+def test_float32_keyed_log_fold_is_the_oracle_bitwise(gpu, keys, rows, width):
+    """The float32 fold through the C-ABI, on both of its forms (a thread a
+    pair, a wave a pair): each run added in float from +0 in lane order, the
+    float32 oracle's bits; cells no pair names keep their values."""
+    g = rng(keys + 7 * rows + 31 * width + 32)
+    v = (g.normal(size=(width, keys * rows)) * np.exp(3 * g.normal(size=(width, keys * rows)))).astype(np.float32)
+    cells = keys * width + 13
+    c = g.permutation(cells)[:keys * width].reshape(width, keys).astype(np.int32)
+    init = g.normal(size=cells).astype(np.float32)
+    want = init.copy()
+    assert O.keyed_log_fold(v, c, rows, want) == 0
+    print(f"float32 log fold keys={keys} rows={rows} width={width}", flush=True)
+    out, status = _log_fold(gpu, v, c, rows, init)
+    assert out.dtype == np.float32 and out.tobytes() == want.tobytes()
+    assert status == [0, 2 ** 31 - 1]
+
+
+@pytest.mark.parametrize("keys,group", [(1000, 40), (777, 64), (3001, 5), (300, 100), (9, 2000)])
+def test_float32_ordered_fold_in_lds_and_through_a_log(gpu, tmp_path, keys, group):
+    """The gradient wrt a per-key table under an ordered keyed sum in a
+    float32 build, folded in the stage's LDS (groups 40, 64, 5) and through
+    the log and the fold stage (100, 2000).  Integer inputs keep every
+    product and sum exact in float32, so the float32 gradient equals the
+    IR's contributions folded exactly."""
+    import hawk_amd as hawk
+    from hawk_amd.diff import vjp
+    from hawk_amd.emit_hip import fold_block
+    from hawk_amd.trace import Kernel
+    from ir_eval import evaluate
+    back = Kernel("kt_vjp", vjp(_keyed_table_kernel(group), wrt=("t",)))
+    hawk.build([back], tmp_path, mode="float32")
+    kern = hawk.load(tmp_path, "kt_vjp")
+    assert kern.team[0]["op"] == ("fused_fold" if fold_block(group) else "ordered_fold")
+    n = keys * group
+    g = rng(keys + group + 32)
+    t = g.integers(-4, 5, keys * 3).astype(np.float32)
+    x = g.integers(-8, 9, n).astype(np.float32)
+    bar = g.integers(-4, 5, keys).astype(np.float32)
+    bt = dev(np.full(keys * 3, np.nan, np.float32), gpu)
+    print(f"float32 fold keys={keys} group={group} {kern.team[0]['op']}", flush=True)
+    hawk.run(kern, t=dev(t, gpu), x=dev(x, gpu), bar_out=dev(bar, gpu), bar_t=bt)
+    values, cells = evaluate(back.program, {"t": t.astype(np.float64), "x": x.astype(np.float64),
+                                            "bar_out": bar.astype(np.float64)}, n)["bar_t"]
+    want = np.full(keys * 3, np.nan)
+    assert O.keyed_log_fold(np.stack(values), np.stack([c[::group] for c in cells]), group, want) == 0
+    assert (np.abs(want) < 2.0 ** 24).all()                       # exact in float32
+    assert host(bt).tobytes() == want.astype(np.float32).tobytes()

@@ -814,3 +814,26 @@ def test_float32_ordered_scatter_is_the_serial_chunk_walk():
     np.add.at(exact, ki, xi.astype(np.float64))
     got, _ = O.ordered_scatter(ki, xi, np.zeros(300, np.float32))
     assert (got.astype(np.float64) == exact).all()
+
+
+def test_float32_keyed_log_fold_is_each_runs_float32_walk():
+    """The float32 fold: each (slot, key) run added in np.float32 from 0 in
+    lane order and stored at its cell; a cell outside the plane is reported
+    and not stored."""
+    g = np.random.default_rng(44)
+    keys, rows, width = 30, 17, 3
+    v = g.normal(size=(width, keys * rows)).astype(np.float32)
+    cells = keys * width + 5
+    c = g.permutation(cells)[:keys * width].reshape(width, keys).astype(np.int32)
+    out = np.full(cells, 7.0, np.float32)
+    assert O.keyed_log_fold(v, c, rows, out) == 0
+    want = np.full(cells, 7.0, np.float32)
+    for e in range(width):
+        for k in range(keys):
+            s = np.float32(0.0)
+            for r in range(rows):
+                s = np.float32(s + v[e, k * rows + r])
+            want[c[e, k]] = s
+    assert out.tobytes() == want.tobytes()
+    c[1, 4] = cells + 3
+    assert O.keyed_log_fold(v, c, rows, np.zeros(cells, np.float32)) == 1
