@@ -18,6 +18,7 @@ from dataclasses import dataclass
 from pathlib import Path
 
 from . import compile as _compile
+from . import policy as _policy
 from .emit_hip import fp_ops_per_sample
 from .resources import kernel_resources
 from .emit_hip import plan_kernel
@@ -138,9 +139,77 @@ def _cut_chains(kernels, mode: str, register_line: int | None, target) -> tuple:
     return out, chains
 
 
+#: The reference's build options and the values it accepts
+#: (reference hawk/emit/policy.py FORMS / LINALG_FORMS / WIDE_FORMS,
+#: hawk/compile/toolchain.py:625 and :928).
+EMIT_FORMS = _policy.FORMS
+LINALG_FORMS = _policy.LINALG_FORMS
+WIDE_FORMS = _policy.WIDE_FORMS
+HOST_PROFILES = ("native", "portable", "native-vector-math", "native-vector-math-nofma")
+OPT_LEVELS = ("O0", "O1", "O2", "O3")
+
+
+def _reference_options(kind, layout_sizes_override, defines, device_arch, host_profile, opt_level,
+                       literal_table, embedded_profile, emit_form, linalg_form, wide_form,
+                       launch_bounds) -> tuple:
+    """Check the reference's build options (reference
+    hawk/artifact/bundle.py:1349-1420) and return ``(compile options, block
+    fixed by launch_bounds or None, what the sidecar records)``.  The forms
+    choose how the reference spells a site; this target's stages add in the
+    order they are written whatever the spelling, so they are checked and
+    recorded.  ``opt_level`` and ``defines`` reach hipRTC; ``launch_bounds``
+    fixes the block as the reference's ``launch.block = threads`` does."""
+    if kind is not None:
+        raise HawkError("kind=: an execution kind (hawk.ext lanes or an active-set guard) has no hip form in this "
+                        "build")
+    if layout_sizes_override is not None:
+        raise HawkError("layout_sizes_override= is the reference host build's test-only door; the hip target's "
+                        "mirror sizes are the library's (hk_layout_sizes)")
+    if embedded_profile is not None:
+        raise HawkError("embedded_profile= belongs to the reference's MISRA C target, which this build does not have")
+    if device_arch not in ("", "gfx950"):
+        raise HawkError(f"device_arch={device_arch!r}: the hip target builds gfx950")
+    for what, value, allowed in (("emit_form", emit_form, EMIT_FORMS), ("linalg_form", linalg_form, LINALG_FORMS),
+                                 ("wide_form", wide_form, WIDE_FORMS)):
+        if value is not None and value not in allowed:
+            raise HawkError(f"{what} must be one of {allowed}, got {value!r}")
+    if host_profile and host_profile not in HOST_PROFILES:
+        raise HawkError(f"host_profile must be one of {HOST_PROFILES}, got {host_profile!r}")
+    if opt_level and opt_level not in OPT_LEVELS:
+        raise HawkError(f"opt_level must be one of {OPT_LEVELS}, got {opt_level!r}")
+    block = None
+    launch_bounds = _policy.check_launch_bounds(launch_bounds)
+    if launch_bounds is not None:
+        threads, blocks = launch_bounds
+        if threads % 64 or threads > 1024:
+            raise HawkError(f"launch_bounds={launch_bounds!r}: gfx950 runs wave64 workgroups of at most 1024 "
+                            "threads, so threads must be a multiple of 64 up to 1024")
+        block = int(threads)
+    options = list(_compile.RTC_OPTIONS)
+    if opt_level:
+        options = [f"-{opt_level}" if o.startswith("-O") else o for o in options]
+    for d in defines or ():
+        d = str(d)
+        if not d or d.startswith("-") or any(c.isspace() for c in d):
+            raise HawkError(f"defines: {d!r} is not NAME or NAME=VALUE")
+        options.append(f"-D{d}")
+    contraction = _policy.contraction()
+    record = {k: v for k, v in (("emit_form", emit_form), ("linalg_form", linalg_form), ("wide_form", wide_form),
+                                ("contraction", contraction if contraction != "direct" else None),
+                                ("launch_bounds", list(launch_bounds) if launch_bounds else None),
+                                ("host_profile", host_profile or None), ("opt_level", opt_level or None),
+                                ("literal_table", bool(literal_table) or None),
+                                ("defines", [str(d) for d in defines] if defines else None)) if v is not None}
+    return tuple(options), block, record
+
+
 def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64", cache_dir=None,
                  block: int | None = None, per_thread: int | None = None, nontemporal: bool = True,
-                 fuse_folds: bool = True, register_line: int | None = None) -> Bundle:
+                 fuse_folds: bool = True, register_line: int | None = None, kind=None,
+                 layout_sizes_override=None, defines=(), device_arch: str = "", name: str | None = None,
+                 derivative=None, host_profile: str = "", opt_level: str = "", literal_table: bool = False,
+                 embedded_profile=None, emit_form: str | None = None, linalg_form: str | None = None,
+                 wide_form: str | None = None, launch_bounds=None) -> Bundle:
     """Build ``kernels`` (a Kernel or a list of them) into ``directory``.
     ``block`` / ``per_thread`` fix every stage's launch shape; left ``None``
     each stage gets :func:`launch_shape`'s.  A stage that folds an ordered
@@ -148,9 +217,25 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
     (``fuse_folds=False`` logs and folds in a team stage instead).  A
     ``hawk.chain`` is cut where its fused estimate passes ``register_line``
     VGPRs (default: the spill line, 512): its segments build as kernels of
-    their own and its sidecar lists them in order."""
+    their own and its sidecar lists them in order.  The reference's own
+    options (``emit_form`` ... ``launch_bounds``, ``name``, ``derivative``)
+    are taken as :func:`_reference_options` describes."""
     if isinstance(kernels, Kernel):
         kernels = [kernels]
+    # an option left unset is the ambient hawk_amd.policy.using value (reference
+    # hawk/artifact/bundle.py:1359-1360: an explicit argument wins)
+    ambient = _policy.form(), _policy.linalg_form(), _policy.wide_form(), _policy.launch_bounds()
+    emit_form = emit_form if emit_form is not None else (ambient[0] if ambient[0] != "auto" else None)
+    linalg_form = linalg_form if linalg_form is not None else (ambient[1] if ambient[1] != "auto" else None)
+    wide_form = wide_form if wide_form is not None else (ambient[2] if ambient[2] != "auto" else None)
+    launch_bounds = launch_bounds if launch_bounds is not None else ambient[3]
+    options, bounds_block, recorded = _reference_options(
+        kind, layout_sizes_override, defines, device_arch, host_profile, opt_level, literal_table,
+        embedded_profile, emit_form, linalg_form, wide_form, launch_bounds)
+    if block is None and bounds_block is not None:
+        block = bounds_block
+    if derivative is not None and not isinstance(derivative, dict):
+        raise HawkError("derivative= maps kernel names to their primal's name (or (name, unit digest))")
     targets = tuple(targets)
     bad = [t for t in targets if t not in TARGETS]
     if bad:
@@ -184,7 +269,8 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
         plans.append((k, plan, shape))
     staged = [(k, p) for k, p, _ in plans if p.stage is not None]
     compiled = dict(zip([k.name for k, _ in staged],
-                        _compile.compile_units([(k.name, p.source) for k, p in staged], cache_dir=cache_dir)))
+                        _compile.compile_units([(k.name, p.source) for k, p in staged], options=options,
+                                               cache_dir=cache_dir)))
     for k, plan, shape in plans:
         sidecar = {
             "kernel": k.name, "target": target.id, "offload_arch": target.offload_arch, "mode": mode,
@@ -206,7 +292,7 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
                 "format": target.format, "entry_kind": target.entry,
                 "source_sha256": hashlib.sha256(plan.source.encode()).hexdigest(),
                 "code_sha256": hashlib.sha256(code).hexdigest(),
-                "cache_key": key, "compile_options": list(_compile.RTC_OPTIONS),
+                "cache_key": key, "compile_options": list(options),
                 "toolchain": _compile.toolchain(),
                 "resources": kernel_resources(code).get(k.name, {}),
                 # the program's ops as traced (the algorithmic count), and what
@@ -226,6 +312,10 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
                 sidecar["fast_entries"] = {"range": f"{k.name}_range", "persist": f"{k.name}_persist"}
         if getattr(k, "members", None) is not None:
             _chain_record(k, sidecar, mode)
+        if recorded:
+            sidecar["build_options"] = recorded
+        if derivative and k.name in derivative:
+            sidecar["primal"] = derivative[k.name] if isinstance(derivative[k.name], str) else list(derivative[k.name])
         _write(directory / f"{k.name}.json", json.dumps(sidecar, indent=1, sort_keys=True).encode())
         artifacts.append(Artifact(k.name, sidecar))
     for name, sidecar in chains.items():
@@ -239,5 +329,7 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
     digest = hashlib.sha256(json.dumps([a.sidecar for a in artifacts], sort_keys=True).encode()).hexdigest()
     manifest = {"target": target.id, "offload_arch": target.offload_arch, "mode": mode, "digest": digest,
                 "kernels": [a.name for a in artifacts]}
+    if name is not None:
+        manifest["name"] = str(name)
     _write(directory / "manifest.json", json.dumps(manifest, indent=1, sort_keys=True).encode())
     return Bundle(directory, artifacts, digest)

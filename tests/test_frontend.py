@@ -1024,3 +1024,63 @@ def test_a_damaged_cache_entry_is_rebuilt_not_loaded(tmp_path, damage):
     again, key2, hit = C.compile_source(src, "energy", cache_dir=cache)
     assert not hit and key2 == key and again == code       # rebuilt, the same code object
     assert obj.read_bytes() == code and C.compile_source(src, "energy", cache_dir=cache)[2]
+
+
+def test_the_references_build_options_are_taken(tmp_path):
+    """hawk.build accepts the reference's options (reference
+    hawk/artifact/bundle.py:1349-1420): launch_bounds fixes the block,
+    opt_level and defines reach hipRTC, the forms and the rest are recorded,
+    name goes into the manifest and derivative names a kernel's primal."""
+    import json
+    b = hawk.build([E.scale, E.energy], tmp_path, emit_form="static", linalg_form="team", wide_form="thread",
+                   launch_bounds=(128, 2), opt_level="O2", defines=("HAWK_PROBE=1",), name="unit",
+                   derivative={"energy": "scale"}, host_profile="native", literal_table=True)
+    sc = b.sidecar("scale")
+    assert sc["launch"]["block"] == 128
+    assert "-O2" in sc["compile_options"] and "-O3" not in sc["compile_options"]
+    assert "-DHAWK_PROBE=1" in sc["compile_options"]
+    assert sc["build_options"] == {"emit_form": "static", "linalg_form": "team", "wide_form": "thread",
+                                   "launch_bounds": [128, 2], "host_profile": "native", "opt_level": "O2",
+                                   "literal_table": True, "defines": ["HAWK_PROBE=1"]}
+    assert b.sidecar("energy")["primal"] == "scale" and "primal" not in sc
+    assert json.loads((tmp_path / "manifest.json").read_text())["name"] == "unit"
+    plain = hawk.build([E.scale], tmp_path / "plain")
+    assert "build_options" not in plain.sidecar("scale") and "-O3" in plain.sidecar("scale")["compile_options"]
+
+
+@pytest.mark.parametrize("kw, says", [
+    ({"kind": object()}, "execution kind"),
+    ({"layout_sizes_override": [40, 32, 32, 8, 24]}, "test-only door"),
+    ({"embedded_profile": object()}, "MISRA C"),
+    ({"device_arch": "sm_90"}, "builds gfx950"),
+    ({"emit_form": "unrolled"}, "emit_form must be one of"),
+    ({"linalg_form": "warp"}, "linalg_form must be one of"),
+    ({"wide_form": "lane"}, "wide_form must be one of"),
+    ({"opt_level": "O4"}, "opt_level must be one of"),
+    ({"host_profile": "fast"}, "host_profile must be one of"),
+    ({"launch_bounds": (96, 2)}, "multiple of 64"),
+    ({"launch_bounds": (1024, 4)}, "threads*blocks <= 2048"),
+    ({"defines": ("-O0",)}, "NAME or NAME=VALUE"),
+])
+def test_the_references_build_options_are_refused_by_name(tmp_path, kw, says):
+    import re
+    with pytest.raises(hawk.HawkError, match=re.escape(says)):
+        hawk.build([E.scale], tmp_path, **kw)
+
+
+def test_ambient_options_reach_the_build_and_an_explicit_one_wins(tmp_path):
+    """reference tests/test_ambient_policy.py:26-32: launch_bounds from
+    policy.using reaches a build inside the block, an explicit argument wins,
+    and a build outside the block has none; contraction is recorded."""
+    from hawk_amd import policy
+    with policy.using(launch_bounds=(128, 2), contraction="gemm", form="rolled"):
+        amb = hawk.build([E.scale], tmp_path / "a").sidecar("scale")
+        exp = hawk.build([E.scale], tmp_path / "b", launch_bounds=(64, 4)).sidecar("scale")
+    plain = hawk.build([E.scale], tmp_path / "c").sidecar("scale")
+    assert amb["launch"]["block"] == 128 and amb["build_options"]["launch_bounds"] == [128, 2]
+    assert amb["build_options"]["contraction"] == "gemm" and amb["build_options"]["emit_form"] == "rolled"
+    assert exp["launch"]["block"] == 64 and exp["build_options"]["launch_bounds"] == [64, 4]
+    assert "build_options" not in plain and plain["launch"]["block"] == 256     # scale's own shape
+    with pytest.raises(hawk.HawkError, match="contraction must be one of"):
+        with policy.using(contraction="blas"):
+            pass
