@@ -38,8 +38,11 @@ _LAZY = {
     "build": ("artifact", "build_bundle"),
     "load": ("runtime", "load"),
     "run": ("runtime", "run"),
+    "samples_first": ("layout", "samples_first"),
+    "samples_last": ("layout", "samples_last"),
 }
-_SUBMODULES = ("math", "diff", "runtime", "artifact", "compile", "ir", "emit_hip", "trace", "chaining")
+_SUBMODULES = ("math", "diff", "runtime", "artifact", "compile", "ir", "emit_hip", "trace", "chaining", "policy",
+               "layout", "latency")
 
 __all__ = ["Grid", "HawkError", "Index", "Matrix", "Mutable", "Param", "Scalar", "Table", "TensorType", "Terminated",
            "Vector",

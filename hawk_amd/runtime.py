@@ -34,6 +34,8 @@ def _bound_length(role: str, x, n: int) -> int:
 
 
 _PER_SAMPLE = ("per_sample", "vec_in", "mat_in", "mutable", "out", "wide_out", "terminated")
+#: The per-sample roles a launch writes.
+_WRITTEN = ("mutable", "out", "wide_out", "terminated")
 
 #: The finish counter (reference ``hawk/ir/nodes.py:839``): one cell a
 #: finishing kernel adds its newly finished samples to.  The caller may bind
@@ -683,8 +685,8 @@ class _nullcontext:
 
 
 def run(kernel: DeviceKernel, *, base: int = 0, count: int | None = None, n_samples: int | None = None,
-        stream=None, check: bool = True, steps=None, entry: str = "plain", chunk: int = PERSIST_CHUNK,
-        **arrays) -> None:
+        layout: str | None = None, stream=None, check: bool = True, steps=None, entry: str = "plain",
+        chunk: int = PERSIST_CHUNK, **arrays) -> None:
     """Bind ``arrays`` and run the kernel once, in place, on the current HIP
     stream (or ``stream``).  ``count`` defaults to every sample from ``base``.
     A kernel with team stages (``hawk.sum`` / ``hawk.scatter`` with
@@ -696,16 +698,27 @@ def run(kernel: DeviceKernel, *, base: int = 0, count: int | None = None, n_samp
     trips between claims, default :data:`PERSIST_CHUNK`).  Both give the
     plain entry's bits, count samples finished on entry too (the counter then
     holds the batch's finished count), and leave the largest and the total
-    trips run in the kernel's ``steps_max`` and ``steps_sum``."""
+    trips run in the kernel's ``steps_max`` and ``steps_sum``.
+
+    ``layout`` (``"samples_first"`` / ``"samples_last"``) and the markers
+    :func:`hawk_amd.samples_first` / :func:`~hawk_amd.samples_last` say which
+    axis of a per-sample plane holds the samples (:mod:`hawk_amd.layout`)."""
+    from . import layout as _layout
     torch = _torch()
     if isinstance(kernel, ChainedKernel):
         if base != 0 or count is not None:
             raise HawkError(f"{kernel.name}: a cut chain runs over every sample (no base= or count=)")
         for seg, planes in kernel._bindings(dict(arrays), n_samples):
-            run(seg, n_samples=n_samples, stream=stream, check=check, **planes)
+            run(seg, n_samples=n_samples, layout=layout, stream=stream, check=check, **planes)
         return
     if not isinstance(kernel, DeviceKernel):
         raise HawkError("hawk.run takes a kernel loaded with hawk.load")
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    elif hasattr(stream, "cuda_stream"):
+        stream = stream.cuda_stream
+    with _on(int(stream)):
+        arrays, write_back = _layout.resolve(kernel, arrays, layout, _PER_SAMPLE, _WRITTEN)
     n = kernel.check_planes(arrays, n_samples)
     if kernel.team and (base != 0 or count not in (None, n)):
         raise HawkError(f"{kernel.name}: this kernel reduces over every sample, so it runs over every "
@@ -714,13 +727,13 @@ def run(kernel: DeviceKernel, *, base: int = 0, count: int | None = None, n_samp
         count = n - base
     if base < 0 or count < 0 or base + count > n:
         raise HawkError(f"{kernel.name}: [base, base+count) = [{base}, {base + count}) is outside [0, {n})")
-    if stream is None:
-        stream = torch.cuda.current_stream().cuda_stream
-    elif hasattr(stream, "cuda_stream"):
-        stream = stream.cuda_stream
     with kernel._lock:
         kernel._run(arrays, int(base), int(count), int(n), int(stream), check, steps=steps, entry=entry,
                     chunk=chunk)
+    if write_back:
+        with _on(int(stream)):
+            for dst, copy in write_back:       # a sample-major plane the kernel wrote
+                dst.copy_(copy.movedim(-1, 0))
 
 
 class Prepared:
@@ -738,8 +751,13 @@ class Prepared:
 
     def __init__(self, kernel: DeviceKernel, arrays: dict, stream=None, steps=None, entry: str = "plain",
                  chunk: int = PERSIST_CHUNK):
+        from .layout import Marked
         torch = _torch()
         self.kernel = kernel
+        marked = [name for name, x in arrays.items() if isinstance(x, Marked)]
+        if marked:
+            raise HawkError(f"{kernel.name}: prepare binds planes by address, so it takes component-major (w, N) "
+                            f"planes only; {marked} are marked (hawk.run takes a sample-major plane through a copy)")
         self.n = kernel.check_planes(arrays)
         self.arrays = dict(arrays)
         if stream is None:

@@ -522,10 +522,12 @@ def test_mm16_f64_forward_and_vjp_on_mfma(unit, gpu, n):
     ints = [g.integers(-8, 9, size=(16, 16, n)).astype(np.float64) for _ in range(3)]
     normals = [g.normal(0.0, 0.25, size=(16, 16, n)) for _ in range(3)]
     for exact, (A, B, bar_C) in ((True, ints), (False, normals)):
+        # n = 16 makes (16, 16, n) read both ways: the call says the samples are last
         C = dev(np.zeros((16, 16, n)), gpu)
-        hawk.run(_load(unit, "mm16"), A=dev(A, gpu), B=dev(B, gpu), C=C)
+        hawk.run(_load(unit, "mm16"), A=dev(A, gpu), B=dev(B, gpu), C=C, layout="samples_last")
         bA, bB = dev(np.zeros((16, 16, n)), gpu), dev(np.zeros((16, 16, n)), gpu)
-        hawk.run(_load(unit, "mm16_vjp"), A=dev(A, gpu), B=dev(B, gpu), bar_C=dev(bar_C, gpu), bar_A=bA, bar_B=bB)
+        hawk.run(_load(unit, "mm16_vjp"), A=dev(A, gpu), B=dev(B, gpu), bar_C=dev(bar_C, gpu), bar_A=bA, bar_B=bB,
+                 layout="samples_last")
         got = [host(C), host(bA), host(bB)]
         Bt, At = B.transpose(1, 0, 2), A.transpose(1, 0, 2)
         pairs = [(A, B), (bar_C, Bt), (At, bar_C)]
@@ -1604,3 +1606,33 @@ def test_float32_ordered_fold_in_lds_and_through_a_log(gpu, tmp_path, keys, grou
     assert O.keyed_log_fold(np.stack(values), np.stack([c[::group] for c in cells]), group, want) == 0
     assert (np.abs(want) < 2.0 ** 24).all()                       # exact in float32
     assert host(bt).tobytes() == want.astype(np.float32).tobytes()
+
+
+def test_sample_major_planes_through_hawk_run(unit, gpu):
+    """hawk.run with (N, w) planes (reference hawk/runtime.py:542-566): the
+    energy forward and VJP on sample-major v give the component-major run's
+    bits, the VJP's sample-major bar_v is written back, layout= resolves a
+    plane that reads both ways, and prepare refuses a marked plane."""
+    import hawk_amd as hawk
+    n = 10_007
+    v = rng(61).normal(size=(3, n))
+    bar_out = rng(62).normal(size=n)
+    want = dev(np.zeros(n), gpu)
+    hawk.run(_load(unit, "energy"), v=dev(v, gpu), out=want)
+    got = dev(np.zeros(n), gpu)
+    hawk.run(_load(unit, "energy"), v=dev(np.ascontiguousarray(v.T), gpu), out=got)
+    assert host(got).tobytes() == host(want).tobytes()
+    bv_soa = dev(np.zeros((3, n)), gpu)
+    hawk.run(_load(unit, "energy_vjp"), v=dev(v, gpu), bar_out=dev(bar_out, gpu), bar_v=bv_soa)
+    bv_aos = dev(np.zeros((n, 3)), gpu)
+    hawk.run(_load(unit, "energy_vjp"), v=hawk.samples_first(dev(np.ascontiguousarray(v.T), gpu)),
+             bar_out=dev(bar_out, gpu), bar_v=bv_aos)
+    assert host(bv_aos).tobytes() == np.ascontiguousarray(host(bv_soa).T).tobytes()
+    three = rng(63).normal(size=(3, 3))
+    out3 = dev(np.zeros(3), gpu)
+    with pytest.raises(hawk.HawkError, match="reads both as"):
+        hawk.run(_load(unit, "energy"), v=dev(three, gpu), out=out3)
+    hawk.run(_load(unit, "energy"), v=dev(three, gpu), out=out3, layout="samples_first")
+    assert np.allclose(host(out3), 0.5 * (three * three).sum(axis=1), rtol=1e-15, atol=0)
+    with pytest.raises(hawk.HawkError, match="prepare binds planes by address"):
+        _load(unit, "energy").prepare(v=hawk.samples_first(dev(three, gpu)), out=out3)
