@@ -143,7 +143,13 @@ def workload(config: str, device):
             L.hko_tiled(2, O._p(v), None, None, None, O._p(out), None, 0.0, 0.0, n, threads)
             L.hko_tiled(3, O._p(v), O._p(bar_out), None, None, O._p(bv), None, 0.0, 0.0, n, threads)
             L.hko_tiled(4, O._p(v), O._p(dv), None, None, O._p(do), None, 0.0, 0.0, n, threads)
-        return dict(name="energy fwd + VJP + JVP (config 2)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64")
+        # each stage's HBM pattern (element rows read, rows written; one sample a thread), for pattern_ceiling
+        blk = {k.name: k.launch_shape["block"] for k in (kf, kv, kj)}
+        pattern = {"energy": (3, 1, blk["energy"], blk["energy"]),
+                   "energy_vjp": (4, 3, blk["energy_vjp"], blk["energy_vjp"]),
+                   "energy_jvp": (6, 1, blk["energy_jvp"], blk["energy_jvp"])}
+        return dict(name="energy fwd + VJP + JVP (config 2)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
+                    pattern=pattern, esize=8)
     if config == "3":
         n = 1 << 22
         g = np.random.default_rng(3)
