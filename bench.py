@@ -118,7 +118,9 @@ def workload(config: str, device):
             import oracle_lib as O
             out = np.empty(n)
             O.lib().hko_tiled(1, O._p(x), None, None, None, O._p(out), None, 2.0, 1.0, n, threads)
-        return dict(name="scale fwd (config 1)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64")
+        # the stage's HBM pattern (one row read, one written), one sample a thread, for pattern_ceiling
+        return dict(name="scale fwd (config 1)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
+                    pattern={"scale": (1, 1, 256, 256)}, esize=8)
     if config == "2":
         n = 1 << 25
         g = np.random.default_rng(2)
