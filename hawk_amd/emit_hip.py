@@ -1254,19 +1254,57 @@ HK_MATH_QUAL double hk_cos(double x) {
     return hk_quadrant(r, n + 1);
 }
 
+// exp x for x <= 0 or NaN: hk_exp's bits without its upper clamp.
+HK_MATH_QUAL double hk_exp_nonpos(double x) {
+    double k;
+    const double r = hk_exp_reduce(fmax(x, -1200.0), &k);
+    const double e = ldexp(1.0 + fma(r * r, hk_exp_poly(r), r), static_cast<int>(k));
+    return x != x ? x + x : e;
+}
+
+// sqrt x for x in [2^-700, DBL_MAX] or NaN.  y ~ 1/sqrt(x) from the
+// hardware's reciprocal square root, then the coupled Newton-Raphson
+// iteration on g ~ sqrt(x) and h ~ 1/(2 sqrt(x)) and two residual
+// corrections d = x - g^2, each an exact fused multiply-add.  This is the
+// device compiler's own sequence for sqrt, so the bits are sqrt's, less the
+// rescaling of operands below 2^-767 and the test for 0 and infinity.
+HK_MATH_QUAL double hk_sqrt_normal(double x) {
+    const double y = HK_RSQ(x);
+    double g = x * y;
+    double h = y * 0.5;
+    const double e = fma(-h, g, 0.5);
+    g = fma(g, e, g);
+    double d = fma(-g, g, x);
+    h = fma(h, e, h);
+    g = fma(d, h, g);
+    d = fma(-g, g, x);
+    return fma(d, h, g);
+}
+
 // tanh x = sign(x) e / (e + 2), e = expm1(2|x|) >= 0; +-1 from |x| = 22 on.
 HK_MATH_QUAL double hk_tanh(double x) {
     const double a = fabs(x);
     const double e = hk_expm1_pos(fmin(a + a, 64.0));
     return x != x ? x + x : copysign(a >= 22.0 ? 1.0 : e / (e + 2.0), x);
 }
+
+// tanh x for |x| <= 20 or NaN: hk_tanh's bits without its clamp, its
+// saturation test and its NaN select (NaN passes through expm1 and the
+// quotient).
+HK_MATH_QUAL double hk_tanh_mid(double x) {
+    const double a = fabs(x);
+    const double e = hk_expm1_pos(a + a);
+    return copysign(e / (e + 2.0), x);
+}
 """
 
 #: The fp64 math calls this target spells with its own helpers, and the
 #: qualifiers the device build gives them.
-MATH_HELPER_CALLS = ("hk_exp(", "hk_sin(", "hk_cos(", "hk_tanh(")
+MATH_HELPER_CALLS = ("hk_exp(", "hk_sin(", "hk_cos(", "hk_tanh(", "hk_exp_nonpos(", "hk_sqrt_normal(",
+                     "hk_tanh_mid(")
 MATH_DEVICE_DEFINES = ["#define HK_MATH_QUAL __device__ __forceinline__",
-                       "#define HK_MATH_PIN(c) asm(\"\" : \"+s\"(c))"]
+                       "#define HK_MATH_PIN(c) asm(\"\" : \"+s\"(c))",
+                       "#define HK_RSQ(x) __builtin_amdgcn_rsq(x)"]
 
 
 def _whole_fold_lines(folds: list, block: int) -> list:
@@ -1374,7 +1412,7 @@ __device__ __forceinline__ void hk_band_row_sum(double& h, double& l) {
 """
 
 
-_FP_CALL = re.compile(r"\b(?:hk_)?(?:exp|sin|cos|tanh|sqrt|log|fabs)\(")
+_FP_CALL = re.compile(r"\b(?:hk_)?(?:exp|sin|cos|tanh|sqrt|log|fabs)(?:_nonpos|_normal|_mid)?\(")
 _FP_BINARY = re.compile(r"(?<=[\w\)\]]) [-+*/] (?=[\w\(])")
 _PLANE_ACCESS = re.compile(r"hk_p_\w+(?:\[|_m\.|_cs\b)")
 _SAMPLE_LOOP = re.compile(r"^\s*for \(long long \w+ = (-?\d+)LL; \w+ != (-?\d+)LL; \w+ \+= (-?\d+)LL\) \{")

@@ -22,6 +22,92 @@ import math
 
 from .ir import HawkError, Node
 
+_INF = math.inf
+_WHOLE = (-_INF, _INF)
+
+
+def _widen(lo: float, hi: float) -> tuple:
+    """An interval grown outward by a relative 2^-50 at each end, so that a
+    bound computed in Python's doubles still holds for the device's rounded
+    result of the same operation."""
+    if lo != lo or hi != hi:
+        return _WHOLE
+    return lo - abs(lo) * 2.0 ** -50, hi + abs(hi) * 2.0 ** -50
+
+
+def _range_memo(r) -> dict:
+    memo = getattr(r, "_value_ranges", None)
+    if memo is None:
+        memo = {}
+        try:
+            r._value_ranges = memo
+        except AttributeError:
+            pass
+    return memo
+
+
+def value_range(node, memo: dict) -> tuple:
+    """Bounds ``(lo, hi)`` on every non-NaN value an fp64 node can take, by
+    interval arithmetic over its operands: literals, negation, ``abs``,
+    ``+ - *``, the monotone ``exp`` and ``sqrt``, and ``sin``/``cos``/``tanh``
+    in [-1, 1]; any other node is unbounded.  NaN is always possible and is
+    not described: a helper form chosen from these bounds must carry NaN
+    through by itself."""
+    if not isinstance(node, Node):
+        return _WHOLE
+    got = memo.get(node.uid)
+    if got is not None:
+        return got
+    k, ops = node.kind, node.operands
+    out = _WHOLE
+    if k == "const" and isinstance(node.literal, (int, float)) and not isinstance(node.literal, bool):
+        v = float(node.literal)
+        out = (v, v) if v == v else _WHOLE
+    elif k in ("neg", "abs", "exp", "sqrt", "real") and ops:
+        lo, hi = value_range(ops[0], memo)
+        if k == "neg":
+            out = (-hi, -lo)
+        elif k == "abs":
+            out = (lo, hi) if lo >= 0 else (-hi, -lo) if hi <= 0 else (0.0, max(-lo, hi))
+        elif k == "exp":
+            out = _widen(0.0 if lo < -746 else math.exp(lo), _INF if hi > 709 else math.exp(hi))
+            out = (max(out[0], 0.0), out[1])
+        elif k == "sqrt":
+            out = _widen(math.sqrt(lo) if lo > 0 else 0.0, math.sqrt(hi) if hi >= 0 else 0.0)
+            out = (max(out[0], 0.0), out[1])
+        else:
+            out = (lo, hi)
+    elif k in ("sin", "cos", "tanh"):
+        out = (-1.0, 1.0)
+    elif k in ("add", "sub", "mul") and len(ops) == 2:
+        (a, b), (c, d) = value_range(ops[0], memo), value_range(ops[1], memo)
+        if k == "add":
+            ends = (a + c, b + d)
+        elif k == "sub":
+            ends = (a - d, b - c)
+        else:
+            ends = tuple(x * y for x in (a, b) for y in (c, d))
+        out = _widen(min(ends), max(ends)) if all(e == e for e in ends) else _WHOLE
+    memo[node.uid] = out
+    return out
+
+
+#: fp64 calls with a form for a bounded operand: (helper, does it fit the
+#: operand's bounds).  Each form returns the general form's bits on its
+#: domain and NaN for NaN.
+#: * sqrt on [2^-700, DBL_MAX]: the Newton-Raphson square root seeded by the
+#:   hardware reciprocal square root, without the rescaling of tiny operands
+#:   and the test for 0 and infinity that the general form needs;
+#: * tanh on [-20, 20]: no clamp of the argument, no saturation test, no NaN
+#:   select;
+#: * exp on (-inf, 0]: no upper clamp.
+_DOMAIN_FORMS = {
+    "sqrt": ("hk_sqrt_normal", lambda lo, hi: lo >= 2.0 ** -700 and hi <= 1.7e308),
+    "tanh": ("hk_tanh_mid", lambda lo, hi: lo >= -20.0 and hi <= 20.0),
+    "exp": ("hk_exp_nonpos", lambda lo, hi: hi <= 0.0),
+}
+
+
 #: The reference's writer seam, member for member (``hawk/emit/writer.py:29-38``).
 WRITER_MEMBERS = (
     "declare", "carry_type", "tape_decl", "counter_decl", "for_header",
@@ -185,6 +271,11 @@ class HipWriter:
         if k in _UNARY:
             fn = _UNARY[k]
             dtype = node.ttype.dtype if isinstance(node, Node) else "f64"
+            if dtype == "f64" and isinstance(node, Node) and fn in _DOMAIN_FORMS:
+                lo, hi = value_range(node.operands[0], _range_memo(r))
+                form, fits = _DOMAIN_FORMS[fn]
+                if fits(lo, hi):
+                    return f"{form}({args[0]})"
             if dtype == "f64" and fn in ("tanh", "exp", "sin", "cos"):
                 fn = "hk_" + fn
             return f"{fn}({args[0]})"

@@ -334,6 +334,71 @@ def test_ordered_scatter_reports_a_bad_key(unit, gpu):
     assert host(acc).tobytes() == want.tobytes()
 
 
+def test_domain_forms_give_the_general_forms_bits_on_the_device(gpu):
+    """Where interval arithmetic bounds an operand, the emitter spells sqrt,
+    tanh and exp in their bounded forms; on the device each gives the bits of
+    the general form on the same operand: sqrt is numpy's (correctly rounded)
+    over [e^-480, e^480], tanh on 1.5 sin x + 0.25 is the general tanh of
+    the device's own argument, exp(-|x|) is the general exp of -|x|, NaN and
+    infinities included."""
+    import tempfile
+    import hawk_amd as hawk
+    from hawk_amd import Scalar, kernel
+    from hawk_amd import math as m
+
+    @kernel
+    def sq_arg(x: Scalar) -> Scalar:
+        return m.exp(m.tanh(x) * 480.0)
+
+    @kernel
+    def sq(x: Scalar) -> Scalar:
+        return m.sqrt(m.exp(m.tanh(x) * 480.0))
+
+    @kernel
+    def th_arg(x: Scalar) -> Scalar:
+        return m.sin(x) * 1.5 + 0.25
+
+    @kernel
+    def th_mid(x: Scalar) -> Scalar:
+        return m.tanh(m.sin(x) * 1.5 + 0.25)
+
+    @kernel
+    def th_any(x: Scalar) -> Scalar:
+        return m.tanh(x)
+
+    @kernel
+    def ex_neg(x: Scalar) -> Scalar:
+        return m.exp(-m.abs(x))
+
+    @kernel
+    def ex_any(x: Scalar) -> Scalar:
+        return m.exp(x)
+
+    from hawk_amd.emit_hip import plan_kernel
+    assert "= hk_sqrt_normal(" in plan_kernel(sq.program, "sq").source
+    assert "= hk_tanh_mid(" in plan_kernel(th_mid.program, "th_mid").source
+    assert "= hk_exp_nonpos(" in plan_kernel(ex_neg.program, "ex_neg").source
+    d = tempfile.mkdtemp()
+    hawk.build([sq_arg, sq, th_arg, th_mid, th_any, ex_neg, ex_any], d)
+    g = rng(17)
+    x = np.concatenate([g.normal(size=150_000) * 3, g.uniform(-0.02, 0.02, 50_000), g.uniform(-800, 800, 50_000),
+                        [0.0, -0.0, np.inf, -np.inf, np.nan, 5e-324, 1e-300]])
+
+    def run(name, arg):
+        out = dev(np.zeros_like(arg), gpu)
+        hawk.run(hawk.load(d, name), x=dev(arg, gpu), out=out)
+        return host(out)
+
+    def same(a, b):
+        nan = np.isnan(a)
+        assert np.array_equal(nan, np.isnan(b))
+        assert a[~nan].tobytes() == b[~nan].tobytes()
+
+    same(run("sq", x), np.sqrt(run("sq_arg", x)))
+    same(run("th_mid", x), run("th_any", run("th_arg", x)))
+    same(run("ex_neg", x), run("ex_any", -np.abs(x)))
+
+
 @pytest.mark.parametrize("which", ["exp", "sin", "cos", "tanh", "sqrt"])
 def test_transcendentals_are_within_4_ulp_of_glibc(unit, gpu, which):
     """The device's fp64 exp/sin/tanh/sqrt on the chain's argument ranges, in ULP of

@@ -19,7 +19,9 @@ from conftest import ulp_diff
 _DRIVER = """
 extern "C" void hk_eval(int which, const double* x, double* y, long n) {
     for (long i = 0; i < n; ++i)
-        y[i] = which == 0 ? hk_exp(x[i]) : which == 1 ? hk_sin(x[i]) : which == 2 ? hk_cos(x[i]) : hk_tanh(x[i]);
+        y[i] = which == 0 ? hk_exp(x[i]) : which == 1 ? hk_sin(x[i]) : which == 2 ? hk_cos(x[i])
+             : which == 3 ? hk_tanh(x[i]) : which == 4 ? hk_exp_nonpos(x[i]) : which == 5 ? hk_sqrt_normal(x[i])
+             : hk_tanh_mid(x[i]);
 }
 """
 
@@ -30,7 +32,8 @@ def helpers(tmp_path_factory):
     d = tmp_path_factory.mktemp("math")
     src = d / "helpers.cpp"
     src.write_text("#include <cmath>\nusing std::fma; using std::rint; using std::ldexp; using std::fabs;\n"
-                   "#define HK_MATH_QUAL static inline\n#define HK_MATH_PIN(c) (void)(c)\n" + _MATH_HELPERS + _DRIVER)
+                   "#define HK_MATH_QUAL static inline\n#define HK_MATH_PIN(c) (void)(c)\n"
+                   "#define HK_RSQ(x) (1.0 / std::sqrt(x))\n" + _MATH_HELPERS + _DRIVER)
     lib = d / "helpers.so"
     subprocess.run(["g++", "-O2", "-ffp-contract=off", "-fno-math-errno", "-shared", "-fPIC", str(src), "-o",
                     str(lib)], check=True)
@@ -39,7 +42,8 @@ def helpers(tmp_path_factory):
     def run(which, x):
         x = np.ascontiguousarray(x, dtype=np.float64)
         y = np.empty_like(x)
-        handle.hk_eval({"exp": 0, "sin": 1, "cos": 2, "tanh": 3}[which], x.ctypes.data_as(ctypes.c_void_p),
+        handle.hk_eval({"exp": 0, "sin": 1, "cos": 2, "tanh": 3, "exp_nonpos": 4, "sqrt_normal": 5,
+                                "tanh_mid": 6}[which], x.ctypes.data_as(ctypes.c_void_p),
                        y.ctypes.data_as(ctypes.c_void_p), ctypes.c_long(x.size))
         return y
     return run
@@ -93,3 +97,55 @@ def test_helpers_on_special_values(helpers, which):
             assert g_ == w_, (which, xi, g_)
         else:
             assert ulp_diff(np.array([g_]), np.array([w_]))[0] <= 2.0, (which, xi, g_, w_)
+
+
+def _same_bits(a, b):
+    return np.array_equal(a.view(np.int64), b.view(np.int64)) or (
+        np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a[~np.isnan(a)].view(np.int64),
+                                                                    b[~np.isnan(b)].view(np.int64)))
+
+
+def test_domain_forms_are_the_general_forms_on_their_domains(helpers):
+    """The forms the emitter picks for a bounded operand give the general
+    form's bits on their domain: exp on x <= 0, tanh on [-20, 20] (NaN stays
+    NaN in both), and the rsq-seeded square root is the correctly rounded
+    sqrt on [2^-700, DBL_MAX] (the host seed here is 1/sqrt(x) rounded; the
+    device's is its reciprocal square root, and the GPU test holds that form
+    to numpy's sqrt too)."""
+    g = np.random.default_rng(11)
+    x = np.concatenate([-np.abs(g.normal(size=200_000)) * 30, -np.exp(g.uniform(-700, 7, 100_000)),
+                        np.arange(-746, 0, 0.125), [0.0, -0.0, -5e-324, -1e-310, -745.2, -1200.0, -1e300,
+                                                    -np.inf, np.nan]])
+    assert _same_bits(helpers("exp_nonpos", x), helpers("exp", x))
+    t = np.concatenate([g.uniform(-20, 20, 300_000), g.normal(size=50_000) * 1e-4, np.arange(-20, 20, 1e-3),
+                        np.exp(g.uniform(-700, 2.99, 50_000)) * np.sign(g.normal(size=50_000)),
+                        [0.0, -0.0, 5e-324, -5e-324, 19.999, -20.0, 20.0, np.nan]])
+    assert _same_bits(helpers("tanh_mid", t), helpers("tanh", t))
+    s = np.concatenate([1.0 + g.uniform(0, 1, 300_000), np.exp(g.uniform(-480, 709, 300_000)),
+                        np.nextafter(1.0, 2.0) + np.arange(2000) * 2.0 ** -52, 4.0 - np.arange(2000) * 2.0 ** -51,
+                        [2.0 ** -700, 1.7e308, 1.0, 2.0, 3.0, np.nan]])
+    assert _same_bits(helpers("sqrt_normal", s), np.sqrt(s))
+
+
+def test_emitter_picks_the_domain_forms_from_value_ranges():
+    """Interval arithmetic over the IR: the chain's sqrt(|tanh| + 1) is on
+    [1, 2], its tanh argument 1.5 sin + 0.25 is on [-1.25, 1.75] and its
+    last exp argument -|t6| is <= 0, so each gets its bounded form; an
+    unbounded operand keeps the general form."""
+    from hawk_amd import Scalar, kernel
+    from hawk_amd import math as m
+    from hawk_amd.emit_hip import plan_kernel
+    from hawk_amd.examples import chain
+
+    src = plan_kernel(chain.program, "chain").source
+    for form in ("hk_sqrt_normal(", "hk_tanh_mid(", "hk_exp_nonpos("):
+        assert src.count("= " + form) == 1, form
+    assert src.count("= hk_exp(") == 1
+
+    @kernel
+    def free(x: Scalar) -> Scalar:
+        return m.sqrt(x) + m.tanh(x * 2.0) + m.exp(x) + m.sqrt(m.exp(x)) + m.tanh(m.sin(x) * 25.0)
+
+    src = plan_kernel(free.program, "free").source
+    assert "= hk_sqrt_normal(" not in src and "= hk_tanh_mid(" not in src and "= hk_exp_nonpos(" not in src
+    assert src.count("= sqrt(") == 2 and src.count("= hk_tanh(") == 2
