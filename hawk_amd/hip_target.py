@@ -270,7 +270,13 @@ class HipWriter:
             return f"Real({args[0]})"
         if k in _UNARY:
             fn = _UNARY[k]
+            # The IR's dtype is f64 in a float32 build too (there Real is
+            # float): the fp64 helpers and the interval analysis, which
+            # assumes double arithmetic, apply to double builds only; a
+            # float32 build calls the float overloads.
             dtype = node.ttype.dtype if isinstance(node, Node) else "f64"
+            if getattr(r, "mode", "float64") == "float32":
+                dtype = "f32"
             if dtype == "f64" and isinstance(node, Node) and fn in _DOMAIN_FORMS:
                 lo, hi = value_range(node.operands[0], _range_memo(r))
                 form, fits = _DOMAIN_FORMS[fn]

@@ -497,20 +497,48 @@ def test_chain_each_operation_on_its_own_inputs(unit, gpu):
     assert y.tobytes() == ((t7 * x) + t4).tobytes()
 
 
-def test_chain_at_full_size_every_element_within_the_bound(unit, gpu):
-    """N = 2^26 (config 5's size): every y within the per-element bound; the
-    worst error and the count outside the plain 4 ulp / 1e-13 bar are
-    printed (the figures the design notes record)."""
+def _config5_inputs(n):
+    """Config 5's inputs as the benchmark draws them: x ~ N(0,1), then Zipf(1.1)
+    keys folded into 65536 cells, from one generator seeded 5."""
+    g = rng(5)
+    x = g.normal(size=n)
+    key = ((g.zipf(1.1, n) - 1) % (1 << 16)).astype(np.int32)
+    return x, key
+
+
+def test_config5_at_the_benchmarks_own_shape(unit, gpu):
+    """The timed workload itself, N = 2^26 with the benchmark's inputs: one
+    launch of the fused chain + ordered sum + ordered scatter (256 chunks of
+    64 tiles into 65536 cells).  Every y within the per-element bound; the
+    total the fixed tree of the device's y, bit for bit; every bin the serial
+    walk over the device's y, bit for bit; a second launch the same bits.  The
+    worst error and the count outside the plain 4 ulp / 1e-13 bar are printed
+    (the figures the design notes record)."""
     import chain_bound as CB
     import hawk_amd as hawk
     n = 1 << 26
-    x = rng(5).normal(size=n)
-    print("chain full size", flush=True)
+    cells = 1 << 16
+    x, key = _config5_inputs(n)
+    print("config 5 at 2^26: launch", flush=True)
+    k = _load(unit, "chain")
+    X, KEY = dev(x, gpu), dev(key, gpu)
     y = dev(np.zeros(n), gpu)
-    hawk.run(_load(unit, "chain"), x=dev(x, gpu), key=dev(np.zeros(n, np.int32), gpu), y=y,
-             total=dev(np.zeros(1), gpu), bins=dev(np.zeros(1), gpu))
-    got = host(y)
-    del y
+    runs = []
+    for _ in range(2):
+        total, bins = dev(np.zeros(1), gpu), dev(np.zeros(cells), gpu)
+        hawk.run(k, x=X, key=KEY, y=y, total=total, bins=bins)
+        runs.append((host(y), host(total), host(bins)))
+    del X, KEY, y
+    assert k.scatter_chunks == 256
+    got = runs[0][0]
+    assert all(r[0].tobytes() == got.tobytes() and r[1].tobytes() == runs[0][1].tobytes()
+               and r[2].tobytes() == runs[0][2].tobytes() for r in runs[1:])
+    print("config 5 at 2^26: total and bins against the oracle", flush=True)
+    assert runs[0][1][0] == O.ordered_sum(got, threads=16)
+    want_bins, status = O.ordered_scatter(key, got, np.zeros(cells), threads=16)
+    assert not status[1:].any()
+    assert runs[0][2].tobytes() == want_bins.tobytes()
+    print("config 5 at 2^26: y against the per-element bound", flush=True)
     p = CB.parts(x)
     want = p["y"]
     assert want.tobytes() == O.chain(x, threads=16).tobytes()
@@ -523,6 +551,35 @@ def test_chain_at_full_size_every_element_within_the_bound(unit, gpu):
           f"worst {u.max():.1f} ulp ({(err / np.abs(want)).max():.3g} relative, {err.max():.3g} absolute); "
           f"worst error / bound {(err / bound).max():.3f}; bit-identical {(got == want).mean():.4f}", flush=True)
     assert ok.all()
+
+
+def test_ordered_scatter_past_one_tail_batch(unit, gpu):
+    """N = 2^26 + 12345 Zipf keys into 65536 cells: 256 chunks of 262193 lanes,
+    65 tiles a chunk, so the tail ranges read their bins in two batches (64
+    tiles, then one).  Skip keys on 1 % of the lanes.  The serial walk's bits,
+    and the same bits on a replay."""
+    import hawk_amd as hawk
+    n = (1 << 26) + 12345
+    cells = 1 << 16
+    g = rng(n)
+    key = ((g.zipf(1.1, n) - 1) % cells).astype(np.int32)
+    key[g.random(n) < 0.01] = -1
+    x = g.normal(size=n)
+    acc0 = g.normal(size=cells)
+    k = _load(unit, "ordered_add")
+    print(f"scatter zipf n={n} (two tail batches)", flush=True)
+    K, X = dev(key, gpu), dev(x, gpu)
+    outs = []
+    for _ in range(2):
+        acc = dev(acc0, gpu)
+        hawk.run(k, key=K, x=X, acc=acc)
+        outs.append(host(acc))
+    assert k.scatter_chunks == 256
+    span = -(-n // 256)
+    assert -(-span // 4096) == 65
+    want, status = O.ordered_scatter(key, x, acc0, threads=16)
+    assert not status[1:].any()
+    assert outs[0].tobytes() == outs[1].tobytes() == want.tobytes()
 
 
 # -- config 4b --------------------------------------------------------------------
@@ -664,6 +721,34 @@ def test_float32_default_sum_special_values(unit32, gpu):
     assert total_of(np.float32([1e8, 1.0, -1e8])) == 1.0
     x = (np.arange(1, 200_001) % 97).astype(np.float32)
     assert total_of(x) == O.sample_sum_f32(x)
+
+
+def test_float32_transcendentals_on_the_device(gpu, tmp_path):
+    """A float32 build of sqrt(|sin x| + 1e-50) + exp(-|x|) + tanh(2 sin x):
+    the float overloads on float operands, within the north star's 1e-6
+    relative of the float64 value (measured on the sum of the terms'
+    magnitudes); at x = 0 the square root is 0, not NaN (1e-50 rounds to
+    0.0f, so a bounded double form seeded by rsq would give NaN there)."""
+    import hawk_amd as hawk
+    from hawk_amd import Scalar, kernel
+    from hawk_amd import math as m
+
+    @kernel
+    def tiny(x: Scalar) -> Scalar:
+        return m.sqrt(m.abs(m.sin(x)) + 1e-50) + m.exp(-m.abs(x)) + m.tanh(m.sin(x) * 2.0)
+
+    hawk.build([tiny], tmp_path, mode="float32")
+    x = np.concatenate([[0.0, -0.0, 1e-30, np.pi], rng(77).normal(size=100_000) * 3]).astype(np.float32)
+    y = dev(np.full(x.size, np.nan, np.float32), gpu)
+    hawk.run(hawk.load(tmp_path, "tiny"), x=dev(x, gpu), out=y)
+    got = host(y).astype(np.float64)
+    xd = x.astype(np.float64)
+    s = np.sin(xd)
+    want = np.sqrt(np.abs(s)) + np.exp(-np.abs(xd)) + np.tanh(2.0 * s)
+    scale = np.sqrt(np.abs(s)) + np.exp(-np.abs(xd)) + np.abs(np.tanh(2.0 * s))
+    assert not np.isnan(got).any()
+    assert got[0] == 1.0 and got[1] == 1.0
+    assert (np.abs(got - want) <= 1e-6 * scale + 4 * np.spacing(np.float32(scale)).astype(np.float64)).all()
 
 
 def test_default_sum_special_values(unit, gpu):

@@ -149,3 +149,31 @@ def test_emitter_picks_the_domain_forms_from_value_ranges():
     src = plan_kernel(free.program, "free").source
     assert "= hk_sqrt_normal(" not in src and "= hk_tanh_mid(" not in src and "= hk_exp_nonpos(" not in src
     assert src.count("= sqrt(") == 2 and src.count("= hk_tanh(") == 2
+
+
+def test_float32_builds_call_the_float_overloads(helpers):
+    """The IR's dtype is f64 in a float32 build as well, where Real is float:
+    there the emitter spells sqrt, exp, tanh, sin and cos as the float
+    overloads and picks no bounded form, whose bounds assume double
+    arithmetic.  sqrt(|sin x| + 1e-50) is the case that would break: 1e-50
+    rounds to 0.0f, and at x = 0 the bounded square root (seeded by the
+    reciprocal square root) gives NaN where sqrt(0) is 0."""
+    from hawk_amd import Scalar, kernel
+    from hawk_amd import math as m
+    from hawk_amd.emit_hip import plan_kernel
+
+    @kernel
+    def tiny(x: Scalar) -> Scalar:
+        return m.sqrt(m.abs(m.sin(x)) + 1e-50) + m.exp(-m.abs(x)) + m.tanh(m.sin(x) * 2.0) + m.cos(x)
+
+    src64 = plan_kernel(tiny.program, "tiny").source
+    assert "= hk_sqrt_normal(" in src64 and "= hk_exp_nonpos(" in src64 and "= hk_tanh_mid(" in src64
+    src32 = plan_kernel(tiny.program, "tiny", mode="float32").source
+    assert "hk_sqrt_normal(" not in src32.split("extern \"C\"")[-1]
+    body = src32.split("extern \"C\"")[-1]
+    for helper in ("hk_exp", "hk_sin", "hk_cos", "hk_tanh", "hk_sqrt_normal", "hk_exp_nonpos", "hk_tanh_mid"):
+        assert helper + "(" not in body, helper
+    for call in ("= sqrt(", "= exp(", "= tanh(", "= sin(", "= cos("):
+        assert call in body, call
+    # the failure the gate prevents, on the host: the bounded form at 0
+    assert np.isnan(helpers("sqrt_normal", np.array([0.0]))[0])
