@@ -154,11 +154,14 @@ def _reference_options(kind, layout_sizes_override, defines, device_arch, host_p
                        launch_bounds) -> tuple:
     """Check the reference's build options (reference
     hawk/artifact/bundle.py:1349-1420) and return ``(compile options, block
-    fixed by launch_bounds or None, what the sidecar records)``.  The forms
+    fixed by launch_bounds or None, what the sidecar records, launch_bounds'
+    blocks or 1)``.  The forms
     choose how the reference spells a site; this target's stages add in the
     order they are written whatever the spelling, so they are checked and
     recorded.  ``opt_level`` and ``defines`` reach hipRTC; ``launch_bounds``
-    fixes the block as the reference's ``launch.block = threads`` does."""
+    fixes the block as the reference's ``launch.block = threads`` does, and
+    its ``blocks`` becomes each entry's waves-per-EU floor
+    (:func:`waves_per_eu`)."""
     if kind is not None:
         raise HawkError("kind=: an execution kind (hawk.ext lanes or an active-set guard) has no hip form in this "
                         "build")
@@ -178,6 +181,7 @@ def _reference_options(kind, layout_sizes_override, defines, device_arch, host_p
     if opt_level and opt_level not in OPT_LEVELS:
         raise HawkError(f"opt_level must be one of {OPT_LEVELS}, got {opt_level!r}")
     block = None
+    blocks = 1
     launch_bounds = _policy.check_launch_bounds(launch_bounds)
     if launch_bounds is not None:
         threads, blocks = launch_bounds
@@ -200,7 +204,24 @@ def _reference_options(kind, layout_sizes_override, defines, device_arch, host_p
                                 ("host_profile", host_profile or None), ("opt_level", opt_level or None),
                                 ("literal_table", bool(literal_table) or None),
                                 ("defines", [str(d) for d in defines] if defines else None)) if v is not None}
-    return tuple(options), block, record
+    return tuple(options), block, record, int(blocks)
+
+
+def waves_per_eu(block: int, blocks: int) -> int:
+    """The occupancy floor that ``launch_bounds=(threads, blocks)`` asks of a
+    stage launched with ``block`` threads: ``blocks`` workgroups resident on
+    one CU are ``blocks * block / 64`` waves over its four SIMDs, so each
+    SIMD (execution unit) must hold that many / 4, at most 8 on gfx950.  The
+    compiler then caps the stage's registers to fit (the CUDA minimum
+    blocks per multiprocessor, spelled as amdgpu waves per EU)."""
+    return max(1, min(8, -(-blocks * block // 256)))
+
+
+def _with_waves(source: str, block: int, waves: int) -> str:
+    """Every entry's ``__launch_bounds__(block)`` given the occupancy floor."""
+    if waves <= 1:
+        return source
+    return source.replace(f"__launch_bounds__({block})", f"__launch_bounds__({block}, {waves})")
 
 
 def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64", cache_dir=None,
@@ -229,7 +250,7 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
     linalg_form = linalg_form if linalg_form is not None else (ambient[1] if ambient[1] != "auto" else None)
     wide_form = wide_form if wide_form is not None else (ambient[2] if ambient[2] != "auto" else None)
     launch_bounds = launch_bounds if launch_bounds is not None else ambient[3]
-    options, bounds_block, recorded = _reference_options(
+    options, bounds_block, recorded, min_blocks = _reference_options(
         kind, layout_sizes_override, defines, device_arch, host_profile, opt_level, literal_table,
         embedded_profile, emit_form, linalg_form, wide_form, launch_bounds)
     if block is None and bounds_block is not None:
@@ -266,6 +287,8 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
             if shape != (256, 1):
                 plan = plan_kernel(k.program, k.name, mode=mode, block=shape[0], per_thread=shape[1],
                                    nontemporal=nontemporal, fuse_folds=fuse_folds, target=target)
+        if plan.stage is not None and min_blocks > 1:
+            plan.source = _with_waves(plan.source, shape[0], waves_per_eu(shape[0], min_blocks))
         plans.append((k, plan, shape))
     staged = [(k, p) for k, p, _ in plans if p.stage is not None]
     compiled = dict(zip([k.name for k, _ in staged],
@@ -275,7 +298,9 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
         sidecar = {
             "kernel": k.name, "target": target.id, "offload_arch": target.offload_arch, "mode": mode,
             "scalar_type": mode, "planes": plan.planes, "team": plan.team,
-            "launch": {"block": shape[0], "per_thread": shape[1], "nontemporal": nontemporal},
+            "launch": {"block": shape[0], "per_thread": shape[1], "nontemporal": nontemporal,
+                       **({"waves_per_eu": waves_per_eu(shape[0], min_blocks)}
+                          if waves_per_eu(shape[0], min_blocks) > 1 else {})},
             "grid": [list(a) for a in k.program.grid.axes] if k.program.grid is not None else None,
             "tables": {t: [list(a) for a in axes] for t, axes in k.program.tables.items()},
             "entry": None, "arg_spec": [], "descriptor": [],

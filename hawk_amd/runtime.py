@@ -464,7 +464,9 @@ class DeviceKernel:
     def _run_on(self, arrays: dict, base: int, count: int, n: int, stream: int, check: bool, steps,
                 entry: str, chunk: int) -> None:
         torch = _torch()
-        device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
+        device = next((x.device for x in arrays.values() if isinstance(x, torch.Tensor)), None)
+        if device is None:
+            raise HawkError(f"kernel {self.name!r}: no plane is a tensor, so there is no device to run on")
         bound, held = self._counter(dict(arrays), device)
         if held is not None:
             with _on(stream):
@@ -624,7 +626,9 @@ class ChainedKernel:
         n = n_samples if n_samples is not None else (ns.pop() if len(ns) == 1 else None)
         if n is None:
             raise HawkError(f"kernel {self.name!r}: its planes disagree on the sample count, or none is bound")
-        device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
+        device = next((x.device for x in arrays.values() if isinstance(x, torch.Tensor)), None)
+        if device is None:
+            raise HawkError(f"kernel {self.name!r}: no plane is a tensor, so there is no device to run on")
         cross = {}
         for name, info in self.crossing.items():
             key = (name, n, device)
@@ -639,6 +643,16 @@ class ChainedKernel:
             names = seg.caller_planes()
             out.append((seg, {p: (cross[p] if p in cross else arrays[p]) for p in names}))
         return out
+
+    def resolve_call(self, arrays: dict, layout=None, n_samples=None) -> tuple:
+        """``(bindings, write_back)`` of one call: the caller's planes made
+        component-major once (:func:`hawk_amd.layout.resolve`), then each
+        segment's planes (:meth:`_bindings`); ``write_back`` lists the
+        sample-major planes the chain writes, with their component-major
+        copies, to copy back after the last segment."""
+        from . import layout as _layout
+        arrays, write_back = _layout.resolve(self, dict(arrays), layout, _PER_SAMPLE, _WRITTEN)
+        return self._bindings(arrays, n_samples), write_back
 
     def prepare(self, *, stream=None, **arrays):
         return _PreparedChain(self, arrays, stream)
@@ -708,8 +722,19 @@ def run(kernel: DeviceKernel, *, base: int = 0, count: int | None = None, n_samp
     if isinstance(kernel, ChainedKernel):
         if base != 0 or count is not None:
             raise HawkError(f"{kernel.name}: a cut chain runs over every sample (no base= or count=)")
-        for seg, planes in kernel._bindings(dict(arrays), n_samples):
-            run(seg, n_samples=n_samples, layout=layout, stream=stream, check=check, **planes)
+        # The caller's planes are resolved to component-major once, at the
+        # chain: the crossing planes are (w, N), so every segment then runs
+        # on component-major planes, and a sample-major plane the chain
+        # writes is copied back after the last segment.
+        sid = torch.cuda.current_stream().cuda_stream if stream is None else getattr(stream, "cuda_stream", stream)
+        with _on(int(sid)):
+            bindings, write_back = kernel.resolve_call(arrays, layout, n_samples)
+        for seg, planes in bindings:
+            run(seg, n_samples=n_samples, stream=stream, check=check, **planes)
+        if write_back:
+            with _on(int(sid)):
+                for dst, copy in write_back:
+                    dst.copy_(copy.movedim(-1, 0))
         return
     if not isinstance(kernel, DeviceKernel):
         raise HawkError("hawk.run takes a kernel loaded with hawk.load")
@@ -770,7 +795,9 @@ class Prepared:
 
     def _setup(self, kernel, arrays: dict, steps, entry: str, chunk: int) -> None:
         torch = _torch()
-        device = next(x.device for x in arrays.values() if isinstance(x, torch.Tensor))
+        device = next((x.device for x in arrays.values() if isinstance(x, torch.Tensor)), None)
+        if device is None:
+            raise HawkError(f"kernel {self.name!r}: no plane is a tensor, so there is no device to run on")
         bound, held = kernel._counter(dict(arrays), device)
         self.held_counter = held
         if held is not None:

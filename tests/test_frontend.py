@@ -1037,6 +1037,11 @@ def test_the_references_build_options_are_taken(tmp_path):
                    derivative={"energy": "scale"}, host_profile="native", literal_table=True)
     sc = b.sidecar("scale")
     assert sc["launch"]["block"] == 128
+    # blocks=2 of 128 threads: 4 waves a CU, one per SIMD, the default; 8 of 256 ask for 8 waves a SIMD
+    assert "waves_per_eu" not in sc["launch"] and "__launch_bounds__(128)" in (tmp_path / "scale.hip").read_text()
+    dense = hawk.build([E.scale], tmp_path / "dense", launch_bounds=(256, 8)).sidecar("scale")
+    assert dense["launch"]["waves_per_eu"] == 8
+    assert "__launch_bounds__(256, 8)" in (tmp_path / "dense" / "scale.hip").read_text()
     assert "-O2" in sc["compile_options"] and "-O3" not in sc["compile_options"]
     assert "-DHAWK_PROBE=1" in sc["compile_options"]
     assert sc["build_options"] == {"emit_form": "static", "linalg_form": "team", "wide_form": "thread",

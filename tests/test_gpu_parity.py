@@ -1500,6 +1500,12 @@ def test_a_cut_chain_is_the_fused_chain(gpu, tmp_path):
             kern.prepare(x=X, acc=acc, y=y)()
         got.append((host(acc).tobytes(), host(y).tobytes()))
     assert got[0] == got[1] == got[2]
+    # the cut chain with its Vector[3] output sample-major, (N, 3), under layout='samples_first'
+    acc, y = dev(acc0, gpu), dev(np.zeros((n, 3)), gpu)
+    print("chain run samples_first", flush=True)
+    hawk.run(cut, x=X, acc=acc, y=y, layout="samples_first")
+    assert host(acc).tobytes() == got[0][0]
+    assert np.ascontiguousarray(host(y).T).tobytes() == got[0][1]
 
 
 def test_folds_and_keyed_sums_keep_ieee_specials_and_empty_runs(gpu, tmp_path):

@@ -55,3 +55,48 @@ def test_layout_refusals_name_the_problem():
         _resolve({"a": hawk.samples_first(torch.randn(3))})
     with pytest.raises(hawk.HawkError, match="marked samples_first is marked samples_last"):
         hawk.samples_last(hawk.samples_first(torch.randn(3)))
+
+
+def test_a_cut_chain_resolves_the_callers_planes_once(tmp_path):
+    """A chain cut into segments (a register line of 32) with its Vector[3]
+    output given sample-major: the caller's planes are resolved once, at the
+    chain, so every segment binds component-major planes (the crossing plane
+    hwc_a is (3, N)), the sample count is N, and the output's copy is written
+    back after the last segment."""
+    import json
+
+    import chain_members as C
+    from hawk_amd import runtime as R
+
+    class _Segment:                       # a segment's sidecar without its code object (no device here)
+        def __init__(self, directory, name):
+            self.name = name
+            self.planes = json.loads((directory / f"{name}.json").read_text())["planes"]
+
+        def caller_planes(self):
+            return [n for n, p in self.planes.items() if not p.get("scratch")]
+
+    chained = hawk.chain(*C.MEMBERS, name="fixture")
+    hawk.build([chained], tmp_path, register_line=32)
+    side = json.loads((tmp_path / "fixture.json").read_text())
+    saved = R.load
+    R.load = _Segment
+    try:
+        cut = R.ChainedKernel(tmp_path, side)
+    finally:
+        R.load = saved
+    n = 10
+    x, acc, y = torch.rand(n, dtype=torch.float64), torch.rand(n, dtype=torch.float64), torch.zeros(n, 3,
+                                                                                                    dtype=torch.float64)
+    for how in ({"layout": "samples_first"}, {}):
+        bindings, back = cut.resolve_call({"x": x, "acc": acc, "y": y}, **how)
+        assert [seg.name for seg, _ in bindings] == [f"fixture__s{i}" for i in range(4)]
+        for seg, planes in bindings:
+            for name, t in planes.items():
+                lead = tuple((cut.planes.get(name) or cut.crossing[name])["shape"])
+                assert tuple(t.shape) == lead + (n,), (seg.name, name, tuple(t.shape))
+        assert [d is y for d, _ in back] == [True] and back[0][1].shape == (3, n)
+    with pytest.raises(hawk.HawkError, match="sample-major under layout='samples_first'"):
+        cut.resolve_call({"x": x, "acc": acc, "y": torch.zeros(3, n, dtype=torch.float64)}, "samples_first")
+    with pytest.raises(hawk.HawkError, match="no plane is a tensor"):
+        cut._bindings({"x": 1.0, "acc": 2.0, "y": 3.0}, n_samples=5)
