@@ -1089,46 +1089,48 @@ __global__ void hawk_scatter_status(int* status, long long cells) {
 constexpr int kSplitHot = 12288;                 // keys a workgroup keeps in LDS (96 KiB of accumulators)
 constexpr long long kSplitCells = 65536;         // the split walk's largest cell count
 constexpr int kSplitMaxRanges = static_cast<int>((kSplitCells - kSplitHot + kSplitHot - 1) / kSplitHot);  // 5
-constexpr int kSplitClassBase = 16;              // buckets 0..15: window keys 0..15
-constexpr int kSplitTailBase = 32;               // buckets 16..31: classes; 32..: tail ranges
-constexpr int kSplitStride = kSplitTailBase + kSplitMaxRanges + 3;   // 40: a wave's row of bucket counts
+constexpr int kSplitHeads = 32;                  // buckets 0..31: window keys 0..31, a chain each
+constexpr int kSplitClassBase = kSplitHeads;     // buckets 32..47: classes (window keys >= 32 by key & 15)
+constexpr int kSplitTailBase = kSplitClassBase + 16;   // 48..: tail ranges
+constexpr int kSplitStride = kSplitTailBase + kSplitMaxRanges + 3;   // 56: a wave's row of bucket counts
 constexpr int kSplitNone = 63;                   // a lane that adds nothing (skip key, bad key, padding)
-constexpr int kSplitSegs = 64;                   // segments one tail batch can hold
 
 static_assert(kSplitHot < (1 << 14), "class matching covers key bits 4..13");
 static_assert(kSplitStride >= kSplitTailBase + kSplitMaxRanges + 1, "bucket starts need one past the last bucket");
 static_assert(kSplitNone >= kSplitStride, "the no-bucket code is outside the count rows");
 
-constexpr int kSplitPad = 64;                    // entries read (and ignored) past a run's end
+constexpr int kSplitPad = 72;                    // entries read (and ignored) past a run's end
+constexpr unsigned kPeerSlots = 128;             // a class fold's match slots: key bits 4..10
+#ifndef HK_HEAD_BLOCK
+#define HK_HEAD_BLOCK 8
+#endif
+constexpr int kHeadBlock = HK_HEAD_BLOCK;        // a head chain's reads in flight: four blocks of kHeadBlock
+static_assert(4 * kHeadBlock <= kSplitPad, "a head chain reads at most kSplitPad entries past its run");
 
 template <class T>
 struct SplitShared {
     T acc[kSplitHot];                          // 96 KiB: the window's accumulators
     T val[kTile + kSplitPad];                  // 32 KiB: the tile's values, bucket order
     unsigned short key[kTile + kSplitPad];          //  8 KiB: their window-local keys
-    union {                                         // 20 KiB, one phase at a time:
-        unsigned long long win[kWalkWaves][kWalkItems][kSplitStride];  // split: a match table per window
+    union {                                         // 16 KiB, one phase at a time:
+        unsigned long long win[kWalkWaves][kSplitStride];              // split: a match table per wave
         struct {
-            unsigned long long peer[kWalkWaves][64];                   // fold: per-wave match masks
+            unsigned long long peer[kWalkWaves][kPeerSlots];           // fold: per-wave match masks (16 KiB)
         } f;
-        unsigned short seg_pos[kSplitSegs];         // a tail batch: each segment's place in the batch
     };
-    alignas(16) unsigned cnt[kSplitStride][kWalkWaves];  // 2.5 KiB: bucket counts, bucket-major (a 64-byte row each)
+    alignas(16) unsigned cnt[kSplitStride][kWalkWaves];  // 3.5 KiB: bucket counts, bucket-major (a 64-byte row each)
     unsigned bstart[kSplitStride + 1];              // bucket d holds [bstart[d], bstart[d+1])
-    unsigned short grp_lo[kSplitSegs];              // a tail group of 64 tiles: each tile's segment
-    unsigned short grp_hi[kSplitSegs];              //   [lo, hi) in its slot
-    unsigned batch_segs, batch_n;
 };
 
 // The bucket of window-local key kl (0 <= kl < window).
 __device__ __forceinline__ int split_bucket(unsigned kl) {
-    return kl < 16u ? static_cast<int>(kl) : kSplitClassBase + static_cast<int>(kl & 15u);
+    return kl < static_cast<unsigned>(kSplitHeads) ? static_cast<int>(kl) : kSplitClassBase + static_cast<int>(kl & 15u);
 }
 
 // Stable split of the tile held in registers (thread slot j of wave w is tile
 // position w*256 + j*64 + lane) into nb buckets: sh.key/sh.val in bucket order,
 // lane order within a bucket; bucket bounds in sh.bstart.  Each wave matches
-// its four windows at once, one table per window, so a lane's rank is the
+// its four windows one after another in one table, so a lane's rank is the
 // count of its bucket in the wave's earlier windows plus the lanes below it
 // in its own.  Every wave then forms its own positions from all waves'
 // counts.  Starts and ends with every thread of the workgroup.
@@ -1139,28 +1141,33 @@ __device__ void split_tile(SplitShared<T>& sh, const unsigned (&kl)[kWalkItems],
     const int wave = t >> 6;
     const int lane = t & 63;
     const unsigned long long me = 1ull << lane;
-    unsigned long long* tab = &sh.win[wave][0][0];
-    for (int i = lane; i < kWalkItems * kSplitStride; i += 64) tab[i] = 0ull;
-    __builtin_amdgcn_wave_barrier();
+    unsigned long long* tab = sh.win[wave];
+    // Window j: clear the table, OR every lane's bit into its bucket's slot,
+    // read the lane's own slot and (lane b) slot b.  The four windows' LDS
+    // operations run back to back: a wave's LDS operations complete in issue
+    // order, so each window's reads see its own ORs and precede the next
+    // window's clear.
+    const int b = lane < kSplitStride ? lane : 0;
+    unsigned long long own[kWalkItems], mine[kWalkItems];
 #pragma unroll
-    for (int j = 0; j < kWalkItems; ++j)
-        if (d[j] != kSplitNone) atomicOr(&sh.win[wave][j][d[j]], me);
-    __builtin_amdgcn_wave_barrier();
-    // lane b: bucket b's four window masks, their counts and the running
-    // count before each window; each item then takes its bucket's running
-    // count from lane d (a permute) and adds the lanes below it in its window
-    unsigned long long own[kWalkItems];
-#pragma unroll
-    for (int j = 0; j < kWalkItems; ++j) own[j] = sh.win[wave][j][d[j] != kSplitNone ? d[j] : 0];
+    for (int j = 0; j < kWalkItems; ++j) {
+        if (lane < kSplitStride) tab[lane] = 0ull;
+        __builtin_amdgcn_wave_barrier();
+        if (d[j] != kSplitNone) atomicOr(&tab[d[j]], me);
+        __builtin_amdgcn_wave_barrier();
+        own[j] = tab[d[j] != kSplitNone ? d[j] : 0];
+        mine[j] = tab[b];
+        __builtin_amdgcn_wave_barrier();
+    }
+    // lane b: bucket b's count in each window and the running count before
+    // each; each item then takes its bucket's running count from lane d (a
+    // permute) and adds the lanes below it in its window
     unsigned run[kWalkItems];
     unsigned total = 0u;
-    {
-        const int b = lane < kSplitStride ? lane : 0;
 #pragma unroll
-        for (int j = 0; j < kWalkItems; ++j) {
-            run[j] = total;
-            total += static_cast<unsigned>(__popcll(sh.win[wave][j][b]));
-        }
+    for (int j = 0; j < kWalkItems; ++j) {
+        run[j] = total;
+        total += static_cast<unsigned>(__popcll(mine[j]));
     }
     if (lane < kSplitStride) sh.cnt[lane][wave] = total;
     unsigned rank[kWalkItems];
@@ -1214,123 +1221,135 @@ __device__ __forceinline__ float lane_value(float x, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
 
-// a + x[s] + x[s+1] + ... + x[e-1] in that order, by the whole wave: each
-// batch of 64 values arrives in one LDS read (lane q holding x[m + q]) with
-// the next batch's read in flight, and readlane hands the batch to the chain
-// lane by lane.  A chain fed this way costs about 14 cycles an add against 21
-// to 25 for one fed by one lane's own LDS reads while the workgroup's other
-// waves use the LDS.  s and e are the same in every lane; x is readable up to
-// 63 entries past e.
+// The head keys' chains, by one wave: lane c (c < kSplitHeads) adds bucket c
+// (window key c: one contiguous run, lane order) onto acc[c], one addition at
+// a time from its own registers.  Its reads run 32 values ahead of its adds
+// in four rotating blocks of 8, so the chain waits on the adds' latency, not
+// on the LDS.  A lane's loop ends with its run; the wave runs as long as the
+// longest run.  Reads go at most 63 entries past a run's end (the padding).
 template <class T>
-__device__ __forceinline__ T fold_lanes(const T* x, int s, int e, T a) {
-    const int lane = threadIdx.x & 63;
-    s = __builtin_amdgcn_readfirstlane(s);
-    e = __builtin_amdgcn_readfirstlane(e);
-    T cur = x[s + lane];
-    for (int m = s; m < e; m += 64) {
-        const T nxt = m + 64 < e ? x[m + 64 + lane] : T(0);
-        if (e - m >= 64) {
+__device__ __forceinline__ void head_block(T (&r)[kHeadBlock], T& a, const T* src) {
 #pragma unroll
-            for (int q = 0; q < 64; ++q) a = a + lane_value(cur, q);
-        } else {
-            for (int q = 0; q < e - m; ++q) a = a + lane_value(cur, q);
-        }
-        cur = nxt;
-    }
-    return a;
+    for (int q = 0; q < kHeadBlock; ++q) a = a + r[q];
+    // the block's next reads go into the registers its adds just used: no
+    // copies, so the other blocks' reads stay in flight
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < kHeadBlock; ++q) r[q] = src[q];
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 template <class T>
-__device__ void split_fold_class(SplitShared<T>& sh, int c);
-
-// Wave c folds bucket c (window key c) and, as a rule, class c of the split
-// tile onto the LDS accumulators.
-template <class T>
-__device__ void split_fold(SplitShared<T>& sh, int window) {
-    const int wave = threadIdx.x >> 6;
+__device__ void fold_heads(SplitShared<T>& sh) {
     const int lane = threadIdx.x & 63;
-    // the whole wave folds the single key's run (fold_lanes)
-    if (wave < window) {
-        const int s = static_cast<int>(sh.bstart[wave]);
-        const int e = static_cast<int>(sh.bstart[wave + 1]);
-        if (s < e) {
-            const T a = fold_lanes(sh.val, s, e, sh.acc[wave]);
-            if (lane == 0) sh.acc[wave] = a;
-        }
+    if (lane >= kSplitHeads) return;
+    const int s = static_cast<int>(sh.bstart[lane]);
+    const int e = static_cast<int>(sh.bstart[lane + 1]);
+    if (s >= e) return;
+    T a = sh.acc[lane];
+    T r0[kHeadBlock], r1[kHeadBlock], r2[kHeadBlock], r3[kHeadBlock];
+    const T* x = sh.val + s;
+#pragma unroll
+    for (int q = 0; q < kHeadBlock; ++q) {
+        r0[q] = x[q];
+        r1[q] = x[kHeadBlock + q];
+        r2[q] = x[2 * kHeadBlock + q];
+        r3[q] = x[3 * kHeadBlock + q];
     }
-    // When one single-key chain is longer than another by more than a
-    // window, the wave with the longest leaves its class to the wave with
-    // the shortest (every wave finds the same two from the bucket bounds):
-    // any wave may fold a class, as long as one wave folds all of it.
-    const int len = lane < 16 ? static_cast<int>(sh.bstart[lane + 1] - sh.bstart[lane]) : 0;
-    int longest = 0, shortest = 0;
-    int lmax = __builtin_amdgcn_readlane(len, 0), lmin = lmax;
-    for (int c = 1; c < 16; ++c) {
-        const int v = __builtin_amdgcn_readlane(len, c);
-        if (v > lmax) { lmax = v; longest = c; }
-        if (v <= lmin) { lmin = v; shortest = c; }
+    constexpr int kAhead = 4 * kHeadBlock;
+    int left = e - s;
+    for (; left >= kAhead; left -= kAhead, x += kAhead) {
+        head_block(r0, a, x + kAhead);
+        head_block(r1, a, x + kAhead + kHeadBlock);
+        head_block(r2, a, x + kAhead + 2 * kHeadBlock);
+        head_block(r3, a, x + kAhead + 3 * kHeadBlock);
     }
-    sh.f.peer[wave][lane] = 0ull;
-    __builtin_amdgcn_wave_barrier();
-    const bool move = lmax - lmin > 64;
-    if (wave != longest || !move) split_fold_class(sh, wave);
-    if (wave == shortest && move) split_fold_class(sh, longest);
+    // fewer than kAhead left, held in r0..r3 in order
+#pragma unroll
+    for (int q = 0; q < kHeadBlock; ++q)
+        if (q < left) a = a + r0[q];
+#pragma unroll
+    for (int q = 0; q < kHeadBlock; ++q)
+        if (kHeadBlock + q < left) a = a + r1[q];
+#pragma unroll
+    for (int q = 0; q < kHeadBlock; ++q)
+        if (2 * kHeadBlock + q < left) a = a + r2[q];
+#pragma unroll
+    for (int q = 0; q < kHeadBlock; ++q)
+        if (3 * kHeadBlock + q < left) a = a + r3[q];
+    sh.acc[lane] = a;
 }
 
-// The caller's wave folds class c of the split tile, 64 entries a window.
+// The caller's wave folds class c of the split tile (window keys >= 32 with
+// key & 15 == c), 64 entries a window in lane order.  Equal keys of a window
+// find each other through the wave's match table: key bits 4..10 pick one of
+// kPeerSlots slots, every lane ORs its bit into its slot, and three ballots
+// over bits 11..13 keep the lanes whose whole key is equal.  A window whose
+// keys are all distinct adds each value onto its key's accumulator at once.
+// Otherwise the window's values are regrouped in place, key by key (keys in
+// the order of their first lane, each key's values in lane order), and each
+// key's first lane adds its run onto the accumulator.  A wave's LDS
+// operations complete in issue order, so a key's windows meet the
+// accumulator one after another.
 template <class T>
-__device__ void split_fold_class(SplitShared<T>& sh, int c) {
+__device__ void fold_class(SplitShared<T>& sh, int c) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const unsigned long long me = 1ull << lane;
     const int s = static_cast<int>(sh.bstart[kSplitClassBase + c]);
     const int e = static_cast<int>(sh.bstart[kSplitClassBase + c + 1]);
     if (s >= e) return;
-    // 64 entries a window; the next window's entries are read while this one
-    // is folded.  A lane past the end reads (padding or another bucket's
-    // entry) and ignores it; its match bit goes to a slot of its own.
+    unsigned long long* peer = sh.f.peer[wave];
     unsigned k = sh.key[s + lane];
     T x = sh.val[s + lane];
     for (int base = s; base < e; base += 64) {
         const bool valid = base + lane < e;
-        const unsigned nk = sh.key[base + 64 + lane];
-        const T nx = sh.val[base + 64 + lane];
+        unsigned nk = 0u;
+        T nx = T(0);
+        if (base + 64 < e) {
+            nk = sh.key[base + 64 + lane];
+            nx = sh.val[base + 64 + lane];
+        }
         const unsigned kv = valid ? k : 0u;
-        const unsigned h = valid ? (kv >> 4) & 63u : static_cast<unsigned>(lane);
-        atomicOr(&sh.f.peer[wave][h], valid ? me : 0ull);
+        const unsigned h = (kv >> 4) & (kPeerSlots - 1u);
+        if (valid) atomicOr(&peer[h], me);
         __builtin_amdgcn_wave_barrier();
-        unsigned long long pm = sh.f.peer[wave][h];
-        T a = sh.acc[kv];
+        unsigned long long pm = valid ? peer[h] : 0ull;
         __builtin_amdgcn_wave_barrier();
-        sh.f.peer[wave][h] = 0ull;
-        // the slot matched key bits 4..9 (bits 0..3 are the class); bits
-        // 10..13 by ballots
+        if (valid) peer[h] = 0ull;
 #pragma unroll
-        for (int bit = 10; bit < 14; ++bit) {
+        for (int bit = 11; bit < 14; ++bit) {
             const bool one = (kv >> bit) & 1u;
             const unsigned long long ones = __ballot(valid && one);
             pm &= one ? ones : ~ones;
         }
-        // the group's lowest lane adds its own value, then the others' in
-        // lane order, read straight from the bucket four at a time
-        if (valid && (pm & (me - 1ull)) == 0ull) {
-            a = a + x;
-            unsigned long long m = pm & ~me;
-            while (m) {
-                int q[4];
+        // rank: the lanes of my key below me
+        const unsigned rank = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(pm >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(pm), 0u));
+        if (__ballot(valid && rank != 0u) == 0ull) {
+            if (valid) sh.acc[kv] = sh.acc[kv] + x;
+        } else {
+            const unsigned size = static_cast<unsigned>(__popcll(pm));
+            const bool lead = valid && rank == 0u;
+            const unsigned gsz = lead ? size : 0u;
+            const unsigned gs = wave_inclusive_scan(gsz) - gsz;       // where my key's run starts (leaders)
+            const int first = valid ? static_cast<int>(__builtin_ctzll(pm)) : lane;
+            const unsigned g0 = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(first << 2, static_cast<int>(gs)));
+            if (valid) sh.val[base + g0 + rank] = x;
+            __builtin_amdgcn_wave_barrier();
+            if (lead) {
+                T a = sh.acc[kv];
+                const T* run = sh.val + base + gs;
+                for (unsigned u = 0; u < size; u += 8) {
+                    T y[8];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    q[u] = m ? __builtin_ctzll(m) : -1;
-                    m &= m - 1ull;
+                    for (int q = 0; q < 8; ++q) y[q] = run[u + q];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        if (u + q < size) a = a + y[q];
                 }
-                T y[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) y[u] = sh.val[base + (q[u] < 0 ? 0 : q[u])];
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (q[u] >= 0) a = a + y[u];
+                sh.acc[kv] = a;
             }
-            sh.acc[kv] = a;
         }
         __builtin_amdgcn_wave_barrier();
         k = nk;
@@ -1338,6 +1357,23 @@ __device__ void split_fold_class(SplitShared<T>& sh, int c) {
     }
 }
 
+// The split tile's folds: wave 0 the head keys' chains, wave w (1..15) class
+// w, and wave 1 class 0 as well.  A class wave first clears its match table
+// (it shares LDS with the split's tables); each window leaves it clear.
+template <class T>
+__device__ void split_fold(SplitShared<T>& sh) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    if (wave == 0) {
+        fold_heads(sh);
+        return;
+    }
+#pragma unroll
+    for (unsigned i = 0; i < kPeerSlots; i += 64) sh.f.peer[wave][i + lane] = 0ull;
+    __builtin_amdgcn_wave_barrier();
+    fold_class(sh, wave);
+    if (wave == 1) fold_class(sh, 0);
+}
 // The window's partials of chunk b, every key [klo, klo+window): a key no
 // lane named holds +0.0, the walk's starting value.
 template <class T>
@@ -1379,23 +1415,20 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
         unsigned kl[kWalkItems];
         int d[kWalkItems];
         T vv[kWalkItems];
+        // each lane's bucket, without branches: a skip or bad key none, a
+        // window key its head bucket or class, a tail key its range
 #pragma unroll
         for (int j = 0; j < kWalkItems; ++j) {
-            const int k = nk[j];
+            const unsigned u = static_cast<unsigned>(nk[j]);
             vv[j] = nv[j];
-            const bool valid = k >= 0 && k < cells;
-            bad = bad || (k != -1 && !valid);
-            if (!valid) {
-                d[j] = kSplitNone;
-                kl[j] = 0u;
-            } else if (k < window) {
-                d[j] = split_bucket(static_cast<unsigned>(k));
-                kl[j] = static_cast<unsigned>(k);
-            } else {
-                const int r = (k - kSplitHot) / kSplitHot;
-                d[j] = kSplitTailBase + r;
-                kl[j] = static_cast<unsigned>(k - kSplitHot - r * kSplitHot);
-            }
+            const bool valid = u < static_cast<unsigned>(cells);
+            bad = bad | ((nk[j] != -1) & !valid);
+            const unsigned tl = u - static_cast<unsigned>(kSplitHot);
+            const unsigned r = tl / static_cast<unsigned>(kSplitHot);
+            const bool in_win = u < static_cast<unsigned>(window);
+            const int dw = split_bucket(u);
+            d[j] = !valid ? kSplitNone : in_win ? dw : kSplitTailBase + static_cast<int>(r);
+            kl[j] = in_win ? u : tl - r * static_cast<unsigned>(kSplitHot);
         }
         if (base + kTile < hi) walk_load(key, v, base + kTile, hi, nk, nv);
         split_tile(sh, kl, d, vv, nb);
@@ -1409,7 +1442,7 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
             }
             if (t <= ranges) bin_off[(b * tiles + tile) * (ranges + 1) + t] = sh.bstart[kSplitTailBase + t] - ts;
         }
-        split_fold(sh, window);
+        split_fold(sh);
         __syncthreads();
     }
     // a chunk with fewer tiles than `tiles` (the last, short one) leaves its
@@ -1421,94 +1454,139 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
     if (bad) status[1 + b] = 1;
 }
 
+// The tail ranges' stream: for workgroup (chunk b, range r), the range's
+// segment of each tile slot of the chunk, slot after slot (lane order).  Each
+// wave holds a group of up to kTailGroup segments in registers: lane l,
+// register k describes segment g = 64k + l by its first stream position
+// P[k] and the offset that turns a stream position q of it into its bin
+// entry, base + A[k] + q (base: the group's first slot).  Segments past the group's end start at the group's
+// length, so no position of the group falls in them.
+constexpr int kTailGroup = 128;
+
+struct TailSegs {
+    unsigned P[kTailGroup / 64];
+    int A[kTailGroup / 64];
+    long long base;        // the group's first slot
+    unsigned count;        // entries in the group
+    int n;                 // segments in the group
+};
+
+__device__ __forceinline__ unsigned tail_reg(const unsigned (&x)[kTailGroup / 64], int m) {
+    static_assert(kTailGroup == 128, "two registers a lane");
+    const unsigned v = m < 64 ? x[0] : x[1];
+    return static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(v), m & 63));
+}
+__device__ __forceinline__ int tail_reg(const int (&x)[kTailGroup / 64], int m) {
+    const int v = m < 64 ? x[0] : x[1];
+    return __builtin_amdgcn_readlane(v, m & 63);
+}
+
+// Group [g0, g0 + gn) of chunk b's slots, range r: every wave reads the
+// group's bounds (hawk_split_hot wrote 0 <= o[r] <= o[r+1] <= 4096; the
+// clamps keep every read inside its slot whatever the plane holds).
+__device__ __forceinline__ TailSegs tail_segs(const unsigned* __restrict__ bin_off, long long b, int tiles, int ranges,
+                                              int r, int g0, int gn) {
+    const int lane = threadIdx.x & 63;
+    TailSegs S;
+    unsigned carry = 0u;
+#pragma unroll
+    for (int k = 0; k < kTailGroup / 64; ++k) {
+        const int g = k * 64 + lane;
+        unsigned lo = 0u, hi = 0u;
+        if (g < gn) {
+            const unsigned* o = bin_off + (b * tiles + g0 + g) * (ranges + 1);
+            const unsigned a = o[r], z = o[r + 1];
+            lo = a < static_cast<unsigned>(kTile) ? a : static_cast<unsigned>(kTile);
+            hi = z < lo ? lo : (z < static_cast<unsigned>(kTile) ? z : static_cast<unsigned>(kTile));
+        }
+        const unsigned c = hi - lo;
+        const unsigned incl = wave_inclusive_scan(c) + carry;
+        S.P[k] = incl - c;
+        S.A[k] = g * kTile + static_cast<int>(lo) - static_cast<int>(S.P[k]);
+        carry = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
+    }
+    S.count = carry;
+    S.n = gn;
+    S.base = (b * tiles + g0) * kTile;
+#pragma unroll
+    for (int k = 0; k < kTailGroup / 64; ++k)
+        if (k * 64 + lane >= gn) S.P[k] = carry;
+    return S;
+}
+
+// The batch at stream position qb: thread slot j of wave w takes position
+// qb + w*256 + j*64 + lane (positions past the group's end read as nothing).
+// Each window of 64 positions finds the segment of its first position with
+// two ballots, then steps over the segments that start inside it.
+template <class T>
+__device__ __forceinline__ void tail_load(const TailSegs& S, const unsigned short* __restrict__ bin_key,
+                                          const T* __restrict__ bin_val, unsigned qb, unsigned (&kk)[kWalkItems],
+                                          T (&vv)[kWalkItems]) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < kWalkItems; ++j) {
+        const unsigned qw = qb + static_cast<unsigned>(wave * (kWalkItems * 64) + j * 64);
+        const unsigned q = qw + static_cast<unsigned>(lane);
+        kk[j] = 0u;
+        vv[j] = T(0);
+        if (qw >= S.count) continue;
+        int g = -1;
+#pragma unroll
+        for (int k = 0; k < kTailGroup / 64; ++k) g += __popcll(__ballot(S.P[k] <= qw));
+        int a = tail_reg(S.A, g);
+        for (int m = g + 1; m < S.n; ++m) {
+            // both reads with every lane active: the lane read from must
+            // have computed its register select
+            const unsigned pm = tail_reg(S.P, m);
+            if (pm > qw + 63u) break;
+            const int am = tail_reg(S.A, m);
+            a = q >= pm ? am : a;
+        }
+        if (q < S.count) {
+            const long long at = S.base + a + static_cast<long long>(q);
+            kk[j] = bin_key[at];
+            vv[j] = bin_val[at];
+        }
+    }
+}
+
 // (chunk b, tail range r) = (blockIdx.x / ranges, blockIdx.x % ranges): keys
-// [kSplitHot*(r+1), +kSplitHot) of chunk b, read from the bin's slots in tile
-// order.
+// [kSplitHot*(r+1), +kSplitHot) of chunk b, read as a stream from the bin's
+// slots in tile order, kTile entries a batch, the next batch's reads in
+// flight while a batch is split and folded.
 template <class T>
 __global__ __launch_bounds__(kWalkThreads) void hawk_split_tail(
         long long cells, int tiles, int ranges, const unsigned short* __restrict__ bin_key,
         const T* __restrict__ bin_val, const unsigned* __restrict__ bin_off, T* __restrict__ parts) {
     __shared__ SplitShared<T> sh;
-    const int t = threadIdx.x;
-    const int wave = t >> 6;
-    const int lane = t & 63;
     const long long b = blockIdx.x / ranges;
     const int r = static_cast<int>(blockIdx.x % ranges);
     const long long klo = static_cast<long long>(kSplitHot) * (r + 1);
     const int window = cells - klo < kSplitHot ? static_cast<int>(cells - klo) : kSplitHot;
     split_clear(sh, window);
-    for (int g0 = 0; g0 < tiles; g0 += kSplitSegs) {
-        // the group's segments: hawk_split_hot wrote 0 <= o[r] <= o[r+1] <=
-        // 4096; the clamps keep every read inside its slot whatever the plane
-        // holds
-        const int gn = tiles - g0 < kSplitSegs ? tiles - g0 : kSplitSegs;
-        if (wave == 0) {
-            unsigned a0 = 0u, a1 = 0u;
-            if (lane < gn) {
-                const unsigned* o = bin_off + (b * tiles + g0 + lane) * (ranges + 1);
-                a0 = o[r] < static_cast<unsigned>(kTile) ? o[r] : static_cast<unsigned>(kTile);
-                a1 = o[r + 1] < a0 ? a0 : (o[r + 1] < static_cast<unsigned>(kTile) ? o[r + 1]
-                                                                                : static_cast<unsigned>(kTile));
-            }
-            sh.grp_lo[lane] = static_cast<unsigned short>(a0);
-            sh.grp_hi[lane] = static_cast<unsigned short>(a1);
-        }
-        __syncthreads();
-        for (int t0 = 0; t0 < gn;) {
-            if (wave == 0) {
-                const int tt = t0 + lane;
-                const unsigned c = tt < gn ? static_cast<unsigned>(sh.grp_hi[tt] - sh.grp_lo[tt]) : 0u;
-                const unsigned incl = wave_inclusive_scan(c);
-                const unsigned long long fits = __ballot(tt < gn && incl <= static_cast<unsigned>(kTile));
-                const int segs = __popcll(fits);
-                if (lane < segs) sh.seg_pos[lane] = static_cast<unsigned short>(incl - c);
-                if (lane == segs - 1) sh.batch_n = incl;
-                if (lane == 0) sh.batch_segs = static_cast<unsigned>(segs);
-            }
-            __syncthreads();
-            const int segs = static_cast<int>(sh.batch_segs);
-            const int total = static_cast<int>(sh.batch_n);
-            for (int g = wave; g < segs; g += kWalkWaves) {
-                const int tt = t0 + g;
-                const long long src = (b * tiles + g0 + tt) * kTile + sh.grp_lo[tt];
-                const unsigned pos = sh.seg_pos[g];
-                const unsigned c = static_cast<unsigned>(sh.grp_hi[tt] - sh.grp_lo[tt]);
-                for (unsigned i0 = 0; i0 < c; i0 += 4 * 64) {
-                    unsigned short kk[4];
-                    T vv[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const unsigned i = i0 + q * 64 + lane;
-                        kk[q] = i < c ? bin_key[src + i] : 0;
-                        vv[q] = i < c ? bin_val[src + i] : T(0);
-                    }
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const unsigned i = i0 + q * 64 + lane;
-                        if (i < c) {
-                            sh.key[pos + i] = kk[q];
-                            sh.val[pos + i] = vv[q];
-                        }
-                    }
-                }
-            }
-            __syncthreads();
+    for (int g0 = 0; g0 < tiles; g0 += kTailGroup) {
+        const int gn = tiles - g0 < kTailGroup ? tiles - g0 : kTailGroup;
+        const TailSegs S = tail_segs(bin_off, b, tiles, ranges, r, g0, gn);
+        unsigned nk[kWalkItems];
+        T nv[kWalkItems];
+        if (S.count > 0u) tail_load(S, bin_key, bin_val, 0u, nk, nv);
+        for (unsigned qb = 0; qb < S.count; qb += kTile) {
             unsigned kl[kWalkItems];
             int d[kWalkItems];
             T vv[kWalkItems];
 #pragma unroll
             for (int j = 0; j < kWalkItems; ++j) {
-                const int i = wave * (kWalkItems * 64) + j * 64 + lane;
-                const bool on = i < total;
-                kl[j] = on ? sh.key[i] : 0u;
-                vv[j] = on ? sh.val[i] : T(0);
-                d[j] = on ? split_bucket(kl[j]) : kSplitNone;
+                const unsigned q = qb + static_cast<unsigned>((threadIdx.x >> 6) * (kWalkItems * 64) + j * 64 +
+                                                              (threadIdx.x & 63));
+                kl[j] = nk[j];
+                vv[j] = nv[j];
+                d[j] = q < S.count ? split_bucket(kl[j]) : kSplitNone;
             }
-            __syncthreads();
+            if (qb + kTile < S.count) tail_load(S, bin_key, bin_val, qb + kTile, nk, nv);
             split_tile(sh, kl, d, vv, kSplitTailBase);
-            split_fold(sh, window);
+            split_fold(sh);
             __syncthreads();
-            t0 += segs;
         }
     }
     split_store(sh, b, cells, klo, window, parts);

@@ -553,6 +553,28 @@ def test_config5_at_the_benchmarks_own_shape(unit, gpu):
     assert ok.all()
 
 
+def test_ordered_scatter_past_one_tail_group(unit, gpu):
+    """N = 2^27 + 12295 Zipf keys into 65536 cells: 256 chunks of 524336
+    lanes, 129 tiles a chunk, so each tail range streams its bins in two
+    groups of slots (128, then one).  The serial walk's bits."""
+    import hawk_amd as hawk
+    n = (1 << 27) + 12295
+    cells = 1 << 16
+    g = rng(n)
+    key = ((g.zipf(1.1, n) - 1) % cells).astype(np.int32)
+    x = g.normal(size=n)
+    span = -(-n // 256)
+    assert -(-span // 4096) == 129
+    k = _load(unit, "ordered_add")
+    print(f"scatter zipf n={n} (two tail groups)", flush=True)
+    acc = dev(np.zeros(cells), gpu)
+    hawk.run(k, key=dev(key, gpu), x=dev(x, gpu), acc=acc)
+    got = host(acc)
+    want, status = O.ordered_scatter(key, x, np.zeros(cells), threads=16)
+    assert not status[1:].any()
+    assert got.tobytes() == want.tobytes()
+
+
 def test_ordered_scatter_past_one_tail_batch(unit, gpu):
     """N = 2^26 + 12345 Zipf keys into 65536 cells: 256 chunks of 262193 lanes,
     65 tiles a chunk, so the tail ranges read their bins in two batches (64
