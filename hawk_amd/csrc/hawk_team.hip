@@ -1118,7 +1118,7 @@ struct SplitShared {
             unsigned long long peer[kWalkWaves][kPeerSlots];           // fold: per-wave match masks (16 KiB)
         } f;
     };
-    alignas(16) unsigned cnt[kSplitStride][kWalkWaves];  // 3.5 KiB: bucket counts, bucket-major (a 64-byte row each)
+    unsigned cnt[kWalkWaves][kSplitStride];         // 3.5 KiB: bucket counts, a row per wave (lane b reads word b)
     unsigned bstart[kSplitStride + 1];              // bucket d holds [bstart[d], bstart[d+1])
 };
 
@@ -1169,7 +1169,7 @@ __device__ void split_tile(SplitShared<T>& sh, const unsigned (&kl)[kWalkItems],
         run[j] = total;
         total += static_cast<unsigned>(__popcll(mine[j]));
     }
-    if (lane < kSplitStride) sh.cnt[lane][wave] = total;
+    if (lane < kSplitStride) sh.cnt[wave][lane] = total;
     unsigned rank[kWalkItems];
 #pragma unroll
     for (int j = 0; j < kWalkItems; ++j) {
@@ -1183,16 +1183,12 @@ __device__ void split_tile(SplitShared<T>& sh, const unsigned (&kl)[kWalkItems],
     // and (a scan over the lanes) where bucket b starts
     unsigned before = 0u, sum = 0u;
     if (lane < nb) {
-        const uint4* row = reinterpret_cast<const uint4*>(&sh.cnt[lane][0]);
+        // word b of every wave's row: consecutive lanes, consecutive banks
 #pragma unroll
-        for (int q = 0; q < kWalkWaves / 4; ++q) {
-            const uint4 c = row[q];
-            const unsigned cw[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                before += q * 4 + i < wave ? cw[i] : 0u;
-                sum += cw[i];
-            }
+        for (int w = 0; w < kWalkWaves; ++w) {
+            const unsigned c = sh.cnt[w][lane];
+            before += w < wave ? c : 0u;
+            sum += c;
         }
     }
     const unsigned start = wave_inclusive_scan(sum) - sum;
