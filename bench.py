@@ -32,9 +32,11 @@ model named.
 The default run (config 2, without ``--only``) also records configs 1, 3, 4a,
 4b and 5 under ``config.configs``: each one's stages (HIP events, median of 5
 steps after 2 warm-ups), its dominant stage against its roofline and the
-oracle's rate on every host core.  Config 3's FLOPs are algorithmic: the
-traced operations of the forward, and of the VJP's forward and reverse
-without its checkpoint replay.
+oracle's rate on every host core (the median of at least 5 repetitions);
+config 5's record also carries its dominant stage's HBM traffic.  An
+FP64-bound stage (config 3) is set against the FP64 peak by the FLOPs it
+executes, measured by one more ``rocprofv3 --pmc`` pass (the FP64 VALU
+instruction counters over SQ_WAVES, per sample).
 """
 
 from __future__ import annotations
@@ -179,8 +181,9 @@ def workload(config: str, device):
                         n, threads)
         return dict(name="two-body leapfrog fwd + VJP (config 3)", n=n, kernels=kernels, work=work, cpu=cpu,
                     dtype="f64", bound="fp64",
-                    flops_basis="traced operations per sample, each + - * / and sqrt one: the forward (1280), "
-                                "the VJP's forward and reverse without its checkpoint replay")
+                    flops_basis="traced operations per sample (not measured in this run; the executed count "
+                                "needs the rocprofv3 pass that --no-traffic skips): the forward's, and the VJP's "
+                                "forward and reverse without its checkpoint replay")
     if config == "4a":
         n = 1 << 20
         g = np.random.default_rng(4)
@@ -623,8 +626,10 @@ def _with_pattern(w, device, per_stage: dict) -> dict:
 
 
 def _pmc_pass(counter: str, config: str) -> dict:
-    """One ``rocprofv3 --pmc <counter>`` pass over a short run of this bench
-    (plus the 1 GiB copy probe) in a child process: ``{kernel: [KiB per dispatch]}``."""
+    """One ``rocprofv3 --pmc <counter ...>`` pass over a short run of this bench
+    (plus the 1 GiB copy probe) in a child process: ``{kernel: [value per
+    dispatch]}`` for one counter, ``{counter: {kernel: [...]}}`` for several
+    (space-separated, one hardware pass)."""
     import csv
     import shutil
     import signal
@@ -634,7 +639,8 @@ def _pmc_pass(counter: str, config: str) -> dict:
     if prof is None:
         raise RuntimeError("rocprofv3 is not on PATH")
     out = Path(tempfile.mkdtemp(prefix="hawk_pmc_"))
-    cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(out), "-o", "run", "--",
+    names = counter.split()
+    cmd = [prof, "--pmc", *names, "--output-format", "csv", "-d", str(out), "-o", "run", "--",
            sys.executable, str(ROOT / "bench.py"), "--config", config, "--steps", "2", "--warmup", "1",
            "--no-cpu", "--no-traffic", "--copy-probe"]
     proc = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE, text=True,
@@ -648,12 +654,38 @@ def _pmc_pass(counter: str, config: str) -> dict:
     table = out / "run_counter_collection.csv"
     if not table.exists():       # the profiler can end badly after a complete run; only a missing table counts
         raise RuntimeError(f"rocprofv3 --pmc {counter} wrote no counters (exit {proc.returncode}): {err[-300:]}")
-    seen: dict = {}
+    seen: dict = {c: {} for c in names}
     with table.open() as f:
         for row in csv.DictReader(f):
-            if row["Counter_Name"] == counter:
-                seen.setdefault(_kernel_base(row["Kernel_Name"]), []).append(float(row["Counter_Value"]))
-    return seen
+            if row["Counter_Name"] in seen:
+                seen[row["Counter_Name"]].setdefault(_kernel_base(row["Kernel_Name"]), []).append(
+                    float(row["Counter_Value"]))
+    return seen[names[0]] if len(names) == 1 else seen
+
+
+#: The FP64 VALU instruction counters; FLOPs = 64 lanes x (ADD + MUL + TRANS + 2 FMA).
+FP64_COUNTERS = ("SQ_INSTS_VALU_ADD_F64", "SQ_INSTS_VALU_MUL_F64", "SQ_INSTS_VALU_FMA_F64",
+                 "SQ_INSTS_VALU_TRANS_F64", "SQ_WAVES")
+
+
+def measure_fp64(config: str, kernels: list) -> dict:
+    """Executed FP64 FLOPs per sample of each per-sample kernel (one sample a
+    lane): one ``rocprofv3 --pmc`` pass with the FP64 instruction counters and
+    SQ_WAVES; per wave, 64 x (ADD + MUL + TRANS + 2 FMA) / 64 lanes.  Dividing
+    by the waves the same pass counted keeps the figure right whichever share
+    of the chip's counters the pass samples."""
+    log(f"fp64: rocprofv3 --pmc {' '.join(FP64_COUNTERS)} pass over --config {config}")
+    seen = _pmc_pass(" ".join(FP64_COUNTERS), config)
+    out = {}
+    for k in kernels:
+        if not all(k in seen[c] for c in FP64_COUNTERS):
+            raise RuntimeError(f"fp64 counters: {k} was not seen")
+        med = {c: statistics.median(seen[c][k]) for c in FP64_COUNTERS}
+        per_wave = (med["SQ_INSTS_VALU_ADD_F64"] + med["SQ_INSTS_VALU_MUL_F64"] + med["SQ_INSTS_VALU_TRANS_F64"]
+                    + 2.0 * med["SQ_INSTS_VALU_FMA_F64"]) / med["SQ_WAVES"]
+        out[k] = {"flops_per_sample": per_wave, "counts_per_wave": {c.replace("SQ_INSTS_VALU_", ""): round(
+            med[c] / med["SQ_WAVES"], 2) for c in FP64_COUNTERS[:4]}}
+    return out
 
 
 def measure_traffic(config: str, kernels: list, occurrence: int = 0, per_step: int = 1) -> dict:
@@ -688,6 +720,22 @@ def _stages_of(w) -> list:
                 label = label.split("#")[0] + "#" + str(int(label.split("#")[1]) + 1 if "#" in label else 2)
             stages.append((label, launch))
     return stages
+
+
+def use_fp64_counts(w, per_stage: dict, counts: dict) -> None:
+    """Replace each FP64-bound stage's FLOPs per sample by the executed count
+    measured by :func:`measure_fp64` (the roofline's numerator)."""
+    n = w["n"]
+    for label, rec in per_stage.items():
+        c = counts.get(label)
+        if not c:
+            continue
+        f_per = c["flops_per_sample"]
+        tf = f_per * n / (rec["ms"] * 1e-3) / 1e12
+        rec.update({"flops_per_sample": round(f_per, 2), "fp64_counts_per_wave": c["counts_per_wave"],
+                    "achieved_TFLOPs": tf, "fp64_frac": tf / FP64_PEAK_TFLOPS})
+    w["flops_basis"] = ("FP64 FLOPs executed, per sample: 64 x (ADD + MUL + TRANS + 2 FMA) VALU instructions "
+                        "per wave over SQ_WAVES, one rocprofv3 --pmc pass of this bench")
 
 
 def time_steps(w, steps: int, warmup: int) -> dict:
@@ -762,17 +810,18 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_rate(w, threads: int, profile: str, seconds: float) -> tuple:
+def cpu_rate(w, threads: int, profile: str, seconds: float, min_reps: int = 5) -> tuple:
     """Samples/s of the oracle's step on ``threads`` threads in build
     ``profile`` (one warm-up, then repetitions for about ``seconds``; at
-    least one): ``(rate, repetitions, seconds of CPU work)``."""
+    least ``min_reps``): ``(rate, repetitions, seconds of CPU work)``; the
+    rate is the median repetition's."""
     import oracle_lib as O
     O.use_profile(profile)
     cores = w.get("cpu_threads") or threads
     w["cpu"](cores)
     times = []
     begin = time.perf_counter()
-    while not times or (time.perf_counter() - begin < seconds and len(times) < 2000):
+    while len(times) < min_reps or (time.perf_counter() - begin < seconds and len(times) < 2000):
         t = time.perf_counter()
         w["cpu"](cores)
         times.append(time.perf_counter() - t)
@@ -783,26 +832,63 @@ def cpu_rate(w, threads: int, profile: str, seconds: float) -> tuple:
 OTHER_CONFIGS = ("1", "3", "4a", "4b", "5")
 
 
-def config_record(config: str, device, steps: int = 5, warmup: int = 2) -> dict:
+#: Configurations whose record measures the dominant stage's HBM traffic too.
+TRAFFIC_CONFIGS = ("5",)
+
+
+def _fp64_stages(w, per_stage: dict) -> list:
+    """The FP64-bound per-sample stages (one sample a lane), by label."""
+    if w.get("bound") != "fp64":
+        return []
+    return [label for label in per_stage if label.split("#")[0] not in STAGE_KERNELS]
+
+
+def _traffic_of(config: str, per_stage: dict, dominant: str):
+    if dominant in STAGE_KERNELS:
+        kernels, occurrence, per_step = STAGE_KERNELS[dominant], 0, 1
+    else:
+        base_label = dominant.split("#")[0]
+        kernels = STAGE_KERNELS.get(base_label, (base_label,))
+        occurrence = int(dominant.split("#")[1]) - 1 if "#" in dominant else 0
+        per_step = sum(1 for x in per_stage if x.split("#")[0] == base_label)
+    return measure_traffic(config, kernels, occurrence, per_step)
+
+
+def config_record(config: str, device, steps: int = 5, warmup: int = 2, pmc: bool = True) -> dict:
     """One configuration's record for the default run: its stages timed on
     the GPU (HIP events, median of ``steps``), the dominant stage against its
-    roofline, and the oracle on every host core (one timed repetition after a
+    roofline (an FP64-bound one by its executed FLOPs, and for
+    :data:`TRAFFIC_CONFIGS` with its HBM traffic, when ``pmc``), and the
+    oracle on every host core (the median of at least 5 repetitions after a
     warm-up)."""
     import torch
     log(f"config {config}: record")
     w = workload(config, device)
     t = time_steps(w, steps, warmup)
     ceiling = _with_pattern(w, device, t["per_stage"])
-    rate, reps, cpu_s = cpu_rate(w, host_cores(), "native", 0.0)
+    traffic = None
+    if pmc:
+        try:
+            fp64 = _fp64_stages(w, t["per_stage"])
+            if fp64:
+                use_fp64_counts(w, t["per_stage"], measure_fp64(config, fp64))
+            if config in TRAFFIC_CONFIGS:
+                dominant = max(t["per_stage"], key=lambda k: t["per_stage"][k]["ms"])
+                traffic = round(_traffic_of(config, t["per_stage"], dominant)["bytes"])
+                log(f"config {config}: traffic of {dominant}: {traffic / 1e6:.1f} MB per launch")
+        except Exception as exc:        # counters are evidence, not the measurement
+            log(f"config {config}: counters not measured: {exc}")
+    rate, reps, cpu_s = cpu_rate(w, host_cores(), "native", 0.0, min_reps=5)
     rec = {"workload": w["name"], "N": w["n"], "dtype": w["dtype"], "ms_per_step": round(t["ms_step"], 5),
            "samples_per_s": w["n"] / (t["ms_step"] * 1e-3),
            "stages": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                       for k, v in t["per_stage"].items()},
-           "roofline": roofline_of(w, t["per_stage"]),
+           "roofline": roofline_of(w, t["per_stage"], traffic),
            **({"pattern_ceiling": ceiling} if ceiling else {}),
            "cpu_baseline": {"value": rate, "unit": "samples/s", "cores": w.get("cpu_threads") or host_cores(),
-                            "kind": "port", "sample": f"the full step on the C oracle (native profile), "
-                                                      f"{reps} repetition(s) after 1 warm-up"}}
+                            "kind": "port", "sample": f"the full step on the C oracle (native profile), median of "
+                                                      f"{reps} repetitions ({cpu_s:.1f} s of CPU work) after 1 "
+                                                      "warm-up"}}
     del w
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -848,16 +934,14 @@ def main() -> int:
     dominant = max(per_stage, key=lambda k: per_stage[k]["ms"])
     d = per_stage[dominant]
     traffic = None
+    if not args.no_traffic and _fp64_stages(w, per_stage):
+        try:
+            use_fp64_counts(w, per_stage, measure_fp64(args.config, _fp64_stages(w, per_stage)))
+        except Exception as exc:        # counters are evidence, not the measurement
+            log(f"fp64 FLOPs not measured: {exc}")
     if not args.no_traffic:
         try:
-            if dominant in STAGE_KERNELS:
-                kernels, occurrence, per_step = STAGE_KERNELS[dominant], 0, 1
-            else:
-                base_label = dominant.split("#")[0]
-                kernels = STAGE_KERNELS.get(base_label, (base_label,))
-                occurrence = int(dominant.split("#")[1]) - 1 if "#" in dominant else 0
-                per_step = sum(1 for x in per_stage if x.split("#")[0] == base_label)
-            tr = measure_traffic(args.config, kernels, occurrence, per_step)
+            tr = _traffic_of(args.config, per_stage, dominant)
             traffic = round(tr["bytes"])
             log(f"traffic of {dominant}: {traffic / 1e6:.1f} MB per launch "
                 f"(algorithmic {d['bytes_per_sample'] * n / 1e6:.1f} MB; counter factors {tr['factors']})")
@@ -895,7 +979,7 @@ def main() -> int:
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
         for c in OTHER_CONFIGS:
-            records[c] = config_record(c, device)
+            records[c] = config_record(c, device, pmc=not args.no_traffic)
     line = {
         "metric": METRIC, "value": n / (ms_step * 1e-3), "unit": "samples/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
