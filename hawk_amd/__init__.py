@@ -42,7 +42,7 @@ _LAZY = {
     "samples_last": ("layout", "samples_last"),
 }
 _SUBMODULES = ("math", "diff", "runtime", "artifact", "compile", "ir", "emit_hip", "trace", "chaining", "policy",
-               "layout", "latency")
+               "layout")
 
 __all__ = ["Grid", "HawkError", "Index", "Matrix", "Mutable", "Param", "Scalar", "Table", "TensorType", "Terminated",
            "Vector",

@@ -110,11 +110,15 @@ def test_the_build_records_what_the_row_says(tmp_path):
     assert bundle.digest == manifest["digest"]
 
 
-def test_the_latency_probe_builds_for_gfx950(tmp_path):
-    """hawk_amd.latency's probe kernel compiles through the build's hipRTC path
-    and carries the ABI tag every loaded code object is checked for."""
-    from hawk_amd import latency
+def test_the_benchs_latency_probe_builds_for_gfx950(tmp_path):
+    """bench.py --latency's probe kernel compiles through the build's hipRTC
+    path and carries the ABI tag every loaded code object is checked for; it
+    is a measurement mode of the bench, not part of the package."""
+    import importlib
+
+    import bench
     from hawk_amd.compile import compile_source
-    code, _key, hit = compile_source(latency._SOURCE, "hawk_latency", cache_dir=tmp_path)
+    code, _key, hit = compile_source(bench.LATENCY_SOURCE, "hawk_latency", cache_dir=tmp_path)
     assert not hit and code[:4] == b"\x7fELF" and b"aether-abi/2" in code
-    assert sorted(latency.PROBES) == list(range(len(latency.PROBES)))
+    assert sorted(bench.LATENCY_PROBES) == list(range(len(bench.LATENCY_PROBES)))
+    assert importlib.util.find_spec("hawk_amd.latency") is None
