@@ -102,12 +102,12 @@ __global__ __launch_bounds__(256) void hawk_sum_fold(const T* __restrict__ lanes
 // `BANDED`, hawk/emit/team.py:26-49 and :225-245): every partial is a band, a
 // normalised double-double (h, l) with |l| <= ulp(h)/2, folded in the same
 // fixed order as the float64 stages, and the stored cell is the final band's
-// h.  The adds are those of Hida, Li and Bailey's QD library: a term joins a
-// band by TwoSum of the leading parts plus a quick renormalisation, two bands
-// join by TwoSum of the leading and of the low parts and two
-// renormalisations.  Knuth's TwoSum is exact in either operand order, so both
-// adds are symmetric.  A non-finite leading sum drops the low part, so Inf and
-// NaN follow IEEE through h.
+// h.  Two bands join as in Hida, Li and Bailey's QD library: TwoSum of the
+// leading and of the low parts and two quick renormalisations; Knuth's TwoSum
+// is exact in either operand order, so the add is symmetric.  A virtual
+// lane's run of terms accumulates by Neumaier's compensated sum and becomes a
+// band at its end (lane_add, lane_band).  A non-finite leading sum drops the
+// low part, so Inf and NaN follow IEEE through h.
 // ---------------------------------------------------------------------------
 struct Band {
     double h, l;
@@ -124,10 +124,29 @@ __device__ __forceinline__ Band band_quick(double a, double b) {
     return Band{s, b - (s - a)};
 }
 
-__device__ __forceinline__ Band band_add_term(Band a, double x) {
-    const Band s = band_two(a.h, x);
-    if (!((s.h - s.h) == 0.0)) return Band{s.h, 0.0};
-    return band_quick(s.h, s.l + a.l);
+// A virtual lane's run of rows (the banded ordered sum): Neumaier's
+// compensated sum, the running sum s one addition a row and each addition's
+// exact error added to c beside it, so a row costs the chain one dependent
+// add; renormalised into a band once, at the run's end, by TwoSum of (s, c);
+// a non-finite s drops c.
+struct LaneSum {
+    double s, c;
+};
+
+__device__ __forceinline__ void lane_add(LaneSum& a, double x) {
+    // the error by TwoSum: the exact error of t = s + x whichever operand is
+    // larger, so the same value as Neumaier's branch on |s| >= |x|, without a
+    // compare and select
+    const double t = a.s + x;
+    const double bb = t - a.s;
+    a.c = a.c + ((a.s - (t - bb)) + (x - bb));
+    a.s = t;
+}
+
+__device__ __forceinline__ Band lane_band(LaneSum a) {
+    const Band b = band_two(a.s, a.c);
+    const bool finite = (a.s - a.s) == 0.0;
+    return Band{finite ? b.h : a.s, finite ? b.l : 0.0};
 }
 
 __device__ __forceinline__ Band band_add(Band a, Band b) {
@@ -138,43 +157,110 @@ __device__ __forceinline__ Band band_add(Band a, Band b) {
     return band_quick(s.h, s.l + t.l);
 }
 
-constexpr size_t kBandLanesBytes = sizeof(Band) * kVirtualLanes;
+// The banded ordered sum's geometry, reference hawk/emit/team.py:26-30
+// (BAND_LANES, BAND_VIRTUAL_LANES) and :225-245: group g's 128 virtual lanes
+// l = g*128 + t each add rows l, l + 8192, ... as terms of one band.
+constexpr int kBandLanes = 128;
+constexpr int kBandVirtual = kBandLanes * kGroups;   // 8192
+constexpr size_t kBandLanesBytes = sizeof(Band) * kBandVirtual;
 constexpr size_t kBandGpBytes = sizeof(Band) * kGroups;
 constexpr size_t kBandSumScratch = kBandLanesBytes + kBandGpBytes + 256;
 
-// Virtual lane l adds u[l], u[l+65536], ... as terms of its band, in order
-// from (+0, +0); kSumUnroll loads in flight before their adds.  Clears the
-// fold's ticket one launch ahead of the fold.
-__global__ __launch_bounds__(kLaneBlock) void hawk_band_sum_lanes(const double* __restrict__ u, long long n,
-                                                                   Band* __restrict__ lanes,
-                                                                   unsigned* __restrict__ ticket) {
-    const long long l = static_cast<long long>(blockIdx.x) * kLaneBlock + threadIdx.x;
-    if (l == 0) *ticket = 0u;
-    Band s{0.0, 0.0};
-    long long r = l;
-    constexpr long long kStep = kVirtualLanes;
-    for (; r + (kSumUnroll - 1) * kStep < n; r += kSumUnroll * kStep) {
-        double a[kSumUnroll];
+// One workgroup per kBandChains virtual lanes.  The first kBandChainWaves
+// waves are the chains: lane c < kBandPerWave of chain wave w adds column
+// w * kBandPerWave + c of each stage (kBandStage row blocks of kBandChains
+// contiguous values) to its lane sum, row after row, from an LDS buffer.
+// The kBandLoaders threads after them read the rows:
+// each stage into registers three stages ahead of the chains and into the
+// LDS buffer one stage ahead, so a read has two stages' worth of chain work
+// to arrive.  Clears the fold's ticket one launch ahead of the fold.
+constexpr int kBandChains = 32;
+// One chain wave: measured on MI355X at N = 2^26, 236 us against 282 and 358
+// with the chains spread over two and four waves.
+constexpr int kBandChainWaves = 1;
+constexpr int kBandPerWave = kBandChains / kBandChainWaves;
+constexpr int kBandStage = 64;
+constexpr int kBandLoaders = 256;
+constexpr int kBandThreads = 64 * kBandChainWaves + kBandLoaders;
+constexpr int kBandPer = kBandStage * kBandChains / kBandLoaders;   // values a loader reads a stage
+static_assert(kBandVirtual % kBandChains == 0, "whole workgroups of chains");
+
+__global__ __launch_bounds__(kBandThreads) void hawk_band_sum_lanes(const double* __restrict__ u, long long n,
+                                                                     Band* __restrict__ lanes,
+                                                                     unsigned* __restrict__ ticket) {
+    __shared__ double buf[2][kBandStage * kBandChains];
+    const int t = threadIdx.x;
+    const bool chains = t < 64 * kBandChainWaves;
+    const int lt = t - 64 * kBandChainWaves;     // a loader's index
+    const int col = (t >> 6) * kBandPerWave + (t & 63);   // a chain lane's column
+    const bool chain = chains && (t & 63) < kBandPerWave;
+    const long long l0 = static_cast<long long>(blockIdx.x) * kBandChains;
+    if (blockIdx.x == 0 && t == 0) *ticket = 0u;
+    // row blocks of lane l0, the workgroup's longest lane, and its stages
+    const long long blocks = n > l0 ? (n - l0 + kBandVirtual - 1) / kBandVirtual : 0;
+    const long long stages = (blocks + kBandStage - 1) / kBandStage;
+    double r0[kBandPer], r1[kBandPer];
+    auto load = [&](long long st, double (&reg)[kBandPer]) {
+        if (chains || st >= stages) return;
 #pragma unroll
-        for (int k = 0; k < kSumUnroll; ++k) a[k] = __builtin_nontemporal_load(u + r + k * kStep);
+        for (int q = 0; q < kBandPer; ++q) {
+            const int i = lt + q * kBandLoaders;
+            const long long r = (st * kBandStage + i / kBandChains) * kBandVirtual + l0 + i % kBandChains;
+            reg[q] = r < n ? __builtin_nontemporal_load(u + r) : 0.0;
+        }
+    };
+    auto store = [&](long long st, int slot, const double (&reg)[kBandPer]) {
+        if (chains || st >= stages) return;
 #pragma unroll
-        for (int k = 0; k < kSumUnroll; ++k) s = band_add_term(s, a[k]);
+        for (int q = 0; q < kBandPer; ++q) buf[slot][lt + q * kBandLoaders] = reg[q];
+    };
+    const long long mine = chain && l0 + col < n ? (n - l0 - col + kBandVirtual - 1) / kBandVirtual : 0;
+    LaneSum acc{0.0, 0.0};
+    load(0, r0);
+    load(1, r1);
+    store(0, 0, r0);
+    load(2, r0);
+    __syncthreads();
+    for (long long st = 0; st < stages; ++st) {
+        const int slot = static_cast<int>(st & 1);
+        if (chain) {
+            const long long left = mine - st * kBandStage;
+            const int m = left < 0 ? 0 : (left < kBandStage ? static_cast<int>(left) : kBandStage);
+            double v[kBandStage];
+#pragma unroll
+            for (int k = 0; k < kBandStage; ++k) v[k] = buf[slot][k * kBandChains + col];
+            if (m == kBandStage) {
+#pragma unroll
+                for (int k = 0; k < kBandStage; ++k) lane_add(acc, v[k]);
+            } else {
+                for (int k = 0; k < m; ++k) lane_add(acc, v[k]);
+            }
+        }
+        // stage st+1 sits in r1 (st even) or r0 (st odd), read two stages ago;
+        // that register set then takes stage st+3
+        if (slot == 0) {
+            store(st + 1, 1, r1);
+            load(st + 3, r1);
+        } else {
+            store(st + 1, 0, r0);
+            load(st + 3, r0);
+        }
+        __syncthreads();
     }
-    for (; r < n; r += kStep) s = band_add_term(s, u[r]);
-    lanes[l] = s;
+    if (chain) lanes[l0 + col] = lane_band(acc);
 }
 
-// Group g's 1024 lane bands by the halving tree into gp[g]; the last group
+// Group g's 128 lane bands by the halving tree into gp[g]; the last group
 // to finish folds the 64 group bands by the same tree and stores h.
 __global__ __launch_bounds__(256) void hawk_band_sum_fold(const Band* __restrict__ lanes, Band* __restrict__ gp,
                                                           unsigned* __restrict__ ticket, double* __restrict__ out) {
-    __shared__ Band sh[kFoldLanes];
+    __shared__ Band sh[kBandLanes];
     __shared__ unsigned last;
     const int g = blockIdx.x;
     const int t = threadIdx.x;
-    for (int i = t; i < kFoldLanes; i += 256) sh[i] = lanes[g * kFoldLanes + i];
+    for (int i = t; i < kBandLanes; i += 256) sh[i] = lanes[g * kBandLanes + i];
     __syncthreads();
-    for (int w = kFoldLanes / 2; w > 0; w >>= 1) {
+    for (int w = kBandLanes / 2; w > 0; w >>= 1) {
         for (int i = t; i < w; i += 256) sh[i] = band_add(sh[i], sh[i + w]);
         __syncthreads();
     }
@@ -2107,7 +2193,7 @@ int hk_band_ordered_sum_f64(const double* u, int64_t n, double* out, void* scrat
     auto* gp = reinterpret_cast<Band*>(base + kBandLanesBytes);
     auto* ticket = reinterpret_cast<unsigned*>(base + kBandLanesBytes + kBandGpBytes);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(hawk_band_sum_lanes, dim3(kVirtualLanes / kLaneBlock), dim3(kLaneBlock), 0, s, u,
+    hipLaunchKernelGGL(hawk_band_sum_lanes, dim3(kBandVirtual / kBandChains), dim3(kBandThreads), 0, s, u,
                        static_cast<long long>(n), lanes, ticket);
     int rc = launch_error("hawk_band_sum_lanes launch");
     if (rc != HK_OK) return rc;

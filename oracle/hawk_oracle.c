@@ -399,10 +399,24 @@ static hko_band band_quick(double a, double b) {        /* quick-two-sum, |a| >=
     return r;
 }
 
-static hko_band band_add_term(hko_band a, double x) {
-    hko_band s = band_two(a.h, x);
-    if (!fin(s.h)) { s.l = 0.0; return s; }
-    return band_quick(s.h, s.l + a.l);
+/* A virtual lane's run of rows (the banded ordered sum): Neumaier's
+ * compensated sum, the running sum s one addition a row and each addition's
+ * exact error added to c beside it (the larger operand first), renormalised
+ * into a band once, at the run's end, by TwoSum of (s, c); a non-finite s
+ * drops c.  (The reference's accumulator likewise renormalises only every
+ * BandAccum::period terms, hawk/emit/team.py:32-34.) */
+typedef struct { double s, c; } hko_lane;
+
+static void lane_add(hko_lane* a, double x) {
+    const double t = a->s + x;
+    const double e = fabs(a->s) >= fabs(x) ? (a->s - t) + x : (x - t) + a->s;
+    a->c = a->c + e;
+    a->s = t;
+}
+
+static hko_band lane_band(hko_lane a) {
+    if (!fin(a.s)) { const hko_band r = {a.s, 0.0}; return r; }
+    return band_two(a.s, a.c);
 }
 
 static hko_band band_add(hko_band a, hko_band b) {
@@ -486,17 +500,21 @@ HKO_EXPORT double hko_band_sample_sum(const double* t, int64_t n) {
     return out;
 }
 
-/* The banded ordered sum: the ordered sum's fixed tree (65536 virtual lanes adding their rows in order,
- * the halving tree over each group of 1024 lanes, then over the 64 groups) with band accumulators: a
- * lane adds each row as a term, the trees add bands. */
+/* The banded ordered sum, reference hawk/emit/team.py:26-30 (BAND_LANES = 128, BAND_VIRTUAL_LANES =
+ * 128 x 64) and :225-245 (the `cells` form of `_block_part`): group g's 128 virtual lanes l = g*128 + t
+ * each add rows l, l + 8192, ... in order into one lane accumulator from (+0, +0), the halving tree
+ * w = 64..1 over the group's 128 bands gives gp[g], and the tree w = 32..1 over the 64 group bands
+ * (:160-171) gives the sum; the cell is the final band's h. */
+#define HKO_BW 128
+#define HKO_BV (HKO_BW * HKO_G)
 static hko_band band_group_part(const double* u, int64_t rows, int g) {
-    hko_band sh[HKO_W];
-    for (int t = 0; t < HKO_W; ++t) sh[t].h = sh[t].l = 0.0;
-    for (int64_t b = (int64_t)g * HKO_W; b < rows; b += HKO_V) {
-        const int64_t m = rows - b < HKO_W ? rows - b : HKO_W;
-        for (int64_t t = 0; t < m; ++t) sh[t] = band_add_term(sh[t], u[b + t]);
+    hko_band sh[HKO_BW];
+    for (int t = 0; t < HKO_BW; ++t) {
+        hko_lane a = {0.0, 0.0};
+        for (int64_t r = (int64_t)g * HKO_BW + t; r < rows; r += HKO_BV) lane_add(&a, u[r]);
+        sh[t] = lane_band(a);
     }
-    for (int w = HKO_W / 2; w > 0; w >>= 1)
+    for (int w = HKO_BW / 2; w > 0; w >>= 1)
         for (int i = 0; i < w; ++i) sh[i] = band_add(sh[i], sh[i + w]);
     return sh[0];
 }

@@ -1584,12 +1584,18 @@ def _band_data(kind, n):
     if kind == "exact_integers":        # every partial fits a double-double
         k = rng(n).integers(-(1 << 40), 1 << 40, n, dtype=np.int64)
         return k.astype(np.float64) * 2.0 ** -20
+    if kind == "one_lane":              # seven terms on one virtual lane's rows (l, l + 8192, ...), zeros elsewhere
+        from test_oracle import BAND_LANE_TERMS
+        x = np.zeros(n)
+        rows = 5 + 8192 * np.arange(7)
+        x[rows[rows < n]] = np.array(BAND_LANE_TERMS)[rows < n]
+        return x
     g = rng(n + 7)
     return g.normal(size=n) * np.exp(g.normal(size=n) * 8)
 
 
-@pytest.mark.parametrize("kind", ["cancel_lanes", "reference_series", "exact_integers", "wide"])
-@pytest.mark.parametrize("n", [1, 31, 33, 1000, 65537, 3 * 65536 + 777, (1 << 20) + 5])
+@pytest.mark.parametrize("kind", ["cancel_lanes", "reference_series", "exact_integers", "wide", "one_lane"])
+@pytest.mark.parametrize("n", [1, 31, 33, 1000, 8193, 65537, 3 * 65536 + 777, (1 << 20) + 5])
 def test_banded_sums_are_the_oracles_bits_and_replay(unit_banded, gpu, kind, n):
     """The banded mode's sample sums on the device (band rows in the stage, the
     banded canonical finish, the banded ordered tree) are the oracle's bits,
@@ -1605,6 +1611,9 @@ def test_banded_sums_are_the_oracles_bits_and_replay(unit_banded, gpu, kind, n):
         hawk.run(k, x=X, **cells)
         got = tuple(float(host(cells[c])[0]) for c in ("s", "s_sq", "s_ord"))
         assert np.array(got).tobytes() == np.array(want).tobytes(), (got, want)
+    if kind == "one_lane" and n > 6 * 8192 + 5:
+        from test_oracle import BAND_LANE_TERMS
+        assert want[2] == BAND_LANE_TERMS[1]          # the reference's geometry: one band of seven terms
 
 
 def test_banded_sums_on_the_device_hold_the_reference_bounds(unit_banded, gpu):

@@ -674,6 +674,28 @@ def test_band_sums_where_the_plain_ordered_tree_loses_terms():
     assert O.band_sample_sum(x) == 2.0 * V
 
 
+#: Seven terms whose exact sum is the second (the rest cancel in pairs), and
+#: which a double-double keeps only when they join one band in this order: as
+#: the bands of seven lanes folded by the 64-group tree the sum comes out 0.
+BAND_LANE_TERMS = [9.4039548065783e-37, -1.1419282818997418e-54, 8.077935669463161e-28, -9.4039548065783e-37,
+                   -8.077935669463161e-28, -1.75, 1.75]
+
+
+@pytest.mark.parametrize("lane", [0, 5, 127, 128, 8191])
+def test_band_ordered_sum_adds_one_virtual_lanes_rows_as_one_band(lane):
+    """The reference's banded geometry (hawk/emit/team.py:26-30, :225-245):
+    128 lanes a group, 8192 virtual lanes, lane l adding rows l, l + 8192, ...
+    as terms of one band.  With the seven terms above on rows lane + 8192 j
+    and zeros elsewhere, the sum is exactly the second term; the 65536-lane
+    geometry would fold them as seven lanes' bands and give 0."""
+    from fractions import Fraction
+    n = 7 * 8192 + 3
+    x = np.zeros(n)
+    x[lane + 8192 * np.arange(7)] = BAND_LANE_TERMS
+    assert sum(Fraction(v) for v in BAND_LANE_TERMS) == Fraction(BAND_LANE_TERMS[1])
+    assert O.band_ordered_sum(x) == BAND_LANE_TERMS[1]
+
+
 def _ulp53(got: float, exact) -> float:
     from fractions import Fraction
     if exact == 0:
