@@ -32,6 +32,9 @@ _LAZY = {
     "Kernel": ("trace", "Kernel"),
     "Value": ("trace", "Value"),
     "sum": ("trace", "sum"),
+    "max": ("trace", "max"),
+    "min": ("trace", "min"),
+    "mean": ("trace", "mean"),
     "scatter": ("trace", "scatter"),
     "chain": ("chaining", "chain"),
     "steps": ("trace", "steps"),

@@ -66,6 +66,8 @@ def _declare(lib) -> None:
         "hk_rows_finish_scratch_bytes": (SZ, [I64]),
         "hk_rows_finish_f64": (I, [V, V, I64, V, V, V]),
         "hk_rows_finish_f32": (I, [V, V, I64, V, V, V]),
+        "hk_rows_extreme_f64": (I, [V, I64, ctypes.c_int32, V, V, V]),
+        "hk_rows_extreme_f32": (I, [V, I64, ctypes.c_int32, V, V, V]),
         "hk_band_rows_finish_scratch_bytes": (SZ, [I64]),
         "hk_band_rows_finish_f64": (I, [V, V, I64, V, V, V]),
         "hk_band_ordered_sum_scratch_bytes": (SZ, []),
@@ -421,6 +423,20 @@ def rows_finish_f32(hi: int, comp: int, rows: int, out: int, scratch: int, strea
     """The same finish of float32 rows, in float32."""
     check(lib().hk_rows_finish_f32(ctypes.c_void_p(hi), ctypes.c_void_p(comp), int(rows), ctypes.c_void_p(out),
                                    ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
+
+
+def rows_extreme(hi: int, rows: int, op: int, out: int, scratch: int, stream: int = 0) -> None:
+    """The finish of ``hawk.max`` (op 1) / ``hawk.min`` (op 2): ``rows``
+    row extremes folded in the canonical tree, the extreme stored at ``out``.
+    Scratch: :func:`rows_finish_scratch_bytes` bytes."""
+    check(lib().hk_rows_extreme_f64(ctypes.c_void_p(hi), int(rows), int(op), ctypes.c_void_p(out),
+                                    ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
+
+
+def rows_extreme_f32(hi: int, rows: int, op: int, out: int, scratch: int, stream: int = 0) -> None:
+    """The same finish of float32 rows."""
+    check(lib().hk_rows_extreme_f32(ctypes.c_void_p(hi), int(rows), int(op), ctypes.c_void_p(out),
+                                    ctypes.c_void_p(scratch), ctypes.c_void_p(stream or None)))
 
 
 def band_rows_finish_scratch_bytes(rows: int) -> int:

@@ -402,6 +402,59 @@ __global__ __launch_bounds__(256) void hawk_rows_levels(T* __restrict__ buf, lon
     if (threadIdx.x == 0) *out = finite_bits(vh[0]) ? vh[0] + vc[0] : vh[0];
 }
 
+// The rows' finish of hawk.max / hawk.min (reference hawk/_cells.py:66-71 and
+// `finish`): the same tree, every add the extreme a > b ? a : b (max) or
+// a < b ? a : b (min) of (the earlier partial, the later); exact, and a NaN
+// partial on the left gives way to the right one.  OP 1 is max, 2 min.
+template <int OP, class T>
+__device__ __forceinline__ T tree_extreme(T a, T b) {
+    return OP == 1 ? (a > b ? a : b) : (a < b ? a : b);
+}
+
+template <class T, int OP>
+__global__ __launch_bounds__(kRowSlots) void hawk_rows_ext_leaves(const T* __restrict__ hi, long long rows,
+                                                                  T* __restrict__ leaf_h) {
+    __shared__ T sh[kRowSlots];
+    const int s = threadIdx.x;
+    const long long lo = static_cast<long long>(blockIdx.x) * kRowLeaf;
+    const long long rest = rows - lo;
+    const int cnt = rest < kRowLeaf ? static_cast<int>(rest) : static_cast<int>(kRowLeaf);
+    const int live = cnt < kRowSlots ? cnt : kRowSlots;
+    if (s < live) {
+        T h = hi[lo + s];
+        for (int k = 1; k < kRowTerms; ++k) {
+            const int m = live < cnt - k * kRowSlots ? live : cnt - k * kRowSlots;
+            if (m <= 0 || s >= m) break;
+            h = tree_extreme<OP>(h, hi[lo + k * kRowSlots + s]);
+        }
+        sh[s] = h;
+    }
+    __syncthreads();
+    for (int off = kRowSlots / 2; off > 0; off >>= 1) {
+        const int lim = live > off ? (off < live - off ? off : live - off) : 0;
+        if (s < lim) sh[s] = tree_extreme<OP>(sh[s], sh[s + off]);
+        __syncthreads();
+    }
+    if (s == 0) leaf_h[blockIdx.x] = sh[0];
+}
+
+template <class T, int OP>
+__global__ __launch_bounds__(256) void hawk_rows_ext_levels(T* __restrict__ buf, long long leaves,
+                                                            T* __restrict__ out) {
+    T* vh = buf;
+    T* nh = buf + leaves;
+    long long m = leaves;
+    while (m > 1) {
+        const long long pairs = m / 2;
+        for (long long p = threadIdx.x; p < pairs; p += 256) nh[p] = tree_extreme<OP>(vh[2 * p], vh[2 * p + 1]);
+        if ((m & 1) && threadIdx.x == 0) nh[pairs] = vh[m - 1];
+        __syncthreads();
+        T* th = vh; vh = nh; nh = th;
+        m = pairs + (m & 1);
+    }
+    if (threadIdx.x == 0) *out = vh[0];
+}
+
 // The banded rows' finish: the canonical tree above (leaves of 4096 rows over
 // 256 slots, the in-leaf halving tree, the leaves pairwise level by level)
 // with every add a band add; the cell is the final band's h.  Row r of the
@@ -1951,6 +2004,32 @@ int rows_finish(const T* hi, const T* comp, int64_t rows, T* out, void* scratch,
     return launch_error("hawk_rows_levels launch");
 }
 
+// The rows' extreme in T (op 1 max, 2 min): the leaves, then the levels.
+template <class T>
+int rows_extreme(const T* hi, int64_t rows, int32_t op, T* out, void* scratch, void* stream, const char* name) {
+    const std::string who(name);
+    if (rows < 1) return hawk_internal::set_error(HK_EVALUE, who + ": rows must be >= 1");
+    if (op != 1 && op != 2) return hawk_internal::set_error(HK_EVALUE, who + ": op must be 1 (max) or 2 (min)");
+    if (!hi || !out || !scratch) return hawk_internal::set_error(HK_EVALUE, who + ": hi, out and scratch are required");
+    const long long leaves = (rows + kRowLeaf - 1) / kRowLeaf;
+    if (leaves > 0x7fffffffLL) return hawk_internal::set_error(HK_EVALUE, who + ": too many rows");
+    auto* buf = static_cast<T*>(scratch);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (op == 1)
+        hipLaunchKernelGGL((hawk_rows_ext_leaves<T, 1>), dim3(static_cast<unsigned>(leaves)), dim3(kRowSlots), 0, s,
+                           hi, static_cast<long long>(rows), buf);
+    else
+        hipLaunchKernelGGL((hawk_rows_ext_leaves<T, 2>), dim3(static_cast<unsigned>(leaves)), dim3(kRowSlots), 0, s,
+                           hi, static_cast<long long>(rows), buf);
+    int rc = launch_error("hawk_rows_ext_leaves launch");
+    if (rc != HK_OK) return rc;
+    if (op == 1)
+        hipLaunchKernelGGL((hawk_rows_ext_levels<T, 1>), dim3(1), dim3(256), 0, s, buf, leaves, out);
+    else
+        hipLaunchKernelGGL((hawk_rows_ext_levels<T, 2>), dim3(1), dim3(256), 0, s, buf, leaves, out);
+    return launch_error("hawk_rows_ext_levels launch");
+}
+
 // The keyed default-policy sum in T (hk_keyed_sample_sum_f64 / _f32).
 template <class T>
 int keyed_sample_sum(const T* u, int64_t n, int64_t group, T* out, void* stream, const char* name) {
@@ -2161,6 +2240,14 @@ int hk_rows_finish_f64(const double* hi, const double* comp, int64_t rows, doubl
 int hk_rows_finish_f32(const float* hi, const float* comp, int64_t rows, float* out, void* scratch,
                        void* stream) {
     return rows_finish(hi, comp, rows, out, scratch, stream, "hk_rows_finish_f32");
+}
+
+int hk_rows_extreme_f64(const double* hi, int64_t rows, int32_t op, double* out, void* scratch, void* stream) {
+    return rows_extreme(hi, rows, op, out, scratch, stream, "hk_rows_extreme_f64");
+}
+
+int hk_rows_extreme_f32(const float* hi, int64_t rows, int32_t op, float* out, void* scratch, void* stream) {
+    return rows_extreme(hi, rows, op, out, scratch, stream, "hk_rows_extreme_f32");
 }
 
 size_t hk_band_rows_finish_scratch_bytes(int64_t rows) { return hk_rows_finish_scratch_bytes(rows); }

@@ -87,7 +87,7 @@ _UNARY_D = {
     "tanh": lambda n, x: _o("sub", _c(1.0), _o("mul", n, n)),
 }
 
-_TERMINAL = ("leaf", "const", "iconst", "loop_index", "carry", "tape_read", "lane_axis", "gather")
+_TERMINAL = ("leaf", "const", "iconst", "loop_index", "carry", "tape_read", "lane_axis", "gather", "sample_count")
 _NO_DERIVATIVE = ("lt", "le", "gt", "ge", "eq", "ne", "chol_info", "real")
 
 
@@ -405,6 +405,20 @@ def _seed(sink, seed_name: str) -> tuple:
     return ir.leaf(role_of(t), seed_name, t), role_of(t)
 
 
+def _refuse_extremes(program: Program, transform: str) -> None:
+    """A max or a min over the samples has no derivative to take (reference
+    ``tests/test_reduce_samples.py``: "subgradient is ambiguous at a tie");
+    the reverse of a vector cell's sum would seed a vector uniform, which this
+    build does not declare."""
+    for s in program.sinks:
+        if isinstance(s, SampleSum) and s.op != "sum":
+            raise HawkError(f"{transform}: {s.name!r} is hawk.{s.op} over the samples; its subgradient is "
+                            "ambiguous at a tie (two samples holding the extreme), so it has no derivative")
+        if transform == "vjp" and isinstance(s, SampleSum) and s.column is not None:
+            raise HawkError(f"vjp: {s.name!r} is hawk.sum of a vector over the samples; its adjoint is not "
+                            "taken in this build: store each component's hawk.sum in a Scalar cell of its own")
+
+
 def vjp(kernel, wrt=None) -> Program:
     """The reverse-mode derivative: a program reading the primal inputs and an
     adjoint seed plane ``bar_<sink>`` per per-sample sink, and writing
@@ -414,6 +428,7 @@ def vjp(kernel, wrt=None) -> Program:
     policy."""
     program = _program_of(kernel)
     _refuse_prior_reads(program, "vjp")
+    _refuse_extremes(program, "vjp")
     name = _namer(program, "bar")
     targets = _differentiable_inputs(program, wrt, params=True)
     roots = [s.value for s in program.sinks]
@@ -607,6 +622,7 @@ def jvp(kernel, wrt=None) -> Program:
     for each per-sample sink ``y``."""
     program = _program_of(kernel)
     _refuse_prior_reads(program, "jvp")
+    _refuse_extremes(program, "jvp")
     name = _namer(program, "dot")
     targets = _differentiable_inputs(program, wrt)
     roots = [s.value for s in program.sinks]
@@ -631,12 +647,14 @@ def jvp(kernel, wrt=None) -> Program:
         tv = fwd.t(s.value)
         if tv is None:
             tv = zero_like(s.value.ttype)
-        out.decls[tname] = Decl(tname, "mutable", s.value.ttype)
+        column = s.column if isinstance(s, SampleSum) else None
+        # a vector cell's column sinks share the cell's declaration
+        out.decls[tname] = Decl(tname, "mutable", s.value.ttype if column is None else program.decls[s.name].ttype)
         # the tangent sink is the primal's kind at the same lane (reference
         # hawk/diff/transform.py:1003-1022): a sum of tangents, or a keyed add of
         # tangents at the primal's key under the primal's policy
         if isinstance(s, SampleSum):
-            out.sinks.append(SampleSum(tname, tv, s.policy, s.group))
+            out.sinks.append(SampleSum(tname, tv, s.policy, s.group, column=column))
         elif isinstance(s, AccumWrite):
             out.sinks.append(AccumWrite(tname, tv, s.key, s.policy))
         else:

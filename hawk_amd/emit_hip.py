@@ -247,6 +247,9 @@ class _Writer:
 
     _iconst = _const
 
+    def _sample_count(self, n: Node) -> list:
+        return [self.let("f64", "static_cast<Real>(nSamples)", "ns")]
+
     def _real(self, n: Node) -> list:
         return [self.spell.op(self, n, [x]) for x in self.value(n.operands[0])]
 
@@ -524,20 +527,23 @@ class _Writer:
 def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: list,
                   row_sums: list = (), key_writes: list = (), fused_folds: list = ()) -> Stage:
     """The plane table and arg_spec of the per-sample stage of ``program``;
-    ``row_sums`` = ``[(cell, node)]`` are default-policy sample sums whose
-    compensated 32-sample rows the stage writes; ``key_writes`` =
+    ``row_sums`` = ``[(rows, node, red)]`` are default-policy sample
+    reductions ("sum": compensated 32-sample rows; "max" / "min": one extreme
+    a row) the stage writes into planes named after ``rows`` (a cell, or a
+    cell's entry ``<cell>_<k>``); ``key_writes`` =
     ``[(plane, nodes, group)]`` are integer planes of one entry per key (every
     lane of the key's run of ``group`` samples stores the same value)."""
     writes = [(s.name, s.value) for s in program.sinks if isinstance(s, Assign)] + extra_writes
     finish = next((s for s in program.sinks if isinstance(s, Finish)), None)
-    roots = ([node for _, node in writes] + [node for _, node in row_sums]
+    roots = ([node for _, node in writes] + [node for _, node, _ in row_sums]
              + [node for _, nodes, _ in key_writes for node in nodes]
              + [node for f in fused_folds for node in tuple(f[2]) + tuple(f[3])]
              + ([finish.value] if finish is not None else []))
     used_leaves = ir.leaves_of(roots)
-    rows = [(cell, node, f"hk_rows_{cell}", f"hk_rows_{cell}_comp") for cell, node in row_sums]
+    rows = [(cell, node, f"hk_rows_{cell}", f"hk_rows_{cell}_comp" if red == "sum" else None, red)
+            for cell, node, red in row_sums]
     used = ({n.literal[1] for n in used_leaves} | {name for name, _ in writes}
-            | {p for r in rows for p in r[2:]} | {name for name, _, _ in key_writes}
+            | {p for r in rows for p in r[2:4] if p} | {name for name, _, _ in key_writes}
             | {f[0] for f in fused_folds} | {f[1] for f in fused_folds})
     used |= {n.literal.count for n in ir.topo(roots) if n.kind == "loop" and n.literal.count}
     guard = GUARD_MASK if GUARD_MASK in program.decls and program.decls[GUARD_MASK].role == "terminated" else None
@@ -555,8 +561,8 @@ def _stage_planes(program: Program, stage_name: str, mode: str, extra_writes: li
     for out, scratch, *_ in fused_folds:
         decls[out] = ir.Decl(out, "accum_out", ir.TensorType((), "f64"))
         decls[scratch] = ir.Decl(scratch, "fold_scratch", ir.TensorType((), "i32"))
-    for _, _, hi, comp in rows:
-        for pname in (hi, comp):
+    for _, _, hi, comp, _ in rows:
+        for pname in (hi, comp) if comp else (hi,):
             decls[pname] = ir.Decl(pname, "rows_out", ir.TensorType((), "f32" if mode == "float32" else "f64"))
     prog2 = Program(decls, program.sinks, program.grid, program.tables)
     spec = ir.arg_spec(prog2, used)
@@ -612,7 +618,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     if xcd_order is None:
         xcd_order = component_planes(stage) >= XCD_ORDER_PLANES
     w = _Writer(stage, mode, nontemporal, spell=target.writer)
-    roots = ([node for _, node in stage.writes] + [node for _, node, _, _ in stage.row_sums]
+    roots = ([node for _, node in stage.writes] + [node for _, node, _, _, _ in stage.row_sums]
              + [node for _, nodes, _ in stage.key_writes for node in nodes]
              + [node for f in stage.fused_folds for node in tuple(f[2]) + tuple(f[3])]
              + ([stage.finish[2]] if stage.finish is not None else []))
@@ -676,8 +682,8 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         if w.lines or len(stores) != len(deferred[0]):
             deferred = None               # the stores computed a value of their own: keep one pass
         w.lines = []
-    row_terms = [(w.value(node)[0], stage.planes[hi]["var"], stage.planes[comp]["var"])
-                 for _, node, hi, comp in stage.row_sums]
+    row_terms = [(w.value(node)[0], stage.planes[hi]["var"], stage.planes[comp]["var"] if comp else None, red)
+                 for _, node, hi, comp, red in stage.row_sums]
     folds = [(stage.planes[out]["var"], stage.planes[scratch]["var"], [w.value(v)[0] for v in values],
               [w.value(c)[0] for c in cells], group) for out, scratch, values, cells, group in stage.fused_folds]
     body += w.lines                                   # (memoized: nothing new unless a term is a bare leaf)
@@ -702,8 +708,10 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     text = "\n".join(body + stores)
     if any(c in text for c in MATH_HELPER_CALLS):
         out += MATH_DEVICE_DEFINES + _MATH_HELPERS.splitlines()
-    if row_terms:
+    if any(red == "sum" for *_, red in row_terms):
         out += (_BAND_ROW_SUM_HELPERS if stage.banded else _ROW_SUM_HELPERS).splitlines()
+    if any(red != "sum" for *_, red in row_terms):
+        out += _ROW_EXTREME_HELPERS.splitlines()
     if folds:
         out += _FOLD_HELPERS.splitlines()
     if stage.finish is not None:
@@ -743,8 +751,11 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += body
         opened, closed = wrap.sample_sum_frame(len(row_terms), "Real", "")
         out += opened + ["    " + line for line in stores] + closed
-        for k, (term, hi, comp) in enumerate(row_terms):
-            out += w.spell.sample_sum(w, stage.banded, term, hi, comp)
+        for k, (term, hi, comp, red) in enumerate(row_terms):
+            if red == "sum":
+                out += w.spell.sample_sum(w, stage.banded, term, hi, comp)
+            else:
+                out += w.spell.sample_extreme(w, red, term, hi)
         out += _fused_fold_lines(folds, block, whole)
     out += wrap.index_epilogue()
     if auto is not None:
@@ -1375,6 +1386,31 @@ __device__ __forceinline__ void hk_row_sum(Real& h, Real& c) {
 """
 
 
+#: The row extremes of ``hawk.max`` / ``hawk.min`` (reference
+#: ``hawk/emit/wrapper.py:543-600``: ``ssExtreme_``, ``ssIdentity_``,
+#: ``sampleSumRow_``'s pairs): a row's 32 lanes combine by the pairs
+#: (l, l ^ 16), ..., (l, l ^ 1), each pair as the extreme of (the lower
+#: lane's value, the upper lane's) that ignores a NaN operand, so every lane of
+#: the half ends with the row's extreme; a lane past ``count`` holds -inf (max)
+#: or +inf (min).  The operand order is the reference's row walk's, slot l
+#: with slot l + off: it decides the sign of an extreme of +0 and -0.
+_ROW_EXTREME_HELPERS = """
+__device__ __forceinline__ Real hk_extreme(int op, Real a, Real b) {
+    if (a != a) return b;
+    if (b != b) return a;
+    return op == 1 ? (b > a ? b : a) : (b < a ? b : a);
+}
+__device__ __forceinline__ void hk_row_extreme(int op, Real& h) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) {
+        const Real h2 = __shfl_xor(h, off, 64);
+        const bool low = (threadIdx.x & off) == 0;
+        h = low ? hk_extreme(op, h, h2) : hk_extreme(op, h2, h);
+    }
+}
+"""
+
+
 #: The row sum of the banded mode: each lane's term is the double-double
 #: band (term, +0), and the 32 lanes of a row combine by the pairs of the
 #: default sum's row with the band add of Hida, Li and Bailey's QD library
@@ -1586,19 +1622,29 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
             team.append({"op": "ordered_fold", "v": values, "c": cells, "out": s.name, "group": s.group,
                          "width": width})
             continue
-        if isinstance(s, SampleSum) and s.policy != "ordered" and s.group is None:
-            row_sums.append((s.name, s.value))
-            team.append({"op": "band_rows" if banded else "row_sum", "hi": f"hk_rows_{s.name}",
-                         "comp": f"hk_rows_{s.name}_comp", "out": s.name})
+        if isinstance(s, SampleSum) and s.group is None and (s.policy != "ordered" or s.op != "sum"):
+            # the default policy, and max / min whatever the policy (exact either
+            # way): rows of 32 samples in the stage, the canonical finish after
+            rows = s.name if s.column is None else f"{s.name}_{s.column}"
+            row_sums.append((rows, s.value, s.op))
+            if s.op == "sum":
+                t = {"op": "band_rows" if banded else "row_sum", "hi": f"hk_rows_{rows}",
+                     "comp": f"hk_rows_{rows}_comp", "out": s.name}
+            else:
+                t = {"op": "row_extreme", "red": s.op, "hi": f"hk_rows_{rows}", "out": s.name}
+            if s.column is not None:
+                t["column"] = s.column            # the entry of a vector cell this stage stores
+            team.append(t)
         elif isinstance(s, SampleSum):
             src = assigned.get(id(s.value))
             if src is None and s.value.kind == "leaf" and s.value.literal[0] == "per_sample":
                 src = s.value.literal[1]
             if src is None:
-                src = f"hk_sum_{s.name}"
+                src = f"hk_sum_{s.name}" if s.column is None else f"hk_sum_{s.name}_{s.column}"
                 extra.append((src, s.value))
             if s.group is None:
-                team.append({"op": "band_ordered_sum" if banded else "ordered_sum", "u": src, "out": s.name})
+                team.append({"op": "band_ordered_sum" if banded else "ordered_sum", "u": src, "out": s.name,
+                             **({} if s.column is None else {"column": s.column})})
             elif s.policy == "ordered":
                 team.append({"op": "keyed_sum", "u": src, "out": s.name, "group": s.group})
             else:                                   # the default policy over some axes
@@ -1644,10 +1690,12 @@ def plan_kernel(program: Program, name: str, mode: str = "float64", block: int =
         for key in ("out", "target"):
             pname = t.get(key)
             if pname and isinstance(pname, str):
+                # a vector cell (one entry a column) keeps its declared shape
+                shape = list(program.decls[pname].ttype.shape) if t.get("column") is not None else []
                 planes[pname] = {"role": "cell" if t["op"] in ("ordered_sum", "row_sum", "keyed_sum", "keyed_comp",
-                                                              "band_rows", "band_ordered_sum")
+                                                              "band_rows", "band_ordered_sum", "row_extreme")
                                  else "accum_out",
-                                 "shape": [], "dtype": "f32" if mode == "float32" else "f64"}
+                                 "shape": shape, "dtype": "f32" if mode == "float32" else "f64"}
                 if t["op"] in ("keyed_sum", "keyed_comp"):
                     planes[pname]["group"] = t["group"]       # one cell per `group` samples
     for pname, info in planes.items():

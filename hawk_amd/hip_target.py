@@ -325,6 +325,17 @@ class HipWriter:
                 f"              {comp}[hk_r] = hk_rc;",
                 "          } }"]
 
+    def sample_extreme(self, r, red: str, term: str, hi: str) -> list:
+        """A ``hawk.max`` / ``hawk.min`` row: the lane's term joins its
+        half-wave's row of 32 (a lane past ``count`` holds -inf / +inf, the
+        op's identity) and lane 0 of the half stores the row's extreme."""
+        op, ident = (1, "-__builtin_inf()") if red == "max" else (2, "__builtin_inf()")
+        return [f"        {{ Real hk_rh = hk_live ? static_cast<Real>({term}) : static_cast<Real>({ident});",
+                f"          hk_row_extreme({op}, hk_rh);",
+                "          if ((threadIdx.x & 31) == 0 && hk_live) {",
+                f"              {hi}[(base + hk_flat) >> 5] = hk_rh;",
+                "          } }"]
+
     def tape_write(self, r, tape: str, slot: str, value: str) -> str:
         return f"{tape}[{slot}] = {value};"
 

@@ -177,6 +177,10 @@ def make(kind: str, operands: tuple, literal=None) -> Node:
     if kind == "sum":
         (a,) = ops
         return Node(kind, (a,), TensorType((), a.ttype.dtype))
+    if kind == "sample_count":
+        # the run's sample count (the entry's nSamples: every sample of the
+        # run, not only this launch's partition), as a real
+        return Node(kind, (), TensorType((), "f64"))
     if kind == "component":
         (a,) = ops
         shape = a.ttype.shape
@@ -469,12 +473,18 @@ class SampleSum:
     """``name = hawk.sum(value, policy=...)``: one cell over every sample; with
     ``group`` (``hawk.sum(value, over=<trailing lane axes>)``), one cell per
     run of ``group`` consecutive samples (one per coordinate of the kept
-    leading axes)."""
+    leading axes).  ``op`` is the reduction: "sum" (``hawk.mean`` is the sum
+    of each term over the sample count), "max" or "min" (reference
+    ``hawk/trace/reduce.py:304-334``).  ``column`` is the flat entry of a
+    vector or matrix cell this scalar reduction commits (one row plane per
+    column, reference ``hawk/_cells.py:33-35``); None for a scalar cell."""
 
     name: str
     value: Node
     policy: str = "ordered"
     group: int | None = None
+    op: str = "sum"
+    column: int | None = None
 
 
 @dataclass

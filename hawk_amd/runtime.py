@@ -288,8 +288,14 @@ class DeviceKernel:
             elif role == "cell" and info.get("group"):
                 keyed.append((name, x, info["group"]))
             elif role == "cell":
-                if x.numel() != 1:
-                    problems.append(f"{name!r} is a one-cell result of hawk.sum: bind 1 element, got {x.numel()}")
+                cells = 1
+                for e in info["shape"]:
+                    cells *= e
+                if x.numel() != cells:
+                    problems.append(f"{name!r} is " + (f"the {tuple(info['shape'])} result of a reduction over "
+                                    f"the samples: bind {cells} elements" if info["shape"] else
+                                    "a one-cell result of a reduction over the samples: bind 1 element")
+                                    + f", got {x.numel()}")
             elif role == "accum_out":
                 if x.dim() != 1:
                     problems.append(f"{name!r} is the 1-D plane of cells hawk.scatter adds into")
@@ -346,24 +352,38 @@ class DeviceKernel:
             self._scratch[key] = held
         return held
 
+    @staticmethod
+    def _cell_ptr(t: dict, out) -> int:
+        """The address of a team stage's cell: entry ``column`` of a vector
+        cell (``hawk.sum`` of a vector commits one entry a column)."""
+        return out.data_ptr() + (t.get("column") or 0) * out.element_size()
+
     def _row_sum(self, t: dict, bound: dict, n: int, device, stream: int) -> None:
-        """Fold the stage's row partials into the cell (a run of no samples sums to 0):
-        compensated (hi, comp) rows, or band rows (hi, lo) in the banded mode."""
+        """Fold the stage's row partials into the cell: compensated (hi, comp)
+        rows, band rows (hi, lo) in the banded mode, or one extreme a row
+        (``hawk.max`` / ``hawk.min``).  A run of no samples leaves the
+        reduction's identity: 0, -inf (max), +inf (min)."""
         out = bound[t["out"]]
         rows = -(-n // 32)
+        col = t.get("column")
         if rows == 0:
+            empty = {"max": float("-inf"), "min": float("inf")}.get(t.get("red"), 0.0)
             with _on(stream):
-                out.zero_()
+                (out.view(-1)[col:col + 1] if col is not None else out).fill_(empty)
             return
         band = t["op"] == "band_rows"
+        f32 = self.planes[t["hi"]]["dtype"] == "f32"      # the rows are the stage's Real: the finish runs in it
         with _on(stream):
             nbytes = (_core.band_rows_finish_scratch_bytes if band else _core.rows_finish_scratch_bytes)(rows)
-            scratch = self._buffer(("rows", t["out"], rows), nbytes, device, zero=False)
-        if band:
-            finish = _core.band_rows_finish
-        else:       # the rows are the stage's Real: the finish runs in it
-            finish = _core.rows_finish_f32 if self.planes[t["hi"]]["dtype"] == "f32" else _core.rows_finish
-        finish(bound[t["hi"]].data_ptr(), bound[t["comp"]].data_ptr(), rows, out.data_ptr(), scratch.data_ptr(), stream)
+            scratch = self._buffer(("rows", t["hi"], rows), nbytes, device, zero=False)
+        if t["op"] == "row_extreme":
+            (_core.rows_extreme_f32 if f32 else _core.rows_extreme)(
+                bound[t["hi"]].data_ptr(), rows, 1 if t["red"] == "max" else 2, self._cell_ptr(t, out),
+                scratch.data_ptr(), stream)
+            return
+        finish = _core.band_rows_finish if band else _core.rows_finish_f32 if f32 else _core.rows_finish
+        finish(bound[t["hi"]].data_ptr(), bound[t["comp"]].data_ptr(), rows, self._cell_ptr(t, out),
+               scratch.data_ptr(), stream)
 
     def _term_plane(self, name: str, n: int, device):
         torch = _torch()
@@ -504,7 +524,7 @@ class DeviceKernel:
                 u = bound[t["u"]]
                 scratch = self._buffer(("sum", t["out"]), _core.ordered_sum_scratch_bytes(), device)
                 fn = _core.ordered_sum_f32 if self._is_f32(t["out"]) else _core.ordered_sum
-                fn(u.data_ptr(), n, bound[t["out"]].data_ptr(), scratch.data_ptr(), stream)
+                fn(u.data_ptr(), n, self._cell_ptr(t, bound[t["out"]]), scratch.data_ptr(), stream)
             elif t["op"] == "ordered_scatter":
                 target = bound[t["target"]]
                 cells = int(target.numel())
@@ -521,13 +541,14 @@ class DeviceKernel:
             elif t["op"] == "mm16":
                 _core.mm16([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
                            t["products"], n, stream, t.get("dtype", "f32"))
-            elif t["op"] in ("row_sum", "band_rows"):
+            elif t["op"] in ("row_sum", "band_rows", "row_extreme"):
                 self._row_sum(t, bound, n, device, stream)
             elif t["op"] == "band_ordered_sum":
                 u = bound[t["u"]]
                 scratch = self._buffer(("band_sum", t["out"]), _core.band_ordered_sum_scratch_bytes(), device,
                                        zero=False)
-                _core.band_ordered_sum(u.data_ptr(), n, bound[t["out"]].data_ptr(), scratch.data_ptr(), stream)
+                _core.band_ordered_sum(u.data_ptr(), n, self._cell_ptr(t, bound[t["out"]]), scratch.data_ptr(),
+                                       stream)
             elif t["op"] == "keyed_sum":
                 scratch = self._buffer(("keyed", t["out"], n), _core.keyed_ordered_sum_scratch_bytes(n, t["group"]),
                                        device)
@@ -848,7 +869,7 @@ class Prepared:
                 continue
             if t["op"] == "ordered_sum":
                 scratch = kernel._buffer(("sum", t["out"]), _core.ordered_sum_scratch_bytes(), device)
-                args = (bound[t["u"]].data_ptr(), self.n, bound[t["out"]].data_ptr(), scratch.data_ptr())
+                args = (bound[t["u"]].data_ptr(), self.n, kernel._cell_ptr(t, bound[t["out"]]), scratch.data_ptr())
                 self.steps.append((_core.ordered_sum_f32 if kernel._is_f32(t["out"]) else _core.ordered_sum, args))
             elif t["op"] == "ordered_scatter":
                 target = bound[t["target"]]
@@ -867,12 +888,12 @@ class Prepared:
                 args = ([bound[p].data_ptr() for p in t["in"]], [bound[p].data_ptr() for p in t["out"]],
                         t["products"], self.n)
                 self.steps.append((_core.mm16_f64 if t.get("dtype") == "f64" else _core.mm16, args))
-            elif t["op"] in ("row_sum", "band_rows"):
+            elif t["op"] in ("row_sum", "band_rows", "row_extreme"):
                 self.steps.append((kernel._row_sum, (t, bound, self.n, device)))
             elif t["op"] == "band_ordered_sum":
                 scratch = kernel._buffer(("band_sum", t["out"]), _core.band_ordered_sum_scratch_bytes(), device,
                                          zero=False)
-                args = (bound[t["u"]].data_ptr(), self.n, bound[t["out"]].data_ptr(), scratch.data_ptr())
+                args = (bound[t["u"]].data_ptr(), self.n, kernel._cell_ptr(t, bound[t["out"]]), scratch.data_ptr())
                 self.steps.append((_core.band_ordered_sum, args))
             elif t["op"] == "keyed_sum":
                 scratch = kernel._buffer(("keyed", t["out"], self.n),

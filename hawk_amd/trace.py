@@ -194,11 +194,12 @@ class Reduced:
     samples each).  It can be committed (assigned to a ``Mutable`` or
     returned), not read back."""
 
-    def __init__(self, node: Node, policy: str, group: int | None = None, kept: tuple = ()):
+    def __init__(self, node: Node, policy: str, group: int | None = None, kept: tuple = (), op: str = "sum"):
         self.node = node
         self.policy = policy
         self.group = group
         self.kept = kept
+        self.op = op
 
     def _refuse(self, *_):
         raise HawkError("a value reduced over every sample (hawk.sum) is read back in the body: "
@@ -319,10 +320,76 @@ class _Trace:
         return cls.stack[-1]
 
 
-def sum(x: Any, over: Any = None, policy: str = "auto") -> Reduced:  # noqa: A001 - hawk's spelling
+_IDENTITY = {"sum": 0.0, "max": float("-inf"), "min": float("inf")}
+
+
+def _reduce(op: str, x: Any, over: Any, where: Any, policy: str) -> Reduced:
+    """The reductions' common front (reference ``hawk/trace/reduce.py:234-271``):
+    the policy, ``where=`` (a masked lane contributes the op's identity), the
+    mean's division by the sample count (over every sample) or by the reduced
+    axes' extent (over some), and the lane axes ``over`` names."""
+    call = f"hawk.{op}(x, over={over!r})" if over is not None else f"hawk.{op}(x)"
+    if policy not in SUM_POLICIES:
+        raise HawkError(f"{call}: policy={policy!r} is not one of {SUM_POLICIES}")
+    base = "sum" if op == "mean" else op
+    n = _projected(node_of(x))
+    if n.ttype.dtype == "bool" and not n.ttype.shape:
+        n = make("select", (n, ir.const(1.0), ir.const(0.0)))   # hawk.sum(mask): the count of true lanes
+    if where is not None:
+        mask = _projected(node_of(where))
+        if mask.ttype.dtype != "bool" or mask.ttype.shape:
+            raise HawkError(f"{call}: where= is this lane's bool mask, got {mask.ttype!r}")
+        if op == "mean":
+            raise HawkError(f"{call}: the mean of the masked lanes needs their count, a second reduction: "
+                            "hawk.sum(x, where=mask) / hawk.sum(mask)")
+        n = make("select", (mask, n, ir.const(_IDENTITY[base])))
+    if over is None:
+        if op == "mean":
+            n = make("div", (n, make("sample_count", ())))
+        return Reduced(n, policy, op=base)
+    if n.ttype.shape:
+        raise HawkError(f"{call}: a reduction over some lane axes takes a scalar in this build; reduce each "
+                        "component")
+    grid = _Trace.current(f"hawk.{op}").grid
+    if grid is None:
+        raise HawkError(f"{call} names lane axes: declare the kernel's lanes with a Grid parameter, e.g. "
+                        'lane: Grid["key", "sample":1024]')
+    labels = [a for a, _ in grid.axes]
+    items = over if isinstance(over, tuple) else (over,)
+    reduced = set()
+    for item in items:
+        if isinstance(item, str) and item in labels:
+            reduced.add(labels.index(item))
+        elif isinstance(item, int) and not isinstance(item, bool) and -len(labels) <= item < len(labels):
+            reduced.add(item % len(labels))
+        else:
+            raise HawkError(f"{call}: {item!r} is not an axis of the Grid {labels}")
+    if len(reduced) == len(labels):
+        if op == "mean":
+            n = make("div", (n, make("sample_count", ())))
+        return Reduced(n, policy, op=base)
+    if base != "sum":
+        raise HawkError(f"{call}: a {op} over some of the lane axes is in the next release; hawk.{op}(x) "
+                        f"(one value for the run) and hawk.sum/mean(x, over=...) work now")
+    spelled = f"over={over!r}"
+    if reduced != set(range(len(labels) - len(reduced), len(labels))):
+        raise HawkError(f"hawk.{op}(x, {spelled}, policy={policy!r}): policy={policy!r} sums over the trailing "
+                        f"lane axes only (the Grid's axes are {labels}): each key's samples are one run")
+    group = 1
+    for pos in reduced:
+        group *= grid.axes[pos][1]
+    if op == "mean":
+        n = make("div", (n, ir.const(float(group))))
+    kept = tuple(labels[:len(labels) - len(reduced)])
+    return Reduced(n, policy, group, kept, op="sum")
+
+
+def sum(x: Any, over: Any = None, where: Any = None, policy: str = "auto") -> Reduced:  # noqa: A001
     """The sum of ``x`` over every sample of the run, or over the lane axes
     ``over`` names (a label, a position, or a tuple of them) of the kernel's
-    ``Grid`` (reference ``hawk/trace/reduce.py:277-301``).
+    ``Grid`` (reference ``hawk/trace/reduce.py:277-301``).  A masked lane
+    (``where=`` false) adds nothing.  A vector or matrix ``x`` sums each entry
+    into its own cell entry (one row plane per entry).
 
     ``policy="ordered"`` adds in a fixed tree that depends on the sample count
     only: 65536 virtual lanes, each adding its rows in order, folded in groups
@@ -335,39 +402,30 @@ def sum(x: Any, over: Any = None, policy: str = "auto") -> Reduced:  # noqa: A00
     reference ``hawk/_cells.py``; over some axes each key's run is such a sum
     of its own (the reference commits keys atomically, in launch-dependent
     order once a key spans three warps)."""
-    if policy not in SUM_POLICIES:
-        raise HawkError(f"hawk.sum(x, policy={policy!r}): policy={policy!r} is not one of {SUM_POLICIES}")
-    n = _projected(node_of(x))
-    if n.ttype.shape:
-        raise HawkError("hawk.sum over samples of a vector or matrix is not in this build; "
-                        "sum each component")
-    if over is None:
-        return Reduced(n, policy)
-    grid = _Trace.current("hawk.sum").grid
-    if grid is None:
-        raise HawkError("hawk.sum(x, over=...) names lane axes: declare the kernel's lanes with a "
-                        'Grid parameter, e.g. lane: Grid["key", "sample":1024]')
-    labels = [a for a, _ in grid.axes]
-    items = over if isinstance(over, tuple) else (over,)
-    reduced = set()
-    for item in items:
-        if isinstance(item, str) and item in labels:
-            reduced.add(labels.index(item))
-        elif isinstance(item, int) and not isinstance(item, bool) and -len(labels) <= item < len(labels):
-            reduced.add(item % len(labels))
-        else:
-            raise HawkError(f"hawk.sum(x, over={over!r}): {item!r} is not an axis of the Grid {labels}")
-    if len(reduced) == len(labels):
-        return Reduced(n, policy)
-    spelled = f"over={over!r}"
-    if reduced != set(range(len(labels) - len(reduced), len(labels))):
-        raise HawkError(f"hawk.sum(x, {spelled}, policy={policy!r}): policy={policy!r} sums over the trailing "
-                        f"lane axes only (the Grid's axes are {labels}): each key's samples are one run")
-    group = 1
-    for pos in reduced:
-        group *= grid.axes[pos][1]
-    kept = tuple(labels[:len(labels) - len(reduced)])
-    return Reduced(n, policy, group, kept)
+    return _reduce("sum", x, over, where, policy)
+
+
+def max(x: Any, over: Any = None, where: Any = None, policy: str = "auto") -> Reduced:  # noqa: A001
+    """The maximum of ``x`` over every sample (reference
+    ``hawk/trace/reduce.py:304-307``): each row of 32 samples by a butterfly
+    that ignores a NaN operand, then the rows in the canonical tree of
+    ``hawk/_cells.py`` (``a > b ? a : b``); exact.  A masked lane
+    (``where=`` false) is -inf."""
+    return _reduce("max", x, over, where, policy)
+
+
+def min(x: Any, over: Any = None, where: Any = None, policy: str = "auto") -> Reduced:  # noqa: A001
+    """The minimum of ``x`` over every sample, as :func:`max` with ``<``; a
+    masked lane is +inf (reference ``hawk/trace/reduce.py:310-313``)."""
+    return _reduce("min", x, over, where, policy)
+
+
+def mean(x: Any, over: Any = None, where: Any = None, policy: str = "auto") -> Reduced:
+    """The mean of ``x`` over the samples ``over`` names: the sum of each term
+    divided by the count of reduced samples (the run's sample count over
+    every sample; the reduced axes' extent over some), reference
+    ``hawk/trace/reduce.py:263-273``, ``:316-320``."""
+    return _reduce("mean", x, over, where, policy)
 
 
 class _Stored:
@@ -689,14 +747,23 @@ def trace(fn, scope: dict | None = None) -> Program:
             if axes:
                 raise HawkError(f"{name!r} is declared with lane axes {[a for a, _ in axes]} but assigned a sum "
                                 "over every sample (one cell); declare Mutable[Scalar]")
-            return SampleSum(name, red.node, red.policy)
+            shape = red.node.ttype.shape
+            if not shape:
+                return [SampleSum(name, red.node, red.policy, op=red.op)]
+            # a vector or matrix cell: one scalar reduction per entry, row-major
+            count = 1
+            for e in shape:
+                count *= e
+            idx = [divmod(k, shape[1]) if len(shape) == 2 else k for k in range(count)]
+            return [SampleSum(name, make("component", (red.node,), i), red.policy, op=red.op, column=k)
+                    for k, i in enumerate(idx)]
         grid_axes = dict(program.grid.axes)
         if axes is not None:
             if tuple(a for a, _ in axes) != red.kept or any(
                     e is not None and grid_axes[a] is not None and e != grid_axes[a] for a, e in axes):
                 raise HawkError(f"{name!r} is declared with lane axes {list(axes)} but holds the sum over the "
                                 f"other axes, one value per {list(red.kept)} coordinate")
-        return SampleSum(name, red.node, red.policy, red.group)
+        return [SampleSum(name, red.node, red.policy, red.group)]
     sinks = list(tr.sinks)
     for name in mutables:
         final = finals[name]
@@ -704,12 +771,14 @@ def trace(fn, scope: dict | None = None) -> Program:
         if isinstance(final, MutableRef) and final.name == name:
             continue                      # never assigned per lane (a scatter target, or unused)
         if isinstance(final, Reduced):
-            if decl.ttype.shape:
-                raise HawkError(f"{name!r}: hawk.sum commits a scalar cell; declare Mutable[Scalar]")
+            if decl.ttype.shape != final.node.ttype.shape:
+                raise HawkError(f"{name!r}: hawk.{final.op} of a value of shape {final.node.ttype.shape or 'scalar'} "
+                                f"commits a cell of that shape; {name!r} is declared "
+                                f"{decl.ttype.shape or 'scalar'}")
             if final.group is not None and name not in axes_of:
                 raise HawkError(f"{name!r} holds hawk.sum over some lane axes, one value per "
                                 f"{list(final.kept)} coordinate: declare it Mutable[{', '.join(repr(k) for k in final.kept)}]")
-            sinks.append(keyed(name, final))
+            sinks.extend(keyed(name, final))
             continue
         if name in axes_of:
             raise HawkError(f"{name!r} is declared with lane axes: it holds hawk.sum(x, over=...), "
@@ -725,8 +794,8 @@ def trace(fn, scope: dict | None = None) -> Program:
     if ret is not None:
         ret_ann = _annotation(fn, sig.return_annotation, ns)
         if isinstance(ret, Reduced):
-            program.decls["out"] = Decl("out", "mutable", TensorType((), "f64"))
-            sinks.append(keyed("out", ret))
+            program.decls["out"] = Decl("out", "mutable", TensorType(ret.node.ttype.shape, "f64"))
+            sinks.extend(keyed("out", ret))
         else:
             node = ir.as_real(_projected(node_of(ret)))
             if isinstance(ret_ann, TensorType) and ret_ann.shape != node.ttype.shape:
@@ -755,7 +824,7 @@ def trace(fn, scope: dict | None = None) -> Program:
     if not sinks:
         raise HawkError(f"{fn.__name__}: the kernel commits nothing (assign a Mutable, return a value, "
                         "or hawk.scatter into one)")
-    names = [s.name for s in sinks if not isinstance(s, AccumWrite)]
+    names = [s.name for s in sinks if not isinstance(s, AccumWrite) and not (isinstance(s, SampleSum) and s.column)]
     dup = sorted({n for n in names if names.count(n) > 1})
     if dup:
         raise HawkError(f"{fn.__name__}: {dup} are committed twice")

@@ -235,6 +235,20 @@ int hk_rows_finish_f64(const double* hi, const double* comp, int64_t rows,
 int hk_rows_finish_f32(const float* hi, const float* comp, int64_t rows,
                        float* out, void* scratch, void* stream);
 
+/* The finish of `hawk.max(x)` (op 1) / `hawk.min(x)` (op 2): `rows` row
+ * extremes (one per 32 samples; a row's NaN-ignoring extreme, -inf / +inf
+ * past the last sample, reference `hawk/emit/wrapper.py:543-600`) folded in
+ * the same canonical tree as the sum (reference `hawk/_cells.py:66-71` and
+ * `finish`), every add the extreme a > b ? a : b (max) or a < b ? a : b
+ * (min) of the earlier partial and the later, and stored to *out.  Exact;
+ * the cell is the reference host finish's bit for bit.  Scratch:
+ * hk_rows_finish_scratch_bytes(rows) bytes.  HK_EVALUE for rows < 1 or
+ * another op. */
+int hk_rows_extreme_f64(const double* hi, int64_t rows, int32_t op, double* out,
+                        void* scratch, void* stream);
+int hk_rows_extreme_f32(const float* hi, int64_t rows, int32_t op, float* out,
+                        void* scratch, void* stream);
+
 /* Banded reductions: the sample sums of the banded scalar mode (reference
  * `hawk/emit/wrapper.py:140` BANDED and its row sum `:542-665`,
  * `hawk/emit/team.py:26-49` and `:225-245`: band partials folded in the

@@ -377,6 +377,77 @@ HKO_EXPORT void hko_keyed_sample_sum(const double* u, int64_t n, int64_t group, 
     for (int64_t k = 0; k * group < n; ++k) out[k] = hko_sample_sum(u + k * group, group);
 }
 
+/* ---- hawk.max / hawk.min: row extremes, the canonical finish -------------
+ * Reference hawk/emit/wrapper.py:543-600 (ssExtreme_: the extreme of two
+ * values that ignores a NaN operand; ssIdentity_: -inf (max) / +inf (min)
+ * past the last sample; sampleSumRow_: slot l with slot l + off, off = 16 ..
+ * 1) and hawk/_cells.py:66-71 with `finish` (the sum's leaves and levels,
+ * every add np.where(a > b, a, b) for max, np.where(a < b, a, b) for min, so
+ * a NaN partial on the left gives way and one on the right wins).
+ * op 1 = max, 2 = min; T is double or float. */
+#define HKO_EXTREME_FNS(T, SUF)                                                          \
+static T ss_extreme##SUF(int op, T a, T b) {                                             \
+    if (a != a) return b;                                                                \
+    if (b != b) return a;                                                                \
+    return op == 1 ? (b > a ? b : a) : (b < a ? b : a);                                  \
+}                                                                                        \
+static T tree_extreme##SUF(int op, T a, T b) { return op == 1 ? (a > b ? a : b) : (a < b ? a : b); } \
+HKO_EXPORT void hko_row_extremes##SUF(const T* t, int64_t n, int op, T* hi) {            \
+    const int64_t rows = (n + 31) / 32;                                                  \
+    const T ident = op == 1 ? -(T)INFINITY : (T)INFINITY;                                \
+    for (int64_t r = 0; r < rows; ++r) {                                                 \
+        T h[32];                                                                         \
+        for (int l = 0; l < 32; ++l) h[l] = r * 32 + l < n ? t[r * 32 + l] : ident;      \
+        for (int off = 16; off >= 1; off >>= 1)                                          \
+            for (int l = 0; l < off; ++l) h[l] = ss_extreme##SUF(op, h[l], h[l + off]);  \
+        hi[r] = h[0];                                                                    \
+    }                                                                                    \
+}                                                                                        \
+HKO_EXPORT T hko_rows_extreme##SUF(const T* hi, int64_t rows, int op) {                  \
+    if (rows <= 0) return op == 1 ? -(T)INFINITY : (T)INFINITY;                          \
+    const int64_t leaves = (rows + 4095) / 4096;                                         \
+    T* vh = (T*)malloc(sizeof(T) * (size_t)leaves);                                      \
+    for (int64_t j = 0; j < leaves; ++j) {                                               \
+        const T* x = hi + j * 4096;                                                      \
+        const int64_t rest = rows - j * 4096;                                            \
+        const int cnt = (int)(rest < 4096 ? rest : 4096), live = cnt < 256 ? cnt : 256;  \
+        T sh[256];                                                                       \
+        for (int s = 0; s < live; ++s) sh[s] = x[s];                                     \
+        for (int k = 1; k < 16; ++k) {                                                   \
+            const int m = live < cnt - k * 256 ? live : cnt - k * 256;                   \
+            if (m <= 0) break;                                                           \
+            for (int s = 0; s < m; ++s) sh[s] = tree_extreme##SUF(op, sh[s], x[k * 256 + s]); \
+        }                                                                                \
+        for (int off = 128; off > 0; off >>= 1) {                                        \
+            const int lim = live > off ? (off < live - off ? off : live - off) : 0;      \
+            for (int s = 0; s < lim; ++s) sh[s] = tree_extreme##SUF(op, sh[s], sh[s + off]); \
+        }                                                                                \
+        vh[j] = sh[0];                                                                   \
+    }                                                                                    \
+    int64_t m = leaves;                                                                  \
+    while (m > 1) {                                                                      \
+        const int64_t pairs = m / 2;                                                     \
+        for (int64_t q = 0; q < pairs; ++q) vh[q] = tree_extreme##SUF(op, vh[2 * q], vh[2 * q + 1]); \
+        if (m & 1) vh[pairs] = vh[m - 1];                                                \
+        m = pairs + (m & 1);                                                             \
+    }                                                                                    \
+    const T out = vh[0];                                                                 \
+    free(vh);                                                                            \
+    return out;                                                                          \
+}                                                                                        \
+HKO_EXPORT T hko_sample_extreme##SUF(const T* t, int64_t n, int op) {                    \
+    const int64_t rows = (n + 31) / 32;                                                  \
+    if (rows == 0) return op == 1 ? -(T)INFINITY : (T)INFINITY;                          \
+    T* hi = (T*)malloc(sizeof(T) * (size_t)rows);                                        \
+    hko_row_extremes##SUF(t, n, op, hi);                                                 \
+    const T out = hko_rows_extreme##SUF(hi, rows, op);                                   \
+    free(hi);                                                                            \
+    return out;                                                                          \
+}
+
+HKO_EXTREME_FNS(double, )
+HKO_EXTREME_FNS(float, _f32)
+
 /* ---- banded reductions: double-double band accumulators ----------------
  * The banded scalar mode's reductions (reference hawk/emit/wrapper.py:140
  * `BANDED`, hawk/emit/team.py:26-49 and :225-245: every partial is a

@@ -57,6 +57,8 @@ class Evaluator:
             return np.full(n, m.literal)
         if k == "iconst":
             return np.full(n, m.literal)
+        if k == "sample_count":
+            return np.full(n, float(self.env.get("__n_samples__", n)))
         if k == "real":
             return self._op(m, 0).astype(np.float64)
         if k in ("add", "sub", "mul", "div"):

@@ -76,6 +76,12 @@ def lib(profile: str | None = None):
         "hko_sample_sum_f32": (ctypes.c_float, [_P, _I64]),
         "hko_band_row_sums": (None, [_P, _I64, _P, _P]),
         "hko_band_rows_finish": (_D, [_P, _P, _I64]),
+        "hko_row_extremes": (None, [_P, _I64, ctypes.c_int, _P]),
+        "hko_rows_extreme": (_D, [_P, _I64, ctypes.c_int]),
+        "hko_sample_extreme": (_D, [_P, _I64, ctypes.c_int]),
+        "hko_row_extremes_f32": (None, [_P, _I64, ctypes.c_int, _P]),
+        "hko_rows_extreme_f32": (ctypes.c_float, [_P, _I64, ctypes.c_int]),
+        "hko_sample_extreme_f32": (ctypes.c_float, [_P, _I64, ctypes.c_int]),
         "hko_band_sample_sum": (_D, [_P, _I64]),
         "hko_band_ordered_sum": (_D, [_P, _I64]),
         "hko_scatter_chunks": (ctypes.c_int, [_I64, _I64]),
@@ -327,6 +333,38 @@ def sample_sum_f32(t) -> np.float32:
     """The float32 mode's default-policy hawk.sum of the terms t (rows, then the canonical finish, in float32)."""
     t = np.ascontiguousarray(t, dtype=np.float32)
     return np.float32(lib().hko_sample_sum_f32(_p(t), t.size))
+
+
+_EXTREME_OP = {"max": 1, "min": 2}
+
+
+def row_extremes(t, op: str):
+    """One value a row of 32 terms: the NaN-ignoring extreme ("max" or
+    "min"), -inf / +inf past the last term; float32 terms give float32 rows."""
+    f32 = np.asarray(t).dtype == np.float32
+    t = np.ascontiguousarray(t, dtype=np.float32 if f32 else np.float64)
+    hi = np.empty(-(-t.size // 32), dtype=t.dtype)
+    (lib().hko_row_extremes_f32 if f32 else lib().hko_row_extremes)(_p(t), t.size, _EXTREME_OP[op], _p(hi))
+    return hi
+
+
+def rows_extreme(hi, op: str):
+    """The canonical finish of row extremes (in the rows' dtype)."""
+    f32 = np.asarray(hi).dtype == np.float32
+    hi = np.ascontiguousarray(hi, dtype=np.float32 if f32 else np.float64)
+    if f32:
+        return np.float32(lib().hko_rows_extreme_f32(_p(hi), hi.size, _EXTREME_OP[op]))
+    return lib().hko_rows_extreme(_p(hi), hi.size, _EXTREME_OP[op])
+
+
+def sample_extreme(t, op: str):
+    """hawk.max / hawk.min of the terms t: row extremes, then the canonical
+    finish, in t's dtype (float32 terms: the float32 mode)."""
+    f32 = np.asarray(t).dtype == np.float32
+    t = np.ascontiguousarray(t, dtype=np.float32 if f32 else np.float64)
+    if f32:
+        return np.float32(lib().hko_sample_extreme_f32(_p(t), t.size, _EXTREME_OP[op]))
+    return lib().hko_sample_extreme(_p(t), t.size, _EXTREME_OP[op])
 
 
 def band_row_sums(t):

@@ -429,6 +429,71 @@ def test_sample_sum_special_values():
     assert O.sample_sum(np.arange(1.0, 100001.0)) == 100000 * 100001 / 2
 
 
+EXTREME_SIZES = [1, 31, 32, 33, 1000, 100_003, 300_007]
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("n", EXTREME_SIZES)
+def test_sample_extremes_are_numpys_max_and_min(n, dtype):
+    """hawk.max / hawk.min on NaN-free data are exact: the oracle's rows and
+    finish give numpy's max and min bit for bit (a dropped row, a wrong
+    identity or a swapped op fails), in either dtype."""
+    g = np.random.default_rng(n)
+    x = (g.normal(size=n) * np.exp(3 * g.normal(size=n))).astype(dtype)
+    got_max, got_min = O.sample_extreme(x, "max"), O.sample_extreme(x, "min")
+    assert got_max.dtype == dtype if hasattr(got_max, "dtype") else dtype == np.float64
+    assert np.asarray(got_max, dtype).tobytes() == np.max(x).tobytes()
+    assert np.asarray(got_min, dtype).tobytes() == np.min(x).tobytes()
+
+
+@pytest.mark.parametrize("n", [1, 31, 33, 1000, 65536 + 17])
+def test_row_extremes_are_the_padded_rows_max_and_min(n):
+    """The rows, as the reference's own test checks them
+    (tests/test_sample_sum.py:303-306): a masked lane's identity (-inf for
+    max, +inf for min) fills the mask and the ragged row's tail."""
+    x = np.random.default_rng(n).uniform(-2, 2, n)
+    rows = -(-n // 32)
+
+    def per_row(t, fill):
+        return np.pad(t, (0, rows * 32 - n), constant_values=fill).reshape(rows, 32)
+    hi = O.row_extremes(np.where(x > 0, x, -np.inf), "max")
+    lo = O.row_extremes(np.where(x < 0, x, np.inf), "min")
+    assert np.array_equal(hi, per_row(np.where(x > 0, x, -np.inf), -np.inf).max(1))
+    assert np.array_equal(lo, per_row(np.where(x < 0, x, np.inf), np.inf).min(1))
+
+
+def test_extreme_nans_zeros_and_the_empty_run():
+    """What the reference's operators fix beyond numpy: a row ignores a NaN
+    (ssExtreme_, hawk/emit/wrapper.py:543-550) unless every lane is NaN; the
+    finish's np.where(a > b, a, b) (hawk/_cells.py:66-71) lets a NaN partial
+    on the left give way and one on the right win; +0 against -0 keeps the
+    row's lower slot and the finish's right operand; no samples give the
+    identity.  A transposed operand in either combine fails one of these."""
+    row = np.full(32, np.nan)
+    row[5], row[20] = 3.0, -1.0
+    assert O.sample_extreme(row, "max") == 3.0 and O.sample_extreme(row, "min") == -1.0
+    assert np.isnan(O.sample_extreme(np.full(32, np.nan), "max"))
+    # 40 NaNs: row 0 is NaN, row 1 ignores its 8 NaNs (-inf), the finish keeps the right
+    assert O.sample_extreme(np.full(40, np.nan), "max") == -np.inf
+    # rows [NaN, 1]: NaN > 1 is false, so the finish keeps 1; rows [1, NaN]: NaN
+    nan_then_one = np.concatenate([np.full(32, np.nan), np.ones(32)])
+    assert O.rows_extreme(np.array([np.nan, 1.0]), "max") == 1.0
+    assert O.sample_extreme(nan_then_one, "max") == 1.0
+    assert np.isnan(O.rows_extreme(np.array([1.0, np.nan]), "max"))
+    assert np.isnan(O.sample_extreme(nan_then_one[::-1].copy(), "min"))
+    # signed zeros: the row keeps slot l against slot l + off, the finish b on a tie
+    assert not np.signbit(O.sample_extreme(np.array([0.0, -0.0]), "max"))
+    assert np.signbit(O.sample_extreme(np.array([-0.0, 0.0]), "max"))
+    assert np.signbit(O.rows_extreme(np.array([0.0, -0.0]), "max"))
+    assert not np.signbit(O.rows_extreme(np.array([-0.0, 0.0]), "min"))
+    assert O.sample_extreme(np.zeros(0), "max") == -np.inf
+    assert O.sample_extreme(np.zeros(0, np.float32), "min") == np.float32(np.inf)
+    # a NaN that is a row's only finite-breaking value among infinities
+    x = np.full(64, -np.inf)
+    x[40] = np.nan
+    assert O.sample_extreme(x, "max") == -np.inf
+
+
 def _chain_kinks(x):
     """|t4| and |t6| of the chain: where either is near 0 the chain has a kink."""
     t4 = np.tanh(1.5 * np.sin(np.exp(x)) + 0.25)
