@@ -4,10 +4,12 @@ Reference ``hawk/trace/chain.py`` (the entry) and ``hawk/ir/chain.py`` (the
 binding).  Member ``j``'s read of a name binds to the value an earlier member
 committed under that name; any other read is an input of the chain.  A name
 no later member reads is an output; a name several members update in turn
-(each reading it first) keeps its last value.  The binding is a substitution
-in the IR: the composed body holds each intermediate as one value, read by
-any number of members, and stores none of them, so one per-sample stage runs
-the whole chain and the intermediates never reach HBM.
+(each reading it first) keeps its last value.  Binding replaces each such
+read with the committing member's node, so the composed program is one
+expression graph: an intermediate is computed once in a lane's registers,
+shared by every member that reads it, and never written to a plane.  One
+per-sample stage then runs the whole chain, and HBM sees only the chain's
+inputs and outputs.
 
 On gfx950 every boundary is fused, as the reference fuses every boundary
 on a GPU (``hawk/ir/fusion.py:10``): a lane's registers hold the chain.  The

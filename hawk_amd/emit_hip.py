@@ -35,7 +35,7 @@ from .ir import (FINISHED_PLANE, GUARD_MASK, AccumWrite, Assign, Deps, Finish, H
                  Program, SampleSum, free_inputs,
                  level_order)
 
-from .hip_target import HIP_WRITER, _literal  # noqa: E402  (the hip row's spellings)
+from .hip_target import HIP_WRITER, StageWalk, _literal  # noqa: E402  (the hip row's spellings)
 from .targets import TARGETS  # noqa: E402
 
 ABI_TAG = "aether-abi/2"
@@ -693,7 +693,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
 
     real = "float" if mode == "float32" else "double"
     wrap = target.wrapper
-    params, unpack = wrap.params(stage), wrap.unpack(stage)
+    walk = StageWalk.of(stage, block, per_thread, xcd_order)
     out = [
         f"// hawk gfx950 stage '{stage.name}' (generated; mode {'banded' if stage.banded else mode}).",
         f"typedef {real} Real;",
@@ -716,18 +716,18 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += _FOLD_HELPERS.splitlines()
     if stage.finish is not None:
         out += _FINISH_HELPER.splitlines()
-    out += wrap.entry_signature(stage, stage.name, block, params)
-    out += ["    " + u for u in unpack]
+    out += wrap.entry_signature(walk, stage.name).splitlines()
+    out += wrap.unpack(walk).splitlines()
     auto = _auto_loop(stage)
     if stage.guard is not None:
-        out += wrap.index_prologue(block, per_thread, xcd_order, form="guard")
+        out += wrap.index_prologue(form="guard").splitlines()
         out += _guarded_lines(stage, w, body, stores)
     elif not row_terms and not folds:
         if per_thread > 1 and deferred and deferred[0]:
             # a full block in two passes: every sample's values (and so every
             # load) first, then every store, so no load waits behind a store
             keep, commit = deferred
-            head = wrap.index_prologue(block, per_thread, xcd_order, form="full")
+            head = wrap.index_prologue(form="full").splitlines()
             at = next(i for i, line in enumerate(head) if line.startswith("    if (")) + 1
             out += head[:at] + [f"    Real hk_sv[{per_thread}][{len(keep)}];"] + head[at:]
             out += body + ["        " + line for line in keep]
@@ -736,34 +736,35 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
                     f"        const long long hk_i = base + (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * "
                     f"{block} + static_cast<long long>(threadIdx.x);"]
             out += ["        " + line for line in commit]
-            out += wrap.index_partial(block, per_thread)
+            out += wrap.index_partial().splitlines()
         elif per_thread > 1:
-            out += wrap.index_prologue(block, per_thread, xcd_order, form="full")
+            out += wrap.index_prologue(form="full").splitlines()
             out += body + stores
-            out += wrap.index_partial(block, per_thread)
+            out += wrap.index_partial().splitlines()
         else:
-            out += wrap.index_prologue(block, per_thread, xcd_order, form="plain")
+            out += wrap.index_prologue().splitlines()
         out += body + stores
     else:
         # Every lane of a half-wave takes part in its row's butterfly: a lane
         # past `count` computes sample `base` (always bound) and adds +0.
-        out += wrap.index_prologue(block, per_thread, xcd_order, form="live")
+        out += wrap.index_prologue(form="live").splitlines()
         out += body
         opened, closed = wrap.sample_sum_frame(len(row_terms), "Real", "")
-        out += opened + ["    " + line for line in stores] + closed
+        out += opened.splitlines() + ["    " + line for line in stores] + closed.splitlines()
         for k, (term, hi, comp, red) in enumerate(row_terms):
             if red == "sum":
                 out += w.spell.sample_sum(w, stage.banded, term, hi, comp)
             else:
                 out += w.spell.sample_extreme(w, red, term, hi)
         out += _fused_fold_lines(folds, block, whole)
-    out += wrap.index_epilogue()
+    out += wrap.index_epilogue().split("\n")
     if auto is not None:
         head = out.index(f'extern "C" __global__ void __launch_bounds__({block}) {stage.name}(')
         top = out[:head]
         if _STEPS_HELPERS.splitlines()[1] not in top:
             top += _STEPS_HELPERS.splitlines()
         out = top + out[head:]
+        params, unpack = wrap.params(walk), wrap.unpack(walk).splitlines()
         out += _range_entry(stage, w, body, stores, params, unpack, block, per_thread, xcd_order, auto)
         out += _persist_entry(stage, mode, params, unpack, block, nontemporal, auto)
     return "\n".join(out)
@@ -849,7 +850,7 @@ def _range_entry(stage, w, body, stores, params, unpack, block, per_thread, xcd_
            "        " + ",\n        ".join(params[:-3] + ["ScalarHandle hk_steps_m", "ScalarHandle hk_stepsum_m"]
                                          + params[-3:]) + ") {",
            "    (void)nSamples;"]
-    out += ["    " + u for u in unpack]
+    out += unpack                       # indented, as the wrapper spells it
     out += ["    unsigned int* hk_steps = reinterpret_cast<unsigned int*>(hk_steps_m.data);",
             "    unsigned long long* hk_stepsum = reinterpret_cast<unsigned long long*>(hk_stepsum_m.data);",
             "    unsigned int hk_ran = 0u;",
@@ -947,7 +948,7 @@ def _persist_entry(stage, mode, params, unpack, block, nontemporal, loop) -> lis
                                                       "ScalarHandle hk_stepsum_m", "long long hk_chunk"]
                                          + params[-3:]) + ") {",
            "    (void)nSamples;"]
-    out += ["    " + u for u in unpack]
+    out += unpack                       # indented, as the wrapper spells it
     out += ["    unsigned int* hk_next = reinterpret_cast<unsigned int*>(hk_next_m.data);",
             "    unsigned int* hk_steps = reinterpret_cast<unsigned int*>(hk_steps_m.data);",
             "    unsigned long long* hk_stepsum = reinterpret_cast<unsigned long long*>(hk_stepsum_m.data);",

@@ -19,6 +19,9 @@ reference's writers use their renderer's ``_emit`` and walk.
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
+from types import MappingProxyType
+from typing import Mapping
 
 from .ir import HawkError, Node
 
@@ -356,18 +359,67 @@ class HipWriter:
         _refuse("a zeroed plane row ahead of a lowered loop")
 
 
+@dataclass(frozen=True)
+class StageWalk:
+    """A per-sample stage seen the way the reference's wrapper seam sees a
+    kernel (``hawk/ir/walk.py:80-106``, the frozen ``Walk``): the slots in
+    ``arg_spec`` order, ``slot_of`` / ``slot_types`` (the inverse and type
+    projection of ``arg_spec``), the rows planes of the stage's reductions
+    over samples (``sample_sums``), and the finish's ``(mask, counter)``.
+    ``planes`` carries what the HIP spelling needs beyond the types (each
+    slot's variable and mirror kind), and the launch shape the geometry seam
+    binds: ``block`` threads a workgroup, ``per_thread`` samples a thread,
+    ``xcd_order`` (each XCD takes a contiguous eighth of the grid)."""
+
+    name: str
+    arg_spec: tuple
+    slot_of: Mapping
+    slot_types: Mapping
+    planes: Mapping
+    sample_sums: tuple = ()
+    finish: tuple | None = None
+    block: int = 256
+    per_thread: int = 1
+    xcd_order: bool = False
+
+    @classmethod
+    def of(cls, stage, block: int, per_thread: int = 1, xcd_order: bool = False) -> "StageWalk":
+        from .ir import TensorType
+
+        spec = tuple((role, name) for role, name in stage.arg_spec)
+        return cls(name=stage.name, arg_spec=spec,
+                   slot_of=MappingProxyType({slot: k for k, slot in enumerate(spec)}),
+                   slot_types=MappingProxyType({(role, name): TensorType(tuple(stage.planes[name]["shape"]),
+                                                                         stage.planes[name]["dtype"])
+                                                for role, name in spec}),
+                   planes=MappingProxyType({name: dict(stage.planes[name]) for _, name in spec}),
+                   sample_sums=tuple(r[2] for r in stage.row_sums),
+                   finish=tuple(stage.finish[:2]) if stage.finish is not None else None,
+                   block=int(block), per_thread=int(per_thread), xcd_order=bool(xcd_order))
+
+
+#: The output roles: a mirror the stage writes through (not const).
+_WRITTEN = ("mutable", "out", "wide_out", "key_out", "accum_out", "rows_out", "fold_scratch")
+
+
 class HipWrapper:
-    """How a per-sample stage is wrapped for the gfx950 launch: the entry's
-    signature (one by-value mirror per slot in ``arg_spec`` order, then the
-    partition triple, reference ``hawk/emit/cuda.py:46-54``), the unpacking of
-    the mirrors, and the one geometry seam (``i = base + flat``)."""
+    """How a per-sample stage is wrapped for the gfx950 launch, with the
+    reference wrapper seam's members and signatures
+    (``hawk/emit/wrapper.py:225-284``): ``entry_signature(walk, name)`` (one
+    by-value mirror per slot in ``arg_spec`` order, then the partition triple,
+    reference ``hawk/emit/cuda.py:46-54``; the body's first lines name the
+    launch shape as constants), ``unpack(walk)`` (each mirror's pointer),
+    ``index_prologue(segment=None, *, active=None, box=None)`` (THE one
+    geometry seam, ``i = base + flat`` over those constants) and
+    ``index_epilogue()``.  Each returns C++ text.  The reference's segmented,
+    active-map and box prologues have no form here and are refused by name."""
 
     qualifier = "__device__ __forceinline__"
 
-    def params(self, stage) -> list:
+    def params(self, walk) -> list:
         out = []
-        for role, name in stage.arg_spec:
-            info = stage.planes[name]
+        for role, name in walk.arg_spec:
+            info = walk.planes[name]
             var = info["var"]
             if info["kind"] in ("f64", "f32"):
                 out.append(f"Real {var}")
@@ -377,24 +429,26 @@ class HipWrapper:
                 out.append(f"ScalarHandle {var}_m")
         return out + ["long long base", "long long count", "long long nSamples"]
 
-    def entry_signature(self, stage, name: str, block: int, params: list | None = None) -> list:
-        params = self.params(stage) if params is None else params
-        return [f'extern "C" __global__ void __launch_bounds__({block}) {name}(',
-                "        " + ",\n        ".join(params) + ") {",
-                "    (void)nSamples;"]
+    def entry_signature(self, walk, name: str) -> str:
+        """The entry's declaration and opening: role mirrors in ``arg_spec``
+        order, the int64 partition triple, and the launch shape as the
+        constants ``hk_block``, ``hk_per_thread``, ``hk_xcd_order`` that the
+        geometry seam reads."""
+        return "\n".join([f'extern "C" __global__ void __launch_bounds__({walk.block}) {name}(',
+                          "        " + ",\n        ".join(self.params(walk)) + ") {",
+                          "    (void)nSamples;",
+                          f"    constexpr int hk_block = {walk.block}, hk_per_thread = {walk.per_thread};",
+                          f"    constexpr bool hk_xcd_order = {'true' if walk.xcd_order else 'false'};"])
 
-    def unpack(self, stage) -> list:
+    def unpack(self, walk) -> str:
         """Each mirror's pointer (and component stride, and a table's cells)."""
         out = []
-        for role, name in stage.arg_spec:
-            info = stage.planes[name]
+        for role, name in walk.arg_spec:
+            info = walk.planes[name]
             var, kind = info["var"], info["kind"]
             if kind in ("f64", "f32"):
                 continue
-            is_input = role not in ("mutable", "out", "wide_out", "key_out", "accum_out", "rows_out",
-                                    "fold_scratch")
-            if stage.finish is not None and name in stage.finish[:2]:
-                is_input = False          # the mask a finish sets and its counter
+            is_input = role not in _WRITTEN and not (walk.finish is not None and name in walk.finish)
             cq = "const " if is_input else ""
             elem = {"i32": "int", "u32": "unsigned int", "bool": "unsigned char"}.get(info["dtype"], "Real")
             if kind == "gref":
@@ -404,32 +458,37 @@ class HipWrapper:
                 out.append(f"{cq}{elem}* __restrict__ {var} = reinterpret_cast<{cq}{elem}*>({var}_m.data);")
                 if role in ("lookup", "accum_out", "fold_scratch"):
                     out.append(f"const unsigned long long {var}_n = {var}_m.samples;   // cells")
-        return out
+        return "\n".join("    " + line for line in out)
 
-    def index_prologue(self, block: int, per_thread: int, xcd_order: bool, form: str = "plain") -> list:
+    def index_prologue(self, segment=None, *, active=None, box=None, form: str = "plain") -> str:
         """The launch geometry: block ``i`` of the grid (XCD x takes a
-        contiguous eighth when ``xcd_order``), ``per_thread`` samples a thread,
-        and the lane's sample ``hk_i = base + hk_flat``.  ``form``: "plain" (a
-        lane past ``count`` leaves), "live" (it computes sample ``base`` and
-        stores nothing: a row sum or a fold needs every lane), "guard" (the
-        guarded stage binds ``hk_i`` itself)."""
-        if xcd_order:
-            # Workgroup i runs on XCD i % 8: with a grid of 8k workgroups, XCD x
-            # takes the contiguous blocks [x*k, (x+1)*k) (any other grid keeps the
-            # plain order), so each XCD's L2 streams one contiguous eighth.
-            out = ["    const unsigned hk_blk = (gridDim.x & 7u) ? blockIdx.x"
-                   " : (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3);"]
-        else:
-            out = ["    const unsigned hk_blk = blockIdx.x;"]
+        contiguous eighth when ``hk_xcd_order``), ``hk_per_thread`` samples a
+        thread, and the lane's sample ``hk_i = base + hk_flat``.  ``form``:
+        "plain" (a lane past ``count`` leaves), "live" (it computes sample
+        ``base`` and stores nothing: a row reduction or a fold needs every
+        lane), "full" (a block wholly below ``count`` runs an unguarded copy,
+        closed by :meth:`index_partial`), "guard" (the guarded stage binds
+        ``hk_i`` itself)."""
+        if segment is not None:
+            _refuse("a segmented unit's prologue (offsets-plane runs)")
+        if active is not None:
+            _refuse("an active-lane prologue (a device-read live count and lane map)")
+        if box is not None:
+            _refuse("a box prologue (a thread over several lanes of a box)")
+        # Workgroup i runs on XCD i % 8: with a grid of 8k workgroups, XCD x
+        # takes the contiguous blocks [x*k, (x+1)*k) (any other grid keeps the
+        # plain order), so each XCD's L2 streams one contiguous eighth.
+        out = ["    const unsigned hk_blk = (!hk_xcd_order || (gridDim.x & 7u)) ? blockIdx.x"
+               " : (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3);"]
         if form == "full":
             # a block whose samples all lie below `count` runs the unguarded
             # copy of the body: no exit between samples, so every sample's
             # loads can issue before the first store (the partial last block
             # takes the guarded copy that index_partial opens)
-            out += [f"    if ((static_cast<long long>(hk_blk) + 1) * {per_thread * block} <= count) {{"]
+            out += ["    if ((static_cast<long long>(hk_blk) + 1) * (hk_per_thread * hk_block) <= count) {"]
         out += ["#pragma unroll",
-                f"    for (int hk_v = 0; hk_v < {per_thread}; ++hk_v) {{",
-                f"        const long long hk_flat = (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * {block}"
+                "    for (int hk_v = 0; hk_v < hk_per_thread; ++hk_v) {",
+                "        const long long hk_flat = (static_cast<long long>(hk_blk) * hk_per_thread + hk_v) * hk_block"
                 " + static_cast<long long>(threadIdx.x);"]
         if form == "full":
             out += ["        const long long hk_i = base + hk_flat;"]
@@ -439,32 +498,36 @@ class HipWrapper:
         elif form == "live":
             out += ["        const bool hk_live = hk_flat < count;",
                     "        const long long hk_i = base + (hk_live ? hk_flat : 0LL);"]
-        return out
+        return "\n".join(out)
 
-    def index_partial(self, block: int, per_thread: int) -> list:
+    def index_partial(self) -> str:
         """After the full block's body (``form="full"``): close it and open the
         guarded loop of the partial last block."""
-        return ["    }", "    return;", "    }",
-                "#pragma unroll",
-                f"    for (int hk_v = 0; hk_v < {per_thread}; ++hk_v) {{",
-                f"        const long long hk_flat = (static_cast<long long>(hk_blk) * {per_thread} + hk_v) * {block}"
-                " + static_cast<long long>(threadIdx.x);",
-                "        if (hk_flat >= count) break;",
-                "        const long long hk_i = base + hk_flat;"]
+        return "\n".join(["    }", "    return;", "    }",
+                          "#pragma unroll",
+                          "    for (int hk_v = 0; hk_v < hk_per_thread; ++hk_v) {",
+                          "        const long long hk_flat = (static_cast<long long>(hk_blk) * hk_per_thread + hk_v)"
+                          " * hk_block + static_cast<long long>(threadIdx.x);",
+                          "        if (hk_flat >= count) break;",
+                          "        const long long hk_i = base + hk_flat;"])
 
-    def index_epilogue(self) -> list:
-        return ["    }", "}", ""]
+    def index_epilogue(self) -> str:
+        return "    }\n}\n"
 
     def fold_rows(self, width: int) -> int:
         """Rows of 32 samples a wave64 reduces at once: a half-wave is a row."""
         return 2
 
     def sample_sum_frame(self, width: int, elem: str, store: str, op: str = "sum", live: str | None = None) -> tuple:
-        """(open, close) around the row sums of a stage: every lane takes part
-        (``hk_live``), the stores of a live lane only."""
-        if op != "sum":
+        """(open, close) around the row reductions of a stage: every lane
+        takes part (``hk_live``), the stores of a live lane only.  A sum, a
+        max and a min share it; a prefix form's device-read ``live`` count
+        has no form here."""
+        if op not in ("sum", "max", "min"):
             _refuse(f"a sample reduction by {op!r}")
-        return (["        if (hk_live) {"], ["        }"])
+        if live is not None:
+            _refuse("a sample reduction over a device-read live count")
+        return ("        if (hk_live) {", "        }")
 
     def dispatch(self, kind_spelling: str, branch_spellings, policy: str, **kw) -> str:
         _refuse("a multi-branch dispatch")

@@ -192,7 +192,9 @@ def test_chain_forward_is_the_oracle_expression():
 def test_emitted_source_has_one_geometry_prologue():
     from hawk_amd.emit_hip import plan_kernel
     src = plan_kernel(E.energy.program, "energy").source
-    assert src.count("blockIdx.x") == 1 and src.count("hk_i = base + hk_flat") == 1
+    geometry = [line for line in src.splitlines() if "blockIdx.x" in line]
+    assert len(geometry) == 1 and "const unsigned hk_blk =" in geometry[0]
+    assert src.count("hk_i = base + hk_flat") == 1
     assert 'eagle_abi_tag[] = "aether-abi/2"' in src
     assert "eagle_layout_sizes[5] = {40, 32, 32, 8, 24}" in src
 

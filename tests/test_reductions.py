@@ -310,3 +310,32 @@ def test_nan_rows_follow_the_reference_operators(built, gpu):
         hawk.run(k, x=dev(x, gpu), t=out)
         want = np.asarray(O.sample_extreme(x * np.dtype(mode).type(1.5), "max"), mode)
         assert host(out)[0].tobytes() == want.tobytes(), x
+
+
+@pytest.fixture(scope="module")
+def built_banded(tmp_path_factory):
+    root = tmp_path_factory.mktemp("reduce_banded")
+    hawk.build([cell_max, cell_min, cell_mean, fold_vec], root, mode="banded")
+    return root
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", (1, 33, 100_003))
+def test_banded_cells(built_banded, gpu, n):
+    """The banded mode: max / min take the same exact rows and finish; a mean
+    and a vector cell's entries are band sums (the oracle's band rows and
+    finish), bit for bit."""
+    x = _x(n, "float64")
+    print(f"banded reductions n={n}", flush=True)
+    for op in ("max", "min"):
+        out = dev(np.full(1, np.nan), gpu)
+        hawk.run(hawk.load(built_banded, f"cell_{op}"), x=dev(x, gpu), t=out)
+        want = (x * 1.5).max() if op == "max" else (x * 1.5).min()
+        assert host(out)[0] == want
+    out = dev(np.full(1, np.nan), gpu)
+    hawk.run(hawk.load(built_banded, "cell_mean"), x=dev(x, gpu), t=out)
+    assert host(out)[0] == O.band_sample_sum((x * x) / float(n))
+    v = rng(n + 9).normal(size=(3, n))
+    t = dev(np.full(3, np.nan), gpu)
+    hawk.run(hawk.load(built_banded, "fold_vec"), v=dev(v, gpu), t=t)
+    assert host(t).tolist() == [O.band_sample_sum(v[k] * 2.0) for k in range(3)]

@@ -57,13 +57,75 @@ def test_the_renderer_spells_through_the_rows_writer():
 
 def test_the_renderer_wraps_through_the_rows_wrapper():
     class Ordered(HipWrapper):
-        def index_prologue(self, block, per_thread, xcd_order, form="plain"):
-            return super().index_prologue(block, per_thread, True, form)
+        def entry_signature(self, walk, name):
+            return super().entry_signature(dataclasses.replace(walk, xcd_order=True), name)
     base = plan_kernel(E.twobody.program, "twobody").source
     other = plan_kernel(E.twobody.program, "twobody",
                         target=dataclasses.replace(TARGETS["hip"], wrapper=Ordered())).source
-    assert "const unsigned hk_blk = blockIdx.x;" in base and "(gridDim.x & 7u)" not in base
-    assert "(gridDim.x & 7u)" in other and "const unsigned hk_blk = blockIdx.x;" not in other
+    assert "constexpr bool hk_xcd_order = false;" in base
+    assert other == base.replace("constexpr bool hk_xcd_order = false;", "constexpr bool hk_xcd_order = true;")
+
+
+#: The reference's wrapper seam (hawk/emit/wrapper.py:225-284): each member's
+#: parameters as (name, kind, default), ``self`` left out.
+_P, _K, _V = "POSITIONAL_OR_KEYWORD", "KEYWORD_ONLY", "VAR_KEYWORD"
+_NONE = object()
+REFERENCE_WRAPPER = {
+    "entry_signature": [("walk", _P, _NONE), ("name", _P, _NONE)],
+    "index_prologue": [("segment", _P, None), ("active", _K, None), ("box", _K, None)],
+    "index_epilogue": [],
+    "unpack": [("walk", _P, _NONE)],
+    "fold_rows": [("width", _P, _NONE)],
+    "sample_sum_frame": [("width", _P, _NONE), ("elem", _P, _NONE), ("store", _P, _NONE), ("op", _P, "sum"),
+                         ("live", _P, None)],
+    "dispatch": [("kind_spelling", _P, _NONE), ("branch_spellings", _P, _NONE), ("policy", _P, _NONE),
+                 ("kw", _V, _NONE)],
+}
+
+
+@pytest.mark.parametrize("member", sorted(REFERENCE_WRAPPER))
+def test_the_wrapper_members_take_the_reference_parameters(member):
+    """Each member accepts the reference's parameters, in its order and
+    kinds, with its defaults; extra parameters only after them, keyword-only
+    with a default (the hip prologue's ``form``), so a reference call binds."""
+    import inspect
+    params = list(inspect.signature(getattr(TARGETS["hip"].wrapper, member)).parameters.values())
+    want = REFERENCE_WRAPPER[member]
+    got = [(q.name, q.kind.name, _NONE if q.default is inspect.Parameter.empty else q.default)
+           for q in params[:len(want)]]
+    assert got == want
+    for extra in params[len(want):]:
+        assert extra.kind is inspect.Parameter.KEYWORD_ONLY and extra.default is not inspect.Parameter.empty
+
+
+def test_the_wrapper_answers_the_reference_calls():
+    """The calls the reference's renderer makes (hawk/emit/render.py), over a
+    walk of a planned stage: the text of each member is the stage's own."""
+    import re
+
+    from hawk_amd.hip_target import StageWalk
+    plan = plan_kernel(E.twobody.program, "twobody", block=128)
+    per_thread = int(re.search(r"hk_per_thread = (\d+);", plan.source).group(1))
+    walk = StageWalk.of(plan.stage, 128, per_thread)
+    wrap = TARGETS["hip"].wrapper
+    assert walk.arg_spec == tuple(tuple(x) for x in plan.stage.arg_spec)
+    assert [walk.slot_of[slot] for slot in walk.arg_spec] == list(range(len(walk.arg_spec)))
+    assert walk.slot_types[("uniform", "mu")].dtype == "f64"
+    assert walk.slot_types[("vec_in", "r0")].shape == (3,)
+    sig = wrap.entry_signature(walk, "twobody")
+    unpack = wrap.unpack(walk)
+    prologue = wrap.index_prologue()
+    epilogue = wrap.index_epilogue()
+    for text in (sig, unpack, prologue, epilogue):
+        assert isinstance(text, str) and text in plan.source
+    assert sig.startswith('extern "C" __global__ void __launch_bounds__(128) twobody(')
+    assert "GRefMirror hk_p_r0_m" in sig and sig.index("hk_p_r0_m") < sig.index("long long base")
+    assert "const Real* __restrict__ hk_p_r0" in unpack and "Real* __restrict__ hk_p_r =" in unpack
+    assert "const long long hk_i = base + hk_flat;" in prologue
+    for kw, words in (({"segment": object()}, "segmented unit"), ({"active": object()}, "active-lane"),
+                      ({"box": object()}, "box prologue")):
+        with pytest.raises(HawkError, match=words):
+            wrap.index_prologue(**kw)
 
 
 def test_a_row_builds_only_its_modes():
@@ -88,8 +150,10 @@ def test_writer_members_without_a_form_are_refused_by_name(member, args, words):
 def test_wrapper_members_without_a_form_are_refused_by_name():
     with pytest.raises(HawkError, match="multi-branch dispatch"):
         TARGETS["hip"].wrapper.dispatch("k", ["a", "b"], "select")
-    with pytest.raises(HawkError, match="sample reduction by 'max'"):
-        TARGETS["hip"].wrapper.sample_sum_frame(1, "double", "", op="max")
+    with pytest.raises(HawkError, match="sample reduction by 'prod'"):
+        TARGETS["hip"].wrapper.sample_sum_frame(1, "double", "", op="prod")
+    with pytest.raises(HawkError, match="device-read live count"):
+        TARGETS["hip"].wrapper.sample_sum_frame(1, "double", "", live="hawk_live")
 
 
 def test_an_unknown_row_is_refused():
