@@ -1162,13 +1162,15 @@ __global__ __launch_bounds__(256) void hawk_fill_zero(T* __restrict__ p, long lo
 
 // Cell c adds its chunk partials in chunk order from +0.0, then onto the
 // target: target[c] += sum (reference hawk/emit/team.py:437-460).  Two blocks
-// of kAhead chunks are in flight while a third is added.
+// of kAhead chunks are in flight while a third is added: 64 loads a thread,
+// since a grid of one thread per cell (65536 at the split walk's largest)
+// holds only a wave or two per SIMD to cover HBM's latency.
 template <class T>
 __global__ __launch_bounds__(256) void hawk_scatter_cells(const T* __restrict__ parts, long long cells,
                                                           int chunks, T* __restrict__ target) {
     const long long c = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     if (c >= cells) return;
-    constexpr int kAhead = 8;
+    constexpr int kAhead = 32;
     auto fetch = [&](int b, T (&x)[kAhead]) {
 #pragma unroll
         for (int q = 0; q < kAhead; ++q) {
@@ -1210,61 +1212,98 @@ __global__ void hawk_scatter_status(int* status, long long cells) {
 //
 // * hawk_split_hot: one workgroup per chunk, keys [0, kSplitHot) in LDS.  Each
 //   tile of 4096 lanes is split stably into buckets in one pass: window keys
-//   0..15 each a bucket of their own, keys 16..kSplitHot-1 sixteen classes by
-//   key & 15, and keys from kSplitHot up one bucket per tail range of
-//   kSplitHot keys.  Wave c then folds bucket c (a single key: one chain of
-//   adds over a contiguous run) and class c (64 entries at a time: equal keys
-//   find each other, and the lowest lane adds its group in lane order onto the
-//   key's accumulator; a wave's LDS operations complete in issue order, so a
-//   key's groups meet the accumulator window after window).  The tail buckets
-//   are one contiguous run, copied to the tile's slot of the chunk's bin with
-//   the offset of each range.
-// * hawk_split_tail: one workgroup per (chunk, tail range), keys of the range
-//   in LDS; it reads the range's segment of every slot in tile order (lane
-//   order), a batch of whole segments at a time, and folds them as above.
+//   0..31 each a bucket of their own, keys 32..kSplitHot-1 fifteen classes by
+//   (key - 32) % 15, and keys from kSplitHot up one bucket per tail range of
+//   kTailRange keys.  Wave 0 then folds the head buckets (lane c the chain of
+//   key c over its contiguous run) and wave w class w - 1 (64 entries at a
+//   time: equal keys find each other, and the lowest lane adds its group in
+//   lane order onto the key's accumulator; a wave's LDS operations complete in
+//   issue order, so a key's groups meet the accumulator window after window).
+//   The tail buckets go from registers to the tile's slot of the chunk's bin,
+//   with the offset of each range.
+// * hawk_split_tail: one workgroup of 8 waves per (chunk, tail range), the
+//   range's keys in LDS, two workgroups a CU; it reads the range's segment of
+//   every slot in tile order (lane order), a batch of 2048 entries at a time,
+//   and folds them in eight classes by key & 7 as above.
 //
 // Both write every key's accumulator of their window to parts[b] (+0.0 for a
 // key no lane named); hawk_scatter_cells then adds the partials in chunk order.
-constexpr int kSplitHot = 12288;                 // keys a workgroup keeps in LDS (96 KiB of accumulators)
+constexpr int kSplitHot = 12288;                 // keys hawk_split_hot keeps in LDS (96 KiB of accumulators)
+constexpr int kTailRange = 6144;                 // keys a hawk_split_tail workgroup keeps in LDS (48 KiB)
 constexpr long long kSplitCells = 65536;         // the split walk's largest cell count
-constexpr int kSplitMaxRanges = static_cast<int>((kSplitCells - kSplitHot + kSplitHot - 1) / kSplitHot);  // 5
+constexpr int kSplitMaxRanges = static_cast<int>((kSplitCells - kSplitHot + kTailRange - 1) / kTailRange);  // 9
 constexpr int kSplitHeads = 32;                  // buckets 0..31: window keys 0..31, a chain each
-constexpr int kSplitClassBase = kSplitHeads;     // buckets 32..47: classes (window keys >= 32 by key & 15)
-constexpr int kSplitTailBase = kSplitClassBase + 16;   // 48..: tail ranges
-constexpr int kSplitStride = kSplitTailBase + kSplitMaxRanges + 3;   // 56: a wave's row of bucket counts
+constexpr int kSplitClassBase = kSplitHeads;     // classes from bucket 32 (hot: 32..46; tail: 32..39)
+constexpr int kSplitTailBase = kSplitClassBase + 16;   // 48..56: hawk_split_hot's tail ranges
 constexpr int kSplitNone = 63;                   // a lane that adds nothing (skip key, bad key, padding)
+constexpr int kHotStride = kSplitTailBase + kSplitMaxRanges + 3;   // 60: a wave's row of bucket counts
+constexpr int kTailClassBits = 3;                // hawk_split_tail's classes: key & 7
+constexpr int kTailClasses = 1 << kTailClassBits;
+constexpr int kTailStride = kSplitClassBase + kTailClasses + 8;   // 48
+constexpr int kTailWaves = kTailClasses;         // a wave per class
+constexpr int kTailThreads = 64 * kTailWaves;
+constexpr int kTailBatch = kTailThreads * kWalkItems;   // 2048 entries a batch
 
-static_assert(kSplitHot < (1 << 14), "class matching covers key bits 4..13");
-static_assert(kSplitStride >= kSplitTailBase + kSplitMaxRanges + 1, "bucket starts need one past the last bucket");
-static_assert(kSplitNone >= kSplitStride, "the no-bucket code is outside the count rows");
+static_assert(kSplitHot - kSplitHeads < (1 << 15), "hot_class_index is exact below 2^15");
+static_assert((kSplitHot - kSplitHeads) / 15 < 1024 && (kTailRange >> kTailClassBits) <= 1024,
+              "class matching covers a class index of ten bits");
+static_assert(kHotStride >= kSplitTailBase + kSplitMaxRanges + 1, "bucket starts need one past the last bucket");
+static_assert(kTailStride >= kSplitClassBase + kTailClasses + 1, "bucket starts need one past the last bucket");
+static_assert(kSplitNone >= kHotStride && kSplitNone >= kTailStride, "the no-bucket code is outside the count rows");
+static_assert(kTailRange < (1 << 16), "bins hold window-local keys as u16");
 
 constexpr int kSplitPad = 72;                    // entries read (and ignored) past a run's end
-constexpr unsigned kPeerSlots = 128;             // a class fold's match slots: key bits 4..10
-#ifndef HK_HEAD_BLOCK
-#define HK_HEAD_BLOCK 8
-#endif
-constexpr int kHeadBlock = HK_HEAD_BLOCK;        // a head chain's reads in flight: four blocks of kHeadBlock
+constexpr unsigned kPeerSlots = 128;             // a class fold's match slots: class-index bits 0..6
+constexpr int kHeadBlock = 8;                    // a head chain's reads in flight: four blocks of kHeadBlock
 static_assert(4 * kHeadBlock <= kSplitPad, "a head chain reads at most kSplitPad entries past its run");
 
-template <class T>
+// A split walk workgroup's LDS: Waves waves, Window accumulators, count rows
+// of Stride buckets, and the split tile (Waves * 256 entries).
+template <class T, int Waves, int Window, int Stride>
 struct SplitShared {
-    T acc[kSplitHot];                          // 96 KiB: the window's accumulators
-    T val[kTile + kSplitPad];                  // 32 KiB: the tile's values, bucket order
-    unsigned short key[kTile + kSplitPad];          //  8 KiB: their window-local keys
-    union {                                         // 16 KiB, one phase at a time:
-        unsigned long long win[kWalkWaves][kSplitStride];              // split: a match table per wave
+    static constexpr int kWaves = Waves;
+    static constexpr int kStride = Stride;
+    static constexpr int kSpan = Waves * 64 * kWalkItems;
+    T acc[Window];                              // the window's accumulators
+    T val[kSpan + kSplitPad];                   // the tile's values, bucket order
+    unsigned short key[kSpan + kSplitPad];      // their window-local keys
+    union {                                     // one phase at a time:
+        unsigned long long win[Waves][Stride];                 // split: a match table per wave
         struct {
-            unsigned long long peer[kWalkWaves][kPeerSlots];           // fold: per-wave match masks (16 KiB)
+            unsigned long long peer[Waves][kPeerSlots];        // fold: per-wave match masks
         } f;
     };
-    unsigned cnt[kWalkWaves][kSplitStride];         // 3.5 KiB: bucket counts, a row per wave (lane b reads word b)
-    unsigned bstart[kSplitStride + 1];              // bucket d holds [bstart[d], bstart[d+1])
+    unsigned cnt[Waves][Stride];                // bucket counts, a row per wave (lane b reads word b)
+    unsigned bstart[Stride + 1];                // bucket d holds [bstart[d], bstart[d+1])
 };
+template <class T>
+using HotShared = SplitShared<T, kWalkWaves, kSplitHot, kHotStride>;      // 157 KiB (float64)
+template <class T>
+using TailShared = SplitShared<T, kTailWaves, kTailRange, kTailStride>;   // 78 KiB (float64): two a CU
+static_assert(sizeof(TailShared<double>) <= 80 * 1024, "two tail workgroups share a CU's 160 KiB");
 
-// The bucket of window-local key kl (0 <= kl < window).
-__device__ __forceinline__ int split_bucket(unsigned kl) {
-    return kl < static_cast<unsigned>(kSplitHeads) ? static_cast<int>(kl) : kSplitClassBase + static_cast<int>(kl & 15u);
+// The bucket of window-local key kl (0 <= kl < window) in hawk_split_hot:
+// keys 0..31 a head bucket each; keys from 32 up one of fifteen classes by
+// (kl - 32) % 15, so the fifteen class waves share the window evenly.
+__device__ __forceinline__ unsigned hot_class_index(unsigned kl) {   // (kl - 32) / 15, exact below 2^15
+    return ((kl - static_cast<unsigned>(kSplitHeads)) * 34953u) >> 19;
 }
+__device__ __forceinline__ int split_bucket(unsigned kl) {
+    const unsigned u = kl - static_cast<unsigned>(kSplitHeads);
+    return kl < static_cast<unsigned>(kSplitHeads) ? static_cast<int>(kl)
+                                                   : kSplitClassBase + static_cast<int>(u - 15u * hot_class_index(kl));
+}
+
+// Where hawk_split_hot's split puts the tile's tail entries: straight from
+// registers into the tile's slot of the chunk's bin, in bucket order, with
+// the offset of each tail range in the tile's row of bin_off.
+template <class T>
+struct TailSink {
+    unsigned short* key = nullptr;
+    T* val = nullptr;
+    unsigned* off = nullptr;
+    int ranges = 0;
+};
 
 // Stable split of the tile held in registers (thread slot j of wave w is tile
 // position w*256 + j*64 + lane) into nb buckets: sh.key/sh.val in bucket order,
@@ -1272,25 +1311,26 @@ __device__ __forceinline__ int split_bucket(unsigned kl) {
 // its four windows one after another in one table, so a lane's rank is the
 // count of its bucket in the wave's earlier windows plus the lanes below it
 // in its own.  Every wave then forms its own positions from all waves'
-// counts.  Starts and ends with every thread of the workgroup.
-template <class T>
-__device__ void split_tile(SplitShared<T>& sh, const unsigned (&kl)[kWalkItems], const int (&d)[kWalkItems],
-                           const T (&vv)[kWalkItems], int nb) {
+// counts.  With Sink, entries of a tail bucket go to the sink instead of LDS.
+// Starts and ends with every thread of the workgroup.
+template <class T, class Sh, bool Sink>
+__device__ void split_tile(Sh& sh, const unsigned (&kl)[kWalkItems], const int (&d)[kWalkItems],
+                           const T (&vv)[kWalkItems], int nb, const TailSink<T>& sink) {
     const int t = threadIdx.x;
     const int wave = t >> 6;
     const int lane = t & 63;
     const unsigned long long me = 1ull << lane;
-    unsigned long long* tab = sh.win[wave];
+    unsigned long long own[kWalkItems], mine[kWalkItems];
     // Window j: clear the table, OR every lane's bit into its bucket's slot,
     // read the lane's own slot and (lane b) slot b.  The four windows' LDS
     // operations run back to back: a wave's LDS operations complete in issue
     // order, so each window's reads see its own ORs and precede the next
     // window's clear.
-    const int b = lane < kSplitStride ? lane : 0;
-    unsigned long long own[kWalkItems], mine[kWalkItems];
+    unsigned long long* tab = sh.win[wave];
+    const int b = lane < Sh::kStride ? lane : 0;
 #pragma unroll
     for (int j = 0; j < kWalkItems; ++j) {
-        if (lane < kSplitStride) tab[lane] = 0ull;
+        if (lane < Sh::kStride) tab[lane] = 0ull;
         __builtin_amdgcn_wave_barrier();
         if (d[j] != kSplitNone) atomicOr(&tab[d[j]], me);
         __builtin_amdgcn_wave_barrier();
@@ -1299,24 +1339,18 @@ __device__ void split_tile(SplitShared<T>& sh, const unsigned (&kl)[kWalkItems],
         __builtin_amdgcn_wave_barrier();
     }
     // lane b: bucket b's count in each window and the running count before
-    // each; each item then takes its bucket's running count from lane d (a
+    // each; each item later takes its bucket's position from lane d (a
     // permute) and adds the lanes below it in its window
-    unsigned run[kWalkItems];
+    unsigned run[kWalkItems], below[kWalkItems];
     unsigned total = 0u;
 #pragma unroll
     for (int j = 0; j < kWalkItems; ++j) {
         run[j] = total;
         total += static_cast<unsigned>(__popcll(mine[j]));
+        below[j] = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(own[j] >> 32),
+                                             __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(own[j]), 0u));
     }
-    if (lane < kSplitStride) sh.cnt[wave][lane] = total;
-    unsigned rank[kWalkItems];
-#pragma unroll
-    for (int j = 0; j < kWalkItems; ++j) {
-        const int dj = d[j] != kSplitNone ? d[j] : 0;
-        rank[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(dj << 2, static_cast<int>(run[j]))) +
-                  __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(own[j] >> 32),
-                                            __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(own[j]), 0u));
-    }
+    if (lane < Sh::kStride) sh.cnt[wave][lane] = total;
     __syncthreads();
     // lane b: bucket b's total over the waves, the earlier waves' share of it,
     // and (a scan over the lanes) where bucket b starts
@@ -1324,7 +1358,7 @@ __device__ void split_tile(SplitShared<T>& sh, const unsigned (&kl)[kWalkItems],
     if (lane < nb) {
         // word b of every wave's row: consecutive lanes, consecutive banks
 #pragma unroll
-        for (int w = 0; w < kWalkWaves; ++w) {
+        for (int w = 0; w < Sh::kWaves; ++w) {
             const unsigned c = sh.cnt[w][lane];
             before += w < wave ? c : 0u;
             sum += c;
@@ -1333,13 +1367,25 @@ __device__ void split_tile(SplitShared<T>& sh, const unsigned (&kl)[kWalkItems],
     const unsigned start = wave_inclusive_scan(sum) - sum;
     if (wave == 0 && lane <= nb) sh.bstart[lane] = start;
     const unsigned base = start + before;
+    unsigned ts = 0u;
+    if constexpr (Sink) {
+        ts = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(start), kSplitTailBase));
+        if (sink.ranges > 0 && wave == 0 && lane >= kSplitTailBase && lane <= kSplitTailBase + sink.ranges)
+            sink.off[lane - kSplitTailBase] = start - ts;
+    }
 #pragma unroll
     for (int j = 0; j < kWalkItems; ++j) {
         const int dj = d[j] != kSplitNone ? d[j] : 0;
-        const unsigned p = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(dj << 2, static_cast<int>(base))) + rank[j];
+        const unsigned p =
+                static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(dj << 2, static_cast<int>(base + run[j]))) + below[j];
         if (d[j] != kSplitNone) {
-            sh.key[p] = static_cast<unsigned short>(kl[j]);
-            sh.val[p] = vv[j];
+            if (Sink && d[j] >= kSplitTailBase) {
+                sink.key[p - ts] = static_cast<unsigned short>(kl[j]);
+                sink.val[p - ts] = vv[j];
+            } else {
+                sh.key[p] = static_cast<unsigned short>(kl[j]);
+                sh.val[p] = vv[j];
+            }
         }
     }
     __syncthreads();
@@ -1374,8 +1420,8 @@ __device__ __forceinline__ void head_block(T (&r)[kHeadBlock], T& a, const T* sr
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <class T>
-__device__ void fold_heads(SplitShared<T>& sh) {
+template <class T, class Sh>
+__device__ void fold_heads(Sh& sh) {
     const int lane = threadIdx.x & 63;
     if (lane >= kSplitHeads) return;
     const int s = static_cast<int>(sh.bstart[lane]);
@@ -1415,19 +1461,18 @@ __device__ void fold_heads(SplitShared<T>& sh) {
     sh.acc[lane] = a;
 }
 
-// The caller's wave folds class c of the split tile (window keys >= 32 with
-// key & 15 == c), 64 entries a window in lane order.  Equal keys of a window
-// find each other through the wave's match table: key bits 4..10 pick one of
-// kPeerSlots slots, every lane ORs its bit into its slot, and three ballots
-// over bits 11..13 keep the lanes whose whole key is equal.  A window whose
-// keys are all distinct adds each value onto its key's accumulator at once.
-// Otherwise the window's values are regrouped in place, key by key (keys in
-// the order of their first lane, each key's values in lane order), and each
-// key's first lane adds its run onto the accumulator.  A wave's LDS
-// operations complete in issue order, so a key's windows meet the
+// The caller's wave folds class c of the split tile, 64 entries a window in
+// lane order.  Within a class a key is named by its index m (hot: (kl - 32)
+// / 15; tail: kl >> 3), below 1024.  Equal keys of a window find each other
+// through the wave's match table: bits 0..6 of m pick one of kPeerSlots
+// slots, every lane ORs its bit into its slot, and three ballots over bits
+// 7..9 keep the lanes whose whole key is equal.  The lowest lane of each key
+// adds its own value and then its peers' (read back from the class's run, in
+// lane order) onto the accumulator it read with the match.  A wave's LDS
+// operations complete in issue order, so a key's windows meet its
 // accumulator one after another.
-template <class T>
-__device__ void fold_class(SplitShared<T>& sh, int c) {
+template <class T, class Sh, bool Hot>
+__device__ void fold_class(Sh& sh, int c) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const unsigned long long me = 1ull << lane;
@@ -1446,45 +1491,40 @@ __device__ void fold_class(SplitShared<T>& sh, int c) {
             nx = sh.val[base + 64 + lane];
         }
         const unsigned kv = valid ? k : 0u;
-        const unsigned h = (kv >> 4) & (kPeerSlots - 1u);
+        const unsigned m = Hot ? hot_class_index(kv) : (kv >> kTailClassBits);
+        const unsigned h = m & (kPeerSlots - 1u);
         if (valid) atomicOr(&peer[h], me);
         __builtin_amdgcn_wave_barrier();
         unsigned long long pm = valid ? peer[h] : 0ull;
+        const T a0 = valid ? sh.acc[kv] : T(0);
         __builtin_amdgcn_wave_barrier();
         if (valid) peer[h] = 0ull;
 #pragma unroll
-        for (int bit = 11; bit < 14; ++bit) {
-            const bool one = (kv >> bit) & 1u;
+        for (int bit = 7; bit < 10; ++bit) {
+            const bool one = (m >> bit) & 1u;
             const unsigned long long ones = __ballot(valid && one);
             pm &= one ? ones : ~ones;
         }
-        // rank: the lanes of my key below me
-        const unsigned rank = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(pm >> 32),
-                                                        __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(pm), 0u));
-        if (__ballot(valid && rank != 0u) == 0ull) {
-            if (valid) sh.acc[kv] = sh.acc[kv] + x;
-        } else {
-            const unsigned size = static_cast<unsigned>(__popcll(pm));
-            const bool lead = valid && rank == 0u;
-            const unsigned gsz = lead ? size : 0u;
-            const unsigned gs = wave_inclusive_scan(gsz) - gsz;       // where my key's run starts (leaders)
-            const int first = valid ? static_cast<int>(__builtin_ctzll(pm)) : lane;
-            const unsigned g0 = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(first << 2, static_cast<int>(gs)));
-            if (valid) sh.val[base + g0 + rank] = x;
-            __builtin_amdgcn_wave_barrier();
-            if (lead) {
-                T a = sh.acc[kv];
-                const T* run = sh.val + base + gs;
-                for (unsigned u = 0; u < size; u += 8) {
-                    T y[8];
+        if (valid && (pm & (me - 1ull)) == 0ull) {
+            // the key's lowest lane: its value, then its peers' in lane order
+            T a = a0 + x;
+            unsigned long long rest = pm & ~me;
+            while (rest != 0ull) {
+                T y[8];
+                int got = 0;
 #pragma unroll
-                    for (int q = 0; q < 8; ++q) y[q] = run[u + q];
-#pragma unroll
-                    for (int q = 0; q < 8; ++q)
-                        if (u + q < size) a = a + y[q];
+                for (int q = 0; q < 8; ++q) {
+                    if (rest != 0ull) {
+                        y[q] = sh.val[base + static_cast<int>(__builtin_ctzll(rest))];
+                        rest &= rest - 1ull;
+                        got = q + 1;
+                    }
                 }
-                sh.acc[kv] = a;
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    if (q < got) a = a + y[q];
             }
+            sh.acc[kv] = a;
         }
         __builtin_amdgcn_wave_barrier();
         k = nk;
@@ -1492,55 +1532,66 @@ __device__ void fold_class(SplitShared<T>& sh, int c) {
     }
 }
 
-// The split tile's folds: wave 0 the head keys' chains, wave w (1..15) class
-// w, and wave 1 class 0 as well.  A class wave first clears its match table
-// (it shares LDS with the split's tables); each window leaves it clear.
+// The split tile's folds in hawk_split_hot: wave 0 the head keys' chains,
+// wave w (1..15) class w - 1.  A class wave first clears its match table (it
+// shares LDS with the split's tables); each window leaves it clear.
 template <class T>
-__device__ void split_fold(SplitShared<T>& sh) {
+__device__ void split_fold(HotShared<T>& sh) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     if (wave == 0) {
-        fold_heads(sh);
+        fold_heads<T>(sh);
         return;
     }
 #pragma unroll
     for (unsigned i = 0; i < kPeerSlots; i += 64) sh.f.peer[wave][i + lane] = 0ull;
     __builtin_amdgcn_wave_barrier();
-    fold_class(sh, wave);
-    if (wave == 1) fold_class(sh, 0);
+    fold_class<T, HotShared<T>, true>(sh, wave - 1);
 }
+
+// hawk_split_tail's folds: wave w folds class w (keys with kl & 7 == w).
+template <class T>
+__device__ void split_fold_tail(TailShared<T>& sh) {
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (unsigned i = 0; i < kPeerSlots; i += 64) sh.f.peer[wave][i + lane] = 0ull;
+    __builtin_amdgcn_wave_barrier();
+    fold_class<T, TailShared<T>, false>(sh, wave);
+}
+
 // The window's partials of chunk b, every key [klo, klo+window): a key no
 // lane named holds +0.0, the walk's starting value.
-template <class T>
-__device__ void split_store(SplitShared<T>& sh, long long b, long long cells, long long klo, int window,
+template <class T, class Sh>
+__device__ void split_store(Sh& sh, long long b, long long cells, long long klo, int window,
                             T* __restrict__ parts) {
     __syncthreads();
     T* row = parts + b * cells + klo;
-    for (int k = threadIdx.x; k < window; k += kWalkThreads) row[k] = sh.acc[k];
+    for (int k = threadIdx.x; k < window; k += Sh::kWaves * 64) row[k] = sh.acc[k];
 }
 
-template <class T>
-__device__ void split_clear(SplitShared<T>& sh, int window) {
-    for (int k = threadIdx.x; k < window; k += kWalkThreads) sh.acc[k] = T(0);
+template <class T, class Sh>
+__device__ void split_clear(Sh& sh, int window) {
+    for (int k = threadIdx.x; k < window; k += Sh::kWaves * 64) sh.acc[k] = T(0);
     __syncthreads();
 }
 
 // Chunk b = blockIdx.x: lanes [b*span, min((b+1)*span, n)), keys below
-// kSplitHot folded here, the others copied to the chunk's bin (slot = tile,
+// kSplitHot folded here, the others written to the chunk's bin (slot = tile,
 // offsets of the `ranges` tail ranges in bin_off[b][tile][0..ranges]).
 template <class T>
 __global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
         const int* __restrict__ key, const T* __restrict__ v, long long n, long long cells, long long span,
         int tiles, int ranges, unsigned short* __restrict__ bin_key, T* __restrict__ bin_val,
         unsigned* __restrict__ bin_off, T* __restrict__ parts, int* __restrict__ status) {
-    __shared__ SplitShared<T> sh;
+    __shared__ HotShared<T> sh;
     const int t = threadIdx.x;
     const long long b = blockIdx.x;
     const long long lo = b * span;
     const long long hi = lo + span < n ? lo + span : n;
     const int window = cells < kSplitHot ? static_cast<int>(cells) : kSplitHot;
     const int nb = kSplitTailBase + ranges;
-    split_clear(sh, window);
+    split_clear<T>(sh, window);
     bool bad = false;
     int nk[kWalkItems];
     T nv[kWalkItems];
@@ -1559,23 +1610,23 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
             const bool valid = u < static_cast<unsigned>(cells);
             bad = bad | ((nk[j] != -1) & !valid);
             const unsigned tl = u - static_cast<unsigned>(kSplitHot);
-            const unsigned r = tl / static_cast<unsigned>(kSplitHot);
+            const unsigned r = tl / static_cast<unsigned>(kTailRange);
             const bool in_win = u < static_cast<unsigned>(window);
             const int dw = split_bucket(u);
             d[j] = !valid ? kSplitNone : in_win ? dw : kSplitTailBase + static_cast<int>(r);
-            kl[j] = in_win ? u : tl - r * static_cast<unsigned>(kSplitHot);
+            kl[j] = in_win ? u : tl - r * static_cast<unsigned>(kTailRange);
         }
         if (base + kTile < hi) walk_load(key, v, base + kTile, hi, nk, nv);
-        split_tile(sh, kl, d, vv, nb);
-        if (ranges > 0) {
-            const unsigned ts = sh.bstart[kSplitTailBase];
-            const unsigned te = sh.bstart[kSplitTailBase + ranges];
-            const long long slot = (b * tiles + tile) * kTile;
-            for (unsigned i = ts + t; i < te; i += kWalkThreads) {
-                bin_key[slot + (i - ts)] = sh.key[i];
-                bin_val[slot + (i - ts)] = sh.val[i];
+        {
+            TailSink<T> sink;
+            if (ranges > 0) {
+                const long long slot = (b * tiles + tile) * kTile;
+                sink.key = bin_key + slot;
+                sink.val = bin_val + slot;
+                sink.off = bin_off + (b * tiles + tile) * (ranges + 1);
+                sink.ranges = ranges;
             }
-            if (t <= ranges) bin_off[(b * tiles + tile) * (ranges + 1) + t] = sh.bstart[kSplitTailBase + t] - ts;
+            split_tile<T, HotShared<T>, true>(sh, kl, d, vv, nb, sink);
         }
         split_fold(sh);
         __syncthreads();
@@ -1585,7 +1636,7 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
     if (ranges > 0)
         for (int i = t; i < (tiles - tile) * (ranges + 1); i += kWalkThreads)
             bin_off[(b * tiles + tile) * (ranges + 1) + i] = 0u;
-    split_store(sh, b, cells, 0, window, parts);
+    split_store<T>(sh, b, cells, 0, window, parts);
     if (bad) status[1 + b] = 1;
 }
 
@@ -1687,26 +1738,26 @@ __device__ __forceinline__ void tail_load(const TailSegs& S, const unsigned shor
 }
 
 // (chunk b, tail range r) = (blockIdx.x / ranges, blockIdx.x % ranges): keys
-// [kSplitHot*(r+1), +kSplitHot) of chunk b, read as a stream from the bin's
-// slots in tile order, kTile entries a batch, the next batch's reads in
-// flight while a batch is split and folded.
+// [kSplitHot + kTailRange*r, +kTailRange) of chunk b, read as a stream from the
+// bin's slots in tile order, kTailBatch entries a batch, the next batch's reads
+// in flight while a batch is split and folded.
 template <class T>
-__global__ __launch_bounds__(kWalkThreads) void hawk_split_tail(
+__global__ __launch_bounds__(kTailThreads, 2) void hawk_split_tail(
         long long cells, int tiles, int ranges, const unsigned short* __restrict__ bin_key,
         const T* __restrict__ bin_val, const unsigned* __restrict__ bin_off, T* __restrict__ parts) {
-    __shared__ SplitShared<T> sh;
+    __shared__ TailShared<T> sh;
     const long long b = blockIdx.x / ranges;
     const int r = static_cast<int>(blockIdx.x % ranges);
-    const long long klo = static_cast<long long>(kSplitHot) * (r + 1);
-    const int window = cells - klo < kSplitHot ? static_cast<int>(cells - klo) : kSplitHot;
-    split_clear(sh, window);
+    const long long klo = kSplitHot + static_cast<long long>(kTailRange) * r;
+    const int window = cells - klo < kTailRange ? static_cast<int>(cells - klo) : kTailRange;
+    split_clear<T>(sh, window);
     for (int g0 = 0; g0 < tiles; g0 += kTailGroup) {
         const int gn = tiles - g0 < kTailGroup ? tiles - g0 : kTailGroup;
         const TailSegs S = tail_segs(bin_off, b, tiles, ranges, r, g0, gn);
         unsigned nk[kWalkItems];
         T nv[kWalkItems];
         if (S.count > 0u) tail_load(S, bin_key, bin_val, 0u, nk, nv);
-        for (unsigned qb = 0; qb < S.count; qb += kTile) {
+        for (unsigned qb = 0; qb < S.count; qb += kTailBatch) {
             unsigned kl[kWalkItems];
             int d[kWalkItems];
             T vv[kWalkItems];
@@ -1716,15 +1767,15 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_tail(
                                                               (threadIdx.x & 63));
                 kl[j] = nk[j];
                 vv[j] = nv[j];
-                d[j] = q < S.count ? split_bucket(kl[j]) : kSplitNone;
+                d[j] = q < S.count ? kSplitClassBase + static_cast<int>(kl[j] & (kTailClasses - 1u)) : kSplitNone;
             }
-            if (qb + kTile < S.count) tail_load(S, bin_key, bin_val, qb + kTile, nk, nv);
-            split_tile(sh, kl, d, vv, kSplitTailBase);
-            split_fold(sh);
+            if (qb + kTailBatch < S.count) tail_load(S, bin_key, bin_val, qb + kTailBatch, nk, nv);
+            split_tile<T, TailShared<T>, false>(sh, kl, d, vv, kSplitClassBase + kTailClasses, TailSink<T>());
+            split_fold_tail(sh);
             __syncthreads();
         }
     }
-    split_store(sh, b, cells, klo, window, parts);
+    split_store<T>(sh, b, cells, klo, window, parts);
 }
 
 // The ordered scatter's scratch, in this order (each part 256-byte aligned):
@@ -1754,7 +1805,7 @@ ScatterLayout scatter_layout(int64_t n, int64_t cells, int chunks) {
     if (L.split) {
         const long long tiles = (L.span + kTile - 1) / kTile;
         L.tiles = static_cast<int>(tiles < 1 ? 1 : tiles);
-        L.ranges = cells > kSplitHot ? static_cast<int>((cells - kSplitHot + kSplitHot - 1) / kSplitHot) : 0;
+        L.ranges = cells > kSplitHot ? static_cast<int>((cells - kSplitHot + kTailRange - 1) / kTailRange) : 0;
         if (L.ranges > 0) {
             const size_t slots = c * static_cast<size_t>(L.tiles);
             L.bin_off = at;
@@ -2131,7 +2182,7 @@ int ordered_scatter(const int32_t* key, const T* v, int64_t n, T* target, int64_
         rc = launch_error("hawk_split_hot launch");
         if (rc != HK_OK) return rc;
         if (L.ranges > 0) {
-            hipLaunchKernelGGL(hawk_split_tail<T>, dim3(static_cast<unsigned>(chunks * L.ranges)), dim3(kWalkThreads),
+            hipLaunchKernelGGL(hawk_split_tail<T>, dim3(static_cast<unsigned>(chunks * L.ranges)), dim3(kTailThreads),
                                0, s, static_cast<long long>(cells), L.tiles, L.ranges, bin_key, bin_val, bin_off,
                                parts);
             rc = launch_error("hawk_split_tail launch");

@@ -200,14 +200,16 @@ def test_ordered_sum_is_the_numpy_tree_bitwise_and_replays(unit, gpu, n):
     assert runs[0][0] == O.ordered_sum(x)
 
 
-# The split walk's window is 12288 keys and each tail range 12288 more:
-# 12288 has no tail, 12289 a one-key range, 24577 a second range of one key,
-# 3 cells over 1000 lanes leaves empty chunks; 65536 is config 5's cell count.
+# The split walk's window is 12288 keys and each tail range 6144 more:
+# 12288 has no tail, 12289 a one-key range, 18433 a second range of one key,
+# 61440 eight full ranges, 3 cells over 1000 lanes leaves empty chunks; 65536
+# is config 5's cell count (eight full ranges and one of 4096 keys).
 @pytest.mark.parametrize("cells, n, heavy", [(7, 30_000, False), (1000, 30_000, False), (1500, 30_000, False),
                                              (7, 20_000, True), (1, 3000, False), (200, 50, False),
                                              (1000, 1000, False), (3, 1000, False), (65536, 400_000, False),
                                              (12288, 300_001, False), (12289, 300_001, False),
-                                             (24577, 500_000, False), (40_000, 2_000_003, True),
+                                             (18433, 500_000, False), (61440, 700_000, False),
+                                             (40_000, 2_000_003, True),
                                              (65536, 3_000_017, False),
                                              (70_000, 300_000, False), (600_000, 1_300_000, False)])
 def test_ordered_scatter_is_the_serial_walk_bitwise(unit, gpu, cells, n, heavy):
@@ -290,7 +292,7 @@ def test_ordered_scatter_zipf_keys_into_65536_cells(unit, gpu, n):
 @pytest.mark.parametrize("cells", [5, 30_000])
 def test_ordered_scatter_special_values(unit, gpu, cells):
     """-0.0, infinities, NaN and subnormals through every bucket kind (window
-    keys 0..15, classes, a tail range): the oracle's bits, NaN as NaN.  A key
+    keys 0..31, classes, tail ranges): the oracle's bits, NaN as NaN.  A key
     whose only values are -0.0 sums to +0.0 (the walk starts at +0.0)."""
     import hawk_amd as hawk
     n = 50_000
@@ -577,9 +579,9 @@ def test_ordered_scatter_past_one_tail_group(unit, gpu):
 
 def test_ordered_scatter_past_one_tail_batch(unit, gpu):
     """N = 2^26 + 12345 Zipf keys into 65536 cells: 256 chunks of 262193 lanes,
-    65 tiles a chunk, so the tail ranges read their bins in two batches (64
-    tiles, then one).  Skip keys on 1 % of the lanes.  The serial walk's bits,
-    and the same bits on a replay."""
+    65 tiles a chunk (one slot past the benchmark's 64), each tail range read
+    from its bins in batches of 2048 entries.  Skip keys on 1 % of the lanes.
+    The serial walk's bits, and the same bits on a replay."""
     import hawk_amd as hawk
     n = (1 << 26) + 12345
     cells = 1 << 16
