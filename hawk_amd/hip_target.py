@@ -103,11 +103,13 @@ def value_range(node, memo: dict) -> tuple:
 #:   and the test for 0 and infinity that the general form needs;
 #: * tanh on [-20, 20]: no clamp of the argument, no saturation test, no NaN
 #:   select;
-#: * exp on (-inf, 0]: no upper clamp.
+#: * exp on (-inf, 0]: no upper clamp;
+#: * sin on [0, inf): no test for tiny arguments (it only keeps -0's sign).
 _DOMAIN_FORMS = {
     "sqrt": ("hk_sqrt_normal", lambda lo, hi: lo >= 2.0 ** -700 and hi <= 1.7e308),
     "tanh": ("hk_tanh_mid", lambda lo, hi: lo >= -20.0 and hi <= 20.0),
     "exp": ("hk_exp_nonpos", lambda lo, hi: hi <= 0.0),
+    "sin": ("hk_sin_nonneg", lambda lo, hi: lo >= 0.0),
 }
 
 

@@ -341,8 +341,9 @@ def test_domain_forms_give_the_general_forms_bits_on_the_device(gpu):
     tanh and exp in their bounded forms; on the device each gives the bits of
     the general form on the same operand: sqrt is numpy's (correctly rounded)
     over [e^-480, e^480], tanh on 1.5 sin x + 0.25 is the general tanh of
-    the device's own argument, exp(-|x|) is the general exp of -|x|, NaN and
-    infinities included."""
+    the device's own argument, exp(-|x|) is the general exp of -|x|, sin of
+    exp(x) is the general sin of the device's own exp(x), NaN and infinities
+    included."""
     import tempfile
     import hawk_amd as hawk
     from hawk_amd import Scalar, kernel
@@ -376,12 +377,21 @@ def test_domain_forms_give_the_general_forms_bits_on_the_device(gpu):
     def ex_any(x: Scalar) -> Scalar:
         return m.exp(x)
 
+    @kernel
+    def sn_pos(x: Scalar) -> Scalar:
+        return m.sin(m.exp(x))
+
+    @kernel
+    def sn_any(x: Scalar) -> Scalar:
+        return m.sin(x)
+
     from hawk_amd.emit_hip import plan_kernel
     assert "= hk_sqrt_normal(" in plan_kernel(sq.program, "sq").source
     assert "= hk_tanh_mid(" in plan_kernel(th_mid.program, "th_mid").source
     assert "= hk_exp_nonpos(" in plan_kernel(ex_neg.program, "ex_neg").source
+    assert "= hk_sin_nonneg(" in plan_kernel(sn_pos.program, "sn_pos").source
     d = tempfile.mkdtemp()
-    hawk.build([sq_arg, sq, th_arg, th_mid, th_any, ex_neg, ex_any], d)
+    hawk.build([sq_arg, sq, th_arg, th_mid, th_any, ex_neg, ex_any, sn_pos, sn_any], d)
     g = rng(17)
     x = np.concatenate([g.normal(size=150_000) * 3, g.uniform(-0.02, 0.02, 50_000), g.uniform(-800, 800, 50_000),
                         [0.0, -0.0, np.inf, -np.inf, np.nan, 5e-324, 1e-300]])
@@ -399,6 +409,50 @@ def test_domain_forms_give_the_general_forms_bits_on_the_device(gpu):
     same(run("sq", x), np.sqrt(run("sq_arg", x)))
     same(run("th_mid", x), run("th_any", run("th_arg", x)))
     same(run("ex_neg", x), run("ex_any", -np.abs(x)))
+    same(run("sn_pos", x), run("sn_any", run("ex_any", x)))
+
+
+@pytest.mark.parametrize("which", ["exp", "sin", "cos", "tanh"])
+def test_device_helpers_are_the_host_builds_bits(gpu, which, tmp_path):
+    """exp, sin and cos (below 2^17, where they run their own reduction) and
+    tanh on the device are the host build of the same text bit for bit: the
+    operations are IEEE's on both sides.  For tanh this pins the quotient
+    e / (e + 2) taken without the division's scaling and fixup: seeded by
+    the hardware's reciprocal estimate on the device and by the correctly
+    rounded 1/b on the host, both give the correctly rounded quotient."""
+    import tempfile
+    import hawk_amd as hawk
+    import math_host
+    from hawk_amd import Scalar, kernel
+    from hawk_amd import math as m
+
+    fn = {"exp": m.exp, "sin": m.sin, "cos": m.cos, "tanh": m.tanh}[which]
+
+    @kernel
+    def one(x: Scalar) -> Scalar:
+        return fn(x)
+
+    d = tempfile.mkdtemp()
+    hawk.build([one], d)
+    g = rng(23)
+    if which == "exp":
+        x = np.concatenate([g.normal(size=400_000) * 5, g.uniform(-745.2, 709.8, 400_000),
+                            [0.0, -0.0, np.inf, -np.inf, np.nan, 5e-324, -1e-310, 709.8, -745.2, 1e300]])
+    elif which == "tanh":
+        x = np.concatenate([g.uniform(-2, 2, 400_000), g.uniform(-30, 30, 200_000),
+                            np.exp(g.uniform(-745, 3, 100_000)) * np.sign(g.normal(size=100_000)),
+                            [0.0, -0.0, np.inf, -np.inf, np.nan, 5e-324, 22.0, -21.999]])
+    else:
+        x = np.concatenate([np.exp(g.normal(size=400_000)), g.uniform(-200, 200, 200_000),
+                            g.uniform(-1.3e5, 1.3e5, 200_000), np.pi / 2 * np.arange(-3000, 3000),
+                            g.uniform(-1e-7, 1e-7, 20_000), [0.0, -0.0, 5e-324, -1e-310, 131071.99]])
+    out = dev(np.zeros_like(x), gpu)
+    hawk.run(hawk.load(d, "one"), x=dev(x, gpu), out=out)
+    got = host(out)
+    want = math_host.build(tmp_path)(which, x)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert got[~nan].tobytes() == want[~nan].tobytes()
 
 
 @pytest.mark.parametrize("which", ["exp", "sin", "cos", "tanh", "sqrt"])

@@ -3,50 +3,20 @@
 glibc, the reference's host math (reference tests/test_math_parity.py:279:
 host ``native`` is glibc bit for bit; the device is held within ULP of it).
 
-The helpers use only IEEE operations (fused multiply-add, rint, ldexp, a
-correctly rounded add and multiply), so a host build computes the device's
-bits; the device's own results are held to the same glibc values by the GPU
-sweeps in tests/test_gpu_parity.py."""
-
-import ctypes
-import subprocess
+The helpers use only IEEE operations, so a host build (tests/math_host.py)
+computes the device's bits; tests/test_gpu_parity.py holds the device to
+the host build's bits and to the same glibc values."""
 
 import numpy as np
 import pytest
 
 from conftest import ulp_diff
 
-_DRIVER = """
-extern "C" void hk_eval(int which, const double* x, double* y, long n) {
-    for (long i = 0; i < n; ++i)
-        y[i] = which == 0 ? hk_exp(x[i]) : which == 1 ? hk_sin(x[i]) : which == 2 ? hk_cos(x[i])
-             : which == 3 ? hk_tanh(x[i]) : which == 4 ? hk_exp_nonpos(x[i]) : which == 5 ? hk_sqrt_normal(x[i])
-             : hk_tanh_mid(x[i]);
-}
-"""
-
 
 @pytest.fixture(scope="module")
 def helpers(tmp_path_factory):
-    from hawk_amd.emit_hip import _MATH_HELPERS
-    d = tmp_path_factory.mktemp("math")
-    src = d / "helpers.cpp"
-    src.write_text("#include <cmath>\nusing std::fma; using std::rint; using std::ldexp; using std::fabs;\n"
-                   "#define HK_MATH_QUAL static inline\n#define HK_MATH_PIN(c) (void)(c)\n"
-                   "#define HK_RSQ(x) (1.0 / std::sqrt(x))\n" + _MATH_HELPERS + _DRIVER)
-    lib = d / "helpers.so"
-    subprocess.run(["g++", "-O2", "-ffp-contract=off", "-fno-math-errno", "-shared", "-fPIC", str(src), "-o",
-                    str(lib)], check=True)
-    handle = ctypes.CDLL(str(lib))
-
-    def run(which, x):
-        x = np.ascontiguousarray(x, dtype=np.float64)
-        y = np.empty_like(x)
-        handle.hk_eval({"exp": 0, "sin": 1, "cos": 2, "tanh": 3, "exp_nonpos": 4, "sqrt_normal": 5,
-                                "tanh_mid": 6}[which], x.ctypes.data_as(ctypes.c_void_p),
-                       y.ctypes.data_as(ctypes.c_void_p), ctypes.c_long(x.size))
-        return y
-    return run
+    import math_host
+    return math_host.build(tmp_path_factory.mktemp("math"))
 
 
 def _sweep(which, g):
@@ -108,10 +78,12 @@ def _same_bits(a, b):
 def test_domain_forms_are_the_general_forms_on_their_domains(helpers):
     """The forms the emitter picks for a bounded operand give the general
     form's bits on their domain: exp on x <= 0, tanh on [-20, 20] (NaN stays
-    NaN in both), and the rsq-seeded square root is the correctly rounded
-    sqrt on [2^-700, DBL_MAX] (the host seed here is 1/sqrt(x) rounded; the
-    device's is its reciprocal square root, and the GPU test holds that form
-    to numpy's sqrt too)."""
+    NaN in both), sin on [0, inf), and the rsq-seeded square root is the
+    correctly rounded sqrt on [2^-700, DBL_MAX] (the host seed here is
+    1/sqrt(x) rounded; the device's is its reciprocal square root, and the
+    GPU test holds that form to numpy's sqrt too).  The tanh's quotient
+    e / (e + 2) without the division's scaling and fixup is the correctly
+    rounded quotient over its whole range, tiny and subnormal e included."""
     g = np.random.default_rng(11)
     x = np.concatenate([-np.abs(g.normal(size=200_000)) * 30, -np.exp(g.uniform(-700, 7, 100_000)),
                         np.arange(-746, 0, 0.125), [0.0, -0.0, -5e-324, -1e-310, -745.2, -1200.0, -1e300,
@@ -125,20 +97,27 @@ def test_domain_forms_are_the_general_forms_on_their_domains(helpers):
                         np.nextafter(1.0, 2.0) + np.arange(2000) * 2.0 ** -52, 4.0 - np.arange(2000) * 2.0 ** -51,
                         [2.0 ** -700, 1.7e308, 1.0, 2.0, 3.0, np.nan]])
     assert _same_bits(helpers("sqrt_normal", s), np.sqrt(s))
+    p = np.concatenate([np.exp(g.normal(size=200_000)) * 3, g.uniform(0, 200, 200_000),
+                        np.exp(g.uniform(-700, 20, 100_000)), np.arange(0, 2000, 0.01), g.uniform(0, 1e-8, 20_000),
+                        [0.0, 5e-324, 1e-310, 2.0 ** -26, 2.0 ** -27, 131071.99, 131072.0, 1e300, np.inf, np.nan]])
+    assert _same_bits(helpers("sin_nonneg", p), helpers("sin", p))
+    e = np.concatenate([np.expm1(g.uniform(0, 128, 300_000)), np.exp(g.uniform(-745, 0, 100_000)),
+                        g.uniform(0, 1, 100_000), [0.0, 5e-324, 1e-310, 2.0 ** -52, 6.2e27, np.nan]])
+    assert _same_bits(helpers("div_mid", e), e / (e + 2.0))
 
 
 def test_emitter_picks_the_domain_forms_from_value_ranges():
     """Interval arithmetic over the IR: the chain's sqrt(|tanh| + 1) is on
-    [1, 2], its tanh argument 1.5 sin + 0.25 is on [-1.25, 1.75] and its
-    last exp argument -|t6| is <= 0, so each gets its bounded form; an
-    unbounded operand keeps the general form."""
+    [1, 2], its tanh argument 1.5 sin + 0.25 is on [-1.25, 1.75], its sin
+    argument exp(x) is >= 0 and its last exp argument -|t6| is <= 0, so each
+    gets its bounded form; an unbounded operand keeps the general form."""
     from hawk_amd import Scalar, kernel
     from hawk_amd import math as m
     from hawk_amd.emit_hip import plan_kernel
     from hawk_amd.examples import chain
 
     src = plan_kernel(chain.program, "chain").source
-    for form in ("hk_sqrt_normal(", "hk_tanh_mid(", "hk_exp_nonpos("):
+    for form in ("hk_sqrt_normal(", "hk_tanh_mid(", "hk_exp_nonpos(", "hk_sin_nonneg("):
         assert src.count("= " + form) == 1, form
     assert src.count("= hk_exp(") == 1
 
@@ -148,6 +127,7 @@ def test_emitter_picks_the_domain_forms_from_value_ranges():
 
     src = plan_kernel(free.program, "free").source
     assert "= hk_sqrt_normal(" not in src and "= hk_tanh_mid(" not in src and "= hk_exp_nonpos(" not in src
+    assert "= hk_sin_nonneg(" not in src
     assert src.count("= sqrt(") == 2 and src.count("= hk_tanh(") == 2
 
 
@@ -171,7 +151,8 @@ def test_float32_builds_call_the_float_overloads(helpers):
     src32 = plan_kernel(tiny.program, "tiny", mode="float32").source
     assert "hk_sqrt_normal(" not in src32.split("extern \"C\"")[-1]
     body = src32.split("extern \"C\"")[-1]
-    for helper in ("hk_exp", "hk_sin", "hk_cos", "hk_tanh", "hk_sqrt_normal", "hk_exp_nonpos", "hk_tanh_mid"):
+    for helper in ("hk_exp", "hk_sin", "hk_cos", "hk_tanh", "hk_sqrt_normal", "hk_exp_nonpos", "hk_tanh_mid",
+                   "hk_sin_nonneg"):
         assert helper + "(" not in body, helper
     for call in ("= sqrt(", "= exp(", "= tanh(", "= sin(", "= cos("):
         assert call in body, call
