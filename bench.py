@@ -122,9 +122,10 @@ def workload(config: str, device):
             import oracle_lib as O
             out = np.empty(n)
             O.lib().hko_tiled(1, O._p(x), None, None, None, O._p(out), None, 2.0, 1.0, n, threads)
-        # the stage's HBM pattern (one row read, one written), one sample a thread, for pattern_ceiling
+        # the stage's HBM pattern (one row read, one written) in its own launch shape, for pattern_ceiling
+        sh = k.launch_shape
         return dict(name="scale fwd (config 1)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
-                    pattern={"scale": (1, 1, 256, 256)}, esize=8)
+                    pattern={"scale": (1, 1, sh["block"], sh["block"], sh["per_thread"])}, esize=8)
     if config == "2":
         n = 1 << 25
         g = np.random.default_rng(2)
@@ -149,11 +150,12 @@ def workload(config: str, device):
             L.hko_tiled(2, O._p(v), None, None, None, O._p(out), None, 0.0, 0.0, n, threads)
             L.hko_tiled(3, O._p(v), O._p(bar_out), None, None, O._p(bv), None, 0.0, 0.0, n, threads)
             L.hko_tiled(4, O._p(v), O._p(dv), None, None, O._p(do), None, 0.0, 0.0, n, threads)
-        # each stage's HBM pattern (element rows read, rows written; one sample a thread), for pattern_ceiling
-        blk = {k.name: k.launch_shape["block"] for k in (kf, kv, kj)}
-        pattern = {"energy": (3, 1, blk["energy"], blk["energy"]),
-                   "energy_vjp": (4, 3, blk["energy_vjp"], blk["energy_vjp"]),
-                   "energy_jvp": (6, 1, blk["energy_jvp"], blk["energy_jvp"])}
+        # each stage's HBM pattern (element rows read, rows written) in its own launch shape, for
+        # pattern_ceiling
+        sh = {k.name: (k.launch_shape["block"], k.launch_shape["per_thread"]) for k in (kf, kv, kj)}
+        pattern = {"energy": (3, 1, sh["energy"][0], sh["energy"][0], sh["energy"][1]),
+                   "energy_vjp": (4, 3, sh["energy_vjp"][0], sh["energy_vjp"][0], sh["energy_vjp"][1]),
+                   "energy_jvp": (6, 1, sh["energy_jvp"][0], sh["energy_jvp"][0], sh["energy_jvp"][1])}
         return dict(name="energy fwd + VJP + JVP (config 2)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
                     pattern=pattern, esize=8)
     if config == "3":
@@ -206,9 +208,10 @@ def workload(config: str, device):
             import oracle_lib as O
             O.spd_solve(A, b, threads=threads)
             O.spd_solve_vjp(A, b, bar_x, threads=threads)
-        # each stage's HBM pattern: element rows read and written, one sample a thread
-        bf, bv = kf.launch_shape["block"], kv.launch_shape["block"]
-        pattern = {"spd_solve": (42, 6, bf, bf), "spd_solve_vjp": (48, 42, bv, bv)}
+        # each stage's HBM pattern: element rows read and written, in the stage's launch shape
+        sf, sv = kf.launch_shape, kv.launch_shape
+        pattern = {"spd_solve": (42, 6, sf["block"], sf["block"], sf["per_thread"]),
+                   "spd_solve_vjp": (48, 42, sv["block"], sv["block"], sv["per_thread"])}
         return dict(name="6x6 SPD solve fwd + VJP (config 4a)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
                     pattern=pattern, esize=8)
     if config in ("4b", "4b64"):
@@ -236,7 +239,8 @@ def workload(config: str, device):
         what = "fp64 16x16 product fwd + VJP (config 4b in float64)" if f64 else "fp32 16x16 product fwd + VJP (config 4b)"
         # each stage's HBM pattern (element rows read, rows written, tile samples, threads), for pattern_ceiling
         tile = 256 // esize      # hawk_linalg.hip's shapes: 16 threads a sample (fp32), 32 (fp64 forward)
-        pattern = {"mm16": (512, 256, tile, (32 if f64 else 16) * tile), "mm16#2": (768, 512, tile // 2, 8 * tile)}
+        pattern = {"mm16": (512, 256, tile, (32 if f64 else 16) * tile, 1),
+                   "mm16#2": (768, 512, tile // 2, 8 * tile, 1)}
         return dict(name=what, n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64" if f64 else "f32",
                     pattern=pattern, esize=esize)
     if config == "5":
@@ -529,90 +533,217 @@ typedef {elem} E;
 struct GRefMirror {{ void* data_; unsigned long long samples_, compStride_, sampleStride_; int deviceType_, deviceId_; }};
 extern "C" __attribute__((used)) __device__ char eagle_abi_tag[] = "aether-abi/2";
 extern "C" __attribute__((used)) __device__ unsigned long long eagle_layout_sizes[5] = {{40, 32, 32, 8, 24}};
-// The HBM pattern of a per-sample 16x16 product stage without its arithmetic:
-// a workgroup reads a tile of {tile} consecutive samples from {rows_in} element
-// rows (rows nSamples apart) and writes {rows_out} rows, every load issued
-// before the first is used.  Tiles are handed out XCD by XCD like the product's.
+// A stage's HBM pattern without its arithmetic: a workgroup reads {per} tiles
+// of {tile} consecutive samples from {rows_in} element rows (rows nSamples
+// apart) and writes {rows_out} rows, every load issued before the first is
+// used.  Tile v of workgroup w is tile w*{per} + v, the per-sample stages'
+// order (several samples a thread, a block apart); tiles of several threads a
+// sample are handed out XCD by XCD like the 16x16 product's.
 extern "C" __global__ void __launch_bounds__({threads}) hawk_pattern_copy(
         GRefMirror in_m, GRefMirror out_m, long long base, long long count, long long nSamples) {{
     const E* in = static_cast<const E*>(in_m.data_);
     E* out = static_cast<E*>(out_m.data_);
-    constexpr int kStep = {threads} / {tile}, kIn = {rows_in} / kStep, kOut = {rows_out} / kStep;
+    constexpr int kStep = {threads} / {tile}, kIn = {rows_in} / kStep, kOut = {rows_out} / kStep, kPer = {per};
+    const long long groups = count / ({tile} * kPer);
+    const long long per_xcd = (groups + 7) / 8;
+    const long long group = kStep > 1 ? static_cast<long long>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8
+                                      : static_cast<long long>(blockIdx.x);
+    if (group >= groups) return;
+    const int e_own = threadIdx.x / {tile};
+    E x[kPer][kIn];
+#pragma unroll
+    for (int v = 0; v < kPer; ++v) {{
+        const long long s0 = base + (group * kPer + v) * {tile} + threadIdx.x % {tile};
+#pragma unroll
+        for (int r = 0; r < kIn; ++r)
+            x[v][r] = __builtin_nontemporal_load(in + static_cast<long long>(e_own + r * kStep) * nSamples + s0);
+    }}
+    if ({read_only}) {{           // the reads alone: one store a thread, never taken for finite data
+        E a = E(0);
+#pragma unroll
+        for (int v = 0; v < kPer; ++v)
+#pragma unroll
+            for (int r = 0; r < kIn; ++r) a += x[v][r];
+        if (a != a) out[threadIdx.x] = a;
+        return;
+    }}
+#pragma unroll
+    for (int v = 0; v < kPer; ++v) {{
+        const long long s0 = base + (group * kPer + v) * {tile} + threadIdx.x % {tile};
+#pragma unroll
+        for (int r = 0; r < kOut; ++r) {{          // output row r folds input rows r, r + kOut, ...
+            E o = x[v][r];
+#pragma unroll
+            for (int j = r + kOut; j < kIn; j += kOut) o += x[v][j];
+            __builtin_nontemporal_store(o, out + static_cast<long long>(e_own + r * kStep) * nSamples + s0);
+        }}
+    }}
+}}
+"""
+
+
+def _time_copy(src: str, name: str, ab, grid: int, threads: int, n: int, reps: int) -> float:
+    """Milliseconds a launch of copy kernel ``name`` (built from ``src`` by
+    hipRTC, launched through ``hk_launch_grid``) takes over ``n`` samples."""
+    import torch
+
+    from hawk_amd import _core
+    from hawk_amd.compile import compile_source
+    stream = torch.cuda.current_stream()
+    code, _key, _hit = compile_source(src, name)
+    entry = _core.DeviceLibrary(code).entry(name)
+    launch = lambda: entry.run_grid(ab, 0, n, n, grid, threads, stream.cuda_stream)  # noqa: E731
+    for _ in range(3):
+        launch()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(reps):
+        launch()
+    b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def pattern_ceiling(w, device, reps: int = 10) -> dict:
+    """Per stage of ``w`` that names its HBM pattern: the rate (algorithmic
+    GB/s) of a copy kernel with exactly that pattern and no arithmetic:
+    the ceiling that layout and tile shape leave the stage.  A tiled
+    product's pattern (several threads a sample) is also copied in 2, 4 and
+    8 K slices, the next slice's loads in flight, as the product streams its
+    operands; the best of these is its ceiling."""
+    import torch
+
+    from hawk_amd import _core
+    out = {}
+    n, esize = w["n"], w["esize"]
+    dt = torch.float64 if esize == 8 else torch.float32
+    elem = "double" if esize == 8 else "float"
+    for label, (rows_in, rows_out, tile, threads, per) in w["pattern"].items():
+        if n % (tile * per):
+            raise ValueError(f"pattern_ceiling: N={n} is not a multiple of the tiles ({per} x {tile})")
+        src_t = torch.zeros((rows_in, n), dtype=dt, device=device)
+        dst_t = torch.empty((rows_out, n), dtype=dt, device=device)
+        ab = _core.ArgBlock(["gref", "gref"])
+        ab.bind(0, src_t.data_ptr(), n)
+        ab.bind(1, dst_t.data_ptr(), n)
+        grid = 8 * ((n // tile + 7) // 8) if threads > tile else n // (tile * per)
+        rate = {}
+        for read_only in (0, 1):
+            src = _PATTERN_SOURCE.format(elem=elem, rows_in=rows_in, rows_out=rows_out, tile=tile, threads=threads,
+                                         per=per, read_only=read_only)
+            ms = _time_copy(src, "hawk_pattern_copy", ab, grid, threads, n, reps)
+            moved = rows_in if read_only else rows_in + rows_out
+            rate[read_only] = (ms, moved * esize * n / (ms * 1e-3) / 1e9)
+        best = (rate[0][0], 1)
+        step = threads // tile
+        if step > 1:
+            for slices in (2, 4, 8):
+                if rows_in % (step * slices) or 2 * (rows_in // step // slices) + rows_out // step > 160:
+                    continue
+                src = _SWEEP_SOURCE.format(elem=elem, tile=tile, threads=threads, slices=slices, rows_in=rows_in,
+                                           rows_out=rows_out)
+                ms = _time_copy(src, "hawk_pattern_sweep", ab, grid, threads, n, reps)
+                best = min(best, (ms, slices))
+        ms, slices = best
+        out[label] = {"pattern": f"{rows_in} rows in, {rows_out} out, {tile}-sample tiles of {threads} threads, "
+                                 f"{per} a workgroup" + (f", {slices} K slices" if slices > 1 else ""),
+                      "ms": round(ms, 5), "copy_GBs": round((rows_in + rows_out) * esize * n / (ms * 1e-3) / 1e9, 1),
+                      "reads_only_GBs": round(rate[1][1], 1)}
+        del src_t, dst_t, ab
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+_SWEEP_SOURCE = """
+typedef {elem} E;
+struct GRefMirror {{ void* data_; unsigned long long samples_, compStride_, sampleStride_; int deviceType_, deviceId_; }};
+extern "C" __attribute__((used)) __device__ char eagle_abi_tag[] = "aether-abi/2";
+extern "C" __attribute__((used)) __device__ unsigned long long eagle_layout_sizes[5] = {{40, 32, 32, 8, 24}};
+// The 16x16 product's HBM pattern in {slices} K slices: a workgroup of
+// {threads} threads reads a tile of {tile} consecutive samples from {rows_in}
+// element rows, a slice of them at a time with the next slice's loads in
+// flight, and writes {rows_out} rows; tiles are handed out XCD by XCD.
+extern "C" __global__ void __launch_bounds__({threads}) hawk_pattern_sweep(
+        GRefMirror in_m, GRefMirror out_m, long long base, long long count, long long nSamples) {{
+    const E* in = static_cast<const E*>(in_m.data_);
+    E* out = static_cast<E*>(out_m.data_);
+    constexpr int kStep = {threads} / {tile}, kIn = {rows_in} / kStep / {slices}, kOut = {rows_out} / kStep;
     const long long tiles = count / {tile};
     const long long per_xcd = (tiles + 7) / 8;
     const long long tile = static_cast<long long>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (tile >= tiles) return;
     const long long s0 = base + tile * {tile} + threadIdx.x % {tile};
     const int e_own = threadIdx.x / {tile};
-    E x[kIn];
+    E acc[kOut];
+#pragma unroll
+    for (int r = 0; r < kOut; ++r) acc[r] = E(0);
+    E x[kIn], y[kIn];
 #pragma unroll
     for (int r = 0; r < kIn; ++r)
         x[r] = __builtin_nontemporal_load(in + static_cast<long long>(e_own + r * kStep) * nSamples + s0);
-    if ({read_only}) {{           // the reads alone: one store a thread, never taken for finite data
-        E a = x[0];
 #pragma unroll
-        for (int r = 1; r < kIn; ++r) a += x[r];
-        if (a != a) out[threadIdx.x] = a;
-        return;
+    for (int q = 0; q < {slices}; ++q) {{
+        if (q + 1 < {slices}) {{
+#pragma unroll
+            for (int r = 0; r < kIn; ++r)
+                y[r] = __builtin_nontemporal_load(in + static_cast<long long>(e_own + ((q + 1) * kIn + r) * kStep) *
+                                                  nSamples + s0);
+        }}
+#pragma unroll
+        for (int r = 0; r < kIn; ++r) acc[r % kOut] += x[r];
+#pragma unroll
+        for (int r = 0; r < kIn; ++r) x[r] = y[r];
     }}
 #pragma unroll
-    for (int r = 0; r < kOut; ++r) {{              // output row r folds input rows r, r + kOut, ...
-        E v = x[r];
-#pragma unroll
-        for (int j = r + kOut; j < kIn; j += kOut) v += x[j];
-        __builtin_nontemporal_store(v, out + static_cast<long long>(e_own + r * kStep) * nSamples + s0);
-    }}
+    for (int r = 0; r < kOut; ++r)
+        __builtin_nontemporal_store(acc[r], out + static_cast<long long>(e_own + r * kStep) * nSamples + s0);
 }}
 """
 
 
-def pattern_ceiling(w, device, reps: int = 10) -> dict:
-    """Per stage of ``w`` that names its HBM pattern: the rate (algorithmic
-    GB/s) of a copy kernel with exactly that pattern and no arithmetic, built
-    by hipRTC and launched through ``hk_launch_grid`` on the stage's stream:
-    the ceiling that layout and tile shape leave the stage."""
+def pattern_sweep(device, n: int = 1 << 20, reps: int = 10) -> dict:
+    """The fp32 16x16 product's forward (512 element rows in, 256 out) and
+    VJP (768 in, 512 out) HBM patterns at N = 2^20, copied with no
+    arithmetic over every run length (tiles of 32 to 256 samples: 128 B to
+    1 KB a row), workgroup size (256 to 1024 threads) and number of K slices
+    (1 to 8) whose staged rows fit a thread's registers: the rate the
+    layout allows each tiling, against which the product's own tiling is
+    chosen."""
+    import itertools
+
     import torch
 
     from hawk_amd import _core
-    from hawk_amd.compile import compile_source
-    out = {}
-    n, esize = w["n"], w["esize"]
-    dt = torch.float64 if esize == 8 else torch.float32
-    for label, (rows_in, rows_out, tile, threads) in w["pattern"].items():
-        if n % tile:
-            raise ValueError(f"pattern_ceiling: N={n} is not a multiple of the tile ({tile})")
-        src_t = torch.zeros((rows_in, n), dtype=dt, device=device)
-        dst_t = torch.empty((rows_out, n), dtype=dt, device=device)
+    rows = []
+    for name, rows_in, rows_out in (("mm16", 512, 256), ("mm16#2", 768, 512)):
+        src_t = torch.zeros((rows_in, n), dtype=torch.float32, device=device)
+        dst_t = torch.empty((rows_out, n), dtype=torch.float32, device=device)
         ab = _core.ArgBlock(["gref", "gref"])
         ab.bind(0, src_t.data_ptr(), n)
         ab.bind(1, dst_t.data_ptr(), n)
-        grid = 8 * ((n // tile + 7) // 8)
-        stream = torch.cuda.current_stream()
-        rate = {}
-        for read_only in (0, 1):
-            src = _PATTERN_SOURCE.format(elem="double" if esize == 8 else "float", rows_in=rows_in,
-                                         rows_out=rows_out, tile=tile, threads=threads, read_only=read_only)
-            code, _key, _hit = compile_source(src, "hawk_pattern_copy")
-            entry = _core.DeviceLibrary(code).entry("hawk_pattern_copy")
-            launch = lambda: entry.run_grid(ab, 0, n, n, grid, threads, stream.cuda_stream)  # noqa: E731
-            for _ in range(3):
-                launch()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for _ in range(reps):
-                launch()
-            b.record(stream)
-            b.synchronize()
-            ms = a.elapsed_time(b) / reps
-            moved = rows_in if read_only else rows_in + rows_out
-            rate[read_only] = (ms, moved * esize * n / (ms * 1e-3) / 1e9)
-        out[label] = {"pattern": f"{rows_in} rows in, {rows_out} out, {tile}-sample tiles of {threads} threads",
-                      "ms": round(rate[0][0], 5), "copy_GBs": round(rate[0][1], 1),
-                      "reads_only_GBs": round(rate[1][1], 1)}
-        del src_t, dst_t
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
-    return out
+        for tile, threads, slices in itertools.product((32, 64, 128, 256), (256, 512, 1024), (1, 2, 4, 8)):
+            step = threads // tile
+            if threads % tile or rows_in % (step * slices) or rows_out % step:
+                continue
+            regs = 2 * (rows_in // step // slices) + rows_out // step
+            if regs > 160:                  # more staged rows than a thread's registers hold
+                continue
+            src = _SWEEP_SOURCE.format(elem="float", tile=tile, threads=threads, slices=slices, rows_in=rows_in,
+                                       rows_out=rows_out)
+            ms = _time_copy(src, "hawk_pattern_sweep", ab, 8 * ((n // tile + 7) // 8), threads, n, reps)
+            gbs = (rows_in + rows_out) * 4 * n / (ms * 1e-3) / 1e9
+            rows.append({"pattern": name, "run_bytes": tile * 4, "threads": threads, "slices": slices,
+                         "ms": round(ms, 5), "GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+            log(f"pattern sweep: {rows[-1]}")
+        del src_t, dst_t, ab
+        torch.cuda.empty_cache()
+    best = {}
+    for r in rows:
+        key = f"{r['pattern']} {r['run_bytes']} B"
+        if key not in best or r["GBs"] > best[key]["GBs"]:
+            best[key] = r
+    return {"n": n, "dtype": "f32", "best_per_run": best, "all": rows}
 
 
 def _with_pattern(w, device, per_stage: dict) -> dict:
@@ -1111,6 +1242,9 @@ def main() -> int:
     ap.add_argument("--latency", action="store_true",
                     help="print the CU latencies the ordered scatter is built around (one probe kernel on one "
                          "CU) as one JSON object, and nothing else")
+    ap.add_argument("--pattern-sweep", action="store_true",
+                    help="print the 16x16 product's HBM pattern copy rates over run lengths, workgroup sizes and "
+                         "K slices as one JSON object, and nothing else")
     ap.add_argument("--copy-probe", action="store_true",
                     help="after the timed steps, run one plain 1 GiB device copy (untimed): the "
                          "known-size kernel that scales HBM counters read by rocprofv3 --pmc")
@@ -1124,6 +1258,9 @@ def main() -> int:
     if args.latency:
         print(json.dumps({"device": torch.cuda.get_device_name(0), "cycles_per_op": latency_probes(device)}),
               flush=True)
+        return 0
+    if args.pattern_sweep:
+        print(json.dumps({"device": torch.cuda.get_device_name(0), **pattern_sweep(device)}), flush=True)
         return 0
     log(f"config {args.config}: building and uploading inputs")
     w = workload(args.config, device)

@@ -708,6 +708,8 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     text = "\n".join(body + stores)
     if any(c in text for c in MATH_HELPER_CALLS):
         out += MATH_DEVICE_DEFINES + _MATH_HELPERS.splitlines()
+    if row_terms:
+        out += _LANE_XOR_HELPERS.splitlines()
     if any(red == "sum" for *_, red in row_terms):
         out += (_BAND_ROW_SUM_HELPERS if stage.banded else _ROW_SUM_HELPERS).splitlines()
     if any(red != "sum" for *_, red in row_terms):
@@ -1395,6 +1397,28 @@ __device__ __forceinline__ void hk_fold_store(Real s, int c, unsigned long long 
 #: (l, l ^ 8), ..., (l, l ^ 1) — the pairs of the reference's warp butterfly
 #: and of its host row walk.  The combine is symmetric, so both lanes of a
 #: pair hold its bits and every lane of the half ends with the row's partial.
+_LANE_XOR_HELPERS = """
+// The value of lane l ^ off (off = 1, 2, 4, 8, 16: a lane of the same half
+// wave): DPP quad permutations for 1 and 2 and the bit mode of ds_swizzle (and
+// mask 0x1f, xor mask off) for the others, with no lane address to compute
+// and no LDS memory touched, where __shfl_xor issues a ds_bpermute on a
+// computed address (the rows of a default-policy sum: 0.39-0.44 ms against
+// 0.30-0.35 ms for two sums over 2^26 samples, the same bits).
+__device__ __forceinline__ int hk_lane_xor_b32(int v, int off) {
+    if (off == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+    if (off == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    if (off == 4) return __builtin_amdgcn_ds_swizzle(v, 0x101F);
+    if (off == 8) return __builtin_amdgcn_ds_swizzle(v, 0x201F);
+    return __builtin_amdgcn_ds_swizzle(v, 0x401F);
+}
+__device__ __forceinline__ double hk_lane_xor(double v, int off) {
+    return __hiloint2double(hk_lane_xor_b32(__double2hiint(v), off), hk_lane_xor_b32(__double2loint(v), off));
+}
+__device__ __forceinline__ float hk_lane_xor(float v, int off) {
+    return __int_as_float(hk_lane_xor_b32(__float_as_int(v), off));
+}
+"""
+
 _ROW_SUM_HELPERS = """
 __device__ __forceinline__ bool hk_finite(Real x) { return (x - x) == Real(0); }
 __device__ __forceinline__ Real hk_two_sum_err(Real a, Real b, Real s) {
@@ -1406,8 +1430,8 @@ __device__ __forceinline__ Real hk_two_sum_err(Real a, Real b, Real s) {
 __device__ __forceinline__ void hk_row_sum(Real& h, Real& c) {
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1) {
-        const Real h2 = __shfl_xor(h, off, 64);
-        const Real c2 = __shfl_xor(c, off, 64);
+        const Real h2 = hk_lane_xor(h, off);
+        const Real c2 = hk_lane_xor(c, off);
         const Real t = h + h2;
         c = hk_finite(t) ? (c + c2) + hk_two_sum_err(h, h2, t) : Real(0);
         h = t;
@@ -1433,7 +1457,7 @@ __device__ __forceinline__ Real hk_extreme(int op, Real a, Real b) {
 __device__ __forceinline__ void hk_row_extreme(int op, Real& h) {
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1) {
-        const Real h2 = __shfl_xor(h, off, 64);
+        const Real h2 = hk_lane_xor(h, off);
         const bool low = (threadIdx.x & off) == 0;
         h = low ? hk_extreme(op, h, h2) : hk_extreme(op, h2, h);
     }
@@ -1470,8 +1494,8 @@ __device__ __forceinline__ void hk_band_add(double& h, double& l, double h2, dou
 __device__ __forceinline__ void hk_band_row_sum(double& h, double& l) {
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1) {
-        const double h2 = __shfl_xor(h, off, 64);
-        const double l2 = __shfl_xor(l, off, 64);
+        const double h2 = hk_lane_xor(h, off);
+        const double l2 = hk_lane_xor(l, off);
         hk_band_add(h, l, h2, l2);
     }
 }
