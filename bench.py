@@ -289,6 +289,28 @@ def workload(config: str, device):
             O.band_ordered_sum(x)
         return dict(name="banded sample sums: default policy over x and x*x, ordered over x (mode='banded')",
                     n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64 (double-double bands)", cpu_threads=1)
+    if config == "sum":
+        # the default-policy sample sums in the float64 mode over config 5's input size: band_total's
+        # kernel (the default policy over x and over x*x, the ordered policy over x) without the bands:
+        # compensated 32-sample rows in the stage, then the canonical finish of each row plane
+        n = 1 << 26
+        x = np.random.default_rng(5).normal(size=n)
+        hawk.build([E.band_total], unit)
+        k = hawk.load(unit, "band_total")
+        X = _dev(x, device)
+        cells = {c: torch.zeros(1, dtype=torch.float64, device=device) for c in ("s", "s_sq", "s_ord")}
+        kernels = [k.prepare(x=X, **cells)]
+        rows = 16 / 32                          # a (hi, comp) row per 32 samples
+        work = {"band_total": (8 + 2 * rows, 0), "row_sum": (rows, 1), "row_sum#2": (rows, 1),
+                "ordered_sum": (8, 1)}
+
+        def cpu(threads):
+            import oracle_lib as O
+            O.sample_sum(x)
+            O.sample_sum(x * x)
+            O.ordered_sum(x, threads=threads)
+        return dict(name="default-policy sample sums over x and x*x, ordered over x (float64)", n=n,
+                    kernels=kernels, work=work, cpu=cpu, dtype="f64")
     if config == "5k":
         # config 5b in the reference's keyed spelling (tests/test_ordered_fixed_tree.py:43-47), over
         # 16384 keys of 4096 samples: hawk.sum(x, over="sample", policy="ordered") per key
