@@ -102,6 +102,11 @@ def twobody_vjp_algorithmic_ops() -> int:
     return plan_kernel(program, "twobody_vjp_one_tape").algorithmic_ops
 
 
+def _xcd(unit: Path, name: str) -> bool:
+    """Whether a built per-sample stage hands its blocks out XCD by XCD."""
+    return "hk_xcd_order = true" in (unit / f"{name}.hip").read_text()
+
+
 def workload(config: str, device):
     import torch
 
@@ -125,7 +130,8 @@ def workload(config: str, device):
         # the stage's HBM pattern (one row read, one written) in its own launch shape, for pattern_ceiling
         sh = k.launch_shape
         return dict(name="scale fwd (config 1)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
-                    pattern={"scale": (1, 1, sh["block"], sh["block"], sh["per_thread"])}, esize=8)
+                    pattern={"scale": (1, 1, sh["block"], sh["block"], sh["per_thread"], _xcd(unit, "scale"))},
+                    esize=8)
     if config == "2":
         n = 1 << 25
         g = np.random.default_rng(2)
@@ -152,10 +158,10 @@ def workload(config: str, device):
             L.hko_tiled(4, O._p(v), O._p(dv), None, None, O._p(do), None, 0.0, 0.0, n, threads)
         # each stage's HBM pattern (element rows read, rows written) in its own launch shape, for
         # pattern_ceiling
-        sh = {k.name: (k.launch_shape["block"], k.launch_shape["per_thread"]) for k in (kf, kv, kj)}
-        pattern = {"energy": (3, 1, sh["energy"][0], sh["energy"][0], sh["energy"][1]),
-                   "energy_vjp": (4, 3, sh["energy_vjp"][0], sh["energy_vjp"][0], sh["energy_vjp"][1]),
-                   "energy_jvp": (6, 1, sh["energy_jvp"][0], sh["energy_jvp"][0], sh["energy_jvp"][1])}
+        sh = {k.name: (k.launch_shape["block"], k.launch_shape["per_thread"], _xcd(unit, k.name)) for k in (kf, kv, kj)}
+        pattern = {"energy": (3, 1, sh["energy"][0], *sh["energy"]),
+                   "energy_vjp": (4, 3, sh["energy_vjp"][0], *sh["energy_vjp"]),
+                   "energy_jvp": (6, 1, sh["energy_jvp"][0], *sh["energy_jvp"])}
         return dict(name="energy fwd + VJP + JVP (config 2)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
                     pattern=pattern, esize=8)
     if config == "3":
@@ -210,8 +216,8 @@ def workload(config: str, device):
             O.spd_solve_vjp(A, b, bar_x, threads=threads)
         # each stage's HBM pattern: element rows read and written, in the stage's launch shape
         sf, sv = kf.launch_shape, kv.launch_shape
-        pattern = {"spd_solve": (42, 6, sf["block"], sf["block"], sf["per_thread"]),
-                   "spd_solve_vjp": (48, 42, sv["block"], sv["block"], sv["per_thread"])}
+        pattern = {"spd_solve": (42, 6, sf["block"], sf["block"], sf["per_thread"], _xcd(unit, "spd_solve")),
+                   "spd_solve_vjp": (48, 42, sv["block"], sv["block"], sv["per_thread"], _xcd(unit, "spd_solve_vjp"))}
         return dict(name="6x6 SPD solve fwd + VJP (config 4a)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
                     pattern=pattern, esize=8)
     if config in ("4b", "4b64"):
@@ -239,8 +245,8 @@ def workload(config: str, device):
         what = "fp64 16x16 product fwd + VJP (config 4b in float64)" if f64 else "fp32 16x16 product fwd + VJP (config 4b)"
         # each stage's HBM pattern (element rows read, rows written, tile samples, threads), for pattern_ceiling
         tile = 256 // esize      # hawk_linalg.hip's shapes: 16 threads a sample (fp32), 32 (fp64 forward)
-        pattern = {"mm16": (512, 256, tile, (32 if f64 else 16) * tile, 1),
-                   "mm16#2": (768, 512, tile // 2, 8 * tile, 1)}
+        pattern = {"mm16": (512, 256, tile, (32 if f64 else 16) * tile, 1, True),
+                   "mm16#2": (768, 512, tile // 2, 8 * tile, 1, True)}
         return dict(name=what, n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64" if f64 else "f32",
                     pattern=pattern, esize=esize)
     if config == "5":
@@ -559,8 +565,8 @@ extern "C" __attribute__((used)) __device__ unsigned long long eagle_layout_size
 // of {tile} consecutive samples from {rows_in} element rows (rows nSamples
 // apart) and writes {rows_out} rows, every load issued before the first is
 // used.  Tile v of workgroup w is tile w*{per} + v, the per-sample stages'
-// order (several samples a thread, a block apart); tiles of several threads a
-// sample are handed out XCD by XCD like the 16x16 product's.
+// order (several samples a thread, a block apart); with {xcd}, workgroups are
+// handed out XCD by XCD (a stage with its XCD order, the 16x16 product).
 extern "C" __global__ void __launch_bounds__({threads}) hawk_pattern_copy(
         GRefMirror in_m, GRefMirror out_m, long long base, long long count, long long nSamples) {{
     const E* in = static_cast<const E*>(in_m.data_);
@@ -568,8 +574,8 @@ extern "C" __global__ void __launch_bounds__({threads}) hawk_pattern_copy(
     constexpr int kStep = {threads} / {tile}, kIn = {rows_in} / kStep, kOut = {rows_out} / kStep, kPer = {per};
     const long long groups = count / ({tile} * kPer);
     const long long per_xcd = (groups + 7) / 8;
-    const long long group = kStep > 1 ? static_cast<long long>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8
-                                      : static_cast<long long>(blockIdx.x);
+    const long long group = {xcd} ? static_cast<long long>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8
+                                  : static_cast<long long>(blockIdx.x);
     if (group >= groups) return;
     const int e_own = threadIdx.x / {tile};
     E x[kPer][kIn];
@@ -602,6 +608,14 @@ extern "C" __global__ void __launch_bounds__({threads}) hawk_pattern_copy(
     }}
 }}
 """
+
+
+def _gen(device):
+    """A seeded generator on ``device`` for the pattern copies' input planes."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(7)
+    return g
 
 
 def _time_copy(src: str, name: str, ab, grid: int, threads: int, n: int, reps: int) -> float:
@@ -640,19 +654,23 @@ def pattern_ceiling(w, device, reps: int = 10) -> dict:
     n, esize = w["n"], w["esize"]
     dt = torch.float64 if esize == 8 else torch.float32
     elem = "double" if esize == 8 else "float"
-    for label, (rows_in, rows_out, tile, threads, per) in w["pattern"].items():
+    for label, (rows_in, rows_out, tile, threads, per, xcd) in w["pattern"].items():
         if n % (tile * per):
             raise ValueError(f"pattern_ceiling: N={n} is not a multiple of the tiles ({per} x {tile})")
-        src_t = torch.zeros((rows_in, n), dtype=dt, device=device)
+        # normal variates like the workloads' planes: a plane of zeros copies some 5 % faster (the
+        # energy forward's pattern: 7.52 TB/s from zeros, 7.15 from its own v), so zeros overstate the
+        # ceiling
+        src_t = torch.randn((rows_in, n), dtype=dt, device=device, generator=_gen(device))
         dst_t = torch.empty((rows_out, n), dtype=dt, device=device)
         ab = _core.ArgBlock(["gref", "gref"])
         ab.bind(0, src_t.data_ptr(), n)
         ab.bind(1, dst_t.data_ptr(), n)
-        grid = 8 * ((n // tile + 7) // 8) if threads > tile else n // (tile * per)
+        groups = n // (tile * per)
+        grid = 8 * ((groups + 7) // 8) if xcd else groups
         rate = {}
         for read_only in (0, 1):
             src = _PATTERN_SOURCE.format(elem=elem, rows_in=rows_in, rows_out=rows_out, tile=tile, threads=threads,
-                                         per=per, read_only=read_only)
+                                         per=per, xcd="true" if xcd else "false", read_only=read_only)
             ms = _time_copy(src, "hawk_pattern_copy", ab, grid, threads, n, reps)
             moved = rows_in if read_only else rows_in + rows_out
             rate[read_only] = (ms, moved * esize * n / (ms * 1e-3) / 1e9)
@@ -668,7 +686,8 @@ def pattern_ceiling(w, device, reps: int = 10) -> dict:
                 best = min(best, (ms, slices))
         ms, slices = best
         out[label] = {"pattern": f"{rows_in} rows in, {rows_out} out, {tile}-sample tiles of {threads} threads, "
-                                 f"{per} a workgroup" + (f", {slices} K slices" if slices > 1 else ""),
+                                 f"{per} a workgroup" + (", XCD order" if xcd else "")
+                                 + (f", {slices} K slices" if slices > 1 else ""),
                       "ms": round(ms, 5), "copy_GBs": round((rows_in + rows_out) * esize * n / (ms * 1e-3) / 1e9, 1),
                       "reads_only_GBs": round(rate[1][1], 1)}
         del src_t, dst_t, ab
@@ -739,7 +758,7 @@ def pattern_sweep(device, n: int = 1 << 20, reps: int = 10) -> dict:
     from hawk_amd import _core
     rows = []
     for name, rows_in, rows_out in (("mm16", 512, 256), ("mm16#2", 768, 512)):
-        src_t = torch.zeros((rows_in, n), dtype=torch.float32, device=device)
+        src_t = torch.randn((rows_in, n), dtype=torch.float32, device=device, generator=_gen(device))
         dst_t = torch.empty((rows_out, n), dtype=torch.float32, device=device)
         ab = _core.ArgBlock(["gref", "gref"])
         ab.bind(0, src_t.data_ptr(), n)
