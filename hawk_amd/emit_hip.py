@@ -1421,11 +1421,13 @@ __device__ __forceinline__ float hk_lane_xor(float v, int off) {
 
 _ROW_SUM_HELPERS = """
 __device__ __forceinline__ bool hk_finite(Real x) { return (x - x) == Real(0); }
+// The rounding error of s = a + b, +0 for an exact sum: Knuth's TwoSum,
+// exact for any finite a and b, so the same value as the reference's Fast2Sum
+// on the operands ordered by magnitude (aether::accum::twoSumErr), without the
+// ordering's compare and selects.  Its callers drop it when s is not finite.
 __device__ __forceinline__ Real hk_two_sum_err(Real a, Real b, Real s) {
-    const bool big_a = fabs(a) >= fabs(b);
-    const Real big = big_a ? a : b;
-    const Real small = big_a ? b : a;
-    return hk_finite(s) ? (small - (s - big)) + Real(0) : Real(__builtin_nan(""));
+    const Real bb = s - a;
+    return ((a - (s - bb)) + (b - bb)) + Real(0);
 }
 __device__ __forceinline__ void hk_row_sum(Real& h, Real& c) {
 #pragma unroll
