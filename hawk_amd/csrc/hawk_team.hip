@@ -304,14 +304,14 @@ constexpr long long kRowLeaf = static_cast<long long>(kRowSlots) * kRowTerms;
 template <class T>
 __device__ __forceinline__ bool finite_bits(T x) { return (x - x) == T(0); }
 
-// The exact residual of s == a + b, the larger magnitude first, a zero
-// residual +0 (reference hawk/_cells.py:46-52); NaN when s is not finite.
+// The exact residual of s == a + b, a zero residual +0, NaN when s is not
+// finite (reference hawk/_cells.py:46-52, Fast2Sum on the operands ordered by
+// magnitude).  Knuth's TwoSum gives the same exact residual for any finite
+// a and b without the ordering's compare and selects.
 template <class T>
 __device__ __forceinline__ T two_sum_err(T a, T b, T s) {
-    const bool big_a = fabs(a) >= fabs(b);
-    const T big = big_a ? a : b;
-    const T small = big_a ? b : a;
-    return finite_bits(s) ? (small - (s - big)) + T(0) : T(__builtin_nan(""));
+    const T bb = s - a;
+    return finite_bits(s) ? ((a - (s - bb)) + (b - bb)) + T(0) : T(__builtin_nan(""));
 }
 
 // Neumaier's add of (x, xc) onto (h, c) (reference hawk/_cells.py:55-58).
