@@ -15,8 +15,12 @@ ordered loss and its gradient wrt its weights (the ordered log fold);
 launch (``hawk.steps``), over 2^24 samples, and ``--config persist`` 2^22 such
 oscillators of 1-256 steps each run to their finish in one launch of the
 persistent entry (the plain and range entries timed beside it).
+``--config sum`` times config 5's sums in the default policy (the compensated
+row sums, in float64) over the same 2^26 samples.
 ``python bench.py --latency`` prints the CU latencies the ordered scatter is
-built around instead (a single-workgroup probe kernel).
+built around instead (a single-workgroup probe kernel), and
+``python bench.py --pattern-sweep`` the per-sample 16x16 product's copy
+ceilings over tilings (a K-sliced copy per tile shape).
 
 Each stage launch of the timed steps (a per-sample kernel, or a team stage:
 the ordered sum or the ordered scatter) is bracketed by HIP events on the
