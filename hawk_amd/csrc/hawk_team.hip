@@ -1240,6 +1240,7 @@ constexpr int kHotStride = kSplitTailBase + kSplitMaxRanges + 3;   // 60: a wave
 constexpr int kTailClassBits = 3;                // hawk_split_tail's classes: key & 7
 constexpr int kTailClasses = 1 << kTailClassBits;
 constexpr int kTailStride = kSplitClassBase + kTailClasses + 8;   // 48
+constexpr int kTailKeys = kTailRange >> kTailClassBits;   // 768 keys a class
 constexpr int kTailWaves = kTailClasses;         // a wave per class
 constexpr int kTailThreads = 64 * kTailWaves;
 constexpr int kTailBatch = kTailThreads * kWalkItems;   // 2048 entries a batch
@@ -1287,6 +1288,16 @@ static_assert(sizeof(TailShared<double>) <= 80 * 1024, "two tail workgroups shar
 // (kl - 32) % 15, so the fifteen class waves share the window evenly.
 __device__ __forceinline__ unsigned hot_class_index(unsigned kl) {   // (kl - 32) / 15, exact below 2^15
     return ((kl - static_cast<unsigned>(kSplitHeads)) * 34953u) >> 19;
+}
+// hawk_split_tail keeps a class's accumulators together (class c = kl & 7 at
+// [768c, 768c + 768), key index m = kl >> 3), so a class wave's reads and
+// writes of distinct keys spread over the LDS banks; in key order all of a
+// class's keys sit 64 bytes apart, on four bank positions.  m is XORed with
+// 8c, which keeps it below 768 and turns the final store's reads (eight
+// classes a wave) from eight-way bank conflicts into two-way ones.
+__device__ __forceinline__ unsigned tail_slot(unsigned kl) {
+    const unsigned c = kl & (kTailClasses - 1u);
+    return c * static_cast<unsigned>(kTailKeys) + ((kl >> kTailClassBits) ^ (c << 3));
 }
 __device__ __forceinline__ int split_bucket(unsigned kl) {
     const unsigned u = kl - static_cast<unsigned>(kSplitHeads);
@@ -1430,13 +1441,21 @@ __device__ void fold_heads(Sh& sh) {
     T a = sh.acc[lane];
     T r0[kHeadBlock], r1[kHeadBlock], r2[kHeadBlock], r3[kHeadBlock];
     const T* x = sh.val + s;
+    // the first reads in block order, as the loop issues them: the loop's
+    // waits count LDS operations, and on its entry they follow this order
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < kHeadBlock; ++q) {
-        r0[q] = x[q];
-        r1[q] = x[kHeadBlock + q];
-        r2[q] = x[2 * kHeadBlock + q];
-        r3[q] = x[3 * kHeadBlock + q];
-    }
+    for (int q = 0; q < kHeadBlock; ++q) r0[q] = x[q];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < kHeadBlock; ++q) r1[q] = x[kHeadBlock + q];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < kHeadBlock; ++q) r2[q] = x[2 * kHeadBlock + q];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < kHeadBlock; ++q) r3[q] = x[3 * kHeadBlock + q];
+    __builtin_amdgcn_sched_barrier(0);
     constexpr int kAhead = 4 * kHeadBlock;
     int left = e - s;
     for (; left >= kAhead; left -= kAhead, x += kAhead) {
@@ -1496,7 +1515,8 @@ __device__ void fold_class(Sh& sh, int c) {
         if (valid) atomicOr(&peer[h], me);
         __builtin_amdgcn_wave_barrier();
         unsigned long long pm = valid ? peer[h] : 0ull;
-        const T a0 = valid ? sh.acc[kv] : T(0);
+        const unsigned ai = Hot ? kv : tail_slot(kv);
+        const T a0 = valid ? sh.acc[ai] : T(0);
         __builtin_amdgcn_wave_barrier();
         if (valid) peer[h] = 0ull;
 #pragma unroll
@@ -1524,7 +1544,7 @@ __device__ void fold_class(Sh& sh, int c) {
                 for (int q = 0; q < 8; ++q)
                     if (q < got) a = a + y[q];
             }
-            sh.acc[kv] = a;
+            sh.acc[ai] = a;
         }
         __builtin_amdgcn_wave_barrier();
         k = nk;
@@ -1637,7 +1657,15 @@ __global__ __launch_bounds__(kWalkThreads) void hawk_split_hot(
         for (int i = t; i < (tiles - tile) * (ranges + 1); i += kWalkThreads)
             bin_off[(b * tiles + tile) * (ranges + 1) + i] = 0u;
     split_store<T>(sh, b, cells, 0, window, parts);
-    if (bad) status[1 + b] = 1;
+    // the status plane (hawk_scatter_status's values, written here in the
+    // split walk): chunk b's flag, and from chunk 0 the cell count and the
+    // flags of the chunks past the last
+    const int any = __syncthreads_or(bad ? 1 : 0);
+    if (t == 0) status[1 + b] = any ? 1 : 0;
+    if (b == 0) {
+        if (t == 0) status[0] = static_cast<int>(cells);
+        for (int i = static_cast<int>(gridDim.x) + t; i < kScatterChunks; i += kWalkThreads) status[1 + i] = 0;
+    }
 }
 
 // The tail ranges' stream: for workgroup (chunk b, range r), the range's
@@ -1750,7 +1778,7 @@ __global__ __launch_bounds__(kTailThreads, 2) void hawk_split_tail(
     const int r = static_cast<int>(blockIdx.x % ranges);
     const long long klo = kSplitHot + static_cast<long long>(kTailRange) * r;
     const int window = cells - klo < kTailRange ? static_cast<int>(cells - klo) : kTailRange;
-    split_clear<T>(sh, window);
+    split_clear<T>(sh, kTailRange);
     for (int g0 = 0; g0 < tiles; g0 += kTailGroup) {
         const int gn = tiles - g0 < kTailGroup ? tiles - g0 : kTailGroup;
         const TailSegs S = tail_segs(bin_off, b, tiles, ranges, r, g0, gn);
@@ -1775,7 +1803,9 @@ __global__ __launch_bounds__(kTailThreads, 2) void hawk_split_tail(
             __syncthreads();
         }
     }
-    split_store<T>(sh, b, cells, klo, window, parts);
+    __syncthreads();
+    T* row = parts + b * cells + klo;
+    for (int k = threadIdx.x; k < window; k += kTailThreads) row[k] = sh.acc[tail_slot(static_cast<unsigned>(k))];
 }
 
 // The ordered scatter's scratch, in this order (each part 256-byte aligned):
@@ -2168,10 +2198,13 @@ int ordered_scatter(const int32_t* key, const T* v, int64_t n, T* target, int64_
     const ScatterLayout L = scatter_layout(n, cells, chunks);
     unsigned char* base = static_cast<unsigned char*>(scratch);
     auto* parts = reinterpret_cast<T*>(base + L.parts);     // a float scatter uses the front of each region
-    hipLaunchKernelGGL(hawk_scatter_status, dim3(1), dim3(kScatterChunks + 64), 0, s, status,
-                       static_cast<long long>(cells));
-    int rc = launch_error("hawk_scatter_status launch");
-    if (rc != HK_OK) return rc;
+    int rc = HK_OK;
+    if (!L.split) {
+        hipLaunchKernelGGL(hawk_scatter_status, dim3(1), dim3(kScatterChunks + 64), 0, s, status,
+                           static_cast<long long>(cells));
+        rc = launch_error("hawk_scatter_status launch");
+        if (rc != HK_OK) return rc;
+    }
     if (L.split) {
         auto* bin_off = reinterpret_cast<unsigned*>(base + L.bin_off);
         auto* bin_key = reinterpret_cast<unsigned short*>(base + L.bin_key);
