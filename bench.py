@@ -37,7 +37,9 @@ model named.
 
 The default run (config 2, without ``--only``) also records configs 1, 3, 4a,
 4b and 5 under ``config.configs``: each one's stages (HIP events, median of 5
-steps after 2 warm-ups), its dominant stage against its roofline and the
+steps after warm-up steps for at least 0.25 s: each record follows a CPU
+baseline, and a GPU that idled runs its first milliseconds of VALU-bound work
+at a lower clock), its dominant stage against its roofline and the
 oracle's rate on every host core (the median of at least 5 repetitions);
 config 5's record also carries its dominant stage's HBM traffic.  An
 FP64-bound stage (config 3) is set against the FP64 peak by the FLOPs it
@@ -916,15 +918,24 @@ def use_fp64_counts(w, per_stage: dict, counts: dict) -> None:
                         "per wave over SQ_WAVES, one rocprofv3 --pmc pass of this bench")
 
 
-def time_steps(w, steps: int, warmup: int) -> dict:
+def time_steps(w, steps: int, warmup: int, settle_s: float = 0.0) -> dict:
     """Warm up, then time ``steps`` steps of workload ``w``: every stage launch
     bracketed by HIP events on the stream it runs on (torch's current stream,
-    the stream the launchers were prepared on), the whole run by two more."""
+    the stream the launchers were prepared on), the whole run by two more.
+    With ``settle_s``, the warm-up goes on past ``warmup`` steps until that
+    many seconds of them have run: a GPU that sat idle (during a CPU
+    baseline) comes back at a lower shader clock, and its first milliseconds
+    of work run 10-15 % slower in the VALU- and LDS-bound stages."""
     import torch
     stages = _stages_of(w)
-    for _ in range(warmup):
+    done = 0
+    t_warm = time.perf_counter()
+    while done < warmup or (settle_s > 0.0 and time.perf_counter() - t_warm < settle_s):
         for _label, launch in stages:
             launch()
+        done += 1
+        if done >= warmup and settle_s > 0.0 and done % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     events = {label: [] for label, _ in stages}
@@ -955,7 +966,8 @@ def time_steps(w, steps: int, warmup: int) -> dict:
         if w.get("bound") == "fp64" and f_per:
             tf = f_per * n / (med * 1e-3) / 1e12
             per_stage[label].update({"achieved_TFLOPs": tf, "fp64_frac": tf / FP64_PEAK_TFLOPS})
-    return {"ms_step": start_all.elapsed_time(end_all) / steps, "per_stage": per_stage, "wall": wall}
+    return {"ms_step": start_all.elapsed_time(end_all) / steps, "per_stage": per_stage, "wall": wall,
+            "warmup": done}
 
 
 def roofline_of(w, per_stage: dict, traffic=None) -> dict:
@@ -1032,9 +1044,12 @@ def _traffic_of(config: str, per_stage: dict, dominant: str):
     return measure_traffic(config, kernels, occurrence, per_step)
 
 
-def config_record(config: str, device, steps: int = 5, warmup: int = 2, pmc: bool = True) -> dict:
+def config_record(config: str, device, steps: int = 5, warmup: int = 2, pmc: bool = True,
+                  settle_s: float = 0.25) -> dict:
     """One configuration's record for the default run: its stages timed on
-    the GPU (HIP events, median of ``steps``), the dominant stage against its
+    the GPU (HIP events, median of ``steps``, after warm-up steps for at least
+    ``settle_s`` seconds: the record follows a CPU baseline, during which the
+    GPU idles), the dominant stage against its
     roofline (an FP64-bound one by its executed FLOPs, and for
     :data:`TRAFFIC_CONFIGS` with its HBM traffic, when ``pmc``), and the
     oracle on every host core (the median of at least 5 repetitions after a
@@ -1042,7 +1057,7 @@ def config_record(config: str, device, steps: int = 5, warmup: int = 2, pmc: boo
     import torch
     log(f"config {config}: record")
     w = workload(config, device)
-    t = time_steps(w, steps, warmup)
+    t = time_steps(w, steps, warmup, settle_s)
     ceiling = _with_pattern(w, device, t["per_stage"])
     traffic = None
     if pmc:
@@ -1058,6 +1073,7 @@ def config_record(config: str, device, steps: int = 5, warmup: int = 2, pmc: boo
             log(f"config {config}: counters not measured: {exc}")
     rate, reps, cpu_s = cpu_rate(w, host_cores(), "native", 0.0, min_reps=5)
     rec = {"workload": w["name"], "N": w["n"], "dtype": w["dtype"], "ms_per_step": round(t["ms_step"], 5),
+           "steps": steps, "warmup": t["warmup"],
            "samples_per_s": w["n"] / (t["ms_step"] * 1e-3),
            "stages": {k: {kk: (round(vv, 6) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                       for k, v in t["per_stage"].items()},
