@@ -62,37 +62,48 @@ __global__ __launch_bounds__(kLaneBlock) void hawk_sum_lanes(const T* __restrict
 // Group g of 1024 lanes folded by s[i] += s[i+w], w = 512..1, into gp[g]; the
 // last group to finish folds the 64 group values by the same tree, w = 32..1,
 // and stores the result.  The ticket is left at zero for the next call.
+// Thread t holds lanes t, t+256, t+512 and t+768, so levels 512 and 256 are
+// its own adds; levels 128 and 64 cross waves through LDS, and levels 32..1
+// run in wave 0, lane i adding lane i+w's value taken by a permute: the same
+// additions in the same order as the tree over an LDS array, with two
+// barriers in place of ten.
 template <class T>
 __global__ __launch_bounds__(256) void hawk_sum_fold(const T* __restrict__ lanes,
                                                      T* __restrict__ gp,
                                                      unsigned* __restrict__ ticket,
                                                      T* __restrict__ out) {
-    __shared__ T sh[kFoldLanes];
+    static_assert(kFoldLanes == 1024 && kGroups == 64, "four lanes a thread, one wave of group values");
+    __shared__ T up128[128];
+    __shared__ T up64[64];
     __shared__ unsigned last;
     const int g = blockIdx.x;
     const int t = threadIdx.x;
-    for (int i = t; i < kFoldLanes; i += 256) sh[i] = lanes[g * kFoldLanes + i];
+    const T* src = lanes + static_cast<long long>(g) * kFoldLanes;
+    const T x0 = src[t], x1 = src[t + 256], x2 = src[t + 512], x3 = src[t + 768];
+    T a = (x0 + x2) + (x1 + x3);                 // w = 512 (lanes t and t+256), then w = 256
+    if (t >= 128) up128[t - 128] = a;
     __syncthreads();
-    for (int w = kFoldLanes / 2; w > 0; w >>= 1) {
-        for (int i = t; i < w; i += 256) sh[i] = sh[i] + sh[i + w];
-        __syncthreads();
-    }
-    if (t == 0) {
-        gp[g] = sh[0];
-        __threadfence();
-        last = atomicAdd(ticket, 1u);
+    if (t < 128) a = a + up128[t];               // w = 128
+    if (t >= 64 && t < 128) up64[t - 64] = a;
+    __syncthreads();
+    if (t < 64) {
+        a = a + up64[t];                         // w = 64
+#pragma unroll
+        for (int w = 32; w > 0; w >>= 1) a = a + __shfl_down(a, w, 64);
+        if (t == 0) {
+            gp[g] = a;
+            __threadfence();
+            last = atomicAdd(ticket, 1u);
+        }
     }
     __syncthreads();
-    if (last != kGroups - 1) return;
+    if (last != kGroups - 1 || t >= 64) return;
     __threadfence();   // acquire: every group's gp store is visible
-    if (t < kGroups) sh[t] = __builtin_nontemporal_load(gp + t);
-    __syncthreads();
-    for (int w = kGroups / 2; w > 0; w >>= 1) {
-        if (t < w) sh[t] = sh[t] + sh[t + w];
-        __syncthreads();
-    }
+    T b = __builtin_nontemporal_load(gp + t);
+#pragma unroll
+    for (int w = 32; w > 0; w >>= 1) b = b + __shfl_down(b, w, 64);
     if (t == 0) {
-        *out = sh[0];
+        *out = b;
         *ticket = 0u;
     }
 }
