@@ -92,7 +92,11 @@ def launch_shape(plan, mode: str) -> tuple:
     nbytes = _stage_bytes(plan, mode)
     if nbytes <= STREAM_BYTES and fp_ops_per_sample(plan.source) <= STREAM_OPS:
         return 256, 4
-    return (256, 1) if 32 < nbytes <= 64 else (128, 1)
+    shape = (256, 1) if 32 < nbytes <= 64 else (128, 1)
+    if stage.row_sums and not stage.fused_folds and not getattr(stage, "banded", False):
+        # row reductions take two samples a lane (the paired layout)
+        shape = (shape[0], 2)
+    return shape
 
 
 def _chain_record(k, sidecar: dict, mode: str) -> None:

@@ -746,6 +746,23 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         else:
             out += wrap.index_prologue().splitlines()
         out += body + stores
+    elif row_samples(stage, per_thread) > 1:
+        # Two or four samples a lane (j + 16v or j + 8v of its row), so a
+        # row's first butterfly levels join in registers and 16 or 8 lanes
+        # carry the rest: the same additions as the half-wave form with a half
+        # or a quarter of its lane exchanges and adds a sample.  A lane past
+        # `count` computes sample `base` and brings its row the identity.
+        per = row_samples(stage, per_thread)
+        out += wrap.index_prologue(form="rows", rows=len(row_terms), per_lane=per).splitlines()
+        out += body
+        opened, closed = wrap.sample_sum_frame(len(row_terms), "Real", "")
+        out += opened.splitlines() + ["    " + line for line in stores] + closed.splitlines()
+        out += wrap.rows_close([(term, w.spell.row_identity(red)) for term, _hi, _comp, red in row_terms]).splitlines()
+        for k, (term, hi, comp, red) in enumerate(row_terms):
+            if red == "sum":
+                out += w.spell.sample_sum_rows(w, k, hi, comp, per)
+            else:
+                out += w.spell.sample_extreme_rows(w, red, k, hi, per)
     else:
         # Every lane of a half-wave takes part in its row's butterfly: a lane
         # past `count` computes sample `base` (always bound) and adds +0.
@@ -770,6 +787,15 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += _range_entry(stage, w, body, stores, params, unpack, block, per_thread, xcd_order, auto)
         out += _persist_entry(stage, mode, params, unpack, block, nontemporal, auto)
     return "\n".join(out)
+
+
+def row_samples(stage: Stage, per_thread: int) -> int:
+    """Samples of a row each lane holds in a stage with row reductions: 4 at
+    a multiple of four samples a thread, 2 at an even number, else 1 (a
+    half-wave a row); 1 for rows with fused folds and in the banded mode."""
+    if not stage.row_sums or stage.fused_folds or stage.banded:
+        return 1
+    return 4 if per_thread % 4 == 0 else 2 if per_thread % 2 == 0 else 1
 
 
 def _auto_loop(stage: Stage):
@@ -1439,6 +1465,32 @@ __device__ __forceinline__ void hk_row_sum(Real& h, Real& c) {
         h = t;
     }
 }
+// Two compensated pairs joined, as at each level of hk_row_sum.
+__device__ __forceinline__ void hk_row_join(Real& h, Real& c, Real h2, Real c2) {
+    const Real t = h + h2;
+    c = hk_finite(t) ? (c + c2) + hk_two_sum_err(h, h2, t) : Real(0);
+    h = t;
+}
+// A row held two or four samples a lane (lane j of a 16- or 8-lane group:
+// samples j + 16v, or j + 8v): the pairs whose lanes share a register file
+// join in registers, the first level's (+0 + +0) + err being err, and the
+// lanes then take the remaining pairs (l, l ^ off) as in hk_row_sum: the same
+// additions on a half or a quarter of the lanes.
+__device__ __forceinline__ void hk_row_sum2(const Real (&s)[2], Real& h, Real& c) {
+    h = s[0] + s[1];
+    c = hk_finite(h) ? hk_two_sum_err(s[0], s[1], h) : Real(0);
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) hk_row_join(h, c, hk_lane_xor(h, off), hk_lane_xor(c, off));
+}
+__device__ __forceinline__ void hk_row_sum4(const Real (&s)[4], Real& h, Real& c) {
+    h = s[0] + s[2];                                            // pair (j, j + 16)
+    c = hk_finite(h) ? hk_two_sum_err(s[0], s[2], h) : Real(0);
+    Real h8 = s[1] + s[3];                                      // pair (j + 8, j + 24)
+    const Real c8 = hk_finite(h8) ? hk_two_sum_err(s[1], s[3], h8) : Real(0);
+    hk_row_join(h, c, h8, c8);                                  // pair (j, j + 8)
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1) hk_row_join(h, c, hk_lane_xor(h, off), hk_lane_xor(c, off));
+}
 """
 
 
@@ -1463,6 +1515,25 @@ __device__ __forceinline__ void hk_row_extreme(int op, Real& h) {
         const bool low = (threadIdx.x & off) == 0;
         h = low ? hk_extreme(op, h, h2) : hk_extreme(op, h2, h);
     }
+}
+// Two or four samples a lane (j + 16v or j + 8v of the row): the pairs in
+// the lane's registers first, the lower slot the left operand, then the pairs
+// (l, l ^ off) across the lanes.
+__device__ __forceinline__ Real hk_row_extreme_lanes(int op, Real h, int top) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) {
+        if (off > top) continue;
+        const Real h2 = hk_lane_xor(h, off);
+        const bool low = (threadIdx.x & off) == 0;
+        h = low ? hk_extreme(op, h, h2) : hk_extreme(op, h2, h);
+    }
+    return h;
+}
+__device__ __forceinline__ Real hk_row_extreme2(int op, const Real (&s)[2]) {
+    return hk_row_extreme_lanes(op, hk_extreme(op, s[0], s[1]), 8);
+}
+__device__ __forceinline__ Real hk_row_extreme4(int op, const Real (&s)[4]) {
+    return hk_row_extreme_lanes(op, hk_extreme(op, hk_extreme(op, s[0], s[2]), hk_extreme(op, s[1], s[3])), 4);
 }
 """
 

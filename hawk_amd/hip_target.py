@@ -330,6 +330,33 @@ class HipWriter:
                 f"              {comp}[hk_r] = hk_rc;",
                 "          } }"]
 
+    def sample_sum_rows(self, r, k: int, hi: str, comp: str, per: int) -> list:
+        """A default-policy ``hawk.sum``'s row with ``per`` (2 or 4) samples
+        a lane: row term ``k`` of the lane's samples (``hk_rt[k]``: samples
+        j + (32/per)v of its row) joins its (32/per)-lane group's row, and
+        lane 0 of the group stores the row when the row's first sample is
+        live."""
+        return [f"        {{ Real hk_rh, hk_rc;",
+                f"          hk_row_sum{per}(hk_rt[{k}], hk_rh, hk_rc);",
+                f"          if ((threadIdx.x & {32 // per - 1}) == 0 && hk_lv0) {{",
+                "              const long long hk_r = (base + hk_fl0) >> 5;",
+                f"              {hi}[hk_r] = hk_rh;",
+                f"              {comp}[hk_r] = hk_rc;",
+                "          } }"]
+
+    def sample_extreme_rows(self, r, red: str, k: int, hi: str, per: int) -> list:
+        """A ``hawk.max`` / ``hawk.min`` row with ``per`` samples a lane."""
+        op = 1 if red == "max" else 2
+        return [f"        {{ const Real hk_rh = hk_row_extreme{per}({op}, hk_rt[{k}]);",
+                f"          if ((threadIdx.x & {32 // per - 1}) == 0 && hk_lv0) {{",
+                f"              {hi}[(base + hk_fl0) >> 5] = hk_rh;",
+                "          } }"]
+
+    def row_identity(self, red: str) -> str:
+        """The term a lane past ``count`` brings to its row."""
+        return {"sum": "Real(0)", "max": "static_cast<Real>(-__builtin_inf())",
+                "min": "static_cast<Real>(__builtin_inf())"}[red]
+
     def sample_extreme(self, r, red: str, term: str, hi: str) -> list:
         """A ``hawk.max`` / ``hawk.min`` row: the lane's term joins its
         half-wave's row of 32 (a lane past ``count`` holds -inf / +inf, the
@@ -462,7 +489,8 @@ class HipWrapper:
                     out.append(f"const unsigned long long {var}_n = {var}_m.samples;   // cells")
         return "\n".join("    " + line for line in out)
 
-    def index_prologue(self, segment=None, *, active=None, box=None, form: str = "plain") -> str:
+    def index_prologue(self, segment=None, *, active=None, box=None, form: str = "plain", rows: int = 0,
+                       per_lane: int = 2) -> str:
         """The launch geometry: block ``i`` of the grid (XCD x takes a
         contiguous eighth when ``hk_xcd_order``), ``hk_per_thread`` samples a
         thread, and the lane's sample ``hk_i = base + hk_flat``.  ``form``:
@@ -470,7 +498,12 @@ class HipWrapper:
         ``base`` and stores nothing: a row reduction or a fold needs every
         lane), "full" (a block wholly below ``count`` runs an unguarded copy,
         closed by :meth:`index_partial`), "guard" (the guarded stage binds
-        ``hk_i`` itself)."""
+        ``hk_i`` itself), "rows" (the live form ``per_lane`` (2 or 4) samples
+        of a row at a time for ``rows`` row terms: each wave takes 64 *
+        per_lane consecutive samples, rows of 32, and lane j of the
+        (32/per_lane)-lane group g takes samples 32g + j + (32/per_lane)v;
+        ``hk_rt[k][v]`` holds row term k of sample v, closed by
+        :meth:`rows_close`)."""
         if segment is not None:
             _refuse("a segmented unit's prologue (offsets-plane runs)")
         if active is not None:
@@ -482,6 +515,24 @@ class HipWrapper:
         # plain order), so each XCD's L2 streams one contiguous eighth.
         out = ["    const unsigned hk_blk = (!hk_xcd_order || (gridDim.x & 7u)) ? blockIdx.x"
                " : (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3);"]
+        if form == "rows":
+            if per_lane not in (2, 4):
+                _refuse(f"rows of {per_lane} samples a lane")
+            g = 32 // per_lane
+            gb = g.bit_length() - 1
+            out += ["#pragma unroll",
+                    f"    for (int hk_p = 0; hk_p < hk_per_thread / {per_lane}; ++hk_p) {{",
+                    f"        Real hk_rt[{rows}][{per_lane}];",
+                    "        bool hk_lv0 = false;",
+                    "        long long hk_fl0 = 0;",
+                    "#pragma unroll",
+                    f"        for (int hk_v = 0; hk_v < {per_lane}; ++hk_v) {{",
+                    f"        const long long hk_flat = (static_cast<long long>(hk_blk) * (hk_per_thread / {per_lane})"
+                    f" + hk_p) * ({per_lane} * hk_block) + ((threadIdx.x >> {gb}) << 5) + (threadIdx.x & {g - 1})"
+                    f" + (hk_v << {gb});",
+                    "        const bool hk_live = hk_flat < count;",
+                    "        const long long hk_i = base + (hk_live ? hk_flat : 0LL);"]
+            return "\n".join(out)
         if form == "full":
             # a block whose samples all lie below `count` runs the unguarded
             # copy of the body: no exit between samples, so every sample's
@@ -512,6 +563,15 @@ class HipWrapper:
                           " * hk_block + static_cast<long long>(threadIdx.x);",
                           "        if (hk_flat >= count) break;",
                           "        const long long hk_i = base + hk_flat;"])
+
+    def rows_close(self, terms: list) -> str:
+        """The end of one of a lane's row samples (``form="rows"``): its row terms
+        (``(term, identity)``: a lane past ``count`` brings the identity) kept
+        for the rows, and the first sample's liveness and index."""
+        out = [f"        hk_rt[{k}][hk_v] = hk_live ? static_cast<Real>({term}) : {ident};"
+               for k, (term, ident) in enumerate(terms)]
+        out += ["        if (hk_v == 0) { hk_lv0 = hk_live; hk_fl0 = hk_flat; }", "        }"]
+        return "\n".join(out)
 
     def index_epilogue(self) -> str:
         return "    }\n}\n"

@@ -97,7 +97,14 @@ def test_a_max_is_a_row_extreme_team_stage(tmp_path):
     assert sc["planes"]["t"]["role"] == "cell" and sc["planes"]["t"]["shape"] == []
     assert b.sidecar("cell_mean")["team"][0]["op"] == "row_sum"
     src = (tmp_path / "cell_max.hip").read_text()
-    assert "hk_row_extreme(1, hk_rh)" in src and "-__builtin_inf()" in src     # a lane past the run is -inf
+    # four samples of a row a lane (its launch shape takes four samples a
+    # thread); a lane past the run brings -inf
+    assert "hk_row_extreme4(1, hk_rt[0])" in src and "-__builtin_inf()" in src
+    for pt, form in ((1, "hk_row_extreme(1, hk_rh)"), (2, "hk_row_extreme2(1, hk_rt[0])"),
+                     (6, "hk_row_extreme2(1, hk_rt[0])"), (8, "hk_row_extreme4(1, hk_rt[0])")):
+        hawk.build([cell_max], tmp_path / f"pt{pt}", per_thread=pt)
+        body = (tmp_path / f"pt{pt}" / "cell_max.hip").read_text().split('extern "C" __global__')[-1]
+        assert form in body, (pt, form)
 
 
 def test_a_vector_cell_is_one_row_stage_per_column(tmp_path):
@@ -282,6 +289,29 @@ def test_vector_cells_are_each_columns_reduction(built, gpu, n):
     m = dev(np.full(3, np.nan, mode), gpu)
     hawk.run(hawk.load(root, "vec_max"), v=dev(v, gpu), t=m)
     assert host(m).tobytes() == v.max(axis=1).tobytes()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", (1, 17, 33, 4096 * 3 + 81, 100_003))
+def test_both_row_layouts_are_the_oracles_bits(gpu, tmp_path, n):
+    """The rows four samples a lane (samples j + 8v of a row in lane j of an
+    8-lane group, at a multiple of four samples a thread: the default for
+    these kernels), two (j + 16v, at an even number) and one
+    (``per_thread=1``: a half-wave a row) give the oracle's bits for a sum, a
+    max and a min, in both scalar modes."""
+    for mode in ("float64", "float32"):
+        x = _x(n, mode)
+        for pt, form in ((1, "hk_row_sum(hk_rh"), (2, "hk_row_sum2("), (4, "hk_row_sum4("), (6, "hk_row_sum2(")):
+            root = tmp_path / f"{mode}_{pt}"
+            hawk.build([cell_sum, cell_max, cell_min], root, mode=mode, per_thread=pt)
+            body = (root / "cell_sum.hip").read_text().split('extern "C" __global__')[-1]
+            assert form in body, (pt, form)
+            for op in ("sum", "max", "min"):
+                print(f"row layout {mode} per_thread={pt} {op} n={n}", flush=True)
+                out = dev(np.full(1, np.nan, dtype=mode), gpu)
+                hawk.run(hawk.load(root, f"cell_{op}"), x=dev(x, gpu), t=out)
+                want = np.asarray(_want(op, x, mode), dtype=mode)
+                assert host(out)[0].tobytes() == want.tobytes(), (mode, pt, op, host(out)[0], want)
 
 
 @pytest.mark.gpu
