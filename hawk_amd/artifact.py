@@ -93,7 +93,7 @@ def launch_shape(plan, mode: str) -> tuple:
     if nbytes <= STREAM_BYTES and fp_ops_per_sample(plan.source) <= STREAM_OPS:
         return 256, 4
     shape = (256, 1) if 32 < nbytes <= 64 else (128, 1)
-    if stage.row_sums and not stage.fused_folds and not getattr(stage, "banded", False):
+    if stage.row_sums and not stage.fused_folds:
         # row reductions take two samples a lane (the paired layout)
         shape = (shape[0], 2)
     return shape

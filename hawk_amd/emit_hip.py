@@ -760,7 +760,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += wrap.rows_close([(term, w.spell.row_identity(red)) for term, _hi, _comp, red in row_terms]).splitlines()
         for k, (term, hi, comp, red) in enumerate(row_terms):
             if red == "sum":
-                out += w.spell.sample_sum_rows(w, k, hi, comp, per)
+                out += w.spell.sample_sum_rows(w, k, hi, comp, per, stage.banded)
             else:
                 out += w.spell.sample_extreme_rows(w, red, k, hi, per)
     else:
@@ -792,8 +792,8 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
 def row_samples(stage: Stage, per_thread: int) -> int:
     """Samples of a row each lane holds in a stage with row reductions: 4 at
     a multiple of four samples a thread, 2 at an even number, else 1 (a
-    half-wave a row); 1 for rows with fused folds and in the banded mode."""
-    if not stage.row_sums or stage.fused_folds or stage.banded:
+    half-wave a row); 1 for a stage with fused folds."""
+    if not stage.row_sums or stage.fused_folds:
         return 1
     return 4 if per_thread % 4 == 0 else 2 if per_thread % 2 == 0 else 1
 
@@ -1571,6 +1571,26 @@ __device__ __forceinline__ void hk_band_row_sum(double& h, double& l) {
         const double l2 = hk_lane_xor(l, off);
         hk_band_add(h, l, h2, l2);
     }
+}
+// Two or four samples of a row a lane (j + 16v or j + 8v): the pairs whose
+// lanes share a register file join in registers, each sample the band
+// (term, +0), then the lanes take the remaining pairs (l, l ^ off).
+__device__ __forceinline__ void hk_band_row_sum2(const double (&s)[2], double& h, double& l) {
+    h = s[0];
+    l = 0.0;
+    hk_band_add(h, l, s[1], 0.0);
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) hk_band_add(h, l, hk_lane_xor(h, off), hk_lane_xor(l, off));
+}
+__device__ __forceinline__ void hk_band_row_sum4(const double (&s)[4], double& h, double& l) {
+    h = s[0];
+    l = 0.0;
+    hk_band_add(h, l, s[2], 0.0);                 // pair (j, j + 16)
+    double h8 = s[1], l8 = 0.0;
+    hk_band_add(h8, l8, s[3], 0.0);               // pair (j + 8, j + 24)
+    hk_band_add(h, l, h8, l8);                    // pair (j, j + 8)
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1) hk_band_add(h, l, hk_lane_xor(h, off), hk_lane_xor(l, off));
 }
 """
 

@@ -330,14 +330,14 @@ class HipWriter:
                 f"              {comp}[hk_r] = hk_rc;",
                 "          } }"]
 
-    def sample_sum_rows(self, r, k: int, hi: str, comp: str, per: int) -> list:
+    def sample_sum_rows(self, r, k: int, hi: str, comp: str, per: int, banded: bool = False) -> list:
         """A default-policy ``hawk.sum``'s row with ``per`` (2 or 4) samples
         a lane: row term ``k`` of the lane's samples (``hk_rt[k]``: samples
-        j + (32/per)v of its row) joins its (32/per)-lane group's row, and
-        lane 0 of the group stores the row when the row's first sample is
-        live."""
+        j + (32/per)v of its row) joins its (32/per)-lane group's row
+        (compensated pairs, or bands in the banded mode), and lane 0 of the
+        group stores the row when the row's first sample is live."""
         return [f"        {{ Real hk_rh, hk_rc;",
-                f"          hk_row_sum{per}(hk_rt[{k}], hk_rh, hk_rc);",
+                f"          {'hk_band_row_sum' if banded else 'hk_row_sum'}{per}(hk_rt[{k}], hk_rh, hk_rc);",
                 f"          if ((threadIdx.x & {32 // per - 1}) == 0 && hk_lv0) {{",
                 "              const long long hk_r = (base + hk_fl0) >> 5;",
                 f"              {hi}[hk_r] = hk_rh;",

@@ -298,7 +298,8 @@ def test_both_row_layouts_are_the_oracles_bits(gpu, tmp_path, n):
     8-lane group, at a multiple of four samples a thread: the default for
     these kernels), two (j + 16v, at an even number) and one
     (``per_thread=1``: a half-wave a row) give the oracle's bits for a sum, a
-    max and a min, in both scalar modes."""
+    max and a min, in both scalar modes, and for a sum of bands in the banded
+    mode."""
     for mode in ("float64", "float32"):
         x = _x(n, mode)
         for pt, form in ((1, "hk_row_sum(hk_rh"), (2, "hk_row_sum2("), (4, "hk_row_sum4("), (6, "hk_row_sum2(")):
@@ -312,6 +313,16 @@ def test_both_row_layouts_are_the_oracles_bits(gpu, tmp_path, n):
                 hawk.run(hawk.load(root, f"cell_{op}"), x=dev(x, gpu), t=out)
                 want = np.asarray(_want(op, x, mode), dtype=mode)
                 assert host(out)[0].tobytes() == want.tobytes(), (mode, pt, op, host(out)[0], want)
+    # the banded mode's rows (bands) in the same three layouts
+    x = _x(n, "float64")
+    for pt, form in ((1, "hk_band_row_sum(hk_rh"), (2, "hk_band_row_sum2("), (4, "hk_band_row_sum4(")):
+        root = tmp_path / f"banded_{pt}"
+        hawk.build([cell_sum], root, mode="banded", per_thread=pt)
+        assert form in (root / "cell_sum.hip").read_text().split('extern "C" __global__')[-1], (pt, form)
+        print(f"row layout banded per_thread={pt} n={n}", flush=True)
+        out = dev(np.full(1, np.nan), gpu)
+        hawk.run(hawk.load(root, "cell_sum"), x=dev(x, gpu), t=out)
+        assert host(out)[0] == O.band_sample_sum(x * x), (pt, host(out)[0])
 
 
 @pytest.mark.gpu
