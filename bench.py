@@ -136,7 +136,8 @@ def workload(config: str, device):
         # the stage's HBM pattern (one row read, one written) in its own launch shape, for pattern_ceiling
         sh = k.launch_shape
         return dict(name="scale fwd (config 1)", n=n, kernels=kernels, work=work, cpu=cpu, dtype="f64",
-                    pattern={"scale": (1, 1, sh["block"], sh["block"], sh["per_thread"], _xcd(unit, "scale"))},
+                    pattern={"scale": (1, 1, sh["block"], sh["block"], sh["per_thread"], _xcd(unit, "scale"),
+                                       "hk_pair_" in (unit / "scale.hip").read_text())},
                     esize=8)
     if config == "2":
         n = 1 << 25
@@ -616,6 +617,53 @@ extern "C" __global__ void __launch_bounds__({threads}) hawk_pattern_copy(
 """
 
 
+# The pattern of a stage that runs in pairs of adjacent samples (16 bytes a
+# lane a row): thread t of workgroup g takes pairs (g*{per} + v)*{threads} + t.
+_PAIR_SOURCE = """
+typedef {elem} E;
+typedef E V __attribute__((ext_vector_type(2)));
+struct GRefMirror {{ void* data_; unsigned long long samples_, compStride_, sampleStride_; int deviceType_, deviceId_; }};
+extern "C" __attribute__((used)) __device__ char eagle_abi_tag[] = "aether-abi/2";
+extern "C" __attribute__((used)) __device__ unsigned long long eagle_layout_sizes[5] = {{40, 32, 32, 8, 24}};
+extern "C" __global__ void __launch_bounds__({threads}) hawk_pattern_pairs(
+        GRefMirror in_m, GRefMirror out_m, long long base, long long count, long long nSamples) {{
+    const E* in = static_cast<const E*>(in_m.data_);
+    E* out = static_cast<E*>(out_m.data_);
+    const long long groups = count / (2 * {threads} * {per});
+    const long long group = blockIdx.x;
+    if (group >= groups) return;
+    V x[{per}][{rows_in}];
+#pragma unroll
+    for (int v = 0; v < {per}; ++v) {{
+        const long long s0 = base + ((group * {per} + v) * {threads} + threadIdx.x) * 2;
+#pragma unroll
+        for (int r = 0; r < {rows_in}; ++r)
+            x[v][r] = __builtin_nontemporal_load(reinterpret_cast<const V*>(in + static_cast<long long>(r) * nSamples + s0));
+    }}
+    if ({read_only}) {{           // the reads alone: one store a thread, never taken for finite data
+        E a = E(0);
+#pragma unroll
+        for (int v = 0; v < {per}; ++v)
+#pragma unroll
+            for (int r = 0; r < {rows_in}; ++r) a += x[v][r].x + x[v][r].y;
+        if (a != a) out[threadIdx.x] = a;
+        return;
+    }}
+#pragma unroll
+    for (int v = 0; v < {per}; ++v) {{
+        const long long s0 = base + ((group * {per} + v) * {threads} + threadIdx.x) * 2;
+#pragma unroll
+        for (int r = 0; r < {rows_out}; ++r) {{     // output row r folds input rows r, r + rows_out, ...
+            V o = x[v][r];
+#pragma unroll
+            for (int j = r + {rows_out}; j < {rows_in}; j += {rows_out}) o += x[v][j];
+            __builtin_nontemporal_store(o, reinterpret_cast<V*>(out + static_cast<long long>(r) * nSamples + s0));
+        }}
+    }}
+}}
+"""
+
+
 def _gen(device):
     """A seeded generator on ``device`` for the pattern copies' input planes."""
     import torch
@@ -660,9 +708,29 @@ def pattern_ceiling(w, device, reps: int = 10) -> dict:
     n, esize = w["n"], w["esize"]
     dt = torch.float64 if esize == 8 else torch.float32
     elem = "double" if esize == 8 else "float"
-    for label, (rows_in, rows_out, tile, threads, per, xcd) in w["pattern"].items():
+    for label, (rows_in, rows_out, tile, threads, per, xcd, *pairs) in w["pattern"].items():
         if n % (tile * per):
             raise ValueError(f"pattern_ceiling: N={n} is not a multiple of the tiles ({per} x {tile})")
+        if pairs and pairs[0]:
+            # a stage in pairs of adjacent samples: its pattern, 16 bytes a lane a row
+            src_t = torch.randn((rows_in, n), dtype=dt, device=device, generator=_gen(device))
+            dst_t = torch.empty((rows_out, n), dtype=dt, device=device)
+            ab = _core.ArgBlock(["gref", "gref"])
+            ab.bind(0, src_t.data_ptr(), n)
+            ab.bind(1, dst_t.data_ptr(), n)
+            rate = {}
+            for read_only in (0, 1):
+                src = _PAIR_SOURCE.format(elem=elem, rows_in=rows_in, rows_out=rows_out, threads=threads,
+                                          per=per // 2, read_only=read_only)
+                ms = _time_copy(src, "hawk_pattern_pairs", ab, n // (threads * per), threads, n, reps)
+                moved = rows_in if read_only else rows_in + rows_out
+                rate[read_only] = (ms, moved * esize * n / (ms * 1e-3) / 1e9)
+            out[label] = {"pattern": f"{rows_in} rows in, {rows_out} out, pairs of adjacent samples on "
+                                     f"{threads} threads, {per // 2} a thread",
+                          "ms": round(rate[0][0], 5), "copy_GBs": round(rate[0][1], 1),
+                          "reads_only_GBs": round(rate[1][1], 1)}
+            del src_t, dst_t, ab
+            continue
         # normal variates like the workloads' planes: a plane of zeros copies some 5 % faster (the
         # energy forward's pattern: 7.52 TB/s from zeros, 7.15 from its own v), so zeros overstate the
         # ceiling

@@ -81,17 +81,26 @@ def _stage_bytes(plan, mode: str) -> int:
 #: 0.36 at 512 x 2, 0.28 at 1024 x 2, 0.41 at 1024 x 4).
 GATHER_SHAPE = (1024, 2)
 
+#: The launch shape of a light stream whose planes are all scalar float64
+#: planes: 64 threads of one pair of adjacent samples, read and written 16
+#: bytes a lane (``emit_hip._pair_lines``).  A copy of ``scale``'s pattern
+#: measured 0.1634 ms at 64 threads x 16 B, 0.1655-0.1666 at 128-512 x 16 B,
+#: and 0.1683-0.1703 for 8 B a lane at 256 x 4, 512 x 2 and 128 x 4 (2^26
+#: samples, one box).
+PAIR_SHAPE = (64, 2)
+STREAM_SHAPE = (256, 4)
+
 
 def launch_shape(plan, mode: str) -> tuple:
     """``(block, per_thread)`` a stage runs with when the build does not fix them."""
-    from .emit_hip import fp_ops_per_sample
+    from .emit_hip import fp_ops_per_sample, pair_candidate
     stage = plan.stage
     if (any(info["role"] == "lookup" for info in stage.planes.values()) and not stage.row_sums
             and not stage.fused_folds and not stage.key_writes and stage.guard is None and stage.finish is None):
         return GATHER_SHAPE
     nbytes = _stage_bytes(plan, mode)
     if nbytes <= STREAM_BYTES and fp_ops_per_sample(plan.source) <= STREAM_OPS:
-        return 256, 4
+        return PAIR_SHAPE if pair_candidate(stage, mode) else STREAM_SHAPE
     shape = (256, 1) if 32 < nbytes <= 64 else (128, 1)
     if stage.row_sums and not stage.fused_folds:
         # row reductions take two samples a lane (the paired layout)
@@ -289,6 +298,12 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
             auto = launch_shape(plan, mode)
             shape = (block or auto[0], per_thread or auto[1])
             if shape != (256, 1):
+                plan = plan_kernel(k.program, k.name, mode=mode, block=shape[0], per_thread=shape[1],
+                                   nontemporal=nontemporal, fuse_folds=fuse_folds, target=target)
+            if shape == PAIR_SHAPE and "hk_pair_" not in plan.source:
+                # the body reads a plane other than at its own sample: the
+                # one-sample stream shape
+                shape = STREAM_SHAPE
                 plan = plan_kernel(k.program, k.name, mode=mode, block=shape[0], per_thread=shape[1],
                                    nontemporal=nontemporal, fuse_folds=fuse_folds, target=target)
         if plan.stage is not None and min_blocks > 1:

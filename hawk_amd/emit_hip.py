@@ -669,6 +669,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
     # the same commits with their values taken from hk_sv[hk_v][k] (the
     # two-pass full-block form): only when every written plane holds Real
     deferred = None
+    targets = []                          # (plane var, component) of each deferred value
     if not stage.key_writes and all(stage.planes[p].get("dtype") in (None, "f64", "f32") for p, _ in stage.writes):
         deferred = ([], [])
         for plane, node in stage.writes:
@@ -679,6 +680,7 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
                 k = len(deferred[0])
                 deferred[0].append(f"hk_sv[hk_v][{k}] = {vals[0 if c is None else c]};")
                 deferred[1].append(w.spell.component_commit(w, var, c, "=", f"hk_sv[hk_v][{k}]"))
+                targets.append((var, c))
         if w.lines or len(stores) != len(deferred[0]):
             deferred = None               # the stores computed a value of their own: keep one pass
         w.lines = []
@@ -725,7 +727,13 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += wrap.index_prologue(form="guard").splitlines()
         out += _guarded_lines(stage, w, body, stores)
     elif not row_terms and not folds:
-        if per_thread > 1 and deferred and deferred[0]:
+        pair_loads = _adjacent_pairs(stage, mode, per_thread, deferred, targets, body)
+        if pair_loads is not None:
+            out.insert(out.index(f"typedef {real} Real;") + 1, "typedef Real hk_d2 __attribute__((ext_vector_type(2)));")
+            head = wrap.index_prologue(form="full").splitlines()
+            out += _pair_lines(head[0], pair_loads, deferred[0], targets, body, nontemporal)
+            out += wrap.index_partial().splitlines()[3:]
+        elif per_thread > 1 and deferred and deferred[0]:
             # a full block in two passes: every sample's values (and so every
             # load) first, then every store, so no load waits behind a store
             keep, commit = deferred
@@ -787,6 +795,87 @@ def render_stage(stage: Stage, mode: str, block: int, per_thread: int, unroll_ta
         out += _range_entry(stage, w, body, stores, params, unpack, block, per_thread, xcd_order, auto)
         out += _persist_entry(stage, mode, params, unpack, block, nontemporal, auto)
     return "\n".join(out)
+
+
+_PLANE_INDEX = re.compile(r"(hk_p_\w+)\[")
+
+
+def _adjacent_pairs(stage: Stage, mode: str, per_thread: int, deferred, targets: list, body: list):
+    """The planes a light float64 stage loads, when its full blocks can run
+    as pairs of adjacent samples (one 16-byte load and store a plane a pair):
+    an even number of samples a thread, every written plane a scalar plane of
+    Real, and every plane access in the body a scalar plane read at the lane's
+    own sample.  ``None`` when the stage keeps the one-sample form."""
+    if mode != "float64" or per_thread % 2 or not deferred or not deferred[0] or stage.guard is not None:
+        return None
+    if any(c is not None for _var, c in targets):
+        return None
+    text = "\n".join(body)
+    if "hk_flat" in text or "threadIdx" in text:
+        return None
+    scalar = {info["var"] for info in stage.planes.values() if not info.get("shape") and info.get("dtype") in (None, "f64")}
+    loads = []
+    for m in _PLANE_INDEX.finditer(text):
+        var = m.group(1)
+        if not text.startswith("hk_i]", m.end()) or var not in scalar:
+            return None
+        if var not in loads:
+            loads.append(var)
+    return loads
+
+
+def pair_candidate(stage: Stage, mode: str) -> bool:
+    """Whether a stage can take the adjacent-pairs form at an even number of
+    samples a thread, from its planes alone (the body's plane accesses are
+    checked when it is rendered): float64, no reduction, fold, keyed write or
+    guard, and every per-sample plane a scalar plane of Real."""
+    if mode != "float64" or stage.row_sums or stage.fused_folds or stage.key_writes or stage.guard is not None:
+        return False
+    for info in stage.planes.values():
+        if info["role"] in ("uniform", "nsamples"):
+            continue
+        if info["role"] not in ("per_sample", "mutable", "out") or info.get("shape") or info.get("dtype") not in (None, "f64"):
+            return False
+    return True
+
+
+def _pair_lines(blk_line: str, loads: list, keep: list, targets: list, body: list, nontemporal: bool) -> list:
+    """The full blocks of a stage as pairs of adjacent samples (see
+    :func:`_adjacent_pairs`): thread t of block b takes samples 2t and 2t + 1
+    of each 2 * hk_block of the block's span, the same samples the block
+    covers one at a time, so a row of results is the same bits; the planes are
+    read and written 16 bytes a lane.  Taken when every plane pointer and
+    ``base`` keep a pair 16-byte aligned; the partial last block, and a launch
+    that is not aligned, run the one-sample loop that follows."""
+    ptrs = sorted(set(loads) | {var for var, _c in targets})
+    aligned = " | ".join(f"reinterpret_cast<unsigned long long>({v})" for v in ptrs)
+    out = [blk_line,
+           f"    const bool hk_al = (({aligned}) & 15ull) == 0 && (base & 1LL) == 0;",
+           "    if (hk_al && (static_cast<long long>(hk_blk) + 1) * (hk_per_thread * hk_block) <= count) {",
+           "#pragma unroll",
+           "    for (int hk_q = 0; hk_q < hk_per_thread / 2; ++hk_q) {",
+           "        const long long hk_i0 = base + ((static_cast<long long>(hk_blk) * (hk_per_thread / 2) + hk_q)"
+           " * hk_block + static_cast<long long>(threadIdx.x)) * 2;"]
+    for v in loads:
+        at = f"reinterpret_cast<const hk_d2*>(&{v}[hk_i0])"
+        out.append(f"        const hk_d2 hk_pair_{v} = " + (f"__builtin_nontemporal_load({at});" if nontemporal else f"*{at};"))
+    out += [f"        Real hk_sv[2][{len(keep)}];",
+            "#pragma unroll",
+            "        for (int hk_v = 0; hk_v < 2; ++hk_v) {",
+            "        const long long hk_i = hk_i0 + hk_v;"]
+    for line in body:
+        for v in loads:
+            line = line.replace(f"__builtin_nontemporal_load(&{v}[hk_i])", f"hk_pair_{v}[hk_v]").replace(
+                f"{v}[hk_i]", f"hk_pair_{v}[hk_v]")
+        out.append(line)
+    out += ["        " + line for line in keep]
+    out += ["        }"]
+    for k, (var, _c) in enumerate(targets):
+        at = f"reinterpret_cast<hk_d2*>(&{var}[hk_i0])"
+        out += [f"        hk_d2 hk_st{k};", f"        hk_st{k}.x = hk_sv[0][{k}];", f"        hk_st{k}.y = hk_sv[1][{k}];",
+                f"        __builtin_nontemporal_store(hk_st{k}, {at});" if nontemporal else f"        *{at} = hk_st{k};"]
+    out += ["    }", "    return;", "    }"]
+    return out
 
 
 def row_samples(stage: Stage, per_thread: int) -> int:

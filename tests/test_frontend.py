@@ -1087,7 +1087,8 @@ def test_ambient_options_reach_the_build_and_an_explicit_one_wins(tmp_path):
     assert amb["launch"]["block"] == 128 and amb["build_options"]["launch_bounds"] == [128, 2]
     assert amb["build_options"]["contraction"] == "gemm" and amb["build_options"]["emit_form"] == "rolled"
     assert exp["launch"]["block"] == 64 and exp["build_options"]["launch_bounds"] == [64, 4]
-    assert "build_options" not in plain and plain["launch"]["block"] == 256     # scale's own shape
+    assert "build_options" not in plain and (plain["launch"]["block"], plain["launch"]["per_thread"]) == (64, 2)
+    # (scale's own shape: pairs of adjacent samples)
     with pytest.raises(hawk.HawkError, match="contraction must be one of"):
         with policy.using(contraction="blas"):
             pass

@@ -79,6 +79,35 @@ def test_a_partition_writes_its_range_only(unit, gpu):
     assert got[base:base + count].tobytes() == want[base:base + count].tobytes()
 
 
+def test_scale_in_pairs_of_adjacent_samples(unit, gpu):
+    """``scale`` runs its full blocks as pairs of adjacent samples, 16 bytes a
+    lane, when the planes and ``base`` keep a pair 16-byte aligned, and the
+    one-sample loop otherwise: both give the oracle's bits, over a partition
+    with an even base (pairs, then a partial block), an odd base, planes that
+    start one element into their buffers, and in place."""
+    import hawk_amd as hawk
+    k = _load(unit, "scale")
+    assert (k.launch_shape["block"], k.launch_shape["per_thread"]) == (64, 2)
+    n = 100_003
+    x = rng(12).uniform(-1.0, 1.0, n + 1)
+    want = O.scale(x, 2.0, 1.0)
+    for base, count in ((4096, 50_001), (31_337, 40_009), (0, n)):
+        print(f"scale pairs: base={base} count={count}", flush=True)
+        out = dev(np.full(n, -12345.0), gpu)
+        hawk.run(k, x=dev(x[:n], gpu), a=2.0, b=1.0, out=out, base=base, count=count)
+        got = host(out)
+        assert np.all(got[:base] == -12345.0) and np.all(got[base + count:] == -12345.0)
+        assert got[base:base + count].tobytes() == want[base:base + count].tobytes()
+    print("scale pairs: planes one element into their buffers", flush=True)
+    X, OUT = dev(x, gpu), dev(np.zeros(n + 1), gpu)
+    hawk.run(k, x=X[1:], a=2.0, b=1.0, out=OUT[1:])
+    assert host(OUT)[1:].tobytes() == want[1:].tobytes()
+    print("scale pairs: in place", flush=True)
+    Y = dev(x[:n].copy(), gpu)
+    hawk.run(k, x=Y, a=2.0, b=1.0, out=Y)
+    assert host(Y).tobytes() == want[:n].tobytes()
+
+
 def test_empty_run_touches_nothing(unit, gpu):
     import hawk_amd as hawk
     x = dev(np.zeros(16), gpu)
