@@ -300,10 +300,10 @@ def build_bundle(kernels, directory, *, targets=("hip",), mode: str = "float64",
             if shape != (256, 1):
                 plan = plan_kernel(k.program, k.name, mode=mode, block=shape[0], per_thread=shape[1],
                                    nontemporal=nontemporal, fuse_folds=fuse_folds, target=target)
-            if shape == PAIR_SHAPE and "hk_pair_" not in plan.source:
+            if auto == PAIR_SHAPE and "hk_pair_" not in plan.source:
                 # the body reads a plane other than at its own sample: the
-                # one-sample stream shape
-                shape = STREAM_SHAPE
+                # one-sample stream shape (for what the build left open)
+                shape = (block or STREAM_SHAPE[0], per_thread or STREAM_SHAPE[1])
                 plan = plan_kernel(k.program, k.name, mode=mode, block=shape[0], per_thread=shape[1],
                                    nontemporal=nontemporal, fuse_folds=fuse_folds, target=target)
         if plan.stage is not None and min_blocks > 1:

@@ -1092,3 +1092,27 @@ def test_ambient_options_reach_the_build_and_an_explicit_one_wins(tmp_path):
     with pytest.raises(hawk.HawkError, match="contraction must be one of"):
         with policy.using(contraction="blas"):
             pass
+
+
+def test_light_scalar_streams_run_in_pairs_of_adjacent_samples(tmp_path):
+    """A light stream whose planes are all scalar float64 planes (``scale``)
+    builds 64 threads of a pair of adjacent samples, each plane read and
+    written 16 bytes a lane behind an alignment test, with the one-sample
+    loop after it; at an even number of samples a thread the pair form is
+    taken whatever the block; the float32 mode, an odd number of samples a
+    thread and a stage with a vector plane keep one sample a lane."""
+    sc = hawk.build([E.scale], tmp_path / "a").sidecar("scale")
+    assert (sc["launch"]["block"], sc["launch"]["per_thread"]) == (64, 2)
+    src = (tmp_path / "a" / "scale.hip").read_text().split('extern "C" __global__')[-1]
+    assert "const hk_d2 hk_pair_hk_p_x = __builtin_nontemporal_load(reinterpret_cast<const hk_d2*>(&hk_p_x[hk_i0]))" in src
+    assert "__builtin_nontemporal_store(hk_st0, reinterpret_cast<hk_d2*>(&hk_p_out[hk_i0]))" in src
+    assert "& 15ull) == 0 && (base & 1LL) == 0" in src
+    assert "if (hk_flat >= count) break;" in src                   # the one-sample loop after the pairs
+    hawk.build([E.scale], tmp_path / "b", block=256, per_thread=4)
+    assert "hk_pair_" in (tmp_path / "b" / "scale.hip").read_text()
+    for d, kw in (("c", {"mode": "float32"}), ("d", {"per_thread": 3})):
+        sc = hawk.build([E.scale], tmp_path / d, **kw).sidecar("scale")
+        assert "hk_pair_" not in (tmp_path / d / "scale.hip").read_text(), kw
+    assert sc["launch"]["per_thread"] == 3
+    hawk.build([E.energy], tmp_path / "e", block=64, per_thread=2)
+    assert "hk_pair_" not in (tmp_path / "e" / "energy.hip").read_text()   # a Vector[3] plane
