@@ -863,10 +863,13 @@ def _pair_lines(blk_line: str, loads: list, keep: list, targets: list, body: lis
             "#pragma unroll",
             "        for (int hk_v = 0; hk_v < 2; ++hk_v) {",
             "        const long long hk_i = hk_i0 + hk_v;"]
+    # each read of a loaded plane at the lane's sample (streamed or plain),
+    # the plane's name not a suffix of a longer name
+    reads = [(re.compile(r"__builtin_nontemporal_load\(&" + re.escape(v) + r"\[hk_i\]\)|(?<!\w)" + re.escape(v)
+                         + r"\[hk_i\]"), f"hk_pair_{v}[hk_v]") for v in loads]
     for line in body:
-        for v in loads:
-            line = line.replace(f"__builtin_nontemporal_load(&{v}[hk_i])", f"hk_pair_{v}[hk_v]").replace(
-                f"{v}[hk_i]", f"hk_pair_{v}[hk_v]")
+        for pattern, pair in reads:
+            line = re.sub(pattern, pair, line)
         out.append(line)
     out += ["        " + line for line in keep]
     out += ["        }"]
