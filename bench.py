@@ -1380,7 +1380,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build's hot path runs on a single MI355X "
-              "(multi-GPU sharding is described in DESIGN.md, not launched)", file=sys.stderr)
+              "(sharding over several GPUs is a design, not launched)", file=sys.stderr)
         return 2
     import torch
     device = torch.device("cuda:0")
