@@ -177,42 +177,45 @@ constexpr size_t kBandLanesBytes = sizeof(Band) * kBandVirtual;
 constexpr size_t kBandGpBytes = sizeof(Band) * kGroups;
 constexpr size_t kBandSumScratch = kBandLanesBytes + kBandGpBytes + 256;
 
-// One workgroup per kBandChains virtual lanes.  The first kBandChainWaves
-// waves are the chains: lane c < kBandPerWave of chain wave w adds column
-// w * kBandPerWave + c of each stage (kBandStage row blocks of kBandChains
-// contiguous values) to its lane sum, row after row, from an LDS buffer.
-// The kBandLoaders threads after them read the rows:
-// each stage into registers three stages ahead of the chains and into the
-// LDS buffer one stage ahead, so a read has two stages' worth of chain work
-// to arrive.  Clears the fold's ticket one launch ahead of the fold.
+// One workgroup per kBandChains virtual lanes: wave 0 is the chains (lane c
+// < kBandChains adds column c of each stage, kBandStage row blocks of
+// kBandChains contiguous values, to its lane sum, row after row) and the
+// kBandLoaders threads after it read the rows.  A stage reaches the loaders'
+// registers kBandAhead stages before the chains add it and their LDS ring
+// (kBandSlots stages) two stages before; the chain wave reads each stage into
+// registers one stage ahead, so neither the rows' nor the LDS's latency
+// meets the chain.  Clears the fold's ticket one launch ahead of the fold.
+// Measured on MI355X at N = 2^26: 0.204 ms, against 0.227 for a two-stage
+// ring of 64-row stages read after each barrier with 256 loaders, and 0.209
+// with 256 loaders here (two loader waves leave the chains' SIMD to them).
+// Chains spread over two or four waves measured slower (282 and 358 us
+// against 236 in the two-stage form).
 constexpr int kBandChains = 32;
-// One chain wave: measured on MI355X at N = 2^26, 236 us against 282 and 358
-// with the chains spread over two and four waves.
-constexpr int kBandChainWaves = 1;
-constexpr int kBandPerWave = kBandChains / kBandChainWaves;
-constexpr int kBandStage = 64;
-constexpr int kBandLoaders = 256;
-constexpr int kBandThreads = 64 * kBandChainWaves + kBandLoaders;
+constexpr int kBandStage = 32;
+constexpr int kBandSlots = 3;
+constexpr int kBandAhead = 6;                 // stages a row read has before its chain adds it
+constexpr int kBandSets = kBandAhead - 2;     // loader register sets: stage s read at s - 6, stored at s - 2
+constexpr int kBandLoaders = 128;
+constexpr int kBandThreads = 64 + kBandLoaders;
 constexpr int kBandPer = kBandStage * kBandChains / kBandLoaders;   // values a loader reads a stage
-static_assert(kBandVirtual % kBandChains == 0, "whole workgroups of chains");
+static_assert(kBandVirtual % kBandChains == 0 && kBandSets == 4, "whole workgroups of chains, four register sets");
 
 __global__ __launch_bounds__(kBandThreads) void hawk_band_sum_lanes(const double* __restrict__ u, long long n,
                                                                      Band* __restrict__ lanes,
                                                                      unsigned* __restrict__ ticket) {
-    __shared__ double buf[2][kBandStage * kBandChains];
+    __shared__ double buf[kBandSlots][kBandStage * kBandChains];
     const int t = threadIdx.x;
-    const bool chains = t < 64 * kBandChainWaves;
-    const int lt = t - 64 * kBandChainWaves;     // a loader's index
-    const int col = (t >> 6) * kBandPerWave + (t & 63);   // a chain lane's column
-    const bool chain = chains && (t & 63) < kBandPerWave;
+    const bool loader = t >= 64;
+    const int lt = t - 64;
+    const bool chain = t < kBandChains;
     const long long l0 = static_cast<long long>(blockIdx.x) * kBandChains;
     if (blockIdx.x == 0 && t == 0) *ticket = 0u;
     // row blocks of lane l0, the workgroup's longest lane, and its stages
     const long long blocks = n > l0 ? (n - l0 + kBandVirtual - 1) / kBandVirtual : 0;
     const long long stages = (blocks + kBandStage - 1) / kBandStage;
-    double r0[kBandPer], r1[kBandPer];
+    double ld[kBandSets][kBandPer];
     auto load = [&](long long st, double (&reg)[kBandPer]) {
-        if (chains || st >= stages) return;
+        if (!loader || st >= stages) return;
 #pragma unroll
         for (int q = 0; q < kBandPer; ++q) {
             const int i = lt + q * kBandLoaders;
@@ -220,45 +223,58 @@ __global__ __launch_bounds__(kBandThreads) void hawk_band_sum_lanes(const double
             reg[q] = r < n ? __builtin_nontemporal_load(u + r) : 0.0;
         }
     };
-    auto store = [&](long long st, int slot, const double (&reg)[kBandPer]) {
-        if (chains || st >= stages) return;
+    auto store = [&](long long st, const double (&reg)[kBandPer]) {
+        if (!loader || st >= stages) return;
+        double* slot = buf[st % kBandSlots];
 #pragma unroll
-        for (int q = 0; q < kBandPer; ++q) buf[slot][lt + q * kBandLoaders] = reg[q];
+        for (int q = 0; q < kBandPer; ++q) slot[lt + q * kBandLoaders] = reg[q];
     };
-    const long long mine = chain && l0 + col < n ? (n - l0 - col + kBandVirtual - 1) / kBandVirtual : 0;
+    const long long mine = chain && l0 + t < n ? (n - l0 - t + kBandVirtual - 1) / kBandVirtual : 0;
     LaneSum acc{0.0, 0.0};
-    load(0, r0);
-    load(1, r1);
-    store(0, 0, r0);
-    load(2, r0);
-    __syncthreads();
-    for (long long st = 0; st < stages; ++st) {
-        const int slot = static_cast<int>(st & 1);
-        if (chain) {
-            const long long left = mine - st * kBandStage;
-            const int m = left < 0 ? 0 : (left < kBandStage ? static_cast<int>(left) : kBandStage);
-            double v[kBandStage];
+    double v[2][kBandStage];
+    auto fetch = [&](long long st, double (&v)[kBandStage]) {
+        if (!chain || st >= stages) return;
+        const double* slot = buf[st % kBandSlots];
 #pragma unroll
-            for (int k = 0; k < kBandStage; ++k) v[k] = buf[slot][k * kBandChains + col];
-            if (m == kBandStage) {
+        for (int k = 0; k < kBandStage; ++k) v[k] = slot[k * kBandChains + t];
+    };
+    auto add = [&](long long st, const double (&v)[kBandStage]) {
+        if (!chain) return;
+        const long long left = mine - st * kBandStage;
+        if (left >= kBandStage) {
 #pragma unroll
-                for (int k = 0; k < kBandStage; ++k) lane_add(acc, v[k]);
-            } else {
-                for (int k = 0; k < m; ++k) lane_add(acc, v[k]);
-            }
-        }
-        // stage st+1 sits in r1 (st even) or r0 (st odd), read two stages ago;
-        // that register set then takes stage st+3
-        if (slot == 0) {
-            store(st + 1, 1, r1);
-            load(st + 3, r1);
+            for (int k = 0; k < kBandStage; ++k) lane_add(acc, v[k]);
         } else {
-            store(st + 1, 0, r0);
-            load(st + 3, r0);
+#pragma unroll
+            for (int k = 0; k < kBandStage; ++k)
+                if (k < left) lane_add(acc, v[k]);
         }
-        __syncthreads();
+    };
+    // stages 0 .. 3 into the loaders' registers, 0 and 1 into the ring
+#pragma unroll
+    for (int j = 0; j < kBandSets; ++j) load(j, ld[j]);
+    store(0, ld[0]);
+    store(1, ld[1]);
+    load(kBandSets, ld[0]);
+    load(kBandSets + 1, ld[1]);
+    __syncthreads();
+    fetch(0, v[0]);
+    // iteration s: the chains read stage s + 1 and add stage s; the loaders
+    // store stage s + 2 (set (s + 2) % 4) and read stage s + 6 into that set
+    for (long long s0 = 0; s0 < stages; s0 += kBandSets) {
+#pragma unroll
+        for (int j = 0; j < kBandSets; ++j) {
+            const long long s = s0 + j;
+            if (s < stages) {
+                fetch(s + 1, v[(j + 1) & 1]);
+                add(s, v[j & 1]);
+                store(s + 2, ld[(j + 2) % kBandSets]);
+                load(s + kBandAhead, ld[(j + 2) % kBandSets]);
+            }
+            __syncthreads();
+        }
     }
-    if (chain) lanes[l0 + col] = lane_band(acc);
+    if (chain) lanes[l0 + t] = lane_band(acc);
 }
 
 // Group g's 128 lane bands by the halving tree into gp[g]; the last group
