@@ -1701,6 +1701,22 @@ def test_banded_sums_are_the_oracles_bits_and_replay(unit_banded, gpu, kind, n):
         assert want[2] == BAND_LANE_TERMS[1]          # the reference's geometry: one band of seven terms
 
 
+@pytest.mark.parametrize("kind", ["cancel_lanes", "wide"])
+@pytest.mark.parametrize("n", [9 * 8192 * 32 + 12345, (1 << 24) + 3])
+def test_band_ordered_sum_across_many_stages(unit_banded, gpu, kind, n):
+    """The banded ordered sum where each virtual lane's walk spans many
+    32-row stages of the lanes kernel's ring (10 stages, the last partial and
+    not a multiple of the four loader register sets; and 64 stages): the
+    oracle's bits."""
+    import hawk_amd as hawk
+    x = _band_data(kind, n)
+    k = _load(unit_banded, "band_total")
+    print(f"band_total stages {kind} n={n}", flush=True)
+    cells = {c: dev(np.full(1, np.nan), gpu) for c in ("s", "s_sq", "s_ord")}
+    hawk.run(k, x=dev(x, gpu), **cells)
+    assert float(host(cells["s_ord"])[0]) == O.band_ordered_sum(x)
+
+
 def test_banded_sums_on_the_device_hold_the_reference_bounds(unit_banded, gpu):
     """Against exact rational sums: the reference's cancelling series within
     0.01 ULP53 (tests/test_banded_sum.py), a lane-cancelling series the plain
